@@ -1,0 +1,187 @@
+/*
+ * zinc_hip.h — C ABI of the MI355X (gfx950) HIP backend for ZINC's per-token
+ * decode loop. Built as libzinc_hip.so by hipcc. Every entry point is a plain
+ * C function over opaque handles, plain pointers and sizes, returning an int
+ * status (ZH_OK == 0). The ABI follows the reference's Metal shim pattern
+ * (src/metal/shim.h:23-80: opaque context/buffer handles, create_buffer,
+ * dispatch with push-constant style scalars, commit_and_wait) but with one
+ * typed entry point per kernel family instead of generic pipelines.
+ *
+ * Threading: one HIP stream per context; a context is not re-entrant
+ * (reference: one command buffer and queue per engine, forward.zig:4361-4363).
+ * Ordering: calls enqueue work on the context's stream and return; results are
+ * visible to the host after zh_sync (reference: submitAndWait,
+ * forward.zig:7757-7772).
+ * Buffers: zh_buf_alloc pads every allocation by 256 bytes so kernels may
+ * issue dword-aligned 128-bit loads that straddle the logical end.
+ */
+#ifndef ZINC_HIP_H
+#define ZINC_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (map to the reference's Zig error set) ---------------- */
+enum {
+    ZH_OK = 0,
+    ZH_ERR_UNSUPPORTED_QUANT_TYPE = 1, /* error.UnsupportedQuantType  dmmv.zig:722,822 */
+    ZH_ERR_INVALID_ARGUMENT = 2,       /* error.InvalidArgument       dmmv.zig:767,944,1065 */
+    ZH_ERR_HIP = 3,                    /* device/runtime failure */
+    ZH_ERR_CONTEXT_LENGTH_EXCEEDED = 4,/* error.ContextLengthExceeded forward.zig:4300 */
+    ZH_ERR_OUT_OF_MEMORY = 5,
+    ZH_ERR_TENSOR_NOT_FOUND = 6        /* error.TensorNotFound        forward.zig:7377 */
+};
+
+/* ---- GGMLType values used on the path (src/model/gguf.zig:38-69) -------- */
+enum { ZH_F32 = 0, ZH_F16 = 1, ZH_Q8_0 = 8, ZH_Q4_K = 12, ZH_Q6_K = 14, ZH_MXFP4 = 39 };
+
+typedef struct zh_ctx zh_ctx;
+typedef struct zh_buf zh_buf;
+typedef struct zh_engine zh_engine;
+
+/* ---- device lifecycle: replaces Instance.init / mtl_init (shim.h:24-25) -- */
+int  zh_init(int device, zh_ctx **out);
+void zh_destroy(zh_ctx *ctx);
+const char *zh_last_error(const zh_ctx *ctx);
+const char *zh_status_string(int status);
+/* name (>=64 bytes), CU count, total HBM bytes */
+int  zh_device_info(zh_ctx *ctx, char *name, size_t name_len, int *cu_count, uint64_t *hbm_bytes);
+int  zh_sync(zh_ctx *ctx);
+
+/* ---- buffers: replaces Buffer.initDeviceLocal (vulkan/buffer.zig:102) and
+ *      mtl_create_buffer / mtl_free_buffer (shim.h:37-41) ----------------- */
+int      zh_buf_alloc(zh_ctx *ctx, uint64_t size, zh_buf **out);
+void     zh_buf_free(zh_ctx *ctx, zh_buf *buf);
+uint64_t zh_buf_size(const zh_buf *buf);
+void    *zh_buf_device_ptr(const zh_buf *buf);
+int      zh_buf_upload(zh_ctx *ctx, zh_buf *buf, uint64_t offset, const void *src, uint64_t n);
+int      zh_buf_download(zh_ctx *ctx, const zh_buf *buf, uint64_t offset, void *dst, uint64_t n);
+int      zh_buf_fill_u8(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint8_t v, uint64_t n);
+
+/* ---- timing (the build's counterpart of the reference's timestamp-query
+ *      profiling, forward.zig:2443-2476) ------------------------------- */
+int zh_event_record(zh_ctx *ctx, int slot);          /* slot 0..63 */
+int zh_event_elapsed_ms(zh_ctx *ctx, int a, int b, float *ms);
+
+/* ---- synthetic data (seeded, bit-identical to oracle/zinc_oracle.c) ----- */
+/* Fill rows x cols of `qtype` blocks at `offset` per the BASELINE distributions. */
+int zh_synth_tensor(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint32_t qtype,
+                    uint64_t rows, uint64_t cols, uint64_t seed, uint64_t stream);
+/* kind 0: N(0,1)*scale f32; 1: N(0,1) f16; 2: norm weight 1+U(-.01,.01) f32 */
+int zh_synth_vector(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint32_t kind, uint64_t n,
+                    float scale, uint64_t seed, uint64_t stream);
+
+/* ---- quantized DMMV --------------------------------------------------- */
+/* y[y_off..] (=, or += when acc_mode==1) = dequant(W[a_off..]) (MxK) * x[x_off..].
+ * Replaces DmmvDispatch.recordDispatch (dmmv.zig:806-874) / dispatchDmmvInner
+ * (forward.zig:8431-8540) with DmmvPushConstants{M,K,a_offset,x_offset,
+ * y_offset,acc_mode} (dmmv.zig:21-28). Offsets are BYTES. qtype: Q4_K, Q6_K,
+ * Q8_0 (K % 64 == 0), MXFP4 (K % 32 == 0). K % 256 == 0 for K-quants. */
+int zh_dmmv(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off,
+            const zh_buf *x, uint64_t x_off, zh_buf *y, uint64_t y_off,
+            uint32_t M, uint32_t K, uint32_t acc_mode);
+/* y = silu(Wg x) * (Wu x): dispatchDmmvFusedGateUpSwiglu (forward.zig:8237-8273,
+ * dmmv_q4k_fused_gate_up_swiglu.comp). Both matrices share qtype. */
+int zh_dmmv_fused_gate_up_swiglu(zh_ctx *ctx, uint32_t qtype, const zh_buf *Wg, uint64_t g_off,
+                                 const zh_buf *Wu, uint64_t u_off, const zh_buf *x, uint64_t x_off,
+                                 zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K);
+/* Expert-gathered DMMV (recordMoeDispatch, dmmv.zig:709; MoeDmmvPushConstants
+ * dmmv.zig:41-48; dmmv_q4k_moe_kpar.comp:56-95): for slot s < n_used,
+ * e = routing[s] (u32 ids at the start of `routing`),
+ * y[y_off + s*M*4 ..] = W[e*expert_stride ..] * x[x_off + s*x_expert_stride*4 ..]. */
+int zh_dmmv_moe(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t expert_stride,
+                const zh_buf *routing, const zh_buf *x, uint32_t x_expert_stride, uint64_t x_off,
+                zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t n_used);
+/* Bit-exact dequantisation of rows [row0, row0+n_rows) to f32 (dequantRow,
+ * forward.zig:242-465), used for the embedding gather and for parity tests. */
+int zh_dequant_rows(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off,
+                    uint32_t row0, uint32_t n_rows, uint32_t K, zh_buf *out, uint64_t out_off);
+
+/* ---- elementwise / norm / rope / attention / routing / sampling --------- */
+/* rms_norm_mul.comp via dispatchRmsNorm (forward.zig:3408); cpuRmsNormMul
+ * (forward.zig:618-626): out = w[i % w_len] * (x * 1/sqrt(mean(x^2)+eps)). */
+int zh_rms_norm(zh_ctx *ctx, const zh_buf *x, uint64_t x_off, const zh_buf *w, uint32_t w_len,
+                zh_buf *out, uint64_t out_off, uint32_t n, uint32_t n_groups, float eps);
+/* swiglu.comp / cpuSwiGLU (forward_metal.zig:6567-6572) */
+int zh_swiglu(zh_ctx *ctx, const zh_buf *g, uint64_t g_off, const zh_buf *u, uint64_t u_off,
+              zh_buf *out, uint64_t out_off, uint32_t n);
+/* Fused per-head Q/K RMSNorm + NeoX RoPE + fp16 KV write
+ * (qk_norm_rope_kv_write.comp, dispatchQkNormRopeKvWrite forward.zig:4008).
+ * q (f32, n_q_heads*head_dim) is normed+rotated in place; k is normed+rotated
+ * and, with raw v, stored as fp16 into the caches at the physical slot of
+ * logical token `position` (page table of 16-token pages, forward.zig:677-698).
+ * Cache layout: [n_kv_heads][cache_tokens][head_dim] fp16. inv_freq holds
+ * head_dim/2 f32 inverse frequencies (forward.zig:1495-1500). */
+int zh_qk_norm_rope_kv_write(zh_ctx *ctx, zh_buf *q, const zh_buf *q_norm_w, const zh_buf *k,
+                             const zh_buf *k_norm_w, const zh_buf *v, const zh_buf *inv_freq,
+                             zh_buf *k_cache, zh_buf *v_cache, const zh_buf *page_table,
+                             uint32_t n_pages, uint32_t cache_tokens, uint32_t n_q_heads,
+                             uint32_t n_kv_heads, uint32_t head_dim, uint32_t position, float eps);
+/* Paged GQA flash-decode over the fp16 cache, split along context with a
+ * log-sum-exp merge (flash_attn.comp + flash_attn_split_merge.comp via
+ * AttentionDispatch.recordFlashAttnSplit/SplitMerge, attention.zig:199-316;
+ * oracle cpuAttention forward_metal.zig:6600-6646). out: f32[n_heads*head_dim].
+ * attn_scale 0 => 1/sqrt(head_dim). */
+int zh_flash_decode(zh_ctx *ctx, const zh_buf *q, const zh_buf *k_cache, const zh_buf *v_cache,
+                    const zh_buf *page_table, uint32_t n_pages, uint32_t cache_tokens, zh_buf *out,
+                    uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_len,
+                    float attn_scale);
+/* softmax_topk_v2.comp / topKSoftmax (forward.zig:496-537): routing gets
+ * [ids u32 x k][weights f32 x k]. n <= 256, k <= 16. */
+int zh_softmax_topk(zh_ctx *ctx, const zh_buf *logits, uint32_t n, uint32_t k, zh_buf *routing);
+/* moe_weighted_acc.comp:23-33: a[i] += sum_j w_j * b[j*src_stride + i] with
+ * w_j read from routing[k + j]. */
+int zh_moe_weighted_acc(zh_ctx *ctx, zh_buf *a, const zh_buf *b, const zh_buf *routing,
+                        uint32_t n, uint32_t n_used, uint32_t src_stride);
+/* ArgmaxDispatch.record (argmax.zig:66-87): first (lowest-index) maximum,
+ * as sampleGreedy's CPU scan (forward.zig:10343-10356). result: u32. */
+int zh_argmax(zh_ctx *ctx, const zh_buf *logits, uint32_t n, zh_buf *result, uint64_t result_off);
+
+/* ---- engine: InferenceEngine surface (forward.zig:1226-10983) ---------- */
+typedef struct zh_model_config {
+    uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab;
+    uint32_t n_experts, n_experts_used, expert_ffn; /* n_experts == 0 => dense */
+    uint32_t max_ctx;                               /* KV capacity in tokens */
+    uint32_t type_attn, type_ffn_gate_up, type_ffn_down, type_lm_head, type_embd, type_router;
+    float rope_base, eps;
+    uint64_t seed;                                  /* synthetic weights seed */
+} zh_model_config;
+
+/* InferenceEngine.init (forward.zig:1226) on a seeded random-init model whose
+ * tensors use the same stream numbering as the oracle. */
+int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engine **out);
+void zh_engine_destroy(zh_engine *eng);                 /* deinit forward.zig:10849 */
+/* Fill KV positions [0, n_tokens) with seeded N(0,1) fp16 values. */
+int zh_engine_prefill_kv_random(zh_engine *eng, uint32_t n_tokens, uint64_t seed);
+/* decodeStep(state, token, collect_output) (forward.zig:4299): runs one token
+ * at `position`; with collect_output the greedy token is produced on device. */
+int zh_engine_decode_step(zh_engine *eng, uint32_t token, uint32_t position, int collect_output);
+/* sampleGreedy (forward.zig:10338): waits and returns the last argmax token. */
+int zh_engine_sample_greedy(zh_engine *eng, uint32_t *token);
+/* generate (forward.zig:10983-11192): feed prompt tokens from `start_pos`,
+ * then greedy-decode max_tokens tokens (stopping after eos if eos != UINT32_MAX).
+ * out_tokens receives up to max_tokens ids; *n_out the count. The decode
+ * loop feeds each argmax back on device (no host round trip per token). */
+int zh_engine_generate(zh_engine *eng, const uint32_t *prompt, uint32_t n_prompt, uint32_t start_pos,
+                       uint32_t max_tokens, uint32_t eos, uint32_t *out_tokens, uint32_t *n_out);
+/* Copy the last logits (vocab f32) to host. */
+int zh_engine_logits(zh_engine *eng, float *dst);
+/* Copy the hidden state (hidden f32) after the last step to host. */
+int zh_engine_hidden(zh_engine *eng, float *dst);
+/* Weight tensor by oracle stream id ((layer+1)<<8 | kind, or 1/2/3 globals). */
+int zh_engine_tensor(zh_engine *eng, uint64_t stream, zh_buf **buf, uint64_t *offset, uint64_t *bytes);
+/* Gather n logical tokens of layer `layer` K (which=0) or V (1) as fp16,
+ * logical-token-major [t][kv_head][head_dim] (the oracle's layout). */
+int zh_engine_read_kv(zh_engine *eng, uint32_t layer, uint32_t which, uint32_t t0, uint32_t n,
+                      uint16_t *dst);
+/* Model bytes touched per decoded token at context length L (weights + fp16
+ * KV + activations), the numerator of the bandwidth roofline. */
+uint64_t zh_engine_bytes_per_token(zh_engine *eng, uint32_t L);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZINC_HIP_H */

@@ -1,0 +1,114 @@
+// zh_device.h — device-side helpers shared by the gfx950 kernels.
+//
+// Conventions:
+//  * wave64 everywhere (gfx950); workgroups are multiples of 64 lanes.
+//  * Weight buffers are raw GGUF blocks addressed by byte offsets, exactly as
+//    the reference's DmmvPushConstants (src/compute/dmmv.zig:21-28).
+//  * Activations feeding a DMMV are block-quantised once into "XQ" form (see
+//    below) so the mat-vec inner loop runs on v_dot4_i32_i8 instead of
+//    per-weight int->float conversion plus FMA.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));  // dword-aligned 128-bit load
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define ZH_DEV static __device__ __forceinline__
+#define ZH_DEVM __device__ __forceinline__  // for static member functions
+
+// ---------------------------------------------------------------------------
+// XQ activation format.
+// A vector of K floats (K % 32 == 0) is cut into K/32 blocks. Block j stores
+//   limb[j][3][32] int8 : X_i = L0 + 256*L1 + 65536*L2, |X_i| < 2^22
+//   xs[j]  float        : x_i ~= X_i * xs[j], xs = 2^(E-22), max|x| < 2^E
+//   xsum[j][2] float    : sum of the quantised x over each 16-element half
+// X carries 22 magnitude bits relative to the block maximum, so the
+// representation error (<= 2^-23 of the block max per element) is below the
+// rounding of an f32 serial dot product. Dot products against 4..8-bit
+// weight codes accumulate exactly in int32.
+// ---------------------------------------------------------------------------
+struct XQView {
+    int8_t *limb;   // [nblk][3][32]
+    float *xs;      // [nblk]
+    float *xsum;    // [nblk][2]
+};
+ZH_DEV XQView xq_view(void *base, uint32_t nblk) {
+    XQView v;
+    v.limb = (int8_t *)base;
+    v.xs = (float *)((char *)base + (size_t)nblk * 96);
+    v.xsum = v.xs + nblk;
+    return v;
+}
+static inline size_t xq_bytes(uint32_t K) { return (size_t)(K / 32) * (96 + 12); }
+
+ZH_DEV float bits_f(uint32_t u) { return __uint_as_float(u); }
+
+// Quantise one value given the block's inverse scale 2^(22-E).
+ZH_DEV int xq_quant(float x, float inv) {
+    int X = (int)__builtin_rintf(x * inv);  // power-of-two scaling is exact
+    X = X > 4194303 ? 4194303 : (X < -4194303 ? -4194303 : X);
+    return X;
+}
+// Block exponent for max|x|: returns inverse scale 2^(22-E) and scale 2^(E-22)
+// with max|x| < 2^E. amax == 0 (or denormal) gives zero scales.
+ZH_DEV void xq_scales(float amax, float &inv, float &scale) {
+    uint32_t eb = __float_as_uint(amax) >> 23;  // biased exponent of amax
+    if (eb == 0) { inv = 0.f; scale = 0.f; return; }
+    int E = (int)eb - 126;                     // amax < 2^E
+    int ei = 22 - E + 127, es = E - 22 + 127;
+    ei = ei < 1 ? 1 : (ei > 254 ? 254 : ei);
+    es = es < 1 ? 1 : (es > 254 ? 254 : es);
+    inv = __uint_as_float((uint32_t)ei << 23);
+    scale = __uint_as_float((uint32_t)es << 23);
+}
+// Split X into three balanced int8 limbs.
+ZH_DEV void xq_limbs(int X, int &l0, int &l1, int &l2) {
+    l0 = (int)(int8_t)(X & 0xFF);
+    int X1 = (X - l0) >> 8;
+    l1 = (int)(int8_t)(X1 & 0xFF);
+    l2 = (X1 - l1) >> 8;
+}
+ZH_DEV uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
+           ((uint32_t)(d & 0xFF) << 24);
+}
+
+ZH_DEV int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (DPP/permute lowered by the compiler).
+// ---------------------------------------------------------------------------
+template <int WIDTH>
+ZH_DEV float team_sum(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+ZH_DEV float wave_sum(float v) { return team_sum<64>(v); }
+ZH_DEV float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+ZH_DEV float h2f(uint32_t h16) { return (float)__ushort_as_half((unsigned short)(h16 & 0xFFFF)); }
+ZH_DEV uint16_t f2h_rn(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// Load n dwords starting at an arbitrary byte address (byte-aligned) using
+// dword-aligned loads and v_alignbyte. `out` receives n dwords.
+template <int N>
+ZH_DEV void load_unaligned(const uint8_t *p, uint32_t *out) {
+    uintptr_t a = (uintptr_t)p;
+    const uint32_t *q = (const uint32_t *)(a & ~(uintptr_t)3);
+    uint32_t sh = (uint32_t)(a & 3);
+    uint32_t t[N + 1];
+#pragma unroll
+    for (int i = 0; i < N + 1; i++) t[i] = q[i];
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
+}

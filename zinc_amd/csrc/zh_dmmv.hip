@@ -1,0 +1,670 @@
+// zh_dmmv.hip — dequantise-fused mat-vec (DMMV) for Q4_K, Q6_K, Q8_0 and
+// MXFP4 on gfx950, plus the activation quantiser and bit-exact dequant.
+//
+// Design (MI355X-first, not a translation of dmmv_*.comp):
+//  * A "unit" is a fixed 64-element column slice of a row (32 for MXFP4).
+//    Lane t of a team always owns unit t of every row it visits, so its slice
+//    of the activation vector is loaded ONCE into registers (as XQ int8 limbs)
+//    and reused for every row: no LDS or L1 traffic for x in the row loop.
+//  * A team is K/64 lanes (power-of-two padded when it fits in a wave, or
+//    whole waves when K > 4096). Teams walk R rows at a time, issuing all R
+//    rows' 128-bit weight loads before any arithmetic (memory-level
+//    parallelism for HBM3E), then reduce across the team with wave shuffles.
+//  * Inner products run on v_dot4_i32_i8 against the 4/6/8-bit codes with
+//    exact int32 accumulation; per-sub-block scales and mins are applied in
+//    f32 afterwards: y = sum_j d*sc_j*(xs_j*S_j) - dmin*m_j*sum(x_j).
+//  * Weights are read in GGUF layout straight from HBM (dword-aligned loads
+//    plus v_alignbyte for the 210/34/17-byte block formats).
+#include "zh_device.h"
+#include "zh_internal.h"
+
+#include <vector>
+
+// ---------------------------------------------------------------------------
+// Activation quantiser: x (f32) -> XQ. One 32-lane half-wave per block.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_quantize_xq(const float *__restrict__ x, uint8_t *__restrict__ xq,
+                                                     uint32_t K, uint32_t x_stride, uint64_t xq_stride) {
+    const uint32_t nblk = K / 32;
+    const uint32_t vec = blockIdx.y;
+    const uint32_t blk = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const uint32_t l = threadIdx.x & 31;
+    if (blk >= nblk) return;
+    const float *xv = x + (size_t)vec * x_stride;
+    XQView v = xq_view(xq + vec * xq_stride, nblk);
+    float xi = xv[blk * 32 + l];
+    float a = fabsf(xi);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
+    float inv, sc;
+    xq_scales(a, inv, sc);
+    int X = xq_quant(xi, inv);
+    int l0, l1, l2;
+    xq_limbs(X, l0, l1, l2);
+    v.limb[blk * 96 + l] = (int8_t)l0;
+    v.limb[blk * 96 + 32 + l] = (int8_t)l1;
+    v.limb[blk * 96 + 64 + l] = (int8_t)l2;
+    int s = X;
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 32);  // sum within 16-lane halves
+    if (l == 0) v.xs[blk] = sc;
+    if ((l & 15) == 0) v.xsum[blk * 2 + (l >> 4)] = (float)s * sc;
+}
+
+int zhk_quantize_xq(zh_ctx *c, const float *x, void *xq, uint32_t K, uint32_t n_vec, uint32_t x_stride) {
+    uint32_t nblk = K / 32;
+    hipLaunchKernelGGL(k_quantize_xq, dim3((nblk + 7) / 8, n_vec), dim3(256), 0, c->stream, x,
+                       (uint8_t *)xq, K, x_stride, (uint64_t)zh_xq_bytes(K));
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Per-lane activation registers: 48 limb dwords + 4 scale/sum pairs.
+// ---------------------------------------------------------------------------
+struct XReg {
+    uint32_t L[48];
+    float xs[4];
+    float xz[4];
+};
+
+ZH_DEV void load_limbs(uint32_t *dst, const int8_t *src, int ndw) {
+    const u32x4 *p = (const u32x4 *)src;
+#pragma unroll
+    for (int i = 0; i < ndw / 4; i++) {
+        u32x4 v = p[i];
+        dst[4 * i + 0] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
+    }
+}
+
+ZH_DEV u32x4 ld4(const uint8_t *p) { return *(const u32x4_a4 *)p; }
+
+ZH_DEV int comb_int(int d0, int d1, int d2) { return (d2 * 256 + d1) * 256 + d0; }
+ZH_DEV float comb_f32(int d0, int d1, int d2) { return fmaf((float)d2, 65536.f, (float)(d1 * 256 + d0)); }
+
+// ---------------------------------------------------------------------------
+// Q4_K: 144-byte blocks {f16 d, f16 dmin, 12 B packed 6-bit scales/mins,
+// 128 B nibbles} (forward.zig:370-409). Unit u = (block u>>2, sub-pair p=u&3):
+// qs[32p..32p+31] low nibbles -> sub-block 2p, high -> 2p+1.
+// ---------------------------------------------------------------------------
+struct FmtQ4K {
+    static constexpr int EPU = 64, RAW = 12, QK = 256, BPB = 144;
+    ZH_DEVM static void load_x(XReg &xr, XQView v, int u) {
+        int xb = 2 * u;  // (256*(u>>2) + 64*(u&3)) / 32
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            load_limbs(&xr.L[s * 24], v.limb + (size_t)(xb + s) * 96, 24);
+            xr.xs[s] = v.xs[xb + s];
+            xr.xz[s] = v.xsum[(xb + s) * 2] + v.xsum[(xb + s) * 2 + 1];
+        }
+    }
+    ZH_DEVM static void load_raw(const uint8_t *row, int u, uint32_t *raw) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 144;
+        int p = u & 3;
+        u32x4 h = ld4(b), q0 = ld4(b + 16 + 32 * p), q1 = ld4(b + 32 + 32 * p);
+        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+        raw[4] = q0.x; raw[5] = q0.y; raw[6] = q0.z; raw[7] = q0.w;
+        raw[8] = q1.x; raw[9] = q1.y; raw[10] = q1.z; raw[11] = q1.w;
+    }
+    ZH_DEVM static float compute(const uint32_t *raw, const XReg &xr, int u) {
+        int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            uint32_t w = raw[4 + i];
+            uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                D[0][k] = sdot4(lo, xr.L[k * 8 + i], D[0][k]);
+                D[1][k] = sdot4(hi, xr.L[24 + k * 8 + i], D[1][k]);
+            }
+        }
+        // getScaleMinK4 (forward.zig:229-238) for j = 2p, 2p+1.
+        int p = u & 3;
+        uint32_t w1 = raw[1], w2 = raw[2], w3 = raw[3];
+        uint32_t sc[2], mn[2];
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            int j = 2 * p + s;
+            if (p < 2) {
+                sc[s] = (w1 >> (8 * j)) & 63;
+                mn[s] = (w2 >> (8 * j)) & 63;
+            } else {
+                int i4 = j - 4;
+                sc[s] = ((w3 >> (8 * i4)) & 15) | (((w1 >> (8 * i4 + 6)) & 3) << 4);
+                mn[s] = ((w3 >> (8 * i4 + 4)) & 15) | (((w2 >> (8 * i4 + 6)) & 3) << 4);
+            }
+        }
+        float d = h2f(raw[0]), dmin = h2f(raw[0] >> 16);
+        float S0 = (float)comb_int(D[0][0], D[0][1], D[0][2]);
+        float S1 = (float)comb_int(D[1][0], D[1][1], D[1][2]);
+        float A = fmaf((float)sc[1] * xr.xs[1], S1, (float)sc[0] * xr.xs[0] * S0);
+        float B = fmaf((float)mn[1], xr.xz[1], (float)mn[0] * xr.xz[0]);
+        return fmaf(d, A, -dmin * B);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q6_K: 210-byte blocks {ql[128], qh[64], int8 sc[16], f16 d}
+// (forward.zig:276-325). Unit u = (block u>>2, half h=(u>>1)&1, l0=16*(u&1)):
+// l in [l0, l0+16) of all four quarters g (element 128h + 32g + l).
+// ---------------------------------------------------------------------------
+struct FmtQ6K {
+    static constexpr int EPU = 64, RAW = 22, QK = 256, BPB = 210;
+    ZH_DEVM static void load_x(XReg &xr, XQView v, int u) {
+        int b = u >> 2, h = (u >> 1) & 1, half = u & 1;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            int xb = 8 * b + 4 * h + g;
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                u32x4 t = *(const u32x4 *)(v.limb + (size_t)xb * 96 + k * 32 + half * 16);
+                xr.L[(g * 3 + k) * 4 + 0] = t.x; xr.L[(g * 3 + k) * 4 + 1] = t.y;
+                xr.L[(g * 3 + k) * 4 + 2] = t.z; xr.L[(g * 3 + k) * 4 + 3] = t.w;
+            }
+            xr.xs[g] = v.xs[xb];
+            xr.xz[g] = -32.f * v.xsum[xb * 2 + half];
+        }
+    }
+    ZH_DEVM static void load_raw(const uint8_t *row, int u, uint32_t *raw) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 210;
+        int h = (u >> 1) & 1, l0 = 16 * (u & 1);
+        const uint8_t *pA = b + 64 * h + l0, *pB = pA + 32, *pC = b + 128 + 32 * h + l0;
+        const uint8_t *srcs[3] = {pA, pB, pC};
+#pragma unroll
+        for (int s = 0; s < 3; s++) {
+            uintptr_t a = (uintptr_t)srcs[s] & ~(uintptr_t)3;
+            u32x4 t = *(const u32x4 *)a;
+            raw[s * 5 + 0] = t.x; raw[s * 5 + 1] = t.y; raw[s * 5 + 2] = t.z; raw[s * 5 + 3] = t.w;
+            raw[s * 5 + 4] = *(const uint32_t *)(a + 16);
+        }
+        {   // scales sc[0..16) and d: bytes 192..211 of the block
+            uintptr_t a = (uintptr_t)(b + 192) & ~(uintptr_t)3;
+            u32x4 t = *(const u32x4 *)a;
+            raw[15] = t.x; raw[16] = t.y; raw[17] = t.z; raw[18] = t.w;
+            raw[19] = *(const uint32_t *)(a + 16);
+            raw[20] = *(const uint32_t *)(a + 20);
+        }
+        raw[21] = (uint32_t)((uintptr_t)b & 3);
+    }
+    ZH_DEVM static float compute(const uint32_t *raw, const XReg &xr, int u) {
+        uint32_t sh = raw[21];
+        uint32_t A[4], B[4], C[4], S[5];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            A[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
+            B[i] = __builtin_amdgcn_alignbyte(raw[5 + i + 1], raw[5 + i], sh);
+            C[i] = __builtin_amdgcn_alignbyte(raw[10 + i + 1], raw[10 + i], sh);
+        }
+#pragma unroll
+        for (int i = 0; i < 5; i++) S[i] = __builtin_amdgcn_alignbyte(raw[15 + i + 1], raw[15 + i], sh);
+        int D[4][3];
+#pragma unroll
+        for (int g = 0; g < 4; g++) D[g][0] = D[g][1] = D[g][2] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t a = A[i], bq = B[i], c = C[i];
+            uint32_t q[4];
+            q[0] = (a & 0x0F0F0F0Fu) | ((c << 4) & 0x30303030u);
+            q[1] = (bq & 0x0F0F0F0Fu) | ((c << 2) & 0x30303030u);
+            q[2] = ((a >> 4) & 0x0F0F0F0Fu) | (c & 0x30303030u);
+            q[3] = ((bq >> 4) & 0x0F0F0F0Fu) | ((c >> 2) & 0x30303030u);
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+#pragma unroll
+                for (int k = 0; k < 3; k++) D[g][k] = sdot4(q[g], xr.L[(g * 3 + k) * 4 + i], D[g][k]);
+        }
+        int h = (u >> 1) & 1, half = u & 1;
+        float d = h2f(S[4]);  // bytes 208..209
+        float acc = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            int idx = 8 * h + half + 2 * g;  // sc[is + 2g], is = 8h + l/16
+            int scv = (int)(int8_t)((S[idx >> 2] >> (8 * (idx & 3))) & 0xFF);
+            float Sg = comb_f32(D[g][0], D[g][1], D[g][2]);
+            // sum_l d*sc*(q-32)*x = d*sc*(xs*S - 32*sum x)
+            acc = fmaf((float)scv, fmaf(xr.xs[g], Sg, xr.xz[g]), acc);
+        }
+        return d * acc;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q8_0: 34-byte blocks {f16 d, int8 q[32]} (forward.zig:258-275). Unit u = two
+// consecutive blocks (68 bytes, dword aligned when K % 64 == 0).
+// ---------------------------------------------------------------------------
+struct FmtQ80 {
+    static constexpr int EPU = 64, RAW = 17, QK = 64, BPB = 68;
+    ZH_DEVM static void load_x(XReg &xr, XQView v, int u) {
+        int xb = 2 * u;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            load_limbs(&xr.L[s * 24], v.limb + (size_t)(xb + s) * 96, 24);
+            xr.xs[s] = v.xs[xb + s];
+        }
+    }
+    ZH_DEVM static void load_raw(const uint8_t *row, int u, uint32_t *raw) {
+        const uint8_t *b = row + (size_t)u * 68;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            u32x4 t = ld4(b + 16 * i);
+            raw[4 * i] = t.x; raw[4 * i + 1] = t.y; raw[4 * i + 2] = t.z; raw[4 * i + 3] = t.w;
+        }
+        raw[16] = *(const uint32_t *)(b + 64);
+    }
+    ZH_DEVM static float compute(const uint32_t *raw, const XReg &xr, int u) {
+        int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            uint32_t q0 = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2);
+            uint32_t q1 = raw[9 + i];
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                D[0][k] = sdot4(q0, xr.L[k * 8 + i], D[0][k]);
+                D[1][k] = sdot4(q1, xr.L[24 + k * 8 + i], D[1][k]);
+            }
+        }
+        float d0 = h2f(raw[0]), d1 = h2f(raw[8] >> 16);
+        float S0 = comb_f32(D[0][0], D[0][1], D[0][2]);
+        float S1 = comb_f32(D[1][0], D[1][1], D[1][2]);
+        return fmaf(d1 * xr.xs[1], S1, d0 * xr.xs[0] * S0);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// MXFP4: 17-byte blocks {e8m0 e, 16 B of E2M1 codes}; low nibble -> element j,
+// high -> j+16 (forward.zig:441-459). Unit = one block (32 elements).
+// 2*value is an int8 in {0,+-1,2,3,4,6,8,12}: looked up 4 at a time with
+// v_perm_b32 and dotted against the limbs; the scale is 2^(e-127)/2.
+// ---------------------------------------------------------------------------
+struct FmtMXFP4 {
+    static constexpr int EPU = 32, RAW = 6, QK = 32, BPB = 17;
+    ZH_DEVM static void load_x(XReg &xr, XQView v, int u) {
+        load_limbs(xr.L, v.limb + (size_t)u * 96, 24);
+        xr.xs[0] = v.xs[u];
+    }
+    ZH_DEVM static void load_raw(const uint8_t *row, int u, uint32_t *raw) {
+        const uint8_t *b = row + (size_t)u * 17;
+        uintptr_t a = (uintptr_t)b & ~(uintptr_t)3;
+        u32x4 t = *(const u32x4 *)a;
+        raw[0] = t.x; raw[1] = t.y; raw[2] = t.z; raw[3] = t.w;
+        raw[4] = *(const uint32_t *)(a + 16);
+        raw[5] = (uint32_t)((uintptr_t)b & 3);
+    }
+    ZH_DEVM static uint32_t e2m1x2(uint32_t nib) {
+        uint32_t sel = nib & 0x07070707u;
+        uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, sel);
+        uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, sel);
+        uint32_t sm = (nib >> 3) & 0x01010101u;
+        uint32_t mask = (sm << 8) - sm;
+        return (neg & mask) | (pos & ~mask);
+    }
+    ZH_DEVM static float compute(const uint32_t *raw, const XReg &xr, int u) {
+        uint32_t sh = raw[5];
+        uint32_t w[5];
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
+        w[4] = __builtin_amdgcn_alignbyte(0u, raw[4], sh);  // byte 16 of the block in bits 0..7
+        uint32_t e = w[0] & 0xFF;
+        int D[3] = {0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t c = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 1);  // code bytes 1+4i..4+4i
+            uint32_t lo = e2m1x2(c & 0x0F0F0F0Fu), hi = e2m1x2((c >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                D[k] = sdot4(lo, xr.L[k * 8 + i], D[k]);
+                D[k] = sdot4(hi, xr.L[k * 8 + 4 + i], D[k]);
+            }
+        }
+        float d = __uint_as_float(e == 0 ? 0x00400000u : (e << 23));
+        return d * (0.5f * xr.xs[0]) * (float)comb_int(D[0], D[1], D[2]);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Team kernel.
+// ---------------------------------------------------------------------------
+struct DmmvP {
+    const uint8_t *W, *W2;  // W2: up matrix for the fused gate/up/SwiGLU mode
+    const uint8_t *xq;
+    float *y;
+    uint32_t M, K;
+    uint64_t row_bytes;
+    uint32_t acc;
+    const uint32_t *routing;  // MoE: expert id per grid.y slot
+    uint64_t expert_stride, xq_slot_stride;
+    uint32_t y_slot_stride;
+};
+
+enum { MODE_PLAIN = 0, MODE_GATE_UP = 1 };
+
+ZH_DEV float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+template <class F, int TL, int NW, int R, int MODE, bool MOE>
+__global__ __launch_bounds__(NW == 1 ? 256 : NW * 64) void k_dmmv(DmmvP p) {
+    constexpr int TPW = (NW == 1) ? 256 / TL : 1;  // teams per workgroup
+    constexpr int NM = (MODE == MODE_GATE_UP) ? 2 : 1;
+    const int tid = threadIdx.x;
+    const int tlane = (NW == 1) ? (tid % TL) : tid;
+    const int team_in_wg = (NW == 1) ? (tid / TL) : 0;
+    const uint32_t U = p.K / F::EPU;
+    const bool active = (uint32_t)tlane < U;
+
+    const uint8_t *Wm[2] = {p.W, p.W2};
+    const uint8_t *xqb = p.xq;
+    float *y = p.y;
+    if (MOE) {
+        const uint32_t slot = blockIdx.y;
+        const uint64_t e = p.routing[slot];
+        Wm[0] += e * p.expert_stride;
+        if (NM == 2) Wm[1] += e * p.expert_stride;
+        xqb += slot * p.xq_slot_stride;
+        y += (size_t)slot * p.y_slot_stride;
+    }
+    XQView v = xq_view((void *)xqb, p.K / 32);
+    XReg xr;
+    if (active) F::load_x(xr, v, tlane);
+
+    __shared__ float red[NW > 1 ? NW * R * NM : 1];
+    const uint32_t nteams = gridDim.x * TPW;
+    for (uint32_t r0 = (blockIdx.x * TPW + team_in_wg) * R; r0 < p.M; r0 += nteams * R) {
+        uint32_t raw[NM][R][F::RAW];
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (active && r0 + r < p.M) F::load_raw(Wm[m] + (size_t)(r0 + r) * p.row_bytes, tlane, raw[m][r]);
+        float part[NM][R];
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                part[m][r] = (active && r0 + r < p.M) ? F::compute(raw[m][r], xr, tlane) : 0.f;
+        if (NW == 1) {
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int r = 0; r < R; r++) part[m][r] = team_sum<TL>(part[m][r]);
+        } else {
+            const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    float s = wave_sum(part[m][r]);
+                    if (lane == 0) red[(m * R + r) * NW + wave] = s;
+                }
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    float s = 0.f;
+#pragma unroll
+                    for (int w = 0; w < NW; w++) s += red[(m * R + r) * NW + w];
+                    part[m][r] = s;
+                }
+            __syncthreads();
+        }
+        // lane r of the team writes row r0 + r
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (tlane == r && r0 + r < p.M) {
+                float out;
+                if (MODE == MODE_GATE_UP) out = silu_mul(part[0][r], part[NM - 1][r]);
+                else out = part[0][r];
+                if (p.acc) out += y[r0 + r];
+                y[r0 + r] = out;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+// ---------------------------------------------------------------------------
+template <class F, int TL, int NW, int R, int MODE, bool MOE>
+static int launch_one(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
+    constexpr int TPW = (NW == 1) ? 256 / TL : 1;
+    constexpr int BS = (NW == 1) ? 256 : NW * 64;
+    uint32_t teams = (p.M + R - 1) / R;
+    uint32_t wgs = (teams + TPW - 1) / TPW;
+    uint32_t cap = (uint32_t)c->cu_count * (NW == 1 ? 8u : 16u / NW + 1u);
+    if (MOE) cap = (cap + n_slots - 1) / n_slots;
+    if (wgs > cap) wgs = cap;
+    if (wgs == 0) wgs = 1;
+    hipLaunchKernelGGL((k_dmmv<F, TL, NW, R, MODE, MOE>), dim3(wgs, MOE ? n_slots : 1), dim3(BS), 0,
+                       c->stream, p);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+template <class F, int MODE, bool MOE>
+static int launch_fmt(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
+    constexpr int R = 4;
+    uint32_t U = p.K / F::EPU;
+    if (U <= 8) return launch_one<F, 8, 1, R, MODE, MOE>(c, p, n_slots);
+    if (U <= 16) return launch_one<F, 16, 1, R, MODE, MOE>(c, p, n_slots);
+    if (U <= 32) return launch_one<F, 32, 1, R, MODE, MOE>(c, p, n_slots);
+    if (U <= 64) return launch_one<F, 64, 1, R, MODE, MOE>(c, p, n_slots);
+    if (U <= 128) return launch_one<F, 64, 2, R, MODE, MOE>(c, p, n_slots);
+    if (U <= 192) return launch_one<F, 64, 3, R, MODE, MOE>(c, p, n_slots);
+    if (U <= 256) return launch_one<F, 64, 4, R, MODE, MOE>(c, p, n_slots);
+    if (U <= 512) return launch_one<F, 64, 8, R, MODE, MOE>(c, p, n_slots);
+    if (U <= 1024) return launch_one<F, 64, 16, R, MODE, MOE>(c, p, n_slots);
+    return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "K=%u too large", p.K);
+}
+
+template <int MODE, bool MOE>
+static int launch_dmmv(zh_ctx *c, uint32_t qtype, const DmmvP &p, uint32_t n_slots) {
+    switch (qtype) {
+    case ZH_Q4_K: return launch_fmt<FmtQ4K, MODE, MOE>(c, p, n_slots);
+    case ZH_Q6_K: return launch_fmt<FmtQ6K, MODE, MOE>(c, p, n_slots);
+    case ZH_Q8_0: return launch_fmt<FmtQ80, MODE, MOE>(c, p, n_slots);
+    case ZH_MXFP4: return launch_fmt<FmtMXFP4, MODE, MOE>(c, p, n_slots);
+    default: return zh_set_err(c, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "qtype %u has no DMMV kernel", qtype);
+    }
+}
+
+static int check_k(zh_ctx *c, uint32_t qtype, uint32_t K) {
+    switch (qtype) {
+    case ZH_Q4_K: case ZH_Q6_K:
+        if (K % 256) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "K=%u not a multiple of 256", K);
+        return ZH_OK;
+    case ZH_Q8_0:
+        if (K % 64) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "Q8_0 needs K %% 64 == 0 (K=%u)", K);
+        return ZH_OK;
+    case ZH_MXFP4:
+        if (K % 32) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "K=%u not a multiple of 32", K);
+        return ZH_OK;
+    default: return zh_set_err(c, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "qtype %u has no DMMV kernel", qtype);
+    }
+}
+
+int zhk_dmmv(zh_ctx *c, uint32_t qtype, const uint8_t *W, const void *xq, float *y, uint32_t M,
+             uint32_t K, uint32_t acc) {
+    DmmvP p = {};
+    p.W = W; p.W2 = W; p.xq = (const uint8_t *)xq; p.y = y; p.M = M; p.K = K;
+    p.row_bytes = zh_tensor_bytes(qtype, 1, K); p.acc = acc;
+    return launch_dmmv<MODE_PLAIN, false>(c, qtype, p, 1);
+}
+
+int zhk_dmmv_gate_up(zh_ctx *c, uint32_t qtype, const uint8_t *Wg, const uint8_t *Wu, const void *xq,
+                     float *y, uint32_t M, uint32_t K) {
+    DmmvP p = {};
+    p.W = Wg; p.W2 = Wu; p.xq = (const uint8_t *)xq; p.y = y; p.M = M; p.K = K;
+    p.row_bytes = zh_tensor_bytes(qtype, 1, K);
+    return launch_dmmv<MODE_GATE_UP, false>(c, qtype, p, 1);
+}
+
+int zhk_dmmv_moe(zh_ctx *c, uint32_t qtype, const uint8_t *W, uint64_t expert_stride,
+                 const uint32_t *routing, const void *xq, uint64_t xq_slot_stride, float *y, uint32_t M,
+                 uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2) {
+    DmmvP p = {};
+    p.W = W; p.W2 = W2 ? W2 : W; p.xq = (const uint8_t *)xq; p.y = y; p.M = M; p.K = K;
+    p.row_bytes = zh_tensor_bytes(qtype, 1, K);
+    p.routing = routing; p.expert_stride = expert_stride; p.xq_slot_stride = xq_slot_stride;
+    p.y_slot_stride = M;
+    if (gate_up) return launch_dmmv<MODE_GATE_UP, true>(c, qtype, p, n_used);
+    return launch_dmmv<MODE_PLAIN, true>(c, qtype, p, n_used);
+}
+
+// ---------------------------------------------------------------------------
+// C ABI wrappers with argument validation (shapes are checked on the host
+// before any launch so a kernel never sees a shape it does not assume).
+// ---------------------------------------------------------------------------
+static bool in_range(const zh_buf *b, uint64_t off, uint64_t n) { return b && off <= b->size && n <= b->size - off; }
+
+extern "C" int zh_dmmv(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a_off, const zh_buf *x,
+                       uint64_t x_off, zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t acc_mode) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    int rc = check_k(c, qtype, K);
+    if (rc) return rc;
+    if (M == 0 || K == 0) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "empty shape");
+    if (acc_mode > 1) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "acc_mode %u", acc_mode);
+    if (!in_range(W, a_off, zh_tensor_bytes(qtype, M, K)) || !in_range(x, x_off, (uint64_t)K * 4) ||
+        !in_range(y, y_off, (uint64_t)M * 4))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "buffer too small for M=%u K=%u", M, K);
+    if ((a_off & 3) || (x_off & 3) || (y_off & 3))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "offsets must be 4-byte aligned");
+    if (qtype == ZH_Q4_K && (a_off & 15)) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "Q4_K a_off must be 16-byte aligned");
+    void *xq;
+    if ((rc = zh_scratch(c, zh_xq_bytes(K), &xq))) return rc;
+    if ((rc = zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), xq, K, 1, 0))) return rc;
+    return zhk_dmmv(c, qtype, (const uint8_t *)W->ptr + a_off, xq, (float *)((char *)y->ptr + y_off), M, K, acc_mode);
+}
+
+extern "C" int zh_dmmv_fused_gate_up_swiglu(zh_ctx *c, uint32_t qtype, const zh_buf *Wg, uint64_t g_off,
+                                            const zh_buf *Wu, uint64_t u_off, const zh_buf *x, uint64_t x_off,
+                                            zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    int rc = check_k(c, qtype, K);
+    if (rc) return rc;
+    uint64_t wb = zh_tensor_bytes(qtype, M, K);
+    if (M == 0 || !in_range(Wg, g_off, wb) || !in_range(Wu, u_off, wb) || !in_range(x, x_off, (uint64_t)K * 4) ||
+        !in_range(y, y_off, (uint64_t)M * 4))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "buffer too small for M=%u K=%u", M, K);
+    if ((g_off & 15) || (u_off & 15) || (x_off & 3) || (y_off & 3))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "misaligned offsets");
+    void *xq;
+    if ((rc = zh_scratch(c, zh_xq_bytes(K), &xq))) return rc;
+    if ((rc = zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), xq, K, 1, 0))) return rc;
+    return zhk_dmmv_gate_up(c, qtype, (const uint8_t *)Wg->ptr + g_off, (const uint8_t *)Wu->ptr + u_off, xq,
+                            (float *)((char *)y->ptr + y_off), M, K);
+}
+
+extern "C" int zh_dmmv_moe(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t expert_stride,
+                           const zh_buf *routing, const zh_buf *x, uint32_t x_expert_stride, uint64_t x_off,
+                           zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t n_used) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    int rc = check_k(c, qtype, K);
+    if (rc) return rc;
+    if (n_used == 0 || n_used > 64 || M == 0) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "n_used/M");
+    if (!routing || routing->size < (uint64_t)n_used * 4) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "routing");
+    if (expert_stride < zh_tensor_bytes(qtype, M, K) || (expert_stride & 15))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "expert_stride");
+    if (!in_range(x, x_off, ((uint64_t)(n_used - 1) * x_expert_stride + K) * 4) ||
+        !in_range(y, y_off, (uint64_t)n_used * M * 4) || (x_off & 3) || (y_off & 3))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "x/y range");
+    // Expert ids are validated on the host against the weight buffer size.
+    std::vector<uint32_t> ids(n_used);
+    if ((rc = zh_buf_download(c, routing, 0, ids.data(), n_used * 4ull))) return rc;
+    for (uint32_t s = 0; s < n_used; s++)
+        if (!in_range(W, (uint64_t)ids[s] * expert_stride, zh_tensor_bytes(qtype, M, K)))
+            return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "expert id %u out of range", ids[s]);
+    void *xq;
+    uint64_t xqs = zh_xq_bytes(K);
+    if ((rc = zh_scratch(c, xqs * n_used, &xq))) return rc;
+    if ((rc = zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), xq, K, n_used, x_expert_stride)))
+        return rc;
+    return zhk_dmmv_moe(c, qtype, (const uint8_t *)W->ptr, expert_stride, (const uint32_t *)routing->ptr, xq, xqs,
+                        (float *)((char *)y->ptr + y_off), M, K, n_used, 0, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// Bit-exact dequantisation (dequantRow, forward.zig:242-465): one thread per
+// output element, every product and difference rounded separately (_rn
+// intrinsics), matching Zig's unfused f32 arithmetic.
+// ---------------------------------------------------------------------------
+ZH_DEV uint32_t blk_elems(uint32_t t) { return (t == ZH_Q4_K || t == ZH_Q6_K) ? 256 : (t == ZH_Q8_0 || t == ZH_MXFP4) ? 32 : 1; }
+ZH_DEV uint32_t blk_bytes(uint32_t t) {
+    return t == ZH_Q4_K ? 144 : t == ZH_Q6_K ? 210 : t == ZH_Q8_0 ? 34 : t == ZH_MXFP4 ? 17 : t == ZH_F16 ? 2 : 4;
+}
+
+__global__ void k_dequant(uint32_t qtype, const uint8_t *__restrict__ W, uint32_t row0, uint32_t n_rows,
+                          uint32_t K, float *__restrict__ out, const uint32_t *row_from_dev, uint32_t clamp_rows) {
+    uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t rr = blockIdx.y;
+    if (e >= K || rr >= n_rows) return;
+    uint32_t row = row0 + rr;
+    if (row_from_dev) {
+        row = row_from_dev[0] + rr;
+        if (row >= clamp_rows) row = clamp_rows - 1;  // embedToken safe_id clamp (forward.zig:4271)
+    }
+    uint64_t rb = (uint64_t)(K / blk_elems(qtype)) * blk_bytes(qtype);
+    const uint8_t *r = W + (uint64_t)row * rb;
+    float v = 0.f;
+    switch (qtype) {
+    case ZH_Q4_K: {
+        const uint8_t *b = r + (e / 256) * 144;
+        uint32_t w = e % 256, p = w / 64, hi = (w / 32) & 1, l = w % 32, j = 2 * p + hi;
+        const uint8_t *s = b + 4;
+        uint32_t sc, m;
+        if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
+        else { sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+        uint32_t q = (b[16 + 32 * p + l] >> (4 * hi)) & 0xF;
+        float d = h2f(b[0] | (b[1] << 8)), dmin = h2f(b[2] | (b[3] << 8));
+        v = __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)q), __fmul_rn(dmin, (float)m));
+        break;
+    }
+    case ZH_Q6_K: {
+        const uint8_t *b = r + (e / 256) * 210;
+        uint32_t w = e % 256, h = w / 128, g = (w % 128) / 32, l = w % 32;
+        uint32_t qlb = b[64 * h + l + 32 * (g & 1)];
+        uint32_t lo = (g >> 1) ? (qlb >> 4) : (qlb & 0xF);
+        uint32_t hb = (b[128 + 32 * h + l] >> (2 * g)) & 3;
+        int q = (int)(lo | (hb << 4)) - 32;
+        float sc = (float)(int8_t)b[192 + 8 * h + l / 16 + 2 * g];
+        float d = h2f(b[208] | (b[209] << 8));
+        v = __fmul_rn(__fmul_rn(d, sc), (float)q);
+        break;
+    }
+    case ZH_Q8_0: {
+        const uint8_t *b = r + (e / 32) * 34;
+        v = __fmul_rn((float)(int8_t)b[2 + e % 32], h2f(b[0] | (b[1] << 8)));
+        break;
+    }
+    case ZH_MXFP4: {
+        const uint8_t *b = r + (e / 32) * 17;
+        uint32_t j = e % 32, code = j < 16 ? (b[1 + j] & 0xF) : (b[1 + j - 16] >> 4);
+        const float lut[16] = {0.f, .5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f, -0.f, -.5f, -1.f, -1.5f, -2.f, -3.f, -4.f, -6.f};
+        uint32_t ex = b[0];
+        float d = __uint_as_float(ex == 0 ? 0x00400000u : (ex << 23));
+        v = __fmul_rn(d, lut[code]);
+        break;
+    }
+    case ZH_F16: v = h2f(((const uint16_t *)r)[e]); break;
+    case ZH_F32: v = ((const float *)r)[e]; break;
+    }
+    out[(size_t)rr * K + e] = v;
+}
+
+int zhk_dequant_rows(zh_ctx *c, uint32_t qtype, const uint8_t *W, uint32_t row0, uint32_t n_rows, uint32_t K,
+                     float *out, const uint32_t *row_from_dev, uint32_t clamp_rows) {
+    hipLaunchKernelGGL(k_dequant, dim3((K + 255) / 256, n_rows), dim3(256), 0, c->stream, qtype, W, row0, n_rows,
+                       K, out, row_from_dev, clamp_rows);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+extern "C" int zh_dequant_rows(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a_off, uint32_t row0,
+                               uint32_t n_rows, uint32_t K, zh_buf *out, uint64_t out_off) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    if (zh_bytes_per_block(qtype) == 0) return zh_set_err(c, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "qtype %u", qtype);
+    if (K % zh_block_size(qtype) || n_rows == 0) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "shape");
+    if (!in_range(W, a_off, zh_tensor_bytes(qtype, (uint64_t)row0 + n_rows, K)) ||
+        !in_range(out, out_off, (uint64_t)n_rows * K * 4) || (out_off & 3))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "range");
+    return zhk_dequant_rows(c, qtype, (const uint8_t *)W->ptr + a_off, row0, n_rows, K,
+                            (float *)((char *)out->ptr + out_off), nullptr, 0);
+}

@@ -1,0 +1,477 @@
+// zh_engine.hip — the decode-loop engine: InferenceEngine's init /
+// decodeStep / sampleGreedy / generate (src/compute/forward.zig:1226,
+// :4299-7865, :10338, :10983-11192) on one MI355X.
+//
+// A token step is a fixed sequence of kernel launches whose every varying
+// input (token id, position, generated-token slot) lives in a small device
+// state block, so one step is captured once into a hipGraph and replayed:
+// greedy decode feeds each argmax back on the device with no host round trip
+// (the reference does one submitAndWait + 4-byte readback per token).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <vector>
+
+#include "zh_device.h"
+#include "zh_internal.h"
+
+// Tensor stream ids (shared with oracle/zinc_oracle.c).
+enum : uint64_t { S_TOKEN_EMBD = 1, S_OUTPUT_NORM = 2, S_OUTPUT = 3 };
+enum { K_ATTN_NORM = 1, K_WQ, K_WK, K_WV, K_WO, K_Q_NORM, K_K_NORM, K_FFN_NORM, K_GATE, K_UP, K_DOWN, K_ROUTER,
+       K_EXP_GATE, K_EXP_UP, K_EXP_DOWN };
+static inline uint64_t S_LAYER(uint32_t l, int kind) { return ((uint64_t)(l + 1) << 8) | (uint64_t)kind; }
+static inline uint64_t S_KV(uint32_t l, uint32_t which) { return 0x100000ull + 2ull * l + which; }
+
+// Device state words.
+enum { ST_STEP = 0, ST_NPROMPT = 2, ST_TOKEN_OUT = 3, ST_POS = 5, ST_TOKEN_IN = 6, ST_GEN = 7, ST_WORDS = 16 };
+constexpr uint32_t MAX_PROMPT = 8192;
+constexpr uint32_t MAX_GEN = 65536;
+
+struct Tensor {
+    uint64_t off = 0, bytes = 0;
+    uint32_t type = 0;
+    uint64_t rows = 0, cols = 0;
+};
+
+struct Layer {
+    Tensor attn_norm, wq, wk, wv, wo, q_norm, k_norm, ffn_norm, gate, up, down, router, egate, eup, edown;
+    uint16_t *kc = nullptr, *vc = nullptr;
+};
+
+struct zh_engine {
+    zh_ctx *ctx = nullptr;
+    zh_model_config c{};
+    uint8_t *arena = nullptr;  // all weights
+    uint64_t arena_bytes = 0;
+    std::map<uint64_t, Tensor> tensors;
+    Tensor embd, out_norm, lm;
+    std::vector<Layer> L;
+    uint16_t *kv = nullptr;  // all caches
+    uint32_t *pages = nullptr, n_pages = 0;
+    float *inv_freq = nullptr;
+    // activations
+    float *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+    float *s = nullptr, *logits = nullptr, *rl = nullptr, *edown_out = nullptr, *fd_part = nullptr;
+    uint8_t *xq_h = nullptr, *xq_q = nullptr, *xq_f = nullptr;
+    uint32_t *routing = nullptr, *am_part = nullptr, *st = nullptr, *prompt = nullptr, *ring = nullptr;
+    void *act_arena = nullptr;
+    hipGraphExec_t g_out = nullptr, g_noout = nullptr;
+    bool have_logits = false;
+};
+
+#define EHIP(e, call) ZH_HIP((e)->ctx, call)
+#define ERC(x)                 \
+    do {                       \
+        int rc_ = (x);         \
+        if (rc_) return rc_;   \
+    } while (0)
+
+static uint64_t align256(uint64_t x) { return (x + 255) & ~255ull; }
+
+// ---------------------------------------------------------------------------
+// Small kernels owned by the engine.
+// ---------------------------------------------------------------------------
+__global__ void k_advance(uint32_t *st, const uint32_t *prompt) {
+    // End of a step: count the generated token, move to the next position and
+    // pick the next input token (prompt while it lasts, else the argmax).
+    uint32_t s = st[ST_STEP], np = st[ST_NPROMPT];
+    if (s + 1 >= np) st[ST_GEN] += 1;
+    s += 1;
+    st[ST_STEP] = s;
+    st[ST_POS] += 1;
+    st[ST_TOKEN_IN] = (s < np) ? prompt[s] : st[ST_TOKEN_OUT];
+}
+
+// Seeded N(0,1) fp16 values for logical tokens [0, n) of one layer, written
+// into the head-major cache; counter = t*kv_dim + h*head_dim + d, as the
+// oracle's token-major fill.
+__global__ void k_prefill_kv(uint16_t *cache, uint32_t nkv, uint32_t cache_tokens, uint32_t hd, uint32_t n,
+                             uint64_t key) {
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t total = (uint64_t)n * nkv * hd;
+    if (i >= total) return;
+    uint32_t d = i % hd;
+    uint64_t r = i / hd;
+    uint32_t h = r % nkv;
+    uint32_t t = (uint32_t)(r / nkv);
+    uint64_t z = key + (i + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z = z ^ (z >> 31);
+    int sm = (int)(z & 0xFFFF) + (int)((z >> 16) & 0xFFFF) + (int)((z >> 32) & 0xFFFF) + (int)((z >> 48) & 0xFFFF) -
+             131070;
+    cache[((size_t)h * cache_tokens + t) * hd + d] = f2h_rn(__fmul_rn((float)sm, 2.6429573e-05f));
+}
+
+__global__ void k_gather_kv(const uint16_t *cache, uint32_t nkv, uint32_t cache_tokens, uint32_t hd,
+                            const uint32_t *pages, uint32_t t0, uint32_t n, uint16_t *dst) {
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * nkv * hd) return;
+    uint32_t d = i % hd;
+    uint64_t r = i / hd;
+    uint32_t h = r % nkv, t = t0 + (uint32_t)(r / nkv);
+    uint32_t phys = pages[t / 16] * 16 + t % 16;
+    dst[i] = cache[((size_t)h * cache_tokens + phys) * hd + d];
+}
+
+__global__ void k_fill_pages(uint32_t *pages, uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) pages[i] = i;
+}
+
+static uint64_t host_key(uint64_t seed, uint64_t stream) {
+    uint64_t z = seed ^ (stream * 0xD1B54A32D192ED03ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// ---------------------------------------------------------------------------
+// init
+// ---------------------------------------------------------------------------
+static bool dmmv_type_ok(uint32_t t) { return t == ZH_Q4_K || t == ZH_Q6_K || t == ZH_Q8_0 || t == ZH_MXFP4; }
+
+extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engine **out) {
+    if (!ctx || !cfg || !out) return ZH_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    const zh_model_config &c = *cfg;
+    if (c.n_layers == 0 || c.hidden % 256 || c.head_dim != 128 || c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads ||
+        c.n_heads / c.n_kv_heads > 8 || c.vocab == 0 || c.max_ctx == 0 || c.max_ctx % 16)
+        return zh_set_err(ctx, ZH_ERR_INVALID_ARGUMENT, "unsupported model shape");
+    if (c.n_experts == 0 && (c.ffn == 0 || c.ffn % 256))
+        return zh_set_err(ctx, ZH_ERR_INVALID_ARGUMENT, "ffn must be a positive multiple of 256");
+    if (c.n_experts && (c.n_experts > 256 || c.n_experts_used == 0 || c.n_experts_used > 16 ||
+                        c.n_experts_used > c.n_experts || c.expert_ffn % 256))
+        return zh_set_err(ctx, ZH_ERR_INVALID_ARGUMENT, "unsupported MoE shape");
+    uint32_t types[] = {c.type_attn, c.type_ffn_gate_up, c.type_ffn_down, c.type_lm_head, c.type_embd};
+    for (uint32_t t : types)
+        if (!dmmv_type_ok(t)) return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "type %u", t);
+    if (c.n_experts && !dmmv_type_ok(c.type_router)) return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "router");
+
+    zh_engine *e = new zh_engine();
+    e->ctx = ctx;
+    e->c = c;
+    const uint32_t H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    // --- weight layout
+    uint64_t off = 0;
+    auto add = [&](uint64_t stream, uint32_t type, uint64_t rows, uint64_t cols) -> Tensor {
+        Tensor t;
+        t.type = type;
+        t.rows = rows;
+        t.cols = cols;
+        t.bytes = (type == ZH_F32) ? rows * cols * 4 : zh_tensor_bytes(type, rows, cols);
+        t.off = off;
+        off = align256(off + t.bytes);
+        e->tensors[stream] = t;
+        return t;
+    };
+    e->embd = add(S_TOKEN_EMBD, c.type_embd, c.vocab, H);
+    e->out_norm = add(S_OUTPUT_NORM, ZH_F32, 1, H);
+    e->lm = add(S_OUTPUT, c.type_lm_head, c.vocab, H);
+    e->L.resize(c.n_layers);
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        Layer &y = e->L[l];
+        y.attn_norm = add(S_LAYER(l, K_ATTN_NORM), ZH_F32, 1, H);
+        y.wq = add(S_LAYER(l, K_WQ), c.type_attn, qd, H);
+        y.wk = add(S_LAYER(l, K_WK), c.type_attn, kvd, H);
+        y.wv = add(S_LAYER(l, K_WV), c.type_attn, kvd, H);
+        y.wo = add(S_LAYER(l, K_WO), c.type_attn, H, qd);
+        y.q_norm = add(S_LAYER(l, K_Q_NORM), ZH_F32, 1, hd);
+        y.k_norm = add(S_LAYER(l, K_K_NORM), ZH_F32, 1, hd);
+        y.ffn_norm = add(S_LAYER(l, K_FFN_NORM), ZH_F32, 1, H);
+        if (c.n_experts == 0) {
+            y.gate = add(S_LAYER(l, K_GATE), c.type_ffn_gate_up, c.ffn, H);
+            y.up = add(S_LAYER(l, K_UP), c.type_ffn_gate_up, c.ffn, H);
+            y.down = add(S_LAYER(l, K_DOWN), c.type_ffn_down, H, c.ffn);
+        } else {
+            y.router = add(S_LAYER(l, K_ROUTER), c.type_router, c.n_experts, H);
+            y.egate = add(S_LAYER(l, K_EXP_GATE), c.type_ffn_gate_up, (uint64_t)c.n_experts * c.expert_ffn, H);
+            y.eup = add(S_LAYER(l, K_EXP_UP), c.type_ffn_gate_up, (uint64_t)c.n_experts * c.expert_ffn, H);
+            y.edown = add(S_LAYER(l, K_EXP_DOWN), c.type_ffn_down, (uint64_t)c.n_experts * H, c.expert_ffn);
+        }
+    }
+    e->arena_bytes = off + 256;
+    hipError_t he = hipMalloc((void **)&e->arena, e->arena_bytes);
+    if (he != hipSuccess) {
+        delete e;
+        return zh_set_err(ctx, ZH_ERR_OUT_OF_MEMORY, "weights (%llu B): %s", (unsigned long long)off, hipGetErrorString(he));
+    }
+    // --- synthetic weights (same streams as the oracle)
+    for (auto &kv : e->tensors) {
+        const Tensor &t = kv.second;
+        int rc;
+        uint64_t kind = kv.first & 0xFF;
+        bool is_norm = kv.first == S_OUTPUT_NORM || (kv.first > 0xFF && (kind == K_ATTN_NORM || kind == K_Q_NORM ||
+                                                                         kind == K_K_NORM || kind == K_FFN_NORM));
+        if (is_norm) rc = zhk_synth_vector(ctx, e->arena + t.off, 2, t.rows * t.cols, 1.f, c.seed, kv.first);
+        else rc = zhk_synth_tensor(ctx, e->arena + t.off, t.type, t.rows, t.cols, c.seed, kv.first);
+        if (rc) { zh_engine_destroy(e); return rc; }
+    }
+    // --- KV cache [layer][K|V][nkv][max_ctx][hd] fp16 and identity page table
+    uint64_t per = (uint64_t)c.n_kv_heads * c.max_ctx * hd;
+    he = hipMalloc((void **)&e->kv, per * 2 * 2 * c.n_layers + 256);
+    if (he != hipSuccess) { zh_engine_destroy(e); return zh_set_err(ctx, ZH_ERR_OUT_OF_MEMORY, "kv cache"); }
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        e->L[l].kc = e->kv + per * (2 * l);
+        e->L[l].vc = e->kv + per * (2 * l + 1);
+    }
+    e->n_pages = c.max_ctx / 16;
+    // --- activations in one arena
+    uint32_t F = c.n_experts ? c.expert_ffn * c.n_experts_used : c.ffn;
+    uint32_t XK = H > qd ? H : qd;
+    struct { void **p; uint64_t bytes; } acts[] = {
+        {(void **)&e->hidden, 4ull * H}, {(void **)&e->norm, 4ull * XK}, {(void **)&e->q, 4ull * qd},
+        {(void **)&e->k, 4ull * kvd}, {(void **)&e->v, 4ull * kvd}, {(void **)&e->attn, 4ull * qd},
+        {(void **)&e->s, 4ull * F}, {(void **)&e->logits, 4ull * c.vocab}, {(void **)&e->rl, 4ull * 256},
+        {(void **)&e->edown_out, 4ull * H * (c.n_experts_used ? c.n_experts_used : 1)},
+        {(void **)&e->fd_part, zhk_flash_decode_partials_bytes(c.n_heads, hd, c.max_ctx)},
+        {(void **)&e->xq_h, zh_xq_bytes(H)}, {(void **)&e->xq_q, zh_xq_bytes(qd)},
+        {(void **)&e->xq_f, zh_xq_bytes(c.n_experts ? c.expert_ffn : c.ffn) * (c.n_experts_used ? c.n_experts_used : 1)},
+        {(void **)&e->routing, 8ull * 16}, {(void **)&e->am_part, 8ull * 256}, {(void **)&e->st, 4ull * ST_WORDS},
+        {(void **)&e->prompt, 4ull * MAX_PROMPT}, {(void **)&e->ring, 4ull * MAX_GEN}, {(void **)&e->pages, 4ull * e->n_pages},
+        {(void **)&e->inv_freq, 4ull * hd / 2},
+    };
+    uint64_t aoff = 0;
+    for (auto &a : acts) aoff = align256(aoff + a.bytes);
+    he = hipMalloc(&e->act_arena, aoff + 256);
+    if (he != hipSuccess) { zh_engine_destroy(e); return zh_set_err(ctx, ZH_ERR_OUT_OF_MEMORY, "activations"); }
+    aoff = 0;
+    for (auto &a : acts) {
+        *a.p = (char *)e->act_arena + aoff;
+        aoff = align256(aoff + a.bytes);
+    }
+    hipError_t me = hipMemsetAsync(e->act_arena, 0, aoff, ctx->stream);
+    if (me != hipSuccess) { zh_engine_destroy(e); return ZH_ERR_HIP; }
+    me = hipMemsetAsync(e->kv, 0, per * 4 * c.n_layers, ctx->stream);
+    if (me != hipSuccess) { zh_engine_destroy(e); return ZH_ERR_HIP; }
+    hipLaunchKernelGGL(k_fill_pages, dim3((e->n_pages + 255) / 256), dim3(256), 0, ctx->stream, e->pages, e->n_pages);
+    // RoPE inverse frequencies: 1/base^(2k/rope_dim) on the host in f32
+    // (forward.zig:1495-1500).
+    std::vector<float> inv(hd / 2);
+    for (uint32_t k = 0; k < hd / 2; k++) inv[k] = 1.0f / powf(c.rope_base, (float)(2 * k) / (float)hd);
+    me = hipMemcpyAsync(e->inv_freq, inv.data(), 4ull * hd / 2, hipMemcpyHostToDevice, ctx->stream);
+    if (me != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        zh_engine_destroy(e);
+        return zh_set_err(ctx, ZH_ERR_HIP, "engine init");
+    }
+    *out = e;
+    return ZH_OK;
+}
+
+extern "C" void zh_engine_destroy(zh_engine *e) {
+    if (!e) return;
+    hipStreamSynchronize(e->ctx->stream);
+    if (e->g_out) hipGraphExecDestroy(e->g_out);
+    if (e->g_noout) hipGraphExecDestroy(e->g_noout);
+    if (e->arena) hipFree(e->arena);
+    if (e->kv) hipFree(e->kv);
+    if (e->act_arena) hipFree(e->act_arena);
+    delete e;
+}
+
+extern "C" int zh_engine_prefill_kv_random(zh_engine *e, uint32_t n, uint64_t seed) {
+    if (!e) return ZH_ERR_INVALID_ARGUMENT;
+    if (n > e->c.max_ctx) return zh_set_err(e->ctx, ZH_ERR_CONTEXT_LENGTH_EXCEEDED, "prefill %u > max_ctx", n);
+    uint32_t nkv = e->c.n_kv_heads, hd = e->c.head_dim;
+    uint64_t total = (uint64_t)n * nkv * hd;
+    if (total == 0) return ZH_OK;
+    for (uint32_t l = 0; l < e->c.n_layers; l++)
+        for (uint32_t w = 0; w < 2; w++) {
+            hipLaunchKernelGGL(k_prefill_kv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, e->ctx->stream,
+                               w ? e->L[l].vc : e->L[l].kc, nkv, e->c.max_ctx, hd, n, host_key(seed, S_KV(l, w)));
+            ZH_LAUNCH_CHECK(e->ctx);
+        }
+    return ZH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// One token step (the body of decodeStep, forward.zig:4376-7754).
+// ---------------------------------------------------------------------------
+static int record_step(zh_engine *e, bool collect) {
+    zh_ctx *c = e->ctx;
+    const zh_model_config &m = e->c;
+    const uint32_t H = m.hidden, hd = m.head_dim, qd = m.n_heads * hd, kvd = m.n_kv_heads * hd;
+    const uint8_t *A = e->arena;
+    auto W = [&](const Tensor &t) { return A + t.off; };
+    auto Wf = [&](const Tensor &t) { return (const float *)(A + t.off); };
+    zh_pos_src pos{0, e->st + ST_POS}, seq{1, e->st + ST_POS};
+    const float scale = 1.0f / sqrtf((float)hd);
+    // embedToken (forward.zig:4255-4290), on the device.
+    ERC(zhk_dequant_rows(c, m.type_embd, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
+    for (uint32_t l = 0; l < m.n_layers; l++) {
+        const Layer &y = e->L[l];
+        ERC(zhk_rms_norm(c, e->hidden, Wf(y.attn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
+        ERC(zhk_dmmv(c, m.type_attn, W(y.wq), e->xq_h, e->q, qd, H, 0));
+        ERC(zhk_dmmv(c, m.type_attn, W(y.wk), e->xq_h, e->k, kvd, H, 0));
+        ERC(zhk_dmmv(c, m.type_attn, W(y.wv), e->xq_h, e->v, kvd, H, 0));
+        ERC(zhk_qk_norm_rope_kv(c, e->q, Wf(y.q_norm), e->k, Wf(y.k_norm), e->v, e->inv_freq, y.kc, y.vc, e->pages,
+                                e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd, pos, m.eps));
+        ERC(zhk_flash_decode(c, e->q, y.kc, y.vc, e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads,
+                             m.n_kv_heads, hd, seq, m.max_ctx, scale, e->fd_part));
+        ERC(zhk_dmmv(c, m.type_attn, W(y.wo), e->xq_q, e->hidden, H, qd, 1));
+        ERC(zhk_rms_norm(c, e->hidden, Wf(y.ffn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
+        if (m.n_experts == 0) {
+            ERC(zhk_dmmv_gate_up(c, m.type_ffn_gate_up, W(y.gate), W(y.up), e->xq_h, e->s, m.ffn, H));
+            ERC(zhk_quantize_xq(c, e->s, e->xq_f, m.ffn, 1, 0));
+            ERC(zhk_dmmv(c, m.type_ffn_down, W(y.down), e->xq_f, e->hidden, H, m.ffn, 1));
+        } else {
+            const uint32_t F = m.expert_ffn, k = m.n_experts_used;
+            ERC(zhk_dmmv(c, m.type_router, W(y.router), e->xq_h, e->rl, m.n_experts, H, 0));
+            ERC(zhk_softmax_topk(c, e->rl, m.n_experts, k, e->routing));
+            ERC(zhk_dmmv_moe(c, m.type_ffn_gate_up, W(y.egate), zh_tensor_bytes(m.type_ffn_gate_up, F, H), e->routing,
+                             e->xq_h, 0, e->s, F, H, k, 1, W(y.eup)));
+            ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
+            ERC(zhk_dmmv_moe(c, m.type_ffn_down, W(y.edown), zh_tensor_bytes(m.type_ffn_down, H, F), e->routing,
+                             e->xq_f, zh_xq_bytes(F), e->edown_out, H, F, k, 0, nullptr));
+            ERC(zhk_moe_weighted_acc(c, e->hidden, e->edown_out, e->routing, H, k, H));
+        }
+    }
+    if (collect) {
+        ERC(zhk_rms_norm(c, e->hidden, Wf(e->out_norm), H, e->norm, e->xq_h, H, 1, m.eps));
+        ERC(zhk_dmmv(c, m.type_lm_head, W(e->lm), e->xq_h, e->logits, m.vocab, H, 0));
+        ERC(zhk_argmax(c, e->logits, m.vocab, e->st + ST_TOKEN_OUT, e->am_part, e->ring, e->st + ST_GEN));
+    }
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, c->stream, e->st, (const uint32_t *)e->prompt);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+static int ensure_graphs(zh_engine *e) {
+    if (e->g_out && e->g_noout) return ZH_OK;
+    zh_ctx *c = e->ctx;
+    for (int collect = 0; collect < 2; collect++) {
+        hipGraph_t g;
+        EHIP(e, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        int rc = record_step(e, collect != 0);
+        hipError_t ce = hipStreamEndCapture(c->stream, &g);
+        if (rc) return rc;
+        if (ce != hipSuccess) return zh_set_err(c, ZH_ERR_HIP, "capture: %s", hipGetErrorString(ce));
+        hipGraphExec_t x;
+        ce = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (ce != hipSuccess) return zh_set_err(c, ZH_ERR_HIP, "instantiate: %s", hipGetErrorString(ce));
+        (collect ? e->g_out : e->g_noout) = x;
+    }
+    return ZH_OK;
+}
+
+static int set_state(zh_engine *e, uint32_t n_prompt, uint32_t pos, uint32_t first_token) {
+    uint32_t st[ST_WORDS] = {0};
+    st[ST_STEP] = 0;
+    st[ST_NPROMPT] = n_prompt;
+    st[ST_POS] = pos;
+    st[ST_TOKEN_IN] = first_token;
+    st[ST_GEN] = 0;
+    EHIP(e, hipMemcpyAsync(e->st, st, sizeof st, hipMemcpyHostToDevice, e->ctx->stream));
+    return ZH_OK;
+}
+
+static int run_step(zh_engine *e, bool collect) {
+    if (getenv("ZH_NO_GRAPH")) return record_step(e, collect);
+    ERC(ensure_graphs(e));
+    EHIP(e, hipGraphLaunch(collect ? e->g_out : e->g_noout, e->ctx->stream));
+    return ZH_OK;
+}
+
+extern "C" int zh_engine_decode_step(zh_engine *e, uint32_t token, uint32_t position, int collect) {
+    if (!e) return ZH_ERR_INVALID_ARGUMENT;
+    if (position >= e->c.max_ctx)
+        return zh_set_err(e->ctx, ZH_ERR_CONTEXT_LENGTH_EXCEEDED, "position %u >= %u", position, e->c.max_ctx);
+    ERC(set_state(e, 1, position, token));
+    ERC(run_step(e, collect != 0));
+    if (collect) e->have_logits = true;
+    return ZH_OK;
+}
+
+extern "C" int zh_engine_sample_greedy(zh_engine *e, uint32_t *token) {
+    if (!e || !token) return ZH_ERR_INVALID_ARGUMENT;
+    EHIP(e, hipMemcpyAsync(token, e->st + ST_TOKEN_OUT, 4, hipMemcpyDeviceToHost, e->ctx->stream));
+    EHIP(e, hipStreamSynchronize(e->ctx->stream));
+    return ZH_OK;
+}
+
+extern "C" int zh_engine_generate(zh_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t start_pos,
+                                  uint32_t max_tokens, uint32_t eos, uint32_t *out_tokens, uint32_t *n_out) {
+    if (!e || !prompt || n_prompt == 0 || !out_tokens || !n_out) return ZH_ERR_INVALID_ARGUMENT;
+    *n_out = 0;
+    if (n_prompt > MAX_PROMPT || max_tokens > MAX_GEN) return zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "too long");
+    if ((uint64_t)start_pos + n_prompt + max_tokens > e->c.max_ctx + 1ull)
+        return zh_set_err(e->ctx, ZH_ERR_CONTEXT_LENGTH_EXCEEDED, "context %u + %u + %u > %u", start_pos, n_prompt,
+                          max_tokens, e->c.max_ctx);
+    if (max_tokens == 0) return ZH_OK;
+    EHIP(e, hipMemcpyAsync(e->prompt, prompt, 4ull * n_prompt, hipMemcpyHostToDevice, e->ctx->stream));
+    ERC(set_state(e, n_prompt, start_pos, prompt[0]));
+    for (uint32_t i = 0; i + 1 < n_prompt; i++) ERC(run_step(e, false));
+    for (uint32_t i = 0; i < max_tokens; i++) ERC(run_step(e, true));
+    EHIP(e, hipMemcpyAsync(out_tokens, e->ring, 4ull * max_tokens, hipMemcpyDeviceToHost, e->ctx->stream));
+    EHIP(e, hipStreamSynchronize(e->ctx->stream));
+    e->have_logits = true;
+    uint32_t n = max_tokens;
+    if (eos != 0xFFFFFFFFu)
+        for (uint32_t i = 0; i < max_tokens; i++)
+            if (out_tokens[i] == eos) { n = i + 1; break; }
+    *n_out = n;
+    return ZH_OK;
+}
+
+extern "C" int zh_engine_logits(zh_engine *e, float *dst) {
+    if (!e || !dst) return ZH_ERR_INVALID_ARGUMENT;
+    EHIP(e, hipMemcpyAsync(dst, e->logits, 4ull * e->c.vocab, hipMemcpyDeviceToHost, e->ctx->stream));
+    EHIP(e, hipStreamSynchronize(e->ctx->stream));
+    return ZH_OK;
+}
+extern "C" int zh_engine_hidden(zh_engine *e, float *dst) {
+    if (!e || !dst) return ZH_ERR_INVALID_ARGUMENT;
+    EHIP(e, hipMemcpyAsync(dst, e->hidden, 4ull * e->c.hidden, hipMemcpyDeviceToHost, e->ctx->stream));
+    EHIP(e, hipStreamSynchronize(e->ctx->stream));
+    return ZH_OK;
+}
+
+extern "C" int zh_engine_tensor(zh_engine *e, uint64_t stream, zh_buf **buf, uint64_t *offset, uint64_t *bytes) {
+    if (!e || !buf || !offset || !bytes) return ZH_ERR_INVALID_ARGUMENT;
+    auto it = e->tensors.find(stream);
+    if (it == e->tensors.end()) return zh_set_err(e->ctx, ZH_ERR_TENSOR_NOT_FOUND, "stream %llu", (unsigned long long)stream);
+    static thread_local zh_buf view;
+    view.ptr = e->arena;
+    view.size = e->arena_bytes;
+    *buf = &view;
+    *offset = it->second.off;
+    *bytes = it->second.bytes;
+    return ZH_OK;
+}
+
+extern "C" int zh_engine_read_kv(zh_engine *e, uint32_t layer, uint32_t which, uint32_t t0, uint32_t n, uint16_t *dst) {
+    if (!e || !dst || layer >= e->c.n_layers || which > 1) return ZH_ERR_INVALID_ARGUMENT;
+    if ((uint64_t)t0 + n > e->c.max_ctx) return zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "kv range");
+    if (n == 0) return ZH_OK;
+    uint32_t nkv = e->c.n_kv_heads, hd = e->c.head_dim;
+    uint64_t cnt = (uint64_t)n * nkv * hd;
+    void *scr;
+    ERC(zh_scratch(e->ctx, cnt * 2, &scr));
+    hipLaunchKernelGGL(k_gather_kv, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, e->ctx->stream,
+                       (const uint16_t *)(which ? e->L[layer].vc : e->L[layer].kc), nkv, e->c.max_ctx, hd,
+                       (const uint32_t *)e->pages, t0, n, (uint16_t *)scr);
+    ZH_LAUNCH_CHECK(e->ctx);
+    EHIP(e, hipMemcpyAsync(dst, scr, cnt * 2, hipMemcpyDeviceToHost, e->ctx->stream));
+    EHIP(e, hipStreamSynchronize(e->ctx->stream));
+    return ZH_OK;
+}
+
+extern "C" uint64_t zh_engine_bytes_per_token(zh_engine *e, uint32_t Lctx) {
+    if (!e) return 0;
+    const zh_model_config &c = e->c;
+    uint64_t b = e->lm.bytes + e->out_norm.bytes + zh_tensor_bytes(c.type_embd, 1, c.hidden);
+    for (const Layer &y : e->L) {
+        b += y.attn_norm.bytes + y.wq.bytes + y.wk.bytes + y.wv.bytes + y.wo.bytes + y.q_norm.bytes + y.k_norm.bytes +
+             y.ffn_norm.bytes;
+        if (c.n_experts == 0) b += y.gate.bytes + y.up.bytes + y.down.bytes;
+        else
+            b += y.router.bytes + (uint64_t)c.n_experts_used *
+                                      (zh_tensor_bytes(c.type_ffn_gate_up, c.expert_ffn, c.hidden) * 2 +
+                                       zh_tensor_bytes(c.type_ffn_down, c.hidden, c.expert_ffn));
+        b += 2ull * c.n_kv_heads * c.head_dim * 2ull * Lctx;  // fp16 K and V
+    }
+    return b;
+}

@@ -1,0 +1,96 @@
+// zh_internal.h — host-side internals shared by the libzinc_hip.so sources.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/zinc_hip.h"
+
+struct zh_buf {
+    void *ptr;
+    uint64_t size;
+};
+
+struct zh_ctx {
+    int device = 0;
+    int cu_count = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev[64] = {};
+    std::string err;
+    // Stream-ordered scratch for zh_dmmv's activation quantisation.
+    void *scratch = nullptr;
+    uint64_t scratch_size = 0;
+};
+
+int zh_set_err(zh_ctx *ctx, int code, const char *fmt, ...);
+#define ZH_HIP(ctx, call)                                                                    \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return zh_set_err((ctx), ZH_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+#define ZH_LAUNCH_CHECK(ctx) ZH_HIP(ctx, hipGetLastError())
+
+// Scratch (grows; stream ordered, so reuse across sequential calls is safe).
+int zh_scratch(zh_ctx *ctx, uint64_t bytes, void **out);
+
+static inline uint32_t zh_block_size(uint32_t t) {
+    switch (t) {
+    case ZH_Q8_0: case ZH_MXFP4: return 32;
+    case ZH_Q4_K: case ZH_Q6_K: return 256;
+    default: return 1;
+    }
+}
+static inline uint32_t zh_bytes_per_block(uint32_t t) {
+    switch (t) {
+    case ZH_F32: return 4;
+    case ZH_F16: return 2;
+    case ZH_Q8_0: return 34;
+    case ZH_MXFP4: return 17;
+    case ZH_Q4_K: return 144;
+    case ZH_Q6_K: return 210;
+    default: return 0;
+    }
+}
+static inline uint64_t zh_tensor_bytes(uint32_t t, uint64_t rows, uint64_t cols) {
+    return rows * (cols / zh_block_size(t)) * zh_bytes_per_block(t);
+}
+static inline uint64_t zh_xq_bytes(uint32_t K) { return (uint64_t)(K / 32) * 108; }
+
+// ---- raw-pointer launchers (stream = ctx->stream); validation done by callers
+int zhk_quantize_xq(zh_ctx *ctx, const float *x, void *xq, uint32_t K, uint32_t n_vec,
+                    uint32_t x_stride);
+int zhk_dmmv(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, const void *xq, float *y, uint32_t M,
+             uint32_t K, uint32_t acc);
+int zhk_dmmv_gate_up(zh_ctx *ctx, uint32_t qtype, const uint8_t *Wg, const uint8_t *Wu,
+                     const void *xq, float *y, uint32_t M, uint32_t K);
+int zhk_dmmv_moe(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint64_t expert_stride,
+                 const uint32_t *routing, const void *xq, uint64_t xq_slot_stride, float *y,
+                 uint32_t M, uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2);
+int zhk_dequant_rows(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint32_t row0, uint32_t n_rows,
+                     uint32_t K, float *out, const uint32_t *row_from_dev, uint32_t clamp_rows);
+int zhk_synth_tensor(zh_ctx *ctx, uint8_t *dst, uint32_t qtype, uint64_t rows, uint64_t cols,
+                     uint64_t seed, uint64_t stream);
+int zhk_synth_vector(zh_ctx *ctx, void *dst, uint32_t kind, uint64_t n, float scale, uint64_t seed,
+                     uint64_t stream);
+int zhk_rms_norm(zh_ctx *ctx, const float *x, const float *w, uint32_t w_len, float *out, void *xq,
+                 uint32_t n, uint32_t n_groups, float eps);
+int zhk_swiglu(zh_ctx *ctx, const float *g, const float *u, float *out, uint32_t n);
+struct zh_pos_src {  // where a kernel reads the position: host scalar or device word
+    uint32_t value;
+    const uint32_t *dev;  // if non-null: position = *dev + value
+};
+int zhk_qk_norm_rope_kv(zh_ctx *ctx, float *q, const float *qw, const float *k, const float *kw,
+                        const float *v, const float *inv_freq, uint16_t *kc, uint16_t *vc,
+                        const uint32_t *pages, uint32_t n_pages, uint32_t cache_tokens,
+                        uint32_t nq, uint32_t nkv, uint32_t hd, zh_pos_src pos, float eps);
+int zhk_flash_decode(zh_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc,
+                     const uint32_t *pages, uint32_t n_pages, uint32_t cache_tokens, float *out,
+                     void *xq_out, uint32_t nh, uint32_t nkv, uint32_t hd, zh_pos_src seq_len,
+                     uint32_t max_seq, float scale, float *partials);
+uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t hd, uint32_t max_seq);
+int zhk_softmax_topk(zh_ctx *ctx, const float *logits, uint32_t n, uint32_t k, uint32_t *routing);
+int zhk_moe_weighted_acc(zh_ctx *ctx, float *a, const float *b, const uint32_t *routing, uint32_t n,
+                         uint32_t n_used, uint32_t src_stride);
+int zhk_argmax(zh_ctx *ctx, const float *logits, uint32_t n, uint32_t *result, uint32_t *partials,
+               uint32_t *token_ring, const uint32_t *ring_index);

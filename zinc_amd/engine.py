@@ -1,0 +1,97 @@
+"""Python mirror of the reference engine surface (src/compute/forward.zig):
+InferenceEngine.init / decodeStep / sampleGreedy / deinit and the free
+function generate, over the HIP engine in libzinc_hip.so."""
+import ctypes as C
+
+import numpy as np
+
+from . import hip
+from .hip import Q4_K, Q6_K, Q8_0, ModelConfig, lib
+
+# 8B-shaped dense decoder, Q4_K_M mix (Q4_K attention/FFN,
+# Q6_K ffn_down and lm-head).
+DENSE_8B = dict(n_layers=36, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=12288, vocab=151936,
+                n_experts=0, n_experts_used=0, expert_ffn=0, max_ctx=4096 + 16 + 256,
+                type_attn=Q4_K, type_ffn_gate_up=Q4_K, type_ffn_down=Q6_K, type_lm_head=Q6_K, type_embd=Q4_K,
+                type_router=Q8_0, rope_base=1e6, eps=1e-6, seed=1237)
+
+# sparse MoE, 48 layers, 128 experts top-8, expert FFN 768;
+# experts Q4_K, router/attention Q8_0, lm-head Q6_K.
+MOE_48L = dict(n_layers=48, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=128, ffn=0, vocab=151936,
+               n_experts=128, n_experts_used=8, expert_ffn=768, max_ctx=8192 + 16 + 256,
+               type_attn=Q8_0, type_ffn_gate_up=Q4_K, type_ffn_down=Q4_K, type_lm_head=Q6_K, type_embd=Q4_K,
+               type_router=Q8_0, rope_base=1e6, eps=1e-6, seed=1238)
+
+
+class DecodeState:
+    """DecodeState (forward.zig:63-92)."""
+
+    def __init__(self):
+        self.position = 0
+        self.generated_tokens = []
+        self.requested_context_tokens = 0
+
+
+class InferenceEngine:
+    def __init__(self, ctx: hip.Context, config: dict):
+        self.ctx = ctx
+        self.config = dict(config)
+        self._cfg = ModelConfig(**self.config)
+        h = C.c_void_p()
+        ctx.check(lib().zh_engine_create(ctx.h, C.byref(self._cfg), C.byref(h)))
+        self.h = h
+
+    def deinit(self):
+        if self.h:
+            lib().zh_engine_destroy(self.h)
+            self.h = None
+
+    close = deinit
+
+    def prefill_kv_random(self, n_tokens, seed):
+        self.ctx.check(lib().zh_engine_prefill_kv_random(self.h, n_tokens, seed))
+
+    def decode_step(self, state: DecodeState, token_id: int, collect_output: bool = True):
+        """decodeStep (forward.zig:4299): one token at state.position."""
+        self.ctx.check(lib().zh_engine_decode_step(self.h, token_id, state.position, int(collect_output)))
+        state.position += 1
+
+    def sample_greedy(self) -> int:
+        t = C.c_uint32()
+        self.ctx.check(lib().zh_engine_sample_greedy(self.h, C.byref(t)))
+        return t.value
+
+    def generate(self, prompt, max_tokens, eos=0xFFFFFFFF, start_pos=0):
+        """generate (forward.zig:10983): prompt then greedy decode on device."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(max_tokens, 1), dtype=np.uint32)
+        n = C.c_uint32()
+        self.ctx.check(lib().zh_engine_generate(self.h, C.c_void_p(p.ctypes.data), len(p), start_pos, max_tokens,
+                                                eos, C.c_void_p(out.ctypes.data), C.byref(n)))
+        return out[:n.value].tolist()
+
+    def logits(self):
+        out = np.empty(self.config["vocab"], dtype=np.float32)
+        self.ctx.check(lib().zh_engine_logits(self.h, C.c_void_p(out.ctypes.data)))
+        return out
+
+    def hidden(self):
+        out = np.empty(self.config["hidden"], dtype=np.float32)
+        self.ctx.check(lib().zh_engine_hidden(self.h, C.c_void_p(out.ctypes.data)))
+        return out
+
+    def tensor_bytes(self, stream):
+        b, off, n = C.c_void_p(), C.c_uint64(), C.c_uint64()
+        self.ctx.check(lib().zh_engine_tensor(self.h, stream, C.byref(b), C.byref(off), C.byref(n)))
+        out = np.empty(n.value, dtype=np.uint8)
+        self.ctx.check(lib().zh_buf_download(self.ctx.h, b, off.value, C.c_void_p(out.ctypes.data), n.value))
+        return out
+
+    def read_kv(self, layer, which, t0, n):
+        c = self.config
+        out = np.empty(n * c["n_kv_heads"] * c["head_dim"], dtype=np.uint16)
+        self.ctx.check(lib().zh_engine_read_kv(self.h, layer, which, t0, n, C.c_void_p(out.ctypes.data)))
+        return out
+
+    def bytes_per_token(self, L):
+        return lib().zh_engine_bytes_per_token(self.h, L)
