@@ -33,6 +33,29 @@ def assert_close(got, ref, what, rtol=RTOL, atol=ATOL):
                            f"got {got[bad[:5]]} ref {ref[bad[:5]]}; max err {err.max():.3g}")
 
 
+# Noise floor for ill-conditioned (cancelling) dot products: f32 rounding in
+# any summation order scales with sum_i |w_i x_i|; the reference's own serial
+# f32 path reaches ~3e-7 of it at K=4096.
+NOISE = 1e-6
+
+
+def assert_dot_close(got, ref32, ref64, mag, what):
+    """Parity bar for DMMV-like outputs. A row passes if it is within the
+    north-star tolerance of the oracle (f32 serial dot, the reference's CPU
+    path). Rows where the oracle's own rounding already uses more than half of
+    that tolerance against the exact (f64) dot -- cancellation,
+    |y| << sum|w x| -- are judged against the exact value with the same
+    tolerance plus NOISE * sum|w x|."""
+    got = got.astype(np.float64)
+    ok1 = np.abs(got - ref32) <= ATOL + RTOL * np.abs(ref32)
+    ill = np.abs(ref32 - ref64) > 0.5 * (ATOL + RTOL * np.abs(ref64))
+    ok2 = ill & (np.abs(got - ref64) <= ATOL + RTOL * np.abs(ref64) + NOISE * mag)
+    bad = np.nonzero(~(ok1 | ok2))[0]
+    assert len(bad) == 0, (f"{what}: {len(bad)}/{len(got)} rows outside tol; idx {bad[:5]} got {got[bad[:5]]} "
+                           f"ref32 {ref32[bad[:5]]} ref64 {ref64[bad[:5]]} mag {mag[bad[:5]]}")
+    return int((~ok1).sum())
+
+
 QTYPES = [12, 14, 8, 39]
 
 
@@ -84,9 +107,11 @@ def run_dmmv(ctx, orc, qtype, M, K, seed, acc=False, a_off=0):
     ctx.dmmv(qtype, Wb, a_off, xb, 0, yb, 0, M, K, int(acc))
     got = yb.download(np.float32, M)
     ref = orc.dmmv(W, qtype, x, M, K, y=y0.copy(), acc_mode=int(acc))
+    ref64 = orc.dmmv_f64(W, qtype, x, M, K) + (y0.astype(np.float64) if acc else 0.0)
+    mag = orc.dmmv_absdot(W, qtype, x, M, K) + (np.abs(y0.astype(np.float64)) if acc else 0.0)
     for b in (Wb, xb, yb):
         ctx.free(b)
-    return got, ref, W, x
+    return got, ref, ref64, mag
 
 
 @pytest.mark.parametrize("qtype,M,K", [
@@ -97,14 +122,14 @@ def run_dmmv(ctx, orc, qtype, M, K, seed, acc=False, a_off=0):
     (39, 257, 2880), (39, 4, 32), (39, 100, 1024),
 ])
 def test_dmmv_matches_oracle(ctx, orc, qtype, M, K):
-    got, ref, W, x = run_dmmv(ctx, orc, qtype, M, K, 1000 + M + K)
-    assert_close(got, ref, f"dmmv q{qtype} {M}x{K}")
+    got, ref, ref64, mag = run_dmmv(ctx, orc, qtype, M, K, 1000 + M + K)
+    assert_dot_close(got, ref, ref64, mag, f"dmmv q{qtype} {M}x{K}")
 
 
 @pytest.mark.parametrize("qtype", [12, 14, 8])
 def test_dmmv_acc_mode_and_offset(ctx, orc, qtype):
-    got, ref, _, _ = run_dmmv(ctx, orc, qtype, 300, 1024, 5, acc=True, a_off=4096)
-    assert_close(got, ref, "acc")
+    got, ref, ref64, mag = run_dmmv(ctx, orc, qtype, 300, 1024, 5, acc=True, a_off=4096)
+    assert_dot_close(got, ref, ref64, mag, "acc")
 
 
 def test_dmmv_mxfp4_reference_kat(ctx):
@@ -140,11 +165,16 @@ def test_fused_gate_up_swiglu(ctx, orc, qtype, M, K):
     g = orc.dmmv(Wg, qtype, x, M, K)
     u = orc.dmmv(Wu, qtype, x, M, K)
     ref = orc.swiglu(g, u)
+    g64, u64 = orc.dmmv_f64(Wg, qtype, x, M, K), orc.dmmv_f64(Wu, qtype, x, M, K)
+    sig = 1 / (1 + np.exp(-g64))
+    ref64 = g64 * sig * u64
+    # first-order propagation of the two dot products' magnitudes through silu(g)*u
+    dsilu = np.abs(sig * (1 + g64 * (1 - sig)))
+    mag = dsilu * orc.dmmv_absdot(Wg, qtype, x, M, K) * np.abs(u64) + np.abs(g64 * sig) * orc.dmmv_absdot(Wu, qtype, x, M, K)
     bg, bu, bx, by = ctx.upload(Wg), ctx.upload(Wu), ctx.upload(x), ctx.alloc(M * 4)
     ctx.dmmv_fused_gate_up_swiglu(qtype, bg, 0, bu, 0, bx, 0, by, 0, M, K)
     got = by.download(np.float32, M)
-    # silu amplifies the DMMV error by |d silu/dg| <= 1.1; same relative bar
-    assert_close(got, ref, "gate_up")
+    assert_dot_close(got, ref, ref64, mag, "gate_up")
 
 
 def test_dmmv_moe_expert_gather(ctx, orc):
@@ -159,8 +189,9 @@ def test_dmmv_moe_expert_gather(ctx, orc):
     ctx.dmmv_moe(qt, bW, stride, br, bx, K, 0, by, 0, M, K, k)
     got = by.download(np.float32, k * M).reshape(k, M)
     for s in range(k):
-        ref = orc.dmmv(W[ids[s] * stride:(ids[s] + 1) * stride], qt, xs[s * K:(s + 1) * K], M, K)
-        assert_close(got[s], ref, f"moe slot {s}")
+        We, xe = W[ids[s] * stride:(ids[s] + 1) * stride], xs[s * K:(s + 1) * K]
+        assert_dot_close(got[s], orc.dmmv(We, qt, xe, M, K), orc.dmmv_f64(We, qt, xe, M, K),
+                         orc.dmmv_absdot(We, qt, xe, M, K), f"moe slot {s}")
 
 
 def test_rms_norm(ctx, orc):
@@ -238,7 +269,8 @@ def test_qk_norm_rope_kv_write(ctx, orc):
     qw, kw = orc.synth_norm_weight(hd, 8, 4), orc.synth_norm_weight(hd, 8, 5)
     inv = orc.rope_inv_freq(hd, 1e6)
     bq, bqw, bk, bkw, bv, binv = (ctx.upload(a) for a in (q, qw, k, kw, v, inv))
-    bkc, bvc = ctx.alloc(nkv * cache_tokens * hd * 2), ctx.alloc(nkv * cache_tokens * hd * 2)
+    bkc = ctx.upload(np.zeros(nkv * cache_tokens * hd, np.uint16))
+    bvc = ctx.upload(np.zeros(nkv * cache_tokens * hd, np.uint16))
     bp = ctx.upload(pages)
     ctx.qk_norm_rope_kv_write(bq, bqw, bk, bkw, bv, binv, bkc, bvc, bp, n_pages, cache_tokens, nq, nkv, hd, pos, 1e-6)
     rq = orc.rope(orc.per_head_rms_norm(q, qw, hd, nq, 1e-6), hd, hd, nq, pos, inv)

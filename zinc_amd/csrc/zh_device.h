@@ -97,7 +97,24 @@ ZH_DEV float wave_max(float v) {
 }
 
 ZH_DEV float h2f(uint32_t h16) { return (float)__ushort_as_half((unsigned short)(h16 & 0xFFFF)); }
-ZH_DEV uint16_t f2h_rn(float f) { return __half_as_ushort(__float2half_rn(f)); }
+// f32 -> f16 round-to-nearest-even in integer arithmetic (subnormals kept,
+// overflow to inf), independent of the hardware's fp16 denormal mode.
+ZH_DEV uint16_t f2h_rn(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (a > 0x7F800000u ? 0x200u : 0u));
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (a < 0x38800000u) {
+        if (a < 0x33000000u) return (uint16_t)sign;
+        uint32_t e = a >> 23, man = (a & 0x7FFFFFu) | 0x800000u, shift = 126u - e;
+        uint32_t q = man >> shift, rem = man & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = (a - 0x38000000u) >> 13, rem = a & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
 
 // Load n dwords starting at an arbitrary byte address (byte-aligned) using
 // dword-aligned loads and v_alignbyte. `out` receives n dwords.
