@@ -66,8 +66,18 @@ int      zh_buf_fill_u8(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint8_t v, ui
 int zh_event_record(zh_ctx *ctx, int slot);          /* slot 0..63 */
 int zh_event_elapsed_ms(zh_ctx *ctx, int a, int b, float *ms);
 
+/* ---- calibration probes (counterparts of the reference's microbenchmarks
+ *      benchmarks/dispatch_overhead.c and benchmarks/bandwidth.zig) ------ */
+/* Streaming 128-bit reads over the first `bytes` of buf, `iters` times: GB/s. */
+int zh_stream_read_probe(zh_ctx *ctx, const zh_buf *buf, uint64_t bytes, uint32_t iters, float *gbs);
+/* n_kernels empty launches of `wgs` workgroups, in a hipGraph (use_graph) or
+ * as plain launches: average microseconds per kernel. */
+int zh_dispatch_overhead(zh_ctx *ctx, uint32_t n_kernels, uint32_t wgs, int use_graph, float *us_per_kernel);
+
 /* ---- synthetic data (seeded, bit-identical to oracle/zinc_oracle.c) ----- */
-/* Fill rows x cols of `qtype` blocks at `offset` per the BASELINE distributions. */
+/* Fill rows x cols of `qtype` blocks at `offset` per the BASELINE distributions.
+ * qtype | 0x100 (Q4_K only): model-init variant with dmin = f16(7.5*d), so
+ * sub-block weights are zero-mean; the synthetic models use it. */
 int zh_synth_tensor(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint32_t qtype,
                     uint64_t rows, uint64_t cols, uint64_t seed, uint64_t stream);
 /* kind 0: N(0,1)*scale f32; 1: N(0,1) f16; 2: norm weight 1+U(-.01,.01) f32 */
@@ -95,6 +105,21 @@ int zh_dmmv_fused_gate_up_swiglu(zh_ctx *ctx, uint32_t qtype, const zh_buf *Wg, 
 int zh_dmmv_moe(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t expert_stride,
                 const zh_buf *routing, const zh_buf *x, uint32_t x_expert_stride, uint64_t x_off,
                 zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t n_used);
+/* Pre-quantised activations ("XQ": per 32-element block, three int8 limbs of
+ * a 22-bit fixed-point value plus an f32 power-of-two scale and partial
+ * sums; zh_xq_bytes(K) bytes per vector). A caller that feeds one activation
+ * to several matrices (Q/K/V, gate/up) quantises once; the reference has no
+ * counterpart (its shaders read f32 x directly, dmmv_q4k.comp:90-104).
+ * x_stride: floats between vectors; vector v goes to xq_off + v*zh_xq_bytes(K). */
+uint64_t zh_xq_bytes(uint32_t K);
+int zh_quantize_activation(zh_ctx *ctx, const zh_buf *x, uint64_t x_off, uint32_t K, uint32_t n_vec,
+                           uint32_t x_stride, zh_buf *xq, uint64_t xq_off);
+/* zh_dmmv / zh_dmmv_fused_gate_up_swiglu over an XQ activation. */
+int zh_dmmv_xq(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off, const zh_buf *xq, uint64_t xq_off,
+               zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t acc_mode);
+int zh_dmmv_fused_gate_up_swiglu_xq(zh_ctx *ctx, uint32_t qtype, const zh_buf *Wg, uint64_t g_off,
+                                    const zh_buf *Wu, uint64_t u_off, const zh_buf *xq, uint64_t xq_off,
+                                    zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K);
 /* Bit-exact dequantisation of rows [row0, row0+n_rows) to f32 (dequantRow,
  * forward.zig:242-465), used for the embedding gather and for parity tests. */
 int zh_dequant_rows(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off,

@@ -235,7 +235,8 @@ def normal(r):
 
 
 def synth_tensor(qtype, rows, cols, seed, stream):
-    out = np.empty(tensor_bytes(qtype, rows, cols), dtype=np.uint8)
+    """qtype | 0x100: centered model-init variant (Q4_K dmin = f16(7.5*d))."""
+    out = np.empty(tensor_bytes(qtype & 0xFF, rows, cols), dtype=np.uint8)
     if lib().zo_synth_tensor(u8(out), qtype, rows, cols, seed, stream) != 0:
         raise ValueError("bad synth args")
     return out

@@ -420,8 +420,12 @@ float zo_normal(uint64_t r) {
 }
 static inline uint16_t scale_f16(uint64_t r) { return zo_f32_to_f16(fabsf(zo_normal(r)) * 0.02f); }
 
-int zo_synth_tensor(uint8_t *dst, uint32_t type, uint64_t rows, uint64_t cols,
+int zo_synth_tensor(uint8_t *dst, uint32_t type_flags, uint64_t rows, uint64_t cols,
                     uint64_t seed, uint64_t stream) {
+    /* type | 0x100: model-init variant of Q4_K with dmin = f16(7.5 * d) (zero-mean
+     * sub-blocks); the synthetic models use it for every Q4_K tensor. */
+    uint32_t type = type_flags & 0xFF;
+    int centered = (type_flags & 0x100) != 0;
     uint64_t bs = zo_block_size(type), bpb = zo_bytes_per_block(type);
     if (bpb == 0 || cols % bs) return -1;
     uint64_t nb = rows * (cols / bs);
@@ -430,7 +434,7 @@ int zo_synth_tensor(uint8_t *dst, uint32_t type, uint64_t rows, uint64_t cols,
         switch (type) {
         case ZO_Q4_K: { /* d, dmin = f16(|N(0,.02)|); 12 scale bytes + 128 qs bytes uniform */
             uint16_t d = scale_f16(zo_rand(seed, stream, b * 32 + 0));
-            uint16_t dm = scale_f16(zo_rand(seed, stream, b * 32 + 1));
+            uint16_t dm = centered ? zo_f32_to_f16(zo_f16_to_f32(d) * 7.5f) : scale_f16(zo_rand(seed, stream, b * 32 + 1));
             o[0] = d & 0xFF; o[1] = d >> 8; o[2] = dm & 0xFF; o[3] = dm >> 8;
             for (int i = 0; i < 140; i++) {
                 uint64_t r = zo_rand(seed, stream, b * 32 + 2 + i / 8);
@@ -530,7 +534,7 @@ struct zo_model {
 
 static uint8_t *alloc_tensor(uint32_t type, uint64_t rows, uint64_t cols, uint64_t seed, uint64_t stream) {
     uint8_t *p = (uint8_t *)malloc(zo_tensor_bytes(type, rows, cols));
-    zo_synth_tensor(p, type, rows, cols, seed, stream);
+    zo_synth_tensor(p, type | 0x100, rows, cols, seed, stream);
     return p;
 }
 static float *alloc_norm(uint64_t n, uint64_t seed, uint64_t stream) {

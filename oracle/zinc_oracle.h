@@ -92,7 +92,8 @@ uint32_t zo_kv_page_count(uint32_t context_tokens);
 /* ---- Seeded synthetic data (shared spec with the HIP generator) ---- */
 uint64_t zo_rand(uint64_t seed, uint64_t stream, uint64_t ctr);
 float    zo_normal(uint64_t r);
-/* Fill a rows x cols tensor of `type` with BASELINE-distributed random blocks. */
+/* Fill a rows x cols tensor of `type` with BASELINE-distributed random blocks.
+ * type | 0x100 (Q4_K): model-init variant, dmin = f16(7.5*d). */
 int  zo_synth_tensor(uint8_t *dst, uint32_t type, uint64_t rows, uint64_t cols,
                      uint64_t seed, uint64_t stream);
 void zo_synth_normal_f32(float *dst, uint64_t n, float scale, uint64_t seed, uint64_t stream);

@@ -59,10 +59,10 @@ def assert_dot_close(got, ref32, ref64, mag, what):
 QTYPES = [12, 14, 8, 39]
 
 
-@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("qtype", QTYPES + [12 | 0x100])
 def test_synth_generator_bit_identical(ctx, orc, qtype):
     rows, cols = 7, (2880 if qtype == 39 else 1024)
-    n = orc.tensor_bytes(qtype, rows, cols)
+    n = orc.tensor_bytes(qtype & 0xFF, rows, cols)
     buf = ctx.alloc(n)
     ctx.synth_tensor(buf, 0, qtype, rows, cols, 77, 5)
     got = buf.download(np.uint8, n)

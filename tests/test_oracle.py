@@ -417,3 +417,18 @@ def test_synthetic_distributions(orc):
     # determinism and stream separation
     assert np.array_equal(orc.synth_tensor(orc.Q4_K, 4, 256, 1, 2), W[:4].ravel())
     assert not np.array_equal(orc.synth_tensor(orc.Q4_K, 4, 256, 1, 9), W[:4].ravel())
+
+
+def test_centered_q4k_model_init_is_zero_mean(orc):
+    """The model-init variant (dmin = f16(7.5 d)) removes the positive mean of
+    BASELINE-distributed Q4_K weights, so mat-vec outputs have no common mode."""
+    W0 = orc.synth_tensor(orc.Q4_K, 64, 4096, 3, 4)
+    W1 = orc.synth_tensor(orc.Q4_K | 0x100, 64, 4096, 3, 4)
+    d0, d1 = orc.dequant(W0, 64, 4096, orc.Q4_K), orc.dequant(W1, 64, 4096, orc.Q4_K)
+    assert d0.mean() > 1.0                      # BASELINE blocks: strongly positive mean
+    assert abs(d1.mean()) < 0.02 * d1.std()     # centered
+    b = W1.reshape(-1, 144)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32).ravel()
+    dm = b[:, 2:4].copy().view(np.float16).ravel()
+    assert np.array_equal(dm, (d * np.float32(7.5)).astype(np.float16))
+    assert np.array_equal(b[:, 4:], W0.reshape(-1, 144)[:, 4:])  # scales and codes unchanged

@@ -42,7 +42,6 @@ ZH_DEV XQView xq_view(void *base, uint32_t nblk) {
     v.xsum = v.xs + nblk;
     return v;
 }
-static inline size_t xq_bytes(uint32_t K) { return (size_t)(K / 32) * (96 + 12); }
 
 ZH_DEV float bits_f(uint32_t u) { return __uint_as_float(u); }
 

@@ -18,6 +18,8 @@
 #include "zh_device.h"
 #include "zh_internal.h"
 
+#include <stdlib.h>
+
 #include <vector>
 
 // ---------------------------------------------------------------------------
@@ -54,7 +56,7 @@ __global__ __launch_bounds__(256) void k_quantize_xq(const float *__restrict__ x
 int zhk_quantize_xq(zh_ctx *c, const float *x, void *xq, uint32_t K, uint32_t n_vec, uint32_t x_stride) {
     uint32_t nblk = K / 32;
     hipLaunchKernelGGL(k_quantize_xq, dim3((nblk + 7) / 8, n_vec), dim3(256), 0, c->stream, x,
-                       (uint8_t *)xq, K, x_stride, (uint64_t)zh_xq_bytes(K));
+                       (uint8_t *)xq, K, x_stride, (uint64_t)zh_xq_bytes_int(K));
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
 }
@@ -118,21 +120,21 @@ struct FmtQ4K {
                 D[1][k] = sdot4(hi, xr.L[24 + k * 8 + i], D[1][k]);
             }
         }
-        // getScaleMinK4 (forward.zig:229-238) for j = 2p, 2p+1.
-        int p = u & 3;
-        uint32_t w1 = raw[1], w2 = raw[2], w3 = raw[3];
+        // getScaleMinK4 (forward.zig:229-238) for j = 2p, 2p+1, branch-free:
+        // p < 2: sc = s[j] & 63, m = s[j+4] & 63 (6-bit fields of w1, w2);
+        // p >= 2: sc = low nibble of s[j+4] | (s[j-4] >> 6) << 4,
+        //          m = high nibble of s[j+4] | (s[j] >> 6) << 4.
+        const int p = u & 3;
+        const bool lo4 = p < 2;
+        const uint32_t w1 = raw[1], w2 = raw[2], w3 = raw[3];
+        const uint32_t srcS = lo4 ? w1 : w3, srcM = lo4 ? w2 : w3;
+        const uint32_t wa = lo4 ? 6u : 4u, wb = lo4 ? 0u : 2u, mo = lo4 ? 0u : 4u;
         uint32_t sc[2], mn[2];
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            int j = 2 * p + s;
-            if (p < 2) {
-                sc[s] = (w1 >> (8 * j)) & 63;
-                mn[s] = (w2 >> (8 * j)) & 63;
-            } else {
-                int i4 = j - 4;
-                sc[s] = ((w3 >> (8 * i4)) & 15) | (((w1 >> (8 * i4 + 6)) & 3) << 4);
-                mn[s] = ((w3 >> (8 * i4 + 4)) & 15) | (((w2 >> (8 * i4 + 6)) & 3) << 4);
-            }
+        for (int s2 = 0; s2 < 2; s2++) {
+            const uint32_t off = 16u * (uint32_t)(p & 1) + 8u * (uint32_t)s2;
+            sc[s2] = __builtin_amdgcn_ubfe(srcS, off, wa) | (__builtin_amdgcn_ubfe(w1, off + 6u, wb) << 4);
+            mn[s2] = __builtin_amdgcn_ubfe(srcM, off + mo, wa) | (__builtin_amdgcn_ubfe(w2, off + 6u, wb) << 4);
         }
         float d = h2f(raw[0]), dmin = h2f(raw[0] >> 16);
         float S0 = (float)comb_int(D[0][0], D[0][1], D[0][2]);
@@ -334,16 +336,62 @@ struct DmmvP {
     const uint32_t *routing;  // MoE: expert id per grid.y slot
     uint64_t expert_stride, xq_slot_stride;
     uint32_t y_slot_stride;
+    // Plain mode may stack up to three matrices that share K and x (Q/K/V):
+    // rows [seg_end[s-1], seg_end[s]) come from segW[s] and go to segY[s].
+    // Segment sizes are multiples of the row batch R.
+    uint32_t nseg;
+    const uint8_t *segW[3];
+    float *segY[3];
+    uint32_t seg_end[3];
 };
 
 enum { MODE_PLAIN = 0, MODE_GATE_UP = 1 };
+static int dmmv_rows_per_batch(int mode);
 
 ZH_DEV float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+// Joint reduction of V per-lane partials (V a power of two) across a team of
+// TL lanes: log2(V) halving-exchange steps, then plain xor steps. Returns
+// the team sum of partial `owner_index(lane)`; every lane of the team gets a
+// valid result for its index.
+template <int TL, int V>
+ZH_DEV float team_reduce_multi(float (&a)[V], int tlane) {
+    int n = V;
+    int o = TL / 2;
+#pragma unroll
+    for (int step = V; step > 1; step >>= 1) {
+        const bool up = (tlane & o) != 0;
+#pragma unroll
+        for (int i = 0; i < step / 2; i++) {
+            float lo = a[i], hi = a[i + step / 2];
+            float send = up ? lo : hi, keep = up ? hi : lo;
+            a[i] = keep + __shfl_xor(send, o, 64);
+        }
+        o >>= 1;
+        n >>= 1;
+    }
+    float v = a[0];
+#pragma unroll
+    for (; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+template <int TL, int V>
+ZH_DEV int owner_index(int tlane) {
+    int idx = 0, o = TL / 2;
+#pragma unroll
+    for (int step = V; step > 1; step >>= 1) {
+        idx = idx * 2 + ((tlane & o) ? 1 : 0);
+        o >>= 1;
+    }
+    return idx;
+}
 
 template <class F, int TL, int NW, int R, int MODE, bool MOE>
 __global__ __launch_bounds__(NW == 1 ? 256 : NW * 64) void k_dmmv(DmmvP p) {
     constexpr int TPW = (NW == 1) ? 256 / TL : 1;  // teams per workgroup
     constexpr int NM = (MODE == MODE_GATE_UP) ? 2 : 1;
+    constexpr int V = NM * R;
+    constexpr bool UNIFORM = (NW > 1) || (TL == 64);  // one team per wave or wider
     const int tid = threadIdx.x;
     const int tlane = (NW == 1) ? (tid % TL) : tid;
     const int team_in_wg = (NW == 1) ? (tid / TL) : 0;
@@ -365,56 +413,79 @@ __global__ __launch_bounds__(NW == 1 ? 256 : NW * 64) void k_dmmv(DmmvP p) {
     XReg xr;
     if (active) F::load_x(xr, v, tlane);
 
-    __shared__ float red[NW > 1 ? NW * R * NM : 1];
+    __shared__ float red[NW > 1 ? NW * V : 1];
     const uint32_t nteams = gridDim.x * TPW;
-    for (uint32_t r0 = (blockIdx.x * TPW + team_in_wg) * R; r0 < p.M; r0 += nteams * R) {
+    uint32_t r0 = (blockIdx.x * TPW + team_in_wg) * R;
+    if (UNIFORM) r0 = __builtin_amdgcn_readfirstlane(r0);
+    for (; r0 < p.M; r0 += nteams * R) {
         uint32_t raw[NM][R][F::RAW];
+        // segment of this batch (batches never straddle segments)
+        uint32_t seg_start = 0, seg_rows = p.M;
+        const uint8_t *Wb[2] = {Wm[0], Wm[1]};
+        float *yb = y;
+        if (!MOE && MODE == MODE_PLAIN && p.nseg > 1) {
+            const uint32_t sg = (r0 >= p.seg_end[0] ? 1u : 0u) + (p.nseg > 2 && r0 >= p.seg_end[1] ? 1u : 0u);
+            seg_start = sg ? p.seg_end[sg - 1] : 0u;
+            seg_rows = p.seg_end[sg] - seg_start;
+            Wb[0] = p.segW[sg];
+            yb = p.segY[sg];
+        }
+        const uint32_t rr0 = r0 - seg_start;
+        // rows past the segment end are clamped to its last row (loaded, computed, not written)
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-            for (int r = 0; r < R; r++)
-                if (active && r0 + r < p.M) F::load_raw(Wm[m] + (size_t)(r0 + r) * p.row_bytes, tlane, raw[m][r]);
-        float part[NM][R];
+            for (int r = 0; r < R; r++) {
+                const uint32_t row = min(rr0 + r, seg_rows - 1);
+                if (active) F::load_raw(Wb[m] + (size_t)row * p.row_bytes, tlane, raw[m][r]);
+            }
+        float part[V];
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-            for (int r = 0; r < R; r++)
-                part[m][r] = (active && r0 + r < p.M) ? F::compute(raw[m][r], xr, tlane) : 0.f;
+            for (int r = 0; r < R; r++) {
+#ifdef ZH_EXP_NOCOMPUTE
+            uint32_t hx = 0;
+#pragma unroll
+            for (int q = 0; q < F::RAW; q++) hx ^= raw[m][r][q];
+            part[m * R + r] = active ? (float)(hx & 0xFF) : 0.f;
+#else
+            part[m * R + r] = active ? F::compute(raw[m][r], xr, tlane) : 0.f;
+#endif
+        }
+        float res;
+        int idx;
         if (NW == 1) {
-#pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-                for (int r = 0; r < R; r++) part[m][r] = team_sum<TL>(part[m][r]);
+            res = team_reduce_multi<TL, V>(part, tlane);
+            idx = owner_index<TL, V>(tlane);
         } else {
             const int wave = tid >> 6, lane = tid & 63;
-#pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-                    float s = wave_sum(part[m][r]);
-                    if (lane == 0) red[(m * R + r) * NW + wave] = s;
-                }
+            float s = team_reduce_multi<64, V>(part, lane);
+            int wi = owner_index<64, V>(lane);
+            if ((lane & (64 / V - 1)) == 0) red[wi * NW + wave] = s;
             __syncthreads();
+            idx = tid;
+            res = 0.f;
+            if (tid < V) {
 #pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-                    float s = 0.f;
-#pragma unroll
-                    for (int w = 0; w < NW; w++) s += red[(m * R + r) * NW + w];
-                    part[m][r] = s;
-                }
+                for (int w = 0; w < NW; w++) res += red[tid * NW + w];
+            }
             __syncthreads();
         }
-        // lane r of the team writes row r0 + r
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (tlane == r && r0 + r < p.M) {
-                float out;
-                if (MODE == MODE_GATE_UP) out = silu_mul(part[0][r], part[NM - 1][r]);
-                else out = part[0][r];
-                if (p.acc) out += y[r0 + r];
-                y[r0 + r] = out;
+        // idx = m*R + r. The team sum of index i sits on team lane i*(TL/V)
+        // (NW > 1: on thread i). In gate/up mode the up value of row r is
+        // index R + r.
+        constexpr int STRIDE = (NW == 1) ? (TL / V) : 1;
+        const bool writer = (NW == 1) ? ((tlane % STRIDE) == 0) : (tid < V);
+        if (MODE == MODE_GATE_UP) {
+            const int lane = tid & 63;
+            const float upv = __shfl(res, (lane + R * STRIDE) & 63, 64);
+            if (writer && idx < R && rr0 + idx < seg_rows) yb[rr0 + idx] = silu_mul(res, upv);
+        } else {
+            if (writer && rr0 + idx < seg_rows) {
+                float out = res;
+                if (p.acc) out += yb[rr0 + idx];
+                yb[rr0 + idx] = out;
             }
         }
     }
@@ -429,7 +500,13 @@ static int launch_one(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
     constexpr int BS = (NW == 1) ? 256 : NW * 64;
     uint32_t teams = (p.M + R - 1) / R;
     uint32_t wgs = (teams + TPW - 1) / TPW;
-    uint32_t cap = (uint32_t)c->cu_count * (NW == 1 ? 8u : 16u / NW + 1u);
+    static int capm = -1;
+    if (capm < 0) {
+        const char *e = getenv("ZH_DMMV_CAP");
+        capm = e ? atoi(e) : 0;
+    }
+    uint32_t cap = capm > 0 ? (uint32_t)c->cu_count * (uint32_t)capm
+                            : (uint32_t)c->cu_count * (NW == 1 ? 8u : 16u / NW + 1u);
     if (MOE) cap = (cap + n_slots - 1) / n_slots;
     if (wgs > cap) wgs = cap;
     if (wgs == 0) wgs = 1;
@@ -439,9 +516,8 @@ static int launch_one(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
     return ZH_OK;
 }
 
-template <class F, int MODE, bool MOE>
-static int launch_fmt(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
-    constexpr int R = 4;
+template <class F, int R, int MODE, bool MOE>
+static int launch_fmt_r(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
     uint32_t U = p.K / F::EPU;
     if (U <= 8) return launch_one<F, 8, 1, R, MODE, MOE>(c, p, n_slots);
     if (U <= 16) return launch_one<F, 16, 1, R, MODE, MOE>(c, p, n_slots);
@@ -451,8 +527,23 @@ static int launch_fmt(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
     if (U <= 192) return launch_one<F, 64, 3, R, MODE, MOE>(c, p, n_slots);
     if (U <= 256) return launch_one<F, 64, 4, R, MODE, MOE>(c, p, n_slots);
     if (U <= 512) return launch_one<F, 64, 8, R, MODE, MOE>(c, p, n_slots);
-    if (U <= 1024) return launch_one<F, 64, 16, R, MODE, MOE>(c, p, n_slots);
     return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "K=%u too large", p.K);
+}
+
+static int dmmv_rows_per_batch(int mode) {
+    static int env = -1;
+    if (env < 0) {
+        const char *e = getenv("ZH_DMMV_R");
+        env = e ? atoi(e) : 0;
+    }
+    if (env == 2 || env == 4) return env;
+    return mode == MODE_GATE_UP ? 2 : 4;
+}
+
+template <class F, int MODE, bool MOE>
+static int launch_fmt(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
+    if (dmmv_rows_per_batch(MODE) == 2) return launch_fmt_r<F, 2, MODE, MOE>(c, p, n_slots);
+    return launch_fmt_r<F, 4, MODE, MOE>(c, p, n_slots);
 }
 
 template <int MODE, bool MOE>
@@ -486,6 +577,33 @@ int zhk_dmmv(zh_ctx *c, uint32_t qtype, const uint8_t *W, const void *xq, float 
     DmmvP p = {};
     p.W = W; p.W2 = W; p.xq = (const uint8_t *)xq; p.y = y; p.M = M; p.K = K;
     p.row_bytes = zh_tensor_bytes(qtype, 1, K); p.acc = acc;
+    p.nseg = 1; p.segW[0] = W; p.segY[0] = y; p.seg_end[0] = M;
+    return launch_dmmv<MODE_PLAIN, false>(c, qtype, p, 1);
+}
+
+int zhk_dmmv_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, float *const *y,
+                   const uint32_t *M, const void *xq, uint32_t K) {
+    int R = dmmv_rows_per_batch(MODE_PLAIN);
+    bool ok = nseg >= 1 && nseg <= 3;
+    for (uint32_t s2 = 0; ok && s2 < nseg; s2++) ok = (M[s2] % (uint32_t)R) == 0 && M[s2] > 0;
+    if (!ok) {  // fall back to one launch per matrix
+        for (uint32_t s2 = 0; s2 < nseg; s2++) {
+            int rc = zhk_dmmv(c, qtype, W[s2], xq, y[s2], M[s2], K, 0);
+            if (rc) return rc;
+        }
+        return ZH_OK;
+    }
+    DmmvP p = {};
+    p.W = W[0]; p.W2 = W[0]; p.xq = (const uint8_t *)xq; p.y = y[0]; p.K = K;
+    p.row_bytes = zh_tensor_bytes(qtype, 1, K);
+    p.nseg = nseg;
+    uint32_t end = 0;
+    for (uint32_t s2 = 0; s2 < nseg; s2++) {
+        p.segW[s2] = W[s2]; p.segY[s2] = y[s2];
+        end += M[s2];
+        p.seg_end[s2] = end;
+    }
+    p.M = end;
     return launch_dmmv<MODE_PLAIN, false>(c, qtype, p, 1);
 }
 
@@ -529,9 +647,50 @@ extern "C" int zh_dmmv(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a_of
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "offsets must be 4-byte aligned");
     if (qtype == ZH_Q4_K && (a_off & 15)) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "Q4_K a_off must be 16-byte aligned");
     void *xq;
-    if ((rc = zh_scratch(c, zh_xq_bytes(K), &xq))) return rc;
+    if ((rc = zh_scratch(c, zh_xq_bytes_int(K), &xq))) return rc;
     if ((rc = zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), xq, K, 1, 0))) return rc;
     return zhk_dmmv(c, qtype, (const uint8_t *)W->ptr + a_off, xq, (float *)((char *)y->ptr + y_off), M, K, acc_mode);
+}
+
+extern "C" uint64_t zh_xq_bytes(uint32_t K) { return zh_xq_bytes_int(K); }
+
+extern "C" int zh_quantize_activation(zh_ctx *c, const zh_buf *x, uint64_t x_off, uint32_t K, uint32_t n_vec,
+                                      uint32_t x_stride, zh_buf *xq, uint64_t xq_off) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    if (K == 0 || K % 32 || n_vec == 0 || (n_vec > 1 && x_stride < K) || (x_off & 3) || (xq_off & 15))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "quantize_activation shape");
+    if (!in_range(x, x_off, 4ull * ((uint64_t)(n_vec - 1) * x_stride + K)) ||
+        !in_range(xq, xq_off, zh_xq_bytes_int(K) * n_vec))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "quantize_activation range");
+    return zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), (char *)xq->ptr + xq_off, K, n_vec,
+                           x_stride);
+}
+
+extern "C" int zh_dmmv_xq(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a_off, const zh_buf *xq,
+                          uint64_t xq_off, zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t acc_mode) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    int rc = check_k(c, qtype, K);
+    if (rc) return rc;
+    if (M == 0 || acc_mode > 1) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "shape");
+    if (!in_range(W, a_off, zh_tensor_bytes(qtype, M, K)) || !in_range(xq, xq_off, zh_xq_bytes_int(K)) ||
+        !in_range(y, y_off, 4ull * M) || (a_off & (qtype == ZH_Q4_K ? 15 : 3)) || (xq_off & 15) || (y_off & 3))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "range/alignment");
+    return zhk_dmmv(c, qtype, (const uint8_t *)W->ptr + a_off, (const char *)xq->ptr + xq_off,
+                    (float *)((char *)y->ptr + y_off), M, K, acc_mode);
+}
+
+extern "C" int zh_dmmv_fused_gate_up_swiglu_xq(zh_ctx *c, uint32_t qtype, const zh_buf *Wg, uint64_t g_off,
+                                               const zh_buf *Wu, uint64_t u_off, const zh_buf *xq, uint64_t xq_off,
+                                               zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    int rc = check_k(c, qtype, K);
+    if (rc) return rc;
+    uint64_t wb = zh_tensor_bytes(qtype, M, K);
+    if (M == 0 || !in_range(Wg, g_off, wb) || !in_range(Wu, u_off, wb) || !in_range(xq, xq_off, zh_xq_bytes_int(K)) ||
+        !in_range(y, y_off, 4ull * M) || (g_off & 15) || (u_off & 15) || (xq_off & 15) || (y_off & 3))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "range/alignment");
+    return zhk_dmmv_gate_up(c, qtype, (const uint8_t *)Wg->ptr + g_off, (const uint8_t *)Wu->ptr + u_off,
+                            (const char *)xq->ptr + xq_off, (float *)((char *)y->ptr + y_off), M, K);
 }
 
 extern "C" int zh_dmmv_fused_gate_up_swiglu(zh_ctx *c, uint32_t qtype, const zh_buf *Wg, uint64_t g_off,
@@ -547,7 +706,7 @@ extern "C" int zh_dmmv_fused_gate_up_swiglu(zh_ctx *c, uint32_t qtype, const zh_
     if ((g_off & 15) || (u_off & 15) || (x_off & 3) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "misaligned offsets");
     void *xq;
-    if ((rc = zh_scratch(c, zh_xq_bytes(K), &xq))) return rc;
+    if ((rc = zh_scratch(c, zh_xq_bytes_int(K), &xq))) return rc;
     if ((rc = zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), xq, K, 1, 0))) return rc;
     return zhk_dmmv_gate_up(c, qtype, (const uint8_t *)Wg->ptr + g_off, (const uint8_t *)Wu->ptr + u_off, xq,
                             (float *)((char *)y->ptr + y_off), M, K);
@@ -573,7 +732,7 @@ extern "C" int zh_dmmv_moe(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t 
         if (!in_range(W, (uint64_t)ids[s] * expert_stride, zh_tensor_bytes(qtype, M, K)))
             return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "expert id %u out of range", ids[s]);
     void *xq;
-    uint64_t xqs = zh_xq_bytes(K);
+    uint64_t xqs = zh_xq_bytes_int(K);
     if ((rc = zh_scratch(c, xqs * n_used, &xq))) return rc;
     if ((rc = zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), xq, K, n_used, x_expert_stride)))
         return rc;

@@ -206,7 +206,8 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
         bool is_norm = kv.first == S_OUTPUT_NORM || (kv.first > 0xFF && (kind == K_ATTN_NORM || kind == K_Q_NORM ||
                                                                          kind == K_K_NORM || kind == K_FFN_NORM));
         if (is_norm) rc = zhk_synth_vector(ctx, e->arena + t.off, 2, t.rows * t.cols, 1.f, c.seed, kv.first);
-        else rc = zhk_synth_tensor(ctx, e->arena + t.off, t.type, t.rows, t.cols, c.seed, kv.first);
+        else rc = zhk_synth_tensor(ctx, e->arena + t.off, t.type | 0x100u /* centered model init */, t.rows, t.cols,
+                                   c.seed, kv.first);
         if (rc) { zh_engine_destroy(e); return rc; }
     }
     // --- KV cache [layer][K|V][nkv][max_ctx][hd] fp16 and identity page table
@@ -227,8 +228,8 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
         {(void **)&e->s, 4ull * F}, {(void **)&e->logits, 4ull * c.vocab}, {(void **)&e->rl, 4ull * 256},
         {(void **)&e->edown_out, 4ull * H * (c.n_experts_used ? c.n_experts_used : 1)},
         {(void **)&e->fd_part, zhk_flash_decode_partials_bytes(c.n_heads, hd, c.max_ctx)},
-        {(void **)&e->xq_h, zh_xq_bytes(H)}, {(void **)&e->xq_q, zh_xq_bytes(qd)},
-        {(void **)&e->xq_f, zh_xq_bytes(c.n_experts ? c.expert_ffn : c.ffn) * (c.n_experts_used ? c.n_experts_used : 1)},
+        {(void **)&e->xq_h, zh_xq_bytes_int(H)}, {(void **)&e->xq_q, zh_xq_bytes_int(qd)},
+        {(void **)&e->xq_f, zh_xq_bytes_int(c.n_experts ? c.expert_ffn : c.ffn) * (c.n_experts_used ? c.n_experts_used : 1)},
         {(void **)&e->routing, 8ull * 16}, {(void **)&e->am_part, 8ull * 256}, {(void **)&e->st, 4ull * ST_WORDS},
         {(void **)&e->prompt, 4ull * MAX_PROMPT}, {(void **)&e->ring, 4ull * MAX_GEN}, {(void **)&e->pages, 4ull * e->n_pages},
         {(void **)&e->inv_freq, 4ull * hd / 2},
@@ -303,9 +304,12 @@ static int record_step(zh_engine *e, bool collect) {
     for (uint32_t l = 0; l < m.n_layers; l++) {
         const Layer &y = e->L[l];
         ERC(zhk_rms_norm(c, e->hidden, Wf(y.attn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
-        ERC(zhk_dmmv(c, m.type_attn, W(y.wq), e->xq_h, e->q, qd, H, 0));
-        ERC(zhk_dmmv(c, m.type_attn, W(y.wk), e->xq_h, e->k, kvd, H, 0));
-        ERC(zhk_dmmv(c, m.type_attn, W(y.wv), e->xq_h, e->v, kvd, H, 0));
+        {
+            const uint8_t *ws[3] = {W(y.wq), W(y.wk), W(y.wv)};
+            float *ys[3] = {e->q, e->k, e->v};
+            const uint32_t ms[3] = {qd, kvd, kvd};
+            ERC(zhk_dmmv_multi(c, m.type_attn, 3, ws, ys, ms, e->xq_h, H));
+        }
         ERC(zhk_qk_norm_rope_kv(c, e->q, Wf(y.q_norm), e->k, Wf(y.k_norm), e->v, e->inv_freq, y.kc, y.vc, e->pages,
                                 e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd, pos, m.eps));
         ERC(zhk_flash_decode(c, e->q, y.kc, y.vc, e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads,
@@ -324,7 +328,7 @@ static int record_step(zh_engine *e, bool collect) {
                              e->xq_h, 0, e->s, F, H, k, 1, W(y.eup)));
             ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
             ERC(zhk_dmmv_moe(c, m.type_ffn_down, W(y.edown), zh_tensor_bytes(m.type_ffn_down, H, F), e->routing,
-                             e->xq_f, zh_xq_bytes(F), e->edown_out, H, F, k, 0, nullptr));
+                             e->xq_f, zh_xq_bytes_int(F), e->edown_out, H, F, k, 0, nullptr));
             ERC(zhk_moe_weighted_acc(c, e->hidden, e->edown_out, e->routing, H, k, H));
         }
     }

@@ -55,13 +55,16 @@ static inline uint32_t zh_bytes_per_block(uint32_t t) {
 static inline uint64_t zh_tensor_bytes(uint32_t t, uint64_t rows, uint64_t cols) {
     return rows * (cols / zh_block_size(t)) * zh_bytes_per_block(t);
 }
-static inline uint64_t zh_xq_bytes(uint32_t K) { return (uint64_t)(K / 32) * 108; }
+static inline uint64_t zh_xq_bytes_int(uint32_t K) { return (uint64_t)(K / 32) * 108; }
 
 // ---- raw-pointer launchers (stream = ctx->stream); validation done by callers
 int zhk_quantize_xq(zh_ctx *ctx, const float *x, void *xq, uint32_t K, uint32_t n_vec,
                     uint32_t x_stride);
 int zhk_dmmv(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, const void *xq, float *y, uint32_t M,
              uint32_t K, uint32_t acc);
+// Up to three stacked matrices sharing K and x (e.g. Q, K, V) in one launch.
+int zhk_dmmv_multi(zh_ctx *ctx, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, float *const *y,
+                   const uint32_t *M, const void *xq, uint32_t K);
 int zhk_dmmv_gate_up(zh_ctx *ctx, uint32_t qtype, const uint8_t *Wg, const uint8_t *Wu,
                      const void *xq, float *y, uint32_t M, uint32_t K);
 int zhk_dmmv_moe(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint64_t expert_stride,

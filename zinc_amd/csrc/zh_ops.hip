@@ -33,33 +33,48 @@ ZH_DEV uint32_t read_pos(zh_pos_src p) { return p.dev ? (*p.dev + p.value) : p.v
 // RMSNorm (rms_norm_mul.comp / cpuRmsNormMul forward.zig:618-626).
 // One 256-thread workgroup per group; optional XQ output for a DMMV consumer.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w,
-                                                  uint32_t w_len, float *__restrict__ out, uint8_t *xq,
-                                                  uint32_t n, float eps) {
-    const uint32_t g = blockIdx.x;
+// 1024 threads; every element a thread owns is loaded before any reduction so
+// the kernel pays one memory latency, not one per loop trip.
+constexpr int RMS_T = 1024, RMS_E = 8;  // up to 8192 elements per group in registers
+__global__ __launch_bounds__(RMS_T) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w,
+                                                    uint32_t w_len, float *__restrict__ out, uint8_t *xq,
+                                                    uint32_t n, float eps) {
+    const uint32_t g = blockIdx.x, t = threadIdx.x;
     const float *xg = x + (size_t)g * n;
-    __shared__ float red[4];
+    __shared__ float red[RMS_T / 64];
+    float v[RMS_E], wv[RMS_E];
+#pragma unroll
+    for (int j = 0; j < RMS_E; j++) {
+        uint32_t i = t + RMS_T * j;
+        v[j] = i < n ? xg[i] : 0.f;
+        wv[j] = i < n ? w[i % w_len] : 0.f;
+    }
     float sq = 0.f;
-    for (uint32_t i = threadIdx.x; i < n; i += 256) sq = fmaf(xg[i], xg[i], sq);
+#pragma unroll
+    for (int j = 0; j < RMS_E; j++) sq = fmaf(v[j], v[j], sq);
     sq = wave_sum(sq);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+    if ((t & 63) == 0) red[t >> 6] = sq;
     __syncthreads();
-    float tot = red[0] + red[1] + red[2] + red[3];
-    float rms_inv = 1.0f / sqrtf(tot / (float)n + eps);
-    XQView v = xq_view(xq, n / 32);
-    for (uint32_t i = threadIdx.x; i < ((n + 255) & ~255u); i += 256) {
-        float o = 0.f;
-        if (i < n) {
-            o = w[i % w_len] * (xg[i] * rms_inv);
-            out[(size_t)g * n + i] = o;
-        }
-        if (xq && i < n) xq_store_block32(o, threadIdx.x & 31, v, (g * n + i) / 32);
+    float tot = 0.f;
+#pragma unroll
+    for (int k = 0; k < RMS_T / 64; k++) tot += red[k];
+    const float rms_inv = 1.0f / sqrtf(tot / (float)n + eps);
+    XQView q = xq_view(xq, n / 32);
+#pragma unroll
+    for (int j = 0; j < RMS_E; j++) {
+        uint32_t i = t + RMS_T * j;
+        if (RMS_T * j >= n) break;  // uniform across the workgroup
+        float o = wv[j] * (v[j] * rms_inv);
+        if (i < n) out[(size_t)g * n + i] = o;
+        if (xq && i < n) xq_store_block32(o, t & 31, q, (g * n + i) / 32);
     }
 }
 
 int zhk_rms_norm(zh_ctx *c, const float *x, const float *w, uint32_t w_len, float *out, void *xq, uint32_t n,
                  uint32_t n_groups, float eps) {
-    hipLaunchKernelGGL(k_rms_norm, dim3(n_groups), dim3(256), 0, c->stream, x, w, w_len, out, (uint8_t *)xq, n, eps);
+    if (n > RMS_T * RMS_E) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "rms_norm n=%u > %d", n, RMS_T * RMS_E);
+    if (xq && n % 32) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "rms_norm xq needs n %% 32 == 0");
+    hipLaunchKernelGGL(k_rms_norm, dim3(n_groups), dim3(RMS_T), 0, c->stream, x, w, w_len, out, (uint8_t *)xq, n, eps);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
 }
@@ -186,20 +201,25 @@ extern "C" int zh_qk_norm_rope_kv_write(zh_ctx *c, zh_buf *q, const zh_buf *qw, 
 constexpr int FD_THREADS = 256;
 constexpr int FD_MAXG = 8;     // q heads per kv head handled per workgroup
 constexpr int FD_HD = 128;     // head_dim supported by the fast kernel
+constexpr int FD_CMAX = 256;   // max tokens per chunk
+constexpr int FD_TPG = FD_CMAX / 32;  // tokens per 8-lane group in the score phase
+constexpr int FD_TPW = FD_CMAX / 4;   // tokens per wave in the PV phase
 
 static uint32_t fd_chunk(uint32_t max_seq, uint32_t nkv, int cus) {
-    // enough chunks that n_kv_heads * n_chunks covers ~2 waves of workgroups per CU
+    // enough chunks that n_kv_heads * n_chunks covers ~2 workgroups per CU
     uint32_t target = (uint32_t)cus * 2;
-    uint32_t C = 64;
-    while (C < 1024 && (uint64_t)((max_seq + C - 1) / C) * nkv > target) C *= 2;
+    uint32_t C = 32;
+    while (C < FD_CMAX && (uint64_t)((max_seq + C - 1) / C) * nkv > target) C *= 2;
     return C;
 }
 
 uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t hd, uint32_t max_seq) {
-    uint32_t C = 64;  // worst case (most chunks)
+    uint32_t C = 32;  // worst case (most chunks)
     return (uint64_t)nh * ((max_seq + C - 1) / C) * (hd + 2) * 4 + 256;
 }
 
+// Every global load a thread needs in a phase is issued before the phase's
+// arithmetic, so a workgroup pays ~3 memory latencies in total.
 __global__ __launch_bounds__(FD_THREADS) void k_flash_decode(const float *__restrict__ q,
                                                              const uint16_t *__restrict__ kc,
                                                              const uint16_t *__restrict__ vc,
@@ -212,49 +232,69 @@ __global__ __launch_bounds__(FD_THREADS) void k_flash_decode(const float *__rest
     const uint32_t seq_len = read_pos(seq_src);
     const uint32_t t0 = chunk * C;
     if (t0 >= seq_len) return;
-    const uint32_t t1 = min(t0 + C, seq_len), nt = t1 - t0;
+    const uint32_t nt = min(t0 + C, seq_len) - t0;
     __shared__ float qs[FD_MAXG][FD_HD];
-    __shared__ float sc[FD_MAXG][1024];
+    __shared__ float sc[FD_MAXG][FD_CMAX];
     __shared__ float ored[4][FD_MAXG][FD_HD];
-    __shared__ uint32_t tok_base[1024];
+    __shared__ uint32_t tok_base[FD_CMAX];
+    __shared__ float mh[FD_MAXG], lh[FD_MAXG];
     for (uint32_t i = tid; i < G * FD_HD; i += FD_THREADS)
         qs[i / FD_HD][i % FD_HD] = q[(size_t)(kvh * G + i / FD_HD) * FD_HD + i % FD_HD] * scale;
-    for (uint32_t i = tid; i < nt; i += FD_THREADS) {
-        uint32_t t = t0 + i, pg = t / 16;
+    if (tid < nt) {
+        uint32_t t = t0 + tid, pg = t / 16;
         uint32_t phys = (pg < n_pages) ? pages[pg] * 16 + t % 16 : 0;
-        if (phys >= cache_tokens) phys = 0;
-        tok_base[i] = phys;
+        tok_base[tid] = phys < cache_tokens ? phys : 0;
     }
     __syncthreads();
     const uint16_t *kh = kc + (size_t)kvh * cache_tokens * FD_HD;
     const uint16_t *vh = vc + (size_t)kvh * cache_tokens * FD_HD;
-    // Phase 1: scores. 8 lanes per token (16 dims each), 32 tokens per pass.
+    // Phase 1: scores. Group gi (8 lanes, 16 dims each) takes tokens gi + 32*j.
     {
-        const uint32_t sub = lane & 7, tl = (tid >> 3);
-        for (uint32_t i = tl; i < nt; i += FD_THREADS / 8) {
-            const u32x4 *kp = (const u32x4 *)(kh + (size_t)tok_base[i] * FD_HD + sub * 16);
-            u32x4 a = kp[0], b = kp[1];
-            uint32_t kw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const uint32_t sub = lane & 7, gi = tid >> 3;
+        u32x4 kr[FD_TPG][2];
+#pragma unroll
+        for (int j = 0; j < FD_TPG; j++) {
+            uint32_t i = gi + 32 * j;
+            if (i < nt) {
+                const u32x4 *kp = (const u32x4 *)(kh + (size_t)tok_base[i] * FD_HD + sub * 16);
+                kr[j][0] = kp[0];
+                kr[j][1] = kp[1];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FD_TPG; j++) {
+            uint32_t i = gi + 32 * j;
+            if (32 * j >= nt) break;  // uniform
+            uint32_t kw[8] = {kr[j][0].x, kr[j][0].y, kr[j][0].z, kr[j][0].w,
+                              kr[j][1].x, kr[j][1].y, kr[j][1].z, kr[j][1].w};
             float kf[16];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                kf[2 * j] = h2f(kw[j]);
-                kf[2 * j + 1] = h2f(kw[j] >> 16);
+            for (int e = 0; e < 8; e++) {
+                kf[2 * e] = h2f(kw[e]);
+                kf[2 * e + 1] = h2f(kw[e] >> 16);
             }
-            for (uint32_t g = 0; g < G; g++) {
+#pragma unroll
+            for (int g = 0; g < FD_MAXG; g++) {
+                if (g >= (int)G) break;
                 float s = 0.f;
 #pragma unroll
-                for (int j = 0; j < 16; j++) s = fmaf(qs[g][sub * 16 + j], kf[j], s);
+                for (int e = 0; e < 16; e++) s = fmaf(qs[g][sub * 16 + e], kf[e], s);
                 s += __shfl_xor(s, 1, 64);
                 s += __shfl_xor(s, 2, 64);
                 s += __shfl_xor(s, 4, 64);
-                if (sub == 0) sc[g][i] = s;
+                if (sub == 0 && i < nt) sc[g][i] = s;
             }
         }
     }
+    // Phase 3 loads (V) do not depend on the softmax: issue them now.
+    uint32_t vr[FD_TPW];
+#pragma unroll
+    for (int j = 0; j < FD_TPW; j++) {
+        uint32_t i = wave + 4 * j;
+        vr[j] = (i < nt) ? *(const uint32_t *)(vh + (size_t)tok_base[i] * FD_HD + 2 * lane) : 0u;
+    }
     __syncthreads();
     // Phase 2: per-head max / exp / sum over the chunk (one wave per head).
-    __shared__ float mh[FD_MAXG], lh[FD_MAXG];
     for (uint32_t g = wave; g < G; g += 4) {
         float m = -INFINITY;
         for (uint32_t i = lane; i < nt; i += 64) m = fmaxf(m, sc[g][i]);
@@ -269,20 +309,21 @@ __global__ __launch_bounds__(FD_THREADS) void k_flash_decode(const float *__rest
         if (lane == 0) { mh[g] = m; lh[g] = l; }
     }
     __syncthreads();
-    // Phase 3: O = sum_t p_t V_t. Lane owns dims {2*lane, 2*lane+1}; waves split tokens.
+    // Phase 3: O = sum_t p_t V_t over this wave's token slice; lane owns dims {2l, 2l+1}.
     float acc[FD_MAXG][2];
 #pragma unroll
     for (int g = 0; g < FD_MAXG; g++) acc[g][0] = acc[g][1] = 0.f;
-    for (uint32_t i = wave; i < nt; i += 4) {
-        uint32_t vv = *(const uint32_t *)(vh + (size_t)tok_base[i] * FD_HD + 2 * lane);
-        float v0 = h2f(vv), v1 = h2f(vv >> 16);
+#pragma unroll
+    for (int j = 0; j < FD_TPW; j++) {
+        uint32_t i = wave + 4 * j;
+        if (i >= nt) break;
+        float v0 = h2f(vr[j]), v1 = h2f(vr[j] >> 16);
 #pragma unroll
         for (int g = 0; g < FD_MAXG; g++) {
-            if (g < (int)G) {
-                float p = sc[g][i];
-                acc[g][0] = fmaf(p, v0, acc[g][0]);
-                acc[g][1] = fmaf(p, v1, acc[g][1]);
-            }
+            if (g >= (int)G) break;
+            float p = sc[g][i];
+            acc[g][0] = fmaf(p, v0, acc[g][0]);
+            acc[g][1] = fmaf(p, v1, acc[g][1]);
         }
     }
 #pragma unroll
@@ -301,27 +342,49 @@ __global__ __launch_bounds__(FD_THREADS) void k_flash_decode(const float *__rest
     }
 }
 
-// LSE merge: one 128-thread workgroup per q head.
-__global__ __launch_bounds__(FD_HD) void k_flash_merge(const float *__restrict__ part, uint32_t n_chunks, uint32_t C,
-                                                       zh_pos_src seq_src, float *__restrict__ out, uint8_t *xq) {
-    const uint32_t h = blockIdx.x, d = threadIdx.x;
+// LSE merge: one 256-thread workgroup per q head. Chunk statistics are read
+// in parallel, then each (dim, chunk-quarter) thread accumulates its share.
+__global__ __launch_bounds__(256) void k_flash_merge(const float *__restrict__ part, uint32_t n_chunks, uint32_t C,
+                                                     zh_pos_src seq_src, float *__restrict__ out, uint8_t *xq) {
+    const uint32_t h = blockIdx.x, tid = threadIdx.x;
     const uint32_t seq_len = read_pos(seq_src);
     const uint32_t nv = min(n_chunks, (seq_len + C - 1) / C);
     const float *pp = part + (size_t)h * n_chunks * (FD_HD + 2);
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < nv; c++) M = fmaxf(M, pp[c * (FD_HD + 2) + FD_HD]);
-    float L = 0.f, O = 0.f;
-    for (uint32_t c = 0; c < nv; c++) {
-        const float *pc = pp + c * (FD_HD + 2);
-        float w = expf(pc[FD_HD] - M);
-        L = fmaf(pc[FD_HD + 1], w, L);
-        O = fmaf(pc[d], w, O);
+    __shared__ float wsh[1024];
+    __shared__ float red[4];
+    __shared__ float osum[2][FD_HD];
+    // chunk maxima
+    float m = -INFINITY;
+    for (uint32_t c = tid; c < nv; c += 256) m = fmaxf(m, pp[c * (FD_HD + 2) + FD_HD]);
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float l = 0.f;
+    for (uint32_t c = tid; c < nv; c += 256) {
+        float w = expf(pp[c * (FD_HD + 2) + FD_HD] - M);
+        wsh[c] = w;
+        l = fmaf(pp[c * (FD_HD + 2) + FD_HD + 1], w, l);
     }
-    float o = L > 0.f ? O / L : 0.f;
-    out[(size_t)h * FD_HD + d] = o;
-    if (xq) {
-        XQView v = xq_view(xq, gridDim.x * FD_HD / 32);
-        xq_store_block32(o, d & 31, v, (h * FD_HD + d) / 32);
+    l = wave_sum(l);
+    if ((tid & 63) == 0) red[tid >> 6] = l;
+    __syncthreads();
+    const float L = red[0] + red[1] + red[2] + red[3];
+    // O: thread (d, half) sums chunks c = half, half+2, ...
+    const uint32_t d = tid & (FD_HD - 1), half = tid >> 7;
+    float O = 0.f;
+#pragma unroll 8
+    for (uint32_t c = half; c < nv; c += 2) O = fmaf(pp[c * (FD_HD + 2) + d], wsh[c], O);
+    osum[half][d] = O;
+    __syncthreads();
+    if (tid < FD_HD) {
+        float o = L > 0.f ? (osum[0][tid] + osum[1][tid]) / L : 0.f;
+        out[(size_t)h * FD_HD + tid] = o;
+        if (xq) {
+            XQView v = xq_view(xq, gridDim.x * FD_HD / 32);
+            xq_store_block32(o, tid & 31, v, (h * FD_HD + tid) / 32);
+        }
     }
 }
 
@@ -334,7 +397,8 @@ int zhk_flash_decode(zh_ctx *c, const float *q, const uint16_t *kc, const uint16
     hipLaunchKernelGGL(k_flash_decode, dim3(nkv, n_chunks), dim3(FD_THREADS), 0, c->stream, q, kc, vc, pages, n_pages,
                        cache_tokens, G, C, n_chunks, seq_len, scale, partials);
     ZH_LAUNCH_CHECK(c);
-    hipLaunchKernelGGL(k_flash_merge, dim3(nh), dim3(FD_HD), 0, c->stream, (const float *)partials, n_chunks, C,
+    if (n_chunks > 1024) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "context too long for merge (%u chunks)", n_chunks);
+    hipLaunchKernelGGL(k_flash_merge, dim3(nh), dim3(256), 0, c->stream, (const float *)partials, n_chunks, C,
                        seq_len, out, (uint8_t *)xq_out);
     ZH_LAUNCH_CHECK(c);
     (void)hd;

@@ -11,7 +11,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libzinc_hip.so")
+LIB_PATH = os.environ.get("ZH_LIB_PATH") or os.path.join(HERE, "libzinc_hip.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K, MXFP4 = 0, 1, 8, 12, 14, 39
 OK = 0
@@ -60,11 +60,17 @@ SIGNATURES = {
     "zh_buf_fill_u8": (_i32, [_P, _P, _u64, C.c_uint8, _u64]),
     "zh_event_record": (_i32, [_P, _i32]),
     "zh_event_elapsed_ms": (_i32, [_P, _i32, _i32, C.POINTER(_f32)]),
+    "zh_stream_read_probe": (_i32, [_P, _P, _u64, _u32, C.POINTER(_f32)]),
+    "zh_dispatch_overhead": (_i32, [_P, _u32, _u32, _i32, C.POINTER(_f32)]),
     "zh_synth_tensor": (_i32, [_P, _P, _u64, _u32, _u64, _u64, _u64, _u64]),
     "zh_synth_vector": (_i32, [_P, _P, _u64, _u32, _u64, _f32, _u64, _u64]),
     "zh_dmmv": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _u32, _u32, _u32]),
     "zh_dmmv_fused_gate_up_swiglu": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _P, _u64, _u32, _u32]),
     "zh_dmmv_moe": (_i32, [_P, _u32, _P, _u64, _P, _P, _u32, _u64, _P, _u64, _u32, _u32, _u32]),
+    "zh_xq_bytes": (_u64, [_u32]),
+    "zh_quantize_activation": (_i32, [_P, _P, _u64, _u32, _u32, _u32, _P, _u64]),
+    "zh_dmmv_xq": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _u32, _u32, _u32]),
+    "zh_dmmv_fused_gate_up_swiglu_xq": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _P, _u64, _u32, _u32]),
     "zh_dequant_rows": (_i32, [_P, _u32, _P, _u64, _u32, _u32, _u32, _P, _u64]),
     "zh_rms_norm": (_i32, [_P, _P, _u64, _P, _u32, _P, _u64, _u32, _u32, _f32]),
     "zh_swiglu": (_i32, [_P, _P, _u64, _P, _u64, _P, _u64, _u32]),
@@ -200,6 +206,16 @@ class Context:
         self.check(lib().zh_event_elapsed_ms(self.h, a, b, C.byref(ms)))
         return ms.value
 
+    def stream_read_probe(self, buf, nbytes, iters=20):
+        g = C.c_float()
+        self.check(lib().zh_stream_read_probe(self.h, buf.h, nbytes, iters, C.byref(g)))
+        return g.value
+
+    def dispatch_overhead(self, n_kernels=500, wgs=1, use_graph=True):
+        us = C.c_float()
+        self.check(lib().zh_dispatch_overhead(self.h, n_kernels, wgs, int(use_graph), C.byref(us)))
+        return us.value
+
     # ---- ops (thin wrappers; argument meaning as include/zinc_hip.h) ----
     def synth_tensor(self, buf, offset, qtype, rows, cols, seed, stream):
         self.check(lib().zh_synth_tensor(self.h, buf.h, offset, qtype, rows, cols, seed, stream))
@@ -217,6 +233,19 @@ class Context:
     def dmmv_moe(self, qtype, W, expert_stride, routing, x, x_expert_stride, x_off, y, y_off, M, K, n_used):
         self.check(lib().zh_dmmv_moe(self.h, qtype, W.h, expert_stride, routing.h, x.h, x_expert_stride, x_off,
                                      y.h, y_off, M, K, n_used))
+
+    def xq_bytes(self, K):
+        return lib().zh_xq_bytes(K)
+
+    def quantize_activation(self, x, x_off, K, xq, xq_off=0, n_vec=1, x_stride=0):
+        self.check(lib().zh_quantize_activation(self.h, x.h, x_off, K, n_vec, x_stride, xq.h, xq_off))
+
+    def dmmv_xq(self, qtype, W, a_off, xq, xq_off, y, y_off, M, K, acc_mode=0):
+        self.check(lib().zh_dmmv_xq(self.h, qtype, W.h, a_off, xq.h, xq_off, y.h, y_off, M, K, acc_mode))
+
+    def dmmv_fused_gate_up_swiglu_xq(self, qtype, Wg, g_off, Wu, u_off, xq, xq_off, y, y_off, M, K):
+        self.check(lib().zh_dmmv_fused_gate_up_swiglu_xq(self.h, qtype, Wg.h, g_off, Wu.h, u_off, xq.h, xq_off,
+                                                         y.h, y_off, M, K))
 
     def dequant_rows(self, qtype, W, a_off, row0, n_rows, K, out, out_off=0):
         self.check(lib().zh_dequant_rows(self.h, qtype, W.h, a_off, row0, n_rows, K, out.h, out_off))
