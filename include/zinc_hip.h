@@ -73,6 +73,9 @@ int zh_stream_read_probe(zh_ctx *ctx, const zh_buf *buf, uint64_t bytes, uint32_
 /* n_kernels empty launches of `wgs` workgroups, in a hipGraph (use_graph) or
  * as plain launches: average microseconds per kernel. */
 int zh_dispatch_overhead(zh_ctx *ctx, uint32_t n_kernels, uint32_t wgs, int use_graph, float *us_per_kernel);
+/* Cost of one device-wide barrier in a cooperative grid of wgs_per_cu
+ * 256-thread workgroups per CU (bounded spin; fails rather than hangs). */
+int zh_grid_barrier_probe(zh_ctx *ctx, uint32_t n_barriers, uint32_t wgs_per_cu, float *us_per_barrier);
 
 /* ---- synthetic data (seeded, bit-identical to oracle/zinc_oracle.c) ----- */
 /* Fill rows x cols of `qtype` blocks at `offset` per the BASELINE distributions.

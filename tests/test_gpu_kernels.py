@@ -40,17 +40,17 @@ NOISE = 1e-6
 
 
 def assert_dot_close(got, ref32, ref64, mag, what):
-    """Parity bar for DMMV-like outputs. A row passes if it is within the
-    north-star tolerance of the oracle (f32 serial dot, the reference's CPU
-    path). Rows where the oracle's own rounding already uses more than half of
-    that tolerance against the exact (f64) dot -- cancellation,
-    |y| << sum|w x| -- are judged against the exact value with the same
-    tolerance plus NOISE * sum|w x|."""
+    """Parity bar for DMMV-like outputs: every row within the north-star
+    tolerance of the oracle (f32 serial dot, the reference's CPU path),
+    |gpu - ref| <= 1e-4 + 1e-3*|ref|, widened by the f32 rounding floor of a
+    dot product, NOISE * sum_i |w_i x_i| (~16 unit roundoffs). The floor only
+    matters for cancelling rows (|y| << sum|w x|), where any two f32 summation
+    orders -- including the reference's own serial loop versus the exact
+    value -- already differ by more than 1e-4 + 1e-3*|y|."""
     got = got.astype(np.float64)
-    ok1 = np.abs(got - ref32) <= ATOL + RTOL * np.abs(ref32)
-    ill = np.abs(ref32 - ref64) > 0.5 * (ATOL + RTOL * np.abs(ref64))
-    ok2 = ill & (np.abs(got - ref64) <= ATOL + RTOL * np.abs(ref64) + NOISE * mag)
-    bad = np.nonzero(~(ok1 | ok2))[0]
+    ok1 = np.abs(got - ref32) <= ATOL + RTOL * np.abs(ref32) + NOISE * mag
+    ok2 = np.abs(got - ref64) <= ATOL + RTOL * np.abs(ref64) + NOISE * mag
+    bad = np.nonzero(~(ok1 & ok2))[0]
     assert len(bad) == 0, (f"{what}: {len(bad)}/{len(got)} rows outside tol; idx {bad[:5]} got {got[bad[:5]]} "
                            f"ref32 {ref32[bad[:5]]} ref64 {ref64[bad[:5]]} mag {mag[bad[:5]]}")
     return int((~ok1).sum())
@@ -116,6 +116,7 @@ def run_dmmv(ctx, orc, qtype, M, K, seed, acc=False, a_off=0):
 
 @pytest.mark.parametrize("qtype,M,K", [
     (12, 4096, 4096),     # config 1
+    (12, 256, 512), (12, 1000, 768), (12, 12288, 4096), (14, 2000, 4096), (14, 4096, 12288),
     (12, 257, 512), (12, 33, 768), (12, 100, 2048), (12, 64, 12288),
     (14, 257, 512), (14, 512, 4096), (14, 64, 12288), (14, 40, 768),
     (8, 257, 4096), (8, 128, 2048), (8, 16, 768),

@@ -646,6 +646,14 @@ extern "C" int zh_dmmv(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a_of
     if ((a_off & 3) || (x_off & 3) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "offsets must be 4-byte aligned");
     if (qtype == ZH_Q4_K && (a_off & 15)) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "Q4_K a_off must be 16-byte aligned");
+    if (zhk_lpb_supported(qtype, K) && (x_off & 15) == 0 && !getenv("ZH_NO_LPB")) {
+        const uint8_t *w = (const uint8_t *)W->ptr + a_off;
+        float *yy = (float *)((char *)y->ptr + y_off);
+        int R = 2;
+        if (M % R == 0)
+            return zhk_dmmv_lpb(c, qtype, 0, 1, &w, nullptr, &yy, &M, (const float *)((const char *)x->ptr + x_off),
+                                nullptr, 0.f, nullptr, K, acc_mode);
+    }
     void *xq;
     if ((rc = zh_scratch(c, zh_xq_bytes_int(K), &xq))) return rc;
     if ((rc = zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), xq, K, 1, 0))) return rc;
@@ -675,6 +683,12 @@ extern "C" int zh_dmmv_xq(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a
     if (!in_range(W, a_off, zh_tensor_bytes(qtype, M, K)) || !in_range(xq, xq_off, zh_xq_bytes_int(K)) ||
         !in_range(y, y_off, 4ull * M) || (a_off & (qtype == ZH_Q4_K ? 15 : 3)) || (xq_off & 15) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "range/alignment");
+    if (zhk_lpb_supported(qtype, K) && !getenv("ZH_NO_LPB")) {
+        const uint8_t *w = (const uint8_t *)W->ptr + a_off;
+        float *yy = (float *)((char *)y->ptr + y_off);
+        return zhk_dmmv_lpb(c, qtype, 0, 1, &w, nullptr, &yy, &M, nullptr, nullptr, 0.f, nullptr, K, acc_mode,
+                            (const char *)xq->ptr + xq_off);
+    }
     return zhk_dmmv(c, qtype, (const uint8_t *)W->ptr + a_off, (const char *)xq->ptr + xq_off,
                     (float *)((char *)y->ptr + y_off), M, K, acc_mode);
 }
@@ -689,6 +703,12 @@ extern "C" int zh_dmmv_fused_gate_up_swiglu_xq(zh_ctx *c, uint32_t qtype, const 
     if (M == 0 || !in_range(Wg, g_off, wb) || !in_range(Wu, u_off, wb) || !in_range(xq, xq_off, zh_xq_bytes_int(K)) ||
         !in_range(y, y_off, 4ull * M) || (g_off & 15) || (u_off & 15) || (xq_off & 15) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "range/alignment");
+    if (qtype == ZH_Q4_K && zhk_lpb_supported(qtype, K) && !getenv("ZH_NO_LPB")) {
+        const uint8_t *wg = (const uint8_t *)Wg->ptr + g_off;
+        float *yy = (float *)((char *)y->ptr + y_off);
+        return zhk_dmmv_lpb(c, qtype, 1, 1, &wg, (const uint8_t *)Wu->ptr + u_off, &yy, &M, nullptr, nullptr, 0.f,
+                            nullptr, K, 0, (const char *)xq->ptr + xq_off);
+    }
     return zhk_dmmv_gate_up(c, qtype, (const uint8_t *)Wg->ptr + g_off, (const uint8_t *)Wu->ptr + u_off,
                             (const char *)xq->ptr + xq_off, (float *)((char *)y->ptr + y_off), M, K);
 }
@@ -705,6 +725,12 @@ extern "C" int zh_dmmv_fused_gate_up_swiglu(zh_ctx *c, uint32_t qtype, const zh_
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "buffer too small for M=%u K=%u", M, K);
     if ((g_off & 15) || (u_off & 15) || (x_off & 3) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "misaligned offsets");
+    if (qtype == ZH_Q4_K && zhk_lpb_supported(qtype, K) && (x_off & 15) == 0 && !getenv("ZH_NO_LPB")) {
+        const uint8_t *wg = (const uint8_t *)Wg->ptr + g_off;
+        float *yy = (float *)((char *)y->ptr + y_off);
+        return zhk_dmmv_lpb(c, qtype, 1, 1, &wg, (const uint8_t *)Wu->ptr + u_off, &yy, &M,
+                            (const float *)((const char *)x->ptr + x_off), nullptr, 0.f, nullptr, K, 0);
+    }
     void *xq;
     if ((rc = zh_scratch(c, zh_xq_bytes_int(K), &xq))) return rc;
     if ((rc = zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), xq, K, 1, 0))) return rc;

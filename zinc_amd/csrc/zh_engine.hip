@@ -11,6 +11,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <stdlib.h>
+
 #include <map>
 #include <vector>
 
@@ -138,7 +140,7 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
     *out = nullptr;
     const zh_model_config &c = *cfg;
     if (c.n_layers == 0 || c.hidden % 256 || c.head_dim != 128 || c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads ||
-        c.n_heads / c.n_kv_heads > 8 || c.vocab == 0 || c.max_ctx == 0 || c.max_ctx % 16)
+        c.n_heads / c.n_kv_heads > 8 || ((c.n_heads / c.n_kv_heads) & (c.n_heads / c.n_kv_heads - 1)) || c.vocab == 0 || c.max_ctx == 0 || c.max_ctx % 16)
         return zh_set_err(ctx, ZH_ERR_INVALID_ARGUMENT, "unsupported model shape");
     if (c.n_experts == 0 && (c.ffn == 0 || c.ffn % 256))
         return zh_set_err(ctx, ZH_ERR_INVALID_ARGUMENT, "ffn must be a positive multiple of 256");
@@ -301,10 +303,23 @@ static int record_step(zh_engine *e, bool collect) {
     const float scale = 1.0f / sqrtf((float)hd);
     // embedToken (forward.zig:4255-4290), on the device.
     ERC(zhk_dequant_rows(c, m.type_embd, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
+    const bool lpb = !getenv("ZH_NO_LPB");
+    const bool lpb_attn = lpb && zhk_lpb_supported(m.type_attn, H) && zhk_lpb_supported(m.type_attn, qd) &&
+                          qd % 2 == 0 && kvd % 2 == 0;
+    const bool lpb_ffn = lpb && m.n_experts == 0 && m.type_ffn_gate_up == ZH_Q4_K &&
+                         zhk_lpb_supported(ZH_Q4_K, H) && zhk_lpb_supported(m.type_ffn_down, m.ffn);
+    const bool lpb_head = lpb && zhk_lpb_supported(m.type_lm_head, H) && m.vocab % 2 == 0;
     for (uint32_t l = 0; l < m.n_layers; l++) {
         const Layer &y = e->L[l];
-        ERC(zhk_rms_norm(c, e->hidden, Wf(y.attn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
-        {
+        if (lpb_attn) {
+            // attn_norm fused into the Q/K/V mat-vec (every workgroup normalises x)
+            const uint8_t *ws[3] = {W(y.wq), W(y.wk), W(y.wv)};
+            float *ys[3] = {e->q, e->k, e->v};
+            const uint32_t ms[3] = {qd, kvd, kvd};
+            ERC(zhk_dmmv_lpb(c, m.type_attn, 0, 3, ws, nullptr, ys, ms, e->hidden, Wf(y.attn_norm), m.eps, nullptr,
+                             H, 0));
+        } else {
+            ERC(zhk_rms_norm(c, e->hidden, Wf(y.attn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
             const uint8_t *ws[3] = {W(y.wq), W(y.wk), W(y.wv)};
             float *ys[3] = {e->q, e->k, e->v};
             const uint32_t ms[3] = {qd, kvd, kvd};
@@ -314,7 +329,30 @@ static int record_step(zh_engine *e, bool collect) {
                                 e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd, pos, m.eps));
         ERC(zhk_flash_decode(c, e->q, y.kc, y.vc, e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads,
                              m.n_kv_heads, hd, seq, m.max_ctx, scale, e->fd_part));
-        ERC(zhk_dmmv(c, m.type_attn, W(y.wo), e->xq_q, e->hidden, H, qd, 1));
+        if (lpb_attn) {
+            // the merge kernel already emitted the attention output as XQ
+            const uint8_t *wo = W(y.wo);
+            float *yo = e->hidden;
+            const uint32_t mo = H;
+            ERC(zhk_dmmv_lpb(c, m.type_attn, 0, 1, &wo, nullptr, &yo, &mo, nullptr, nullptr, 0.f, nullptr, qd, 1,
+                             e->xq_q));
+        } else {
+            ERC(zhk_dmmv(c, m.type_attn, W(y.wo), e->xq_q, e->hidden, H, qd, 1));
+        }
+        if (lpb_ffn) {
+            // ffn_norm fused into gate/up; SwiGLU fused into its epilogue
+            const uint8_t *wg = W(y.gate);
+            float *ys = e->s;
+            const uint32_t mf = m.ffn;
+            ERC(zhk_dmmv_lpb(c, ZH_Q4_K, 1, 1, &wg, W(y.up), &ys, &mf, e->hidden, Wf(y.ffn_norm), m.eps, nullptr, H,
+                             0));
+            // down: K = ffn is large and M = hidden small, so per-workgroup
+            // staging of x would dominate; quantise once and use the
+            // 64-element-unit kernel, which measures fastest at this shape.
+            ERC(zhk_quantize_xq(c, e->s, e->xq_f, m.ffn, 1, 0));
+            ERC(zhk_dmmv(c, m.type_ffn_down, W(y.down), e->xq_f, e->hidden, H, m.ffn, 1));
+            continue;
+        }
         ERC(zhk_rms_norm(c, e->hidden, Wf(y.ffn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
         if (m.n_experts == 0) {
             ERC(zhk_dmmv_gate_up(c, m.type_ffn_gate_up, W(y.gate), W(y.up), e->xq_h, e->s, m.ffn, H));
@@ -333,8 +371,16 @@ static int record_step(zh_engine *e, bool collect) {
         }
     }
     if (collect) {
-        ERC(zhk_rms_norm(c, e->hidden, Wf(e->out_norm), H, e->norm, e->xq_h, H, 1, m.eps));
-        ERC(zhk_dmmv(c, m.type_lm_head, W(e->lm), e->xq_h, e->logits, m.vocab, H, 0));
+        if (lpb_head) {
+            const uint8_t *wl = W(e->lm);
+            float *yl = e->logits;
+            const uint32_t mv = m.vocab;
+            ERC(zhk_dmmv_lpb(c, m.type_lm_head, 0, 1, &wl, nullptr, &yl, &mv, e->hidden, Wf(e->out_norm), m.eps,
+                             nullptr, H, 0));
+        } else {
+            ERC(zhk_rms_norm(c, e->hidden, Wf(e->out_norm), H, e->norm, e->xq_h, H, 1, m.eps));
+            ERC(zhk_dmmv(c, m.type_lm_head, W(e->lm), e->xq_h, e->logits, m.vocab, H, 0));
+        }
         ERC(zhk_argmax(c, e->logits, m.vocab, e->st + ST_TOKEN_OUT, e->am_part, e->ring, e->st + ST_GEN));
     }
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, c->stream, e->st, (const uint32_t *)e->prompt);

@@ -97,3 +97,11 @@ int zhk_moe_weighted_acc(zh_ctx *ctx, float *a, const float *b, const uint32_t *
                          uint32_t n_used, uint32_t src_stride);
 int zhk_argmax(zh_ctx *ctx, const float *logits, uint32_t n, uint32_t *result, uint32_t *partials,
                uint32_t *token_ring, const uint32_t *ring_index);
+
+// Lane-per-block K-quant DMMV (zh_dmmv_lpb.hip): stages f32 x (optionally
+// RMS-normalised with norm_w) into LDS itself. mode 0: plain (up to 3 stacked
+// matrices), mode 1: fused gate/up/SwiGLU (Q4_K, W = gate, W2 = up).
+bool zhk_lpb_supported(uint32_t qtype, uint32_t K);
+int zhk_dmmv_lpb(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
+                 float *const *y, const uint32_t *M, const float *x, const float *norm_w, float eps,
+                 float *normed_out, uint32_t K, uint32_t acc, const void *xq = nullptr);

@@ -198,147 +198,128 @@ extern "C" int zh_qk_norm_rope_kv_write(zh_ctx *c, zh_buf *q, const zh_buf *qw, 
 // A merge kernel combines chunks with log-sum-exp weights.
 // Cache layout [kv_head][token][head_dim] fp16, read through 16-token pages.
 // ---------------------------------------------------------------------------
-constexpr int FD_THREADS = 256;
-constexpr int FD_MAXG = 8;     // q heads per kv head handled per workgroup
-constexpr int FD_HD = 128;     // head_dim supported by the fast kernel
-constexpr int FD_CMAX = 256;   // max tokens per chunk
-constexpr int FD_TPG = FD_CMAX / 32;  // tokens per 8-lane group in the score phase
-constexpr int FD_TPW = FD_CMAX / 4;   // tokens per wave in the PV phase
-
-static uint32_t fd_chunk(uint32_t max_seq, uint32_t nkv, int cus) {
-    // enough chunks that n_kv_heads * n_chunks covers ~2 workgroups per CU
-    uint32_t target = (uint32_t)cus * 2;
-    uint32_t C = 32;
-    while (C < FD_CMAX && (uint64_t)((max_seq + C - 1) / C) * nkv > target) C *= 2;
-    return C;
-}
+constexpr int FD_MAXG = 8;     // q heads per kv head (GQA group) handled per wave
+constexpr int FD_HD = 128;     // head_dim supported by the kernel
+constexpr int FD_T = 32;       // tokens per chunk; one wave per (kv head, chunk)
 
 uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t hd, uint32_t max_seq) {
-    uint32_t C = 32;  // worst case (most chunks)
-    return (uint64_t)nh * ((max_seq + C - 1) / C) * (hd + 2) * 4 + 256;
+    return (uint64_t)nh * ((max_seq + FD_T - 1) / FD_T) * (hd + 2) * 4 + 256;
 }
 
-// Every global load a thread needs in a phase is issued before the phase's
-// arithmetic, so a workgroup pays ~3 memory latencies in total.
-__global__ __launch_bounds__(FD_THREADS) void k_flash_decode(const float *__restrict__ q,
-                                                             const uint16_t *__restrict__ kc,
-                                                             const uint16_t *__restrict__ vc,
-                                                             const uint32_t *__restrict__ pages, uint32_t n_pages,
-                                                             uint32_t cache_tokens, uint32_t G, uint32_t C,
-                                                             uint32_t n_chunks, zh_pos_src seq_src, float scale,
-                                                             float *__restrict__ part) {
-    const uint32_t kvh = blockIdx.x, chunk = blockIdx.y, tid = threadIdx.x;
-    const uint32_t lane = tid & 63, wave = tid >> 6;
+// One wave = one (kv head, 32-token chunk): all K and V loads are issued up
+// front (16 KB per wave, one memory latency), scores use 8 lanes per token
+// (16 dims each), the chunk softmax stays in registers, and P*V runs with
+// lane = 2 output dims. Writes unnormalised O, chunk max m and sum l per q head.
+template <int G>
+__global__ __launch_bounds__(64) void k_flash_decode(const float *__restrict__ q, const uint16_t *__restrict__ kc,
+                                                     const uint16_t *__restrict__ vc,
+                                                     const uint32_t *__restrict__ pages, uint32_t n_pages,
+                                                     uint32_t cache_tokens, uint32_t n_chunks, zh_pos_src seq_src,
+                                                     float scale, float *__restrict__ part) {
+    const uint32_t kvh = blockIdx.x, chunk = blockIdx.y, lane = threadIdx.x;
     const uint32_t seq_len = read_pos(seq_src);
-    const uint32_t t0 = chunk * C;
+    const uint32_t t0 = chunk * FD_T;
     if (t0 >= seq_len) return;
-    const uint32_t nt = min(t0 + C, seq_len) - t0;
-    __shared__ float qs[FD_MAXG][FD_HD];
-    __shared__ float sc[FD_MAXG][FD_CMAX];
-    __shared__ float ored[4][FD_MAXG][FD_HD];
-    __shared__ uint32_t tok_base[FD_CMAX];
-    __shared__ float mh[FD_MAXG], lh[FD_MAXG];
-    for (uint32_t i = tid; i < G * FD_HD; i += FD_THREADS)
-        qs[i / FD_HD][i % FD_HD] = q[(size_t)(kvh * G + i / FD_HD) * FD_HD + i % FD_HD] * scale;
-    if (tid < nt) {
-        uint32_t t = t0 + tid, pg = t / 16;
-        uint32_t phys = (pg < n_pages) ? pages[pg] * 16 + t % 16 : 0;
-        tok_base[tid] = phys < cache_tokens ? phys : 0;
-    }
-    __syncthreads();
+    const uint32_t nt = min(t0 + FD_T, seq_len) - t0;
+    const uint32_t sub = lane & 7, grp = lane >> 3;
     const uint16_t *kh = kc + (size_t)kvh * cache_tokens * FD_HD;
     const uint16_t *vh = vc + (size_t)kvh * cache_tokens * FD_HD;
-    // Phase 1: scores. Group gi (8 lanes, 16 dims each) takes tokens gi + 32*j.
-    {
-        const uint32_t sub = lane & 7, gi = tid >> 3;
-        u32x4 kr[FD_TPG][2];
+    auto phys_of = [&](uint32_t i) -> uint32_t {
+        uint32_t t = t0 + (i < nt ? i : nt - 1), pg = t / 16;
+        uint32_t ph = (pg < n_pages) ? pages[pg] * 16 + t % 16 : 0;
+        return ph < cache_tokens ? ph : 0;
+    };
+    // K: pass j covers tokens 8j + grp; lane reads dims sub*16 .. +15 (32 B)
+    u32x4 kr[FD_T / 8][2];
 #pragma unroll
-        for (int j = 0; j < FD_TPG; j++) {
-            uint32_t i = gi + 32 * j;
-            if (i < nt) {
-                const u32x4 *kp = (const u32x4 *)(kh + (size_t)tok_base[i] * FD_HD + sub * 16);
-                kr[j][0] = kp[0];
-                kr[j][1] = kp[1];
-            }
-        }
+    for (int j = 0; j < FD_T / 8; j++) {
+        const u32x4 *kp = (const u32x4 *)(kh + (size_t)phys_of(8 * j + grp) * FD_HD + sub * 16);
+        kr[j][0] = kp[0];
+        kr[j][1] = kp[1];
+    }
+    // V: token i, dims 2*lane, 2*lane+1
+    uint32_t vr[FD_T];
 #pragma unroll
-        for (int j = 0; j < FD_TPG; j++) {
-            uint32_t i = gi + 32 * j;
-            if (32 * j >= nt) break;  // uniform
-            uint32_t kw[8] = {kr[j][0].x, kr[j][0].y, kr[j][0].z, kr[j][0].w,
-                              kr[j][1].x, kr[j][1].y, kr[j][1].z, kr[j][1].w};
-            float kf[16];
+    for (int i = 0; i < FD_T; i++) vr[i] = *(const uint32_t *)(vh + (size_t)phys_of(i) * FD_HD + 2 * lane);
+    // q for this lane's 16 dims, pre-scaled
+    float qf[G][16];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                kf[2 * e] = h2f(kw[e]);
-                kf[2 * e + 1] = h2f(kw[e] >> 16);
-            }
+    for (int g = 0; g < G; g++) {
+        const f32x4 *qp = (const f32x4 *)(q + (size_t)(kvh * G + g) * FD_HD + sub * 16);
 #pragma unroll
-            for (int g = 0; g < FD_MAXG; g++) {
-                if (g >= (int)G) break;
-                float s = 0.f;
-#pragma unroll
-                for (int e = 0; e < 16; e++) s = fmaf(qs[g][sub * 16 + e], kf[e], s);
-                s += __shfl_xor(s, 1, 64);
-                s += __shfl_xor(s, 2, 64);
-                s += __shfl_xor(s, 4, 64);
-                if (sub == 0 && i < nt) sc[g][i] = s;
-            }
+        for (int e4 = 0; e4 < 4; e4++) {
+            f32x4 t = qp[e4];
+            qf[g][4 * e4 + 0] = t.x * scale; qf[g][4 * e4 + 1] = t.y * scale;
+            qf[g][4 * e4 + 2] = t.z * scale; qf[g][4 * e4 + 3] = t.w * scale;
         }
     }
-    // Phase 3 loads (V) do not depend on the softmax: issue them now.
-    uint32_t vr[FD_TPW];
+    // scores s[j][g] for token 8j + grp (replicated over the 8 lanes of grp)
+    float sc[FD_T / 8][G];
 #pragma unroll
-    for (int j = 0; j < FD_TPW; j++) {
-        uint32_t i = wave + 4 * j;
-        vr[j] = (i < nt) ? *(const uint32_t *)(vh + (size_t)tok_base[i] * FD_HD + 2 * lane) : 0u;
+    for (int j = 0; j < FD_T / 8; j++) {
+        uint32_t kw[8] = {kr[j][0].x, kr[j][0].y, kr[j][0].z, kr[j][0].w,
+                          kr[j][1].x, kr[j][1].y, kr[j][1].z, kr[j][1].w};
+        float kf[16];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            kf[2 * e] = h2f(kw[e]);
+            kf[2 * e + 1] = h2f(kw[e] >> 16);
+        }
+        const bool valid = (uint32_t)(8 * j) + grp < nt;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float s = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; e++) s = fmaf(qf[g][e], kf[e], s);
+            s += __shfl_xor(s, 1, 64);
+            s += __shfl_xor(s, 2, 64);
+            s += __shfl_xor(s, 4, 64);
+            sc[j][g] = valid ? s : -INFINITY;
+        }
     }
-    __syncthreads();
-    // Phase 2: per-head max / exp / sum over the chunk (one wave per head).
-    for (uint32_t g = wave; g < G; g += 4) {
-        float m = -INFINITY;
-        for (uint32_t i = lane; i < nt; i += 64) m = fmaxf(m, sc[g][i]);
-        m = wave_max(m);
+    // chunk softmax per head: max and sum over passes and the 8 groups
+    __shared__ float ps[G][FD_T];
+    float mx[G], ls[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float m = sc[0][g];
+#pragma unroll
+        for (int j = 1; j < FD_T / 8; j++) m = fmaxf(m, sc[j][g]);
+        m = fmaxf(m, __shfl_xor(m, 8, 64));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
         float l = 0.f;
-        for (uint32_t i = lane; i < nt; i += 64) {
-            float p = expf(sc[g][i] - m);
-            sc[g][i] = p;
+#pragma unroll
+        for (int j = 0; j < FD_T / 8; j++) {
+            float p = expf(sc[j][g] - m);  // exp(-inf) = 0 for invalid tokens
+            if (sub == 0) ps[g][8 * j + grp] = p;
             l += p;
         }
-        l = wave_sum(l);
-        if (lane == 0) { mh[g] = m; lh[g] = l; }
+        l += __shfl_xor(l, 8, 64);
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        mx[g] = m;
+        ls[g] = l;
     }
-    __syncthreads();
-    // Phase 3: O = sum_t p_t V_t over this wave's token slice; lane owns dims {2l, 2l+1}.
-    float acc[FD_MAXG][2];
+    __syncthreads();  // single wave: orders the LDS probability writes
+    float acc[G][2];
 #pragma unroll
-    for (int g = 0; g < FD_MAXG; g++) acc[g][0] = acc[g][1] = 0.f;
+    for (int g = 0; g < G; g++) acc[g][0] = acc[g][1] = 0.f;
 #pragma unroll
-    for (int j = 0; j < FD_TPW; j++) {
-        uint32_t i = wave + 4 * j;
-        if (i >= nt) break;
-        float v0 = h2f(vr[j]), v1 = h2f(vr[j] >> 16);
+    for (int i = 0; i < FD_T; i++) {
+        const float v0 = h2f(vr[i]), v1 = h2f(vr[i] >> 16);
 #pragma unroll
-        for (int g = 0; g < FD_MAXG; g++) {
-            if (g >= (int)G) break;
-            float p = sc[g][i];
+        for (int g = 0; g < G; g++) {
+            const float p = ps[g][i];
             acc[g][0] = fmaf(p, v0, acc[g][0]);
             acc[g][1] = fmaf(p, v1, acc[g][1]);
         }
     }
 #pragma unroll
-    for (int g = 0; g < FD_MAXG; g++)
-        if (g < (int)G) {
-            ored[wave][g][2 * lane] = acc[g][0];
-            ored[wave][g][2 * lane + 1] = acc[g][1];
-        }
-    __syncthreads();
-    for (uint32_t i = tid; i < G * FD_HD; i += FD_THREADS) {
-        uint32_t g = i / FD_HD, d = i % FD_HD;
-        float o = ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d];
+    for (int g = 0; g < G; g++) {
         float *pp = part + ((size_t)(kvh * G + g) * n_chunks + chunk) * (FD_HD + 2);
-        pp[d] = o;
-        if (d == 0) { pp[FD_HD] = mh[g]; pp[FD_HD + 1] = lh[g]; }
+        *(float2 *)(pp + 2 * lane) = make_float2(acc[g][0], acc[g][1]);
+        if (lane == 0) { pp[FD_HD] = mx[g]; pp[FD_HD + 1] = ls[g]; }
     }
 }
 
@@ -391,13 +372,23 @@ __global__ __launch_bounds__(256) void k_flash_merge(const float *__restrict__ p
 int zhk_flash_decode(zh_ctx *c, const float *q, const uint16_t *kc, const uint16_t *vc, const uint32_t *pages,
                      uint32_t n_pages, uint32_t cache_tokens, float *out, void *xq_out, uint32_t nh, uint32_t nkv,
                      uint32_t hd, zh_pos_src seq_len, uint32_t max_seq, float scale, float *partials) {
-    uint32_t G = nh / nkv;
-    uint32_t C = fd_chunk(max_seq, nkv, c->cu_count);
-    uint32_t n_chunks = (max_seq + C - 1) / C;
-    hipLaunchKernelGGL(k_flash_decode, dim3(nkv, n_chunks), dim3(FD_THREADS), 0, c->stream, q, kc, vc, pages, n_pages,
-                       cache_tokens, G, C, n_chunks, seq_len, scale, partials);
-    ZH_LAUNCH_CHECK(c);
+    const uint32_t G = nh / nkv;
+    const uint32_t C = FD_T;
+    const uint32_t n_chunks = (max_seq + C - 1) / C;
     if (n_chunks > 1024) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "context too long for merge (%u chunks)", n_chunks);
+    dim3 grid(nkv, n_chunks);
+#define FD_LAUNCH(GG)                                                                                              \
+    hipLaunchKernelGGL(k_flash_decode<GG>, grid, dim3(64), 0, c->stream, q, kc, vc, pages, n_pages, cache_tokens, \
+                       n_chunks, seq_len, scale, partials)
+    switch (G) {
+    case 1: FD_LAUNCH(1); break;
+    case 2: FD_LAUNCH(2); break;
+    case 4: FD_LAUNCH(4); break;
+    case 8: FD_LAUNCH(8); break;
+    default: return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "GQA group %u unsupported (1, 2, 4, 8)", G);
+    }
+#undef FD_LAUNCH
+    ZH_LAUNCH_CHECK(c);
     hipLaunchKernelGGL(k_flash_merge, dim3(nh), dim3(256), 0, c->stream, (const float *)partials, n_chunks, C,
                        seq_len, out, (uint8_t *)xq_out);
     ZH_LAUNCH_CHECK(c);
@@ -410,7 +401,7 @@ extern "C" int zh_flash_decode(zh_ctx *c, const zh_buf *q, const zh_buf *kc, con
                                uint32_t hd, uint32_t seq_len, float attn_scale) {
     if (!c) return ZH_ERR_INVALID_ARGUMENT;
     if (hd != FD_HD) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "head_dim %u unsupported (128 only)", hd);
-    if (nkv == 0 || nh % nkv || nh / nkv > FD_MAXG || seq_len == 0)
+    if (nkv == 0 || nh % nkv || nh / nkv > FD_MAXG || ((nh / nkv) & (nh / nkv - 1)) || seq_len == 0)
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "heads/seq_len");
     if ((seq_len + 15) / 16 > n_pages) return zh_set_err(c, ZH_ERR_CONTEXT_LENGTH_EXCEEDED, "seq_len %u", seq_len);
     if (!in_range(q, 0, 4ull * nh * hd) || !in_range(out, 0, 4ull * nh * hd) ||
