@@ -477,6 +477,281 @@ __global__ __launch_bounds__(LPB_T, ZH_LPB_MINB) void k_dmmv_q6k_lpb(LpbP p) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Coalesced-tile variant for Q4_K. In the lane-per-block load pattern the 64
+// lanes of one 16-byte load sit 144 bytes apart, so each load instruction
+// touches 64 cache lines; on MI355X that caps a pure read at ~2.2 TB/s against
+// ~6.2 TB/s when consecutive lanes read consecutive 16-byte chunks. Here each
+// batch of rows -- a contiguous byte range of the weight matrix -- is read
+// with the contiguous pattern into registers and written to an LDS tile, and
+// every lane then reads its own super-block from LDS (16-byte reads at a
+// 144-byte lane stride hit all 64 banks once per 16 lanes: conflict-free).
+// The next batch's loads are in flight while the current batch is computed.
+// ---------------------------------------------------------------------------
+constexpr uint32_t TILE_BYTES = LPB_T * 144;  // 256 Q4_K super-blocks
+
+#ifdef ZH_EXP_TRACE
+__device__ uint64_t g_exp_trace[8192 * 8];
+#define TRACE(slot) do { if (threadIdx.x == 0 && blockIdx.x < 8192 && (slot) < 8) \
+    g_exp_trace[blockIdx.x * 8 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+extern "C" int zh_exp_trace_dump(uint64_t *host, uint32_t n) {
+    int rc = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_trace), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
+    static uint64_t zeros[8192 * 8];
+    return rc | (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_trace), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+#else
+#define TRACE(slot) do { } while (0)
+#endif
+
+
+// Split staging for the tile kernel: the activation loads are issued before
+// the first weight tile's loads (vector memory returns in order, so loads
+// issued after 36 KB of tile data would wait for all of it), held in
+// registers, and turned into the LDS image in one pass once they land.
+// XCH = f32x4 chunks per lane = ceil(K / 1024); with the team width
+// TL = pow2ceil(K / 256) that is max(1, TL / 4).
+template <int XCH>
+struct XRegsF {
+    f32x4 x[XCH], w[XCH];
+};
+template <int XCH>
+ZH_DEV void stage_x_issue(const float *__restrict__ x, const float *__restrict__ norm_w, uint32_t K,
+                          XRegsF<XCH> &r) {
+#pragma unroll
+    for (int i = 0; i < XCH; i++) {
+        const uint32_t e0 = min((i * LPB_T + threadIdx.x) * 4, K - 4);  // clamped: static load count
+        r.x[i] = *(const f32x4 *)(x + e0);
+        r.w[i] = *(const f32x4 *)((norm_w ? norm_w : x) + e0);
+    }
+}
+template <int XCH>
+ZH_DEV void stage_x_finish(const XRegsF<XCH> &r, bool has_norm, float eps, uint32_t K, XLds lx, float *red,
+                           float *normed_out) {
+    const uint32_t tid = threadIdx.x;
+    float rms_inv = 1.f;
+    if (has_norm) {
+        float sq = 0.f;
+#pragma unroll
+        for (int i = 0; i < XCH; i++) {
+            if ((i * LPB_T + tid) * 4 < K) {
+                const f32x4 v = r.x[i];
+                sq = fmaf(v.x, v.x, sq); sq = fmaf(v.y, v.y, sq); sq = fmaf(v.z, v.z, sq); sq = fmaf(v.w, v.w, sq);
+            }
+        }
+        sq = wave_sum(sq);
+        if ((tid & 63) == 0) red[tid >> 6] = sq;
+        __syncthreads();
+        const float tot = red[0] + red[1] + red[2] + red[3];
+        rms_inv = 1.0f / sqrtf(tot / (float)K + eps);
+    }
+#pragma unroll
+    for (int i = 0; i < XCH; i++) {
+        const uint32_t e0 = (i * LPB_T + tid) * 4;
+        if (e0 >= K) break;  // uniform per 8-lane group (K % 32 == 0)
+        f32x4 v = r.x[i];
+        if (has_norm) {
+            const f32x4 w = r.w[i];
+            v.x = w.x * (v.x * rms_inv); v.y = w.y * (v.y * rms_inv);
+            v.z = w.z * (v.z * rms_inv); v.w = w.w * (v.w * rms_inv);
+            if (normed_out && blockIdx.x == 0) *(f32x4 *)(normed_out + e0) = v;
+        }
+        float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        a = fmaxf(a, __shfl_xor(a, 1, 64));
+        a = fmaxf(a, __shfl_xor(a, 2, 64));
+        a = fmaxf(a, __shfl_xor(a, 4, 64));
+        float inv, sc;
+        xq_scales(a, inv, sc);
+        int X[4] = {xq_quant(v.x, inv), xq_quant(v.y, inv), xq_quant(v.z, inv), xq_quant(v.w, inv)};
+        int l0[4], l1[4], l2[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) xq_limbs(X[q], l0[q], l1[q], l2[q]);
+        const uint32_t blk32 = e0 / 32, b = blk32 / 8, j = blk32 % 8, lo = e0 % 32;
+        uint8_t *dst = lx.limb + (size_t)b * XB_STRIDE + j * 96 + lo;
+        *(uint32_t *)(dst) = pack4(l0[0], l0[1], l0[2], l0[3]);
+        *(uint32_t *)(dst + 32) = pack4(l1[0], l1[1], l1[2], l1[3]);
+        *(uint32_t *)(dst + 64) = pack4(l2[0], l2[1], l2[2], l2[3]);
+        int sm = X[0] + X[1] + X[2] + X[3];
+        sm += __shfl_xor(sm, 1, 64);
+        sm += __shfl_xor(sm, 2, 64);
+        const uint32_t sub = (tid & 7);
+        if (sub == 0) lx.xs[b * 8 + j] = sc;
+        if ((sub & 3) == 0) lx.xz16[b * 16 + j * 2 + (sub >> 2)] = (float)sm * sc;
+    }
+    __syncthreads();
+}
+
+// Pre-quantised XQ: limbs (96 B per 32 elements), xs, xsum16 held in registers.
+// XQCH = 16-byte limb chunks per lane = ceil(6 * K/32 / 256) <= ceil(3 TL / 16).
+template <int XQCH>
+struct XRegsQ {
+    u32x4 limb[XQCH];
+    float xs;
+    float xz[2];
+};
+template <int XQCH>
+ZH_DEV void stage_xq_issue(const uint8_t *__restrict__ xq, uint32_t K, XRegsQ<XQCH> &r) {
+    const uint32_t tid = threadIdx.x, nblk = K / 32;
+    const XQView v = xq_view((void *)xq, nblk);
+#pragma unroll
+    for (int i = 0; i < XQCH; i++) {
+        const uint32_t c = min(i * LPB_T + tid, nblk * 6 - 1);  // clamped: static load count
+        r.limb[i] = *(const u32x4 *)(v.limb + (size_t)c * 16);
+    }
+    r.xs = v.xs[min(tid, nblk - 1)];
+    r.xz[0] = v.xsum[min(tid, nblk * 2 - 1)];
+    if (XQCH > 3) r.xz[1] = v.xsum[min(LPB_T + tid, nblk * 2 - 1)];  // nblk > 128 only when TL = 32
+}
+template <int XQCH>
+ZH_DEV void stage_xq_finish(const XRegsQ<XQCH> &r, uint32_t K, XLds lx) {
+    const uint32_t tid = threadIdx.x, nblk = K / 32;
+#pragma unroll
+    for (int i = 0; i < XQCH; i++) {
+        const uint32_t c = i * LPB_T + tid;
+        if (c < nblk * 6) {
+            const uint32_t blk32 = c / 6, part = c % 6;
+            *(u32x4 *)(lx.limb + (size_t)(blk32 / 8) * XB_STRIDE + (blk32 % 8) * 96 + part * 16) = r.limb[i];
+        }
+    }
+    if (tid < nblk) lx.xs[tid] = r.xs;
+    if (tid < nblk * 2) lx.xz16[tid] = r.xz[0];
+    if (XQCH > 3 && LPB_T + tid < nblk * 2) lx.xz16[LPB_T + tid] = r.xz[1];
+    __syncthreads();
+}
+
+template <int NM, int NCH, int RPB>
+ZH_DEV void q4k_tile_fetch(const LpbP &p, uint32_t bi, uint32_t row_bytes, u32x4 (&st)[NM][NCH]) {
+    uint32_t seg_rows, rr0, sg;
+    lpb_geom(p, bi * RPB, seg_rows, rr0, sg);
+    const uint32_t n16 = min((uint32_t)RPB, seg_rows - rr0) * row_bytes / 16;
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        const u32x4 *src = (const u32x4 *)((m ? p.segW2 : p.segW[sg]) + (size_t)rr0 * row_bytes);
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            // unconditional (clamped) loads keep the outstanding-load count
+            // static, so waits on earlier loads need not drain the tile
+            const uint32_t c = min(j * LPB_T + threadIdx.x, n16 - 1);
+            st[m][j] = __builtin_nontemporal_load(src + c);
+        }
+    }
+}
+
+template <int TL, int MODE>
+__global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    __shared__ float red[4];
+    __shared__ float gate_res[LPB_T / TL];
+    constexpr int NM = MODE == LPB_GATE_UP ? 2 : 1;
+    constexpr int TPB = LPB_T / TL;         // teams (one row each) per batch
+    constexpr int RPB = TPB / NM;           // rows of each matrix per batch
+    constexpr int NCH = (9 + NM - 1) / NM;  // 16-byte chunks per lane per matrix
+    const uint32_t nb = p.K / 256, row_bytes = nb * 144, sub_bytes = RPB * row_bytes;
+    XLds lx = xlds_view(lds_raw, nb);
+    uint8_t *tile = lds_raw + (size_t)nb * (XB_STRIDE + 96);
+    const int tid = threadIdx.x, tlane = tid % TL, team = tid / TL;
+    const int mat = team / RPB, rt = team % RPB;
+    const bool active = (uint32_t)tlane < nb;
+    const uint32_t b = active ? tlane : 0;
+    const uint8_t *xl = lx.limb + (size_t)b * XB_STRIDE;
+    const uint32_t nbatch = (p.M + RPB - 1) / RPB;
+    u32x4 st[NM][NCH];
+    uint32_t bi = blockIdx.x;
+    TRACE(0);
+    if (p.xq) {
+        XRegsQ<(3 * TL + 15) / 16> xr;
+        stage_xq_issue(p.xq, p.K, xr);
+        q4k_tile_fetch<NM, NCH, RPB>(p, bi, row_bytes, st);  // grid <= nbatch (host)
+        stage_xq_finish(xr, p.K, lx);
+    } else {
+        XRegsF<(TL / 4 > 1 ? TL / 4 : 1)> xr;
+        stage_x_issue(p.x, p.norm_w, p.K, xr);
+        q4k_tile_fetch<NM, NCH, RPB>(p, bi, row_bytes, st);
+        stage_x_finish(xr, p.norm_w != nullptr, p.eps, p.K, lx, red, p.normed_out);
+    }
+    TRACE(1);
+    int it = 0;
+    for (; bi < nbatch; bi += gridDim.x, it++) {
+        uint32_t seg_rows, rr0, sg;
+        lpb_geom(p, bi * RPB, seg_rows, rr0, sg);
+        const uint32_t nrows = min((uint32_t)RPB, seg_rows - rr0);
+        const uint32_t n16 = nrows * row_bytes / 16;
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int j = 0; j < NCH; j++) {
+                const uint32_t c = j * LPB_T + tid;
+                if (c < n16) *(u32x4 *)(tile + m * sub_bytes + c * 16) = st[m][j];
+            }
+        __syncthreads();
+        TRACE(2 + min(it, 4));
+        if (bi + gridDim.x < nbatch) q4k_tile_fetch<NM, NCH, RPB>(p, bi + gridDim.x, row_bytes, st);
+        uint32_t raw[LpbQ4K::RAW];
+        {
+            const uint8_t *blk = tile + mat * sub_bytes + rt * row_bytes + b * 144;
+#pragma unroll
+            for (int i = 0; i < 9; i++) {
+                const u32x4 v = *(const u32x4 *)(blk + 16 * i);
+                raw[4 * i] = v.x; raw[4 * i + 1] = v.y; raw[4 * i + 2] = v.z; raw[4 * i + 3] = v.w;
+            }
+        }
+        const LpbQ4K::Hdr h = LpbQ4K::header(raw);
+        float accd = 0.f, accm = 0.f;
+#ifdef ZH_EXP_TILE
+        uint32_t xx = 0;
+        for (int i = 0; i < 36; i++) xx ^= raw[i];
+        accd = (float)(xx & 1);
+#else
+#pragma unroll
+        for (int pp = 0; pp < 4; pp++) {
+            uint32_t xo = (uint32_t)(2 * pp) * 96u;
+            asm volatile("" : "+v"(xo) : "v"(accd));
+            uint32_t L[2][24];
+            lds_load_limbs(L[0], xl + xo);
+            lds_load_limbs(L[1], xl + xo + 96);
+            const float xs0 = lx.xs[b * 8 + 2 * pp], xs1 = lx.xs[b * 8 + 2 * pp + 1];
+            const float xz0 = lx.xz16[b * 16 + 4 * pp] + lx.xz16[b * 16 + 4 * pp + 1];
+            const float xz1 = lx.xz16[b * 16 + 4 * pp + 2] + lx.xz16[b * 16 + 4 * pp + 3];
+            int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t w = raw[4 + 8 * pp + i];
+                const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                for (int k = 0; k < 3; k++) {
+                    D[0][k] = sdot4(lo, L[0][k * 8 + i], D[0][k]);
+                    D[1][k] = sdot4(hi, L[1][k * 8 + i], D[1][k]);
+                }
+            }
+            const uint32_t scw = (2 * pp < 4) ? h.scA : h.scB, mw = (2 * pp < 4) ? h.mA : h.mB;
+            const float sc0 = ubyte_f(scw, (2 * pp) & 3), sc1 = ubyte_f(scw, (2 * pp + 1) & 3);
+            const float m0 = ubyte_f(mw, (2 * pp) & 3), m1 = ubyte_f(mw, (2 * pp + 1) & 3);
+            const float S0 = (float)comb_i(D[0][0], D[0][1], D[0][2]);
+            const float S1 = (float)comb_i(D[1][0], D[1][1], D[1][2]);
+            accd = fmaf(sc0 * xs0, S0, accd);
+            accd = fmaf(sc1 * xs1, S1, accd);
+            accm = fmaf(m0, xz0, accm);
+            accm = fmaf(m1, xz1, accm);
+        }
+#endif
+        float res = active ? fmaf(h.d, accd, -h.dmin * accm) : 0.f;
+#pragma unroll
+        for (int o = TL / 2; o > 0; o >>= 1) res += __shfl_xor(res, o, 64);
+        float *yb = p.segY[sg];
+        if (MODE == LPB_GATE_UP) {
+            if (mat == 0 && tlane == 0) gate_res[rt] = res;
+            __syncthreads();
+            if (mat == 1 && tlane == 0 && (uint32_t)rt < nrows) yb[rr0 + rt] = silu_mul(gate_res[rt], res);
+        } else if (tlane == 0 && (uint32_t)rt < nrows) {
+            float out = res;
+            if (p.acc) out += yb[rr0 + rt];
+            yb[rr0 + rt] = out;
+        }
+        __syncthreads();  // the tile is rewritten by the next batch
+    }
+    TRACE(7);
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -500,6 +775,48 @@ static int launch_q6k(zh_ctx *c, const LpbP &p, uint32_t wgs, uint32_t lds) {
     hipLaunchKernelGGL((k_dmmv_q6k_lpb<TL, 1>), dim3(wgs), dim3(LPB_T), lds, c->stream, p);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
+}
+
+
+template <int TL>
+static int launch_q4k_tile(zh_ctx *c, const LpbP &p, uint32_t wgs, uint32_t lds) {
+    if (p.mode == LPB_GATE_UP)
+        hipLaunchKernelGGL((k_dmmv_q4k_tile<TL, LPB_GATE_UP>), dim3(wgs), dim3(LPB_T), lds, c->stream, p);
+    else
+        hipLaunchKernelGGL((k_dmmv_q4k_tile<TL, LPB_PLAIN>), dim3(wgs), dim3(LPB_T), lds, c->stream, p);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+// Tile path: Q4_K with K <= 8192 (team of <= 32 lanes, LDS image + tile
+// within 64 KB), 16-byte aligned matrices, and every segment but the last a
+// whole number of batches.
+static int try_q4k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t *M) {
+    static int off = -1, capm = -1;
+    if (off < 0) {
+        off = getenv("ZH_NO_TILE") ? 1 : 0;
+        const char *e = getenv("ZH_TILE_CAP");
+        capm = e ? atoi(e) : 3;
+    }
+    const uint32_t nb = p.K / 256;
+    if (off || nb > 32) return -1;
+    const uint32_t TL = pow2ceil(nb < 4 ? 4 : nb);
+    const uint32_t nm = p.mode == LPB_GATE_UP ? 2 : 1;
+    const uint32_t rpb = LPB_T / TL / nm;
+    for (uint32_t s = 0; s < nseg; s++) {
+        if (((uintptr_t)p.segW[s] & 15) || (s + 1 < nseg && M[s] % rpb)) return -1;
+    }
+    if (nm == 2 && ((uintptr_t)p.segW2 & 15)) return -1;
+    const uint32_t nbatch = (p.M + rpb - 1) / rpb;
+    uint32_t wgs = nbatch, cap = (uint32_t)c->cu_count * (uint32_t)(capm > 0 ? capm : 3);
+    if (wgs > cap) wgs = cap;
+    const uint32_t lds = nb * (XB_STRIDE + 96) + TILE_BYTES;
+    switch (TL) {
+    case 4: return launch_q4k_tile<4>(c, p, wgs, lds);
+    case 8: return launch_q4k_tile<8>(c, p, wgs, lds);
+    case 16: return launch_q4k_tile<16>(c, p, wgs, lds);
+    default: return launch_q4k_tile<32>(c, p, wgs, lds);
+    }
 }
 
 bool zhk_lpb_supported(uint32_t qtype, uint32_t K) {
@@ -529,6 +846,10 @@ int zhk_dmmv_lpb(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const uint8
     }
     p.segW2 = W2;
     p.M = end;
+    if (qtype == ZH_Q4_K) {
+        const int rc = try_q4k_tile(c, p, nseg, M);
+        if (rc >= 0) return rc;
+    }
     const uint32_t lanes = qtype == ZH_Q4_K ? K / 256 : K / 128;
     const uint32_t TL = pow2ceil(lanes < 4 ? 4 : lanes);
     const uint32_t teams = (p.M + R - 1) / R;
