@@ -515,14 +515,14 @@ template <int XCH>
 struct XRegsF {
     f32x4 x[XCH], w[XCH];
 };
-template <int XCH>
+template <int XCH, bool NORM>
 ZH_DEV void stage_x_issue(const float *__restrict__ x, const float *__restrict__ norm_w, uint32_t K,
                           XRegsF<XCH> &r) {
 #pragma unroll
     for (int i = 0; i < XCH; i++) {
         const uint32_t e0 = min((i * LPB_T + threadIdx.x) * 4, K - 4);  // clamped: static load count
         r.x[i] = *(const f32x4 *)(x + e0);
-        r.w[i] = *(const f32x4 *)((norm_w ? norm_w : x) + e0);
+        if (NORM) r.w[i] = *(const f32x4 *)(norm_w + e0);
     }
 }
 template <int XCH>
@@ -619,8 +619,32 @@ ZH_DEV void stage_xq_finish(const XRegsQ<XQCH> &r, uint32_t K, XLds lx) {
     __syncthreads();
 }
 
+// Stages the activation into the LDS image (XQ copy, f32, or f32 with a
+// fused RMSNorm), calling fetch() -- the first weight tile's loads -- after
+// the activation loads are issued and before they are waited on. Each of the
+// three paths is straight-line so the wait counts stay exact.
+template <int XQCH, int XCH, class Fetch>
+ZH_DEV void stage_and_fetch(const LpbP &p, XLds lx, float *red, const Fetch &fetch) {
+    if (p.xq) {
+        XRegsQ<XQCH> xr;
+        stage_xq_issue(p.xq, p.K, xr);
+        fetch();
+        stage_xq_finish(xr, p.K, lx);
+    } else if (p.norm_w) {
+        XRegsF<XCH> xr;
+        stage_x_issue<XCH, true>(p.x, p.norm_w, p.K, xr);
+        fetch();
+        stage_x_finish(xr, true, p.eps, p.K, lx, red, p.normed_out);
+    } else {
+        XRegsF<XCH> xr;
+        stage_x_issue<XCH, false>(p.x, nullptr, p.K, xr);
+        fetch();
+        stage_x_finish(xr, false, p.eps, p.K, lx, red, nullptr);
+    }
+}
+
 template <int NM, int NCH, int RPB>
-ZH_DEV void q4k_tile_fetch(const LpbP &p, uint32_t bi, uint32_t row_bytes, u32x4 (&st)[NM][NCH]) {
+ZH_DEV void tile_fetch(const LpbP &p, uint32_t bi, uint32_t row_bytes, u32x4 (&st)[NM][NCH]) {
     uint32_t seg_rows, rr0, sg;
     lpb_geom(p, bi * RPB, seg_rows, rr0, sg);
     const uint32_t n16 = min((uint32_t)RPB, seg_rows - rr0) * row_bytes / 16;
@@ -658,17 +682,9 @@ __global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
     u32x4 st[NM][NCH];
     uint32_t bi = blockIdx.x;
     TRACE(0);
-    if (p.xq) {
-        XRegsQ<(3 * TL + 15) / 16> xr;
-        stage_xq_issue(p.xq, p.K, xr);
-        q4k_tile_fetch<NM, NCH, RPB>(p, bi, row_bytes, st);  // grid <= nbatch (host)
-        stage_xq_finish(xr, p.K, lx);
-    } else {
-        XRegsF<(TL / 4 > 1 ? TL / 4 : 1)> xr;
-        stage_x_issue(p.x, p.norm_w, p.K, xr);
-        q4k_tile_fetch<NM, NCH, RPB>(p, bi, row_bytes, st);
-        stage_x_finish(xr, p.norm_w != nullptr, p.eps, p.K, lx, red, p.normed_out);
-    }
+    // grid <= nbatch (host), so the first batch always exists
+    stage_and_fetch<(3 * TL + 15) / 16, (TL / 4 > 1 ? TL / 4 : 1)>(
+        p, lx, red, [&] { tile_fetch<NM, NCH, RPB>(p, bi, row_bytes, st); });
     TRACE(1);
     int it = 0;
     for (; bi < nbatch; bi += gridDim.x, it++) {
@@ -685,7 +701,7 @@ __global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
             }
         __syncthreads();
         TRACE(2 + min(it, 4));
-        if (bi + gridDim.x < nbatch) q4k_tile_fetch<NM, NCH, RPB>(p, bi + gridDim.x, row_bytes, st);
+        if (bi + gridDim.x < nbatch) tile_fetch<NM, NCH, RPB>(p, bi + gridDim.x, row_bytes, st);
         uint32_t raw[LpbQ4K::RAW];
         {
             const uint8_t *blk = tile + mat * sub_bytes + rt * row_bytes + b * 144;
@@ -750,6 +766,115 @@ __global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
         __syncthreads();  // the tile is rewritten by the next batch
     }
     TRACE(7);
+}
+
+
+// Q6_K on the coalesced tile: one lane per half super-block (128 elements,
+// ql[64h..), qh[32h..), sc[8h..), d) as in k_dmmv_q6k_lpb, with the block
+// bytes read from the LDS tile. Q6_K blocks are 210 bytes, so a block starts
+// 2-byte aligned; dword reads are realigned with alignbyte.
+template <int TL>
+__global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    __shared__ float red[4];
+    constexpr int RPB = LPB_T / TL;  // rows per batch
+    constexpr int NCH = 7;           // ceil(128 blocks * 210 B / 4 KB)
+    const uint32_t nb = p.K / 256, row_bytes = nb * 210, nh = nb * 2;
+    XLds lx = xlds_view(lds_raw, nb);
+    uint8_t *tile = lds_raw + (size_t)nb * (XB_STRIDE + 96);
+    const int tid = threadIdx.x, tlane = tid % TL, rt = tid / TL;
+    const bool active = (uint32_t)tlane < nh;
+    const uint32_t hb = active ? tlane : 0, b = hb >> 1, h = hb & 1;
+    const uint8_t *xl = lx.limb + (size_t)b * XB_STRIDE + h * 4 * 96;  // sub-blocks 4h..4h+3
+    const uint32_t nbatch = (p.M + RPB - 1) / RPB;
+    u32x4 st[1][NCH];
+    uint32_t bi = blockIdx.x;
+    stage_and_fetch<(3 * TL / 2 + 15) / 16, (TL / 8 > 1 ? TL / 8 : 1)>(
+        p, lx, red, [&] { tile_fetch<1, NCH, RPB>(p, bi, row_bytes, st); });
+    for (; bi < nbatch; bi += gridDim.x) {
+        uint32_t seg_rows, rr0, sg;
+        lpb_geom(p, bi * RPB, seg_rows, rr0, sg);
+        const uint32_t nrows = min((uint32_t)RPB, seg_rows - rr0);
+        const uint32_t n16 = nrows * row_bytes / 16;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const uint32_t c = j * LPB_T + tid;
+            if (c < n16) *(u32x4 *)(tile + c * 16) = st[0][j];
+        }
+        __syncthreads();
+        if (bi + gridDim.x < nbatch) tile_fetch<1, NCH, RPB>(p, bi + gridDim.x, row_bytes, st);
+        const uint32_t boff = rt * row_bytes + b * 210;
+        const uint32_t sh = boff & 3;
+        uint32_t rq[17], rh[9], rs[6];
+        {
+            const uint32_t *a = (const uint32_t *)(tile + ((boff + 64 * h) & ~3u));
+#pragma unroll
+            for (int i = 0; i < 17; i++) rq[i] = a[i];
+            const uint32_t *c = (const uint32_t *)(tile + ((boff + 128 + 32 * h) & ~3u));
+#pragma unroll
+            for (int i = 0; i < 9; i++) rh[i] = c[i];
+            const uint32_t *sp = (const uint32_t *)(tile + ((boff + 192) & ~3u));
+#pragma unroll
+            for (int i = 0; i < 6; i++) rs[i] = sp[i];
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t xo = (uint32_t)g * 96u;
+            asm volatile("" : "+v"(xo) : "v"(acc));
+            uint32_t L[24];
+            lds_load_limbs(L, xl + xo);
+            const float xs = lx.xs[b * 8 + 4 * h + g];
+            const float z0 = -32.f * lx.xz16[b * 16 + (4 * h + g) * 2];
+            const float z1 = -32.f * lx.xz16[b * 16 + (4 * h + g) * 2 + 1];
+            int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int qi = (g & 1) * 8 + i;
+                const uint32_t av = __builtin_amdgcn_alignbyte(rq[qi + 1], rq[qi], sh);
+                const uint32_t cv = __builtin_amdgcn_alignbyte(rh[i + 1], rh[i], sh);
+                const uint32_t lo4 = (g >> 1) ? ((av >> 4) & 0x0F0F0F0Fu) : (av & 0x0F0F0F0Fu);
+                const uint32_t hi2 = ((cv >> (2 * g)) << 4) & 0x30303030u;
+                const uint32_t q = lo4 | hi2;  // unsigned 6-bit code; the -32 offset enters via z0/z1
+                const int grp = i >> 2;
+#pragma unroll
+                for (int k = 0; k < 3; k++) D[grp][k] = sdot4(q, L[k * 8 + i], D[grp][k]);
+            }
+            const uint32_t s0 = __builtin_amdgcn_alignbyte(rs[1], rs[0], sh);
+            const uint32_t s1 = __builtin_amdgcn_alignbyte(rs[2], rs[1], sh);
+            const uint32_t s2 = __builtin_amdgcn_alignbyte(rs[3], rs[2], sh);
+            const uint32_t s3 = __builtin_amdgcn_alignbyte(rs[4], rs[3], sh);
+            const uint32_t scw[4] = {s0, s1, s2, s3};
+            const int i0 = 8 * h + 2 * g, i1 = i0 + 1;
+            const int sc0 = (int)(int8_t)((scw[i0 >> 2] >> (8 * (i0 & 3))) & 0xFF);
+            const int sc1 = (int)(int8_t)((scw[i1 >> 2] >> (8 * (i1 & 3))) & 0xFF);
+            const float S0 = comb_f(D[0][0], D[0][1], D[0][2]);
+            const float S1 = comb_f(D[1][0], D[1][1], D[1][2]);
+            acc = fmaf((float)sc0, fmaf(xs, S0, z0), acc);
+            acc = fmaf((float)sc1, fmaf(xs, S1, z1), acc);
+        }
+        const uint32_t dw = __builtin_amdgcn_alignbyte(rs[5], rs[4], sh);  // bytes 208..211
+        float res = active ? h2f(dw) * acc : 0.f;
+        constexpr int TLW = TL > 64 ? 64 : TL;
+#pragma unroll
+        for (int o = TLW / 2; o > 0; o >>= 1) res += __shfl_xor(res, o, 64);
+        if (TL > 64) {  // team spans TL/64 waves
+            __shared__ float xred[LPB_T / 64];
+            if ((tid & 63) == 0) xred[tid >> 6] = res;
+            __syncthreads();
+            float t = 0.f;
+#pragma unroll
+            for (int w = 0; w < TL / 64; w++) t += xred[(rt * TL) / 64 + w];
+            res = t;
+        }
+        float *yb = p.segY[sg];
+        if (tlane == 0 && (uint32_t)rt < nrows) {
+            float out = res;
+            if (p.acc) out += yb[rr0 + rt];
+            yb[rr0 + rt] = out;
+        }
+        __syncthreads();  // the tile (and xred) are rewritten by the next batch
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -819,6 +944,49 @@ static int try_q4k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t 
     }
 }
 
+
+template <int TL>
+static int launch_q6k_tile(zh_ctx *c, const LpbP &p, uint32_t wgs, uint32_t lds) {
+    hipLaunchKernelGGL((k_dmmv_q6k_tile<TL>), dim3(wgs), dim3(LPB_T), lds, c->stream, p);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+// Q6_K tile path: rows a multiple of 16 bytes (K % 2048 == 0), team of <= 128
+// lanes (K <= 16384) and LDS image + tile within 64 KB.
+static int try_q6k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t *M) {
+    static int off = -1, capm = -1;
+    if (off < 0) {
+        off = getenv("ZH_NO_TILE") ? 1 : 0;
+        const char *e = getenv("ZH_TILE6_CAP");
+        capm = e ? atoi(e) : 2;
+    }
+    const uint32_t nb = p.K / 256, row_bytes = nb * 210;
+    // Very tall matrices (the LM head) give every workgroup dozens of batches;
+    // there the per-row limb re-reads from LDS and the Q6_K unpack bound the
+    // tile kernel, and the lane-per-block kernel measures faster.
+    if (off || row_bytes % 16 || nb > 64 || p.M >= 65536) return -1;
+    const uint32_t TL = pow2ceil(2 * nb < 4 ? 4 : 2 * nb);
+    const uint32_t rpb = LPB_T / TL;
+    const uint32_t lds = nb * (XB_STRIDE + 96) + rpb * row_bytes;
+    if (lds > 65536) return -1;
+    for (uint32_t s = 0; s < nseg; s++)
+        if (((uintptr_t)p.segW[s] & 15) || (s + 1 < nseg && M[s] % rpb)) return -1;
+    const uint32_t nbatch = (p.M + rpb - 1) / rpb;
+    uint32_t per_cu = 163840 / (lds + 1024);
+    if (per_cu > (uint32_t)(capm > 0 ? capm : 2)) per_cu = (uint32_t)(capm > 0 ? capm : 2);
+    uint32_t wgs = nbatch, cap = (uint32_t)c->cu_count * (per_cu ? per_cu : 1);
+    if (wgs > cap) wgs = cap;
+    switch (TL) {
+    case 4: return launch_q6k_tile<4>(c, p, wgs, lds);
+    case 8: return launch_q6k_tile<8>(c, p, wgs, lds);
+    case 16: return launch_q6k_tile<16>(c, p, wgs, lds);
+    case 32: return launch_q6k_tile<32>(c, p, wgs, lds);
+    case 64: return launch_q6k_tile<64>(c, p, wgs, lds);
+    default: return launch_q6k_tile<128>(c, p, wgs, lds);
+    }
+}
+
 bool zhk_lpb_supported(uint32_t qtype, uint32_t K) {
     if (K % 256 || K == 0) return false;
     if (qtype == ZH_Q4_K) return K / 256 <= 256;
@@ -846,8 +1014,8 @@ int zhk_dmmv_lpb(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const uint8
     }
     p.segW2 = W2;
     p.M = end;
-    if (qtype == ZH_Q4_K) {
-        const int rc = try_q4k_tile(c, p, nseg, M);
+    {
+        const int rc = qtype == ZH_Q4_K ? try_q4k_tile(c, p, nseg, M) : try_q6k_tile(c, p, nseg, M);
         if (rc >= 0) return rc;
     }
     const uint32_t lanes = qtype == ZH_Q4_K ? K / 256 : K / 128;

@@ -346,11 +346,10 @@ static int record_step(zh_engine *e, bool collect) {
             const uint32_t mf = m.ffn;
             ERC(zhk_dmmv_lpb(c, ZH_Q4_K, 1, 1, &wg, W(y.up), &ys, &mf, e->hidden, Wf(y.ffn_norm), m.eps, nullptr, H,
                              0));
-            // down: K = ffn is large and M = hidden small, so per-workgroup
-            // staging of x would dominate; quantise once and use the
-            // 64-element-unit kernel, which measures fastest at this shape.
-            ERC(zhk_quantize_xq(c, e->s, e->xq_f, m.ffn, 1, 0));
-            ERC(zhk_dmmv(c, m.type_ffn_down, W(y.down), e->xq_f, e->hidden, H, m.ffn, 1));
+            const uint8_t *wd = W(y.down);
+            float *yd = e->hidden;
+            const uint32_t mh = H;
+            ERC(zhk_dmmv_lpb(c, m.type_ffn_down, 0, 1, &wd, nullptr, &yd, &mh, e->s, nullptr, 0.f, nullptr, m.ffn, 1));
             continue;
         }
         ERC(zhk_rms_norm(c, e->hidden, Wf(y.ffn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
