@@ -79,6 +79,7 @@ def lib():
             "zo_model_decode_step": (C.c_uint32, [C.c_void_p, C.c_uint32, C.c_uint32, f32p]),
             "zo_model_tensor": (C.c_void_p, [C.c_void_p, C.c_uint64, C.POINTER(C.c_uint64)]),
             "zo_model_hidden": (C.c_void_p, [C.c_void_p]),
+            "zo_model_kv": (C.c_void_p, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -299,6 +300,12 @@ class Model:
         if not p:
             return None
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), shape=(n.value,)).copy()
+
+    def kv(self, layer, which, token):
+        """fp16 bits of the K (which=0) or V (1) cache row of `token`."""
+        p = lib().zo_model_kv(self.h, layer, which, token)
+        n = self.cfg["n_kv_heads"] * self.cfg["head_dim"]
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), shape=(n,)).copy()
 
     def hidden(self):
         p = lib().zo_model_hidden(self.h)

@@ -663,6 +663,11 @@ const uint8_t *zo_model_tensor(zo_model *m, uint64_t stream, uint64_t *bytes) {
     }
 }
 const float *zo_model_hidden(zo_model *m) { return m->hidden; }
+const uint16_t *zo_model_kv(zo_model *m, uint32_t layer, uint32_t which, uint32_t token) {
+    if (layer >= m->c.n_layers || which > 1 || token >= m->c.max_ctx) return NULL;
+    const zo_layer *y = &m->L[layer];
+    return (which ? y->vc : y->kc) + (size_t)token * m->c.n_kv_heads * m->c.head_dim;
+}
 
 typedef struct { const float *q; const uint16_t *k, *v; float *out; uint32_t hd, nh, nkv, L, h0, h1; } attn_job;
 static void *attn_worker(void *a) {

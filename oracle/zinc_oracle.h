@@ -121,6 +121,8 @@ uint32_t  zo_model_decode_step(zo_model *m, uint32_t token, uint32_t pos, float 
 /* Raw access for tests: tensor bytes by stream id, hidden state after step. */
 const uint8_t *zo_model_tensor(zo_model *m, uint64_t stream, uint64_t *bytes);
 const float   *zo_model_hidden(zo_model *m);
+/* fp16 K (which 0) or V (1) cache row of `token` in `layer`: n_kv_heads*head_dim values. */
+const uint16_t *zo_model_kv(zo_model *m, uint32_t layer, uint32_t which, uint32_t token);
 
 #ifdef __cplusplus
 }

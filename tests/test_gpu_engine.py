@@ -62,11 +62,16 @@ def test_engine_decode_matches_oracle(ctx, orc, cfg):
     assert np.allclose(g_log, o_log, rtol=1e-3, atol=1e-4 + 1e-3 * np.abs(o_log).max()), \
         f"max |d| {np.abs(g_log - o_log).max()} vs scale {np.abs(o_log).max()}"
     assert g_tok == o_tok
-    # the K/V just written match the oracle's fp16 entries
+    # the K/V rows written for the new token: finite, and equal to the
+    # oracle's fp16 rows except where the f32 inputs themselves differ by
+    # rounding (then by at most one f16 ulp)
     for l in range(cfg["n_layers"]):
-        gk = eng.read_kv(l, 0, prefill, 1).view(np.float16).astype(np.float32)
-        gv = eng.read_kv(l, 1, prefill, 1).view(np.float16).astype(np.float32)
-        assert np.isfinite(gk).all() and np.isfinite(gv).all()
+        for which in (0, 1):
+            g = eng.read_kv(l, which, prefill, 1)
+            o = om.kv(l, which, prefill)
+            assert np.isfinite(g.view(np.float16)).all()
+            d = np.abs(g.view(np.int16).astype(np.int32) - o.view(np.int16).astype(np.int32))
+            assert d.max() <= 1 and (d > 0).mean() < 0.05, (l, which, d.max(), (d > 0).mean())
     eng.deinit()
     om.close()
 

@@ -88,12 +88,32 @@ ZH_DEV float team_sum(float v) {
     for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
-ZH_DEV float wave_sum(float v) { return team_sum<64>(v); }
-ZH_DEV float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+// DPP lane exchanges inside a 16-lane row and readlane across rows: a few
+// cycles each instead of an LDS-crossbar round trip. All 64 lanes of the
+// wave must be active. Controls: quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] =
+// 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+ZH_DEV float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+ZH_DEV float lane_f(float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); }
+ZH_DEV float row8_sum(float v) {  // sum over each aligned group of 8 lanes, in every lane of it
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    return v + dpp_f<0x141>(v);
+}
+ZH_DEV float row8_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    return fmaxf(v, dpp_f<0x141>(v));
+}
+ZH_DEV float row16_sum(float v) { v = row8_sum(v); return v + dpp_f<0x140>(v); }
+ZH_DEV float row16_max(float v) { v = row8_max(v); return fmaxf(v, dpp_f<0x140>(v)); }
+// v uniform within each 16-lane row -> wave-uniform total
+ZH_DEV float rows_sum(float v) { return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48)); }
+ZH_DEV float rows_max(float v) { return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48))); }
+ZH_DEV float wave_sum(float v) { return rows_sum(row16_sum(v)); }
+ZH_DEV float wave_max(float v) { return rows_max(row16_max(v)); }
 
 ZH_DEV float h2f(uint32_t h16) { return (float)__ushort_as_half((unsigned short)(h16 & 0xFFFF)); }
 // f32 -> f16 round-to-nearest-even in integer arithmetic (subnormals kept,

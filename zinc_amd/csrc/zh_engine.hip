@@ -53,6 +53,7 @@ struct zh_engine {
     uint16_t *kv = nullptr;  // all caches
     uint32_t *pages = nullptr, n_pages = 0;
     float *inv_freq = nullptr;
+    float *rope_cs = nullptr;  // [max_ctx][64] (cos, sin)
     // activations
     float *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     float *s = nullptr, *logits = nullptr, *rl = nullptr, *edown_out = nullptr, *fd_part = nullptr;
@@ -234,7 +235,7 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
         {(void **)&e->xq_f, zh_xq_bytes_int(c.n_experts ? c.expert_ffn : c.ffn) * (c.n_experts_used ? c.n_experts_used : 1)},
         {(void **)&e->routing, 8ull * 16}, {(void **)&e->am_part, 8ull * 256}, {(void **)&e->st, 4ull * ST_WORDS},
         {(void **)&e->prompt, 4ull * MAX_PROMPT}, {(void **)&e->ring, 4ull * MAX_GEN}, {(void **)&e->pages, 4ull * e->n_pages},
-        {(void **)&e->inv_freq, 4ull * hd / 2},
+        {(void **)&e->inv_freq, 4ull * hd / 2}, {(void **)&e->rope_cs, 8ull * c.max_ctx * (hd / 2)},
     };
     uint64_t aoff = 0;
     for (auto &a : acts) aoff = align256(aoff + a.bytes);
@@ -255,6 +256,7 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
     std::vector<float> inv(hd / 2);
     for (uint32_t k = 0; k < hd / 2; k++) inv[k] = 1.0f / powf(c.rope_base, (float)(2 * k) / (float)hd);
     me = hipMemcpyAsync(e->inv_freq, inv.data(), 4ull * hd / 2, hipMemcpyHostToDevice, ctx->stream);
+    if (me == hipSuccess && zhk_rope_table(ctx, e->inv_freq, c.max_ctx, e->rope_cs) != ZH_OK) me = hipErrorUnknown;
     if (me != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess) {
         zh_engine_destroy(e);
         return zh_set_err(ctx, ZH_ERR_HIP, "engine init");
@@ -325,10 +327,9 @@ static int record_step(zh_engine *e, bool collect) {
             const uint32_t ms[3] = {qd, kvd, kvd};
             ERC(zhk_dmmv_multi(c, m.type_attn, 3, ws, ys, ms, e->xq_h, H));
         }
-        ERC(zhk_qk_norm_rope_kv(c, e->q, Wf(y.q_norm), e->k, Wf(y.k_norm), e->v, e->inv_freq, y.kc, y.vc, e->pages,
-                                e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd, pos, m.eps));
-        ERC(zhk_flash_decode(c, e->q, y.kc, y.vc, e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads,
-                             m.n_kv_heads, hd, seq, m.max_ctx, scale, e->fd_part));
+        ERC(zhk_attn_decode_fused(c, e->q, e->k, e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc,
+                                  e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads, m.n_kv_heads, pos,
+                                  m.max_ctx, scale, m.eps, e->fd_part));
         if (lpb_attn) {
             // the merge kernel already emitted the attention output as XQ
             const uint8_t *wo = W(y.wo);

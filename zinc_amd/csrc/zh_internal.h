@@ -92,6 +92,16 @@ int zhk_flash_decode(zh_ctx *ctx, const float *q, const uint16_t *kc, const uint
                      void *xq_out, uint32_t nh, uint32_t nkv, uint32_t hd, zh_pos_src seq_len,
                      uint32_t max_seq, float scale, float *partials);
 uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t hd, uint32_t max_seq);
+// Fused decode attention: q/k RMSNorm + RoPE, KV write of the new token at
+// `pos`, attention over [0, pos], chunk merge. `partials` as above, with its
+// trailing counter words zero before the first launch.
+// RoPE table cs[pos][64] = (cos, sin) of pos * inv_freq (head_dim 128)
+int zhk_rope_table(zh_ctx *ctx, const float *inv_freq, uint32_t n_pos, float *cs);
+int zhk_attn_decode_fused(zh_ctx *ctx, const float *q, const float *k, const float *v, const float *qw,
+                          const float *kw, const float *rope_cs, uint16_t *kc, uint16_t *vc,
+                          const uint32_t *pages, uint32_t n_pages, uint32_t cache_tokens, float *out,
+                          void *xq_out, uint32_t nh, uint32_t nkv, zh_pos_src pos, uint32_t max_seq,
+                          float scale, float eps, float *partials);
 int zhk_softmax_topk(zh_ctx *ctx, const float *logits, uint32_t n, uint32_t k, uint32_t *routing);
 int zhk_moe_weighted_acc(zh_ctx *ctx, float *a, const float *b, const uint32_t *routing, uint32_t n,
                          uint32_t n_used, uint32_t src_stride);

@@ -8,10 +8,16 @@ static bool in_range(const zh_buf *b, uint64_t off, uint64_t n) { return b && of
 
 // Quantise one 32-element block held one value per lane across a 32-lane
 // group (l = lane index within the group) into XQ block `blk`.
+// Quantises one 32-element block held one value per lane by 32 consecutive
+// lanes (l = lane & 31). Each 32-lane half of the wave is either fully
+// active or fully inactive.
+ZH_DEV float half_max(float v) {  // max over each 32-lane half, in every lane of it
+    v = row16_max(v);
+    const float lo = fmaxf(lane_f(v, 0), lane_f(v, 16)), hi = fmaxf(lane_f(v, 32), lane_f(v, 48));
+    return (threadIdx.x & 32) ? hi : lo;
+}
 ZH_DEV void xq_store_block32(float xi, int l, XQView v, uint32_t blk) {
-    float a = fabsf(xi);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
+    float a = half_max(fabsf(xi));
     float inv, sc;
     xq_scales(a, inv, sc);
     int X = xq_quant(xi, inv);
@@ -20,9 +26,12 @@ ZH_DEV void xq_store_block32(float xi, int l, XQView v, uint32_t blk) {
     v.limb[blk * 96 + l] = (int8_t)l0;
     v.limb[blk * 96 + 32 + l] = (int8_t)l1;
     v.limb[blk * 96 + 64 + l] = (int8_t)l2;
+    // integer sum over each 16-lane row: the block's two 16-element sums
     int s = X;
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 32);
+    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x141, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x140, 0xF, 0xF, false);
     if (l == 0) v.xs[blk] = sc;
     if ((l & 15) == 0) v.xsum[blk * 2 + (l >> 4)] = (float)s * sc;
 }
@@ -192,73 +201,233 @@ extern "C" int zh_qk_norm_rope_kv_write(zh_ctx *c, zh_buf *q, const zh_buf *qw, 
 }
 
 // ---------------------------------------------------------------------------
-// Flash-decode. Grid (n_kv_heads, n_chunks): workgroup (h, c) handles the
-// GQA group of kv head h over tokens [c*C, c*C+C) and writes, per q head,
-// the chunk's unnormalised output O, running max m and denominator l.
-// A merge kernel combines chunks with log-sum-exp weights.
-// Cache layout [kv_head][token][head_dim] fp16, read through 16-token pages.
+// Decode attention (flash_decode.comp + the qk_norm_rope_kv_write.comp work
+// of the new token, forward.zig decodeStep attention block), one kernel:
+//
+//   grid (n_kv_heads, n_chunks), 256 threads = 4 waves x 32 tokens, so a
+//   workgroup covers a 128-token chunk of one kv head's GQA group.
+//   - FUSED: q (raw Q projection), the new token's raw k/v, per-head RMSNorm
+//     weights and RoPE frequencies come in; every wave normalises and ropes q
+//     in registers, and the wave that owns the new position also normalises
+//     and ropes k, writes k/v to the fp16 cache and substitutes them for the
+//     cache rows it loaded before the write.
+//   - scores / chunk softmax / P*V per wave, the 4 waves combined in LDS
+//     with log-sum-exp weights, one partial (O, m, l) per q head and chunk.
+//   - the last workgroup to finish for a kv head (agent-scope counter) merges
+//     the chunks and writes the attention output (f32, optional XQ) and
+//     resets the counter for the next launch.
+// Dims are held as (d, d+64) pairs, sub*8..sub*8+7 and 64+sub*8.., so NeoX
+// RoPE pairs stay inside a lane. Cache layout [kv_head][token][128] fp16,
+// addressed through 16-token pages.
 // ---------------------------------------------------------------------------
-constexpr int FD_MAXG = 8;     // q heads per kv head (GQA group) handled per wave
-constexpr int FD_HD = 128;     // head_dim supported by the kernel
-constexpr int FD_T = 32;       // tokens per chunk; one wave per (kv head, chunk)
+#ifdef ZH_EXP_TRACE
+__device__ uint64_t g_exp_trace_ops[16384 * 8];
+#define TRACE_OPS(slot) do { const uint32_t bl_ = blockIdx.x + blockIdx.y * gridDim.x; \
+    if (threadIdx.x == 0 && bl_ < 16384) g_exp_trace_ops[bl_ * 8 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+extern "C" int zh_exp_trace_ops_dump(uint64_t *host, uint32_t n) {
+    int rc = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_trace_ops), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
+    static uint64_t zeros[16384 * 8];
+    return rc | (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_trace_ops), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+#else
+#define TRACE_OPS(slot) do { } while (0)
+#endif
+constexpr int FD_MAXG = 8;   // q heads per kv head
+constexpr int FD_HD = 128;   // head_dim supported
+constexpr int AD_W = 4;      // waves per workgroup
+constexpr int AD_TW = 32;    // tokens per wave
+constexpr int AD_TC = AD_W * AD_TW;  // tokens per chunk
 
 uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t hd, uint32_t max_seq) {
-    return (uint64_t)nh * ((max_seq + FD_T - 1) / FD_T) * (hd + 2) * 4 + 256;
+    // partials + one counter word per head (the counters never exceed nh)
+    return (uint64_t)nh * ((max_seq + AD_TC - 1) / AD_TC) * (hd + 2) * 4 + 4ull * nh + 256;
 }
 
-// One wave = one (kv head, 32-token chunk): all K and V loads are issued up
-// front (16 KB per wave, one memory latency), scores use 8 lanes per token
-// (16 dims each), the chunk softmax stays in registers, and P*V runs with
-// lane = 2 output dims. Writes unnormalised O, chunk max m and sum l per q head.
-template <int G>
-__global__ __launch_bounds__(64) void k_flash_decode(const float *__restrict__ q, const uint16_t *__restrict__ kc,
-                                                     const uint16_t *__restrict__ vc,
-                                                     const uint32_t *__restrict__ pages, uint32_t n_pages,
-                                                     uint32_t cache_tokens, uint32_t n_chunks, zh_pos_src seq_src,
-                                                     float scale, float *__restrict__ part) {
-    const uint32_t kvh = blockIdx.x, chunk = blockIdx.y, lane = threadIdx.x;
-    const uint32_t seq_len = read_pos(seq_src);
-    const uint32_t t0 = chunk * FD_T;
-    if (t0 >= seq_len) return;
-    const uint32_t nt = min(t0 + FD_T, seq_len) - t0;
-    const uint32_t sub = lane & 7, grp = lane >> 3;
-    const uint16_t *kh = kc + (size_t)kvh * cache_tokens * FD_HD;
-    const uint16_t *vh = vc + (size_t)kvh * cache_tokens * FD_HD;
-    auto phys_of = [&](uint32_t i) -> uint32_t {
-        uint32_t t = t0 + (i < nt ? i : nt - 1), pg = t / 16;
-        uint32_t ph = (pg < n_pages) ? pages[pg] * 16 + t % 16 : 0;
-        return ph < cache_tokens ? ph : 0;
-    };
-    // K: pass j covers tokens 8j + grp; lane reads dims sub*16 .. +15 (32 B)
-    u32x4 kr[FD_T / 8][2];
+struct AttnP {
+    const float *q;                // FUSED: raw Q projection; else prepared (normed, roped) q
+    const float *k_new, *v_new;    // FUSED: raw K/V projection of the new token
+    const float *q_norm, *k_norm;  // FUSED: per-head RMSNorm weights (128)
+    const float *rope_cs;          // FUSED: [position][64] (cos, sin) pairs of pos * inv_freq
+    uint16_t *kc, *vc;
+    const uint32_t *pages;
+    uint32_t n_pages, cache_tokens;
+    zh_pos_src pos;  // FUSED: position of the new token (seq = pos + 1); else seq_len
+    float scale, eps;
+    float *part;     // [nq][n_chunks][130]
+    uint32_t n_chunks;
+    uint32_t *counters;  // [nkv], zero between launches
+    float *out;          // [nq * 128]
+    uint8_t *xq;         // optional XQ image of out
+    uint32_t nq;
+};
+
+ZH_DEV float sum8(float v) { return row8_sum(v); }  // over the 8 lanes of a token group
+
+// RMSNorm (weights w) + NeoX RoPE on one head held as lo[e] = x[sub*8+e],
+// hi[e] = x[64+sub*8+e] (qk_norm_rope_kv_write.comp:67-171 arithmetic).
+ZH_DEV void norm_rope16(float (&lo)[8], float (&hi)[8], const float (&wlo)[8], const float (&whi)[8],
+                        const float (&co)[8], const float (&sn)[8], float eps) {
+    float sq = 0.f;
 #pragma unroll
-    for (int j = 0; j < FD_T / 8; j++) {
-        const u32x4 *kp = (const u32x4 *)(kh + (size_t)phys_of(8 * j + grp) * FD_HD + sub * 16);
-        kr[j][0] = kp[0];
-        kr[j][1] = kp[1];
+    for (int e = 0; e < 8; e++) sq = fmaf(lo[e], lo[e], fmaf(hi[e], hi[e], sq));
+    sq = sum8(sq);
+    const float rms_inv = 1.0f / sqrtf(sq / (float)FD_HD + eps);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float a = wlo[e] * (lo[e] * rms_inv);
+        const float b = whi[e] * (hi[e] * rms_inv);
+        lo[e] = a * co[e] - b * sn[e];
+        hi[e] = a * sn[e] + b * co[e];
     }
-    // V: token i, dims 2*lane, 2*lane+1
-    uint32_t vr[FD_T];
-#pragma unroll
-    for (int i = 0; i < FD_T; i++) vr[i] = *(const uint32_t *)(vh + (size_t)phys_of(i) * FD_HD + 2 * lane);
-    // q for this lane's 16 dims, pre-scaled
-    float qf[G][16];
+}
+
+// Device-scope (all XCDs) store / load of one float: coherent without L2
+// write-back or invalidation of other data.
+ZH_DEV void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+#ifdef ZH_EXP_PLAIN
+ZH_DEV float ld_dev(const float *p) { return *p; }
+ZH_DEV uint64_t ld_dev64(const float *p) { return *(const uint64_t *)p; }
+#else
+ZH_DEV float ld_dev(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+ZH_DEV uint64_t ld_dev64(const float *p) {  // two floats, 8-byte aligned
+    return __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+#endif
+
+// Two f32 -> packed f16 with the hardware conversion (round to nearest
+// even; fp16 denormals are kept in this build's default FP mode), as the
+// cache write's @floatCast.
+ZH_DEV uint32_t pack_h2(float a, float b) {
+    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+template <int G, bool FUSED>
+__global__ __launch_bounds__(256, 2) void k_attn_decode(AttnP p) {
+    const uint32_t kvh = blockIdx.x, tid = threadIdx.x;
+    // chunks are dispatched last-first: the chunk holding the newest tokens
+    // (and, FUSED, the KV write) must never wait in the dispatch tail
+    const uint32_t seq_hint = FUSED ? read_pos(p.pos) + 1 : read_pos(p.pos);
+    const uint32_t nv_hint = (seq_hint + AD_TC - 1) / AD_TC;
+    const uint32_t chunk = blockIdx.y < nv_hint ? nv_hint - 1 - blockIdx.y : blockIdx.y;
+    const uint32_t wave = tid >> 6, lane = tid & 63, sub = lane & 7, grp = lane >> 3;
+    TRACE_OPS(0);
+    const uint32_t t0 = chunk * AD_TC, tw0 = t0 + wave * AD_TW;
+    // position and this wave's two page entries are independent loads
+    const uint32_t pg0 = min(tw0 / 16, p.n_pages - 1), pg1 = min(tw0 / 16 + 1, p.n_pages - 1);
+    const uint32_t page0 = p.pages[pg0], page1 = p.pages[pg1];
+    const uint32_t posv = read_pos(p.pos);
+    const uint32_t seq = FUSED ? posv + 1 : posv;
+    if (t0 >= seq) return;  // uniform over the workgroup
+    const uint32_t nt = seq > tw0 ? min(seq - tw0, (uint32_t)AD_TW) : 0u;
+    // K/V rows of this wave's 32 tokens: two 16-token pages, each a
+    // contiguous 4 KB run, so every row is a constant offset from a page
+    // base. Rows past the end of the sequence are read (in-bounds) and masked.
+    const uint32_t ptok = p.cache_tokens / 16;
+    const size_t pa = page0 < ptok ? page0 : 0u, pb = page1 < ptok ? page1 : 0u;
+    const uint16_t *kh = p.kc + (size_t)kvh * p.cache_tokens * FD_HD;
+    const uint16_t *vh = p.vc + (size_t)kvh * p.cache_tokens * FD_HD;
+    const uint16_t *kb[2] = {kh + pa * 16 * FD_HD, kh + pb * 16 * FD_HD};
+    const uint16_t *vb[2] = {vh + pa * 16 * FD_HD, vh + pb * 16 * FD_HD};
+    // ---- loads: q (and the new token's raw k/v) first, then K, then V
+    float qlo[G][8], qhi[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        const f32x4 *qp = (const f32x4 *)(q + (size_t)(kvh * G + g) * FD_HD + sub * 16);
+        const float *qp = p.q + (size_t)(kvh * G + g) * FD_HD;
+        const f32x4 a = *(const f32x4 *)(qp + sub * 8), b = *(const f32x4 *)(qp + sub * 8 + 4);
+        const f32x4 c = *(const f32x4 *)(qp + 64 + sub * 8), d = *(const f32x4 *)(qp + 64 + sub * 8 + 4);
+        qlo[g][0] = a.x; qlo[g][1] = a.y; qlo[g][2] = a.z; qlo[g][3] = a.w;
+        qlo[g][4] = b.x; qlo[g][5] = b.y; qlo[g][6] = b.z; qlo[g][7] = b.w;
+        qhi[g][0] = c.x; qhi[g][1] = c.y; qhi[g][2] = c.z; qhi[g][3] = c.w;
+        qhi[g][4] = d.x; qhi[g][5] = d.y; qhi[g][6] = d.z; qhi[g][7] = d.w;
+    }
+    float klo[8], khi[8], vn0 = 0.f, vn1 = 0.f;
+    if (FUSED) {
+        const float *kp = p.k_new + (size_t)kvh * FD_HD;
+        const f32x4 a = *(const f32x4 *)(kp + sub * 8), b = *(const f32x4 *)(kp + sub * 8 + 4);
+        const f32x4 c = *(const f32x4 *)(kp + 64 + sub * 8), d = *(const f32x4 *)(kp + 64 + sub * 8 + 4);
+        klo[0] = a.x; klo[1] = a.y; klo[2] = a.z; klo[3] = a.w; klo[4] = b.x; klo[5] = b.y; klo[6] = b.z; klo[7] = b.w;
+        khi[0] = c.x; khi[1] = c.y; khi[2] = c.z; khi[3] = c.w; khi[4] = d.x; khi[5] = d.y; khi[6] = d.z; khi[7] = d.w;
+        const float2 vv = *(const float2 *)(p.v_new + (size_t)kvh * FD_HD + 2 * lane);
+        vn0 = vv.x;
+        vn1 = vv.y;
+    }
+    float co[8], sn[8], qwl[8], qwh[8], kwl[8], kwh[8];
+    if (FUSED) {
+        const f32x4 *w4 = (const f32x4 *)(p.q_norm + sub * 8), *w5 = (const f32x4 *)(p.q_norm + 64 + sub * 8);
+        const f32x4 *w6 = (const f32x4 *)(p.k_norm + sub * 8), *w7 = (const f32x4 *)(p.k_norm + 64 + sub * 8);
 #pragma unroll
-        for (int e4 = 0; e4 < 4; e4++) {
-            f32x4 t = qp[e4];
-            qf[g][4 * e4 + 0] = t.x * scale; qf[g][4 * e4 + 1] = t.y * scale;
-            qf[g][4 * e4 + 2] = t.z * scale; qf[g][4 * e4 + 3] = t.w * scale;
+        for (int h2 = 0; h2 < 2; h2++) {
+            const f32x4 a = w4[h2], b = w5[h2], c = w6[h2], d = w7[h2];
+            qwl[4 * h2] = a.x; qwl[4 * h2 + 1] = a.y; qwl[4 * h2 + 2] = a.z; qwl[4 * h2 + 3] = a.w;
+            qwh[4 * h2] = b.x; qwh[4 * h2 + 1] = b.y; qwh[4 * h2 + 2] = b.z; qwh[4 * h2 + 3] = b.w;
+            kwl[4 * h2] = c.x; kwl[4 * h2 + 1] = c.y; kwl[4 * h2 + 2] = c.z; kwl[4 * h2 + 3] = c.w;
+            kwh[4 * h2] = d.x; kwh[4 * h2 + 1] = d.y; kwh[4 * h2 + 2] = d.z; kwh[4 * h2 + 3] = d.w;
+        }
+        const f32x4 *cs = (const f32x4 *)(p.rope_cs + ((size_t)posv * 64 + sub * 8) * 2);
+#pragma unroll
+        for (int e2 = 0; e2 < 4; e2++) {
+            const f32x4 t = cs[e2];
+            co[2 * e2] = t.x; sn[2 * e2] = t.y; co[2 * e2 + 1] = t.z; sn[2 * e2 + 1] = t.w;
         }
     }
-    // scores s[j][g] for token 8j + grp (replicated over the 8 lanes of grp)
-    float sc[FD_T / 8][G];
+    // Memory returns in issue order: keep the compiler from interleaving or
+    // sinking the groups (q / new token / RoPE first, then K, then V), so the
+    // q preparation waits only for its own loads.
+    asm volatile("" ::: "memory");
+    u32x4 kr[AD_TW / 8][2];
 #pragma unroll
-    for (int j = 0; j < FD_T / 8; j++) {
-        uint32_t kw[8] = {kr[j][0].x, kr[j][0].y, kr[j][0].z, kr[j][0].w,
-                          kr[j][1].x, kr[j][1].y, kr[j][1].z, kr[j][1].w};
+    for (int j = 0; j < AD_TW / 8; j++) {
+        const uint16_t *kp = kb[j >> 1] + (8 * (j & 1) + grp) * FD_HD;
+        kr[j][0] = *(const u32x4 *)(kp + sub * 8);
+        kr[j][1] = *(const u32x4 *)(kp + 64 + sub * 8);
+    }
+    asm volatile("" ::: "memory");
+    uint32_t vr[AD_TW];
+#pragma unroll
+    for (int i = 0; i < AD_TW; i++) vr[i] = *(const uint32_t *)(vb[i >> 4] + (i & 15) * FD_HD + 2 * lane);
+    asm volatile("" ::: "memory");
+
+    // ---- q (and new k) preparation
+    bool owner = false;  // this wave's tokens include the new position (uniform per wave)
+    uint32_t inew = 0, vnew = 0;
+    u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0};
+    if (FUSED) {
+#pragma unroll
+        for (int g = 0; g < G; g++) norm_rope16(qlo[g], qhi[g], qwl, qwh, co, sn, p.eps);
+        owner = posv >= tw0 && posv < tw0 + AD_TW;
+        if (owner) {
+            // the cache rows loaded above for this position predate the write
+            // below; scores and P*V select these values for it instead
+            norm_rope16(klo, khi, kwl, kwh, co, sn, p.eps);
+            n0 = u32x4{pack_h2(klo[0], klo[1]), pack_h2(klo[2], klo[3]), pack_h2(klo[4], klo[5]),
+                       pack_h2(klo[6], klo[7])};
+            n1 = u32x4{pack_h2(khi[0], khi[1]), pack_h2(khi[2], khi[3]), pack_h2(khi[4], khi[5]),
+                       pack_h2(khi[6], khi[7])};
+            vnew = pack_h2(vn0, vn1);
+            inew = posv - tw0;
+            // logicalTokenToPhysicalToken for the new position; the host has
+            // checked the context length, an unmapped slot is skipped
+            const uint32_t slot = posv / 16;
+            uint32_t ph = slot < p.n_pages ? p.pages[slot] * 16 + posv % 16 : p.cache_tokens;
+            if (ph < p.cache_tokens) {
+                if (grp == (inew & 7)) {
+                    *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + sub * 8) = n0;
+                    *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 64 + sub * 8) = n1;
+                }
+                *(uint32_t *)(p.vc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 2 * lane) = vnew;
+            }
+        }
+    }
+    TRACE_OPS(1);
+
+    // ---- scores: token 8j + grp, 16 dims per lane, reduced over 8 lanes
+    float sc[AD_TW / 8][G];
+#pragma unroll
+    for (int j = 0; j < AD_TW / 8; j++) {
+        const bool sel = owner && (uint32_t)(8 * j) + grp == inew;
+        const u32x4 k0 = sel ? n0 : kr[j][0], k1 = sel ? n1 : kr[j][1];
+        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
         float kf[16];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -268,132 +437,277 @@ __global__ __launch_bounds__(64) void k_flash_decode(const float *__restrict__ q
         const bool valid = (uint32_t)(8 * j) + grp < nt;
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            float s = 0.f;
+            float sacc = 0.f;
 #pragma unroll
-            for (int e = 0; e < 16; e++) s = fmaf(qf[g][e], kf[e], s);
-            s += __shfl_xor(s, 1, 64);
-            s += __shfl_xor(s, 2, 64);
-            s += __shfl_xor(s, 4, 64);
-            sc[j][g] = valid ? s : -INFINITY;
+            for (int e = 0; e < 8; e++) {
+                sacc = fmaf(qlo[g][e], kf[e], sacc);
+                sacc = fmaf(qhi[g][e], kf[8 + e], sacc);
+            }
+            sacc = sum8(sacc) * p.scale;  // dot * scale, as cpuAttention
+            sc[j][g] = valid ? sacc : -INFINITY;
         }
     }
-    // chunk softmax per head: max and sum over passes and the 8 groups
-    __shared__ float ps[G][FD_T];
-    float mx[G], ls[G];
+    TRACE_OPS(2);
+    // ---- per-wave softmax over its 32 tokens, P*V with lane = 2 output dims
+    __shared__ float ps[AD_W][G][AD_TW];
+    __shared__ float wm[AD_W][G], wl[AD_W][G];
+    __shared__ float wo[AD_W][G][FD_HD];
+    float mx[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         float m = sc[0][g];
 #pragma unroll
-        for (int j = 1; j < FD_T / 8; j++) m = fmaxf(m, sc[j][g]);
-        m = fmaxf(m, __shfl_xor(m, 8, 64));
-        m = fmaxf(m, __shfl_xor(m, 16, 64));
-        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        for (int j = 1; j < AD_TW / 8; j++) m = fmaxf(m, sc[j][g]);
+        m = rows_max(fmaxf(m, dpp_f<0x140>(m)));  // m is uniform within each 8-lane token group
+        const float ms = m == -INFINITY ? 0.f : m;  // a wave past the end has no valid token
         float l = 0.f;
 #pragma unroll
-        for (int j = 0; j < FD_T / 8; j++) {
-            float p = expf(sc[j][g] - m);  // exp(-inf) = 0 for invalid tokens
-            if (sub == 0) ps[g][8 * j + grp] = p;
-            l += p;
+        for (int j = 0; j < AD_TW / 8; j++) {
+            const float pr = expf(sc[j][g] - ms);
+            if (sub == 0) ps[wave][g][8 * j + grp] = pr;
+            l += pr;
         }
-        l += __shfl_xor(l, 8, 64);
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        l = rows_sum(l + dpp_f<0x140>(l));
         mx[g] = m;
-        ls[g] = l;
+        if (lane == 0) { wm[wave][g] = m; wl[wave][g] = l; }
     }
-    __syncthreads();  // single wave: orders the LDS probability writes
+    __syncthreads();
     float acc[G][2];
 #pragma unroll
     for (int g = 0; g < G; g++) acc[g][0] = acc[g][1] = 0.f;
 #pragma unroll
-    for (int i = 0; i < FD_T; i++) {
-        const float v0 = h2f(vr[i]), v1 = h2f(vr[i] >> 16);
+    for (int i4 = 0; i4 < AD_TW; i4 += 4) {
+        f32x4 pr[G];
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float p = ps[g][i];
-            acc[g][0] = fmaf(p, v0, acc[g][0]);
-            acc[g][1] = fmaf(p, v1, acc[g][1]);
+        for (int g = 0; g < G; g++) pr[g] = *(const f32x4 *)&ps[wave][g][i4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i4 + u;
+            uint32_t vv = owner && (uint32_t)i == inew ? vnew : vr[i];
+            vv = (uint32_t)i < nt ? vv : 0u;  // rows past the end may hold anything
+            const float v0 = h2f(vv), v1 = h2f(vv >> 16);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float q = pr[g][u];
+                acc[g][0] = fmaf(q, v0, acc[g][0]);
+                acc[g][1] = fmaf(q, v1, acc[g][1]);
+            }
         }
     }
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        float *pp = part + ((size_t)(kvh * G + g) * n_chunks + chunk) * (FD_HD + 2);
-        *(float2 *)(pp + 2 * lane) = make_float2(acc[g][0], acc[g][1]);
-        if (lane == 0) { pp[FD_HD] = mx[g]; pp[FD_HD + 1] = ls[g]; }
+    for (int g = 0; g < G; g++) *(float2 *)&wo[wave][g][2 * lane] = make_float2(acc[g][0], acc[g][1]);
+    (void)mx;
+    __syncthreads();
+    // ---- combine the 4 waves: thread -> (head, dim) outputs
+    for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += 256) {
+        const uint32_t g = o / FD_HD, d = o % FD_HD;
+        float M = wm[0][g];
+#pragma unroll
+        for (int w = 1; w < AD_W; w++) M = fmaxf(M, wm[w][g]);
+        const float Ms = M == -INFINITY ? 0.f : M;
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < AD_W; w++) {
+            const float f = wm[w][g] == -INFINITY ? 0.f : expf(wm[w][g] - Ms);
+            L = fmaf(wl[w][g], f, L);
+            O = fmaf(wo[w][g][d], f, O);
+        }
+        float *pp = p.part + ((size_t)(kvh * G + g) * p.n_chunks + chunk) * (FD_HD + 2);
+        st_dev(pp + d, O);
+        if (d == 0) { st_dev(pp + FD_HD, M); st_dev(pp + FD_HD + 1, L); }
     }
+    TRACE_OPS(3);
+    // ---- last workgroup of this kv head merges the chunks
+    const uint32_t nv = (seq + AD_TC - 1) / AD_TC;
+    __shared__ uint32_t s_last;
+    // The partials went out as device-scope stores, coherent across the
+    // XCDs' L2s. Waiting for them to complete (s_waitcnt 0 in every wave,
+    // then the barrier) before a relaxed device-scope counter increment
+    // publishes them without the full L2 write-back / invalidate that
+    // agent-scope release / acquire fences imply; the reader uses
+    // device-scope loads.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(p.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == nv - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    TRACE_OPS(4);
+    if (!s_last) return;
+    // Chunk merge. The first batch of each thread's O dims (NBAT chunks) is
+    // requested before the chunk statistics, so both arrive in about one
+    // round trip; the statistics pass leaves m_c in LDS for the weights.
+    constexpr int OPT = G * FD_HD >= 256 ? G * FD_HD / 256 : 1;  // dims per thread
+    constexpr int NTH = G * FD_HD / OPT;
+    constexpr int NBAT = G <= 4 ? 40 : 12;  // chunks per round of O loads
+    constexpr int MB = 256;                 // chunk statistics kept in LDS
+    __shared__ __align__(16) float sm[G][MB];
+    __shared__ float hM[G], hL[G];
+    __shared__ float ob[G * FD_HD];
+    float O[OPT];
+#pragma unroll
+    for (int k = 0; k < OPT; k++) O[k] = 0.f;
+    const uint32_t g_t = min(tid * OPT / FD_HD, (uint32_t)G - 1), d0 = (tid * OPT) % FD_HD;
+    const float *pt = p.part + (size_t)(kvh * G + g_t) * p.n_chunks * (FD_HD + 2);
+    float v[NBAT][OPT];
+    auto load_o = [&](uint32_t cb) {
+#pragma unroll
+        for (int u = 0; u < NBAT; u++) {
+            const float *pc = pt + (size_t)min(cb + u, nv - 1) * (FD_HD + 2) + d0;
+            if (OPT == 1) {
+                v[u][0] = ld_dev(pc);
+            } else {
+#pragma unroll
+                for (int w = 0; w < OPT / 2; w++) {
+                    const uint64_t x = ld_dev64(pc + 2 * w);
+                    v[u][2 * w] = __uint_as_float((uint32_t)x);
+                    v[u][2 * w + 1] = __uint_as_float((uint32_t)(x >> 32));
+                }
+            }
+        }
+    };
+    const bool one_batch = nv <= (uint32_t)NBAT;  // uniform
+    if (one_batch) load_o(0);
+    asm volatile("" ::: "memory");  // the O loads go out before the statistics loads
+    for (uint32_t g = wave; g < (uint32_t)G; g += AD_W) {
+        const float *pp = p.part + (size_t)(kvh * G + g) * p.n_chunks * (FD_HD + 2);
+        float m = -INFINITY, l = 0.f;
+        for (uint32_t c = lane; c < nv; c += 64) {
+            const uint64_t ml = ld_dev64(pp + (size_t)c * (FD_HD + 2) + FD_HD);
+            const float mc = __uint_as_float((uint32_t)ml), lc = __uint_as_float((uint32_t)(ml >> 32));
+            if (c < MB) sm[g][c] = mc;
+            const float mn = fmaxf(m, mc);
+            l = fmaf(l, m == -INFINITY ? 0.f : expf(m - mn), lc * expf(mc - mn));
+            m = mn;
+        }
+        const float M = wave_max(m);
+        l = wave_sum(m == -INFINITY ? 0.f : l * expf(m - M));
+        if (lane == 0) { hM[g] = M; hL[g] = l; }
+    }
+#ifdef ZH_EXP_MERGE_TRACE
+    TRACE_OPS(1);
+#endif
+    __syncthreads();
+#ifdef ZH_EXP_MERGE_TRACE
+    TRACE_OPS(2);
+#endif
+    const float Mt = hM[g_t];
+    if (one_batch) {
+        // weights exp(m_c - M) once per (head, chunk), in place in LDS
+        for (uint32_t i = tid; i < (uint32_t)G * NBAT; i += 256) {
+            const uint32_t g = i / NBAT, c = i % NBAT;
+            sm[g][c] = c < nv ? expf(sm[g][c] - hM[g]) : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u4 = 0; u4 < NBAT; u4 += 4) {
+            const f32x4 w4 = *(const f32x4 *)&sm[g_t][u4];
+#pragma unroll
+            for (int k = 0; k < OPT; k++) {
+                O[k] = fmaf(v[u4][k], w4.x, O[k]);
+                O[k] = fmaf(v[u4 + 1][k], w4.y, O[k]);
+                O[k] = fmaf(v[u4 + 2][k], w4.z, O[k]);
+                O[k] = fmaf(v[u4 + 3][k], w4.w, O[k]);
+            }
+        }
+    } else {
+        // long contexts: one round of loads per NBAT chunks
+        for (uint32_t cb = 0; cb < nv; cb += NBAT) {
+            load_o(cb);
+#pragma unroll
+            for (int u = 0; u < NBAT; u++) {
+                const uint32_t c = cb + u;
+                const float mc = c < MB ? sm[g_t][c < MB ? c : 0] : ld_dev(pt + (size_t)min(c, nv - 1) * (FD_HD + 2) + FD_HD);
+                const float wgt = c < nv ? expf(mc - Mt) : 0.f;
+#pragma unroll
+                for (int k = 0; k < OPT; k++) O[k] = fmaf(v[u][k], wgt, O[k]);
+            }
+        }
+    }
+    TRACE_OPS(6);
+    if (tid < (uint32_t)NTH) {
+#pragma unroll
+        for (int k = 0; k < OPT; k++) {
+            const float r = hL[g_t] > 0.f ? O[k] / hL[g_t] : 0.f;
+            ob[tid * OPT + k] = r;
+            if (p.out) p.out[(size_t)(kvh * G) * FD_HD + tid * OPT + k] = r;
+        }
+    }
+    TRACE_OPS(7);
+    if (p.xq) {
+        __syncthreads();
+        XQView v = xq_view(p.xq, p.nq * FD_HD / 32);
+        for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += 256)  // whole 32-lane groups (G*128 % 32 == 0)
+            xq_store_block32(ob[o], o & 31, v, (kvh * G * FD_HD + o) / 32);
+    }
+    if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    TRACE_OPS(5);
 }
 
-// LSE merge: one 256-thread workgroup per q head. Chunk statistics are read
-// in parallel, then each (dim, chunk-quarter) thread accumulates its share.
-__global__ __launch_bounds__(256) void k_flash_merge(const float *__restrict__ part, uint32_t n_chunks, uint32_t C,
-                                                     zh_pos_src seq_src, float *__restrict__ out, uint8_t *xq) {
-    const uint32_t h = blockIdx.x, tid = threadIdx.x;
-    const uint32_t seq_len = read_pos(seq_src);
-    const uint32_t nv = min(n_chunks, (seq_len + C - 1) / C);
-    const float *pp = part + (size_t)h * n_chunks * (FD_HD + 2);
-    __shared__ float wsh[1024];
-    __shared__ float red[4];
-    __shared__ float osum[2][FD_HD];
-    // chunk maxima
-    float m = -INFINITY;
-    for (uint32_t c = tid; c < nv; c += 256) m = fmaxf(m, pp[c * (FD_HD + 2) + FD_HD]);
-    m = wave_max(m);
-    if ((tid & 63) == 0) red[tid >> 6] = m;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float l = 0.f;
-    for (uint32_t c = tid; c < nv; c += 256) {
-        float w = expf(pp[c * (FD_HD + 2) + FD_HD] - M);
-        wsh[c] = w;
-        l = fmaf(pp[c * (FD_HD + 2) + FD_HD + 1], w, l);
+// partials: zhk_flash_decode_partials_bytes(nh, hd, max_seq) bytes; the
+// counter words at its end must be zero before the first launch (each
+// launch leaves them zero).
+static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uint32_t max_seq, bool fused) {
+    AttnP p = p0;
+    p.n_chunks = (max_seq + AD_TC - 1) / AD_TC;
+    dim3 grid(nkv, p.n_chunks);
+#define AD_LAUNCH(GG)                                                                                  \
+    if (fused) hipLaunchKernelGGL((k_attn_decode<GG, true>), grid, dim3(256), 0, c->stream, p);       \
+    else hipLaunchKernelGGL((k_attn_decode<GG, false>), grid, dim3(256), 0, c->stream, p)
+    switch (G) {
+    case 1: AD_LAUNCH(1); break;
+    case 2: AD_LAUNCH(2); break;
+    case 4: AD_LAUNCH(4); break;
+    case 8: AD_LAUNCH(8); break;
+    default: return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "GQA group %u unsupported (1, 2, 4, 8)", G);
     }
-    l = wave_sum(l);
-    if ((tid & 63) == 0) red[tid >> 6] = l;
-    __syncthreads();
-    const float L = red[0] + red[1] + red[2] + red[3];
-    // O: thread (d, half) sums chunks c = half, half+2, ...
-    const uint32_t d = tid & (FD_HD - 1), half = tid >> 7;
-    float O = 0.f;
-#pragma unroll 8
-    for (uint32_t c = half; c < nv; c += 2) O = fmaf(pp[c * (FD_HD + 2) + d], wsh[c], O);
-    osum[half][d] = O;
-    __syncthreads();
-    if (tid < FD_HD) {
-        float o = L > 0.f ? (osum[0][tid] + osum[1][tid]) / L : 0.f;
-        out[(size_t)h * FD_HD + tid] = o;
-        if (xq) {
-            XQView v = xq_view(xq, gridDim.x * FD_HD / 32);
-            xq_store_block32(o, tid & 31, v, (h * FD_HD + tid) / 32);
-        }
-    }
+#undef AD_LAUNCH
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+static uint32_t *attn_counters(float *partials, uint32_t nh, uint32_t hd, uint32_t max_seq) {
+    return (uint32_t *)((char *)partials + (uint64_t)nh * ((max_seq + AD_TC - 1) / AD_TC) * (hd + 2) * 4);
 }
 
 int zhk_flash_decode(zh_ctx *c, const float *q, const uint16_t *kc, const uint16_t *vc, const uint32_t *pages,
                      uint32_t n_pages, uint32_t cache_tokens, float *out, void *xq_out, uint32_t nh, uint32_t nkv,
                      uint32_t hd, zh_pos_src seq_len, uint32_t max_seq, float scale, float *partials) {
-    const uint32_t G = nh / nkv;
-    const uint32_t C = FD_T;
-    const uint32_t n_chunks = (max_seq + C - 1) / C;
-    if (n_chunks > 1024) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "context too long for merge (%u chunks)", n_chunks);
-    dim3 grid(nkv, n_chunks);
-#define FD_LAUNCH(GG)                                                                                              \
-    hipLaunchKernelGGL(k_flash_decode<GG>, grid, dim3(64), 0, c->stream, q, kc, vc, pages, n_pages, cache_tokens, \
-                       n_chunks, seq_len, scale, partials)
-    switch (G) {
-    case 1: FD_LAUNCH(1); break;
-    case 2: FD_LAUNCH(2); break;
-    case 4: FD_LAUNCH(4); break;
-    case 8: FD_LAUNCH(8); break;
-    default: return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "GQA group %u unsupported (1, 2, 4, 8)", G);
-    }
-#undef FD_LAUNCH
+    AttnP p = {};
+    p.q = q; p.kc = (uint16_t *)kc; p.vc = (uint16_t *)vc; p.pages = pages; p.n_pages = n_pages;
+    p.cache_tokens = cache_tokens; p.pos = seq_len; p.scale = scale; p.part = partials;
+    p.counters = attn_counters(partials, nh, hd, max_seq); p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
+    return attn_launch(c, p, nkv, nh / nkv, max_seq, false);
+}
+
+// RoPE table: cs[pos][i] = (cos, sin) of (float)pos * inv_freq[i], i < 64,
+// the same f32 expression the per-position kernels evaluate.
+__global__ void k_rope_table(const float *inv_freq, uint32_t n_pos, float *cs) {
+    const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= n_pos * 64) return;
+    const uint32_t pos = idx / 64, i = idx % 64;
+    float sn, co;
+    sincosf((float)pos * inv_freq[i], &sn, &co);
+    cs[2 * idx] = co;
+    cs[2 * idx + 1] = sn;
+}
+int zhk_rope_table(zh_ctx *c, const float *inv_freq, uint32_t n_pos, float *cs) {
+    hipLaunchKernelGGL(k_rope_table, dim3((n_pos * 64 + 255) / 256), dim3(256), 0, c->stream, inv_freq, n_pos, cs);
     ZH_LAUNCH_CHECK(c);
-    hipLaunchKernelGGL(k_flash_merge, dim3(nh), dim3(256), 0, c->stream, (const float *)partials, n_chunks, C,
-                       seq_len, out, (uint8_t *)xq_out);
-    ZH_LAUNCH_CHECK(c);
-    (void)hd;
     return ZH_OK;
+}
+
+int zhk_attn_decode_fused(zh_ctx *c, const float *q, const float *k, const float *v, const float *qw, const float *kw,
+                          const float *rope_cs, uint16_t *kc, uint16_t *vc, const uint32_t *pages, uint32_t n_pages,
+                          uint32_t cache_tokens, float *out, void *xq_out, uint32_t nh, uint32_t nkv, zh_pos_src pos,
+                          uint32_t max_seq, float scale, float eps, float *partials) {
+    AttnP p = {};
+    p.q = q; p.k_new = k; p.v_new = v; p.q_norm = qw; p.k_norm = kw; p.rope_cs = rope_cs;
+    p.kc = kc; p.vc = vc; p.pages = pages; p.n_pages = n_pages; p.cache_tokens = cache_tokens; p.pos = pos;
+    p.scale = scale; p.eps = eps; p.part = partials; p.counters = attn_counters(partials, nh, FD_HD, max_seq);
+    p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
+    return attn_launch(c, p, nkv, nh / nkv, max_seq, true);
 }
 
 extern "C" int zh_flash_decode(zh_ctx *c, const zh_buf *q, const zh_buf *kc, const zh_buf *vc, const zh_buf *pages,
@@ -411,6 +725,7 @@ extern "C" int zh_flash_decode(zh_ctx *c, const zh_buf *q, const zh_buf *kc, con
     void *scr;
     int rc = zh_scratch(c, zhk_flash_decode_partials_bytes(nh, hd, seq_len), &scr);
     if (rc) return rc;
+    ZH_HIP(c, hipMemsetAsync(attn_counters((float *)scr, nh, hd, seq_len), 0, 4ull * nh, c->stream));
     float scale = attn_scale != 0.f ? attn_scale : 1.0f / sqrtf((float)hd);
     return zhk_flash_decode(c, (const float *)q->ptr, (const uint16_t *)kc->ptr, (const uint16_t *)vc->ptr,
                             (const uint32_t *)pages->ptr, n_pages, cache_tokens, (float *)out->ptr, nullptr, nh, nkv,
