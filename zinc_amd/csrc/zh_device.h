@@ -113,6 +113,20 @@ ZH_DEV float row16_max(float v) { v = row8_max(v); return fmaxf(v, dpp_f<0x140>(
 ZH_DEV float rows_sum(float v) { return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48)); }
 ZH_DEV float rows_max(float v) { return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48))); }
 ZH_DEV float wave_sum(float v) { return rows_sum(row16_sum(v)); }
+// Sum over aligned teams of TL lanes (TL = 4..64), result in every lane of
+// the team. All lanes of the wave active.
+template <int TL>
+ZH_DEV float team_sum_dpp(float v) {
+    if (TL == 4) {
+        v += dpp_f<0xB1>(v);
+        return v + dpp_f<0x4E>(v);
+    }
+    if (TL == 8) return row8_sum(v);
+    v = row16_sum(v);
+    if (TL == 32) return v + __shfl_xor(v, 16, 64);
+    if (TL >= 64) return rows_sum(v);
+    return v;
+}
 ZH_DEV float wave_max(float v) { return rows_max(row16_max(v)); }
 
 ZH_DEV float h2f(uint32_t h16) { return (float)__ushort_as_half((unsigned short)(h16 & 0xFFFF)); }

@@ -62,10 +62,8 @@ ZH_DEV void stage_x(const float *__restrict__ x, const float *__restrict__ norm_
             v.z = w.z * (v.z * rms_inv); v.w = w.w * (v.w * rms_inv);
             if (normed_out && blockIdx.x == 0 && blockIdx.y == 0) *(f32x4 *)(normed_out + e0) = v;
         }
-        float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        a = fmaxf(a, __shfl_xor(a, 1, 64));
-        a = fmaxf(a, __shfl_xor(a, 2, 64));
-        a = fmaxf(a, __shfl_xor(a, 4, 64));
+        // block max over the 8 lanes of this 32-element block (DPP)
+        const float a = row8_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         float inv, sc;
         xq_scales(a, inv, sc);
         int X[4] = {xq_quant(v.x, inv), xq_quant(v.y, inv), xq_quant(v.z, inv), xq_quant(v.w, inv)};
@@ -78,8 +76,8 @@ ZH_DEV void stage_x(const float *__restrict__ x, const float *__restrict__ norm_
         *(uint32_t *)(dst + 32) = pack4(l1[0], l1[1], l1[2], l1[3]);
         *(uint32_t *)(dst + 64) = pack4(l2[0], l2[1], l2[2], l2[3]);
         int s = X[0] + X[1] + X[2] + X[3];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);  // sum over 16 elements (4 lanes)
+        s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);  // 16 elements = 4 lanes
+        s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
         const uint32_t sub = (tid & 7);
         if (sub == 0) lx.xs[b * 8 + j] = sc;
         if ((sub & 3) == 0) lx.xz16[b * 16 + j * 2 + (sub >> 2)] = (float)s * sc;
@@ -556,10 +554,8 @@ ZH_DEV void stage_x_finish(const XRegsF<XCH> &r, bool has_norm, float eps, uint3
             v.z = w.z * (v.z * rms_inv); v.w = w.w * (v.w * rms_inv);
             if (normed_out && blockIdx.x == 0) *(f32x4 *)(normed_out + e0) = v;
         }
-        float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        a = fmaxf(a, __shfl_xor(a, 1, 64));
-        a = fmaxf(a, __shfl_xor(a, 2, 64));
-        a = fmaxf(a, __shfl_xor(a, 4, 64));
+        // block max over the 8 lanes of this 32-element block (DPP)
+        const float a = row8_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         float inv, sc;
         xq_scales(a, inv, sc);
         int X[4] = {xq_quant(v.x, inv), xq_quant(v.y, inv), xq_quant(v.z, inv), xq_quant(v.w, inv)};
@@ -572,8 +568,8 @@ ZH_DEV void stage_x_finish(const XRegsF<XCH> &r, bool has_norm, float eps, uint3
         *(uint32_t *)(dst + 32) = pack4(l1[0], l1[1], l1[2], l1[3]);
         *(uint32_t *)(dst + 64) = pack4(l2[0], l2[1], l2[2], l2[3]);
         int sm = X[0] + X[1] + X[2] + X[3];
-        sm += __shfl_xor(sm, 1, 64);
-        sm += __shfl_xor(sm, 2, 64);
+        sm += __builtin_amdgcn_update_dpp(0, sm, 0xB1, 0xF, 0xF, false);  // 16 elements = 4 lanes
+        sm += __builtin_amdgcn_update_dpp(0, sm, 0x4E, 0xF, 0xF, false);
         const uint32_t sub = (tid & 7);
         if (sub == 0) lx.xs[b * 8 + j] = sc;
         if ((sub & 3) == 0) lx.xz16[b * 16 + j * 2 + (sub >> 2)] = (float)sm * sc;
@@ -751,8 +747,7 @@ __global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
         }
 #endif
         float res = active ? fmaf(h.d, accd, -h.dmin * accm) : 0.f;
-#pragma unroll
-        for (int o = TL / 2; o > 0; o >>= 1) res += __shfl_xor(res, o, 64);
+        res = team_sum_dpp<TL>(res);
         float *yb = p.segY[sg];
         if (MODE == LPB_GATE_UP) {
             if (mat == 0 && tlane == 0) gate_res[rt] = res;
@@ -856,8 +851,7 @@ __global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
         const uint32_t dw = __builtin_amdgcn_alignbyte(rs[5], rs[4], sh);  // bytes 208..211
         float res = active ? h2f(dw) * acc : 0.f;
         constexpr int TLW = TL > 64 ? 64 : TL;
-#pragma unroll
-        for (int o = TLW / 2; o > 0; o >>= 1) res += __shfl_xor(res, o, 64);
+        res = team_sum_dpp<TLW>(res);
         if (TL > 64) {  // team spans TL/64 waves
             __shared__ float xred[LPB_T / 64];
             if ((tid & 63) == 0) xred[tid >> 6] = res;
