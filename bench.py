@@ -9,6 +9,7 @@ Prints ONE JSON line on stdout.
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -26,50 +27,25 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_roofline(ctx, zinc_amd, iters=200):
-    """Time the dominant decode kernel -- the fused Q4_K gate/up/SwiGLU DMMV at
-    the 8B FFN shape (2 x 12288x4096, 56.6 MB of weights per launch) -- with
-    HIP events on the library's stream, rotating 10 distinct weight copies
-    (566 MB, more than the 256 MB MALL) so every launch streams from HBM."""
-    M, K = 12288, 4096
-    wb = zinc_amd.tensor_bytes(zinc_amd.Q4_K, M, K)
-    n_copies = 10
-    W = ctx.alloc(wb * 2 * n_copies)
-    for i in range(2 * n_copies):
-        ctx.synth_tensor(W, i * wb, zinc_amd.Q4_K, M, K, 4242, 100 + i)
-    x = ctx.alloc(K * 4)
-    ctx.synth_vector(x, 0, 0, K, 1.0, 4242, 99)
-    xq = ctx.alloc(ctx.xq_bytes(K))
-    ctx.quantize_activation(x, 0, K, xq)
-    y = ctx.alloc(M * 4)
-
-    def launch(i):
-        c = i % n_copies
-        ctx.dmmv_fused_gate_up_swiglu_xq(zinc_amd.Q4_K, W, 2 * c * wb, W, (2 * c + 1) * wb, xq, 0, y, 0, M, K)
-
-    for i in range(20):
-        launch(i)
-    ctx.sync()
-    ctx.record(0)
-    for i in range(iters):
-        launch(i)
-    ctx.record(1)
-    ms = ctx.elapsed_ms(0, 1)
-    for b in (W, x, xq, y):
-        ctx.free(b)
-    per_launch_us = ms * 1e3 / iters
-    # algorithmic bytes: both weight matrices + the XQ activation + y
-    alg_bytes = 2 * wb + ctx.xq_bytes(K) + M * 4
-    achieved = alg_bytes / (per_launch_us * 1e-6) / 1e9
-    return {
-        "kernel": "k_dmmv<FmtQ4K,64,1,4,MODE_GATE_UP,false> (fused gate/up/SwiGLU, Q4_K 2x12288x4096)",
-        "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-        "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-        "bytes_per_launch": alg_bytes, "us_per_launch": round(per_launch_us, 3),
-    }
+def kernel_roofline(ctx):
+    """Roofline of the step's dominant kernel (largest share of decode-step
+    time in profiles/decode_step_kernel_trace.md): the ffn_down Q6_K DMMV,
+    timed with HIP events on the library stream over 14 rotating weight
+    copies (578 MB > 256 MB MALL). `traffic` is the counter-measured HBM
+    bytes per launch from profiles/dmmv_q6k_down_4096x12288_pmc.md."""
+    from zinc_amd import roofline_probe
+    r = roofline_probe.time_dominant_kernel(ctx)
+    traffic = None
+    pm = os.path.join(ROOT, "profiles", "dmmv_q6k_down_4096x12288_pmc.md")
+    if os.path.exists(pm):
+        m = re.search(r"^traffic_bytes_per_launch: (\d+)", open(pm).read(), re.M)
+        traffic = int(m.group(1)) if m else None
+    return {"kernel": r["kernel"], "bound": "hbm", "achieved": r["achieved_GBs"], "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(r["achieved_GBs"] / PEAK_HBM_GBS, 4), "traffic": traffic,
+            "bytes_per_launch": r["bytes_per_launch"], "us_per_launch": r["us_per_launch"]}
 
 
-def cpu_baseline(cfg, n_tokens=2):
+def cpu_baseline(cfg, n_tokens=16):
     """The CPU oracle (C restatement of the reference's dequantRow + serial f32
     dot path, threaded over rows as forward_metal.zig:3932-3933) decoding
     `n_tokens` tokens of the same model at position PREFILL."""
@@ -97,7 +73,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=2)
+    ap.add_argument("--cpu-tokens", type=int, default=16)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -140,7 +116,7 @@ def main():
         f"({bytes_tok * tok_s / 1e9 / PEAK_HBM_GBS:.1%} of 8 TB/s); distinct tokens {len(set(toks))}")
     eng.deinit()
 
-    roof = kernel_roofline(ctx, zinc_amd)
+    roof = kernel_roofline(ctx)
     log(f"dominant kernel: {roof['achieved']} GB/s ({roof['frac']:.1%}), {roof['us_per_launch']} us/launch")
     ctx.close()
 
