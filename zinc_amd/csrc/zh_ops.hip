@@ -498,23 +498,33 @@ __global__ __launch_bounds__(256, 2) void k_attn_decode(AttnP p) {
     for (int g = 0; g < G; g++) *(float2 *)&wo[wave][g][2 * lane] = make_float2(acc[g][0], acc[g][1]);
     (void)mx;
     __syncthreads();
-    // ---- combine the 4 waves: thread -> (head, dim) outputs
-    for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += 256) {
-        const uint32_t g = o / FD_HD, d = o % FD_HD;
+    // ---- combine the 4 waves: per-head weights once, then thread -> (head, dim)
+    __shared__ float cf[AD_W][G], cM[G], cL[G];
+    if (tid < (uint32_t)G) {
+        const uint32_t g = tid;
         float M = wm[0][g];
 #pragma unroll
         for (int w = 1; w < AD_W; w++) M = fmaxf(M, wm[w][g]);
         const float Ms = M == -INFINITY ? 0.f : M;
-        float L = 0.f, O = 0.f;
+        float L = 0.f;
 #pragma unroll
         for (int w = 0; w < AD_W; w++) {
             const float f = wm[w][g] == -INFINITY ? 0.f : expf(wm[w][g] - Ms);
+            cf[w][g] = f;
             L = fmaf(wl[w][g], f, L);
-            O = fmaf(wo[w][g][d], f, O);
         }
+        cM[g] = M;
+        cL[g] = L;
+    }
+    __syncthreads();
+    for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += 256) {
+        const uint32_t g = o / FD_HD, d = o % FD_HD;
+        float O = 0.f;
+#pragma unroll
+        for (int w = 0; w < AD_W; w++) O = fmaf(wo[w][g][d], cf[w][g], O);
         float *pp = p.part + ((size_t)(kvh * G + g) * p.n_chunks + chunk) * (FD_HD + 2);
         st_dev(pp + d, O);
-        if (d == 0) { st_dev(pp + FD_HD, M); st_dev(pp + FD_HD + 1, L); }
+        if (d == 0) { st_dev(pp + FD_HD, cM[g]); st_dev(pp + FD_HD + 1, cL[g]); }
     }
     TRACE_OPS(3);
     // ---- last workgroup of this kv head merges the chunks
