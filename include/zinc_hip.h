@@ -169,6 +169,15 @@ int zh_moe_weighted_acc(zh_ctx *ctx, zh_buf *a, const zh_buf *b, const zh_buf *r
 int zh_argmax(zh_ctx *ctx, const zh_buf *logits, uint32_t n, zh_buf *result, uint64_t result_off);
 
 /* ---- engine: InferenceEngine surface (forward.zig:1226-10983) ---------- */
+/* Batched prefill projection (dispatchProjectionBatched, forward.zig:8147-8216;
+ * recordMulMmQ4K dmmv.zig:1045-1094 / mul_mm_q4k.comp): Y[n][m] (+= when
+ * acc_mode == 1) sum_k X[n][k] * W[m][k] for N tokens, on the MFMA units.
+ * X: fp16, token-major [N][K] (16-byte aligned offset); Y: f32 token-major
+ * [N][M]; W: Q4_K or Q6_K rows (K % 256 == 0), dequantised to fp16 tiles,
+ * f32 accumulation. */
+int zh_gemm_xw(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off, const zh_buf *X, uint64_t x_off,
+               zh_buf *Y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t N, uint32_t acc_mode);
+
 typedef struct zh_model_config {
     uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab;
     uint32_t n_experts, n_experts_used, expert_ffn; /* n_experts == 0 => dense */
@@ -187,6 +196,13 @@ int zh_engine_prefill_kv_random(zh_engine *eng, uint32_t n_tokens, uint64_t seed
 /* decodeStep(state, token, collect_output) (forward.zig:4299): runs one token
  * at `position`; with collect_output the greedy token is produced on device. */
 int zh_engine_decode_step(zh_engine *eng, uint32_t token, uint32_t position, int collect_output);
+/* prefillBatched(state, tokens) (forward.zig:9330-9735): tokens at positions
+ * start_pos .. start_pos+n-1 as MFMA dequant-GEMM batches of up to 512 tokens
+ * (fp16 operands, f32 accumulation); writes their K/V and leaves the last
+ * token's hidden state as the decode state. With collect, its logits and
+ * greedy token are produced (read them with zh_engine_sample_greedy /
+ * zh_engine_logits). MoE models run the decode step per token. */
+int zh_engine_prefill(zh_engine *eng, const uint32_t *tokens, uint32_t n, uint32_t start_pos, int collect);
 /* sampleGreedy (forward.zig:10338): waits and returns the last argmax token. */
 int zh_engine_sample_greedy(zh_engine *eng, uint32_t *token);
 /* generate (forward.zig:10983-11192): feed prompt tokens from `start_pos`,

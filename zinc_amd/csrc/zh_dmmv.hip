@@ -777,13 +777,15 @@ ZH_DEV uint32_t blk_bytes(uint32_t t) {
 }
 
 __global__ void k_dequant(uint32_t qtype, const uint8_t *__restrict__ W, uint32_t row0, uint32_t n_rows,
-                          uint32_t K, float *__restrict__ out, const uint32_t *row_from_dev, uint32_t clamp_rows) {
+                          uint32_t K, float *__restrict__ out, const uint32_t *row_from_dev, uint32_t clamp_rows,
+                          uint32_t gather) {
     uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
     uint32_t rr = blockIdx.y;
     if (e >= K || rr >= n_rows) return;
     uint32_t row = row0 + rr;
     if (row_from_dev) {
-        row = row_from_dev[0] + rr;
+        // one id and consecutive rows, or (gather) one id per output row
+        row = gather ? row_from_dev[rr] : row_from_dev[0] + rr;
         if (row >= clamp_rows) row = clamp_rows - 1;  // embedToken safe_id clamp (forward.zig:4271)
     }
     uint64_t rb = (uint64_t)(K / blk_elems(qtype)) * blk_bytes(qtype);
@@ -835,9 +837,9 @@ __global__ void k_dequant(uint32_t qtype, const uint8_t *__restrict__ W, uint32_
 }
 
 int zhk_dequant_rows(zh_ctx *c, uint32_t qtype, const uint8_t *W, uint32_t row0, uint32_t n_rows, uint32_t K,
-                     float *out, const uint32_t *row_from_dev, uint32_t clamp_rows) {
+                     float *out, const uint32_t *row_from_dev, uint32_t clamp_rows, uint32_t gather) {
     hipLaunchKernelGGL(k_dequant, dim3((K + 255) / 256, n_rows), dim3(256), 0, c->stream, qtype, W, row0, n_rows,
-                       K, out, row_from_dev, clamp_rows);
+                       K, out, row_from_dev, clamp_rows, gather);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
 }

@@ -62,7 +62,16 @@ struct zh_engine {
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
+    // batched prefill activations (allocated on first use, PF_CHUNK tokens)
+    struct {
+        float *hid = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *g = nullptr, *u = nullptr;
+        _Float16 *xh = nullptr, *att = nullptr, *s = nullptr;
+        float *s_unscale = nullptr;
+        uint32_t *ids = nullptr;
+        void *arena = nullptr;
+    } pf;
 };
+constexpr uint32_t PF_CHUNK = 512;  // tokens per prefill batch
 
 #define EHIP(e, call) ZH_HIP((e)->ctx, call)
 #define ERC(x)                 \
@@ -273,6 +282,7 @@ extern "C" void zh_engine_destroy(zh_engine *e) {
     if (e->arena) hipFree(e->arena);
     if (e->kv) hipFree(e->kv);
     if (e->act_arena) hipFree(e->act_arena);
+    if (e->pf.arena) hipFree(e->pf.arena);
     delete e;
 }
 
@@ -294,6 +304,26 @@ extern "C" int zh_engine_prefill_kv_random(zh_engine *e, uint32_t n, uint64_t se
 // ---------------------------------------------------------------------------
 // One token step (the body of decodeStep, forward.zig:4376-7754).
 // ---------------------------------------------------------------------------
+// output_norm -> LM head -> greedy argmax on e->hidden (forward.zig:7757-7772,
+// sampleGreedy :10338-10357); the token goes to ST_TOKEN_OUT and the ring.
+static int record_collect(zh_engine *e) {
+    zh_ctx *c = e->ctx;
+    const zh_model_config &m = e->c;
+    const uint32_t H = m.hidden;
+    const uint8_t *A = e->arena;
+    if (!getenv("ZH_NO_LPB") && zhk_lpb_supported(m.type_lm_head, H) && m.vocab % 2 == 0) {
+        const uint8_t *wl = A + e->lm.off;
+        float *yl = e->logits;
+        const uint32_t mv = m.vocab;
+        ERC(zhk_dmmv_lpb(c, m.type_lm_head, 0, 1, &wl, nullptr, &yl, &mv, e->hidden,
+                         (const float *)(A + e->out_norm.off), m.eps, nullptr, H, 0));
+    } else {
+        ERC(zhk_rms_norm(c, e->hidden, (const float *)(A + e->out_norm.off), H, e->norm, e->xq_h, H, 1, m.eps));
+        ERC(zhk_dmmv(c, m.type_lm_head, A + e->lm.off, e->xq_h, e->logits, m.vocab, H, 0));
+    }
+    return zhk_argmax(c, e->logits, m.vocab, e->st + ST_TOKEN_OUT, e->am_part, e->ring, e->st + ST_GEN);
+}
+
 static int record_step(zh_engine *e, bool collect) {
     zh_ctx *c = e->ctx;
     const zh_model_config &m = e->c;
@@ -370,19 +400,7 @@ static int record_step(zh_engine *e, bool collect) {
             ERC(zhk_moe_weighted_acc(c, e->hidden, e->edown_out, e->routing, H, k, H));
         }
     }
-    if (collect) {
-        if (lpb_head) {
-            const uint8_t *wl = W(e->lm);
-            float *yl = e->logits;
-            const uint32_t mv = m.vocab;
-            ERC(zhk_dmmv_lpb(c, m.type_lm_head, 0, 1, &wl, nullptr, &yl, &mv, e->hidden, Wf(e->out_norm), m.eps,
-                             nullptr, H, 0));
-        } else {
-            ERC(zhk_rms_norm(c, e->hidden, Wf(e->out_norm), H, e->norm, e->xq_h, H, 1, m.eps));
-            ERC(zhk_dmmv(c, m.type_lm_head, W(e->lm), e->xq_h, e->logits, m.vocab, H, 0));
-        }
-        ERC(zhk_argmax(c, e->logits, m.vocab, e->st + ST_TOKEN_OUT, e->am_part, e->ring, e->st + ST_GEN));
-    }
+    if (collect) ERC(record_collect(e));
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, c->stream, e->st, (const uint32_t *)e->prompt);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
@@ -463,6 +481,100 @@ extern "C" int zh_engine_generate(zh_engine *e, const uint32_t *prompt, uint32_t
         for (uint32_t i = 0; i < max_tokens; i++)
             if (out_tokens[i] == eos) { n = i + 1; break; }
     *n_out = n;
+    return ZH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Batched prefill (prefillBatched, forward.zig:9330-9735): tokens at
+// positions start_pos .. start_pos+n-1 in chunks of PF_CHUNK, every
+// projection as an MFMA dequant-GEMM over the chunk, per layer:
+// RMSNorm -> Q/K/V -> q/k norm + RoPE + KV write -> causal attention ->
+// O (+residual) -> RMSNorm -> gate, up -> SwiGLU -> down (+residual).
+// The last token's hidden state becomes the decode state; with `collect`
+// its logits and greedy token are produced as decodeStep(collect) does.
+// MoE models (no batched expert GEMM here) run the decode step per token.
+// ---------------------------------------------------------------------------
+static bool prefill_batched_ok(const zh_model_config &m) {
+    auto gemm_t = [](uint32_t t) { return t == ZH_Q4_K || t == ZH_Q6_K; };
+    return m.n_experts == 0 && m.head_dim == 128 && gemm_t(m.type_attn) && gemm_t(m.type_ffn_gate_up) &&
+           gemm_t(m.type_ffn_down) && m.hidden % 256 == 0 && m.ffn % 256 == 0 &&
+           (m.n_heads * m.head_dim) % 256 == 0;
+}
+
+static int ensure_prefill(zh_engine *e) {
+    if (e->pf.arena) return ZH_OK;
+    const zh_model_config &m = e->c;
+    const uint64_t C = PF_CHUNK, H = m.hidden, qd = (uint64_t)m.n_heads * m.head_dim,
+                   kvd = (uint64_t)m.n_kv_heads * m.head_dim, F = m.ffn, XK = H > qd ? H : qd;
+    struct { void **p; uint64_t bytes; } a[] = {
+        {(void **)&e->pf.hid, 4 * C * H}, {(void **)&e->pf.q, 4 * C * qd}, {(void **)&e->pf.k, 4 * C * kvd},
+        {(void **)&e->pf.v, 4 * C * kvd}, {(void **)&e->pf.g, 4 * C * F}, {(void **)&e->pf.u, 4 * C * F},
+        {(void **)&e->pf.xh, 2 * C * XK}, {(void **)&e->pf.att, 2 * C * qd}, {(void **)&e->pf.s, 2 * C * F},
+        {(void **)&e->pf.ids, 4ull * MAX_PROMPT}, {(void **)&e->pf.s_unscale, 4 * C},
+    };
+    uint64_t off = 0;
+    for (auto &x : a) off = align256(off + x.bytes);
+    EHIP(e, hipMalloc(&e->pf.arena, off + 256));
+    off = 0;
+    for (auto &x : a) {
+        *x.p = (char *)e->pf.arena + off;
+        off = align256(off + x.bytes);
+    }
+    return ZH_OK;
+}
+
+extern "C" int zh_engine_prefill(zh_engine *e, const uint32_t *tokens, uint32_t n, uint32_t start_pos, int collect) {
+    if (!e || !tokens || n == 0) return ZH_ERR_INVALID_ARGUMENT;
+    if (n > MAX_PROMPT) return zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "prefill of %u tokens > %u", n, MAX_PROMPT);
+    if ((uint64_t)start_pos + n > e->c.max_ctx)
+        return zh_set_err(e->ctx, ZH_ERR_CONTEXT_LENGTH_EXCEEDED, "context %u + %u > %u", start_pos, n, e->c.max_ctx);
+    zh_ctx *c = e->ctx;
+    const zh_model_config &m = e->c;
+    if (!prefill_batched_ok(m)) {
+        EHIP(e, hipMemcpyAsync(e->prompt, tokens, 4ull * n, hipMemcpyHostToDevice, c->stream));
+        ERC(set_state(e, n, start_pos, tokens[0]));
+        for (uint32_t i = 0; i < n; i++) ERC(run_step(e, collect && i + 1 == n));
+        if (collect) e->have_logits = true;
+        return ZH_OK;
+    }
+    ERC(ensure_prefill(e));
+    const uint32_t H = m.hidden, hd = m.head_dim, qd = m.n_heads * hd, kvd = m.n_kv_heads * hd, F = m.ffn;
+    const uint8_t *A = e->arena;
+    auto W = [&](const Tensor &t) { return A + t.off; };
+    auto Wf = [&](const Tensor &t) { return (const float *)(A + t.off); };
+    const float scale = 1.0f / sqrtf((float)hd);
+    EHIP(e, hipMemcpyAsync(e->pf.ids, tokens, 4ull * n, hipMemcpyHostToDevice, c->stream));
+    uint32_t last = 0;
+    for (uint32_t off = 0; off < n; off += PF_CHUNK) {
+        const uint32_t nt = n - off < PF_CHUNK ? n - off : PF_CHUNK, pos0 = start_pos + off;
+        last = nt;
+        ERC(zhk_dequant_rows(c, m.type_embd, W(e->embd), 0, nt, H, e->pf.hid, e->pf.ids + off, m.vocab, 1));
+        for (uint32_t l = 0; l < m.n_layers; l++) {
+            const Layer &y = e->L[l];
+            ERC(zhk_rms_norm_rows_f16(c, e->pf.hid, Wf(y.attn_norm), e->pf.xh, H, nt, m.eps));
+            ERC(zhk_gemm(c, m.type_attn, W(y.wq), e->pf.xh, H, e->pf.q, qd, qd, H, nt, 0));
+            ERC(zhk_gemm(c, m.type_attn, W(y.wk), e->pf.xh, H, e->pf.k, kvd, kvd, H, nt, 0));
+            ERC(zhk_gemm(c, m.type_attn, W(y.wv), e->pf.xh, H, e->pf.v, kvd, kvd, H, nt, 0));
+            ERC(zhk_qk_norm_rope_kv(c, e->pf.q, Wf(y.q_norm), e->pf.k, Wf(y.k_norm), e->pf.v, e->inv_freq, y.kc, y.vc,
+                                    e->pages, e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd,
+                                    zh_pos_src{pos0, nullptr}, m.eps, nt));
+            ERC(zhk_attn_prefill(c, e->pf.q, y.kc, y.vc, e->pages, e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd,
+                                 pos0, nt, scale, e->pf.att));
+            ERC(zhk_gemm(c, m.type_attn, W(y.wo), e->pf.att, qd, e->pf.hid, H, H, qd, nt, 1));
+            ERC(zhk_rms_norm_rows_f16(c, e->pf.hid, Wf(y.ffn_norm), e->pf.xh, H, nt, m.eps));
+            ERC(zhk_gemm(c, m.type_ffn_gate_up, W(y.gate), e->pf.xh, H, e->pf.g, F, F, H, nt, 0));
+            ERC(zhk_gemm(c, m.type_ffn_gate_up, W(y.up), e->pf.xh, H, e->pf.u, F, F, H, nt, 0));
+            ERC(zhk_swiglu_rows_f16(c, e->pf.g, e->pf.u, e->pf.s, e->pf.s_unscale, F, nt));
+            ERC(zhk_gemm(c, m.type_ffn_down, W(y.down), e->pf.s, F, e->pf.hid, H, H, F, nt, 1, e->pf.s_unscale));
+        }
+    }
+    EHIP(e, hipMemcpyAsync(e->hidden, e->pf.hid + (size_t)(last - 1) * H, 4ull * H, hipMemcpyDeviceToDevice,
+                           c->stream));
+    if (collect) {
+        ERC(set_state(e, 1, start_pos + n - 1, tokens[n - 1]));
+        ERC(record_collect(e));
+        e->have_logits = true;
+    }
     return ZH_OK;
 }
 

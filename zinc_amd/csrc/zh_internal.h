@@ -71,7 +71,7 @@ int zhk_dmmv_moe(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint64_t expert_
                  const uint32_t *routing, const void *xq, uint64_t xq_slot_stride, float *y,
                  uint32_t M, uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2);
 int zhk_dequant_rows(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint32_t row0, uint32_t n_rows,
-                     uint32_t K, float *out, const uint32_t *row_from_dev, uint32_t clamp_rows);
+                     uint32_t K, float *out, const uint32_t *row_from_dev, uint32_t clamp_rows, uint32_t gather = 0);
 int zhk_synth_tensor(zh_ctx *ctx, uint8_t *dst, uint32_t qtype, uint64_t rows, uint64_t cols,
                      uint64_t seed, uint64_t stream);
 int zhk_synth_vector(zh_ctx *ctx, void *dst, uint32_t kind, uint64_t n, float scale, uint64_t seed,
@@ -86,7 +86,8 @@ struct zh_pos_src {  // where a kernel reads the position: host scalar or device
 int zhk_qk_norm_rope_kv(zh_ctx *ctx, float *q, const float *qw, const float *k, const float *kw,
                         const float *v, const float *inv_freq, uint16_t *kc, uint16_t *vc,
                         const uint32_t *pages, uint32_t n_pages, uint32_t cache_tokens,
-                        uint32_t nq, uint32_t nkv, uint32_t hd, zh_pos_src pos, float eps);
+                        uint32_t nq, uint32_t nkv, uint32_t hd, zh_pos_src pos, float eps,
+                        uint32_t n_tok = 1);  // n_tok rows of q / k / v at positions pos .. pos + n_tok - 1
 int zhk_flash_decode(zh_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc,
                      const uint32_t *pages, uint32_t n_pages, uint32_t cache_tokens, float *out,
                      void *xq_out, uint32_t nh, uint32_t nkv, uint32_t hd, zh_pos_src seq_len,
@@ -102,6 +103,16 @@ int zhk_attn_decode_fused(zh_ctx *ctx, const float *q, const float *k, const flo
                           const uint32_t *pages, uint32_t n_pages, uint32_t cache_tokens, float *out,
                           void *xq_out, uint32_t nh, uint32_t nkv, zh_pos_src pos, uint32_t max_seq,
                           float scale, float eps, float *partials);
+// Prefill (zh_prefill.hip)
+int zhk_gemm(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, const _Float16 *X, uint32_t ldx, float *Y, uint32_t ldy,
+             uint32_t M, uint32_t K, uint32_t N, uint32_t acc, const float *x_unscale = nullptr);
+int zhk_rms_norm_rows_f16(zh_ctx *ctx, const float *x, const float *w, _Float16 *out, uint32_t n, uint32_t rows,
+                          float eps);
+int zhk_swiglu_rows_f16(zh_ctx *ctx, const float *g, const float *u, _Float16 *out, float *unscale, uint32_t n,
+                        uint32_t rows);
+int zhk_attn_prefill(zh_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, const uint32_t *pages,
+                     uint32_t n_pages, uint32_t cache_tokens, uint32_t nq, uint32_t nkv, uint32_t hd, uint32_t pos0,
+                     uint32_t N, float scale, _Float16 *out);
 int zhk_softmax_topk(zh_ctx *ctx, const float *logits, uint32_t n, uint32_t k, uint32_t *routing);
 int zhk_moe_weighted_acc(zh_ctx *ctx, float *a, const float *b, const uint32_t *routing, uint32_t n,
                          uint32_t n_used, uint32_t src_stride);

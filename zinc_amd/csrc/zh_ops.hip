@@ -128,13 +128,18 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_kv(float *q, const float *q
                                                         const float *v, const float *inv_freq, uint16_t *kc,
                                                         uint16_t *vc, const uint32_t *pages, uint32_t n_pages,
                                                         uint32_t cache_tokens, uint32_t nq, uint32_t hd,
-                                                        zh_pos_src pos_src, float eps) {
-    const uint32_t wg = blockIdx.x, lane = threadIdx.x;
+                                                        zh_pos_src pos_src, float eps, uint32_t q_stride,
+                                                        uint32_t kv_stride) {
+    // blockIdx.y = token of a batch (prefill): rows q_stride / kv_stride apart, position + token
+    const uint32_t wg = blockIdx.x, lane = threadIdx.x, tok = blockIdx.y;
+    q += (size_t)tok * q_stride;
+    k += (size_t)tok * kv_stride;
+    v += (size_t)tok * kv_stride;
     const bool is_q = wg < nq;
     const uint32_t head = is_q ? wg : wg - nq;
     const float *src = is_q ? q + (size_t)head * hd : k + (size_t)head * hd;
     const float *wt = is_q ? qw : kw;
-    const uint32_t pos = read_pos(pos_src);
+    const uint32_t pos = read_pos(pos_src) + tok;
     float sq = 0.f;
     for (uint32_t i = lane; i < hd; i += 64) sq = fmaf(src[i], src[i], sq);
     sq = wave_sum(sq);
@@ -168,9 +173,10 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_kv(float *q, const float *q
 
 int zhk_qk_norm_rope_kv(zh_ctx *c, float *q, const float *qw, const float *k, const float *kw, const float *v,
                         const float *inv_freq, uint16_t *kc, uint16_t *vc, const uint32_t *pages, uint32_t n_pages,
-                        uint32_t cache_tokens, uint32_t nq, uint32_t nkv, uint32_t hd, zh_pos_src pos, float eps) {
-    hipLaunchKernelGGL(k_qk_norm_rope_kv, dim3(nq + nkv), dim3(64), 0, c->stream, q, qw, k, kw, v, inv_freq, kc, vc,
-                       pages, n_pages, cache_tokens, nq, hd, pos, eps);
+                        uint32_t cache_tokens, uint32_t nq, uint32_t nkv, uint32_t hd, zh_pos_src pos, float eps,
+                        uint32_t n_tok) {
+    hipLaunchKernelGGL(k_qk_norm_rope_kv, dim3(nq + nkv, n_tok), dim3(64), 0, c->stream, q, qw, k, kw, v, inv_freq,
+                       kc, vc, pages, n_pages, cache_tokens, nq, hd, pos, eps, nq * hd, nkv * hd);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
 }

@@ -56,6 +56,15 @@ class InferenceEngine:
         self.ctx.check(lib().zh_engine_decode_step(self.h, token_id, state.position, int(collect_output)))
         state.position += 1
 
+    def prefill(self, tokens, start_pos=0, collect_output=True, state: DecodeState = None):
+        """prefillBatched (forward.zig:9330): all tokens at once (MFMA GEMMs);
+        state.position (if given) advances past them."""
+        p = np.ascontiguousarray(tokens, dtype=np.uint32)
+        self.ctx.check(lib().zh_engine_prefill(self.h, C.c_void_p(p.ctypes.data), len(p), start_pos,
+                                               int(collect_output)))
+        if state is not None:
+            state.position = start_pos + len(p)
+
     def sample_greedy(self) -> int:
         t = C.c_uint32()
         self.ctx.check(lib().zh_engine_sample_greedy(self.h, C.byref(t)))

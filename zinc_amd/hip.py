@@ -81,6 +81,8 @@ SIGNATURES = {
     "zh_softmax_topk": (_i32, [_P, _P, _u32, _u32, _P]),
     "zh_moe_weighted_acc": (_i32, [_P, _P, _P, _P, _u32, _u32, _u32]),
     "zh_argmax": (_i32, [_P, _P, _u32, _P, _u64]),
+    "zh_engine_prefill": (_i32, [_P, _P, _u32, _u32, _i32]),
+    "zh_gemm_xw": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _u32, _u32, _u32, _u32]),
     "zh_engine_create": (_i32, [_P, C.POINTER(ModelConfig), C.POINTER(_P)]),
     "zh_engine_destroy": (None, [_P]),
     "zh_engine_prefill_kv_random": (_i32, [_P, _u32, _u64]),
@@ -279,3 +281,7 @@ class Context:
 
     def argmax(self, logits, n, result, result_off=0):
         self.check(lib().zh_argmax(self.h, logits.h, n, result.h, result_off))
+
+    def gemm_xw(self, qtype, W, a_off, X, x_off, Y, y_off, M, K, N, acc_mode=0):
+        """Y[n][m] (+)= X[n] . W[m] for N tokens (X fp16 [N][K], Y f32 [N][M])."""
+        self.check(lib().zh_gemm_xw(self.h, qtype, W.h, a_off, X.h, x_off, Y.h, y_off, M, K, N, acc_mode))
