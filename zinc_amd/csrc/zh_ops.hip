@@ -217,7 +217,7 @@ extern "C" int zh_qk_norm_rope_kv_write(zh_ctx *c, zh_buf *q, const zh_buf *qw, 
 //     in registers, and the wave that owns the new position also normalises
 //     and ropes k, writes k/v to the fp16 cache and substitutes them for the
 //     cache rows it loaded before the write.
-//   - scores / chunk softmax / P*V per wave, the 4 waves combined in LDS
+//   - scores / chunk softmax / P*V per wave, the waves combined in LDS
 //     with log-sum-exp weights, one partial (O, m, l) per q head and chunk.
 //   - the last workgroup to finish for a kv head (agent-scope counter) merges
 //     the chunks and writes the attention output (f32, optional XQ) and
@@ -240,8 +240,9 @@ extern "C" int zh_exp_trace_ops_dump(uint64_t *host, uint32_t n) {
 #endif
 constexpr int FD_MAXG = 8;   // q heads per kv head
 constexpr int FD_HD = 128;   // head_dim supported
-constexpr int AD_W = 4;      // waves per workgroup
-constexpr int AD_TW = 32;    // tokens per wave
+constexpr int AD_W = 4;      // waves per workgroup (two workgroups fit a CU: all chunks resident at once)
+constexpr int AD_TW = 32;    // tokens per wave (two 16-token pages)
+constexpr int AD_T = AD_W * 64;
 constexpr int AD_TC = AD_W * AD_TW;  // tokens per chunk
 
 uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t hd, uint32_t max_seq) {
@@ -309,7 +310,7 @@ ZH_DEV uint32_t pack_h2(float a, float b) {
 }
 
 template <int G, bool FUSED>
-__global__ __launch_bounds__(256, 2) void k_attn_decode(AttnP p) {
+__global__ __launch_bounds__(AD_T, 2) void k_attn_decode(AttnP p) {
     const uint32_t kvh = blockIdx.x, tid = threadIdx.x;
     // chunks are dispatched last-first: the chunk holding the newest tokens
     // (and, FUSED, the KV write) must never wait in the dispatch tail
@@ -523,7 +524,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_decode(AttnP p) {
         cL[g] = L;
     }
     __syncthreads();
-    for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += 256) {
+    for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += AD_T) {
         const uint32_t g = o / FD_HD, d = o % FD_HD;
         float O = 0.f;
 #pragma unroll
@@ -554,7 +555,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_decode(AttnP p) {
     // Chunk merge. The first batch of each thread's O dims (NBAT chunks) is
     // requested before the chunk statistics, so both arrive in about one
     // round trip; the statistics pass leaves m_c in LDS for the weights.
-    constexpr int OPT = G * FD_HD >= 256 ? G * FD_HD / 256 : 1;  // dims per thread
+    constexpr int OPT = G * FD_HD >= AD_T ? G * FD_HD / AD_T : 1;  // dims per thread
     constexpr int NTH = G * FD_HD / OPT;
     constexpr int NBAT = G <= 4 ? 40 : 12;  // chunks per round of O loads
     constexpr int MB = 256;                 // chunk statistics kept in LDS
@@ -611,7 +612,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_decode(AttnP p) {
     const float Mt = hM[g_t];
     if (one_batch) {
         // weights exp(m_c - M) once per (head, chunk), in place in LDS
-        for (uint32_t i = tid; i < (uint32_t)G * NBAT; i += 256) {
+        for (uint32_t i = tid; i < (uint32_t)G * NBAT; i += AD_T) {
             const uint32_t g = i / NBAT, c = i % NBAT;
             sm[g][c] = c < nv ? expf(sm[g][c] - hM[g]) : 0.f;
         }
@@ -654,7 +655,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_decode(AttnP p) {
     if (p.xq) {
         __syncthreads();
         XQView v = xq_view(p.xq, p.nq * FD_HD / 32);
-        for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += 256)  // whole 32-lane groups (G*128 % 32 == 0)
+        for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += AD_T)  // whole 32-lane groups (G*128 % 32 == 0)
             xq_store_block32(ob[o], o & 31, v, (kvh * G * FD_HD + o) / 32);
     }
     if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -669,8 +670,8 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
     p.n_chunks = (max_seq + AD_TC - 1) / AD_TC;
     dim3 grid(nkv, p.n_chunks);
 #define AD_LAUNCH(GG)                                                                                  \
-    if (fused) hipLaunchKernelGGL((k_attn_decode<GG, true>), grid, dim3(256), 0, c->stream, p);       \
-    else hipLaunchKernelGGL((k_attn_decode<GG, false>), grid, dim3(256), 0, c->stream, p)
+    if (fused) hipLaunchKernelGGL((k_attn_decode<GG, true>), grid, dim3(AD_T), 0, c->stream, p);      \
+    else hipLaunchKernelGGL((k_attn_decode<GG, false>), grid, dim3(AD_T), 0, c->stream, p)
     switch (G) {
     case 1: AD_LAUNCH(1); break;
     case 2: AD_LAUNCH(2); break;
