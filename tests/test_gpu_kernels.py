@@ -127,6 +127,29 @@ def test_dmmv_matches_oracle(ctx, orc, qtype, M, K):
     assert_dot_close(got, ref, ref64, mag, f"dmmv q{qtype} {M}x{K}")
 
 
+@pytest.mark.parametrize("qtype,M,K", [
+    (12, 4096, 4096), (12, 12288, 4096), (12, 257, 512), (12, 64, 12288),
+    (14, 4096, 12288), (14, 64, 12288), (14, 2000, 4096), (14, 4096, 6144), (14, 40, 768),
+    (8, 257, 4096),
+])
+def test_dmmv_xq_matches_oracle(ctx, orc, qtype, M, K):
+    """The activation pre-quantised once (zh_quantize_activation: three int8
+    limbs under a power-of-two block scale, 24 significant bits) and read by
+    zh_dmmv_xq meets the same bar as the f32 entry point. K = 12288 stages
+    384 block scales and 768 block sums, more than one per lane of a workgroup."""
+    W = orc.synth_tensor(qtype, M, K, 77 + M, 1)
+    x = orc.synth_normal_f32(K, 77 + K, 2)
+    Wb, xb, yb = ctx.upload(W), ctx.upload(x), ctx.alloc(4 * M)
+    xq = ctx.alloc(ctx.xq_bytes(K))
+    ctx.quantize_activation(xb, 0, K, xq, 0)
+    ctx.dmmv_xq(qtype, Wb, 0, xq, 0, yb, 0, M, K)
+    got = yb.download(np.float32, M)
+    assert_dot_close(got, orc.dmmv(W, qtype, x, M, K), orc.dmmv_f64(W, qtype, x, M, K),
+                     orc.dmmv_absdot(W, qtype, x, M, K), f"dmmv_xq q{qtype} {M}x{K}")
+    for b in (Wb, xb, yb, xq):
+        ctx.free(b)
+
+
 @pytest.mark.parametrize("qtype", [12, 14, 8])
 def test_dmmv_acc_mode_and_offset(ctx, orc, qtype):
     got, ref, ref64, mag = run_dmmv(ctx, orc, qtype, 300, 1024, 5, acc=True, a_off=4096)

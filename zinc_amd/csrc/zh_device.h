@@ -162,3 +162,41 @@ ZH_DEV void load_unaligned(const uint8_t *p, uint32_t *out) {
 #pragma unroll
     for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
 }
+
+// Device-scope (all XCDs) store / load: coherent across the XCDs' L2s
+// without writing back or invalidating other data (an agent-scope fence
+// writes back / invalidates a whole XCD L2).
+ZH_DEV void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+ZH_DEV float ld_dev(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+ZH_DEV uint64_t ld_dev64(const float *p) {  // two floats, 8-byte aligned
+    return __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Quantises one 32-element block held one value per lane by 32 consecutive
+// lanes (l = lane & 31). Each 32-lane half of the wave is either fully
+// active or fully inactive.
+ZH_DEV float half_max(float v) {  // max over each 32-lane half, in every lane of it
+    v = row16_max(v);
+    const float lo = fmaxf(lane_f(v, 0), lane_f(v, 16)), hi = fmaxf(lane_f(v, 32), lane_f(v, 48));
+    return (threadIdx.x & 32) ? hi : lo;
+}
+ZH_DEV void xq_store_block32(float xi, int l, XQView v, uint32_t blk) {
+    float a = half_max(fabsf(xi));
+    float inv, sc;
+    xq_scales(a, inv, sc);
+    int X = xq_quant(xi, inv);
+    int l0, l1, l2;
+    xq_limbs(X, l0, l1, l2);
+    v.limb[blk * 96 + l] = (int8_t)l0;
+    v.limb[blk * 96 + 32 + l] = (int8_t)l1;
+    v.limb[blk * 96 + 64 + l] = (int8_t)l2;
+    // integer sum over each 16-lane row: the block's two 16-element sums
+    int s = X;
+    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x141, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x140, 0xF, 0xF, false);
+    if (l == 0) v.xs[blk] = sc;
+    if ((l & 15) == 0) v.xsum[blk * 2 + (l >> 4)] = (float)s * sc;
+}
+

@@ -196,6 +196,8 @@ struct LpbP {
     const uint8_t *segW2;  // up matrix (gate/up mode)
     float *segY[3];
     uint32_t seg_end[3];
+    uint8_t *xq_out;       // gate/up mode, optional: the SwiGLU output also as XQ (M % 32 == 0)
+    uint32_t *grp_cnt;     // with xq_out: one zeroed counter per 32-row group
 };
 
 enum { LPB_PLAIN = 0, LPB_GATE_UP = 1 };
@@ -578,12 +580,15 @@ ZH_DEV void stage_x_finish(const XRegsF<XCH> &r, bool has_norm, float eps, uint3
 }
 
 // Pre-quantised XQ: limbs (96 B per 32 elements), xs, xsum16 held in registers.
-// XQCH = 16-byte limb chunks per lane = ceil(6 * K/32 / 256) <= ceil(3 TL / 16).
+// XQCH = 16-byte limb chunks per lane = ceil(6 * K/32 / 256) <= ceil(3 TL / 16);
+// the K/32 block scales and 2 K/32 sums take ceil(XQCH / 6) and ceil(XQCH / 3)
+// values per lane.
 template <int XQCH>
 struct XRegsQ {
+    static constexpr int NXS = (XQCH + 5) / 6, NXZ = (XQCH + 2) / 3;
     u32x4 limb[XQCH];
-    float xs;
-    float xz[2];
+    float xs[NXS];
+    float xz[NXZ];
 };
 template <int XQCH>
 ZH_DEV void stage_xq_issue(const uint8_t *__restrict__ xq, uint32_t K, XRegsQ<XQCH> &r) {
@@ -594,9 +599,10 @@ ZH_DEV void stage_xq_issue(const uint8_t *__restrict__ xq, uint32_t K, XRegsQ<XQ
         const uint32_t c = min(i * LPB_T + tid, nblk * 6 - 1);  // clamped: static load count
         r.limb[i] = *(const u32x4 *)(v.limb + (size_t)c * 16);
     }
-    r.xs = v.xs[min(tid, nblk - 1)];
-    r.xz[0] = v.xsum[min(tid, nblk * 2 - 1)];
-    if (XQCH > 3) r.xz[1] = v.xsum[min(LPB_T + tid, nblk * 2 - 1)];  // nblk > 128 only when TL = 32
+#pragma unroll
+    for (int i = 0; i < XRegsQ<XQCH>::NXS; i++) r.xs[i] = v.xs[min(i * LPB_T + tid, nblk - 1)];
+#pragma unroll
+    for (int i = 0; i < XRegsQ<XQCH>::NXZ; i++) r.xz[i] = v.xsum[min(i * LPB_T + tid, nblk * 2 - 1)];
 }
 template <int XQCH>
 ZH_DEV void stage_xq_finish(const XRegsQ<XQCH> &r, uint32_t K, XLds lx) {
@@ -609,9 +615,12 @@ ZH_DEV void stage_xq_finish(const XRegsQ<XQCH> &r, uint32_t K, XLds lx) {
             *(u32x4 *)(lx.limb + (size_t)(blk32 / 8) * XB_STRIDE + (blk32 % 8) * 96 + part * 16) = r.limb[i];
         }
     }
-    if (tid < nblk) lx.xs[tid] = r.xs;
-    if (tid < nblk * 2) lx.xz16[tid] = r.xz[0];
-    if (XQCH > 3 && LPB_T + tid < nblk * 2) lx.xz16[LPB_T + tid] = r.xz[1];
+#pragma unroll
+    for (int i = 0; i < XRegsQ<XQCH>::NXS; i++)
+        if (i * LPB_T + tid < nblk) lx.xs[i * LPB_T + tid] = r.xs[i];
+#pragma unroll
+    for (int i = 0; i < XRegsQ<XQCH>::NXZ; i++)
+        if (i * LPB_T + tid < nblk * 2) lx.xz16[i * LPB_T + tid] = r.xz[i];
     __syncthreads();
 }
 
@@ -752,7 +761,32 @@ __global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
         if (MODE == LPB_GATE_UP) {
             if (mat == 0 && tlane == 0) gate_res[rt] = res;
             __syncthreads();
-            if (mat == 1 && tlane == 0 && (uint32_t)rt < nrows) yb[rr0 + rt] = silu_mul(gate_res[rt], res);
+            if (mat == 1 && tlane == 0 && (uint32_t)rt < nrows) {
+                const float v = silu_mul(gate_res[rt], res);
+                if (p.xq_out) st_dev(yb + rr0 + rt, v);  // device scope: read by another workgroup below
+                else yb[rr0 + rt] = v;
+            }
+            if (p.xq_out) {
+                // The SwiGLU output as XQ (the down projection's input): the
+                // batches of a 32-row group publish their rows and count; the
+                // last of the 32 / RPB arrivals quantises the group's block.
+                __shared__ uint32_t s_q;
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
+                const uint32_t grp = rr0 / 32;
+                if (tid == 0) {
+                    const uint32_t prev =
+                        __hip_atomic_fetch_add(p.grp_cnt + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    s_q = prev == 32 / RPB - 1 ? 1u : 0u;
+                }
+                __syncthreads();
+                if (s_q && tid < 64) {
+                    // both 32-lane halves quantise the same block (identical writes)
+                    const float v = ld_dev(yb + grp * 32 + (tid & 31));
+                    xq_store_block32(v, tid & 31, xq_view(p.xq_out, p.M / 32), grp);
+                    if (tid == 0) __hip_atomic_store(p.grp_cnt + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
         } else if (tlane == 0 && (uint32_t)rt < nrows) {
             float out = res;
             if (p.acc) out += yb[rr0 + rt];
@@ -990,7 +1024,7 @@ bool zhk_lpb_supported(uint32_t qtype, uint32_t K) {
 
 int zhk_dmmv_lpb(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
                  float *const *y, const uint32_t *M, const float *x, const float *norm_w, float eps,
-                 float *normed_out, uint32_t K, uint32_t acc, const void *xq) {
+                 float *normed_out, uint32_t K, uint32_t acc, const void *xq, uint8_t *xq_out, uint32_t *grp_cnt) {
     if (!zhk_lpb_supported(qtype, K) || (mode == LPB_GATE_UP && qtype != ZH_Q4_K) || nseg < 1 || nseg > 3)
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "lpb: unsupported qtype/K/mode");
     LpbP p = {};
@@ -1008,10 +1042,15 @@ int zhk_dmmv_lpb(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const uint8
     }
     p.segW2 = W2;
     p.M = end;
+    p.xq_out = xq_out;
+    p.grp_cnt = grp_cnt;
+    if (xq_out && (mode != LPB_GATE_UP || nseg != 1 || p.M % 32 || !grp_cnt))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "lpb: XQ output needs gate/up mode, one segment, M %% 32 == 0");
     {
         const int rc = qtype == ZH_Q4_K ? try_q4k_tile(c, p, nseg, M) : try_q6k_tile(c, p, nseg, M);
         if (rc >= 0) return rc;
     }
+    if (xq_out) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "lpb: XQ output needs the tile kernel (K <= 8192)");
     const uint32_t lanes = qtype == ZH_Q4_K ? K / 256 : K / 128;
     const uint32_t TL = pow2ceil(lanes < 4 ? 4 : lanes);
     const uint32_t teams = (p.M + R - 1) / R;

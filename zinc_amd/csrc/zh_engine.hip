@@ -59,6 +59,7 @@ struct zh_engine {
     float *s = nullptr, *logits = nullptr, *rl = nullptr, *edown_out = nullptr, *fd_part = nullptr;
     uint8_t *xq_h = nullptr, *xq_q = nullptr, *xq_f = nullptr;
     uint32_t *routing = nullptr, *am_part = nullptr, *st = nullptr, *prompt = nullptr, *ring = nullptr;
+    uint32_t *grp_cnt = nullptr;  // SwiGLU-output XQ: one counter per 32-row group (kept zero between launches)
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
@@ -245,6 +246,7 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
         {(void **)&e->routing, 8ull * 16}, {(void **)&e->am_part, 8ull * 256}, {(void **)&e->st, 4ull * ST_WORDS},
         {(void **)&e->prompt, 4ull * MAX_PROMPT}, {(void **)&e->ring, 4ull * MAX_GEN}, {(void **)&e->pages, 4ull * e->n_pages},
         {(void **)&e->inv_freq, 4ull * hd / 2}, {(void **)&e->rope_cs, 8ull * c.max_ctx * (hd / 2)},
+        {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)},
     };
     uint64_t aoff = 0;
     for (auto &a : acts) aoff = align256(aoff + a.bytes);
@@ -375,12 +377,17 @@ static int record_step(zh_engine *e, bool collect) {
             const uint8_t *wg = W(y.gate);
             float *ys = e->s;
             const uint32_t mf = m.ffn;
+            // gate/up also emits its output as XQ (quantised per 32-row group by
+            // the group's last batch), so the down projection copies XQ instead of
+            // every workgroup re-quantising the f32 vector
+            const bool swiglu_xq = m.ffn % 32 == 0 && H / 256 <= 32 && !getenv("ZH_NO_TILE");
             ERC(zhk_dmmv_lpb(c, ZH_Q4_K, 1, 1, &wg, W(y.up), &ys, &mf, e->hidden, Wf(y.ffn_norm), m.eps, nullptr, H,
-                             0));
+                             0, nullptr, swiglu_xq ? e->xq_f : nullptr, swiglu_xq ? e->grp_cnt : nullptr));
             const uint8_t *wd = W(y.down);
             float *yd = e->hidden;
             const uint32_t mh = H;
-            ERC(zhk_dmmv_lpb(c, m.type_ffn_down, 0, 1, &wd, nullptr, &yd, &mh, e->s, nullptr, 0.f, nullptr, m.ffn, 1));
+            ERC(zhk_dmmv_lpb(c, m.type_ffn_down, 0, 1, &wd, nullptr, &yd, &mh, swiglu_xq ? nullptr : e->s, nullptr,
+                             0.f, nullptr, m.ffn, 1, swiglu_xq ? e->xq_f : nullptr));
             continue;
         }
         ERC(zhk_rms_norm(c, e->hidden, Wf(y.ffn_norm), H, e->norm, e->xq_h, H, 1, m.eps));

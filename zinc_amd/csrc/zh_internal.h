@@ -125,4 +125,5 @@ int zhk_argmax(zh_ctx *ctx, const float *logits, uint32_t n, uint32_t *result, u
 bool zhk_lpb_supported(uint32_t qtype, uint32_t K);
 int zhk_dmmv_lpb(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
                  float *const *y, const uint32_t *M, const float *x, const float *norm_w, float eps,
-                 float *normed_out, uint32_t K, uint32_t acc, const void *xq = nullptr);
+                 float *normed_out, uint32_t K, uint32_t acc, const void *xq = nullptr,
+                 uint8_t *xq_out = nullptr, uint32_t *grp_cnt = nullptr);

@@ -8,34 +8,6 @@ static bool in_range(const zh_buf *b, uint64_t off, uint64_t n) { return b && of
 
 // Quantise one 32-element block held one value per lane across a 32-lane
 // group (l = lane index within the group) into XQ block `blk`.
-// Quantises one 32-element block held one value per lane by 32 consecutive
-// lanes (l = lane & 31). Each 32-lane half of the wave is either fully
-// active or fully inactive.
-ZH_DEV float half_max(float v) {  // max over each 32-lane half, in every lane of it
-    v = row16_max(v);
-    const float lo = fmaxf(lane_f(v, 0), lane_f(v, 16)), hi = fmaxf(lane_f(v, 32), lane_f(v, 48));
-    return (threadIdx.x & 32) ? hi : lo;
-}
-ZH_DEV void xq_store_block32(float xi, int l, XQView v, uint32_t blk) {
-    float a = half_max(fabsf(xi));
-    float inv, sc;
-    xq_scales(a, inv, sc);
-    int X = xq_quant(xi, inv);
-    int l0, l1, l2;
-    xq_limbs(X, l0, l1, l2);
-    v.limb[blk * 96 + l] = (int8_t)l0;
-    v.limb[blk * 96 + 32 + l] = (int8_t)l1;
-    v.limb[blk * 96 + 64 + l] = (int8_t)l2;
-    // integer sum over each 16-lane row: the block's two 16-element sums
-    int s = X;
-    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
-    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
-    s += __builtin_amdgcn_update_dpp(0, s, 0x141, 0xF, 0xF, false);
-    s += __builtin_amdgcn_update_dpp(0, s, 0x140, 0xF, 0xF, false);
-    if (l == 0) v.xs[blk] = sc;
-    if ((l & 15) == 0) v.xsum[blk * 2 + (l >> 4)] = (float)s * sc;
-}
-
 ZH_DEV uint32_t read_pos(zh_pos_src p) { return p.dev ? (*p.dev + p.value) : p.value; }
 
 // ---------------------------------------------------------------------------
@@ -210,8 +182,8 @@ extern "C" int zh_qk_norm_rope_kv_write(zh_ctx *c, zh_buf *q, const zh_buf *qw, 
 // Decode attention (flash_decode.comp + the qk_norm_rope_kv_write.comp work
 // of the new token, forward.zig decodeStep attention block), one kernel:
 //
-//   grid (n_kv_heads, n_chunks), 256 threads = 4 waves x 32 tokens, so a
-//   workgroup covers a 128-token chunk of one kv head's GQA group.
+//   grid (n_kv_heads, n_chunks), 256 threads = 4 waves x 40 tokens, so a
+//   workgroup covers a 160-token chunk of one kv head's GQA group.
 //   - FUSED: q (raw Q projection), the new token's raw k/v, per-head RMSNorm
 //     weights and RoPE frequencies come in; every wave normalises and ropes q
 //     in registers, and the wave that owns the new position also normalises
@@ -240,8 +212,12 @@ extern "C" int zh_exp_trace_ops_dump(uint64_t *host, uint32_t n) {
 #endif
 constexpr int FD_MAXG = 8;   // q heads per kv head
 constexpr int FD_HD = 128;   // head_dim supported
-constexpr int AD_W = 4;      // waves per workgroup (two workgroups fit a CU: all chunks resident at once)
-constexpr int AD_TW = 32;    // tokens per wave (two 16-token pages)
+// 4 waves x 40 tokens: one wave per SIMD, and the 8 kv heads map one per XCD
+// (workgroups go round robin over the 8 XCDs), so a context of up to
+// 32 x 160 = 5120 tokens puts at most one chunk workgroup on each of an
+// XCD's 32 CUs.
+constexpr int AD_W = 4;      // waves per workgroup
+constexpr int AD_TW = 40;    // tokens per wave: starts 8-aligned, spans at most 3 pages
 constexpr int AD_T = AD_W * 64;
 constexpr int AD_TC = AD_W * AD_TW;  // tokens per chunk
 
@@ -288,18 +264,6 @@ ZH_DEV void norm_rope16(float (&lo)[8], float (&hi)[8], const float (&wlo)[8], c
     }
 }
 
-// Device-scope (all XCDs) store / load of one float: coherent without L2
-// write-back or invalidation of other data.
-ZH_DEV void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-#ifdef ZH_EXP_PLAIN
-ZH_DEV float ld_dev(const float *p) { return *p; }
-ZH_DEV uint64_t ld_dev64(const float *p) { return *(const uint64_t *)p; }
-#else
-ZH_DEV float ld_dev(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-ZH_DEV uint64_t ld_dev64(const float *p) {  // two floats, 8-byte aligned
-    return __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-#endif
 
 // Two f32 -> packed f16 with the hardware conversion (round to nearest
 // even; fp16 denormals are kept in this build's default FP mode), as the
@@ -309,8 +273,15 @@ ZH_DEV uint32_t pack_h2(float a, float b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
 }
 
+// Row o (0..47) of the three pages a wave reads, page bases pa, pb, pc.
+ZH_DEV const uint16_t *kv_row(const uint16_t *h, size_t pa, size_t pb, size_t pc, uint32_t o) {
+    const uint32_t pi = o >> 4;
+    const size_t pg = pi == 0 ? pa : pi == 1 ? pb : pc;
+    return h + (pg * 16 + (o & 15)) * FD_HD;
+}
+
 template <int G, bool FUSED>
-__global__ __launch_bounds__(AD_T, 2) void k_attn_decode(AttnP p) {
+__global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     const uint32_t kvh = blockIdx.x, tid = threadIdx.x;
     // chunks are dispatched last-first: the chunk holding the newest tokens
     // (and, FUSED, the KV write) must never wait in the dispatch tail
@@ -320,22 +291,24 @@ __global__ __launch_bounds__(AD_T, 2) void k_attn_decode(AttnP p) {
     const uint32_t wave = tid >> 6, lane = tid & 63, sub = lane & 7, grp = lane >> 3;
     TRACE_OPS(0);
     const uint32_t t0 = chunk * AD_TC, tw0 = t0 + wave * AD_TW;
-    // position and this wave's two page entries are independent loads
-    const uint32_t pg0 = min(tw0 / 16, p.n_pages - 1), pg1 = min(tw0 / 16 + 1, p.n_pages - 1);
-    const uint32_t page0 = p.pages[pg0], page1 = p.pages[pg1];
+    static_assert(AD_TW % 8 == 0 && AD_TW + 8 <= 48, "a wave's tokens must fit 3 pages from an 8-aligned start");
+    // position and this wave's three page entries are independent loads
+    const uint32_t pgb = tw0 / 16, o16 = tw0 & 15;
+    const uint32_t page0 = p.pages[min(pgb, p.n_pages - 1)], page1 = p.pages[min(pgb + 1, p.n_pages - 1)];
+    const uint32_t page2 = p.pages[min(pgb + 2, p.n_pages - 1)];
     const uint32_t posv = read_pos(p.pos);
     const uint32_t seq = FUSED ? posv + 1 : posv;
     if (t0 >= seq) return;  // uniform over the workgroup
     const uint32_t nt = seq > tw0 ? min(seq - tw0, (uint32_t)AD_TW) : 0u;
-    // K/V rows of this wave's 32 tokens: two 16-token pages, each a
-    // contiguous 4 KB run, so every row is a constant offset from a page
-    // base. Rows past the end of the sequence are read (in-bounds) and masked.
+    // K/V rows of this wave's tokens: up to three 16-token pages, each a
+    // contiguous 4 KB run, so every row is an offset from a page base that
+    // is uniform per 8-token pass. Rows past the end of the sequence are read
+    // (in-bounds) and masked.
     const uint32_t ptok = p.cache_tokens / 16;
-    const size_t pa = page0 < ptok ? page0 : 0u, pb = page1 < ptok ? page1 : 0u;
+    const size_t pa = page0 < ptok ? page0 : 0u, pb = page1 < ptok ? page1 : 0u, pc = page2 < ptok ? page2 : 0u;
     const uint16_t *kh = p.kc + (size_t)kvh * p.cache_tokens * FD_HD;
     const uint16_t *vh = p.vc + (size_t)kvh * p.cache_tokens * FD_HD;
-    const uint16_t *kb[2] = {kh + pa * 16 * FD_HD, kh + pb * 16 * FD_HD};
-    const uint16_t *vb[2] = {vh + pa * 16 * FD_HD, vh + pb * 16 * FD_HD};
+
     // ---- loads: q (and the new token's raw k/v) first, then K, then V
     float qlo[G][8], qhi[G][8];
 #pragma unroll
@@ -385,14 +358,15 @@ __global__ __launch_bounds__(AD_T, 2) void k_attn_decode(AttnP p) {
     u32x4 kr[AD_TW / 8][2];
 #pragma unroll
     for (int j = 0; j < AD_TW / 8; j++) {
-        const uint16_t *kp = kb[j >> 1] + (8 * (j & 1) + grp) * FD_HD;
+        // o16 + 8j is 8-aligned: the pass stays in one page
+        const uint16_t *kp = kv_row(kh, pa, pb, pc, o16 + 8 * j) + grp * FD_HD;
         kr[j][0] = *(const u32x4 *)(kp + sub * 8);
         kr[j][1] = *(const u32x4 *)(kp + 64 + sub * 8);
     }
     asm volatile("" ::: "memory");
     uint32_t vr[AD_TW];
 #pragma unroll
-    for (int i = 0; i < AD_TW; i++) vr[i] = *(const uint32_t *)(vb[i >> 4] + (i & 15) * FD_HD + 2 * lane);
+    for (int i = 0; i < AD_TW; i++) vr[i] = *(const uint32_t *)(kv_row(vh, pa, pb, pc, o16 + i) + 2 * lane);
     asm volatile("" ::: "memory");
 
     // ---- q (and new k) preparation
@@ -555,7 +529,8 @@ __global__ __launch_bounds__(AD_T, 2) void k_attn_decode(AttnP p) {
     // Chunk merge. The first batch of each thread's O dims (NBAT chunks) is
     // requested before the chunk statistics, so both arrive in about one
     // round trip; the statistics pass leaves m_c in LDS for the weights.
-    constexpr int OPT = G * FD_HD >= AD_T ? G * FD_HD / AD_T : 1;  // dims per thread
+    // dims per thread: power of two with G*128/OPT <= AD_T
+    constexpr int OPT = G * FD_HD <= AD_T ? 1 : G * FD_HD <= 2 * AD_T ? 2 : G * FD_HD <= 4 * AD_T ? 4 : 8;
     constexpr int NTH = G * FD_HD / OPT;
     constexpr int NBAT = G <= 4 ? 40 : 12;  // chunks per round of O loads
     constexpr int MB = 256;                 // chunk statistics kept in LDS
