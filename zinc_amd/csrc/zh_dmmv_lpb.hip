@@ -201,6 +201,7 @@ struct LpbP {
 };
 
 enum { LPB_PLAIN = 0, LPB_GATE_UP = 1 };
+constexpr uint32_t LPB_XQ_MAX_GROUPS = 16;  // 32-row groups one gate/up workgroup may publish
 
 // Segment lookup for the batch starting at stacked row r0 (batches never
 // straddle segments).
@@ -684,15 +685,24 @@ __global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
     const uint32_t b = active ? tlane : 0;
     const uint8_t *xl = lx.limb + (size_t)b * XB_STRIDE;
     const uint32_t nbatch = (p.M + RPB - 1) / RPB;
+    // Batches are dealt round-robin, except when the SwiGLU output is emitted
+    // as XQ: then each workgroup takes a contiguous run of `per` batches so it
+    // completes whole 32-row groups where it can and publishes once, after its
+    // loop (the host sizes the grid so every run is non-empty).
+    const bool contig = MODE == LPB_GATE_UP && p.xq_out;
+    const uint32_t per = (nbatch + gridDim.x - 1) / gridDim.x;
+    const uint32_t b0 = contig ? blockIdx.x * per : blockIdx.x;
+    const uint32_t b1 = contig ? min(nbatch, b0 + per) : nbatch;
+    const uint32_t bstep = contig ? 1u : gridDim.x;
     u32x4 st[NM][NCH];
-    uint32_t bi = blockIdx.x;
+    uint32_t bi = b0;
     TRACE(0);
     // grid <= nbatch (host), so the first batch always exists
     stage_and_fetch<(3 * TL + 15) / 16, (TL / 4 > 1 ? TL / 4 : 1)>(
         p, lx, red, [&] { tile_fetch<NM, NCH, RPB>(p, bi, row_bytes, st); });
     TRACE(1);
     int it = 0;
-    for (; bi < nbatch; bi += gridDim.x, it++) {
+    for (; bi < b1; bi += bstep, it++) {
         uint32_t seg_rows, rr0, sg;
         lpb_geom(p, bi * RPB, seg_rows, rr0, sg);
         const uint32_t nrows = min((uint32_t)RPB, seg_rows - rr0);
@@ -706,7 +716,7 @@ __global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
             }
         __syncthreads();
         TRACE(2 + min(it, 4));
-        if (bi + gridDim.x < nbatch) tile_fetch<NM, NCH, RPB>(p, bi + gridDim.x, row_bytes, st);
+        if (bi + bstep < b1) tile_fetch<NM, NCH, RPB>(p, bi + bstep, row_bytes, st);
         uint32_t raw[LpbQ4K::RAW];
         {
             const uint8_t *blk = tile + mat * sub_bytes + rt * row_bytes + b * 144;
@@ -766,33 +776,40 @@ __global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
                 if (p.xq_out) st_dev(yb + rr0 + rt, v);  // device scope: read by another workgroup below
                 else yb[rr0 + rt] = v;
             }
-            if (p.xq_out) {
-                // The SwiGLU output as XQ (the down projection's input): the
-                // batches of a 32-row group publish their rows and count; the
-                // last of the 32 / RPB arrivals quantises the group's block.
-                __shared__ uint32_t s_q;
-                __builtin_amdgcn_s_waitcnt(0);
-                __syncthreads();
-                const uint32_t grp = rr0 / 32;
-                if (tid == 0) {
-                    const uint32_t prev =
-                        __hip_atomic_fetch_add(p.grp_cnt + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    s_q = prev == 32 / RPB - 1 ? 1u : 0u;
-                }
-                __syncthreads();
-                if (s_q && tid < 64) {
-                    // both 32-lane halves quantise the same block (identical writes)
-                    const float v = ld_dev(yb + grp * 32 + (tid & 31));
-                    xq_store_block32(v, tid & 31, xq_view(p.xq_out, p.M / 32), grp);
-                    if (tid == 0) __hip_atomic_store(p.grp_cnt + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
         } else if (tlane == 0 && (uint32_t)rt < nrows) {
             float out = res;
             if (p.acc) out += yb[rr0 + rt];
             yb[rr0 + rt] = out;
         }
         __syncthreads();  // the tile is rewritten by the next batch
+    }
+    if (contig) {
+        // The SwiGLU output as XQ, the down projection's input: each 32-row
+        // group is counted up to 32 published rows; the workgroup whose rows
+        // complete it quantises the group's block. Rows were stored at device
+        // scope, so after this workgroup's stores drain they are visible to
+        // whichever workgroup's counter increment comes last.
+        __shared__ uint32_t s_last[LPB_XQ_MAX_GROUPS];
+        const uint32_t r0 = b0 * RPB, r1 = min(p.M, b1 * RPB);
+        const uint32_t g0 = r0 / 32, ng = (r1 - 1) / 32 - g0 + 1;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if ((uint32_t)tid < ng) {
+            const uint32_t g = g0 + tid;
+            const uint32_t n = min(r1, g * 32 + 32) - max(r0, g * 32);
+            const uint32_t prev = __hip_atomic_fetch_add(p.grp_cnt + g, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last[tid] = prev + n == 32 ? 1u : 0u;
+        }
+        __syncthreads();
+        const float *yb = p.segY[0];
+        for (uint32_t i = tid / 64; i < ng; i += LPB_T / 64) {
+            if (!s_last[i]) continue;
+            const uint32_t g = g0 + i;
+            // both 32-lane halves quantise the same block (identical writes)
+            const float v = ld_dev(yb + g * 32 + (tid & 31));
+            xq_store_block32(v, tid & 31, xq_view(p.xq_out, p.M / 32), g);
+            if ((tid & 63) == 0) __hip_atomic_store(p.grp_cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     TRACE(7);
 }
@@ -963,6 +980,12 @@ static int try_q4k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t 
     const uint32_t nbatch = (p.M + rpb - 1) / rpb;
     uint32_t wgs = nbatch, cap = (uint32_t)c->cu_count * (uint32_t)(capm > 0 ? capm : 3);
     if (wgs > cap) wgs = cap;
+    if (p.xq_out) {
+        // contiguous batch runs: every workgroup gets a non-empty run
+        const uint32_t per = (nbatch + wgs - 1) / wgs;
+        wgs = (nbatch + per - 1) / per;
+        if (nseg != 1 || nm != 2 || p.M % 32 || per * rpb / 32 + 2 > LPB_XQ_MAX_GROUPS) return -1;
+    }
     const uint32_t lds = nb * (XB_STRIDE + 96) + TILE_BYTES;
     switch (TL) {
     case 4: return launch_q4k_tile<4>(c, p, wgs, lds);
