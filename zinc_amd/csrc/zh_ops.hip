@@ -199,12 +199,12 @@ extern "C" int zh_qk_norm_rope_kv_write(zh_ctx *c, zh_buf *q, const zh_buf *qw, 
 // addressed through 16-token pages.
 // ---------------------------------------------------------------------------
 #ifdef ZH_EXP_TRACE
-__device__ uint64_t g_exp_trace_ops[16384 * 8];
+__device__ uint64_t g_exp_trace_ops[16384 * 16];
 #define TRACE_OPS(slot) do { const uint32_t bl_ = blockIdx.x + blockIdx.y * gridDim.x; \
-    if (threadIdx.x == 0 && bl_ < 16384) g_exp_trace_ops[bl_ * 8 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+    if (threadIdx.x == 0 && bl_ < 8192) g_exp_trace_ops[bl_ * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
 extern "C" int zh_exp_trace_ops_dump(uint64_t *host, uint32_t n) {
     int rc = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_trace_ops), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
-    static uint64_t zeros[16384 * 8];
+    static uint64_t zeros[16384 * 16];
     return rc | (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_trace_ops), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
 }
 #else
@@ -280,32 +280,32 @@ ZH_DEV const uint16_t *kv_row(const uint16_t *h, size_t pa, size_t pb, size_t pc
     return h + (pg * 16 + (o & 15)) * FD_HD;
 }
 
-template <int G, bool FUSED>
+template <int G, bool FUSED, bool REV>
 __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     const uint32_t kvh = blockIdx.x, tid = threadIdx.x;
-    // chunks are dispatched last-first: the chunk holding the newest tokens
-    // (and, FUSED, the KV write) must never wait in the dispatch tail
-    const uint32_t seq_hint = FUSED ? read_pos(p.pos) + 1 : read_pos(p.pos);
-    const uint32_t nv_hint = (seq_hint + AD_TC - 1) / AD_TC;
-    const uint32_t chunk = blockIdx.y < nv_hint ? nv_hint - 1 - blockIdx.y : blockIdx.y;
-    const uint32_t wave = tid >> 6, lane = tid & 63, sub = lane & 7, grp = lane >> 3;
+    // REV (grids larger than the device holds at once): chunks are dispatched
+    // last-first, so the chunk holding the newest tokens (and, FUSED, the KV
+    // write) never waits in the dispatch tail; that order needs the position
+    // before the page entries. Otherwise the chunk is blockIdx.y and the
+    // page entries, the position and the q loads all go out at once.
+    uint32_t chunk = blockIdx.y;
+    if (REV) {
+        const uint32_t seq_hint = FUSED ? read_pos(p.pos) + 1 : read_pos(p.pos);
+        const uint32_t nv_hint = (seq_hint + AD_TC - 1) / AD_TC;
+        chunk = blockIdx.y < nv_hint ? nv_hint - 1 - blockIdx.y : blockIdx.y;
+    }
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, sub = lane & 7, grp = lane >> 3;
     TRACE_OPS(0);
     const uint32_t t0 = chunk * AD_TC, tw0 = t0 + wave * AD_TW;
     static_assert(AD_TW % 8 == 0 && AD_TW + 8 <= 48, "a wave's tokens must fit 3 pages from an 8-aligned start");
-    // position and this wave's three page entries are independent loads
+    // position and this wave's three page entries: wave-uniform (scalar) loads
     const uint32_t pgb = tw0 / 16, o16 = tw0 & 15;
     const uint32_t page0 = p.pages[min(pgb, p.n_pages - 1)], page1 = p.pages[min(pgb + 1, p.n_pages - 1)];
     const uint32_t page2 = p.pages[min(pgb + 2, p.n_pages - 1)];
-    const uint32_t posv = read_pos(p.pos);
+    // branch-free position read (a branch would wait for the load at its join)
+    const uint32_t pos_raw = *(p.pos.dev ? p.pos.dev : p.pages);
+    const uint32_t posv = p.pos.dev ? pos_raw + p.pos.value : p.pos.value;
     const uint32_t seq = FUSED ? posv + 1 : posv;
-    if (t0 >= seq) return;  // uniform over the workgroup
-    const uint32_t nt = seq > tw0 ? min(seq - tw0, (uint32_t)AD_TW) : 0u;
-    // K/V rows of this wave's tokens: up to three 16-token pages, each a
-    // contiguous 4 KB run, so every row is an offset from a page base that
-    // is uniform per 8-token pass. Rows past the end of the sequence are read
-    // (in-bounds) and masked.
-    const uint32_t ptok = p.cache_tokens / 16;
-    const size_t pa = page0 < ptok ? page0 : 0u, pb = page1 < ptok ? page1 : 0u, pc = page2 < ptok ? page2 : 0u;
     const uint16_t *kh = p.kc + (size_t)kvh * p.cache_tokens * FD_HD;
     const uint16_t *vh = p.vc + (size_t)kvh * p.cache_tokens * FD_HD;
 
@@ -344,6 +344,13 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
             kwl[4 * h2] = c.x; kwl[4 * h2 + 1] = c.y; kwl[4 * h2 + 2] = c.z; kwl[4 * h2 + 3] = c.w;
             kwh[4 * h2] = d.x; kwh[4 * h2 + 1] = d.y; kwh[4 * h2 + 2] = d.z; kwh[4 * h2 + 3] = d.w;
         }
+    }
+    // The loads above need neither the position nor the page entries (both
+    // scalar loads in flight meanwhile); a chunk past the sequence ends here.
+    asm volatile("" ::: "memory");
+    if (t0 >= seq) return;  // uniform over the workgroup
+    const uint32_t nt = seq > tw0 ? min(seq - tw0, (uint32_t)AD_TW) : 0u;
+    if (FUSED) {
         const f32x4 *cs = (const f32x4 *)(p.rope_cs + ((size_t)posv * 64 + sub * 8) * 2);
 #pragma unroll
         for (int e2 = 0; e2 < 4; e2++) {
@@ -355,6 +362,12 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     // sinking the groups (q / new token / RoPE first, then K, then V), so the
     // q preparation waits only for its own loads.
     asm volatile("" ::: "memory");
+    // K/V rows of this wave's tokens: up to three 16-token pages, each a
+    // contiguous 4 KB run, so every row is an offset from a page base that
+    // is uniform per 8-token pass. Rows past the end of the sequence are read
+    // (in-bounds) and masked.
+    const uint32_t ptok = p.cache_tokens / 16;
+    const size_t pa = page0 < ptok ? page0 : 0u, pb = page1 < ptok ? page1 : 0u, pc = page2 < ptok ? page2 : 0u;
     u32x4 kr[AD_TW / 8][2];
 #pragma unroll
     for (int j = 0; j < AD_TW / 8; j++) {
@@ -387,10 +400,12 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
                        pack_h2(khi[6], khi[7])};
             vnew = pack_h2(vn0, vn1);
             inew = posv - tw0;
-            // logicalTokenToPhysicalToken for the new position; the host has
-            // checked the context length, an unmapped slot is skipped
-            const uint32_t slot = posv / 16;
-            uint32_t ph = slot < p.n_pages ? p.pages[slot] * 16 + posv % 16 : p.cache_tokens;
+            // logicalTokenToPhysicalToken for the new position, from the page
+            // entries loaded above (the position lies in page pgb + 0..2); the
+            // host has checked the context length, an unmapped slot is skipped
+            const uint32_t slot = posv / 16, pi = slot - pgb;
+            const uint32_t pg = pi == 0 ? page0 : pi == 1 ? page1 : page2;
+            uint32_t ph = slot < p.n_pages ? pg * 16 + posv % 16 : p.cache_tokens;
             if (ph < p.cache_tokens) {
                 if (grp == (inew & 7)) {
                     *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + sub * 8) = n0;
@@ -453,6 +468,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         if (lane == 0) { wm[wave][g] = m; wl[wave][g] = l; }
     }
     __syncthreads();
+    TRACE_OPS(8);
     float acc[G][2];
 #pragma unroll
     for (int g = 0; g < G; g++) acc[g][0] = acc[g][1] = 0.f;
@@ -479,6 +495,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     for (int g = 0; g < G; g++) *(float2 *)&wo[wave][g][2 * lane] = make_float2(acc[g][0], acc[g][1]);
     (void)mx;
     __syncthreads();
+    TRACE_OPS(9);
     // ---- combine the 4 waves: per-head weights once, then thread -> (head, dim)
     __shared__ float cf[AD_W][G], cM[G], cL[G];
     if (tid < (uint32_t)G) {
@@ -498,6 +515,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         cL[g] = L;
     }
     __syncthreads();
+    TRACE_OPS(10);
     for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += AD_T) {
         const uint32_t g = o / FD_HD, d = o % FD_HD;
         float O = 0.f;
@@ -644,9 +662,17 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
     AttnP p = p0;
     p.n_chunks = (max_seq + AD_TC - 1) / AD_TC;
     dim3 grid(nkv, p.n_chunks);
-#define AD_LAUNCH(GG)                                                                                  \
-    if (fused) hipLaunchKernelGGL((k_attn_decode<GG, true>), grid, dim3(AD_T), 0, c->stream, p);      \
-    else hipLaunchKernelGGL((k_attn_decode<GG, false>), grid, dim3(AD_T), 0, c->stream, p)
+    // one workgroup per CU: a grid within the CU count is resident at once
+    const bool rev = (uint64_t)nkv * p.n_chunks > (uint64_t)c->cu_count;
+#define AD_LAUNCH1(GG, FF)                                                                             \
+    if (rev) hipLaunchKernelGGL((k_attn_decode<GG, FF, true>), grid, dim3(AD_T), 0, c->stream, p);     \
+    else hipLaunchKernelGGL((k_attn_decode<GG, FF, false>), grid, dim3(AD_T), 0, c->stream, p)
+#define AD_LAUNCH(GG)          \
+    if (fused) {               \
+        AD_LAUNCH1(GG, true);  \
+    } else {                   \
+        AD_LAUNCH1(GG, false); \
+    }
     switch (G) {
     case 1: AD_LAUNCH(1); break;
     case 2: AD_LAUNCH(2); break;
@@ -655,6 +681,7 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
     default: return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "GQA group %u unsupported (1, 2, 4, 8)", G);
     }
 #undef AD_LAUNCH
+#undef AD_LAUNCH1
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
 }
