@@ -835,9 +835,12 @@ __global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
     const uint32_t nbatch = (p.M + RPB - 1) / RPB;
     u32x4 st[1][NCH];
     uint32_t bi = blockIdx.x;
+    TRACE(0);
     stage_and_fetch<(3 * TL / 2 + 15) / 16, (TL / 8 > 1 ? TL / 8 : 1)>(
         p, lx, red, [&] { tile_fetch<1, NCH, RPB>(p, bi, row_bytes, st); });
-    for (; bi < nbatch; bi += gridDim.x) {
+    TRACE(1);
+    int it = 0;
+    for (; bi < nbatch; bi += gridDim.x, it++) {
         uint32_t seg_rows, rr0, sg;
         lpb_geom(p, bi * RPB, seg_rows, rr0, sg);
         const uint32_t nrows = min((uint32_t)RPB, seg_rows - rr0);
@@ -848,6 +851,7 @@ __global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
             if (c < n16) *(u32x4 *)(tile + c * 16) = st[0][j];
         }
         __syncthreads();
+        TRACE(2 + min(it, 4));
         if (bi + gridDim.x < nbatch) tile_fetch<1, NCH, RPB>(p, bi + gridDim.x, row_bytes, st);
         const uint32_t boff = rt * row_bytes + b * 210;
         const uint32_t sh = boff & 3;
@@ -920,6 +924,7 @@ __global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
         }
         __syncthreads();  // the tile (and xred) are rewritten by the next batch
     }
+    TRACE(7);
 }
 
 // ---------------------------------------------------------------------------

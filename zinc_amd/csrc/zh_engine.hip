@@ -361,7 +361,7 @@ static int record_step(zh_engine *e, bool collect) {
         }
         ERC(zhk_attn_decode_fused(c, e->q, e->k, e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc,
                                   e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads, m.n_kv_heads, pos,
-                                  m.max_ctx, scale, m.eps, e->fd_part));
+                                  m.max_ctx, scale, m.eps, e->fd_part, true));  // pages[i] = i (k_fill_pages)
         if (lpb_attn) {
             // the merge kernel already emitted the attention output as XQ
             const uint8_t *wo = W(y.wo);

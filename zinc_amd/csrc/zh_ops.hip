@@ -219,11 +219,27 @@ constexpr int FD_HD = 128;   // head_dim supported
 constexpr int AD_W = 4;      // waves per workgroup
 constexpr int AD_TW = 40;    // tokens per wave: starts 8-aligned, spans at most 3 pages
 constexpr int AD_T = AD_W * 64;
-constexpr int AD_TC = AD_W * AD_TW;  // tokens per chunk
+constexpr int AD_TC = AD_W * AD_TW;  // tokens per chunk (at most)
+constexpr int AD_ND = 32;            // chunks per kv head (CUs per XCD) in the identity-page mode
+// Chunk geometry modes: page-table lookups with chunk = blockIdx.y, the same
+// dispatched newest-first (grids larger than the device), or an identity page
+// table (physical token = logical token), where nothing waits on page entries
+// and the chunk length follows the context: ceil(seq / 32) rounded up to 8
+// tokens (at least 40) while that fits 160, so a context of up to 5120 tokens
+// spreads over all 32 CUs of each kv head's XCD.
+enum { AD_PAGED = 0, AD_PAGED_REV = 1, AD_IDENT = 2 };
+ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq) {
+    const uint32_t ct = ((seq + AD_ND - 1) / AD_ND + 7) / 8 * 8;
+    return seq > (uint32_t)(AD_ND * AD_TC) ? (uint32_t)AD_TC : max(ct, (uint32_t)AD_TW);
+}
+static uint32_t attn_n_chunks(uint32_t max_seq) {
+    const uint32_t n = (max_seq + AD_TC - 1) / AD_TC;
+    return n > (uint32_t)AD_ND ? n : (uint32_t)AD_ND;
+}
 
 uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t hd, uint32_t max_seq) {
-    // partials + one counter word per head (the counters never exceed nh)
-    return (uint64_t)nh * ((max_seq + AD_TC - 1) / AD_TC) * (hd + 2) * 4 + 4ull * nh + 256;
+    // partials + two counter words per kv head (at most nh words)
+    return (uint64_t)nh * attn_n_chunks(max_seq) * (hd + 2) * 4 + 4ull * nh + 256;
 }
 
 struct AttnP {
@@ -280,32 +296,155 @@ ZH_DEV const uint16_t *kv_row(const uint16_t *h, size_t pa, size_t pb, size_t pc
     return h + (pg * 16 + (o & 15)) * FD_HD;
 }
 
-template <int G, bool FUSED, bool REV>
+// Merges the chunk partials of q heads h0 .. h0+GM-1: O = sum_c exp(m_c - M) O_c
+// / sum_c exp(m_c - M) l_c (the split-K combine of flash_decode.comp's
+// reduction). Reads partials published at device scope; `poison` (a wait that
+// timed out) turns the outputs into NaN.
+template <int GM>
+ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    TRACE_OPS(11);
+    // Chunk merge. The first batch of each thread's O dims (NBAT chunks) is
+    // requested before the chunk statistics, so both arrive in about one
+    // round trip; the statistics pass leaves m_c in LDS for the weights.
+    // dims per thread: power of two with G*128/OPT <= AD_T
+    constexpr int OPT = GM * FD_HD <= AD_T ? 1 : GM * FD_HD <= 2 * AD_T ? 2 : GM * FD_HD <= 4 * AD_T ? 4 : 8;
+    constexpr int NTH = GM * FD_HD / OPT;
+    constexpr int NBAT = GM <= 4 ? 40 : 12;  // chunks per round of O loads
+    constexpr int MB = 256;                 // chunk statistics kept in LDS
+    __shared__ __align__(16) float sm[GM][MB];
+    __shared__ float hM[GM], hL[GM];
+    __shared__ float ob[GM * FD_HD];
+    float O[OPT];
+#pragma unroll
+    for (int k = 0; k < OPT; k++) O[k] = 0.f;
+    const uint32_t g_t = min(tid * OPT / FD_HD, (uint32_t)GM - 1), d0 = (tid * OPT) % FD_HD;
+    const float *pt = p.part + (size_t)(h0 + g_t) * p.n_chunks * (FD_HD + 2);
+    float v[NBAT][OPT];
+    auto load_o = [&](uint32_t cb) {
+#pragma unroll
+        for (int u = 0; u < NBAT; u++) {
+            const float *pc = pt + (size_t)min(cb + u, nv - 1) * (FD_HD + 2) + d0;
+            if (OPT == 1) {
+                v[u][0] = ld_dev(pc);
+            } else {
+#pragma unroll
+                for (int w = 0; w < OPT / 2; w++) {
+                    const uint64_t x = ld_dev64(pc + 2 * w);
+                    v[u][2 * w] = __uint_as_float((uint32_t)x);
+                    v[u][2 * w + 1] = __uint_as_float((uint32_t)(x >> 32));
+                }
+            }
+        }
+    };
+    const bool one_batch = nv <= (uint32_t)NBAT;  // uniform
+    if (one_batch) load_o(0);
+    asm volatile("" ::: "memory");  // the O loads go out before the statistics loads
+    for (uint32_t g = wave; g < (uint32_t)GM; g += AD_W) {
+        const float *pp = p.part + (size_t)(h0 + g) * p.n_chunks * (FD_HD + 2);
+        float m = -INFINITY, l = 0.f;
+        for (uint32_t c = lane; c < nv; c += 64) {
+            const uint64_t ml = ld_dev64(pp + (size_t)c * (FD_HD + 2) + FD_HD);
+            const float mc = __uint_as_float((uint32_t)ml), lc = __uint_as_float((uint32_t)(ml >> 32));
+            if (c < MB) sm[g][c] = mc;
+            const float mn = fmaxf(m, mc);
+            l = fmaf(l, m == -INFINITY ? 0.f : expf(m - mn), lc * expf(mc - mn));
+            m = mn;
+        }
+        const float M = wave_max(m);
+        l = wave_sum(m == -INFINITY ? 0.f : l * expf(m - M));
+        if (lane == 0) { hM[g] = M; hL[g] = l; }
+    }
+    TRACE_OPS(12);
+    __syncthreads();
+    TRACE_OPS(13);
+    const float Mt = hM[g_t];
+    if (one_batch) {
+        // weights exp(m_c - M) once per (head, chunk), in place in LDS
+        for (uint32_t i = tid; i < (uint32_t)GM * NBAT; i += AD_T) {
+            const uint32_t g = i / NBAT, c = i % NBAT;
+            sm[g][c] = c < nv ? expf(sm[g][c] - hM[g]) : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u4 = 0; u4 < NBAT; u4 += 4) {
+            const f32x4 w4 = *(const f32x4 *)&sm[g_t][u4];
+#pragma unroll
+            for (int k = 0; k < OPT; k++) {
+                O[k] = fmaf(v[u4][k], w4.x, O[k]);
+                O[k] = fmaf(v[u4 + 1][k], w4.y, O[k]);
+                O[k] = fmaf(v[u4 + 2][k], w4.z, O[k]);
+                O[k] = fmaf(v[u4 + 3][k], w4.w, O[k]);
+            }
+        }
+    } else {
+        // long contexts: one round of loads per NBAT chunks
+        for (uint32_t cb = 0; cb < nv; cb += NBAT) {
+            load_o(cb);
+#pragma unroll
+            for (int u = 0; u < NBAT; u++) {
+                const uint32_t c = cb + u;
+                const float mc = c < MB ? sm[g_t][c < MB ? c : 0] : ld_dev(pt + (size_t)min(c, nv - 1) * (FD_HD + 2) + FD_HD);
+                const float wgt = c < nv ? expf(mc - Mt) : 0.f;
+#pragma unroll
+                for (int k = 0; k < OPT; k++) O[k] = fmaf(v[u][k], wgt, O[k]);
+            }
+        }
+    }
+    TRACE_OPS(6);
+    if (tid < (uint32_t)NTH) {
+#pragma unroll
+        for (int k = 0; k < OPT; k++) {
+            const float r = poison ? __builtin_nanf("") : hL[g_t] > 0.f ? O[k] / hL[g_t] : 0.f;
+            ob[tid * OPT + k] = r;
+            if (p.out) p.out[(size_t)h0 * FD_HD + tid * OPT + k] = r;
+        }
+    }
+    TRACE_OPS(7);
+    if (p.xq) {
+        __syncthreads();
+        XQView v = xq_view(p.xq, p.nq * FD_HD / 32);
+        for (uint32_t o = tid; o < (uint32_t)GM * FD_HD; o += AD_T)  // whole 32-lane groups (GM*128 % 32 == 0)
+            xq_store_block32(ob[o], o & 31, v, (h0 * FD_HD + o) / 32);
+    }
+    TRACE_OPS(5);
+}
+
+template <int G, bool FUSED, int MODE>
 __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     const uint32_t kvh = blockIdx.x, tid = threadIdx.x;
-    // REV (grids larger than the device holds at once): chunks are dispatched
-    // last-first, so the chunk holding the newest tokens (and, FUSED, the KV
-    // write) never waits in the dispatch tail; that order needs the position
-    // before the page entries. Otherwise the chunk is blockIdx.y and the
-    // page entries, the position and the q loads all go out at once.
-    uint32_t chunk = blockIdx.y;
-    if (REV) {
-        const uint32_t seq_hint = FUSED ? read_pos(p.pos) + 1 : read_pos(p.pos);
-        const uint32_t nv_hint = (seq_hint + AD_TC - 1) / AD_TC;
-        chunk = blockIdx.y < nv_hint ? nv_hint - 1 - blockIdx.y : blockIdx.y;
-    }
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, sub = lane & 7, grp = lane >> 3;
     TRACE_OPS(0);
-    const uint32_t t0 = chunk * AD_TC, tw0 = t0 + wave * AD_TW;
     static_assert(AD_TW % 8 == 0 && AD_TW + 8 <= 48, "a wave's tokens must fit 3 pages from an 8-aligned start");
-    // position and this wave's three page entries: wave-uniform (scalar) loads
-    const uint32_t pgb = tw0 / 16, o16 = tw0 & 15;
-    const uint32_t page0 = p.pages[min(pgb, p.n_pages - 1)], page1 = p.pages[min(pgb + 1, p.n_pages - 1)];
-    const uint32_t page2 = p.pages[min(pgb + 2, p.n_pages - 1)];
-    // branch-free position read (a branch would wait for the load at its join)
+    // Position: a branch-free read (a branch would wait for the load at its
+    // join). AD_PAGED: the chunk is blockIdx.y, so the page entries (scalar
+    // loads), the position and the q loads all go out at once. AD_PAGED_REV:
+    // chunks are dispatched last-first so the chunk holding the newest tokens
+    // (and, FUSED, the KV write) never waits in the dispatch tail; that order
+    // needs the position first. AD_IDENT: no page entries; the geometry
+    // follows the position (and is reversed the same way).
     const uint32_t pos_raw = *(p.pos.dev ? p.pos.dev : p.pages);
     const uint32_t posv = p.pos.dev ? pos_raw + p.pos.value : p.pos.value;
     const uint32_t seq = FUSED ? posv + 1 : posv;
+    const uint32_t CT = MODE == AD_IDENT ? attn_chunk_tokens(seq) : (uint32_t)AD_TC;
+    uint32_t chunk = blockIdx.y;
+    if (MODE != AD_PAGED) {
+        const uint32_t nv_hint = (seq + CT - 1) / CT;
+        chunk = blockIdx.y < nv_hint ? nv_hint - 1 - blockIdx.y : blockIdx.y;
+    }
+    const uint32_t t0 = chunk * CT, tw0 = t0 + wave * AD_TW;
+    // this wave's tokens within the chunk (a chunk shorter than 160 leaves
+    // the last waves fewer, or none)
+    const uint32_t wtok = CT > wave * AD_TW ? min(CT - wave * AD_TW, (uint32_t)AD_TW) : 0u;
+    const uint32_t pgb = tw0 / 16, o16 = tw0 & 15;
+    uint32_t page0, page1, page2;
+    if (MODE == AD_IDENT) {
+        page0 = pgb; page1 = pgb + 1; page2 = pgb + 2;
+    } else {
+        page0 = p.pages[min(pgb, p.n_pages - 1)];
+        page1 = p.pages[min(pgb + 1, p.n_pages - 1)];
+        page2 = p.pages[min(pgb + 2, p.n_pages - 1)];
+    }
     const uint16_t *kh = p.kc + (size_t)kvh * p.cache_tokens * FD_HD;
     const uint16_t *vh = p.vc + (size_t)kvh * p.cache_tokens * FD_HD;
 
@@ -349,7 +488,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     // scalar loads in flight meanwhile); a chunk past the sequence ends here.
     asm volatile("" ::: "memory");
     if (t0 >= seq) return;  // uniform over the workgroup
-    const uint32_t nt = seq > tw0 ? min(seq - tw0, (uint32_t)AD_TW) : 0u;
+    const uint32_t nt = seq > tw0 ? min(seq - tw0, wtok) : 0u;
     if (FUSED) {
         const f32x4 *cs = (const f32x4 *)(p.rope_cs + ((size_t)posv * 64 + sub * 8) * 2);
 #pragma unroll
@@ -389,7 +528,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     if (FUSED) {
 #pragma unroll
         for (int g = 0; g < G; g++) norm_rope16(qlo[g], qhi[g], qwl, qwh, co, sn, p.eps);
-        owner = posv >= tw0 && posv < tw0 + AD_TW;
+        owner = posv >= tw0 && posv < tw0 + wtok;
         if (owner) {
             // the cache rows loaded above for this position predate the write
             // below; scores and P*V select these values for it instead
@@ -526,147 +665,71 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         if (d == 0) { st_dev(pp + FD_HD, cM[g]); st_dev(pp + FD_HD + 1, cL[g]); }
     }
     TRACE_OPS(3);
-    // ---- last workgroup of this kv head merges the chunks
-    const uint32_t nv = (seq + AD_TC - 1) / AD_TC;
-    __shared__ uint32_t s_last;
+    // ---- the last arrivals of this kv head merge the chunks
+    const uint32_t nv = (seq + CT - 1) / CT;
+    __shared__ uint32_t s_prev;
     // The partials went out as device-scope stores, coherent across the
     // XCDs' L2s. Waiting for them to complete (s_waitcnt 0 in every wave,
     // then the barrier) before a relaxed device-scope counter increment
     // publishes them without the full L2 write-back / invalidate that
-    // agent-scope release / acquire fences imply; the reader uses
+    // agent-scope release / acquire fences imply; the readers use
     // device-scope loads.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(p.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == nv - 1 ? 1u : 0u;
-    }
+    if (tid == 0) s_prev = __hip_atomic_fetch_add(p.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     TRACE_OPS(4);
-    if (!s_last) return;
-    // Chunk merge. The first batch of each thread's O dims (NBAT chunks) is
-    // requested before the chunk statistics, so both arrive in about one
-    // round trip; the statistics pass leaves m_c in LDS for the weights.
-    // dims per thread: power of two with G*128/OPT <= AD_T
-    constexpr int OPT = G * FD_HD <= AD_T ? 1 : G * FD_HD <= 2 * AD_T ? 2 : G * FD_HD <= 4 * AD_T ? 4 : 8;
-    constexpr int NTH = G * FD_HD / OPT;
-    constexpr int NBAT = G <= 4 ? 40 : 12;  // chunks per round of O loads
-    constexpr int MB = 256;                 // chunk statistics kept in LDS
-    __shared__ __align__(16) float sm[G][MB];
-    __shared__ float hM[G], hL[G];
-    __shared__ float ob[G * FD_HD];
-    float O[OPT];
-#pragma unroll
-    for (int k = 0; k < OPT; k++) O[k] = 0.f;
-    const uint32_t g_t = min(tid * OPT / FD_HD, (uint32_t)G - 1), d0 = (tid * OPT) % FD_HD;
-    const float *pt = p.part + (size_t)(kvh * G + g_t) * p.n_chunks * (FD_HD + 2);
-    float v[NBAT][OPT];
-    auto load_o = [&](uint32_t cb) {
-#pragma unroll
-        for (int u = 0; u < NBAT; u++) {
-            const float *pc = pt + (size_t)min(cb + u, nv - 1) * (FD_HD + 2) + d0;
-            if (OPT == 1) {
-                v[u][0] = ld_dev(pc);
-            } else {
-#pragma unroll
-                for (int w = 0; w < OPT / 2; w++) {
-                    const uint64_t x = ld_dev64(pc + 2 * w);
-                    v[u][2 * w] = __uint_as_float((uint32_t)x);
-                    v[u][2 * w + 1] = __uint_as_float((uint32_t)(x >> 32));
-                }
+    const uint32_t prev = s_prev;
+    // With at least G chunks the last G arrivals merge one q head each (a
+    // merger reads 1/G of the partials); otherwise the last arrival merges all.
+    const bool split = G > 1 && nv >= (uint32_t)G;
+    const uint32_t nm = split ? (uint32_t)G : 1u;
+    if (prev + nm < nv) return;
+    const uint32_t slot = prev + nm - nv;  // nm - 1: the last arrival
+    if (!split) {
+        attn_merge<G>(p, kvh * G, nv, false);
+        if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    // earlier mergers wait until every chunk has arrived; the wait is bounded
+    // (50 ms) and a timeout poisons this head's output instead of hanging
+    __shared__ uint32_t s_ok;
+    if (tid == 0) {
+        uint32_t ok = 1;
+        if (slot != nm - 1) {
+            const uint64_t t_0 = __builtin_amdgcn_s_memrealtime();
+            while (__hip_atomic_load(p.counters + kvh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nv) {
+                if (__builtin_amdgcn_s_memrealtime() - t_0 > 5000000ull) { ok = 0; break; }
+                __builtin_amdgcn_s_sleep(1);
             }
         }
-    };
-    const bool one_batch = nv <= (uint32_t)NBAT;  // uniform
-    if (one_batch) load_o(0);
-    asm volatile("" ::: "memory");  // the O loads go out before the statistics loads
-    for (uint32_t g = wave; g < (uint32_t)G; g += AD_W) {
-        const float *pp = p.part + (size_t)(kvh * G + g) * p.n_chunks * (FD_HD + 2);
-        float m = -INFINITY, l = 0.f;
-        for (uint32_t c = lane; c < nv; c += 64) {
-            const uint64_t ml = ld_dev64(pp + (size_t)c * (FD_HD + 2) + FD_HD);
-            const float mc = __uint_as_float((uint32_t)ml), lc = __uint_as_float((uint32_t)(ml >> 32));
-            if (c < MB) sm[g][c] = mc;
-            const float mn = fmaxf(m, mc);
-            l = fmaf(l, m == -INFINITY ? 0.f : expf(m - mn), lc * expf(mc - mn));
-            m = mn;
+        s_ok = ok;
+        // counters[nkv + kvh] counts mergers past the wait; the last one
+        // clears both words for the next launch (no one reads them after)
+        uint32_t *done = p.counters + gridDim.x + kvh;
+        if (__hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nm - 1) {
+            __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        const float M = wave_max(m);
-        l = wave_sum(m == -INFINITY ? 0.f : l * expf(m - M));
-        if (lane == 0) { hM[g] = M; hL[g] = l; }
     }
-#ifdef ZH_EXP_MERGE_TRACE
-    TRACE_OPS(1);
-#endif
     __syncthreads();
-#ifdef ZH_EXP_MERGE_TRACE
-    TRACE_OPS(2);
-#endif
-    const float Mt = hM[g_t];
-    if (one_batch) {
-        // weights exp(m_c - M) once per (head, chunk), in place in LDS
-        for (uint32_t i = tid; i < (uint32_t)G * NBAT; i += AD_T) {
-            const uint32_t g = i / NBAT, c = i % NBAT;
-            sm[g][c] = c < nv ? expf(sm[g][c] - hM[g]) : 0.f;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int u4 = 0; u4 < NBAT; u4 += 4) {
-            const f32x4 w4 = *(const f32x4 *)&sm[g_t][u4];
-#pragma unroll
-            for (int k = 0; k < OPT; k++) {
-                O[k] = fmaf(v[u4][k], w4.x, O[k]);
-                O[k] = fmaf(v[u4 + 1][k], w4.y, O[k]);
-                O[k] = fmaf(v[u4 + 2][k], w4.z, O[k]);
-                O[k] = fmaf(v[u4 + 3][k], w4.w, O[k]);
-            }
-        }
-    } else {
-        // long contexts: one round of loads per NBAT chunks
-        for (uint32_t cb = 0; cb < nv; cb += NBAT) {
-            load_o(cb);
-#pragma unroll
-            for (int u = 0; u < NBAT; u++) {
-                const uint32_t c = cb + u;
-                const float mc = c < MB ? sm[g_t][c < MB ? c : 0] : ld_dev(pt + (size_t)min(c, nv - 1) * (FD_HD + 2) + FD_HD);
-                const float wgt = c < nv ? expf(mc - Mt) : 0.f;
-#pragma unroll
-                for (int k = 0; k < OPT; k++) O[k] = fmaf(v[u][k], wgt, O[k]);
-            }
-        }
-    }
-    TRACE_OPS(6);
-    if (tid < (uint32_t)NTH) {
-#pragma unroll
-        for (int k = 0; k < OPT; k++) {
-            const float r = hL[g_t] > 0.f ? O[k] / hL[g_t] : 0.f;
-            ob[tid * OPT + k] = r;
-            if (p.out) p.out[(size_t)(kvh * G) * FD_HD + tid * OPT + k] = r;
-        }
-    }
-    TRACE_OPS(7);
-    if (p.xq) {
-        __syncthreads();
-        XQView v = xq_view(p.xq, p.nq * FD_HD / 32);
-        for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += AD_T)  // whole 32-lane groups (G*128 % 32 == 0)
-            xq_store_block32(ob[o], o & 31, v, (kvh * G * FD_HD + o) / 32);
-    }
-    if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    TRACE_OPS(5);
+    attn_merge<1>(p, kvh * G + slot, nv, !s_ok);
 }
 
 // partials: zhk_flash_decode_partials_bytes(nh, hd, max_seq) bytes; the
 // counter words at its end must be zero before the first launch (each
 // launch leaves them zero).
-static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uint32_t max_seq, bool fused) {
+static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uint32_t max_seq, bool fused,
+                       bool ident) {
     AttnP p = p0;
-    p.n_chunks = (max_seq + AD_TC - 1) / AD_TC;
+    p.n_chunks = attn_n_chunks(max_seq);
     dim3 grid(nkv, p.n_chunks);
     // one workgroup per CU: a grid within the CU count is resident at once
     const bool rev = (uint64_t)nkv * p.n_chunks > (uint64_t)c->cu_count;
-#define AD_LAUNCH1(GG, FF)                                                                             \
-    if (rev) hipLaunchKernelGGL((k_attn_decode<GG, FF, true>), grid, dim3(AD_T), 0, c->stream, p);     \
-    else hipLaunchKernelGGL((k_attn_decode<GG, FF, false>), grid, dim3(AD_T), 0, c->stream, p)
+#define AD_LAUNCH1(GG, FF)                                                                                   \
+    if (ident) hipLaunchKernelGGL((k_attn_decode<GG, FF, AD_IDENT>), grid, dim3(AD_T), 0, c->stream, p);      \
+    else if (rev) hipLaunchKernelGGL((k_attn_decode<GG, FF, AD_PAGED_REV>), grid, dim3(AD_T), 0, c->stream, p); \
+    else hipLaunchKernelGGL((k_attn_decode<GG, FF, AD_PAGED>), grid, dim3(AD_T), 0, c->stream, p)
 #define AD_LAUNCH(GG)          \
     if (fused) {               \
         AD_LAUNCH1(GG, true);  \
@@ -687,7 +750,7 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
 }
 
 static uint32_t *attn_counters(float *partials, uint32_t nh, uint32_t hd, uint32_t max_seq) {
-    return (uint32_t *)((char *)partials + (uint64_t)nh * ((max_seq + AD_TC - 1) / AD_TC) * (hd + 2) * 4);
+    return (uint32_t *)((char *)partials + (uint64_t)nh * attn_n_chunks(max_seq) * (hd + 2) * 4);
 }
 
 int zhk_flash_decode(zh_ctx *c, const float *q, const uint16_t *kc, const uint16_t *vc, const uint32_t *pages,
@@ -697,7 +760,7 @@ int zhk_flash_decode(zh_ctx *c, const float *q, const uint16_t *kc, const uint16
     p.q = q; p.kc = (uint16_t *)kc; p.vc = (uint16_t *)vc; p.pages = pages; p.n_pages = n_pages;
     p.cache_tokens = cache_tokens; p.pos = seq_len; p.scale = scale; p.part = partials;
     p.counters = attn_counters(partials, nh, hd, max_seq); p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
-    return attn_launch(c, p, nkv, nh / nkv, max_seq, false);
+    return attn_launch(c, p, nkv, nh / nkv, max_seq, false, false);
 }
 
 // RoPE table: cs[pos][i] = (cos, sin) of (float)pos * inv_freq[i], i < 64,
@@ -720,13 +783,13 @@ int zhk_rope_table(zh_ctx *c, const float *inv_freq, uint32_t n_pos, float *cs) 
 int zhk_attn_decode_fused(zh_ctx *c, const float *q, const float *k, const float *v, const float *qw, const float *kw,
                           const float *rope_cs, uint16_t *kc, uint16_t *vc, const uint32_t *pages, uint32_t n_pages,
                           uint32_t cache_tokens, float *out, void *xq_out, uint32_t nh, uint32_t nkv, zh_pos_src pos,
-                          uint32_t max_seq, float scale, float eps, float *partials) {
+                          uint32_t max_seq, float scale, float eps, float *partials, bool ident_pages) {
     AttnP p = {};
     p.q = q; p.k_new = k; p.v_new = v; p.q_norm = qw; p.k_norm = kw; p.rope_cs = rope_cs;
     p.kc = kc; p.vc = vc; p.pages = pages; p.n_pages = n_pages; p.cache_tokens = cache_tokens; p.pos = pos;
     p.scale = scale; p.eps = eps; p.part = partials; p.counters = attn_counters(partials, nh, FD_HD, max_seq);
     p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
-    return attn_launch(c, p, nkv, nh / nkv, max_seq, true);
+    return attn_launch(c, p, nkv, nh / nkv, max_seq, true, ident_pages);
 }
 
 extern "C" int zh_flash_decode(zh_ctx *c, const zh_buf *q, const zh_buf *kc, const zh_buf *vc, const zh_buf *pages,
