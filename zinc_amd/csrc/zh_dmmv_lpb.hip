@@ -819,12 +819,12 @@ __global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
 // ql[64h..), qh[32h..), sc[8h..), d) as in k_dmmv_q6k_lpb, with the block
 // bytes read from the LDS tile. Q6_K blocks are 210 bytes, so a block starts
 // 2-byte aligned; dword reads are realigned with alignbyte.
-template <int TL>
+template <int TL, int NCH>
 __global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     __shared__ float red[4];
     constexpr int RPB = LPB_T / TL;  // rows per batch
-    constexpr int NCH = 7;           // ceil(128 blocks * 210 B / 4 KB)
+    // NCH = ceil(RPB * row bytes / 4 KB) 16-byte chunks per lane and tile
     const uint32_t nb = p.K / 256, row_bytes = nb * 210, nh = nb * 2;
     XLds lx = xlds_view(lds_raw, nb);
     uint8_t *tile = lds_raw + (size_t)nb * (XB_STRIDE + 96);
@@ -836,6 +836,7 @@ __global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
     u32x4 st[1][NCH];
     uint32_t bi = blockIdx.x;
     TRACE(0);
+    // grid <= nbatch (host), so the first batch always exists
     stage_and_fetch<(3 * TL / 2 + 15) / 16, (TL / 8 > 1 ? TL / 8 : 1)>(
         p, lx, red, [&] { tile_fetch<1, NCH, RPB>(p, bi, row_bytes, st); });
     TRACE(1);
@@ -1002,8 +1003,13 @@ static int try_q4k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t 
 
 
 template <int TL>
-static int launch_q6k_tile(zh_ctx *c, const LpbP &p, uint32_t wgs, uint32_t lds) {
-    hipLaunchKernelGGL((k_dmmv_q6k_tile<TL>), dim3(wgs), dim3(LPB_T), lds, c->stream, p);
+static int launch_q6k_tile(zh_ctx *c, const LpbP &p, uint32_t wgs, uint32_t lds, uint32_t nch) {
+    switch (nch) {
+#define Q6T(N) case N: hipLaunchKernelGGL((k_dmmv_q6k_tile<TL, N>), dim3(wgs), dim3(LPB_T), lds, c->stream, p); break;
+    Q6T(4) Q6T(5) Q6T(6) Q6T(7)  // RPB * K/256 is in (64, 128], so a tile is 3.3 .. 6.6 x 4 KB
+#undef Q6T
+    default: return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "q6k tile: %u chunks", nch);
+    }
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
 }
@@ -1033,13 +1039,14 @@ static int try_q6k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t 
     if (per_cu > (uint32_t)(capm > 0 ? capm : 2)) per_cu = (uint32_t)(capm > 0 ? capm : 2);
     uint32_t wgs = nbatch, cap = (uint32_t)c->cu_count * (per_cu ? per_cu : 1);
     if (wgs > cap) wgs = cap;
+    const uint32_t nch = (rpb * row_bytes + 4095) / 4096;
     switch (TL) {
-    case 4: return launch_q6k_tile<4>(c, p, wgs, lds);
-    case 8: return launch_q6k_tile<8>(c, p, wgs, lds);
-    case 16: return launch_q6k_tile<16>(c, p, wgs, lds);
-    case 32: return launch_q6k_tile<32>(c, p, wgs, lds);
-    case 64: return launch_q6k_tile<64>(c, p, wgs, lds);
-    default: return launch_q6k_tile<128>(c, p, wgs, lds);
+    case 4: return launch_q6k_tile<4>(c, p, wgs, lds, nch);
+    case 8: return launch_q6k_tile<8>(c, p, wgs, lds, nch);
+    case 16: return launch_q6k_tile<16>(c, p, wgs, lds, nch);
+    case 32: return launch_q6k_tile<32>(c, p, wgs, lds, nch);
+    case 64: return launch_q6k_tile<64>(c, p, wgs, lds, nch);
+    default: return launch_q6k_tile<128>(c, p, wgs, lds, nch);
     }
 }
 

@@ -1,0 +1,98 @@
+"""Configs 1-2 measurement: one DMMV launch per shape at batch 1, timed with
+HIP events on the library stream over a rotating set of weight copies larger
+than the 256 MB MALL (so every launch streams its weights from HBM), as the
+reference's bench_hot_decode rotates a 16-slot working set.
+
+    python -m zinc_amd.dmmv_sweep [--iters 60] [--md OUT.md]
+
+Per shape: zh_dmmv (f32 activation, the C-ABI entry that replaces
+DmmvDispatch.recordDispatch, dmmv.zig:806-874) and zh_dmmv_xq (the
+activation pre-quantised once, as the engine feeds the projections that share
+an input). Algorithmic bytes = weight blocks + 4 K (x) + 4 M (y), the
+per-kernel figure of the bandwidth roofline; fraction of the 8 TB/s peak.
+A streaming read of 1 GiB gives the measured ceiling beside it.
+"""
+import argparse
+import json
+import sys
+
+from . import hip
+
+PEAK = 8000.0  # GB/s
+ROTATE_BYTES = 600 << 20
+
+SHAPES = [
+    ("config 1: Q4_K 4096x4096", hip.Q4_K, 4096, 4096),
+    ("Q4_K 4096->12288 (gate/up)", hip.Q4_K, 12288, 4096),
+    ("Q4_K 12288->4096 (down)", hip.Q4_K, 4096, 12288),
+    ("Q6_K 4096->151936 (lm-head)", hip.Q6_K, 151936, 4096),
+    ("Q8_0 4096x4096", hip.Q8_0, 4096, 4096),
+    ("MXFP4 2880x2880", hip.MXFP4, 2880, 2880),
+]
+
+
+def measure(ctx, name, qt, M, K, iters):
+    wb = hip.tensor_bytes(qt, M, K)
+    ncp = max(2, -(-ROTATE_BYTES // wb))
+    W = ctx.alloc(wb * ncp)
+    for i in range(ncp):
+        ctx.synth_tensor(W, i * wb, qt, M, K, 1234 + 2, 100 + i)
+    x = ctx.alloc(K * 4)
+    ctx.synth_vector(x, 0, 0, K, 1.0, 1234 + 2, 99)
+    xq = ctx.alloc(ctx.xq_bytes(K))
+    ctx.quantize_activation(x, 0, K, xq)
+    y = ctx.alloc(M * 4)
+    alg = wb + 4 * K + 4 * M
+    res = {"shape": name, "qtype": qt, "M": M, "K": K, "weight_bytes": wb, "alg_bytes": alg, "copies": ncp}
+    for label, fn in (("f32_x", lambda c: ctx.dmmv(qt, W, c * wb, x, 0, y, 0, M, K, 0)),
+                      ("xq_x", lambda c: ctx.dmmv_xq(qt, W, c * wb, xq, 0, y, 0, M, K, 0))):
+        try:
+            fn(0)
+        except hip.ZincError as e:  # a format without an XQ-input kernel
+            res[label] = {"error": e.name}
+            continue
+        for i in range(2 * ncp):
+            fn(i % ncp)
+        ctx.sync()
+        ctx.record(0)
+        for i in range(iters):
+            fn(i % ncp)
+        ctx.record(1)
+        ctx.sync()
+        us = ctx.elapsed_ms(0, 1) * 1e3 / iters
+        gbs = alg / (us * 1e-6) / 1e9
+        res[label] = {"us": round(us, 3), "GBs": round(gbs, 1), "frac": round(gbs / PEAK, 4)}
+    for b in (W, x, xq, y):
+        ctx.free(b)
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--iters", type=int, default=60)
+    ap.add_argument("--md", default=None, help="also write a markdown table here")
+    a = ap.parse_args()
+    ctx = hip.Context(0)
+    cal = ctx.alloc(1 << 30)
+    ctx.synth_vector(cal, 0, 1, (1 << 30) // 2, 1.0, 7, 7)
+    stream_gbs = ctx.stream_read_probe(cal, 1 << 30, 3)
+    ctx.free(cal)
+    rows = [measure(ctx, *s, a.iters) for s in SHAPES]
+    ctx.close()
+    out = {"workload": "configs 1-2: single DMMV launches at batch 1, rotating weight copies > 256 MB MALL",
+           "peak_GBs": PEAK, "stream_read_GBs": round(stream_gbs, 1), "shapes": rows}
+    print(json.dumps(out), flush=True)
+    if a.md:
+        with open(a.md, "w") as f:
+            f.write("| shape | alg bytes | f32 x: us | GB/s | of 8 TB/s | XQ x: us | GB/s | of 8 TB/s |\n")
+            f.write("|---|---|---|---|---|---|---|---|\n")
+            def cells(m):
+                return f"{m['us']} | {m['GBs']} | {m['frac']:.1%}" if "us" in m else f"{m['error']} | - | -"
+            for r in rows:
+                f.write(f"| {r['shape']} | {r['alg_bytes']:,} | {cells(r['f32_x'])} | {cells(r['xq_x'])} |\n")
+            f.write(f"\nStreaming read of 1 GiB (k_stream_read): {stream_gbs:.0f} GB/s.\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

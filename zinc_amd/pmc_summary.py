@@ -20,7 +20,7 @@ import sys
 
 from .roofline_probe import CAL_BYTES, down_bytes
 
-KERNEL = "k_dmmv_q6k_tile<128>"
+KERNEL = "k_dmmv_q6k_tile<128"
 
 
 def _rows(d):
