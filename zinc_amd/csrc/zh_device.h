@@ -200,3 +200,39 @@ ZH_DEV void xq_store_block32(float xi, int l, XQView v, uint32_t blk) {
     if ((l & 15) == 0) v.xsum[blk * 2 + (l >> 4)] = (float)s * sc;
 }
 
+// Router top-k with softmax over the selected logits (softmax_topk_v2.comp,
+// topKSoftmax forward.zig:496-537), in one wave: lane l holds logits l,
+// l+64, l+128, l+192 (n <= 256). Exact f32 comparisons, the lowest index wins
+// ties; routing = [ids u32 x k][weights f32 x k] with weights
+// exp(sel_j - sel_0) / sum.
+ZH_DEV void topk_softmax_wave(const float (&vals)[4], uint32_t n, uint32_t k, uint32_t *routing) {
+    const uint32_t lane = threadIdx.x & 63;
+    bool avail[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) avail[i] = lane + 64 * i < n;
+    float mysel = 0.f, m0 = 0.f;
+    for (uint32_t j = 0; j < k; j++) {
+        // best remaining (value desc, index asc) in this lane
+        float bv = -INFINITY;
+        uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (avail[i] && (bi == 0xFFFFFFFFu || vals[i] > bv)) { bv = vals[i]; bi = lane + 64 * i; }
+        // wave maximum, then the lowest index holding it (indices < 256 are
+        // exact as floats; DPP reductions, no LDS crossbar)
+        const float m = wave_max(bv);
+        const float candf = (bi != 0xFFFFFFFFu && bv == m) ? (float)bi : INFINITY;
+        const float cmin = -wave_max(-candf);
+        const uint32_t cand = cmin == INFINITY ? 0xFFFFFFFFu : (uint32_t)cmin;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (lane + 64 * i == cand) avail[i] = false;
+        if (lane == 0) routing[j] = cand;
+        if (lane == j) mysel = m;
+        if (j == 0) m0 = m;
+    }
+    const float my = lane < k ? expf(mysel - m0) : 0.f;
+    const float s = wave_sum(my);
+    if (lane < k) ((float *)routing)[k + lane] = my / s;
+}
+

@@ -334,6 +334,7 @@ struct DmmvP {
     uint64_t row_bytes;
     uint32_t acc;
     const uint32_t *routing;  // MoE: expert id per grid.y slot
+    uint32_t n_experts;       // MoE: ids are clamped below this (a NaN router yields id ~0)
     uint64_t expert_stride, xq_slot_stride;
     uint32_t y_slot_stride;
     // Plain mode may stack up to three matrices that share K and x (Q/K/V):
@@ -403,7 +404,7 @@ __global__ __launch_bounds__(NW == 1 ? 256 : NW * 64) void k_dmmv(DmmvP p) {
     float *y = p.y;
     if (MOE) {
         const uint32_t slot = blockIdx.y;
-        const uint64_t e = p.routing[slot];
+        const uint64_t e = min(p.routing[slot], p.n_experts - 1);
         Wm[0] += e * p.expert_stride;
         if (NM == 2) Wm[1] += e * p.expert_stride;
         xqb += slot * p.xq_slot_stride;
@@ -617,14 +618,278 @@ int zhk_dmmv_gate_up(zh_ctx *c, uint32_t qtype, const uint8_t *Wg, const uint8_t
 
 int zhk_dmmv_moe(zh_ctx *c, uint32_t qtype, const uint8_t *W, uint64_t expert_stride,
                  const uint32_t *routing, const void *xq, uint64_t xq_slot_stride, float *y, uint32_t M,
-                 uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2) {
+                 uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2, uint32_t n_experts) {
+    if (n_experts == 0) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "n_experts");
     DmmvP p = {};
+    p.n_experts = n_experts;
     p.W = W; p.W2 = W2 ? W2 : W; p.xq = (const uint8_t *)xq; p.y = y; p.M = M; p.K = K;
     p.row_bytes = zh_tensor_bytes(qtype, 1, K);
     p.routing = routing; p.expert_stride = expert_stride; p.xq_slot_stride = xq_slot_stride;
     p.y_slot_stride = M;
     if (gate_up) return launch_dmmv<MODE_GATE_UP, true>(c, qtype, p, n_used);
     return launch_dmmv<MODE_PLAIN, true>(c, qtype, p, n_used);
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged team kernel (MoE decode path). The activation is staged once per
+// workgroup into an LDS XQ image from f32 -- with the RMSNorm fused when a
+// norm weight is given -- so the standalone rms_norm / quantise launches
+// disappear; every lane then reads its unit's limbs from LDS.
+//  * DL_PLAIN: y = W x (or y += W x) over up to three stacked matrices
+//    (attn_norm fused into Q/K/V; ffn_norm fused into the router). Optional:
+//    workgroup 0 stores the staged image as XQ for later kernels, and the
+//    last workgroup to finish selects the router top-k (softmax_topk_v2.comp)
+//    from the M outputs, published with device-scope stores and a counter.
+//  * DL_DOWN_ACC: the expert down projections of all selected slots and the
+//    routing-weighted sum, y[r] += sum_j w_j (W_{e_j} x_j)[r] in slot order
+//    (dmmv down :6361-6408 + moe_weighted_acc.comp:23-33 in one launch), on
+//    XQ inputs that every lane reads for its own unit (staging them per
+//    workgroup re-quantised every slot in every workgroup and measured slower).
+// ---------------------------------------------------------------------------
+constexpr int DL_T = 256;
+constexpr int DL_MAXS = 8;   // expert slots held in flight by DL_DOWN_ACC
+enum { DL_PLAIN = 0, DL_DOWN_ACC = 1 };
+
+struct DlP {
+    uint32_t M, K;
+    uint64_t row_bytes;
+    const float *xf;       // DL_PLAIN: f32 activation
+    const uint8_t *xq;     // DL_DOWN_ACC: XQ inputs, slot j at xq + j * 108 K/32
+    const float *norm_w;   // DL_PLAIN: fused RMSNorm weight (nullptr: none)
+    float eps;
+    uint8_t *xq_out;       // DL_PLAIN: workgroup 0 stores the staged XQ image here
+    uint32_t acc;          // DL_PLAIN: y += W x
+    uint32_t nseg;         // DL_PLAIN: stacked matrices, rows [seg_end[s-1], seg_end[s]) -> segY[s]
+    const uint8_t *segW[3];
+    float *segY[3];
+    uint32_t seg_end[3];
+    const uint8_t *W;      // DL_DOWN_ACC: expert-stacked weights
+    uint64_t expert_stride;
+    const uint32_t *routing;  // [ids u32 x n_slots][weights f32 x n_slots]
+    uint32_t n_slots;
+    uint32_t n_experts;    // ids are clamped below this (a NaN router yields id ~0)
+    float *y;
+    uint32_t topk;         // DL_PLAIN router: k > 0 selects the top-k of the M outputs
+    uint32_t *routing_out;
+    uint32_t *cnt;         // zero between launches
+};
+
+// Stages the f32 activation of K (a multiple of 32, at most DL_XE * DL_T)
+// elements, RMSNorm'ed with w when w != nullptr (w[i] * (x[i] * rms_inv),
+// cpuRmsNormMul forward.zig:618-626), into an XQ image in LDS. Every element
+// a thread owns is loaded before any arithmetic, so staging costs one memory
+// latency; each 32-element block is quantised by the 32 lanes that own it (a
+// 32-lane group covers 32 consecutive elements, so each half-wave is wholly
+// active or inactive).
+constexpr int DL_XE = 16;
+ZH_DEV void dl_stage(const float *__restrict__ x, const float *__restrict__ w, float eps, uint32_t K, uint8_t *lds,
+                     float *red) {
+    const uint32_t t = threadIdx.x, nblk = K / 32;
+    float xr[DL_XE], wr[DL_XE];
+#pragma unroll
+    for (int j = 0; j < DL_XE; j++) {
+        const uint32_t i = t + DL_T * j;
+        xr[j] = i < K ? x[i] : 0.f;
+        wr[j] = i < K && w ? w[i] : 1.f;
+    }
+    float rms_inv = 1.f;
+    if (w) {
+        float sq = 0.f;
+#pragma unroll
+        for (int j = 0; j < DL_XE; j++) sq = fmaf(xr[j], xr[j], sq);
+        sq = wave_sum(sq);
+        if ((t & 63) == 0) red[t >> 6] = sq;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int k = 0; k < DL_T / 64; k++) tot += red[k];
+        rms_inv = 1.0f / sqrtf(tot / (float)K + eps);
+    }
+    const XQView q = xq_view(lds, nblk);
+#pragma unroll
+    for (int j = 0; j < DL_XE; j++) {
+        const uint32_t i = t + DL_T * j;
+        if (DL_T * j >= K) break;  // uniform
+        if (i < K) xq_store_block32(w ? wr[j] * (xr[j] * rms_inv) : xr[j], t & 31, q, i / 32);
+    }
+    __syncthreads();
+}
+
+template <class F, int TL, int R, int MODE>
+__global__ __launch_bounds__(DL_T) void k_dmmv_lds(DlP p) {
+    extern __shared__ __align__(16) uint8_t dl_lds[];
+    __shared__ float red[DL_T / 64];
+    constexpr int TPW = DL_T / TL;
+    const int tid = threadIdx.x, tlane = tid % TL, team = tid / TL;
+    const uint32_t U = p.K / F::EPU, nblk = p.K / 32;
+    const bool active = (uint32_t)tlane < U;
+    const uint32_t nteams = gridDim.x * TPW;
+    if (MODE == DL_PLAIN) {
+        // segment of a batch (batches never straddle segments); rows past a
+        // segment are clamped to its last row (loaded, computed, not written)
+        auto geom = [&](uint32_t r0, uint32_t &sg, uint32_t &rr0, uint32_t &seg_rows) {
+            uint32_t seg_start = 0;
+            sg = 0;
+            seg_rows = p.M;
+            if (p.nseg > 1) {
+                sg = (r0 >= p.seg_end[0] ? 1u : 0u) + (p.nseg > 2 && r0 >= p.seg_end[1] ? 1u : 0u);
+                seg_start = sg ? p.seg_end[sg - 1] : 0u;
+                seg_rows = p.seg_end[sg] - seg_start;
+            }
+            rr0 = r0 - seg_start;
+        };
+        auto fetch = [&](uint32_t r0, uint32_t (&raw)[R][F::RAW]) {
+            uint32_t sg, rr0, seg_rows;
+            geom(min(r0, p.M - 1), sg, rr0, seg_rows);
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (active) F::load_raw(p.segW[sg] + (size_t)min(rr0 + r, seg_rows - 1) * p.row_bytes, tlane, raw[r]);
+        };
+        uint32_t r0 = (blockIdx.x * TPW + team) * R;
+        uint32_t raw[R][F::RAW];
+        fetch(r0, raw);  // the first batch's weights are in flight while x is staged
+        dl_stage(p.xf, p.norm_w, p.eps, p.K, dl_lds, red);
+        if (p.xq_out && blockIdx.x == 0)
+            for (uint32_t i = tid; i < nblk * 27; i += DL_T)  // 108 B per block = 27 dwords
+                ((uint32_t *)p.xq_out)[i] = ((const uint32_t *)dl_lds)[i];
+        XReg xr;
+        if (active) F::load_x(xr, xq_view(dl_lds, nblk), tlane);
+        for (; r0 < p.M; r0 += nteams * R) {
+            uint32_t sg, rr0, seg_rows;
+            geom(r0, sg, rr0, seg_rows);
+            if (r0 != (blockIdx.x * TPW + team) * R) fetch(r0, raw);
+            float part[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) part[r] = active ? F::compute(raw[r], xr, tlane) : 0.f;
+            const float res = team_reduce_multi<TL, R>(part, tlane);
+            const int idx = owner_index<TL, R>(tlane);
+            if (tlane % (TL / R) == 0 && rr0 + idx < seg_rows) {
+                float *yo = p.segY[sg] + rr0 + idx;
+                const float out = p.acc ? res + *yo : res;
+                if (p.topk) st_dev(yo, out);  // read by another workgroup below
+                else *yo = out;
+            }
+        }
+        if (p.topk) {
+            __shared__ uint32_t s_last;
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0)
+                s_last = __hip_atomic_fetch_add(p.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         gridDim.x - 1;
+            __syncthreads();
+            if (s_last && tid < 64) {
+                float vals[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t e = tid + 64 * i;
+                    vals[i] = e < p.M ? ld_dev(p.segY[0] + e) : -INFINITY;
+                }
+                topk_softmax_wave(vals, p.M, p.topk, p.routing_out);
+                if (tid == 0) __hip_atomic_store(p.cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    } else {
+        // one row per team; every slot's weight unit is requested before any
+        // arithmetic, then the slots are reduced and weighted in order
+        uint32_t ex[DL_MAXS];
+        float wgt[DL_MAXS];
+#pragma unroll
+        for (int j = 0; j < DL_MAXS; j++) {
+            ex[j] = (uint32_t)j < p.n_slots ? min(p.routing[j], p.n_experts - 1) : 0u;
+            wgt[j] = (uint32_t)j < p.n_slots ? __uint_as_float(p.routing[p.n_slots + j]) : 0.f;
+        }
+        uint32_t raw[DL_MAXS][F::RAW];
+        auto fetch = [&](uint32_t r) {
+#pragma unroll
+            for (int j = 0; j < DL_MAXS; j++)
+                if (active && (uint32_t)j < p.n_slots)
+                    F::load_raw(p.W + ex[j] * p.expert_stride + (size_t)min(r, p.M - 1) * p.row_bytes, tlane, raw[j]);
+        };
+        const uint32_t r_first = blockIdx.x * TPW + team;
+        fetch(r_first);
+        for (uint32_t r = r_first; r < p.M; r += nteams) {
+            if (r != r_first) fetch(r);
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < DL_MAXS; j++) {
+                if ((uint32_t)j >= p.n_slots) break;  // uniform
+                XReg xr;
+                if (active) F::load_x(xr, xq_view((uint8_t *)p.xq + (size_t)j * nblk * 108, nblk), tlane);
+                const float dot = team_sum_dpp<TL>(active ? F::compute(raw[j], xr, tlane) : 0.f);
+                s += wgt[j] * dot;
+            }
+            if (tlane == 0) p.y[r] += s;
+        }
+    }
+}
+
+template <class F, int MODE>
+static int launch_dl(zh_ctx *c, const DlP &p) {
+    const uint32_t U = p.K / F::EPU;
+    const uint32_t lds = MODE == DL_DOWN_ACC ? 0u : (p.K / 32) * 108;
+    constexpr int R = MODE == DL_PLAIN ? 2 : 1;
+    const uint32_t tl = U <= 16 ? 16 : U <= 32 ? 32 : 64;
+    if (U > 64 || p.K > (uint32_t)(DL_XE * DL_T))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "LDS-staged DMMV: K=%u too large", p.K);
+    const uint32_t teams = (p.M + R - 1) / R, tpw = DL_T / tl;
+    uint32_t wgs = (teams + tpw - 1) / tpw, cap = (uint32_t)c->cu_count * 4u;
+    if (wgs > cap) wgs = cap;
+#define DL_L(TT) hipLaunchKernelGGL((k_dmmv_lds<F, TT, R, MODE>), dim3(wgs), dim3(DL_T), lds, c->stream, p)
+    if (tl == 16) DL_L(16);
+    else if (tl == 32) DL_L(32);
+    else DL_L(64);
+#undef DL_L
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+template <int MODE>
+static int launch_dl_q(zh_ctx *c, uint32_t qtype, const DlP &p) {
+    switch (qtype) {
+    case ZH_Q4_K: return launch_dl<FmtQ4K, MODE>(c, p);
+    case ZH_Q6_K: return launch_dl<FmtQ6K, MODE>(c, p);
+    case ZH_Q8_0: return launch_dl<FmtQ80, MODE>(c, p);
+    case ZH_MXFP4: return launch_dl<FmtMXFP4, MODE>(c, p);
+    default: return zh_set_err(c, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "qtype %u has no DMMV kernel", qtype);
+    }
+}
+
+bool zhk_dmmv_lds_supported(uint32_t qtype, uint32_t K) {
+    const uint32_t epu = qtype == ZH_MXFP4 ? 32 : 64;
+    const uint32_t q = (qtype == ZH_Q4_K || qtype == ZH_Q6_K) ? 256 : epu;
+    return K > 0 && K % q == 0 && K % 32 == 0 && K / epu <= 64;
+}
+
+int zhk_dmmv_lds_plain(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, float *const *y,
+                       const uint32_t *M, const float *x, const float *norm_w, float eps, uint32_t K,
+                       uint32_t acc, void *xq_out, uint32_t topk, uint32_t *routing_out, uint32_t *cnt) {
+    if (nseg < 1 || nseg > 3 || !zhk_dmmv_lds_supported(qtype, K) || (topk && (nseg != 1 || M[0] > 256)))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "LDS-staged DMMV shape");
+    DlP p = {};
+    p.K = K; p.row_bytes = zh_tensor_bytes(qtype, 1, K); p.xf = x; p.norm_w = norm_w; p.eps = eps;
+    p.xq_out = (uint8_t *)xq_out; p.acc = acc; p.nseg = nseg;
+    uint32_t end = 0;
+    for (uint32_t s = 0; s < nseg; s++) {
+        if (s + 1 < nseg && M[s] % 2) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "segment rows must be even");
+        p.segW[s] = W[s]; p.segY[s] = y[s];
+        end += M[s];
+        p.seg_end[s] = end;
+    }
+    p.M = end; p.topk = topk; p.routing_out = routing_out; p.cnt = cnt;
+    return launch_dl_q<DL_PLAIN>(c, qtype, p);
+}
+
+int zhk_dmmv_lds_down_acc(zh_ctx *c, uint32_t qtype, const uint8_t *W, uint64_t expert_stride,
+                          const uint32_t *routing, uint32_t n_slots, uint32_t n_experts, const void *xq, float *y,
+                          uint32_t M, uint32_t K) {
+    if (n_slots == 0 || n_slots > DL_MAXS || n_experts == 0 || !zhk_dmmv_lds_supported(qtype, K))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "expert down shape");
+    DlP p = {};
+    p.M = M; p.K = K; p.row_bytes = zh_tensor_bytes(qtype, 1, K);
+    p.W = W; p.expert_stride = expert_stride; p.routing = routing; p.n_slots = n_slots; p.y = y;
+    p.n_experts = n_experts; p.xq = (const uint8_t *)xq;
+    return launch_dl_q<DL_DOWN_ACC>(c, qtype, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -763,7 +1028,8 @@ extern "C" int zh_dmmv_moe(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t 
     if ((rc = zhk_quantize_xq(c, (const float *)((const char *)x->ptr + x_off), xq, K, n_used, x_expert_stride)))
         return rc;
     return zhk_dmmv_moe(c, qtype, (const uint8_t *)W->ptr, expert_stride, (const uint32_t *)routing->ptr, xq, xqs,
-                        (float *)((char *)y->ptr + y_off), M, K, n_used, 0, nullptr);
+                        (float *)((char *)y->ptr + y_off), M, K, n_used, 0, nullptr,
+                        (uint32_t)((W->size - zh_tensor_bytes(qtype, M, K)) / expert_stride + 1));
 }
 
 // ---------------------------------------------------------------------------

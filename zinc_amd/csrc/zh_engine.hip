@@ -60,6 +60,7 @@ struct zh_engine {
     uint8_t *xq_h = nullptr, *xq_q = nullptr, *xq_f = nullptr;
     uint32_t *routing = nullptr, *am_part = nullptr, *st = nullptr, *prompt = nullptr, *ring = nullptr;
     uint32_t *grp_cnt = nullptr;  // SwiGLU-output XQ: one counter per 32-row group (kept zero between launches)
+    uint32_t *router_cnt = nullptr;  // router top-k: workgroups finished (kept zero between launches)
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
@@ -240,13 +241,13 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
         {(void **)&e->k, 4ull * kvd}, {(void **)&e->v, 4ull * kvd}, {(void **)&e->attn, 4ull * qd},
         {(void **)&e->s, 4ull * F}, {(void **)&e->logits, 4ull * c.vocab}, {(void **)&e->rl, 4ull * 256},
         {(void **)&e->edown_out, 4ull * H * (c.n_experts_used ? c.n_experts_used : 1)},
-        {(void **)&e->fd_part, zhk_flash_decode_partials_bytes(c.n_heads, hd, c.max_ctx)},
+        {(void **)&e->fd_part, zhk_flash_decode_partials_bytes(c.n_heads, c.n_kv_heads, hd, c.max_ctx)},
         {(void **)&e->xq_h, zh_xq_bytes_int(H)}, {(void **)&e->xq_q, zh_xq_bytes_int(qd)},
         {(void **)&e->xq_f, zh_xq_bytes_int(c.n_experts ? c.expert_ffn : c.ffn) * (c.n_experts_used ? c.n_experts_used : 1)},
         {(void **)&e->routing, 8ull * 16}, {(void **)&e->am_part, 8ull * 256}, {(void **)&e->st, 4ull * ST_WORDS},
         {(void **)&e->prompt, 4ull * MAX_PROMPT}, {(void **)&e->ring, 4ull * MAX_GEN}, {(void **)&e->pages, 4ull * e->n_pages},
         {(void **)&e->inv_freq, 4ull * hd / 2}, {(void **)&e->rope_cs, 8ull * c.max_ctx * (hd / 2)},
-        {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)},
+        {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)}, {(void **)&e->router_cnt, 4},
     };
     uint64_t aoff = 0;
     for (auto &a : acts) aoff = align256(aoff + a.bytes);
@@ -343,6 +344,11 @@ static int record_step(zh_engine *e, bool collect) {
     const bool lpb_ffn = lpb && m.n_experts == 0 && m.type_ffn_gate_up == ZH_Q4_K &&
                          zhk_lpb_supported(ZH_Q4_K, H) && zhk_lpb_supported(m.type_ffn_down, m.ffn);
     const bool lpb_head = lpb && zhk_lpb_supported(m.type_lm_head, H) && m.vocab % 2 == 0;
+    // LDS-staged kernels with the norms, router top-k and expert combine fused
+    const bool lds = !getenv("ZH_NO_LDS_DMMV");
+    const bool lds_moe = lds && m.n_experts && m.n_experts <= 256 && m.n_experts_used <= 8 &&
+                         zhk_dmmv_lds_supported(m.type_router, H) && zhk_dmmv_lds_supported(m.type_ffn_down, m.expert_ffn) &&
+                         m.expert_ffn % 32 == 0;
     for (uint32_t l = 0; l < m.n_layers; l++) {
         const Layer &y = e->L[l];
         if (lpb_attn) {
@@ -390,6 +396,23 @@ static int record_step(zh_engine *e, bool collect) {
                              0.f, nullptr, m.ffn, 1, swiglu_xq ? e->xq_f : nullptr));
             continue;
         }
+        if (lds_moe) {
+            // ffn_norm + router + top-k in one launch (it also leaves the
+            // normed activation as XQ for the experts); experts gate/up +
+            // SwiGLU; their outputs as XQ; then the selected down projections
+            // with the weighted sum added to the residual
+            const uint32_t F = m.expert_ffn, k = m.n_experts_used, E = m.n_experts;
+            const uint8_t *wr = W(y.router);
+            float *rl = e->rl;
+            ERC(zhk_dmmv_lds_plain(c, m.type_router, 1, &wr, &rl, &E, e->hidden, Wf(y.ffn_norm), m.eps, H, 0, e->xq_h,
+                                   k, e->routing, e->router_cnt));
+            ERC(zhk_dmmv_moe(c, m.type_ffn_gate_up, W(y.egate), zh_tensor_bytes(m.type_ffn_gate_up, F, H), e->routing,
+                             e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
+            ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
+            ERC(zhk_dmmv_lds_down_acc(c, m.type_ffn_down, W(y.edown), zh_tensor_bytes(m.type_ffn_down, H, F),
+                                      e->routing, k, m.n_experts, e->xq_f, e->hidden, H, F));
+            continue;
+        }
         ERC(zhk_rms_norm(c, e->hidden, Wf(y.ffn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
         if (m.n_experts == 0) {
             ERC(zhk_dmmv_gate_up(c, m.type_ffn_gate_up, W(y.gate), W(y.up), e->xq_h, e->s, m.ffn, H));
@@ -400,10 +423,10 @@ static int record_step(zh_engine *e, bool collect) {
             ERC(zhk_dmmv(c, m.type_router, W(y.router), e->xq_h, e->rl, m.n_experts, H, 0));
             ERC(zhk_softmax_topk(c, e->rl, m.n_experts, k, e->routing));
             ERC(zhk_dmmv_moe(c, m.type_ffn_gate_up, W(y.egate), zh_tensor_bytes(m.type_ffn_gate_up, F, H), e->routing,
-                             e->xq_h, 0, e->s, F, H, k, 1, W(y.eup)));
+                             e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
             ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
             ERC(zhk_dmmv_moe(c, m.type_ffn_down, W(y.edown), zh_tensor_bytes(m.type_ffn_down, H, F), e->routing,
-                             e->xq_f, zh_xq_bytes_int(F), e->edown_out, H, F, k, 0, nullptr));
+                             e->xq_f, zh_xq_bytes_int(F), e->edown_out, H, F, k, 0, nullptr, m.n_experts));
             ERC(zhk_moe_weighted_acc(c, e->hidden, e->edown_out, e->routing, H, k, H));
         }
     }

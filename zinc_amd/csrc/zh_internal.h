@@ -67,9 +67,21 @@ int zhk_dmmv_multi(zh_ctx *ctx, uint32_t qtype, uint32_t nseg, const uint8_t *co
                    const uint32_t *M, const void *xq, uint32_t K);
 int zhk_dmmv_gate_up(zh_ctx *ctx, uint32_t qtype, const uint8_t *Wg, const uint8_t *Wu,
                      const void *xq, float *y, uint32_t M, uint32_t K);
+// LDS-staged DMMV (MoE router): f32 activation staged per workgroup with an
+// optional fused RMSNorm; optional XQ copy of the staged activation and router
+// top-k by the last workgroup (cnt zero between launches).
+bool zhk_dmmv_lds_supported(uint32_t qtype, uint32_t K);
+int zhk_dmmv_lds_plain(zh_ctx *ctx, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, float *const *y,
+                       const uint32_t *M, const float *x, const float *norm_w, float eps, uint32_t K,
+                       uint32_t acc, void *xq_out, uint32_t topk, uint32_t *routing_out, uint32_t *cnt);
+// Expert down projections of n_slots selected experts + routing-weighted sum into y (y += ...);
+// XQ inputs, slot stride 108 K/32 bytes.
+int zhk_dmmv_lds_down_acc(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint64_t expert_stride,
+                          const uint32_t *routing, uint32_t n_slots, uint32_t n_experts, const void *xq, float *y,
+                          uint32_t M, uint32_t K);
 int zhk_dmmv_moe(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint64_t expert_stride,
                  const uint32_t *routing, const void *xq, uint64_t xq_slot_stride, float *y,
-                 uint32_t M, uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2);
+                 uint32_t M, uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2, uint32_t n_experts);
 int zhk_dequant_rows(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint32_t row0, uint32_t n_rows,
                      uint32_t K, float *out, const uint32_t *row_from_dev, uint32_t clamp_rows, uint32_t gather = 0);
 int zhk_synth_tensor(zh_ctx *ctx, uint8_t *dst, uint32_t qtype, uint64_t rows, uint64_t cols,
@@ -92,7 +104,7 @@ int zhk_flash_decode(zh_ctx *ctx, const float *q, const uint16_t *kc, const uint
                      const uint32_t *pages, uint32_t n_pages, uint32_t cache_tokens, float *out,
                      void *xq_out, uint32_t nh, uint32_t nkv, uint32_t hd, zh_pos_src seq_len,
                      uint32_t max_seq, float scale, float *partials);
-uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t hd, uint32_t max_seq);
+uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_seq);
 // Fused decode attention: q/k RMSNorm + RoPE, KV write of the new token at
 // `pos`, attention over [0, pos], chunk merge. `partials` as above, with its
 // trailing counter words zero before the first launch.

@@ -220,26 +220,31 @@ constexpr int AD_W = 4;      // waves per workgroup
 constexpr int AD_TW = 40;    // tokens per wave: starts 8-aligned, spans at most 3 pages
 constexpr int AD_T = AD_W * 64;
 constexpr int AD_TC = AD_W * AD_TW;  // tokens per chunk (at most)
-constexpr int AD_ND = 32;            // chunks per kv head (CUs per XCD) in the identity-page mode
 // Chunk geometry modes: page-table lookups with chunk = blockIdx.y, the same
 // dispatched newest-first (grids larger than the device), or an identity page
 // table (physical token = logical token), where nothing waits on page entries
-// and the chunk length follows the context: ceil(seq / 32) rounded up to 8
-// tokens (at least 40) while that fits 160, so a context of up to 5120 tokens
-// spreads over all 32 CUs of each kv head's XCD.
+// and the chunk length follows the context: ceil(seq / nd) rounded up to 8
+// tokens (at least 40) while that fits 160, with nd = CUs / kv heads, so the
+// chunks of all kv heads cover the device once (32 per head for 8 kv heads:
+// one XCD each).
 enum { AD_PAGED = 0, AD_PAGED_REV = 1, AD_IDENT = 2 };
-ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq) {
-    const uint32_t ct = ((seq + AD_ND - 1) / AD_ND + 7) / 8 * 8;
-    return seq > (uint32_t)(AD_ND * AD_TC) ? (uint32_t)AD_TC : max(ct, (uint32_t)AD_TW);
+ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq, uint32_t nd) {
+    const uint32_t ct = ((seq + nd - 1) / nd + 7) / 8 * 8;
+    return seq > nd * AD_TC ? (uint32_t)AD_TC : max(ct, (uint32_t)AD_TW);
 }
-static uint32_t attn_n_chunks(uint32_t max_seq) {
+static uint32_t attn_nd(uint32_t nkv, int cu_count) {
+    const uint32_t cu = cu_count > 0 && cu_count < 256 ? (uint32_t)cu_count : 256u;
+    return cu / nkv > 0 ? cu / nkv : 1u;
+}
+// chunk slots per head: the partials of a device with at most 256 CUs fit
+static uint32_t attn_n_chunks(uint32_t max_seq, uint32_t nd) {
     const uint32_t n = (max_seq + AD_TC - 1) / AD_TC;
-    return n > (uint32_t)AD_ND ? n : (uint32_t)AD_ND;
+    return n > nd ? n : nd;
 }
 
-uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t hd, uint32_t max_seq) {
+uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_seq) {
     // partials + two counter words per kv head (at most nh words)
-    return (uint64_t)nh * attn_n_chunks(max_seq) * (hd + 2) * 4 + 4ull * nh + 256;
+    return (uint64_t)nh * attn_n_chunks(max_seq, attn_nd(nkv, 256)) * (hd + 2) * 4 + 4ull * nh + 256;
 }
 
 struct AttnP {
@@ -258,6 +263,7 @@ struct AttnP {
     float *out;          // [nq * 128]
     uint8_t *xq;         // optional XQ image of out
     uint32_t nq;
+    uint32_t nd;         // AD_IDENT: target chunks per kv head
 };
 
 ZH_DEV float sum8(float v) { return row8_sum(v); }  // over the 8 lanes of a token group
@@ -298,9 +304,10 @@ ZH_DEV const uint16_t *kv_row(const uint16_t *h, size_t pa, size_t pb, size_t pc
 
 // Merges the chunk partials of q heads h0 .. h0+GM-1: O = sum_c exp(m_c - M) O_c
 // / sum_c exp(m_c - M) l_c (the split-K combine of flash_decode.comp's
-// reduction). Reads partials published at device scope; `poison` (a wait that
+// reduction). NBAT chunks per round of O loads (every load is issued, with
+// clamped addresses, so the wait counts stay static). Reads partials published at device scope; `poison` (a wait that
 // timed out) turns the outputs into NaN.
-template <int GM>
+template <int GM, int NBAT>
 ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     TRACE_OPS(11);
@@ -310,7 +317,6 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
     // dims per thread: power of two with G*128/OPT <= AD_T
     constexpr int OPT = GM * FD_HD <= AD_T ? 1 : GM * FD_HD <= 2 * AD_T ? 2 : GM * FD_HD <= 4 * AD_T ? 4 : 8;
     constexpr int NTH = GM * FD_HD / OPT;
-    constexpr int NBAT = GM <= 4 ? 40 : 12;  // chunks per round of O loads
     constexpr int MB = 256;                 // chunk statistics kept in LDS
     __shared__ __align__(16) float sm[GM][MB];
     __shared__ float hM[GM], hL[GM];
@@ -426,7 +432,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     const uint32_t pos_raw = *(p.pos.dev ? p.pos.dev : p.pages);
     const uint32_t posv = p.pos.dev ? pos_raw + p.pos.value : p.pos.value;
     const uint32_t seq = FUSED ? posv + 1 : posv;
-    const uint32_t CT = MODE == AD_IDENT ? attn_chunk_tokens(seq) : (uint32_t)AD_TC;
+    const uint32_t CT = MODE == AD_IDENT ? attn_chunk_tokens(seq, p.nd) : (uint32_t)AD_TC;
     uint32_t chunk = blockIdx.y;
     if (MODE != AD_PAGED) {
         const uint32_t nv_hint = (seq + CT - 1) / CT;
@@ -687,7 +693,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     if (prev + nm < nv) return;
     const uint32_t slot = prev + nm - nv;  // nm - 1: the last arrival
     if (!split) {
-        attn_merge<G>(p, kvh * G, nv, false);
+        attn_merge<G, G <= 4 ? 40 : 12>(p, kvh * G, nv, false);
         if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
@@ -713,16 +719,18 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         }
     }
     __syncthreads();
-    attn_merge<1>(p, kvh * G + slot, nv, !s_ok);
+    if (nv <= 32) attn_merge<1, 32>(p, kvh * G + slot, nv, !s_ok);
+    else attn_merge<1, 64>(p, kvh * G + slot, nv, !s_ok);
 }
 
-// partials: zhk_flash_decode_partials_bytes(nh, hd, max_seq) bytes; the
+// partials: zhk_flash_decode_partials_bytes(nh, nkv, hd, max_seq) bytes; the
 // counter words at its end must be zero before the first launch (each
 // launch leaves them zero).
 static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uint32_t max_seq, bool fused,
                        bool ident) {
     AttnP p = p0;
-    p.n_chunks = attn_n_chunks(max_seq);
+    p.nd = attn_nd(nkv, c->cu_count);
+    p.n_chunks = attn_n_chunks(max_seq, p.nd);
     dim3 grid(nkv, p.n_chunks);
     // one workgroup per CU: a grid within the CU count is resident at once
     const bool rev = (uint64_t)nkv * p.n_chunks > (uint64_t)c->cu_count;
@@ -749,8 +757,8 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
     return ZH_OK;
 }
 
-static uint32_t *attn_counters(float *partials, uint32_t nh, uint32_t hd, uint32_t max_seq) {
-    return (uint32_t *)((char *)partials + (uint64_t)nh * attn_n_chunks(max_seq) * (hd + 2) * 4);
+static uint32_t *attn_counters(float *partials, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_seq) {
+    return (uint32_t *)((char *)partials + (uint64_t)nh * attn_n_chunks(max_seq, attn_nd(nkv, 256)) * (hd + 2) * 4);
 }
 
 int zhk_flash_decode(zh_ctx *c, const float *q, const uint16_t *kc, const uint16_t *vc, const uint32_t *pages,
@@ -759,7 +767,7 @@ int zhk_flash_decode(zh_ctx *c, const float *q, const uint16_t *kc, const uint16
     AttnP p = {};
     p.q = q; p.kc = (uint16_t *)kc; p.vc = (uint16_t *)vc; p.pages = pages; p.n_pages = n_pages;
     p.cache_tokens = cache_tokens; p.pos = seq_len; p.scale = scale; p.part = partials;
-    p.counters = attn_counters(partials, nh, hd, max_seq); p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
+    p.counters = attn_counters(partials, nh, nkv, hd, max_seq); p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
     return attn_launch(c, p, nkv, nh / nkv, max_seq, false, false);
 }
 
@@ -787,7 +795,7 @@ int zhk_attn_decode_fused(zh_ctx *c, const float *q, const float *k, const float
     AttnP p = {};
     p.q = q; p.k_new = k; p.v_new = v; p.q_norm = qw; p.k_norm = kw; p.rope_cs = rope_cs;
     p.kc = kc; p.vc = vc; p.pages = pages; p.n_pages = n_pages; p.cache_tokens = cache_tokens; p.pos = pos;
-    p.scale = scale; p.eps = eps; p.part = partials; p.counters = attn_counters(partials, nh, FD_HD, max_seq);
+    p.scale = scale; p.eps = eps; p.part = partials; p.counters = attn_counters(partials, nh, nkv, FD_HD, max_seq);
     p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
     return attn_launch(c, p, nkv, nh / nkv, max_seq, true, ident_pages);
 }
@@ -805,9 +813,9 @@ extern "C" int zh_flash_decode(zh_ctx *c, const zh_buf *q, const zh_buf *kc, con
         !in_range(pages, 0, 4ull * n_pages))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "flash_decode range");
     void *scr;
-    int rc = zh_scratch(c, zhk_flash_decode_partials_bytes(nh, hd, seq_len), &scr);
+    int rc = zh_scratch(c, zhk_flash_decode_partials_bytes(nh, nkv, hd, seq_len), &scr);
     if (rc) return rc;
-    ZH_HIP(c, hipMemsetAsync(attn_counters((float *)scr, nh, hd, seq_len), 0, 4ull * nh, c->stream));
+    ZH_HIP(c, hipMemsetAsync(attn_counters((float *)scr, nh, nkv, hd, seq_len), 0, 4ull * nh, c->stream));
     float scale = attn_scale != 0.f ? attn_scale : 1.0f / sqrtf((float)hd);
     return zhk_flash_decode(c, (const float *)q->ptr, (const uint16_t *)kc->ptr, (const uint16_t *)vc->ptr,
                             (const uint32_t *)pages->ptr, n_pages, cache_tokens, (float *)out->ptr, nullptr, nh, nkv,
@@ -820,45 +828,13 @@ extern "C" int zh_flash_decode(zh_ctx *c, const zh_buf *q, const zh_buf *kc, con
 // lowest index winning ties. routing = [ids u32 x k][weights f32 x k].
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void k_softmax_topk(const float *logits, uint32_t n, uint32_t k, uint32_t *routing) {
-    const uint32_t lane = threadIdx.x;
     float vals[4];
-    bool avail[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        uint32_t e = lane + 64 * i;
-        avail[i] = e < n;
-        vals[i] = avail[i] ? logits[e] : -INFINITY;
+        const uint32_t e = threadIdx.x + 64 * i;
+        vals[i] = e < n ? logits[e] : -INFINITY;
     }
-    __shared__ float sel[16];
-    for (uint32_t j = 0; j < k; j++) {
-        // best remaining (value desc, index asc) in this lane
-        float bv = -INFINITY;
-        uint32_t bi = 0xFFFFFFFFu;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (avail[i] && (bi == 0xFFFFFFFFu || vals[i] > bv)) { bv = vals[i]; bi = lane + 64 * i; }
-        float m = bv;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            float ov = __shfl_xor(m, o, 64);
-            m = (ov > m || m != m) ? ov : m;
-        }
-        uint32_t cand = (bi != 0xFFFFFFFFu && bv == m) ? bi : 0xFFFFFFFFu;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) cand = min(cand, (uint32_t)__shfl_xor((int)cand, o, 64));
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (lane + 64 * i == cand) avail[i] = false;
-        if (lane == 0) {
-            routing[j] = cand;
-            sel[j] = m;
-        }
-    }
-    __syncthreads();
-    float mx = sel[0];
-    float my = lane < k ? expf(sel[lane] - mx) : 0.f;
-    float s = wave_sum(my);
-    if (lane < k) ((float *)routing)[k + lane] = my / s;
+    topk_softmax_wave(vals, n, k, routing);
 }
 
 int zhk_softmax_topk(zh_ctx *c, const float *logits, uint32_t n, uint32_t k, uint32_t *routing) {
