@@ -27,22 +27,26 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_roofline(ctx):
-    """Roofline of the step's dominant kernel (largest share of decode-step
-    time in profiles/decode_step_kernel_trace.md): the ffn_down Q6_K DMMV,
-    timed with HIP events on the library stream over 14 rotating weight
-    copies (578 MB > 256 MB MALL). `traffic` is the counter-measured HBM
-    bytes per launch from profiles/dmmv_q6k_down_4096x12288_pmc.md."""
+def kernel_roofline(eng, L):
+    """Per-kernel bandwidth of every per-layer launch group of the decode step
+    (zinc_amd.roofline_probe: the engine replays its own launches with HIP
+    events on its stream, rotating through the layers) and the roofline of the
+    dominant one (largest launch duration = largest share of step time).
+    `traffic` is the counter-measured HBM bytes per launch of that group from
+    profiles/decode_kernels_pmc.md."""
     from zinc_amd import roofline_probe
-    r = roofline_probe.time_dominant_kernel(ctx)
+    rows, dom = roofline_probe.per_kernel(eng, L)
+    r = rows[dom]
     traffic = None
-    pm = os.path.join(ROOT, "profiles", "dmmv_q6k_down_4096x12288_pmc.md")
+    pm = os.path.join(ROOT, "profiles", "decode_kernels_pmc.md")
     if os.path.exists(pm):
-        m = re.search(r"^traffic_bytes_per_launch: (\d+)", open(pm).read(), re.M)
+        m = re.search(r"^traffic_bytes_per_launch\[%s\]: (\d+)" % dom, open(pm).read(), re.M)
         traffic = int(m.group(1)) if m else None
-    return {"kernel": r["kernel"], "bound": "hbm", "achieved": r["achieved_GBs"], "peak": PEAK_HBM_GBS,
-            "unit": "GB/s", "frac": round(r["achieved_GBs"] / PEAK_HBM_GBS, 4), "traffic": traffic,
-            "bytes_per_launch": r["bytes_per_launch"], "us_per_launch": r["us_per_launch"]}
+    roof = {"kernel": r["kernel"], "bound": "hbm", "achieved": r["achieved_GBs"], "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": r["frac"], "traffic": traffic, "bytes_per_launch": r["bytes_per_launch"],
+            "us_per_launch": r["us_per_launch"], "group": dom}
+    per = {g: {"us": v["us_per_launch"], "GBs": v["achieved_GBs"], "frac": v["frac"]} for g, v in rows.items()}
+    return roof, per
 
 
 def cpu_baseline(cfg, n_tokens=16):
@@ -114,10 +118,12 @@ def main():
     log(f"decode: {tok_s:.1f} tok/s ({ms_per_step:.3f} ms/token wall, {gpu_ms / args.steps:.3f} ms/token GPU), "
         f"{bytes_tok / 1e9:.3f} GB/token -> {bytes_tok * tok_s / 1e9:.0f} GB/s "
         f"({bytes_tok * tok_s / 1e9 / PEAK_HBM_GBS:.1%} of 8 TB/s); distinct tokens {len(set(toks))}")
-    eng.deinit()
 
-    roof = kernel_roofline(ctx)
-    log(f"dominant kernel: {roof['achieved']} GB/s ({roof['frac']:.1%}), {roof['us_per_launch']} us/launch")
+    # per-kernel bandwidth (after the timed region; it changes the activations)
+    roof, per_kernel = kernel_roofline(eng, pos + args.steps)
+    log(f"dominant kernel ({roof['group']}): {roof['achieved']} GB/s ({roof['frac']:.1%}), "
+        f"{roof['us_per_launch']} us/launch; per kernel: {per_kernel}")
+    eng.deinit()
     ctx.close()
 
     cpu = None
@@ -137,6 +143,7 @@ def main():
                    "token_roofline_frac": round(bytes_tok * tok_s / 1e9 / PEAK_HBM_GBS, 4),
                    "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
         "roofline": roof,
+        "per_kernel": per_kernel,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

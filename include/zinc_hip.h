@@ -225,6 +225,21 @@ int zh_engine_read_kv(zh_engine *eng, uint32_t layer, uint32_t which, uint32_t t
  * KV + activations), the numerator of the bandwidth roofline. */
 uint64_t zh_engine_bytes_per_token(zh_engine *eng, uint32_t L);
 
+/* Measurement entries (no counterpart in the reference; the benchmark uses
+ * them for per-kernel bandwidth). A launch group is one per-layer stage of
+ * the decode step: */
+#define ZH_GROUP_QKV 1u      /* attn_norm + Q/K/V projections (one launch when fused) */
+#define ZH_GROUP_ATTN 2u     /* q/k norm + RoPE + KV write + split-K attention + merge */
+#define ZH_GROUP_O 4u        /* O projection + residual */
+#define ZH_GROUP_FFN_IN 8u   /* ffn_norm + gate/up + SwiGLU (MoE: + router, top-k) */
+#define ZH_GROUP_FFN_OUT 16u /* down projection + residual (MoE: + weighted expert sum) */
+/* Average duration of one launch of `group`, replayed with the engine's own
+ * arguments and state over `iters` launches rotating through the layers, by
+ * HIP events on the engine's stream. Leaves the activations changed. */
+int zh_engine_time_kernel(zh_engine *eng, uint32_t group, uint32_t iters, float *us_per_launch);
+/* Algorithmic bytes of one launch of `group` at context length L. */
+uint64_t zh_engine_group_bytes(zh_engine *eng, uint32_t group, uint32_t L);
+
 #ifdef __cplusplus
 }
 #endif

@@ -327,7 +327,13 @@ static int record_collect(zh_engine *e) {
     return zhk_argmax(c, e->logits, m.vocab, e->st + ST_TOKEN_OUT, e->am_part, e->ring, e->st + ST_GEN);
 }
 
-static int record_step(zh_engine *e, bool collect) {
+// Launch groups of one layer (the unit zh_engine_time_kernel replays).
+enum : uint32_t { SK_QKV = 1, SK_ATTN = 2, SK_O = 4, SK_FFN_IN = 8, SK_FFN_OUT = 16, SK_ALL = 31 };
+
+// Records the decode step: embedding, layers [l0, l1) (only the launch
+// groups in `mask`), then (whole steps only) the output head and the step
+// advance.
+static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 = ~0u, uint32_t mask = SK_ALL) {
     zh_ctx *c = e->ctx;
     const zh_model_config &m = e->c;
     const uint32_t H = m.hidden, hd = m.head_dim, qd = m.n_heads * hd, kvd = m.n_kv_heads * hd;
@@ -336,8 +342,9 @@ static int record_step(zh_engine *e, bool collect) {
     auto Wf = [&](const Tensor &t) { return (const float *)(A + t.off); };
     zh_pos_src pos{0, e->st + ST_POS}, seq{1, e->st + ST_POS};
     const float scale = 1.0f / sqrtf((float)hd);
+    const bool whole = mask == SK_ALL && l0 == 0 && l1 >= m.n_layers;
     // embedToken (forward.zig:4255-4290), on the device.
-    ERC(zhk_dequant_rows(c, m.type_embd, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
+    if (whole) ERC(zhk_dequant_rows(c, m.type_embd, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
     const bool lpb = !getenv("ZH_NO_LPB");
     const bool lpb_attn = lpb && zhk_lpb_supported(m.type_attn, H) && zhk_lpb_supported(m.type_attn, qd) &&
                           qd % 2 == 0 && kvd % 2 == 0;
@@ -349,9 +356,10 @@ static int record_step(zh_engine *e, bool collect) {
     const bool lds_moe = lds && m.n_experts && m.n_experts <= 256 && m.n_experts_used <= 8 &&
                          zhk_dmmv_lds_supported(m.type_router, H) && zhk_dmmv_lds_supported(m.type_ffn_down, m.expert_ffn) &&
                          m.expert_ffn % 32 == 0;
-    for (uint32_t l = 0; l < m.n_layers; l++) {
+    for (uint32_t l = l0; l < m.n_layers && l < l1; l++) {
         const Layer &y = e->L[l];
-        if (lpb_attn) {
+        if (!(mask & SK_QKV)) {
+        } else if (lpb_attn) {
             // attn_norm fused into the Q/K/V mat-vec (every workgroup normalises x)
             const uint8_t *ws[3] = {W(y.wq), W(y.wk), W(y.wv)};
             float *ys[3] = {e->q, e->k, e->v};
@@ -365,10 +373,12 @@ static int record_step(zh_engine *e, bool collect) {
             const uint32_t ms[3] = {qd, kvd, kvd};
             ERC(zhk_dmmv_multi(c, m.type_attn, 3, ws, ys, ms, e->xq_h, H));
         }
-        ERC(zhk_attn_decode_fused(c, e->q, e->k, e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc,
+        if (mask & SK_ATTN)
+            ERC(zhk_attn_decode_fused(c, e->q, e->k, e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc,
                                   e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads, m.n_kv_heads, pos,
                                   m.max_ctx, scale, m.eps, e->fd_part, true));  // pages[i] = i (k_fill_pages)
-        if (lpb_attn) {
+        if (!(mask & SK_O)) {
+        } else if (lpb_attn) {
             // the merge kernel already emitted the attention output as XQ
             const uint8_t *wo = W(y.wo);
             float *yo = e->hidden;
@@ -387,13 +397,15 @@ static int record_step(zh_engine *e, bool collect) {
             // the group's last batch), so the down projection copies XQ instead of
             // every workgroup re-quantising the f32 vector
             const bool swiglu_xq = m.ffn % 32 == 0 && H / 256 <= 32 && !getenv("ZH_NO_TILE");
-            ERC(zhk_dmmv_lpb(c, ZH_Q4_K, 1, 1, &wg, W(y.up), &ys, &mf, e->hidden, Wf(y.ffn_norm), m.eps, nullptr, H,
-                             0, nullptr, swiglu_xq ? e->xq_f : nullptr, swiglu_xq ? e->grp_cnt : nullptr));
+            if (mask & SK_FFN_IN)
+                ERC(zhk_dmmv_lpb(c, ZH_Q4_K, 1, 1, &wg, W(y.up), &ys, &mf, e->hidden, Wf(y.ffn_norm), m.eps, nullptr,
+                                 H, 0, nullptr, swiglu_xq ? e->xq_f : nullptr, swiglu_xq ? e->grp_cnt : nullptr));
             const uint8_t *wd = W(y.down);
             float *yd = e->hidden;
             const uint32_t mh = H;
-            ERC(zhk_dmmv_lpb(c, m.type_ffn_down, 0, 1, &wd, nullptr, &yd, &mh, swiglu_xq ? nullptr : e->s, nullptr,
-                             0.f, nullptr, m.ffn, 1, swiglu_xq ? e->xq_f : nullptr));
+            if (mask & SK_FFN_OUT)
+                ERC(zhk_dmmv_lpb(c, m.type_ffn_down, 0, 1, &wd, nullptr, &yd, &mh, swiglu_xq ? nullptr : e->s,
+                                 nullptr, 0.f, nullptr, m.ffn, 1, swiglu_xq ? e->xq_f : nullptr));
             continue;
         }
         if (lds_moe) {
@@ -404,15 +416,20 @@ static int record_step(zh_engine *e, bool collect) {
             const uint32_t F = m.expert_ffn, k = m.n_experts_used, E = m.n_experts;
             const uint8_t *wr = W(y.router);
             float *rl = e->rl;
-            ERC(zhk_dmmv_lds_plain(c, m.type_router, 1, &wr, &rl, &E, e->hidden, Wf(y.ffn_norm), m.eps, H, 0, e->xq_h,
-                                   k, e->routing, e->router_cnt));
-            ERC(zhk_dmmv_moe(c, m.type_ffn_gate_up, W(y.egate), zh_tensor_bytes(m.type_ffn_gate_up, F, H), e->routing,
-                             e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
-            ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
-            ERC(zhk_dmmv_lds_down_acc(c, m.type_ffn_down, W(y.edown), zh_tensor_bytes(m.type_ffn_down, H, F),
-                                      e->routing, k, m.n_experts, e->xq_f, e->hidden, H, F));
+            if (mask & SK_FFN_IN) {
+                ERC(zhk_dmmv_lds_plain(c, m.type_router, 1, &wr, &rl, &E, e->hidden, Wf(y.ffn_norm), m.eps, H, 0,
+                                       e->xq_h, k, e->routing, e->router_cnt));
+                ERC(zhk_dmmv_moe(c, m.type_ffn_gate_up, W(y.egate), zh_tensor_bytes(m.type_ffn_gate_up, F, H),
+                                 e->routing, e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
+            }
+            if (mask & SK_FFN_OUT) {
+                ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
+                ERC(zhk_dmmv_lds_down_acc(c, m.type_ffn_down, W(y.edown), zh_tensor_bytes(m.type_ffn_down, H, F),
+                                          e->routing, k, m.n_experts, e->xq_f, e->hidden, H, F));
+            }
             continue;
         }
+        if (!(mask & SK_FFN_IN) || !(mask & SK_FFN_OUT)) continue;  // not split: timed as whole steps only
         ERC(zhk_rms_norm(c, e->hidden, Wf(y.ffn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
         if (m.n_experts == 0) {
             ERC(zhk_dmmv_gate_up(c, m.type_ffn_gate_up, W(y.gate), W(y.up), e->xq_h, e->s, m.ffn, H));
@@ -430,10 +447,40 @@ static int record_step(zh_engine *e, bool collect) {
             ERC(zhk_moe_weighted_acc(c, e->hidden, e->edown_out, e->routing, H, k, H));
         }
     }
+    if (!whole) return ZH_OK;
     if (collect) ERC(record_collect(e));
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, c->stream, e->st, (const uint32_t *)e->prompt);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
+}
+
+// Measurement entry (no counterpart in the reference; the benchmark uses it
+// for per-kernel bandwidth): the average duration of one launch group --
+// exactly the launches, arguments and state of the decode step -- over
+// `iters` launches rotating through the layers (so weights stream from HBM),
+// timed with HIP events on the engine's stream. Activations are left changed.
+extern "C" int zh_engine_time_kernel(zh_engine *e, uint32_t group, uint32_t iters, float *us_per_launch) {
+    if (!e || !us_per_launch || group == 0 || (group & ~(uint32_t)SK_ALL) || iters == 0)
+        return e ? zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "time_kernel group %u", group) : ZH_ERR_INVALID_ARGUMENT;
+    zh_ctx *c = e->ctx;
+    const uint32_t L = e->c.n_layers;
+    for (uint32_t l = 0; l < L; l++) ERC(record_step(e, false, l, l + 1, group));
+    hipEvent_t ev[2];
+    EHIP(e, hipEventCreate(&ev[0]));
+    if (hipEventCreate(&ev[1]) != hipSuccess) {
+        hipEventDestroy(ev[0]);
+        return zh_set_err(c, ZH_ERR_HIP, "event");
+    }
+    int rc = hipEventRecord(ev[0], c->stream) == hipSuccess ? ZH_OK : ZH_ERR_HIP;
+    for (uint32_t i = 0; rc == ZH_OK && i < iters; i++) rc = record_step(e, false, i % L, i % L + 1, group);
+    float ms = 0.f;
+    if (rc == ZH_OK && (hipEventRecord(ev[1], c->stream) != hipSuccess || hipEventSynchronize(ev[1]) != hipSuccess ||
+                        hipEventElapsedTime(&ms, ev[0], ev[1]) != hipSuccess))
+        rc = zh_set_err(c, ZH_ERR_HIP, "time_kernel events");
+    hipEventDestroy(ev[0]);
+    hipEventDestroy(ev[1]);
+    if (rc == ZH_OK) *us_per_launch = ms * 1e3f / (float)iters;
+    return rc;
 }
 
 static int ensure_graphs(zh_engine *e) {
@@ -666,4 +713,32 @@ extern "C" uint64_t zh_engine_bytes_per_token(zh_engine *e, uint32_t Lctx) {
         b += 2ull * c.n_kv_heads * c.head_dim * 2ull * Lctx;  // fp16 K and V
     }
     return b;
+}
+
+// Algorithmic bytes of one launch group of layer 0 at context length Lctx:
+// the weights it reads, its activation inputs and outputs, the KV rows the
+// attention reads and writes (internal scratch traffic such as attention
+// partials is not counted).
+extern "C" uint64_t zh_engine_group_bytes(zh_engine *e, uint32_t group, uint32_t Lctx) {
+    if (!e || e->L.empty()) return 0;
+    const zh_model_config &c = e->c;
+    const Layer &y = e->L[0];
+    const uint64_t H = c.hidden, hd = c.head_dim, qd = (uint64_t)c.n_heads * hd, kvd = (uint64_t)c.n_kv_heads * hd;
+    const uint64_t F = c.n_experts ? c.expert_ffn : c.ffn, k = c.n_experts ? c.n_experts_used : 1;
+    auto xqb = [](uint64_t n) { return n / 32 * 108; };
+    switch (group) {
+    case SK_QKV: return y.wq.bytes + y.wk.bytes + y.wv.bytes + 2 * H * 4 + (qd + 2 * kvd) * 4;
+    case SK_ATTN:
+        return 2 * kvd * 2 * Lctx + (qd + 2 * kvd) * 4 + 2 * hd * 4 + hd * 4 + 2 * kvd * 2 + qd * 4 + xqb(qd);
+    case SK_O: return y.wo.bytes + xqb(qd) + 2 * H * 4;
+    case SK_FFN_IN:
+        if (c.n_experts == 0) return y.gate.bytes + y.up.bytes + 2 * H * 4 + F * 4 + xqb(F);
+        return y.router.bytes + 2 * k * zh_tensor_bytes(c.type_ffn_gate_up, (uint32_t)F, (uint32_t)H) + 2 * H * 4 +
+               xqb(H) + (uint64_t)c.n_experts * 4 + 8 * k + k * F * 4;
+    case SK_FFN_OUT:
+        if (c.n_experts == 0) return y.down.bytes + xqb(F) + 2 * H * 4;
+        return k * zh_tensor_bytes(c.type_ffn_down, (uint32_t)H, (uint32_t)F) + k * F * 4 + 2 * k * xqb(F) + 8 * k +
+               2 * H * 4;
+    default: return 0;
+    }
 }

@@ -104,3 +104,16 @@ class InferenceEngine:
 
     def bytes_per_token(self, L):
         return lib().zh_engine_bytes_per_token(self.h, L)
+
+    # per-layer launch groups of the decode step (zinc_hip.h ZH_GROUP_*)
+    GROUPS = {"qkv": 1, "attn": 2, "o": 4, "ffn_in": 8, "ffn_out": 16}
+
+    def time_kernel(self, group, iters=200):
+        """Average us per launch of one launch group, replayed with the
+        engine's own arguments rotating through the layers."""
+        us = C.c_float()
+        self.ctx.check(lib().zh_engine_time_kernel(self.h, self.GROUPS[group], iters, C.byref(us)))
+        return us.value
+
+    def group_bytes(self, group, L):
+        return lib().zh_engine_group_bytes(self.h, self.GROUPS[group], L)

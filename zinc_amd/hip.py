@@ -94,6 +94,8 @@ SIGNATURES = {
     "zh_engine_tensor": (_i32, [_P, _u64, C.POINTER(_P), C.POINTER(_u64), C.POINTER(_u64)]),
     "zh_engine_read_kv": (_i32, [_P, _u32, _u32, _u32, _u32, _P]),
     "zh_engine_bytes_per_token": (_u64, [_P, _u32]),
+    "zh_engine_time_kernel": (_i32, [_P, _u32, _u32, _P]),
+    "zh_engine_group_bytes": (_u64, [_P, _u32, _u32]),
 }
 
 _lib = None

@@ -1,93 +1,83 @@
-"""Roofline measurement of the decode step's dominant kernel, and the launch
-sequence its hardware-counter profile is taken from.
+"""Per-kernel roofline of the 8B-shape decode step, and the launch sequence
+its hardware-counter profile is taken from.
 
-The dominant kernel of the 8B-shape decode step (largest share of step time
-in the kernel-trace profile) is the ffn_down projection: Q6_K 4096 x 12288
-with the f32 SwiGLU output staged in every workgroup and the residual added
-in place (acc_mode 1), i.e. `dispatchDmmvAcc` at forward.zig:7420 with
-dmmv_q6k.comp. Its algorithmic bytes per launch are the weight blocks, the
-activation and the read-modify-write of y.
+Every per-layer launch group of the decode step (Q/K/V with attn_norm fused,
+attention, O projection, gate/up + SwiGLU with ffn_norm fused, down
+projection) is replayed by the engine itself (zh_engine_time_kernel) with its
+own arguments and state, rotating through the 36 layers so the weights stream
+from HBM (4.9 GB of weights > 256 MB MALL). Each group is one kernel in the
+dense model; achieved GB/s = the group's algorithmic bytes per launch
+(zh_engine_group_bytes: weights, activation in/out, KV rows) / the average
+launch duration by HIP events on the engine's stream. The dominant kernel is
+the group with the largest duration (each runs once per layer, so also the
+largest share of step time).
 
-    python -m zinc_amd.roofline_probe            # timing only
+    python -m zinc_amd.roofline_probe            # per-kernel table (JSON)
     rocprofv3 --pmc FETCH_SIZE -- python3 -m zinc_amd.roofline_probe --pmc
 
 With --pmc the script launches, in order: a streaming read of CAL_BYTES
-(cold, known size), a write of CAL_BYTES (known size), then PMC_LAUNCHES
-launches of the down projection; the counter of each launch is read from
-the profiler output and the first two give the bytes-per-counter factors.
+(known size), a write of CAL_BYTES (known size), then for each group in
+GROUP_ORDER one warm pass over the layers and PMC_ITERS timed launches;
+zinc_amd.pmc_summary turns the counters into bytes per launch.
 """
 import argparse
 import json
 import sys
 
 from . import hip
+from .engine import DENSE_8B, InferenceEngine
 
-M_DOWN, K_DOWN = 4096, 12288
-N_COPIES = 14            # 14 x 41.3 MB = 578 MB of distinct weights > 256 MB MALL
+PEAK = 8000.0
 CAL_BYTES = 1 << 30      # calibration read / write size
-PMC_LAUNCHES = 20
+PREFILL = 4096           # KV context of the bench (config 3)
+GROUP_ORDER = ["qkv", "attn", "o", "ffn_in", "ffn_out"]
+PMC_ITERS = 36
+KERNELS = {  # the dense 8B step's kernel per group
+    "qkv": "k_dmmv_q4k_tile<16, 0> (attn_norm + Q/K/V, Q4_K 6144x4096)",
+    "attn": "k_attn_decode<4, true, 2> (q/k norm + RoPE + KV write + split-K attention + merge)",
+    "o": "k_dmmv_q4k_tile<16, 0> (O projection + residual, Q4_K 4096x4096, XQ input)",
+    "ffn_in": "k_dmmv_q4k_tile<16, 1> (ffn_norm + gate/up + SwiGLU, 2 x Q4_K 12288x4096, XQ output)",
+    "ffn_out": "k_dmmv_q6k_tile<128, 5> (ffn_down + residual, Q6_K 4096x12288, XQ input)",
+}
 
 
-def down_bytes():
-    wb = hip.tensor_bytes(hip.Q6_K, M_DOWN, K_DOWN)
-    return wb, wb + K_DOWN * 4 + 2 * M_DOWN * 4
+def probe_engine(ctx, max_ctx):
+    cfg = dict(DENSE_8B)
+    cfg["max_ctx"] = max_ctx
+    eng = InferenceEngine(ctx, cfg)
+    eng.prefill_kv_random(PREFILL, 7)
+    eng.generate([17, 18], 2, start_pos=PREFILL)  # a valid decode state at context PREFILL + 2
+    return eng
 
 
-class DownProjection:
-    """N_COPIES seeded weight copies, the activation and the output."""
-
-    def __init__(self, ctx):
-        self.ctx = ctx
-        self.wb, self.alg_bytes = down_bytes()
-        self.W = ctx.alloc(self.wb * N_COPIES)
-        for i in range(N_COPIES):
-            ctx.synth_tensor(self.W, i * self.wb, hip.Q6_K | 0x100, M_DOWN, K_DOWN, 4242, 300 + i)
-        self.x = ctx.alloc(K_DOWN * 4)
-        ctx.synth_vector(self.x, 0, 0, K_DOWN, 1.0, 4242, 299)
-        self.y = ctx.alloc(M_DOWN * 4)
-        ctx.synth_vector(self.y, 0, 0, M_DOWN, 1.0, 4242, 298)
-
-    def launch(self, i):
-        c = i % N_COPIES
-        self.ctx.dmmv(hip.Q6_K, self.W, c * self.wb, self.x, 0, self.y, 0, M_DOWN, K_DOWN, 1)
-
-    def close(self):
-        for b in (self.W, self.x, self.y):
-            self.ctx.free(b)
-
-
-def time_dominant_kernel(ctx, iters=200):
-    """Average launch duration (HIP events on the library stream) and the
-    achieved algorithmic GB/s of the down projection."""
-    d = DownProjection(ctx)
-    for i in range(2 * N_COPIES):
-        d.launch(i)
-    ctx.sync()
-    ctx.record(0)
-    for i in range(iters):
-        d.launch(i)
-    ctx.record(1)
-    ms = ctx.elapsed_ms(0, 1)
-    d.close()
-    us = ms * 1e3 / iters
-    return {"kernel": "k_dmmv_q6k_tile<128> (ffn_down, Q6_K 4096x12288, f32 x staged per workgroup, y += W x)",
-            "us_per_launch": round(us, 3), "bytes_per_launch": d.alg_bytes,
-            "achieved_GBs": round(d.alg_bytes / (us * 1e-6) / 1e9, 1)}
+def per_kernel(eng, L, iters=108):
+    """{group: us, bytes, GB/s, frac} for every launch group, and the dominant one."""
+    rows = {}
+    for g in GROUP_ORDER:
+        us = eng.time_kernel(g, iters)
+        b = eng.group_bytes(g, L)
+        gbs = b / (us * 1e-6) / 1e9
+        rows[g] = {"kernel": KERNELS[g], "us_per_launch": round(us, 3), "bytes_per_launch": b,
+                   "achieved_GBs": round(gbs, 1), "frac": round(gbs / PEAK, 4)}
+    dom = max(rows, key=lambda g: rows[g]["us_per_launch"])
+    return rows, dom
 
 
 def pmc_sequence(ctx):
-    """Calibration read, calibration write, then PMC_LAUNCHES down launches."""
+    """Calibration read, calibration write, then every group's launches."""
     cal = ctx.alloc(CAL_BYTES)
     ctx.synth_vector(cal, 0, 1, CAL_BYTES // 2, 1.0, 7, 7)  # warm the pages (not used)
-    d = DownProjection(ctx)
+    eng = probe_engine(ctx, PREFILL + 64)
     ctx.sync()
     ctx.stream_read_probe(cal, CAL_BYTES, 1)             # k_stream_read: reads CAL_BYTES (twice: warm + timed)
     ctx.synth_vector(cal, 0, 0, CAL_BYTES // 4, 1.0, 8, 8)  # k_synth_vector: writes CAL_BYTES
-    for i in range(PMC_LAUNCHES):
-        d.launch(i)
+    for g in GROUP_ORDER:
+        eng.time_kernel(g, PMC_ITERS)
     ctx.sync()
-    d.close()
+    b = {g: eng.group_bytes(g, PREFILL + 2) for g in GROUP_ORDER}
+    eng.deinit()
     ctx.free(cal)
+    return b
 
 
 def main():
@@ -96,11 +86,14 @@ def main():
     a = ap.parse_args()
     ctx = hip.Context(0)
     if a.pmc:
-        pmc_sequence(ctx)
-        print(json.dumps({"cal_bytes": CAL_BYTES, "down_launches": PMC_LAUNCHES,
-                          "alg_bytes": down_bytes()[1]}), flush=True)
+        b = pmc_sequence(ctx)
+        print(json.dumps({"cal_bytes": CAL_BYTES, "groups": GROUP_ORDER, "iters": PMC_ITERS,
+                          "layers": DENSE_8B["n_layers"], "alg_bytes": b}), flush=True)
     else:
-        print(json.dumps(time_dominant_kernel(ctx)), flush=True)
+        eng = probe_engine(ctx, PREFILL + 64)
+        rows, dom = per_kernel(eng, PREFILL + 2)
+        eng.deinit()
+        print(json.dumps({"dominant": dom, "kernels": rows}), flush=True)
     ctx.close()
     return 0
 
