@@ -5,7 +5,7 @@ decode over a 32768-position fp16 KV cache.
     python -m zinc_amd.prefill_bench [--prefill 512] [--long-ctx 32768] [--steps 128]
 
 Prints one JSON line. GEMM FLOPs per prefill = 2 * N * sum(M * K) over the
-36 layers' Q, K, V, O, gate, up, down projections (SURVEY config 5: 7.11 TFLOP
+36 layers' Q, K, V, O, gate, up, down projections (7.11 TFLOP
 for N = 512); attention FLOPs are not counted in that figure.
 """
 import argparse
