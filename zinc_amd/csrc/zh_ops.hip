@@ -466,7 +466,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         qhi[g][0] = c.x; qhi[g][1] = c.y; qhi[g][2] = c.z; qhi[g][3] = c.w;
         qhi[g][4] = d.x; qhi[g][5] = d.y; qhi[g][6] = d.z; qhi[g][7] = d.w;
     }
-    float klo[8], khi[8], vn0 = 0.f, vn1 = 0.f;
+    float klo[8], khi[8], vn0 = 0.f, vn1 = 0.f, vn8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (FUSED) {
         const float *kp = p.k_new + (size_t)kvh * FD_HD;
         const f32x4 a = *(const f32x4 *)(kp + sub * 8), b = *(const f32x4 *)(kp + sub * 8 + 4);
@@ -476,6 +476,10 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         const float2 vv = *(const float2 *)(p.v_new + (size_t)kvh * FD_HD + 2 * lane);
         vn0 = vv.x;
         vn1 = vv.y;
+        const f32x4 va = *(const f32x4 *)(p.v_new + (size_t)kvh * FD_HD + 8 * (lane & 15));
+        const f32x4 vb = *(const f32x4 *)(p.v_new + (size_t)kvh * FD_HD + 8 * (lane & 15) + 4);
+        vn8[0] = va.x; vn8[1] = va.y; vn8[2] = va.z; vn8[3] = va.w;
+        vn8[4] = vb.x; vn8[5] = vb.y; vn8[6] = vb.z; vn8[7] = vb.w;
     }
     float co[8], sn[8], qwl[8], qwh[8], kwl[8], kwh[8];
     if (FUSED) {
@@ -522,15 +526,20 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         kr[j][1] = *(const u32x4 *)(kp + 64 + sub * 8);
     }
     asm volatile("" ::: "memory");
-    uint32_t vr[AD_TW];
+    // V rows: lane = (vrow = lane / 16, vcol = lane % 16) holds dims
+    // 8 vcol .. 8 vcol + 7 of the wave's tokens vrow, vrow + 4, .., 36 + vrow:
+    // 16-byte loads, one instruction covering 4 tokens x 256 B (4 tokens from
+    // a 4-aligned offset never straddle a 16-token page)
+    const uint32_t vrow = lane >> 4, vcol = lane & 15;
+    u32x4 vr[AD_TW / 4];
 #pragma unroll
-    for (int i = 0; i < AD_TW; i++) vr[i] = *(const uint32_t *)(kv_row(vh, pa, pb, pc, o16 + i) + 2 * lane);
+    for (int k = 0; k < AD_TW / 4; k++) vr[k] = *(const u32x4 *)(kv_row(vh, pa, pb, pc, o16 + 4 * k + vrow) + 8 * vcol);
     asm volatile("" ::: "memory");
 
     // ---- q (and new k) preparation
     bool owner = false;  // this wave's tokens include the new position (uniform per wave)
     uint32_t inew = 0, vnew = 0;
-    u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0};
+    u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0}, vnew4 = {0, 0, 0, 0};
     if (FUSED) {
 #pragma unroll
         for (int g = 0; g < G; g++) norm_rope16(qlo[g], qhi[g], qwl, qwh, co, sn, p.eps);
@@ -544,6 +553,8 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
             n1 = u32x4{pack_h2(khi[0], khi[1]), pack_h2(khi[2], khi[3]), pack_h2(khi[4], khi[5]),
                        pack_h2(khi[6], khi[7])};
             vnew = pack_h2(vn0, vn1);
+            vnew4 = u32x4{pack_h2(vn8[0], vn8[1]), pack_h2(vn8[2], vn8[3]), pack_h2(vn8[4], vn8[5]),
+                          pack_h2(vn8[6], vn8[7])};
             inew = posv - tw0;
             // logicalTokenToPhysicalToken for the new position, from the page
             // entries loaded above (the position lies in page pgb + 0..2); the
@@ -589,10 +600,10 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         }
     }
     TRACE_OPS(2);
-    // ---- per-wave softmax over its 32 tokens, P*V with lane = 2 output dims
+    // ---- per-wave softmax over its tokens; P*V with lane = (token row, 8 dims)
     __shared__ float ps[AD_W][G][AD_TW];
     __shared__ float wm[AD_W][G], wl[AD_W][G];
-    __shared__ float wo[AD_W][G][FD_HD];
+    __shared__ float wo[AD_W][4][G][FD_HD];  // per wave and token row
     float mx[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -614,30 +625,35 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     }
     __syncthreads();
     TRACE_OPS(8);
-    float acc[G][2];
+    float acc[G][8];
 #pragma unroll
-    for (int g = 0; g < G; g++) acc[g][0] = acc[g][1] = 0.f;
+    for (int g = 0; g < G; g++)
 #pragma unroll
-    for (int i4 = 0; i4 < AD_TW; i4 += 4) {
-        f32x4 pr[G];
+        for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
 #pragma unroll
-        for (int g = 0; g < G; g++) pr[g] = *(const f32x4 *)&ps[wave][g][i4];
+    for (int k = 0; k < AD_TW / 4; k++) {
+        const uint32_t i = 4 * k + vrow;
+        u32x4 v = owner && i == inew ? vnew4 : vr[k];
+        if (i >= nt) v = u32x4{0, 0, 0, 0};  // rows past the end may hold anything
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+        float vf[8];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int i = i4 + u;
-            uint32_t vv = owner && (uint32_t)i == inew ? vnew : vr[i];
-            vv = (uint32_t)i < nt ? vv : 0u;  // rows past the end may hold anything
-            const float v0 = h2f(vv), v1 = h2f(vv >> 16);
+        for (int e = 0; e < 4; e++) {
+            vf[2 * e] = h2f(vw[e]);
+            vf[2 * e + 1] = h2f(vw[e] >> 16);
+        }
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float q = pr[g][u];
-                acc[g][0] = fmaf(q, v0, acc[g][0]);
-                acc[g][1] = fmaf(q, v1, acc[g][1]);
-            }
+        for (int g = 0; g < G; g++) {
+            const float q = ps[wave][g][i];
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[g][e] = fmaf(q, vf[e], acc[g][e]);
         }
     }
 #pragma unroll
-    for (int g = 0; g < G; g++) *(float2 *)&wo[wave][g][2 * lane] = make_float2(acc[g][0], acc[g][1]);
+    for (int g = 0; g < G; g++) {
+        *(f32x4 *)&wo[wave][vrow][g][8 * vcol] = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+        *(f32x4 *)&wo[wave][vrow][g][8 * vcol + 4] = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+    }
     (void)mx;
     __syncthreads();
     TRACE_OPS(9);
@@ -665,7 +681,8 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         const uint32_t g = o / FD_HD, d = o % FD_HD;
         float O = 0.f;
 #pragma unroll
-        for (int w = 0; w < AD_W; w++) O = fmaf(wo[w][g][d], cf[w][g], O);
+        for (int w = 0; w < AD_W; w++)
+            O = fmaf((wo[w][0][g][d] + wo[w][1][g][d]) + (wo[w][2][g][d] + wo[w][3][g][d]), cf[w][g], O);
         float *pp = p.part + ((size_t)(kvh * G + g) * p.n_chunks + chunk) * (FD_HD + 2);
         st_dev(pp + d, O);
         if (d == 0) { st_dev(pp + FD_HD, cM[g]); st_dev(pp + FD_HD + 1, cL[g]); }
