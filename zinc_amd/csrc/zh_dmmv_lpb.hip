@@ -667,8 +667,9 @@ ZH_DEV void tile_fetch(const LpbP &p, uint32_t bi, uint32_t row_bytes, u32x4 (&s
     }
 }
 
+// 64-lane teams (K > 8192) stage an XQ image of up to 56 KB: two workgroups per CU
 template <int TL, int MODE>
-__global__ __launch_bounds__(LPB_T, 3) void k_dmmv_q4k_tile(LpbP p) {
+__global__ __launch_bounds__(LPB_T, TL >= 64 ? 2 : 3) void k_dmmv_q4k_tile(LpbP p) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     __shared__ float red[4];
     __shared__ float gate_res[LPB_T / TL];
@@ -975,7 +976,7 @@ static int try_q4k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t 
         capm = e ? atoi(e) : 3;
     }
     const uint32_t nb = p.K / 256;
-    if (off || nb > 32) return -1;
+    if (off || nb > 64) return -1;
     const uint32_t TL = pow2ceil(nb < 4 ? 4 : nb);
     const uint32_t nm = p.mode == LPB_GATE_UP ? 2 : 1;
     const uint32_t rpb = LPB_T / TL / nm;
@@ -997,7 +998,8 @@ static int try_q4k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t 
     case 4: return launch_q4k_tile<4>(c, p, wgs, lds);
     case 8: return launch_q4k_tile<8>(c, p, wgs, lds);
     case 16: return launch_q4k_tile<16>(c, p, wgs, lds);
-    default: return launch_q4k_tile<32>(c, p, wgs, lds);
+    case 32: return launch_q4k_tile<32>(c, p, wgs, lds);
+    default: return launch_q4k_tile<64>(c, p, wgs, lds);
     }
 }
 
