@@ -629,9 +629,12 @@ extern "C" int zh_engine_prefill(zh_engine *e, const uint32_t *tokens, uint32_t 
         for (uint32_t l = 0; l < m.n_layers; l++) {
             const Layer &y = e->L[l];
             ERC(zhk_rms_norm_rows_f16(c, e->pf.hid, Wf(y.attn_norm), e->pf.xh, H, nt, m.eps));
-            ERC(zhk_gemm(c, m.type_attn, W(y.wq), e->pf.xh, H, e->pf.q, qd, qd, H, nt, 0));
-            ERC(zhk_gemm(c, m.type_attn, W(y.wk), e->pf.xh, H, e->pf.k, kvd, kvd, H, nt, 0));
-            ERC(zhk_gemm(c, m.type_attn, W(y.wv), e->pf.xh, H, e->pf.v, kvd, kvd, H, nt, 0));
+            {  // Q, K and V in one launch
+                const uint8_t *ws[3] = {W(y.wq), W(y.wk), W(y.wv)};
+                float *ys[3] = {e->pf.q, e->pf.k, e->pf.v};
+                const uint32_t ld[3] = {qd, kvd, kvd}, ms[3] = {qd, kvd, kvd};
+                ERC(zhk_gemm_multi(c, m.type_attn, 3, ws, e->pf.xh, H, ys, ld, ms, H, nt, 0));
+            }
             ERC(zhk_qk_norm_rope_kv(c, e->pf.q, Wf(y.q_norm), e->pf.k, Wf(y.k_norm), e->pf.v, e->inv_freq, y.kc, y.vc,
                                     e->pages, e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd,
                                     zh_pos_src{pos0, nullptr}, m.eps, nt));
@@ -639,8 +642,12 @@ extern "C" int zh_engine_prefill(zh_engine *e, const uint32_t *tokens, uint32_t 
                                  pos0, nt, scale, e->pf.att));
             ERC(zhk_gemm(c, m.type_attn, W(y.wo), e->pf.att, qd, e->pf.hid, H, H, qd, nt, 1));
             ERC(zhk_rms_norm_rows_f16(c, e->pf.hid, Wf(y.ffn_norm), e->pf.xh, H, nt, m.eps));
-            ERC(zhk_gemm(c, m.type_ffn_gate_up, W(y.gate), e->pf.xh, H, e->pf.g, F, F, H, nt, 0));
-            ERC(zhk_gemm(c, m.type_ffn_gate_up, W(y.up), e->pf.xh, H, e->pf.u, F, F, H, nt, 0));
+            {  // gate and up in one launch
+                const uint8_t *ws[2] = {W(y.gate), W(y.up)};
+                float *ys[2] = {e->pf.g, e->pf.u};
+                const uint32_t ld[2] = {F, F}, ms[2] = {F, F};
+                ERC(zhk_gemm_multi(c, m.type_ffn_gate_up, 2, ws, e->pf.xh, H, ys, ld, ms, H, nt, 0));
+            }
             ERC(zhk_swiglu_rows_f16(c, e->pf.g, e->pf.u, e->pf.s, e->pf.s_unscale, F, nt));
             ERC(zhk_gemm(c, m.type_ffn_down, W(y.down), e->pf.s, F, e->pf.hid, H, H, F, nt, 1, e->pf.s_unscale));
         }

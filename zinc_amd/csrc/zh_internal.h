@@ -118,6 +118,10 @@ int zhk_attn_decode_fused(zh_ctx *ctx, const float *q, const float *k, const flo
 // Prefill (zh_prefill.hip)
 int zhk_gemm(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, const _Float16 *X, uint32_t ldx, float *Y, uint32_t ldy,
              uint32_t M, uint32_t K, uint32_t N, uint32_t acc, const float *x_unscale = nullptr);
+// Up to three stacked matrices sharing X (segment rows multiples of 64).
+int zhk_gemm_multi(zh_ctx *ctx, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, const _Float16 *X,
+                   uint32_t ldx, float *const *Y, const uint32_t *ldy, const uint32_t *M, uint32_t K, uint32_t N,
+                   uint32_t acc, const float *x_unscale = nullptr);
 int zhk_rms_norm_rows_f16(zh_ctx *ctx, const float *x, const float *w, _Float16 *out, uint32_t n, uint32_t rows,
                           float eps);
 int zhk_swiglu_rows_f16(zh_ctx *ctx, const float *g, const float *u, _Float16 *out, float *unscale, uint32_t n,

@@ -25,40 +25,47 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int GT = 256;         // threads (4 waves)
 constexpr int TI = 128;         // tokens per tile
-constexpr int KS = 256;         // k per step: one super-block
-constexpr int LDR = KS + 8;     // halfs per LDS row (528 B: conflict-free 16 B reads)
+constexpr int KS = 128;         // k per step: half a super-block
+constexpr int LDR = KS + 8;     // halfs per LDS row (272 B: 16-byte reads of 8 rows hit distinct banks)
 
 struct GemmP {
-    const uint8_t *W;
+    // up to three stacked weight matrices sharing X (Q/K/V, gate/up): rows
+    // [seg_end[s-1], seg_end[s]) come from segW[s] and go to segY[s] (row
+    // stride segLdy[s]); segment sizes are multiples of the row tile
+    uint32_t nseg;
+    const uint8_t *segW[3];
+    float *segY[3];
+    uint32_t segLdy[3], seg_end[3];
     uint64_t row_bytes;
     const _Float16 *X;       // [N][ldx]
     const float *x_unscale;  // optional [N]: row n of X was stored times 1/x_unscale[n] (a power of two)
-    float *Y;                // [N][ldy]
-    uint32_t M, K, N, ldx, ldy, acc;
+    uint32_t M, K, N, ldx, acc;
 };
 
 ZH_DEV _Float16 to_h(float v) { return (_Float16)v; }  // round to nearest even
 
-// Raw bytes of one row's half super-block, loaded a K-step ahead.
-struct RawQ4K {  // header 16 B + qs[64h .. 64h+63]
-    u32x4 hdr, q[4];
+// Raw bytes of one dequantisation unit -- 32 elements of one weight row --
+// loaded a K-step ahead.
+struct RawQ4K {  // header 16 B + qs[32p .. 32p+31] of sub-pair p
+    u32x4 hdr, q[2];
 };
-struct RawQ6K {  // dword-aligned cover of ql[64h..+64], qh[32h..+32], sc[8h..+8], d
-    uint32_t ql[17], qh[9], sc[3], dw[2], sh;
+struct RawQ6K {  // dword-aligned covers of the 32 ql / 32 qh bytes of group g, the half's scales, d
+    uint32_t ql[9], qh[9], sc[3], dw[2], sh;
 };
 
-ZH_DEV void load_q4k_half(const uint8_t *blk, uint32_t h, RawQ4K &r) {
+ZH_DEV void load_q4k_unit(const uint8_t *blk, uint32_t p, RawQ4K &r) {
     r.hdr = *(const u32x4 *)blk;
-    const u32x4 *q4 = (const u32x4 *)(blk + 16 + 64 * h);
-#pragma unroll
-    for (int c = 0; c < 4; c++) r.q[c] = q4[c];
+    const u32x4 *q4 = (const u32x4 *)(blk + 16 + 32 * p);
+    r.q[0] = q4[0];
+    r.q[1] = q4[1];
 }
-ZH_DEV void load_q6k_half(const uint8_t *blk, uint32_t h, RawQ6K &r) {
+// group g of half h: ql[64h + 32(g&1) .. +32], qh[32h .. +32], sc[8h .. 8h+8]
+ZH_DEV void load_q6k_unit(const uint8_t *blk, uint32_t h, uint32_t g, RawQ6K &r) {
     const uintptr_t a = (uintptr_t)blk;
     r.sh = (uint32_t)(a & 3);
     const uint32_t *base = (const uint32_t *)(a & ~(uintptr_t)3);
 #pragma unroll
-    for (int i = 0; i < 17; i++) r.ql[i] = base[16 * h + i];
+    for (int i = 0; i < 9; i++) r.ql[i] = base[16 * h + 8 * (g & 1) + i];
 #pragma unroll
     for (int i = 0; i < 9; i++) r.qh[i] = base[32 + 8 * h + i];
 #pragma unroll
@@ -67,142 +74,144 @@ ZH_DEV void load_q6k_half(const uint8_t *blk, uint32_t h, RawQ6K &r) {
     r.dw[1] = base[53];
 }
 
-// Q4_K half super-block h (elements 128h..128h+127) into LDS.
-// dequantRow Q4_K (forward.zig:370-409): sub-pair p, d1 = d*sc[2p],
-// m1 = dmin*m[2p]: out[64p+l] = d1*(q&15) - m1, out[64p+32+l] = d2*(q>>4) - m2;
-// f32 operations rounded one by one (no contraction), then to fp16.
-ZH_DEV void deq_q4k_half(const RawQ4K &r, uint32_t h, _Float16 *dst) {
+// Q4_K sub-block j = 2p + nib (32 elements: nibble nib of qs[32p .. 32p+31])
+// into LDS. dequantRow Q4_K (forward.zig:370-409): dj = d*sc[j],
+// mj = dmin*m[j], out = dj*q - mj; the f32 operations rounded one by one (no
+// contraction), then to fp16 (nearest even).
+ZH_DEV void deq_q4k_unit(const RawQ4K &r, uint32_t p, uint32_t nib, _Float16 *dst) {
     const uint32_t w0 = r.hdr.x, w1 = r.hdr.y, w2 = r.hdr.z, w3 = r.hdr.w;
     const float d = h2f(w0), dmin = h2f(w0 >> 16);
     const uint32_t scA = w1 & 0x3F3F3F3Fu, mA = w2 & 0x3F3F3F3Fu;
     const uint32_t scB = (w3 & 0x0F0F0F0Fu) | ((w1 >> 2) & 0x30303030u);
     const uint32_t mB = ((w3 >> 4) & 0x0F0F0F0Fu) | ((w2 >> 2) & 0x30303030u);
+    const uint32_t j = 2 * p + nib;
+    const uint32_t scw = p < 2 ? scA : scB, mw = p < 2 ? mA : mB;
+    const float dj = __fmul_rn(d, (float)((scw >> (8 * (j & 3))) & 0xFF));
+    const float mj = __fmul_rn(dmin, (float)((mw >> (8 * (j & 3))) & 0xFF));
 #pragma unroll
-    for (int pp = 0; pp < 2; pp++) {
-        const uint32_t p = 2 * h + pp;  // sub-pair
-        const uint32_t j0 = 2 * p, j1 = 2 * p + 1;
-        const uint32_t scw = p < 2 ? scA : scB, mw = p < 2 ? mA : mB;
-        const float d1 = __fmul_rn(d, (float)((scw >> (8 * (j0 & 3))) & 0xFF));
-        const float m1 = __fmul_rn(dmin, (float)((mw >> (8 * (j0 & 3))) & 0xFF));
-        const float d2 = __fmul_rn(d, (float)((scw >> (8 * (j1 & 3))) & 0xFF));
-        const float m2 = __fmul_rn(dmin, (float)((mw >> (8 * (j1 & 3))) & 0xFF));
+    for (int c = 0; c < 2; c++) {
+        const u32x4 qv = r.q[c];
+        const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+        half8 o[2];
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const u32x4 qv = r.q[2 * pp + c];
-            const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
-            half8 lo[2], hi[2];
+        for (int w = 0; w < 4; w++) {
+            const uint32_t n4 = (qw[w] >> (4 * nib)) & 0x0F0F0F0Fu;
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const uint32_t byte = (qw[e >> 2] >> (8 * (e & 3))) & 0xFF;
-                lo[e >> 3][e & 7] = to_h(__fsub_rn(__fmul_rn(d1, (float)(byte & 15)), m1));
-                hi[e >> 3][e & 7] = to_h(__fsub_rn(__fmul_rn(d2, (float)(byte >> 4)), m2));
+            for (int b = 0; b < 4; b++) {  // byte-to-float conversions (v_cvt_f32_ubyteN)
+                const int e = 4 * w + b;
+                o[e >> 3][e & 7] = to_h(__fsub_rn(__fmul_rn(dj, (float)((n4 >> (8 * b)) & 0xFF)), mj));
             }
-            // elements 64p + 16c + 0..15 (low nibbles), 64p + 32 + 16c + 0..15 (high)
-            *(half8 *)(dst + 64 * pp + 16 * c) = lo[0];
-            *(half8 *)(dst + 64 * pp + 16 * c + 8) = lo[1];
-            *(half8 *)(dst + 64 * pp + 32 + 16 * c) = hi[0];
-            *(half8 *)(dst + 64 * pp + 32 + 16 * c + 8) = hi[1];
         }
+        *(half8 *)(dst + 16 * c) = o[0];
+        *(half8 *)(dst + 16 * c + 8) = o[1];
     }
 }
 
-// Q6_K half super-block h (dequantRow Q6_K, forward.zig:276-325): element
-// 128h + 32g + l: q = (ql[64h + l + 32(g&1)] >> 4(g>>1)) & 15 |
-// ((qh[32h + l] >> 2g) & 3) << 4; out = (d * sc[8h + l/16 + 2g]) * (q - 32).
+// Q6_K group g of half h (dequantRow Q6_K, forward.zig:276-325): element
+// 128h + 32g + l: q6 = (ql[64h + l + 32(g&1)] >> 4(g>>1)) & 15 |
+// ((qh[32h + l] >> 2g) & 3) << 4; out = (d * sc[8h + l/16 + 2g]) * (q6 - 32).
 // The block may start 2-byte aligned: its bytes are realigned with alignbyte.
-ZH_DEV void deq_q6k_half(const RawQ6K &r, _Float16 *dst) {
+ZH_DEV void deq_q6k_unit(const RawQ6K &r, uint32_t g, _Float16 *dst) {
     const uint32_t sh = r.sh;
     const float d = h2f(__builtin_amdgcn_alignbyte(r.dw[1], r.dw[0], sh));
     const uint32_t s0 = __builtin_amdgcn_alignbyte(r.sc[1], r.sc[0], sh), s1 = __builtin_amdgcn_alignbyte(r.sc[2], r.sc[1], sh);
+    const uint32_t i0 = 2 * g, i1 = 2 * g + 1;
+    const float ds0 = __fmul_rn(d, (float)(int8_t)(((i0 < 4 ? s0 : s1) >> (8 * (i0 & 3))) & 0xFF));
+    const float ds1 = __fmul_rn(d, (float)(int8_t)(((i1 < 4 ? s0 : s1) >> (8 * (i1 & 3))) & 0xFF));
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-        const float ds0 = __fmul_rn(d, (float)(int8_t)((((2 * g) < 4 ? s0 : s1) >> (8 * ((2 * g) & 3))) & 0xFF));
-        const float ds1 = __fmul_rn(d, (float)(int8_t)((((2 * g + 1) < 4 ? s0 : s1) >> (8 * ((2 * g + 1) & 3))) & 0xFF));
+    for (int c = 0; c < 4; c++) {  // 8 elements l = 8c .. 8c+7
+        const uint32_t qlw0 = __builtin_amdgcn_alignbyte(r.ql[2 * c + 1], r.ql[2 * c], sh);
+        const uint32_t qlw1 = __builtin_amdgcn_alignbyte(r.ql[2 * c + 2], r.ql[2 * c + 1], sh);
+        const uint32_t qhw0 = __builtin_amdgcn_alignbyte(r.qh[2 * c + 1], r.qh[2 * c], sh);
+        const uint32_t qhw1 = __builtin_amdgcn_alignbyte(r.qh[2 * c + 2], r.qh[2 * c + 1], sh);
+        half8 o;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {  // 8 elements l = 8c .. 8c+7
-            const uint32_t qlw0 = __builtin_amdgcn_alignbyte(r.ql[(g & 1) * 8 + 2 * c + 1], r.ql[(g & 1) * 8 + 2 * c], sh);
-            const uint32_t qlw1 = __builtin_amdgcn_alignbyte(r.ql[(g & 1) * 8 + 2 * c + 2], r.ql[(g & 1) * 8 + 2 * c + 1], sh);
-            const uint32_t qhw0 = __builtin_amdgcn_alignbyte(r.qh[2 * c + 1], r.qh[2 * c], sh);
-            const uint32_t qhw1 = __builtin_amdgcn_alignbyte(r.qh[2 * c + 2], r.qh[2 * c + 1], sh);
-            half8 o;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const uint32_t lb = ((e < 4 ? qlw0 : qlw1) >> (8 * (e & 3))) & 0xFF;
-                const uint32_t hb = ((e < 4 ? qhw0 : qhw1) >> (8 * (e & 3))) & 0xFF;
-                const int q = (int)(((lb >> (4 * (g >> 1))) & 15) | (((hb >> (2 * g)) & 3) << 4));
-                o[e] = to_h(__fmul_rn(c < 2 ? ds0 : ds1, (float)(q - 32)));
-            }
-            *(half8 *)(dst + 32 * g + 8 * c) = o;
+        for (int e = 0; e < 8; e++) {
+            const uint32_t lb = ((e < 4 ? qlw0 : qlw1) >> (8 * (e & 3))) & 0xFF;
+            const uint32_t hb = ((e < 4 ? qhw0 : qhw1) >> (8 * (e & 3))) & 0xFF;
+            const int q6 = (int)(((lb >> (4 * (g >> 1))) & 15) | (((hb >> (2 * g)) & 3) << 4));
+            o[e] = to_h(__fmul_rn(c < 2 ? ds0 : ds1, (float)(q6 - 32)));
         }
+        *(half8 *)(dst + 8 * c) = o;
     }
 }
 
+// Tile = TI tokens x TJ weight rows, K in steps of KS = half a super-block.
+// Waves 2 x 2: wave (wi, wj) owns tokens 64 wi .. +63 and rows TJ/2 wj ..
+// +TJ/2 (4 x TJ/32 MFMA tiles). Each step the threads dequantise the tile's
+// TJ x 4 units of 32 elements (UPT per thread) into LDS while the X chunks
+// and raw weight bytes of the next step are in flight in registers. 70 KB of
+// LDS (TJ = 128): two workgroups per CU, so one's dequantisation overlaps
+// the other's MFMAs.
 template <int QT, int TJ>
-__global__ __launch_bounds__(GT, 1) void k_gemm(GemmP p) {
+__global__ __launch_bounds__(GT, 2) void k_gemm(GemmP p) {
     extern __shared__ __align__(16) uint8_t lds[];
     _Float16 *xs = (_Float16 *)lds;       // [TI][LDR]
     _Float16 *ws = xs + TI * LDR;          // [TJ][LDR]
-    constexpr int JW = TJ / 4;             // weight rows per wave
-    constexpr int NJ = JW / 16, NI = TI / 16;
+    constexpr int WJ = TJ / 2;             // weight rows per wave
+    constexpr int NJ = WJ / 16, NI = 64 / 16;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t j0 = blockIdx.x * TJ, n0 = blockIdx.y * TI;
-    const uint32_t nb = p.K / KS;
+    const uint32_t wi = wave & 1, wj = wave >> 1;
+    const uint32_t n0 = blockIdx.y * TI;
+    // segment of this row tile
+    const uint32_t jg = blockIdx.x * TJ;
+    const uint32_t sg = (jg >= p.seg_end[0] ? 1u : 0u) + (p.nseg > 2 && jg >= p.seg_end[1] ? 1u : 0u);
+    const uint32_t seg_start = sg ? p.seg_end[sg - 1] : 0u, Ms = p.seg_end[sg] - seg_start;
+    const uint32_t j0 = jg - seg_start;
+    const uint8_t *Wseg = p.segW[sg];
+    const uint32_t nst = p.K / KS;
     const uint32_t bpb = QT == ZH_Q4_K ? 144 : 210;
     f32x4v acc[NI][NJ];
 #pragma unroll
     for (int i = 0; i < NI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    // Software pipeline: the next K-step's X chunks and raw weight bytes are
-    // loaded into registers while the current step's MFMAs run.
-    constexpr int XC = TI * 32 / GT;          // 16-byte X chunks per thread per step
-    constexpr int WU = (TJ * 2 + GT - 1) / GT;  // (row, half) units per thread
+    constexpr int XC = TI * KS / 8 / GT;  // 16-byte X chunks per thread per step
+    constexpr int UPT = TJ * 4 / GT;      // units (row, 32-element group u4) per thread per step
     half8 xr[XC];
     typedef typename std::conditional<QT == ZH_Q4_K, RawQ4K, RawQ6K>::type Raw;
-    Raw wr[WU];
-    auto load_step = [&](uint32_t sb) {
+    Raw wr[UPT];
+    auto load_step = [&](uint32_t st) {
 #pragma unroll
         for (int c = 0; c < XC; c++) {
-            const uint32_t idx = c * GT + tid, t = idx / 32, ch = idx % 32;
+            const uint32_t idx = c * GT + tid, t = idx / (KS / 8), ch = idx % (KS / 8);
             const uint32_t tok = min(n0 + t, p.N - 1);
-            xr[c] = *(const half8 *)(p.X + (size_t)tok * p.ldx + (size_t)sb * KS + ch * 8);
+            xr[c] = *(const half8 *)(p.X + (size_t)tok * p.ldx + (size_t)st * KS + ch * 8);
         }
 #pragma unroll
-        for (int w = 0; w < WU; w++) {
-            const uint32_t u = min(w * GT + tid, (uint32_t)TJ * 2 - 1), r = u >> 1, h = u & 1;
-            const uint32_t row = min(j0 + r, p.M - 1);
-            const uint8_t *blk = p.W + (size_t)row * p.row_bytes + (size_t)sb * bpb;
-            if constexpr (QT == ZH_Q4_K) load_q4k_half(blk, h, wr[w]);
-            else load_q6k_half(blk, h, wr[w]);
+        for (int k = 0; k < UPT; k++) {
+            const uint32_t u = k * GT + tid, r = u >> 2, u4 = u & 3;
+            const uint32_t row = min(j0 + r, Ms - 1);  // rows past the segment: loaded clamped, never written
+            const uint8_t *blk = Wseg + (size_t)row * p.row_bytes + (size_t)(st >> 1) * bpb;
+            if constexpr (QT == ZH_Q4_K) load_q4k_unit(blk, 2 * (st & 1) + (u4 >> 1), wr[k]);
+            else load_q6k_unit(blk, st & 1, u4, wr[k]);
         }
     };
     load_step(0);
-    for (uint32_t sb = 0; sb < nb; sb++) {
+    for (uint32_t st = 0; st < nst; st++) {
 #pragma unroll
         for (int c = 0; c < XC; c++) {
-            const uint32_t idx = c * GT + tid, t = idx / 32, ch = idx % 32;
+            const uint32_t idx = c * GT + tid, t = idx / (KS / 8), ch = idx % (KS / 8);
             *(half8 *)(xs + t * LDR + ch * 8) = xr[c];
         }
 #pragma unroll
-        for (int w = 0; w < WU; w++) {
-            const uint32_t u = w * GT + tid;
-            if (u < (uint32_t)TJ * 2) {
-                const uint32_t r = u >> 1, h = u & 1;
-                if constexpr (QT == ZH_Q4_K) deq_q4k_half(wr[w], h, ws + r * LDR + 128 * h);
-                else deq_q6k_half(wr[w], ws + r * LDR + 128 * h);
-            }
+        for (int k = 0; k < UPT; k++) {
+            const uint32_t u = k * GT + tid, r = u >> 2, u4 = u & 3;
+            // Q4_K: u4 = (sub-pair within the half, nibble) -> elements 32 u4 of the step
+            if constexpr (QT == ZH_Q4_K) deq_q4k_unit(wr[k], 2 * (st & 1) + (u4 >> 1), u4 & 1, ws + r * LDR + 32 * u4);
+            else deq_q6k_unit(wr[k], u4, ws + r * LDR + 32 * u4);
         }
         __syncthreads();
-        if (sb + 1 < nb) load_step(sb + 1);
+        if (st + 1 < nst) load_step(st + 1);
 #pragma unroll
         for (int kk = 0; kk < KS / 32; kk++) {
             const uint32_t ko = kk * 32 + 8 * (lane / 16);
             half8 b[NJ];
 #pragma unroll
-            for (int j = 0; j < NJ; j++) b[j] = *(const half8 *)(ws + (wave * JW + j * 16 + lane % 16) * LDR + ko);
+            for (int j = 0; j < NJ; j++) b[j] = *(const half8 *)(ws + (wj * WJ + j * 16 + lane % 16) * LDR + ko);
 #pragma unroll
             for (int i = 0; i < NI; i++) {
-                const half8 a = *(const half8 *)(xs + (i * 16 + lane % 16) * LDR + ko);
+                const half8 a = *(const half8 *)(xs + (wi * 64 + i * 16 + lane % 16) * LDR + ko);
 #pragma unroll
                 for (int j = 0; j < NJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], acc[i][j], 0, 0, 0);
             }
@@ -213,12 +222,12 @@ __global__ __launch_bounds__(GT, 1) void k_gemm(GemmP p) {
     for (int i = 0; i < NI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
-            const uint32_t row = j0 + wave * JW + j * 16 + lane % 16;
+            const uint32_t row = j0 + wj * WJ + j * 16 + lane % 16;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const uint32_t tok = n0 + i * 16 + 4 * (lane / 16) + r;
-                if (tok < p.N && row < p.M) {
-                    float *yp = p.Y + (size_t)tok * p.ldy + row;
+                const uint32_t tok = n0 + wi * 64 + i * 16 + 4 * (lane / 16) + r;
+                if (tok < p.N && row < Ms) {
+                    float *yp = p.segY[sg] + (size_t)tok * p.segLdy[sg] + row;
                     const float v = p.x_unscale ? acc[i][j][r] * p.x_unscale[tok] : acc[i][j][r];  // exact
                     *yp = p.acc ? *yp + v : v;
                 }
@@ -228,25 +237,45 @@ __global__ __launch_bounds__(GT, 1) void k_gemm(GemmP p) {
 
 }  // namespace
 
-int zhk_gemm(zh_ctx *c, uint32_t qtype, const uint8_t *W, const _Float16 *X, uint32_t ldx, float *Y, uint32_t ldy,
-             uint32_t M, uint32_t K, uint32_t N, uint32_t acc, const float *x_unscale) {
-    if ((qtype != ZH_Q4_K && qtype != ZH_Q6_K) || K % KS || M == 0 || N == 0)
-        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: qtype %u M %u K %u N %u", qtype, M, K, N);
-    GemmP p;
-    p.W = W; p.row_bytes = zh_tensor_bytes(qtype, 1, K); p.X = X; p.x_unscale = x_unscale; p.Y = Y;
-    p.M = M; p.K = K; p.N = N; p.ldx = ldx; p.ldy = ldy; p.acc = acc;
+int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, const _Float16 *X, uint32_t ldx,
+                   float *const *Y, const uint32_t *ldy, const uint32_t *M, uint32_t K, uint32_t N, uint32_t acc,
+                   const float *x_unscale) {
+    if ((qtype != ZH_Q4_K && qtype != ZH_Q6_K) || K % 256 || N == 0 || nseg < 1 || nseg > 3)
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: qtype %u K %u N %u nseg %u", qtype, K, N, nseg);
+    GemmP p = {};
+    p.nseg = nseg; p.row_bytes = zh_tensor_bytes(qtype, 1, K); p.X = X; p.x_unscale = x_unscale;
+    p.K = K; p.N = N; p.ldx = ldx; p.acc = acc;
+    uint32_t end = 0;
+    for (uint32_t s = 0; s < nseg; s++) {
+        if (M[s] == 0) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: empty segment");
+        p.segW[s] = W[s]; p.segY[s] = Y[s]; p.segLdy[s] = ldy[s];
+        end += M[s];
+        p.seg_end[s] = end;
+    }
+    for (uint32_t s = nseg; s < 3; s++) p.seg_end[s] = end;
+    p.M = end;
     const uint32_t ni = (N + TI - 1) / TI;
-    // 64-row tiles when 128-row tiles would leave CUs idle
-    const bool small = (uint64_t)((M + 127) / 128) * ni < (uint64_t)c->cu_count;
+    // 64-row tiles when 128-row tiles would leave CUs idle; every segment but
+    // the last must then be a whole number of tiles
+    bool small = (uint64_t)((end + 127) / 128) * ni < (uint64_t)c->cu_count;
+    for (uint32_t s = 0; s + 1 < nseg; s++)
+        if (M[s] % 128) small = true;
+    for (uint32_t s = 0; s + 1 < nseg; s++)
+        if (M[s] % 64) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: segment rows %u not a multiple of 64", M[s]);
     const uint32_t TJv = small ? 64 : 128;
     const uint32_t lds = (TI + TJv) * LDR * 2;
-    dim3 grid((M + TJv - 1) / TJv, ni);
+    dim3 grid((end + TJv - 1) / TJv, ni);
 #define GL(Q, J) hipLaunchKernelGGL((k_gemm<Q, J>), grid, dim3(GT), lds, c->stream, p)
     if (qtype == ZH_Q4_K) { if (small) GL(ZH_Q4_K, 64); else GL(ZH_Q4_K, 128); }
     else { if (small) GL(ZH_Q6_K, 64); else GL(ZH_Q6_K, 128); }
 #undef GL
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
+}
+
+int zhk_gemm(zh_ctx *c, uint32_t qtype, const uint8_t *W, const _Float16 *X, uint32_t ldx, float *Y, uint32_t ldy,
+             uint32_t M, uint32_t K, uint32_t N, uint32_t acc, const float *x_unscale) {
+    return zhk_gemm_multi(c, qtype, 1, &W, X, ldx, &Y, &ldy, &M, K, N, acc, x_unscale);
 }
 
 // Y[n][m] (+)= X[n][:] . W[m][:], X fp16 token-major, Y f32 token-major
