@@ -287,7 +287,7 @@ struct FmtMXFP4 {
     ZH_DEVM static void load_raw(const uint8_t *row, int u, uint32_t *raw) {
         const uint8_t *b = row + (size_t)u * 17;
         uintptr_t a = (uintptr_t)b & ~(uintptr_t)3;
-        u32x4 t = *(const u32x4 *)a;
+        u32x4 t = *(const u32x4_a4 *)a;  // dword-aligned (also read from LDS tiles)
         raw[0] = t.x; raw[1] = t.y; raw[2] = t.z; raw[3] = t.w;
         raw[4] = *(const uint32_t *)(a + 16);
         raw[5] = (uint32_t)((uintptr_t)b & 3);
@@ -573,8 +573,13 @@ static int check_k(zh_ctx *c, uint32_t qtype, uint32_t K) {
     }
 }
 
+static int try_ftile(zh_ctx *c, uint32_t qtype, const uint8_t *W, const void *xq, const float *xf, float *y,
+                     uint32_t M, uint32_t K, uint32_t acc);
+
 int zhk_dmmv(zh_ctx *c, uint32_t qtype, const uint8_t *W, const void *xq, float *y, uint32_t M,
              uint32_t K, uint32_t acc) {
+    const int rc = try_ftile(c, qtype, W, xq, nullptr, y, M, K, acc);
+    if (rc >= 0) return rc;
     DmmvP p = {};
     p.W = W; p.W2 = W; p.xq = (const uint8_t *)xq; p.y = y; p.M = M; p.K = K;
     p.row_bytes = zh_tensor_bytes(qtype, 1, K); p.acc = acc;
@@ -893,6 +898,109 @@ int zhk_dmmv_lds_down_acc(zh_ctx *c, uint32_t qtype, const uint8_t *W, uint64_t 
 }
 
 // ---------------------------------------------------------------------------
+// Coalesced-tile kernel for a format of the team kernel (used for MXFP4):
+// the activation is staged once per workgroup as an XQ image in LDS (copied,
+// or quantised from f32), each batch of rows -- a contiguous byte range -- is
+// fetched with consecutive lanes on consecutive 16-byte chunks (one batch
+// ahead) into an LDS tile, and each row is reduced by one wave whose lanes
+// walk the row's units, reading limbs and weight bytes from LDS. Batches hold
+// RPB = 4, 8 or 16 rows so that a batch is a whole number of 16-byte chunks.
+// ---------------------------------------------------------------------------
+constexpr int FT_NCH = 8;  // 16-byte chunks per lane per batch (tile <= 32 KB)
+struct FtP {
+    const uint8_t *W;
+    uint32_t M, K, rpb;
+    uint64_t row_bytes;
+    const uint8_t *xq;  // XQ activation, or
+    const float *xf;    // f32 activation (quantised while staging)
+    float *y;
+    uint32_t acc;
+};
+
+template <class F>
+__global__ __launch_bounds__(256, 2) void k_dmmv_ftile(FtP p) {
+    extern __shared__ __align__(16) uint8_t ft_lds[];
+    __shared__ float red[4];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t nblk = p.K / 32, U = p.K / F::EPU;
+    uint8_t *tile = ft_lds + ((size_t)nblk * 108 + 15) / 16 * 16;
+    const uint32_t nbatch = (p.M + p.rpb - 1) / p.rpb;
+    const uint32_t batch_bytes = p.rpb * (uint32_t)p.row_bytes;
+    u32x4 st[FT_NCH];
+    auto fetch = [&](uint32_t bi) {
+        const uint32_t nr = min(p.rpb, p.M - bi * p.rpb), n16 = (nr * (uint32_t)p.row_bytes + 15) / 16;
+        const u32x4 *src = (const u32x4 *)(p.W + (size_t)bi * batch_bytes);
+#pragma unroll
+        for (int j = 0; j < FT_NCH; j++) st[j] = src[min(j * 256 + tid, n16 - 1)];  // clamped: static count
+    };
+    uint32_t bi = blockIdx.x;  // grid <= nbatch (host)
+    fetch(bi);
+    // activation -> LDS XQ image
+    if (p.xq) {
+        for (uint32_t i = tid; i < nblk * 27; i += 256) ((uint32_t *)ft_lds)[i] = ((const uint32_t *)p.xq)[i];
+        __syncthreads();
+    } else {
+        dl_stage(p.xf, nullptr, 0.f, p.K, ft_lds, red);
+    }
+    const XQView xv = xq_view(ft_lds, nblk);
+    for (; bi < nbatch; bi += gridDim.x) {
+        const uint32_t nr = min(p.rpb, p.M - bi * p.rpb), n16 = (nr * (uint32_t)p.row_bytes + 15) / 16;
+#pragma unroll
+        for (int j = 0; j < FT_NCH; j++) {
+            const uint32_t c = j * 256 + tid;
+            if (c < n16) *(u32x4 *)(tile + c * 16) = st[j];
+        }
+        __syncthreads();
+        if (bi + gridDim.x < nbatch) fetch(bi + gridDim.x);
+        for (uint32_t r = wave; r < p.rpb; r += 4) {  // uniform per wave
+            const uint8_t *row = tile + (size_t)r * p.row_bytes;
+            float part = 0.f;
+            for (uint32_t u = lane; u < U; u += 64) {
+                XReg xr;
+                uint32_t raw[F::RAW];
+                F::load_x(xr, xv, u);
+                F::load_raw(row, u, raw);
+                part += F::compute(raw, xr, u);
+            }
+            part = wave_sum(part);
+            if (lane == 0 && r < nr) {
+                float *yo = p.y + (size_t)bi * p.rpb + r;
+                *yo = p.acc ? *yo + part : part;
+            }
+        }
+        __syncthreads();  // the tile is rewritten by the next batch
+    }
+}
+
+// Launches the tile kernel when it applies; returns -1 to use the team kernel.
+static int try_ftile(zh_ctx *c, uint32_t qtype, const uint8_t *W, const void *xq, const float *xf, float *y,
+                     uint32_t M, uint32_t K, uint32_t acc) {
+    static int off = -1;
+    if (off < 0) off = getenv("ZH_NO_FTILE") ? 1 : 0;
+    // MXFP4 only: for Q8_0 the team kernel (x in registers, four rows per
+    // team in flight) measured faster than 4-row tiles
+    if (off || qtype != ZH_MXFP4 || ((uintptr_t)W & 15)) return -1;
+    if (!xq && K > (uint32_t)(DL_XE * DL_T)) return -1;  // f32 staging holds K <= 4096
+    const uint64_t rb = zh_tensor_bytes(qtype, 1, K);
+    uint32_t rpb = 4;
+    while ((rpb * rb) % 16) rpb *= 2;  // 4, 8 or 16 rows
+    // whole batches only: every 16-byte chunk lies inside the matrix
+    if (M % rpb) return -1;
+    if (rpb * rb > (uint64_t)FT_NCH * 256 * 16) return -1;
+    const uint32_t lds = ((K / 32) * 108 + 15) / 16 * 16 + (uint32_t)(rpb * rb);
+    if (lds > 65536) return -1;
+    FtP p = {};
+    p.W = W; p.M = M; p.K = K; p.rpb = rpb; p.row_bytes = rb; p.xq = (const uint8_t *)xq; p.xf = xf; p.y = y;
+    p.acc = acc;
+    const uint32_t nbatch = (M + rpb - 1) / rpb;
+    uint32_t wgs = nbatch, cap = (uint32_t)c->cu_count * 2;
+    if (wgs > cap) wgs = cap;
+    hipLaunchKernelGGL(k_dmmv_ftile<FmtMXFP4>, dim3(wgs), dim3(256), lds, c->stream, p);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+// ---------------------------------------------------------------------------
 // C ABI wrappers with argument validation (shapes are checked on the host
 // before any launch so a kernel never sees a shape it does not assume).
 // ---------------------------------------------------------------------------
@@ -918,6 +1026,11 @@ extern "C" int zh_dmmv(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a_of
         if (M % R == 0)
             return zhk_dmmv_lpb(c, qtype, 0, 1, &w, nullptr, &yy, &M, (const float *)((const char *)x->ptr + x_off),
                                 nullptr, 0.f, nullptr, K, acc_mode);
+    }
+    if ((x_off & 15) == 0) {  // f32 staged and quantised per workgroup
+        rc = try_ftile(c, qtype, (const uint8_t *)W->ptr + a_off, nullptr, (const float *)((const char *)x->ptr + x_off),
+                       (float *)((char *)y->ptr + y_off), M, K, acc_mode);
+        if (rc >= 0) return rc;
     }
     void *xq;
     if ((rc = zh_scratch(c, zh_xq_bytes_int(K), &xq))) return rc;
