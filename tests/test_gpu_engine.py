@@ -133,3 +133,42 @@ def test_engine_context_overflow_is_an_error(ctx):
     with pytest.raises(zinc_amd.ZincError):
         eng.decode_step(st, 1)
     eng.deinit()
+
+
+# 16 kv heads put 256 / 16 = 16 chunks per kv head on the device, so a
+# context above 2 x 16 x 160 = 5120 tokens makes every attention chunk hold
+# several 160-token sub-chunks reduced with an online softmax (here 3 at
+# 12000 tokens); the new token's K/V write and substitution then happen in a
+# later sub-chunk than the first.
+LONG_SUBCHUNK = dict(n_layers=1, hidden=1024, n_heads=16, n_kv_heads=16, head_dim=128, ffn=1024, vocab=1000,
+                     n_experts=0, n_experts_used=0, expert_ffn=0, max_ctx=12048,
+                     type_attn=12, type_ffn_gate_up=12, type_ffn_down=14, type_lm_head=14, type_embd=12,
+                     type_router=8, rope_base=1e6, eps=1e-6, seed=96)
+
+
+@pytest.mark.parametrize("prefill", [12000, 10001], ids=["12000", "10001"])
+def test_engine_long_context_subchunks(ctx, orc, prefill):
+    import zinc_amd
+    cfg = LONG_SUBCHUNK
+    eng = zinc_amd.InferenceEngine(ctx, cfg)
+    om = orc.Model(cfg)
+    eng.prefill_kv_random(prefill, 11)
+    om.prefill_kv_random(prefill, 11)
+    state = zinc_amd.DecodeState()
+    tok = 5
+    for step in range(3):
+        state.position = prefill + step
+        eng.decode_step(state, tok, True)
+        g_tok, g_log = eng.sample_greedy(), eng.logits()
+        o_tok, o_log = om.decode_step(tok, prefill + step, want_logits=True)
+        scale = np.abs(o_log).max()
+        assert np.abs(g_log - o_log).max() <= 1e-4 + 1e-3 * scale, (step, np.abs(g_log - o_log).max(), scale)
+        if margin(o_log) > 1e-3 * scale:
+            assert g_tok == o_tok
+        for which in (0, 1):
+            g = eng.read_kv(0, which, prefill + step, 1).view(np.float16).astype(np.float32)
+            o = om.kv(0, which, prefill + step).view(np.float16).astype(np.float32)
+            assert np.abs(g - o).max() <= 2e-3 * np.abs(o).max(), (step, which)
+        tok = int(o_tok)
+    eng.deinit()
+    om.close()

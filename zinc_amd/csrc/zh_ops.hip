@@ -228,10 +228,21 @@ constexpr int AD_TC = AD_W * AD_TW;  // tokens per chunk (at most)
 // chunks of all kv heads cover the device once (32 per head for 8 kv heads:
 // one XCD each).
 enum { AD_PAGED = 0, AD_PAGED_REV = 1, AD_IDENT = 2 };
-ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq, uint32_t nd) {
-    const uint32_t ct = ((seq + nd - 1) / nd + 7) / 8 * 8;
-    return seq > nd * AD_TC ? (uint32_t)AD_TC : max(ct, (uint32_t)AD_TW);
+// Longer contexts: up to 2 nd chunks of 160 tokens, then chunks of nsub
+// consecutive 160-token sub-chunks (a workgroup runs them in turn with an
+// online softmax), so a kv head never has more than 2 nd chunks: the grid
+// stays one round of two workgroups per CU and the merge reads 2 nd partials.
+ZH_DEV uint32_t attn_nsub(uint32_t seq, uint32_t nd) {
+    const uint32_t span = 2 * nd * AD_TC;
+    return seq > span ? (seq + span - 1) / span : 1u;
 }
+ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq, uint32_t nd, bool sub) {
+    const uint32_t ct = ((seq + nd - 1) / nd + 7) / 8 * 8;
+    return seq > nd * AD_TC ? (uint32_t)AD_TC * (sub ? attn_nsub(seq, nd) : 1u) : max(ct, (uint32_t)AD_TW);
+}
+// Sub-chunks are compiled for up to 4 q heads per kv head (G = 8 would spill
+// its loop-carried state); G = 8 keeps 160-token chunks at long contexts.
+template <int G> constexpr bool attn_sub_ok() { return G <= 4; }
 static uint32_t attn_nd(uint32_t nkv, int cu_count) {
     const uint32_t cu = cu_count > 0 && cu_count < 256 ? (uint32_t)cu_count : 256u;
     return cu / nkv > 0 ? cu / nkv : 1u;
@@ -432,15 +443,17 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     const uint32_t pos_raw = *(p.pos.dev ? p.pos.dev : p.pages);
     const uint32_t posv = p.pos.dev ? pos_raw + p.pos.value : p.pos.value;
     const uint32_t seq = FUSED ? posv + 1 : posv;
-    const uint32_t CT = MODE == AD_IDENT ? attn_chunk_tokens(seq, p.nd) : (uint32_t)AD_TC;
+    constexpr bool SUB = MODE == AD_IDENT && attn_sub_ok<G>();
+    const uint32_t CT = MODE == AD_IDENT ? attn_chunk_tokens(seq, p.nd, SUB) : (uint32_t)AD_TC;
+    const uint32_t nsub = SUB ? attn_nsub(seq, p.nd) : 1u;  // 160-token sub-chunks per chunk
     uint32_t chunk = blockIdx.y;
     if (MODE != AD_PAGED) {
         const uint32_t nv_hint = (seq + CT - 1) / CT;
         chunk = blockIdx.y < nv_hint ? nv_hint - 1 - blockIdx.y : blockIdx.y;
     }
     const uint32_t t0 = chunk * CT, tw0 = t0 + wave * AD_TW;
-    // this wave's tokens within the chunk (a chunk shorter than 160 leaves
-    // the last waves fewer, or none)
+    // this wave's tokens within (each sub-chunk of) the chunk: a chunk
+    // shorter than 160 leaves the last waves fewer, or none
     const uint32_t wtok = CT > wave * AD_TW ? min(CT - wave * AD_TW, (uint32_t)AD_TW) : 0u;
     const uint32_t pgb = tw0 / 16, o16 = tw0 & 15;
     uint32_t page0, page1, page2;
@@ -511,150 +524,205 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     // sinking the groups (q / new token / RoPE first, then K, then V), so the
     // q preparation waits only for its own loads.
     asm volatile("" ::: "memory");
-    // K/V rows of this wave's tokens: up to three 16-token pages, each a
-    // contiguous 4 KB run, so every row is an offset from a page base that
-    // is uniform per 8-token pass. Rows past the end of the sequence are read
-    // (in-bounds) and masked.
-    const uint32_t ptok = p.cache_tokens / 16;
-    const size_t pa = page0 < ptok ? page0 : 0u, pb = page1 < ptok ? page1 : 0u, pc = page2 < ptok ? page2 : 0u;
-    u32x4 kr[AD_TW / 8][2];
-#pragma unroll
-    for (int j = 0; j < AD_TW / 8; j++) {
-        // o16 + 8j is 8-aligned: the pass stays in one page
-        const uint16_t *kp = kv_row(kh, pa, pb, pc, o16 + 8 * j) + grp * FD_HD;
-        kr[j][0] = *(const u32x4 *)(kp + sub * 8);
-        kr[j][1] = *(const u32x4 *)(kp + 64 + sub * 8);
-    }
-    asm volatile("" ::: "memory");
-    // V rows: lane = (vrow = lane / 16, vcol = lane % 16) holds dims
-    // 8 vcol .. 8 vcol + 7 of the wave's tokens vrow, vrow + 4, .., 36 + vrow:
-    // 16-byte loads, one instruction covering 4 tokens x 256 B (4 tokens from
-    // a 4-aligned offset never straddle a 16-token page)
-    const uint32_t vrow = lane >> 4, vcol = lane & 15;
-    u32x4 vr[AD_TW / 4];
-#pragma unroll
-    for (int k = 0; k < AD_TW / 4; k++) vr[k] = *(const u32x4 *)(kv_row(vh, pa, pb, pc, o16 + 4 * k + vrow) + 8 * vcol);
-    asm volatile("" ::: "memory");
-
-    // ---- q (and new k) preparation
-    bool owner = false;  // this wave's tokens include the new position (uniform per wave)
-    uint32_t inew = 0, vnew = 0;
-    u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0}, vnew4 = {0, 0, 0, 0};
+    // ---- q preparation (once per workgroup)
     if (FUSED) {
 #pragma unroll
         for (int g = 0; g < G; g++) norm_rope16(qlo[g], qhi[g], qwl, qwh, co, sn, p.eps);
-        owner = posv >= tw0 && posv < tw0 + wtok;
-        if (owner) {
-            // the cache rows loaded above for this position predate the write
-            // below; scores and P*V select these values for it instead
-            norm_rope16(klo, khi, kwl, kwh, co, sn, p.eps);
-            n0 = u32x4{pack_h2(klo[0], klo[1]), pack_h2(klo[2], klo[3]), pack_h2(klo[4], klo[5]),
-                       pack_h2(klo[6], klo[7])};
-            n1 = u32x4{pack_h2(khi[0], khi[1]), pack_h2(khi[2], khi[3]), pack_h2(khi[4], khi[5]),
-                       pack_h2(khi[6], khi[7])};
-            vnew = pack_h2(vn0, vn1);
-            vnew4 = u32x4{pack_h2(vn8[0], vn8[1]), pack_h2(vn8[2], vn8[3]), pack_h2(vn8[4], vn8[5]),
-                          pack_h2(vn8[6], vn8[7])};
-            inew = posv - tw0;
-            // logicalTokenToPhysicalToken for the new position, from the page
-            // entries loaded above (the position lies in page pgb + 0..2); the
-            // host has checked the context length, an unmapped slot is skipped
-            const uint32_t slot = posv / 16, pi = slot - pgb;
-            const uint32_t pg = pi == 0 ? page0 : pi == 1 ? page1 : page2;
-            uint32_t ph = slot < p.n_pages ? pg * 16 + posv % 16 : p.cache_tokens;
-            if (ph < p.cache_tokens) {
-                if (grp == (inew & 7)) {
-                    *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + sub * 8) = n0;
-                    *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 64 + sub * 8) = n1;
-                }
-                *(uint32_t *)(p.vc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 2 * lane) = vnew;
-            }
-        }
     }
-    TRACE_OPS(1);
-
-    // ---- scores: token 8j + grp, 16 dims per lane, reduced over 8 lanes
-    float sc[AD_TW / 8][G];
-#pragma unroll
-    for (int j = 0; j < AD_TW / 8; j++) {
-        const bool sel = owner && (uint32_t)(8 * j) + grp == inew;
-        const u32x4 k0 = sel ? n0 : kr[j][0], k1 = sel ? n1 : kr[j][1];
-        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-        float kf[16];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            kf[2 * e] = h2f(kw[e]);
-            kf[2 * e + 1] = h2f(kw[e] >> 16);
-        }
-        const bool valid = (uint32_t)(8 * j) + grp < nt;
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float sacc = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                sacc = fmaf(qlo[g][e], kf[e], sacc);
-                sacc = fmaf(qhi[g][e], kf[8 + e], sacc);
-            }
-            sacc = sum8(sacc) * p.scale;  // dot * scale, as cpuAttention
-            sc[j][g] = valid ? sacc : -INFINITY;
-        }
-    }
-    TRACE_OPS(2);
-    // ---- per-wave softmax over its tokens; P*V with lane = (token row, 8 dims)
     __shared__ float ps[AD_W][G][AD_TW];
     __shared__ float wm[AD_W][G], wl[AD_W][G];
     __shared__ float wo[AD_W][4][G][FD_HD];  // per wave and token row
-    float mx[G];
+    const uint32_t vrow = lane >> 4, vcol = lane & 15;
+    const uint32_t ptok = p.cache_tokens / 16;
+    // online softmax state of this wave over its sub-chunks (per q head):
+    // running maximum, sum of exp and P*V (lane = token row vrow, dims 8 vcol..)
+    float m_run[G], l_run[G], acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        float m = sc[0][g];
-#pragma unroll
-        for (int j = 1; j < AD_TW / 8; j++) m = fmaxf(m, sc[j][g]);
-        m = rows_max(fmaxf(m, dpp_f<0x140>(m)));  // m is uniform within each 8-lane token group
-        const float ms = m == -INFINITY ? 0.f : m;  // a wave past the end has no valid token
-        float l = 0.f;
-#pragma unroll
-        for (int j = 0; j < AD_TW / 8; j++) {
-            const float pr = expf(sc[j][g] - ms);
-            if (sub == 0) ps[wave][g][8 * j + grp] = pr;
-            l += pr;
-        }
-        l = rows_sum(l + dpp_f<0x140>(l));
-        mx[g] = m;
-        if (lane == 0) { wm[wave][g] = m; wl[wave][g] = l; }
-    }
-    __syncthreads();
-    TRACE_OPS(8);
-    float acc[G][8];
-#pragma unroll
-    for (int g = 0; g < G; g++)
+        m_run[g] = -INFINITY;
+        l_run[g] = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
-#pragma unroll
-    for (int k = 0; k < AD_TW / 4; k++) {
-        const uint32_t i = 4 * k + vrow;
-        u32x4 v = owner && i == inew ? vnew4 : vr[k];
-        if (i >= nt) v = u32x4{0, 0, 0, 0};  // rows past the end may hold anything
-        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-        float vf[8];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            vf[2 * e] = h2f(vw[e]);
-            vf[2 * e + 1] = h2f(vw[e] >> 16);
+    }
+    // K/V rows of this wave's tokens in sub-chunk i (sub-chunk 0: the page
+    // entries computed above; later sub-chunks exist only with the identity
+    // page table): up to three 16-token pages, each a contiguous 4 KB run, so
+    // every row is an offset from a page base that is uniform per 8-token
+    // pass. Rows past the end of the sequence are read (in-bounds) and masked.
+    // V: lane = (vrow = lane / 16, vcol = lane % 16) holds dims 8 vcol ..
+    // 8 vcol + 7 of the wave's tokens vrow, vrow + 4, .., 36 + vrow: 16-byte
+    // loads, one instruction covering 4 tokens x 256 B (4 tokens from a
+    // 4-aligned offset never straddle a 16-token page). Sub-chunk i + 1's K
+    // loads go out once sub-chunk i's scores are computed, its V loads once
+    // sub-chunk i's P*V is done, in the same registers.
+    u32x4 kr[AD_TW / 8][2];
+    u32x4 vr[AD_TW / 4];
+    auto pages_of = [&](uint32_t i, uint32_t &pg0, uint32_t &pg1, uint32_t &pg2, uint32_t &pgbs)
+        __attribute__((always_inline)) {
+        pg0 = page0; pg1 = page1; pg2 = page2; pgbs = pgb;
+        if (i) {
+            pgbs = (tw0 + i * AD_TC) / 16;
+            pg0 = pgbs; pg1 = pgbs + 1; pg2 = pgbs + 2;
         }
+    };
+    auto load_k = [&](uint32_t i) __attribute__((always_inline)) {
+        uint32_t g0, g1, g2, gb;
+        pages_of(i, g0, g1, g2, gb);
+        const size_t pa = g0 < ptok ? g0 : 0u, pb = g1 < ptok ? g1 : 0u, pc = g2 < ptok ? g2 : 0u;
+#pragma unroll
+        for (int j = 0; j < AD_TW / 8; j++) {
+            // o16 + 8j is 8-aligned: the pass stays in one page
+            const uint16_t *kp = kv_row(kh, pa, pb, pc, o16 + 8 * j) + grp * FD_HD;
+            kr[j][0] = *(const u32x4 *)(kp + sub * 8);
+            kr[j][1] = *(const u32x4 *)(kp + 64 + sub * 8);
+        }
+    };
+    auto load_v = [&](uint32_t i) __attribute__((always_inline)) {
+        uint32_t g0, g1, g2, gb;
+        pages_of(i, g0, g1, g2, gb);
+        const size_t pa = g0 < ptok ? g0 : 0u, pb = g1 < ptok ? g1 : 0u, pc = g2 < ptok ? g2 : 0u;
+#pragma unroll
+        for (int k = 0; k < AD_TW / 4; k++)
+            vr[k] = *(const u32x4 *)(kv_row(vh, pa, pb, pc, o16 + 4 * k + vrow) + 8 * vcol);
+    };
+    load_k(0);
+    asm volatile("" ::: "memory");
+    load_v(0);
+    asm volatile("" ::: "memory");
+    for (uint32_t sc_i = 0; sc_i < nsub; sc_i++) {  // uniform over the workgroup
+        const uint32_t tws = tw0 + sc_i * AD_TC;
+        const uint32_t nts = seq > tws ? min(seq - tws, wtok) : 0u;
+        uint32_t pg0, pg1, pg2, pgbs;
+        pages_of(sc_i, pg0, pg1, pg2, pgbs);
+
+        // ---- the new token (its position lies in exactly one wave's range)
+        bool owner = false;  // uniform per wave
+        uint32_t inew = 0;
+        u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0}, vnew4 = {0, 0, 0, 0};
+        if (FUSED) {
+            owner = posv >= tws && posv < tws + wtok;
+            if (owner) {
+                // the cache rows loaded above for this position predate the
+                // write below; scores and P*V select these values for it instead
+                float kl2[8], kh2[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) { kl2[e] = klo[e]; kh2[e] = khi[e]; }
+                norm_rope16(kl2, kh2, kwl, kwh, co, sn, p.eps);
+                n0 = u32x4{pack_h2(kl2[0], kl2[1]), pack_h2(kl2[2], kl2[3]), pack_h2(kl2[4], kl2[5]),
+                           pack_h2(kl2[6], kl2[7])};
+                n1 = u32x4{pack_h2(kh2[0], kh2[1]), pack_h2(kh2[2], kh2[3]), pack_h2(kh2[4], kh2[5]),
+                           pack_h2(kh2[6], kh2[7])};
+                const uint32_t vnew = pack_h2(vn0, vn1);
+                vnew4 = u32x4{pack_h2(vn8[0], vn8[1]), pack_h2(vn8[2], vn8[3]), pack_h2(vn8[4], vn8[5]),
+                              pack_h2(vn8[6], vn8[7])};
+                inew = posv - tws;
+                // logicalTokenToPhysicalToken for the new position, from the
+                // page entries of this range (the position lies in page
+                // pgbs + 0..2); the host has checked the context length, an
+                // unmapped slot is skipped
+                const uint32_t slot = posv / 16, pi = slot - pgbs;
+                const uint32_t pg = pi == 0 ? pg0 : pi == 1 ? pg1 : pg2;
+                uint32_t ph = slot < p.n_pages ? pg * 16 + posv % 16 : p.cache_tokens;
+                if (ph < p.cache_tokens) {
+                    if (grp == (inew & 7)) {
+                        *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + sub * 8) = n0;
+                        *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 64 + sub * 8) = n1;
+                    }
+                    *(uint32_t *)(p.vc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 2 * lane) = vnew;
+                }
+            }
+        }
+        if (sc_i == 0) TRACE_OPS(1);
+
+        // ---- scores: token 8j + grp, 16 dims per lane, reduced over 8 lanes
+        float sc[AD_TW / 8][G];
+#pragma unroll
+        for (int j = 0; j < AD_TW / 8; j++) {
+            const bool sel = owner && (uint32_t)(8 * j) + grp == inew;
+            const u32x4 k0 = sel ? n0 : kr[j][0], k1 = sel ? n1 : kr[j][1];
+            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            float kf[16];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                kf[2 * e] = h2f(kw[e]);
+                kf[2 * e + 1] = h2f(kw[e] >> 16);
+            }
+            const bool valid = (uint32_t)(8 * j) + grp < nts;
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float sacc = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    sacc = fmaf(qlo[g][e], kf[e], sacc);
+                    sacc = fmaf(qhi[g][e], kf[8 + e], sacc);
+                }
+                sacc = sum8(sacc) * p.scale;  // dot * scale, as cpuAttention
+                sc[j][g] = valid ? sacc : -INFINITY;
+            }
+        }
+        if (sc_i == 0) TRACE_OPS(2);
+        if (sc_i + 1 < nsub) {
+            asm volatile("" ::: "memory");
+            load_k(sc_i + 1);
+            asm volatile("" ::: "memory");
+        }
+        // ---- online softmax: new running maximum, rescale the old state
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const float q = ps[wave][g][i];
+            float m = sc[0][g];
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] = fmaf(q, vf[e], acc[g][e]);
+            for (int j = 1; j < AD_TW / 8; j++) m = fmaxf(m, sc[j][g]);
+            m = rows_max(fmaxf(m, dpp_f<0x140>(m)));  // m is uniform within each 8-lane token group
+            const float mn = fmaxf(m_run[g], m);
+            const float ms = mn == -INFINITY ? 0.f : mn;  // no valid token yet
+            const float f = m_run[g] == -INFINITY ? 0.f : expf(m_run[g] - ms);
+            float l = 0.f;
+#pragma unroll
+            for (int j = 0; j < AD_TW / 8; j++) {
+                const float pr = expf(sc[j][g] - ms);
+                if (sub == 0) ps[wave][g][8 * j + grp] = pr;
+                l += pr;
+            }
+            l = rows_sum(l + dpp_f<0x140>(l));
+            l_run[g] = fmaf(l_run[g], f, l);
+            m_run[g] = mn;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[g][e] *= f;
         }
+        __syncthreads();
+        if (sc_i == 0) TRACE_OPS(8);
+#pragma unroll
+        for (int k = 0; k < AD_TW / 4; k++) {
+            const uint32_t i = 4 * k + vrow;
+            u32x4 v = owner && i == inew ? vnew4 : vr[k];
+            if (i >= nts) v = u32x4{0, 0, 0, 0};  // rows past the end may hold anything
+            const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+            float vf[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                vf[2 * e] = h2f(vw[e]);
+                vf[2 * e + 1] = h2f(vw[e] >> 16);
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float q = ps[wave][g][i];
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[g][e] = fmaf(q, vf[e], acc[g][e]);
+            }
+        }
+        if (sc_i + 1 < nsub) {
+            asm volatile("" ::: "memory");
+            load_v(sc_i + 1);
+            asm volatile("" ::: "memory");
+        }
+        __syncthreads();  // ps is rewritten by the next sub-chunk
     }
 #pragma unroll
     for (int g = 0; g < G; g++) {
+        if (lane == 0) { wm[wave][g] = m_run[g]; wl[wave][g] = l_run[g]; }
         *(f32x4 *)&wo[wave][vrow][g][8 * vcol] = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
         *(f32x4 *)&wo[wave][vrow][g][8 * vcol + 4] = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
     }
-    (void)mx;
     __syncthreads();
     TRACE_OPS(9);
     // ---- combine the 4 waves: per-head weights once, then thread -> (head, dim)
@@ -748,6 +816,9 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
     AttnP p = p0;
     p.nd = attn_nd(nkv, c->cu_count);
     p.n_chunks = attn_n_chunks(max_seq, p.nd);
+    // identity pages: at most 2 nd chunks per kv head at any context (longer
+    // chunks hold several sub-chunks)
+    if (ident && G <= 4 && p.n_chunks > 2 * p.nd) p.n_chunks = 2 * p.nd;
     dim3 grid(nkv, p.n_chunks);
     // one workgroup per CU: a grid within the CU count is resident at once
     const bool rev = (uint64_t)nkv * p.n_chunks > (uint64_t)c->cu_count;
