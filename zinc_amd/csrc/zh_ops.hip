@@ -228,12 +228,12 @@ constexpr int AD_TC = AD_W * AD_TW;  // tokens per chunk (at most)
 // chunks of all kv heads cover the device once (32 per head for 8 kv heads:
 // one XCD each).
 enum { AD_PAGED = 0, AD_PAGED_REV = 1, AD_IDENT = 2 };
-// Longer contexts: up to 2 nd chunks of 160 tokens, then chunks of nsub
-// consecutive 160-token sub-chunks (a workgroup runs them in turn with an
-// online softmax), so a kv head never has more than 2 nd chunks: the grid
-// stays one round of two workgroups per CU and the merge reads 2 nd partials.
+// Longer contexts: chunks of nsub consecutive 160-token sub-chunks (a
+// workgroup runs them in turn with an online softmax), so a kv head never has
+// more than nd chunks: the grid stays one round of one workgroup per CU (the
+// kernel's registers allow one) and the merge reads at most nd partials.
 ZH_DEV uint32_t attn_nsub(uint32_t seq, uint32_t nd) {
-    const uint32_t span = 2 * nd * AD_TC;
+    const uint32_t span = nd * AD_TC;
     return seq > span ? (seq + span - 1) / span : 1u;
 }
 ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq, uint32_t nd, bool sub) {
@@ -816,9 +816,9 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
     AttnP p = p0;
     p.nd = attn_nd(nkv, c->cu_count);
     p.n_chunks = attn_n_chunks(max_seq, p.nd);
-    // identity pages: at most 2 nd chunks per kv head at any context (longer
+    // identity pages: at most nd chunks per kv head at any context (longer
     // chunks hold several sub-chunks)
-    if (ident && G <= 4 && p.n_chunks > 2 * p.nd) p.n_chunks = 2 * p.nd;
+    if (ident && G <= 4 && p.n_chunks > p.nd) p.n_chunks = p.nd;
     dim3 grid(nkv, p.n_chunks);
     // one workgroup per CU: a grid within the CU count is resident at once
     const bool rev = (uint64_t)nkv * p.n_chunks > (uint64_t)c->cu_count;
