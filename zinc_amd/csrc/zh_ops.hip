@@ -522,13 +522,9 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     }
     // Memory returns in issue order: keep the compiler from interleaving or
     // sinking the groups (q / new token / RoPE first, then K, then V), so the
-    // q preparation waits only for its own loads.
+    // q preparation (after the K and V loads are issued) waits only for its
+    // own loads.
     asm volatile("" ::: "memory");
-    // ---- q preparation (once per workgroup)
-    if (FUSED) {
-#pragma unroll
-        for (int g = 0; g < G; g++) norm_rope16(qlo[g], qhi[g], qwl, qwh, co, sn, p.eps);
-    }
     __shared__ float ps[AD_W][G][AD_TW];
     __shared__ float wm[AD_W][G], wl[AD_W][G];
     __shared__ float wo[AD_W][4][G][FD_HD];  // per wave and token row
@@ -589,50 +585,61 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     asm volatile("" ::: "memory");
     load_v(0);
     asm volatile("" ::: "memory");
-    for (uint32_t sc_i = 0; sc_i < nsub; sc_i++) {  // uniform over the workgroup
-        const uint32_t tws = tw0 + sc_i * AD_TC;
-        const uint32_t nts = seq > tws ? min(seq - tws, wtok) : 0u;
-        uint32_t pg0, pg1, pg2, pgbs;
-        pages_of(sc_i, pg0, pg1, pg2, pgbs);
-
-        // ---- the new token (its position lies in exactly one wave's range)
-        bool owner = false;  // uniform per wave
-        uint32_t inew = 0;
-        u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0}, vnew4 = {0, 0, 0, 0};
-        if (FUSED) {
-            owner = posv >= tws && posv < tws + wtok;
-            if (owner) {
-                // the cache rows loaded above for this position predate the
-                // write below; scores and P*V select these values for it instead
-                float kl2[8], kh2[8];
+    // ---- q preparation (once per workgroup), while K and V are in flight
+    if (FUSED) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) { kl2[e] = klo[e]; kh2[e] = khi[e]; }
-                norm_rope16(kl2, kh2, kwl, kwh, co, sn, p.eps);
-                n0 = u32x4{pack_h2(kl2[0], kl2[1]), pack_h2(kl2[2], kl2[3]), pack_h2(kl2[4], kl2[5]),
-                           pack_h2(kl2[6], kl2[7])};
-                n1 = u32x4{pack_h2(kh2[0], kh2[1]), pack_h2(kh2[2], kh2[3]), pack_h2(kh2[4], kh2[5]),
-                           pack_h2(kh2[6], kh2[7])};
-                const uint32_t vnew = pack_h2(vn0, vn1);
-                vnew4 = u32x4{pack_h2(vn8[0], vn8[1]), pack_h2(vn8[2], vn8[3]), pack_h2(vn8[4], vn8[5]),
-                              pack_h2(vn8[6], vn8[7])};
-                inew = posv - tws;
-                // logicalTokenToPhysicalToken for the new position, from the
-                // page entries of this range (the position lies in page
-                // pgbs + 0..2); the host has checked the context length, an
-                // unmapped slot is skipped
-                const uint32_t slot = posv / 16, pi = slot - pgbs;
-                const uint32_t pg = pi == 0 ? pg0 : pi == 1 ? pg1 : pg2;
-                uint32_t ph = slot < p.n_pages ? pg * 16 + posv % 16 : p.cache_tokens;
-                if (ph < p.cache_tokens) {
-                    if (grp == (inew & 7)) {
-                        *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + sub * 8) = n0;
-                        *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 64 + sub * 8) = n1;
-                    }
-                    *(uint32_t *)(p.vc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 2 * lane) = vnew;
+        for (int g = 0; g < G; g++) norm_rope16(qlo[g], qhi[g], qwl, qwh, co, sn, p.eps);
+    }
+
+    // ---- the new token: its position lies in exactly one wave's range of
+    // one sub-chunk (s_own); that wave writes it to the cache here, once, and
+    // its scores and P*V select these values for it instead of the cache rows
+    // loaded for that position (which predate the write)
+    uint32_t s_own = ~0u, inew = 0;  // uniform per wave
+    u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0}, vnew4 = {0, 0, 0, 0};
+    if (FUSED && posv >= tw0) {
+        const uint32_t rel = posv - tw0;
+        if (rel % AD_TC < wtok && rel / AD_TC < nsub) {
+            s_own = rel / AD_TC;
+            inew = rel % AD_TC;
+            norm_rope16(klo, khi, kwl, kwh, co, sn, p.eps);
+            n0 = u32x4{pack_h2(klo[0], klo[1]), pack_h2(klo[2], klo[3]), pack_h2(klo[4], klo[5]),
+                       pack_h2(klo[6], klo[7])};
+            n1 = u32x4{pack_h2(khi[0], khi[1]), pack_h2(khi[2], khi[3]), pack_h2(khi[4], khi[5]),
+                       pack_h2(khi[6], khi[7])};
+            const uint32_t vnew = pack_h2(vn0, vn1);
+            vnew4 = u32x4{pack_h2(vn8[0], vn8[1]), pack_h2(vn8[2], vn8[3]), pack_h2(vn8[4], vn8[5]),
+                          pack_h2(vn8[6], vn8[7])};
+            // logicalTokenToPhysicalToken for the new position, from the page
+            // entries of its sub-chunk (the position lies in page pgbs + 0..2);
+            // the host has checked the context length, an unmapped slot is
+            // skipped
+            uint32_t pg0, pg1, pg2, pgbs;
+            pages_of(s_own, pg0, pg1, pg2, pgbs);
+            const uint32_t slot = posv / 16, pi = slot - pgbs;
+            const uint32_t pg = pi == 0 ? pg0 : pi == 1 ? pg1 : pg2;
+            const uint32_t ph = slot < p.n_pages ? pg * 16 + posv % 16 : p.cache_tokens;
+            if (ph < p.cache_tokens) {
+                if (grp == (inew & 7)) {
+                    *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + sub * 8) = n0;
+                    *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 64 + sub * 8) = n1;
                 }
+                *(uint32_t *)(p.vc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 2 * lane) = vnew;
             }
         }
-        if (sc_i == 0) TRACE_OPS(1);
+    }
+    TRACE_OPS(1);
+
+    // One sub-chunk. PF: the next sub-chunk's K loads go out once this one's
+    // scores are computed, its V loads once this one's P*V is done. The loads
+    // are unconditional inside the loop (the last sub-chunk is peeled off), so
+    // the compiler's waits count exactly the loads in flight: the scores wait
+    // for this sub-chunk's K only, P*V for its V only.
+    auto body = [&](uint32_t sc_i, auto pf) __attribute__((always_inline)) {
+        constexpr bool PF = decltype(pf)::value;
+        const uint32_t tws = tw0 + sc_i * AD_TC;
+        const uint32_t nts = seq > tws ? min(seq - tws, wtok) : 0u;
+        const bool owner = sc_i == s_own;  // uniform per wave
 
         // ---- scores: token 8j + grp, 16 dims per lane, reduced over 8 lanes
         float sc[AD_TW / 8][G];
@@ -661,7 +668,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
             }
         }
         if (sc_i == 0) TRACE_OPS(2);
-        if (sc_i + 1 < nsub) {
+        if (PF) {
             asm volatile("" ::: "memory");
             load_k(sc_i + 1);
             asm volatile("" ::: "memory");
@@ -710,13 +717,17 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
                 for (int e = 0; e < 8; e++) acc[g][e] = fmaf(q, vf[e], acc[g][e]);
             }
         }
-        if (sc_i + 1 < nsub) {
+        if (PF) {
             asm volatile("" ::: "memory");
             load_v(sc_i + 1);
             asm volatile("" ::: "memory");
         }
         __syncthreads();  // ps is rewritten by the next sub-chunk
+    };
+    if (SUB) {
+        for (uint32_t sc_i = 0; sc_i + 1 < nsub; sc_i++) body(sc_i, std::true_type{});  // uniform
     }
+    body(nsub - 1, std::false_type{});
 #pragma unroll
     for (int g = 0; g < G; g++) {
         if (lane == 0) { wm[wave][g] = m_run[g]; wl[wave][g] = l_run[g]; }
