@@ -32,7 +32,13 @@ enum {
     ZH_ERR_HIP = 3,                    /* device/runtime failure */
     ZH_ERR_CONTEXT_LENGTH_EXCEEDED = 4,/* error.ContextLengthExceeded forward.zig:4300 */
     ZH_ERR_OUT_OF_MEMORY = 5,
-    ZH_ERR_TENSOR_NOT_FOUND = 6        /* error.TensorNotFound        forward.zig:7377 */
+    ZH_ERR_TENSOR_NOT_FOUND = 6,       /* error.TensorNotFound        forward.zig:7377 */
+    ZH_ERR_INVALID_MAGIC = 7,          /* error.InvalidMagic          gguf.zig:347 */
+    ZH_ERR_UNKNOWN_METADATA_TYPE = 8,  /* error.UnknownMetadataType   gguf.zig:513,540 */
+    ZH_ERR_UNSUPPORTED_ARCHITECTURE = 9,/* error.UnsupportedArchitecture loader.zig:449 */
+    ZH_ERR_TRUNCATED_FILE = 10,        /* a header or tensor runs past the end of the file */
+    ZH_ERR_IO = 11,                    /* open / stat / mmap failure (std.fs errors) */
+    ZH_ERR_NOT_FOUND = 12              /* metadata key absent or not of the asked type (null) */
 };
 
 /* ---- GGMLType values used on the path (src/model/gguf.zig:38-69) -------- */
@@ -185,6 +191,11 @@ typedef struct zh_model_config {
     uint32_t type_attn, type_ffn_gate_up, type_ffn_down, type_lm_head, type_embd, type_router;
     float rope_base, eps;
     uint64_t seed;                                  /* synthetic weights seed */
+    /* 0: off. Else the layers llama.cpp's Q4_K_M / Q5_K_M recipe gives more
+     * bits (use_more_bits: the first and last eighth of the layers and every
+     * third layer between) hold attn_v and ffn_down (dense or expert) in this
+     * type; the other layers use type_attn / type_ffn_down. */
+    uint32_t type_more_bits, reserved;
 } zh_model_config;
 
 /* InferenceEngine.init (forward.zig:1226) on a seeded random-init model whose
@@ -224,6 +235,64 @@ int zh_engine_read_kv(zh_engine *eng, uint32_t layer, uint32_t which, uint32_t t
 /* Model bytes touched per decoded token at context length L (weights + fp16
  * KV + activations), the numerator of the bandwidth roofline. */
 uint64_t zh_engine_bytes_per_token(zh_engine *eng, uint32_t L);
+
+/* ---- GGUF model files: src/model/gguf.zig (parse) and src/model/loader.zig
+ *      (extractConfig, load) --------------------------------------------- */
+typedef struct zh_gguf zh_gguf;
+/* Metadata value tags (GGUFType, gguf.zig:20-35). */
+enum { ZH_GGUF_U8 = 0, ZH_GGUF_I8 = 1, ZH_GGUF_U16 = 2, ZH_GGUF_I16 = 3, ZH_GGUF_U32 = 4, ZH_GGUF_I32 = 5,
+       ZH_GGUF_F32 = 6, ZH_GGUF_BOOL = 7, ZH_GGUF_STRING = 8, ZH_GGUF_ARRAY = 9, ZH_GGUF_U64 = 10,
+       ZH_GGUF_I64 = 11, ZH_GGUF_F64 = 12 };
+/* gguf.parse over a read-only private mmap of `path` (loader.zig:420-445,
+ * gguf.zig:340-419): header, metadata map, tensor table; tensor data starts at
+ * the next general.alignment boundary (default 32). Unlike the reference,
+ * every read is bounds-checked: ZH_ERR_TRUNCATED_FILE instead of a fault. */
+int  zh_gguf_open(const char *path, zh_gguf **out);
+void zh_gguf_close(zh_gguf *f);
+const char *zh_gguf_last_error(const zh_gguf *f);  /* detail of the last failure on f (or of open) */
+uint32_t zh_gguf_version(const zh_gguf *f);
+uint64_t zh_gguf_tensor_count(const zh_gguf *f);
+uint64_t zh_gguf_metadata_count(const zh_gguf *f);
+uint64_t zh_gguf_data_offset(const zh_gguf *f);    /* tensor_data_offset */
+const void *zh_gguf_data(const zh_gguf *f);        /* the mapped file */
+uint64_t zh_gguf_file_size(const zh_gguf *f);
+/* Tensor i of the table: name (NUL-terminated, owned by f), n_dims, dims[4]
+ * (unused dims 1), GGMLType, offset in the data section and sizeBytes
+ * (gguf.zig:222-229; ZH_ERR_UNSUPPORTED_QUANT_TYPE for a type without a
+ * block size). */
+int zh_gguf_tensor_info(const zh_gguf *f, uint64_t i, const char **name, uint32_t *n_dims, uint64_t *dims,
+                        uint32_t *type, uint64_t *offset, uint64_t *bytes);
+/* findTensor (gguf.zig:305-310): index, or -1. */
+int64_t zh_gguf_find_tensor(const zh_gguf *f, const char *name);
+/* Metadata lookups with the reference's conversions (MetadataValue.asU32 /
+ * asU64 / asF32 / asBool / asString, gguf.zig:143-193); ZH_ERR_NOT_FOUND when
+ * the key is absent or the value does not convert (the reference's null). */
+int zh_gguf_get_u32(const zh_gguf *f, const char *key, uint32_t *v);
+int zh_gguf_get_u64(const zh_gguf *f, const char *key, uint64_t *v);
+int zh_gguf_get_f32(const zh_gguf *f, const char *key, float *v);
+int zh_gguf_get_bool(const zh_gguf *f, const char *key, int *v);
+int zh_gguf_get_string(const zh_gguf *f, const char *key, const char **s, uint64_t *len);
+/* Metadata entry i: key, value tag, and for arrays the element tag and count. */
+int zh_gguf_metadata_entry(const zh_gguf *f, uint64_t i, const char **key, uint32_t *type, uint32_t *elem_type,
+                           uint64_t *count);
+/* extractConfig (loader.zig:81-346) for the families on the path (qwen2 /
+ * qwen3 dense, qwen2moe / qwen3moe): dimensions, eps, rope base, experts,
+ * vocab (metadata, else output.weight / token_embd.weight rows), with the
+ * per-class types read from blk.0's tensors (type_more_bits 0: the engine
+ * takes each tensor's own type from the file). max_ctx is the caller's KV
+ * capacity (rounded up to 16 tokens). Other architectures:
+ * ZH_ERR_UNSUPPORTED_ARCHITECTURE. */
+int zh_gguf_model_config(const zh_gguf *f, uint32_t max_ctx, zh_model_config *cfg);
+/* loader.load + InferenceEngine.init (loader.zig:414-486, forward.zig:1226):
+ * an engine whose weights are the file's tensors, each uploaded to the device
+ * in its own storage type (a Q4_K_M file's Q6_K attn_v / ffn_down layers
+ * included). Missing tensors: ZH_ERR_TENSOR_NOT_FOUND; a tensor whose shape
+ * differs from the config: ZH_ERR_INVALID_ARGUMENT; a format the kernels do
+ * not take: ZH_ERR_UNSUPPORTED_QUANT_TYPE. Without output.weight the LM head
+ * reads token_embd.weight (tied embeddings). */
+int zh_engine_create_gguf(zh_ctx *ctx, const zh_gguf *f, uint32_t max_ctx, zh_engine **out);
+/* The storage type of an engine tensor (by stream id, as zh_engine_tensor). */
+int zh_engine_tensor_type(zh_engine *eng, uint64_t stream, uint32_t *type);
 
 /* Measurement entries (no counterpart in the reference; the benchmark uses
  * them for per-kernel bandwidth). A launch group is one per-layer stage of

@@ -78,6 +78,9 @@ def lib():
             "zo_model_prefill_kv_random": (None, [C.c_void_p, C.c_uint32, C.c_uint64]),
             "zo_model_decode_step": (C.c_uint32, [C.c_void_p, C.c_uint32, C.c_uint32, f32p]),
             "zo_model_tensor": (C.c_void_p, [C.c_void_p, C.c_uint64, C.POINTER(C.c_uint64)]),
+            "zo_model_tensor_type": (C.c_int, [C.c_void_p, C.c_uint64]),
+            "zo_model_set_tensor": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_uint64]),
+            "zo_more_bits_layer": (C.c_int, [C.c_uint32, C.c_uint32]),
             "zo_model_hidden": (C.c_void_p, [C.c_void_p]),
             "zo_model_kv": (C.c_void_p, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32]),
         }
@@ -266,7 +269,8 @@ class ModelConfig(C.Structure):
         "n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab",
         "n_experts", "n_experts_used", "expert_ffn", "max_ctx",
         "type_attn", "type_ffn_gate_up", "type_ffn_down", "type_lm_head", "type_embd",
-        "type_router")] + [("rope_base", C.c_float), ("eps", C.c_float), ("seed", C.c_uint64)]
+        "type_router")] + [("rope_base", C.c_float), ("eps", C.c_float), ("seed", C.c_uint64),
+                            ("type_more_bits", C.c_uint32), ("reserved", C.c_uint32)]
 
 
 class Model:
@@ -300,6 +304,16 @@ class Model:
         if not p:
             return None
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), shape=(n.value,)).copy()
+
+    def tensor_type(self, stream):
+        return lib().zo_model_tensor_type(self.h, stream)
+
+    def set_tensor(self, stream, qtype, data):
+        """Replace a weight (data: its bytes in storage type qtype)."""
+        a = np.ascontiguousarray(np.frombuffer(memoryview(data).cast("B"), dtype=np.uint8))
+        rc = lib().zo_model_set_tensor(self.h, stream, qtype, C.c_void_p(a.ctypes.data), a.size)
+        if rc != 0:
+            raise ValueError(f"zo_model_set_tensor(stream {stream:#x}, type {qtype}, {a.size} B): {rc}")
 
     def kv(self, layer, which, token):
         """fp16 bits of the K (which=0) or V (1) cache row of `token`."""

@@ -518,6 +518,7 @@ enum { ZK_ATTN_NORM = 1, ZK_WQ, ZK_WK, ZK_WV, ZK_WO, ZK_Q_NORM, ZK_K_NORM, ZK_FF
 #define ZS_KV(l, which) (0x100000ull + 2ull * (l) + (which))
 
 typedef struct {
+    uint32_t t[16]; /* storage type of each tensor kind (ZK_*) in this layer */
     uint8_t *wq, *wk, *wv, *wo, *gate, *up, *down, *router, *egate, *eup, *edown;
     float *attn_norm, *q_norm, *k_norm, *ffn_norm;
     uint16_t *kc, *vc; /* [max_ctx][kv_dim] fp16, logical == physical (identity pages) */
@@ -526,6 +527,7 @@ typedef struct {
 struct zo_model {
     zo_model_config c;
     int nthreads;
+    uint32_t t_embd, t_lm; /* storage types of token_embd and output */
     uint8_t *embd, *lm;
     float *out_norm, *inv_freq;
     zo_layer *L;
@@ -543,6 +545,10 @@ static float *alloc_norm(uint64_t n, uint64_t seed, uint64_t stream) {
     return p;
 }
 
+int zo_more_bits_layer(uint32_t i, uint32_t n) {
+    return i < n / 8 || i >= 7 * n / 8 || (i - n / 8) % 3 == 2;
+}
+
 typedef struct { zo_model *m; uint32_t l0, l1; } build_job;
 static void build_layer(zo_model *m, uint32_t l) {
     zo_model_config *c = &m->c;
@@ -550,23 +556,29 @@ static void build_layer(zo_model *m, uint32_t l) {
     uint32_t H = c->hidden, qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
     zo_layer *y = &m->L[l];
     memset(y, 0, sizeof(*y));
+    const int more = c->type_more_bits && zo_more_bits_layer(l, c->n_layers);
+    y->t[ZK_WQ] = y->t[ZK_WK] = y->t[ZK_WO] = c->type_attn;
+    y->t[ZK_WV] = more ? c->type_more_bits : c->type_attn;
+    y->t[ZK_GATE] = y->t[ZK_UP] = y->t[ZK_EXP_GATE] = y->t[ZK_EXP_UP] = c->type_ffn_gate_up;
+    y->t[ZK_DOWN] = y->t[ZK_EXP_DOWN] = more ? c->type_more_bits : c->type_ffn_down;
+    y->t[ZK_ROUTER] = c->type_router;
     y->attn_norm = alloc_norm(H, s, ZS_LAYER(l, ZK_ATTN_NORM));
-    y->wq = alloc_tensor(c->type_attn, qd, H, s, ZS_LAYER(l, ZK_WQ));
-    y->wk = alloc_tensor(c->type_attn, kvd, H, s, ZS_LAYER(l, ZK_WK));
-    y->wv = alloc_tensor(c->type_attn, kvd, H, s, ZS_LAYER(l, ZK_WV));
-    y->wo = alloc_tensor(c->type_attn, H, qd, s, ZS_LAYER(l, ZK_WO));
+    y->wq = alloc_tensor(y->t[ZK_WQ], qd, H, s, ZS_LAYER(l, ZK_WQ));
+    y->wk = alloc_tensor(y->t[ZK_WK], kvd, H, s, ZS_LAYER(l, ZK_WK));
+    y->wv = alloc_tensor(y->t[ZK_WV], kvd, H, s, ZS_LAYER(l, ZK_WV));
+    y->wo = alloc_tensor(y->t[ZK_WO], H, qd, s, ZS_LAYER(l, ZK_WO));
     y->q_norm = alloc_norm(c->head_dim, s, ZS_LAYER(l, ZK_Q_NORM));
     y->k_norm = alloc_norm(c->head_dim, s, ZS_LAYER(l, ZK_K_NORM));
     y->ffn_norm = alloc_norm(H, s, ZS_LAYER(l, ZK_FFN_NORM));
     if (c->n_experts == 0) {
-        y->gate = alloc_tensor(c->type_ffn_gate_up, c->ffn, H, s, ZS_LAYER(l, ZK_GATE));
-        y->up = alloc_tensor(c->type_ffn_gate_up, c->ffn, H, s, ZS_LAYER(l, ZK_UP));
-        y->down = alloc_tensor(c->type_ffn_down, H, c->ffn, s, ZS_LAYER(l, ZK_DOWN));
+        y->gate = alloc_tensor(y->t[ZK_GATE], c->ffn, H, s, ZS_LAYER(l, ZK_GATE));
+        y->up = alloc_tensor(y->t[ZK_UP], c->ffn, H, s, ZS_LAYER(l, ZK_UP));
+        y->down = alloc_tensor(y->t[ZK_DOWN], H, c->ffn, s, ZS_LAYER(l, ZK_DOWN));
     } else {
-        y->router = alloc_tensor(c->type_router, c->n_experts, H, s, ZS_LAYER(l, ZK_ROUTER));
-        y->egate = alloc_tensor(c->type_ffn_gate_up, (uint64_t)c->n_experts * c->expert_ffn, H, s, ZS_LAYER(l, ZK_EXP_GATE));
-        y->eup = alloc_tensor(c->type_ffn_gate_up, (uint64_t)c->n_experts * c->expert_ffn, H, s, ZS_LAYER(l, ZK_EXP_UP));
-        y->edown = alloc_tensor(c->type_ffn_down, (uint64_t)c->n_experts * H, c->expert_ffn, s, ZS_LAYER(l, ZK_EXP_DOWN));
+        y->router = alloc_tensor(y->t[ZK_ROUTER], c->n_experts, H, s, ZS_LAYER(l, ZK_ROUTER));
+        y->egate = alloc_tensor(y->t[ZK_EXP_GATE], (uint64_t)c->n_experts * c->expert_ffn, H, s, ZS_LAYER(l, ZK_EXP_GATE));
+        y->eup = alloc_tensor(y->t[ZK_EXP_UP], (uint64_t)c->n_experts * c->expert_ffn, H, s, ZS_LAYER(l, ZK_EXP_UP));
+        y->edown = alloc_tensor(y->t[ZK_EXP_DOWN], (uint64_t)c->n_experts * H, c->expert_ffn, s, ZS_LAYER(l, ZK_EXP_DOWN));
     }
     y->kc = (uint16_t *)calloc((size_t)c->max_ctx * kvd, 2);
     y->vc = (uint16_t *)calloc((size_t)c->max_ctx * kvd, 2);
@@ -583,6 +595,8 @@ zo_model *zo_model_create(const zo_model_config *cfg, int nthreads) {
     m->nthreads = nthreads < 1 ? 1 : nthreads;
     zo_model_config *c = &m->c;
     uint32_t H = c->hidden;
+    m->t_embd = c->type_embd;
+    m->t_lm = c->type_lm_head;
     m->embd = alloc_tensor(c->type_embd, c->vocab, H, c->seed, ZS_TOKEN_EMBD);
     m->out_norm = alloc_norm(H, c->seed, ZS_OUTPUT_NORM);
     m->lm = alloc_tensor(c->type_lm_head, c->vocab, H, c->seed, ZS_OUTPUT);
@@ -638,29 +652,76 @@ void zo_model_prefill_kv_random(zo_model *m, uint32_t n, uint64_t seed) {
     }
 }
 
-const uint8_t *zo_model_tensor(zo_model *m, uint64_t stream, uint64_t *bytes) {
+/* The storage slot of a tensor: its data pointer, storage type (NULL for
+ * the f32 norm weights) and shape. Returns 0 when the model has no such
+ * tensor. */
+static int tensor_slot(zo_model *m, uint64_t stream, uint8_t ***data, uint32_t **type, uint64_t *rows,
+                       uint64_t *cols) {
     zo_model_config *c = &m->c;
-    uint32_t H = c->hidden, qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
-    if (stream == ZS_TOKEN_EMBD) { *bytes = zo_tensor_bytes(c->type_embd, c->vocab, H); return m->embd; }
-    if (stream == ZS_OUTPUT) { *bytes = zo_tensor_bytes(c->type_lm_head, c->vocab, H); return m->lm; }
-    if (stream == ZS_OUTPUT_NORM) { *bytes = (uint64_t)H * 4; return (const uint8_t *)m->out_norm; }
+    uint64_t H = c->hidden, qd = (uint64_t)c->n_heads * c->head_dim, kvd = (uint64_t)c->n_kv_heads * c->head_dim;
+    uint64_t E = c->n_experts, F = c->expert_ffn;
+    *type = NULL;
+    if (stream == ZS_TOKEN_EMBD) { *data = &m->embd; *type = &m->t_embd; *rows = c->vocab; *cols = H; return 1; }
+    if (stream == ZS_OUTPUT) { *data = &m->lm; *type = &m->t_lm; *rows = c->vocab; *cols = H; return 1; }
+    if (stream == ZS_OUTPUT_NORM) { *data = (uint8_t **)&m->out_norm; *rows = 1; *cols = H; return 1; }
     uint64_t l = (stream >> 8) - 1, kind = stream & 0xFF;
-    if (l >= c->n_layers) { *bytes = 0; return NULL; }
+    if (stream <= 0xFF || l >= c->n_layers || kind == 0 || kind > ZK_EXP_DOWN) return 0;
     zo_layer *y = &m->L[l];
+    const int dense = E == 0;
     switch (kind) {
-    case ZK_WQ: *bytes = zo_tensor_bytes(c->type_attn, qd, H); return y->wq;
-    case ZK_WK: *bytes = zo_tensor_bytes(c->type_attn, kvd, H); return y->wk;
-    case ZK_WV: *bytes = zo_tensor_bytes(c->type_attn, kvd, H); return y->wv;
-    case ZK_WO: *bytes = zo_tensor_bytes(c->type_attn, H, qd); return y->wo;
-    case ZK_GATE: *bytes = y->gate ? zo_tensor_bytes(c->type_ffn_gate_up, c->ffn, H) : 0; return y->gate;
-    case ZK_UP: *bytes = y->up ? zo_tensor_bytes(c->type_ffn_gate_up, c->ffn, H) : 0; return y->up;
-    case ZK_DOWN: *bytes = y->down ? zo_tensor_bytes(c->type_ffn_down, H, c->ffn) : 0; return y->down;
-    case ZK_ATTN_NORM: *bytes = (uint64_t)H * 4; return (const uint8_t *)y->attn_norm;
-    case ZK_FFN_NORM: *bytes = (uint64_t)H * 4; return (const uint8_t *)y->ffn_norm;
-    case ZK_Q_NORM: *bytes = (uint64_t)c->head_dim * 4; return (const uint8_t *)y->q_norm;
-    case ZK_K_NORM: *bytes = (uint64_t)c->head_dim * 4; return (const uint8_t *)y->k_norm;
-    default: *bytes = 0; return NULL;
+    case ZK_ATTN_NORM: *data = (uint8_t **)&y->attn_norm; *rows = 1; *cols = H; return 1;
+    case ZK_FFN_NORM: *data = (uint8_t **)&y->ffn_norm; *rows = 1; *cols = H; return 1;
+    case ZK_Q_NORM: *data = (uint8_t **)&y->q_norm; *rows = 1; *cols = c->head_dim; return 1;
+    case ZK_K_NORM: *data = (uint8_t **)&y->k_norm; *rows = 1; *cols = c->head_dim; return 1;
+    case ZK_WQ: *data = &y->wq; *rows = qd; *cols = H; break;
+    case ZK_WK: *data = &y->wk; *rows = kvd; *cols = H; break;
+    case ZK_WV: *data = &y->wv; *rows = kvd; *cols = H; break;
+    case ZK_WO: *data = &y->wo; *rows = H; *cols = qd; break;
+    case ZK_GATE: if (!dense) return 0; *data = &y->gate; *rows = c->ffn; *cols = H; break;
+    case ZK_UP: if (!dense) return 0; *data = &y->up; *rows = c->ffn; *cols = H; break;
+    case ZK_DOWN: if (!dense) return 0; *data = &y->down; *rows = H; *cols = c->ffn; break;
+    case ZK_ROUTER: if (dense) return 0; *data = &y->router; *rows = E; *cols = H; break;
+    case ZK_EXP_GATE: if (dense) return 0; *data = &y->egate; *rows = E * F; *cols = H; break;
+    case ZK_EXP_UP: if (dense) return 0; *data = &y->eup; *rows = E * F; *cols = H; break;
+    case ZK_EXP_DOWN: if (dense) return 0; *data = &y->edown; *rows = E * H; *cols = F; break;
+    default: return 0;
     }
+    *type = &y->t[kind];
+    return 1;
+}
+
+const uint8_t *zo_model_tensor(zo_model *m, uint64_t stream, uint64_t *bytes) {
+    uint8_t **d;
+    uint32_t *t;
+    uint64_t rows, cols;
+    if (!tensor_slot(m, stream, &d, &t, &rows, &cols)) { *bytes = 0; return NULL; }
+    *bytes = t ? zo_tensor_bytes(*t, rows, cols) : rows * cols * 4;
+    return *d;
+}
+
+int zo_model_tensor_type(zo_model *m, uint64_t stream) {
+    uint8_t **d;
+    uint32_t *t;
+    uint64_t rows, cols;
+    if (!tensor_slot(m, stream, &d, &t, &rows, &cols)) return -1;
+    return t ? (int)*t : 0;
+}
+
+int zo_model_set_tensor(zo_model *m, uint64_t stream, uint32_t type, const void *src, uint64_t n) {
+    uint8_t **d;
+    uint32_t *t;
+    uint64_t rows, cols;
+    if (!tensor_slot(m, stream, &d, &t, &rows, &cols)) return -1;
+    if (!t && type != 0) return -2; /* norm weights stay f32 */
+    const uint64_t want = t ? zo_tensor_bytes(type, rows, cols) : rows * cols * 4;
+    if (want == 0 || n != want) return -3;
+    uint8_t *p = (uint8_t *)malloc(n);
+    if (!p) return -4;
+    memcpy(p, src, n);
+    free(*d);
+    *d = p;
+    if (t) *t = type;
+    return 0;
 }
 const float *zo_model_hidden(zo_model *m) { return m->hidden; }
 const uint16_t *zo_model_kv(zo_model *m, uint32_t layer, uint32_t which, uint32_t token) {
@@ -710,13 +771,13 @@ uint32_t zo_model_decode_step(zo_model *m, uint32_t token, uint32_t pos, float *
     if (pos >= c->max_ctx) return UINT32_MAX; /* ContextLengthExceeded, forward.zig:4300 */
     /* embedToken: forward.zig:4255-4290 (safe_id clamp) */
     uint32_t tid = token < c->vocab ? token : c->vocab - 1;
-    zo_dequant_row(m->embd, tid, H, c->type_embd, m->hidden);
+    zo_dequant_row(m->embd, tid, H, m->t_embd, m->hidden);
     for (uint32_t l = 0; l < c->n_layers; l++) {
         zo_layer *y = &m->L[l];
         zo_rms_norm_mul(m->hidden, y->attn_norm, H, m->norm, H, 1, c->eps);
-        zo_dmmv(y->wq, c->type_attn, m->norm, m->q, qd, H, 0, nt);
-        zo_dmmv(y->wk, c->type_attn, m->norm, m->k, kvd, H, 0, nt);
-        zo_dmmv(y->wv, c->type_attn, m->norm, m->v, kvd, H, 0, nt);
+        zo_dmmv(y->wq, y->t[ZK_WQ], m->norm, m->q, qd, H, 0, nt);
+        zo_dmmv(y->wk, y->t[ZK_WK], m->norm, m->k, kvd, H, 0, nt);
+        zo_dmmv(y->wv, y->t[ZK_WV], m->norm, m->v, kvd, H, 0, nt);
         zo_per_head_rms_norm(m->q, y->q_norm, hd, c->n_heads, c->eps);
         zo_per_head_rms_norm(m->k, y->k_norm, hd, c->n_kv_heads, c->eps);
         zo_rope(m->q, hd, hd, c->n_heads, pos, m->inv_freq);
@@ -737,28 +798,28 @@ uint32_t zo_model_decode_step(zo_model *m, uint32_t token, uint32_t pos, float *
             }
             for (int t = 0; t < ntt; t++) pthread_join(th[t], NULL);
         }
-        zo_dmmv(y->wo, c->type_attn, m->attn, m->hidden, H, qd, 1, nt);
+        zo_dmmv(y->wo, y->t[ZK_WO], m->attn, m->hidden, H, qd, 1, nt);
         zo_rms_norm_mul(m->hidden, y->ffn_norm, H, m->norm, H, 1, c->eps);
         if (c->n_experts == 0) {
-            zo_dmmv(y->gate, c->type_ffn_gate_up, m->norm, m->g, c->ffn, H, 0, nt);
-            zo_dmmv(y->up, c->type_ffn_gate_up, m->norm, m->u, c->ffn, H, 0, nt);
+            zo_dmmv(y->gate, y->t[ZK_GATE], m->norm, m->g, c->ffn, H, 0, nt);
+            zo_dmmv(y->up, y->t[ZK_UP], m->norm, m->u, c->ffn, H, 0, nt);
             zo_swiglu(m->g, m->u, m->s, c->ffn);
-            zo_dmmv(y->down, c->type_ffn_down, m->s, m->hidden, H, c->ffn, 1, nt);
+            zo_dmmv(y->down, y->t[ZK_DOWN], m->s, m->hidden, H, c->ffn, 1, nt);
         } else {
             /* MoE FFN: forward.zig:5958-6500 (router -> topKSoftmax -> experts -> weighted acc) */
             uint32_t ids[64];
             float w[64];
             uint32_t F = c->expert_ffn;
-            zo_dmmv(y->router, c->type_router, m->norm, m->rl, c->n_experts, H, 0, nt);
+            zo_dmmv(y->router, y->t[ZK_ROUTER], m->norm, m->rl, c->n_experts, H, 0, nt);
             zo_topk_softmax(m->rl, c->n_experts, c->n_experts_used, ids, w);
-            uint64_t gstride = zo_tensor_bytes(c->type_ffn_gate_up, F, H);
-            uint64_t dstride = zo_tensor_bytes(c->type_ffn_down, H, F);
+            uint64_t gstride = zo_tensor_bytes(y->t[ZK_EXP_GATE], F, H), ustride = zo_tensor_bytes(y->t[ZK_EXP_UP], F, H);
+            uint64_t dstride = zo_tensor_bytes(y->t[ZK_EXP_DOWN], H, F);
             float *dout = (float *)malloc((size_t)c->n_experts_used * H * 4);
             for (uint32_t j = 0; j < c->n_experts_used; j++) {
-                zo_dmmv(y->egate + ids[j] * gstride, c->type_ffn_gate_up, m->norm, m->g, F, H, 0, nt);
-                zo_dmmv(y->eup + ids[j] * gstride, c->type_ffn_gate_up, m->norm, m->u, F, H, 0, nt);
+                zo_dmmv(y->egate + ids[j] * gstride, y->t[ZK_EXP_GATE], m->norm, m->g, F, H, 0, nt);
+                zo_dmmv(y->eup + ids[j] * ustride, y->t[ZK_EXP_UP], m->norm, m->u, F, H, 0, nt);
                 zo_swiglu(m->g, m->u, m->s, F);
-                zo_dmmv(y->edown + ids[j] * dstride, c->type_ffn_down, m->s, dout + (size_t)j * H, H, F, 0, nt);
+                zo_dmmv(y->edown + ids[j] * dstride, y->t[ZK_EXP_DOWN], m->s, dout + (size_t)j * H, H, F, 0, nt);
             }
             /* moe_weighted_acc.comp:23-33: sum_j w_j*b_j then a += sum */
             for (uint32_t i = 0; i < H; i++) {
@@ -770,7 +831,7 @@ uint32_t zo_model_decode_step(zo_model *m, uint32_t token, uint32_t pos, float *
         }
     }
     zo_rms_norm_mul(m->hidden, m->out_norm, H, m->norm, H, 1, c->eps);
-    zo_dmmv(m->lm, c->type_lm_head, m->norm, m->logits, c->vocab, H, 0, nt);
+    zo_dmmv(m->lm, m->t_lm, m->norm, m->logits, c->vocab, H, 0, nt);
     if (logits_out) memcpy(logits_out, m->logits, (size_t)c->vocab * 4);
     return zo_argmax(m->logits, c->vocab);
 }

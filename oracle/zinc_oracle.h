@@ -108,7 +108,15 @@ typedef struct zo_model_config {
     uint32_t type_attn, type_ffn_gate_up, type_ffn_down, type_lm_head, type_embd, type_router;
     float rope_base, eps;
     uint64_t seed;
+    /* 0: off. Else the layers llama.cpp's Q4_K_M / Q5_K_M recipe gives more
+     * bits (use_more_bits: the first and last eighth of the layers and every
+     * third layer between) hold attn_v and ffn_down (dense or expert) in this
+     * type; the other layers use type_attn / type_ffn_down. */
+    uint32_t type_more_bits, reserved;
 } zo_model_config;
+/* use_more_bits(i_layer, n_layers) of llama.cpp's quantizer (the rule the
+ * Q4_K_M mix of GGUF files follows). */
+int zo_more_bits_layer(uint32_t i, uint32_t n);
 
 typedef struct zo_model zo_model;
 zo_model *zo_model_create(const zo_model_config *cfg, int nthreads);
@@ -120,6 +128,11 @@ void      zo_model_prefill_kv_random(zo_model *m, uint32_t n, uint64_t seed);
 uint32_t  zo_model_decode_step(zo_model *m, uint32_t token, uint32_t pos, float *logits);
 /* Raw access for tests: tensor bytes by stream id, hidden state after step. */
 const uint8_t *zo_model_tensor(zo_model *m, uint64_t stream, uint64_t *bytes);
+/* Storage type of a tensor (0 for the f32 norms), -1 if the model has none. */
+int       zo_model_tensor_type(zo_model *m, uint64_t stream);
+/* Replace a tensor's data and storage type (a weight loaded from a file):
+ * n must be its size in that type; 0 on success, < 0 on a mismatch. */
+int       zo_model_set_tensor(zo_model *m, uint64_t stream, uint32_t type, const void *src, uint64_t n);
 const float   *zo_model_hidden(zo_model *m);
 /* fp16 K (which 0) or V (1) cache row of `token` in `layer`: n_kv_heads*head_dim values. */
 const uint16_t *zo_model_kv(zo_model *m, uint32_t layer, uint32_t which, uint32_t token);

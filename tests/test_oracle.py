@@ -432,3 +432,40 @@ def test_centered_q4k_model_init_is_zero_mean(orc):
     dm = b[:, 2:4].copy().view(np.float16).ravel()
     assert np.array_equal(dm, (d * np.float32(7.5)).astype(np.float16))
     assert np.array_equal(b[:, 4:], W0.reshape(-1, 144)[:, 4:])  # scales and codes unchanged
+
+
+def test_more_bits_rule_counts(orc):
+    # llama.cpp's use_more_bits: the first and last eighth of the layers and
+    # every third layer between, i.e. half of a 32-layer model's attn_v /
+    # ffn_down (the Q4_K_M mix of 7B-class GGUF files: layers 0-3, 6, 9, ..,
+    # 27, 28-31)
+    L = orc.lib()
+    sel32 = [i for i in range(32) if L.zo_more_bits_layer(i, 32)]
+    assert sel32 == [0, 1, 2, 3, 6, 9, 12, 15, 18, 21, 24, 27, 28, 29, 30, 31]
+    sel36 = [i for i in range(36) if L.zo_more_bits_layer(i, 36)]
+    assert sel36[:4] == [0, 1, 2, 3] and sel36[-5:] == [31, 32, 33, 34, 35] and len(sel36) == 18
+
+
+def test_model_set_tensor_matches_more_bits_config(orc):
+    """A model whose more_bits layers were replaced tensor by tensor decodes
+    exactly as the model built with type_more_bits (same bytes, same types)."""
+    base = dict(n_layers=8, hidden=256, n_heads=2, n_kv_heads=1, head_dim=128, ffn=512, vocab=300,
+                n_experts=0, n_experts_used=0, expert_ffn=0, max_ctx=64, type_attn=12, type_ffn_gate_up=12,
+                type_ffn_down=12, type_lm_head=14, type_embd=12, type_router=8, rope_base=1e6, eps=1e-6, seed=5)
+    a = orc.Model(dict(base, type_more_bits=14), nthreads=4)
+    b = orc.Model(base, nthreads=4)
+    for l in (0, 3, 6, 7):
+        for kind, shape in ((orc.K_WV, (128, 256)), (orc.K_DOWN, (256, 512))):
+            s = orc.S_LAYER(l, kind)
+            assert a.tensor_type(s) == 14 and b.tensor_type(s) == 12
+            b.set_tensor(s, 14, orc.synth_tensor(14 | 0x100, *shape, base["seed"], s))
+            assert np.array_equal(a.tensor(s), b.tensor(s))
+    assert a.tensor_type(orc.S_LAYER(1, orc.K_WV)) == 12
+    with pytest.raises(ValueError):
+        b.set_tensor(orc.S_LAYER(1, orc.K_WV), 14, np.zeros(10, np.uint8))
+    for pos, tok in enumerate((3, 7, 11)):
+        ta, la = a.decode_step(tok, pos, want_logits=True)
+        tb, lb = b.decode_step(tok, pos, want_logits=True)
+        assert ta == tb and np.array_equal(la, lb)
+    a.close()
+    b.close()

@@ -13,7 +13,9 @@
 
 #include <stdlib.h>
 
+#include <functional>
 #include <map>
+#include <string>
 #include <vector>
 
 #include "zh_device.h"
@@ -57,6 +59,7 @@ struct zh_engine {
     // activations
     float *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     float *s = nullptr, *logits = nullptr, *rl = nullptr, *edown_out = nullptr, *fd_part = nullptr;
+    float *u = nullptr;  // up projection when gate and up differ in format (dense)
     uint8_t *xq_h = nullptr, *xq_q = nullptr, *xq_f = nullptr;
     uint32_t *routing = nullptr, *am_part = nullptr, *st = nullptr, *prompt = nullptr, *ring = nullptr;
     uint32_t *grp_cnt = nullptr;  // SwiGLU-output XQ: one counter per 32-row group (kept zero between launches)
@@ -147,7 +150,30 @@ static uint64_t host_key(uint64_t seed, uint64_t stream) {
 // ---------------------------------------------------------------------------
 static bool dmmv_type_ok(uint32_t t) { return t == ZH_Q4_K || t == ZH_Q6_K || t == ZH_Q8_0 || t == ZH_MXFP4; }
 
-extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engine **out) {
+// use_more_bits(i_layer, n_layers) of llama.cpp's quantizer: the layers the
+// Q4_K_M / Q5_K_M mix stores attn_v and ffn_down in more bits.
+static bool more_bits_layer(uint32_t i, uint32_t n) { return i < n / 8 || i >= 7 * n / 8 || (i - n / 8) % 3 == 2; }
+
+// The storage type a tensor gets from the model config: the per-class types,
+// with attn_v and ffn_down of the use_more_bits layers in type_more_bits
+// when that is set.
+static uint32_t config_type(const zh_model_config &c, uint64_t stream, uint32_t cls_type) {
+    if (!c.type_more_bits || stream <= 0xFF) return cls_type;
+    const uint32_t l = (uint32_t)(stream >> 8) - 1, kind = (uint32_t)(stream & 0xFF);
+    if ((kind == K_WV || kind == K_DOWN || kind == K_EXP_DOWN) && more_bits_layer(l, c.n_layers)) return c.type_more_bits;
+    return cls_type;
+}
+
+// How engine_build fills the weights: per-tensor types (default: from the
+// config), seeded synthetic values or left for the caller to upload, and
+// whether the LM head shares token_embd (a GGUF file without output.weight).
+struct BuildOpts {
+    std::function<uint32_t(uint64_t stream, uint32_t dflt)> type_of;
+    bool synth = true;
+    bool tied_lm = false;
+};
+
+static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts &opt, zh_engine **out) {
     if (!ctx || !cfg || !out) return ZH_ERR_INVALID_ARGUMENT;
     *out = nullptr;
     const zh_model_config &c = *cfg;
@@ -163,6 +189,8 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
     for (uint32_t t : types)
         if (!dmmv_type_ok(t)) return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "type %u", t);
     if (c.n_experts && !dmmv_type_ok(c.type_router)) return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "router");
+    if (c.type_more_bits && !dmmv_type_ok(c.type_more_bits))
+        return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "type_more_bits %u", c.type_more_bits);
 
     zh_engine *e = new zh_engine();
     e->ctx = ctx;
@@ -172,6 +200,10 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
     uint64_t off = 0;
     auto add = [&](uint64_t stream, uint32_t type, uint64_t rows, uint64_t cols) -> Tensor {
         Tensor t;
+        if (type != ZH_F32) {
+            type = config_type(c, stream, type);
+            if (opt.type_of) type = opt.type_of(stream, type);
+        }
         t.type = type;
         t.rows = rows;
         t.cols = cols;
@@ -183,7 +215,8 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
     };
     e->embd = add(S_TOKEN_EMBD, c.type_embd, c.vocab, H);
     e->out_norm = add(S_OUTPUT_NORM, ZH_F32, 1, H);
-    e->lm = add(S_OUTPUT, c.type_lm_head, c.vocab, H);
+    if (opt.tied_lm) e->tensors[S_OUTPUT] = e->lm = e->embd;
+    else e->lm = add(S_OUTPUT, c.type_lm_head, c.vocab, H);
     e->L.resize(c.n_layers);
     for (uint32_t l = 0; l < c.n_layers; l++) {
         Layer &y = e->L[l];
@@ -206,6 +239,21 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
             y.edown = add(S_LAYER(l, K_EXP_DOWN), c.type_ffn_down, (uint64_t)c.n_experts * H, c.expert_ffn);
         }
     }
+    // every matrix in a format the mat-vec kernels take; the embedding in one
+    // the row gather takes; expert gate and up in one format
+    for (auto &kv : e->tensors) {
+        const Tensor &t = kv.second;
+        if (t.type != ZH_F32 && !dmmv_type_ok(t.type)) {
+            const uint64_t st = kv.first;
+            delete e;
+            return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "tensor %llu: type %u", (unsigned long long)st, t.type);
+        }
+    }
+    for (const Layer &y : e->L)
+        if (c.n_experts && y.egate.type != y.eup.type) {
+            delete e;
+            return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "expert gate/up types differ");
+        }
     e->arena_bytes = off + 256;
     hipError_t he = hipMalloc((void **)&e->arena, e->arena_bytes);
     if (he != hipSuccess) {
@@ -214,6 +262,8 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
     }
     // --- synthetic weights (same streams as the oracle)
     for (auto &kv : e->tensors) {
+        if (!opt.synth) break;
+        if (kv.first == S_OUTPUT && opt.tied_lm) continue;
         const Tensor &t = kv.second;
         int rc;
         uint64_t kind = kv.first & 0xFF;
@@ -239,7 +289,8 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
     struct { void **p; uint64_t bytes; } acts[] = {
         {(void **)&e->hidden, 4ull * H}, {(void **)&e->norm, 4ull * XK}, {(void **)&e->q, 4ull * qd},
         {(void **)&e->k, 4ull * kvd}, {(void **)&e->v, 4ull * kvd}, {(void **)&e->attn, 4ull * qd},
-        {(void **)&e->s, 4ull * F}, {(void **)&e->logits, 4ull * c.vocab}, {(void **)&e->rl, 4ull * 256},
+        {(void **)&e->s, 4ull * F}, {(void **)&e->u, 4ull * F}, {(void **)&e->logits, 4ull * c.vocab},
+        {(void **)&e->rl, 4ull * 256},
         {(void **)&e->edown_out, 4ull * H * (c.n_experts_used ? c.n_experts_used : 1)},
         {(void **)&e->fd_part, zhk_flash_decode_partials_bytes(c.n_heads, c.n_kv_heads, hd, c.max_ctx)},
         {(void **)&e->xq_h, zh_xq_bytes_int(H)}, {(void **)&e->xq_q, zh_xq_bytes_int(qd)},
@@ -274,6 +325,85 @@ extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engi
         return zh_set_err(ctx, ZH_ERR_HIP, "engine init");
     }
     *out = e;
+    return ZH_OK;
+}
+
+extern "C" int zh_engine_create(zh_ctx *ctx, const zh_model_config *cfg, zh_engine **out) {
+    return engine_build(ctx, cfg, BuildOpts{}, out);
+}
+
+// GGUF tensor name of an engine tensor (llama.cpp's naming, as the
+// reference's forward pass looks tensors up: "blk.{l}.attn_q.weight", ...).
+static std::string gguf_name(uint64_t stream) {
+    if (stream == S_TOKEN_EMBD) return "token_embd.weight";
+    if (stream == S_OUTPUT_NORM) return "output_norm.weight";
+    if (stream == S_OUTPUT) return "output.weight";
+    static const char *kinds[] = {nullptr, "attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "attn_q_norm",
+                                  "attn_k_norm", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down", "ffn_gate_inp",
+                                  "ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"};
+    const uint64_t kind = stream & 0xFF, l = (stream >> 8) - 1;
+    if (stream <= 0xFF || kind == 0 || kind > K_EXP_DOWN) return std::string();
+    return "blk." + std::to_string(l) + "." + kinds[kind] + ".weight";
+}
+
+// loader.load + InferenceEngine.init (loader.zig:414-486, forward.zig:1226):
+// the engine's layout with each tensor in the file's storage type, then every
+// tensor copied from the mapped file into its slot.
+extern "C" int zh_engine_create_gguf(zh_ctx *ctx, const zh_gguf *f, uint32_t max_ctx, zh_engine **out) {
+    if (!ctx || !f || !out) return ZH_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    zh_model_config cfg;
+    int rc = zh_gguf_model_config(f, max_ctx, &cfg);
+    if (rc) return zh_set_err(ctx, rc, "%s", zh_gguf_last_error(f));
+    BuildOpts o;
+    o.synth = false;
+    o.tied_lm = zh_gguf_find_tensor(f, "output.weight") < 0;
+    o.type_of = [f](uint64_t stream, uint32_t dflt) {
+        const int64_t ti = zh_gguf_find_tensor(f, gguf_name(stream).c_str());
+        uint32_t t = dflt;
+        if (ti >= 0) zh_gguf_tensor_info(f, (uint64_t)ti, nullptr, nullptr, nullptr, &t, nullptr, nullptr);
+        return t;
+    };
+    zh_engine *e = nullptr;
+    ERC(engine_build(ctx, &cfg, o, &e));
+    const uint8_t *data = (const uint8_t *)zh_gguf_data(f);
+    const uint64_t fsize = zh_gguf_file_size(f), doff = zh_gguf_data_offset(f);
+    for (auto &kv : e->tensors) {
+        if (kv.first == S_OUTPUT && o.tied_lm) continue;
+        const Tensor &t = kv.second;
+        const std::string name = gguf_name(kv.first);
+        const int64_t ti = zh_gguf_find_tensor(f, name.c_str());
+        uint32_t nd = 0, type = 0;
+        uint64_t dims[4], off = 0, bytes = 0;
+        if (ti < 0) rc = zh_set_err(ctx, ZH_ERR_TENSOR_NOT_FOUND, "%s", name.c_str());
+        else zh_gguf_tensor_info(f, (uint64_t)ti, nullptr, &nd, dims, &type, &off, &bytes);
+        // ggml order: dims[0] is the contiguous (column) extent; rows are the
+        // product of the rest (expert tensors stack n_experts matrices)
+        const uint64_t rows = dims[1] * dims[2] * dims[3];
+        if (!rc && (type != t.type || dims[0] != t.cols || rows != t.rows || bytes != t.bytes))
+            rc = zh_set_err(ctx, ZH_ERR_INVALID_ARGUMENT,
+                            "%s: type %u dims [%llu, %llu, %llu] (%llu B), engine expects type %u %llu x %llu", name.c_str(),
+                            type, (unsigned long long)dims[0], (unsigned long long)dims[1], (unsigned long long)dims[2],
+                            (unsigned long long)bytes, t.type, (unsigned long long)t.rows, (unsigned long long)t.cols);
+        if (!rc && (doff + off < doff || doff + off > fsize || bytes > fsize - doff - off))
+            rc = zh_set_err(ctx, ZH_ERR_TRUNCATED_FILE, "%s: data [%llu, +%llu) past the end of the file", name.c_str(),
+                            (unsigned long long)(doff + off), (unsigned long long)bytes);
+        if (!rc && hipMemcpy(e->arena + t.off, data + doff + off, bytes, hipMemcpyHostToDevice) != hipSuccess)
+            rc = zh_set_err(ctx, ZH_ERR_HIP, "upload of %s", name.c_str());
+        if (rc) {
+            zh_engine_destroy(e);
+            return rc;
+        }
+    }
+    *out = e;
+    return ZH_OK;
+}
+
+extern "C" int zh_engine_tensor_type(zh_engine *e, uint64_t stream, uint32_t *type) {
+    if (!e || !type) return ZH_ERR_INVALID_ARGUMENT;
+    auto it = e->tensors.find(stream);
+    if (it == e->tensors.end()) return zh_set_err(e->ctx, ZH_ERR_TENSOR_NOT_FOUND, "stream %llu", (unsigned long long)stream);
+    *type = it->second.type;
     return ZH_OK;
 }
 
@@ -314,15 +444,15 @@ static int record_collect(zh_engine *e) {
     const zh_model_config &m = e->c;
     const uint32_t H = m.hidden;
     const uint8_t *A = e->arena;
-    if (!getenv("ZH_NO_LPB") && zhk_lpb_supported(m.type_lm_head, H) && m.vocab % 2 == 0) {
+    if (!getenv("ZH_NO_LPB") && zhk_lpb_supported(e->lm.type, H) && m.vocab % 2 == 0) {
         const uint8_t *wl = A + e->lm.off;
         float *yl = e->logits;
         const uint32_t mv = m.vocab;
-        ERC(zhk_dmmv_lpb(c, m.type_lm_head, 0, 1, &wl, nullptr, &yl, &mv, e->hidden,
+        ERC(zhk_dmmv_lpb(c, e->lm.type, 0, 1, &wl, nullptr, &yl, &mv, e->hidden,
                          (const float *)(A + e->out_norm.off), m.eps, nullptr, H, 0));
     } else {
         ERC(zhk_rms_norm(c, e->hidden, (const float *)(A + e->out_norm.off), H, e->norm, e->xq_h, H, 1, m.eps));
-        ERC(zhk_dmmv(c, m.type_lm_head, A + e->lm.off, e->xq_h, e->logits, m.vocab, H, 0));
+        ERC(zhk_dmmv(c, e->lm.type, A + e->lm.off, e->xq_h, e->logits, m.vocab, H, 0));
     }
     return zhk_argmax(c, e->logits, m.vocab, e->st + ST_TOKEN_OUT, e->am_part, e->ring, e->st + ST_GEN);
 }
@@ -344,34 +474,48 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     const float scale = 1.0f / sqrtf((float)hd);
     const bool whole = mask == SK_ALL && l0 == 0 && l1 >= m.n_layers;
     // embedToken (forward.zig:4255-4290), on the device.
-    if (whole) ERC(zhk_dequant_rows(c, m.type_embd, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
+    if (whole) ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
     const bool lpb = !getenv("ZH_NO_LPB");
-    const bool lpb_attn = lpb && zhk_lpb_supported(m.type_attn, H) && zhk_lpb_supported(m.type_attn, qd) &&
-                          qd % 2 == 0 && kvd % 2 == 0;
-    const bool lpb_ffn = lpb && m.n_experts == 0 && m.type_ffn_gate_up == ZH_Q4_K &&
-                         zhk_lpb_supported(ZH_Q4_K, H) && zhk_lpb_supported(m.type_ffn_down, m.ffn);
-    const bool lpb_head = lpb && zhk_lpb_supported(m.type_lm_head, H) && m.vocab % 2 == 0;
     // LDS-staged kernels with the norms, router top-k and expert combine fused
     const bool lds = !getenv("ZH_NO_LDS_DMMV");
-    const bool lds_moe = lds && m.n_experts && m.n_experts <= 256 && m.n_experts_used <= 8 &&
-                         zhk_dmmv_lds_supported(m.type_router, H) && zhk_dmmv_lds_supported(m.type_ffn_down, m.expert_ffn) &&
-                         m.expert_ffn % 32 == 0;
     for (uint32_t l = l0; l < m.n_layers && l < l1; l++) {
         const Layer &y = e->L[l];
+        // kernel choice per layer, from the layer's own tensor types (a GGUF
+        // Q4_K_M file mixes Q4_K and Q6_K attn_v / ffn_down across layers)
+        const bool lpb_attn = lpb && zhk_lpb_supported(y.wq.type, H) && zhk_lpb_supported(y.wk.type, H) &&
+                              zhk_lpb_supported(y.wv.type, H) && zhk_lpb_supported(y.wo.type, qd) && qd % 2 == 0 &&
+                              kvd % 2 == 0;
+        const bool lpb_ffn = lpb && m.n_experts == 0 && y.gate.type == ZH_Q4_K && y.up.type == ZH_Q4_K &&
+                             zhk_lpb_supported(ZH_Q4_K, H) && zhk_lpb_supported(y.down.type, m.ffn);
+        const bool lds_moe = lds && m.n_experts && m.n_experts <= 256 && m.n_experts_used <= 8 &&
+                             zhk_dmmv_lds_supported(y.router.type, H) &&
+                             zhk_dmmv_lds_supported(y.edown.type, m.expert_ffn) && m.expert_ffn % 32 == 0;
+        // Q, K and V: one launch per run of equal types (one launch when all agree)
+        const Tensor *qkv_t[3] = {&y.wq, &y.wk, &y.wv};
+        float *qkv_y[3] = {e->q, e->k, e->v};
+        const uint32_t qkv_m[3] = {qd, kvd, kvd};
         if (!(mask & SK_QKV)) {
         } else if (lpb_attn) {
             // attn_norm fused into the Q/K/V mat-vec (every workgroup normalises x)
-            const uint8_t *ws[3] = {W(y.wq), W(y.wk), W(y.wv)};
-            float *ys[3] = {e->q, e->k, e->v};
-            const uint32_t ms[3] = {qd, kvd, kvd};
-            ERC(zhk_dmmv_lpb(c, m.type_attn, 0, 3, ws, nullptr, ys, ms, e->hidden, Wf(y.attn_norm), m.eps, nullptr,
-                             H, 0));
+            for (uint32_t i0 = 0; i0 < 3;) {
+                uint32_t i1 = i0 + 1;
+                while (i1 < 3 && qkv_t[i1]->type == qkv_t[i0]->type) i1++;
+                const uint8_t *ws[3];
+                for (uint32_t i = i0; i < i1; i++) ws[i - i0] = W(*qkv_t[i]);
+                ERC(zhk_dmmv_lpb(c, qkv_t[i0]->type, 0, i1 - i0, ws, nullptr, qkv_y + i0, qkv_m + i0, e->hidden,
+                                 Wf(y.attn_norm), m.eps, nullptr, H, 0));
+                i0 = i1;
+            }
         } else {
             ERC(zhk_rms_norm(c, e->hidden, Wf(y.attn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
-            const uint8_t *ws[3] = {W(y.wq), W(y.wk), W(y.wv)};
-            float *ys[3] = {e->q, e->k, e->v};
-            const uint32_t ms[3] = {qd, kvd, kvd};
-            ERC(zhk_dmmv_multi(c, m.type_attn, 3, ws, ys, ms, e->xq_h, H));
+            for (uint32_t i0 = 0; i0 < 3;) {
+                uint32_t i1 = i0 + 1;
+                while (i1 < 3 && qkv_t[i1]->type == qkv_t[i0]->type) i1++;
+                const uint8_t *ws[3];
+                for (uint32_t i = i0; i < i1; i++) ws[i - i0] = W(*qkv_t[i]);
+                ERC(zhk_dmmv_multi(c, qkv_t[i0]->type, i1 - i0, ws, qkv_y + i0, qkv_m + i0, e->xq_h, H));
+                i0 = i1;
+            }
         }
         if (mask & SK_ATTN)
             ERC(zhk_attn_decode_fused(c, e->q, e->k, e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc,
@@ -383,10 +527,10 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             const uint8_t *wo = W(y.wo);
             float *yo = e->hidden;
             const uint32_t mo = H;
-            ERC(zhk_dmmv_lpb(c, m.type_attn, 0, 1, &wo, nullptr, &yo, &mo, nullptr, nullptr, 0.f, nullptr, qd, 1,
+            ERC(zhk_dmmv_lpb(c, y.wo.type, 0, 1, &wo, nullptr, &yo, &mo, nullptr, nullptr, 0.f, nullptr, qd, 1,
                              e->xq_q));
         } else {
-            ERC(zhk_dmmv(c, m.type_attn, W(y.wo), e->xq_q, e->hidden, H, qd, 1));
+            ERC(zhk_dmmv(c, y.wo.type, W(y.wo), e->xq_q, e->hidden, H, qd, 1));
         }
         if (lpb_ffn) {
             // ffn_norm fused into gate/up; SwiGLU fused into its epilogue
@@ -404,7 +548,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             float *yd = e->hidden;
             const uint32_t mh = H;
             if (mask & SK_FFN_OUT)
-                ERC(zhk_dmmv_lpb(c, m.type_ffn_down, 0, 1, &wd, nullptr, &yd, &mh, swiglu_xq ? nullptr : e->s,
+                ERC(zhk_dmmv_lpb(c, y.down.type, 0, 1, &wd, nullptr, &yd, &mh, swiglu_xq ? nullptr : e->s,
                                  nullptr, 0.f, nullptr, m.ffn, 1, swiglu_xq ? e->xq_f : nullptr));
             continue;
         }
@@ -417,14 +561,14 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             const uint8_t *wr = W(y.router);
             float *rl = e->rl;
             if (mask & SK_FFN_IN) {
-                ERC(zhk_dmmv_lds_plain(c, m.type_router, 1, &wr, &rl, &E, e->hidden, Wf(y.ffn_norm), m.eps, H, 0,
+                ERC(zhk_dmmv_lds_plain(c, y.router.type, 1, &wr, &rl, &E, e->hidden, Wf(y.ffn_norm), m.eps, H, 0,
                                        e->xq_h, k, e->routing, e->router_cnt));
-                ERC(zhk_dmmv_moe(c, m.type_ffn_gate_up, W(y.egate), zh_tensor_bytes(m.type_ffn_gate_up, F, H),
+                ERC(zhk_dmmv_moe(c, y.egate.type, W(y.egate), zh_tensor_bytes(y.egate.type, F, H),
                                  e->routing, e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
             }
             if (mask & SK_FFN_OUT) {
                 ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
-                ERC(zhk_dmmv_lds_down_acc(c, m.type_ffn_down, W(y.edown), zh_tensor_bytes(m.type_ffn_down, H, F),
+                ERC(zhk_dmmv_lds_down_acc(c, y.edown.type, W(y.edown), zh_tensor_bytes(y.edown.type, H, F),
                                           e->routing, k, m.n_experts, e->xq_f, e->hidden, H, F));
             }
             continue;
@@ -432,17 +576,24 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         if (!(mask & SK_FFN_IN) || !(mask & SK_FFN_OUT)) continue;  // not split: timed as whole steps only
         ERC(zhk_rms_norm(c, e->hidden, Wf(y.ffn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
         if (m.n_experts == 0) {
-            ERC(zhk_dmmv_gate_up(c, m.type_ffn_gate_up, W(y.gate), W(y.up), e->xq_h, e->s, m.ffn, H));
+            if (y.gate.type == y.up.type) {
+                ERC(zhk_dmmv_gate_up(c, y.gate.type, W(y.gate), W(y.up), e->xq_h, e->s, m.ffn, H));
+            } else {  // gate and up in different formats: two mat-vecs, then SwiGLU
+                const uint32_t F = m.ffn;
+                ERC(zhk_dmmv(c, y.gate.type, W(y.gate), e->xq_h, e->s, F, H, 0));
+                ERC(zhk_dmmv(c, y.up.type, W(y.up), e->xq_h, e->u, F, H, 0));
+                ERC(zhk_swiglu(c, e->s, e->u, e->s, F));
+            }
             ERC(zhk_quantize_xq(c, e->s, e->xq_f, m.ffn, 1, 0));
-            ERC(zhk_dmmv(c, m.type_ffn_down, W(y.down), e->xq_f, e->hidden, H, m.ffn, 1));
+            ERC(zhk_dmmv(c, y.down.type, W(y.down), e->xq_f, e->hidden, H, m.ffn, 1));
         } else {
             const uint32_t F = m.expert_ffn, k = m.n_experts_used;
-            ERC(zhk_dmmv(c, m.type_router, W(y.router), e->xq_h, e->rl, m.n_experts, H, 0));
+            ERC(zhk_dmmv(c, y.router.type, W(y.router), e->xq_h, e->rl, m.n_experts, H, 0));
             ERC(zhk_softmax_topk(c, e->rl, m.n_experts, k, e->routing));
-            ERC(zhk_dmmv_moe(c, m.type_ffn_gate_up, W(y.egate), zh_tensor_bytes(m.type_ffn_gate_up, F, H), e->routing,
+            ERC(zhk_dmmv_moe(c, y.egate.type, W(y.egate), zh_tensor_bytes(y.egate.type, F, H), e->routing,
                              e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
             ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
-            ERC(zhk_dmmv_moe(c, m.type_ffn_down, W(y.edown), zh_tensor_bytes(m.type_ffn_down, H, F), e->routing,
+            ERC(zhk_dmmv_moe(c, y.edown.type, W(y.edown), zh_tensor_bytes(y.edown.type, H, F), e->routing,
                              e->xq_f, zh_xq_bytes_int(F), e->edown_out, H, F, k, 0, nullptr, m.n_experts));
             ERC(zhk_moe_weighted_acc(c, e->hidden, e->edown_out, e->routing, H, k, H));
         }
@@ -571,11 +722,16 @@ extern "C" int zh_engine_generate(zh_engine *e, const uint32_t *prompt, uint32_t
 // its logits and greedy token are produced as decodeStep(collect) does.
 // MoE models (no batched expert GEMM here) run the decode step per token.
 // ---------------------------------------------------------------------------
-static bool prefill_batched_ok(const zh_model_config &m) {
-    auto gemm_t = [](uint32_t t) { return t == ZH_Q4_K || t == ZH_Q6_K; };
-    return m.n_experts == 0 && m.head_dim == 128 && gemm_t(m.type_attn) && gemm_t(m.type_ffn_gate_up) &&
-           gemm_t(m.type_ffn_down) && m.hidden % 256 == 0 && m.ffn % 256 == 0 &&
-           (m.n_heads * m.head_dim) % 256 == 0;
+static bool prefill_batched_ok(const zh_engine *e) {
+    const zh_model_config &m = e->c;
+    auto gemm_t = [](const Tensor &t) { return t.type == ZH_Q4_K || t.type == ZH_Q6_K; };
+    if (m.n_experts || m.head_dim != 128 || m.hidden % 256 || m.ffn % 256 || (m.n_heads * m.head_dim) % 256)
+        return false;
+    for (const Layer &y : e->L)
+        if (!gemm_t(y.wq) || !gemm_t(y.wk) || !gemm_t(y.wv) || !gemm_t(y.wo) || !gemm_t(y.gate) || !gemm_t(y.up) ||
+            !gemm_t(y.down))
+            return false;
+    return true;
 }
 
 static int ensure_prefill(zh_engine *e) {
@@ -607,7 +763,7 @@ extern "C" int zh_engine_prefill(zh_engine *e, const uint32_t *tokens, uint32_t 
         return zh_set_err(e->ctx, ZH_ERR_CONTEXT_LENGTH_EXCEEDED, "context %u + %u > %u", start_pos, n, e->c.max_ctx);
     zh_ctx *c = e->ctx;
     const zh_model_config &m = e->c;
-    if (!prefill_batched_ok(m)) {
+    if (!prefill_batched_ok(e)) {
         EHIP(e, hipMemcpyAsync(e->prompt, tokens, 4ull * n, hipMemcpyHostToDevice, c->stream));
         ERC(set_state(e, n, start_pos, tokens[0]));
         for (uint32_t i = 0; i < n; i++) ERC(run_step(e, collect && i + 1 == n));
@@ -625,31 +781,41 @@ extern "C" int zh_engine_prefill(zh_engine *e, const uint32_t *tokens, uint32_t 
     for (uint32_t off = 0; off < n; off += PF_CHUNK) {
         const uint32_t nt = n - off < PF_CHUNK ? n - off : PF_CHUNK, pos0 = start_pos + off;
         last = nt;
-        ERC(zhk_dequant_rows(c, m.type_embd, W(e->embd), 0, nt, H, e->pf.hid, e->pf.ids + off, m.vocab, 1));
+        ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, nt, H, e->pf.hid, e->pf.ids + off, m.vocab, 1));
         for (uint32_t l = 0; l < m.n_layers; l++) {
             const Layer &y = e->L[l];
             ERC(zhk_rms_norm_rows_f16(c, e->pf.hid, Wf(y.attn_norm), e->pf.xh, H, nt, m.eps));
-            {  // Q, K and V in one launch
-                const uint8_t *ws[3] = {W(y.wq), W(y.wk), W(y.wv)};
+            {  // Q, K and V: one launch per run of equal types (one when all agree)
+                const Tensor *ts[3] = {&y.wq, &y.wk, &y.wv};
                 float *ys[3] = {e->pf.q, e->pf.k, e->pf.v};
                 const uint32_t ld[3] = {qd, kvd, kvd}, ms[3] = {qd, kvd, kvd};
-                ERC(zhk_gemm_multi(c, m.type_attn, 3, ws, e->pf.xh, H, ys, ld, ms, H, nt, 0));
+                for (uint32_t i0 = 0; i0 < 3;) {
+                    uint32_t i1 = i0 + 1;
+                    while (i1 < 3 && ts[i1]->type == ts[i0]->type) i1++;
+                    const uint8_t *ws[3];
+                    for (uint32_t i = i0; i < i1; i++) ws[i - i0] = W(*ts[i]);
+                    ERC(zhk_gemm_multi(c, ts[i0]->type, i1 - i0, ws, e->pf.xh, H, ys + i0, ld + i0, ms + i0, H, nt, 0));
+                    i0 = i1;
+                }
             }
             ERC(zhk_qk_norm_rope_kv(c, e->pf.q, Wf(y.q_norm), e->pf.k, Wf(y.k_norm), e->pf.v, e->inv_freq, y.kc, y.vc,
                                     e->pages, e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd,
                                     zh_pos_src{pos0, nullptr}, m.eps, nt));
             ERC(zhk_attn_prefill(c, e->pf.q, y.kc, y.vc, e->pages, e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd,
                                  pos0, nt, scale, e->pf.att));
-            ERC(zhk_gemm(c, m.type_attn, W(y.wo), e->pf.att, qd, e->pf.hid, H, H, qd, nt, 1));
+            ERC(zhk_gemm(c, y.wo.type, W(y.wo), e->pf.att, qd, e->pf.hid, H, H, qd, nt, 1));
             ERC(zhk_rms_norm_rows_f16(c, e->pf.hid, Wf(y.ffn_norm), e->pf.xh, H, nt, m.eps));
-            {  // gate and up in one launch
+            if (y.gate.type == y.up.type) {  // gate and up in one launch
                 const uint8_t *ws[2] = {W(y.gate), W(y.up)};
                 float *ys[2] = {e->pf.g, e->pf.u};
                 const uint32_t ld[2] = {F, F}, ms[2] = {F, F};
-                ERC(zhk_gemm_multi(c, m.type_ffn_gate_up, 2, ws, e->pf.xh, H, ys, ld, ms, H, nt, 0));
+                ERC(zhk_gemm_multi(c, y.gate.type, 2, ws, e->pf.xh, H, ys, ld, ms, H, nt, 0));
+            } else {
+                ERC(zhk_gemm(c, y.gate.type, W(y.gate), e->pf.xh, H, e->pf.g, F, F, H, nt, 0));
+                ERC(zhk_gemm(c, y.up.type, W(y.up), e->pf.xh, H, e->pf.u, F, F, H, nt, 0));
             }
             ERC(zhk_swiglu_rows_f16(c, e->pf.g, e->pf.u, e->pf.s, e->pf.s_unscale, F, nt));
-            ERC(zhk_gemm(c, m.type_ffn_down, W(y.down), e->pf.s, F, e->pf.hid, H, H, F, nt, 1, e->pf.s_unscale));
+            ERC(zhk_gemm(c, y.down.type, W(y.down), e->pf.s, F, e->pf.hid, H, H, F, nt, 1, e->pf.s_unscale));
         }
     }
     EHIP(e, hipMemcpyAsync(e->hidden, e->pf.hid + (size_t)(last - 1) * H, 4ull * H, hipMemcpyDeviceToDevice,
@@ -708,15 +874,15 @@ extern "C" int zh_engine_read_kv(zh_engine *e, uint32_t layer, uint32_t which, u
 extern "C" uint64_t zh_engine_bytes_per_token(zh_engine *e, uint32_t Lctx) {
     if (!e) return 0;
     const zh_model_config &c = e->c;
-    uint64_t b = e->lm.bytes + e->out_norm.bytes + zh_tensor_bytes(c.type_embd, 1, c.hidden);
+    uint64_t b = e->lm.bytes + e->out_norm.bytes + zh_tensor_bytes(e->embd.type, 1, c.hidden);
     for (const Layer &y : e->L) {
         b += y.attn_norm.bytes + y.wq.bytes + y.wk.bytes + y.wv.bytes + y.wo.bytes + y.q_norm.bytes + y.k_norm.bytes +
              y.ffn_norm.bytes;
         if (c.n_experts == 0) b += y.gate.bytes + y.up.bytes + y.down.bytes;
         else
             b += y.router.bytes + (uint64_t)c.n_experts_used *
-                                      (zh_tensor_bytes(c.type_ffn_gate_up, c.expert_ffn, c.hidden) * 2 +
-                                       zh_tensor_bytes(c.type_ffn_down, c.hidden, c.expert_ffn));
+                                      (zh_tensor_bytes(y.egate.type, c.expert_ffn, c.hidden) * 2 +
+                                       zh_tensor_bytes(y.edown.type, c.hidden, c.expert_ffn));
         b += 2ull * c.n_kv_heads * c.head_dim * 2ull * Lctx;  // fp16 K and V
     }
     return b;
@@ -740,11 +906,11 @@ extern "C" uint64_t zh_engine_group_bytes(zh_engine *e, uint32_t group, uint32_t
     case SK_O: return y.wo.bytes + xqb(qd) + 2 * H * 4;
     case SK_FFN_IN:
         if (c.n_experts == 0) return y.gate.bytes + y.up.bytes + 2 * H * 4 + F * 4 + xqb(F);
-        return y.router.bytes + 2 * k * zh_tensor_bytes(c.type_ffn_gate_up, (uint32_t)F, (uint32_t)H) + 2 * H * 4 +
+        return y.router.bytes + 2 * k * zh_tensor_bytes(y.egate.type, (uint32_t)F, (uint32_t)H) + 2 * H * 4 +
                xqb(H) + (uint64_t)c.n_experts * 4 + 8 * k + k * F * 4;
     case SK_FFN_OUT:
         if (c.n_experts == 0) return y.down.bytes + xqb(F) + 2 * H * 4;
-        return k * zh_tensor_bytes(c.type_ffn_down, (uint32_t)H, (uint32_t)F) + k * F * 4 + 2 * k * xqb(F) + 8 * k +
+        return k * zh_tensor_bytes(y.edown.type, (uint32_t)H, (uint32_t)F) + k * F * 4 + 2 * k * xqb(F) + 8 * k +
                2 * H * 4;
     default: return 0;
     }

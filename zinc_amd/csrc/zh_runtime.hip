@@ -29,6 +29,12 @@ extern "C" const char *zh_status_string(int s) {
     case ZH_ERR_CONTEXT_LENGTH_EXCEEDED: return "ContextLengthExceeded";
     case ZH_ERR_OUT_OF_MEMORY: return "OutOfMemory";
     case ZH_ERR_TENSOR_NOT_FOUND: return "TensorNotFound";
+    case ZH_ERR_INVALID_MAGIC: return "InvalidMagic";
+    case ZH_ERR_UNKNOWN_METADATA_TYPE: return "UnknownMetadataType";
+    case ZH_ERR_UNSUPPORTED_ARCHITECTURE: return "UnsupportedArchitecture";
+    case ZH_ERR_TRUNCATED_FILE: return "TruncatedFile";
+    case ZH_ERR_IO: return "IoError";
+    case ZH_ERR_NOT_FOUND: return "NotFound";
     default: return "unknown";
     }
 }

@@ -41,6 +41,23 @@ class InferenceEngine:
         ctx.check(lib().zh_engine_create(ctx.h, C.byref(self._cfg), C.byref(h)))
         self.h = h
 
+    @classmethod
+    def from_gguf(cls, ctx: hip.Context, path, max_ctx=0):
+        """loader.load + InferenceEngine.init (loader.zig:414-486,
+        forward.zig:1226): an engine on a GGUF file's weights, each tensor in
+        its stored format. max_ctx: KV capacity in tokens (0: the file's
+        context_length)."""
+        from .gguf import GGUFFile
+        with GGUFFile(path) as f:
+            eng = cls.__new__(cls)
+            eng.ctx = ctx
+            eng.config = f.model_config(max_ctx)
+            eng._cfg = ModelConfig(**eng.config)
+            h = C.c_void_p()
+            ctx.check(lib().zh_engine_create_gguf(ctx.h, f.h, max_ctx, C.byref(h)))
+            eng.h = h
+        return eng
+
     def deinit(self):
         if self.h:
             lib().zh_engine_destroy(self.h)
@@ -95,6 +112,11 @@ class InferenceEngine:
         out = np.empty(n.value, dtype=np.uint8)
         self.ctx.check(lib().zh_buf_download(self.ctx.h, b, off.value, C.c_void_p(out.ctypes.data), n.value))
         return out
+
+    def tensor_type(self, stream):
+        t = C.c_uint32()
+        self.ctx.check(lib().zh_engine_tensor_type(self.h, stream, C.byref(t)))
+        return t.value
 
     def read_kv(self, layer, which, t0, n):
         c = self.config

@@ -16,7 +16,9 @@ LIB_PATH = os.environ.get("ZH_LIB_PATH") or os.path.join(HERE, "libzinc_hip.so")
 F32, F16, Q8_0, Q4_K, Q6_K, MXFP4 = 0, 1, 8, 12, 14, 39
 OK = 0
 STATUS = {1: "UnsupportedQuantType", 2: "InvalidArgument", 3: "HipError",
-          4: "ContextLengthExceeded", 5: "OutOfMemory", 6: "TensorNotFound"}
+          4: "ContextLengthExceeded", 5: "OutOfMemory", 6: "TensorNotFound", 7: "InvalidMagic",
+          8: "UnknownMetadataType", 9: "UnsupportedArchitecture", 10: "TruncatedFile", 11: "IoError",
+          12: "NotFound"}
 
 BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34), MXFP4: (32, 17), F32: (1, 4), F16: (1, 2)}
 
@@ -38,7 +40,8 @@ class ModelConfig(C.Structure):
         "n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab",
         "n_experts", "n_experts_used", "expert_ffn", "max_ctx",
         "type_attn", "type_ffn_gate_up", "type_ffn_down", "type_lm_head", "type_embd",
-        "type_router")] + [("rope_base", C.c_float), ("eps", C.c_float), ("seed", C.c_uint64)]
+        "type_router")] + [("rope_base", C.c_float), ("eps", C.c_float), ("seed", C.c_uint64),
+                            ("type_more_bits", C.c_uint32), ("reserved", C.c_uint32)]
 
 
 _P = C.c_void_p
@@ -96,6 +99,28 @@ SIGNATURES = {
     "zh_engine_bytes_per_token": (_u64, [_P, _u32]),
     "zh_engine_time_kernel": (_i32, [_P, _u32, _u32, _P]),
     "zh_engine_group_bytes": (_u64, [_P, _u32, _u32]),
+    "zh_engine_tensor_type": (_i32, [_P, _u64, C.POINTER(_u32)]),
+    "zh_engine_create_gguf": (_i32, [_P, _P, _u32, C.POINTER(_P)]),
+    "zh_gguf_open": (_i32, [C.c_char_p, C.POINTER(_P)]),
+    "zh_gguf_close": (None, [_P]),
+    "zh_gguf_last_error": (C.c_char_p, [_P]),
+    "zh_gguf_version": (_u32, [_P]),
+    "zh_gguf_tensor_count": (_u64, [_P]),
+    "zh_gguf_metadata_count": (_u64, [_P]),
+    "zh_gguf_data_offset": (_u64, [_P]),
+    "zh_gguf_data": (_P, [_P]),
+    "zh_gguf_file_size": (_u64, [_P]),
+    "zh_gguf_tensor_info": (_i32, [_P, _u64, C.POINTER(C.c_char_p), C.POINTER(_u32), C.POINTER(_u64),
+                                   C.POINTER(_u32), C.POINTER(_u64), C.POINTER(_u64)]),
+    "zh_gguf_find_tensor": (C.c_int64, [_P, C.c_char_p]),
+    "zh_gguf_get_u32": (_i32, [_P, C.c_char_p, C.POINTER(_u32)]),
+    "zh_gguf_get_u64": (_i32, [_P, C.c_char_p, C.POINTER(_u64)]),
+    "zh_gguf_get_f32": (_i32, [_P, C.c_char_p, C.POINTER(_f32)]),
+    "zh_gguf_get_bool": (_i32, [_P, C.c_char_p, C.POINTER(_i32)]),
+    "zh_gguf_get_string": (_i32, [_P, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(_u64)]),
+    "zh_gguf_metadata_entry": (_i32, [_P, _u64, C.POINTER(C.c_char_p), C.POINTER(_u32), C.POINTER(_u32),
+                                      C.POINTER(_u64)]),
+    "zh_gguf_model_config": (_i32, [_P, _u32, _P]),
 }
 
 _lib = None
