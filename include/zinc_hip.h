@@ -236,6 +236,28 @@ int zh_engine_read_kv(zh_engine *eng, uint32_t layer, uint32_t which, uint32_t t
  * KV + activations), the numerator of the bandwidth roofline. */
 uint64_t zh_engine_bytes_per_token(zh_engine *eng, uint32_t L);
 
+/* ---- sampling: SamplingParams / sampleFromLogits / sample
+ *      (src/compute/forward.zig:95-105, 10229-10367) -------------------- */
+typedef struct zh_sampling_params {
+    float temperature;        /* 0: greedy */
+    float top_p;              /* 1: off */
+    float repetition_penalty; /* 1: off */
+    uint32_t top_k;           /* candidates, clamped to 1..128 */
+} zh_sampling_params;
+/* sampleFromLogits over n f32 logits in a device buffer, on the device (the
+ * reference reads the logits back and scans them on the host; here only the
+ * token returns). history: the generated tokens (host memory; read only when
+ * a repetition penalty applies). u: the value the reference draws with
+ * random.float(f64) at that point, in [0, 1), used only when the choice is
+ * random. No final-logit softcap (the models on the path have none).
+ * n at most 262144. */
+int zh_sample_logits(zh_ctx *ctx, const zh_buf *logits, uint64_t offset, uint32_t n, const zh_sampling_params *p,
+                     const uint32_t *history, uint32_t n_history, double u, uint32_t *token);
+/* InferenceEngine.sample (forward.zig:10360-10367) on the last step's logits:
+ * sampleGreedy when the params need no logits, else sampleFromLogits. */
+int zh_engine_sample(zh_engine *eng, const zh_sampling_params *p, const uint32_t *history, uint32_t n_history,
+                     double u, uint32_t *token);
+
 /* ---- GGUF model files: src/model/gguf.zig (parse) and src/model/loader.zig
  *      (extractConfig, load) --------------------------------------------- */
 typedef struct zh_gguf zh_gguf;

@@ -79,6 +79,9 @@ def lib():
             "zo_model_decode_step": (C.c_uint32, [C.c_void_p, C.c_uint32, C.c_uint32, f32p]),
             "zo_model_tensor": (C.c_void_p, [C.c_void_p, C.c_uint64, C.POINTER(C.c_uint64)]),
             "zo_model_tensor_type": (C.c_int, [C.c_void_p, C.c_uint64]),
+            "zo_sampling_requires_readback": (C.c_int, [C.c_float, C.c_float, C.c_float]),
+            "zo_sample_from_logits": (C.c_uint32, [f32p, C.c_uint32, u32p, C.c_uint32, C.c_float, C.c_float,
+                                                   C.c_float, C.c_uint32, C.c_double]),
             "zo_model_set_tensor": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_uint64]),
             "zo_more_bits_layer": (C.c_int, [C.c_uint32, C.c_uint32]),
             "zo_model_hidden": (C.c_void_p, [C.c_void_p]),
@@ -223,6 +226,19 @@ def topk_softmax(logits, k):
     w = np.empty(k, dtype=np.float32)
     lib().zo_topk_softmax(f32(lg), len(lg), k, _p(ids, C.c_uint32), f32(w))
     return ids, w
+
+
+def sample_from_logits(logits, history=(), temperature=0.0, top_p=1.0, repetition_penalty=1.0, top_k=64, u=0.0):
+    """sampleFromLogits (forward.zig:10261-10334) with the draw u = random.float(f64)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    h = np.ascontiguousarray(history, dtype=np.uint32)
+    if h.size == 0:
+        h = np.zeros(1, np.uint32)
+        nh = 0
+    else:
+        nh = h.size
+    return int(lib().zo_sample_from_logits(f32(lg), lg.size, _p(h, C.c_uint32), nh, temperature, top_p,
+                                           repetition_penalty, top_k, u))
 
 
 def argmax(logits):

@@ -389,6 +389,94 @@ uint32_t zo_argmax(const float *logits, uint32_t n) {
     return mi;
 }
 
+/* SamplingParams.requiresLogitsReadback (forward.zig:102-104). */
+int zo_sampling_requires_readback(float temperature, float top_p, float repetition_penalty) {
+    return temperature > 0.0001f || top_p < 0.9999f || repetition_penalty > 1.0001f;
+}
+
+/* adjustedLogit (forward.zig:10241-10245) with tokenSeen's linear scan
+ * (:10229-10234); the models on this path have no final-logit softcap. */
+static float adjusted_logit(float logit, uint32_t token, const uint32_t *hist, uint32_t nh, float pen) {
+    if (pen <= 1.0001f) return logit;
+    int seen = 0;
+    for (uint32_t i = 0; i < nh && !seen; i++) seen = hist[i] == token;
+    if (!seen) return logit;
+    return logit >= 0 ? logit / pen : logit * pen;
+}
+
+/* argmaxFromLogits (forward.zig:10247-10259): first strict maximum, starting
+ * from logits[0] (a NaN there is never replaced). */
+static uint32_t argmax_adjusted(const float *logits, uint32_t n, const uint32_t *hist, uint32_t nh, float pen) {
+    uint32_t best = 0;
+    float bv = adjusted_logit(logits[0], 0, hist, nh, pen);
+    for (uint32_t i = 1; i < n; i++) {
+        float v = adjusted_logit(logits[i], i, hist, nh, pen);
+        if (v > bv) { bv = v; best = i; }
+    }
+    return best;
+}
+
+/* sampleFromLogits (forward.zig:10261-10334) without a softcap. `u` is the
+ * value the reference draws with random.float(f64) (consumed only when the
+ * choice is random). Candidates: the top_k (1..128) finite adjusted logits,
+ * kept by an insertion that places a value after equal ones (earlier token
+ * first); weights exp(l/T - l0/T) in f64; top_p keeps the shortest prefix
+ * whose cumulative share reaches top_p (at least two candidates once
+ * reached past the first); then the first candidate whose cumulative weight
+ * reaches u * kept_weight. */
+uint32_t zo_sample_from_logits(const float *logits, uint32_t n, const uint32_t *hist, uint32_t nh,
+                               float temperature, float top_p, float rep_pen, uint32_t top_k, double u) {
+    if (n == 0) return 0;
+    if (!zo_sampling_requires_readback(temperature, top_p, rep_pen)) return argmax_adjusted(logits, n, hist, nh, 1.0f);
+    if (temperature <= 0.0001f) return argmax_adjusted(logits, n, hist, nh, rep_pen);
+    enum { MAXC = 128 };
+    uint32_t k = top_k < 1 ? 1 : top_k > MAXC ? MAXC : top_k;
+    float tp = top_p < 0.f ? 0.f : top_p > 1.f ? 1.f : top_p;
+    float temp = temperature > 0.0001f ? temperature : 0.0001f;
+    uint32_t ids[MAXC];
+    float lv[MAXC];
+    uint32_t cnt = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        if (!isfinite(logits[i])) continue;
+        float v = adjusted_logit(logits[i], i, hist, nh, rep_pen);
+        uint32_t at = cnt;
+        while (at > 0 && v > lv[at - 1]) at--;
+        if (at >= k) continue;
+        if (cnt < k) cnt++;
+        for (uint32_t j = cnt - 1; j > at; j--) { ids[j] = ids[j - 1]; lv[j] = lv[j - 1]; }
+        ids[at] = i;
+        lv[at] = v;
+    }
+    if (cnt == 0) return 0;
+    if (cnt == 1) return ids[0];
+    double w[MAXC], total = 0.0;
+    const double m0 = (double)lv[0] / (double)temp;
+    for (uint32_t i = 0; i < cnt; i++) {
+        w[i] = exp((double)lv[i] / (double)temp - m0);
+        total += w[i];
+    }
+    if (!(total > 0.0) || !isfinite(total)) return ids[0];
+    uint32_t keep = cnt;
+    if (tp < 0.9999f) {
+        double cum = 0.0;
+        for (uint32_t i = 0; i < cnt; i++) {
+            cum += w[i] / total;
+            keep = i + 1;
+            if (cum >= (double)tp && i > 0) break;
+        }
+    }
+    double kept = 0.0;
+    for (uint32_t i = 0; i < keep; i++) kept += w[i];
+    if (!(kept > 0.0) || !isfinite(kept)) return ids[0];
+    const double target = u * kept;
+    double cum = 0.0;
+    for (uint32_t i = 0; i < keep; i++) {
+        cum += w[i];
+        if (target <= cum) return ids[i];
+    }
+    return ids[keep - 1];
+}
+
 uint32_t zo_kv_page_count(uint32_t ctx) { return ctx == 0 ? 0 : (ctx + 15) / 16; }
 int64_t zo_logical_to_physical(const uint32_t *page_ids, uint32_t n_pages, uint32_t logical) {
     uint32_t slot = logical / 16;

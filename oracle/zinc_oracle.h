@@ -84,6 +84,12 @@ void zo_attention_f16(const float *q, const uint16_t *k, const uint16_t *v, floa
 void zo_topk_softmax(const float *logits, uint32_t n, uint32_t k, uint32_t *ids, float *w);
 /* sampleGreedy CPU scan: src/compute/forward.zig:10343-10356 (first max wins) */
 uint32_t zo_argmax(const float *logits, uint32_t n);
+/* SamplingParams.requiresLogitsReadback and sampleFromLogits
+ * (src/compute/forward.zig:95-105, 10229-10334), no softcap; u is the
+ * caller's random.float(f64) draw. */
+int      zo_sampling_requires_readback(float temperature, float top_p, float repetition_penalty);
+uint32_t zo_sample_from_logits(const float *logits, uint32_t n, const uint32_t *hist, uint32_t nh,
+                               float temperature, float top_p, float rep_pen, uint32_t top_k, double u);
 /* kvPageCountForContext / logicalTokenToPhysicalToken: src/compute/forward.zig:677-698.
  * Returns -1 for ContextLengthExceeded. */
 int64_t zo_logical_to_physical(const uint32_t *page_ids, uint32_t n_pages, uint32_t logical);

@@ -469,3 +469,80 @@ def test_model_set_tensor_matches_more_bits_config(orc):
         assert ta == tb and np.array_equal(la, lb)
     a.close()
     b.close()
+
+
+# ---- sampleFromLogits (forward.zig:10261-10334) ----------------------------
+def test_sampling_reference_cases(orc):
+    # forward.zig:11425-11459
+    L = orc.lib()
+    assert not L.zo_sampling_requires_readback(0.0, 1.0, 1.0)
+    assert L.zo_sampling_requires_readback(0.7, 1.0, 1.0)
+    assert L.zo_sampling_requires_readback(0.0, 0.9, 1.0)
+    assert L.zo_sampling_requires_readback(0.0, 1.0, 1.1)
+    assert orc.sample_from_logits([0.5, 2.0, 1.25], u=0.3) == 1
+    assert orc.sample_from_logits([10.0, 9.0, 1.0], [0, 0, 0], temperature=0.0, repetition_penalty=2.0) == 1
+    for u in (0.0, 0.3, 0.97):
+        assert orc.sample_from_logits([8.0, 5.0, 1.0], temperature=0.8, top_p=0.5, top_k=8, u=u) == 0
+    # the top_p scan stops only past the first candidate (forward.zig:10311),
+    # so two candidates stay: the second (share exp(-3.75) / (1 + exp(-3.75))
+    # = 0.0230) takes the top of the draw
+    assert orc.sample_from_logits([8.0, 5.0, 1.0], temperature=0.8, top_p=0.5, top_k=8, u=0.99) == 1
+
+
+def _support_and_freq(orc, logits, n_u=20000, **kw):
+    us = (np.arange(n_u) + 0.5) / n_u
+    toks = np.array([orc.sample_from_logits(logits, u=float(u), **kw) for u in us])
+    ids, cnt = np.unique(toks, return_counts=True)
+    return dict(zip(ids.tolist(), (cnt / n_u).tolist()))
+
+
+def test_sampling_distribution_is_topk_softmax(orc):
+    rng = np.random.default_rng(0)
+    lg = rng.normal(0, 2, 300).astype(np.float32)
+    T, k = 0.7, 12
+    freq = _support_and_freq(orc, lg, temperature=T, top_k=k)
+    top = np.argsort(-lg, kind="stable")[:k]
+    assert set(freq) == set(top.tolist())
+    z = lg[top].astype(np.float64) / T
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    for t, pt in zip(top.tolist(), p):
+        assert abs(freq[t] - pt) < 2e-4, (t, freq[t], pt)
+
+
+def test_sampling_top_p_support_is_minimal_prefix(orc):
+    rng = np.random.default_rng(1)
+    lg = rng.normal(0, 1.5, 200).astype(np.float32)
+    T, k, tp = 1.0, 40, 0.6
+    freq = _support_and_freq(orc, lg, temperature=T, top_k=k, top_p=tp)
+    top = np.argsort(-lg, kind="stable")[:k]
+    z = lg[top].astype(np.float64) / T
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    # shortest prefix with cumulative share >= top_p, at least two candidates
+    keep = max(int(np.searchsorted(np.cumsum(p), tp) + 1), 2)
+    assert set(freq) == set(top[:keep].tolist())
+    q = p[:keep] / p[:keep].sum()
+    for t, pt in zip(top[:keep].tolist(), q):
+        assert abs(freq[t] - pt) < 2e-4
+
+
+def test_sampling_ties_nonfinite_and_penalty(orc):
+    # equal logits at the top-k boundary: the earlier token is kept
+    lg = np.array([1.0, 3.0, 2.0, 2.0, 2.0], np.float32)
+    assert set(_support_and_freq(orc, lg, n_u=2000, temperature=1.0, top_k=2)) == {1, 2}
+    # non-finite logits never become candidates when sampling ...
+    lg = np.array([np.nan, 1.0, np.inf, 0.5, -np.inf], np.float32)
+    assert set(_support_and_freq(orc, lg, n_u=2000, temperature=1.0, top_k=8)) == {1, 3}
+    # ... but the greedy scan compares them: +inf wins, a NaN at index 0 stays
+    assert orc.sample_from_logits(lg, repetition_penalty=1.5, temperature=0.0) == 0
+    assert orc.sample_from_logits(np.array([0.0, np.inf, 1.0], np.float32), top_p=0.5, temperature=0.0) == 1
+    # penalty: positive seen logits shrink (/p), negative ones grow (*p)
+    assert orc.sample_from_logits(np.array([4.0, 2.5], np.float32), [0], temperature=0.0,
+                                  repetition_penalty=2.0) == 1
+    assert orc.sample_from_logits(np.array([-1.0, -1.5], np.float32), [0], temperature=0.0,
+                                  repetition_penalty=2.0) == 1
+    assert orc.sample_from_logits(np.array([-1.0, -2.5], np.float32), [0], temperature=0.0,
+                                  repetition_penalty=2.0) == 0
+    # a single finite candidate is returned whatever u is
+    assert orc.sample_from_logits(np.array([np.nan, 7.0, np.nan], np.float32), temperature=0.9, u=0.99) == 1

@@ -399,6 +399,17 @@ extern "C" int zh_engine_create_gguf(zh_ctx *ctx, const zh_gguf *f, uint32_t max
     return ZH_OK;
 }
 
+// InferenceEngine.sample (forward.zig:10360-10367): the greedy token of the
+// last step when the params need no logits, else sampleFromLogits on the
+// device over the last step's logits.
+extern "C" int zh_engine_sample(zh_engine *e, const zh_sampling_params *p, const uint32_t *history, uint32_t nh,
+                                double u, uint32_t *token) {
+    if (!e || !p || !token) return ZH_ERR_INVALID_ARGUMENT;
+    if (!zhk_sampling_requires_readback(p)) return zh_engine_sample_greedy(e, token);
+    if (!e->have_logits) return zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "sample: no logits (run a step with collect_output)");
+    return zhk_sample_host(e->ctx, e->logits, e->c.vocab, p, history, nh, u, token);
+}
+
 extern "C" int zh_engine_tensor_type(zh_engine *e, uint64_t stream, uint32_t *type) {
     if (!e || !type) return ZH_ERR_INVALID_ARGUMENT;
     auto it = e->tensors.find(stream);

@@ -138,6 +138,13 @@ int zhk_argmax(zh_ctx *ctx, const float *logits, uint32_t n, uint32_t *result, u
 // Lane-per-block K-quant DMMV (zh_dmmv_lpb.hip): stages f32 x (optionally
 // RMS-normalised with norm_w) into LDS itself. mode 0: plain (up to 3 stacked
 // matrices), mode 1: fused gate/up/SwiGLU (Q4_K, W = gate, W2 = up).
+// Device sampling (zh_sample.hip).
+bool zhk_sampling_requires_readback(const zh_sampling_params *s);
+uint32_t zhk_sample_max_vocab();
+int zhk_sample(zh_ctx *ctx, const float *logits, uint32_t n, const uint32_t *hist, uint32_t nh,
+               const zh_sampling_params *s, double u, uint64_t *keys, uint32_t *out);
+int zhk_sample_host(zh_ctx *ctx, const float *logits, uint32_t n, const zh_sampling_params *s,
+                    const uint32_t *history, uint32_t nh, double u, uint32_t *token);
 bool zhk_lpb_supported(uint32_t qtype, uint32_t K);
 int zhk_dmmv_lpb(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
                  float *const *y, const uint32_t *M, const float *x, const float *norm_w, float eps,

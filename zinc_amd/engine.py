@@ -87,6 +87,20 @@ class InferenceEngine:
         self.ctx.check(lib().zh_engine_sample_greedy(self.h, C.byref(t)))
         return t.value
 
+    def sample(self, state: DecodeState, params, random=None):
+        """InferenceEngine.sample (forward.zig:10360-10367): sampleGreedy when
+        the params need no logits, else sampleFromLogits on the device over
+        the last step's logits with state.generated_tokens as the history.
+        random: a callable returning a float in [0, 1) (the reference's
+        random.float(f64)); called only when the params sample."""
+        h = np.ascontiguousarray(state.generated_tokens, dtype=np.uint32)
+        u = float(random()) if params.draws() else 0.0
+        t = C.c_uint32()
+        pc = params.c()
+        self.ctx.check(lib().zh_engine_sample(self.h, C.byref(pc), C.c_void_p(h.ctypes.data) if h.size else None,
+                                              h.size, u, C.byref(t)))
+        return t.value
+
     def generate(self, prompt, max_tokens, eos=0xFFFFFFFF, start_pos=0):
         """generate (forward.zig:10983): prompt then greedy decode on device."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)

@@ -44,6 +44,30 @@ class ModelConfig(C.Structure):
                             ("type_more_bits", C.c_uint32), ("reserved", C.c_uint32)]
 
 
+class SamplingParamsC(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("repetition_penalty", C.c_float),
+                ("top_k", C.c_uint32)]
+
+
+class SamplingParams:
+    """SamplingParams (forward.zig:95-105), with its defaults."""
+
+    def __init__(self, temperature=0.0, top_p=1.0, repetition_penalty=1.0, top_k=64):
+        self.temperature, self.top_p = temperature, top_p
+        self.repetition_penalty, self.top_k = repetition_penalty, top_k
+
+    def requires_logits_readback(self):
+        return self.temperature > 0.0001 or self.top_p < 0.9999 or self.repetition_penalty > 1.0001
+
+    def draws(self):
+        """Whether sampleFromLogits draws from the random source (it does so
+        only when sampling with a temperature and at least two candidates)."""
+        return self.requires_logits_readback() and self.temperature > 0.0001
+
+    def c(self):
+        return SamplingParamsC(self.temperature, self.top_p, self.repetition_penalty, self.top_k)
+
+
 _P = C.c_void_p
 _u32, _u64, _f32, _i32 = C.c_uint32, C.c_uint64, C.c_float, C.c_int
 
@@ -100,6 +124,9 @@ SIGNATURES = {
     "zh_engine_time_kernel": (_i32, [_P, _u32, _u32, _P]),
     "zh_engine_group_bytes": (_u64, [_P, _u32, _u32]),
     "zh_engine_tensor_type": (_i32, [_P, _u64, C.POINTER(_u32)]),
+    "zh_sample_logits": (_i32, [_P, _P, _u64, _u32, C.POINTER(SamplingParamsC), _P, _u32, C.c_double,
+                                C.POINTER(_u32)]),
+    "zh_engine_sample": (_i32, [_P, C.POINTER(SamplingParamsC), _P, _u32, C.c_double, C.POINTER(_u32)]),
     "zh_engine_create_gguf": (_i32, [_P, _P, _u32, C.POINTER(_P)]),
     "zh_gguf_open": (_i32, [C.c_char_p, C.POINTER(_P)]),
     "zh_gguf_close": (None, [_P]),
@@ -308,6 +335,15 @@ class Context:
 
     def argmax(self, logits, n, result, result_off=0):
         self.check(lib().zh_argmax(self.h, logits.h, n, result.h, result_off))
+
+    def sample_logits(self, logits, off, n, params, history=(), u=0.0):
+        """sampleFromLogits on the device (u: the random.float(f64) draw)."""
+        h = np.ascontiguousarray(history, dtype=np.uint32)
+        t = C.c_uint32()
+        pc = params.c()
+        self.check(lib().zh_sample_logits(self.h, logits.h, off, n, C.byref(pc), _ptr(h) if h.size else None,
+                                          h.size, u, C.byref(t)))
+        return t.value
 
     def gemm_xw(self, qtype, W, a_off, X, x_off, Y, y_off, M, K, N, acc_mode=0):
         """Y[n][m] (+)= X[n] . W[m] for N tokens (X fp16 [N][K], Y f32 [N][M])."""
