@@ -40,6 +40,11 @@ struct GemmP {
     const _Float16 *X;       // [N][ldx]
     const float *x_unscale;  // optional [N]: row n of X was stored times 1/x_unscale[n] (a power of two)
     uint32_t M, K, N, ldx, acc;
+    // split-K (one segment only): workgroup z of ksplit takes K-steps
+    // [z nst / ksplit, (z+1) nst / ksplit) and writes its f32 sums to
+    // part[z][N][M]; k_gemm_reduce adds them up in order
+    uint32_t ksplit;
+    float *part;
 };
 
 ZH_DEV _Float16 to_h(float v) { return (_Float16)v; }  // round to nearest even
@@ -159,7 +164,8 @@ __global__ __launch_bounds__(GT, 2) void k_gemm(GemmP p) {
     const uint32_t seg_start = sg ? p.seg_end[sg - 1] : 0u, Ms = p.seg_end[sg] - seg_start;
     const uint32_t j0 = jg - seg_start;
     const uint8_t *Wseg = p.segW[sg];
-    const uint32_t nst = p.K / KS;
+    const uint32_t nst_all = p.K / KS, z = blockIdx.z;
+    const uint32_t st_begin = z * nst_all / p.ksplit, nst = (z + 1) * nst_all / p.ksplit;
     const uint32_t bpb = QT == ZH_Q4_K ? 144 : 210;
     f32x4v acc[NI][NJ];
 #pragma unroll
@@ -187,8 +193,8 @@ __global__ __launch_bounds__(GT, 2) void k_gemm(GemmP p) {
             else load_q6k_unit(blk, st & 1, u4, wr[k]);
         }
     };
-    load_step(0);
-    for (uint32_t st = 0; st < nst; st++) {
+    load_step(st_begin);
+    for (uint32_t st = st_begin; st < nst; st++) {
 #pragma unroll
         for (int c = 0; c < XC; c++) {
             const uint32_t idx = c * GT + tid, t = idx / (KS / 8), ch = idx % (KS / 8);
@@ -226,13 +232,30 @@ __global__ __launch_bounds__(GT, 2) void k_gemm(GemmP p) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint32_t tok = n0 + wi * 64 + i * 16 + 4 * (lane / 16) + r;
-                if (tok < p.N && row < Ms) {
+                if (p.ksplit > 1) {
+                    if (tok < p.N && row < Ms) p.part[((size_t)z * p.N + tok) * p.M + row] = acc[i][j][r];
+                } else if (tok < p.N && row < Ms) {
                     float *yp = p.segY[sg] + (size_t)tok * p.segLdy[sg] + row;
                     const float v = p.x_unscale ? acc[i][j][r] * p.x_unscale[tok] : acc[i][j][r];  // exact
                     *yp = p.acc ? *yp + v : v;
                 }
             }
         }
+}
+
+// Split-K epilogue: Y[n][m] (+)= (sum over z of part[z][n][m]) * unscale[n],
+// the partial sums added in split order.
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part, uint32_t ksplit, uint32_t N,
+                                                     uint32_t M, float *__restrict__ Y, uint32_t ldy, uint32_t acc,
+                                                     const float *__restrict__ x_unscale) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint64_t)N * M) return;
+    const uint32_t n = (uint32_t)(i / M), m = (uint32_t)(i % M);
+    float v = part[i];
+    for (uint32_t z = 1; z < ksplit; z++) v += part[(size_t)z * N * M + i];
+    if (x_unscale) v *= x_unscale[n];  // exact: a power of two
+    float *yp = Y + (size_t)n * ldy + m;
+    *yp = acc ? *yp + v : v;
 }
 
 }  // namespace
@@ -264,11 +287,32 @@ int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *cons
         if (M[s] % 64) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: segment rows %u not a multiple of 64", M[s]);
     const uint32_t TJv = small ? 64 : 128;
     const uint32_t lds = (TI + TJv) * LDR * 2;
-    dim3 grid((end + TJv - 1) / TJv, ni);
+    // A single matrix with fewer tiles than two per CU (O, down) splits K so
+    // two workgroups share each CU (one's dequantisation overlapping the
+    // other's MFMAs); at least 8 K-steps per split.
+    const uint64_t tiles = (uint64_t)((end + TJv - 1) / TJv) * ni, slots = 2ull * (uint64_t)c->cu_count;
+    p.ksplit = 1;
+    if (nseg == 1 && tiles < slots && !getenv("ZH_NO_SPLITK")) {
+        uint32_t sk = (uint32_t)((slots + tiles - 1) / tiles);
+        while (sk > 1 && K / KS < 8 * sk) sk--;
+        p.ksplit = sk;
+    }
+    if (p.ksplit > 1) {
+        void *scr = nullptr;
+        int rc = zh_scratch(c, 4ull * p.ksplit * N * end, &scr);
+        if (rc) return rc;
+        p.part = (float *)scr;
+    }
+    dim3 grid((end + TJv - 1) / TJv, ni, p.ksplit);
 #define GL(Q, J) hipLaunchKernelGGL((k_gemm<Q, J>), grid, dim3(GT), lds, c->stream, p)
     if (qtype == ZH_Q4_K) { if (small) GL(ZH_Q4_K, 64); else GL(ZH_Q4_K, 128); }
     else { if (small) GL(ZH_Q6_K, 64); else GL(ZH_Q6_K, 128); }
 #undef GL
+    if (p.ksplit > 1) {
+        const uint64_t n = (uint64_t)N * end;
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c->stream, p.part, p.ksplit,
+                           N, end, Y[0], ldy[0], acc, x_unscale);
+    }
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
 }
