@@ -116,6 +116,9 @@ ZH_DEV void deq_q4k_unit(const RawQ4K &r, uint32_t p, uint32_t nib, _Float16 *ds
 // 128h + 32g + l: q6 = (ql[64h + l + 32(g&1)] >> 4(g>>1)) & 15 |
 // ((qh[32h + l] >> 2g) & 3) << 4; out = (d * sc[8h + l/16 + 2g]) * (q6 - 32).
 // The block may start 2-byte aligned: its bytes are realigned with alignbyte.
+// Four 6-bit values are assembled per dword (masks on the packed bytes); each
+// element is then one byte conversion and fma(ds, q6, -32 ds), which equals
+// the rounded product ds * (q6 - 32) (-32 ds is exact), then fp16.
 ZH_DEV void deq_q6k_unit(const RawQ6K &r, uint32_t g, _Float16 *dst) {
     const uint32_t sh = r.sh;
     const float d = h2f(__builtin_amdgcn_alignbyte(r.dw[1], r.dw[0], sh));
@@ -123,20 +126,20 @@ ZH_DEV void deq_q6k_unit(const RawQ6K &r, uint32_t g, _Float16 *dst) {
     const uint32_t i0 = 2 * g, i1 = 2 * g + 1;
     const float ds0 = __fmul_rn(d, (float)(int8_t)(((i0 < 4 ? s0 : s1) >> (8 * (i0 & 3))) & 0xFF));
     const float ds1 = __fmul_rn(d, (float)(int8_t)(((i1 < 4 ? s0 : s1) >> (8 * (i1 & 3))) & 0xFF));
+    const uint32_t nsh = 4 * (g >> 1), hsh = 2 * g;
 #pragma unroll
     for (int c = 0; c < 4; c++) {  // 8 elements l = 8c .. 8c+7
-        const uint32_t qlw0 = __builtin_amdgcn_alignbyte(r.ql[2 * c + 1], r.ql[2 * c], sh);
-        const uint32_t qlw1 = __builtin_amdgcn_alignbyte(r.ql[2 * c + 2], r.ql[2 * c + 1], sh);
-        const uint32_t qhw0 = __builtin_amdgcn_alignbyte(r.qh[2 * c + 1], r.qh[2 * c], sh);
-        const uint32_t qhw1 = __builtin_amdgcn_alignbyte(r.qh[2 * c + 2], r.qh[2 * c + 1], sh);
+        const float ds = c < 2 ? ds0 : ds1, nb = -32.f * ds;
+        uint32_t q[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t qlw = __builtin_amdgcn_alignbyte(r.ql[2 * c + h + 1], r.ql[2 * c + h], sh);
+            const uint32_t qhw = __builtin_amdgcn_alignbyte(r.qh[2 * c + h + 1], r.qh[2 * c + h], sh);
+            q[h] = ((qlw >> nsh) & 0x0F0F0F0Fu) | (((qhw >> hsh) & 0x03030303u) << 4);
+        }
         half8 o;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const uint32_t lb = ((e < 4 ? qlw0 : qlw1) >> (8 * (e & 3))) & 0xFF;
-            const uint32_t hb = ((e < 4 ? qhw0 : qhw1) >> (8 * (e & 3))) & 0xFF;
-            const int q6 = (int)(((lb >> (4 * (g >> 1))) & 15) | (((hb >> (2 * g)) & 3) << 4));
-            o[e] = to_h(__fmul_rn(c < 2 ? ds0 : ds1, (float)(q6 - 32)));
-        }
+        for (int e = 0; e < 8; e++) o[e] = to_h(fmaf(ds, (float)((q[e >> 2] >> (8 * (e & 3))) & 0xFF), nb));
         *(half8 *)(dst + 8 * c) = o;
     }
 }
@@ -278,9 +281,11 @@ int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *cons
     for (uint32_t s = nseg; s < 3; s++) p.seg_end[s] = end;
     p.M = end;
     const uint32_t ni = (N + TI - 1) / TI;
-    // 64-row tiles when 128-row tiles would leave CUs idle; every segment but
-    // the last must then be a whole number of tiles
-    bool small = (uint64_t)((end + 127) / 128) * ni < (uint64_t)c->cu_count;
+    // Stacked matrices: 64-row tiles when 128-row tiles would leave CUs idle;
+    // every segment but the last must then be a whole number of tiles. A
+    // single matrix keeps 128-row tiles and splits K instead (below).
+    bool small = (uint64_t)((end + 127) / 128) * ni < (uint64_t)c->cu_count &&
+                 (nseg > 1 || getenv("ZH_GEMM_TJ64"));
     for (uint32_t s = 0; s + 1 < nseg; s++)
         if (M[s] % 128) small = true;
     for (uint32_t s = 0; s + 1 < nseg; s++)
