@@ -163,6 +163,17 @@ int zh_flash_decode(zh_ctx *ctx, const zh_buf *q, const zh_buf *k_cache, const z
                     const zh_buf *page_table, uint32_t n_pages, uint32_t cache_tokens, zh_buf *out,
                     uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_len,
                     float attn_scale);
+/* Causal batched attention for prefill (flash_attn_batched.comp via
+ * AttentionDispatch.recordFlashAttnBatched, attention.zig:240-316): queries
+ * seq_start .. seq_start+n_queries-1 (q: f32 [n_queries][n_heads*head_dim],
+ * normed and roped), each over cache positions 0 .. its own, through the page
+ * table. out: fp16 [n_queries][n_heads*head_dim] (the O projection's GEMM
+ * input). fp16 operands on the MFMA units, f32 softmax and accumulation.
+ * head_dim 128; attn_scale 0 => 1/sqrt(head_dim). */
+int zh_flash_attn_batched(zh_ctx *ctx, const zh_buf *q, const zh_buf *k_cache, const zh_buf *v_cache,
+                          const zh_buf *page_table, uint32_t n_pages, uint32_t cache_tokens, zh_buf *out,
+                          uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_start,
+                          uint32_t n_queries, float attn_scale);
 /* softmax_topk_v2.comp / topKSoftmax (forward.zig:496-537): routing gets
  * [ids u32 x k][weights f32 x k]. n <= 256, k <= 16. */
 int zh_softmax_topk(zh_ctx *ctx, const zh_buf *logits, uint32_t n, uint32_t k, zh_buf *routing);

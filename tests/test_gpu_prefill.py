@@ -149,3 +149,46 @@ def test_engine_prefill_then_decode_continues(ctx, orc):
     assert got == ref, (got, ref)
     eng.deinit()
     om.close()
+
+
+def _causal_ref(q, k16, v16, pages, nh, nkv, seq_start, scale):
+    """f64 causal attention over the paged fp16 cache (cpuAttention per query,
+    forward_metal.zig:6600-6646, at positions seq_start + i)."""
+    n = q.shape[0]
+    hd = 128
+    out = np.zeros((n, nh * hd))
+    for i in range(n):
+        L = seq_start + i + 1
+        phys = np.array([pages[t // 16] * 16 + t % 16 for t in range(L)])
+        for h in range(nh):
+            kvh = h // (nh // nkv)
+            K = k16[kvh, phys].astype(np.float64)
+            V = v16[kvh, phys].astype(np.float64)
+            s = K @ q[i, h * hd:(h + 1) * hd].astype(np.float64) * scale
+            p = np.exp(s - s.max())
+            out[i, h * hd:(h + 1) * hd] = p @ V / p.sum()
+    return out
+
+
+@pytest.mark.parametrize("nh,nkv,seq_start,n", [(32, 8, 0, 200), (8, 8, 700, 70), (4, 1, 40, 130)],
+                         ids=["gqa4-200at0", "mha-70at700", "gqa4-130at40"])
+def test_flash_attn_batched_matches_reference(ctx, nh, nkv, seq_start, n):
+    """Causal batched attention vs an f64 reference on a permuted page table.
+    Operands are fp16 (q and P rounded, relative 2^-11), the output fp16:
+    |d| <= 4e-3 * max|row of the reference| + 1e-3."""
+    rng = np.random.default_rng(nh * 1000 + seq_start + n)
+    cache_tokens = 1024
+    n_pages = cache_tokens // 16
+    pages = rng.permutation(n_pages).astype(np.uint32)
+    k16 = rng.standard_normal((nkv, cache_tokens, 128)).astype(np.float16)
+    v16 = rng.standard_normal((nkv, cache_tokens, 128)).astype(np.float16)
+    q = rng.standard_normal((n, nh * 128)).astype(np.float32)
+    out = ctx.alloc(2 * n * nh * 128)
+    ctx.flash_attn_batched(ctx.upload(q), ctx.upload(k16), ctx.upload(v16), ctx.upload(pages), n_pages, cache_tokens,
+                           out, nh, nkv, 128, seq_start, n)
+    ctx.sync()
+    got = out.download(np.float16, n * nh * 128).astype(np.float64).reshape(n, -1)
+    ref = _causal_ref(q, k16, v16, pages, nh, nkv, seq_start, 1 / np.sqrt(128))
+    bound = 4e-3 * np.abs(ref).reshape(n, nh, 128).max(axis=2).repeat(128, axis=1) + 1e-3
+    err = np.abs(got - ref)
+    assert (err <= bound).all(), (err.max(), np.unravel_index(err.argmax(), err.shape))

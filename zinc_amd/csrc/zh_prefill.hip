@@ -392,86 +392,131 @@ __global__ __launch_bounds__(256) void k_swiglu_rows_f16(const float *__restrict
     for (uint32_t i = t; i < n; i += 256) out[(size_t)r * n + i] = (_Float16)(silu_mul_f(gr[i], ur[i]) * s2);
 }
 
-// Causal attention for a batch of queries (flash_attn_batched.comp; per query
-// the arithmetic of cpuAttention, forward_metal.zig:6600-6646: score =
-// dot(q, k) * scale, softmax, P * V). Workgroup = (q head, 16 queries): wave w
-// owns queries 4w..4w+3; keys go 64 per chunk (lane = key) with an online
-// softmax; P * V with lane = 2 output dims. Query i sits at position pos0 + i
-// and sees keys 0..pos0+i of the paged fp16 cache. Output fp16 [N][nq*128].
-constexpr int AP_Q = 16;
-__global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ q, const uint16_t *__restrict__ kc,
-                                                      const uint16_t *__restrict__ vc, const uint32_t *__restrict__ pages,
-                                                      uint32_t n_pages, uint32_t cache_tokens, uint32_t nq, uint32_t nkv,
-                                                      uint32_t pos0, uint32_t N, float scale, _Float16 *__restrict__ out) {
+// Causal prefill attention on the MFMA units (flash attention): workgroup =
+// one q head x AQ = 64 queries (16 per wave), key blocks of AK = 64 staged in
+// LDS (K row-major, V transposed to [d][key]). Per block each wave computes
+// S = Q K^T (16 x 64, v_mfma_f32_16x16x32_f16 over d), scales and masks it,
+// updates the running row maximum and sum (online softmax, f32), writes
+// P = exp(S - m) as fp16 to its own LDS tile (the D layout of S holds 4 rows
+// per lane; the A layout of the next product holds 8 keys of one row) and
+// accumulates O += P V (16 x 128). Q, K, V and P are fp16 operands with f32
+// accumulation. Query tiles run longest first (causal: tile t sees t + 1
+// blocks).
+constexpr int AQ = 64, AK = 64;
+constexpr int AKLD = 128 + 8;  // halfs per K row (272 B)
+constexpr int AVLD = AK + 8;   // halfs per transposed V row and per P row (144 B)
+__global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float *__restrict__ q, const uint16_t *__restrict__ kc,
+                                                           const uint16_t *__restrict__ vc,
+                                                           const uint32_t *__restrict__ pages, uint32_t n_pages,
+                                                           uint32_t cache_tokens, uint32_t nq, uint32_t nkv,
+                                                           uint32_t pos0, uint32_t N, float scale,
+                                                           _Float16 *__restrict__ out) {
     constexpr int HD = 128;
-    const uint32_t h = blockIdx.x, i0 = blockIdx.y * AP_Q, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t kvh = h / (nq / nkv);
-    __shared__ float qs[AP_Q][HD];
-    __shared__ float ps[4][4][64];
-    for (uint32_t e = tid; e < AP_Q * HD; e += 256) {
-        const uint32_t qi = e / HD, d = e % HD;
-        qs[qi][d] = q[(size_t)min(i0 + qi, N - 1) * nq * HD + (size_t)h * HD + d];
-    }
-    __syncthreads();
+    __shared__ __align__(16) _Float16 ks[AK * AKLD];
+    __shared__ __align__(16) uint16_t vt[HD * AVLD];
+    __shared__ __align__(16) _Float16 pl[4][16 * AVLD];
+    const uint32_t h = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t i0 = (gridDim.y - 1 - blockIdx.y) * AQ;  // longest tiles first
+    const uint32_t kvh = h / (nq / nkv), li = lane % 16, lg = lane / 16;
     const uint16_t *kh = kc + (size_t)kvh * cache_tokens * HD;
     const uint16_t *vh = vc + (size_t)kvh * cache_tokens * HD;
-    const uint32_t kmax = pos0 + min(i0 + AP_Q, N) - 1;  // last key any query of the workgroup sees
-    float m[4], l[4], acc[4][2];
+    // Q fragments (A operand): row i0 + 16 wave + li, d = 32 ks + 8 lg .. +7
+    half8 qa[4];
+    {
+        const float *qp = q + (size_t)min(i0 + 16 * wave + li, N - 1) * nq * HD + (size_t)h * HD + 8 * lg;
 #pragma unroll
-    for (int a = 0; a < 4; a++) { m[a] = -INFINITY; l[a] = 0.f; acc[a][0] = acc[a][1] = 0.f; }
-    for (uint32_t c0 = 0; c0 <= kmax; c0 += 64) {
-        const uint32_t t = min(c0 + lane, kmax);
-        const uint32_t pg = min(t / 16, n_pages - 1);
-        uint32_t ph = pages[pg] * 16 + t % 16;
-        ph = ph < cache_tokens ? ph : 0u;
-        const u32x4 *kr = (const u32x4 *)(kh + (size_t)ph * HD);
-        float s[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-        for (int c = 0; c < HD / 8; c++) {
-            const u32x4 kv = kr[c];
-            const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float kf = h2f(kw[e >> 1] >> (16 * (e & 1)));
-#pragma unroll
-                for (int a = 0; a < 4; a++) s[a] = fmaf(qs[4 * wave + a][8 * c + e], kf, s[a]);
-            }
-        }
-#pragma unroll
-        for (int a = 0; a < 4; a++) {
-            const uint32_t qpos = pos0 + i0 + 4 * wave + a;
-            const float sv = (c0 + lane <= qpos) ? s[a] * scale : -INFINITY;
-            const float mn = fmaxf(m[a], wave_max(sv));  // finite: key 0 is always visible
-            const float pr = expf(sv - mn), f = expf(m[a] - mn);
-            l[a] = fmaf(l[a], f, wave_sum(pr));
-            acc[a][0] *= f;
-            acc[a][1] *= f;
-            m[a] = mn;
-            ps[wave][a][lane] = pr;
-        }
-        // the wave's own LDS writes are visible to it after the wait the compiler inserts
-        const uint32_t nk = min(64u, kmax + 1 - c0);
-        for (uint32_t j = 0; j < nk; j++) {
-            const uint32_t tj = c0 + j;
-            const uint32_t pgj = min(tj / 16, n_pages - 1);
-            uint32_t phj = pages[pgj] * 16 + tj % 16;
-            phj = phj < cache_tokens ? phj : 0u;
-            const uint32_t vv = *(const uint32_t *)(vh + (size_t)phj * HD + 2 * lane);
-            const float v0 = h2f(vv), v1 = h2f(vv >> 16);
-#pragma unroll
-            for (int a = 0; a < 4; a++) {
-                acc[a][0] = fmaf(ps[wave][a][j], v0, acc[a][0]);
-                acc[a][1] = fmaf(ps[wave][a][j], v1, acc[a][1]);
-            }
+        for (int k4 = 0; k4 < 4; k4++) {
+            const f32x4 a = *(const f32x4 *)(qp + 32 * k4), b = *(const f32x4 *)(qp + 32 * k4 + 4);
+            qa[k4] = half8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                           (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
         }
     }
+    f32x4v o[8];
 #pragma unroll
-    for (int a = 0; a < 4; a++) {
-        const uint32_t i = i0 + 4 * wave + a;
+    for (int db = 0; db < 8; db++) o[db] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) { m[r] = -INFINITY; l[r] = 0.f; }
+    const uint32_t kmax = pos0 + min(i0 + AQ, N) - 1;  // last key any query of the workgroup sees
+    const uint32_t qpos = pos0 + i0 + 16 * wave + 4 * lg;  // position of this lane's row r = 0
+    _Float16 *pw = pl[wave];
+    for (uint32_t kb = 0; kb * AK <= kmax; kb++) {
+        // stage the key block: K rows as they are, V transposed (rows past
+        // kmax are loaded clamped and masked below)
+        for (uint32_t c = tid; c < AK * 16; c += 256) {
+            const uint32_t key = c / 16, ch = c % 16, t = min(kb * AK + key, kmax);
+            uint32_t ph = pages[min(t / 16, n_pages - 1)] * 16 + t % 16;
+            ph = ph < cache_tokens ? ph : 0u;
+            const u32x4 kv = *(const u32x4 *)(kh + (size_t)ph * HD + ch * 8);
+            const u32x4 vv = *(const u32x4 *)(vh + (size_t)ph * HD + ch * 8);
+            *(u32x4 *)(ks + key * AKLD + ch * 8) = kv;
+            const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) vt[(ch * 8 + e) * AVLD + key] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        }
+        __syncthreads();
+        f32x4v sc[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++) {
+            sc[jb] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k4 = 0; k4 < 4; k4++) {
+                const half8 b = *(const half8 *)(ks + (16 * jb + li) * AKLD + 32 * k4 + 8 * lg);
+                sc[jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[k4], b, sc[jb], 0, 0, 0);
+            }
+        }
+        float mb[4], f[4], ls[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            mb[r] = -INFINITY;
+#pragma unroll
+            for (int jb = 0; jb < 4; jb++) {
+                const uint32_t key = kb * AK + 16 * jb + li;
+                const float v = key <= qpos + r ? sc[jb][r] * scale : -INFINITY;
+                sc[jb][r] = v;
+                mb[r] = fmaxf(mb[r], v);
+            }
+            // block 0 holds key 0, visible to every row: m is finite from then on
+            const float mn = fmaxf(m[r], row16_max(mb[r]));
+            f[r] = expf(m[r] - mn);
+            m[r] = mn;
+            ls[r] = 0.f;
+        }
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float p = expf(sc[jb][r] - m[r]);
+                ls[r] += p;
+                pw[(4 * lg + r) * AVLD + 16 * jb + li] = (_Float16)p;
+            }
+#pragma unroll
+        for (int r = 0; r < 4; r++) l[r] = fmaf(l[r], f[r], row16_sum(ls[r]));
+#pragma unroll
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[db][r] *= f[r];
+        // the wave reads back its own P tile (LDS operations of a wave complete in order)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int k2 = 0; k2 < 2; k2++) {
+            const half8 a = *(const half8 *)(pw + li * AVLD + 32 * k2 + 8 * lg);
+#pragma unroll
+            for (int db = 0; db < 8; db++) {
+                const half8 b = *(const half8 *)(vt + (16 * db + li) * AVLD + 32 * k2 + 8 * lg);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, o[db], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // the block's K / V tiles are rewritten next
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t i = i0 + 16 * wave + 4 * lg + r;
         if (i < N) {
-            _Float16 *o = out + (size_t)i * nq * HD + (size_t)h * HD + 2 * lane;
-            o[0] = (_Float16)(acc[a][0] / l[a]);
-            o[1] = (_Float16)(acc[a][1] / l[a]);
+            const float inv = 1.0f / l[r];
+            _Float16 *op = out + (size_t)i * nq * HD + (size_t)h * HD + li;
+#pragma unroll
+            for (int db = 0; db < 8; db++) op[16 * db] = (_Float16)(o[db][r] * inv);
         }
     }
 }
@@ -494,8 +539,30 @@ int zhk_attn_prefill(zh_ctx *c, const float *q, const uint16_t *kc, const uint16
                      uint32_t n_pages, uint32_t cache_tokens, uint32_t nq, uint32_t nkv, uint32_t hd, uint32_t pos0,
                      uint32_t N, float scale, _Float16 *out) {
     if (hd != 128 || nkv == 0 || nq % nkv) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "attn_prefill heads");
-    hipLaunchKernelGGL(k_attn_prefill, dim3(nq, (N + AP_Q - 1) / AP_Q), dim3(256), 0, c->stream, q, kc, vc, pages,
+    hipLaunchKernelGGL(k_attn_prefill_mfma, dim3(nq, (N + AQ - 1) / AQ), dim3(256), 0, c->stream, q, kc, vc, pages,
                        n_pages, cache_tokens, nq, nkv, pos0, N, scale, out);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
+}
+
+// recordFlashAttnBatched (attention.zig:240-316) over caller buffers.
+extern "C" int zh_flash_attn_batched(zh_ctx *c, const zh_buf *q, const zh_buf *kc, const zh_buf *vc,
+                                     const zh_buf *pages, uint32_t n_pages, uint32_t cache_tokens, zh_buf *out,
+                                     uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t seq_start, uint32_t nq_tok,
+                                     float attn_scale) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    if (!q || !kc || !vc || !pages || !out || hd != 128 || nkv == 0 || nh % nkv || nq_tok == 0)
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "flash_attn_batched: heads %u/%u head_dim %u n %u", nh, nkv, hd,
+                          nq_tok);
+    if ((uint64_t)seq_start + nq_tok > 16ull * n_pages)
+        return zh_set_err(c, ZH_ERR_CONTEXT_LENGTH_EXCEEDED, "positions %u + %u", seq_start, nq_tok);
+    const uint64_t row = (uint64_t)nh * hd;
+    if (4ull * row * nq_tok > q->size || 2ull * row * nq_tok > out->size ||
+        2ull * nkv * cache_tokens * hd > kc->size || 2ull * nkv * cache_tokens * hd > vc->size ||
+        4ull * n_pages > pages->size)
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "flash_attn_batched range");
+    const float scale = attn_scale != 0.f ? attn_scale : 1.0f / sqrtf((float)hd);
+    return zhk_attn_prefill(c, (const float *)q->ptr, (const uint16_t *)kc->ptr, (const uint16_t *)vc->ptr,
+                            (const uint32_t *)pages->ptr, n_pages, cache_tokens, nh, nkv, hd, seq_start, nq_tok, scale,
+                            (_Float16 *)out->ptr);
 }

@@ -124,6 +124,7 @@ SIGNATURES = {
     "zh_engine_time_kernel": (_i32, [_P, _u32, _u32, _P]),
     "zh_engine_group_bytes": (_u64, [_P, _u32, _u32]),
     "zh_engine_tensor_type": (_i32, [_P, _u64, C.POINTER(_u32)]),
+    "zh_flash_attn_batched": (_i32, [_P, _P, _P, _P, _P, _u32, _u32, _P, _u32, _u32, _u32, _u32, _u32, _f32]),
     "zh_sample_logits": (_i32, [_P, _P, _u64, _u32, C.POINTER(SamplingParamsC), _P, _u32, C.c_double,
                                 C.POINTER(_u32)]),
     "zh_engine_sample": (_i32, [_P, C.POINTER(SamplingParamsC), _P, _u32, C.c_double, C.POINTER(_u32)]),
@@ -335,6 +336,10 @@ class Context:
 
     def argmax(self, logits, n, result, result_off=0):
         self.check(lib().zh_argmax(self.h, logits.h, n, result.h, result_off))
+
+    def flash_attn_batched(self, q, kc, vc, pages, n_pages, cache_tokens, out, nh, nkv, hd, seq_start, n, scale=0.0):
+        self.check(lib().zh_flash_attn_batched(self.h, q.h, kc.h, vc.h, pages.h, n_pages, cache_tokens, out.h, nh, nkv,
+                                               hd, seq_start, n, scale))
 
     def sample_logits(self, logits, off, n, params, history=(), u=0.0):
         """sampleFromLogits on the device (u: the random.float(f64) draw)."""
