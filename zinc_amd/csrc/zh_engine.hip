@@ -736,7 +736,8 @@ extern "C" int zh_engine_generate(zh_engine *e, const uint32_t *prompt, uint32_t
 static bool prefill_batched_ok(const zh_engine *e) {
     const zh_model_config &m = e->c;
     auto gemm_t = [](const Tensor &t) { return t.type == ZH_Q4_K || t.type == ZH_Q6_K; };
-    if (m.n_experts || m.head_dim != 128 || m.hidden % 256 || m.ffn % 256 || (m.n_heads * m.head_dim) % 256)
+    if (m.n_experts || m.head_dim != 128 || m.hidden % 256 || m.ffn % 256 || (m.n_heads * m.head_dim) % 256 ||
+        m.hidden > 16384 || m.ffn > 16384)  // the row kernels hold a row in registers
         return false;
     for (const Layer &y : e->L)
         if (!gemm_t(y.wq) || !gemm_t(y.wk) || !gemm_t(y.wv) || !gemm_t(y.wo) || !gemm_t(y.gate) || !gemm_t(y.up) ||

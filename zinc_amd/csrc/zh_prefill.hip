@@ -349,6 +349,12 @@ extern "C" int zh_gemm_xw(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a
 // ---------------------------------------------------------------------------
 namespace {
 
+// Row kernels: one workgroup per token row, the row held in registers
+// between the reduction and the write (RV 16-byte chunks per thread cover
+// n <= 1024 RV elements; n a multiple of 4).
+constexpr int RV = 16;
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
 // RMSNorm of `rows` rows of n (cpuRmsNormMul, forward.zig:618-626:
 // w[i] * (x[i] * (1/sqrt(sum x^2 / n + eps)))), written as fp16 GEMM input.
 __global__ __launch_bounds__(256) void k_rms_norm_rows_f16(const float *__restrict__ x, const float *__restrict__ w,
@@ -356,13 +362,28 @@ __global__ __launch_bounds__(256) void k_rms_norm_rows_f16(const float *__restri
     const uint32_t r = blockIdx.x, t = threadIdx.x;
     const float *xr = x + (size_t)r * n;
     __shared__ float red[4];
+    f32x4 v[RV];
     float sq = 0.f;
-    for (uint32_t i = t; i < n; i += 256) sq = fmaf(xr[i], xr[i], sq);
+#pragma unroll
+    for (int j = 0; j < RV; j++) {
+        const uint32_t i = 4 * (t + 256 * j);
+        v[j] = i < n ? *(const f32x4 *)(xr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+        sq = fmaf(v[j].x, v[j].x, fmaf(v[j].y, v[j].y, fmaf(v[j].z, v[j].z, fmaf(v[j].w, v[j].w, sq))));
+    }
     sq = wave_sum(sq);
     if ((t & 63) == 0) red[t >> 6] = sq;
     __syncthreads();
     const float rms_inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)n + eps);
-    for (uint32_t i = t; i < n; i += 256) out[(size_t)r * n + i] = (_Float16)(w[i] * (xr[i] * rms_inv));
+#pragma unroll
+    for (int j = 0; j < RV; j++) {
+        const uint32_t i = 4 * (t + 256 * j);
+        if (i < n) {
+            const f32x4 wv = *(const f32x4 *)(w + i);
+            *(half4 *)(out + (size_t)r * n + i) =
+                half4{(_Float16)(wv.x * (v[j].x * rms_inv)), (_Float16)(wv.y * (v[j].y * rms_inv)),
+                      (_Float16)(wv.z * (v[j].z * rms_inv)), (_Float16)(wv.w * (v[j].w * rms_inv))};
+        }
+    }
 }
 
 // SwiGLU (cpuSwiGLU, forward_metal.zig:6567-6572), one row per workgroup, to
@@ -376,8 +397,19 @@ __global__ __launch_bounds__(256) void k_swiglu_rows_f16(const float *__restrict
     const uint32_t r = blockIdx.x, t = threadIdx.x;
     const float *gr = g + (size_t)r * n, *ur = u + (size_t)r * n;
     __shared__ float red[4];
+    f32x4 v[RV];
     float mx = 0.f;
-    for (uint32_t i = t; i < n; i += 256) mx = fmaxf(mx, fabsf(silu_mul_f(gr[i], ur[i])));
+#pragma unroll
+    for (int j = 0; j < RV; j++) {
+        const uint32_t i = 4 * (t + 256 * j);
+        if (i < n) {
+            const f32x4 gv = *(const f32x4 *)(gr + i), uv = *(const f32x4 *)(ur + i);
+            v[j] = f32x4{silu_mul_f(gv.x, uv.x), silu_mul_f(gv.y, uv.y), silu_mul_f(gv.z, uv.z), silu_mul_f(gv.w, uv.w)};
+        } else {
+            v[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
     mx = wave_max(mx);
     if ((t & 63) == 0) red[t >> 6] = mx;
     __syncthreads();
@@ -389,7 +421,13 @@ __global__ __launch_bounds__(256) void k_swiglu_rows_f16(const float *__restrict
     const float sc = ldexpf(1.0f, 14 - E), inv = ldexpf(1.0f, E - 14);
     if (t == 0) unscale[r] = (mx > 0.f && mx < INFINITY) ? inv : 1.0f;
     const float s2 = (mx > 0.f && mx < INFINITY) ? sc : 1.0f;
-    for (uint32_t i = t; i < n; i += 256) out[(size_t)r * n + i] = (_Float16)(silu_mul_f(gr[i], ur[i]) * s2);
+#pragma unroll
+    for (int j = 0; j < RV; j++) {
+        const uint32_t i = 4 * (t + 256 * j);
+        if (i < n)
+            *(half4 *)(out + (size_t)r * n + i) =
+                half4{(_Float16)(v[j].x * s2), (_Float16)(v[j].y * s2), (_Float16)(v[j].z * s2), (_Float16)(v[j].w * s2)};
+    }
 }
 
 // Causal prefill attention on the MFMA units (flash attention): workgroup =
@@ -525,12 +563,14 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float *__restri
 
 int zhk_rms_norm_rows_f16(zh_ctx *c, const float *x, const float *w, _Float16 *out, uint32_t n, uint32_t rows,
                           float eps) {
+    if (n % 4 || n > 1024u * RV) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "rms_norm_rows n %u", n);
     hipLaunchKernelGGL(k_rms_norm_rows_f16, dim3(rows), dim3(256), 0, c->stream, x, w, out, n, eps);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
 }
 int zhk_swiglu_rows_f16(zh_ctx *c, const float *g, const float *u, _Float16 *out, float *unscale, uint32_t n,
                         uint32_t rows) {
+    if (n % 4 || n > 1024u * RV) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "swiglu_rows n %u", n);
     hipLaunchKernelGGL(k_swiglu_rows_f16, dim3(rows), dim3(256), 0, c->stream, g, u, out, unscale, n);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
