@@ -517,6 +517,13 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
                                  Wf(y.attn_norm), m.eps, nullptr, H, 0));
                 i0 = i1;
             }
+        } else if (lds && qkv_t[0]->type == qkv_t[1]->type && qkv_t[1]->type == qkv_t[2]->type &&
+                   zhk_dmmv_lds_supported(y.wq.type, H) && qkv_m[0] % 2 == 0 && qkv_m[1] % 2 == 0) {
+            // formats without a tile kernel (Q8_0, MXFP4): attn_norm fused into
+            // the LDS-staged mat-vec of the three stacked matrices
+            const uint8_t *ws[3] = {W(y.wq), W(y.wk), W(y.wv)};
+            ERC(zhk_dmmv_lds_plain(c, y.wq.type, 3, ws, qkv_y, qkv_m, e->hidden, Wf(y.attn_norm), m.eps, H, 0,
+                                   nullptr, 0, nullptr, nullptr));
         } else {
             ERC(zhk_rms_norm(c, e->hidden, Wf(y.attn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
             for (uint32_t i0 = 0; i0 < 3;) {
