@@ -164,6 +164,45 @@ def test_per_tensor_mix_matches_oracle(ctx, orc, tmp_path):
     om.close()
 
 
+def test_moe_f32_router_matches_oracle(ctx, orc, tmp_path):
+    """llama.cpp keeps ffn_gate_inp (the MoE router) in f32: a qwen3moe file
+    with f32 routers loads, and engine and oracle given the same bytes agree."""
+    import zinc_amd
+    print("moe f32 router vs oracle", flush=True)
+    cfg = SMALL_MOE
+    src = zinc_amd.InferenceEngine(ctx, cfg)
+    rng = np.random.default_rng(17)
+    routers = {orc.S_LAYER(l, orc.K_ROUTER): (rng.standard_normal((cfg["n_experts"], cfg["hidden"])) * 0.05)
+               .astype(np.float32) for l in range(cfg["n_layers"])}
+    tensors = []
+    for stream, name, dims in G.engine_tensor_list(cfg):
+        if stream in routers:
+            tensors.append((name, dims, 0, routers[stream]))
+        else:
+            tensors.append((name, dims, src.tensor_type(stream), src.tensor_bytes(stream)))
+    p = "qwen3moe."
+    meta = [("general.architecture", "qwen3moe"), (p + "block_count", (G.U32, cfg["n_layers"])),
+            (p + "embedding_length", (G.U32, cfg["hidden"])), (p + "attention.head_count", (G.U32, cfg["n_heads"])),
+            (p + "attention.head_count_kv", (G.U32, cfg["n_kv_heads"])), (p + "attention.key_length", (G.U32, 128)),
+            (p + "expert_count", (G.U32, cfg["n_experts"])), (p + "expert_used_count", (G.U32, cfg["n_experts_used"])),
+            (p + "expert_feed_forward_length", (G.U32, cfg["expert_ffn"])), (p + "rope.freq_base", (G.F32, 1e6)),
+            (p + "attention.layer_norm_rms_epsilon", (G.F32, 1e-6))]
+    path = tmp_path / "moe_f32router.gguf"
+    G.write_gguf(path, meta, tensors)
+    eng = zinc_amd.InferenceEngine.from_gguf(ctx, path, cfg["max_ctx"])
+    assert eng.config["type_router"] == 0
+    om = orc.Model(cfg)
+    for stream, w in routers.items():
+        om.set_tensor(stream, 0, w)
+        assert eng.tensor_type(stream) == 0 and np.array_equal(eng.tensor_bytes(stream).view(np.float32), w.ravel())
+    g, o = _decode(eng), _oracle_decode(om)
+    assert _close(g[1], o[1]), np.abs(g[1] - o[1]).max()
+    assert g[0] == o[0] and g[2] == o[2]
+    src.deinit()
+    eng.deinit()
+    om.close()
+
+
 def test_tied_embeddings(ctx, tmp_path):
     """No output.weight: the LM head reads token_embd.weight, exactly as a
     file whose output.weight is a copy of token_embd.weight."""

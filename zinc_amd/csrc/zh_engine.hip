@@ -188,7 +188,8 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
     uint32_t types[] = {c.type_attn, c.type_ffn_gate_up, c.type_ffn_down, c.type_lm_head, c.type_embd};
     for (uint32_t t : types)
         if (!dmmv_type_ok(t)) return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "type %u", t);
-    if (c.n_experts && !dmmv_type_ok(c.type_router)) return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "router");
+    if (c.n_experts && !dmmv_type_ok(c.type_router) && c.type_router != ZH_F32)
+        return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "router");
     if (c.type_more_bits && !dmmv_type_ok(c.type_more_bits))
         return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "type_more_bits %u", c.type_more_bits);
 
@@ -241,9 +242,16 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
     }
     // every matrix in a format the mat-vec kernels take; the embedding in one
     // the row gather takes; expert gate and up in one format
+    // norm weights are f32; a MoE router is f32 or a mat-vec format; every
+    // other matrix is in a mat-vec format
     for (auto &kv : e->tensors) {
         const Tensor &t = kv.second;
-        if (t.type != ZH_F32 && !dmmv_type_ok(t.type)) {
+        const uint64_t kind = kv.first & 0xFF;
+        const bool norm = kv.first == S_OUTPUT_NORM || (kv.first > 0xFF && (kind == K_ATTN_NORM || kind == K_Q_NORM ||
+                                                                             kind == K_K_NORM || kind == K_FFN_NORM));
+        const bool router = kv.first > 0xFF && kind == K_ROUTER;
+        const bool ok = norm ? t.type == ZH_F32 : (dmmv_type_ok(t.type) || (router && t.type == ZH_F32));
+        if (!ok) {
             const uint64_t st = kv.first;
             delete e;
             return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "tensor %llu: type %u", (unsigned long long)st, t.type);
@@ -499,7 +507,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         const bool lpb_ffn = lpb && m.n_experts == 0 && y.gate.type == ZH_Q4_K && y.up.type == ZH_Q4_K &&
                              zhk_lpb_supported(ZH_Q4_K, H) && zhk_lpb_supported(y.down.type, m.ffn);
         const bool lds_moe = lds && m.n_experts && m.n_experts <= 256 && m.n_experts_used <= 8 &&
-                             zhk_dmmv_lds_supported(y.router.type, H) &&
+                             (y.router.type == ZH_F32 || zhk_dmmv_lds_supported(y.router.type, H)) &&
                              zhk_dmmv_lds_supported(y.edown.type, m.expert_ffn) && m.expert_ffn % 32 == 0;
         // Q, K and V: one launch per run of equal types (one launch when all agree)
         const Tensor *qkv_t[3] = {&y.wq, &y.wk, &y.wv};
@@ -579,8 +587,16 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             const uint8_t *wr = W(y.router);
             float *rl = e->rl;
             if (mask & SK_FFN_IN) {
-                ERC(zhk_dmmv_lds_plain(c, y.router.type, 1, &wr, &rl, &E, e->hidden, Wf(y.ffn_norm), m.eps, H, 0,
-                                       e->xq_h, k, e->routing, e->router_cnt));
+                if (y.router.type == ZH_F32) {
+                    // an f32 router: ffn_norm (also leaving the XQ activation
+                    // for the experts), the f32 mat-vec, then top-k
+                    ERC(zhk_rms_norm(c, e->hidden, Wf(y.ffn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
+                    ERC(zhk_matvec_f32(c, Wf(y.router), e->norm, e->rl, E, H));
+                    ERC(zhk_softmax_topk(c, e->rl, E, k, e->routing));
+                } else {
+                    ERC(zhk_dmmv_lds_plain(c, y.router.type, 1, &wr, &rl, &E, e->hidden, Wf(y.ffn_norm), m.eps, H, 0,
+                                           e->xq_h, k, e->routing, e->router_cnt));
+                }
                 ERC(zhk_dmmv_moe(c, y.egate.type, W(y.egate), zh_tensor_bytes(y.egate.type, F, H),
                                  e->routing, e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
             }
@@ -606,7 +622,8 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             ERC(zhk_dmmv(c, y.down.type, W(y.down), e->xq_f, e->hidden, H, m.ffn, 1));
         } else {
             const uint32_t F = m.expert_ffn, k = m.n_experts_used;
-            ERC(zhk_dmmv(c, y.router.type, W(y.router), e->xq_h, e->rl, m.n_experts, H, 0));
+            if (y.router.type == ZH_F32) ERC(zhk_matvec_f32(c, Wf(y.router), e->norm, e->rl, m.n_experts, H));
+            else ERC(zhk_dmmv(c, y.router.type, W(y.router), e->xq_h, e->rl, m.n_experts, H, 0));
             ERC(zhk_softmax_topk(c, e->rl, m.n_experts, k, e->routing));
             ERC(zhk_dmmv_moe(c, y.egate.type, W(y.egate), zh_tensor_bytes(y.egate.type, F, H), e->routing,
                              e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));

@@ -91,6 +91,8 @@ int zhk_synth_vector(zh_ctx *ctx, void *dst, uint32_t kind, uint64_t n, float sc
 int zhk_rms_norm(zh_ctx *ctx, const float *x, const float *w, uint32_t w_len, float *out, void *xq,
                  uint32_t n, uint32_t n_groups, float eps);
 int zhk_swiglu(zh_ctx *ctx, const float *g, const float *u, float *out, uint32_t n);
+// y = W x for f32 weights (row-major M x K, K % 4 == 0).
+int zhk_matvec_f32(zh_ctx *ctx, const float *W, const float *x, float *y, uint32_t M, uint32_t K);
 struct zh_pos_src {  // where a kernel reads the position: host scalar or device word
     uint32_t value;
     const uint32_t *dev;  // if non-null: position = *dev + value

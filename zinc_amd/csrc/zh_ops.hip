@@ -936,6 +936,33 @@ __global__ __launch_bounds__(64) void k_softmax_topk(const float *logits, uint32
     topk_softmax_wave(vals, n, k, routing);
 }
 
+// f32 weights (a MoE router kept unquantised, as llama.cpp's quantiser leaves
+// ffn_gate_inp): y[r] = sum_k W[r][k] x[k], one wave per row, each lane
+// summing its 4-element chunks in order, then a fixed DPP reduction.
+__global__ __launch_bounds__(256) void k_matvec_f32(const float *__restrict__ W, const float *__restrict__ x,
+                                                    float *__restrict__ y, uint32_t M, uint32_t K) {
+    const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= M) return;  // uniform per wave
+    const float *w = W + (size_t)r * K;
+    float s = 0.f;
+    for (uint32_t k = 4 * lane; k < K; k += 256) {
+        const f32x4 a = *(const f32x4 *)(w + k), b = *(const f32x4 *)(x + k);
+        s = fmaf(a.x, b.x, s);
+        s = fmaf(a.y, b.y, s);
+        s = fmaf(a.z, b.z, s);
+        s = fmaf(a.w, b.w, s);
+    }
+    s = wave_sum(s);
+    if (lane == 0) y[r] = s;
+}
+
+int zhk_matvec_f32(zh_ctx *c, const float *W, const float *x, float *y, uint32_t M, uint32_t K) {
+    if (M == 0 || K % 4) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "matvec_f32 M %u K %u", M, K);
+    hipLaunchKernelGGL(k_matvec_f32, dim3((M + 3) / 4), dim3(256), 0, c->stream, W, x, y, M, K);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
 int zhk_softmax_topk(zh_ctx *c, const float *logits, uint32_t n, uint32_t k, uint32_t *routing) {
     hipLaunchKernelGGL(k_softmax_topk, dim3(1), dim3(64), 0, c->stream, logits, n, k, routing);
     ZH_LAUNCH_CHECK(c);
