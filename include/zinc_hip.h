@@ -324,6 +324,13 @@ int zh_gguf_model_config(const zh_gguf *f, uint32_t max_ctx, zh_model_config *cf
  * not take: ZH_ERR_UNSUPPORTED_QUANT_TYPE. Without output.weight the LM head
  * reads token_embd.weight (tied embeddings). */
 int zh_engine_create_gguf(zh_ctx *ctx, const zh_gguf *f, uint32_t max_ctx, zh_engine **out);
+/* Concurrent sequences (no counterpart in the reference, whose engine decodes
+ * one sequence): a second engine on context `ctx` (its own HIP stream) over
+ * the weights of `base` -- own KV cache (max_ctx tokens, 0: base's), own
+ * activations and step graph. Engines on different contexts decode
+ * independent sequences at the same time from different host threads,
+ * sharing one copy of the weights. Destroy sharing engines before base. */
+int zh_engine_create_shared(zh_ctx *ctx, zh_engine *base, uint32_t max_ctx, zh_engine **out);
 /* The storage type of an engine tensor (by stream id, as zh_engine_tensor). */
 int zh_engine_tensor_type(zh_engine *eng, uint64_t stream, uint32_t *type);
 

@@ -48,6 +48,7 @@ struct zh_engine {
     zh_ctx *ctx = nullptr;
     zh_model_config c{};
     uint8_t *arena = nullptr;  // all weights
+    bool owns_arena = true;    // false: the weights of another engine (zh_engine_create_shared)
     uint64_t arena_bytes = 0;
     std::map<uint64_t, Tensor> tensors;
     Tensor embd, out_norm, lm;
@@ -171,6 +172,7 @@ struct BuildOpts {
     std::function<uint32_t(uint64_t stream, uint32_t dflt)> type_of;
     bool synth = true;
     bool tied_lm = false;
+    uint8_t *shared_arena = nullptr;  // use these weights (same layout) instead of allocating
 };
 
 static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts &opt, zh_engine **out) {
@@ -263,14 +265,21 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
             return zh_set_err(ctx, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "expert gate/up types differ");
         }
     e->arena_bytes = off + 256;
-    hipError_t he = hipMalloc((void **)&e->arena, e->arena_bytes);
-    if (he != hipSuccess) {
-        delete e;
-        return zh_set_err(ctx, ZH_ERR_OUT_OF_MEMORY, "weights (%llu B): %s", (unsigned long long)off, hipGetErrorString(he));
+    hipError_t he = hipSuccess;
+    if (opt.shared_arena) {
+        e->arena = opt.shared_arena;
+        e->owns_arena = false;
+    } else {
+        he = hipMalloc((void **)&e->arena, e->arena_bytes);
+        if (he != hipSuccess) {
+            delete e;
+            return zh_set_err(ctx, ZH_ERR_OUT_OF_MEMORY, "weights (%llu B): %s", (unsigned long long)off,
+                              hipGetErrorString(he));
+        }
     }
     // --- synthetic weights (same streams as the oracle)
     for (auto &kv : e->tensors) {
-        if (!opt.synth) break;
+        if (!opt.synth || opt.shared_arena) break;
         if (kv.first == S_OUTPUT && opt.tied_lm) continue;
         const Tensor &t = kv.second;
         int rc;
@@ -418,6 +427,48 @@ extern "C" int zh_engine_sample(zh_engine *e, const zh_sampling_params *p, const
     return zhk_sample_host(e->ctx, e->logits, e->c.vocab, p, history, nh, u, token);
 }
 
+// A second engine over the weights of `base`, on its own context (stream),
+// with its own KV cache, activations and step graph: independent sequences
+// decode concurrently on one device, reading one copy of the weights. Both
+// contexts are marked concurrent (the attention merge then never waits on
+// other workgroups of its grid; base's captured step graphs are dropped and
+// re-captured that way). Destroy sharing engines before base.
+extern "C" int zh_engine_create_shared(zh_ctx *ctx, zh_engine *base, uint32_t max_ctx, zh_engine **out) {
+    if (!ctx || !base || !out) return ZH_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    if (base->ctx->device != ctx->device) return zh_set_err(ctx, ZH_ERR_INVALID_ARGUMENT, "shared engine on another device");
+    zh_model_config cfg = base->c;
+    if (max_ctx) cfg.max_ctx = (max_ctx + 15) / 16 * 16;
+    BuildOpts o;
+    o.synth = false;
+    o.shared_arena = base->arena;
+    o.tied_lm = base->lm.off == base->embd.off;
+    o.type_of = [base](uint64_t stream, uint32_t dflt) {
+        auto it = base->tensors.find(stream);
+        return it == base->tensors.end() ? dflt : it->second.type;
+    };
+    zh_engine *e = nullptr;
+    ERC(engine_build(ctx, &cfg, o, &e));
+    for (auto &kv : e->tensors) {  // same layout over the same arena
+        auto it = base->tensors.find(kv.first);
+        if (it == base->tensors.end() || it->second.off != kv.second.off || it->second.bytes != kv.second.bytes) {
+            zh_engine_destroy(e);
+            return zh_set_err(ctx, ZH_ERR_INVALID_ARGUMENT, "shared engine layout differs (tensor %llu)",
+                              (unsigned long long)kv.first);
+        }
+    }
+    ctx->concurrent = true;
+    if (!base->ctx->concurrent) {
+        base->ctx->concurrent = true;
+        hipStreamSynchronize(base->ctx->stream);
+        if (base->g_out) hipGraphExecDestroy(base->g_out);
+        if (base->g_noout) hipGraphExecDestroy(base->g_noout);
+        base->g_out = base->g_noout = nullptr;
+    }
+    *out = e;
+    return ZH_OK;
+}
+
 extern "C" int zh_engine_tensor_type(zh_engine *e, uint64_t stream, uint32_t *type) {
     if (!e || !type) return ZH_ERR_INVALID_ARGUMENT;
     auto it = e->tensors.find(stream);
@@ -431,7 +482,7 @@ extern "C" void zh_engine_destroy(zh_engine *e) {
     hipStreamSynchronize(e->ctx->stream);
     if (e->g_out) hipGraphExecDestroy(e->g_out);
     if (e->g_noout) hipGraphExecDestroy(e->g_noout);
-    if (e->arena) hipFree(e->arena);
+    if (e->arena && e->owns_arena) hipFree(e->arena);
     if (e->kv) hipFree(e->kv);
     if (e->act_arena) hipFree(e->act_arena);
     if (e->pf.arena) hipFree(e->pf.arena);

@@ -20,6 +20,10 @@ struct zh_ctx {
     // Stream-ordered scratch for zh_dmmv's activation quantisation.
     void *scratch = nullptr;
     uint64_t scratch_size = 0;
+    // Other contexts run kernels on this device at the same time (engines
+    // sharing weights): kernels must not wait on workgroups of their own grid
+    // that may not be resident (the attention merge then needs no waiting).
+    bool concurrent = false;
 };
 
 int zh_set_err(zh_ctx *ctx, int code, const char *fmt, ...);

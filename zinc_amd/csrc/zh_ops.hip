@@ -275,6 +275,7 @@ struct AttnP {
     uint8_t *xq;         // optional XQ image of out
     uint32_t nq;
     uint32_t nd;         // AD_IDENT: target chunks per kv head
+    uint32_t no_wait;    // the last arrival merges every q head (no merger waits for others)
 };
 
 ZH_DEV float sum8(float v) { return row8_sum(v); }  // over the 8 lanes of a token group
@@ -784,7 +785,9 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     const uint32_t prev = s_prev;
     // With at least G chunks the last G arrivals merge one q head each (a
     // merger reads 1/G of the partials); otherwise the last arrival merges all.
-    const bool split = G > 1 && nv >= (uint32_t)G;
+    // (no_wait: other kernels share the device, so the earlier mergers'
+    // bounded wait could wait on chunks that are not resident.)
+    const bool split = G > 1 && nv >= (uint32_t)G && !p.no_wait;
     const uint32_t nm = split ? (uint32_t)G : 1u;
     if (prev + nm < nv) return;
     const uint32_t slot = prev + nm - nv;  // nm - 1: the last arrival
@@ -826,6 +829,7 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
                        bool ident) {
     AttnP p = p0;
     p.nd = attn_nd(nkv, c->cu_count);
+    p.no_wait = c->concurrent ? 1u : 0u;
     p.n_chunks = attn_n_chunks(max_seq, p.nd);
     // identity pages: at most nd chunks per kv head at any context (longer
     // chunks hold several sub-chunks)

@@ -58,6 +58,21 @@ class InferenceEngine:
             eng.h = h
         return eng
 
+    def share(self, ctx: hip.Context, max_ctx=0):
+        """A second engine over these weights on `ctx` (its own stream, KV
+        cache and activations), for decoding another sequence concurrently
+        from another host thread. Deinit it before this engine."""
+        eng = type(self).__new__(type(self))
+        eng.ctx = ctx
+        eng.config = dict(self.config)
+        if max_ctx:
+            eng.config["max_ctx"] = (max_ctx + 15) // 16 * 16
+        eng._cfg = ModelConfig(**eng.config)
+        h = C.c_void_p()
+        ctx.check(lib().zh_engine_create_shared(ctx.h, self.h, max_ctx, C.byref(h)))
+        eng.h = h
+        return eng
+
     def deinit(self):
         if self.h:
             lib().zh_engine_destroy(self.h)

@@ -129,6 +129,7 @@ SIGNATURES = {
                                 C.POINTER(_u32)]),
     "zh_engine_sample": (_i32, [_P, C.POINTER(SamplingParamsC), _P, _u32, C.c_double, C.POINTER(_u32)]),
     "zh_engine_create_gguf": (_i32, [_P, _P, _u32, C.POINTER(_P)]),
+    "zh_engine_create_shared": (_i32, [_P, _P, _u32, C.POINTER(_P)]),
     "zh_gguf_open": (_i32, [C.c_char_p, C.POINTER(_P)]),
     "zh_gguf_close": (None, [_P]),
     "zh_gguf_last_error": (C.c_char_p, [_P]),
