@@ -42,7 +42,7 @@ enum {
 };
 
 /* ---- GGMLType values used on the path (src/model/gguf.zig:38-69) -------- */
-enum { ZH_F32 = 0, ZH_F16 = 1, ZH_Q8_0 = 8, ZH_Q4_K = 12, ZH_Q6_K = 14, ZH_MXFP4 = 39 };
+enum { ZH_F32 = 0, ZH_F16 = 1, ZH_Q8_0 = 8, ZH_Q4_K = 12, ZH_Q5_K = 13, ZH_Q6_K = 14, ZH_MXFP4 = 39 };
 
 typedef struct zh_ctx zh_ctx;
 typedef struct zh_buf zh_buf;
@@ -85,7 +85,8 @@ int zh_grid_barrier_probe(zh_ctx *ctx, uint32_t n_barriers, uint32_t wgs_per_cu,
 
 /* ---- synthetic data (seeded, bit-identical to oracle/zinc_oracle.c) ----- */
 /* Fill rows x cols of `qtype` blocks at `offset` per the BASELINE distributions.
- * qtype | 0x100 (Q4_K only): model-init variant with dmin = f16(7.5*d), so
+ * qtype | 0x100 (Q4_K / Q5_K): model-init variant with dmin = f16(7.5*d) /
+ * f16(15.5*d), so
  * sub-block weights are zero-mean; the synthetic models use it. */
 int zh_synth_tensor(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint32_t qtype,
                     uint64_t rows, uint64_t cols, uint64_t seed, uint64_t stream);
@@ -97,7 +98,7 @@ int zh_synth_vector(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint32_t kind, ui
 /* y[y_off..] (=, or += when acc_mode==1) = dequant(W[a_off..]) (MxK) * x[x_off..].
  * Replaces DmmvDispatch.recordDispatch (dmmv.zig:806-874) / dispatchDmmvInner
  * (forward.zig:8431-8540) with DmmvPushConstants{M,K,a_offset,x_offset,
- * y_offset,acc_mode} (dmmv.zig:21-28). Offsets are BYTES. qtype: Q4_K, Q6_K,
+ * y_offset,acc_mode} (dmmv.zig:21-28). Offsets are BYTES. qtype: Q4_K, Q5_K, Q6_K,
  * Q8_0 (K % 64 == 0), MXFP4 (K % 32 == 0). K % 256 == 0 for K-quants. */
 int zh_dmmv(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off,
             const zh_buf *x, uint64_t x_off, zh_buf *y, uint64_t y_off,

@@ -12,7 +12,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libzinc_oracle.so")
 
-F32, F16, Q8_0, Q4_K, Q6_K, MXFP4 = 0, 1, 8, 12, 14, 39
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, MXFP4 = 0, 1, 8, 12, 13, 14, 39
 
 # Tensor stream ids shared with the HIP engine's synthetic model.
 S_TOKEN_EMBD, S_OUTPUT_NORM, S_OUTPUT = 1, 2, 3
@@ -255,7 +255,7 @@ def normal(r):
 
 
 def synth_tensor(qtype, rows, cols, seed, stream):
-    """qtype | 0x100: centered model-init variant (Q4_K dmin = f16(7.5*d))."""
+    """qtype | 0x100: centered model-init variant (Q4_K dmin = f16(7.5*d), Q5_K f16(15.5*d))."""
     out = np.empty(tensor_bytes(qtype & 0xFF, rows, cols), dtype=np.uint8)
     if lib().zo_synth_tensor(u8(out), qtype, rows, cols, seed, stream) != 0:
         raise ValueError("bad synth args")

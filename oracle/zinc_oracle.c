@@ -19,7 +19,7 @@ uint32_t zo_block_size(uint32_t t) {
     switch (t) {
     case ZO_F32: case ZO_F16: return 1;
     case ZO_Q8_0: case ZO_MXFP4: return 32;
-    case ZO_Q4_K: case ZO_Q6_K: return 256;
+    case ZO_Q4_K: case ZO_Q5_K: case ZO_Q6_K: return 256;
     default: return 1;
     }
 }
@@ -30,6 +30,7 @@ uint32_t zo_bytes_per_block(uint32_t t) {
     case ZO_Q8_0: return 34;
     case ZO_MXFP4: return 17;
     case ZO_Q4_K: return 144;
+    case ZO_Q5_K: return 176;
     case ZO_Q6_K: return 210;
     default: return 0;
     }
@@ -159,6 +160,30 @@ int zo_dequant_row(const uint8_t *raw, uint32_t row, uint32_t cols, uint32_t typ
                 float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
                 for (int l = 0; l < 32; l++) o[64 * p + l] = d1 * (float)(qs[32 * p + l] & 0xF) - mm1;
                 for (int l = 0; l < 32; l++) o[64 * p + 32 + l] = d2 * (float)(qs[32 * p + l] >> 4) - mm2;
+            }
+        }
+        return 0;
+    }
+    case ZO_Q5_K: { /* forward.zig:326-368: the fifth bit of element l of the
+                     * 64-group p comes from qh[l] bit 2p (low half) / 2p+1 (high half) */
+        size_t bpr = cols / 256, ro = (size_t)row * bpr * 176;
+        for (size_t b = 0; b < bpr; b++) {
+            const uint8_t *bb = raw + ro + b * 176;
+            float d = rd_f16(bb), dmin = rd_f16(bb + 2);
+            const uint8_t *scales = bb + 4, *qh = bb + 16, *qs = bb + 48;
+            float *o = out + b * 256;
+            for (int p = 0; p < 4; p++) {
+                uint8_t sc0, m0, sc1, m1;
+                zo_get_scale_min_k4(2 * p, scales, &sc0, &m0);
+                zo_get_scale_min_k4(2 * p + 1, scales, &sc1, &m1);
+                float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+                float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+                for (int l = 0; l < 32; l++) {
+                    int lo = (qs[32 * p + l] & 0xF) | (((qh[l] >> (2 * p)) & 1) << 4);
+                    int hi = (qs[32 * p + l] >> 4) | (((qh[l] >> (2 * p + 1)) & 1) << 4);
+                    o[64 * p + l] = d1 * (float)lo - mm1;
+                    o[64 * p + 32 + l] = d2 * (float)hi - mm2;
+                }
             }
         }
         return 0;
@@ -510,7 +535,7 @@ static inline uint16_t scale_f16(uint64_t r) { return zo_f32_to_f16(fabsf(zo_nor
 
 int zo_synth_tensor(uint8_t *dst, uint32_t type_flags, uint64_t rows, uint64_t cols,
                     uint64_t seed, uint64_t stream) {
-    /* type | 0x100: model-init variant of Q4_K with dmin = f16(7.5 * d) (zero-mean
+    /* type | 0x100: model-init variant of Q4_K / Q5_K with dmin = f16(7.5 * d) / f16(15.5 * d) (zero-mean
      * sub-blocks); the synthetic models use it for every Q4_K tensor. */
     uint32_t type = type_flags & 0xFF;
     int centered = (type_flags & 0x100) != 0;
@@ -525,6 +550,17 @@ int zo_synth_tensor(uint8_t *dst, uint32_t type_flags, uint64_t rows, uint64_t c
             uint16_t dm = centered ? zo_f32_to_f16(zo_f16_to_f32(d) * 7.5f) : scale_f16(zo_rand(seed, stream, b * 32 + 1));
             o[0] = d & 0xFF; o[1] = d >> 8; o[2] = dm & 0xFF; o[3] = dm >> 8;
             for (int i = 0; i < 140; i++) {
+                uint64_t r = zo_rand(seed, stream, b * 32 + 2 + i / 8);
+                o[4 + i] = (uint8_t)(r >> (8 * (i % 8)));
+            }
+            break;
+        }
+        case ZO_Q5_K: { /* as Q4_K (d, dmin, then 172 bytes: scales, qh, qs uniform);
+                         * centered: dmin = f16(15.5 * d), the mean 5-bit quant */
+            uint16_t d = scale_f16(zo_rand(seed, stream, b * 32 + 0));
+            uint16_t dm = centered ? zo_f32_to_f16(zo_f16_to_f32(d) * 15.5f) : scale_f16(zo_rand(seed, stream, b * 32 + 1));
+            o[0] = d & 0xFF; o[1] = d >> 8; o[2] = dm & 0xFF; o[3] = dm >> 8;
+            for (int i = 0; i < 172; i++) {
                 uint64_t r = zo_rand(seed, stream, b * 32 + 2 + i / 8);
                 o[4 + i] = (uint8_t)(r >> (8 * (i % 8)));
             }

@@ -23,7 +23,7 @@ extern "C" {
 
 /* GGMLType enum values: src/model/gguf.zig:38-69 */
 enum {
-    ZO_F32 = 0, ZO_F16 = 1, ZO_Q8_0 = 8, ZO_Q4_K = 12, ZO_Q6_K = 14, ZO_MXFP4 = 39
+    ZO_F32 = 0, ZO_F16 = 1, ZO_Q8_0 = 8, ZO_Q4_K = 12, ZO_Q5_K = 13, ZO_Q6_K = 14, ZO_MXFP4 = 39
 };
 
 /* GGMLType.blockSize / bytesPerBlock: src/model/gguf.zig:75-124 */
@@ -39,7 +39,7 @@ uint16_t zo_f32_to_f16(float f);
 /* getScaleMinK4: src/compute/forward.zig:229-238 */
 void zo_get_scale_min_k4(uint32_t j, const uint8_t *scales, uint8_t *sc, uint8_t *m);
 
-/* dequantRow: src/compute/forward.zig:242-465 (F32, F16, Q8_0, Q6_K, Q4_K, MXFP4).
+/* dequantRow: src/compute/forward.zig:242-465 (F32, F16, Q8_0, Q6_K, Q5_K, Q4_K, MXFP4).
  * Returns 0 on success, -1 for an unsupported type (reference logs and zero-fills). */
 int zo_dequant_row(const uint8_t *raw, uint32_t row, uint32_t cols, uint32_t type, float *out);
 
@@ -99,7 +99,7 @@ uint32_t zo_kv_page_count(uint32_t context_tokens);
 uint64_t zo_rand(uint64_t seed, uint64_t stream, uint64_t ctr);
 float    zo_normal(uint64_t r);
 /* Fill a rows x cols tensor of `type` with BASELINE-distributed random blocks.
- * type | 0x100 (Q4_K): model-init variant, dmin = f16(7.5*d). */
+ * type | 0x100 (Q4_K / Q5_K): model-init variant, dmin = f16(7.5*d) / f16(15.5*d). */
 int  zo_synth_tensor(uint8_t *dst, uint32_t type, uint64_t rows, uint64_t cols,
                      uint64_t seed, uint64_t stream);
 void zo_synth_normal_f32(float *dst, uint64_t n, float scale, uint64_t seed, uint64_t stream);

@@ -8,13 +8,16 @@ src/model/loader.zig:414-486, forward.zig:1226).
 - A file mixing formats per tensor (Q/K/V in three formats, gate and up in
   different ones, ffn_down per layer) feeds both the engine and the oracle
   the same bytes: logits within the decode tolerance, greedy tokens equal.
+- Q5_K: a Q5_K_M-style dense mix (Q5_K, Q6_K on the use_more_bits layers,
+  Q5_K token embeddings) and a MoE model with Q5_K experts decode like the
+  oracle and survive a GGUF round trip.
 - Without output.weight the LM head reads token_embd.weight.
 - Missing tensors, wrong shapes and formats the kernels do not take fail
   with the reference's errors."""
 import numpy as np
 import pytest
 
-from zinc_amd import Q4_K, Q6_K, Q8_0, ZincError
+from zinc_amd import Q4_K, Q5_K, Q6_K, Q8_0, ZincError
 from zinc_amd import gguf as G
 
 pytestmark = pytest.mark.gpu
@@ -29,6 +32,9 @@ SMALL_MOE = dict(n_layers=2, hidden=512, n_heads=8, n_kv_heads=1, head_dim=128, 
                  type_router=8, rope_base=1e6, eps=1e-6, seed=98)
 # 8 layers: use_more_bits picks layers 0, 3, 6 and 7
 Q4KM_8L = dict(SMALL_DENSE, n_layers=8, type_ffn_down=Q4_K, type_more_bits=Q6_K, seed=95)
+Q5KM_8L = dict(SMALL_DENSE, n_layers=8, type_attn=Q5_K, type_ffn_gate_up=Q5_K, type_ffn_down=Q5_K,
+               type_embd=Q5_K, type_more_bits=Q6_K, seed=94)
+MOE_Q5K = dict(SMALL_MOE, type_ffn_gate_up=Q5_K, type_ffn_down=Q5_K, seed=93)
 
 
 @pytest.fixture(scope="module")
@@ -114,6 +120,29 @@ def test_q4km_mix_matches_oracle(ctx, orc, tmp_path):
     assert g[0] == o[0] and g[2] == o[2]
     # and through a GGUF file: identical to the engine it came from
     e2 = zinc_amd.InferenceEngine.from_gguf(ctx, G.export_engine(eng, tmp_path / "q4km.gguf"), Q4KM_8L["max_ctx"])
+    g2 = _decode(e2)
+    assert g2[0] == g[0] and g2[2] == g[2] and np.array_equal(g2[1], g[1])
+    eng.deinit()
+    e2.deinit()
+    om.close()
+
+
+@pytest.mark.parametrize("cfg", [Q5KM_8L, MOE_Q5K], ids=["q5km_dense", "moe_q5k_experts"])
+def test_q5k_models_match_oracle(ctx, orc, tmp_path, cfg):
+    import zinc_amd
+    print(f"q5k model vs oracle seed={cfg['seed']}", flush=True)
+    eng = zinc_amd.InferenceEngine(ctx, cfg)
+    om = orc.Model(cfg)
+    kinds = (orc.K_EXP_GATE, orc.K_EXP_UP, orc.K_EXP_DOWN) if cfg["n_experts"] else (orc.K_WQ, orc.K_GATE, orc.K_UP)
+    for l in range(cfg["n_layers"]):
+        for kind in kinds:
+            s = orc.S_LAYER(l, kind)
+            assert eng.tensor_type(s) == Q5_K and om.tensor_type(s) == Q5_K
+            assert np.array_equal(eng.tensor_bytes(s), om.tensor(s))
+    g, o = _decode(eng), _oracle_decode(om)
+    assert _close(g[1], o[1]), np.abs(g[1] - o[1]).max()
+    assert g[0] == o[0] and g[2] == o[2]
+    e2 = zinc_amd.InferenceEngine.from_gguf(ctx, G.export_engine(eng, tmp_path / "q5k.gguf"), cfg["max_ctx"])
     g2 = _decode(e2)
     assert g2[0] == g[0] and g2[2] == g[2] and np.array_equal(g2[1], g[1])
     eng.deinit()

@@ -56,10 +56,10 @@ def assert_dot_close(got, ref32, ref64, mag, what):
     return int((~ok1).sum())
 
 
-QTYPES = [12, 14, 8, 39]
+QTYPES = [12, 13, 14, 8, 39]
 
 
-@pytest.mark.parametrize("qtype", QTYPES + [12 | 0x100])
+@pytest.mark.parametrize("qtype", QTYPES + [12 | 0x100, 13 | 0x100])
 def test_synth_generator_bit_identical(ctx, orc, qtype):
     rows, cols = 7, (2880 if qtype == 39 else 1024)
     n = orc.tensor_bytes(qtype & 0xFF, rows, cols)
@@ -120,6 +120,7 @@ def run_dmmv(ctx, orc, qtype, M, K, seed, acc=False, a_off=0):
     (12, 257, 512), (12, 33, 768), (12, 100, 2048), (12, 64, 12288),
     (14, 257, 512), (14, 512, 4096), (14, 64, 12288), (14, 40, 768),
     (8, 257, 4096), (8, 128, 2048), (8, 16, 768),
+    (13, 4096, 4096), (13, 257, 512), (13, 1000, 768), (13, 64, 12288), (13, 1536, 2048),
     (39, 257, 2880), (39, 4, 32), (39, 100, 1024),
 ])
 def test_dmmv_matches_oracle(ctx, orc, qtype, M, K):
@@ -130,7 +131,7 @@ def test_dmmv_matches_oracle(ctx, orc, qtype, M, K):
 @pytest.mark.parametrize("qtype,M,K", [
     (12, 4096, 4096), (12, 12288, 4096), (12, 257, 512), (12, 64, 12288),
     (14, 4096, 12288), (14, 64, 12288), (14, 2000, 4096), (14, 4096, 6144), (14, 40, 768),
-    (8, 257, 4096),
+    (8, 257, 4096), (13, 4096, 4096), (13, 64, 12288),
 ])
 def test_dmmv_xq_matches_oracle(ctx, orc, qtype, M, K):
     """The activation pre-quantised once (zh_quantize_activation: three int8
@@ -150,7 +151,7 @@ def test_dmmv_xq_matches_oracle(ctx, orc, qtype, M, K):
         ctx.free(b)
 
 
-@pytest.mark.parametrize("qtype", [12, 14, 8])
+@pytest.mark.parametrize("qtype", [12, 13, 14, 8])
 def test_dmmv_acc_mode_and_offset(ctx, orc, qtype):
     got, ref, ref64, mag = run_dmmv(ctx, orc, qtype, 300, 1024, 5, acc=True, a_off=4096)
     assert_dot_close(got, ref, ref64, mag, "acc")
@@ -181,7 +182,7 @@ def test_dmmv_rejects_bad_shapes(ctx):
     assert e.value.name == "InvalidArgument"
 
 
-@pytest.mark.parametrize("qtype,M,K", [(12, 1024, 4096), (12, 768, 2048), (14, 200, 1024)])
+@pytest.mark.parametrize("qtype,M,K", [(12, 1024, 4096), (12, 768, 2048), (14, 200, 1024), (13, 768, 2048)])
 def test_fused_gate_up_swiglu(ctx, orc, qtype, M, K):
     Wg = orc.synth_tensor(qtype, M, K, 21, 1)
     Wu = orc.synth_tensor(qtype, M, K, 21, 2)
@@ -201,9 +202,9 @@ def test_fused_gate_up_swiglu(ctx, orc, qtype, M, K):
     assert_dot_close(got, ref, ref64, mag, "gate_up")
 
 
-def test_dmmv_moe_expert_gather(ctx, orc):
+@pytest.mark.parametrize("qt", [12, 13])
+def test_dmmv_moe_expert_gather(ctx, orc, qt):
     E, M, K, k = 16, 768, 2048, 4
-    qt = 12
     W = orc.synth_tensor(qt, E * M, K, 31, 1)
     stride = orc.tensor_bytes(qt, M, K)
     ids = np.array([3, 15, 0, 7], np.uint32)

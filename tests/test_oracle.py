@@ -40,6 +40,7 @@ def test_block_geometry(orc):
     # gguf.zig:75-124
     assert (orc.block_size(orc.Q4_K), orc.bytes_per_block(orc.Q4_K)) == (256, 144)
     assert (orc.block_size(orc.Q6_K), orc.bytes_per_block(orc.Q6_K)) == (256, 210)
+    assert (orc.block_size(orc.Q5_K), orc.bytes_per_block(orc.Q5_K)) == (256, 176)
     assert (orc.block_size(orc.Q8_0), orc.bytes_per_block(orc.Q8_0)) == (32, 34)
     assert (orc.block_size(orc.MXFP4), orc.bytes_per_block(orc.MXFP4)) == (32, 17)
     # forward.zig:11410-11416 expertSliceBytes KAT: Q4_K 512x2048 -> 589,824
@@ -145,6 +146,87 @@ def test_dequant_q4k_closed_form_scales_and_mins(orc):
             v = np.float32(np.float32(d) * np.float32(sc[j])) * np.float32(q) - \
                 np.float32(np.float32(dmin) * np.float32(m[j]))
             assert np.all(out[32 * j:32 * j + 32] == np.float32(v)), j
+
+
+# ---------------------------------------------------------------- Q5_K
+def test_dequant_q5k_kat_contiguous_halves(orc):
+    # forward.zig:11499-11527: d=1, sc0=sc1=1, qh=0, qs[0]=0x3A -> out[0]=10, out[32]=3
+    blk = np.zeros(176, np.uint8)
+    put16(blk, 0, 1.0)
+    blk[4], blk[5] = 1, 1
+    blk[48] = 0x3A
+    out = orc.dequant_row(blk, 0, 256, orc.Q5_K)
+    assert abs(out[0] - 10.0) < 0.01 and abs(out[32] - 3.0) < 0.01
+
+
+def test_dequant_q5k_single_bit_layout(orc):
+    """d=1, every sc=1, dmin=0. A qs bit lands where Q4_K's does (element
+    64*(b//32) + 32*(k//4) + b%32, value 2^(k%4)); bit k of qh[l] is the fifth
+    bit (16) of element 32*k + l (ggml's dequantize_row_q5_K: bit 2p / 2p+1
+    of qh[l] for the low / high half of 64-group p)."""
+    def base():
+        blk = np.zeros(176, np.uint8)
+        put16(blk, 0, 1.0)
+        blk[4:16] = pack_scale_min_k4([1] * 8, [0] * 8)
+        return blk
+    for b in range(128):
+        for k in range(8):
+            blk = base()
+            blk[48 + b] = 1 << k
+            exp = np.zeros(256, np.float32)
+            exp[64 * (b // 32) + 32 * (k // 4) + b % 32] = 2 ** (k % 4)
+            assert np.array_equal(orc.dequant_row(blk, 0, 256, orc.Q5_K), exp), ("qs", b, k)
+    for l in range(32):
+        for k in range(8):
+            blk = base()
+            blk[16 + l] = 1 << k
+            exp = np.zeros(256, np.float32)
+            exp[32 * k + l] = 16.0
+            assert np.array_equal(orc.dequant_row(blk, 0, 256, orc.Q5_K), exp), ("qh", l, k)
+
+
+def test_dequant_q5k_reduces_to_q4k(orc):
+    """With qh = 0 a Q5_K block is the Q4_K block of the same header and qs;
+    with qh = 0xFF every element gains d*sc_j*16 (exactly, in f32 for these
+    small scales)."""
+    rng = np.random.default_rng(21)
+    for _ in range(20):
+        b5 = rng.integers(0, 256, 176).astype(np.uint8)
+        put16(b5, 0, np.float16(rng.random() * 0.05))
+        put16(b5, 2, np.float16(rng.random() * 0.05))
+        b4 = np.concatenate([b5[:16], b5[48:]])
+        b5[16:48] = 0
+        assert np.array_equal(orc.dequant_row(b5, 0, 256, orc.Q5_K), orc.dequant_row(b4, 0, 256, orc.Q4_K))
+    for _ in range(20):
+        sc = rng.integers(0, 64, 8)
+        m = rng.integers(0, 64, 8)
+        q = int(rng.integers(0, 16))
+        d, dmin = np.float16(rng.random() * 0.05), np.float16(rng.random() * 0.05)
+        blk = np.zeros(176, np.uint8)
+        put16(blk, 0, d)
+        put16(blk, 2, dmin)
+        blk[4:16] = pack_scale_min_k4(sc, m)
+        blk[16:48] = 0xFF
+        blk[48:] = q | (q << 4)
+        out = orc.dequant_row(blk, 0, 256, orc.Q5_K)
+        for j in range(8):
+            v = np.float32(np.float32(d) * np.float32(sc[j])) * np.float32(q + 16) - \
+                np.float32(np.float32(dmin) * np.float32(m[j]))
+            assert np.all(out[32 * j:32 * j + 32] == np.float32(v)), j
+
+
+def test_centered_q5k_model_init_is_zero_mean(orc):
+    W = orc.synth_tensor(orc.Q5_K | 0x100, 64, 4096, 3, 4)
+    w = orc.dequant(W, 64, 4096, orc.Q5_K).astype(np.float64)
+    blk = W.reshape(-1, 176)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float64).ravel()
+    dm = blk[:, 2:4].copy().view(np.float16).astype(np.float64).ravel()
+    assert np.allclose(dm, (d * 15.5).astype(np.float16), rtol=0)
+    assert abs(w.mean()) < 0.02 * np.abs(w).mean()
+    # the header bytes follow the Q4_K generator's stream layout
+    W4 = orc.synth_tensor(orc.Q4_K, 8, 256, 3, 4).reshape(-1, 144)
+    W5 = orc.synth_tensor(orc.Q5_K, 8, 256, 3, 4).reshape(-1, 176)
+    assert np.array_equal(W4[:, :144], W5[:, :144])
 
 
 # ---------------------------------------------------------------- Q6_K
@@ -269,7 +351,7 @@ def test_dequant_mxfp4_kat_and_specials(orc):
 
 
 # ---------------------------------------------------------------- DMMV
-@pytest.mark.parametrize("qtype,M,K", [(12, 64, 4096), (14, 64, 4096), (8, 64, 4096), (39, 64, 2880)])
+@pytest.mark.parametrize("qtype,M,K", [(12, 64, 4096), (13, 64, 4096), (14, 64, 4096), (8, 64, 4096), (39, 64, 2880)])
 def test_dmmv_matches_independent_f64(orc, qtype, M, K):
     W = orc.synth_tensor(qtype, M, K, 1234, 7)
     x = orc.synth_normal_f32(K, 1234, 99)

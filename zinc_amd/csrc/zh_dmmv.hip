@@ -84,6 +84,30 @@ ZH_DEV u32x4 ld4(const uint8_t *p) { return *(const u32x4_a4 *)p; }
 ZH_DEV int comb_int(int d0, int d1, int d2) { return (d2 * 256 + d1) * 256 + d0; }
 ZH_DEV float comb_f32(int d0, int d1, int d2) { return fmaf((float)d2, 65536.f, (float)(d1 * 256 + d0)); }
 
+// Q4_K / Q5_K sub-pair epilogue: raw[0..3] hold {d, dmin, scales[12]}, S0/S1
+// the code . limb sums of sub-blocks 2p and 2p+1.
+// getScaleMinK4 (forward.zig:229-238) for j = 2p, 2p+1, branch-free:
+// p < 2: sc = s[j] & 63, m = s[j+4] & 63 (6-bit fields of w1, w2);
+// p >= 2: sc = low nibble of s[j+4] | (s[j-4] >> 6) << 4,
+//          m = high nibble of s[j+4] | (s[j] >> 6) << 4.
+ZH_DEV float k4_epilogue(const uint32_t *raw, const XReg &xr, int p, float S0, float S1) {
+    const bool lo4 = p < 2;
+    const uint32_t w1 = raw[1], w2 = raw[2], w3 = raw[3];
+    const uint32_t srcS = lo4 ? w1 : w3, srcM = lo4 ? w2 : w3;
+    const uint32_t wa = lo4 ? 6u : 4u, wb = lo4 ? 0u : 2u, mo = lo4 ? 0u : 4u;
+    uint32_t sc[2], mn[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++) {
+        const uint32_t off = 16u * (uint32_t)(p & 1) + 8u * (uint32_t)s2;
+        sc[s2] = __builtin_amdgcn_ubfe(srcS, off, wa) | (__builtin_amdgcn_ubfe(w1, off + 6u, wb) << 4);
+        mn[s2] = __builtin_amdgcn_ubfe(srcM, off + mo, wa) | (__builtin_amdgcn_ubfe(w2, off + 6u, wb) << 4);
+    }
+    float d = h2f(raw[0]), dmin = h2f(raw[0] >> 16);
+    float A = fmaf((float)sc[1] * xr.xs[1], S1, (float)sc[0] * xr.xs[0] * S0);
+    float B = fmaf((float)mn[1], xr.xz[1], (float)mn[0] * xr.xz[0]);
+    return fmaf(d, A, -dmin * B);
+}
+
 // ---------------------------------------------------------------------------
 // Q4_K: 144-byte blocks {f16 d, f16 dmin, 12 B packed 6-bit scales/mins,
 // 128 B nibbles} (forward.zig:370-409). Unit u = (block u>>2, sub-pair p=u&3):
@@ -120,28 +144,45 @@ struct FmtQ4K {
                 D[1][k] = sdot4(hi, xr.L[24 + k * 8 + i], D[1][k]);
             }
         }
-        // getScaleMinK4 (forward.zig:229-238) for j = 2p, 2p+1, branch-free:
-        // p < 2: sc = s[j] & 63, m = s[j+4] & 63 (6-bit fields of w1, w2);
-        // p >= 2: sc = low nibble of s[j+4] | (s[j-4] >> 6) << 4,
-        //          m = high nibble of s[j+4] | (s[j] >> 6) << 4.
-        const int p = u & 3;
-        const bool lo4 = p < 2;
-        const uint32_t w1 = raw[1], w2 = raw[2], w3 = raw[3];
-        const uint32_t srcS = lo4 ? w1 : w3, srcM = lo4 ? w2 : w3;
-        const uint32_t wa = lo4 ? 6u : 4u, wb = lo4 ? 0u : 2u, mo = lo4 ? 0u : 4u;
-        uint32_t sc[2], mn[2];
+        return k4_epilogue(raw, xr, u & 3, (float)comb_int(D[0][0], D[0][1], D[0][2]),
+                           (float)comb_int(D[1][0], D[1][1], D[1][2]));
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q5_K: 176-byte blocks {f16 d, f16 dmin, 12 B packed scales/mins, qh[32],
+// qs[128]} (forward.zig:326-368). Units as Q4_K; the fifth bit of element l
+// of 64-group p is bit 2p (low half) / 2p+1 (high half) of qh[l]. Codes reach
+// 31, so 31 * 32 * 2^22 overflows int32: the limb sums combine in f32.
+// ---------------------------------------------------------------------------
+struct FmtQ5K {
+    static constexpr int EPU = 64, RAW = 20, QK = 256, BPB = 176;
+    ZH_DEVM static void load_x(XReg &xr, XQView v, int u) { FmtQ4K::load_x(xr, v, u); }
+    ZH_DEVM static void load_raw(const uint8_t *row, int u, uint32_t *raw) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 176;
+        int p = u & 3;
+        u32x4 h = ld4(b), q0 = ld4(b + 48 + 32 * p), q1 = ld4(b + 64 + 32 * p), e0 = ld4(b + 16), e1 = ld4(b + 32);
+        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+        raw[4] = q0.x; raw[5] = q0.y; raw[6] = q0.z; raw[7] = q0.w;
+        raw[8] = q1.x; raw[9] = q1.y; raw[10] = q1.z; raw[11] = q1.w;
+        raw[12] = e0.x; raw[13] = e0.y; raw[14] = e0.z; raw[15] = e0.w;
+        raw[16] = e1.x; raw[17] = e1.y; raw[18] = e1.z; raw[19] = e1.w;
+    }
+    ZH_DEVM static float compute(const uint32_t *raw, const XReg &xr, int u) {
+        const uint32_t p2 = 2u * (uint32_t)(u & 3);
+        int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++) {
-            const uint32_t off = 16u * (uint32_t)(p & 1) + 8u * (uint32_t)s2;
-            sc[s2] = __builtin_amdgcn_ubfe(srcS, off, wa) | (__builtin_amdgcn_ubfe(w1, off + 6u, wb) << 4);
-            mn[s2] = __builtin_amdgcn_ubfe(srcM, off + mo, wa) | (__builtin_amdgcn_ubfe(w2, off + 6u, wb) << 4);
+        for (int i = 0; i < 8; i++) {
+            const uint32_t w = raw[4 + i], h = raw[12 + i];
+            const uint32_t lo = (w & 0x0F0F0F0Fu) | (((h >> p2) & 0x01010101u) << 4);
+            const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> (p2 + 1u)) & 0x01010101u) << 4);
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                D[0][k] = sdot4(lo, xr.L[k * 8 + i], D[0][k]);
+                D[1][k] = sdot4(hi, xr.L[24 + k * 8 + i], D[1][k]);
+            }
         }
-        float d = h2f(raw[0]), dmin = h2f(raw[0] >> 16);
-        float S0 = (float)comb_int(D[0][0], D[0][1], D[0][2]);
-        float S1 = (float)comb_int(D[1][0], D[1][1], D[1][2]);
-        float A = fmaf((float)sc[1] * xr.xs[1], S1, (float)sc[0] * xr.xs[0] * S0);
-        float B = fmaf((float)mn[1], xr.xz[1], (float)mn[0] * xr.xz[0]);
-        return fmaf(d, A, -dmin * B);
+        return k4_epilogue(raw, xr, u & 3, comb_f32(D[0][0], D[0][1], D[0][2]), comb_f32(D[1][0], D[1][1], D[1][2]));
     }
 };
 
@@ -551,6 +592,7 @@ template <int MODE, bool MOE>
 static int launch_dmmv(zh_ctx *c, uint32_t qtype, const DmmvP &p, uint32_t n_slots) {
     switch (qtype) {
     case ZH_Q4_K: return launch_fmt<FmtQ4K, MODE, MOE>(c, p, n_slots);
+    case ZH_Q5_K: return launch_fmt<FmtQ5K, MODE, MOE>(c, p, n_slots);
     case ZH_Q6_K: return launch_fmt<FmtQ6K, MODE, MOE>(c, p, n_slots);
     case ZH_Q8_0: return launch_fmt<FmtQ80, MODE, MOE>(c, p, n_slots);
     case ZH_MXFP4: return launch_fmt<FmtMXFP4, MODE, MOE>(c, p, n_slots);
@@ -560,7 +602,7 @@ static int launch_dmmv(zh_ctx *c, uint32_t qtype, const DmmvP &p, uint32_t n_slo
 
 static int check_k(zh_ctx *c, uint32_t qtype, uint32_t K) {
     switch (qtype) {
-    case ZH_Q4_K: case ZH_Q6_K:
+    case ZH_Q4_K: case ZH_Q5_K: case ZH_Q6_K:
         if (K % 256) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "K=%u not a multiple of 256", K);
         return ZH_OK;
     case ZH_Q8_0:
@@ -853,6 +895,7 @@ template <int MODE>
 static int launch_dl_q(zh_ctx *c, uint32_t qtype, const DlP &p) {
     switch (qtype) {
     case ZH_Q4_K: return launch_dl<FmtQ4K, MODE>(c, p);
+    case ZH_Q5_K: return launch_dl<FmtQ5K, MODE>(c, p);
     case ZH_Q6_K: return launch_dl<FmtQ6K, MODE>(c, p);
     case ZH_Q8_0: return launch_dl<FmtQ80, MODE>(c, p);
     case ZH_MXFP4: return launch_dl<FmtMXFP4, MODE>(c, p);
@@ -862,7 +905,7 @@ static int launch_dl_q(zh_ctx *c, uint32_t qtype, const DlP &p) {
 
 bool zhk_dmmv_lds_supported(uint32_t qtype, uint32_t K) {
     const uint32_t epu = qtype == ZH_MXFP4 ? 32 : 64;
-    const uint32_t q = (qtype == ZH_Q4_K || qtype == ZH_Q6_K) ? 256 : epu;
+    const uint32_t q = (qtype == ZH_Q4_K || qtype == ZH_Q5_K || qtype == ZH_Q6_K) ? 256 : epu;
     return K > 0 && K % q == 0 && K % 32 == 0 && K / epu <= 64;
 }
 
@@ -1150,9 +1193,9 @@ extern "C" int zh_dmmv_moe(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t 
 // output element, every product and difference rounded separately (_rn
 // intrinsics), matching Zig's unfused f32 arithmetic.
 // ---------------------------------------------------------------------------
-ZH_DEV uint32_t blk_elems(uint32_t t) { return (t == ZH_Q4_K || t == ZH_Q6_K) ? 256 : (t == ZH_Q8_0 || t == ZH_MXFP4) ? 32 : 1; }
+ZH_DEV uint32_t blk_elems(uint32_t t) { return (t == ZH_Q4_K || t == ZH_Q5_K || t == ZH_Q6_K) ? 256 : (t == ZH_Q8_0 || t == ZH_MXFP4) ? 32 : 1; }
 ZH_DEV uint32_t blk_bytes(uint32_t t) {
-    return t == ZH_Q4_K ? 144 : t == ZH_Q6_K ? 210 : t == ZH_Q8_0 ? 34 : t == ZH_MXFP4 ? 17 : t == ZH_F16 ? 2 : 4;
+    return t == ZH_Q4_K ? 144 : t == ZH_Q5_K ? 176 : t == ZH_Q6_K ? 210 : t == ZH_Q8_0 ? 34 : t == ZH_MXFP4 ? 17 : t == ZH_F16 ? 2 : 4;
 }
 
 __global__ void k_dequant(uint32_t qtype, const uint8_t *__restrict__ W, uint32_t row0, uint32_t n_rows,
@@ -1179,6 +1222,18 @@ __global__ void k_dequant(uint32_t qtype, const uint8_t *__restrict__ W, uint32_
         if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
         else { sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
         uint32_t q = (b[16 + 32 * p + l] >> (4 * hi)) & 0xF;
+        float d = h2f(b[0] | (b[1] << 8)), dmin = h2f(b[2] | (b[3] << 8));
+        v = __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)q), __fmul_rn(dmin, (float)m));
+        break;
+    }
+    case ZH_Q5_K: {
+        const uint8_t *b = r + (e / 256) * 176;
+        uint32_t w = e % 256, p = w / 64, hi = (w / 32) & 1, l = w % 32, j = 2 * p + hi;
+        const uint8_t *s = b + 4;
+        uint32_t sc, m;
+        if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
+        else { sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+        uint32_t q = ((b[48 + 32 * p + l] >> (4 * hi)) & 0xF) | (((b[16 + l] >> j) & 1) << 4);
         float d = h2f(b[0] | (b[1] << 8)), dmin = h2f(b[2] | (b[3] << 8));
         v = __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)q), __fmul_rn(dmin, (float)m));
         break;

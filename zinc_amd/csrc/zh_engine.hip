@@ -149,7 +149,7 @@ static uint64_t host_key(uint64_t seed, uint64_t stream) {
 // ---------------------------------------------------------------------------
 // init
 // ---------------------------------------------------------------------------
-static bool dmmv_type_ok(uint32_t t) { return t == ZH_Q4_K || t == ZH_Q6_K || t == ZH_Q8_0 || t == ZH_MXFP4; }
+static bool dmmv_type_ok(uint32_t t) { return t == ZH_Q4_K || t == ZH_Q5_K || t == ZH_Q6_K || t == ZH_Q8_0 || t == ZH_MXFP4; }
 
 // use_more_bits(i_layer, n_layers) of llama.cpp's quantizer: the layers the
 // Q4_K_M / Q5_K_M mix stores attn_v and ffn_down in more bits.

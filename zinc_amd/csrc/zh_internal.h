@@ -41,7 +41,7 @@ int zh_scratch(zh_ctx *ctx, uint64_t bytes, void **out);
 static inline uint32_t zh_block_size(uint32_t t) {
     switch (t) {
     case ZH_Q8_0: case ZH_MXFP4: return 32;
-    case ZH_Q4_K: case ZH_Q6_K: return 256;
+    case ZH_Q4_K: case ZH_Q5_K: case ZH_Q6_K: return 256;
     default: return 1;
     }
 }
@@ -52,6 +52,7 @@ static inline uint32_t zh_bytes_per_block(uint32_t t) {
     case ZH_Q8_0: return 34;
     case ZH_MXFP4: return 17;
     case ZH_Q4_K: return 144;
+    case ZH_Q5_K: return 176;
     case ZH_Q6_K: return 210;
     default: return 0;
     }

@@ -180,9 +180,10 @@ ZH_DEV float synth_normal(uint64_t r) {
 }
 ZH_DEV uint16_t synth_scale_f16(uint64_t r) { return f2h_rn(__fmul_rn(fabsf(synth_normal(r)), 0.02f)); }
 
-// qtype | ZH_SYNTH_CENTERED selects the model-init variant of Q4_K: dmin =
-// f16(7.5 * d), which makes every sub-block's expected weight d*7.5*(sc - m)
-// zero-mean over random (sc, m), so mat-vec outputs carry no common mode.
+// qtype | ZH_SYNTH_CENTERED selects the model-init variant of Q4_K / Q5_K:
+// dmin = f16(7.5 * d) / f16(15.5 * d) (the mean 4- / 5-bit code), which makes
+// every sub-block's expected weight zero-mean over random (sc, m), so mat-vec
+// outputs carry no common mode.
 #define ZH_SYNTH_CENTERED 0x100u
 __global__ void k_synth_tensor(uint8_t *dst, uint32_t qtype_flags, uint64_t b0, uint64_t b1, uint64_t key) {
     uint64_t b = b0 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -196,6 +197,17 @@ __global__ void k_synth_tensor(uint8_t *dst, uint32_t qtype_flags, uint64_t b0, 
         uint16_t dm = centered ? f2h_rn(__fmul_rn(h2f(d), 7.5f)) : synth_scale_f16(synth_rand(key, b * 32 + 1));
         o[0] = d & 0xFF; o[1] = d >> 8; o[2] = dm & 0xFF; o[3] = dm >> 8;
         for (int i = 0; i < 140; i++) {
+            uint64_t r = synth_rand(key, b * 32 + 2 + i / 8);
+            o[4 + i] = (uint8_t)(r >> (8 * (i % 8)));
+        }
+        break;
+    }
+    case ZH_Q5_K: {  // as Q4_K, then 172 uniform bytes (scales, qh, qs)
+        uint8_t *o = dst + b * 176;
+        uint16_t d = synth_scale_f16(synth_rand(key, b * 32 + 0));
+        uint16_t dm = centered ? f2h_rn(__fmul_rn(h2f(d), 15.5f)) : synth_scale_f16(synth_rand(key, b * 32 + 1));
+        o[0] = d & 0xFF; o[1] = d >> 8; o[2] = dm & 0xFF; o[3] = dm >> 8;
+        for (int i = 0; i < 172; i++) {
             uint64_t r = synth_rand(key, b * 32 + 2 + i / 8);
             o[4 + i] = (uint8_t)(r >> (8 * (i % 8)));
         }

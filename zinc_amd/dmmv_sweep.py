@@ -26,6 +26,9 @@ SHAPES = [
     ("Q4_K 4096->12288 (gate/up)", hip.Q4_K, 12288, 4096),
     ("Q4_K 12288->4096 (down)", hip.Q4_K, 4096, 12288),
     ("Q6_K 4096->151936 (lm-head)", hip.Q6_K, 151936, 4096),
+    ("Q5_K 4096x4096", hip.Q5_K, 4096, 4096),
+    ("Q5_K 4096->12288 (gate/up)", hip.Q5_K, 12288, 4096),
+    ("Q5_K 12288->4096 (down)", hip.Q5_K, 4096, 12288),
     ("Q8_0 4096x4096", hip.Q8_0, 4096, 4096),
     ("MXFP4 2880x2880", hip.MXFP4, 2880, 2880),
 ]

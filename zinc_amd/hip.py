@@ -13,14 +13,14 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("ZH_LIB_PATH") or os.path.join(HERE, "libzinc_hip.so")
 
-F32, F16, Q8_0, Q4_K, Q6_K, MXFP4 = 0, 1, 8, 12, 14, 39
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, MXFP4 = 0, 1, 8, 12, 13, 14, 39
 OK = 0
 STATUS = {1: "UnsupportedQuantType", 2: "InvalidArgument", 3: "HipError",
           4: "ContextLengthExceeded", 5: "OutOfMemory", 6: "TensorNotFound", 7: "InvalidMagic",
           8: "UnknownMetadataType", 9: "UnsupportedArchitecture", 10: "TruncatedFile", 11: "IoError",
           12: "NotFound"}
 
-BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34), MXFP4: (32, 17), F32: (1, 4), F16: (1, 2)}
+BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), MXFP4: (32, 17), F32: (1, 4), F16: (1, 2)}
 
 
 def tensor_bytes(qtype, rows, cols):
