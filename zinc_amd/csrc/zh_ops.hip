@@ -182,8 +182,9 @@ extern "C" int zh_qk_norm_rope_kv_write(zh_ctx *c, zh_buf *q, const zh_buf *qw, 
 // Decode attention (flash_decode.comp + the qk_norm_rope_kv_write.comp work
 // of the new token, forward.zig decodeStep attention block), one kernel:
 //
-//   grid (n_kv_heads, n_chunks), 256 threads = 4 waves x 40 tokens, so a
-//   workgroup covers a 160-token chunk of one kv head's GQA group.
+//   grid (n_kv_heads, n_chunks), 256 threads = 4 waves x TW tokens, so a
+//   workgroup covers a chunk (of 4 TW-token sub-chunks) of one kv head's GQA
+//   group.
 //   - FUSED: q (raw Q projection), the new token's raw k/v, per-head RMSNorm
 //     weights and RoPE frequencies come in; every wave normalises and ropes q
 //     in registers, and the wave that owns the new position also normalises
@@ -212,44 +213,53 @@ extern "C" int zh_exp_trace_ops_dump(uint64_t *host, uint32_t n) {
 #endif
 constexpr int FD_MAXG = 8;   // q heads per kv head
 constexpr int FD_HD = 128;   // head_dim supported
-// 4 waves x 40 tokens: one wave per SIMD, and the 8 kv heads map one per XCD
-// (workgroups go round robin over the 8 XCDs), so a context of up to
-// 32 x 160 = 5120 tokens puts at most one chunk workgroup on each of an
-// XCD's 32 CUs.
+// 4 waves x TW tokens: one wave per SIMD, and the 8 kv heads map one per XCD
+// (workgroups go round robin over the 8 XCDs), so the chunks of a kv head
+// spread over its XCD's 32 CUs. TW (tokens per wave per sub-chunk) is a
+// template parameter chosen at launch:
+//  * 24 when the context capacity is at most 8192 tokens: a 4K context then
+//    runs 2 pipelined 96-token sub-chunks per workgroup over 22 chunks per
+//    kv head (15.6 us per layer against 16.4 us for one 136-token chunk over
+//    32 chunks: the second sub-chunk's K/V loads are in flight while the
+//    first is computed, and fewer partials are merged);
+//  * 32 for longer contexts: 128-token sub-chunks (32K context: 36.9 us
+//    against 38.8 us with 96 and 40.2 us with 160);
+//  * 40 for 8 q heads per kv head, which has no sub-chunk loop.
 constexpr int AD_W = 4;      // waves per workgroup
-constexpr int AD_TW = 40;    // tokens per wave: starts 8-aligned, spans at most 3 pages
 constexpr int AD_T = AD_W * 64;
-constexpr int AD_TC = AD_W * AD_TW;  // tokens per chunk (at most)
+constexpr int AD_TC_MIN = AD_W * 24;  // the shortest sub-chunk: sizes the partials
 // Chunk geometry modes: page-table lookups with chunk = blockIdx.y, the same
 // dispatched newest-first (grids larger than the device), or an identity page
 // table (physical token = logical token), where nothing waits on page entries
 // and the chunk length follows the context: ceil(seq / nd) rounded up to 8
-// tokens (at least 40) while that fits 160, with nd = CUs / kv heads, so the
-// chunks of all kv heads cover the device once (32 per head for 8 kv heads:
-// one XCD each).
+// tokens (at least TW) while that fits TC = 4 TW, with nd = CUs / kv heads, so
+// the chunks of all kv heads cover the device once (32 per head for 8 kv
+// heads: one XCD each).
 enum { AD_PAGED = 0, AD_PAGED_REV = 1, AD_IDENT = 2 };
-// Longer contexts: chunks of nsub consecutive 160-token sub-chunks (a
+// Longer contexts: chunks of nsub consecutive TC-token sub-chunks (a
 // workgroup runs them in turn with an online softmax), so a kv head never has
 // more than nd chunks: the grid stays one round of one workgroup per CU (the
 // kernel's registers allow one) and the merge reads at most nd partials.
-ZH_DEV uint32_t attn_nsub(uint32_t seq, uint32_t nd) {
-    const uint32_t span = nd * AD_TC;
+ZH_DEV uint32_t attn_nsub(uint32_t seq, uint32_t nd, uint32_t tc) {
+    const uint32_t span = nd * tc;
     return seq > span ? (seq + span - 1) / span : 1u;
 }
-ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq, uint32_t nd, bool sub) {
-    const uint32_t ct = ((seq + nd - 1) / nd + 7) / 8 * 8;
-    return seq > nd * AD_TC ? (uint32_t)AD_TC * (sub ? attn_nsub(seq, nd) : 1u) : max(ct, (uint32_t)AD_TW);
+ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq, uint32_t nd, bool sub, uint32_t tw) {
+    const uint32_t tc = AD_W * tw, ct = ((seq + nd - 1) / nd + 7) / 8 * 8;
+    return seq > nd * tc ? tc * (sub ? attn_nsub(seq, nd, tc) : 1u) : max(ct, tw);
 }
 // Sub-chunks are compiled for up to 4 q heads per kv head (G = 8 would spill
-// its loop-carried state); G = 8 keeps 160-token chunks at long contexts.
+// its loop-carried state); G = 8 keeps TC-token chunks at long contexts.
 template <int G> constexpr bool attn_sub_ok() { return G <= 4; }
 static uint32_t attn_nd(uint32_t nkv, int cu_count) {
     const uint32_t cu = cu_count > 0 && cu_count < 256 ? (uint32_t)cu_count : 256u;
-    return cu / nkv > 0 ? cu / nkv : 1u;
+    const uint32_t nd = cu / nkv > 0 ? cu / nkv : 1u;
+    return nd < 256u ? nd : 256u;  // the merge keeps at most 256 chunk statistics in LDS
 }
-// chunk slots per head: the partials of a device with at most 256 CUs fit
-static uint32_t attn_n_chunks(uint32_t max_seq, uint32_t nd) {
-    const uint32_t n = (max_seq + AD_TC - 1) / AD_TC;
+// chunk slots per head for sub-chunks of tc tokens (the partials, sized with
+// the shortest, hold any; a device with at most 256 CUs fits)
+static uint32_t attn_n_chunks(uint32_t max_seq, uint32_t nd, uint32_t tc = AD_TC_MIN) {
+    const uint32_t n = (max_seq + tc - 1) / tc;
     return n > nd ? n : nd;
 }
 
@@ -428,12 +438,13 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
     TRACE_OPS(5);
 }
 
-template <int G, bool FUSED, int MODE>
+template <int G, bool FUSED, int MODE, int TW>
 __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
+    constexpr int TC = AD_W * TW;  // tokens per sub-chunk
     const uint32_t kvh = blockIdx.x, tid = threadIdx.x;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, sub = lane & 7, grp = lane >> 3;
     TRACE_OPS(0);
-    static_assert(AD_TW % 8 == 0 && AD_TW + 8 <= 48, "a wave's tokens must fit 3 pages from an 8-aligned start");
+    static_assert(TW % 8 == 0 && TW + 8 <= 48, "a wave's tokens must fit 3 pages from an 8-aligned start");
     // Position: a branch-free read (a branch would wait for the load at its
     // join). AD_PAGED: the chunk is blockIdx.y, so the page entries (scalar
     // loads), the position and the q loads all go out at once. AD_PAGED_REV:
@@ -445,17 +456,17 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     const uint32_t posv = p.pos.dev ? pos_raw + p.pos.value : p.pos.value;
     const uint32_t seq = FUSED ? posv + 1 : posv;
     constexpr bool SUB = MODE == AD_IDENT && attn_sub_ok<G>();
-    const uint32_t CT = MODE == AD_IDENT ? attn_chunk_tokens(seq, p.nd, SUB) : (uint32_t)AD_TC;
-    const uint32_t nsub = SUB ? attn_nsub(seq, p.nd) : 1u;  // 160-token sub-chunks per chunk
+    const uint32_t CT = MODE == AD_IDENT ? attn_chunk_tokens(seq, p.nd, SUB, TW) : (uint32_t)TC;
+    const uint32_t nsub = SUB ? attn_nsub(seq, p.nd, TC) : 1u;  // TC-token sub-chunks per chunk
     uint32_t chunk = blockIdx.y;
     if (MODE != AD_PAGED) {
         const uint32_t nv_hint = (seq + CT - 1) / CT;
         chunk = blockIdx.y < nv_hint ? nv_hint - 1 - blockIdx.y : blockIdx.y;
     }
-    const uint32_t t0 = chunk * CT, tw0 = t0 + wave * AD_TW;
+    const uint32_t t0 = chunk * CT, tw0 = t0 + wave * TW;
     // this wave's tokens within (each sub-chunk of) the chunk: a chunk
-    // shorter than 160 leaves the last waves fewer, or none
-    const uint32_t wtok = CT > wave * AD_TW ? min(CT - wave * AD_TW, (uint32_t)AD_TW) : 0u;
+    // shorter than TC leaves the last waves fewer, or none
+    const uint32_t wtok = CT > wave * TW ? min(CT - wave * TW, (uint32_t)TW) : 0u;
     const uint32_t pgb = tw0 / 16, o16 = tw0 & 15;
     uint32_t page0, page1, page2;
     if (MODE == AD_IDENT) {
@@ -526,7 +537,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     // q preparation (after the K and V loads are issued) waits only for its
     // own loads.
     asm volatile("" ::: "memory");
-    __shared__ float ps[AD_W][G][AD_TW];
+    __shared__ float ps[AD_W][G][TW];
     __shared__ float wm[AD_W][G], wl[AD_W][G];
     __shared__ float wo[AD_W][4][G][FD_HD];  // per wave and token row
     const uint32_t vrow = lane >> 4, vcol = lane & 15;
@@ -552,13 +563,13 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     // 4-aligned offset never straddle a 16-token page). Sub-chunk i + 1's K
     // loads go out once sub-chunk i's scores are computed, its V loads once
     // sub-chunk i's P*V is done, in the same registers.
-    u32x4 kr[AD_TW / 8][2];
-    u32x4 vr[AD_TW / 4];
+    u32x4 kr[TW / 8][2];
+    u32x4 vr[TW / 4];
     auto pages_of = [&](uint32_t i, uint32_t &pg0, uint32_t &pg1, uint32_t &pg2, uint32_t &pgbs)
         __attribute__((always_inline)) {
         pg0 = page0; pg1 = page1; pg2 = page2; pgbs = pgb;
         if (i) {
-            pgbs = (tw0 + i * AD_TC) / 16;
+            pgbs = (tw0 + i * TC) / 16;
             pg0 = pgbs; pg1 = pgbs + 1; pg2 = pgbs + 2;
         }
     };
@@ -567,7 +578,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         pages_of(i, g0, g1, g2, gb);
         const size_t pa = g0 < ptok ? g0 : 0u, pb = g1 < ptok ? g1 : 0u, pc = g2 < ptok ? g2 : 0u;
 #pragma unroll
-        for (int j = 0; j < AD_TW / 8; j++) {
+        for (int j = 0; j < TW / 8; j++) {
             // o16 + 8j is 8-aligned: the pass stays in one page
             const uint16_t *kp = kv_row(kh, pa, pb, pc, o16 + 8 * j) + grp * FD_HD;
             kr[j][0] = *(const u32x4 *)(kp + sub * 8);
@@ -579,7 +590,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         pages_of(i, g0, g1, g2, gb);
         const size_t pa = g0 < ptok ? g0 : 0u, pb = g1 < ptok ? g1 : 0u, pc = g2 < ptok ? g2 : 0u;
 #pragma unroll
-        for (int k = 0; k < AD_TW / 4; k++)
+        for (int k = 0; k < TW / 4; k++)
             vr[k] = *(const u32x4 *)(kv_row(vh, pa, pb, pc, o16 + 4 * k + vrow) + 8 * vcol);
     };
     load_k(0);
@@ -600,9 +611,9 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0}, vnew4 = {0, 0, 0, 0};
     if (FUSED && posv >= tw0) {
         const uint32_t rel = posv - tw0;
-        if (rel % AD_TC < wtok && rel / AD_TC < nsub) {
-            s_own = rel / AD_TC;
-            inew = rel % AD_TC;
+        if (rel % TC < wtok && rel / TC < nsub) {
+            s_own = rel / TC;
+            inew = rel % TC;
             norm_rope16(klo, khi, kwl, kwh, co, sn, p.eps);
             n0 = u32x4{pack_h2(klo[0], klo[1]), pack_h2(klo[2], klo[3]), pack_h2(klo[4], klo[5]),
                        pack_h2(klo[6], klo[7])};
@@ -638,14 +649,14 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
     // for this sub-chunk's K only, P*V for its V only.
     auto body = [&](uint32_t sc_i, auto pf) __attribute__((always_inline)) {
         constexpr bool PF = decltype(pf)::value;
-        const uint32_t tws = tw0 + sc_i * AD_TC;
+        const uint32_t tws = tw0 + sc_i * TC;
         const uint32_t nts = seq > tws ? min(seq - tws, wtok) : 0u;
         const bool owner = sc_i == s_own;  // uniform per wave
 
         // ---- scores: token 8j + grp, 16 dims per lane, reduced over 8 lanes
-        float sc[AD_TW / 8][G];
+        float sc[TW / 8][G];
 #pragma unroll
-        for (int j = 0; j < AD_TW / 8; j++) {
+        for (int j = 0; j < TW / 8; j++) {
             const bool sel = owner && (uint32_t)(8 * j) + grp == inew;
             const u32x4 k0 = sel ? n0 : kr[j][0], k1 = sel ? n1 : kr[j][1];
             const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
@@ -679,14 +690,14 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         for (int g = 0; g < G; g++) {
             float m = sc[0][g];
 #pragma unroll
-            for (int j = 1; j < AD_TW / 8; j++) m = fmaxf(m, sc[j][g]);
+            for (int j = 1; j < TW / 8; j++) m = fmaxf(m, sc[j][g]);
             m = rows_max(fmaxf(m, dpp_f<0x140>(m)));  // m is uniform within each 8-lane token group
             const float mn = fmaxf(m_run[g], m);
             const float ms = mn == -INFINITY ? 0.f : mn;  // no valid token yet
             const float f = m_run[g] == -INFINITY ? 0.f : expf(m_run[g] - ms);
             float l = 0.f;
 #pragma unroll
-            for (int j = 0; j < AD_TW / 8; j++) {
+            for (int j = 0; j < TW / 8; j++) {
                 const float pr = expf(sc[j][g] - ms);
                 if (sub == 0) ps[wave][g][8 * j + grp] = pr;
                 l += pr;
@@ -700,7 +711,7 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
         __syncthreads();
         if (sc_i == 0) TRACE_OPS(8);
 #pragma unroll
-        for (int k = 0; k < AD_TW / 4; k++) {
+        for (int k = 0; k < TW / 4; k++) {
             const uint32_t i = 4 * k + vrow;
             u32x4 v = owner && i == inew ? vnew4 : vr[k];
             if (i >= nts) v = u32x4{0, 0, 0, 0};  // rows past the end may hold anything
@@ -830,17 +841,24 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
     AttnP p = p0;
     p.nd = attn_nd(nkv, c->cu_count);
     p.no_wait = c->concurrent ? 1u : 0u;
-    p.n_chunks = attn_n_chunks(max_seq, p.nd);
+    // tokens per wave (see AD_W): sub-chunks only with identity pages and at
+    // most 4 q heads per kv head
+    const bool sub = ident && G <= 4;
+    const uint32_t tw = !sub ? 40u : max_seq <= 8192 ? 24u : 32u;
+    p.n_chunks = attn_n_chunks(max_seq, p.nd, AD_W * tw);
     // identity pages: at most nd chunks per kv head at any context (longer
     // chunks hold several sub-chunks)
-    if (ident && G <= 4 && p.n_chunks > p.nd) p.n_chunks = p.nd;
+    if (sub && p.n_chunks > p.nd) p.n_chunks = p.nd;
     dim3 grid(nkv, p.n_chunks);
     // one workgroup per CU: a grid within the CU count is resident at once
     const bool rev = (uint64_t)nkv * p.n_chunks > (uint64_t)c->cu_count;
-#define AD_LAUNCH1(GG, FF)                                                                                   \
-    if (ident) hipLaunchKernelGGL((k_attn_decode<GG, FF, AD_IDENT>), grid, dim3(AD_T), 0, c->stream, p);      \
-    else if (rev) hipLaunchKernelGGL((k_attn_decode<GG, FF, AD_PAGED_REV>), grid, dim3(AD_T), 0, c->stream, p); \
-    else hipLaunchKernelGGL((k_attn_decode<GG, FF, AD_PAGED>), grid, dim3(AD_T), 0, c->stream, p)
+#define AD_K(GG, FF, MM, TT) hipLaunchKernelGGL((k_attn_decode<GG, FF, MM, TT>), grid, dim3(AD_T), 0, c->stream, p)
+#define AD_LAUNCH1(GG, FF)                                                   \
+    if (ident && GG <= 4 && tw == 24) AD_K(GG, FF, AD_IDENT, GG <= 4 ? 24 : 40); \
+    else if (ident && GG <= 4) AD_K(GG, FF, AD_IDENT, GG <= 4 ? 32 : 40);        \
+    else if (ident) AD_K(GG, FF, AD_IDENT, 40);                                 \
+    else if (rev) AD_K(GG, FF, AD_PAGED_REV, 40);                               \
+    else AD_K(GG, FF, AD_PAGED, 40)
 #define AD_LAUNCH(GG)          \
     if (fused) {               \
         AD_LAUNCH1(GG, true);  \
@@ -856,6 +874,7 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
     }
 #undef AD_LAUNCH
 #undef AD_LAUNCH1
+#undef AD_K
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
 }
