@@ -103,6 +103,22 @@ int zh_synth_vector(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint32_t kind, ui
 int zh_dmmv(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off,
             const zh_buf *x, uint64_t x_off, zh_buf *y, uint64_t y_off,
             uint32_t M, uint32_t K, uint32_t acc_mode);
+/* Batched DMMV (a skinny GEMM over num_cols activation vectors): replaces
+ * DmmvDispatch.recordBatchDispatchPush (dmmv.zig:880-925, BatchDmmvPushConstants
+ * {M,K,a_offset,x_offset,y_offset,num_cols} dmmv.zig:31-38; dmmv_q4k_batch.comp /
+ * dmmv_q6k_batch.comp). X: f32 [num_cols][K] (column v at X + v*K*4 bytes,
+ * 16-byte aligned offset); Y: f32 [num_cols][M] (= or += when acc_mode == 1).
+ * qtype Q4_K or Q6_K, K % 256 == 0, num_cols 1..ZH_DMMV_MAX_COLS. The weights
+ * stream from HBM once for all columns; each column's result equals zh_dmmv on
+ * that column bit for bit. */
+#define ZH_DMMV_MAX_COLS 16
+int zh_dmmv_batched(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off, const zh_buf *X, uint64_t x_off,
+                    zh_buf *Y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t num_cols, uint32_t acc_mode);
+/* Y[v] = silu(Wg X[v]) * (Wu X[v]) for v < num_cols (Q4_K), the batched form of
+ * zh_dmmv_fused_gate_up_swiglu below; layouts as zh_dmmv_batched. */
+int zh_dmmv_fused_gate_up_swiglu_batched(zh_ctx *ctx, uint32_t qtype, const zh_buf *Wg, uint64_t g_off,
+                                         const zh_buf *Wu, uint64_t u_off, const zh_buf *X, uint64_t x_off,
+                                         zh_buf *Y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t num_cols);
 /* y = silu(Wg x) * (Wu x): dispatchDmmvFusedGateUpSwiglu (forward.zig:8237-8273,
  * dmmv_q4k_fused_gate_up_swiglu.comp). Both matrices share qtype. */
 int zh_dmmv_fused_gate_up_swiglu(zh_ctx *ctx, uint32_t qtype, const zh_buf *Wg, uint64_t g_off,

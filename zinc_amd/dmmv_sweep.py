@@ -11,6 +11,14 @@ activation pre-quantised once, as the engine feeds the projections that share
 an input). Algorithmic bytes = weight blocks + 4 K (x) + 4 M (y), the
 per-kernel figure of the bandwidth roofline; fraction of the 8 TB/s peak.
 A streaming read of 1 GiB gives the measured ceiling beside it.
+
+    python -m zinc_amd.dmmv_sweep --batched [--md OUT.md]
+
+instead times the batched DMMV (zh_dmmv_batched / the gate/up form, the
+skinny GEMM of recordBatchDispatchPush, dmmv.zig:880-925) on the config-3
+decode shapes at 1, 2, 4 and 8 activation vectors: microseconds per launch
+and the weight bytes streamed per vector-microsecond (the one-vector rate
+times the speed-up over one launch per vector).
 """
 import argparse
 import json
@@ -70,12 +78,70 @@ def measure(ctx, name, qt, M, K, iters):
     return res
 
 
+BATCH_SHAPES = [
+    ("Q/K/V Q4_K 6144x4096", hip.Q4_K, 6144, 4096, False),
+    ("O Q4_K 4096x4096", hip.Q4_K, 4096, 4096, False),
+    ("gate/up Q4_K 2 x 12288x4096 + SwiGLU", hip.Q4_K, 12288, 4096, True),
+    ("down Q6_K 4096x12288", hip.Q6_K, 4096, 12288, False),
+    ("LM head Q6_K 151936x4096", hip.Q6_K, 151936, 4096, False),
+]
+
+
+def measure_batched(ctx, name, qt, M, K, gate_up, ncols=(1, 2, 4, 8), iters=40):
+    wb = hip.tensor_bytes(qt, M, K)
+    nm = 2 if gate_up else 1
+    ncp = max(2, -(-ROTATE_BYTES // (wb * nm)))
+    W = ctx.alloc(wb * nm * ncp)
+    for i in range(nm * ncp):
+        ctx.synth_tensor(W, i * wb, qt | (0x100 if qt == hip.Q4_K else 0), M, K, 1234 + 3, 100 + i)
+    nmax = max(ncols)
+    X = ctx.alloc(4 * K * nmax)
+    ctx.synth_vector(X, 0, 0, K * nmax, 1.0, 1234 + 3, 99)
+    Y = ctx.alloc(4 * M * nmax)
+    res = {"shape": name, "qtype": qt, "M": M, "K": K, "weight_bytes": wb * nm, "cols": {}}
+    for n in ncols:
+        def fn(c):
+            if gate_up:
+                ctx.dmmv_fused_gate_up_swiglu_batched(qt, W, 2 * c * wb, W, (2 * c + 1) * wb, X, 0, Y, 0, M, K, n)
+            else:
+                ctx.dmmv_batched(qt, W, c * wb, X, 0, Y, 0, M, K, n)
+        for i in range(2 * ncp):
+            fn(i % ncp)
+        ctx.sync()
+        ctx.record(0)
+        for i in range(iters):
+            fn(i % ncp)
+        ctx.record(1)
+        ctx.sync()
+        us = ctx.elapsed_ms(0, 1) * 1e3 / iters
+        res["cols"][n] = {"us": round(us, 2), "us_per_col": round(us / n, 2)}
+    for b in (W, X, Y):
+        ctx.free(b)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--batched", action="store_true", help="time the batched DMMV at 1, 2, 4, 8 vectors")
     ap.add_argument("--iters", type=int, default=60)
     ap.add_argument("--md", default=None, help="also write a markdown table here")
     a = ap.parse_args()
     ctx = hip.Context(0)
+    if a.batched:
+        rows = [measure_batched(ctx, *s) for s in BATCH_SHAPES]
+        ctx.close()
+        print(json.dumps({"workload": "batched DMMV on config-3 decode shapes, rotating weight copies > 256 MB MALL",
+                          "shapes": rows}), flush=True)
+        if a.md:
+            with open(a.md, "w") as f:
+                f.write("| shape | 1 col: us | 2 cols: us (per col) | 4 cols: us (per col) | 8 cols: us (per col) | "
+                        "speed-up at 4 cols |\n|---|---|---|---|---|---|\n")
+                for r in rows:
+                    c = r["cols"]
+                    f.write(f"| {r['shape']} | {c[1]['us']} | {c[2]['us']} ({c[2]['us_per_col']}) | "
+                            f"{c[4]['us']} ({c[4]['us_per_col']}) | {c[8]['us']} ({c[8]['us_per_col']}) | "
+                            f"{c[1]['us'] / c[4]['us_per_col']:.2f}x |\n")
+        return 0
     cal = ctx.alloc(1 << 30)
     ctx.synth_vector(cal, 0, 1, (1 << 30) // 2, 1.0, 7, 7)
     stream_gbs = ctx.stream_read_probe(cal, 1 << 30, 3)

@@ -98,6 +98,9 @@ SIGNATURES = {
     "zh_xq_bytes": (_u64, [_u32]),
     "zh_quantize_activation": (_i32, [_P, _P, _u64, _u32, _u32, _u32, _P, _u64]),
     "zh_dmmv_xq": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _u32, _u32, _u32]),
+    "zh_dmmv_batched": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _u32, _u32, _u32, _u32]),
+    "zh_dmmv_fused_gate_up_swiglu_batched": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _P, _u64, _u32, _u32,
+                                                    _u32]),
     "zh_dmmv_fused_gate_up_swiglu_xq": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _P, _u64, _u32, _u32]),
     "zh_dequant_rows": (_i32, [_P, _u32, _P, _u64, _u32, _u32, _u32, _P, _u64]),
     "zh_rms_norm": (_i32, [_P, _P, _u64, _P, _u32, _P, _u64, _u32, _u32, _f32]),
@@ -293,6 +296,15 @@ class Context:
     def dmmv_fused_gate_up_swiglu(self, qtype, Wg, g_off, Wu, u_off, x, x_off, y, y_off, M, K):
         self.check(lib().zh_dmmv_fused_gate_up_swiglu(self.h, qtype, Wg.h, g_off, Wu.h, u_off, x.h, x_off,
                                                       y.h, y_off, M, K))
+
+    def dmmv_batched(self, qtype, W, a_off, X, x_off, Y, y_off, M, K, num_cols, acc_mode=0):
+        """recordBatchDispatchPush: Y[v] (+)= W X[v], X [num_cols][K], Y [num_cols][M]."""
+        self.check(lib().zh_dmmv_batched(self.h, qtype, W.h, a_off, X.h, x_off, Y.h, y_off, M, K, num_cols,
+                                          acc_mode))
+
+    def dmmv_fused_gate_up_swiglu_batched(self, qtype, Wg, g_off, Wu, u_off, X, x_off, Y, y_off, M, K, num_cols):
+        self.check(lib().zh_dmmv_fused_gate_up_swiglu_batched(self.h, qtype, Wg.h, g_off, Wu.h, u_off, X.h, x_off,
+                                                              Y.h, y_off, M, K, num_cols))
 
     def dmmv_moe(self, qtype, W, expert_stride, routing, x, x_expert_stride, x_off, y, y_off, M, K, n_used):
         self.check(lib().zh_dmmv_moe(self.h, qtype, W.h, expert_stride, routing.h, x.h, x_expert_stride, x_off,

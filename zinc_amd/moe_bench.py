@@ -8,7 +8,9 @@ random-id prompt, seeded random-init weights.
 
 Prints one JSON line: decode tok/s, the engine's bytes-per-token model
 (dmmvMetrics + flashAttnMetrics with fp16 KV and the 8 selected experts) and
-the fraction of the 8 TB/s roofline.
+the fraction of the 8 TB/s roofline, and per-layer launch-group times (HIP
+events over replays with the step's arguments) against their algorithmic
+bytes.
 """
 import argparse
 import json
@@ -50,13 +52,21 @@ def main():
     gpu_ms = ctx.elapsed_ms(0, 1)
     tok_s = a.steps / wall
     bpt = eng.bytes_per_token(pos + a.steps // 2)
+    # per-layer launch groups, replayed with the step's own arguments
+    L = pos + a.steps
+    per = {}
+    for g in eng.GROUPS:
+        us = eng.time_kernel(g, 4 * cfg["n_layers"])
+        nb = eng.group_bytes(g, L)
+        per[g] = {"us": round(us, 3), "GBs": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / PEAK, 4)}
     eng.deinit()
     ctx.close()
     out = {"workload": "config 4: sparse-MoE decoder (48L, 2048 hidden, 32q/4kv heads, 128 experts top-8, "
                        "expert FFN 768, vocab 151936), batch 1, greedy decode at KV context 8192+",
            "steps": a.steps, "tok_s": round(tok_s, 2), "ms_per_token": round(wall * 1e3 / a.steps, 4),
            "gpu_ms_per_token": round(gpu_ms / a.steps, 4), "context_start": pos, "bytes_per_token": bpt,
-           "token_roofline_frac": round(bpt * tok_s / 1e9 / PEAK, 4), "distinct_tokens": len(set(toks))}
+           "token_roofline_frac": round(bpt * tok_s / 1e9 / PEAK, 4), "distinct_tokens": len(set(toks)),
+           "per_kernel": per}
     print(json.dumps(out), flush=True)
     return 0
 
