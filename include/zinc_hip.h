@@ -250,6 +250,18 @@ int zh_engine_sample_greedy(zh_engine *eng, uint32_t *token);
  * loop feeds each argmax back on device (no host round trip per token). */
 int zh_engine_generate(zh_engine *eng, const uint32_t *prompt, uint32_t n_prompt, uint32_t start_pos,
                        uint32_t max_tokens, uint32_t eos, uint32_t *out_tokens, uint32_t *n_out);
+/* Batched greedy decode of n_seq sequences in lockstep, one token each per
+ * step: the decode batch of the reference's scheduler (src/scheduler/
+ * scheduler.zig:27-110 activeDecoding, each request a generate(),
+ * forward.zig:10983) on one weight stream. engines[v] (distinct) share the
+ * weights of engines[0] and its context (zh_engine_create_shared(ctx, base,
+ * ...) with base's own ctx); prompts [n_seq][n_prompt]; all sequences start
+ * at start_pos; out_tokens [n_seq][max_tokens] (no EOS stop). The Q/K/V, O,
+ * gate/up, down and LM-head mat-vecs run as batched DMMV launches
+ * (zh_dmmv_batched), attention per sequence. Dense models whose projections
+ * are Q4_K / Q6_K (ZH_ERR_UNSUPPORTED_QUANT_TYPE otherwise). */
+int zh_engine_generate_batch(zh_engine *const *engines, uint32_t n_seq, const uint32_t *prompts, uint32_t n_prompt,
+                             uint32_t start_pos, uint32_t max_tokens, uint32_t *out_tokens);
 /* Copy the last logits (vocab f32) to host. */
 int zh_engine_logits(zh_engine *eng, float *dst);
 /* Copy the hidden state (hidden f32) after the last step to host. */

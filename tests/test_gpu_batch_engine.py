@@ -1,0 +1,70 @@
+"""Batched decode (zh_engine_generate_batch): several sequences over one copy
+of the weights step in lockstep, the projections as batched DMMV launches.
+
+Each sequence must decode exactly as it does alone (generate() on its own
+engine: the single-sequence path that test_gpu_engine.py pins token-exact to
+the oracle), and its last logits must agree with that run's within the DMMV
+tolerance (the batched path stages the SwiGLU output from f32 where the
+single path copies its XQ image, so the last bits may differ)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+# Q4_K_M-style mix: attn_v / ffn_down Q6_K on the use_more_bits layers, so
+# the Q/K/V launches split into runs of equal types; K = 1024 / 2048 keep the
+# Q6_K rows 16-byte multiples (the Q6_K tile kernels)
+CFG = dict(n_layers=4, hidden=1024, n_heads=8, n_kv_heads=2, head_dim=128, ffn=2048, vocab=4096,
+           n_experts=0, n_experts_used=0, expert_ffn=0, max_ctx=512, type_attn=12, type_ffn_gate_up=12,
+           type_ffn_down=12, type_lm_head=14, type_embd=12, type_router=8, type_more_bits=14,
+           rope_base=1e6, eps=1e-6, seed=57)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import zinc_amd
+    c = zinc_amd.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("n_seq", [3, 4])
+def test_batch_matches_single_sequences(ctx, n_seq):
+    import zinc_amd
+    print(f"batch engine n_seq={n_seq}", flush=True)
+    base = zinc_amd.InferenceEngine(ctx, CFG)
+    engines = [base] + [base.share(ctx) for _ in range(n_seq - 1)]
+    rng = np.random.default_rng(n_seq)
+    prompts = rng.integers(0, CFG["vocab"], (n_seq, 5)).astype(np.uint32)
+    prefill, steps = 40, 12
+    solo, solo_logits = [], []
+    for v, e in enumerate(engines):
+        e.prefill_kv_random(prefill, 100 + v)
+        solo.append(e.generate(prompts[v].tolist(), steps, start_pos=prefill))
+        solo_logits.append(e.logits())
+    for v, e in enumerate(engines):
+        e.prefill_kv_random(prefill, 100 + v)
+    got = zinc_amd.InferenceEngine.generate_batch(engines, prompts, steps, start_pos=prefill)
+    for v, e in enumerate(engines):
+        assert got[v] == solo[v], (v, got[v], solo[v])
+        lg = e.logits()
+        ref = solo_logits[v]
+        assert np.allclose(lg, ref, rtol=1e-3, atol=1e-4 + 1e-3 * np.abs(ref).max()), (v, np.abs(lg - ref).max())
+    assert len({tuple(t) for t in got}) == n_seq  # the sequences really differ
+    for e in engines[1:]:
+        e.deinit()
+    base.deinit()
+
+
+def test_batch_rejects_foreign_engines(ctx):
+    import zinc_amd
+    a = zinc_amd.InferenceEngine(ctx, dict(CFG, n_layers=2))
+    b = zinc_amd.InferenceEngine(ctx, dict(CFG, n_layers=2, seed=58))  # other weights
+    with pytest.raises(zinc_amd.ZincError) as e:
+        zinc_amd.InferenceEngine.generate_batch([a, b], [[1, 2], [3, 4]], 2, start_pos=0)
+    assert e.value.name == "InvalidArgument"
+    with pytest.raises(zinc_amd.ZincError) as e:
+        zinc_amd.InferenceEngine.generate_batch([a, a], [[1, 2], [3, 4]], 2, start_pos=0)
+    assert e.value.name == "InvalidArgument"
+    a.deinit()
+    b.deinit()

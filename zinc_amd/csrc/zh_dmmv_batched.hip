@@ -14,14 +14,16 @@
 
 #define TRACE(slot) do { } while (0)
 
-// Batched tile kernels (NV > 1 activation vectors): vector v reads
-// x + v * x_stride (or xq + v * xq_stride) and writes segY[s] + v * y_stride.
-// (A second kernel argument, so the one-vector kernels' argument block and
-// code stay as they are.)
+// Batched tile kernels (NV > 1 activation vectors): vector v reads x[v] (f32)
+// or xq[v] (XQ) and writes y[s][v] for segment s (LpbP's x / xq / segY are
+// unused). A second kernel argument, so the one-vector kernels' argument
+// block and code stay as they are.
+constexpr int BT_MAXV = 4;
 struct LpbB {
-    uint32_t x_stride, y_stride;
-    uint64_t xq_stride;
-    uint32_t nv;  // activation vectors of the launch (1, 2 or 4)
+    const float *x[BT_MAXV];
+    const uint8_t *xq[BT_MAXV];
+    float *y[3][BT_MAXV];
+    uint32_t nv;  // activation vectors of the launch (2 or 4)
 };
 
 // Batched staging: NV activation vectors into NV LDS images. Every vector's
@@ -29,24 +31,24 @@ struct LpbB {
 // built in turn, with the arithmetic of stage_and_fetch for one vector.
 template <int NV, int XQCH, int XCH, class Fetch>
 ZH_DEV void stage_and_fetch_nv(const LpbP &p, const LpbB &bt, const XLds (&lx)[NV], float *red, const Fetch &fetch) {
-    if (p.xq) {
+    if (bt.xq[0]) {
         XRegsQ<XQCH> xr[NV];
 #pragma unroll
-        for (int v = 0; v < NV; v++) stage_xq_issue(p.xq + (size_t)v * bt.xq_stride, p.K, xr[v]);
+        for (int v = 0; v < NV; v++) stage_xq_issue(bt.xq[v], p.K, xr[v]);
         fetch();
 #pragma unroll
         for (int v = 0; v < NV; v++) stage_xq_finish(xr[v], p.K, lx[v]);
     } else if (p.norm_w) {
         XRegsF<XCH> xr[NV];
 #pragma unroll
-        for (int v = 0; v < NV; v++) stage_x_issue<XCH, true>(p.x + (size_t)v * bt.x_stride, p.norm_w, p.K, xr[v]);
+        for (int v = 0; v < NV; v++) stage_x_issue<XCH, true>(bt.x[v], p.norm_w, p.K, xr[v]);
         fetch();
 #pragma unroll
         for (int v = 0; v < NV; v++) stage_x_finish(xr[v], true, p.eps, p.K, lx[v], red, nullptr);
     } else {
         XRegsF<XCH> xr[NV];
 #pragma unroll
-        for (int v = 0; v < NV; v++) stage_x_issue<XCH, false>(p.x + (size_t)v * bt.x_stride, nullptr, p.K, xr[v]);
+        for (int v = 0; v < NV; v++) stage_x_issue<XCH, false>(bt.x[v], nullptr, p.K, xr[v]);
         fetch();
 #pragma unroll
         for (int v = 0; v < NV; v++) stage_x_finish(xr[v], false, p.eps, p.K, lx[v], red, nullptr);
@@ -174,14 +176,14 @@ __global__ __launch_bounds__(LPB_T, NV == 2 ? 2 : 1) void k_dmmv_q4k_tile_nv(Lpb
             if (mat == 1 && tlane == 0 && (uint32_t)rt < nrows) {
 #pragma unroll
                 for (int v = 0; v < NV; v++) {
-                    float *yb = p.segY[sg] + (size_t)v * bt.y_stride;
+                    float *yb = bt.y[sg][v];
                     yb[rr0 + rt] = silu_mul(gate_res[v][rt], res[v]);
                 }
             }
         } else if (tlane == 0 && (uint32_t)rt < nrows) {
 #pragma unroll
             for (int v = 0; v < NV; v++) {
-                float *yb = p.segY[sg] + (size_t)v * bt.y_stride;
+                float *yb = bt.y[sg][v];
                 float out = res[v];
                 if (p.acc) out += yb[rr0 + rt];
                 yb[rr0 + rt] = out;
@@ -310,7 +312,7 @@ __global__ __launch_bounds__(LPB_T, 1) void k_dmmv_q6k_tile_nv(LpbP p, LpbB bt) 
         if (tlane == 0 && (uint32_t)rt < nrows) {
 #pragma unroll
             for (int v = 0; v < NV; v++) {
-                float *yb = p.segY[sg] + (size_t)v * bt.y_stride;
+                float *yb = bt.y[sg][v];
                 float out = res[v];
                 if (p.acc) out += yb[rr0 + rt];
                 yb[rr0 + rt] = out;
@@ -418,35 +420,30 @@ static int try_q6k_nv(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t *M
     }
 }
 
-// Batched DMMV on the tile kernels: y[s] + v * y_stride (= or +=) W[s] x_v for
-// v < n_vec, x_v = x + v * x_stride (f32, with the optional fused RMSNorm) or
-// xq + v * xq_stride (XQ). Vectors go in launches of 4, 2 or 1 (the widest
-// whose LDS images fit beside the weight tile); single vectors take the
-// one-vector path. Per vector the arithmetic is that of the one-vector
+// Batched DMMV on the tile kernels: y[s * n_vec + v] (= or +=) W[s] x_v for
+// v < n_vec, x_v = x[v] (f32, with the optional fused RMSNorm) or xq[v] (XQ;
+// x == nullptr). Vectors go in launches of 4 or 2 (the widest whose LDS
+// images fit beside the weight tile); a single vector left over takes the
+// one-vector path. Per vector the arithmetic is that of the one-vector tile
 // kernel, so every output equals its single-vector DMMV bit for bit.
 int zhk_dmmv_batched(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
-                     float *const *y, uint32_t y_stride, const uint32_t *M, const float *x, uint32_t x_stride,
-                     const void *xq, uint64_t xq_stride, const float *norm_w, float eps, uint32_t K, uint32_t acc,
-                     uint32_t n_vec) {
+                     const uint32_t *M, uint32_t K, uint32_t n_vec, const float *const *x, const void *const *xq,
+                     float *const *y, const float *norm_w, float eps, uint32_t acc) {
     if (!zhk_lpb_supported(qtype, K) || (mode == LPB_GATE_UP && qtype != ZH_Q4_K) || nseg < 1 || nseg > 3 ||
         n_vec == 0 || (!x && !xq))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "batched dmmv: unsupported qtype/K/mode/vectors");
     uint32_t v0 = 0;
     while (v0 < n_vec) {
         const uint32_t left = n_vec - v0;
-        const float *xv = x ? x + (size_t)v0 * x_stride : nullptr;
-        const void *xqv = xq ? (const char *)xq + (size_t)v0 * xq_stride : nullptr;
-        float *yv[3];
-        for (uint32_t s = 0; s < nseg; s++) yv[s] = y[s] + (size_t)v0 * y_stride;
         uint32_t done = 0;
         for (uint32_t nv = left >= 4 ? 4u : left >= 2 ? 2u : 0u; nv >= 2 && !done; nv /= 2) {
             LpbP p = {};
-            p.x = xv; p.norm_w = norm_w; p.eps = eps; p.xq = (const uint8_t *)xqv;
+            p.norm_w = norm_w; p.eps = eps;
             p.K = K; p.acc = acc; p.nseg = nseg; p.mode = (uint32_t)mode;
             p.row_bytes = zh_tensor_bytes(qtype, 1, K);
             uint32_t end = 0;
             for (uint32_t s = 0; s < nseg; s++) {
-                p.segW[s] = W[s]; p.segY[s] = yv[s];
+                p.segW[s] = W[s];
                 end += M[s];
                 p.seg_end[s] = end;
             }
@@ -454,13 +451,20 @@ int zhk_dmmv_batched(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const u
             p.M = end;
             LpbB bt = {};
             bt.nv = nv;
-            bt.x_stride = x_stride; bt.y_stride = y_stride; bt.xq_stride = xq_stride;
+            for (uint32_t v = 0; v < nv; v++) {
+                bt.x[v] = x ? x[v0 + v] : nullptr;
+                bt.xq[v] = x ? nullptr : (const uint8_t *)xq[v0 + v];
+                for (uint32_t s = 0; s < nseg; s++) bt.y[s][v] = y[s * n_vec + v0 + v];
+            }
             const int rc = qtype == ZH_Q4_K ? try_q4k_nv(c, p, nseg, M, bt) : try_q6k_nv(c, p, nseg, M, bt);
             if (rc > 0) return rc;
             if (rc == 0) done = nv;
         }
         if (!done) {  // one vector
-            const int rc = zhk_dmmv_lpb(c, qtype, mode, nseg, W, W2, yv, M, xv, norm_w, eps, nullptr, K, acc, xqv);
+            float *yv[3];
+            for (uint32_t s = 0; s < nseg; s++) yv[s] = y[s * n_vec + v0];
+            const int rc = zhk_dmmv_lpb(c, qtype, mode, nseg, W, W2, yv, M, x ? x[v0] : nullptr, norm_w, eps, nullptr,
+                                        K, acc, x ? nullptr : xq[v0]);
             if (rc) return rc;
             done = 1;
         }
@@ -484,10 +488,14 @@ extern "C" int zh_dmmv_batched(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint6
         !buf_range(Y, y_off, 4ull * M * num_cols) || (a_off & 15) || (x_off & 15) || (y_off & 3) || (K % 4))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "batched dmmv: range/alignment");
     const uint8_t *w = (const uint8_t *)W->ptr + a_off;
-    float *y = (float *)((char *)Y->ptr + y_off);
-    return zhk_dmmv_batched(c, qtype, LPB_PLAIN, 1, &w, nullptr, &y, M, &M,
-                            (const float *)((const char *)X->ptr + x_off), K, nullptr, 0, nullptr, 0.f, K, acc_mode,
-                            num_cols);
+    const float *xs[ZH_DMMV_MAX_COLS];
+    float *ys[ZH_DMMV_MAX_COLS];
+    for (uint32_t v = 0; v < num_cols; v++) {
+        xs[v] = (const float *)((const char *)X->ptr + x_off) + (size_t)v * K;
+        ys[v] = (float *)((char *)Y->ptr + y_off) + (size_t)v * M;
+    }
+    return zhk_dmmv_batched(c, qtype, LPB_PLAIN, 1, &w, nullptr, &M, K, num_cols, xs, nullptr, ys, nullptr, 0.f,
+                            acc_mode);
 }
 
 extern "C" int zh_dmmv_fused_gate_up_swiglu_batched(zh_ctx *c, uint32_t qtype, const zh_buf *Wg, uint64_t g_off,
@@ -503,8 +511,12 @@ extern "C" int zh_dmmv_fused_gate_up_swiglu_batched(zh_ctx *c, uint32_t qtype, c
         !buf_range(Y, y_off, 4ull * M * num_cols) || (g_off & 15) || (u_off & 15) || (x_off & 15) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "batched gate/up: range/alignment");
     const uint8_t *wg = (const uint8_t *)Wg->ptr + g_off;
-    float *y = (float *)((char *)Y->ptr + y_off);
-    return zhk_dmmv_batched(c, qtype, LPB_GATE_UP, 1, &wg, (const uint8_t *)Wu->ptr + u_off, &y, M, &M,
-                            (const float *)((const char *)X->ptr + x_off), K, nullptr, 0, nullptr, 0.f, K, 0,
-                            num_cols);
+    const float *xs[ZH_DMMV_MAX_COLS];
+    float *ys[ZH_DMMV_MAX_COLS];
+    for (uint32_t v = 0; v < num_cols; v++) {
+        xs[v] = (const float *)((const char *)X->ptr + x_off) + (size_t)v * K;
+        ys[v] = (float *)((char *)Y->ptr + y_off) + (size_t)v * M;
+    }
+    return zhk_dmmv_batched(c, qtype, LPB_GATE_UP, 1, &wg, (const uint8_t *)Wu->ptr + u_off, &M, K, num_cols, xs,
+                            nullptr, ys, nullptr, 0.f, 0);
 }

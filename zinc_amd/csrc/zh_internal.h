@@ -157,7 +157,8 @@ int zhk_dmmv_lpb(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uin
                  float *const *y, const uint32_t *M, const float *x, const float *norm_w, float eps,
                  float *normed_out, uint32_t K, uint32_t acc, const void *xq = nullptr,
                  uint8_t *xq_out = nullptr, uint32_t *grp_cnt = nullptr);
+// Batched DMMV: y[s * n_vec + v] (+)= W[s] x_v, x_v = x[v] (f32, optional
+// fused RMSNorm) or xq[v] (XQ, x == nullptr); mode 0 plain, 1 gate/up+SwiGLU.
 int zhk_dmmv_batched(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
-                     float *const *y, uint32_t y_stride, const uint32_t *M, const float *x, uint32_t x_stride,
-                     const void *xq, uint64_t xq_stride, const float *norm_w, float eps, uint32_t K, uint32_t acc,
-                     uint32_t n_vec);
+                     const uint32_t *M, uint32_t K, uint32_t n_vec, const float *const *x, const void *const *xq,
+                     float *const *y, const float *norm_w, float eps, uint32_t acc);

@@ -125,6 +125,22 @@ class InferenceEngine:
                                                 eos, C.c_void_p(out.ctypes.data), C.byref(n)))
         return out[:n.value].tolist()
 
+    @staticmethod
+    def generate_batch(engines, prompts, max_tokens, start_pos=0):
+        """Greedy decode of len(engines) sequences in lockstep on one weight
+        stream (zh_engine_generate_batch): engines[0] and engines built with
+        share() on its context; prompts: one equal-length prompt per engine.
+        Returns one token list per sequence."""
+        n = len(engines)
+        P = np.ascontiguousarray(prompts, dtype=np.uint32)
+        if P.ndim != 2 or P.shape[0] != n:
+            raise ValueError("one prompt per engine, all of the same length")
+        out = np.zeros((n, max(max_tokens, 1)), dtype=np.uint32)
+        hs = (C.c_void_p * n)(*[e.h for e in engines])
+        engines[0].ctx.check(lib().zh_engine_generate_batch(hs, n, C.c_void_p(P.ctypes.data), P.shape[1], start_pos,
+                                                            max_tokens, C.c_void_p(out.ctypes.data)))
+        return [out[v, :max_tokens].tolist() for v in range(n)]
+
     def logits(self):
         out = np.empty(self.config["vocab"], dtype=np.float32)
         self.ctx.check(lib().zh_engine_logits(self.h, C.c_void_p(out.ctypes.data)))

@@ -119,6 +119,7 @@ SIGNATURES = {
     "zh_engine_decode_step": (_i32, [_P, _u32, _u32, _i32]),
     "zh_engine_sample_greedy": (_i32, [_P, C.POINTER(_u32)]),
     "zh_engine_generate": (_i32, [_P, _P, _u32, _u32, _u32, _u32, _P, C.POINTER(_u32)]),
+    "zh_engine_generate_batch": (_i32, [_P, _u32, _P, _u32, _u32, _u32, _P]),
     "zh_engine_logits": (_i32, [_P, _P]),
     "zh_engine_hidden": (_i32, [_P, _P]),
     "zh_engine_tensor": (_i32, [_P, _u64, C.POINTER(_P), C.POINTER(_u64), C.POINTER(_u64)]),
