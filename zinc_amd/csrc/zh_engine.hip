@@ -826,16 +826,37 @@ static int record_step_batch(zh_engine *const *es, uint32_t n, bool collect) {
                                  ys.data(), Wf(y.attn_norm), m.eps, 0));
             i0 = i1;
         }
-        // attention over each sequence's own KV cache, in turn (forking the
-        // sequences onto auxiliary streams, joined before O, measured slower:
-        // 548 against 574 tok/s for 4 sequences of the config-3 model)
-        for (uint32_t v = 0; v < n; v++) {
-            zh_engine *ev = es[v];
-            const Layer &yv = ev->L[l];
-            zh_pos_src pos{0, ev->st + ST_POS};
-            ERC(zhk_attn_decode_fused(c, ev->q, ev->k, ev->v, Wf(y.q_norm), Wf(y.k_norm), ev->rope_cs, yv.kc, yv.vc,
-                                      ev->pages, ev->n_pages, m.max_ctx, ev->attn, ev->xq_q, m.n_heads, m.n_kv_heads,
-                                      pos, m.max_ctx, scale, m.eps, ev->fd_part, true));
+        // attention over each sequence's own KV cache: up to 4 sequences per
+        // launch (grid z = sequence) when they share a 1-4 q-head group,
+        // else one launch each (forking the sequences onto auxiliary streams,
+        // joined before O, measured slower than in-order launches)
+        if (m.n_heads / m.n_kv_heads <= 4) {
+            for (uint32_t v0 = 0; v0 < n; v0 += 4) {
+                const uint32_t nz = n - v0 < 4 ? n - v0 : 4;
+                const float *aq[4], *ak[4], *av[4];
+                uint16_t *akc[4], *avc[4];
+                float *aout[4], *apart[4];
+                void *axq[4];
+                const uint32_t *apos[4];
+                for (uint32_t z = 0; z < nz; z++) {
+                    zh_engine *ev = es[v0 + z];
+                    aq[z] = ev->q; ak[z] = ev->k; av[z] = ev->v;
+                    akc[z] = ev->L[l].kc; avc[z] = ev->L[l].vc;
+                    aout[z] = ev->attn; axq[z] = ev->xq_q; apart[z] = ev->fd_part; apos[z] = ev->st + ST_POS;
+                }
+                ERC(zhk_attn_decode_fused_z(c, nz, aq, ak, av, Wf(y.q_norm), Wf(y.k_norm), e0->rope_cs, akc, avc,
+                                            e0->pages, e0->n_pages, m.max_ctx, aout, axq, m.n_heads, m.n_kv_heads,
+                                            apos, m.max_ctx, scale, m.eps, apart));
+            }
+        } else {
+            for (uint32_t v = 0; v < n; v++) {
+                zh_engine *ev = es[v];
+                const Layer &yv = ev->L[l];
+                zh_pos_src pos{0, ev->st + ST_POS};
+                ERC(zhk_attn_decode_fused(c, ev->q, ev->k, ev->v, Wf(y.q_norm), Wf(y.k_norm), ev->rope_cs, yv.kc,
+                                          yv.vc, ev->pages, ev->n_pages, m.max_ctx, ev->attn, ev->xq_q, m.n_heads,
+                                          m.n_kv_heads, pos, m.max_ctx, scale, m.eps, ev->fd_part, true));
+            }
         }
         // O (+ residual) on each sequence's XQ attention output
         const uint8_t *wo = W(y.wo), *wg = W(y.gate), *wd = W(y.down);

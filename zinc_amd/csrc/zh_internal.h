@@ -122,6 +122,12 @@ int zhk_attn_decode_fused(zh_ctx *ctx, const float *q, const float *k, const flo
                           const uint32_t *pages, uint32_t n_pages, uint32_t cache_tokens, float *out,
                           void *xq_out, uint32_t nh, uint32_t nkv, zh_pos_src pos, uint32_t max_seq,
                           float scale, float eps, float *partials, bool ident_pages);
+int zhk_attn_decode_fused_z(zh_ctx *ctx, uint32_t n, const float *const *q, const float *const *k,
+                            const float *const *v, const float *qw, const float *kw, const float *rope_cs,
+                            uint16_t *const *kc, uint16_t *const *vc, const uint32_t *pages, uint32_t n_pages,
+                            uint32_t cache_tokens, float *const *out, void *const *xq_out, uint32_t nh, uint32_t nkv,
+                            const uint32_t *const *pos_dev, uint32_t max_seq, float scale, float eps,
+                            float *const *partials);
 // Prefill (zh_prefill.hip)
 int zhk_gemm(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, const _Float16 *X, uint32_t ldx, float *Y, uint32_t ldy,
              uint32_t M, uint32_t K, uint32_t N, uint32_t acc, const float *x_unscale = nullptr);

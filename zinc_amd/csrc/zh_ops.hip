@@ -440,397 +440,35 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
 
 template <int G, bool FUSED, int MODE, int TW>
 __global__ __launch_bounds__(AD_T, 1) void k_attn_decode(AttnP p) {
-    constexpr int TC = AD_W * TW;  // tokens per sub-chunk
-    const uint32_t kvh = blockIdx.x, tid = threadIdx.x;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, sub = lane & 7, grp = lane >> 3;
-    TRACE_OPS(0);
-    static_assert(TW % 8 == 0 && TW + 8 <= 48, "a wave's tokens must fit 3 pages from an 8-aligned start");
-    // Position: a branch-free read (a branch would wait for the load at its
-    // join). AD_PAGED: the chunk is blockIdx.y, so the page entries (scalar
-    // loads), the position and the q loads all go out at once. AD_PAGED_REV:
-    // chunks are dispatched last-first so the chunk holding the newest tokens
-    // (and, FUSED, the KV write) never waits in the dispatch tail; that order
-    // needs the position first. AD_IDENT: no page entries; the geometry
-    // follows the position (and is reversed the same way).
-    const uint32_t pos_raw = *(p.pos.dev ? p.pos.dev : p.pages);
-    const uint32_t posv = p.pos.dev ? pos_raw + p.pos.value : p.pos.value;
-    const uint32_t seq = FUSED ? posv + 1 : posv;
-    constexpr bool SUB = MODE == AD_IDENT && attn_sub_ok<G>();
-    const uint32_t CT = MODE == AD_IDENT ? attn_chunk_tokens(seq, p.nd, SUB, TW) : (uint32_t)TC;
-    const uint32_t nsub = SUB ? attn_nsub(seq, p.nd, TC) : 1u;  // TC-token sub-chunks per chunk
-    uint32_t chunk = blockIdx.y;
-    if (MODE != AD_PAGED) {
-        const uint32_t nv_hint = (seq + CT - 1) / CT;
-        chunk = blockIdx.y < nv_hint ? nv_hint - 1 - blockIdx.y : blockIdx.y;
-    }
-    const uint32_t t0 = chunk * CT, tw0 = t0 + wave * TW;
-    // this wave's tokens within (each sub-chunk of) the chunk: a chunk
-    // shorter than TC leaves the last waves fewer, or none
-    const uint32_t wtok = CT > wave * TW ? min(CT - wave * TW, (uint32_t)TW) : 0u;
-    const uint32_t pgb = tw0 / 16, o16 = tw0 & 15;
-    uint32_t page0, page1, page2;
-    if (MODE == AD_IDENT) {
-        page0 = pgb; page1 = pgb + 1; page2 = pgb + 2;
-    } else {
-        page0 = p.pages[min(pgb, p.n_pages - 1)];
-        page1 = p.pages[min(pgb + 1, p.n_pages - 1)];
-        page2 = p.pages[min(pgb + 2, p.n_pages - 1)];
-    }
-    const uint16_t *kh = p.kc + (size_t)kvh * p.cache_tokens * FD_HD;
-    const uint16_t *vh = p.vc + (size_t)kvh * p.cache_tokens * FD_HD;
+#include "zh_attn_body.inc"
 
-    // ---- loads: q (and the new token's raw k/v) first, then K, then V
-    float qlo[G][8], qhi[G][8];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        const float *qp = p.q + (size_t)(kvh * G + g) * FD_HD;
-        const f32x4 a = *(const f32x4 *)(qp + sub * 8), b = *(const f32x4 *)(qp + sub * 8 + 4);
-        const f32x4 c = *(const f32x4 *)(qp + 64 + sub * 8), d = *(const f32x4 *)(qp + 64 + sub * 8 + 4);
-        qlo[g][0] = a.x; qlo[g][1] = a.y; qlo[g][2] = a.z; qlo[g][3] = a.w;
-        qlo[g][4] = b.x; qlo[g][5] = b.y; qlo[g][6] = b.z; qlo[g][7] = b.w;
-        qhi[g][0] = c.x; qhi[g][1] = c.y; qhi[g][2] = c.z; qhi[g][3] = c.w;
-        qhi[g][4] = d.x; qhi[g][5] = d.y; qhi[g][6] = d.z; qhi[g][7] = d.w;
-    }
-    float klo[8], khi[8], vn0 = 0.f, vn1 = 0.f, vn8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (FUSED) {
-        const float *kp = p.k_new + (size_t)kvh * FD_HD;
-        const f32x4 a = *(const f32x4 *)(kp + sub * 8), b = *(const f32x4 *)(kp + sub * 8 + 4);
-        const f32x4 c = *(const f32x4 *)(kp + 64 + sub * 8), d = *(const f32x4 *)(kp + 64 + sub * 8 + 4);
-        klo[0] = a.x; klo[1] = a.y; klo[2] = a.z; klo[3] = a.w; klo[4] = b.x; klo[5] = b.y; klo[6] = b.z; klo[7] = b.w;
-        khi[0] = c.x; khi[1] = c.y; khi[2] = c.z; khi[3] = c.w; khi[4] = d.x; khi[5] = d.y; khi[6] = d.z; khi[7] = d.w;
-        const float2 vv = *(const float2 *)(p.v_new + (size_t)kvh * FD_HD + 2 * lane);
-        vn0 = vv.x;
-        vn1 = vv.y;
-        const f32x4 va = *(const f32x4 *)(p.v_new + (size_t)kvh * FD_HD + 8 * (lane & 15));
-        const f32x4 vb = *(const f32x4 *)(p.v_new + (size_t)kvh * FD_HD + 8 * (lane & 15) + 4);
-        vn8[0] = va.x; vn8[1] = va.y; vn8[2] = va.z; vn8[3] = va.w;
-        vn8[4] = vb.x; vn8[5] = vb.y; vn8[6] = vb.z; vn8[7] = vb.w;
-    }
-    float co[8], sn[8], qwl[8], qwh[8], kwl[8], kwh[8];
-    if (FUSED) {
-        const f32x4 *w4 = (const f32x4 *)(p.q_norm + sub * 8), *w5 = (const f32x4 *)(p.q_norm + 64 + sub * 8);
-        const f32x4 *w6 = (const f32x4 *)(p.k_norm + sub * 8), *w7 = (const f32x4 *)(p.k_norm + 64 + sub * 8);
-#pragma unroll
-        for (int h2 = 0; h2 < 2; h2++) {
-            const f32x4 a = w4[h2], b = w5[h2], c = w6[h2], d = w7[h2];
-            qwl[4 * h2] = a.x; qwl[4 * h2 + 1] = a.y; qwl[4 * h2 + 2] = a.z; qwl[4 * h2 + 3] = a.w;
-            qwh[4 * h2] = b.x; qwh[4 * h2 + 1] = b.y; qwh[4 * h2 + 2] = b.z; qwh[4 * h2 + 3] = b.w;
-            kwl[4 * h2] = c.x; kwl[4 * h2 + 1] = c.y; kwl[4 * h2 + 2] = c.z; kwl[4 * h2 + 3] = c.w;
-            kwh[4 * h2] = d.x; kwh[4 * h2 + 1] = d.y; kwh[4 * h2 + 2] = d.z; kwh[4 * h2 + 3] = d.w;
-        }
-    }
-    // The loads above need neither the position nor the page entries (both
-    // scalar loads in flight meanwhile); a chunk past the sequence ends here.
-    asm volatile("" ::: "memory");
-    if (t0 >= seq) return;  // uniform over the workgroup
-    const uint32_t nt = seq > tw0 ? min(seq - tw0, wtok) : 0u;
-    if (FUSED) {
-        const f32x4 *cs = (const f32x4 *)(p.rope_cs + ((size_t)posv * 64 + sub * 8) * 2);
-#pragma unroll
-        for (int e2 = 0; e2 < 4; e2++) {
-            const f32x4 t = cs[e2];
-            co[2 * e2] = t.x; sn[2 * e2] = t.y; co[2 * e2 + 1] = t.z; sn[2 * e2 + 1] = t.w;
-        }
-    }
-    // Memory returns in issue order: keep the compiler from interleaving or
-    // sinking the groups (q / new token / RoPE first, then K, then V), so the
-    // q preparation (after the K and V loads are issued) waits only for its
-    // own loads.
-    asm volatile("" ::: "memory");
-    __shared__ float ps[AD_W][G][TW];
-    __shared__ float wm[AD_W][G], wl[AD_W][G];
-    __shared__ float wo[AD_W][4][G][FD_HD];  // per wave and token row
-    const uint32_t vrow = lane >> 4, vcol = lane & 15;
-    const uint32_t ptok = p.cache_tokens / 16;
-    // online softmax state of this wave over its sub-chunks (per q head):
-    // running maximum, sum of exp and P*V (lane = token row vrow, dims 8 vcol..)
-    float m_run[G], l_run[G], acc[G][8];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        m_run[g] = -INFINITY;
-        l_run[g] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
-    }
-    // K/V rows of this wave's tokens in sub-chunk i (sub-chunk 0: the page
-    // entries computed above; later sub-chunks exist only with the identity
-    // page table): up to three 16-token pages, each a contiguous 4 KB run, so
-    // every row is an offset from a page base that is uniform per 8-token
-    // pass. Rows past the end of the sequence are read (in-bounds) and masked.
-    // V: lane = (vrow = lane / 16, vcol = lane % 16) holds dims 8 vcol ..
-    // 8 vcol + 7 of the wave's tokens vrow, vrow + 4, .., 36 + vrow: 16-byte
-    // loads, one instruction covering 4 tokens x 256 B (4 tokens from a
-    // 4-aligned offset never straddle a 16-token page). Sub-chunk i + 1's K
-    // loads go out once sub-chunk i's scores are computed, its V loads once
-    // sub-chunk i's P*V is done, in the same registers.
-    u32x4 kr[TW / 8][2];
-    u32x4 vr[TW / 4];
-    auto pages_of = [&](uint32_t i, uint32_t &pg0, uint32_t &pg1, uint32_t &pg2, uint32_t &pgbs)
-        __attribute__((always_inline)) {
-        pg0 = page0; pg1 = page1; pg2 = page2; pgbs = pgb;
-        if (i) {
-            pgbs = (tw0 + i * TC) / 16;
-            pg0 = pgbs; pg1 = pgbs + 1; pg2 = pgbs + 2;
-        }
-    };
-    auto load_k = [&](uint32_t i) __attribute__((always_inline)) {
-        uint32_t g0, g1, g2, gb;
-        pages_of(i, g0, g1, g2, gb);
-        const size_t pa = g0 < ptok ? g0 : 0u, pb = g1 < ptok ? g1 : 0u, pc = g2 < ptok ? g2 : 0u;
-#pragma unroll
-        for (int j = 0; j < TW / 8; j++) {
-            // o16 + 8j is 8-aligned: the pass stays in one page
-            const uint16_t *kp = kv_row(kh, pa, pb, pc, o16 + 8 * j) + grp * FD_HD;
-            kr[j][0] = *(const u32x4 *)(kp + sub * 8);
-            kr[j][1] = *(const u32x4 *)(kp + 64 + sub * 8);
-        }
-    };
-    auto load_v = [&](uint32_t i) __attribute__((always_inline)) {
-        uint32_t g0, g1, g2, gb;
-        pages_of(i, g0, g1, g2, gb);
-        const size_t pa = g0 < ptok ? g0 : 0u, pb = g1 < ptok ? g1 : 0u, pc = g2 < ptok ? g2 : 0u;
-#pragma unroll
-        for (int k = 0; k < TW / 4; k++)
-            vr[k] = *(const u32x4 *)(kv_row(vh, pa, pb, pc, o16 + 4 * k + vrow) + 8 * vcol);
-    };
-    load_k(0);
-    asm volatile("" ::: "memory");
-    load_v(0);
-    asm volatile("" ::: "memory");
-    // ---- q preparation (once per workgroup), while K and V are in flight
-    if (FUSED) {
-#pragma unroll
-        for (int g = 0; g < G; g++) norm_rope16(qlo[g], qhi[g], qwl, qwh, co, sn, p.eps);
-    }
+}
 
-    // ---- the new token: its position lies in exactly one wave's range of
-    // one sub-chunk (s_own); that wave writes it to the cache here, once, and
-    // its scores and P*V select these values for it instead of the cache rows
-    // loaded for that position (which predate the write)
-    uint32_t s_own = ~0u, inew = 0;  // uniform per wave
-    u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0}, vnew4 = {0, 0, 0, 0};
-    if (FUSED && posv >= tw0) {
-        const uint32_t rel = posv - tw0;
-        if (rel % TC < wtok && rel / TC < nsub) {
-            s_own = rel / TC;
-            inew = rel % TC;
-            norm_rope16(klo, khi, kwl, kwh, co, sn, p.eps);
-            n0 = u32x4{pack_h2(klo[0], klo[1]), pack_h2(klo[2], klo[3]), pack_h2(klo[4], klo[5]),
-                       pack_h2(klo[6], klo[7])};
-            n1 = u32x4{pack_h2(khi[0], khi[1]), pack_h2(khi[2], khi[3]), pack_h2(khi[4], khi[5]),
-                       pack_h2(khi[6], khi[7])};
-            const uint32_t vnew = pack_h2(vn0, vn1);
-            vnew4 = u32x4{pack_h2(vn8[0], vn8[1]), pack_h2(vn8[2], vn8[3]), pack_h2(vn8[4], vn8[5]),
-                          pack_h2(vn8[6], vn8[7])};
-            // logicalTokenToPhysicalToken for the new position, from the page
-            // entries of its sub-chunk (the position lies in page pgbs + 0..2);
-            // the host has checked the context length, an unmapped slot is
-            // skipped
-            uint32_t pg0, pg1, pg2, pgbs;
-            pages_of(s_own, pg0, pg1, pg2, pgbs);
-            const uint32_t slot = posv / 16, pi = slot - pgbs;
-            const uint32_t pg = pi == 0 ? pg0 : pi == 1 ? pg1 : pg2;
-            const uint32_t ph = slot < p.n_pages ? pg * 16 + posv % 16 : p.cache_tokens;
-            if (ph < p.cache_tokens) {
-                if (grp == (inew & 7)) {
-                    *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + sub * 8) = n0;
-                    *(u32x4 *)(p.kc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 64 + sub * 8) = n1;
-                }
-                *(uint32_t *)(p.vc + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + 2 * lane) = vnew;
-            }
-        }
-    }
-    TRACE_OPS(1);
 
-    // One sub-chunk. PF: the next sub-chunk's K loads go out once this one's
-    // scores are computed, its V loads once this one's P*V is done. The loads
-    // are unconditional inside the loop (the last sub-chunk is peeled off), so
-    // the compiler's waits count exactly the loads in flight: the scores wait
-    // for this sub-chunk's K only, P*V for its V only.
-    auto body = [&](uint32_t sc_i, auto pf) __attribute__((always_inline)) {
-        constexpr bool PF = decltype(pf)::value;
-        const uint32_t tws = tw0 + sc_i * TC;
-        const uint32_t nts = seq > tws ? min(seq - tws, wtok) : 0u;
-        const bool owner = sc_i == s_own;  // uniform per wave
-
-        // ---- scores: token 8j + grp, 16 dims per lane, reduced over 8 lanes
-        float sc[TW / 8][G];
-#pragma unroll
-        for (int j = 0; j < TW / 8; j++) {
-            const bool sel = owner && (uint32_t)(8 * j) + grp == inew;
-            const u32x4 k0 = sel ? n0 : kr[j][0], k1 = sel ? n1 : kr[j][1];
-            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-            float kf[16];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                kf[2 * e] = h2f(kw[e]);
-                kf[2 * e + 1] = h2f(kw[e] >> 16);
-            }
-            const bool valid = (uint32_t)(8 * j) + grp < nts;
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                float sacc = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    sacc = fmaf(qlo[g][e], kf[e], sacc);
-                    sacc = fmaf(qhi[g][e], kf[8 + e], sacc);
-                }
-                sacc = sum8(sacc) * p.scale;  // dot * scale, as cpuAttention
-                sc[j][g] = valid ? sacc : -INFINITY;
-            }
-        }
-        if (sc_i == 0) TRACE_OPS(2);
-        if (PF) {
-            asm volatile("" ::: "memory");
-            load_k(sc_i + 1);
-            asm volatile("" ::: "memory");
-        }
-        // ---- online softmax: new running maximum, rescale the old state
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float m = sc[0][g];
-#pragma unroll
-            for (int j = 1; j < TW / 8; j++) m = fmaxf(m, sc[j][g]);
-            m = rows_max(fmaxf(m, dpp_f<0x140>(m)));  // m is uniform within each 8-lane token group
-            const float mn = fmaxf(m_run[g], m);
-            const float ms = mn == -INFINITY ? 0.f : mn;  // no valid token yet
-            const float f = m_run[g] == -INFINITY ? 0.f : expf(m_run[g] - ms);
-            float l = 0.f;
-#pragma unroll
-            for (int j = 0; j < TW / 8; j++) {
-                const float pr = expf(sc[j][g] - ms);
-                if (sub == 0) ps[wave][g][8 * j + grp] = pr;
-                l += pr;
-            }
-            l = rows_sum(l + dpp_f<0x140>(l));
-            l_run[g] = fmaf(l_run[g], f, l);
-            m_run[g] = mn;
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] *= f;
-        }
-        __syncthreads();
-        if (sc_i == 0) TRACE_OPS(8);
-#pragma unroll
-        for (int k = 0; k < TW / 4; k++) {
-            const uint32_t i = 4 * k + vrow;
-            u32x4 v = owner && i == inew ? vnew4 : vr[k];
-            if (i >= nts) v = u32x4{0, 0, 0, 0};  // rows past the end may hold anything
-            const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-            float vf[8];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                vf[2 * e] = h2f(vw[e]);
-                vf[2 * e + 1] = h2f(vw[e] >> 16);
-            }
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float q = ps[wave][g][i];
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc[g][e] = fmaf(q, vf[e], acc[g][e]);
-            }
-        }
-        if (PF) {
-            asm volatile("" ::: "memory");
-            load_v(sc_i + 1);
-            asm volatile("" ::: "memory");
-        }
-        __syncthreads();  // ps is rewritten by the next sub-chunk
-    };
-    if (SUB) {
-        for (uint32_t sc_i = 0; sc_i + 1 < nsub; sc_i++) body(sc_i, std::true_type{});  // uniform
+// Several sequences in one launch (batched decode): blockIdx.z selects the
+// sequence, whose buffers replace those of p0 (the weights, RoPE table and
+// geometry are shared; the sequences are at the same position).
+constexpr int AD_MAXZ = 4;
+struct AttnZ {
+    const float *q[AD_MAXZ], *k_new[AD_MAXZ], *v_new[AD_MAXZ];
+    uint16_t *kc[AD_MAXZ], *vc[AD_MAXZ];
+    const uint32_t *pos[AD_MAXZ];
+    float *part[AD_MAXZ], *out[AD_MAXZ];
+    uint32_t *counters[AD_MAXZ];
+    uint8_t *xq[AD_MAXZ];
+};
+template <int G, int TW>
+__global__ __launch_bounds__(AD_T, 1) void k_attn_decode_z(AttnP p0, AttnZ z) {
+    constexpr bool FUSED = true;
+    constexpr int MODE = AD_IDENT;
+    AttnP p = p0;
+    {
+        const uint32_t s = blockIdx.z;
+        p.q = z.q[s]; p.k_new = z.k_new[s]; p.v_new = z.v_new[s];
+        p.kc = z.kc[s]; p.vc = z.vc[s]; p.pos.dev = z.pos[s];
+        p.part = z.part[s]; p.out = z.out[s]; p.counters = z.counters[s]; p.xq = z.xq[s];
     }
-    body(nsub - 1, std::false_type{});
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        if (lane == 0) { wm[wave][g] = m_run[g]; wl[wave][g] = l_run[g]; }
-        *(f32x4 *)&wo[wave][vrow][g][8 * vcol] = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
-        *(f32x4 *)&wo[wave][vrow][g][8 * vcol + 4] = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
-    }
-    __syncthreads();
-    TRACE_OPS(9);
-    // ---- combine the 4 waves: per-head weights once, then thread -> (head, dim)
-    __shared__ float cf[AD_W][G], cM[G], cL[G];
-    if (tid < (uint32_t)G) {
-        const uint32_t g = tid;
-        float M = wm[0][g];
-#pragma unroll
-        for (int w = 1; w < AD_W; w++) M = fmaxf(M, wm[w][g]);
-        const float Ms = M == -INFINITY ? 0.f : M;
-        float L = 0.f;
-#pragma unroll
-        for (int w = 0; w < AD_W; w++) {
-            const float f = wm[w][g] == -INFINITY ? 0.f : expf(wm[w][g] - Ms);
-            cf[w][g] = f;
-            L = fmaf(wl[w][g], f, L);
-        }
-        cM[g] = M;
-        cL[g] = L;
-    }
-    __syncthreads();
-    TRACE_OPS(10);
-    for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += AD_T) {
-        const uint32_t g = o / FD_HD, d = o % FD_HD;
-        float O = 0.f;
-#pragma unroll
-        for (int w = 0; w < AD_W; w++)
-            O = fmaf((wo[w][0][g][d] + wo[w][1][g][d]) + (wo[w][2][g][d] + wo[w][3][g][d]), cf[w][g], O);
-        float *pp = p.part + ((size_t)(kvh * G + g) * p.n_chunks + chunk) * (FD_HD + 2);
-        st_dev(pp + d, O);
-        if (d == 0) { st_dev(pp + FD_HD, cM[g]); st_dev(pp + FD_HD + 1, cL[g]); }
-    }
-    TRACE_OPS(3);
-    // ---- the last arrivals of this kv head merge the chunks
-    const uint32_t nv = (seq + CT - 1) / CT;
-    __shared__ uint32_t s_prev;
-    // The partials went out as device-scope stores, coherent across the
-    // XCDs' L2s. Waiting for them to complete (s_waitcnt 0 in every wave,
-    // then the barrier) before a relaxed device-scope counter increment
-    // publishes them without the full L2 write-back / invalidate that
-    // agent-scope release / acquire fences imply; the readers use
-    // device-scope loads.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) s_prev = __hip_atomic_fetch_add(p.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    TRACE_OPS(4);
-    const uint32_t prev = s_prev;
-    // With at least G chunks the last G arrivals merge one q head each (a
-    // merger reads 1/G of the partials); otherwise the last arrival merges all.
-    // (no_wait: other kernels share the device, so the earlier mergers'
-    // bounded wait could wait on chunks that are not resident.)
-    const bool split = G > 1 && nv >= (uint32_t)G && !p.no_wait;
-    const uint32_t nm = split ? (uint32_t)G : 1u;
-    if (prev + nm < nv) return;
-    const uint32_t slot = prev + nm - nv;  // nm - 1: the last arrival
-    if (!split) {
-        attn_merge<G, G <= 4 ? 40 : 12>(p, kvh * G, nv, false);
-        if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
-    // earlier mergers wait until every chunk has arrived; the wait is bounded
-    // (50 ms) and a timeout poisons this head's output instead of hanging
-    __shared__ uint32_t s_ok;
-    if (tid == 0) {
-        uint32_t ok = 1;
-        if (slot != nm - 1) {
-            const uint64_t t_0 = __builtin_amdgcn_s_memrealtime();
-            while (__hip_atomic_load(p.counters + kvh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nv) {
-                if (__builtin_amdgcn_s_memrealtime() - t_0 > 5000000ull) { ok = 0; break; }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-        s_ok = ok;
-        // counters[nkv + kvh] counts mergers past the wait; the last one
-        // clears both words for the next launch (no one reads them after)
-        uint32_t *done = p.counters + gridDim.x + kvh;
-        if (__hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nm - 1) {
-            __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    __syncthreads();
-    if (nv <= 32) attn_merge<1, 32>(p, kvh * G + slot, nv, !s_ok);
-    else attn_merge<1, 64>(p, kvh * G + slot, nv, !s_ok);
+#include "zh_attn_body.inc"
 }
 
 // partials: zhk_flash_decode_partials_bytes(nh, nkv, hd, max_seq) bytes; the
@@ -920,6 +558,46 @@ int zhk_attn_decode_fused(zh_ctx *c, const float *q, const float *k, const float
     p.scale = scale; p.eps = eps; p.part = partials; p.counters = attn_counters(partials, nh, nkv, FD_HD, max_seq);
     p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
     return attn_launch(c, p, nkv, nh / nkv, max_seq, true, ident_pages);
+}
+
+// zhk_attn_decode_fused for n <= 4 sequences at one position in one launch
+// (grid z = sequence), identity pages, the no-wait merge. Array arguments hold
+// one entry per sequence; the weights, RoPE table and page table are shared.
+int zhk_attn_decode_fused_z(zh_ctx *c, uint32_t n, const float *const *q, const float *const *k,
+                            const float *const *v, const float *qw, const float *kw, const float *rope_cs,
+                            uint16_t *const *kc, uint16_t *const *vc, const uint32_t *pages, uint32_t n_pages,
+                            uint32_t cache_tokens, float *const *out, void *const *xq_out, uint32_t nh, uint32_t nkv,
+                            const uint32_t *const *pos_dev, uint32_t max_seq, float scale, float eps,
+                            float *const *partials) {
+    const uint32_t G = nkv ? nh / nkv : 0;
+    if (n == 0 || n > (uint32_t)AD_MAXZ || G == 0 || G > 4 || (G & (G - 1)))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "batched attention: %u sequences, group %u", n, G);
+    AttnP p = {};
+    p.q_norm = qw; p.k_norm = kw; p.rope_cs = rope_cs; p.pages = pages; p.n_pages = n_pages;
+    p.cache_tokens = cache_tokens; p.pos = zh_pos_src{0, pos_dev[0]}; p.scale = scale; p.eps = eps; p.nq = nh;
+    p.nd = attn_nd(nkv, c->cu_count);
+    p.no_wait = 1;  // chunks of other sequences share the device: no merger waits
+    const uint32_t tw = max_seq <= 8192 ? 24u : 32u;
+    p.n_chunks = attn_n_chunks(max_seq, p.nd, AD_W * tw);
+    if (p.n_chunks > p.nd) p.n_chunks = p.nd;
+    AttnZ z = {};
+    for (uint32_t s = 0; s < n; s++) {
+        z.q[s] = q[s]; z.k_new[s] = k[s]; z.v_new[s] = v[s]; z.kc[s] = kc[s]; z.vc[s] = vc[s];
+        z.pos[s] = pos_dev[s]; z.part[s] = partials[s]; z.out[s] = out[s]; z.xq[s] = (uint8_t *)xq_out[s];
+        z.counters[s] = attn_counters(partials[s], nh, nkv, FD_HD, max_seq);
+    }
+    dim3 grid(nkv, p.n_chunks, n);
+#define AZ(GG)                                                                                                   \
+    if (tw == 24) hipLaunchKernelGGL((k_attn_decode_z<GG, 24>), grid, dim3(AD_T), 0, c->stream, p, z);           \
+    else hipLaunchKernelGGL((k_attn_decode_z<GG, 32>), grid, dim3(AD_T), 0, c->stream, p, z)
+    switch (G) {
+    case 1: AZ(1); break;
+    case 2: AZ(2); break;
+    default: AZ(4); break;
+    }
+#undef AZ
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
 }
 
 extern "C" int zh_flash_decode(zh_ctx *c, const zh_buf *q, const zh_buf *kc, const zh_buf *vc, const zh_buf *pages,
