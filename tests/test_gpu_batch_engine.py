@@ -51,6 +51,13 @@ def test_batch_matches_single_sequences(ctx, n_seq):
         ref = solo_logits[v]
         assert np.allclose(lg, ref, rtol=1e-3, atol=1e-4 + 1e-3 * np.abs(ref).max()), (v, np.abs(lg - ref).max())
     assert len({tuple(t) for t in got}) == n_seq  # the sequences really differ
+    # a second batched run of the same engine set, after other work on the
+    # same stream (a single-sequence decode), repeats the first
+    base.prefill_kv_random(prefill, 100)
+    assert base.generate(prompts[0].tolist(), steps, start_pos=prefill) == solo[0]
+    for v, e in enumerate(engines):
+        e.prefill_kv_random(prefill, 100 + v)
+    assert zinc_amd.InferenceEngine.generate_batch(engines, prompts, steps, start_pos=prefill) == got
     for e in engines[1:]:
         e.deinit()
     base.deinit()
