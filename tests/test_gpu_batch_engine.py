@@ -28,7 +28,7 @@ def ctx():
     c.close()
 
 
-@pytest.mark.parametrize("n_seq", [3, 4])
+@pytest.mark.parametrize("n_seq", [3, 4, 6])
 def test_batch_matches_single_sequences(ctx, n_seq):
     import zinc_amd
     print(f"batch engine n_seq={n_seq}", flush=True)
