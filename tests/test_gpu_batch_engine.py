@@ -75,3 +75,39 @@ def test_batch_rejects_foreign_engines(ctx):
     assert e.value.name == "InvalidArgument"
     a.deinit()
     b.deinit()
+
+
+def test_batch_groups_on_two_streams(ctx):
+    """Two batches of 2 sequences, each on its own context (HIP stream) and
+    host thread, decode at once; every sequence as it decodes alone."""
+    import threading
+    import zinc_amd
+    ctx2 = zinc_amd.Context(0)
+    cfg = dict(CFG, n_layers=2)
+    base = zinc_amd.InferenceEngine(ctx, cfg)
+    groups = [[base, base.share(ctx)], [base.share(ctx2), base.share(ctx2)]]
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, cfg["vocab"], (2, 3)).astype(np.uint32) for _ in range(2)]
+    prefill, steps = 30, 10
+    solo = []
+    for g in range(2):
+        for v, e in enumerate(groups[g]):
+            e.prefill_kv_random(prefill, 200 + 2 * g + v)
+            solo.append(e.generate(prompts[g][v].tolist(), steps, start_pos=prefill))
+            e.prefill_kv_random(prefill, 200 + 2 * g + v)
+    ctx.sync()
+    ctx2.sync()
+    got = [None, None]
+
+    def run(g):
+        got[g] = zinc_amd.InferenceEngine.generate_batch(groups[g], prompts[g], steps, start_pos=prefill)
+    th = [threading.Thread(target=run, args=(g,)) for g in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert got[0] + got[1] == solo
+    for e in groups[1] + groups[0][1:]:
+        e.deinit()
+    base.deinit()
+    ctx2.close()
