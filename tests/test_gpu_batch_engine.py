@@ -75,6 +75,14 @@ def test_batch_rejects_foreign_engines(ctx):
     assert e.value.name == "InvalidArgument"
     a.deinit()
     b.deinit()
+    # Q8_0 attention: no tile kernel for the batched projections
+    q8 = zinc_amd.InferenceEngine(ctx, dict(CFG, n_layers=2, type_attn=8))
+    q8b = q8.share(ctx)
+    with pytest.raises(zinc_amd.ZincError) as e:
+        zinc_amd.InferenceEngine.generate_batch([q8, q8b], [[1, 2], [3, 4]], 2, start_pos=0)
+    assert e.value.name == "UnsupportedQuantType"
+    q8b.deinit()
+    q8.deinit()
 
 
 def test_batch_groups_on_two_streams(ctx):
