@@ -34,7 +34,7 @@ GROUP_ORDER = ["qkv", "attn", "o", "ffn_in", "ffn_out"]
 PMC_ITERS = 36
 KERNELS = {  # the dense 8B step's kernel per group
     "qkv": "k_dmmv_q4k_tile<16, 0> (attn_norm + Q/K/V, Q4_K 6144x4096)",
-    "attn": "k_attn_decode<4, true, 2> (q/k norm + RoPE + KV write + split-K attention + merge)",
+    "attn": "k_attn_decode<4, true, 2, 24> (q/k norm + RoPE + KV write + split-K attention + merge)",
     "o": "k_dmmv_q4k_tile<16, 0> (O projection + residual, Q4_K 4096x4096, XQ input)",
     "ffn_in": "k_dmmv_q4k_tile<16, 1> (ffn_norm + gate/up + SwiGLU, 2 x Q4_K 12288x4096, XQ output)",
     "ffn_out": "k_dmmv_q6k_tile<128, 5> (ffn_down + residual, Q6_K 4096x12288, XQ input)",
