@@ -29,12 +29,12 @@ def log(*a):
 
 def kernel_roofline(eng, L):
     """Per-kernel bandwidth of every per-layer launch group of the decode step
-    (zinc_amd.roofline_probe: the engine replays its own launches with HIP
+    (benchmarks.roofline_probe: the engine replays its own launches with HIP
     events on its stream, rotating through the layers) and the roofline of the
     dominant one (largest launch duration = largest share of step time).
     `traffic` is the counter-measured HBM bytes per launch of that group from
     profiles/decode_kernels_pmc.md."""
-    from zinc_amd import roofline_probe
+    from benchmarks import roofline_probe
     rows, dom = roofline_probe.per_kernel(eng, L)
     r = rows[dom]
     traffic = None

@@ -3,7 +3,7 @@ weights stepping in lockstep (zh_engine_generate_batch), each with its own KV
 cache pre-filled to 4096 positions (seeded N(0,1) fp16), greedy-decoding from
 a one-token prompt, so every timed step is a decode step of all B sequences.
 
-    python -m zinc_amd.batch_bench [--seqs 1 2 4] [--steps 64] [--streams S]
+    python -m benchmarks.batch_bench [--seqs 1 2 4] [--steps 64] [--streams S]
 
 Prints one JSON line per B: aggregate tok/s (B x steps / wall time) and the
 milliseconds per batched step. The projections and the LM head stream their
@@ -21,8 +21,8 @@ import time
 
 import numpy as np
 
-from . import hip
-from .engine import DENSE_8B, InferenceEngine
+from zinc_amd import hip
+from zinc_amd.engine import DENSE_8B, InferenceEngine
 
 PREFILL = 4096
 

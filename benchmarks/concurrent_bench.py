@@ -3,7 +3,7 @@ of the weights, each on its own context (HIP stream) and host thread, each
 greedy-decoding its own sequence at KV context 4096+ (seeded N(0,1) fp16 KV
 prefill, 16-token random prompt), all at once.
 
-    python -m zinc_amd.concurrent_bench [--seqs 1 2 4] [--steps 128]
+    python -m benchmarks.concurrent_bench [--seqs 1 2 4] [--steps 128]
 
 Prints one JSON line per B: aggregate tok/s (B x steps / wall time of the
 concurrent run) and per-sequence tok/s. The kernels are the single-sequence
@@ -18,8 +18,8 @@ import time
 
 import numpy as np
 
-from . import hip
-from .engine import DENSE_8B, InferenceEngine
+from zinc_amd import hip
+from zinc_amd.engine import DENSE_8B, InferenceEngine
 
 PREFILL = 4096
 N_PROMPT = 16

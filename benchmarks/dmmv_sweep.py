@@ -3,7 +3,7 @@ HIP events on the library stream over a rotating set of weight copies larger
 than the 256 MB MALL (so every launch streams its weights from HBM), as the
 reference's bench_hot_decode rotates a 16-slot working set.
 
-    python -m zinc_amd.dmmv_sweep [--iters 60] [--md OUT.md]
+    python -m benchmarks.dmmv_sweep [--iters 60] [--md OUT.md]
 
 Per shape: zh_dmmv (f32 activation, the C-ABI entry that replaces
 DmmvDispatch.recordDispatch, dmmv.zig:806-874) and zh_dmmv_xq (the
@@ -12,7 +12,7 @@ an input). Algorithmic bytes = weight blocks + 4 K (x) + 4 M (y), the
 per-kernel figure of the bandwidth roofline; fraction of the 8 TB/s peak.
 A streaming read of 1 GiB gives the measured ceiling beside it.
 
-    python -m zinc_amd.dmmv_sweep --batched [--md OUT.md]
+    python -m benchmarks.dmmv_sweep --batched [--md OUT.md]
 
 instead times the batched DMMV (zh_dmmv_batched / the gate/up form, the
 skinny GEMM of recordBatchDispatchPush, dmmv.zig:880-925) on the config-3
@@ -24,7 +24,7 @@ import argparse
 import json
 import sys
 
-from . import hip
+from zinc_amd import hip
 
 PEAK = 8000.0  # GB/s
 ROTATE_BYTES = 600 << 20

@@ -4,7 +4,7 @@ router/attention Q8_0, lm-head Q6_K), batch 1, KV context pre-filled to 8192
 positions with N(0,1) fp16, then greedy decode of 256 tokens from a 16-token
 random-id prompt, seeded random-init weights.
 
-    python -m zinc_amd.moe_bench [--steps 256] [--warmup 16]
+    python -m benchmarks.moe_bench [--steps 256] [--warmup 16]
 
 Prints one JSON line: decode tok/s, the engine's bytes-per-token model
 (dmmvMetrics + flashAttnMetrics with fp16 KV and the 8 selected experts) and
@@ -19,8 +19,8 @@ import time
 
 import numpy as np
 
-from . import hip
-from .engine import MOE_48L, InferenceEngine
+from zinc_amd import hip
+from zinc_amd.engine import MOE_48L, InferenceEngine
 
 PEAK = 8000.0
 PREFILL = 8192

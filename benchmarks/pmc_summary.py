@@ -1,4 +1,4 @@
-"""Turns two rocprofv3 counter runs of `python3 -m zinc_amd.roofline_probe --pmc`
+"""Turns two rocprofv3 counter runs of `python3 -m benchmarks.roofline_probe --pmc`
 (FETCH_SIZE, then WRITE_SIZE; CSV output) into the per-launch HBM traffic of
 every launch group of the decode step, calibrated against kernels of known
 size in the same run:
@@ -8,7 +8,7 @@ size in the same run:
                    (its dispatches right after the reads) / their WRITE_SIZE (KiB)
     traffic      = FETCH_SIZE(kernel) * FETCH factor + WRITE_SIZE(kernel) * WRITE factor
 
-    python -m zinc_amd.pmc_summary FETCH_DIR WRITE_DIR PROBE_JSON OUT.md
+    python -m benchmarks.pmc_summary FETCH_DIR WRITE_DIR PROBE_JSON OUT.md
 
 PROBE_JSON is the probe's stdout (the groups, launches per group and each
 group's algorithmic bytes). After the calibration write, the dispatches come
@@ -76,14 +76,14 @@ def main():
     probe = json.loads(open(sys.argv[3]).read().strip().splitlines()[-1])
     s = summarize(sys.argv[1], sys.argv[2], probe)
     cmd = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && timeout -s KILL 120 rocprofv3 --pmc {c} "
-           "-d gpurun_out/pmc_{d} -o run --output-format csv -- python3 -m zinc_amd.roofline_probe --pmc "
+           "-d gpurun_out/pmc_{d} -o run --output-format csv -- python3 -m benchmarks.roofline_probe --pmc "
            "> gpurun_out/pmc_{d}.json")
     with open(sys.argv[4], "w") as f:
         f.write("# HBM traffic per launch of the 8B decode step's kernels (config 3)\n\n")
         f.write("Commands (one counter per run, from the repository root):\n\n")
         f.write("    " + cmd.format(c="FETCH_SIZE", d="fetch") + "\n")
         f.write("    " + cmd.format(c="WRITE_SIZE", d="write") + "\n")
-        f.write("    python -m zinc_amd.pmc_summary gpurun_out/pmc_fetch gpurun_out/pmc_write "
+        f.write("    python -m benchmarks.pmc_summary gpurun_out/pmc_fetch gpurun_out/pmc_write "
                 "gpurun_out/pmc_fetch.json <this file>\n\n")
         f.write("Calibration (kernels of known size in the same run):\n\n")
         f.write(f"- k_stream_read of {probe['cal_bytes']} B: FETCH_SIZE factor {s['fetch_factor']:.4f} "

@@ -2,7 +2,7 @@
 dense model (MFMA dequant-GEMM, fp16 operands, f32 accumulation), then greedy
 decode over a 32768-position fp16 KV cache.
 
-    python -m zinc_amd.prefill_bench [--prefill 512] [--long-ctx 32768] [--steps 128]
+    python -m benchmarks.prefill_bench [--prefill 512] [--long-ctx 32768] [--steps 128]
 
 Prints one JSON line. GEMM FLOPs per prefill = 2 * N * sum(M * K) over the
 36 layers' Q, K, V, O, gate, up, down projections (7.11 TFLOP
@@ -15,8 +15,8 @@ import time
 
 import numpy as np
 
-from . import hip
-from .engine import DENSE_8B, InferenceEngine
+from zinc_amd import hip
+from zinc_amd.engine import DENSE_8B, InferenceEngine
 
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 

@@ -12,20 +12,20 @@ launch duration by HIP events on the engine's stream. The dominant kernel is
 the group with the largest duration (each runs once per layer, so also the
 largest share of step time).
 
-    python -m zinc_amd.roofline_probe            # per-kernel table (JSON)
-    rocprofv3 --pmc FETCH_SIZE -- python3 -m zinc_amd.roofline_probe --pmc
+    python -m benchmarks.roofline_probe            # per-kernel table (JSON)
+    rocprofv3 --pmc FETCH_SIZE -- python3 -m benchmarks.roofline_probe --pmc
 
 With --pmc the script launches, in order: a streaming read of CAL_BYTES
 (known size), a write of CAL_BYTES (known size), then for each group in
 GROUP_ORDER one warm pass over the layers and PMC_ITERS timed launches;
-zinc_amd.pmc_summary turns the counters into bytes per launch.
+benchmarks.pmc_summary turns the counters into bytes per launch.
 """
 import argparse
 import json
 import sys
 
-from . import hip
-from .engine import DENSE_8B, InferenceEngine
+from zinc_amd import hip
+from zinc_amd.engine import DENSE_8B, InferenceEngine
 
 PEAK = 8000.0
 CAL_BYTES = 1 << 30      # calibration read / write size

@@ -72,16 +72,10 @@ int      zh_buf_fill_u8(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint8_t v, ui
 int zh_event_record(zh_ctx *ctx, int slot);          /* slot 0..63 */
 int zh_event_elapsed_ms(zh_ctx *ctx, int a, int b, float *ms);
 
-/* ---- calibration probes (counterparts of the reference's microbenchmarks
- *      benchmarks/dispatch_overhead.c and benchmarks/bandwidth.zig) ------ */
+/* ---- calibration probe (counterpart of the reference's microbenchmark
+ *      benchmarks/bandwidth.zig) ---------------------------------------- */
 /* Streaming 128-bit reads over the first `bytes` of buf, `iters` times: GB/s. */
 int zh_stream_read_probe(zh_ctx *ctx, const zh_buf *buf, uint64_t bytes, uint32_t iters, float *gbs);
-/* n_kernels empty launches of `wgs` workgroups, in a hipGraph (use_graph) or
- * as plain launches: average microseconds per kernel. */
-int zh_dispatch_overhead(zh_ctx *ctx, uint32_t n_kernels, uint32_t wgs, int use_graph, float *us_per_kernel);
-/* Cost of one device-wide barrier in a cooperative grid of wgs_per_cu
- * 256-thread workgroups per CU (bounded spin; fails rather than hangs). */
-int zh_grid_barrier_probe(zh_ctx *ctx, uint32_t n_barriers, uint32_t wgs_per_cu, float *us_per_barrier);
 
 /* ---- synthetic data (seeded, bit-identical to oracle/zinc_oracle.c) ----- */
 /* Fill rows x cols of `qtype` blocks at `offset` per the BASELINE distributions.

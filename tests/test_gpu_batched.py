@@ -2,10 +2,14 @@
 skinny GEMM of recordBatchDispatchPush, dmmv.zig:880-925) through the C ABI.
 
 Every column of a batched launch must equal the one-vector DMMV of that
-column bit for bit (the weight tile is shared, the per-column arithmetic is
-the one-vector kernel's), and so meet the oracle bar of the one-vector
-kernels: |gpu - ref| <= 1e-4 + 1e-3 |ref| (+ the f32 dot-product noise floor
-of test_gpu_kernels.assert_dot_close). Column counts cover the 4-, 2- and
+column bit for bit where the one-vector path runs the tile kernels (the
+weight tile is shared, the per-column arithmetic is the one-vector
+kernel's); Q4_K with K = 2048 / 4096 runs the streaming kernel one vector at
+a time, whose half-super-block partial sums round in another order, so there
+the columns agree to the f32 summation floor (2^-20 of sum |w x|). Every
+column meets the oracle bar of the one-vector kernels: |gpu - ref| <= 1e-4 +
+1e-3 |ref| (+ the f32 dot-product noise floor of
+test_gpu_kernels.assert_dot_close). Column counts cover the 4-, 2- and
 1-vector launches and their mixtures (3, 5 and 8 columns)."""
 import numpy as np
 import pytest
@@ -21,6 +25,17 @@ def ctx():
     c = zinc_amd.Context(0)
     yield c
     c.close()
+
+
+def _ring(qt, K):
+    """The one-vector path is the streaming kernel (zh_dmmv_ring.hip)."""
+    return qt == 12 and K in (2048, 4096)
+
+
+def _same(got, ref, mag, ring):
+    if not ring:
+        return np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    return bool(np.all(np.abs(got.astype(np.float64) - ref) <= 2.0 ** -20 * mag + 1e-30))
 
 
 def _single(ctx, qt, Wb, x, M, K, y0=None):
@@ -43,9 +58,11 @@ def test_batched_equals_single_columns(ctx, orc, qt, M, K, ncol):
     Wb, Xb, Yb = ctx.upload(W), ctx.upload(X), ctx.alloc(4 * M * ncol)
     ctx.dmmv_batched(qt, Wb, 0, Xb, 0, Yb, 0, M, K, ncol)
     Y = Yb.download(np.float32, M * ncol).reshape(ncol, M)
+    ring = _ring(qt, K)
+    mags = [orc.dmmv_absdot(W, qt, X[v], M, K) for v in range(ncol)] if ring else [None] * ncol
     for v in range(ncol):
         ref = _single(ctx, qt, Wb, X[v], M, K)
-        assert np.array_equal(Y[v].view(np.uint32), ref.view(np.uint32)), (v, np.abs(Y[v] - ref).max())
+        assert _same(Y[v], ref, mags[v], ring), (v, np.abs(Y[v] - ref).max())
     # and the oracle bar on the first and last columns
     for v in {0, ncol - 1}:
         assert_dot_close(Y[v], orc.dmmv(W, qt, X[v], M, K), orc.dmmv_f64(W, qt, X[v], M, K),
@@ -57,7 +74,7 @@ def test_batched_equals_single_columns(ctx, orc, qt, M, K, ncol):
     Y1 = Yb.download(np.float32, M * ncol).reshape(ncol, M)
     for v in range(ncol):
         ref = _single(ctx, qt, Wb, X[v], M, K, Y0[v])
-        assert np.array_equal(Y1[v].view(np.uint32), ref.view(np.uint32)), v
+        assert _same(Y1[v], ref, mags[v] + np.abs(Y0[v]) if ring else None, ring), v
     for b in (Wb, Xb, Yb):
         ctx.free(b)
 
@@ -91,7 +108,8 @@ def test_batched_gate_up_equals_single(ctx, orc, ncol):
         xb, yb = ctx.upload(X[v]), ctx.alloc(4 * M)
         ctx.dmmv_fused_gate_up_swiglu(qt, bg, 0, bu, 0, xb, 0, yb, 0, M, K)
         ref = yb.download(np.float32, M)
-        assert np.array_equal(Y[v].view(np.uint32), ref.view(np.uint32)), v
+        # the one-vector path at K = 4096 is the streaming kernel: f32 summation order differs
+        assert np.allclose(Y[v], ref, rtol=2e-5, atol=2e-6 * np.abs(ref).max()), (v, np.abs(Y[v] - ref).max())
         ctx.free(xb)
         ctx.free(yb)
     g = orc.dmmv(Wg, qt, X[0], M, K)

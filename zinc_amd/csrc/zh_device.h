@@ -19,6 +19,29 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define ZH_DEV static __device__ __forceinline__
 #define ZH_DEVM __device__ __forceinline__  // for static member functions
 
+// Debug build only (-DZH_DEBUG_TRACE): thread 0 of each of the first 8192
+// workgroups of a launch stores s_memrealtime (100 MHz) at numbered points
+// 0..15 of a kernel into this source file's g_zh_trace, read back with the
+// file's zh_debug_trace_<file> entry. The product build compiles the points
+// away.
+#ifdef ZH_DEBUG_TRACE
+static __device__ uint64_t g_zh_trace[8192 * 16];
+#define ZH_TRACE_POINT(slot)                                                                          \
+    do {                                                                                              \
+        const uint32_t bl_ = blockIdx.x + blockIdx.y * gridDim.x;                                     \
+        if (threadIdx.x == 0 && bl_ < 8192 && (slot) < 16) g_zh_trace[bl_ * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define ZH_TRACE_DUMP_FN(name)                                                                        \
+    extern "C" int name(uint64_t *host, uint32_t n) {                                                 \
+        static uint64_t zeros[8192 * 16];                                                             \
+        int rc = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_zh_trace), (size_t)n * 8, 0, hipMemcpyDeviceToHost); \
+        return rc | (int)hipMemcpyToSymbol(HIP_SYMBOL(g_zh_trace), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice); \
+    }
+#else
+#define ZH_TRACE_POINT(slot) do { } while (0)
+#define ZH_TRACE_DUMP_FN(name)
+#endif
+
 // ---------------------------------------------------------------------------
 // XQ activation format.
 // A vector of K floats (K % 32 == 0) is cut into K/32 blocks. Block j stores

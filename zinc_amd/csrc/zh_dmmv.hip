@@ -486,14 +486,7 @@ __global__ __launch_bounds__(NW == 1 ? 256 : NW * 64) void k_dmmv(DmmvP p) {
         for (int m = 0; m < NM; m++)
 #pragma unroll
             for (int r = 0; r < R; r++) {
-#ifdef ZH_EXP_NOCOMPUTE
-            uint32_t hx = 0;
-#pragma unroll
-            for (int q = 0; q < F::RAW; q++) hx ^= raw[m][r][q];
-            part[m * R + r] = active ? (float)(hx & 0xFF) : 0.f;
-#else
             part[m * R + r] = active ? F::compute(raw[m][r], xr, tlane) : 0.f;
-#endif
         }
         float res;
         int idx;
@@ -542,11 +535,7 @@ static int launch_one(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
     constexpr int BS = (NW == 1) ? 256 : NW * 64;
     uint32_t teams = (p.M + R - 1) / R;
     uint32_t wgs = (teams + TPW - 1) / TPW;
-    static int capm = -1;
-    if (capm < 0) {
-        const char *e = getenv("ZH_DMMV_CAP");
-        capm = e ? atoi(e) : 0;
-    }
+    const int capm = zh_knob_int("ZH_DMMV_CAP", 0);
     uint32_t cap = capm > 0 ? (uint32_t)c->cu_count * (uint32_t)capm
                             : (uint32_t)c->cu_count * (NW == 1 ? 8u : 16u / NW + 1u);
     if (MOE) cap = (cap + n_slots - 1) / n_slots;
@@ -573,11 +562,7 @@ static int launch_fmt_r(zh_ctx *c, const DmmvP &p, uint32_t n_slots) {
 }
 
 static int dmmv_rows_per_batch(int mode) {
-    static int env = -1;
-    if (env < 0) {
-        const char *e = getenv("ZH_DMMV_R");
-        env = e ? atoi(e) : 0;
-    }
+    const int env = zh_knob_int("ZH_DMMV_R", 0);
     if (env == 2 || env == 4) return env;
     return mode == MODE_GATE_UP ? 2 : 4;
 }
@@ -1019,7 +1004,7 @@ __global__ __launch_bounds__(256, 2) void k_dmmv_ftile(FtP p) {
 static int try_ftile(zh_ctx *c, uint32_t qtype, const uint8_t *W, const void *xq, const float *xf, float *y,
                      uint32_t M, uint32_t K, uint32_t acc) {
     static int off = -1;
-    if (off < 0) off = getenv("ZH_NO_FTILE") ? 1 : 0;
+    if (off < 0) off = zh_knob("ZH_NO_FTILE")? 1 : 0;
     // MXFP4 only: for Q8_0 the team kernel (x in registers, four rows per
     // team in flight) measured faster than 4-row tiles
     if (off || qtype != ZH_MXFP4 || ((uintptr_t)W & 15)) return -1;
@@ -1062,7 +1047,7 @@ extern "C" int zh_dmmv(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a_of
     if ((a_off & 3) || (x_off & 3) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "offsets must be 4-byte aligned");
     if (qtype == ZH_Q4_K && (a_off & 15)) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "Q4_K a_off must be 16-byte aligned");
-    if (zhk_lpb_supported(qtype, K) && (x_off & 15) == 0 && !getenv("ZH_NO_LPB")) {
+    if (zhk_lpb_supported(qtype, K) && (x_off & 15) == 0 && !zh_knob("ZH_NO_LPB")) {
         const uint8_t *w = (const uint8_t *)W->ptr + a_off;
         float *yy = (float *)((char *)y->ptr + y_off);
         int R = 2;
@@ -1104,7 +1089,7 @@ extern "C" int zh_dmmv_xq(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a
     if (!in_range(W, a_off, zh_tensor_bytes(qtype, M, K)) || !in_range(xq, xq_off, zh_xq_bytes_int(K)) ||
         !in_range(y, y_off, 4ull * M) || (a_off & (qtype == ZH_Q4_K ? 15 : 3)) || (xq_off & 15) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "range/alignment");
-    if (zhk_lpb_supported(qtype, K) && !getenv("ZH_NO_LPB")) {
+    if (zhk_lpb_supported(qtype, K) && !zh_knob("ZH_NO_LPB")) {
         const uint8_t *w = (const uint8_t *)W->ptr + a_off;
         float *yy = (float *)((char *)y->ptr + y_off);
         return zhk_dmmv_lpb(c, qtype, 0, 1, &w, nullptr, &yy, &M, nullptr, nullptr, 0.f, nullptr, K, acc_mode,
@@ -1124,7 +1109,7 @@ extern "C" int zh_dmmv_fused_gate_up_swiglu_xq(zh_ctx *c, uint32_t qtype, const 
     if (M == 0 || !in_range(Wg, g_off, wb) || !in_range(Wu, u_off, wb) || !in_range(xq, xq_off, zh_xq_bytes_int(K)) ||
         !in_range(y, y_off, 4ull * M) || (g_off & 15) || (u_off & 15) || (xq_off & 15) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "range/alignment");
-    if (qtype == ZH_Q4_K && zhk_lpb_supported(qtype, K) && !getenv("ZH_NO_LPB")) {
+    if (qtype == ZH_Q4_K && zhk_lpb_supported(qtype, K) && !zh_knob("ZH_NO_LPB")) {
         const uint8_t *wg = (const uint8_t *)Wg->ptr + g_off;
         float *yy = (float *)((char *)y->ptr + y_off);
         return zhk_dmmv_lpb(c, qtype, 1, 1, &wg, (const uint8_t *)Wu->ptr + u_off, &yy, &M, nullptr, nullptr, 0.f,
@@ -1146,7 +1131,7 @@ extern "C" int zh_dmmv_fused_gate_up_swiglu(zh_ctx *c, uint32_t qtype, const zh_
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "buffer too small for M=%u K=%u", M, K);
     if ((g_off & 15) || (u_off & 15) || (x_off & 3) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "misaligned offsets");
-    if (qtype == ZH_Q4_K && zhk_lpb_supported(qtype, K) && (x_off & 15) == 0 && !getenv("ZH_NO_LPB")) {
+    if (qtype == ZH_Q4_K && zhk_lpb_supported(qtype, K) && (x_off & 15) == 0 && !zh_knob("ZH_NO_LPB")) {
         const uint8_t *wg = (const uint8_t *)Wg->ptr + g_off;
         float *yy = (float *)((char *)y->ptr + y_off);
         return zhk_dmmv_lpb(c, qtype, 1, 1, &wg, (const uint8_t *)Wu->ptr + u_off, &yy, &M,

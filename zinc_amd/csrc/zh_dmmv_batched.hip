@@ -121,11 +121,6 @@ __global__ __launch_bounds__(LPB_T, NV == 2 ? 2 : 1) void k_dmmv_q4k_tile_nv(Lpb
         float accd[NV], accm[NV];
 #pragma unroll
         for (int v = 0; v < NV; v++) accd[v] = accm[v] = 0.f;
-#ifdef ZH_EXP_TILE
-        uint32_t xx = 0;
-        for (int i = 0; i < 36; i++) xx ^= raw[i];
-        accd[0] = (float)(xx & 1);
-#else
 #pragma unroll
         for (int pp = 0; pp < 4; pp++) {
 #pragma unroll
@@ -161,7 +156,6 @@ __global__ __launch_bounds__(LPB_T, NV == 2 ? 2 : 1) void k_dmmv_q4k_tile_nv(Lpb
                 accm[v] = fmaf(m1, xz1, accm[v]);
             }
         }
-#endif
         float res[NV];
 #pragma unroll
         for (int v = 0; v < NV; v++) {

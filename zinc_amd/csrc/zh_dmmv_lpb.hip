@@ -287,18 +287,8 @@ __global__ __launch_bounds__(LPB_T, ZH_LPB_MINB) void k_dmmv_q6k_lpb(LpbP p) {
 // The next batch's loads are in flight while the current batch is computed.
 // ---------------------------------------------------------------------------
 
-#ifdef ZH_EXP_TRACE
-__device__ uint64_t g_exp_trace[8192 * 8];
-#define TRACE(slot) do { if (threadIdx.x == 0 && blockIdx.x < 8192 && (slot) < 8) \
-    g_exp_trace[blockIdx.x * 8 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-extern "C" int zh_exp_trace_dump(uint64_t *host, uint32_t n) {
-    int rc = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_trace), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
-    static uint64_t zeros[8192 * 8];
-    return rc | (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_trace), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
-}
-#else
-#define TRACE(slot) do { } while (0)
-#endif
+#define TRACE(slot) ZH_TRACE_POINT(slot)
+ZH_TRACE_DUMP_FN(zh_debug_trace_lpb)
 
 // 64-lane teams (K > 8192) stage an XQ image of up to 56 KB: two workgroups per CU
 template <int TL, int MODE>
@@ -362,11 +352,6 @@ __global__ __launch_bounds__(LPB_T, TL >= 64 ? 2 : 3) void k_dmmv_q4k_tile(LpbP 
         }
         const LpbQ4K::Hdr h = LpbQ4K::header(raw);
         float accd = 0.f, accm = 0.f;
-#ifdef ZH_EXP_TILE
-        uint32_t xx = 0;
-        for (int i = 0; i < 36; i++) xx ^= raw[i];
-        accd = (float)(xx & 1);
-#else
 #pragma unroll
         for (int pp = 0; pp < 4; pp++) {
             uint32_t xo = (uint32_t)(2 * pp) * 96u;
@@ -398,7 +383,6 @@ __global__ __launch_bounds__(LPB_T, TL >= 64 ? 2 : 3) void k_dmmv_q4k_tile(LpbP 
             accm = fmaf(m0, xz0, accm);
             accm = fmaf(m1, xz1, accm);
         }
-#endif
         float res = active ? fmaf(h.d, accd, -h.dmin * accm) : 0.f;
         res = team_sum_dpp<TL>(res);
         float *yb = p.segY[sg];
@@ -602,12 +586,8 @@ static int launch_q4k_tile(zh_ctx *c, const LpbP &p, uint32_t wgs, uint32_t lds)
 // within 64 KB), 16-byte aligned matrices, and every segment but the last a
 // whole number of batches.
 static int try_q4k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t *M) {
-    static int off = -1, capm = -1;
-    if (off < 0) {
-        off = getenv("ZH_NO_TILE") ? 1 : 0;
-        const char *e = getenv("ZH_TILE_CAP");
-        capm = e ? atoi(e) : 3;
-    }
+    const bool off = zh_knob("ZH_NO_TILE");
+    const int capm = zh_knob_int("ZH_TILE_CAP", 3);
     const uint32_t nb = p.K / 256;
     if (off || nb > 64) return -1;
     const uint32_t TL = pow2ceil(nb < 4 ? 4 : nb);
@@ -652,12 +632,8 @@ static int launch_q6k_tile(zh_ctx *c, const LpbP &p, uint32_t wgs, uint32_t lds,
 // Q6_K tile path: rows a multiple of 16 bytes (K % 2048 == 0), team of <= 128
 // lanes (K <= 16384) and LDS image + tile within 64 KB.
 static int try_q6k_tile(zh_ctx *c, const LpbP &p, uint32_t nseg, const uint32_t *M) {
-    static int off = -1, capm = -1;
-    if (off < 0) {
-        off = getenv("ZH_NO_TILE") ? 1 : 0;
-        const char *e = getenv("ZH_TILE6_CAP");
-        capm = e ? atoi(e) : 2;
-    }
+    const bool off = zh_knob("ZH_NO_TILE");
+    const int capm = zh_knob_int("ZH_TILE6_CAP", 2);
     const uint32_t nb = p.K / 256, row_bytes = nb * 210;
     // Very tall matrices (the LM head) give every workgroup dozens of batches;
     // there the per-row limb re-reads from LDS and the Q6_K unpack bound the
@@ -717,6 +693,11 @@ int zhk_dmmv_lpb(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const uint8
     if (xq_out && (mode != LPB_GATE_UP || nseg != 1 || p.M % 32 || !grp_cnt))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "lpb: XQ output needs gate/up mode, one segment, M %% 32 == 0");
     {
+        const int rc = zhk_dmmv_ring(c, qtype, mode, nseg, W, W2, y, M, x, norm_w, eps, normed_out, K, acc, xq,
+                                     xq_out, grp_cnt);
+        if (rc >= 0) return rc;
+    }
+    {
         const int rc = qtype == ZH_Q4_K ? try_q4k_tile(c, p, nseg, M) : try_q6k_tile(c, p, nseg, M);
         if (rc >= 0) return rc;
     }
@@ -726,11 +707,7 @@ int zhk_dmmv_lpb(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const uint8
     const uint32_t teams = (p.M + R - 1) / R;
     const uint32_t tpw = LPB_T / TL;
     uint32_t wgs = (teams + tpw - 1) / tpw;
-    static int capm = -1;
-    if (capm < 0) {
-        const char *e = getenv("ZH_LPB_CAP");
-        capm = e ? atoi(e) : 0;
-    }
+    const int capm = zh_knob_int("ZH_LPB_CAP", 0);
     const uint32_t cap = (uint32_t)c->cu_count * (capm > 0 ? (uint32_t)capm : 4u);
     if (wgs > cap) wgs = cap;
     const uint32_t lds = xlds_bytes(K);

@@ -514,7 +514,7 @@ static int record_collect(zh_engine *e) {
     const zh_model_config &m = e->c;
     const uint32_t H = m.hidden;
     const uint8_t *A = e->arena;
-    if (!getenv("ZH_NO_LPB") && zhk_lpb_supported(e->lm.type, H) && m.vocab % 2 == 0) {
+    if (!zh_knob("ZH_NO_LPB")&& zhk_lpb_supported(e->lm.type, H) && m.vocab % 2 == 0) {
         const uint8_t *wl = A + e->lm.off;
         float *yl = e->logits;
         const uint32_t mv = m.vocab;
@@ -545,9 +545,9 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     const bool whole = mask == SK_ALL && l0 == 0 && l1 >= m.n_layers;
     // embedToken (forward.zig:4255-4290), on the device.
     if (whole) ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
-    const bool lpb = !getenv("ZH_NO_LPB");
+    const bool lpb = !zh_knob("ZH_NO_LPB");
     // LDS-staged kernels with the norms, router top-k and expert combine fused
-    const bool lds = !getenv("ZH_NO_LDS_DMMV");
+    const bool lds = !zh_knob("ZH_NO_LDS_DMMV");
     for (uint32_t l = l0; l < m.n_layers && l < l1; l++) {
         const Layer &y = e->L[l];
         // kernel choice per layer, from the layer's own tensor types (a GGUF
@@ -617,7 +617,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             // gate/up also emits its output as XQ (quantised per 32-row group by
             // the group's last batch), so the down projection copies XQ instead of
             // every workgroup re-quantising the f32 vector
-            const bool swiglu_xq = m.ffn % 32 == 0 && H / 256 <= 32 && !getenv("ZH_NO_TILE");
+            const bool swiglu_xq = m.ffn % 32 == 0 && H / 256 <= 32 && !zh_knob("ZH_NO_TILE");
             if (mask & SK_FFN_IN)
                 ERC(zhk_dmmv_lpb(c, ZH_Q4_K, 1, 1, &wg, W(y.up), &ys, &mf, e->hidden, Wf(y.ffn_norm), m.eps, nullptr,
                                  H, 0, nullptr, swiglu_xq ? e->xq_f : nullptr, swiglu_xq ? e->grp_cnt : nullptr));
@@ -751,7 +751,7 @@ static int set_state(zh_engine *e, uint32_t n_prompt, uint32_t pos, uint32_t fir
 }
 
 static int run_step(zh_engine *e, bool collect) {
-    if (getenv("ZH_NO_GRAPH")) return record_step(e, collect);
+    if (zh_knob("ZH_NO_GRAPH")) return record_step(e, collect);
     ERC(ensure_graphs(e));
     EHIP(e, hipGraphLaunch(collect ? e->g_out : e->g_noout, e->ctx->stream));
     return ZH_OK;

@@ -4,6 +4,21 @@
 #include <stdint.h>
 #include <string>
 
+// Ablation switches for measuring one kernel path against another. Only a
+// debug build (-DZH_DEBUG_KNOBS) reads them from the environment; the product
+// build compiles every switch to its default.
+#ifdef ZH_DEBUG_KNOBS
+#include <stdlib.h>
+static inline bool zh_knob(const char *name) { return getenv(name) != nullptr; }
+static inline int zh_knob_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+#else
+static inline bool zh_knob(const char *) { return false; }
+static inline int zh_knob_int(const char *, int dflt) { return dflt; }
+#endif
+
 #include "../../include/zinc_hip.h"
 
 struct zh_buf {
@@ -163,6 +178,11 @@ int zhk_dmmv_lpb(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uin
                  float *const *y, const uint32_t *M, const float *x, const float *norm_w, float eps,
                  float *normed_out, uint32_t K, uint32_t acc, const void *xq = nullptr,
                  uint8_t *xq_out = nullptr, uint32_t *grp_cnt = nullptr);
+// Streaming Q4_K DMMV (zh_dmmv_ring.hip), same arguments as zhk_dmmv_lpb;
+// returns -1 (nothing launched) for shapes it does not take.
+int zhk_dmmv_ring(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
+                  float *const *y, const uint32_t *M, const float *x, const float *norm_w, float eps,
+                  float *normed_out, uint32_t K, uint32_t acc, const void *xq, uint8_t *xq_out, uint32_t *grp_cnt);
 // Batched DMMV: y[s * n_vec + v] (+)= W[s] x_v, x_v = x[v] (f32, optional
 // fused RMSNorm) or xq[v] (XQ, x == nullptr); mode 0 plain, 1 gate/up+SwiGLU.
 int zhk_dmmv_batched(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,

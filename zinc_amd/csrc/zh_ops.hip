@@ -199,18 +199,8 @@ extern "C" int zh_qk_norm_rope_kv_write(zh_ctx *c, zh_buf *q, const zh_buf *qw, 
 // RoPE pairs stay inside a lane. Cache layout [kv_head][token][128] fp16,
 // addressed through 16-token pages.
 // ---------------------------------------------------------------------------
-#ifdef ZH_EXP_TRACE
-__device__ uint64_t g_exp_trace_ops[16384 * 16];
-#define TRACE_OPS(slot) do { const uint32_t bl_ = blockIdx.x + blockIdx.y * gridDim.x; \
-    if (threadIdx.x == 0 && bl_ < 8192) g_exp_trace_ops[bl_ * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-extern "C" int zh_exp_trace_ops_dump(uint64_t *host, uint32_t n) {
-    int rc = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_exp_trace_ops), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
-    static uint64_t zeros[16384 * 16];
-    return rc | (int)hipMemcpyToSymbol(HIP_SYMBOL(g_exp_trace_ops), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
-}
-#else
-#define TRACE_OPS(slot) do { } while (0)
-#endif
+#define TRACE_OPS(slot) ZH_TRACE_POINT(slot)
+ZH_TRACE_DUMP_FN(zh_debug_trace_ops)
 constexpr int FD_MAXG = 8;   // q heads per kv head
 constexpr int FD_HD = 128;   // head_dim supported
 // 4 waves x TW tokens: one wave per SIMD, and the 8 kv heads map one per XCD

@@ -285,7 +285,7 @@ int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *cons
     // every segment but the last must then be a whole number of tiles. A
     // single matrix keeps 128-row tiles and splits K instead (below).
     bool small = (uint64_t)((end + 127) / 128) * ni < (uint64_t)c->cu_count &&
-                 (nseg > 1 || getenv("ZH_GEMM_TJ64"));
+                 (nseg > 1 || zh_knob("ZH_GEMM_TJ64"));
     for (uint32_t s = 0; s + 1 < nseg; s++)
         if (M[s] % 128) small = true;
     for (uint32_t s = 0; s + 1 < nseg; s++)
@@ -297,7 +297,7 @@ int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *cons
     // other's MFMAs); at least 8 K-steps per split.
     const uint64_t tiles = (uint64_t)((end + TJv - 1) / TJv) * ni, slots = 2ull * (uint64_t)c->cu_count;
     p.ksplit = 1;
-    if (nseg == 1 && tiles < slots && !getenv("ZH_NO_SPLITK")) {
+    if (nseg == 1 && tiles < slots && !zh_knob("ZH_NO_SPLITK")) {
         uint32_t sk = (uint32_t)((slots + tiles - 1) / tiles);
         while (sk > 1 && K / KS < 8 * sk) sk--;
         p.ksplit = sk;

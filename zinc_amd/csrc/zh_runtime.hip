@@ -333,10 +333,9 @@ extern "C" int zh_synth_vector(zh_ctx *c, zh_buf *buf, uint64_t off, uint32_t ki
 }
 
 // ---------------------------------------------------------------------------
-// Calibration probes (the counterpart of the reference's dispatch-overhead and
-// bandwidth microbenchmarks, benchmarks/dispatch_overhead.c, bandwidth.zig):
-// a streaming-read kernel that gives the achievable HBM read ceiling, and an
-// empty-kernel chain that gives the per-dispatch cost inside a hipGraph.
+// Calibration probe (the counterpart of the reference's bandwidth
+// microbenchmark, benchmarks/bandwidth.zig): a streaming-read
+// kernel that gives the achievable HBM read ceiling.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_stream_read(const u32x4 *__restrict__ p, uint64_t n16, uint32_t *out) {
     uint32_t acc = 0;
@@ -375,124 +374,3 @@ extern "C" int zh_stream_read_probe(zh_ctx *c, const zh_buf *buf, uint64_t bytes
     return ZH_OK;
 }
 
-__global__ void k_empty(uint32_t *p) {
-    if (threadIdx.x == 0 && blockIdx.x == 0 && p[0] == 0xFFFFFFFFu) p[1] = 1;
-}
-
-extern "C" int zh_dispatch_overhead(zh_ctx *c, uint32_t n_kernels, uint32_t wgs, int use_graph, float *us_per_kernel) {
-    if (!c || !us_per_kernel || n_kernels == 0 || wgs == 0) return ZH_ERR_INVALID_ARGUMENT;
-    void *o;
-    int rc = zh_scratch(c, 256, &o);
-    if (rc) return rc;
-    hipGraphExec_t ge = nullptr;
-    if (use_graph) {
-        hipGraph_t g;
-        ZH_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-        for (uint32_t k = 0; k < n_kernels; k++)
-            hipLaunchKernelGGL(k_empty, dim3(wgs), dim3(256), 0, c->stream, (uint32_t *)o);
-        ZH_HIP(c, hipStreamEndCapture(c->stream, &g));
-        ZH_HIP(c, hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
-        (void)hipGraphDestroy(g);
-        ZH_HIP(c, hipGraphLaunch(ge, c->stream));  // warm
-    }
-    ZH_HIP(c, hipStreamSynchronize(c->stream));
-    ZH_HIP(c, hipEventRecord(c->ev[62], c->stream));
-    if (use_graph) {
-        ZH_HIP(c, hipGraphLaunch(ge, c->stream));
-    } else {
-        for (uint32_t k = 0; k < n_kernels; k++)
-            hipLaunchKernelGGL(k_empty, dim3(wgs), dim3(256), 0, c->stream, (uint32_t *)o);
-    }
-    ZH_HIP(c, hipEventRecord(c->ev[63], c->stream));
-    ZH_HIP(c, hipEventSynchronize(c->ev[63]));
-    float ms = 0.f;
-    ZH_HIP(c, hipEventElapsedTime(&ms, c->ev[62], c->ev[63]));
-    if (ge) (void)hipGraphExecDestroy(ge);
-    *us_per_kernel = ms * 1e3f / (float)n_kernels;
-    return ZH_OK;
-}
-
-// ---------------------------------------------------------------------------
-// Grid-barrier probe: a co-resident (cooperative) grid crossing n device-wide
-// barriers. Each barrier is an agent-scope release increment of a counter and
-// a bounded acquire spin; a spin that exceeds its limit sets *err and the
-// workgroup proceeds, so the kernel always terminates.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_barrier_probe(uint32_t *counter, uint32_t n, uint32_t spin_limit,
-                                                       uint32_t *err) {
-    for (uint32_t i = 0; i < n; i++) {
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const uint32_t target = (i + 1) * gridDim.x;
-            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-            uint32_t it = 0;
-            while (__hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++it > spin_limit) {
-                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-            }
-        }
-        __syncthreads();
-    }
-}
-
-// Flag barrier: workgroup w publishes epoch e in flags[w] (no shared atomic);
-// wave 0 of every workgroup polls all flags until each is >= e.
-__global__ __launch_bounds__(256) void k_flag_barrier_probe(uint32_t *flags, uint32_t n, uint32_t spin_limit,
-                                                            uint32_t *err) {
-    const uint32_t nwg = gridDim.x;
-    for (uint32_t i = 0; i < n; i++) {
-        const uint32_t e = i + 1;
-        __syncthreads();
-        if (threadIdx.x == 0) __hip_atomic_store(flags + blockIdx.x, e, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        if (threadIdx.x < 64) {
-            uint32_t it = 0;
-            for (;;) {
-                bool ok = true;
-                for (uint32_t w = threadIdx.x; w < nwg; w += 64)
-                    ok &= __hip_atomic_load(flags + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= e;
-                if (__all(ok)) break;
-                __builtin_amdgcn_s_sleep(1);
-                if (++it > spin_limit) {
-                    if (threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-            }
-            __atomic_thread_fence(__ATOMIC_ACQUIRE);
-        }
-        __syncthreads();
-    }
-}
-
-extern "C" int zh_grid_barrier_probe(zh_ctx *c, uint32_t n_barriers, uint32_t wgs_per_cu, float *us_per_barrier) {
-    const bool flag_mode = getenv("ZH_BARRIER_ATOMIC") == nullptr;
-    if (!c || !us_per_barrier || n_barriers == 0 || wgs_per_cu == 0) return ZH_ERR_INVALID_ARGUMENT;
-    int maxb = 0;
-    ZH_HIP(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb, k_barrier_probe, 256, 0));
-    if ((int)wgs_per_cu > maxb) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "%u WGs/CU > occupancy %d", wgs_per_cu, maxb);
-    uint32_t *buf;
-    uint32_t grid = (uint32_t)c->cu_count * wgs_per_cu;
-    int rc = zh_scratch(c, 4096 * 4 + 256, (void **)&buf);
-    if (rc) return rc;
-    uint32_t spin = 1u << 22;
-    float ms[2] = {0, 0};
-    for (int pass = 0; pass < 2; pass++) {
-        uint32_t nb = pass ? n_barriers : 1;
-        ZH_HIP(c, hipMemsetAsync(buf, 0, 4096 * 4 + 8, c->stream));
-        uint32_t *counter = buf + 2, *err = buf + 1;
-        void *args[] = {&counter, &nb, &spin, &err};
-        ZH_HIP(c, hipEventRecord(c->ev[62], c->stream));
-        ZH_HIP(c, hipLaunchCooperativeKernel(flag_mode ? (const void *)k_flag_barrier_probe : (const void *)k_barrier_probe,
-                                             dim3(grid), dim3(256), args, 0, c->stream));
-        ZH_HIP(c, hipEventRecord(c->ev[63], c->stream));
-        ZH_HIP(c, hipEventSynchronize(c->ev[63]));
-        ZH_HIP(c, hipEventElapsedTime(&ms[pass], c->ev[62], c->ev[63]));
-        uint32_t e = 0;
-        ZH_HIP(c, hipMemcpy(&e, buf + 1, 4, hipMemcpyDeviceToHost));
-        if (e) return zh_set_err(c, ZH_ERR_HIP, "barrier spin limit exceeded");
-    }
-    *us_per_barrier = (ms[1] - ms[0]) * 1e3f / (float)(n_barriers - 1 > 0 ? n_barriers - 1 : 1);
-    return ZH_OK;
-}

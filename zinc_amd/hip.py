@@ -88,8 +88,6 @@ SIGNATURES = {
     "zh_event_record": (_i32, [_P, _i32]),
     "zh_event_elapsed_ms": (_i32, [_P, _i32, _i32, C.POINTER(_f32)]),
     "zh_stream_read_probe": (_i32, [_P, _P, _u64, _u32, C.POINTER(_f32)]),
-    "zh_dispatch_overhead": (_i32, [_P, _u32, _u32, _i32, C.POINTER(_f32)]),
-    "zh_grid_barrier_probe": (_i32, [_P, _u32, _u32, C.POINTER(_f32)]),
     "zh_synth_tensor": (_i32, [_P, _P, _u64, _u32, _u64, _u64, _u64, _u64]),
     "zh_synth_vector": (_i32, [_P, _P, _u64, _u32, _u64, _f32, _u64, _u64]),
     "zh_dmmv": (_i32, [_P, _u32, _P, _u64, _P, _u64, _P, _u64, _u32, _u32, _u32]),
@@ -273,16 +271,6 @@ class Context:
         g = C.c_float()
         self.check(lib().zh_stream_read_probe(self.h, buf.h, nbytes, iters, C.byref(g)))
         return g.value
-
-    def dispatch_overhead(self, n_kernels=500, wgs=1, use_graph=True):
-        us = C.c_float()
-        self.check(lib().zh_dispatch_overhead(self.h, n_kernels, wgs, int(use_graph), C.byref(us)))
-        return us.value
-
-    def grid_barrier_probe(self, n_barriers=1000, wgs_per_cu=1):
-        us = C.c_float()
-        self.check(lib().zh_grid_barrier_probe(self.h, n_barriers, wgs_per_cu, C.byref(us)))
-        return us.value
 
     # ---- ops (thin wrappers; argument meaning as include/zinc_hip.h) ----
     def synth_tensor(self, buf, offset, qtype, rows, cols, seed, stream):
