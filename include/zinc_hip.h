@@ -38,7 +38,8 @@ enum {
     ZH_ERR_UNSUPPORTED_ARCHITECTURE = 9,/* error.UnsupportedArchitecture loader.zig:449 */
     ZH_ERR_TRUNCATED_FILE = 10,        /* a header or tensor runs past the end of the file */
     ZH_ERR_IO = 11,                    /* open / stat / mmap failure (std.fs errors) */
-    ZH_ERR_NOT_FOUND = 12              /* metadata key absent or not of the asked type (null) */
+    ZH_ERR_NOT_FOUND = 12,             /* metadata key absent or not of the asked type (null) */
+    ZH_ERR_KV_CACHE_EXHAUSTED = 13     /* error.KvCacheExhausted      kv_cache.zig:73 */
 };
 
 /* ---- GGMLType values used on the path (src/model/gguf.zig:38-69) -------- */
@@ -47,6 +48,7 @@ enum { ZH_F32 = 0, ZH_F16 = 1, ZH_Q8_0 = 8, ZH_Q4_K = 12, ZH_Q5_K = 13, ZH_Q6_K 
 typedef struct zh_ctx zh_ctx;
 typedef struct zh_buf zh_buf;
 typedef struct zh_engine zh_engine;
+typedef struct zh_kv_pool zh_kv_pool;
 
 /* ---- device lifecycle: replaces Instance.init / mtl_init (shim.h:24-25) -- */
 int  zh_init(int device, zh_ctx **out);
@@ -264,6 +266,23 @@ int zh_engine_hidden(zh_engine *eng, float *dst);
 int zh_engine_tensor(zh_engine *eng, uint64_t stream, zh_buf **buf, uint64_t *offset, uint64_t *bytes);
 /* Gather n logical tokens of layer `layer` K (which=0) or V (1) as fp16,
  * logical-token-major [t][kv_head][head_dim] (the oracle's layout). */
+/* The sequence's KV page table: logical 16-token page i of every layer's
+ * cache lives in physical page pages[i] (logicalTokenToPhysicalToken,
+ * forward.zig:677-698). n == max_ctx / 16, entries < max_ctx / 16. Replaces
+ * handing the request's KvPagePool pages to the engine (the reference keeps
+ * the table in a device buffer, forward.zig:1312). An identity table keeps
+ * the lookup-free attention kernel; any other selects the paged kernel. */
+int zh_engine_set_pages(zh_engine *eng, const uint32_t *pages, uint32_t n);
+
+/* ---- KV page pool: KvPagePool (src/scheduler/kv_cache.zig:43-125) ------ */
+int      zh_kv_pool_create(uint32_t total_pages, uint32_t page_size, zh_kv_pool **out);  /* init */
+void     zh_kv_pool_destroy(zh_kv_pool *pool);                                            /* deinit */
+/* allocPages: pops `count` ids off the free stack (a fresh pool hands out
+ * total_pages-1, total_pages-2, ...); ZH_ERR_KV_CACHE_EXHAUSTED if too few. */
+int      zh_kv_pool_alloc(zh_kv_pool *pool, uint64_t request_id, uint32_t count, uint32_t *page_ids);
+void     zh_kv_pool_free(zh_kv_pool *pool, uint64_t request_id);                          /* freePages */
+uint32_t zh_kv_pool_free_count(const zh_kv_pool *pool);                                  /* freeCount */
+uint32_t zh_kv_pool_max_context(const zh_kv_pool *pool, uint32_t page_count);            /* maxContext */
 int zh_engine_read_kv(zh_engine *eng, uint32_t layer, uint32_t which, uint32_t t0, uint32_t n,
                       uint16_t *dst);
 /* Model bytes touched per decoded token at context length L (weights + fp16

@@ -77,7 +77,11 @@ def test_engine_decode_matches_oracle(ctx, orc, cfg):
     # by several of its own ulps). Layer 0's inputs equal the oracle's, so
     # few elements differ at all; later layers take a hidden state that has
     # been through f32 sums in another order, and more elements round to the
-    # neighbouring f16 value.
+    # neighbouring f16 value. With MoE layers that order difference reaches
+    # 1e-5 .. 1e-4 of the hidden state's scale (measured, with the same size
+    # for either attention kernel: the experts' SwiGLU amplifies it), so past
+    # layer 0 the bound is the decode tolerance, 1e-3 of the head's largest
+    # element.
     hd = cfg["head_dim"]
     for l in range(cfg["n_layers"]):
         for which in (0, 1):
@@ -86,7 +90,7 @@ def test_engine_decode_matches_oracle(ctx, orc, cfg):
             assert np.isfinite(g).all()
             g32, o32 = g.astype(np.float32), o.astype(np.float32)
             rowmax = np.repeat(np.abs(o32).reshape(-1, hd).max(axis=1), hd)
-            bound = np.spacing(np.abs(o)).astype(np.float32) + 1e-5 * rowmax
+            bound = np.spacing(np.abs(o)).astype(np.float32) + (1e-5 if l == 0 else 1e-3) * rowmax
             d = np.abs(g32 - o32)
             frac = 0.05 if l == 0 else 0.2
             assert (d <= bound).all() and (d > 0).mean() < frac, (l, which, (d / bound).max(), (d > 0).mean())
@@ -172,3 +176,93 @@ def test_engine_long_context_subchunks(ctx, orc, prefill):
         tok = int(o_tok)
     eng.deinit()
     om.close()
+
+
+# Paged KV cache: the engine's page table comes from a page pool
+# (KvPagePool, kv_cache.zig:43-125: a fresh pool hands out pages in
+# descending order) or is an arbitrary permutation; the decode kernel then
+# looks every 16-token page up (logicalTokenToPhysicalToken,
+# forward.zig:677-698). Greedy tokens must equal the oracle's (which has no
+# paging), and the rows read back through the table must equal the oracle's.
+def _pages(cfg, order):
+    import zinc_amd
+    n = cfg["max_ctx"] // 16
+    if order == "pool":
+        pool = zinc_amd.KvPagePool(n, 16)
+        pages = pool.alloc_pages(7, n)
+        assert pages.tolist() == list(range(n - 1, -1, -1)) and pool.free_count() == 0
+        return pages
+    return np.random.default_rng(17).permutation(n).astype(np.uint32)
+
+
+@pytest.mark.parametrize("cfg,order", [(SMALL_DENSE, "pool"), (SMALL_DENSE, "shuffle"), (SMALL_MOE, "shuffle"),
+                                       (MOE_C4, "pool")], ids=["dense-pool", "dense-shuffle", "moe-shuffle", "moe_c4-pool"])
+def test_engine_paged_generate_token_exact(ctx, orc, cfg, order):
+    import zinc_amd
+    print(f"paged engine {order} heads {cfg['n_heads']}/{cfg['n_kv_heads']}", flush=True)
+    eng = zinc_amd.InferenceEngine(ctx, cfg)
+    eng.set_pages(_pages(cfg, order))
+    om = orc.Model(cfg)
+    prefill, n_gen = 64, 24
+    eng.prefill_kv_random(prefill, 5)
+    om.prefill_kv_random(prefill, 5)
+    for which in (0, 1):  # the prefilled rows through the table
+        assert np.array_equal(eng.read_kv(0, which, 0, prefill), np.concatenate([om.kv(0, which, t) for t in range(prefill)]))
+    prompt = [int(t) for t in np.random.default_rng(3).integers(0, cfg["vocab"], 6)]
+    got = eng.generate(prompt, n_gen, start_pos=prefill)
+    pos = prefill
+    for t in prompt[:-1]:
+        om.decode_step(t, pos)
+        pos += 1
+    ref, tok = [], prompt[-1]
+    for _ in range(n_gen):
+        tok = om.decode_step(tok, pos)
+        pos += 1
+        ref.append(int(tok))
+    assert got == ref, f"first mismatch at {next(i for i in range(n_gen) if got[i] != ref[i])}"
+    # the rows the decode wrote, read back through the table
+    for t in (prefill, prefill + 10, pos - 1):
+        for which in (0, 1):
+            g = eng.read_kv(1, which, t, 1).view(np.float16).astype(np.float32)
+            o = om.kv(1, which, t).view(np.float16).astype(np.float32)
+            assert np.abs(g - o).max() <= 2e-3 * np.abs(o).max() + 1e-3, (t, which)
+    eng.deinit()
+    om.close()
+
+
+def test_engine_paged_long_context(ctx, orc):
+    """12000 tokens over a shuffled table: every chunk streams several
+    sub-chunks, each looked up page by page."""
+    import zinc_amd
+    cfg = LONG_SUBCHUNK
+    eng = zinc_amd.InferenceEngine(ctx, cfg)
+    eng.set_pages(_pages(cfg, "shuffle"))
+    om = orc.Model(cfg)
+    prefill = 12000
+    eng.prefill_kv_random(prefill, 11)
+    om.prefill_kv_random(prefill, 11)
+    state = zinc_amd.DecodeState()
+    tok = 5
+    for step in range(2):
+        state.position = prefill + step
+        eng.decode_step(state, tok, True)
+        g_tok, g_log = eng.sample_greedy(), eng.logits()
+        o_tok, o_log = om.decode_step(tok, prefill + step, want_logits=True)
+        scale = np.abs(o_log).max()
+        assert np.abs(g_log - o_log).max() <= 1e-4 + 1e-3 * scale, (step, np.abs(g_log - o_log).max(), scale)
+        if margin(o_log) > 1e-3 * scale:
+            assert g_tok == o_tok
+        tok = int(o_tok)
+    eng.deinit()
+    om.close()
+
+
+def test_engine_set_pages_rejects_bad_tables(ctx):
+    import zinc_amd
+    eng = zinc_amd.InferenceEngine(ctx, SMALL_DENSE)
+    n = SMALL_DENSE["max_ctx"] // 16
+    for bad in (np.arange(n - 1, dtype=np.uint32), np.full(n, n, dtype=np.uint32)):
+        with pytest.raises(zinc_amd.ZincError) as e:
+            eng.set_pages(bad)
+        assert e.value.name == "InvalidArgument"
+    eng.deinit()

@@ -6,4 +6,4 @@ InferenceEngine mirror; it has no CPU fallback.
 """
 from .hip import (F16, F32, MXFP4, Q4_K, Q5_K, Q6_K, Q8_0, Buffer, Context, SamplingParams, ZincError,  # noqa: F401
                   lib, tensor_bytes)
-from .engine import DENSE_8B, MOE_48L, DecodeState, InferenceEngine  # noqa: F401
+from .engine import DENSE_8B, MOE_48L, DecodeState, InferenceEngine, KvPagePool  # noqa: F401

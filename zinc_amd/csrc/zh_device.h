@@ -259,3 +259,44 @@ ZH_DEV void topk_softmax_wave(const float (&vals)[4], uint32_t n, uint32_t k, ui
     if (lane < k) ((float *)routing)[k + lane] = my / s;
 }
 
+// ---------------------------------------------------------------------------
+// Asynchronous HBM -> LDS copies (gfx950 global_load_lds_dwordx4). Each is
+// issued from inline assembly, so the compiler tracks none of them: the
+// kernels that use them issue no compiler-visible global loads while copies
+// are in flight (a compiler-generated wait for such a load would be
+// vmcnt(0) and drain every copy) and wait explicitly with wait_vm.
+// ---------------------------------------------------------------------------
+ZH_DEV uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// 64 lanes x 16 bytes from per-lane global addresses into LDS at the
+// wave-uniform byte address `lds` + 16 * lane.
+ZH_DEV void dma16(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+template <int N>
+ZH_DEV void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Waits until at most n of this wave's vector-memory instructions are
+// outstanding; n is one of the counts the ring produces.
+ZH_DEV void wait_vm_dyn(uint32_t n) {
+    switch (n) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<1>(); break;
+    case 2: wait_vm<2>(); break;
+    case 3: wait_vm<3>(); break;
+    case 4: wait_vm<4>(); break;
+    case 5: wait_vm<5>(); break;
+    case 6: wait_vm<6>(); break;
+    case 8: wait_vm<8>(); break;
+    case 10: wait_vm<10>(); break;
+    case 12: wait_vm<12>(); break;
+    case 16: wait_vm<16>(); break;
+    case 24: wait_vm<24>(); break;
+    default: wait_vm<0>(); break;  // conservative: everything
+    }
+}
+// Barrier for LDS data: this wave's LDS accesses complete, then s_barrier.
+// Unlike __syncthreads it does not drain the wave's DMAs in flight.
+ZH_DEV void lds_bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

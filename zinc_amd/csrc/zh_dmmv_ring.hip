@@ -40,36 +40,6 @@ constexpr uint32_t RG_XQ_BYTES = 16384;         // LDS for the XQ image of K <= 
 constexpr uint32_t RG_RAW_BYTES = 32768;        // LDS for the f32 activation and norm weights
 constexpr uint32_t RG_LDS = RG_D * RG_TILE + RG_XQ_BYTES + RG_RAW_BYTES + 2 * RG_MAXROWS * 4 + 64;
 
-ZH_DEV uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-// 64 lanes x 16 bytes from per-lane global addresses into LDS at the
-// wave-uniform byte address `lds` + 16 * lane.
-ZH_DEV void dma16(const void *g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-template <int N>
-ZH_DEV void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// Waits until at most n of this wave's vector-memory instructions are
-// outstanding; n is one of the counts the ring produces.
-ZH_DEV void wait_vm_dyn(uint32_t n) {
-    switch (n) {
-    case 0: wait_vm<0>(); break;
-    case 1: wait_vm<1>(); break;
-    case 2: wait_vm<2>(); break;
-    case 4: wait_vm<4>(); break;
-    case 5: wait_vm<5>(); break;
-    case 8: wait_vm<8>(); break;
-    case 10: wait_vm<10>(); break;
-    default: wait_vm<0>(); break;
-    }
-}
-// Barrier for LDS data: this wave's LDS accesses complete, then s_barrier.
-// Unlike __syncthreads it does not drain the wave's DMAs in flight.
-ZH_DEV void lds_bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 }  // namespace
 
 struct RingP {

@@ -55,6 +55,7 @@ struct zh_engine {
     std::vector<Layer> L;
     uint16_t *kv = nullptr;  // all caches
     uint32_t *pages = nullptr, n_pages = 0;
+    bool pages_ident = true;  // pages[i] == i: the decode step may use the identity-table attention
     float *inv_freq = nullptr;
     float *rope_cs = nullptr;  // [max_ctx][64] (cos, sin)
     // activations
@@ -106,7 +107,7 @@ __global__ void k_advance(uint32_t *st, const uint32_t *prompt) {
 // into the head-major cache; counter = t*kv_dim + h*head_dim + d, as the
 // oracle's token-major fill.
 __global__ void k_prefill_kv(uint16_t *cache, uint32_t nkv, uint32_t cache_tokens, uint32_t hd, uint32_t n,
-                             uint64_t key) {
+                             uint64_t key, const uint32_t *pages) {
     uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     uint64_t total = (uint64_t)n * nkv * hd;
     if (i >= total) return;
@@ -120,7 +121,8 @@ __global__ void k_prefill_kv(uint16_t *cache, uint32_t nkv, uint32_t cache_token
     z = z ^ (z >> 31);
     int sm = (int)(z & 0xFFFF) + (int)((z >> 16) & 0xFFFF) + (int)((z >> 32) & 0xFFFF) + (int)((z >> 48) & 0xFFFF) -
              131070;
-    cache[((size_t)h * cache_tokens + t) * hd + d] = f2h_rn(__fmul_rn((float)sm, 2.6429573e-05f));
+    const uint32_t phys = pages[t / 16] * 16 + t % 16;  // logicalTokenToPhysicalToken
+    cache[((size_t)h * cache_tokens + phys) * hd + d] = f2h_rn(__fmul_rn((float)sm, 2.6429573e-05f));
 }
 
 __global__ void k_gather_kv(const uint16_t *cache, uint32_t nkv, uint32_t cache_tokens, uint32_t hd,
@@ -498,10 +500,86 @@ extern "C" int zh_engine_prefill_kv_random(zh_engine *e, uint32_t n, uint64_t se
     for (uint32_t l = 0; l < e->c.n_layers; l++)
         for (uint32_t w = 0; w < 2; w++) {
             hipLaunchKernelGGL(k_prefill_kv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, e->ctx->stream,
-                               w ? e->L[l].vc : e->L[l].kc, nkv, e->c.max_ctx, hd, n, host_key(seed, S_KV(l, w)));
+                               w ? e->L[l].vc : e->L[l].kc, nkv, e->c.max_ctx, hd, n, host_key(seed, S_KV(l, w)),
+                               (const uint32_t *)e->pages);
             ZH_LAUNCH_CHECK(e->ctx);
         }
     return ZH_OK;
+}
+
+// The sequence's page table: logical 16-token page i of every layer's cache
+// lives in physical page pages[i] (logicalTokenToPhysicalToken,
+// forward.zig:677-698; the pages come from a KvPagePool, kv_cache.zig:43-125,
+// or zh_kv_pool_alloc). n must be max_ctx / 16 and every entry a physical
+// page below that; entries need not be distinct for the kernels, but two
+// logical pages sharing a physical one overwrite each other's tokens. The
+// step graphs are rebuilt: an identity table keeps the attention kernel that
+// skips lookups, any other table selects the paged kernel.
+extern "C" int zh_engine_set_pages(zh_engine *e, const uint32_t *pages, uint32_t n) {
+    if (!e || !pages) return ZH_ERR_INVALID_ARGUMENT;
+    if (n != e->n_pages)
+        return zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "page table of %u entries, the engine has %u pages", n,
+                          e->n_pages);
+    bool ident = true;
+    for (uint32_t i = 0; i < n; i++) {
+        if (pages[i] >= e->n_pages)
+            return zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "page %u of entry %u outside the cache (%u pages)",
+                              pages[i], i, e->n_pages);
+        ident = ident && pages[i] == i;
+    }
+    EHIP(e, hipStreamSynchronize(e->ctx->stream));  // no step in flight reads the old table
+    EHIP(e, hipMemcpy(e->pages, pages, 4ull * n, hipMemcpyHostToDevice));
+    e->pages_ident = ident;
+    if (e->g_out) hipGraphExecDestroy(e->g_out);
+    if (e->g_noout) hipGraphExecDestroy(e->g_noout);
+    e->g_out = e->g_noout = nullptr;
+    return ZH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Host page pool: KvPagePool (src/scheduler/kv_cache.zig:43-125) -- a stack
+// of free page ids (allocation pops from the end, so a fresh pool hands out
+// pages in descending order), an owner per page, KvCacheExhausted when too
+// few pages are free.
+// ---------------------------------------------------------------------------
+struct zh_kv_pool {
+    std::vector<uint64_t> owner;  // request id + 1 (0: free)
+    std::vector<uint32_t> free_list;
+    uint32_t page_size = 16;
+};
+extern "C" int zh_kv_pool_create(uint32_t total_pages, uint32_t page_size, zh_kv_pool **out) {
+    if (!out || total_pages == 0 || page_size == 0) return ZH_ERR_INVALID_ARGUMENT;
+    zh_kv_pool *p = new zh_kv_pool;
+    p->owner.assign(total_pages, 0);
+    p->free_list.resize(total_pages);
+    for (uint32_t i = 0; i < total_pages; i++) p->free_list[i] = i;
+    p->page_size = page_size;
+    *out = p;
+    return ZH_OK;
+}
+extern "C" void zh_kv_pool_destroy(zh_kv_pool *p) { delete p; }
+extern "C" int zh_kv_pool_alloc(zh_kv_pool *p, uint64_t request_id, uint32_t count, uint32_t *page_ids) {
+    if (!p || (count && !page_ids)) return ZH_ERR_INVALID_ARGUMENT;
+    if (p->free_list.size() < count) return ZH_ERR_KV_CACHE_EXHAUSTED;
+    for (uint32_t i = 0; i < count; i++) {
+        const uint32_t id = p->free_list.back();
+        p->free_list.pop_back();
+        p->owner[id] = request_id + 1;
+        page_ids[i] = id;
+    }
+    return ZH_OK;
+}
+extern "C" void zh_kv_pool_free(zh_kv_pool *p, uint64_t request_id) {
+    if (!p) return;
+    for (uint32_t id = 0; id < (uint32_t)p->owner.size(); id++)
+        if (p->owner[id] == request_id + 1) {
+            p->owner[id] = 0;
+            p->free_list.push_back(id);
+        }
+}
+extern "C" uint32_t zh_kv_pool_free_count(const zh_kv_pool *p) { return p ? (uint32_t)p->free_list.size() : 0u; }
+extern "C" uint32_t zh_kv_pool_max_context(const zh_kv_pool *p, uint32_t page_count) {
+    return p ? page_count * p->page_size : 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -597,7 +675,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         if (mask & SK_ATTN)
             ERC(zhk_attn_decode_fused(c, e->q, e->k, e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc,
                                   e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads, m.n_kv_heads, pos,
-                                  m.max_ctx, scale, m.eps, e->fd_part, true));  // pages[i] = i (k_fill_pages)
+                                  m.max_ctx, scale, m.eps, e->fd_part, e->pages_ident));
         if (!(mask & SK_O)) {
         } else if (lpb_attn) {
             // the merge kernel already emitted the attention output as XQ
@@ -830,7 +908,9 @@ static int record_step_batch(zh_engine *const *es, uint32_t n, bool collect) {
         // launch (grid z = sequence) when they share a 1-4 q-head group,
         // else one launch each (forking the sequences onto auxiliary streams,
         // joined before O, measured slower than in-order launches)
-        if (m.n_heads / m.n_kv_heads <= 4) {
+        bool all_ident = true;  // the several-sequence kernel reads identity page tables only
+        for (uint32_t v = 0; v < n; v++) all_ident = all_ident && es[v]->pages_ident;
+        if (m.n_heads / m.n_kv_heads <= 4 && all_ident) {
             for (uint32_t v0 = 0; v0 < n; v0 += 4) {
                 const uint32_t nz = n - v0 < 4 ? n - v0 : 4;
                 const float *aq[4], *ak[4], *av[4];
@@ -855,7 +935,7 @@ static int record_step_batch(zh_engine *const *es, uint32_t n, bool collect) {
                 zh_pos_src pos{0, ev->st + ST_POS};
                 ERC(zhk_attn_decode_fused(c, ev->q, ev->k, ev->v, Wf(y.q_norm), Wf(y.k_norm), ev->rope_cs, yv.kc,
                                           yv.vc, ev->pages, ev->n_pages, m.max_ctx, ev->attn, ev->xq_q, m.n_heads,
-                                          m.n_kv_heads, pos, m.max_ctx, scale, m.eps, ev->fd_part, true));
+                                          m.n_kv_heads, pos, m.max_ctx, scale, m.eps, ev->fd_part, ev->pages_ident));
             }
         }
         // O (+ residual) on each sequence's XQ attention output

@@ -276,6 +276,7 @@ struct AttnP {
     uint32_t nq;
     uint32_t nd;         // AD_IDENT: target chunks per kv head
     uint32_t no_wait;    // the last arrival merges every q head (no merger waits for others)
+    uint32_t ident;      // k_attn_ring: the page table is the identity (no lookups)
 };
 
 ZH_DEV float sum8(float v) { return row8_sum(v); }  // over the 8 lanes of a token group
@@ -321,7 +322,8 @@ ZH_DEV const uint16_t *kv_row(const uint16_t *h, size_t pa, size_t pb, size_t pc
 // timed out) turns the outputs into NaN.
 template <int GM, int NBAT>
 ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // any workgroup size of at least AD_T threads (every thread calls it)
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nthr = blockDim.x;
     TRACE_OPS(11);
     // Chunk merge. The first batch of each thread's O dims (NBAT chunks) is
     // requested before the chunk statistics, so both arrive in about one
@@ -358,7 +360,7 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
     const bool one_batch = nv <= (uint32_t)NBAT;  // uniform
     if (one_batch) load_o(0);
     asm volatile("" ::: "memory");  // the O loads go out before the statistics loads
-    for (uint32_t g = wave; g < (uint32_t)GM; g += AD_W) {
+    for (uint32_t g = wave; g < (uint32_t)GM; g += nthr / 64) {
         const float *pp = p.part + (size_t)(h0 + g) * p.n_chunks * (FD_HD + 2);
         float m = -INFINITY, l = 0.f;
         for (uint32_t c = lane; c < nv; c += 64) {
@@ -379,7 +381,7 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
     const float Mt = hM[g_t];
     if (one_batch) {
         // weights exp(m_c - M) once per (head, chunk), in place in LDS
-        for (uint32_t i = tid; i < (uint32_t)GM * NBAT; i += AD_T) {
+        for (uint32_t i = tid; i < (uint32_t)GM * NBAT; i += nthr) {
             const uint32_t g = i / NBAT, c = i % NBAT;
             sm[g][c] = c < nv ? expf(sm[g][c] - hM[g]) : 0.f;
         }
@@ -422,7 +424,7 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
     if (p.xq) {
         __syncthreads();
         XQView v = xq_view(p.xq, p.nq * FD_HD / 32);
-        for (uint32_t o = tid; o < (uint32_t)GM * FD_HD; o += AD_T)  // whole 32-lane groups (GM*128 % 32 == 0)
+        for (uint32_t o = tid; o < (uint32_t)GM * FD_HD; o += nthr)  // whole 32-lane groups (GM*128 % 32 == 0)
             xq_store_block32(ob[o], o & 31, v, (h0 * FD_HD + o) / 32);
     }
     TRACE_OPS(5);
@@ -460,6 +462,8 @@ __global__ __launch_bounds__(AD_T, 1) void k_attn_decode_z(AttnP p0, AttnZ z) {
     }
 #include "zh_attn_body.inc"
 }
+
+#include "zh_attn_ring.inc"
 
 // partials: zhk_flash_decode_partials_bytes(nh, nkv, hd, max_seq) bytes; the
 // counter words at its end must be zero before the first launch (each
@@ -518,7 +522,8 @@ int zhk_flash_decode(zh_ctx *c, const float *q, const uint16_t *kc, const uint16
     p.q = q; p.kc = (uint16_t *)kc; p.vc = (uint16_t *)vc; p.pages = pages; p.n_pages = n_pages;
     p.cache_tokens = cache_tokens; p.pos = seq_len; p.scale = scale; p.part = partials;
     p.counters = attn_counters(partials, nh, nkv, hd, max_seq); p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
-    return attn_launch(c, p, nkv, nh / nkv, max_seq, false, false);
+    p.ident = 0;
+    return zhk_attn_ring(c, p, nkv, max_seq, false);
 }
 
 // RoPE table: cs[pos][i] = (cos, sin) of (float)pos * inv_freq[i], i < 64,
@@ -547,7 +552,11 @@ int zhk_attn_decode_fused(zh_ctx *c, const float *q, const float *k, const float
     p.kc = kc; p.vc = vc; p.pages = pages; p.n_pages = n_pages; p.cache_tokens = cache_tokens; p.pos = pos;
     p.scale = scale; p.eps = eps; p.part = partials; p.counters = attn_counters(partials, nh, nkv, FD_HD, max_seq);
     p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
-    return attn_launch(c, p, nkv, nh / nkv, max_seq, true, ident_pages);
+    // identity page table: the register-pipelined kernel (measured faster at a
+    // 4K context); any other table: the DMA ring kernel, which looks pages up
+    if (ident_pages) return attn_launch(c, p, nkv, nh / nkv, max_seq, true, true);
+    p.ident = 0;
+    return zhk_attn_ring(c, p, nkv, max_seq, true);
 }
 
 // zhk_attn_decode_fused for n <= 4 sequences at one position in one launch

@@ -35,6 +35,7 @@ extern "C" const char *zh_status_string(int s) {
     case ZH_ERR_TRUNCATED_FILE: return "TruncatedFile";
     case ZH_ERR_IO: return "IoError";
     case ZH_ERR_NOT_FOUND: return "NotFound";
+    case ZH_ERR_KV_CACHE_EXHAUSTED: return "KvCacheExhausted";
     default: return "unknown";
     }
 }

@@ -169,6 +169,11 @@ class InferenceEngine:
         self.ctx.check(lib().zh_engine_read_kv(self.h, layer, which, t0, n, C.c_void_p(out.ctypes.data)))
         return out
 
+    def set_pages(self, pages):
+        """The sequence's KV page table (logical page i -> physical pages[i])."""
+        a = np.ascontiguousarray(pages, dtype=np.uint32)
+        self.ctx.check(lib().zh_engine_set_pages(self.h, C.c_void_p(a.ctypes.data), len(a)))
+
     def bytes_per_token(self, L):
         return lib().zh_engine_bytes_per_token(self.h, L)
 
@@ -184,3 +189,42 @@ class InferenceEngine:
 
     def group_bytes(self, group, L):
         return lib().zh_engine_group_bytes(self.h, self.GROUPS[group], L)
+
+
+class KvPagePool:
+    """KvPagePool (src/scheduler/kv_cache.zig:43-125) over zh_kv_pool_*:
+    alloc_pages pops page ids off a free stack (a fresh pool hands them out
+    in descending order) and raises ZincError("KvCacheExhausted") when too few
+    are free; free_pages returns every page a request owns."""
+
+    def __init__(self, total_pages, page_size=16):
+        h = C.c_void_p()
+        rc = lib().zh_kv_pool_create(total_pages, page_size, C.byref(h))
+        if rc != hip.OK:
+            raise hip.ZincError(rc, "zh_kv_pool_create")
+        self.h = h
+        self.page_size = page_size
+
+    def alloc_pages(self, request_id, count):
+        out = np.empty(count, dtype=np.uint32)
+        rc = lib().zh_kv_pool_alloc(self.h, request_id, count, C.c_void_p(out.ctypes.data))
+        if rc != hip.OK:
+            raise hip.ZincError(rc, f"alloc {count} pages")
+        return out
+
+    def free_pages(self, request_id):
+        lib().zh_kv_pool_free(self.h, request_id)
+
+    def free_count(self):
+        return lib().zh_kv_pool_free_count(self.h)
+
+    def max_context(self, page_count):
+        return lib().zh_kv_pool_max_context(self.h, page_count)
+
+    def close(self):
+        if self.h:
+            lib().zh_kv_pool_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()

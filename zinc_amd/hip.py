@@ -18,7 +18,7 @@ OK = 0
 STATUS = {1: "UnsupportedQuantType", 2: "InvalidArgument", 3: "HipError",
           4: "ContextLengthExceeded", 5: "OutOfMemory", 6: "TensorNotFound", 7: "InvalidMagic",
           8: "UnknownMetadataType", 9: "UnsupportedArchitecture", 10: "TruncatedFile", 11: "IoError",
-          12: "NotFound"}
+          12: "NotFound", 13: "KvCacheExhausted"}
 
 BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), MXFP4: (32, 17), F32: (1, 4), F16: (1, 2)}
 
@@ -122,6 +122,13 @@ SIGNATURES = {
     "zh_engine_hidden": (_i32, [_P, _P]),
     "zh_engine_tensor": (_i32, [_P, _u64, C.POINTER(_P), C.POINTER(_u64), C.POINTER(_u64)]),
     "zh_engine_read_kv": (_i32, [_P, _u32, _u32, _u32, _u32, _P]),
+    "zh_engine_set_pages": (_i32, [_P, _P, _u32]),
+    "zh_kv_pool_create": (_i32, [_u32, _u32, C.POINTER(_P)]),
+    "zh_kv_pool_destroy": (None, [_P]),
+    "zh_kv_pool_alloc": (_i32, [_P, _u64, _u32, _P]),
+    "zh_kv_pool_free": (None, [_P, _u64]),
+    "zh_kv_pool_free_count": (_u32, [_P]),
+    "zh_kv_pool_max_context": (_u32, [_P, _u32]),
     "zh_engine_bytes_per_token": (_u64, [_P, _u32]),
     "zh_engine_time_kernel": (_i32, [_P, _u32, _u32, _P]),
     "zh_engine_group_bytes": (_u64, [_P, _u32, _u32]),
