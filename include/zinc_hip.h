@@ -94,22 +94,30 @@ int zh_synth_vector(zh_ctx *ctx, zh_buf *buf, uint64_t offset, uint32_t kind, ui
 /* y[y_off..] (=, or += when acc_mode==1) = dequant(W[a_off..]) (MxK) * x[x_off..].
  * Replaces DmmvDispatch.recordDispatch (dmmv.zig:806-874) / dispatchDmmvInner
  * (forward.zig:8431-8540) with DmmvPushConstants{M,K,a_offset,x_offset,
- * y_offset,acc_mode} (dmmv.zig:21-28). Offsets are BYTES. qtype: Q4_K, Q5_K, Q6_K,
- * Q8_0 (K % 64 == 0), MXFP4 (K % 32 == 0). K % 256 == 0 for K-quants. */
+ * y_offset,acc_mode} (dmmv.zig:21-28). Offsets are BYTES (4-byte aligned; a_off
+ * 16-byte aligned for Q4_K). qtype: Q4_K, Q5_K, Q6_K (K % 256 == 0), Q8_0 and
+ * MXFP4 (K % 32 == 0). */
 int zh_dmmv(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off,
             const zh_buf *x, uint64_t x_off, zh_buf *y, uint64_t y_off,
             uint32_t M, uint32_t K, uint32_t acc_mode);
+/* 1 when zh_dmmv / zh_dmmv_xq / zh_dmmv_moe have a kernel for (qtype, K), 0
+ * otherwise -- the counterpart of DmmvDispatch.pipelineForType returning null
+ * (dmmv.zig:676-690), so a caller can fall back before it calls. */
+int zh_dmmv_supported(uint32_t qtype, uint32_t K);
 /* Batched DMMV (a skinny GEMM over num_cols activation vectors): replaces
  * DmmvDispatch.recordBatchDispatchPush (dmmv.zig:880-925, BatchDmmvPushConstants
  * {M,K,a_offset,x_offset,y_offset,num_cols} dmmv.zig:31-38; dmmv_q4k_batch.comp /
  * dmmv_q6k_batch.comp). X: f32 [num_cols][K] (column v at X + v*K*4 bytes,
  * 16-byte aligned offset); Y: f32 [num_cols][M] (= or += when acc_mode == 1).
  * qtype Q4_K or Q6_K, K % 256 == 0, num_cols 1..ZH_DMMV_MAX_COLS. The weights
- * stream from HBM once for all columns; each column's result equals zh_dmmv on
- * that column bit for bit. */
+ * stream from HBM once for all columns. */
 #define ZH_DMMV_MAX_COLS 16
 int zh_dmmv_batched(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t a_off, const zh_buf *X, uint64_t x_off,
                     zh_buf *Y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t num_cols, uint32_t acc_mode);
+/* (The columns agree with zh_dmmv run per column to the f32 summation
+ * floor; bit for bit where zh_dmmv runs the same tile kernels, i.e. not for
+ * Q4_K at K = 2048 / 4096, which zh_dmmv streams with another summation
+ * order.) */
 /* Y[v] = silu(Wg X[v]) * (Wu X[v]) for v < num_cols (Q4_K), the batched form of
  * zh_dmmv_fused_gate_up_swiglu below; layouts as zh_dmmv_batched. */
 int zh_dmmv_fused_gate_up_swiglu_batched(zh_ctx *ctx, uint32_t qtype, const zh_buf *Wg, uint64_t g_off,
@@ -123,7 +131,10 @@ int zh_dmmv_fused_gate_up_swiglu(zh_ctx *ctx, uint32_t qtype, const zh_buf *Wg, 
 /* Expert-gathered DMMV (recordMoeDispatch, dmmv.zig:709; MoeDmmvPushConstants
  * dmmv.zig:41-48; dmmv_q4k_moe_kpar.comp:56-95): for slot s < n_used,
  * e = routing[s] (u32 ids at the start of `routing`),
- * y[y_off + s*M*4 ..] = W[e*expert_stride ..] * x[x_off + s*x_expert_stride*4 ..]. */
+ * y[y_off + s*M*4 ..] = W[e*expert_stride ..] * x[x_off + s*x_expert_stride*4 ..].
+ * The ids are read on the device only (the call enqueues and returns): an id
+ * at or past the experts W holds is clamped to the last one, and the next
+ * zh_sync returns ZH_ERR_INVALID_ARGUMENT for it. */
 int zh_dmmv_moe(zh_ctx *ctx, uint32_t qtype, const zh_buf *W, uint64_t expert_stride,
                 const zh_buf *routing, const zh_buf *x, uint32_t x_expert_stride, uint64_t x_off,
                 zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t n_used);

@@ -54,3 +54,15 @@ def test_no_device_reports_error_not_crash():
     import pytest
     with pytest.raises(zinc_amd.ZincError):
         zinc_amd.Context(0)
+
+
+def test_dmmv_supported_query():
+    """zh_dmmv_supported: the counterpart of pipelineForType returning null
+    (dmmv.zig:676-690), answered on the host without a device."""
+    import zinc_amd
+    f = zinc_amd.lib().zh_dmmv_supported
+    assert f(12, 4096) == 1 and f(14, 12288) == 1 and f(13, 4096) == 1
+    assert f(12, 4000) == 0 and f(14, 128) == 0  # K-quants need whole 256-element super-blocks
+    assert f(8, 96) == 1 and f(8, 4096) == 1 and f(8, 100) == 0  # Q8_0: any whole number of 32-blocks
+    assert f(39, 2880) == 1 and f(39, 2890) == 0
+    assert f(1, 4096) == 0 and f(2, 4096) == 0 and f(0, 4096) == 0  # no DMMV kernel for f16 / f32 / Q4_0

@@ -313,6 +313,40 @@ struct FmtQ80 {
     }
 };
 
+// Q8_0 with K % 64 == 32 (GGUF's Q8_0 rows are any whole number of blocks):
+// one 34-byte block per unit. A row of an odd block count is 2 bytes off a
+// dword boundary every other row, so the block is read with dword-aligned
+// loads and realigned (byte shift sh = 0 or 2).
+struct FmtQ80s {
+    static constexpr int EPU = 32, RAW = 10, QK = 32, BPB = 34;
+    ZH_DEVM static void load_x(XReg &xr, XQView v, int u) {
+        load_limbs(xr.L, v.limb + (size_t)u * 96, 24);
+        xr.xs[0] = v.xs[u];
+    }
+    ZH_DEVM static void load_raw(const uint8_t *row, int u, uint32_t *raw) {
+        const uint8_t *b = row + (size_t)u * 34;
+        const uintptr_t a = (uintptr_t)b & ~(uintptr_t)3;
+        const u32x4 t0 = *(const u32x4_a4 *)a, t1 = *(const u32x4_a4 *)(a + 16);
+        raw[0] = t0.x; raw[1] = t0.y; raw[2] = t0.z; raw[3] = t0.w;
+        raw[4] = t1.x; raw[5] = t1.y; raw[6] = t1.z; raw[7] = t1.w;
+        raw[8] = *(const uint32_t *)(a + 32);
+        raw[9] = (uint32_t)((uintptr_t)b & 3);
+    }
+    ZH_DEVM static float compute(const uint32_t *raw, const XReg &xr, int u) {
+        const uint32_t sh = raw[9];
+        int D[3] = {0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            // quant dword i = block bytes 2 + 4i .. : stream offset sh + 2 + 4i
+            const uint32_t q = sh ? raw[i + 1] : __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2);
+#pragma unroll
+            for (int k = 0; k < 3; k++) D[k] = sdot4(q, xr.L[k * 8 + i], D[k]);
+        }
+        const float d = h2f(sh ? raw[0] >> 16 : raw[0]);
+        return d * xr.xs[0] * comb_f32(D[0], D[1], D[2]);
+    }
+};
+
 // ---------------------------------------------------------------------------
 // MXFP4: 17-byte blocks {e8m0 e, 16 B of E2M1 codes}; low nibble -> element j,
 // high -> j+16 (forward.zig:441-459). Unit = one block (32 elements).
@@ -376,6 +410,7 @@ struct DmmvP {
     uint32_t acc;
     const uint32_t *routing;  // MoE: expert id per grid.y slot
     uint32_t n_experts;       // MoE: ids are clamped below this (a NaN router yields id ~0)
+    uint32_t *err;            // MoE, optional: ZH_DEVERR_EXPERT_ID when an id was clamped
     uint64_t expert_stride, xq_slot_stride;
     uint32_t y_slot_stride;
     // Plain mode may stack up to three matrices that share K and x (Q/K/V):
@@ -445,7 +480,9 @@ __global__ __launch_bounds__(NW == 1 ? 256 : NW * 64) void k_dmmv(DmmvP p) {
     float *y = p.y;
     if (MOE) {
         const uint32_t slot = blockIdx.y;
-        const uint64_t e = min(p.routing[slot], p.n_experts - 1);
+        const uint32_t id = p.routing[slot];
+        if (p.err && id >= p.n_experts && blockIdx.x == 0 && threadIdx.x == 0) atomicOr(p.err, ZH_DEVERR_EXPERT_ID);
+        const uint64_t e = min(id, p.n_experts - 1);
         Wm[0] += e * p.expert_stride;
         if (NM == 2) Wm[1] += e * p.expert_stride;
         xqb += slot * p.xq_slot_stride;
@@ -579,7 +616,8 @@ static int launch_dmmv(zh_ctx *c, uint32_t qtype, const DmmvP &p, uint32_t n_slo
     case ZH_Q4_K: return launch_fmt<FmtQ4K, MODE, MOE>(c, p, n_slots);
     case ZH_Q5_K: return launch_fmt<FmtQ5K, MODE, MOE>(c, p, n_slots);
     case ZH_Q6_K: return launch_fmt<FmtQ6K, MODE, MOE>(c, p, n_slots);
-    case ZH_Q8_0: return launch_fmt<FmtQ80, MODE, MOE>(c, p, n_slots);
+    case ZH_Q8_0:
+        return p.K % 64 ? launch_fmt<FmtQ80s, MODE, MOE>(c, p, n_slots) : launch_fmt<FmtQ80, MODE, MOE>(c, p, n_slots);
     case ZH_MXFP4: return launch_fmt<FmtMXFP4, MODE, MOE>(c, p, n_slots);
     default: return zh_set_err(c, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "qtype %u has no DMMV kernel", qtype);
     }
@@ -591,7 +629,7 @@ static int check_k(zh_ctx *c, uint32_t qtype, uint32_t K) {
         if (K % 256) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "K=%u not a multiple of 256", K);
         return ZH_OK;
     case ZH_Q8_0:
-        if (K % 64) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "Q8_0 needs K %% 64 == 0 (K=%u)", K);
+        if (K % 32) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "K=%u not a multiple of 32", K);
         return ZH_OK;
     case ZH_MXFP4:
         if (K % 32) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "K=%u not a multiple of 32", K);
@@ -650,10 +688,11 @@ int zhk_dmmv_gate_up(zh_ctx *c, uint32_t qtype, const uint8_t *Wg, const uint8_t
 
 int zhk_dmmv_moe(zh_ctx *c, uint32_t qtype, const uint8_t *W, uint64_t expert_stride,
                  const uint32_t *routing, const void *xq, uint64_t xq_slot_stride, float *y, uint32_t M,
-                 uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2, uint32_t n_experts) {
+                 uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2, uint32_t n_experts, uint32_t *err) {
     if (n_experts == 0) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "n_experts");
     DmmvP p = {};
     p.n_experts = n_experts;
+    p.err = err;
     p.W = W; p.W2 = W2 ? W2 : W; p.xq = (const uint8_t *)xq; p.y = y; p.M = M; p.K = K;
     p.row_bytes = zh_tensor_bytes(qtype, 1, K);
     p.routing = routing; p.expert_stride = expert_stride; p.xq_slot_stride = xq_slot_stride;
@@ -1034,6 +1073,17 @@ static int try_ftile(zh_ctx *c, uint32_t qtype, const uint8_t *W, const void *xq
 // ---------------------------------------------------------------------------
 static bool in_range(const zh_buf *b, uint64_t off, uint64_t n) { return b && off <= b->size && n <= b->size - off; }
 
+extern "C" int zh_dmmv_supported(uint32_t qtype, uint32_t K) {
+    // the team kernel covers up to 512 units of a row (64 elements per unit
+    // for the K-quants and K % 64 == 0 Q8_0, 32 for MXFP4 and odd-block Q8_0)
+    switch (qtype) {
+    case ZH_Q4_K: case ZH_Q5_K: case ZH_Q6_K: return K > 0 && K % 256 == 0 && K / 64 <= 512 ? 1 : 0;
+    case ZH_Q8_0: return K > 0 && K % 32 == 0 && K / (K % 64 ? 32 : 64) <= 512 ? 1 : 0;
+    case ZH_MXFP4: return K > 0 && K % 32 == 0 && K / 32 <= 512 ? 1 : 0;
+    default: return 0;
+    }
+}
+
 extern "C" int zh_dmmv(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t a_off, const zh_buf *x,
                        uint64_t x_off, zh_buf *y, uint64_t y_off, uint32_t M, uint32_t K, uint32_t acc_mode) {
     if (!c) return ZH_ERR_INVALID_ARGUMENT;
@@ -1157,12 +1207,10 @@ extern "C" int zh_dmmv_moe(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t 
     if (!in_range(x, x_off, ((uint64_t)(n_used - 1) * x_expert_stride + K) * 4) ||
         !in_range(y, y_off, (uint64_t)n_used * M * 4) || (x_off & 3) || (y_off & 3))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "x/y range");
-    // Expert ids are validated on the host against the weight buffer size.
-    std::vector<uint32_t> ids(n_used);
-    if ((rc = zh_buf_download(c, routing, 0, ids.data(), n_used * 4ull))) return rc;
-    for (uint32_t s = 0; s < n_used; s++)
-        if (!in_range(W, (uint64_t)ids[s] * expert_stride, zh_tensor_bytes(qtype, M, K)))
-            return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "expert id %u out of range", ids[s]);
+    if (!in_range(W, 0, zh_tensor_bytes(qtype, M, K))) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "W range");
+    // Expert ids stay on the device: the kernel clamps each to the experts
+    // the weight buffer holds and flags a clamped id in the context's error
+    // word, which zh_sync reports (the call itself only enqueues).
     void *xq;
     uint64_t xqs = zh_xq_bytes_int(K);
     if ((rc = zh_scratch(c, xqs * n_used, &xq))) return rc;
@@ -1170,7 +1218,7 @@ extern "C" int zh_dmmv_moe(zh_ctx *c, uint32_t qtype, const zh_buf *W, uint64_t 
         return rc;
     return zhk_dmmv_moe(c, qtype, (const uint8_t *)W->ptr, expert_stride, (const uint32_t *)routing->ptr, xq, xqs,
                         (float *)((char *)y->ptr + y_off), M, K, n_used, 0, nullptr,
-                        (uint32_t)((W->size - zh_tensor_bytes(qtype, M, K)) / expert_stride + 1));
+                        (uint32_t)((W->size - zh_tensor_bytes(qtype, M, K)) / expert_stride + 1), c->err_dev);
 }
 
 // ---------------------------------------------------------------------------

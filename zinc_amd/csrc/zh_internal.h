@@ -39,7 +39,11 @@ struct zh_ctx {
     // sharing weights): kernels must not wait on workgroups of their own grid
     // that may not be resident (the attention merge then needs no waiting).
     bool concurrent = false;
+    // Device error word: kernels OR in ZH_DEVERR_* bits for input they had
+    // to clamp (the launch still completes); zh_sync reports and clears it.
+    uint32_t *err_dev = nullptr;
 };
+enum : uint32_t { ZH_DEVERR_EXPERT_ID = 1u };
 
 int zh_set_err(zh_ctx *ctx, int code, const char *fmt, ...);
 #define ZH_HIP(ctx, call)                                                                    \
@@ -101,7 +105,8 @@ int zhk_dmmv_lds_down_acc(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint64_
                           uint32_t M, uint32_t K);
 int zhk_dmmv_moe(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint64_t expert_stride,
                  const uint32_t *routing, const void *xq, uint64_t xq_slot_stride, float *y,
-                 uint32_t M, uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2, uint32_t n_experts);
+                 uint32_t M, uint32_t K, uint32_t n_used, int gate_up, const uint8_t *W2, uint32_t n_experts,
+                 uint32_t *err = nullptr);
 int zhk_dequant_rows(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint32_t row0, uint32_t n_rows,
                      uint32_t K, float *out, const uint32_t *row_from_dev, uint32_t clamp_rows, uint32_t gather = 0);
 int zhk_synth_tensor(zh_ctx *ctx, uint8_t *dst, uint32_t qtype, uint64_t rows, uint64_t cols,

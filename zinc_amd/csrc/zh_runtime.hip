@@ -55,6 +55,10 @@ extern "C" int zh_init(int device, zh_ctx **out) {
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) { delete c; return ZH_ERR_HIP; }
     for (int i = 0; i < 64; i++)
         if (hipEventCreate(&c->ev[i]) != hipSuccess) { delete c; return ZH_ERR_HIP; }
+    if (hipMalloc((void **)&c->err_dev, 256) != hipSuccess || hipMemset(c->err_dev, 0, 4) != hipSuccess) {
+        zh_destroy(c);
+        return ZH_ERR_HIP;
+    }
     *out = c;
     return ZH_OK;
 }
@@ -64,6 +68,7 @@ extern "C" void zh_destroy(zh_ctx *c) {
     hipSetDevice(c->device);
     hipStreamSynchronize(c->stream);
     if (c->scratch) hipFree(c->scratch);
+    if (c->err_dev) hipFree(c->err_dev);
     for (int i = 0; i < 64; i++) if (c->ev[i]) hipEventDestroy(c->ev[i]);
     hipStreamDestroy(c->stream);
     delete c;
@@ -84,6 +89,15 @@ extern "C" int zh_device_info(zh_ctx *c, char *name, size_t name_len, int *cu, u
 extern "C" int zh_sync(zh_ctx *c) {
     if (!c) return ZH_ERR_INVALID_ARGUMENT;
     ZH_HIP(c, hipStreamSynchronize(c->stream));
+    // input a kernel had to clamp since the last zh_sync
+    uint32_t e = 0;
+    ZH_HIP(c, hipMemcpy(&e, c->err_dev, 4, hipMemcpyDeviceToHost));
+    if (e) {
+        ZH_HIP(c, hipMemset(c->err_dev, 0, 4));
+        if (e & ZH_DEVERR_EXPERT_ID)
+            return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "an expert id at or past the weights' expert count "
+                                                          "(zh_dmmv_moe clamped it to the last expert)");
+    }
     return ZH_OK;
 }
 

@@ -123,6 +123,7 @@ SIGNATURES = {
     "zh_engine_tensor": (_i32, [_P, _u64, C.POINTER(_P), C.POINTER(_u64), C.POINTER(_u64)]),
     "zh_engine_read_kv": (_i32, [_P, _u32, _u32, _u32, _u32, _P]),
     "zh_engine_set_pages": (_i32, [_P, _P, _u32]),
+    "zh_dmmv_supported": (_i32, [_u32, _u32]),
     "zh_kv_pool_create": (_i32, [_u32, _u32, C.POINTER(_P)]),
     "zh_kv_pool_destroy": (None, [_P]),
     "zh_kv_pool_alloc": (_i32, [_P, _u64, _u32, _P]),
