@@ -361,8 +361,8 @@ int zh_gguf_get_string(const zh_gguf *f, const char *key, const char **s, uint64
 /* Metadata entry i: key, value tag, and for arrays the element tag and count. */
 int zh_gguf_metadata_entry(const zh_gguf *f, uint64_t i, const char **key, uint32_t *type, uint32_t *elem_type,
                            uint64_t *count);
-/* extractConfig (loader.zig:81-346) for the families on the path (qwen2 /
- * qwen3 dense, qwen2moe / qwen3moe): dimensions, eps, rope base, experts,
+/* extractConfig (loader.zig:81-346) for the architectures on the path,
+ * qwen3 (dense) and qwen3moe: dimensions, eps, rope base, experts,
  * vocab (metadata, else output.weight / token_embd.weight rows), with the
  * per-class types read from blk.0's tensors (type_more_bits 0: the engine
  * takes each tensor's own type from the file). max_ctx is the caller's KV
