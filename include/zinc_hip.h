@@ -187,6 +187,19 @@ int zh_flash_decode(zh_ctx *ctx, const zh_buf *q, const zh_buf *k_cache, const z
                     const zh_buf *page_table, uint32_t n_pages, uint32_t cache_tokens, zh_buf *out,
                     uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_len,
                     float attn_scale);
+/* zh_flash_decode that allocates nothing (no counterpart in the reference;
+ * for callers that cannot allocate: code under HIP graph capture, serving
+ * loops that forbid allocation). Same arguments and result as
+ * zh_flash_decode, bit for bit. The split-K partials and merge counters live
+ * in a 2 MiB device array per GPU, held until the process ends, instead of
+ * the context's scratch; a shape whose partials exceed it is rejected with
+ * ZH_ERR_INVALID_ARGUMENT (head_dim 128, GQA group <= 8 and <= 256 CUs always
+ * fit). Every call on one GPU shares that array: calls that overlap on one
+ * GPU (other streams, other contexts) race. */
+int zh_flash_decode_noalloc(zh_ctx *ctx, const zh_buf *q, const zh_buf *k_cache, const zh_buf *v_cache,
+                            const zh_buf *page_table, uint32_t n_pages, uint32_t cache_tokens, zh_buf *out,
+                            uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_len,
+                            float attn_scale);
 /* Causal batched attention for prefill (flash_attn_batched.comp via
  * AttentionDispatch.recordFlashAttnBatched, attention.zig:240-316): queries
  * seq_start .. seq_start+n_queries-1 (q: f32 [n_queries][n_heads*head_dim],

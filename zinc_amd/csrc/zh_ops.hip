@@ -1,5 +1,7 @@
 // zh_ops.hip — RMSNorm, fused QK-norm/RoPE/KV write, split-context
 // flash-decode with LSE merge, SwiGLU, MoE routing and argmax for gfx950.
+#include <mutex>
+
 #include "zh_device.h"
 #include "zh_internal.h"
 
@@ -515,14 +517,24 @@ static uint32_t *attn_counters(float *partials, uint32_t nh, uint32_t nkv, uint3
     return (uint32_t *)((char *)partials + (uint64_t)nh * attn_n_chunks(max_seq, attn_nd(nkv, 256)) * (hd + 2) * 4);
 }
 
+// Partials of the C-ABI decode attention (the DMA ring kernel): nh x nd
+// chunk partials of 130 f32, then one merge counter per kv head.
+static uint64_t ring_partials_bytes(uint32_t nh, uint32_t nkv, int cu_count) {
+    return (uint64_t)nh * attn_nd(nkv, cu_count) * (FD_HD + 2) * 4 + 4ull * nkv;
+}
+static uint32_t *ring_counters(float *partials, uint32_t nh, uint32_t nkv, int cu_count) {
+    return (uint32_t *)(partials + (uint64_t)nh * attn_nd(nkv, cu_count) * (FD_HD + 2));
+}
+
 int zhk_flash_decode(zh_ctx *c, const float *q, const uint16_t *kc, const uint16_t *vc, const uint32_t *pages,
                      uint32_t n_pages, uint32_t cache_tokens, float *out, void *xq_out, uint32_t nh, uint32_t nkv,
                      uint32_t hd, zh_pos_src seq_len, uint32_t max_seq, float scale, float *partials) {
     AttnP p = {};
     p.q = q; p.kc = (uint16_t *)kc; p.vc = (uint16_t *)vc; p.pages = pages; p.n_pages = n_pages;
     p.cache_tokens = cache_tokens; p.pos = seq_len; p.scale = scale; p.part = partials;
-    p.counters = attn_counters(partials, nh, nkv, hd, max_seq); p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
+    p.counters = ring_counters(partials, nh, nkv, c->cu_count); p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh;
     p.ident = 0;
+    (void)hd;
     return zhk_attn_ring(c, p, nkv, max_seq, false);
 }
 
@@ -612,9 +624,73 @@ extern "C" int zh_flash_decode(zh_ctx *c, const zh_buf *q, const zh_buf *kc, con
         !in_range(pages, 0, 4ull * n_pages))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "flash_decode range");
     void *scr;
-    int rc = zh_scratch(c, zhk_flash_decode_partials_bytes(nh, nkv, hd, seq_len), &scr);
+    int rc = zh_scratch(c, ring_partials_bytes(nh, nkv, c->cu_count), &scr);
     if (rc) return rc;
-    ZH_HIP(c, hipMemsetAsync(attn_counters((float *)scr, nh, nkv, hd, seq_len), 0, 4ull * nh, c->stream));
+    ZH_HIP(c, hipMemsetAsync(ring_counters((float *)scr, nh, nkv, c->cu_count), 0, 4ull * nkv, c->stream));
+    float scale = attn_scale != 0.f ? attn_scale : 1.0f / sqrtf((float)hd);
+    return zhk_flash_decode(c, (const float *)q->ptr, (const uint16_t *)kc->ptr, (const uint16_t *)vc->ptr,
+                            (const uint32_t *)pages->ptr, n_pages, cache_tokens, (float *)out->ptr, nullptr, nh, nkv,
+                            hd, zh_pos_src{seq_len, nullptr}, seq_len, scale, (float *)scr);
+}
+
+// ---------------------------------------------------------------------------
+// zh_flash_decode without allocation: the split-K partials and the merge
+// counters live in a file-scope device array (one copy per GPU, held until
+// the process ends) instead of the context's growable scratch. In host code
+// the array's name is only a stand-in: its device address on the current
+// GPU comes from hipGetSymbolAddress, looked up once per device on the first
+// call there and kept per device.
+// ---------------------------------------------------------------------------
+constexpr uint64_t FD_NOALLOC_BYTES = 2ull << 20;  // partials (nh x chunks x 130 f32) + counters
+static __device__ __align__(256) uint8_t scratch[FD_NOALLOC_BYTES];
+
+__global__ void k_zero_u32(uint32_t *p, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+static int noalloc_scratch(zh_ctx *c, void **out) {
+    static std::mutex mu;
+    static void *ptr[64] = {};
+    if (c->device < 0 || c->device >= 64) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "device %d", c->device);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[c->device]) {
+        ZH_HIP(c, hipSetDevice(c->device));
+        void *p = nullptr;
+        ZH_HIP(c, hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return zh_set_err(c, ZH_ERR_HIP, "no device address for the no-alloc scratch");
+        ptr[c->device] = p;
+    }
+    *out = ptr[c->device];
+    return ZH_OK;
+}
+
+extern "C" int zh_flash_decode_noalloc(zh_ctx *c, const zh_buf *q, const zh_buf *kc, const zh_buf *vc,
+                                       const zh_buf *pages, uint32_t n_pages, uint32_t cache_tokens, zh_buf *out,
+                                       uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t seq_len, float attn_scale) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    if (hd != FD_HD) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "head_dim %u unsupported (128 only)", hd);
+    if (nkv == 0 || nh % nkv || nh / nkv > FD_MAXG || ((nh / nkv) & (nh / nkv - 1)) || seq_len == 0)
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "heads/seq_len");
+    if ((seq_len + 15) / 16 > n_pages) return zh_set_err(c, ZH_ERR_CONTEXT_LENGTH_EXCEEDED, "seq_len %u", seq_len);
+    if (!in_range(q, 0, 4ull * nh * hd) || !in_range(out, 0, 4ull * nh * hd) ||
+        !in_range(kc, 0, 2ull * nkv * cache_tokens * hd) || !in_range(vc, 0, 2ull * nkv * cache_tokens * hd) ||
+        !in_range(pages, 0, 4ull * n_pages))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "flash_decode range");
+    // the same partials layout as zh_flash_decode's scratch (counters after
+    // the partials), which must fit the array
+    const uint64_t need = ring_partials_bytes(nh, nkv, c->cu_count);
+    if (need > FD_NOALLOC_BYTES)
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "flash_decode_noalloc: %llu bytes of partials exceed its %llu",
+                          (unsigned long long)need, (unsigned long long)FD_NOALLOC_BYTES);
+    void *scr;
+    int rc = noalloc_scratch(c, &scr);
+    if (rc) return rc;
+    // the merge counters start at zero (a fill kernel, not a memset node, so
+    // the call may be captured into a graph)
+    uint32_t *cnt = ring_counters((float *)scr, nh, nkv, c->cu_count);
+    hipLaunchKernelGGL(k_zero_u32, dim3((nkv + 255) / 256), dim3(256), 0, c->stream, cnt, nkv);
+    ZH_LAUNCH_CHECK(c);
     float scale = attn_scale != 0.f ? attn_scale : 1.0f / sqrtf((float)hd);
     return zhk_flash_decode(c, (const float *)q->ptr, (const uint16_t *)kc->ptr, (const uint16_t *)vc->ptr,
                             (const uint32_t *)pages->ptr, n_pages, cache_tokens, (float *)out->ptr, nullptr, nh, nkv,

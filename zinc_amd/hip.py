@@ -106,6 +106,7 @@ SIGNATURES = {
     "zh_qk_norm_rope_kv_write": (_i32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _u32, _u32, _u32, _u32, _u32,
                                         _u32, _f32]),
     "zh_flash_decode": (_i32, [_P, _P, _P, _P, _P, _u32, _u32, _P, _u32, _u32, _u32, _u32, _f32]),
+    "zh_flash_decode_noalloc": (_i32, [_P, _P, _P, _P, _P, _u32, _u32, _P, _u32, _u32, _u32, _u32, _f32]),
     "zh_softmax_topk": (_i32, [_P, _P, _u32, _u32, _P]),
     "zh_moe_weighted_acc": (_i32, [_P, _P, _P, _P, _u32, _u32, _u32]),
     "zh_argmax": (_i32, [_P, _P, _u32, _P, _u64]),
@@ -337,6 +338,11 @@ class Context:
     def flash_decode(self, q, kc, vc, pages, n_pages, cache_tokens, out, nh, nkv, hd, seq_len, attn_scale=0.0):
         self.check(lib().zh_flash_decode(self.h, q.h, kc.h, vc.h, pages.h, n_pages, cache_tokens, out.h, nh,
                                          nkv, hd, seq_len, attn_scale))
+
+    def flash_decode_noalloc(self, q, kc, vc, pages, n_pages, cache_tokens, out, nh, nkv, hd, seq_len,
+                             attn_scale=0.0):
+        self.check(lib().zh_flash_decode_noalloc(self.h, q.h, kc.h, vc.h, pages.h, n_pages, cache_tokens, out.h,
+                                                 nh, nkv, hd, seq_len, attn_scale))
 
     def softmax_topk(self, logits, n, k, routing):
         self.check(lib().zh_softmax_topk(self.h, logits.h, n, k, routing.h))
