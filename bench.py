@@ -27,6 +27,16 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def stream_ceiling(ctx, nbytes=1 << 30):
+    """Measured streaming-read rate (zh_stream_read_probe: the counterpart of
+    the reference's bandwidth microbenchmark) over nbytes, in GB/s."""
+    buf = ctx.alloc(nbytes)
+    ctx.synth_vector(buf, 0, 1, nbytes // 2, 1.0, 7, 7)  # touch the pages
+    gbs = ctx.stream_read_probe(buf, nbytes, 10)
+    ctx.free(buf)
+    return gbs
+
+
 def kernel_roofline(eng, L):
     """Per-kernel bandwidth of every per-layer launch group of the decode step
     (benchmarks.roofline_probe: the engine replays its own launches with HIP
@@ -42,7 +52,7 @@ def kernel_roofline(eng, L):
     if os.path.exists(pm):
         m = re.search(r"^traffic_bytes_per_launch\[%s\]: (\d+)" % dom, open(pm).read(), re.M)
         traffic = int(m.group(1)) if m else None
-    roof = {"kernel": r["kernel"], "bound": "hbm", "achieved": r["achieved_GBs"], "peak": PEAK_HBM_GBS,
+    roof = {"kernel": eng.group_kernels(dom), "bound": "hbm", "achieved": r["achieved_GBs"], "peak": PEAK_HBM_GBS,
             "unit": "GB/s", "frac": r["frac"], "traffic": traffic, "bytes_per_launch": r["bytes_per_launch"],
             "us_per_launch": r["us_per_launch"], "group": dom}
     per = {g: {"us": v["us_per_launch"], "GBs": v["achieved_GBs"], "frac": v["frac"]} for g, v in rows.items()}
@@ -55,7 +65,8 @@ def cpu_baseline(cfg, n_tokens=16):
     `n_tokens` tokens of the same model at position PREFILL."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
-    threads = min(os.cpu_count() or 1, 16)
+    nproc = os.cpu_count() or 1
+    threads = min(nproc, 16)
     t0 = time.time()
     om = orc.Model(cfg, nthreads=threads)
     om.prefill_kv_random(PREFILL, 7)
@@ -66,7 +77,8 @@ def cpu_baseline(cfg, n_tokens=16):
         tok = om.decode_step(tok, PREFILL + i)
     dt = time.time() - t0
     om.close()
-    return {"value": round(n_tokens / dt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+    return {"value": round(n_tokens / dt, 4), "unit": "tok/s", "cores": threads, "threads": threads,
+            "nproc": nproc, "kind": "port",
             "sample": f"{n_tokens} greedy decode steps of the same 8B-shaped model at context {PREFILL} "
                       f"(oracle build {build_s:.0f}s untimed)"}
 
@@ -121,8 +133,19 @@ def main():
 
     # per-kernel bandwidth (after the timed region; it changes the activations)
     roof, per_kernel = kernel_roofline(eng, pos + args.steps)
-    log(f"dominant kernel ({roof['group']}): {roof['achieved']} GB/s ({roof['frac']:.1%}), "
-        f"{roof['us_per_launch']} us/launch; per kernel: {per_kernel}")
+    # consistency of the isolated group replays with the graph-replayed step:
+    # layers x (sum of the groups' launch durations) + the head, against the
+    # step time measured around the timed graph replays
+    L = cfg["n_layers"]
+    step_from_groups = L * sum(v["us"] for v in per_kernel.values()) + eng.head_us()
+    per_kernel_graph = {"step_us_graph": round(gpu_ms / args.steps * 1e3, 1),
+                        "step_us_from_isolated_groups": round(step_from_groups, 1)}
+    ceiling = stream_ceiling(ctx)
+    roof["stream_ceiling"] = round(ceiling, 1)
+    roof["frac_of_stream_ceiling"] = round(roof["achieved"] / ceiling, 4)
+    log(f"dominant kernel ({roof['group']}): {roof['achieved']} GB/s ({roof['frac']:.1%}, "
+        f"{roof['frac_of_stream_ceiling']:.1%} of the {ceiling:.0f} GB/s stream ceiling), "
+        f"{roof['us_per_launch']} us/launch; per kernel: {per_kernel}; step vs groups: {per_kernel_graph}")
     eng.deinit()
     ctx.close()
 
@@ -141,9 +164,11 @@ def main():
                                "vocab 151936), Q4_K_M, batch 1, greedy decode at KV context 4096+",
                    "context_start": pos, "bytes_per_token": bytes_tok,
                    "token_roofline_frac": round(bytes_tok * tok_s / 1e9 / PEAK_HBM_GBS, 4),
+                   "token_frac_of_stream_ceiling": round(bytes_tok * tok_s / 1e9 / ceiling, 4),
                    "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
         "roofline": roof,
         "per_kernel": per_kernel,
+        "step_consistency": per_kernel_graph,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

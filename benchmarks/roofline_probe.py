@@ -32,13 +32,6 @@ CAL_BYTES = 1 << 30      # calibration read / write size
 PREFILL = 4096           # KV context of the bench (config 3)
 GROUP_ORDER = ["qkv", "attn", "o", "ffn_in", "ffn_out"]
 PMC_ITERS = 36
-KERNELS = {  # the dense 8B step's kernel per group
-    "qkv": "k_dmmv_q4k_tile<16, 0> (attn_norm + Q/K/V, Q4_K 6144x4096)",
-    "attn": "k_attn_decode<4, true, 2, 24> (q/k norm + RoPE + KV write + split-K attention + merge)",
-    "o": "k_dmmv_q4k_tile<16, 0> (O projection + residual, Q4_K 4096x4096, XQ input)",
-    "ffn_in": "k_dmmv_q4k_tile<16, 1> (ffn_norm + gate/up + SwiGLU, 2 x Q4_K 12288x4096, XQ output)",
-    "ffn_out": "k_dmmv_q6k_tile<128, 5> (ffn_down + residual, Q6_K 4096x12288, XQ input)",
-}
 
 
 def probe_engine(ctx, max_ctx):
@@ -57,7 +50,7 @@ def per_kernel(eng, L, iters=108):
         us = eng.time_kernel(g, iters)
         b = eng.group_bytes(g, L)
         gbs = b / (us * 1e-6) / 1e9
-        rows[g] = {"kernel": KERNELS[g], "us_per_launch": round(us, 3), "bytes_per_launch": b,
+        rows[g] = {"kernel": eng.group_kernels(g), "us_per_launch": round(us, 3), "bytes_per_launch": b,
                    "achieved_GBs": round(gbs, 1), "frac": round(gbs / PEAK, 4)}
     dom = max(rows, key=lambda g: rows[g]["us_per_launch"])
     return rows, dom

@@ -412,6 +412,9 @@ int zh_engine_tensor_type(zh_engine *eng, uint64_t stream, uint32_t *type);
  * arguments and state over `iters` launches rotating through the layers, by
  * HIP events on the engine's stream. Leaves the activations changed. */
 int zh_engine_time_kernel(zh_engine *eng, uint32_t group, uint32_t iters, float *us_per_launch);
+/* The kernels one launch group of layer 0 launches (mangled names, read
+ * from the graph its launches capture into), joined with "; " into names. */
+int zh_engine_group_kernels(zh_engine *eng, uint32_t group, char *names, size_t len);
 /* Algorithmic bytes of one launch of `group` at context length L. */
 uint64_t zh_engine_group_bytes(zh_engine *eng, uint32_t group, uint32_t L);
 

@@ -606,7 +606,7 @@ static int record_collect(zh_engine *e) {
 }
 
 // Launch groups of one layer (the unit zh_engine_time_kernel replays).
-enum : uint32_t { SK_QKV = 1, SK_ATTN = 2, SK_O = 4, SK_FFN_IN = 8, SK_FFN_OUT = 16, SK_ALL = 31 };
+enum : uint32_t { SK_QKV = 1, SK_ATTN = 2, SK_O = 4, SK_FFN_IN = 8, SK_FFN_OUT = 16, SK_ALL = 31, SK_HEAD = 32 };
 
 // Records the decode step: embedding, layers [l0, l1) (only the launch
 // groups in `mask`), then (whole steps only) the output head and the step
@@ -769,17 +769,58 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     return ZH_OK;
 }
 
+// Measurement entry (no counterpart in the reference): the kernels one
+// launch group of layer 0 launches, read from the graph the group's launches
+// capture into (each kernel node's function, named by the runtime), joined
+// with "; " into names (at most len bytes, NUL-terminated).
+extern "C" int zh_engine_group_kernels(zh_engine *e, uint32_t group, char *names, size_t len) {
+    if (!e || !names || len == 0 || group == 0 || (group & ~(uint32_t)SK_ALL)) return ZH_ERR_INVALID_ARGUMENT;
+    zh_ctx *c = e->ctx;
+    hipGraph_t g = nullptr;
+    EHIP(e, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    int rc = record_step(e, false, 0, 1, group);
+    const hipError_t ce = hipStreamEndCapture(c->stream, &g);
+    if (rc) return rc;
+    if (ce != hipSuccess) return zh_set_err(c, ZH_ERR_HIP, "capture: %s", hipGetErrorString(ce));
+    size_t n = 0;
+    std::string out;
+    if (hipGraphGetNodes(g, nullptr, &n) == hipSuccess && n) {
+        std::vector<hipGraphNode_t> nodes(n);
+        if (hipGraphGetNodes(g, nodes.data(), &n) == hipSuccess) {
+            // capture order: a node's position in the chain of dependencies
+            for (size_t i = 0; i < n; i++) {
+                hipGraphNodeType t;
+                hipKernelNodeParams kp;
+                if (hipGraphNodeGetType(nodes[i], &t) != hipSuccess || t != hipGraphNodeTypeKernel) continue;
+                if (hipGraphKernelNodeGetParams(nodes[i], &kp) != hipSuccess) continue;
+                hipFunction_t f = nullptr;
+                const char *nm = hipGetFuncBySymbol(&f, kp.func) == hipSuccess && f ? hipKernelNameRef(f) : nullptr;
+                if (!nm) nm = hipKernelNameRefByPtr(kp.func, c->stream);
+                if (!out.empty()) out += "; ";
+                out += nm ? nm : "?";
+            }
+        }
+    }
+    hipGraphDestroy(g);
+    (void)hipGetLastError();  // a name lookup that failed is reported as "?", not by the next launch check
+    snprintf(names, len, "%s", out.c_str());
+    return ZH_OK;
+}
+
+
 // Measurement entry (no counterpart in the reference; the benchmark uses it
 // for per-kernel bandwidth): the average duration of one launch group --
 // exactly the launches, arguments and state of the decode step -- over
 // `iters` launches rotating through the layers (so weights stream from HBM),
 // timed with HIP events on the engine's stream. Activations are left changed.
 extern "C" int zh_engine_time_kernel(zh_engine *e, uint32_t group, uint32_t iters, float *us_per_launch) {
-    if (!e || !us_per_launch || group == 0 || (group & ~(uint32_t)SK_ALL) || iters == 0)
+    const bool head = group == SK_HEAD;  // output norm + LM head + argmax (one launch group, not per layer)
+    if (!e || !us_per_launch || group == 0 || (!head && (group & ~(uint32_t)SK_ALL)) || iters == 0)
         return e ? zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "time_kernel group %u", group) : ZH_ERR_INVALID_ARGUMENT;
     zh_ctx *c = e->ctx;
     const uint32_t L = e->c.n_layers;
-    for (uint32_t l = 0; l < L; l++) ERC(record_step(e, false, l, l + 1, group));
+    auto launch = [&](uint32_t i) { return head ? record_collect(e) : record_step(e, false, i % L, i % L + 1, group); };
+    for (uint32_t l = 0; l < (head ? 1u : L); l++) ERC(launch(l));
     hipEvent_t ev[2];
     EHIP(e, hipEventCreate(&ev[0]));
     if (hipEventCreate(&ev[1]) != hipSuccess) {
@@ -787,7 +828,7 @@ extern "C" int zh_engine_time_kernel(zh_engine *e, uint32_t group, uint32_t iter
         return zh_set_err(c, ZH_ERR_HIP, "event");
     }
     int rc = hipEventRecord(ev[0], c->stream) == hipSuccess ? ZH_OK : ZH_ERR_HIP;
-    for (uint32_t i = 0; rc == ZH_OK && i < iters; i++) rc = record_step(e, false, i % L, i % L + 1, group);
+    for (uint32_t i = 0; rc == ZH_OK && i < iters; i++) rc = launch(i);
     float ms = 0.f;
     if (rc == ZH_OK && (hipEventRecord(ev[1], c->stream) != hipSuccess || hipEventSynchronize(ev[1]) != hipSuccess ||
                         hipEventElapsedTime(&ms, ev[0], ev[1]) != hipSuccess))

@@ -178,7 +178,7 @@ class InferenceEngine:
         return lib().zh_engine_bytes_per_token(self.h, L)
 
     # per-layer launch groups of the decode step (zinc_hip.h ZH_GROUP_*)
-    GROUPS = {"qkv": 1, "attn": 2, "o": 4, "ffn_in": 8, "ffn_out": 16}
+    GROUPS = {"qkv": 1, "attn": 2, "o": 4, "ffn_in": 8, "ffn_out": 16, "head": 32}
 
     def time_kernel(self, group, iters=200):
         """Average us per launch of one launch group, replayed with the
@@ -186,6 +186,16 @@ class InferenceEngine:
         us = C.c_float()
         self.ctx.check(lib().zh_engine_time_kernel(self.h, self.GROUPS[group], iters, C.byref(us)))
         return us.value
+
+    def head_us(self, iters=20):
+        """Output norm + LM head + argmax, us per launch group."""
+        return self.time_kernel("head", iters)
+
+    def group_kernels(self, group):
+        """Names of the kernels one launch group launches (as captured)."""
+        buf = C.create_string_buffer(4096)
+        self.ctx.check(lib().zh_engine_group_kernels(self.h, self.GROUPS[group], buf, 4096))
+        return buf.value.decode()
 
     def group_bytes(self, group, L):
         return lib().zh_engine_group_bytes(self.h, self.GROUPS[group], L)
