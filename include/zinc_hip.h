@@ -39,7 +39,8 @@ enum {
     ZH_ERR_TRUNCATED_FILE = 10,        /* a header or tensor runs past the end of the file */
     ZH_ERR_IO = 11,                    /* open / stat / mmap failure (std.fs errors) */
     ZH_ERR_NOT_FOUND = 12,             /* metadata key absent or not of the asked type (null) */
-    ZH_ERR_KV_CACHE_EXHAUSTED = 13     /* error.KvCacheExhausted      kv_cache.zig:73 */
+    ZH_ERR_KV_CACHE_EXHAUSTED = 13,    /* error.KvCacheExhausted      kv_cache.zig:73 */
+    ZH_ERR_WAIT_TIMEOUT = 14           /* a kernel's bounded cross-workgroup wait gave up */
 };
 
 /* ---- GGMLType values used on the path (src/model/gguf.zig:38-69) -------- */
@@ -58,6 +59,14 @@ const char *zh_status_string(int status);
 /* name (>=64 bytes), CU count, total HBM bytes */
 int  zh_device_info(zh_ctx *ctx, char *name, size_t name_len, int *cu_count, uint64_t *hbm_bytes);
 int  zh_sync(zh_ctx *ctx);
+/* Limit of the bounded wait in the decode attention's in-kernel merge
+ * (default 50000 us; 0 = give up at once). No counterpart in the reference,
+ * which merges split attention in a dispatch of its own
+ * (flash_attn_split_merge.comp); here the first mergers of a kv head wait for
+ * its other chunks. A merger that gives up writes NaN for its q head, the
+ * launch completes, and the next zh_sync returns ZH_ERR_WAIT_TIMEOUT. Takes
+ * effect for later launches, captured graphs included. */
+int  zh_set_attn_wait_limit(zh_ctx *ctx, uint32_t microseconds);
 
 /* ---- buffers: replaces Buffer.initDeviceLocal (vulkan/buffer.zig:102) and
  *      mtl_create_buffer / mtl_free_buffer (shim.h:37-41) ----------------- */
@@ -297,6 +306,13 @@ int zh_engine_tensor(zh_engine *eng, uint64_t stream, zh_buf **buf, uint64_t *of
  * the table in a device buffer, forward.zig:1312). An identity table keeps
  * the lookup-free attention kernel; any other selects the paged kernel. */
 int zh_engine_set_pages(zh_engine *eng, const uint32_t *pages, uint32_t n);
+/* Run the decode step's layers as one persistent launch (on != 0) instead of
+ * per-phase kernels, where the model takes it (dense, Q4_K attention and
+ * gate/up, Q6_K down, hidden 2048 / 4096, FFN 12288 / 14336, 4 q heads per
+ * kv head; no engine sharing the device); elsewhere the per-phase kernels
+ * run. No counterpart in the reference, which records one dispatch per
+ * operation (decodeStep, forward.zig:4299). Default off. */
+int zh_engine_set_persistent(zh_engine *eng, int on);
 
 /* ---- KV page pool: KvPagePool (src/scheduler/kv_cache.zig:43-125) ------ */
 int      zh_kv_pool_create(uint32_t total_pages, uint32_t page_size, zh_kv_pool **out);  /* init */

@@ -85,6 +85,7 @@ def lib():
             "zo_model_set_tensor": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_uint64]),
             "zo_more_bits_layer": (C.c_int, [C.c_uint32, C.c_uint32]),
             "zo_model_hidden": (C.c_void_p, [C.c_void_p]),
+            "zo_model_route_gap": (C.c_float, [C.c_void_p]),
             "zo_model_kv": (C.c_void_p, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32]),
         }
         for name, (res, args) in sig.items():
@@ -336,6 +337,12 @@ class Model:
         p = lib().zo_model_kv(self.h, layer, which, token)
         n = self.cfg["n_kv_heads"] * self.cfg["head_dim"]
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), shape=(n,)).copy()
+
+    def route_gap(self):
+        """Smallest (k-th selected - best unselected) router logit gap of the
+        last decode step over its MoE layers, relative to max |router logit|
+        (inf for a dense model)."""
+        return float(lib().zo_model_route_gap(self.h))
 
     def hidden(self):
         p = lib().zo_model_hidden(self.h)

@@ -656,6 +656,12 @@ struct zo_model {
     float *out_norm, *inv_freq;
     zo_layer *L;
     float *hidden, *norm, *q, *k, *v, *attn, *g, *u, *s, *logits, *rl, *eacc;
+    /* test diagnostic, not part of the restated algorithm: over the MoE
+     * layers of the last decode step, the smallest gap between the k-th
+     * selected router logit and the best unselected one, as a fraction of
+     * the layer's max |router logit| (a near tie that a sum in another order
+     * can flip) */
+    float route_gap;
 };
 
 static uint8_t *alloc_tensor(uint32_t type, uint64_t rows, uint64_t cols, uint64_t seed, uint64_t stream) {
@@ -848,6 +854,7 @@ int zo_model_set_tensor(zo_model *m, uint64_t stream, uint32_t type, const void 
     return 0;
 }
 const float *zo_model_hidden(zo_model *m) { return m->hidden; }
+float zo_model_route_gap(const zo_model *m) { return m->route_gap; }
 const uint16_t *zo_model_kv(zo_model *m, uint32_t layer, uint32_t which, uint32_t token) {
     if (layer >= m->c.n_layers || which > 1 || token >= m->c.max_ctx) return NULL;
     const zo_layer *y = &m->L[layer];
@@ -896,6 +903,7 @@ uint32_t zo_model_decode_step(zo_model *m, uint32_t token, uint32_t pos, float *
     /* embedToken: forward.zig:4255-4290 (safe_id clamp) */
     uint32_t tid = token < c->vocab ? token : c->vocab - 1;
     zo_dequant_row(m->embd, tid, H, m->t_embd, m->hidden);
+    m->route_gap = INFINITY;
     for (uint32_t l = 0; l < c->n_layers; l++) {
         zo_layer *y = &m->L[l];
         zo_rms_norm_mul(m->hidden, y->attn_norm, H, m->norm, H, 1, c->eps);
@@ -936,6 +944,17 @@ uint32_t zo_model_decode_step(zo_model *m, uint32_t token, uint32_t pos, float *
             uint32_t F = c->expert_ffn;
             zo_dmmv(y->router, y->t[ZK_ROUTER], m->norm, m->rl, c->n_experts, H, 0, nt);
             zo_topk_softmax(m->rl, c->n_experts, c->n_experts_used, ids, w);
+            {
+                float kth = INFINITY, rest = -INFINITY, amax = 0.f;
+                for (uint32_t j = 0; j < c->n_experts_used; j++) kth = fminf(kth, m->rl[ids[j]]);
+                for (uint32_t i = 0; i < c->n_experts; i++) {
+                    int sel = 0;
+                    for (uint32_t j = 0; j < c->n_experts_used; j++) sel |= ids[j] == i;
+                    if (!sel) rest = fmaxf(rest, m->rl[i]);
+                    amax = fmaxf(amax, fabsf(m->rl[i]));
+                }
+                if (amax > 0.f) m->route_gap = fminf(m->route_gap, (kth - rest) / amax);
+            }
             uint64_t gstride = zo_tensor_bytes(y->t[ZK_EXP_GATE], F, H), ustride = zo_tensor_bytes(y->t[ZK_EXP_UP], F, H);
             uint64_t dstride = zo_tensor_bytes(y->t[ZK_EXP_DOWN], H, F);
             float *dout = (float *)malloc((size_t)c->n_experts_used * H * 4);

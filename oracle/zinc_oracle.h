@@ -140,6 +140,8 @@ int       zo_model_tensor_type(zo_model *m, uint64_t stream);
  * n must be its size in that type; 0 on success, < 0 on a mismatch. */
 int       zo_model_set_tensor(zo_model *m, uint64_t stream, uint32_t type, const void *src, uint64_t n);
 const float   *zo_model_hidden(zo_model *m);
+/* test diagnostic: smallest relative router top-k gap of the last step */
+float          zo_model_route_gap(const zo_model *m);
 /* fp16 K (which 0) or V (1) cache row of `token` in `layer`: n_kv_heads*head_dim values. */
 const uint16_t *zo_model_kv(zo_model *m, uint32_t layer, uint32_t which, uint32_t token);
 

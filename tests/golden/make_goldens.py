@@ -47,11 +47,12 @@ def greedy_fixture(cfg, prefill, n_gen, out_name):
     for t in prompt[:-1]:
         om.decode_step(t, pos)
         pos += 1
-    tok, toks, margins = prompt[-1], [], []
+    tok, toks, margins, gaps = prompt[-1], [], [], []
     for i in range(n_gen):
         tok, lg = om.decode_step(tok, pos, want_logits=True)
         s = np.sort(lg)
         margins.append(float(s[-1] - s[-2]) / float(np.abs(lg).max()))
+        gaps.append(min(om.route_gap(), 1.0))
         toks.append(int(tok))
         pos += 1
         if i % 16 == 0:
@@ -59,7 +60,7 @@ def greedy_fixture(cfg, prefill, n_gen, out_name):
     om.close()
     out = {"config": {k: (v if not isinstance(v, float) else float(v)) for k, v in cfg.items()},
            "prefill": prefill, "kv_seed": KV_SEED, "prompt": prompt, "tokens": toks,
-           "rel_margins": margins, "generator": "oracle/zinc_oracle.c zo_model_decode_step"}
+           "rel_margins": margins, "route_gaps": gaps, "generator": "oracle/zinc_oracle.c zo_model_decode_step"}
     with open(os.path.join(HERE, out_name), "w") as f:
         json.dump(out, f)
     print(f"{out_name}: min relative margin {min(margins):.3g}, {time.time() - t0:.0f}s", flush=True)

@@ -13,7 +13,8 @@ pytestmark = pytest.mark.gpu
 FIXTURE = os.path.join(os.path.dirname(__file__), "golden", "dense8b_greedy256.json")
 
 
-def test_dense8b_greedy_256_token_exact():
+@pytest.mark.parametrize("persistent", [False, True], ids=["per-phase", "persistent"])
+def test_dense8b_greedy_256_token_exact(persistent):
     import zinc_amd
     g = json.load(open(FIXTURE))
     cfg = dict(g["config"])
@@ -21,6 +22,7 @@ def test_dense8b_greedy_256_token_exact():
     ctx = zinc_amd.Context(0)
     try:
         eng = zinc_amd.InferenceEngine(ctx, cfg)
+        eng.set_persistent(persistent)
         eng.prefill_kv_random(g["prefill"], g["kv_seed"])
         got = eng.generate(g["prompt"], len(g["tokens"]), start_pos=g["prefill"])
         eng.deinit()
@@ -30,3 +32,107 @@ def test_dense8b_greedy_256_token_exact():
     bad = [i for i in range(len(ref)) if got[i] != ref[i]]
     assert not bad, (f"first mismatch at step {bad[0]} (oracle margin there "
                      f"{g['rel_margins'][bad[0]]:.2e} of max |logit|)")
+
+
+# A greedy step whose top-2 logits the oracle separates by less than this
+# fraction of max |logit| is a near tie: a sum in another order may pick the
+# other token (the decode tolerance is 1e-3 of the scale). In an MoE model a
+# step is also a near tie when, in some layer, the oracle's k-th selected
+# router logit beats the best unselected one by less than ROUTE_TIE of that
+# layer's max |router logit|: the GPU's hidden state differs from the
+# oracle's by ~1e-5 of its scale (sums in another order), enough to swap
+# such an expert, and a swapped expert moves the logits by up to tenths of
+# their scale (measured: 0.26 and 0.42 of max |logit| at two such steps of
+# the config-4 fixture, against 2e-5 .. 1e-2 at the others). A mismatch is
+# accepted only at a near-tie step, and the run then continues from the
+# oracle's token (the prompt re-decoded with the oracle's tokens appended).
+NEAR_TIE, ROUTE_TIE = 1e-3, 1e-3
+
+
+def _greedy_fixture(name):
+    import zinc_amd
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", name)))
+    cfg = dict(g["config"])
+    ref, margins = g["tokens"], g["rel_margins"]
+    gaps = g.get("route_gaps", [1.0] * len(ref))
+    print(f"{name}: {cfg['n_layers']} layers, KV prefill {g['prefill']}, {len(ref)} tokens", flush=True)
+    ctx = zinc_amd.Context(0)
+    ties = []
+    try:
+        eng = zinc_amd.InferenceEngine(ctx, cfg)
+        eng.prefill_kv_random(g["prefill"], g["kv_seed"])
+        done = 0
+        while done < len(ref):
+            got = eng.generate(g["prompt"] + ref[:done], len(ref) - done, start_pos=g["prefill"])
+            bad = [i for i in range(len(got)) if got[i] != ref[done + i]]
+            if not bad:
+                break
+            i = done + bad[0]
+            assert margins[i] < NEAR_TIE or gaps[i] < ROUTE_TIE, (
+                f"first mismatch at step {i} (oracle margin there {margins[i]:.2e} of max |logit|, "
+                f"router gap {gaps[i]:.2e})")
+            ties.append(i)
+            done = i + 1
+        eng.deinit()
+    finally:
+        ctx.close()
+    n_near = sum(1 for m, r in zip(margins, gaps) if m < NEAR_TIE or r < ROUTE_TIE)
+    print(f"{name}: token-exact except at near ties {ties} ({n_near} near-tie steps in the fixture)", flush=True)
+    return g
+
+
+def test_moe48_greedy_256_token_exact():
+    """Config 4 at full size: 48 layers, 128 experts top-8 (expert FFN 768,
+    experts Q4_K, router and attention Q8_0), LM head Q6_K over 151936, KV
+    context 8192, 256 greedy tokens equal to the oracle's (fixture written by
+    tests/golden/make_goldens.py moe48)."""
+    g = _greedy_fixture("moe48_greedy256.json")
+    c = g["config"]
+    assert c["n_layers"] == 48 and c["n_experts"] == 128 and c["n_experts_used"] == 8 and c["vocab"] == 151936
+    assert g["prefill"] == 8192
+
+
+def test_dense8b_32k_greedy_128_token_exact():
+    """Config 5's decode: the 8B-shaped model over a 32768-position fp16 KV
+    cache (8 kv heads x 128 dims x 36 layers), 128 greedy tokens equal to the
+    oracle's (fixture: tests/golden/make_goldens.py dense8b_32k)."""
+    g = _greedy_fixture("dense8b_32k_greedy128.json")
+    assert g["config"]["n_layers"] == 36 and g["prefill"] == 32768 and len(g["tokens"]) == 128
+
+
+def test_prefill512_8b_shapes_matches_sequential_oracle():
+    """Config 5's prefill: 512 tokens through the MFMA dequant-GEMM path on the
+    8B layer shapes (4 layers, vocab 8192) against the oracle decoding the same
+    prompt token by token (fixture: tests/golden/make_goldens.py prefill512).
+    The GEMMs multiply fp16 operands (the dequantised weights rounded to fp16,
+    as the north star's fp16 tiles) with f32 accumulation, so logits and K/V
+    rows agree to that rounding, not to the decode path's; the greedy token
+    after the prompt and the 15 decoded after it must equal the oracle's."""
+    import numpy as np
+    import zinc_amd
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "prefill512_8b4l.npz"))
+    cfg = json.loads(str(f["config"]))
+    prompt, toks = f["prompt"], f["tokens"].tolist()
+    ctx = zinc_amd.Context(0)
+    try:
+        eng = zinc_amd.InferenceEngine(ctx, cfg)
+        eng.prefill(prompt, start_pos=0)
+        logits = eng.logits()
+        first = eng.sample_greedy()
+        kv = np.stack([np.stack([eng.read_kv(cfg["n_layers"] - 1, w, int(r), 1) for r in f["kv_rows"]])
+                       for w in (0, 1)])
+        cont = eng.generate([first], len(toks) - 1, start_pos=len(prompt))
+        eng.deinit()
+    finally:
+        ctx.close()
+    ref = f["logits"].astype(np.float64)
+    scale = np.abs(ref).max()
+    d = np.abs(logits - ref).max()
+    print(f"prefill512: max |logit - oracle| = {d / scale:.2e} of max |logit|", flush=True)
+    assert d <= 2e-3 * scale, d / scale
+    g32, o32 = kv.view(np.float16).astype(np.float32), f["kv"].view(np.float16).astype(np.float32)
+    rowmax = np.abs(o32).max(axis=-1, keepdims=True)
+    kd = (np.abs(g32 - o32) / rowmax).max()
+    print(f"prefill512: max |K/V - oracle| = {kd:.2e} of the row maximum", flush=True)
+    assert kd <= 5e-3, kd
+    assert [first] + cont == toks

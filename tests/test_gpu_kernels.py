@@ -284,7 +284,7 @@ def kv_setup(ctx, orc, nkv, hd, cache_tokens, L, seed, shuffle_pages=True):
     return pages, k, v, kc, vc
 
 
-@pytest.mark.parametrize("L", [1, 15, 16, 17, 300, 1000, 4096, 4113])
+@pytest.mark.parametrize("L", [1, 15, 16, 17, 300, 1000, 4096, 4113, 32768])
 def test_flash_decode_paged(ctx, orc, L):
     nh, nkv, hd = 32, 8, 128
     cache_tokens = ((L + 15) // 16 + 3) * 16

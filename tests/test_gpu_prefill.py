@@ -92,8 +92,10 @@ def test_engine_prefill_matches_sequential_oracle(ctx, orc, n_prompt, prefill):
     """prefillBatched vs the oracle's token-by-token decodeStep: the K/V rows
     of every prompt token and the last token's logits. The GEMM operands are
     fp16 (relative rounding 2^-11), so the bounds are relative to each row's
-    magnitude: K/V |d| <= 2e-2 * max|row|, logits |d| <= 5e-3 * max|logit|;
-    the greedy token must agree where the oracle's top-2 margin exceeds 1%."""
+    magnitude: K/V |d| <= 5e-3 * max|row|, logits |d| <= 3e-3 * max|logit|
+    (measured: about 1.4e-3 of each at the 8B layer shapes,
+    test_gpu_golden.py); the greedy token must agree wherever the oracle's
+    top-2 margin exceeds twice the logit bound (6e-3 of the scale)."""
     import zinc_amd
     eng = zinc_amd.InferenceEngine(ctx, SMALL_DENSE)
     om = orc.Model(SMALL_DENSE)
@@ -106,17 +108,17 @@ def test_engine_prefill_matches_sequential_oracle(ctx, orc, n_prompt, prefill):
     for i, t in enumerate(prompt):
         o_tok, o_log = om.decode_step(t, prefill + i, want_logits=True)
     scale = np.abs(o_log).max()
-    assert np.abs(g_log - o_log).max() <= 5e-3 * scale
+    assert np.abs(g_log - o_log).max() <= 3e-3 * scale, np.abs(g_log - o_log).max() / scale
     s = np.sort(o_log)
-    if (s[-1] - s[-2]) > 1e-2 * scale:
+    if (s[-1] - s[-2]) > 6e-3 * scale:
         assert g_tok == o_tok
     for l in range(SMALL_DENSE["n_layers"]):
         for which in (0, 1):
             g = eng.read_kv(l, which, prefill, n_prompt).view(np.float16).astype(np.float32).reshape(n_prompt, -1)
             o = np.stack([om.kv(l, which, prefill + i) for i in range(n_prompt)]).view(np.float16)
             o = o.astype(np.float32)
-            bound = 2e-2 * np.abs(o).max(axis=1, keepdims=True)
-            assert (np.abs(g - o) <= bound).all(), (l, which, np.abs(g - o).max())
+            rowmax = np.abs(o).max(axis=1, keepdims=True)
+            assert (np.abs(g - o) <= 5e-3 * rowmax).all(), (l, which, (np.abs(g - o) / rowmax).max())
     eng.deinit()
     om.close()
 

@@ -1,0 +1,598 @@
+// zh_attn_common.h — decode-attention pieces shared by the attention
+// kernels (zh_ops.hip) and the persistent decode-layers kernel
+// (zh_step.hip): geometry, the kernel parameter block, the per-head
+// norm + RoPE, the chunk merge, and the DMA-ring attention body.
+#pragma once
+#include "zh_device.h"
+#include "zh_internal.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"
+
+ZH_DEV uint32_t read_pos(zh_pos_src p) { return p.dev ? (*p.dev + p.value) : p.value; }
+
+#ifndef TRACE_OPS
+#define TRACE_OPS(slot) ZH_TRACE_POINT(slot)
+#endif
+constexpr int FD_MAXG = 8;   // q heads per kv head
+constexpr int FD_HD = 128;   // head_dim supported
+// 4 waves x TW tokens: one wave per SIMD, and the 8 kv heads map one per XCD
+// (workgroups go round robin over the 8 XCDs), so the chunks of a kv head
+// spread over its XCD's 32 CUs. TW (tokens per wave per sub-chunk) is a
+// template parameter chosen at launch:
+//  * 24 when the context capacity is at most 8192 tokens: a 4K context then
+//    runs 2 pipelined 96-token sub-chunks per workgroup over 22 chunks per
+//    kv head (15.6 us per layer against 16.4 us for one 136-token chunk over
+//    32 chunks: the second sub-chunk's K/V loads are in flight while the
+//    first is computed, and fewer partials are merged);
+//  * 32 for longer contexts: 128-token sub-chunks (32K context: 36.9 us
+//    against 38.8 us with 96 and 40.2 us with 160);
+//  * 40 for 8 q heads per kv head, which has no sub-chunk loop.
+constexpr int AD_W = 4;      // waves per workgroup
+constexpr int AD_T = AD_W * 64;
+constexpr int AD_TC_MIN = AD_W * 24;  // the shortest sub-chunk: sizes the partials
+// Chunk geometry modes: page-table lookups with chunk = blockIdx.y, the same
+// dispatched newest-first (grids larger than the device), or an identity page
+// table (physical token = logical token), where nothing waits on page entries
+// and the chunk length follows the context: ceil(seq / nd) rounded up to 8
+// tokens (at least TW) while that fits TC = 4 TW, with nd = CUs / kv heads, so
+// the chunks of all kv heads cover the device once (32 per head for 8 kv
+// heads: one XCD each).
+enum { AD_PAGED = 0, AD_PAGED_REV = 1, AD_IDENT = 2 };
+// Longer contexts: chunks of nsub consecutive TC-token sub-chunks (a
+// workgroup runs them in turn with an online softmax), so a kv head never has
+// more than nd chunks: the grid stays one round of one workgroup per CU (the
+// kernel's registers allow one) and the merge reads at most nd partials.
+ZH_DEV uint32_t attn_nsub(uint32_t seq, uint32_t nd, uint32_t tc) {
+    const uint32_t span = nd * tc;
+    return seq > span ? (seq + span - 1) / span : 1u;
+}
+ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq, uint32_t nd, bool sub, uint32_t tw) {
+    const uint32_t tc = AD_W * tw, ct = ((seq + nd - 1) / nd + 7) / 8 * 8;
+    return seq > nd * tc ? tc * (sub ? attn_nsub(seq, nd, tc) : 1u) : max(ct, tw);
+}
+// Sub-chunks are compiled for up to 4 q heads per kv head (G = 8 would spill
+// its loop-carried state); G = 8 keeps TC-token chunks at long contexts.
+template <int G> constexpr bool attn_sub_ok() { return G <= 4; }
+static inline uint32_t attn_nd(uint32_t nkv, int cu_count) {
+    const uint32_t cu = cu_count > 0 && cu_count < 256 ? (uint32_t)cu_count : 256u;
+    const uint32_t nd = cu / nkv > 0 ? cu / nkv : 1u;
+    return nd < 256u ? nd : 256u;  // the merge keeps at most 256 chunk statistics in LDS
+}
+// chunk slots per head for sub-chunks of tc tokens (the partials, sized with
+// the shortest, hold any; a device with at most 256 CUs fits)
+static inline uint32_t attn_n_chunks(uint32_t max_seq, uint32_t nd, uint32_t tc = AD_TC_MIN) {
+    const uint32_t n = (max_seq + tc - 1) / tc;
+    return n > nd ? n : nd;
+}
+
+
+struct AttnP {
+    const float *q;                // FUSED: raw Q projection; else prepared (normed, roped) q
+    const float *k_new, *v_new;    // FUSED: raw K/V projection of the new token
+    const float *q_norm, *k_norm;  // FUSED: per-head RMSNorm weights (128)
+    const float *rope_cs;          // FUSED: [position][64] (cos, sin) pairs of pos * inv_freq
+    uint16_t *kc, *vc;
+    const uint32_t *pages;
+    uint32_t n_pages, cache_tokens;
+    zh_pos_src pos;  // FUSED: position of the new token (seq = pos + 1); else seq_len
+    float scale, eps;
+    float *part;     // [nq][n_chunks][130]
+    uint32_t n_chunks;
+    uint32_t *counters;  // [nkv], zero between launches
+    float *out;          // [nq * 128]
+    uint8_t *xq;         // optional XQ image of out
+    uint32_t nq;
+    uint32_t nd;         // AD_IDENT: target chunks per kv head
+    uint32_t no_wait;    // the last arrival merges every q head (no merger waits for others)
+    uint32_t ident;      // k_attn_ring: the page table is the identity (no lookups)
+    uint32_t *ctl;       // device control words: [0] error word, [1] merge wait limit (ticks)
+};
+
+ZH_DEV float sum8(float v) { return row8_sum(v); }  // over the 8 lanes of a token group
+
+// RMSNorm (weights w) + NeoX RoPE on one head held as lo[e] = x[sub*8+e],
+// hi[e] = x[64+sub*8+e] (qk_norm_rope_kv_write.comp:67-171 arithmetic).
+ZH_DEV void norm_rope16(float (&lo)[8], float (&hi)[8], const float (&wlo)[8], const float (&whi)[8],
+                        const float (&co)[8], const float (&sn)[8], float eps) {
+    float sq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) sq = fmaf(lo[e], lo[e], fmaf(hi[e], hi[e], sq));
+    sq = sum8(sq);
+    const float rms_inv = 1.0f / sqrtf(sq / (float)FD_HD + eps);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float a = wlo[e] * (lo[e] * rms_inv);
+        const float b = whi[e] * (hi[e] * rms_inv);
+        lo[e] = a * co[e] - b * sn[e];
+        hi[e] = a * sn[e] + b * co[e];
+    }
+}
+
+
+// Two f32 -> packed f16 with the hardware conversion (round to nearest
+// even; fp16 denormals are kept in this build's default FP mode), as the
+// cache write's @floatCast.
+ZH_DEV uint32_t pack_h2(float a, float b) {
+    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+// Row o (0..47) of the three pages a wave reads, page bases pa, pb, pc.
+ZH_DEV const uint16_t *kv_row(const uint16_t *h, size_t pa, size_t pb, size_t pc, uint32_t o) {
+    const uint32_t pi = o >> 4;
+    const size_t pg = pi == 0 ? pa : pi == 1 ? pb : pc;
+    return h + (pg * 16 + (o & 15)) * FD_HD;
+}
+
+// Merges the chunk partials of q heads h0 .. h0+GM-1: O = sum_c exp(m_c - M) O_c
+// / sum_c exp(m_c - M) l_c (the split-K combine of flash_decode.comp's
+// reduction). NBAT chunks per round of O loads (every load is issued, with
+// clamped addresses, so the wait counts stay static). Reads partials published at device scope; `poison` (a wait that
+// timed out) turns the outputs into NaN.
+template <int GM, int NBAT, bool COH = false>
+ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
+    // any workgroup size of at least AD_T threads (every thread calls it)
+    const uint32_t tid = COH ? phase_tid() : threadIdx.x, wave = tid >> 6, lane = tid & 63, nthr = blockDim.x;
+    TRACE_OPS(11);
+    // Chunk merge. The first batch of each thread's O dims (NBAT chunks) is
+    // requested before the chunk statistics, so both arrive in about one
+    // round trip; the statistics pass leaves m_c in LDS for the weights.
+    // dims per thread: power of two with G*128/OPT <= AD_T
+    constexpr int OPT = GM * FD_HD <= AD_T ? 1 : GM * FD_HD <= 2 * AD_T ? 2 : GM * FD_HD <= 4 * AD_T ? 4 : 8;
+    constexpr int NTH = GM * FD_HD / OPT;
+    constexpr int MB = 256;                 // chunk statistics kept in LDS
+    __shared__ __align__(16) float sm[GM][MB];
+    __shared__ float hM[GM], hL[GM];
+    __shared__ float ob[GM * FD_HD];
+    float O[OPT];
+#pragma unroll
+    for (int k = 0; k < OPT; k++) O[k] = 0.f;
+    const uint32_t g_t = min(tid * OPT / FD_HD, (uint32_t)GM - 1), d0 = (tid * OPT) % FD_HD;
+    const float *pt = p.part + (size_t)(h0 + g_t) * p.n_chunks * (FD_HD + 2);
+    float v[NBAT][OPT];
+    auto load_o = [&](uint32_t cb) {
+#pragma unroll
+        for (int u = 0; u < NBAT; u++) {
+            const float *pc = pt + (size_t)min(cb + u, nv - 1) * (FD_HD + 2) + d0;
+            if (OPT == 1) {
+                v[u][0] = ld_dev(pc);
+            } else {
+#pragma unroll
+                for (int w = 0; w < OPT / 2; w++) {
+                    const uint64_t x = ld_dev64(pc + 2 * w);
+                    v[u][2 * w] = __uint_as_float((uint32_t)x);
+                    v[u][2 * w + 1] = __uint_as_float((uint32_t)(x >> 32));
+                }
+            }
+        }
+    };
+    const bool one_batch = nv <= (uint32_t)NBAT;  // uniform
+    if (one_batch) load_o(0);
+    asm volatile("" ::: "memory");  // the O loads go out before the statistics loads
+    for (uint32_t g = wave; g < (uint32_t)GM; g += nthr / 64) {
+        const float *pp = p.part + (size_t)(h0 + g) * p.n_chunks * (FD_HD + 2);
+        float m = -INFINITY, l = 0.f;
+        for (uint32_t c = lane; c < nv; c += 64) {
+            const uint64_t ml = ld_dev64(pp + (size_t)c * (FD_HD + 2) + FD_HD);
+            const float mc = __uint_as_float((uint32_t)ml), lc = __uint_as_float((uint32_t)(ml >> 32));
+            if (c < MB) sm[g][c] = mc;
+            const float mn = fmaxf(m, mc);
+            l = fmaf(l, m == -INFINITY ? 0.f : expf(m - mn), lc * expf(mc - mn));
+            m = mn;
+        }
+        const float M = wave_max(m);
+        l = wave_sum(m == -INFINITY ? 0.f : l * expf(m - M));
+        if (lane == 0) { hM[g] = M; hL[g] = l; }
+    }
+    TRACE_OPS(12);
+    __syncthreads();
+    TRACE_OPS(13);
+    const float Mt = hM[g_t];
+    if (one_batch) {
+        // weights exp(m_c - M) once per (head, chunk), in place in LDS
+        for (uint32_t i = tid; i < (uint32_t)GM * NBAT; i += nthr) {
+            const uint32_t g = i / NBAT, c = i % NBAT;
+            sm[g][c] = c < nv ? expf(sm[g][c] - hM[g]) : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u4 = 0; u4 < NBAT; u4 += 4) {
+            const f32x4 w4 = *(const f32x4 *)&sm[g_t][u4];
+#pragma unroll
+            for (int k = 0; k < OPT; k++) {
+                O[k] = fmaf(v[u4][k], w4.x, O[k]);
+                O[k] = fmaf(v[u4 + 1][k], w4.y, O[k]);
+                O[k] = fmaf(v[u4 + 2][k], w4.z, O[k]);
+                O[k] = fmaf(v[u4 + 3][k], w4.w, O[k]);
+            }
+        }
+    } else {
+        // long contexts: one round of loads per NBAT chunks
+        for (uint32_t cb = 0; cb < nv; cb += NBAT) {
+            load_o(cb);
+#pragma unroll
+            for (int u = 0; u < NBAT; u++) {
+                const uint32_t c = cb + u;
+                const float mc = c < MB ? sm[g_t][c < MB ? c : 0] : ld_dev(pt + (size_t)min(c, nv - 1) * (FD_HD + 2) + FD_HD);
+                const float wgt = c < nv ? expf(mc - Mt) : 0.f;
+#pragma unroll
+                for (int k = 0; k < OPT; k++) O[k] = fmaf(v[u][k], wgt, O[k]);
+            }
+        }
+    }
+    TRACE_OPS(6);
+    if (tid < (uint32_t)NTH) {
+#pragma unroll
+        for (int k = 0; k < OPT; k++) {
+            const float r = poison ? __builtin_nanf("") : hL[g_t] > 0.f ? O[k] / hL[g_t] : 0.f;
+            ob[tid * OPT + k] = r;
+            if (p.out) {
+                if (COH) st_dev(p.out + (size_t)h0 * FD_HD + tid * OPT + k, r);
+                else p.out[(size_t)h0 * FD_HD + tid * OPT + k] = r;
+            }
+        }
+    }
+    TRACE_OPS(7);
+    if (p.xq) {
+        __syncthreads();
+        XQView v = xq_view(p.xq, p.nq * FD_HD / 32);
+        for (uint32_t o = tid; o < (uint32_t)GM * FD_HD; o += nthr) {  // whole 32-lane groups (GM*128 % 32 == 0)
+            const uint32_t blk = (h0 * FD_HD + o) / 32;
+            if (COH) xq_store_block32_dev(ob[o], o & 31, v, blk);
+            else xq_store_block32(ob[o], o & 31, v, blk);
+            // the quantiser's max drops NaN: a poisoned head's blocks get NaN
+            // scales so that the consumer's sums are NaN too
+            if (poison && (o & 15) == 0) {
+                if ((o & 31) == 0) v.xs[blk] = __builtin_nanf("");
+                v.xsum[blk * 2 + ((o >> 4) & 1)] = __builtin_nanf("");
+            }
+        }
+    }
+    TRACE_OPS(5);
+}
+
+
+// The DMA-ring decode attention over a paged fp16 KV cache with the
+// chunk's K/V streamed HBM -> LDS by asynchronous DMA (included by
+// zh_ops.hip, after AttnP, norm_rope16, pack_h2 and attn_merge).
+//
+// Split-K flash decode (attention.zig:199-316, flash_decode.comp's split +
+// merge) for one token: workgroup (kv head h, chunk c) of a grid of nkv x nd
+// (nd = CUs / nkv, one workgroup per CU) owns the logical tokens
+// [c CT, (c+1) CT) with CT = ceil(seq / nd) rounded up to a 16-token page.
+// The chunk is cut into 64-token sub-chunks (4 pages: 16 KB of K and 16 KB
+// of V) that stream through a ring of AR_D LDS slots: every 1 KB copy is 4
+// tokens of one page, so each lane's address is page base + offset and any
+// page table costs nothing per token (logicalTokenToPhysicalToken,
+// forward.zig:677-698; the chunk's page entries are read once into LDS). All
+// sub-chunks up to the ring depth are requested at once, before any compute.
+//
+// FUSED (the engine's step): q and the new token's k get the per-head
+// RMSNorm and NeoX RoPE (qk_norm_rope_kv_write.comp), the new K/V row is
+// written to the cache, and the workgroup holding the position substitutes
+// it for the row its copy read (which predates the write).
+//
+// Each workgroup publishes one partial (O, m, l) per q head; the last of the
+// kv head's workgroups to arrive (a device-scope counter) merges them
+// (attn_merge) into the output and its XQ image, and resets the counter.
+// No workgroup waits for another.
+constexpr int AR_TS = 64;                            // tokens per sub-chunk
+constexpr uint32_t AR_SLOT = AR_TS * 2 * FD_HD * 2;  // K then V: 32 KB
+constexpr int AR_D = 4;                              // ring slots
+constexpr uint32_t AR_MAXPG = 256;                   // page entries per chunk (CT <= 4096 tokens)
+// waves per workgroup: one group of four (eight, two groups each taking
+// alternate sub-chunks, measured the same at a 4K context)
+template <int G> constexpr int ar_waves() { return 4; }
+// small copies, 1 KB each: q of the group (G / 2 KB), [k_new | v_new],
+// [q_norm | k_norm], [RoPE row | -]; then the new K / V row as f16 (512 B)
+template <int G> constexpr uint32_t ar_qc() { return (G * FD_HD * 4 + 1023) / 1024; }
+template <int G> constexpr uint32_t ar_small() { return (ar_qc<G>() + 3) * 1024 + 512; }
+template <int G, int AW = ar_waves<G>()>
+constexpr uint32_t ar_lds_bytes() {
+    return AR_D * AR_SLOT + ar_small<G>() + AR_MAXPG * 4 + AW * G * 16 * 4;
+}
+
+// AW waves (4 or 8: one or two groups of four taking alternate sub-chunks);
+// COH: q and the new token's k / v were written by other workgroups of the
+// same launch (read at system scope), and the merged output is read by other
+// workgroups of it (stored at device scope).
+template <int G, bool FUSED, int AW, bool COH>
+ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *lds) {
+    constexpr int AT = AW * 64, NG = AW / 4;  // threads, groups
+    constexpr uint32_t QC = ar_qc<G>();
+    constexpr uint32_t NSM = QC + (FUSED ? 2 : 0);  // position-independent small copies
+    constexpr uint32_t KVW = 32 / AW;               // K/V copies per wave and sub-chunk
+    uint8_t *sm = lds + AR_D * AR_SLOT;
+    uint32_t *pgl = (uint32_t *)(sm + ar_small<G>());
+    float *ps = (float *)(pgl + AR_MAXPG);  // [AW][G][16] probabilities of a wave's tokens
+    const uint32_t tid = COH ? phase_tid() : threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), sub = lane & 7, grp = lane >> 3;
+    const uint32_t gq = wave / 4, w4 = wave % 4;  // group, wave within the group
+    const uint32_t lds0 = lds_addr(lds);
+    TRACE_OPS(0);
+    // ---- position-independent small copies first (q, the new token's raw k
+    // and v, the norm weights), while the position is read
+    {
+        const uint32_t l16 = lane * 16, half = lane >> 5, o = (lane & 31) * 16;
+        for (uint32_t k = wave; k < NSM; k += AW) {  // uniform per wave
+            const uint8_t *src;
+            if (k < QC) {
+                src = (const uint8_t *)(p.q + (size_t)kvh * G * FD_HD) + min(k * 1024 + l16, (uint32_t)G * 512 - 16);
+            } else if (k == QC) {
+                src = half ? (const uint8_t *)(p.v_new + (size_t)kvh * FD_HD) + o
+                           : (const uint8_t *)(p.k_new + (size_t)kvh * FD_HD) + o;
+            } else {
+                src = half ? (const uint8_t *)p.k_norm + o : (const uint8_t *)p.q_norm + o;
+            }
+            if (k <= QC) dma16_act<COH>(src, lds0 + AR_D * AR_SLOT + k * 1024);
+            else dma16(src, lds0 + AR_D * AR_SLOT + k * 1024);
+        }
+    }
+    // ---- position and chunk geometry
+    const uint32_t posv = p.pos.dev ? *p.pos.dev + p.pos.value : p.pos.value;
+    const uint32_t seq = FUSED ? posv + 1 : posv;
+    const uint32_t CT = ((seq + p.nd - 1) / p.nd + 15) / 16 * 16;
+    const uint32_t nv = (seq + CT - 1) / CT;
+    if (c >= nv) {  // uniform: no token of this chunk
+        wait_vm<0>();
+        return;
+    }
+    const uint32_t t0 = c * CT, t1 = min(seq, t0 + CT), nsub = (t1 - t0 + AR_TS - 1) / AR_TS;
+    if (!p.ident) {
+        // the chunk's page entries (a compiler-tracked load: its wait also
+        // drains the small copies, which are needed first anyway)
+        for (uint32_t i = tid; i < (t1 - t0 + 15) / 16; i += AT) pgl[i] = p.pages[min(t0 / 16 + i, p.n_pages - 1)];
+        __syncthreads();
+    }
+    if (FUSED && wave == AW - 1)  // the RoPE row of the position
+        dma16((const uint8_t *)(p.rope_cs + (size_t)posv * FD_HD) + min(lane * 16, 496u),
+              lds0 + AR_D * AR_SLOT + (QC + 2) * 1024);
+    const uint16_t *kbase = p.kc + (size_t)kvh * p.cache_tokens * FD_HD;
+    const uint16_t *vbase = p.vc + (size_t)kvh * p.cache_tokens * FD_HD;
+    auto phys = [&](uint32_t t) __attribute__((always_inline)) {  // logical token in [t0, t1)
+        return p.ident ? t : pgl[(t - t0) >> 4] * 16u + (t & 15u);
+    };
+    // ---- K/V copies of sub-chunk s into slot s % AR_D: 32 chunks of 1 KB (4
+    // tokens of one page; K then V), KVW per wave. Rows past the chunk re-read
+    // its last row (masked).
+    auto issue_kv = [&](uint32_t s) __attribute__((always_inline)) {
+        const uint32_t slot = s % AR_D;
+#pragma unroll
+        for (uint32_t i = 0; i < KVW; i++) {
+            const uint32_t j = wave + AW * i, kv = j >> 4;
+            const uint32_t t = min(t0 + s * AR_TS + 4 * (j & 15) + (lane >> 4), t1 - 1);
+            const uint16_t *row = (kv ? vbase : kbase) + (size_t)phys(t) * FD_HD;
+            dma16(row + (lane & 15) * 8, lds0 + slot * AR_SLOT + j * 1024);
+        }
+    };
+    const uint32_t npro = min(nsub, (uint32_t)AR_D);
+    for (uint32_t s = 0; s < npro; s++) issue_kv(s);
+    // the small copies (and the RoPE row, issued before every K/V copy)
+    wait_vm_dyn(npro * KVW);
+    lds_bar();
+    TRACE_OPS(1);
+
+    // ---- q (norm + RoPE), the new token's k / v (the owner only)
+    float qlo[G][8], qhi[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float *qs = (const float *)sm + g * FD_HD;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            qlo[g][e] = qs[sub * 8 + e];
+            qhi[g][e] = qs[64 + sub * 8 + e];
+        }
+    }
+    const bool owner = FUSED && posv >= t0 && posv < t1;  // uniform
+    uint16_t *knew16 = (uint16_t *)(sm + (QC + 3) * 1024), *vnew16 = knew16 + FD_HD;
+    if (FUSED) {
+        const float *kn = (const float *)(sm + QC * 1024), *vn = kn + FD_HD;
+        const float *qw = (const float *)(sm + (QC + 1) * 1024), *kw = qw + FD_HD;
+        const float *cs = (const float *)(sm + (QC + 2) * 1024);
+        float wlo[8], whi[8], co[8], sn[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            wlo[e] = qw[sub * 8 + e];
+            whi[e] = qw[64 + sub * 8 + e];
+            co[e] = cs[2 * (sub * 8 + e)];
+            sn[e] = cs[2 * (sub * 8 + e) + 1];
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) norm_rope16(qlo[g], qhi[g], wlo, whi, co, sn, p.eps);
+        if (owner && wave == 0) {
+            float klo[8], khi[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                klo[e] = kn[sub * 8 + e];
+                khi[e] = kn[64 + sub * 8 + e];
+                wlo[e] = kw[sub * 8 + e];
+                whi[e] = kw[64 + sub * 8 + e];
+            }
+            norm_rope16(klo, khi, wlo, whi, co, sn, p.eps);  // all 64 lanes (8 copies of the head)
+            if (lane < 8) {
+                *(u32x4 *)(knew16 + sub * 8) = u32x4{pack_h2(klo[0], klo[1]), pack_h2(klo[2], klo[3]),
+                                                     pack_h2(klo[4], klo[5]), pack_h2(klo[6], klo[7])};
+                *(u32x4 *)(knew16 + 64 + sub * 8) = u32x4{pack_h2(khi[0], khi[1]), pack_h2(khi[2], khi[3]),
+                                                          pack_h2(khi[4], khi[5]), pack_h2(khi[6], khi[7])};
+            }
+            *(uint32_t *)(vnew16 + 2 * lane) = pack_h2(vn[2 * lane], vn[2 * lane + 1]);
+        }
+    }
+    const uint32_t s_own = owner ? (posv - t0) / AR_TS : ~0u, r_own = owner ? (posv - t0) % AR_TS : 0u;
+
+    // ---- the ring, NG sub-chunks per step (group gq takes sub-chunk
+    // NG k + gq). Wave w4 of a group takes tokens 16 w4 .. 16 w4 + 15 of its
+    // sub-chunk: for the scores, lane group grp (8 lanes, 16 dims each)
+    // tokens grp and grp + 8; for P*V, lane (vrow = lane / 16, vcol = lane %
+    // 16) dims 8 vcol .. of tokens vrow + 4 k.
+    const uint32_t vrow = lane >> 4, vcol = lane & 15;
+    float m_run[G], l_run[G], acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m_run[g] = -INFINITY;
+        l_run[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
+    }
+    float *psw = ps + wave * G * 16;
+    const uint32_t nstep = (nsub + NG - 1) / NG;
+    for (uint32_t k = 0; k < nstep; k++) {
+        // sub-chunks up to NG k + NG - 1 must have landed; later ones stay in
+        // flight (issued so far: the prologue's AR_D, then NG per step from
+        // step 1 on, after its wait)
+        const uint32_t last = min(NG * k + NG, nsub) - 1;
+        const uint32_t issued = min(nsub, k ? NG * k + AR_D - NG : (uint32_t)AR_D);
+        wait_vm_dyn((issued - 1 - last) * KVW);
+        lds_bar();
+        if (k < 2) TRACE_OPS(5 + 2 * k);
+        if (k) {  // refill the slots of step k - 1
+            for (uint32_t s = NG * k + AR_D - NG; s < NG * k + AR_D && s < nsub; s++) issue_kv(s);
+        }
+        if (s_own >= NG * k && s_own < NG * k + NG) {  // uniform: substitute the new token's K and V rows
+            uint8_t *Ks = lds + (s_own % AR_D) * AR_SLOT;
+            if (tid < 16) *(u32x4 *)(Ks + r_own * 256 + tid * 16) = *(const u32x4 *)((const uint8_t *)knew16 + tid * 16);
+            else if (tid < 32)
+                *(u32x4 *)(Ks + AR_SLOT / 2 + r_own * 256 + (tid - 16) * 16) =
+                    *(const u32x4 *)((const uint8_t *)vnew16 + (tid - 16) * 16);
+            lds_bar();
+        }
+        const uint32_t s = NG * k + gq;
+        if (s < nsub) {  // uniform per wave
+            const uint8_t *Ks = lds + (s % AR_D) * AR_SLOT, *Vs = Ks + AR_SLOT / 2;
+            const uint32_t ts = t0 + s * AR_TS;
+            float sc[2][G];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t tt = w4 * 16 + grp + 8 * j;
+                const u32x4 k0 = *(const u32x4 *)(Ks + tt * 256 + sub * 16);
+                const u32x4 k1 = *(const u32x4 *)(Ks + tt * 256 + 128 + sub * 16);
+                const uint32_t kw8[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+                float kf[16];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    kf[2 * e] = h2f(kw8[e]);
+                    kf[2 * e + 1] = h2f(kw8[e] >> 16);
+                }
+                const bool valid = ts + tt < t1;
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    float sacc = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        sacc = fmaf(qlo[g][e], kf[e], sacc);
+                        sacc = fmaf(qhi[g][e], kf[8 + e], sacc);
+                    }
+                    sacc = sum8(sacc) * p.scale;  // dot * scale, as cpuAttention
+                    sc[j][g] = valid ? sacc : -INFINITY;
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float m = fmaxf(sc[0][g], sc[1][g]);
+                m = rows_max(fmaxf(m, dpp_f<0x140>(m)));  // uniform within each 8-lane group: over the wave
+                const float mn = fmaxf(m_run[g], m);
+                const float ms = mn == -INFINITY ? 0.f : mn;
+                const float f = m_run[g] == -INFINITY ? 0.f : expf(m_run[g] - ms);
+                const float p0 = expf(sc[0][g] - ms), p1 = expf(sc[1][g] - ms);
+                if (sub == 0) {
+                    psw[g * 16 + grp] = p0;
+                    psw[g * 16 + grp + 8] = p1;
+                }
+                float l = p0 + p1;
+                l = rows_sum(l + dpp_f<0x140>(l));
+                l_run[g] = fmaf(l_run[g], f, l);
+                m_run[g] = mn;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[g][e] *= f;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's probabilities are in LDS
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const uint32_t i = vrow + 4 * kk, tt = w4 * 16 + i;
+                u32x4 v = *(const u32x4 *)(Vs + tt * 256 + vcol * 16);
+                if (ts + tt >= t1) v = u32x4{0, 0, 0, 0};
+                const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+                float vf[8];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    vf[2 * e] = h2f(vw[e]);
+                    vf[2 * e + 1] = h2f(vw[e] >> 16);
+                }
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float pr = psw[g * 16 + i];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[g][e] = fmaf(pr, vf[e], acc[g][e]);
+                }
+            }
+        }
+        if (k < 2) TRACE_OPS(6 + 2 * k);
+    }
+    TRACE_OPS(2);
+    // ---- the new row to the cache (after every copy of this workgroup)
+    if (owner && tid < 32) {
+        const uint32_t ph = phys(posv);
+        uint16_t *dst = (tid < 16 ? p.kc : p.vc) + ((size_t)kvh * p.cache_tokens + ph) * FD_HD + (tid & 15) * 8;
+        *(u32x4 *)dst = *(const u32x4 *)((const uint8_t *)(tid < 16 ? knew16 : vnew16) + (tid & 15) * 16);
+    }
+    // ---- combine the waves (in the ring's LDS, free now): token rows within
+    // a wave, then waves
+    float *wm = (float *)lds, *wl = wm + AW * G, *wo = wl + AW * G;  // [AW][G], [AW][G], [AW][G][128]
+    lds_bar();  // every wave is done with the ring
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float a = acc[g][e];
+            a += __shfl_xor(a, 16, 64);
+            a += __shfl_xor(a, 32, 64);
+            acc[g][e] = a;
+        }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        if (lane < 16) {
+            *(f32x4 *)(wo + (wave * G + g) * FD_HD + 8 * vcol) = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+            *(f32x4 *)(wo + (wave * G + g) * FD_HD + 8 * vcol + 4) = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+        }
+        if (lane == 0) {
+            wm[wave * G + g] = m_run[g];
+            wl[wave * G + g] = l_run[g];
+        }
+    }
+    __syncthreads();
+    for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += AT) {
+        const uint32_t g = o / FD_HD, d = o % FD_HD;
+        float M = wm[g];
+#pragma unroll
+        for (int w = 1; w < AW; w++) M = fmaxf(M, wm[w * G + g]);
+        const float Ms = M == -INFINITY ? 0.f : M;
+        float O = 0.f, L = 0.f;
+#pragma unroll
+        for (int w = 0; w < AW; w++) {
+            const float f = wm[w * G + g] == -INFINITY ? 0.f : expf(wm[w * G + g] - Ms);
+            O = fmaf(wo[(w * G + g) * FD_HD + d], f, O);
+            L = fmaf(wl[w * G + g], f, L);
+        }
+        float *pp = p.part + ((size_t)(kvh * G + g) * p.n_chunks + c) * (FD_HD + 2);
+        st_dev(pp + d, O);
+        if (d == 0) {
+            st_dev(pp + FD_HD, M);
+            st_dev(pp + FD_HD + 1, L);
+        }
+    }
+    TRACE_OPS(3);
+    // ---- publish; the last arrival of this kv head merges. The partials
+    // went out as device-scope stores (coherent across the XCDs' L2s);
+    // s_waitcnt 0 in every wave and the barrier make them complete before the
+    // counter increment, and the merger reads them with device-scope loads.
+    __shared__ uint32_t s_prev;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) s_prev = __hip_atomic_fetch_add(p.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_prev != nv - 1) return;
+    TRACE_OPS(4);
+    if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    attn_merge<G, G <= 4 ? 40 : 12, COH>(p, kvh * G, nv, false);
+}
+

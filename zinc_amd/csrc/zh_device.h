@@ -223,6 +223,36 @@ ZH_DEV void xq_store_block32(float xi, int l, XQView v, uint32_t blk) {
     if ((l & 15) == 0) v.xsum[blk * 2 + (l >> 4)] = (float)s * sc;
 }
 
+// xq_store_block32 for a consumer in another workgroup of the same launch:
+// every word at device scope (each 4-lane group's limb bytes packed into a
+// dword first).
+ZH_DEV void xq_store_block32_dev(float xi, int l, XQView v, uint32_t blk) {
+    float a = half_max(fabsf(xi));
+    float inv, sc;
+    xq_scales(a, inv, sc);
+    int X = xq_quant(xi, inv);
+    int l0, l1, l2;
+    xq_limbs(X, l0, l1, l2);
+    const uint32_t b = ((uint32_t)(uint8_t)l0) | ((uint32_t)(uint8_t)l1 << 8) | ((uint32_t)(uint8_t)l2 << 16);
+    const uint32_t b1 = __shfl_down(b, 1, 64), b2 = __shfl_down(b, 2, 64), b3 = __shfl_down(b, 3, 64);
+    if ((l & 3) == 0) {
+        uint32_t *limb = (uint32_t *)(v.limb + (size_t)blk * 96);
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const uint32_t w = ((b >> (8 * k)) & 0xFF) | (((b1 >> (8 * k)) & 0xFF) << 8) |
+                               (((b2 >> (8 * k)) & 0xFF) << 16) | (((b3 >> (8 * k)) & 0xFF) << 24);
+            __hip_atomic_store(limb + k * 8 + l / 4, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    int s = X;
+    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x141, 0xF, 0xF, false);
+    s += __builtin_amdgcn_update_dpp(0, s, 0x140, 0xF, 0xF, false);
+    if (l == 0) st_dev(v.xs + blk, sc);
+    if ((l & 15) == 0) st_dev(v.xsum + blk * 2 + (l >> 4), (float)s * sc);
+}
+
 // Router top-k with softmax over the selected logits (softmax_topk_v2.comp,
 // topKSoftmax forward.zig:496-537), in one wave: lane l holds logits l,
 // l+64, l+128, l+192 (n <= 256). Exact f32 comparisons, the lowest index wins
@@ -274,12 +304,24 @@ ZH_DEV uint32_t lds_addr(const void *p) {
 ZH_DEV void dma16(const void *g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
+// The same copy at system scope: it reads past this XCD's L2, for data that
+// another workgroup of the same launch (perhaps on another XCD) stored at
+// device scope.
+ZH_DEV void dma16_sys(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc0 sc1" ::"v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+template <bool COH>
+ZH_DEV void dma16_act(const void *g, uint32_t lds) {
+    if (COH) dma16_sys(g, lds);
+    else dma16(g, lds);
+}
 template <int N>
 ZH_DEV void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 // Waits until at most n of this wave's vector-memory instructions are
-// outstanding; n is one of the counts the ring produces.
+// outstanding (n <= 40; larger counts wait for everything).
 ZH_DEV void wait_vm_dyn(uint32_t n) {
     switch (n) {
     case 0: wait_vm<0>(); break;
@@ -289,13 +331,51 @@ ZH_DEV void wait_vm_dyn(uint32_t n) {
     case 4: wait_vm<4>(); break;
     case 5: wait_vm<5>(); break;
     case 6: wait_vm<6>(); break;
+    case 7: wait_vm<7>(); break;
     case 8: wait_vm<8>(); break;
+    case 9: wait_vm<9>(); break;
     case 10: wait_vm<10>(); break;
+    case 11: wait_vm<11>(); break;
     case 12: wait_vm<12>(); break;
+    case 13: wait_vm<13>(); break;
+    case 14: wait_vm<14>(); break;
+    case 15: wait_vm<15>(); break;
     case 16: wait_vm<16>(); break;
+    case 17: wait_vm<17>(); break;
+    case 18: wait_vm<18>(); break;
+    case 19: wait_vm<19>(); break;
+    case 20: wait_vm<20>(); break;
+    case 21: wait_vm<21>(); break;
+    case 22: wait_vm<22>(); break;
+    case 23: wait_vm<23>(); break;
     case 24: wait_vm<24>(); break;
+    case 25: wait_vm<25>(); break;
+    case 26: wait_vm<26>(); break;
+    case 27: wait_vm<27>(); break;
+    case 28: wait_vm<28>(); break;
+    case 29: wait_vm<29>(); break;
+    case 30: wait_vm<30>(); break;
+    case 31: wait_vm<31>(); break;
+    case 32: wait_vm<32>(); break;
+    case 33: wait_vm<33>(); break;
+    case 34: wait_vm<34>(); break;
+    case 35: wait_vm<35>(); break;
+    case 36: wait_vm<36>(); break;
+    case 37: wait_vm<37>(); break;
+    case 38: wait_vm<38>(); break;
+    case 39: wait_vm<39>(); break;
+    case 40: wait_vm<40>(); break;
     default: wait_vm<0>(); break;  // conservative: everything
     }
+}
+// The thread index, opaque to the optimiser: what a phase of the persistent
+// kernel derives from it is recomputed in that phase instead of being
+// hoisted out of the layer loop (where it would stay live in registers
+// through every other phase).
+ZH_DEV uint32_t phase_tid() {
+    uint32_t t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
 }
 // Barrier for LDS data: this wave's LDS accesses complete, then s_barrier.
 // Unlike __syncthreads it does not drain the wave's DMAs in flight.

@@ -66,6 +66,11 @@ struct zh_engine {
     uint32_t *routing = nullptr, *am_part = nullptr, *st = nullptr, *prompt = nullptr, *ring = nullptr;
     uint32_t *grp_cnt = nullptr;  // SwiGLU-output XQ: one counter per 32-row group (kept zero between launches)
     uint32_t *router_cnt = nullptr;  // router top-k: workgroups finished (kept zero between launches)
+    // persistent decode-layers kernel: barrier / merge words (zero between
+    // launches) and the device table of layer pointers
+    uint32_t *step_ctl = nullptr;
+    zh_step_layer *step_layers = nullptr;
+    bool persistent = false;  // zh_engine_set_persistent
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
@@ -318,6 +323,7 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->prompt, 4ull * MAX_PROMPT}, {(void **)&e->ring, 4ull * MAX_GEN}, {(void **)&e->pages, 4ull * e->n_pages},
         {(void **)&e->inv_freq, 4ull * hd / 2}, {(void **)&e->rope_cs, 8ull * c.max_ctx * (hd / 2)},
         {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)}, {(void **)&e->router_cnt, 4},
+        {(void **)&e->step_ctl, zh_step_ctl_bytes()}, {(void **)&e->step_layers, sizeof(zh_step_layer) * c.n_layers},
     };
     uint64_t aoff = 0;
     for (auto &a : acts) aoff = align256(aoff + a.bytes);
@@ -338,6 +344,19 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
     std::vector<float> inv(hd / 2);
     for (uint32_t k = 0; k < hd / 2; k++) inv[k] = 1.0f / powf(c.rope_base, (float)(2 * k) / (float)hd);
     me = hipMemcpyAsync(e->inv_freq, inv.data(), 4ull * hd / 2, hipMemcpyHostToDevice, ctx->stream);
+    // the layer table of the persistent decode-layers kernel (addresses only:
+    // valid before the weights are written)
+    std::vector<zh_step_layer> tab(c.n_layers);
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const Layer &y = e->L[l];
+        const uint8_t *A = e->arena;
+        tab[l] = zh_step_layer{A + y.wq.off, A + y.wk.off, A + y.wv.off, A + y.wo.off, A + y.gate.off, A + y.up.off,
+                               A + y.down.off, (const float *)(A + y.attn_norm.off), (const float *)(A + y.ffn_norm.off),
+                               (const float *)(A + y.q_norm.off), (const float *)(A + y.k_norm.off), y.kc, y.vc};
+    }
+    if (me == hipSuccess)
+        me = hipMemcpyAsync(e->step_layers, tab.data(), sizeof(zh_step_layer) * c.n_layers, hipMemcpyHostToDevice,
+                            ctx->stream);
     if (me == hipSuccess && zhk_rope_table(ctx, e->inv_freq, c.max_ctx, e->rope_cs) != ZH_OK) me = hipErrorUnknown;
     if (me != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess) {
         zh_engine_destroy(e);
@@ -536,6 +555,18 @@ extern "C" int zh_engine_set_pages(zh_engine *e, const uint32_t *pages, uint32_t
     return ZH_OK;
 }
 
+extern "C" int zh_engine_set_persistent(zh_engine *e, int on) {
+    if (!e) return ZH_ERR_INVALID_ARGUMENT;
+    if (e->persistent != (on != 0)) {
+        ZH_HIP(e->ctx, hipStreamSynchronize(e->ctx->stream));
+        if (e->g_out) hipGraphExecDestroy(e->g_out);
+        if (e->g_noout) hipGraphExecDestroy(e->g_noout);
+        e->g_out = e->g_noout = nullptr;
+        e->persistent = on != 0;
+    }
+    return ZH_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Host page pool: KvPagePool (src/scheduler/kv_cache.zig:43-125) -- a stack
 // of free page ids (allocation pops from the end, so a fresh pool hands out
@@ -608,6 +639,33 @@ static int record_collect(zh_engine *e) {
 // Launch groups of one layer (the unit zh_engine_time_kernel replays).
 enum : uint32_t { SK_QKV = 1, SK_ATTN = 2, SK_O = 4, SK_FFN_IN = 8, SK_FFN_OUT = 16, SK_ALL = 31, SK_HEAD = 32 };
 
+// The persistent decode-layers kernel's arguments for the whole step, and
+// whether it takes this engine's model (dense, every layer in the formats it
+// is built for, no engine sharing the device).
+static bool step_args(zh_engine *e, zh_step_args &a) {
+    const zh_model_config &m = e->c;
+    a = zh_step_args{};
+    a.layers = e->step_layers;
+    a.l0 = 0;
+    a.l1 = m.n_layers;
+    a.hidden = m.hidden; a.n_heads = m.n_heads; a.n_kv_heads = m.n_kv_heads; a.ffn = m.ffn; a.max_ctx = m.max_ctx;
+    a.eps = m.eps; a.scale = 1.0f / sqrtf((float)m.head_dim);
+    a.x = e->hidden; a.q = e->q; a.k = e->k; a.v = e->v; a.attn = e->attn; a.s = e->s;
+    a.xq_attn = e->xq_q; a.xq_s = e->xq_f; a.grp_cnt = e->grp_cnt;
+    a.rope_cs = e->rope_cs; a.pages = e->pages; a.n_pages = e->n_pages; a.ident = e->pages_ident ? 1u : 0u;
+    a.pos = zh_pos_src{0, e->st + ST_POS};
+    a.part = e->fd_part;
+    a.ctl = e->step_ctl;
+    if (!e->persistent || m.n_experts || !zhk_step_supported(e->ctx, a)) return false;
+    for (const Layer &y : e->L) {
+        const Tensor *q4[] = {&y.wq, &y.wk, &y.wv, &y.wo, &y.gate, &y.up};
+        for (const Tensor *t : q4)
+            if (t->type != ZH_Q4_K || t->off % 16) return false;
+        if (y.down.type != ZH_Q6_K || y.down.off % 16) return false;
+    }
+    return true;
+}
+
 // Records the decode step: embedding, layers [l0, l1) (only the launch
 // groups in `mask`), then (whole steps only) the output head and the step
 // advance.
@@ -626,7 +684,11 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     const bool lpb = !zh_knob("ZH_NO_LPB");
     // LDS-staged kernels with the norms, router top-k and expert combine fused
     const bool lds = !zh_knob("ZH_NO_LDS_DMMV");
-    for (uint32_t l = l0; l < m.n_layers && l < l1; l++) {
+    // the whole step's layers in one persistent launch when it takes the model
+    zh_step_args sa;
+    const bool persistent = whole && step_args(e, sa);
+    if (persistent) ERC(zhk_step_layers(c, sa));
+    for (uint32_t l = persistent ? m.n_layers : l0; l < m.n_layers && l < l1; l++) {
         const Layer &y = e->L[l];
         // kernel choice per layer, from the layer's own tensor types (a GGUF
         // Q4_K_M file mixes Q4_K and Q6_K attn_v / ffn_down across layers)

@@ -39,11 +39,17 @@ struct zh_ctx {
     // sharing weights): kernels must not wait on workgroups of their own grid
     // that may not be resident (the attention merge then needs no waiting).
     bool concurrent = false;
-    // Device error word: kernels OR in ZH_DEVERR_* bits for input they had
-    // to clamp (the launch still completes); zh_sync reports and clears it.
+    // Device control words: err_dev[0] is the error word, which kernels OR
+    // ZH_DEVERR_* bits into for input they had to clamp or a bounded wait
+    // that gave up (the launch still completes); zh_sync reports and clears
+    // it. err_dev[1] is the attention merge's wait limit in ticks of the
+    // 100 MHz s_memrealtime clock, read by the kernels at run time so that a
+    // captured graph follows zh_set_attn_wait_limit.
     uint32_t *err_dev = nullptr;
 };
-enum : uint32_t { ZH_DEVERR_EXPERT_ID = 1u };
+enum : uint32_t { ZH_DEVERR_EXPERT_ID = 1u, ZH_DEVERR_ATTN_WAIT = 2u, ZH_DEVERR_STEP_BARRIER = 4u };
+// default merge wait: 50 ms
+constexpr uint32_t ZH_ATTN_WAIT_TICKS = 5000000u;
 
 int zh_set_err(zh_ctx *ctx, int code, const char *fmt, ...);
 #define ZH_HIP(ctx, call)                                                                    \
@@ -193,3 +199,34 @@ int zhk_dmmv_ring(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const ui
 int zhk_dmmv_batched(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
                      const uint32_t *M, uint32_t K, uint32_t n_vec, const float *const *x, const void *const *xq,
                      float *const *y, const float *norm_w, float eps, uint32_t acc);
+
+// Persistent decode-layers kernel (zh_step.hip): the layers [l0, l1) of one
+// decode step in one launch of one workgroup per CU, the phases (Q/K/V,
+// attention, O, gate/up, down) separated by grid barriers.
+struct zh_step_layer {  // one layer's weights and cache (a device table of these)
+    const uint8_t *wq, *wk, *wv, *wo, *gate, *up, *down;
+    const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
+    uint16_t *kc, *vc;
+};
+struct zh_step_args {
+    const zh_step_layer *layers;  // device table, [n_layers]
+    uint32_t l0, l1;
+    uint32_t hidden, n_heads, n_kv_heads, ffn, max_ctx;
+    float eps, scale;
+    float *x, *q, *k, *v, *attn, *s;  // residual stream and activations
+    uint8_t *xq_attn, *xq_s;          // XQ images of the attention and SwiGLU outputs
+    uint32_t *grp_cnt;                // SwiGLU XQ group counters (zero between launches)
+    const float *rope_cs;
+    const uint32_t *pages;
+    uint32_t n_pages, ident;
+    zh_pos_src pos;                   // position of the token
+    float *part;                      // attention partials: n_heads x (CUs / n_kv_heads) x 130 f32
+    uint32_t *ctl;                    // zh_step_ctl_bytes() zeroed bytes (barriers, merge counters)
+};
+uint64_t zh_step_ctl_bytes();
+// The geometry the kernel is built for (hidden 2048 or 4096 = n_heads x 128,
+// FFN 12288 or 14336, 4 q heads per kv head, enough CUs); the caller checks
+// the layer formats (Q4_K Q/K/V/O/gate/up, Q6_K down, 16-byte aligned) and
+// that no other work shares the device. false: use the per-phase kernels.
+bool zhk_step_supported(zh_ctx *ctx, const zh_step_args &a);
+int zhk_step_layers(zh_ctx *ctx, const zh_step_args &a);

@@ -4,13 +4,13 @@
 
 #include "zh_device.h"
 #include "zh_internal.h"
+#include "zh_attn_common.h"
 
 static bool in_range(const zh_buf *b, uint64_t off, uint64_t n) { return b && off <= b->size && n <= b->size - off; }
 #define DPTR(b, off, T) ((T *)((char *)(b)->ptr + (off)))
 
 // Quantise one 32-element block held one value per lane across a 32-lane
 // group (l = lane index within the group) into XQ block `blk`.
-ZH_DEV uint32_t read_pos(zh_pos_src p) { return p.dev ? (*p.dev + p.value) : p.value; }
 
 // ---------------------------------------------------------------------------
 // RMSNorm (rms_norm_mul.comp / cpuRmsNormMul forward.zig:618-626).
@@ -201,235 +201,11 @@ extern "C" int zh_qk_norm_rope_kv_write(zh_ctx *c, zh_buf *q, const zh_buf *qw, 
 // RoPE pairs stay inside a lane. Cache layout [kv_head][token][128] fp16,
 // addressed through 16-token pages.
 // ---------------------------------------------------------------------------
-#define TRACE_OPS(slot) ZH_TRACE_POINT(slot)
 ZH_TRACE_DUMP_FN(zh_debug_trace_ops)
-constexpr int FD_MAXG = 8;   // q heads per kv head
-constexpr int FD_HD = 128;   // head_dim supported
-// 4 waves x TW tokens: one wave per SIMD, and the 8 kv heads map one per XCD
-// (workgroups go round robin over the 8 XCDs), so the chunks of a kv head
-// spread over its XCD's 32 CUs. TW (tokens per wave per sub-chunk) is a
-// template parameter chosen at launch:
-//  * 24 when the context capacity is at most 8192 tokens: a 4K context then
-//    runs 2 pipelined 96-token sub-chunks per workgroup over 22 chunks per
-//    kv head (15.6 us per layer against 16.4 us for one 136-token chunk over
-//    32 chunks: the second sub-chunk's K/V loads are in flight while the
-//    first is computed, and fewer partials are merged);
-//  * 32 for longer contexts: 128-token sub-chunks (32K context: 36.9 us
-//    against 38.8 us with 96 and 40.2 us with 160);
-//  * 40 for 8 q heads per kv head, which has no sub-chunk loop.
-constexpr int AD_W = 4;      // waves per workgroup
-constexpr int AD_T = AD_W * 64;
-constexpr int AD_TC_MIN = AD_W * 24;  // the shortest sub-chunk: sizes the partials
-// Chunk geometry modes: page-table lookups with chunk = blockIdx.y, the same
-// dispatched newest-first (grids larger than the device), or an identity page
-// table (physical token = logical token), where nothing waits on page entries
-// and the chunk length follows the context: ceil(seq / nd) rounded up to 8
-// tokens (at least TW) while that fits TC = 4 TW, with nd = CUs / kv heads, so
-// the chunks of all kv heads cover the device once (32 per head for 8 kv
-// heads: one XCD each).
-enum { AD_PAGED = 0, AD_PAGED_REV = 1, AD_IDENT = 2 };
-// Longer contexts: chunks of nsub consecutive TC-token sub-chunks (a
-// workgroup runs them in turn with an online softmax), so a kv head never has
-// more than nd chunks: the grid stays one round of one workgroup per CU (the
-// kernel's registers allow one) and the merge reads at most nd partials.
-ZH_DEV uint32_t attn_nsub(uint32_t seq, uint32_t nd, uint32_t tc) {
-    const uint32_t span = nd * tc;
-    return seq > span ? (seq + span - 1) / span : 1u;
-}
-ZH_DEV uint32_t attn_chunk_tokens(uint32_t seq, uint32_t nd, bool sub, uint32_t tw) {
-    const uint32_t tc = AD_W * tw, ct = ((seq + nd - 1) / nd + 7) / 8 * 8;
-    return seq > nd * tc ? tc * (sub ? attn_nsub(seq, nd, tc) : 1u) : max(ct, tw);
-}
-// Sub-chunks are compiled for up to 4 q heads per kv head (G = 8 would spill
-// its loop-carried state); G = 8 keeps TC-token chunks at long contexts.
-template <int G> constexpr bool attn_sub_ok() { return G <= 4; }
-static uint32_t attn_nd(uint32_t nkv, int cu_count) {
-    const uint32_t cu = cu_count > 0 && cu_count < 256 ? (uint32_t)cu_count : 256u;
-    const uint32_t nd = cu / nkv > 0 ? cu / nkv : 1u;
-    return nd < 256u ? nd : 256u;  // the merge keeps at most 256 chunk statistics in LDS
-}
-// chunk slots per head for sub-chunks of tc tokens (the partials, sized with
-// the shortest, hold any; a device with at most 256 CUs fits)
-static uint32_t attn_n_chunks(uint32_t max_seq, uint32_t nd, uint32_t tc = AD_TC_MIN) {
-    const uint32_t n = (max_seq + tc - 1) / tc;
-    return n > nd ? n : nd;
-}
 
 uint64_t zhk_flash_decode_partials_bytes(uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_seq) {
     // partials + two counter words per kv head (at most nh words)
     return (uint64_t)nh * attn_n_chunks(max_seq, attn_nd(nkv, 256)) * (hd + 2) * 4 + 4ull * nh + 256;
-}
-
-struct AttnP {
-    const float *q;                // FUSED: raw Q projection; else prepared (normed, roped) q
-    const float *k_new, *v_new;    // FUSED: raw K/V projection of the new token
-    const float *q_norm, *k_norm;  // FUSED: per-head RMSNorm weights (128)
-    const float *rope_cs;          // FUSED: [position][64] (cos, sin) pairs of pos * inv_freq
-    uint16_t *kc, *vc;
-    const uint32_t *pages;
-    uint32_t n_pages, cache_tokens;
-    zh_pos_src pos;  // FUSED: position of the new token (seq = pos + 1); else seq_len
-    float scale, eps;
-    float *part;     // [nq][n_chunks][130]
-    uint32_t n_chunks;
-    uint32_t *counters;  // [nkv], zero between launches
-    float *out;          // [nq * 128]
-    uint8_t *xq;         // optional XQ image of out
-    uint32_t nq;
-    uint32_t nd;         // AD_IDENT: target chunks per kv head
-    uint32_t no_wait;    // the last arrival merges every q head (no merger waits for others)
-    uint32_t ident;      // k_attn_ring: the page table is the identity (no lookups)
-};
-
-ZH_DEV float sum8(float v) { return row8_sum(v); }  // over the 8 lanes of a token group
-
-// RMSNorm (weights w) + NeoX RoPE on one head held as lo[e] = x[sub*8+e],
-// hi[e] = x[64+sub*8+e] (qk_norm_rope_kv_write.comp:67-171 arithmetic).
-ZH_DEV void norm_rope16(float (&lo)[8], float (&hi)[8], const float (&wlo)[8], const float (&whi)[8],
-                        const float (&co)[8], const float (&sn)[8], float eps) {
-    float sq = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; e++) sq = fmaf(lo[e], lo[e], fmaf(hi[e], hi[e], sq));
-    sq = sum8(sq);
-    const float rms_inv = 1.0f / sqrtf(sq / (float)FD_HD + eps);
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float a = wlo[e] * (lo[e] * rms_inv);
-        const float b = whi[e] * (hi[e] * rms_inv);
-        lo[e] = a * co[e] - b * sn[e];
-        hi[e] = a * sn[e] + b * co[e];
-    }
-}
-
-
-// Two f32 -> packed f16 with the hardware conversion (round to nearest
-// even; fp16 denormals are kept in this build's default FP mode), as the
-// cache write's @floatCast.
-ZH_DEV uint32_t pack_h2(float a, float b) {
-    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
-    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
-}
-
-// Row o (0..47) of the three pages a wave reads, page bases pa, pb, pc.
-ZH_DEV const uint16_t *kv_row(const uint16_t *h, size_t pa, size_t pb, size_t pc, uint32_t o) {
-    const uint32_t pi = o >> 4;
-    const size_t pg = pi == 0 ? pa : pi == 1 ? pb : pc;
-    return h + (pg * 16 + (o & 15)) * FD_HD;
-}
-
-// Merges the chunk partials of q heads h0 .. h0+GM-1: O = sum_c exp(m_c - M) O_c
-// / sum_c exp(m_c - M) l_c (the split-K combine of flash_decode.comp's
-// reduction). NBAT chunks per round of O loads (every load is issued, with
-// clamped addresses, so the wait counts stay static). Reads partials published at device scope; `poison` (a wait that
-// timed out) turns the outputs into NaN.
-template <int GM, int NBAT>
-ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
-    // any workgroup size of at least AD_T threads (every thread calls it)
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nthr = blockDim.x;
-    TRACE_OPS(11);
-    // Chunk merge. The first batch of each thread's O dims (NBAT chunks) is
-    // requested before the chunk statistics, so both arrive in about one
-    // round trip; the statistics pass leaves m_c in LDS for the weights.
-    // dims per thread: power of two with G*128/OPT <= AD_T
-    constexpr int OPT = GM * FD_HD <= AD_T ? 1 : GM * FD_HD <= 2 * AD_T ? 2 : GM * FD_HD <= 4 * AD_T ? 4 : 8;
-    constexpr int NTH = GM * FD_HD / OPT;
-    constexpr int MB = 256;                 // chunk statistics kept in LDS
-    __shared__ __align__(16) float sm[GM][MB];
-    __shared__ float hM[GM], hL[GM];
-    __shared__ float ob[GM * FD_HD];
-    float O[OPT];
-#pragma unroll
-    for (int k = 0; k < OPT; k++) O[k] = 0.f;
-    const uint32_t g_t = min(tid * OPT / FD_HD, (uint32_t)GM - 1), d0 = (tid * OPT) % FD_HD;
-    const float *pt = p.part + (size_t)(h0 + g_t) * p.n_chunks * (FD_HD + 2);
-    float v[NBAT][OPT];
-    auto load_o = [&](uint32_t cb) {
-#pragma unroll
-        for (int u = 0; u < NBAT; u++) {
-            const float *pc = pt + (size_t)min(cb + u, nv - 1) * (FD_HD + 2) + d0;
-            if (OPT == 1) {
-                v[u][0] = ld_dev(pc);
-            } else {
-#pragma unroll
-                for (int w = 0; w < OPT / 2; w++) {
-                    const uint64_t x = ld_dev64(pc + 2 * w);
-                    v[u][2 * w] = __uint_as_float((uint32_t)x);
-                    v[u][2 * w + 1] = __uint_as_float((uint32_t)(x >> 32));
-                }
-            }
-        }
-    };
-    const bool one_batch = nv <= (uint32_t)NBAT;  // uniform
-    if (one_batch) load_o(0);
-    asm volatile("" ::: "memory");  // the O loads go out before the statistics loads
-    for (uint32_t g = wave; g < (uint32_t)GM; g += nthr / 64) {
-        const float *pp = p.part + (size_t)(h0 + g) * p.n_chunks * (FD_HD + 2);
-        float m = -INFINITY, l = 0.f;
-        for (uint32_t c = lane; c < nv; c += 64) {
-            const uint64_t ml = ld_dev64(pp + (size_t)c * (FD_HD + 2) + FD_HD);
-            const float mc = __uint_as_float((uint32_t)ml), lc = __uint_as_float((uint32_t)(ml >> 32));
-            if (c < MB) sm[g][c] = mc;
-            const float mn = fmaxf(m, mc);
-            l = fmaf(l, m == -INFINITY ? 0.f : expf(m - mn), lc * expf(mc - mn));
-            m = mn;
-        }
-        const float M = wave_max(m);
-        l = wave_sum(m == -INFINITY ? 0.f : l * expf(m - M));
-        if (lane == 0) { hM[g] = M; hL[g] = l; }
-    }
-    TRACE_OPS(12);
-    __syncthreads();
-    TRACE_OPS(13);
-    const float Mt = hM[g_t];
-    if (one_batch) {
-        // weights exp(m_c - M) once per (head, chunk), in place in LDS
-        for (uint32_t i = tid; i < (uint32_t)GM * NBAT; i += nthr) {
-            const uint32_t g = i / NBAT, c = i % NBAT;
-            sm[g][c] = c < nv ? expf(sm[g][c] - hM[g]) : 0.f;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int u4 = 0; u4 < NBAT; u4 += 4) {
-            const f32x4 w4 = *(const f32x4 *)&sm[g_t][u4];
-#pragma unroll
-            for (int k = 0; k < OPT; k++) {
-                O[k] = fmaf(v[u4][k], w4.x, O[k]);
-                O[k] = fmaf(v[u4 + 1][k], w4.y, O[k]);
-                O[k] = fmaf(v[u4 + 2][k], w4.z, O[k]);
-                O[k] = fmaf(v[u4 + 3][k], w4.w, O[k]);
-            }
-        }
-    } else {
-        // long contexts: one round of loads per NBAT chunks
-        for (uint32_t cb = 0; cb < nv; cb += NBAT) {
-            load_o(cb);
-#pragma unroll
-            for (int u = 0; u < NBAT; u++) {
-                const uint32_t c = cb + u;
-                const float mc = c < MB ? sm[g_t][c < MB ? c : 0] : ld_dev(pt + (size_t)min(c, nv - 1) * (FD_HD + 2) + FD_HD);
-                const float wgt = c < nv ? expf(mc - Mt) : 0.f;
-#pragma unroll
-                for (int k = 0; k < OPT; k++) O[k] = fmaf(v[u][k], wgt, O[k]);
-            }
-        }
-    }
-    TRACE_OPS(6);
-    if (tid < (uint32_t)NTH) {
-#pragma unroll
-        for (int k = 0; k < OPT; k++) {
-            const float r = poison ? __builtin_nanf("") : hL[g_t] > 0.f ? O[k] / hL[g_t] : 0.f;
-            ob[tid * OPT + k] = r;
-            if (p.out) p.out[(size_t)h0 * FD_HD + tid * OPT + k] = r;
-        }
-    }
-    TRACE_OPS(7);
-    if (p.xq) {
-        __syncthreads();
-        XQView v = xq_view(p.xq, p.nq * FD_HD / 32);
-        for (uint32_t o = tid; o < (uint32_t)GM * FD_HD; o += nthr)  // whole 32-lane groups (GM*128 % 32 == 0)
-            xq_store_block32(ob[o], o & 31, v, (h0 * FD_HD + o) / 32);
-    }
-    TRACE_OPS(5);
 }
 
 template <int G, bool FUSED, int MODE, int TW>
@@ -475,6 +251,7 @@ static int attn_launch(zh_ctx *c, const AttnP &p0, uint32_t nkv, uint32_t G, uin
     AttnP p = p0;
     p.nd = attn_nd(nkv, c->cu_count);
     p.no_wait = c->concurrent ? 1u : 0u;
+    p.ctl = c->err_dev;
     // tokens per wave (see AD_W): sub-chunks only with identity pages and at
     // most 4 q heads per kv head
     const bool sub = ident && G <= 4;
@@ -588,6 +365,7 @@ int zhk_attn_decode_fused_z(zh_ctx *c, uint32_t n, const float *const *q, const 
     p.cache_tokens = cache_tokens; p.pos = zh_pos_src{0, pos_dev[0]}; p.scale = scale; p.eps = eps; p.nq = nh;
     p.nd = attn_nd(nkv, c->cu_count);
     p.no_wait = 1;  // chunks of other sequences share the device: no merger waits
+    p.ctl = c->err_dev;
     const uint32_t tw = max_seq <= 8192 ? 24u : 32u;
     p.n_chunks = attn_n_chunks(max_seq, p.nd, AD_W * tw);
     if (p.n_chunks > p.nd) p.n_chunks = p.nd;

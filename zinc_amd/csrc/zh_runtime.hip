@@ -36,6 +36,7 @@ extern "C" const char *zh_status_string(int s) {
     case ZH_ERR_IO: return "IoError";
     case ZH_ERR_NOT_FOUND: return "NotFound";
     case ZH_ERR_KV_CACHE_EXHAUSTED: return "KvCacheExhausted";
+    case ZH_ERR_WAIT_TIMEOUT: return "WaitTimeout";
     default: return "unknown";
     }
 }
@@ -55,7 +56,9 @@ extern "C" int zh_init(int device, zh_ctx **out) {
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) { delete c; return ZH_ERR_HIP; }
     for (int i = 0; i < 64; i++)
         if (hipEventCreate(&c->ev[i]) != hipSuccess) { delete c; return ZH_ERR_HIP; }
-    if (hipMalloc((void **)&c->err_dev, 256) != hipSuccess || hipMemset(c->err_dev, 0, 4) != hipSuccess) {
+    const uint32_t ctl[2] = {0u, ZH_ATTN_WAIT_TICKS};
+    if (hipMalloc((void **)&c->err_dev, 256) != hipSuccess ||
+        hipMemcpy(c->err_dev, ctl, sizeof ctl, hipMemcpyHostToDevice) != hipSuccess) {
         zh_destroy(c);
         return ZH_ERR_HIP;
     }
@@ -94,10 +97,26 @@ extern "C" int zh_sync(zh_ctx *c) {
     ZH_HIP(c, hipMemcpy(&e, c->err_dev, 4, hipMemcpyDeviceToHost));
     if (e) {
         ZH_HIP(c, hipMemset(c->err_dev, 0, 4));
+        if (e & ZH_DEVERR_STEP_BARRIER)
+            return zh_set_err(c, ZH_ERR_WAIT_TIMEOUT, "a grid barrier of the decode-layers kernel gave up waiting "
+                                                      "(its workgroups were not all resident); the step's output "
+                                                      "is not valid");
+        if (e & ZH_DEVERR_ATTN_WAIT)
+            return zh_set_err(c, ZH_ERR_WAIT_TIMEOUT, "a decode-attention merger gave up waiting for the other "
+                                                      "chunks of its kv head; that head's output is NaN");
         if (e & ZH_DEVERR_EXPERT_ID)
             return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "an expert id at or past the weights' expert count "
                                                           "(zh_dmmv_moe clamped it to the last expert)");
     }
+    return ZH_OK;
+}
+
+extern "C" int zh_set_attn_wait_limit(zh_ctx *c, uint32_t microseconds) {
+    if (!c) return ZH_ERR_INVALID_ARGUMENT;
+    if (microseconds > 40000000u) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "wait limit above 40 s");
+    const uint32_t ticks = microseconds * 100u;
+    ZH_HIP(c, hipStreamSynchronize(c->stream));
+    ZH_HIP(c, hipMemcpy(c->err_dev + 1, &ticks, 4, hipMemcpyHostToDevice));
     return ZH_OK;
 }
 

@@ -174,6 +174,10 @@ class InferenceEngine:
         a = np.ascontiguousarray(pages, dtype=np.uint32)
         self.ctx.check(lib().zh_engine_set_pages(self.h, C.c_void_p(a.ctypes.data), len(a)))
 
+    def set_persistent(self, on=True):
+        """Run the step's layers as one persistent launch where the model takes it."""
+        self.ctx.check(lib().zh_engine_set_persistent(self.h, int(bool(on))))
+
     def bytes_per_token(self, L):
         return lib().zh_engine_bytes_per_token(self.h, L)
 

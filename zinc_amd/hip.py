@@ -18,7 +18,7 @@ OK = 0
 STATUS = {1: "UnsupportedQuantType", 2: "InvalidArgument", 3: "HipError",
           4: "ContextLengthExceeded", 5: "OutOfMemory", 6: "TensorNotFound", 7: "InvalidMagic",
           8: "UnknownMetadataType", 9: "UnsupportedArchitecture", 10: "TruncatedFile", 11: "IoError",
-          12: "NotFound", 13: "KvCacheExhausted"}
+          12: "NotFound", 13: "KvCacheExhausted", 14: "WaitTimeout"}
 
 BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), MXFP4: (32, 17), F32: (1, 4), F16: (1, 2)}
 
@@ -78,6 +78,7 @@ SIGNATURES = {
     "zh_status_string": (C.c_char_p, [_i32]),
     "zh_device_info": (_i32, [_P, C.c_char_p, C.c_size_t, C.POINTER(_i32), C.POINTER(_u64)]),
     "zh_sync": (_i32, [_P]),
+    "zh_set_attn_wait_limit": (_i32, [_P, _u32]),
     "zh_buf_alloc": (_i32, [_P, _u64, C.POINTER(_P)]),
     "zh_buf_free": (None, [_P, _P]),
     "zh_buf_size": (_u64, [_P]),
@@ -124,6 +125,7 @@ SIGNATURES = {
     "zh_engine_tensor": (_i32, [_P, _u64, C.POINTER(_P), C.POINTER(_u64), C.POINTER(_u64)]),
     "zh_engine_read_kv": (_i32, [_P, _u32, _u32, _u32, _u32, _P]),
     "zh_engine_set_pages": (_i32, [_P, _P, _u32]),
+    "zh_engine_set_persistent": (_i32, [_P, _i32]),
     "zh_dmmv_supported": (_i32, [_u32, _u32]),
     "zh_engine_group_kernels": (_i32, [_P, _u32, C.c_char_p, C.c_size_t]),
     "zh_kv_pool_create": (_i32, [_u32, _u32, C.POINTER(_P)]),
@@ -254,6 +256,10 @@ class Context:
 
     def sync(self):
         self.check(lib().zh_sync(self.h))
+
+    def set_attn_wait_limit(self, microseconds):
+        """Bound of the decode attention's merge wait (0: give up at once)."""
+        self.check(lib().zh_set_attn_wait_limit(self.h, int(microseconds)))
 
     def alloc(self, size):
         b = Buffer(self, size)
