@@ -90,6 +90,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=16)
+    ap.add_argument("--pages", choices=["ident", "shuffle"], default="ident",
+                    help="KV page table: identity, or a seeded permutation (the paged attention kernel)")
+    ap.add_argument("--persistent", type=int, default=0,
+                    help="1: the step's layers in one persistent launch (zh_engine_set_persistent)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -105,6 +109,9 @@ def main():
     log(f"device: {name}, {cus} CUs, {hbm / 2**30:.0f} GiB")
     t0 = time.time()
     eng = zinc_amd.InferenceEngine(ctx, cfg)
+    if args.pages == "shuffle":
+        eng.set_pages(np.random.default_rng(17).permutation(cfg["max_ctx"] // 16).astype(np.uint32))
+    eng.set_persistent(bool(args.persistent))
     eng.prefill_kv_random(PREFILL, 7)
     ctx.sync()
     log(f"engine init + synthetic weights + KV prefill: {time.time() - t0:.1f}s")
@@ -165,7 +172,8 @@ def main():
                    "context_start": pos, "bytes_per_token": bytes_tok,
                    "token_roofline_frac": round(bytes_tok * tok_s / 1e9 / PEAK_HBM_GBS, 4),
                    "token_frac_of_stream_ceiling": round(bytes_tok * tok_s / 1e9 / ceiling, 4),
-                   "gpu_ms_per_step": round(gpu_ms / args.steps, 4)},
+                   "gpu_ms_per_step": round(gpu_ms / args.steps, 4),
+                   "kv_pages": args.pages, "persistent_layers": bool(args.persistent)},
         "roofline": roof,
         "per_kernel": per_kernel,
         "step_consistency": per_kernel_graph,

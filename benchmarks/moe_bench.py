@@ -31,11 +31,15 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--pages", choices=["ident", "shuffle"], default="ident",
+                    help="KV page table: identity, or a seeded permutation (the paged attention kernel)")
     a = ap.parse_args()
     ctx = hip.Context(0)
     cfg = dict(MOE_48L)
     cfg["max_ctx"] = (PREFILL + N_PROMPT + a.warmup + a.steps + 16 + 15) // 16 * 16
     eng = InferenceEngine(ctx, cfg)
+    if a.pages == "shuffle":
+        eng.set_pages(np.random.default_rng(17).permutation(cfg["max_ctx"] // 16).astype(np.uint32))
     eng.prefill_kv_random(PREFILL, 7)
     ctx.sync()
     rng = np.random.default_rng(4321)

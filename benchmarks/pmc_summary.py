@@ -44,7 +44,8 @@ def _split(rows, groups, per_group):
     if nw == 0:
         raise SystemExit(f"expected the calibration write after the reads, got {after[0]['Kernel_Name']}")
     cal_w = sum(float(r["Counter_Value"]) for r in after[:nw])
-    body = after[nw:]
+    # the runtime's own copies / fills (reading results back) are not groups
+    body = [r for r in after[nw:] if not r["Kernel_Name"].startswith("__amd_rocclr")]
     if len(body) != len(groups) * per_group:
         raise SystemExit(f"expected {len(groups)} x {per_group} dispatches after calibration, got {len(body)}")
     blocks = {g: body[i * per_group:(i + 1) * per_group] for i, g in enumerate(groups)}

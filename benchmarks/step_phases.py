@@ -1,0 +1,71 @@
+"""Per-workgroup timelines of the decode step's phases, from the debug
+build's s_memrealtime trace points (100 MHz clock):
+
+  - the persistent decode-layers kernel (zh_engine_set_persistent): start and
+    end of each of layer 10's five phases in every workgroup, and the start
+    of layer 11 (grid barrier + next-phase prefetch in the gaps);
+  - the attention body inside it: its own trace points, relative to each
+    workgroup's start (small copies landed, q fragments, ring steps,
+    partials, merge).
+
+Build the debug library first (it also compiles the points in):
+
+    python -m zinc_amd.build --debug _work/dbg
+    ZH_LIB_PATH=_work/dbg/libzinc_hip.so python -m benchmarks.step_phases
+
+Config 3's model (8B shapes, KV context 4096 + 2 decoded tokens).
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+
+from zinc_amd import hip
+from zinc_amd.engine import DENSE_8B, InferenceEngine
+
+ATTN_POINTS = {1: "small copies landed", 9: "q fragments", 10: "new K/V row ready", 5: "ring step 0 start",
+               6: "ring step 0 end", 7: "ring step 1 start", 8: "ring step 1 end", 2: "after the ring",
+               3: "partials stored", 4: "merger: start", 11: "merger: merge start", 12: "merger: stats",
+               13: "merger: output"}
+
+
+def main():
+    if not os.environ.get("ZH_LIB_PATH"):
+        sys.exit("set ZH_LIB_PATH to the debug build's libzinc_hip.so")
+    L = hip.lib()
+    L.zh_debug_trace_step.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
+    ctx = hip.Context(0)
+    cfg = dict(DENSE_8B)
+    cfg["max_ctx"] = 4096 + 64
+    eng = InferenceEngine(ctx, cfg)
+    eng.set_persistent(True)
+    eng.prefill_kv_random(4096, 7)
+    eng.generate([17, 18], 4, start_pos=4096)
+    ctx.sync()
+    a = np.zeros(1024 * 32, np.uint64)
+    L.zh_debug_trace_step(a.ctypes.data_as(C.POINTER(C.c_uint64)), 1024 * 32)
+    t = a.reshape(1024, 32)[:ctx.info()[1]].astype(np.int64)
+    base = t[:, 0].min()
+    names = ["Q/K/V", "attention", "O", "gate/up", "down"]
+    print("persistent kernel, layer 10 (us from the first workgroup's start):")
+    for s in list(range(10)) + [10]:
+        r = (t[:, s] - base) * 0.01
+        lab = (names[s // 2] + (" start" if s % 2 == 0 else " end")) if s < 10 else "layer 11 start"
+        print(f"  {lab:16s}: min {r.min():7.2f}  p50 {np.median(r):7.2f}  max {r.max():7.2f}")
+    ta = t[:, 16:]
+    ok = ta[:, 0] > 0
+    print("attention body (last layer of the last step), us from each workgroup's start:")
+    for s in sorted(ATTN_POINTS, key=lambda k: [1, 9, 10, 5, 6, 7, 8, 2, 3, 4, 11, 12, 13].index(k)):
+        col, st = ta[ok, s], ta[ok, 0]
+        m = col >= st  # points the workgroup reached in this launch
+        if not m.any():
+            continue
+        r = (col[m] - st[m]) * 0.01
+        print(f"  {ATTN_POINTS[s]:22s}: n={m.sum():3d}  min {r.min():6.2f}  p50 {np.median(r):6.2f}  max {r.max():6.2f}")
+    eng.deinit()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -660,7 +660,8 @@ struct zo_model {
      * layers of the last decode step, the smallest gap between the k-th
      * selected router logit and the best unselected one, as a fraction of
      * the layer's max |router logit| (a near tie that a sum in another order
-     * can flip) */
+     * can flip); layers whose selection includes a zero-probability expert
+     * have no such tie */
     float route_gap;
 };
 
@@ -945,15 +946,23 @@ uint32_t zo_model_decode_step(zo_model *m, uint32_t token, uint32_t pos, float *
             zo_dmmv(y->router, y->t[ZK_ROUTER], m->norm, m->rl, c->n_experts, H, 0, nt);
             zo_topk_softmax(m->rl, c->n_experts, c->n_experts_used, ids, w);
             {
+                /* selection is by softmax probability; when a selected expert
+                 * has probability 0 (underflow), every expert with a positive
+                 * probability is selected and no order between selected and
+                 * unselected ones matters for the output */
                 float kth = INFINITY, rest = -INFINITY, amax = 0.f;
-                for (uint32_t j = 0; j < c->n_experts_used; j++) kth = fminf(kth, m->rl[ids[j]]);
+                int zero = 0;
+                for (uint32_t j = 0; j < c->n_experts_used; j++) {
+                    kth = fminf(kth, m->rl[ids[j]]);
+                    zero |= w[j] == 0.f;
+                }
                 for (uint32_t i = 0; i < c->n_experts; i++) {
                     int sel = 0;
                     for (uint32_t j = 0; j < c->n_experts_used; j++) sel |= ids[j] == i;
                     if (!sel) rest = fmaxf(rest, m->rl[i]);
                     amax = fmaxf(amax, fabsf(m->rl[i]));
                 }
-                if (amax > 0.f) m->route_gap = fminf(m->route_gap, (kth - rest) / amax);
+                if (amax > 0.f && !zero) m->route_gap = fminf(m->route_gap, (kth - rest) / amax);
             }
             uint64_t gstride = zo_tensor_bytes(y->t[ZK_EXP_GATE], F, H), ustride = zo_tensor_bytes(y->t[ZK_EXP_UP], F, H);
             uint64_t dstride = zo_tensor_bytes(y->t[ZK_EXP_DOWN], H, F);

@@ -243,8 +243,14 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
             // the quantiser's max drops NaN: a poisoned head's blocks get NaN
             // scales so that the consumer's sums are NaN too
             if (poison && (o & 15) == 0) {
-                if ((o & 31) == 0) v.xs[blk] = __builtin_nanf("");
-                v.xsum[blk * 2 + ((o >> 4) & 1)] = __builtin_nanf("");
+                float *xs = v.xs + blk, *xz = v.xsum + blk * 2 + ((o >> 4) & 1);
+                if (COH) {
+                    if ((o & 31) == 0) st_dev(xs, __builtin_nanf(""));
+                    st_dev(xz, __builtin_nanf(""));
+                } else {
+                    if ((o & 31) == 0) *xs = __builtin_nanf("");
+                    *xz = __builtin_nanf("");
+                }
             }
         }
     }
@@ -280,33 +286,94 @@ constexpr int AR_TS = 64;                            // tokens per sub-chunk
 constexpr uint32_t AR_SLOT = AR_TS * 2 * FD_HD * 2;  // K then V: 32 KB
 constexpr int AR_D = 4;                              // ring slots
 constexpr uint32_t AR_MAXPG = 256;                   // page entries per chunk (CT <= 4096 tokens)
-// waves per workgroup: one group of four (eight, two groups each taking
-// alternate sub-chunks, measured the same at a 4K context)
-template <int G> constexpr int ar_waves() { return 4; }
+// waves per workgroup: two groups of four, each taking alternate sub-chunks
+template <int G> constexpr int ar_waves() { return 8; }
 // small copies, 1 KB each: q of the group (G / 2 KB), [k_new | v_new],
 // [q_norm | k_norm], [RoPE row | -]; then the new K / V row as f16 (512 B)
 template <int G> constexpr uint32_t ar_qc() { return (G * FD_HD * 4 + 1023) / 1024; }
 template <int G> constexpr uint32_t ar_small() { return (ar_qc<G>() + 3) * 1024 + 512; }
+// q's MFMA fragments (8 steps x 64 lanes x (hi, lo) 8 bytes) and the
+// heads' 1 / rms
+constexpr uint32_t AR_QFRAG = 8 * 64 * 16 + 64 * 4;
 template <int G, int AW = ar_waves<G>()>
 constexpr uint32_t ar_lds_bytes() {
-    return AR_D * AR_SLOT + ar_small<G>() + AR_MAXPG * 4 + AW * G * 16 * 4;
+    return AR_D * AR_SLOT + ar_small<G>() + AR_MAXPG * 4 + AR_QFRAG;
+}
+
+// Chunk geometry of workgroup (kv head, chunk c) at the position p.pos:
+// chunk length CT = ceil(seq / nd) rounded up to a 16-token page, the chunk's
+// tokens [t0, t1), its nsub 64-token sub-chunks (nv chunks hold tokens).
+struct AttnGeom {
+    uint32_t posv, seq, CT, nv, t0, t1, nsub;
+    ZH_DEVM AttnGeom(const AttnP &p, uint32_t c, bool fused) {
+        posv = p.pos.dev ? *p.pos.dev + p.pos.value : p.pos.value;
+        seq = fused ? posv + 1 : posv;
+        CT = ((seq + p.nd - 1) / p.nd + 15) / 16 * 16;
+        nv = (seq + CT - 1) / CT;
+        t0 = c * CT;
+        t1 = min(seq, t0 + CT);
+        nsub = c < nv ? (t1 - t0 + AR_TS - 1) / AR_TS : 0u;
+    }
+};
+
+// K/V copies of sub-chunk s into slot s % AR_D: 32 chunks of 1 KB (4 tokens
+// of one page; K then V), 32 / AW per wave. Rows past the chunk re-read its
+// last row (masked). 16-byte piece q of LDS row rr holds the row's piece
+// q ^ (rr % 16) (the MFMA fragment reads of 16 rows at one dim then hit 16
+// different bank groups). pgl: the chunk's page entries (unless identity).
+template <int AW>
+ZH_DEV void attn_issue_kv(const AttnP &p, const AttnGeom &g, uint32_t kvh, uint32_t s, uint32_t wave,
+                          uint32_t lane, uint32_t lds0, const uint32_t *pgl) {
+    const uint16_t *kbase = p.kc + (size_t)kvh * p.cache_tokens * FD_HD;
+    const uint16_t *vbase = p.vc + (size_t)kvh * p.cache_tokens * FD_HD;
+    const uint32_t slot = s % AR_D;
+#pragma unroll
+    for (uint32_t i = 0; i < 32 / AW; i++) {
+        const uint32_t j = wave + AW * i, kv = j >> 4;
+        const uint32_t rr = 4 * (j & 15) + (lane >> 4);  // row within the slot
+        const uint32_t t = min(g.t0 + s * AR_TS + rr, g.t1 - 1);
+        const uint32_t ph = p.ident ? t : pgl[(t - g.t0) >> 4] * 16u + (t & 15u);
+        const uint16_t *row = (kv ? vbase : kbase) + (size_t)ph * FD_HD;
+        dma16(row + ((lane & 15) ^ (rr & 15)) * 8, lds0 + slot * AR_SLOT + j * 1024);
+    }
+}
+
+// The chunk's page entries into LDS (a compiler-tracked load) and its first
+// sub-chunks' K/V copies, issued while the persistent kernel waits at the
+// grid barrier before the attention phase (the cache rows before the
+// position do not depend on the Q/K/V phase); returns the count (the body's
+// `pre`). Every thread of the workgroup calls it.
+template <int G, int AW>
+ZH_DEV uint32_t attn_ring_prefetch(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *lds, bool fused) {
+    const uint32_t tid = phase_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const AttnGeom g(p, c, fused);
+    if (g.nsub == 0) return 0;
+    uint32_t *pgl = (uint32_t *)(lds + AR_D * AR_SLOT + ar_small<G>());
+    if (!p.ident) {
+        for (uint32_t i = tid; i < (g.t1 - g.t0 + 15) / 16; i += AW * 64)
+            pgl[i] = p.pages[min(g.t0 / 16 + i, p.n_pages - 1)];
+        __syncthreads();
+    }
+    const uint32_t n = min(g.nsub, (uint32_t)AR_D);
+    for (uint32_t s = 0; s < n; s++) attn_issue_kv<AW>(p, g, kvh, s, wave, lane, lds_addr(lds), pgl);
+    return n;
 }
 
 // AW waves (4 or 8: one or two groups of four taking alternate sub-chunks);
 // COH: q and the new token's k / v were written by other workgroups of the
 // same launch (read at system scope), and the merged output is read by other
-// workgroups of it (stored at device scope).
+// workgroups of it (stored at device scope). pre: sub-chunks 0 .. pre-1
+// already copied (attn_ring_prefetch, page entries included).
 template <int G, bool FUSED, int AW, bool COH>
-ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *lds) {
+ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *lds, uint32_t pre = 0) {
     constexpr int AT = AW * 64, NG = AW / 4;  // threads, groups
     constexpr uint32_t QC = ar_qc<G>();
     constexpr uint32_t NSM = QC + (FUSED ? 2 : 0);  // position-independent small copies
     constexpr uint32_t KVW = 32 / AW;               // K/V copies per wave and sub-chunk
     uint8_t *sm = lds + AR_D * AR_SLOT;
     uint32_t *pgl = (uint32_t *)(sm + ar_small<G>());
-    float *ps = (float *)(pgl + AR_MAXPG);  // [AW][G][16] probabilities of a wave's tokens
     const uint32_t tid = COH ? phase_tid() : threadIdx.x, lane = tid & 63;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), sub = lane & 7, grp = lane >> 3;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), sub = lane & 7;
     const uint32_t gq = wave / 4, w4 = wave % 4;  // group, wave within the group
     const uint32_t lds0 = lds_addr(lds);
     TRACE_OPS(0);
@@ -329,16 +396,13 @@ ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *ld
         }
     }
     // ---- position and chunk geometry
-    const uint32_t posv = p.pos.dev ? *p.pos.dev + p.pos.value : p.pos.value;
-    const uint32_t seq = FUSED ? posv + 1 : posv;
-    const uint32_t CT = ((seq + p.nd - 1) / p.nd + 15) / 16 * 16;
-    const uint32_t nv = (seq + CT - 1) / CT;
-    if (c >= nv) {  // uniform: no token of this chunk
+    const AttnGeom geo(p, c, FUSED);
+    const uint32_t posv = geo.posv, nv = geo.nv, t0 = geo.t0, t1 = geo.t1, nsub = geo.nsub;
+    if (nsub == 0) {  // uniform: no token of this chunk
         wait_vm<0>();
         return;
     }
-    const uint32_t t0 = c * CT, t1 = min(seq, t0 + CT), nsub = (t1 - t0 + AR_TS - 1) / AR_TS;
-    if (!p.ident) {
+    if (!p.ident && pre == 0) {
         // the chunk's page entries (a compiler-tracked load: its wait also
         // drains the small copies, which are needed first anyway)
         for (uint32_t i = tid; i < (t1 - t0 + 15) / 16; i += AT) pgl[i] = p.pages[min(t0 / 16 + i, p.n_pages - 1)];
@@ -347,94 +411,126 @@ ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *ld
     if (FUSED && wave == AW - 1)  // the RoPE row of the position
         dma16((const uint8_t *)(p.rope_cs + (size_t)posv * FD_HD) + min(lane * 16, 496u),
               lds0 + AR_D * AR_SLOT + (QC + 2) * 1024);
-    const uint16_t *kbase = p.kc + (size_t)kvh * p.cache_tokens * FD_HD;
-    const uint16_t *vbase = p.vc + (size_t)kvh * p.cache_tokens * FD_HD;
     auto phys = [&](uint32_t t) __attribute__((always_inline)) {  // logical token in [t0, t1)
         return p.ident ? t : pgl[(t - t0) >> 4] * 16u + (t & 15u);
     };
-    // ---- K/V copies of sub-chunk s into slot s % AR_D: 32 chunks of 1 KB (4
-    // tokens of one page; K then V), KVW per wave. Rows past the chunk re-read
-    // its last row (masked).
     auto issue_kv = [&](uint32_t s) __attribute__((always_inline)) {
-        const uint32_t slot = s % AR_D;
-#pragma unroll
-        for (uint32_t i = 0; i < KVW; i++) {
-            const uint32_t j = wave + AW * i, kv = j >> 4;
-            const uint32_t t = min(t0 + s * AR_TS + 4 * (j & 15) + (lane >> 4), t1 - 1);
-            const uint16_t *row = (kv ? vbase : kbase) + (size_t)phys(t) * FD_HD;
-            dma16(row + (lane & 15) * 8, lds0 + slot * AR_SLOT + j * 1024);
-        }
+        attn_issue_kv<AW>(p, geo, kvh, s, wave, lane, lds0, pgl);
     };
     const uint32_t npro = min(nsub, (uint32_t)AR_D);
-    for (uint32_t s = 0; s < npro; s++) issue_kv(s);
-    // the small copies (and the RoPE row, issued before every K/V copy)
-    wait_vm_dyn(npro * KVW);
+    for (uint32_t s = pre; s < npro; s++) issue_kv(s);
+    // the small copies and the RoPE row (issued before the K/V copies of
+    // this call, after the prefetched ones)
+    wait_vm_dyn((npro - pre) * KVW);
     lds_bar();
     TRACE_OPS(1);
 
-    // ---- q (norm + RoPE), the new token's k / v (the owner only)
-    float qlo[G][8], qhi[G][8];
+    // ---- q as MFMA operand fragments: lane l holds head fg = l % 16 (zero
+    // rows for fg >= G), dims 16 s + 4 fq + 0..3 (fq = l / 16) for the eight
+    // 16-dim steps s, RMS-normalised and roped in place (the RoPE partner of
+    // dim d < 64, d + 64, is step s + 4 of the same lane), then split into
+    // f16 hi + lo parts so that the f16 products carry the f32 q exactly
+    // enough (|q - hi - lo| <= 2^-22 |q|).
+    const uint32_t fg = lane & 15, fq = lane >> 4;
+    half4 qh[8], ql[8];
+    {
+        // computed once per workgroup and shared through LDS: the heads' RMS
+        // (wave g: head g), then group 0's wave w the dims of steps w and
+        // w + 4 (the RoPE pairs), then every wave reads its fragments
+        uint8_t *frag = (uint8_t *)(pgl + AR_MAXPG);
+        float *rinv = (float *)(frag + 8 * 64 * 16);
+        if (FUSED) {
+            for (uint32_t g = wave; g < (uint32_t)G; g += AW) {
+                const float *qs = (const float *)sm + g * FD_HD;
+                const float a = qs[lane], b = qs[lane + 64];
+                const float sq = wave_sum(fmaf(a, a, b * b));
+                if (lane == 0) rinv[g] = 1.0f / sqrtf(sq / (float)FD_HD + p.eps);
+            }
+            lds_bar();
+        }
+        if (wave < 4) {
+            const uint32_t pi = wave;  // steps pi (dims < 64) and pi + 4 (their RoPE partners)
+            const float *qs = (const float *)sm + min(fg, (uint32_t)G - 1) * FD_HD;
+            const f32x4 va = *(const f32x4 *)(qs + 16 * pi + 4 * fq), vb = *(const f32x4 *)(qs + 64 + 16 * pi + 4 * fq);
+            float lo[4] = {va.x, va.y, va.z, va.w}, hi[4] = {vb.x, vb.y, vb.z, vb.w};
+            if (FUSED) {
+                const float *qw = (const float *)(sm + (QC + 1) * 1024);
+                const float *cs = (const float *)(sm + (QC + 2) * 1024);
+                const float ri = rinv[min(fg, (uint32_t)G - 1)];
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        const float *qs = (const float *)sm + g * FD_HD;
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t i = 16 * pi + 4 * fq + j;  // dims i and i + 64
+                    const float a = qw[i] * (lo[j] * ri);
+                    const float b = qw[i + 64] * (hi[j] * ri);
+                    const float co = cs[2 * i], sn = cs[2 * i + 1];
+                    lo[j] = a * co - b * sn;
+                    hi[j] = a * sn + b * co;
+                }
+            }
+            half4 h0, l0, h1, l1;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            qlo[g][e] = qs[sub * 8 + e];
-            qhi[g][e] = qs[64 + sub * 8 + e];
+            for (int j = 0; j < 4; j++) {
+                const float x = fg < (uint32_t)G ? lo[j] : 0.f, y = fg < (uint32_t)G ? hi[j] : 0.f;
+                h0[j] = (_Float16)x;
+                l0[j] = (_Float16)(x - (float)h0[j]);
+                h1[j] = (_Float16)y;
+                l1[j] = (_Float16)(y - (float)h1[j]);
+            }
+            *(half4 *)(frag + (pi * 64 + lane) * 16) = h0;
+            *(half4 *)(frag + (pi * 64 + lane) * 16 + 8) = l0;
+            *(half4 *)(frag + ((pi + 4) * 64 + lane) * 16) = h1;
+            *(half4 *)(frag + ((pi + 4) * 64 + lane) * 16 + 8) = l1;
+        }
+        lds_bar();
+#pragma unroll
+        for (int s8 = 0; s8 < 8; s8++) {
+            qh[s8] = *(const half4 *)(frag + (s8 * 64 + lane) * 16);
+            ql[s8] = *(const half4 *)(frag + (s8 * 64 + lane) * 16 + 8);
         }
     }
+    TRACE_OPS(9);
+    // ---- the new token's k / v (the owner only)
     const bool owner = FUSED && posv >= t0 && posv < t1;  // uniform
     uint16_t *knew16 = (uint16_t *)(sm + (QC + 3) * 1024), *vnew16 = knew16 + FD_HD;
-    if (FUSED) {
+    if (FUSED && owner && wave == 0) {
         const float *kn = (const float *)(sm + QC * 1024), *vn = kn + FD_HD;
-        const float *qw = (const float *)(sm + (QC + 1) * 1024), *kw = qw + FD_HD;
+        const float *kw = (const float *)(sm + (QC + 1) * 1024) + FD_HD;
         const float *cs = (const float *)(sm + (QC + 2) * 1024);
-        float wlo[8], whi[8], co[8], sn[8];
+        float klo[8], khi[8], wlo[8], whi[8], co[8], sn[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            wlo[e] = qw[sub * 8 + e];
-            whi[e] = qw[64 + sub * 8 + e];
+            klo[e] = kn[sub * 8 + e];
+            khi[e] = kn[64 + sub * 8 + e];
+            wlo[e] = kw[sub * 8 + e];
+            whi[e] = kw[64 + sub * 8 + e];
             co[e] = cs[2 * (sub * 8 + e)];
             sn[e] = cs[2 * (sub * 8 + e) + 1];
         }
-#pragma unroll
-        for (int g = 0; g < G; g++) norm_rope16(qlo[g], qhi[g], wlo, whi, co, sn, p.eps);
-        if (owner && wave == 0) {
-            float klo[8], khi[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                klo[e] = kn[sub * 8 + e];
-                khi[e] = kn[64 + sub * 8 + e];
-                wlo[e] = kw[sub * 8 + e];
-                whi[e] = kw[64 + sub * 8 + e];
-            }
-            norm_rope16(klo, khi, wlo, whi, co, sn, p.eps);  // all 64 lanes (8 copies of the head)
-            if (lane < 8) {
-                *(u32x4 *)(knew16 + sub * 8) = u32x4{pack_h2(klo[0], klo[1]), pack_h2(klo[2], klo[3]),
-                                                     pack_h2(klo[4], klo[5]), pack_h2(klo[6], klo[7])};
-                *(u32x4 *)(knew16 + 64 + sub * 8) = u32x4{pack_h2(khi[0], khi[1]), pack_h2(khi[2], khi[3]),
-                                                          pack_h2(khi[4], khi[5]), pack_h2(khi[6], khi[7])};
-            }
-            *(uint32_t *)(vnew16 + 2 * lane) = pack_h2(vn[2 * lane], vn[2 * lane + 1]);
+        norm_rope16(klo, khi, wlo, whi, co, sn, p.eps);  // all 64 lanes (8 copies of the head)
+        if (lane < 8) {
+            *(u32x4 *)(knew16 + sub * 8) = u32x4{pack_h2(klo[0], klo[1]), pack_h2(klo[2], klo[3]),
+                                                 pack_h2(klo[4], klo[5]), pack_h2(klo[6], klo[7])};
+            *(u32x4 *)(knew16 + 64 + sub * 8) = u32x4{pack_h2(khi[0], khi[1]), pack_h2(khi[2], khi[3]),
+                                                      pack_h2(khi[4], khi[5]), pack_h2(khi[6], khi[7])};
         }
+        *(uint32_t *)(vnew16 + 2 * lane) = pack_h2(vn[2 * lane], vn[2 * lane + 1]);
     }
     const uint32_t s_own = owner ? (posv - t0) / AR_TS : ~0u, r_own = owner ? (posv - t0) % AR_TS : 0u;
+    TRACE_OPS(10);
 
     // ---- the ring, NG sub-chunks per step (group gq takes sub-chunk
-    // NG k + gq). Wave w4 of a group takes tokens 16 w4 .. 16 w4 + 15 of its
-    // sub-chunk: for the scores, lane group grp (8 lanes, 16 dims each)
-    // tokens grp and grp + 8; for P*V, lane (vrow = lane / 16, vcol = lane %
-    // 16) dims 8 vcol .. of tokens vrow + 4 k.
-    const uint32_t vrow = lane >> 4, vcol = lane & 15;
-    float m_run[G], l_run[G], acc[G][8];
+    // NG k + gq); wave w4 of a group takes its tokens 16 w4 .. 16 w4 + 15.
+    // Scores: S^T (16 tokens x 16 heads) = K (16 x 128) q^T over eight
+    // 16x16x16 MFMA steps (hi and lo q): lane l ends with tokens 4 fq + r of
+    // head fg. Online softmax per head over the wave's tokens (the waves
+    // are combined at the end). P V: O (16 heads x 128) += P (16 x 16
+    // tokens) V (16 tokens x 128), eight 16-dim tiles: the score layout is
+    // the P operand's (row = head fg, k = token 4 fq + r); lane l holds O
+    // rows 4 fq + r (heads), dim 16 n + fg of tile n.
+    float m_run = -INFINITY, l_run = 0.f;  // head fg (every fq copy)
+    floatx4 acc[8];
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        m_run[g] = -INFINITY;
-        l_run[g] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
-    }
-    float *psw = ps + wave * G * 16;
+    for (int n = 0; n < 8; n++) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
     const uint32_t nstep = (nsub + NG - 1) / NG;
     for (uint32_t k = 0; k < nstep; k++) {
         // sub-chunks up to NG k + NG - 1 must have landed; later ones stay in
@@ -450,80 +546,82 @@ ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *ld
         }
         if (s_own >= NG * k && s_own < NG * k + NG) {  // uniform: substitute the new token's K and V rows
             uint8_t *Ks = lds + (s_own % AR_D) * AR_SLOT;
-            if (tid < 16) *(u32x4 *)(Ks + r_own * 256 + tid * 16) = *(const u32x4 *)((const uint8_t *)knew16 + tid * 16);
+            const uint32_t pc = ((tid & 15) ^ (r_own & 15)) * 16;  // the row's swizzled 16-byte piece
+            if (tid < 16) *(u32x4 *)(Ks + r_own * 256 + pc) = *(const u32x4 *)((const uint8_t *)knew16 + tid * 16);
             else if (tid < 32)
-                *(u32x4 *)(Ks + AR_SLOT / 2 + r_own * 256 + (tid - 16) * 16) =
+                *(u32x4 *)(Ks + AR_SLOT / 2 + r_own * 256 + pc) =
                     *(const u32x4 *)((const uint8_t *)vnew16 + (tid - 16) * 16);
             lds_bar();
         }
         const uint32_t s = NG * k + gq;
         if (s < nsub) {  // uniform per wave
             const uint8_t *Ks = lds + (s % AR_D) * AR_SLOT, *Vs = Ks + AR_SLOT / 2;
-            const uint32_t ts = t0 + s * AR_TS;
-            float sc[2][G];
+            const uint32_t ts = t0 + s * AR_TS, tb = w4 * 16;
+            // every fragment read first (one LDS round trip): K rows of the
+            // wave's tokens tb + fg, V of its tokens tb + 4 fq + r. Rows past
+            // the chunk hold a copy of its last row (finite): their
+            // probabilities are 0.
+            half4 kf[8], vf[8];
+            {
+                const uint32_t t = tb + fg;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const uint32_t tt = w4 * 16 + grp + 8 * j;
-                const u32x4 k0 = *(const u32x4 *)(Ks + tt * 256 + sub * 16);
-                const u32x4 k1 = *(const u32x4 *)(Ks + tt * 256 + 128 + sub * 16);
-                const uint32_t kw8[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-                float kf[16];
+                for (int s8 = 0; s8 < 8; s8++)
+                    kf[s8] = *(const half4 *)(Ks + t * 256 + (((2 * s8 + (fq >> 1)) ^ (t & 15)) * 16) + 8 * (fq & 1));
+                const uint32_t tv = tb + 4 * fq, off = 2 * (fg & 7);
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    kf[2 * e] = h2f(kw8[e]);
-                    kf[2 * e + 1] = h2f(kw8[e] >> 16);
-                }
-                const bool valid = ts + tt < t1;
+                for (int n = 0; n < 8; n++) {
+                    const uint32_t pc = 2 * n + (fg >> 3);
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    float sacc = 0.f;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        sacc = fmaf(qlo[g][e], kf[e], sacc);
-                        sacc = fmaf(qhi[g][e], kf[8 + e], sacc);
+                    for (int r = 0; r < 4; r++) {
+                        const uint32_t t2 = tv + r;
+                        vf[n][r] = *(const _Float16 *)(Vs + t2 * 256 + (pc ^ (t2 & 15)) * 16 + off);
                     }
-                    sacc = sum8(sacc) * p.scale;  // dot * scale, as cpuAttention
-                    sc[j][g] = valid ? sacc : -INFINITY;
                 }
             }
+            // scores
+            floatx4 d1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                float m = fmaxf(sc[0][g], sc[1][g]);
-                m = rows_max(fmaxf(m, dpp_f<0x140>(m)));  // uniform within each 8-lane group: over the wave
-                const float mn = fmaxf(m_run[g], m);
-                const float ms = mn == -INFINITY ? 0.f : mn;
-                const float f = m_run[g] == -INFINITY ? 0.f : expf(m_run[g] - ms);
-                const float p0 = expf(sc[0][g] - ms), p1 = expf(sc[1][g] - ms);
-                if (sub == 0) {
-                    psw[g * 16 + grp] = p0;
-                    psw[g * 16 + grp + 8] = p1;
-                }
-                float l = p0 + p1;
-                l = rows_sum(l + dpp_f<0x140>(l));
-                l_run[g] = fmaf(l_run[g], f, l);
-                m_run[g] = mn;
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc[g][e] *= f;
+            for (int s8 = 0; s8 < 8; s8++) {
+                d1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kf[s8], qh[s8], d1, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kf[s8], ql[s8], d1, 0, 0, 0);
             }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's probabilities are in LDS
+            float sc[4];
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const uint32_t i = vrow + 4 * kk, tt = w4 * 16 + i;
-                u32x4 v = *(const u32x4 *)(Vs + tt * 256 + vcol * 16);
-                if (ts + tt >= t1) v = u32x4{0, 0, 0, 0};
-                const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-                float vf[8];
+            for (int r = 0; r < 4; r++) sc[r] = ts + tb + 4 * fq + r < t1 ? d1[r] * p.scale : -INFINITY;  // dot * scale
+            float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            m = fmaxf(m, __shfl_xor(m, 16, 64));
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            const float mn = fmaxf(m_run, m);
+            const float ms = mn == -INFINITY ? 0.f : mn;
+            const float f = m_run == -INFINITY ? 0.f : expf(m_run - ms);
+            float pr[4], lsum = 0.f;
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    vf[2 * e] = h2f(vw[e]);
-                    vf[2 * e + 1] = h2f(vw[e] >> 16);
-                }
+            for (int r = 0; r < 4; r++) {
+                pr[r] = fg < (uint32_t)G ? expf(sc[r] - ms) : 0.f;
+                lsum += pr[r];
+            }
+            lsum += __shfl_xor(lsum, 16, 64);
+            lsum += __shfl_xor(lsum, 32, 64);
+            l_run = fmaf(l_run, f, lsum);
+            m_run = mn;
+            half4 ph, pl;
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float pr = psw[g * 16 + i];
+            for (int r = 0; r < 4; r++) {
+                const _Float16 h = (_Float16)pr[r];
+                ph[r] = h;
+                pl[r] = (_Float16)(pr[r] - (float)h);
+            }
+            // rescale the output rows (heads 4 fq + r) by their heads' factors
+            // (lane h, fq = 0, holds head h's)
+            float fr[4];
 #pragma unroll
-                    for (int e = 0; e < 8; e++) acc[g][e] = fmaf(pr, vf[e], acc[g][e]);
-                }
+            for (int r = 0; r < 4; r++) fr[r] = G > 4 && fq ? lane_f(f, 4 + r) : lane_f(f, r);
+#pragma unroll
+            for (int n = 0; n < 8; n++) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[n][r] *= fr[r];
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vf[n], acc[n], 0, 0, 0);
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vf[n], acc[n], 0, 0, 0);
             }
         }
         if (k < 2) TRACE_OPS(6 + 2 * k);
@@ -539,25 +637,18 @@ ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *ld
     // a wave, then waves
     float *wm = (float *)lds, *wl = wm + AW * G, *wo = wl + AW * G;  // [AW][G], [AW][G], [AW][G][128]
     lds_bar();  // every wave is done with the ring
+    // lane l: heads 4 fq + r, dim 16 n + fg; the running statistics of head
+    // fg are in the lanes with fq = 0
 #pragma unroll
-    for (int g = 0; g < G; g++)
+    for (int r = 0; r < 4; r++) {
+        const uint32_t g = 4 * fq + r;
+        if (g < (uint32_t)G)
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float a = acc[g][e];
-            a += __shfl_xor(a, 16, 64);
-            a += __shfl_xor(a, 32, 64);
-            acc[g][e] = a;
-        }
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        if (lane < 16) {
-            *(f32x4 *)(wo + (wave * G + g) * FD_HD + 8 * vcol) = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
-            *(f32x4 *)(wo + (wave * G + g) * FD_HD + 8 * vcol + 4) = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
-        }
-        if (lane == 0) {
-            wm[wave * G + g] = m_run[g];
-            wl[wave * G + g] = l_run[g];
-        }
+            for (int n = 0; n < 8; n++) wo[(wave * G + g) * FD_HD + 16 * n + fg] = acc[n][r];
+    }
+    if (fq == 0 && fg < (uint32_t)G) {
+        wm[wave * G + fg] = m_run;
+        wl[wave * G + fg] = l_run;
     }
     __syncthreads();
     for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += AT) {
@@ -585,14 +676,51 @@ ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *ld
     // went out as device-scope stores (coherent across the XCDs' L2s);
     // s_waitcnt 0 in every wave and the barrier make them complete before the
     // counter increment, and the merger reads them with device-scope loads.
-    __shared__ uint32_t s_prev;
+    __shared__ uint32_t s_prev, s_ok;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) s_prev = __hip_atomic_fetch_add(p.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (s_prev != nv - 1) return;
+    if (!COH && p.no_wait) {
+        if (s_prev != nv - 1) return;
+        TRACE_OPS(4);
+        if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        attn_merge<G, G <= 4 ? 40 : 12, COH>(p, kvh * G, nv, false);
+        return;
+    }
+    // Every workgroup resident (the persistent kernel, or a launch with the
+    // device to itself: one workgroup per CU, grid <= CUs): the last G
+    // arrivals merge one q head each; all but the last wait (bounded by
+    // p.ctl[1] ticks, ZH_DEVERR_ATTN_WAIT on giving up) for the kv head's
+    // other chunks. counters[nkv + kvh] counts mergers past the wait; the
+    // last one clears both words (nothing reads them after).
+    const uint32_t nm = nv >= (uint32_t)G ? (uint32_t)G : 1u, prev = s_prev;
+    if (prev + nm < nv) return;
+    const uint32_t slot = prev + nm - nv;
     TRACE_OPS(4);
-    if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    attn_merge<G, G <= 4 ? 40 : 12, COH>(p, kvh * G, nv, false);
+    if (tid == 0) {
+        uint32_t ok = 1;
+        if (slot != nm - 1) {
+            const uint64_t t_0 = __builtin_amdgcn_s_memrealtime();
+            const uint64_t limit = __hip_atomic_load(p.ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            while (limit == 0 || __hip_atomic_load(p.counters + kvh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nv) {
+                if (__builtin_amdgcn_s_memrealtime() - t_0 >= limit) {
+                    ok = 0;
+                    __hip_atomic_fetch_or(p.ctl, ZH_DEVERR_ATTN_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        s_ok = ok;
+        uint32_t *done = p.counters + p.nq / G + kvh;
+        if (__hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nm - 1) {
+            __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+    if (nm == 1) attn_merge<G, G <= 4 ? 40 : 12, COH>(p, kvh * G, nv, !s_ok);
+    else attn_merge<1, 32, COH>(p, kvh * G + slot, nv, !s_ok);
 }
 

@@ -53,6 +53,9 @@ static __device__ uint64_t g_zh_trace[8192 * 16];
 // rounding of an f32 serial dot product. Dot products against 4..8-bit
 // weight codes accumulate exactly in int32.
 // ---------------------------------------------------------------------------
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));  // MFMA f16 operand fragment
+typedef float floatx4 __attribute__((ext_vector_type(4)));    // MFMA 16x16 accumulator fragment
+
 struct XQView {
     int8_t *limb;   // [nblk][3][32]
     float *xs;      // [nblk]

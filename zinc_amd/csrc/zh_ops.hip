@@ -295,9 +295,9 @@ static uint32_t *attn_counters(float *partials, uint32_t nh, uint32_t nkv, uint3
 }
 
 // Partials of the C-ABI decode attention (the DMA ring kernel): nh x nd
-// chunk partials of 130 f32, then one merge counter per kv head.
+// chunk partials of 130 f32, then two merge counters per kv head.
 static uint64_t ring_partials_bytes(uint32_t nh, uint32_t nkv, int cu_count) {
-    return (uint64_t)nh * attn_nd(nkv, cu_count) * (FD_HD + 2) * 4 + 4ull * nkv;
+    return (uint64_t)nh * attn_nd(nkv, cu_count) * (FD_HD + 2) * 4 + 8ull * nkv;
 }
 static uint32_t *ring_counters(float *partials, uint32_t nh, uint32_t nkv, int cu_count) {
     return (uint32_t *)(partials + (uint64_t)nh * attn_nd(nkv, cu_count) * (FD_HD + 2));
@@ -404,7 +404,7 @@ extern "C" int zh_flash_decode(zh_ctx *c, const zh_buf *q, const zh_buf *kc, con
     void *scr;
     int rc = zh_scratch(c, ring_partials_bytes(nh, nkv, c->cu_count), &scr);
     if (rc) return rc;
-    ZH_HIP(c, hipMemsetAsync(ring_counters((float *)scr, nh, nkv, c->cu_count), 0, 4ull * nkv, c->stream));
+    ZH_HIP(c, hipMemsetAsync(ring_counters((float *)scr, nh, nkv, c->cu_count), 0, 8ull * nkv, c->stream));
     float scale = attn_scale != 0.f ? attn_scale : 1.0f / sqrtf((float)hd);
     return zhk_flash_decode(c, (const float *)q->ptr, (const uint16_t *)kc->ptr, (const uint16_t *)vc->ptr,
                             (const uint32_t *)pages->ptr, n_pages, cache_tokens, (float *)out->ptr, nullptr, nh, nkv,
@@ -467,7 +467,7 @@ extern "C" int zh_flash_decode_noalloc(zh_ctx *c, const zh_buf *q, const zh_buf 
     // the merge counters start at zero (a fill kernel, not a memset node, so
     // the call may be captured into a graph)
     uint32_t *cnt = ring_counters((float *)scr, nh, nkv, c->cu_count);
-    hipLaunchKernelGGL(k_zero_u32, dim3((nkv + 255) / 256), dim3(256), 0, c->stream, cnt, nkv);
+    hipLaunchKernelGGL(k_zero_u32, dim3((2 * nkv + 255) / 256), dim3(256), 0, c->stream, cnt, 2 * nkv);
     ZH_LAUNCH_CHECK(c);
     float scale = attn_scale != 0.f ? attn_scale : 1.0f / sqrtf((float)hd);
     return zhk_flash_decode(c, (const float *)q->ptr, (const uint16_t *)kc->ptr, (const uint16_t *)vc->ptr,

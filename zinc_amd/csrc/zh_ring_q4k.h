@@ -97,30 +97,83 @@ struct RingSegs {
 // lanes reading 16 consecutive half-blocks hit distinct banks.
 constexpr uint32_t RG_SEG = 400;
 
-// NB = K / 256 super-blocks per row (8 or 16); MODE LPB_PLAIN or LPB_GATE_UP;
-// XIN 0: f32 x, 1: f32 x with fused RMSNorm, 2: XQ x.
-template <int NB, int MODE, int XIN, bool COH>
-ZH_DEV void q4k_ring_body(const RingP &p, uint32_t wg, uint8_t *lds) {
-    constexpr int TL = 2 * NB;                  // lanes per row: half a super-block each
-    constexpr int TPP = RG_T / TL;              // rows (teams) per pass
-    constexpr int NM = MODE == LPB_GATE_UP ? 2 : 1;
-    constexpr int RPP = TPP / NM;               // output rows per pass
-    constexpr uint32_t ROWB = NB * 144;
-    constexpr uint32_t NBLK = NB * 8;           // 32-element blocks of x
+// The ring's geometry and tile copies for workgroup wg: tile t (output rows
+// r0 + t RPP ..) into ring slot s. Chunk c = wave + 8 i (i < 5): waves 0..3
+// issue 5 chunks, 4..7 issue 4.
+template <int NB, int MODE>
+struct Q4Tiles {
+    static constexpr int TL = 2 * NB;                  // lanes per row: half a super-block each
+    static constexpr int TPP = RG_T / TL;              // rows (teams) per pass
+    static constexpr int NM = MODE == LPB_GATE_UP ? 2 : 1;
+    static constexpr int RPP = TPP / NM;               // output rows per pass
+    static constexpr uint32_t ROWB = NB * 144;
     static_assert(TPP * ROWB == RG_TILE, "one pass covers one tile");
+    uint32_t r0, r1, nt, wave, lane, tcw, lds0;
+    RingSegs sgs;
+    uint64_t dup;
+    ZH_DEVM Q4Tiles(const RingP &p, uint32_t wg, uint32_t tid, const uint8_t *lds) : sgs(p, ROWB) {
+        lane = tid & 63;
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        r0 = wg * p.rpw;
+        r1 = min(p.M, r0 + p.rpw);
+        nt = r0 < p.M ? (r1 - r0 + RPP - 1) / RPP : 0u;
+        tcw = wave < RG_CH % 8 ? RG_CH / 8 + 1 : RG_CH / 8;
+        lds0 = lds_addr(lds);
+        dup = (uint64_t)(uintptr_t)p.W2 - (uint64_t)(uintptr_t)p.segW[0];  // gate/up: up - gate
+    }
+    // tiles copied before the ring's first wait (the others follow as slots free)
+    ZH_DEVM uint32_t prologue() const { return min(nt, (uint32_t)RG_D - 1); }
+    ZH_DEVM void issue(uint32_t t, uint32_t s) const {
+#pragma unroll
+        for (uint32_t i = 0; i < (RG_CH + 7) / 8; i++) {
+            const uint32_t c = wave + 8 * i;
+            if (c < RG_CH) {  // uniform per wave
+                const uint32_t o = c * 1024 + lane * 16;
+                const uint32_t team = o / ROWB, within = o - team * ROWB;
+                const uint32_t m = NM == 2 ? team / RPP : 0;
+                // rows past the range re-read the range's last row (discarded)
+                const uint32_t row = min(r0 + t * RPP + (NM == 2 ? team % RPP : team), r1 - 1);
+                const uint8_t *src;
+                if (NM == 2) {
+                    src = sgs.w(row, ROWB) + (m ? dup : 0ull) + within;
+                } else {
+                    src = sgs.w(row, ROWB) + within;
+                }
+                dma16(src, lds0 + s * RG_TILE + c * 1024);
+            }
+        }
+    }
+};
+
+// The persistent kernel copies a phase's first tiles while it waits at the
+// grid barrier before the phase (the weights do not depend on the previous
+// phase); returns the count, the body's `pre`.
+template <int NB, int MODE>
+ZH_DEV uint32_t q4k_ring_prefetch(const RingP &p, uint32_t wg, uint8_t *lds) {
+    const Q4Tiles<NB, MODE> tl(p, wg, phase_tid(), lds);
+    const uint32_t n = tl.prologue();
+    for (uint32_t t = 0; t < n; t++) tl.issue(t, t);
+    return n;
+}
+
+// NB = K / 256 super-blocks per row (8 or 16); MODE LPB_PLAIN or LPB_GATE_UP;
+// XIN 0: f32 x, 1: f32 x with fused RMSNorm, 2: XQ x. pre: tiles 0 .. pre-1
+// already copied (q4k_ring_prefetch), before the activation's copy.
+template <int NB, int MODE, int XIN, bool COH>
+ZH_DEV void q4k_ring_body(const RingP &p, uint32_t wg, uint8_t *lds, uint32_t pre = 0) {
+    using TT = Q4Tiles<NB, MODE>;
+    constexpr int TL = TT::TL, NM = TT::NM, RPP = TT::RPP;
+    constexpr uint32_t NBLK = NB * 8;           // 32-element blocks of x
     uint8_t *ring = lds;
     uint8_t *xqa = lds + RG_D * RG_TILE;        // XQ image (global XQ layout)
     uint8_t *raw = lds + rg_raw_off<COH>();     // f32 x [K], norm weight [K]
     float *yl = (float *)(lds + rg_yl_off<COH>());  // [NM][RG_MAXROWS]
     float *red = yl + 2 * RG_MAXROWS;           // [8]
     const uint32_t tid = COH ? phase_tid() : threadIdx.x, lane = tid & 63;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t r0 = wg * p.rpw, r1 = min(p.M, r0 + p.rpw);
-    if (r0 >= p.M) return;  // (persistent kernel: more workgroups than row ranges)
-    const uint32_t nt = (r1 - r0 + RPP - 1) / RPP;
-    const uint32_t lds0 = lds_addr(lds);
-    const RingSegs sgs(p, ROWB);
-    const uint64_t dup = (uint64_t)(uintptr_t)p.W2 - (uint64_t)(uintptr_t)p.segW[0];  // gate/up: up - gate
+    const TT tiles(p, wg, tid, lds);
+    const uint32_t wave = tiles.wave, r0 = tiles.r0, r1 = tiles.r1, nt = tiles.nt, lds0 = tiles.lds0;
+    if (nt == 0) return;  // (persistent kernel: more workgroups than row ranges)
+    const RingSegs &sgs = tiles.sgs;
     ZH_TRACE_POINT(0);
 
     // ---- activation DMA (NB chunks of 1 KB per vector: NB / 8 per wave)
@@ -142,34 +195,14 @@ ZH_DEV void q4k_ring_body(const RingP &p, uint32_t wg, uint8_t *lds) {
         }
     }
 
-    // ---- tile DMA: tile t (output rows r0 + t RPP ..) into ring slot s.
-    // Chunk c = wave + 8 i (i < 5): waves 0..3 issue 5 chunks, 4..7 issue 4.
-    const uint32_t tcw = wave < RG_CH % 8 ? RG_CH / 8 + 1 : RG_CH / 8;
-    auto issue_tile = [&](uint32_t t, uint32_t s) __attribute__((always_inline)) {
-#pragma unroll
-        for (uint32_t i = 0; i < (RG_CH + 7) / 8; i++) {
-            const uint32_t c = wave + 8 * i;
-            if (c < RG_CH) {  // uniform per wave
-                const uint32_t o = c * 1024 + lane * 16;
-                const uint32_t team = o / ROWB, within = o - team * ROWB;
-                const uint32_t m = NM == 2 ? team / RPP : 0;
-                // rows past the range re-read the range's last row (discarded)
-                const uint32_t row = min(r0 + t * RPP + (NM == 2 ? team % RPP : team), r1 - 1);
-                const uint8_t *src;
-                if (NM == 2) {
-                    src = sgs.w(row, ROWB) + (m ? dup : 0ull) + within;
-                } else {
-                    src = sgs.w(row, ROWB) + within;
-                }
-                dma16(src, lds0 + s * RG_TILE + c * 1024);
-            }
-        }
-    };
-    const uint32_t npro = min(nt, (uint32_t)RG_D - 1);
-    for (uint32_t t = 0; t < npro; t++) issue_tile(t, t);
+    const uint32_t tcw = tiles.tcw;
+    auto issue_tile = [&](uint32_t t, uint32_t s) __attribute__((always_inline)) { tiles.issue(t, s); };
+    const uint32_t npro = tiles.prologue();
+    for (uint32_t t = pre; t < npro; t++) issue_tile(t, t);
 
-    // ---- the activation as XQ in LDS (the tiles' DMAs are newer: still in flight)
-    wait_vm_dyn(npro * tcw);
+    // ---- the activation as XQ in LDS (the tiles it precedes are still in
+    // flight; prefetched tiles precede it and have landed with it)
+    wait_vm_dyn((npro - pre) * tcw);
     lds_bar();
     ZH_TRACE_POINT(1);
     // image: padded limbs [NB*2][RG_SEG], then xs [NBLK], xsum [NBLK][2]
@@ -255,7 +288,7 @@ ZH_DEV void q4k_ring_body(const RingP &p, uint32_t wg, uint8_t *lds) {
         wait_vm_dyn(min(nt - 1 - t, (uint32_t)RG_D - 2) * tcw);
         lds_bar();
         if (t + RG_D - 1 < nt) issue_tile(t + RG_D - 1, (t + RG_D - 1) % RG_D);
-        const uint8_t *blk = ring + (t % RG_D) * RG_TILE + team * ROWB + b * 144;
+        const uint8_t *blk = ring + (t % RG_D) * RG_TILE + team * TT::ROWB + b * 144;
         uint32_t hd[4], qs[16];
         {
             const u32x4 v = *(const u32x4 *)blk;

@@ -56,14 +56,53 @@ struct R6 {
     static_assert(LIMB % 1024 == 0 && LIMB <= SLOT, "the limbs fit the last ring slot");
 };
 
+// Pass t (rows r0 + t RPP ..) of workgroup wg into slot s. Bytes past the
+// range re-read its last 16 bytes (discarded rows).
+template <int NB>
+struct Q6Tiles {
+    using G = R6<NB>;
+    uint32_t r0, r1, nt, wave, lane, tcw, lds0, wlim;
+    const uint8_t *wbase;
+    ZH_DEVM Q6Tiles(const Ring6P &p, uint32_t wg, uint32_t tid, const uint8_t *lds) {
+        lane = tid & 63;
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        r0 = wg * p.rpw;
+        r1 = min(p.M, r0 + p.rpw);
+        nt = r0 < p.M ? (r1 - r0 + G::RPP - 1) / G::RPP : 0u;
+        tcw = wave < G::CH % 8 ? G::CH / 8 + 1 : G::CH / 8;
+        lds0 = lds_addr(lds);
+        wbase = p.W + (size_t)r0 * G::ROWB;
+        wlim = nt ? (r1 - r0) * G::ROWB - 16 : 0u;
+    }
+    ZH_DEVM uint32_t prologue() const { return min(nt, (uint32_t)R6_D - 1); }
+    ZH_DEVM void issue(uint32_t t, uint32_t s) const {
+#pragma unroll
+        for (uint32_t i = 0; i < (G::CH + 7) / 8; i++) {
+            const uint32_t c = wave + 8 * i;
+            if (c < G::CH) dma16(wbase + min(t * G::RPP * G::ROWB + c * 1024 + lane * 16, wlim), lds0 + s * G::SLOT + c * 1024);
+        }
+    }
+};
+
+// The first passes' copies, issued while the persistent kernel waits at the
+// grid barrier before the phase; returns the count (the body's `pre`).
+template <int NB>
+ZH_DEV uint32_t q6k_ring_prefetch(const Ring6P &p, uint32_t wg, uint8_t *lds) {
+    const Q6Tiles<NB> tl(p, wg, phase_tid(), lds);
+    const uint32_t n = tl.prologue();
+    for (uint32_t t = 0; t < n; t++) tl.issue(t, t);
+    return n;
+}
+
+// pre: passes 0 .. pre-1 already copied (q6k_ring_prefetch), before the
+// activation's copy.
 template <int NB, bool COH>
-ZH_DEV void q6k_ring_body(const Ring6P &p, uint32_t wg, uint8_t *lds) {
+ZH_DEV void q6k_ring_body(const Ring6P &p, uint32_t wg, uint8_t *lds, uint32_t pre = 0) {
     using G = R6<NB>;
     const uint32_t tid = COH ? phase_tid() : threadIdx.x, lane = tid & 63;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t r0 = wg * p.rpw;
-    if (r0 >= p.M) return;  // (persistent kernel: more workgroups than row ranges)
-    const uint32_t r1 = min(p.M, r0 + p.rpw), nt = (r1 - r0 + G::RPP - 1) / G::RPP;
+    const Q6Tiles<NB> tiles(p, wg, tid, lds);
+    const uint32_t wave = tiles.wave, r0 = tiles.r0, r1 = tiles.r1, nt = tiles.nt;
+    if (nt == 0) return;  // (persistent kernel: more workgroups than row ranges)
     uint8_t *ring = lds;
     float *sx = (float *)(lds + R6_D * G::SLOT);  // xs [NBLK], xsum [NBLK][2]
     float *sz = sx + G::NBLK;
@@ -80,21 +119,11 @@ ZH_DEV void q6k_ring_body(const Ring6P &p, uint32_t wg, uint8_t *lds) {
             dma16_act<COH>(p.xq + min(c * 1024 + lane * 16, G::XQB - 16), lds0 + dst);
         }
     }
-    // ---- pass t (rows r0 + t RPP ..) into slot s. Bytes past the range
-    // re-read its last 16 bytes (discarded rows).
-    const uint8_t *wbase = p.W + (size_t)r0 * G::ROWB;
-    const uint32_t wlim = (r1 - r0) * G::ROWB - 16;
-    const uint32_t tcw = wave < G::CH % 8 ? G::CH / 8 + 1 : G::CH / 8;
-    auto issue_tile = [&](uint32_t t, uint32_t s) __attribute__((always_inline)) {
-#pragma unroll
-        for (uint32_t i = 0; i < (G::CH + 7) / 8; i++) {
-            const uint32_t c = wave + 8 * i;
-            if (c < G::CH) dma16(wbase + min(t * G::RPP * G::ROWB + c * 1024 + lane * 16, wlim), lds0 + s * G::SLOT + c * 1024);
-        }
-    };
-    const uint32_t npro = min(nt, (uint32_t)R6_D - 1);
-    for (uint32_t t = 0; t < npro; t++) issue_tile(t, t);
-    wait_vm_dyn(npro * tcw);  // the activation (older than the tiles) has landed
+    const uint32_t tcw = tiles.tcw;
+    auto issue_tile = [&](uint32_t t, uint32_t s) __attribute__((always_inline)) { tiles.issue(t, s); };
+    const uint32_t npro = tiles.prologue();
+    for (uint32_t t = pre; t < npro; t++) issue_tile(t, t);
+    wait_vm_dyn((npro - pre) * tcw);  // the activation (older than the tiles it precedes) has landed
     lds_bar();
 
     // ---- this lane's half super-block: limbs, scales, sums in registers

@@ -73,7 +73,7 @@ constexpr uint32_t ST_GROUPS = 16;
 constexpr uint64_t ST_WAIT_TICKS = 10000000ull;  // 100 ms of the 100 MHz clock
 // ctl words (u32 index): group counters and flags 64 words (256 B) apart
 constexpr uint32_t ST_GC = 0, ST_ROOT = 16 * 64, ST_FLAG = 17 * 64, ST_DONE = 33 * 64, ST_ATTN = 34 * 64;
-constexpr uint32_t ST_CTL_WORDS = ST_ATTN + 64;  // + one merge counter per kv head (<= 64)
+constexpr uint32_t ST_CTL_WORDS = ST_ATTN + 128;  // + two merge words per kv head (<= 64 kv heads)
 
 struct StepP {
     zh_step_args a;
@@ -82,8 +82,10 @@ struct StepP {
     uint32_t rpw_qkv, rpw_o, rpw_ffn, rpw_down;
 };
 
-// Grid barrier number k (1, 2, ...) of this launch.
-ZH_DEV void grid_sync(uint32_t *ctl, uint32_t *err, uint32_t k, uint32_t wg, uint32_t nwg) {
+// Grid barrier number k (1, 2, ...) of this launch, in two halves: the
+// arrival (every store of the workgroup has completed), then the wait. The
+// caller issues the next phase's first copies in between.
+ZH_DEV void grid_arrive(uint32_t *ctl, uint32_t k, uint32_t wg, uint32_t nwg) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -96,6 +98,11 @@ ZH_DEV void grid_sync(uint32_t *ctl, uint32_t *err, uint32_t k, uint32_t wg, uin
                 for (uint32_t f = 0; f < ng; f++)
                     __hip_atomic_store(ctl + ST_FLAG + f * 64, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+    }
+}
+ZH_DEV void grid_wait(uint32_t *ctl, uint32_t *err, uint32_t k, uint32_t wg, uint32_t nwg) {
+    if (threadIdx.x == 0) {
+        const uint32_t ng = nwg < ST_GROUPS ? nwg : ST_GROUPS, g = wg % ng;
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         while (__hip_atomic_load(ctl + ST_FLAG + g * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) {
             if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & ZH_DEVERR_STEP_BARRIER) break;
@@ -116,64 +123,87 @@ __global__ __launch_bounds__(ST_T, 1) void k_step_layers(StepP p) {
     const zh_step_args &a = p.a;
     const uint32_t wg = blockIdx.x, nwg = gridDim.x;
     const uint32_t H = a.hidden, qd = a.n_heads * FD_HD, kvd = a.n_kv_heads * FD_HD;
+    // the position, read once (written before the launch)
+    const uint32_t posv = __builtin_amdgcn_readfirstlane(a.pos.dev ? *a.pos.dev + a.pos.value : a.pos.value);
+    const uint32_t kvh = wg % a.n_kv_heads, chunk = wg / a.n_kv_heads;  // attention: kv head h on XCD h % 8
+    // each phase's parameters for layer l
+    auto qkv_p = [&](const zh_step_layer &L) {
+        RingP r = {};
+        r.x = a.x; r.norm_w = L.attn_norm; r.eps = a.eps;
+        r.K = H; r.nseg = 3; r.acc = 0; r.rpw = p.rpw_qkv;
+        r.segW[0] = L.wq; r.segW[1] = L.wk; r.segW[2] = L.wv;
+        r.segY[0] = a.q; r.segY[1] = a.k; r.segY[2] = a.v;
+        r.seg_end[0] = qd; r.seg_end[1] = qd + kvd; r.seg_end[2] = qd + 2 * kvd;
+        r.M = qd + 2 * kvd;
+        return r;
+    };
+    auto attn_p = [&](const zh_step_layer &L) {
+        AttnP t = {};
+        t.q = a.q; t.k_new = a.k; t.v_new = a.v; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
+        t.rope_cs = a.rope_cs; t.kc = L.kc; t.vc = L.vc; t.pages = a.pages; t.n_pages = a.n_pages;
+        t.cache_tokens = a.max_ctx; t.pos = zh_pos_src{posv, nullptr}; t.scale = a.scale; t.eps = a.eps;
+        t.part = a.part; t.nd = p.nd; t.n_chunks = p.nd; t.counters = a.ctl + ST_ATTN;
+        t.out = a.attn; t.xq = a.xq_attn; t.nq = a.n_heads; t.ident = a.ident; t.ctl = p.err;
+        return t;
+    };
+    auto o_p = [&](const zh_step_layer &L) {
+        RingP r = {};
+        r.xq = a.xq_attn; r.K = qd; r.nseg = 1; r.acc = 1; r.rpw = p.rpw_o;
+        r.segW[0] = L.wo; r.segY[0] = a.x; r.seg_end[0] = H; r.M = H;
+        return r;
+    };
+    auto ffn_p = [&](const zh_step_layer &L) {
+        RingP r = {};
+        r.x = a.x; r.norm_w = L.ffn_norm; r.eps = a.eps;
+        r.K = H; r.nseg = 1; r.acc = 0; r.rpw = p.rpw_ffn;
+        r.segW[0] = L.gate; r.W2 = L.up; r.segY[0] = a.s; r.seg_end[0] = a.ffn; r.M = a.ffn;
+        r.xq_out = a.xq_s; r.grp_cnt = a.grp_cnt;
+        return r;
+    };
+    auto down_p = [&](const zh_step_layer &L) {
+        Ring6P r = {};
+        r.W = L.down; r.xq = a.xq_s; r.y = a.x; r.M = H; r.acc = 1; r.rpw = p.rpw_down;
+        return r;
+    };
     uint32_t nbar = 0;
+    // layer l0's Q/K/V tiles (no barrier before the first phase)
+    uint32_t pre = q4k_ring_prefetch<NBH, LPB_PLAIN>(qkv_p(a.layers[a.l0]), wg, lds);
     for (uint32_t l = a.l0; l < a.l1; l++) {
         const zh_step_layer &L = a.layers[l];
         STEP_TRACE(l - 1, 10);
         STEP_TRACE(l, 0);
-        {  // ---- Q / K / V
-            RingP r = {};
-            r.x = a.x; r.norm_w = L.attn_norm; r.eps = a.eps;
-            r.K = H; r.nseg = 3; r.acc = 0; r.rpw = p.rpw_qkv;
-            r.segW[0] = L.wq; r.segW[1] = L.wk; r.segW[2] = L.wv;
-            r.segY[0] = a.q; r.segY[1] = a.k; r.segY[2] = a.v;
-            r.seg_end[0] = qd; r.seg_end[1] = qd + kvd; r.seg_end[2] = qd + 2 * kvd;
-            r.M = qd + 2 * kvd;
-            q4k_ring_body<NBH, LPB_PLAIN, 1, true>(r, wg, lds);
-        }
+        q4k_ring_body<NBH, LPB_PLAIN, 1, true>(qkv_p(L), wg, lds, pre);
         STEP_TRACE(l, 1);
-        grid_sync(a.ctl, p.err, ++nbar, wg, nwg);
+        // ---- barrier, the attention's first K/V sub-chunks copied meanwhile
+        grid_arrive(a.ctl, ++nbar, wg, nwg);
+        pre = chunk < p.nd ? attn_ring_prefetch<G, 8>(attn_p(L), kvh, chunk, lds, true) : 0u;
+        grid_wait(a.ctl, p.err, nbar, wg, nwg);
         STEP_TRACE(l, 2);
-        {  // ---- attention: workgroup = (kv head, chunk), kv head h on XCD h % 8
-            AttnP t = {};
-            t.q = a.q; t.k_new = a.k; t.v_new = a.v; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
-            t.rope_cs = a.rope_cs; t.kc = L.kc; t.vc = L.vc; t.pages = a.pages; t.n_pages = a.n_pages;
-            t.cache_tokens = a.max_ctx; t.pos = a.pos; t.scale = a.scale; t.eps = a.eps;
-            t.part = a.part; t.nd = p.nd; t.n_chunks = p.nd; t.counters = a.ctl + ST_ATTN;
-            t.out = a.attn; t.xq = a.xq_attn; t.nq = a.n_heads; t.ident = a.ident; t.ctl = p.err;
-            const uint32_t kvh = wg % a.n_kv_heads, c = wg / a.n_kv_heads;
-            if (c < p.nd) attn_ring_body<G, true, 8, true>(t, kvh, c, lds);
-        }
+        if (chunk < p.nd) attn_ring_body<G, true, 8, true>(attn_p(L), kvh, chunk, lds, pre);
         STEP_TRACE(l, 3);
-        grid_sync(a.ctl, p.err, ++nbar, wg, nwg);
+        grid_arrive(a.ctl, ++nbar, wg, nwg);
+        pre = q4k_ring_prefetch<NBH, LPB_PLAIN>(o_p(L), wg, lds);
+        grid_wait(a.ctl, p.err, nbar, wg, nwg);
         STEP_TRACE(l, 4);
-        {  // ---- O projection, added to the residual stream
-            RingP r = {};
-            r.xq = a.xq_attn; r.K = qd; r.nseg = 1; r.acc = 1; r.rpw = p.rpw_o;
-            r.segW[0] = L.wo; r.segY[0] = a.x; r.seg_end[0] = H; r.M = H;
-            q4k_ring_body<NBH, LPB_PLAIN, 2, true>(r, wg, lds);
-        }
+        q4k_ring_body<NBH, LPB_PLAIN, 2, true>(o_p(L), wg, lds, pre);
         STEP_TRACE(l, 5);
-        grid_sync(a.ctl, p.err, ++nbar, wg, nwg);
+        grid_arrive(a.ctl, ++nbar, wg, nwg);
+        pre = q4k_ring_prefetch<NBH, LPB_GATE_UP>(ffn_p(L), wg, lds);
+        grid_wait(a.ctl, p.err, nbar, wg, nwg);
         STEP_TRACE(l, 6);
-        {  // ---- gate / up + SwiGLU, output also as XQ
-            RingP r = {};
-            r.x = a.x; r.norm_w = L.ffn_norm; r.eps = a.eps;
-            r.K = H; r.nseg = 1; r.acc = 0; r.rpw = p.rpw_ffn;
-            r.segW[0] = L.gate; r.W2 = L.up; r.segY[0] = a.s; r.seg_end[0] = a.ffn; r.M = a.ffn;
-            r.xq_out = a.xq_s; r.grp_cnt = a.grp_cnt;
-            q4k_ring_body<NBH, LPB_GATE_UP, 1, true>(r, wg, lds);
-        }
+        q4k_ring_body<NBH, LPB_GATE_UP, 1, true>(ffn_p(L), wg, lds, pre);
         STEP_TRACE(l, 7);
-        grid_sync(a.ctl, p.err, ++nbar, wg, nwg);
+        grid_arrive(a.ctl, ++nbar, wg, nwg);
+        pre = q6k_ring_prefetch<NBF>(down_p(L), wg, lds);
+        grid_wait(a.ctl, p.err, nbar, wg, nwg);
         STEP_TRACE(l, 8);
-        {  // ---- down projection, added to the residual stream
-            Ring6P r = {};
-            r.W = L.down; r.xq = a.xq_s; r.y = a.x; r.M = H; r.acc = 1; r.rpw = p.rpw_down;
-            q6k_ring_body<NBF, true>(r, wg, lds);
-        }
+        q6k_ring_body<NBF, true>(down_p(L), wg, lds, pre);
         STEP_TRACE(l, 9);
-        if (l + 1 < a.l1) grid_sync(a.ctl, p.err, ++nbar, wg, nwg);
+        if (l + 1 < a.l1) {
+            grid_arrive(a.ctl, ++nbar, wg, nwg);
+            pre = q4k_ring_prefetch<NBH, LPB_PLAIN>(qkv_p(a.layers[l + 1]), wg, lds);
+            grid_wait(a.ctl, p.err, nbar, wg, nwg);
+        }
     }
     // ---- every workgroup is past its last barrier wait: the last one to
     // get here clears the barrier words for the next launch
