@@ -12,6 +12,11 @@ Build the debug library first (it also compiles the points in):
 
     python -m zinc_amd.build --debug _work/dbg
     ZH_LIB_PATH=_work/dbg/libzinc_hip.so python -m benchmarks.step_phases
+    ZH_LIB_PATH=_work/dbg/libzinc_hip.so python -m benchmarks.step_phases --standalone
+
+--standalone: the same attention body as its own kernel (the per-phase
+step with a shuffled page table, i.e. k_attn_ring), its launches replayed by
+zh_engine_time_kernel; points relative to each workgroup's start.
 
 Config 3's model (8B shapes, KV context 4096 + 2 decoded tokens).
 """
@@ -30,9 +35,46 @@ ATTN_POINTS = {1: "small copies landed", 9: "q fragments", 10: "new K/V row read
                13: "merger: output"}
 
 
+def print_attn(ta):
+    ok = ta[:, 0] > 0
+    for s in sorted(ATTN_POINTS, key=lambda k: [1, 9, 10, 5, 6, 7, 8, 2, 3, 4, 11, 12, 13].index(k)):
+        col, st = ta[ok, s], ta[ok, 0]
+        m = col >= st  # points the workgroup reached in this launch
+        if not m.any():
+            continue
+        r = (col[m] - st[m]) * 0.01
+        print(f"  {ATTN_POINTS[s]:22s}: n={m.sum():3d}  min {r.min():6.2f}  p50 {np.median(r):6.2f}  max {r.max():6.2f}")
+
+
+def standalone():
+    L = hip.lib()
+    L.zh_debug_trace_ops.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
+    ctx = hip.Context(0)
+    cfg = dict(DENSE_8B)
+    cfg["max_ctx"] = 4096 + 64
+    eng = InferenceEngine(ctx, cfg)
+    eng.set_pages(np.random.default_rng(17).permutation(cfg["max_ctx"] // 16).astype(np.uint32))
+    eng.prefill_kv_random(4096, 7)
+    eng.generate([17, 18], 2, start_pos=4096)
+    ctx.sync()
+    n = 8192 * 16
+    a = np.zeros(n, np.uint64)
+    L.zh_debug_trace_ops(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)  # clears the points
+    us = eng.time_kernel("attn", 36)
+    ctx.sync()
+    L.zh_debug_trace_ops(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+    print(f"standalone attention ({eng.group_kernels('attn')}): {us:.2f} us per launch (events, debug build); "
+          "points of the last launch, us from each workgroup's start:")
+    print_attn(a.reshape(8192, 16)[:ctx.info()[1]].astype(np.int64))
+    eng.deinit()
+    ctx.close()
+
+
 def main():
     if not os.environ.get("ZH_LIB_PATH"):
         sys.exit("set ZH_LIB_PATH to the debug build's libzinc_hip.so")
+    if "--standalone" in sys.argv[1:]:
+        return standalone()
     L = hip.lib()
     L.zh_debug_trace_step.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
     ctx = hip.Context(0)
@@ -53,16 +95,8 @@ def main():
         r = (t[:, s] - base) * 0.01
         lab = (names[s // 2] + (" start" if s % 2 == 0 else " end")) if s < 10 else "layer 11 start"
         print(f"  {lab:16s}: min {r.min():7.2f}  p50 {np.median(r):7.2f}  max {r.max():7.2f}")
-    ta = t[:, 16:]
-    ok = ta[:, 0] > 0
     print("attention body (last layer of the last step), us from each workgroup's start:")
-    for s in sorted(ATTN_POINTS, key=lambda k: [1, 9, 10, 5, 6, 7, 8, 2, 3, 4, 11, 12, 13].index(k)):
-        col, st = ta[ok, s], ta[ok, 0]
-        m = col >= st  # points the workgroup reached in this launch
-        if not m.any():
-            continue
-        r = (col[m] - st[m]) * 0.01
-        print(f"  {ATTN_POINTS[s]:22s}: n={m.sum():3d}  min {r.min():6.2f}  p50 {np.median(r):6.2f}  max {r.max():6.2f}")
+    print_attn(t[:, 16:])
     eng.deinit()
     ctx.close()
 
