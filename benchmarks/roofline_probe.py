@@ -43,10 +43,18 @@ def probe_engine(ctx, max_ctx):
     return eng
 
 
+def step_groups(eng):
+    """The launch groups the step runs: Q/K/V and attention as one group when
+    the engine runs them as one launch (k_qkv_attn), else separately."""
+    if "k_qkv_attn" in eng.group_kernels("qkv_attn"):
+        return ["qkv_attn"] + GROUP_ORDER[2:]
+    return list(GROUP_ORDER)
+
+
 def per_kernel(eng, L, iters=108):
     """{group: us, bytes, GB/s, frac} for every launch group, and the dominant one."""
     rows = {}
-    for g in GROUP_ORDER:
+    for g in step_groups(eng):
         us = eng.time_kernel(g, iters)
         b = eng.group_bytes(g, L)
         gbs = b / (us * 1e-6) / 1e9
@@ -64,10 +72,11 @@ def pmc_sequence(ctx):
     ctx.sync()
     ctx.stream_read_probe(cal, CAL_BYTES, 1)             # k_stream_read: reads CAL_BYTES (twice: warm + timed)
     ctx.synth_vector(cal, 0, 0, CAL_BYTES // 4, 1.0, 8, 8)  # k_synth_vector: writes CAL_BYTES
-    for g in GROUP_ORDER:
+    groups = step_groups(eng)
+    for g in groups:
         eng.time_kernel(g, PMC_ITERS)
     ctx.sync()
-    b = {g: eng.group_bytes(g, PREFILL + 2) for g in GROUP_ORDER}
+    b = {g: eng.group_bytes(g, PREFILL + 2) for g in groups}
     eng.deinit()
     ctx.free(cal)
     return b

@@ -313,6 +313,16 @@ int zh_engine_set_pages(zh_engine *eng, const uint32_t *pages, uint32_t n);
  * run. No counterpart in the reference, which records one dispatch per
  * operation (decodeStep, forward.zig:4299). Default off. */
 int zh_engine_set_persistent(zh_engine *eng, int on);
+/* Run attn_norm + Q/K/V projections and the decode attention of each layer as
+ * one launch (on != 0, the default) where it applies: 8 kv heads of 128 dims
+ * on a device of 8 XCDs x 32 CUs (one kv head per XCD, so the projection's
+ * outputs, the split-K partials and their flags are exchanged through that
+ * XCD's L2), Q4_K Q/K/V over hidden 4096, identity page table, max_ctx <=
+ * 6144, no engine sharing the device; elsewhere the two launches of
+ * ZH_GROUP_QKV and ZH_GROUP_ATTN run. Replaces the reference's Q/K/V DMMV
+ * dispatches plus its fused norm/RoPE/KV-write and flash-decode dispatches
+ * (forward.zig:4776-4800, attention.zig:199-316). */
+int zh_engine_set_fused_attn(zh_engine *eng, int on);
 
 /* ---- KV page pool: KvPagePool (src/scheduler/kv_cache.zig:43-125) ------ */
 int      zh_kv_pool_create(uint32_t total_pages, uint32_t page_size, zh_kv_pool **out);  /* init */
@@ -421,6 +431,8 @@ int zh_engine_tensor_type(zh_engine *eng, uint64_t stream, uint32_t *type);
  * the decode step: */
 #define ZH_GROUP_QKV 1u      /* attn_norm + Q/K/V projections (one launch when fused) */
 #define ZH_GROUP_ATTN 2u     /* q/k norm + RoPE + KV write + split-K attention + merge */
+/* ZH_GROUP_QKV | ZH_GROUP_ATTN: both as the step runs them (one launch when
+ * zh_engine_set_fused_attn applies) */
 #define ZH_GROUP_O 4u        /* O projection + residual */
 #define ZH_GROUP_FFN_IN 8u   /* ffn_norm + gate/up + SwiGLU (MoE: + router, top-k) */
 #define ZH_GROUP_FFN_OUT 16u /* down projection + residual (MoE: + weighted expert sum) */

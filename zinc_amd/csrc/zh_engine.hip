@@ -71,6 +71,8 @@ struct zh_engine {
     uint32_t *step_ctl = nullptr;
     zh_step_layer *step_layers = nullptr;
     bool persistent = false;  // zh_engine_set_persistent
+    bool fused_qa = true;     // zh_engine_set_fused_attn: Q/K/V + attention in one launch where it applies
+    uint32_t *qa_flags = nullptr;  // its XCD-local flag and epoch words (zero at creation)
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
@@ -324,6 +326,7 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->inv_freq, 4ull * hd / 2}, {(void **)&e->rope_cs, 8ull * c.max_ctx * (hd / 2)},
         {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)}, {(void **)&e->router_cnt, 4},
         {(void **)&e->step_ctl, zh_step_ctl_bytes()}, {(void **)&e->step_layers, sizeof(zh_step_layer) * c.n_layers},
+        {(void **)&e->qa_flags, 4ull * zhk_qkv_attn_flag_words()},
     };
     uint64_t aoff = 0;
     for (auto &a : acts) aoff = align256(aoff + a.bytes);
@@ -339,6 +342,7 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
     me = hipMemsetAsync(e->kv, 0, per * 4 * c.n_layers, ctx->stream);
     if (me != hipSuccess) { zh_engine_destroy(e); return ZH_ERR_HIP; }
     hipLaunchKernelGGL(k_fill_pages, dim3((e->n_pages + 255) / 256), dim3(256), 0, ctx->stream, e->pages, e->n_pages);
+    zhk_xcd_round_robin(ctx);  // (once per context, outside any graph capture: it synchronises)
     // RoPE inverse frequencies: 1/base^(2k/rope_dim) on the host in f32
     // (forward.zig:1495-1500).
     std::vector<float> inv(hd / 2);
@@ -555,6 +559,22 @@ extern "C" int zh_engine_set_pages(zh_engine *e, const uint32_t *pages, uint32_t
     return ZH_OK;
 }
 
+static void drop_graphs(zh_engine *e) {
+    if (e->g_out) hipGraphExecDestroy(e->g_out);
+    if (e->g_noout) hipGraphExecDestroy(e->g_noout);
+    e->g_out = e->g_noout = nullptr;
+}
+
+extern "C" int zh_engine_set_fused_attn(zh_engine *e, int on) {
+    if (!e) return ZH_ERR_INVALID_ARGUMENT;
+    if (e->fused_qa != (on != 0)) {
+        ZH_HIP(e->ctx, hipStreamSynchronize(e->ctx->stream));
+        drop_graphs(e);
+        e->fused_qa = on != 0;
+    }
+    return ZH_OK;
+}
+
 extern "C" int zh_engine_set_persistent(zh_engine *e, int on) {
     if (!e) return ZH_ERR_INVALID_ARGUMENT;
     if (e->persistent != (on != 0)) {
@@ -704,7 +724,15 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         const Tensor *qkv_t[3] = {&y.wq, &y.wk, &y.wv};
         float *qkv_y[3] = {e->q, e->k, e->v};
         const uint32_t qkv_m[3] = {qd, kvd, kvd};
-        if (!(mask & SK_QKV)) {
+        // Q/K/V and attention in one launch: 8 kv heads, one per XCD
+        const bool qa = (mask & SK_QKV) && (mask & SK_ATTN) && e->fused_qa && lpb_attn && e->pages_ident &&
+                        y.wq.type == ZH_Q4_K && y.wk.type == ZH_Q4_K && y.wv.type == ZH_Q4_K &&
+                        zhk_qkv_attn_supported(c, H, m.n_heads, m.n_kv_heads, hd, m.max_ctx);
+        if (qa) {
+            ERC(zhk_qkv_attn(c, W(y.wq), W(y.wk), W(y.wv), e->hidden, Wf(y.attn_norm), e->q, e->k, e->v, Wf(y.q_norm),
+                             Wf(y.k_norm), e->rope_cs, y.kc, y.vc, m.max_ctx, e->attn, e->xq_q, m.n_heads, pos, scale,
+                             m.eps, e->fd_part, e->qa_flags));
+        } else if (!(mask & SK_QKV)) {
         } else if (lpb_attn) {
             // attn_norm fused into the Q/K/V mat-vec (every workgroup normalises x)
             for (uint32_t i0 = 0; i0 < 3;) {
@@ -734,7 +762,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
                 i0 = i1;
             }
         }
-        if (mask & SK_ATTN)
+        if ((mask & SK_ATTN) && !qa)
             ERC(zhk_attn_decode_fused(c, e->q, e->k, e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc,
                                   e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads, m.n_kv_heads, pos,
                                   m.max_ctx, scale, m.eps, e->fd_part, e->pages_ident));
@@ -1341,6 +1369,8 @@ extern "C" uint64_t zh_engine_group_bytes(zh_engine *e, uint32_t group, uint32_t
     const uint64_t F = c.n_experts ? c.expert_ffn : c.ffn, k = c.n_experts ? c.n_experts_used : 1;
     auto xqb = [](uint64_t n) { return n / 32 * 108; };
     switch (group) {
+    case SK_QKV | SK_ATTN:
+        return zh_engine_group_bytes(e, SK_QKV, Lctx) + zh_engine_group_bytes(e, SK_ATTN, Lctx) - (qd + 2 * kvd) * 8;
     case SK_QKV: return y.wq.bytes + y.wk.bytes + y.wv.bytes + 2 * H * 4 + (qd + 2 * kvd) * 4;
     case SK_ATTN:
         return 2 * kvd * 2 * Lctx + (qd + 2 * kvd) * 4 + 2 * hd * 4 + hd * 4 + 2 * kvd * 2 + qd * 4 + xqb(qd);

@@ -29,6 +29,7 @@ struct zh_buf {
 struct zh_ctx {
     int device = 0;
     int cu_count = 0;
+    int xcd_rr = -1;  // zhk_xcd_round_robin: -1 unknown, 0 no, 1 yes
     hipStream_t stream = nullptr;
     hipEvent_t ev[64] = {};
     std::string err;
@@ -224,6 +225,16 @@ struct zh_step_args {
     uint32_t *ctl;                    // zh_step_ctl_bytes() zeroed bytes (barriers, merge counters)
 };
 uint64_t zh_step_ctl_bytes();
+// Q/K/V projection + decode attention in one launch (zh_qkv_attn.hip): 8 kv
+// heads, one per XCD of a 256-CU device, Q4_K Q/K/V with K = 4096, identity
+// page table, contexts up to 6144 tokens, the device to itself.
+bool zhk_xcd_round_robin(zh_ctx *ctx);
+bool zhk_qkv_attn_supported(zh_ctx *ctx, uint32_t hidden, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx);
+uint32_t zhk_qkv_attn_flag_words();  // zeroed u32 words the caller keeps per engine
+int zhk_qkv_attn(zh_ctx *ctx, const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x,
+                 const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
+                 const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
+                 uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags);
 // The geometry the kernel is built for (hidden 2048 or 4096 = n_heads x 128,
 // FFN 12288 or 14336, 4 q heads per kv head, enough CUs); the caller checks
 // the layer formats (Q4_K Q/K/V/O/gate/up, Q6_K down, 16-byte aligned) and

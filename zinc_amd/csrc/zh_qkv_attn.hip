@@ -1,0 +1,628 @@
+// zh_qkv_attn.hip — the decode step's Q/K/V projection and attention in one
+// launch, for models with 8 kv heads on a device of 8 XCDs x 32 CUs.
+//
+// Replaces two dispatches of the reference's decode step: the Q/K/V DMMVs
+// (forward.zig:4776-4800, dmmv_q4k.comp) and the fused q/k norm + RoPE + KV
+// write + flash decode (qk_norm_rope_kv_write.comp, attention.zig:199-316,
+// flash_decode.comp with its split-K merge).
+//
+// The dispatcher deals the workgroups of a launch round robin over the 8
+// XCDs, starting where the previous launch stopped (measured: workgroup w
+// lands on XCD (w + s) % 8 for a launch-dependent s; the engine checks this
+// once per context with zhk_xcd_round_robin). Each workgroup reads its XCD
+// from the XCC_ID register and takes kv head h = XCD, slice j = w / 8: every
+// run of 8 consecutive workgroups covers the 8 XCDs once, so the (h, j) are
+// all distinct. The 32 workgroups of XCD h
+//   1. compute the (G + 2) * 128 Q/K/V rows of kv head h (its G q heads, its
+//      k and v head), R = 4 (G + 2) rows each, from attn_norm(x) as XQ
+//      limbs (the arithmetic of the ring DMMV, zh_ring_q4k.h, row for row);
+//   2. meet at an XCD-local flag barrier;
+//   3. run the split-K attention over chunk j of the context (norm + RoPE of
+//      q and the new k, MFMA scores and P V, the new K/V row written to the
+//      cache by its chunk's owner), publish a partial (O, m, l) per q head;
+//   4. meet again: workgroups j < G merge q head h G + j into the attention
+//      output and its XQ image for the O projection.
+// Everything exchanged between steps stays inside XCD h, so it is exchanged
+// through that XCD's L2: the producer's plain stores land in its L2, the
+// consumers read with device-scope (sc1) loads, which return the L2's copy
+// (measured: a flag round trip 0.5 us against 1.0 us for device-scope
+// stores and 3.5-4.5 us for a flag barrier over all 256 workgroups). The
+// next kernel sees the outputs after the end-of-kernel L2 write-back.
+//
+// Flags carry an epoch instead of being reset: at the start every
+// workgroup of XCD h reads the epoch word ep[h] and publishes E = ep[h] + 1;
+// merger 0 stores E into ep[h] once every chunk of the head has published,
+// i.e. after all 32 workgroups read it. Every wait is bounded (the attention
+// merge's limit, ctl[1]); one that gives up sets ZH_DEVERR_ATTN_WAIT and the
+// head's output is NaN, as in the two-kernel path.
+//
+// LDS (155.6 KB of 160): K/V sub-chunks 0 and 1 (64 tokens of K then V,
+// 32 KB each), the workgroup's weight rows (R x 2304 B; afterwards the
+// attention's q, new k / v rows and q fragments), the f32 x and norm weight
+// (then its XQ image, then K/V sub-chunk 2), norm weights and the RoPE row.
+// The weight rows, x, the norm weights and (after the position) the K/V
+// sub-chunks are all requested at the start, so the K/V stream overlaps the
+// projection and the barrier. Contexts up to 32 x 192 tokens (three 64-token
+// sub-chunks per chunk); the engine uses the two-kernel path beyond.
+#include "zh_attn_common.h"
+#include "zh_lpb_common.h"
+
+namespace {
+
+constexpr int QA_T = 512;                       // 8 waves, two per SIMD
+constexpr uint32_t RG_SEG = 400;                // XQ image: bytes per 128-element half super-block (padded)
+constexpr int QA_AW = 8, QA_KVW = 32 / QA_AW;   // K/V copies per wave and sub-chunk
+constexpr uint32_t QA_NB = 16;                  // super-blocks per row (K = 4096)
+constexpr uint32_t QA_ROWB = QA_NB * 144;       // 2304 bytes per Q4_K row
+constexpr uint32_t QA_MAXR = 24;                // rows per workgroup (G = 4)
+constexpr uint32_t QA_W = 2 * AR_SLOT;          // weight rows
+constexpr uint32_t QA_X = QA_W + QA_MAXR * QA_ROWB;  // x | norm weight, XQ image, K/V sub-chunk 2
+constexpr uint32_t QA_NRM = QA_X + AR_SLOT;     // q_norm | k_norm (1 KB)
+constexpr uint32_t QA_ROPE = QA_NRM + 1024;     // the position's (cos, sin) row (1 KB copy)
+constexpr uint32_t QA_YL = QA_ROPE + 1024;      // row results [32], RMS partials [8]
+constexpr uint32_t QA_LDS = QA_YL + 256;
+constexpr uint32_t QA_MAXSUB = 3;               // K/V sub-chunks per chunk
+constexpr uint32_t QA_NXCD = 8, QA_PER = 32;    // XCDs, workgroups per XCD
+static_assert(QA_NB * 2 * RG_SEG + QA_NB * 8 * 12 <= AR_SLOT, "XQ image fits the x region");
+
+}  // namespace
+
+// Flag words (zero when the engine is created): [0, 256) Q/K/V rows
+// published, [256, 512) partials published (head h at h * 32: one 128-byte
+// line per XCD), [512, 520) epochs.
+constexpr uint32_t QA_FLAG_WORDS = 2 * QA_NXCD * QA_PER + QA_NXCD;
+
+struct QaP {
+    AttnP a;                      // q / k_new / v_new: the projection outputs (written here)
+    const uint8_t *wq, *wk, *wv;  // Q4_K [nq * 128 | 8 * 128 | 8 * 128][4096]
+    const float *x, *norm_w;      // residual stream, attn_norm weight
+    uint32_t *flags;              // QA_FLAG_WORDS
+};
+
+ZH_DEV uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xFu;
+}
+
+// 16 B per lane into LDS at device scope: data another workgroup of this XCD
+// stored in the shared L2
+ZH_DEV void dma16_dev(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+
+// LDS offset of K/V sub-chunk s
+ZH_DEV uint32_t qa_slot(uint32_t s) { return s == 0 ? 0u : s == 1 ? AR_SLOT : QA_X; }
+
+// Waits (bounded by ctl[1] ticks) until flag words f[0 .. n) reach epoch E;
+// wave 0 polls, one word per lane. Returns false after giving up (and sets
+// ZH_DEVERR_ATTN_WAIT). Every thread of the workgroup calls it.
+ZH_DEV bool qa_wait(const uint32_t *f, uint32_t n, uint32_t E, uint32_t *ctl, uint32_t tid) {
+    __shared__ uint32_t s_ok;
+    if (tid < 64) {
+        const uint32_t lane = tid;
+        bool ok = true;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        const uint64_t limit = __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        while (true) {
+            const uint32_t v = lane < n ? __hip_atomic_load(f + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : E;
+            if (__builtin_amdgcn_ballot_w64((int32_t)(v - E) < 0) == 0 && limit != 0) break;
+            if (__builtin_amdgcn_s_memrealtime() - t0 >= limit) {
+                ok = false;
+                if (lane == 0) __hip_atomic_fetch_or(ctl, ZH_DEVERR_ATTN_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+        if (lane == 0) s_ok = ok ? 1u : 0u;
+    }
+    __syncthreads();
+    return s_ok != 0;
+}
+
+template <int G>
+__global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr uint32_t R = 4 * (G + 2);          // weight rows per workgroup
+    constexpr uint32_t NCH = R * QA_ROWB / 1024;  // their 1 KB copies
+    constexpr uint32_t NP = (R + 15) / 16;        // passes of 16 rows
+    constexpr uint32_t QC = ar_qc<G>();           // 1 KB copies of the group's q
+    constexpr uint32_t QR = G * FD_HD;            // q rows of a kv head
+    static_assert(R * QA_ROWB % 1024 == 0 && R <= QA_MAXR && R % 4 == 0, "row slice");
+    const AttnP &p = P.a;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // kv head = this workgroup's XCD; slice j = blockIdx / 8 (each run of 8
+    // consecutive workgroups covers the 8 XCDs once)
+    const uint32_t h = min(xcc_id(), QA_NXCD - 1), j = blockIdx.x / QA_NXCD;
+    const uint32_t lds0 = lds_addr(lds);
+    uint32_t *fl_q = P.flags + h * QA_PER, *fl_p = P.flags + QA_NXCD * QA_PER + h * QA_PER;
+    uint32_t *ep = P.flags + 2 * QA_NXCD * QA_PER + h;
+    // position and epoch through the scalar cache (no vector-memory count)
+    const uint32_t posv = *(const __attribute__((address_space(4))) uint32_t *)p.pos.dev + p.pos.value;
+    const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
+
+    // ---- copies that need nothing: x | attn_norm weight (2 + 2 per wave),
+    // the slice's weight rows (nw per wave), q_norm | k_norm (wave 0)
+#pragma unroll
+    for (uint32_t i = 0; i < 2; i++) {
+        const uint32_t c = wave + 8 * i;
+        dma16((const uint8_t *)P.x + c * 1024 + lane * 16, lds0 + QA_X + c * 1024);
+        dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + QA_X + 16384 + c * 1024);
+    }
+    const uint32_t nw = wave < NCH % 8 ? NCH / 8 + 1 : NCH / 8;
+#pragma unroll
+    for (uint32_t i = 0; i < (NCH + 7) / 8; i++) {
+        const uint32_t c = wave + 8 * i;
+        if (c < NCH) {  // uniform per wave
+            const uint32_t o = c * 1024 + lane * 16, r = o / QA_ROWB, within = o - r * QA_ROWB;
+            const uint32_t rr = j * R + r;  // row of the kv head's q | k | v rows
+            const uint8_t *src = rr < QR ? P.wq + (size_t)(h * QR + rr) * QA_ROWB
+                               : rr < QR + FD_HD ? P.wk + (size_t)(h * FD_HD + rr - QR) * QA_ROWB
+                                                 : P.wv + (size_t)(h * FD_HD + rr - QR - FD_HD) * QA_ROWB;
+            dma16(src + within, lds0 + QA_W + c * 1024);
+        }
+    }
+    const uint32_t nnrm = wave == 0 ? 1u : 0u;
+    if (wave == 0)
+        dma16((const uint8_t *)(lane < 32 ? p.q_norm : p.k_norm) + (lane & 31) * 16, lds0 + QA_NRM);
+
+    // ---- chunk geometry (chunk j of 32), then its first two K/V sub-chunks
+    // and the RoPE row of the position
+    const uint32_t seq = posv + 1;
+    const uint32_t CT = ((seq + QA_PER - 1) / QA_PER + 15) / 16 * 16;
+    const uint32_t nv = (seq + CT - 1) / CT;  // chunks holding tokens
+    const uint32_t t0 = j * CT, t1 = min(seq, t0 + CT);
+    uint32_t nsub = j < nv ? (t1 - t0 + AR_TS - 1) / AR_TS : 0u;
+    if (nsub > QA_MAXSUB) {  // (the engine keeps the context within 32 x 192 tokens)
+        if (tid == 0) __hip_atomic_fetch_or(p.ctl, ZH_DEVERR_ATTN_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        nsub = QA_MAXSUB;
+    }
+    const uint16_t *kbase = p.kc + (size_t)h * p.cache_tokens * FD_HD;
+    const uint16_t *vbase = p.vc + (size_t)h * p.cache_tokens * FD_HD;
+    // sub-chunk s: 32 copies of 1 KB (4 token rows of K, then of V); rows
+    // past the chunk re-read its last row (masked). 16-byte piece q of LDS
+    // row rr holds the row's piece q ^ (rr % 16).
+    auto issue_kv = [&](uint32_t s) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t i = 0; i < QA_KVW; i++) {
+            const uint32_t jj = wave + QA_AW * i, kv = jj >> 4;
+            const uint32_t rr = 4 * (jj & 15) + (lane >> 4);
+            const uint32_t t = min(t0 + s * AR_TS + rr, t1 - 1);
+            const uint16_t *row = (kv ? vbase : kbase) + (size_t)t * FD_HD;
+            dma16(row + ((lane & 15) ^ (rr & 15)) * 8, lds0 + qa_slot(s) + jj * 1024);
+        }
+    };
+    const uint32_t n01 = min(nsub, 2u);
+    for (uint32_t s = 0; s < n01; s++) issue_kv(s);
+    const uint32_t nrope = wave == QA_AW - 1 ? 1u : 0u;
+    if (wave == QA_AW - 1)
+        dma16((const uint8_t *)(p.rope_cs + (size_t)posv * FD_HD) + min(lane * 16, 496u), lds0 + QA_ROPE);
+
+    // ---- attn_norm(x) as XQ limbs (the ring DMMV's staging, in place)
+    wait_vm_dyn(nw + nnrm + n01 * QA_KVW + nrope);
+    lds_bar();
+    float *yl = (float *)(lds + QA_YL), *red = yl + 32;
+    uint32_t L[4][24];
+    float xs[4], xz[4];
+    const uint32_t team = tid / 32, tl = tid % 32, b = tl >> 1, hh = tl & 1;
+    {
+        const float *xr = (const float *)(lds + QA_X), *wr = xr + 4096;
+        f32x4 v[2], w[2];
+        float sq = 0.f;
+#pragma unroll
+        for (int it = 0; it < 2; it++) {
+            v[it] = *(const f32x4 *)(xr + (it * QA_T + tid) * 4);
+            w[it] = *(const f32x4 *)(wr + (it * QA_T + tid) * 4);
+            sq = fmaf(v[it].x, v[it].x, sq); sq = fmaf(v[it].y, v[it].y, sq);
+            sq = fmaf(v[it].z, v[it].z, sq); sq = fmaf(v[it].w, v[it].w, sq);
+        }
+        sq = wave_sum(sq);
+        if (lane == 0) red[wave] = sq;
+        lds_bar();  // (also: every x / weight value is in registers before the image overwrites them)
+        float tot = 0.f;
+#pragma unroll
+        for (int w8 = 0; w8 < 8; w8++) tot += red[w8];
+        const float rms_inv = 1.0f / sqrtf(tot / 4096.f + p.eps);
+        uint8_t *xqa = lds + QA_X;
+        float *ixs = (float *)(xqa + QA_NB * 2 * RG_SEG), *ixz = ixs + QA_NB * 8;
+#pragma unroll
+        for (int it = 0; it < 2; it++) {
+            const uint32_t e0 = (it * QA_T + tid) * 4;
+            f32x4 u = v[it];
+            u.x = w[it].x * (u.x * rms_inv); u.y = w[it].y * (u.y * rms_inv);
+            u.z = w[it].z * (u.z * rms_inv); u.w = w[it].w * (u.w * rms_inv);
+            const float a = row8_max(fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+            float inv, sc;
+            xq_scales(a, inv, sc);
+            int X[4] = {xq_quant(u.x, inv), xq_quant(u.y, inv), xq_quant(u.z, inv), xq_quant(u.w, inv)};
+            int l0[4], l1[4], l2[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) xq_limbs(X[q], l0[q], l1[q], l2[q]);
+            const uint32_t blk = e0 / 32, lo = e0 % 32;
+            uint8_t *dst = xqa + (blk / 4) * RG_SEG + (blk % 4) * 96 + lo;
+            *(uint32_t *)(dst) = pack4(l0[0], l0[1], l0[2], l0[3]);
+            *(uint32_t *)(dst + 32) = pack4(l1[0], l1[1], l1[2], l1[3]);
+            *(uint32_t *)(dst + 64) = pack4(l2[0], l2[1], l2[2], l2[3]);
+            int sm = X[0] + X[1] + X[2] + X[3];
+            sm += __builtin_amdgcn_update_dpp(0, sm, 0xB1, 0xF, 0xF, false);
+            sm += __builtin_amdgcn_update_dpp(0, sm, 0x4E, 0xF, 0xF, false);
+            const uint32_t sub = tid & 7;
+            if (sub == 0) ixs[blk] = sc;
+            if ((sub & 3) == 0) ixz[blk * 2 + (sub >> 2)] = (float)sm * sc;
+        }
+        lds_bar();
+        // this lane's half super-block: limbs, block scales and sums
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t jb = b * 8 + 4 * hh + q;
+            lds_load_limbs(L[q], xqa + tl * RG_SEG + q * 96);
+            xs[q] = ixs[jb];
+            xz[q] = ixz[2 * jb] + ixz[2 * jb + 1];
+        }
+        lds_bar();  // the image is read: the region takes K/V sub-chunk 2
+    }
+    const uint32_t n2 = nsub > 2 ? 1u : 0u;
+    if (n2) issue_kv(2);
+
+    // ---- the slice's rows (the ring DMMV's per-row arithmetic)
+    wait_vm_dyn(nnrm + n01 * QA_KVW + nrope + n2 * QA_KVW);
+    lds_bar();
+#pragma unroll
+    for (uint32_t ps = 0; ps < NP; ps++) {
+        const uint32_t r = ps * 16 + team;
+        if (r < R) {  // uniform per wave (R % 4 == 0)
+            const uint8_t *blk = lds + QA_W + r * QA_ROWB + b * 144;
+            uint32_t hd[4], qs[16];
+            {
+                const u32x4 v = *(const u32x4 *)blk;
+                hd[0] = v.x; hd[1] = v.y; hd[2] = v.z; hd[3] = v.w;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const u32x4 w = *(const u32x4 *)(blk + 16 + 64 * hh + 16 * i);
+                    qs[4 * i] = w.x; qs[4 * i + 1] = w.y; qs[4 * i + 2] = w.z; qs[4 * i + 3] = w.w;
+                }
+            }
+            const LpbQ4K::Hdr hdr = LpbQ4K::header(hd);
+            const uint32_t scw = hh ? hdr.scB : hdr.scA, mw = hh ? hdr.mB : hdr.mA;
+            float accd = 0.f, accm = 0.f;
+#pragma unroll
+            for (int pl = 0; pl < 2; pl++) {
+                int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t w = qs[8 * pl + i];
+                    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                    for (int k = 0; k < 3; k++) {
+                        D[0][k] = sdot4(lo, L[2 * pl][k * 8 + i], D[0][k]);
+                        D[1][k] = sdot4(hi, L[2 * pl + 1][k * 8 + i], D[1][k]);
+                    }
+                }
+                const float sc0 = ubyte_f(scw, 2 * pl), sc1 = ubyte_f(scw, 2 * pl + 1);
+                const float m0 = ubyte_f(mw, 2 * pl), m1 = ubyte_f(mw, 2 * pl + 1);
+                const float S0 = (float)comb_i(D[0][0], D[0][1], D[0][2]);
+                const float S1 = (float)comb_i(D[1][0], D[1][1], D[1][2]);
+                accd = fmaf(sc0 * xs[2 * pl], S0, accd);
+                accd = fmaf(sc1 * xs[2 * pl + 1], S1, accd);
+                accm = fmaf(m0, xz[2 * pl], accm);
+                accm = fmaf(m1, xz[2 * pl + 1], accm);
+            }
+            float res = fmaf(hdr.d, accd, -hdr.dmin * accm);
+            res = team_sum_dpp<32>(res);
+            if (tl == 0) yl[r] = res;
+        }
+    }
+    lds_bar();
+    // ---- publish the rows (wave 0), then wait for the kv head's other slices
+    if (wave == 0) {
+        if (lane < R) {
+            const uint32_t rr = j * R + lane;
+            float *dst = rr < QR ? (float *)p.q + h * QR + rr
+                       : rr < QR + FD_HD ? (float *)p.k_new + h * FD_HD + rr - QR
+                                         : (float *)p.v_new + h * FD_HD + rr - QR - FD_HD;
+            *dst = yl[lane];
+        }
+        wait_vm<0>();  // the rows are in the L2 before the flag
+        if (lane == 0) *(volatile uint32_t *)(fl_q + j) = E;
+    }
+    const bool ok_rows = qa_wait(fl_q, QA_PER, E, p.ctl, tid);
+
+    // ---- the attention's inputs from the L2: the group's q, the new k | v
+    uint8_t *sm = lds + QA_W;  // q [G][128] f32 (QC KB), k_new | v_new (1 KB), new K / V rows f16, q fragments
+    for (uint32_t k = wave; k <= QC; k += QA_AW) {  // uniform per wave
+        const uint8_t *src = k < QC ? (const uint8_t *)(p.q + (size_t)h * QR) + min(k * 1024 + lane * 16, QR * 4 - 16)
+                           : lane < 32 ? (const uint8_t *)(p.k_new + (size_t)h * FD_HD) + lane * 16
+                                       : (const uint8_t *)(p.v_new + (size_t)h * FD_HD) + (lane - 32) * 16;
+        dma16_dev(src, lds0 + QA_W + k * 1024);
+    }
+    wait_vm<0>();  // ... and every K/V sub-chunk
+    lds_bar();
+
+    // ---- q as MFMA fragments (RMSNorm, RoPE, f16 hi + lo), shared through LDS
+    const uint32_t sub = lane & 7, fg = lane & 15, fq = lane >> 4;
+    const uint32_t gq = wave / 4, w4 = wave % 4;
+    const float *qw = (const float *)(lds + QA_NRM), *kw = qw + FD_HD;
+    const float *cs = (const float *)(lds + QA_ROPE);
+    uint16_t *knew16 = (uint16_t *)(sm + (QC + 1) * 1024), *vnew16 = knew16 + FD_HD;
+    uint8_t *frag = sm + (QC + 2) * 1024;
+    float *rinv = (float *)(frag + 8 * 64 * 16);
+    half4 qh[8], ql[8];
+    {
+        for (uint32_t g = wave; g < (uint32_t)G; g += QA_AW) {
+            const float *qs = (const float *)sm + g * FD_HD;
+            const float a = qs[lane], bb = qs[lane + 64];
+            const float sq = wave_sum(fmaf(a, a, bb * bb));
+            if (lane == 0) rinv[g] = 1.0f / sqrtf(sq / (float)FD_HD + p.eps);
+        }
+        lds_bar();
+        if (wave < 4) {
+            const uint32_t pi = wave;  // steps pi (dims < 64) and pi + 4 (their RoPE partners)
+            const float *qs = (const float *)sm + min(fg, (uint32_t)G - 1) * FD_HD;
+            const f32x4 va = *(const f32x4 *)(qs + 16 * pi + 4 * fq), vb = *(const f32x4 *)(qs + 64 + 16 * pi + 4 * fq);
+            float lo[4] = {va.x, va.y, va.z, va.w}, hi[4] = {vb.x, vb.y, vb.z, vb.w};
+            const float ri = rinv[min(fg, (uint32_t)G - 1)];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t i = 16 * pi + 4 * fq + e;  // dims i and i + 64
+                const float a = qw[i] * (lo[e] * ri);
+                const float bb = qw[i + 64] * (hi[e] * ri);
+                const float co = cs[2 * i], sn = cs[2 * i + 1];
+                lo[e] = a * co - bb * sn;
+                hi[e] = a * sn + bb * co;
+            }
+            half4 h0, l0, h1, l1;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x0 = fg < (uint32_t)G ? lo[e] : 0.f, y0 = fg < (uint32_t)G ? hi[e] : 0.f;
+                h0[e] = (_Float16)x0;
+                l0[e] = (_Float16)(x0 - (float)h0[e]);
+                h1[e] = (_Float16)y0;
+                l1[e] = (_Float16)(y0 - (float)h1[e]);
+            }
+            *(half4 *)(frag + (pi * 64 + lane) * 16) = h0;
+            *(half4 *)(frag + (pi * 64 + lane) * 16 + 8) = l0;
+            *(half4 *)(frag + ((pi + 4) * 64 + lane) * 16) = h1;
+            *(half4 *)(frag + ((pi + 4) * 64 + lane) * 16 + 8) = l1;
+        }
+        lds_bar();
+#pragma unroll
+        for (int s8 = 0; s8 < 8; s8++) {
+            qh[s8] = *(const half4 *)(frag + (s8 * 64 + lane) * 16);
+            ql[s8] = *(const half4 *)(frag + (s8 * 64 + lane) * 16 + 8);
+        }
+    }
+    // ---- the new token's k (norm + RoPE) and v as f16 rows (the owner only)
+    const bool owner = posv >= t0 && posv < t1;  // uniform
+    if (owner && wave == 0) {
+        const float *kn = (const float *)(sm + QC * 1024), *vn = kn + FD_HD;
+        float klo[8], khi[8], wlo[8], whi[8], co[8], sn[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            klo[e] = kn[sub * 8 + e];
+            khi[e] = kn[64 + sub * 8 + e];
+            wlo[e] = kw[sub * 8 + e];
+            whi[e] = kw[64 + sub * 8 + e];
+            co[e] = cs[2 * (sub * 8 + e)];
+            sn[e] = cs[2 * (sub * 8 + e) + 1];
+        }
+        norm_rope16(klo, khi, wlo, whi, co, sn, p.eps);
+        if (lane < 8) {
+            *(u32x4 *)(knew16 + sub * 8) = u32x4{pack_h2(klo[0], klo[1]), pack_h2(klo[2], klo[3]),
+                                                 pack_h2(klo[4], klo[5]), pack_h2(klo[6], klo[7])};
+            *(u32x4 *)(knew16 + 64 + sub * 8) = u32x4{pack_h2(khi[0], khi[1]), pack_h2(khi[2], khi[3]),
+                                                      pack_h2(khi[4], khi[5]), pack_h2(khi[6], khi[7])};
+        }
+        *(uint32_t *)(vnew16 + 2 * lane) = pack_h2(vn[2 * lane], vn[2 * lane + 1]);
+    }
+    const uint32_t s_own = owner ? (posv - t0) / AR_TS : ~0u, r_own = owner ? (posv - t0) % AR_TS : 0u;
+    lds_bar();
+    if (owner && s_own < nsub) {  // substitute the new row for the copy (which predates it)
+        uint8_t *Ks = lds + qa_slot(s_own);
+        const uint32_t pc = ((tid & 15) ^ (r_own & 15)) * 16;
+        if (tid < 16) *(u32x4 *)(Ks + r_own * 256 + pc) = *(const u32x4 *)((const uint8_t *)knew16 + tid * 16);
+        else if (tid < 32)
+            *(u32x4 *)(Ks + AR_SLOT / 2 + r_own * 256 + pc) = *(const u32x4 *)((const uint8_t *)vnew16 + (tid - 16) * 16);
+    }
+    lds_bar();
+
+    // ---- scores and P V over the landed sub-chunks: group gq (4 waves) takes
+    // sub-chunks gq, gq + 2; wave w4 of a group tokens 16 w4 .. 16 w4 + 15
+    float m_run = -INFINITY, l_run = 0.f;
+    floatx4 acc[8];
+#pragma unroll
+    for (int n = 0; n < 8; n++) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s = gq; s < nsub; s += 2) {  // uniform per wave
+        const uint8_t *Ks = lds + qa_slot(s), *Vs = Ks + AR_SLOT / 2;
+        const uint32_t ts = t0 + s * AR_TS, tb = w4 * 16;
+        half4 kf[8], vf[8];
+        {
+            const uint32_t t = tb + fg;
+#pragma unroll
+            for (int s8 = 0; s8 < 8; s8++)
+                kf[s8] = *(const half4 *)(Ks + t * 256 + (((2 * s8 + (fq >> 1)) ^ (t & 15)) * 16) + 8 * (fq & 1));
+            const uint32_t tv = tb + 4 * fq, off = 2 * (fg & 7);
+#pragma unroll
+            for (int n = 0; n < 8; n++) {
+                const uint32_t pc = 2 * n + (fg >> 3);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t t2 = tv + r;
+                    vf[n][r] = *(const _Float16 *)(Vs + t2 * 256 + (pc ^ (t2 & 15)) * 16 + off);
+                }
+            }
+        }
+        floatx4 d1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s8 = 0; s8 < 8; s8++) {
+            d1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kf[s8], qh[s8], d1, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kf[s8], ql[s8], d1, 0, 0, 0);
+        }
+        float sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) sc[r] = ts + tb + 4 * fq + r < t1 ? d1[r] * p.scale : -INFINITY;
+        float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        const float mn = fmaxf(m_run, m);
+        const float ms = mn == -INFINITY ? 0.f : mn;
+        const float f = m_run == -INFINITY ? 0.f : expf(m_run - ms);
+        float pr[4], lsum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            pr[r] = fg < (uint32_t)G ? expf(sc[r] - ms) : 0.f;
+            lsum += pr[r];
+        }
+        lsum += __shfl_xor(lsum, 16, 64);
+        lsum += __shfl_xor(lsum, 32, 64);
+        l_run = fmaf(l_run, f, lsum);
+        m_run = mn;
+        half4 ph, pl;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const _Float16 hv = (_Float16)pr[r];
+            ph[r] = hv;
+            pl[r] = (_Float16)(pr[r] - (float)hv);
+        }
+        float fr[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) fr[r] = G > 4 && fq ? lane_f(f, 4 + r) : lane_f(f, r);
+#pragma unroll
+        for (int n = 0; n < 8; n++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[n][r] *= fr[r];
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vf[n], acc[n], 0, 0, 0);
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vf[n], acc[n], 0, 0, 0);
+        }
+    }
+    // ---- the new row to the cache
+    if (owner && tid < 32) {
+        uint16_t *dst = (tid < 16 ? p.kc : p.vc) + ((size_t)h * p.cache_tokens + posv) * FD_HD + (tid & 15) * 8;
+        *(u32x4 *)dst = *(const u32x4 *)((const uint8_t *)(tid < 16 ? knew16 : vnew16) + (tid & 15) * 16);
+    }
+    // ---- combine the waves (in sub-chunk 0's slot), publish the partials
+    float *wm = (float *)lds, *wl = wm + QA_AW * G, *wo = wl + QA_AW * G;
+    lds_bar();
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t g = 4 * fq + r;
+        if (g < (uint32_t)G)
+#pragma unroll
+            for (int n = 0; n < 8; n++) wo[(wave * G + g) * FD_HD + 16 * n + fg] = acc[n][r];
+    }
+    if (fq == 0 && fg < (uint32_t)G) {
+        wm[wave * G + fg] = m_run;
+        wl[wave * G + fg] = l_run;
+    }
+    __syncthreads();
+    if (nsub) {
+        for (uint32_t o = tid; o < (uint32_t)G * FD_HD; o += QA_T) {
+            const uint32_t g = o / FD_HD, d = o % FD_HD;
+            float M = wm[g];
+#pragma unroll
+            for (int w = 1; w < QA_AW; w++) M = fmaxf(M, wm[w * G + g]);
+            const float Ms = M == -INFINITY ? 0.f : M;
+            float O = 0.f, Ls = 0.f;
+#pragma unroll
+            for (int w = 0; w < QA_AW; w++) {
+                const float f = wm[w * G + g] == -INFINITY ? 0.f : expf(wm[w * G + g] - Ms);
+                O = fmaf(wo[(w * G + g) * FD_HD + d], f, O);
+                Ls = fmaf(wl[w * G + g], f, Ls);
+            }
+            float *pp = p.part + ((size_t)(h * G + g) * p.n_chunks + j) * (FD_HD + 2);
+            pp[d] = O;
+            if (d == 0) {
+                pp[FD_HD] = M;
+                pp[FD_HD + 1] = Ls;
+            }
+        }
+        wait_vm<0>();  // every wave's partial stores are in the L2 ...
+        __syncthreads();
+        if (tid == 0) *(volatile uint32_t *)(fl_p + j) = E;  // ... before the flag
+    }
+    if (j >= (uint32_t)G) return;
+    // ---- merger j: q head h G + j, once every chunk of the kv head published
+    const bool ok = qa_wait(fl_p, nv, E, p.ctl, tid);
+    if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
+    attn_merge<1, 32, false>(p, h * G + j, nv, !(ok && ok_rows));
+}
+
+// Whether the workgroups of a 256-workgroup grid (one per CU) land on XCDs
+// (blockIdx + s) % 8 for one s: the placement k_qkv_attn's (kv head, slice)
+// assignment relies on (otherwise a slice would be missing and its waits
+// would give up).
+__global__ __launch_bounds__(64) void k_xcd_probe(uint32_t *out) {
+    extern __shared__ uint8_t lds_probe[];
+    if (threadIdx.x == 0) {
+        lds_probe[0] = 0;
+        out[blockIdx.x] = xcc_id();
+    }
+}
+
+bool zhk_xcd_round_robin(zh_ctx *c) {
+    if (c->xcd_rr >= 0) return c->xcd_rr != 0;
+    c->xcd_rr = 0;
+    if (c->cu_count != (int)(QA_NXCD * QA_PER)) return false;
+    uint32_t *d = nullptr, h[QA_NXCD * QA_PER];
+    if (hipMalloc((void **)&d, sizeof h) != hipSuccess) return false;
+    bool ok = false;
+    // 96 KB of LDS: one workgroup per CU, as k_qkv_attn
+    if (hipFuncSetAttribute((const void *)k_xcd_probe, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) ==
+        hipSuccess) {
+        hipLaunchKernelGGL(k_xcd_probe, dim3(QA_NXCD * QA_PER), dim3(64), 96 * 1024, c->stream, d);
+        if (hipStreamSynchronize(c->stream) == hipSuccess &&
+            hipMemcpy(h, d, sizeof h, hipMemcpyDeviceToHost) == hipSuccess) {
+            ok = h[0] < QA_NXCD;
+            for (uint32_t i = 0; i < QA_NXCD * QA_PER; i++) ok = ok && h[i] == (h[0] + i) % QA_NXCD;
+        }
+    }
+    hipFree(d);
+    c->xcd_rr = ok ? 1 : 0;
+    return ok;
+}
+
+uint32_t zhk_qkv_attn_flag_words() { return QA_FLAG_WORDS; }
+
+// Whether k_qkv_attn takes a model of this shape on this context.
+bool zhk_qkv_attn_supported(zh_ctx *c, uint32_t hidden, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx) {
+    const uint32_t G = nkv ? nh / nkv : 0;
+    return hidden == 4096 && nkv == QA_NXCD && hd == FD_HD && nh == G * nkv && (G == 1 || G == 2 || G == 4) &&
+           max_ctx <= QA_PER * QA_MAXSUB * AR_TS && !c->concurrent && zhk_xcd_round_robin(c);
+}
+
+int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x,
+                 const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
+                 const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
+                 uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags) {
+    QaP P = {};
+    AttnP &p = P.a;
+    p.q = q; p.k_new = k; p.v_new = v; p.q_norm = qw; p.k_norm = kw; p.rope_cs = rope_cs;
+    p.kc = kc; p.vc = vc; p.pages = nullptr; p.n_pages = 0; p.cache_tokens = cache_tokens; p.pos = pos;
+    p.scale = scale; p.eps = eps; p.part = partials; p.n_chunks = QA_PER; p.counters = nullptr;
+    p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh; p.nd = QA_PER; p.no_wait = 0; p.ident = 1; p.ctl = c->err_dev;
+    P.wq = wq; P.wk = wk; P.wv = wv; P.x = x; P.norm_w = norm_w; P.flags = flags;
+    const uint32_t G = nh / QA_NXCD;
+    if (!pos.dev || ((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wq & 15) || ((uintptr_t)wk & 15) ||
+        ((uintptr_t)wv & 15))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: device position and 16-byte aligned operands");
+#define QA_L(GG)                                                                                                 \
+    {                                                                                                            \
+        static bool attr = false;                                                                                \
+        if (!attr) {                                                                                             \
+            ZH_HIP(c, hipFuncSetAttribute((const void *)k_qkv_attn<GG>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                          (int)QA_LDS));                                                         \
+            attr = true;                                                                                         \
+        }                                                                                                        \
+        hipLaunchKernelGGL(k_qkv_attn<GG>, dim3(QA_NXCD * QA_PER), dim3(QA_T), QA_LDS, c->stream, P);           \
+        break;                                                                                                   \
+    }
+    switch (G) {
+    case 1: QA_L(1)
+    case 2: QA_L(2)
+    case 4: QA_L(4)
+    default: return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: GQA group %u", G);
+    }
+#undef QA_L
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
