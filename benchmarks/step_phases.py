@@ -14,6 +14,9 @@ Build the debug library first (it also compiles the points in):
     ZH_LIB_PATH=_work/dbg/libzinc_hip.so python -m benchmarks.step_phases
     ZH_LIB_PATH=_work/dbg/libzinc_hip.so python -m benchmarks.step_phases --standalone
 
+--qkv-attn: the Q/K/V + attention launch (k_qkv_attn) of the per-phase
+step, replayed by zh_engine_time_kernel.
+
 --standalone: the same attention body as its own kernel (the per-phase
 step with a shuffled page table, i.e. k_attn_ring), its launches replayed by
 zh_engine_time_kernel; points relative to each workgroup's start.
@@ -70,11 +73,87 @@ def standalone():
     ctx.close()
 
 
+QA_POINTS = ["start", "x landed", "XQ limbs in registers", "weight rows landed", "rows computed",
+             "rows published", "rows of the head seen", "q, k, v, K/V landed", "q fragments", "scores and P V done",
+             "partials published", "merger: chunks seen", "merger: output"]
+
+
+def qkv_attn():
+    """Per-workgroup timeline of k_qkv_attn (Q/K/V + attention in one launch)."""
+    L = hip.lib()
+    L.zh_debug_trace_qa.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
+    ctx = hip.Context(0)
+    cfg = dict(DENSE_8B)
+    cfg["max_ctx"] = 4096 + 64
+    eng = InferenceEngine(ctx, cfg)
+    eng.prefill_kv_random(4096, 7)
+    eng.generate([17, 18], 2, start_pos=4096)
+    ctx.sync()
+    n = 8192 * 16
+    a = np.zeros(n, np.uint64)
+    L.zh_debug_trace_qa(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+    us = eng.time_kernel("qkv_attn", 36)
+    ctx.sync()
+    L.zh_debug_trace_qa(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+    t = a.reshape(8192, 16)[:256].astype(np.int64)
+    base = t[:, 0].min()
+    print(f"k_qkv_attn ({eng.group_kernels('qkv_attn')}): {us:.2f} us per launch (events, debug build); "
+          "points of the last launch, us from the first workgroup's start / from each workgroup's start:")
+    for s, nm in enumerate(QA_POINTS):
+        m = t[:, s] > 0
+        if not m.any():
+            continue
+        g, r = (t[m, s] - base) * 0.01, (t[m, s] - t[m, 0]) * 0.01
+        print(f"  {nm:24s}: n={m.sum():3d}  abs p50 {np.median(g):6.2f} max {g.max():6.2f}   "
+              f"rel min {r.min():6.2f} p50 {np.median(r):6.2f} max {r.max():6.2f}")
+    eng.deinit()
+    ctx.close()
+
+
+RING_POINTS = ["start", "activation landed", "XQ limbs in registers", "ring done", "outputs stored"]
+
+
+def ring(group):
+    """Per-workgroup timeline of a ring DMMV launch group (zh_ring_q4k.h)."""
+    L = hip.lib()
+    L.zh_debug_trace_ring.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
+    ctx = hip.Context(0)
+    cfg = dict(DENSE_8B)
+    cfg["max_ctx"] = 4096 + 64
+    eng = InferenceEngine(ctx, cfg)
+    eng.prefill_kv_random(4096, 7)
+    eng.generate([17, 18], 2, start_pos=4096)
+    ctx.sync()
+    n = 8192 * 16
+    a = np.zeros(n, np.uint64)
+    L.zh_debug_trace_ring(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+    us = eng.time_kernel(group, 36)
+    ctx.sync()
+    L.zh_debug_trace_ring(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+    t = a.reshape(8192, 16)[:256].astype(np.int64)
+    base = t[:, 0].min()
+    print(f"{group} ({eng.group_kernels(group)}): {us:.2f} us per launch (events, debug build); "
+          "points of the last launch, us from the first workgroup's start / from each workgroup's start:")
+    for s, nm in enumerate(RING_POINTS):
+        m = t[:, s] > 0
+        if not m.any():
+            continue
+        g, r = (t[m, s] - base) * 0.01, (t[m, s] - t[m, 0]) * 0.01
+        print(f"  {nm:24s}: n={m.sum():3d}  abs p50 {np.median(g):6.2f} max {g.max():6.2f}   "
+              f"rel min {r.min():6.2f} p50 {np.median(r):6.2f} max {r.max():6.2f}")
+    eng.deinit()
+    ctx.close()
+
+
 def main():
     if not os.environ.get("ZH_LIB_PATH"):
         sys.exit("set ZH_LIB_PATH to the debug build's libzinc_hip.so")
     if "--standalone" in sys.argv[1:]:
         return standalone()
+    if "--qkv-attn" in sys.argv[1:]:
+        return qkv_attn()
+    if "--ring" in sys.argv[1:]:
+        return ring(sys.argv[sys.argv.index("--ring") + 1])
     L = hip.lib()
     L.zh_debug_trace_step.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
     ctx = hip.Context(0)

@@ -44,6 +44,7 @@
 // sub-chunks are all requested at the start, so the K/V stream overlaps the
 // projection and the barrier. Contexts up to 32 x 192 tokens (three 64-token
 // sub-chunks per chunk); the engine uses the two-kernel path beyond.
+#define TRACE_OPS(slot) do { } while (0)  // the shared bodies' points stay off: this file numbers its own
 #include "zh_attn_common.h"
 #include "zh_lpb_common.h"
 
@@ -77,6 +78,7 @@ struct QaP {
     const uint8_t *wq, *wk, *wv;  // Q4_K [nq * 128 | 8 * 128 | 8 * 128][4096]
     const float *x, *norm_w;      // residual stream, attn_norm weight
     uint32_t *flags;              // QA_FLAG_WORDS
+    uint32_t kv_defer;            // K/V copies issued at the start (0), after x landed (1), after the rows landed (2)
 };
 
 ZH_DEV uint32_t xcc_id() {
@@ -141,34 +143,40 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     // position and epoch through the scalar cache (no vector-memory count)
     const uint32_t posv = *(const __attribute__((address_space(4))) uint32_t *)p.pos.dev + p.pos.value;
     const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
+    ZH_TRACE_POINT(0);
 
-    // ---- copies that need nothing: x | attn_norm weight (2 + 2 per wave),
-    // the slice's weight rows (nw per wave), q_norm | k_norm (wave 0)
+    // ---- copies. Waves 0-3 copy what the projection needs (x | attn_norm
+    // weight, then the slice's weight rows); waves 4-7 the attention's (K/V
+    // sub-chunks, q_norm | k_norm, the RoPE row), so that no wave that waits
+    // for the projection's data also waits for K/V, and the row publication
+    // below waits only for its own stores.
+    const bool wa = wave < 4;  // uniform
+    const uint32_t wl4 = wave & 3;
+    const uint32_t nw = wl4 < NCH % 4 ? NCH / 4 + 1 : NCH / 4;  // weight copies of an A wave
+    if (wa) {
 #pragma unroll
-    for (uint32_t i = 0; i < 2; i++) {
-        const uint32_t c = wave + 8 * i;
-        dma16((const uint8_t *)P.x + c * 1024 + lane * 16, lds0 + QA_X + c * 1024);
-        dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + QA_X + 16384 + c * 1024);
-    }
-    const uint32_t nw = wave < NCH % 8 ? NCH / 8 + 1 : NCH / 8;
-#pragma unroll
-    for (uint32_t i = 0; i < (NCH + 7) / 8; i++) {
-        const uint32_t c = wave + 8 * i;
-        if (c < NCH) {  // uniform per wave
-            const uint32_t o = c * 1024 + lane * 16, r = o / QA_ROWB, within = o - r * QA_ROWB;
-            const uint32_t rr = j * R + r;  // row of the kv head's q | k | v rows
-            const uint8_t *src = rr < QR ? P.wq + (size_t)(h * QR + rr) * QA_ROWB
-                               : rr < QR + FD_HD ? P.wk + (size_t)(h * FD_HD + rr - QR) * QA_ROWB
-                                                 : P.wv + (size_t)(h * FD_HD + rr - QR - FD_HD) * QA_ROWB;
-            dma16(src + within, lds0 + QA_W + c * 1024);
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t c = wl4 + 4 * i;
+            dma16((const uint8_t *)P.x + c * 1024 + lane * 16, lds0 + QA_X + c * 1024);
+            dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + QA_X + 16384 + c * 1024);
         }
-    }
-    const uint32_t nnrm = wave == 0 ? 1u : 0u;
-    if (wave == 0)
+#pragma unroll
+        for (uint32_t i = 0; i < (NCH + 3) / 4; i++) {
+            const uint32_t c = wl4 + 4 * i;
+            if (c < NCH) {  // uniform per wave
+                const uint32_t o = c * 1024 + lane * 16, r = o / QA_ROWB, within = o - r * QA_ROWB;
+                const uint32_t rr = j * R + r;  // row of the kv head's q | k | v rows
+                const uint8_t *src = rr < QR ? P.wq + (size_t)(h * QR + rr) * QA_ROWB
+                                   : rr < QR + FD_HD ? P.wk + (size_t)(h * FD_HD + rr - QR) * QA_ROWB
+                                                     : P.wv + (size_t)(h * FD_HD + rr - QR - FD_HD) * QA_ROWB;
+                dma16(src + within, lds0 + QA_W + c * 1024);
+            }
+        }
+    } else if (wave == 4) {
         dma16((const uint8_t *)(lane < 32 ? p.q_norm : p.k_norm) + (lane & 31) * 16, lds0 + QA_NRM);
+    }
 
-    // ---- chunk geometry (chunk j of 32), then its first two K/V sub-chunks
-    // and the RoPE row of the position
+    // ---- chunk geometry (chunk j of 32)
     const uint32_t seq = posv + 1;
     const uint32_t CT = ((seq + QA_PER - 1) / QA_PER + 15) / 16 * 16;
     const uint32_t nv = (seq + CT - 1) / CT;  // chunks holding tokens
@@ -180,13 +188,13 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     }
     const uint16_t *kbase = p.kc + (size_t)h * p.cache_tokens * FD_HD;
     const uint16_t *vbase = p.vc + (size_t)h * p.cache_tokens * FD_HD;
-    // sub-chunk s: 32 copies of 1 KB (4 token rows of K, then of V); rows
-    // past the chunk re-read its last row (masked). 16-byte piece q of LDS
-    // row rr holds the row's piece q ^ (rr % 16).
+    // sub-chunk s (B waves): 32 copies of 1 KB (4 token rows of K, then of
+    // V); rows past the chunk re-read its last row (masked). 16-byte piece q
+    // of LDS row rr holds the row's piece q ^ (rr % 16).
     auto issue_kv = [&](uint32_t s) __attribute__((always_inline)) {
 #pragma unroll
-        for (uint32_t i = 0; i < QA_KVW; i++) {
-            const uint32_t jj = wave + QA_AW * i, kv = jj >> 4;
+        for (uint32_t i = 0; i < 8; i++) {
+            const uint32_t jj = wl4 + 4 * i, kv = jj >> 4;
             const uint32_t rr = 4 * (jj & 15) + (lane >> 4);
             const uint32_t t = min(t0 + s * AR_TS + rr, t1 - 1);
             const uint16_t *row = (kv ? vbase : kbase) + (size_t)t * FD_HD;
@@ -194,14 +202,19 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         }
     };
     const uint32_t n01 = min(nsub, 2u);
-    for (uint32_t s = 0; s < n01; s++) issue_kv(s);
-    const uint32_t nrope = wave == QA_AW - 1 ? 1u : 0u;
-    if (wave == QA_AW - 1)
-        dma16((const uint8_t *)(p.rope_cs + (size_t)posv * FD_HD) + min(lane * 16, 496u), lds0 + QA_ROPE);
+    if (!wa) {
+        if (wave == 5)
+            dma16((const uint8_t *)(p.rope_cs + (size_t)posv * FD_HD) + min(lane * 16, 496u), lds0 + QA_ROPE);
+        if (P.kv_defer == 0)
+            for (uint32_t s = 0; s < n01; s++) issue_kv(s);
+    }
 
     // ---- attn_norm(x) as XQ limbs (the ring DMMV's staging, in place)
-    wait_vm_dyn(nw + nnrm + n01 * QA_KVW + nrope);
+    if (wa) wait_vm_dyn(nw);
     lds_bar();
+    ZH_TRACE_POINT(1);
+    if (!wa && P.kv_defer == 1)
+        for (uint32_t s = 0; s < n01; s++) issue_kv(s);
     float *yl = (float *)(lds + QA_YL), *red = yl + 32;
     uint32_t L[4][24];
     float xs[4], xz[4];
@@ -262,12 +275,15 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         }
         lds_bar();  // the image is read: the region takes K/V sub-chunk 2
     }
-    const uint32_t n2 = nsub > 2 ? 1u : 0u;
-    if (n2) issue_kv(2);
+    ZH_TRACE_POINT(2);
+    if (!wa && P.kv_defer < 2 && nsub > 2) issue_kv(2);
 
     // ---- the slice's rows (the ring DMMV's per-row arithmetic)
-    wait_vm_dyn(nnrm + n01 * QA_KVW + nrope + n2 * QA_KVW);
+    if (wa) wait_vm<0>();
     lds_bar();
+    if (!wa && P.kv_defer == 2)
+        for (uint32_t s = 0; s < nsub; s++) issue_kv(s);
+    ZH_TRACE_POINT(3);
 #pragma unroll
     for (uint32_t ps = 0; ps < NP; ps++) {
         const uint32_t r = ps * 16 + team;
@@ -314,6 +330,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         }
     }
     lds_bar();
+    ZH_TRACE_POINT(4);
     // ---- publish the rows (wave 0), then wait for the kv head's other slices
     if (wave == 0) {
         if (lane < R) {
@@ -326,7 +343,9 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         wait_vm<0>();  // the rows are in the L2 before the flag
         if (lane == 0) *(volatile uint32_t *)(fl_q + j) = E;
     }
+    ZH_TRACE_POINT(5);
     const bool ok_rows = qa_wait(fl_q, QA_PER, E, p.ctl, tid);
+    ZH_TRACE_POINT(6);
 
     // ---- the attention's inputs from the L2: the group's q, the new k | v
     uint8_t *sm = lds + QA_W;  // q [G][128] f32 (QC KB), k_new | v_new (1 KB), new K / V rows f16, q fragments
@@ -338,7 +357,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     }
     wait_vm<0>();  // ... and every K/V sub-chunk
     lds_bar();
-
+    ZH_TRACE_POINT(7);
     // ---- q as MFMA fragments (RMSNorm, RoPE, f16 hi + lo), shared through LDS
     const uint32_t sub = lane & 7, fg = lane & 15, fq = lane >> 4;
     const uint32_t gq = wave / 4, w4 = wave % 4;
@@ -392,6 +411,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
             ql[s8] = *(const half4 *)(frag + (s8 * 64 + lane) * 16 + 8);
         }
     }
+    ZH_TRACE_POINT(8);
     // ---- the new token's k (norm + RoPE) and v as f16 rows (the owner only)
     const bool owner = posv >= t0 && posv < t1;  // uniform
     if (owner && wave == 0) {
@@ -495,6 +515,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
             acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vf[n], acc[n], 0, 0, 0);
         }
     }
+    ZH_TRACE_POINT(9);
     // ---- the new row to the cache
     if (owner && tid < 32) {
         uint16_t *dst = (tid < 16 ? p.kc : p.vc) + ((size_t)h * p.cache_tokens + posv) * FD_HD + (tid & 15) * 8;
@@ -540,12 +561,17 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         __syncthreads();
         if (tid == 0) *(volatile uint32_t *)(fl_p + j) = E;  // ... before the flag
     }
+    ZH_TRACE_POINT(10);
     if (j >= (uint32_t)G) return;
     // ---- merger j: q head h G + j, once every chunk of the kv head published
     const bool ok = qa_wait(fl_p, nv, E, p.ctl, tid);
+    ZH_TRACE_POINT(11);
     if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
     attn_merge<1, 32, false>(p, h * G + j, nv, !(ok && ok_rows));
+    ZH_TRACE_POINT(12);
 }
+
+ZH_TRACE_DUMP_FN(zh_debug_trace_qa)
 
 // Whether the workgroups of a 256-workgroup grid (one per CU) land on XCDs
 // (blockIdx + s) % 8 for one s: the placement k_qkv_attn's (kv head, slice)
@@ -601,6 +627,7 @@ int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t 
     p.scale = scale; p.eps = eps; p.part = partials; p.n_chunks = QA_PER; p.counters = nullptr;
     p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh; p.nd = QA_PER; p.no_wait = 0; p.ident = 1; p.ctl = c->err_dev;
     P.wq = wq; P.wk = wk; P.wv = wv; P.x = x; P.norm_w = norm_w; P.flags = flags;
+    P.kv_defer = (uint32_t)zh_knob_int("ZH_QA_DEFER", 0);
     const uint32_t G = nh / QA_NXCD;
     if (!pos.dev || ((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wq & 15) || ((uintptr_t)wk & 15) ||
         ((uintptr_t)wv & 15))
