@@ -34,6 +34,8 @@ def _engine(ctx, cfg, fused=True):
 def test_fused_launch_is_used(ctx):
     eng = _engine(ctx, FUSED)
     assert "k_qkv_attn" in eng.group_kernels("qkv_attn")
+    # with the O projection: one launch for the three groups
+    assert "k_qkv_attn" in eng.group_kernels("qkv_attn_o") and ";" not in eng.group_kernels("qkv_attn_o")
     eng.set_fused_attn(False)
     names = eng.group_kernels("qkv_attn")
     assert "k_qkv_attn" not in names and "attn" in names

@@ -46,7 +46,7 @@ __global__ __launch_bounds__(LPB_T, ZH_LPB_MINB) void k_dmmv_q4k_lpb(LpbP p) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const uint32_t row = min(rr0 + r, seg_rows - 1);
-                const uint8_t *Wb = m ? p.segW2 : p.segW[sg];
+                const uint8_t *Wb = m ? p.segW2 : lpb_w(p, sg);
                 LpbQ4K::load(Wb + (size_t)row * p.row_bytes + (size_t)b * 144, raw[m][r]);  // inactive lanes read block 0
             }
     }
@@ -57,14 +57,14 @@ __global__ __launch_bounds__(LPB_T, ZH_LPB_MINB) void k_dmmv_q4k_lpb(LpbP p) {
         const uint32_t r0 = min(base + team * R, p.M - 1);
         uint32_t seg_rows, rr0, sg;
         lpb_geom(p, r0, seg_rows, rr0, sg);
-        float *yb = p.segY[sg];
+        float *yb = lpb_y(p, sg);
         if (base != base_first) {
 #pragma unroll
             for (int m = 0; m < NM; m++)
 #pragma unroll
                 for (int r = 0; r < R; r++) {
                     const uint32_t row = min(rr0 + r, seg_rows - 1);
-                    const uint8_t *Wb = m ? p.segW2 : p.segW[sg];
+                    const uint8_t *Wb = m ? p.segW2 : lpb_w(p, sg);
                     LpbQ4K::load(Wb + (size_t)row * p.row_bytes + (size_t)b * 144, raw[m][r]);  // inactive lanes read block 0
                 }
         }
@@ -140,6 +140,7 @@ __global__ __launch_bounds__(LPB_T, ZH_LPB_MINB) void k_dmmv_q4k_lpb(LpbP p) {
             float out = res;
             if (p.acc) out += yb[rr0 + idx];
             yb[rr0 + idx] = out;
+            if (p.ycopy) p.ycopy[rr0 + idx] = out;
         }
     }
 }
@@ -169,8 +170,8 @@ __global__ __launch_bounds__(LPB_T, ZH_LPB_MINB) void k_dmmv_q6k_lpb(LpbP p) {
         const uint32_t r0 = min(base + team * R, p.M - 1);
         uint32_t seg_rows, rr0, sg;
         lpb_geom(p, r0, seg_rows, rr0, sg);
-        const uint8_t *W = p.segW[sg];
-        float *yb = p.segY[sg];
+        const uint8_t *W = lpb_w(p, sg);
+        float *yb = lpb_y(p, sg);
         // per row: ql 64 B (17 dwords w/ realign), qh 32 B (9), sc 8 B + d (6 dwords cover 192+8h..210)
         uint32_t rq[R][17], rh[R][9], rs[R][6], sh[R];
 #pragma unroll
@@ -270,6 +271,7 @@ __global__ __launch_bounds__(LPB_T, ZH_LPB_MINB) void k_dmmv_q6k_lpb(LpbP p) {
             float out = res;
             if (p.acc) out += yb[rr0 + idx];
             yb[rr0 + idx] = out;
+            if (p.ycopy) p.ycopy[rr0 + idx] = out;
         }
     }
 }
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(LPB_T, TL >= 64 ? 2 : 3) void k_dmmv_q4k_tile(LpbP 
         }
         float res = active ? fmaf(h.d, accd, -h.dmin * accm) : 0.f;
         res = team_sum_dpp<TL>(res);
-        float *yb = p.segY[sg];
+        float *yb = lpb_y(p, sg);
         if (MODE == LPB_GATE_UP) {
             if (mat == 0 && tlane == 0) gate_res[rt] = res;
             __syncthreads();
@@ -398,6 +400,7 @@ __global__ __launch_bounds__(LPB_T, TL >= 64 ? 2 : 3) void k_dmmv_q4k_tile(LpbP 
             float out = res;
             if (p.acc) out += yb[rr0 + rt];
             yb[rr0 + rt] = out;
+            if (p.ycopy) p.ycopy[rr0 + rt] = out;
         }
         __syncthreads();  // the tile is rewritten by the next batch
     }
@@ -513,10 +516,12 @@ __global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
             const uint32_t s1 = __builtin_amdgcn_alignbyte(rs[2], rs[1], sh);
             const uint32_t s2 = __builtin_amdgcn_alignbyte(rs[3], rs[2], sh);
             const uint32_t s3 = __builtin_amdgcn_alignbyte(rs[4], rs[3], sh);
-            const uint32_t scw[4] = {s0, s1, s2, s3};
-            const int i0 = 8 * h + 2 * g, i1 = i0 + 1;
-            const int sc0 = (int)(int8_t)((scw[i0 >> 2] >> (8 * (i0 & 3))) & 0xFF);
-            const int sc1 = (int)(int8_t)((scw[i1 >> 2] >> (8 * (i1 & 3))) & 0xFF);
+            // scales 8h + 2g and 8h + 2g + 1: word 2h + g / 2, bytes 2 (g % 2)
+            // and 2 (g % 2) + 1 (a select on the per-lane h, g static: an
+            // indexed register array would become scratch memory)
+            const uint32_t sw = h ? (g < 2 ? s2 : s3) : (g < 2 ? s0 : s1);
+            const int sc0 = (int)(int8_t)((sw >> (16 * (g & 1))) & 0xFF);
+            const int sc1 = (int)(int8_t)((sw >> (16 * (g & 1) + 8)) & 0xFF);
             const float S0 = comb_f(D[0][0], D[0][1], D[0][2]);
             const float S1 = comb_f(D[1][0], D[1][1], D[1][2]);
             acc = fmaf((float)sc0, fmaf(xs, S0, z0), acc);
@@ -535,11 +540,12 @@ __global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
             for (int w = 0; w < TL / 64; w++) t += xred[(rt * TL) / 64 + w];
             res = t;
         }
-        float *yb = p.segY[sg];
+        float *yb = lpb_y(p, sg);
         if (tlane == 0 && (uint32_t)rt < nrows) {
             float out = res;
             if (p.acc) out += yb[rr0 + rt];
             yb[rr0 + rt] = out;
+            if (p.ycopy) p.ycopy[rr0 + rt] = out;
         }
         __syncthreads();  // the tile (and xred) are rewritten by the next batch
     }
@@ -670,8 +676,10 @@ bool zhk_lpb_supported(uint32_t qtype, uint32_t K) {
 
 int zhk_dmmv_lpb(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
                  float *const *y, const uint32_t *M, const float *x, const float *norm_w, float eps,
-                 float *normed_out, uint32_t K, uint32_t acc, const void *xq, uint8_t *xq_out, uint32_t *grp_cnt) {
-    if (!zhk_lpb_supported(qtype, K) || (mode == LPB_GATE_UP && qtype != ZH_Q4_K) || nseg < 1 || nseg > 3)
+                 float *normed_out, uint32_t K, uint32_t acc, const void *xq, uint8_t *xq_out, uint32_t *grp_cnt,
+                 float *ycopy) {
+    if (!zhk_lpb_supported(qtype, K) || (mode == LPB_GATE_UP && qtype != ZH_Q4_K) || nseg < 1 || nseg > 3 ||
+        (ycopy && (qtype != ZH_Q6_K || nseg != 1 || mode != LPB_PLAIN)))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "lpb: unsupported qtype/K/mode");
     LpbP p = {};
     p.x = x; p.norm_w = norm_w; p.eps = eps; p.normed_out = normed_out;
@@ -690,6 +698,7 @@ int zhk_dmmv_lpb(zh_ctx *c, uint32_t qtype, int mode, uint32_t nseg, const uint8
     p.M = end;
     p.xq_out = xq_out;
     p.grp_cnt = grp_cnt;
+    p.ycopy = ycopy;
     if (xq_out && (mode != LPB_GATE_UP || nseg != 1 || p.M % 32 || !grp_cnt))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "lpb: XQ output needs gate/up mode, one segment, M %% 32 == 0");
     {

@@ -73,6 +73,7 @@ struct zh_engine {
     bool persistent = false;  // zh_engine_set_persistent
     bool fused_qa = true;     // zh_engine_set_fused_attn: Q/K/V + attention in one launch where it applies
     uint32_t *qa_flags = nullptr;  // its XCD-local flag and epoch words (zero at creation)
+    float *xin = nullptr;          // with the O projection in that launch: copy of the residual stream at layer entry
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
@@ -332,7 +333,7 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->inv_freq, 4ull * hd / 2}, {(void **)&e->rope_cs, 8ull * c.max_ctx * (hd / 2)},
         {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)}, {(void **)&e->router_cnt, 4},
         {(void **)&e->step_ctl, zh_step_ctl_bytes()}, {(void **)&e->step_layers, sizeof(zh_step_layer) * c.n_layers},
-        {(void **)&e->qa_flags, 4ull * zhk_qkv_attn_flag_words()},
+        {(void **)&e->qa_flags, 4ull * zhk_qkv_attn_flag_words()}, {(void **)&e->xin, 4ull * H},
     };
     uint64_t aoff = 0;
     for (auto &a : acts) aoff = align256(aoff + a.bytes);
@@ -692,6 +693,29 @@ static bool step_args(zh_engine *e, zh_step_args &a) {
     return true;
 }
 
+// Whether a layer's Q/K/V and attention run as one launch (k_qkv_attn).
+static bool layer_qa(zh_engine *e, const Layer &y) {
+    const zh_model_config &m = e->c;
+    const uint32_t H = m.hidden, qd = m.n_heads * m.head_dim;
+    return e->fused_qa && e->pages_ident && !zh_knob("ZH_NO_LPB") && y.wq.type == ZH_Q4_K && y.wk.type == ZH_Q4_K &&
+           y.wv.type == ZH_Q4_K && zhk_lpb_supported(y.wo.type, qd) &&
+           zhk_qkv_attn_supported(e->ctx, H, m.n_heads, m.n_kv_heads, m.head_dim, m.max_ctx);
+}
+
+// Whether every layer's O projection also runs in that launch: then the
+// residual stream is kept twice at layer entry (the embedding and every down
+// projection write e->xin beside e->hidden), the launch reads its input from
+// e->xin and adds the O projection into e->hidden with device atomics.
+static bool step_qa_o(zh_engine *e) {
+    const zh_model_config &m = e->c;
+    if (m.n_experts || m.n_heads != 4 * m.n_kv_heads) return false;
+    for (const Layer &y : e->L)
+        if (!layer_qa(e, y) || y.wo.type != ZH_Q4_K || y.gate.type != ZH_Q4_K || y.up.type != ZH_Q4_K ||
+            y.down.type != ZH_Q6_K || !zhk_lpb_supported(ZH_Q6_K, m.ffn))
+            return false;
+    return true;
+}
+
 // Records the decode step: embedding, layers [l0, l1) (only the launch
 // groups in `mask`), then (whole steps only) the output head and the step
 // advance.
@@ -705,14 +729,18 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     zh_pos_src pos{0, e->st + ST_POS}, seq{1, e->st + ST_POS};
     const float scale = 1.0f / sqrtf((float)hd);
     const bool whole = mask == SK_ALL && l0 == 0 && l1 >= m.n_layers;
-    // embedToken (forward.zig:4255-4290), on the device.
-    if (whole) ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
     const bool lpb = !zh_knob("ZH_NO_LPB");
     // LDS-staged kernels with the norms, router top-k and expert combine fused
     const bool lds = !zh_knob("ZH_NO_LDS_DMMV");
     // the whole step's layers in one persistent launch when it takes the model
     zh_step_args sa;
     const bool persistent = whole && step_args(e, sa);
+    const bool qa_o = !persistent && step_qa_o(e);
+    // embedToken (forward.zig:4255-4290), on the device.
+    if (whole) {
+        ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
+        if (qa_o) ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, 1, H, e->xin, e->st + ST_TOKEN_IN, m.vocab));
+    }
     if (persistent) ERC(zhk_step_layers(c, sa));
     for (uint32_t l = persistent ? m.n_layers : l0; l < m.n_layers && l < l1; l++) {
         const Layer &y = e->L[l];
@@ -731,13 +759,14 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         float *qkv_y[3] = {e->q, e->k, e->v};
         const uint32_t qkv_m[3] = {qd, kvd, kvd};
         // Q/K/V and attention in one launch: 8 kv heads, one per XCD
-        const bool qa = (mask & SK_QKV) && (mask & SK_ATTN) && e->fused_qa && lpb_attn && e->pages_ident &&
-                        y.wq.type == ZH_Q4_K && y.wk.type == ZH_Q4_K && y.wv.type == ZH_Q4_K &&
-                        zhk_qkv_attn_supported(c, H, m.n_heads, m.n_kv_heads, hd, m.max_ctx);
+        // (and the O projection, qa_o, when the launch group includes it)
+        const bool qa = (mask & SK_QKV) && (mask & SK_ATTN) && lpb_attn && layer_qa(e, y);
+        const bool with_o = qa && qa_o && (mask & SK_O);
         if (qa) {
-            ERC(zhk_qkv_attn(c, W(y.wq), W(y.wk), W(y.wv), e->hidden, Wf(y.attn_norm), e->q, e->k, e->v, Wf(y.q_norm),
-                             Wf(y.k_norm), e->rope_cs, y.kc, y.vc, m.max_ctx, e->attn, e->xq_q, m.n_heads, pos, scale,
-                             m.eps, e->fd_part, e->qa_flags));
+            ERC(zhk_qkv_attn(c, W(y.wq), W(y.wk), W(y.wv), qa_o ? e->xin : e->hidden, Wf(y.attn_norm), e->q, e->k,
+                             e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc, m.max_ctx, e->attn, e->xq_q,
+                             m.n_heads, pos, scale, m.eps, e->fd_part, e->qa_flags, with_o ? W(y.wo) : nullptr,
+                             with_o ? e->hidden : nullptr));
         } else if (!(mask & SK_QKV)) {
         } else if (lpb_attn) {
             // attn_norm fused into the Q/K/V mat-vec (every workgroup normalises x)
@@ -772,7 +801,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             ERC(zhk_attn_decode_fused(c, e->q, e->k, e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc,
                                   e->pages, e->n_pages, m.max_ctx, e->attn, e->xq_q, m.n_heads, m.n_kv_heads, pos,
                                   m.max_ctx, scale, m.eps, e->fd_part, e->pages_ident));
-        if (!(mask & SK_O)) {
+        if (!(mask & SK_O) || with_o) {
         } else if (lpb_attn) {
             // the merge kernel already emitted the attention output as XQ
             const uint8_t *wo = W(y.wo);
@@ -800,7 +829,8 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             const uint32_t mh = H;
             if (mask & SK_FFN_OUT)
                 ERC(zhk_dmmv_lpb(c, y.down.type, 0, 1, &wd, nullptr, &yd, &mh, swiglu_xq ? nullptr : e->s,
-                                 nullptr, 0.f, nullptr, m.ffn, 1, swiglu_xq ? e->xq_f : nullptr));
+                                 nullptr, 0.f, nullptr, m.ffn, 1, swiglu_xq ? e->xq_f : nullptr, nullptr, nullptr,
+                                 qa_o ? e->xin : nullptr));
             continue;
         }
         if (lds_moe) {
@@ -1377,6 +1407,8 @@ extern "C" uint64_t zh_engine_group_bytes(zh_engine *e, uint32_t group, uint32_t
     switch (group) {
     case SK_QKV | SK_ATTN:
         return zh_engine_group_bytes(e, SK_QKV, Lctx) + zh_engine_group_bytes(e, SK_ATTN, Lctx) - (qd + 2 * kvd) * 8;
+    case SK_QKV | SK_ATTN | SK_O:  // the attention output stays on chip; O adds into x
+        return zh_engine_group_bytes(e, SK_QKV | SK_ATTN, Lctx) + y.wo.bytes + H * 4 - xqb(qd);
     case SK_QKV: return y.wq.bytes + y.wk.bytes + y.wv.bytes + 2 * H * 4 + (qd + 2 * kvd) * 4;
     case SK_ATTN:
         return 2 * kvd * 2 * Lctx + (qd + 2 * kvd) * 4 + 2 * hd * 4 + hd * 4 + 2 * kvd * 2 + qd * 4 + xqb(qd);

@@ -189,7 +189,7 @@ bool zhk_lpb_supported(uint32_t qtype, uint32_t K);
 int zhk_dmmv_lpb(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
                  float *const *y, const uint32_t *M, const float *x, const float *norm_w, float eps,
                  float *normed_out, uint32_t K, uint32_t acc, const void *xq = nullptr,
-                 uint8_t *xq_out = nullptr, uint32_t *grp_cnt = nullptr);
+                 uint8_t *xq_out = nullptr, uint32_t *grp_cnt = nullptr, float *ycopy = nullptr);
 // Streaming Q4_K DMMV (zh_dmmv_ring.hip), same arguments as zhk_dmmv_lpb;
 // returns -1 (nothing launched) for shapes it does not take.
 int zhk_dmmv_ring(zh_ctx *ctx, uint32_t qtype, int mode, uint32_t nseg, const uint8_t *const *W, const uint8_t *W2,
@@ -234,7 +234,11 @@ uint32_t zhk_qkv_attn_flag_words();  // zeroed u32 words the caller keeps per en
 int zhk_qkv_attn(zh_ctx *ctx, const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x,
                  const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
-                 uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags);
+                 uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
+                 const uint8_t *wo = nullptr, float *x_acc = nullptr);
+// wo != nullptr (4 q heads per kv head): also the O projection, added into
+// x_acc with device atomics; x must then be a copy of x_acc (x_acc changes
+// during the launch).
 // The geometry the kernel is built for (hidden 2048 or 4096 = n_heads x 128,
 // FFN 12288 or 14336, 4 q heads per kv head, enough CUs); the caller checks
 // the layer formats (Q4_K Q/K/V/O/gate/up, Q6_K down, 16-byte aligned) and

@@ -194,9 +194,16 @@ struct LpbP {
     uint32_t seg_end[3];
     uint8_t *xq_out;       // gate/up mode, optional: the SwiGLU output also as XQ (M % 32 == 0)
     uint32_t *grp_cnt;     // with xq_out: one zeroed counter per 32-row group
+    float *ycopy;          // optional (one segment, Q6_K): every output row also stored here
 };
 
 enum { LPB_PLAIN = 0, LPB_GATE_UP = 1 };
+
+// Segment sg's matrix and output by selects: an index into the kernel
+// argument's arrays with a per-batch value makes the compiler copy the
+// arrays to scratch memory.
+ZH_DEV const uint8_t *lpb_w(const LpbP &p, uint32_t sg) { return sg == 0 ? p.segW[0] : sg == 1 ? p.segW[1] : p.segW[2]; }
+ZH_DEV float *lpb_y(const LpbP &p, uint32_t sg) { return sg == 0 ? p.segY[0] : sg == 1 ? p.segY[1] : p.segY[2]; }
 constexpr uint32_t LPB_XQ_MAX_GROUPS = 16;  // 32-row groups one gate/up workgroup may publish
 
 // Segment lookup for the batch starting at stacked row r0 (batches never
@@ -365,7 +372,7 @@ ZH_DEV void tile_fetch(const LpbP &p, uint32_t bi, uint32_t row_bytes, u32x4 (&s
     const uint32_t n16 = min((uint32_t)RPB, seg_rows - rr0) * row_bytes / 16;
 #pragma unroll
     for (int m = 0; m < NM; m++) {
-        const u32x4 *src = (const u32x4 *)((m ? p.segW2 : p.segW[sg]) + (size_t)rr0 * row_bytes);
+        const u32x4 *src = (const u32x4 *)((m ? p.segW2 : lpb_w(p, sg)) + (size_t)rr0 * row_bytes);
 #pragma unroll
         for (int j = 0; j < NCH; j++) {
             // unconditional (clamped) loads keep the outstanding-load count

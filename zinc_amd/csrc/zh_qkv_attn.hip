@@ -69,9 +69,14 @@ static_assert(QA_NB * 2 * RG_SEG + QA_NB * 8 * 12 <= AR_SLOT, "XQ image fits the
 }  // namespace
 
 // Flag words (zero when the engine is created): [0, 256) Q/K/V rows
-// published, [256, 512) partials published (head h at h * 32: one 128-byte
-// line per XCD), [512, 520) epochs.
-constexpr uint32_t QA_FLAG_WORDS = 2 * QA_NXCD * QA_PER + QA_NXCD;
+// published, [256, 512) partials published, [512, 768) merged heads
+// published (head h at h * 32: one 128-byte line per XCD), [768, 776)
+// epochs.
+constexpr uint32_t QA_FLAG_WORDS = 3 * QA_NXCD * QA_PER + QA_NXCD;
+constexpr uint32_t QA_OROWS = 4096 / QA_PER;  // O-projection rows per workgroup (hidden 4096)
+constexpr uint32_t QA_OROWB = 2 * 144;        // a row's two super-blocks of the XCD's 512 columns
+constexpr uint32_t QA_OW = QA_W + 16384;      // their LDS copy (the attention uses the region's first 12.3 KB)
+static_assert(QA_OW + QA_OROWS * QA_OROWB <= QA_X, "O rows fit the weight region");
 
 struct QaP {
     AttnP a;                      // q / k_new / v_new: the projection outputs (written here)
@@ -79,6 +84,12 @@ struct QaP {
     const float *x, *norm_w;      // residual stream, attn_norm weight
     uint32_t *flags;              // QA_FLAG_WORDS
     uint32_t kv_defer;            // K/V copies issued at the start (0), after x landed (1), after the rows landed (2)
+    // WITH_O: the O projection of the XCD's G heads (Q4_K W_o [4096][4096],
+    // super-blocks 2h and 2h + 1 of every row) added to x_acc with device
+    // atomics; x (the Q/K/V input) is then a copy of x_acc taken before the
+    // launch, since x_acc changes during it.
+    const uint8_t *wo;
+    float *x_acc;
 };
 
 ZH_DEV uint32_t xcc_id() {
@@ -122,7 +133,7 @@ ZH_DEV bool qa_wait(const uint32_t *f, uint32_t n, uint32_t E, uint32_t *ctl, ui
     return s_ok != 0;
 }
 
-template <int G>
+template <int G, bool WITH_O>
 __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t R = 4 * (G + 2);          // weight rows per workgroup
@@ -131,6 +142,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     constexpr uint32_t QC = ar_qc<G>();           // 1 KB copies of the group's q
     constexpr uint32_t QR = G * FD_HD;            // q rows of a kv head
     static_assert(R * QA_ROWB % 1024 == 0 && R <= QA_MAXR && R % 4 == 0, "row slice");
+    static_assert(!WITH_O || G == 4, "the O phase takes 4 heads = 2 super-blocks of columns per XCD");
     const AttnP &p = P.a;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -139,7 +151,8 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     const uint32_t h = min(xcc_id(), QA_NXCD - 1), j = blockIdx.x / QA_NXCD;
     const uint32_t lds0 = lds_addr(lds);
     uint32_t *fl_q = P.flags + h * QA_PER, *fl_p = P.flags + QA_NXCD * QA_PER + h * QA_PER;
-    uint32_t *ep = P.flags + 2 * QA_NXCD * QA_PER + h;
+    uint32_t *fl_m = P.flags + 2 * QA_NXCD * QA_PER + h * QA_PER;
+    uint32_t *ep = P.flags + 3 * QA_NXCD * QA_PER + h;
     // position and epoch through the scalar cache (no vector-memory count)
     const uint32_t posv = *(const __attribute__((address_space(4))) uint32_t *)p.pos.dev + p.pos.value;
     const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
@@ -358,6 +371,16 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     wait_vm<0>();  // ... and every K/V sub-chunk
     lds_bar();
     ZH_TRACE_POINT(7);
+    // ---- WITH_O: this workgroup's O rows (128 rows x the XCD's two
+    // super-blocks, 36 KB) into the weight region's free part, by waves 4-7
+    // while the attention runs (HBM is idle from here on)
+    if (WITH_O && !wa) {
+        for (uint32_t c = wl4; c < QA_OROWS * QA_OROWB / 1024; c += 4) {
+            const uint32_t pc = c * 64 + lane, row = pc / 18, within = pc - row * 18;  // 16-byte piece
+            dma16(P.wo + (size_t)(j * QA_OROWS + row) * (16 * 144) + 2 * h * 144 + within * 16,
+                  lds0 + QA_OW + c * 1024);
+        }
+    }
     // ---- q as MFMA fragments (RMSNorm, RoPE, f16 hi + lo), shared through LDS
     const uint32_t sub = lane & 7, fg = lane & 15, fq = lane >> 4;
     const uint32_t gq = wave / 4, w4 = wave % 4;
@@ -562,13 +585,99 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         if (tid == 0) *(volatile uint32_t *)(fl_p + j) = E;  // ... before the flag
     }
     ZH_TRACE_POINT(10);
-    if (j >= (uint32_t)G) return;
-    // ---- merger j: q head h G + j, once every chunk of the kv head published
-    const bool ok = qa_wait(fl_p, nv, E, p.ctl, tid);
-    ZH_TRACE_POINT(11);
-    if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
-    attn_merge<1, 32, false>(p, h * G + j, nv, !(ok && ok_rows));
-    ZH_TRACE_POINT(12);
+    if (!WITH_O && j >= (uint32_t)G) return;
+    if (j < (uint32_t)G) {
+        // ---- merger j: q head h G + j, once every chunk of the kv head published
+        const bool ok = qa_wait(fl_p, nv, E, p.ctl, tid);
+        ZH_TRACE_POINT(11);
+        if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
+        attn_merge<1, 32, false>(p, h * G + j, nv, !(ok && ok_rows));
+        ZH_TRACE_POINT(12);
+        if (WITH_O) {
+            wait_vm<0>();  // the merged head's XQ blocks are in the L2 ...
+            __syncthreads();
+            if (tid == 0) *(volatile uint32_t *)(fl_m + j) = E;  // ... before the flag
+        }
+    }
+    if (!WITH_O) return;
+    // ---- the O projection of the XCD's heads: rows 128 j .. 128 j + 127,
+    // columns 512 h .. 512 h + 511 (the XQ blocks 16 h .. 16 h + 15 of the
+    // merged output), partial sums added to x_acc
+    const bool ok_m = qa_wait(fl_m, G, E, p.ctl, tid);
+    {
+        const uint32_t nblk = p.nq * FD_HD / 32, b0 = h * G * 4;  // 4 G blocks (G = 4: 16)
+        const XQView v = xq_view(p.xq, nblk);
+        // limbs (4 G x 96 B), scales, sums -> LDS (the x region: K/V sub-chunk 2 is done)
+        if (wave < 3) {  // lanes write LDS at base + 16 lane: limbs (2 copies), then xs | xsum
+            const uint8_t *lb = (const uint8_t *)v.limb + b0 * 96;
+            const uint8_t *src = wave < 2 ? lb + min(wave * 1024 + lane * 16, 4u * G * 96 - 16)
+                               : lane < G ? (const uint8_t *)(v.xs + b0) + lane * 16
+                                          : (const uint8_t *)(v.xsum + 2 * b0) + min(lane - G, 2u * G - 1) * 16;
+            dma16_dev(src, lds0 + QA_X + wave * 1024);
+        }
+        wait_vm<0>();  // (also the O rows' copies)
+        lds_bar();
+    }
+    const uint8_t *xlimb = lds + QA_X;
+    const float *oxs = (const float *)(lds + QA_X + 2048), *oxz = oxs + 4 * G;
+    {
+        // lane: row r = tid / 4 of the 128, half super-block q = tid % 4 of the
+        // XCD's 4 G half-blocks (G = 4; fewer heads leave lanes idle)
+        const uint32_t q = tid & 3, r = tid >> 2;
+        const bool act = q < (uint32_t)G;  // 2 G / 2 half-blocks
+        const uint32_t qq = act ? q : 0;
+        uint32_t Lo[4][24];
+        float oxs4[4], oxz4[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t jb = 4 * qq + k;
+            lds_load_limbs(Lo[k], xlimb + jb * 96);
+            oxs4[k] = oxs[jb];
+            oxz4[k] = oxz[2 * jb] + oxz[2 * jb + 1];
+        }
+        const uint8_t *blk = lds + QA_OW + r * QA_OROWB + (qq >> 1) * 144;
+        const uint32_t hh = qq & 1;
+        uint32_t hd[4], qs[16];
+        {
+            const u32x4 v = *(const u32x4 *)blk;
+            hd[0] = v.x; hd[1] = v.y; hd[2] = v.z; hd[3] = v.w;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const u32x4 w = *(const u32x4 *)(blk + 16 + 64 * hh + 16 * i);
+                qs[4 * i] = w.x; qs[4 * i + 1] = w.y; qs[4 * i + 2] = w.z; qs[4 * i + 3] = w.w;
+            }
+        }
+        const LpbQ4K::Hdr hdr = LpbQ4K::header(hd);
+        const uint32_t scw = hh ? hdr.scB : hdr.scA, mw = hh ? hdr.mB : hdr.mA;
+        float accd = 0.f, accm = 0.f;
+#pragma unroll
+        for (int pl = 0; pl < 2; pl++) {
+            int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t w = qs[8 * pl + i];
+                const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                for (int k = 0; k < 3; k++) {
+                    D[0][k] = sdot4(lo, Lo[2 * pl][k * 8 + i], D[0][k]);
+                    D[1][k] = sdot4(hi, Lo[2 * pl + 1][k * 8 + i], D[1][k]);
+                }
+            }
+            const float sc0 = ubyte_f(scw, 2 * pl), sc1 = ubyte_f(scw, 2 * pl + 1);
+            const float m0 = ubyte_f(mw, 2 * pl), m1 = ubyte_f(mw, 2 * pl + 1);
+            const float S0 = (float)comb_i(D[0][0], D[0][1], D[0][2]);
+            const float S1 = (float)comb_i(D[1][0], D[1][1], D[1][2]);
+            accd = fmaf(sc0 * oxs4[2 * pl], S0, accd);
+            accd = fmaf(sc1 * oxs4[2 * pl + 1], S1, accd);
+            accm = fmaf(m0, oxz4[2 * pl], accm);
+            accm = fmaf(m1, oxz4[2 * pl + 1], accm);
+        }
+        float res = act ? fmaf(hdr.d, accd, -hdr.dmin * accm) : 0.f;
+        res = team_sum_dpp<4>(res);
+        if (!ok_m) res = __builtin_nanf("");
+        if (q == 0) __hip_atomic_fetch_add(P.x_acc + j * QA_OROWS + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ZH_TRACE_POINT(13);
 }
 
 ZH_TRACE_DUMP_FN(zh_debug_trace_qa)
@@ -619,7 +728,8 @@ bool zhk_qkv_attn_supported(zh_ctx *c, uint32_t hidden, uint32_t nh, uint32_t nk
 int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x,
                  const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
-                 uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags) {
+                 uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
+                 const uint8_t *wo, float *x_acc) {
     QaP P = {};
     AttnP &p = P.a;
     p.q = q; p.k_new = k; p.v_new = v; p.q_norm = qw; p.k_norm = kw; p.rope_cs = rope_cs;
@@ -627,26 +737,29 @@ int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t 
     p.scale = scale; p.eps = eps; p.part = partials; p.n_chunks = QA_PER; p.counters = nullptr;
     p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh; p.nd = QA_PER; p.no_wait = 0; p.ident = 1; p.ctl = c->err_dev;
     P.wq = wq; P.wk = wk; P.wv = wv; P.x = x; P.norm_w = norm_w; P.flags = flags;
+    P.wo = wo; P.x_acc = x_acc;
     P.kv_defer = (uint32_t)zh_knob_int("ZH_QA_DEFER", 0);
     const uint32_t G = nh / QA_NXCD;
-    if (!pos.dev || ((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wq & 15) || ((uintptr_t)wk & 15) ||
+    if ((wo && (!x_acc || ((uintptr_t)wo & 15))) || !pos.dev || ((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wq & 15) || ((uintptr_t)wk & 15) ||
         ((uintptr_t)wv & 15))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: device position and 16-byte aligned operands");
-#define QA_L(GG)                                                                                                 \
+#define QA_L(GG, WO)                                                                                             \
     {                                                                                                            \
         static bool attr = false;                                                                                \
         if (!attr) {                                                                                             \
-            ZH_HIP(c, hipFuncSetAttribute((const void *)k_qkv_attn<GG>, hipFuncAttributeMaxDynamicSharedMemorySize, \
-                                          (int)QA_LDS));                                                         \
+            ZH_HIP(c, hipFuncSetAttribute((const void *)k_qkv_attn<GG, WO>,                                      \
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)QA_LDS));             \
             attr = true;                                                                                         \
         }                                                                                                        \
-        hipLaunchKernelGGL(k_qkv_attn<GG>, dim3(QA_NXCD * QA_PER), dim3(QA_T), QA_LDS, c->stream, P);           \
+        hipLaunchKernelGGL((k_qkv_attn<GG, WO>), dim3(QA_NXCD * QA_PER), dim3(QA_T), QA_LDS, c->stream, P);      \
         break;                                                                                                   \
     }
-    switch (G) {
-    case 1: QA_L(1)
-    case 2: QA_L(2)
-    case 4: QA_L(4)
+    if (wo && G != 4) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: O phase needs 4 q heads per kv head");
+    switch (G + (wo ? 100 : 0)) {
+    case 1: QA_L(1, false)
+    case 2: QA_L(2, false)
+    case 4: QA_L(4, false)
+    case 104: QA_L(4, true)
     default: return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: GQA group %u", G);
     }
 #undef QA_L

@@ -186,7 +186,7 @@ class InferenceEngine:
         return lib().zh_engine_bytes_per_token(self.h, L)
 
     # per-layer launch groups of the decode step (zinc_hip.h ZH_GROUP_*)
-    GROUPS = {"qkv": 1, "attn": 2, "qkv_attn": 3, "o": 4, "ffn_in": 8, "ffn_out": 16, "head": 32}
+    GROUPS = {"qkv": 1, "attn": 2, "qkv_attn": 3, "qkv_attn_o": 7, "o": 4, "ffn_in": 8, "ffn_out": 16, "head": 32}
 
     def time_kernel(self, group, iters=200):
         """Average us per launch of one launch group, replayed with the
