@@ -75,7 +75,8 @@ def standalone():
 
 QA_POINTS = ["start", "x landed", "XQ limbs in registers", "weight rows landed", "rows computed",
              "rows published", "rows of the head seen", "q, k, v, K/V landed", "q fragments", "scores and P V done",
-             "partials published", "merger: chunks seen", "merger: output"]
+             "partials published", "merger: chunks seen", "merger: output", "O rows added",
+             "merge: start", "merge: statistics done"]
 
 
 def qkv_attn():
@@ -92,12 +93,13 @@ def qkv_attn():
     n = 8192 * 16
     a = np.zeros(n, np.uint64)
     L.zh_debug_trace_qa(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
-    us = eng.time_kernel("qkv_attn", 36)
+    grp = "qkv_attn_o" if ";" not in eng.group_kernels("qkv_attn_o") else "qkv_attn"
+    us = eng.time_kernel(grp, 36)
     ctx.sync()
     L.zh_debug_trace_qa(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
     t = a.reshape(8192, 16)[:256].astype(np.int64)
     base = t[:, 0].min()
-    print(f"k_qkv_attn ({eng.group_kernels('qkv_attn')}): {us:.2f} us per launch (events, debug build); "
+    print(f"{grp} ({eng.group_kernels(grp)}): {us:.2f} us per launch (events, debug build); "
           "points of the last launch, us from the first workgroup's start / from each workgroup's start:")
     for s, nm in enumerate(QA_POINTS):
         m = t[:, s] > 0
@@ -113,10 +115,15 @@ def qkv_attn():
 RING_POINTS = ["start", "activation landed", "XQ limbs in registers", "ring done", "outputs stored"]
 
 
-def ring(group):
-    """Per-workgroup timeline of a ring DMMV launch group (zh_ring_q4k.h)."""
+TILE_POINTS = ["start", "activation staged", "batch 0 in LDS", "batch 1", "batch 2", "batch 3", "batch 4+", "end"]
+
+
+def ring(group, dump="zh_debug_trace_ring", points=None):
+    """Per-workgroup timeline of a ring DMMV launch group (zh_ring_q4k.h) or,
+    with dump="zh_debug_trace_lpb", of a tile kernel (zh_dmmv_lpb.hip)."""
+    points = points or RING_POINTS
     L = hip.lib()
-    L.zh_debug_trace_ring.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
+    getattr(L, dump).argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
     ctx = hip.Context(0)
     cfg = dict(DENSE_8B)
     cfg["max_ctx"] = 4096 + 64
@@ -126,15 +133,15 @@ def ring(group):
     ctx.sync()
     n = 8192 * 16
     a = np.zeros(n, np.uint64)
-    L.zh_debug_trace_ring(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+    getattr(L, dump)(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
     us = eng.time_kernel(group, 36)
     ctx.sync()
-    L.zh_debug_trace_ring(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
-    t = a.reshape(8192, 16)[:256].astype(np.int64)
+    getattr(L, dump)(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+    t = a.reshape(8192, 16)[:512].astype(np.int64)
     base = t[:, 0].min()
     print(f"{group} ({eng.group_kernels(group)}): {us:.2f} us per launch (events, debug build); "
           "points of the last launch, us from the first workgroup's start / from each workgroup's start:")
-    for s, nm in enumerate(RING_POINTS):
+    for s, nm in enumerate(points):
         m = t[:, s] > 0
         if not m.any():
             continue
@@ -154,6 +161,8 @@ def main():
         return qkv_attn()
     if "--ring" in sys.argv[1:]:
         return ring(sys.argv[sys.argv.index("--ring") + 1])
+    if "--tile" in sys.argv[1:]:
+        return ring(sys.argv[sys.argv.index("--tile") + 1], "zh_debug_trace_lpb", TILE_POINTS)
     L = hip.lib()
     L.zh_debug_trace_step.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
     ctx = hip.Context(0)

@@ -129,8 +129,13 @@ ZH_DEV const uint16_t *kv_row(const uint16_t *h, size_t pa, size_t pb, size_t pc
 // reduction). NBAT chunks per round of O loads (every load is issued, with
 // clamped addresses, so the wait counts stay static). Reads partials published at device scope; `poison` (a wait that
 // timed out) turns the outputs into NaN.
-template <int GM, int NBAT, bool COH = false>
-ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
+// LOCAL: every partial was written by a workgroup on this XCD (plain stores,
+// held in the XCD's L2) and this workgroup has not read them before in this
+// launch (its L1 holds no copy): plain loads, which hit the L2.
+template <int GM, int NBAT, bool COH = false, bool LOCAL = false>
+ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison, float *lds_out = nullptr) {
+    auto ld1 = [](const float *q) { return LOCAL ? *q : ld_dev(q); };
+    auto ld2 = [](const float *q) { return LOCAL ? *(const uint64_t *)q : ld_dev64(q); };
     // any workgroup size of at least AD_T threads (every thread calls it)
     const uint32_t tid = COH ? phase_tid() : threadIdx.x, wave = tid >> 6, lane = tid & 63, nthr = blockDim.x;
     TRACE_OPS(11);
@@ -155,11 +160,11 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
         for (int u = 0; u < NBAT; u++) {
             const float *pc = pt + (size_t)min(cb + u, nv - 1) * (FD_HD + 2) + d0;
             if (OPT == 1) {
-                v[u][0] = ld_dev(pc);
+                v[u][0] = ld1(pc);
             } else {
 #pragma unroll
                 for (int w = 0; w < OPT / 2; w++) {
-                    const uint64_t x = ld_dev64(pc + 2 * w);
+                    const uint64_t x = ld2(pc + 2 * w);
                     v[u][2 * w] = __uint_as_float((uint32_t)x);
                     v[u][2 * w + 1] = __uint_as_float((uint32_t)(x >> 32));
                 }
@@ -173,7 +178,7 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
         const float *pp = p.part + (size_t)(h0 + g) * p.n_chunks * (FD_HD + 2);
         float m = -INFINITY, l = 0.f;
         for (uint32_t c = lane; c < nv; c += 64) {
-            const uint64_t ml = ld_dev64(pp + (size_t)c * (FD_HD + 2) + FD_HD);
+            const uint64_t ml = ld2(pp + (size_t)c * (FD_HD + 2) + FD_HD);
             const float mc = __uint_as_float((uint32_t)ml), lc = __uint_as_float((uint32_t)(ml >> 32));
             if (c < MB) sm[g][c] = mc;
             const float mn = fmaxf(m, mc);
@@ -213,7 +218,7 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
 #pragma unroll
             for (int u = 0; u < NBAT; u++) {
                 const uint32_t c = cb + u;
-                const float mc = c < MB ? sm[g_t][c < MB ? c : 0] : ld_dev(pt + (size_t)min(c, nv - 1) * (FD_HD + 2) + FD_HD);
+                const float mc = c < MB ? sm[g_t][c < MB ? c : 0] : ld1(pt + (size_t)min(c, nv - 1) * (FD_HD + 2) + FD_HD);
                 const float wgt = c < nv ? expf(mc - Mt) : 0.f;
 #pragma unroll
                 for (int k = 0; k < OPT; k++) O[k] = fmaf(v[u][k], wgt, O[k]);
@@ -226,6 +231,7 @@ ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison) {
         for (int k = 0; k < OPT; k++) {
             const float r = poison ? __builtin_nanf("") : hL[g_t] > 0.f ? O[k] / hL[g_t] : 0.f;
             ob[tid * OPT + k] = r;
+            if (lds_out) lds_out[tid * OPT + k] = r;  // (the caller's LDS copy of heads h0 ..)
             if (p.out) {
                 if (COH) st_dev(p.out + (size_t)h0 * FD_HD + tid * OPT + k, r);
                 else p.out[(size_t)h0 * FD_HD + tid * OPT + k] = r;

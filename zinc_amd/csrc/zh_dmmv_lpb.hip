@@ -548,7 +548,7 @@ __global__ __launch_bounds__(LPB_T, 2) void k_dmmv_q6k_tile(LpbP p) {
             if (p.ycopy) p.ycopy[rr0 + rt] = out;
         }
         __syncthreads();  // the tile (and xred) are rewritten by the next batch
-    }
+        }
     TRACE(7);
 }
 

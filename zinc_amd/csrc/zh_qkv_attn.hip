@@ -44,7 +44,7 @@
 // sub-chunks are all requested at the start, so the K/V stream overlaps the
 // projection and the barrier. Contexts up to 32 x 192 tokens (three 64-token
 // sub-chunks per chunk); the engine uses the two-kernel path beyond.
-#define TRACE_OPS(slot) do { } while (0)  // the shared bodies' points stay off: this file numbers its own
+#define TRACE_OPS(slot) ZH_TRACE_POINT((slot) == 11 ? 14 : (slot) == 13 ? 15 : 99)  // merge start, merge stats done
 #include "zh_attn_common.h"
 #include "zh_lpb_common.h"
 
@@ -69,10 +69,9 @@ static_assert(QA_NB * 2 * RG_SEG + QA_NB * 8 * 12 <= AR_SLOT, "XQ image fits the
 }  // namespace
 
 // Flag words (zero when the engine is created): [0, 256) Q/K/V rows
-// published, [256, 512) partials published, [512, 768) merged heads
-// published (head h at h * 32: one 128-byte line per XCD), [768, 776)
-// epochs.
-constexpr uint32_t QA_FLAG_WORDS = 3 * QA_NXCD * QA_PER + QA_NXCD;
+// published, [256, 512) partials published (head h at h * 32: one 128-byte
+// line per XCD), [512, 520) epochs.
+constexpr uint32_t QA_FLAG_WORDS = 2 * QA_NXCD * QA_PER + QA_NXCD;
 constexpr uint32_t QA_OROWS = 4096 / QA_PER;  // O-projection rows per workgroup (hidden 4096)
 constexpr uint32_t QA_OROWB = 2 * 144;        // a row's two super-blocks of the XCD's 512 columns
 constexpr uint32_t QA_OW = QA_W + 16384;      // their LDS copy (the attention uses the region's first 12.3 KB)
@@ -151,8 +150,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     const uint32_t h = min(xcc_id(), QA_NXCD - 1), j = blockIdx.x / QA_NXCD;
     const uint32_t lds0 = lds_addr(lds);
     uint32_t *fl_q = P.flags + h * QA_PER, *fl_p = P.flags + QA_NXCD * QA_PER + h * QA_PER;
-    uint32_t *fl_m = P.flags + 2 * QA_NXCD * QA_PER + h * QA_PER;
-    uint32_t *ep = P.flags + 3 * QA_NXCD * QA_PER + h;
+    uint32_t *ep = P.flags + 2 * QA_NXCD * QA_PER + h;
     // position and epoch through the scalar cache (no vector-memory count)
     const uint32_t posv = *(const __attribute__((address_space(4))) uint32_t *)p.pos.dev + p.pos.value;
     const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
@@ -585,41 +583,40 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         if (tid == 0) *(volatile uint32_t *)(fl_p + j) = E;  // ... before the flag
     }
     ZH_TRACE_POINT(10);
-    if (!WITH_O && j >= (uint32_t)G) return;
-    if (j < (uint32_t)G) {
+    if (!WITH_O) {
+        if (j >= (uint32_t)G) return;
         // ---- merger j: q head h G + j, once every chunk of the kv head published
         const bool ok = qa_wait(fl_p, nv, E, p.ctl, tid);
         ZH_TRACE_POINT(11);
         if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
-        attn_merge<1, 32, false>(p, h * G + j, nv, !(ok && ok_rows));
+        attn_merge<1, 32, false, true>(p, h * G + j, nv, !(ok && ok_rows));
         ZH_TRACE_POINT(12);
-        if (WITH_O) {
-            wait_vm<0>();  // the merged head's XQ blocks are in the L2 ...
-            __syncthreads();
-            if (tid == 0) *(volatile uint32_t *)(fl_m + j) = E;  // ... before the flag
-        }
+        return;
     }
-    if (!WITH_O) return;
-    // ---- the O projection of the XCD's heads: rows 128 j .. 128 j + 127,
-    // columns 512 h .. 512 h + 511 (the XQ blocks 16 h .. 16 h + 15 of the
-    // merged output), partial sums added to x_acc
-    const bool ok_m = qa_wait(fl_m, G, E, p.ctl, tid);
+    // ---- WITH_O: every workgroup of the XCD merges the XCD's G heads itself
+    // (their partials are in this XCD's L2) into LDS, as the XQ image of
+    // the O projection's 4 G blocks of 32 (no second publication round)
+    const bool ok = qa_wait(fl_p, nv, E, p.ctl, tid);
+    ZH_TRACE_POINT(11);
+    if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
+    float *mo = (float *)(lds + QA_X + 4096);  // merged heads [G][128]
     {
-        const uint32_t nblk = p.nq * FD_HD / 32, b0 = h * G * 4;  // 4 G blocks (G = 4: 16)
-        const XQView v = xq_view(p.xq, nblk);
-        // limbs (4 G x 96 B), scales, sums -> LDS (the x region: K/V sub-chunk 2 is done)
-        if (wave < 3) {  // lanes write LDS at base + 16 lane: limbs (2 copies), then xs | xsum
-            const uint8_t *lb = (const uint8_t *)v.limb + b0 * 96;
-            const uint8_t *src = wave < 2 ? lb + min(wave * 1024 + lane * 16, 4u * G * 96 - 16)
-                               : lane < G ? (const uint8_t *)(v.xs + b0) + lane * 16
-                                          : (const uint8_t *)(v.xsum + 2 * b0) + min(lane - G, 2u * G - 1) * 16;
-            dma16_dev(src, lds0 + QA_X + wave * 1024);
-        }
-        wait_vm<0>();  // (also the O rows' copies)
+        AttnP pm = p;
+        pm.out = nullptr;
+        pm.xq = nullptr;
+        attn_merge<G, 32, false, true>(pm, h * G, nv, false, mo);
+    }
+    ZH_TRACE_POINT(12);
+    __syncthreads();
+    {
+        const XQView v = xq_view(lds + QA_X, 4 * G);  // limbs [4G][96], xs [4G], xsum [4G][2]
+        if (tid < (uint32_t)G * FD_HD) xq_store_block32(mo[tid], tid & 31, v, tid / 32);
+        lds_bar();
+        wait_vm<0>();  // the O rows' copies (waves 4-7)
         lds_bar();
     }
     const uint8_t *xlimb = lds + QA_X;
-    const float *oxs = (const float *)(lds + QA_X + 2048), *oxz = oxs + 4 * G;
+    const float *oxs = (const float *)(lds + QA_X + 4 * G * 96), *oxz = oxs + 4 * G;
     {
         // lane: row r = tid / 4 of the 128, half super-block q = tid % 4 of the
         // XCD's 4 G half-blocks (G = 4; fewer heads leave lanes idle)
@@ -674,7 +671,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         }
         float res = act ? fmaf(hdr.d, accd, -hdr.dmin * accm) : 0.f;
         res = team_sum_dpp<4>(res);
-        if (!ok_m) res = __builtin_nanf("");
+        if (!(ok && ok_rows)) res = __builtin_nanf("");  // a wait gave up: the rows' sums are poisoned
         if (q == 0) __hip_atomic_fetch_add(P.x_acc + j * QA_OROWS + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     ZH_TRACE_POINT(13);
