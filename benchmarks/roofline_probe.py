@@ -93,7 +93,7 @@ def main():
     ctx = hip.Context(0)
     if a.pmc:
         b = pmc_sequence(ctx)
-        print(json.dumps({"cal_bytes": CAL_BYTES, "groups": GROUP_ORDER, "iters": PMC_ITERS,
+        print(json.dumps({"cal_bytes": CAL_BYTES, "groups": list(b), "iters": PMC_ITERS,
                           "layers": DENSE_8B["n_layers"], "alg_bytes": b}), flush=True)
     else:
         eng = probe_engine(ctx, PREFILL + 64)
