@@ -46,9 +46,11 @@ def probe_engine(ctx, max_ctx):
 def step_groups(eng):
     """The launch groups the step runs: Q/K/V, attention and the O projection
     as one group when the engine runs them as one launch (k_qkv_attn with its
-    O phase), Q/K/V and attention as one when only those are fused, else
-    every group separately."""
+    O phase; then the FFN as one group when it runs as k_ffn_xcd), Q/K/V and
+    attention as one when only those are fused, else every group separately."""
     if eng.group_kernels("qkv_attn_o").count(";") == 0 and "k_qkv_attn" in eng.group_kernels("qkv_attn_o"):
+        if "k_ffn_xcd" in eng.group_kernels("ffn"):
+            return ["qkv_attn_o", "ffn"]
         return ["qkv_attn_o"] + GROUP_ORDER[3:]
     if "k_qkv_attn" in eng.group_kernels("qkv_attn"):
         return ["qkv_attn"] + GROUP_ORDER[2:]

@@ -17,6 +17,8 @@ Build the debug library first (it also compiles the points in):
 --qkv-attn: the Q/K/V + attention launch (k_qkv_attn) of the per-phase
 step, replayed by zh_engine_time_kernel.
 
+--ffn: the per-XCD FFN launch (k_ffn_xcd).
+
 --standalone: the same attention body as its own kernel (the per-phase
 step with a shuffled page table, i.e. k_attn_ring), its launches replayed by
 zh_engine_time_kernel; points relative to each workgroup's start.
@@ -115,6 +117,11 @@ def qkv_attn():
 RING_POINTS = ["start", "activation landed", "XQ limbs in registers", "ring done", "outputs stored"]
 
 
+FFN_POINTS = ["start", "activation landed", "XQ limbs in registers", "gate/up done", "slices ready",
+              "slice XQ in registers", "end", "down tile 0", "down tile 1", "down tile 2", "down tile 3",
+              "gate/up tile 0 in LDS", "slice in LDS", "slice XQ built"]
+
+
 TILE_POINTS = ["start", "activation staged", "batch 0 in LDS", "batch 1", "batch 2", "batch 3", "batch 4+", "end"]
 
 
@@ -161,6 +168,8 @@ def main():
         return qkv_attn()
     if "--ring" in sys.argv[1:]:
         return ring(sys.argv[sys.argv.index("--ring") + 1])
+    if "--ffn" in sys.argv[1:]:
+        return ring("ffn", "zh_debug_trace_ffn", FFN_POINTS)
     if "--tile" in sys.argv[1:]:
         return ring(sys.argv[sys.argv.index("--tile") + 1], "zh_debug_trace_lpb", TILE_POINTS)
     L = hip.lib()

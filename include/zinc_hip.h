@@ -323,6 +323,16 @@ int zh_engine_set_persistent(zh_engine *eng, int on);
  * dispatches plus its fused norm/RoPE/KV-write and flash-decode dispatches
  * (forward.zig:4776-4800, attention.zig:199-316). */
 int zh_engine_set_fused_attn(zh_engine *eng, int on);
+/* The dense FFN (ffn_norm, gate/up + SwiGLU, down + residual) as one launch
+ * split by XCD (default on): XCD h computes FFN rows [1536 h, +1536), its
+ * workgroups exchange the SwiGLU slice through the XCD's L2 and add the
+ * down projection of that slice into the residual with device atomics.
+ * Applies where the O projection runs inside the fused attention launch and
+ * the layer is hidden 4096 / FFN 12288 / Q4_K gate, up / Q6_K down; the
+ * residual stream is then carried between launches as a sum of two vectors.
+ * Replaces the reference's ffn_norm, gate/up/SwiGLU and down dispatches
+ * (forward.zig:8237-8290). */
+int zh_engine_set_fused_ffn(zh_engine *eng, int on);
 
 /* ---- KV page pool: KvPagePool (src/scheduler/kv_cache.zig:43-125) ------ */
 int      zh_kv_pool_create(uint32_t total_pages, uint32_t page_size, zh_kv_pool **out);  /* init */
@@ -436,6 +446,8 @@ int zh_engine_tensor_type(zh_engine *eng, uint64_t stream, uint32_t *type);
 #define ZH_GROUP_O 4u        /* O projection + residual */
 #define ZH_GROUP_FFN_IN 8u   /* ffn_norm + gate/up + SwiGLU (MoE: + router, top-k) */
 #define ZH_GROUP_FFN_OUT 16u /* down projection + residual (MoE: + weighted expert sum) */
+/* ZH_GROUP_FFN_IN | ZH_GROUP_FFN_OUT: both as the step runs them (one launch
+ * when zh_engine_set_fused_ffn applies) */
 /* Average duration of one launch of `group`, replayed with the engine's own
  * arguments and state over `iters` launches rotating through the layers, by
  * HIP events on the engine's stream. Leaves the activations changed. */

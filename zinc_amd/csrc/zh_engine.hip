@@ -74,6 +74,12 @@ struct zh_engine {
     bool fused_qa = true;     // zh_engine_set_fused_attn: Q/K/V + attention in one launch where it applies
     uint32_t *qa_flags = nullptr;  // its XCD-local flag and epoch words (zero at creation)
     float *xin = nullptr;          // with the O projection in that launch: copy of the residual stream at layer entry
+    bool fused_ffn = true;         // zh_engine_set_fused_ffn: the dense FFN as one per-XCD launch where it applies
+    uint32_t *ffn_flags = nullptr; // its XCD-local flag and epoch words (zero at creation)
+    // split residual of the per-XCD launches: the residual stream is
+    // rres[r] + dres[d] (plain rows + atomic sums), alternating per launch
+    float *rres = nullptr;         // [2][H]
+    float *dres = nullptr;         // [3][H]
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
@@ -334,6 +340,8 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)}, {(void **)&e->router_cnt, 4},
         {(void **)&e->step_ctl, zh_step_ctl_bytes()}, {(void **)&e->step_layers, sizeof(zh_step_layer) * c.n_layers},
         {(void **)&e->qa_flags, 4ull * zhk_qkv_attn_flag_words()}, {(void **)&e->xin, 4ull * H},
+        {(void **)&e->ffn_flags, 4ull * zhk_ffn_xcd_flag_words()}, {(void **)&e->rres, 8ull * H},
+        {(void **)&e->dres, 12ull * H},
     };
     uint64_t aoff = 0;
     for (auto &a : acts) aoff = align256(aoff + a.bytes);
@@ -582,6 +590,16 @@ extern "C" int zh_engine_set_fused_attn(zh_engine *e, int on) {
     return ZH_OK;
 }
 
+extern "C" int zh_engine_set_fused_ffn(zh_engine *e, int on) {
+    if (!e) return ZH_ERR_INVALID_ARGUMENT;
+    if (e->fused_ffn != (on != 0)) {
+        ZH_HIP(e->ctx, hipStreamSynchronize(e->ctx->stream));
+        drop_graphs(e);
+        e->fused_ffn = on != 0;
+    }
+    return ZH_OK;
+}
+
 extern "C" int zh_engine_set_persistent(zh_engine *e, int on) {
     if (!e) return ZH_ERR_INVALID_ARGUMENT;
     if (e->persistent != (on != 0)) {
@@ -716,6 +734,28 @@ static bool step_qa_o(zh_engine *e) {
     return true;
 }
 
+// Whether the dense FFN also runs as one per-XCD launch (k_ffn_xcd): then
+// both launches of a layer take the split residual. Launch k of the step
+// (attention 2l, FFN 2l + 1) reads rres[k % 2] + dres[k % 3], writes their
+// sum into rres[(k + 1) % 2], adds its projection into dres[(k + 1) % 3] with
+// device atomics and zeroes dres[(k + 2) % 3] (last read by launch k - 1,
+// next added into by launch k + 1). The step starts from the embedding in
+// rres[0] and dres all zero; k_fold_residual leaves the sum in e->hidden and
+// dres zero again.
+static bool step_xcd(zh_engine *e) {
+    return e->fused_ffn && !zh_knob("ZH_NO_FFN_XCD") && zhk_ffn_xcd_supported(e->ctx, e->c.hidden, e->c.ffn) &&
+           step_qa_o(e);
+}
+
+__global__ void k_fold_residual(float *hidden, const float *r, float *d, uint32_t kd, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    hidden[i] = r[i] + d[kd * n + i];
+    d[i] = 0.f;
+    d[n + i] = 0.f;
+    d[2 * n + i] = 0.f;
+}
+
 // Records the decode step: embedding, layers [l0, l1) (only the launch
 // groups in `mask`), then (whole steps only) the output head and the step
 // advance.
@@ -736,10 +776,15 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     zh_step_args sa;
     const bool persistent = whole && step_args(e, sa);
     const bool qa_o = !persistent && step_qa_o(e);
+    const bool xl = qa_o && step_xcd(e);
+    float *const D = e->dres;
+    auto dr = [&](uint32_t k) { return D + (size_t)(k % 3) * H; };
     // embedToken (forward.zig:4255-4290), on the device.
     if (whole) {
-        ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, 1, H, e->hidden, e->st + ST_TOKEN_IN, m.vocab));
-        if (qa_o) ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, 1, H, e->xin, e->st + ST_TOKEN_IN, m.vocab));
+        ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, 1, H, xl ? e->rres : e->hidden, e->st + ST_TOKEN_IN,
+                             m.vocab));
+        if (qa_o && !xl)
+            ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, 1, H, e->xin, e->st + ST_TOKEN_IN, m.vocab));
     }
     if (persistent) ERC(zhk_step_layers(c, sa));
     for (uint32_t l = persistent ? m.n_layers : l0; l < m.n_layers && l < l1; l++) {
@@ -762,7 +807,13 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         // (and the O projection, qa_o, when the launch group includes it)
         const bool qa = (mask & SK_QKV) && (mask & SK_ATTN) && lpb_attn && layer_qa(e, y);
         const bool with_o = qa && qa_o && (mask & SK_O);
-        if (qa) {
+        const uint32_t ka = 2 * l;  // the split residual's launch index (xl)
+        if (qa && with_o && xl) {
+            ERC(zhk_qkv_attn(c, W(y.wq), W(y.wk), W(y.wv), e->rres, Wf(y.attn_norm), e->q, e->k, e->v,
+                             Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc, m.max_ctx, e->attn, e->xq_q,
+                             m.n_heads, pos, scale, m.eps, e->fd_part, e->qa_flags, W(y.wo), dr(ka + 1), dr(ka),
+                             e->rres + H, dr(ka + 2)));
+        } else if (qa) {
             ERC(zhk_qkv_attn(c, W(y.wq), W(y.wk), W(y.wv), qa_o ? e->xin : e->hidden, Wf(y.attn_norm), e->q, e->k,
                              e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc, m.max_ctx, e->attn, e->xq_q,
                              m.n_heads, pos, scale, m.eps, e->fd_part, e->qa_flags, with_o ? W(y.wo) : nullptr,
@@ -811,6 +862,12 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
                              e->xq_q));
         } else {
             ERC(zhk_dmmv(c, y.wo.type, W(y.wo), e->xq_q, e->hidden, H, qd, 1));
+        }
+        if (lpb_ffn && xl && (mask & SK_FFN_IN) && (mask & SK_FFN_OUT)) {
+            // ffn_norm, gate/up + SwiGLU and down in one launch, split by XCD
+            ERC(zhk_ffn_xcd(c, e->rres + H, dr(ka + 1), Wf(y.ffn_norm), m.eps, W(y.gate), W(y.up), W(y.down), e->s,
+                            e->rres, dr(ka + 2), dr(ka + 3), e->ffn_flags));
+            continue;
         }
         if (lpb_ffn) {
             // ffn_norm fused into gate/up; SwiGLU fused into its epilogue
@@ -889,6 +946,11 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         }
     }
     if (!whole) return ZH_OK;
+    if (xl) {
+        hipLaunchKernelGGL(k_fold_residual, dim3((H + 255) / 256), dim3(256), 0, c->stream, e->hidden, e->rres,
+                           e->dres, (2 * m.n_layers) % 3, H);
+        ZH_LAUNCH_CHECK(c);
+    }
     if (collect) ERC(record_collect(e));
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, c->stream, e->st, (const uint32_t *)e->prompt);
     ZH_LAUNCH_CHECK(c);
@@ -962,6 +1024,10 @@ extern "C" int zh_engine_time_kernel(zh_engine *e, uint32_t group, uint32_t iter
     hipEventDestroy(ev[0]);
     hipEventDestroy(ev[1]);
     if (rc == ZH_OK) *us_per_launch = ms * 1e3f / (float)iters;
+    // the replays leave atomic sums in the split residual's dres, which a
+    // decode step expects zero
+    if (rc == ZH_OK && hipMemsetAsync(e->dres, 0, 12ull * e->c.hidden, c->stream) != hipSuccess)
+        rc = zh_set_err(c, ZH_ERR_HIP, "time_kernel reset");
     return rc;
 }
 
@@ -1413,6 +1479,8 @@ extern "C" uint64_t zh_engine_group_bytes(zh_engine *e, uint32_t group, uint32_t
     case SK_ATTN:
         return 2 * kvd * 2 * Lctx + (qd + 2 * kvd) * 4 + 2 * hd * 4 + hd * 4 + 2 * kvd * 2 + qd * 4 + xqb(qd);
     case SK_O: return y.wo.bytes + xqb(qd) + 2 * H * 4;
+    case SK_FFN_IN | SK_FFN_OUT:  // one launch (k_ffn_xcd): x = two vectors in, one out, the sums added into a third
+        return y.gate.bytes + y.up.bytes + y.down.bytes + 5 * H * 4;
     case SK_FFN_IN:
         if (c.n_experts == 0) return y.gate.bytes + y.up.bytes + 2 * H * 4 + F * 4 + xqb(F);
         return y.router.bytes + 2 * k * zh_tensor_bytes(y.egate.type, (uint32_t)F, (uint32_t)H) + 2 * H * 4 +

@@ -235,7 +235,18 @@ int zhk_qkv_attn(zh_ctx *ctx, const uint8_t *wq, const uint8_t *wk, const uint8_
                  const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
                  uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
-                 const uint8_t *wo = nullptr, float *x_acc = nullptr);
+                 const uint8_t *wo = nullptr, float *x_acc = nullptr, const float *xb = nullptr,
+                 float *x_out = nullptr, float *zero = nullptr);
+// xb != nullptr (with wo): the input is x + xb, stored into x_out (16 rows
+// per workgroup); x_acc starts at zero (it is not x's copy), `zero` (H
+// floats) is cleared. Per-XCD FFN (zh_ffn_xcd.hip) with the same split
+// residual: xa + xb in, xout = xa + xb, the down projection added into acc,
+// `zero` cleared; hidden 4096, FFN 12288, Q4_K gate/up, Q6_K down.
+bool zhk_ffn_xcd_supported(zh_ctx *ctx, uint32_t hidden, uint32_t ffn);
+uint32_t zhk_ffn_xcd_flag_words();
+int zhk_ffn_xcd(zh_ctx *ctx, const float *xa, const float *xb, const float *norm_w, float eps, const uint8_t *wg,
+                const uint8_t *wu, const uint8_t *wd, float *s, float *xout, float *acc, float *zero,
+                uint32_t *flags);
 // wo != nullptr (4 q heads per kv head): also the O projection, added into
 // x_acc with device atomics; x must then be a copy of x_acc (x_acc changes
 // during the launch).

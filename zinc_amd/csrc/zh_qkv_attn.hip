@@ -47,6 +47,7 @@
 #define TRACE_OPS(slot) ZH_TRACE_POINT((slot) == 11 ? 14 : (slot) == 13 ? 15 : 99)  // merge start, merge stats done
 #include "zh_attn_common.h"
 #include "zh_lpb_common.h"
+#include "zh_xcd.h"
 
 namespace {
 
@@ -85,52 +86,20 @@ struct QaP {
     uint32_t kv_defer;            // K/V copies issued at the start (0), after x landed (1), after the rows landed (2)
     // WITH_O: the O projection of the XCD's G heads (Q4_K W_o [4096][4096],
     // super-blocks 2h and 2h + 1 of every row) added to x_acc with device
-    // atomics; x (the Q/K/V input) is then a copy of x_acc taken before the
-    // launch, since x_acc changes during it.
+    // atomics; x (the Q/K/V input) is then not x_acc, which changes during
+    // the launch (a copy of it taken before, or the split residual below).
     const uint8_t *wo;
     float *x_acc;
+    // Split residual (with the O phase): the layer input is x + xb (xb: the
+    // previous launch's atomic sums, staged in K/V sub-chunk 0's slot, whose
+    // copy then waits until x is in registers); every workgroup stores its
+    // 16 rows of x + xb into x_out and zeroes its 16 rows of `zero`.
+    const float *xb;
+    float *x_out, *zero;
 };
-
-ZH_DEV uint32_t xcc_id() {
-    uint32_t v;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-    return v & 0xFu;
-}
-
-// 16 B per lane into LDS at device scope: data another workgroup of this XCD
-// stored in the shared L2
-ZH_DEV void dma16_dev(const void *g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g), "s"(lds)
-                 : "memory", "m0");
-}
 
 // LDS offset of K/V sub-chunk s
 ZH_DEV uint32_t qa_slot(uint32_t s) { return s == 0 ? 0u : s == 1 ? AR_SLOT : QA_X; }
-
-// Waits (bounded by ctl[1] ticks) until flag words f[0 .. n) reach epoch E;
-// wave 0 polls, one word per lane. Returns false after giving up (and sets
-// ZH_DEVERR_ATTN_WAIT). Every thread of the workgroup calls it.
-ZH_DEV bool qa_wait(const uint32_t *f, uint32_t n, uint32_t E, uint32_t *ctl, uint32_t tid) {
-    __shared__ uint32_t s_ok;
-    if (tid < 64) {
-        const uint32_t lane = tid;
-        bool ok = true;
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        const uint64_t limit = __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        while (true) {
-            const uint32_t v = lane < n ? __hip_atomic_load(f + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : E;
-            if (__builtin_amdgcn_ballot_w64((int32_t)(v - E) < 0) == 0 && limit != 0) break;
-            if (__builtin_amdgcn_s_memrealtime() - t0 >= limit) {
-                ok = false;
-                if (lane == 0) __hip_atomic_fetch_or(ctl, ZH_DEVERR_ATTN_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-        if (lane == 0) s_ok = ok ? 1u : 0u;
-    }
-    __syncthreads();
-    return s_ok != 0;
-}
 
 template <int G, bool WITH_O>
 __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
@@ -170,6 +139,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
             const uint32_t c = wl4 + 4 * i;
             dma16((const uint8_t *)P.x + c * 1024 + lane * 16, lds0 + QA_X + c * 1024);
             dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + QA_X + 16384 + c * 1024);
+            if (P.xb) dma16((const uint8_t *)P.xb + c * 1024 + lane * 16, lds0 + qa_slot(0) + c * 1024);
         }
 #pragma unroll
         for (uint32_t i = 0; i < (NCH + 3) / 4; i++) {
@@ -217,7 +187,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         if (wave == 5)
             dma16((const uint8_t *)(p.rope_cs + (size_t)posv * FD_HD) + min(lane * 16, 496u), lds0 + QA_ROPE);
         if (P.kv_defer == 0)
-            for (uint32_t s = 0; s < n01; s++) issue_kv(s);
+            for (uint32_t s = P.xb ? 1u : 0u; s < n01; s++) issue_kv(s);
     }
 
     // ---- attn_norm(x) as XQ limbs (the ring DMMV's staging, in place)
@@ -237,6 +207,11 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
 #pragma unroll
         for (int it = 0; it < 2; it++) {
             v[it] = *(const f32x4 *)(xr + (it * QA_T + tid) * 4);
+            if (P.xb) {
+                const f32x4 d = *(const f32x4 *)((const float *)(lds + qa_slot(0)) + (it * QA_T + tid) * 4);
+                v[it].x += d.x; v[it].y += d.y; v[it].z += d.z; v[it].w += d.w;
+                if ((it * QA_T + tid) / 4 == blockIdx.x) *(f32x4 *)(P.x_out + (it * QA_T + tid) * 4) = v[it];
+            }
             w[it] = *(const f32x4 *)(wr + (it * QA_T + tid) * 4);
             sq = fmaf(v[it].x, v[it].x, sq); sq = fmaf(v[it].y, v[it].y, sq);
             sq = fmaf(v[it].z, v[it].z, sq); sq = fmaf(v[it].w, v[it].w, sq);
@@ -244,6 +219,8 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         sq = wave_sum(sq);
         if (lane == 0) red[wave] = sq;
         lds_bar();  // (also: every x / weight value is in registers before the image overwrites them)
+        if (!wa && P.xb && P.kv_defer == 0 && n01 > 0) issue_kv(0);  // xb is read: sub-chunk 0's slot is free
+        if (P.zero && tid < 16) P.zero[blockIdx.x * 16 + tid] = 0.f;
         float tot = 0.f;
 #pragma unroll
         for (int w8 = 0; w8 < 8; w8++) tot += red[w8];
@@ -355,7 +332,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         if (lane == 0) *(volatile uint32_t *)(fl_q + j) = E;
     }
     ZH_TRACE_POINT(5);
-    const bool ok_rows = qa_wait(fl_q, QA_PER, E, p.ctl, tid);
+    const bool ok_rows = xcd_wait(fl_q, QA_PER, E, p.ctl, tid);
     ZH_TRACE_POINT(6);
 
     // ---- the attention's inputs from the L2: the group's q, the new k | v
@@ -586,7 +563,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     if (!WITH_O) {
         if (j >= (uint32_t)G) return;
         // ---- merger j: q head h G + j, once every chunk of the kv head published
-        const bool ok = qa_wait(fl_p, nv, E, p.ctl, tid);
+        const bool ok = xcd_wait(fl_p, nv, E, p.ctl, tid);
         ZH_TRACE_POINT(11);
         if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
         attn_merge<1, 32, false, true>(p, h * G + j, nv, !(ok && ok_rows));
@@ -596,7 +573,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     // ---- WITH_O: every workgroup of the XCD merges the XCD's G heads itself
     // (their partials are in this XCD's L2) into LDS, as the XQ image of
     // the O projection's 4 G blocks of 32 (no second publication round)
-    const bool ok = qa_wait(fl_p, nv, E, p.ctl, tid);
+    const bool ok = xcd_wait(fl_p, nv, E, p.ctl, tid);
     ZH_TRACE_POINT(11);
     if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
     float *mo = (float *)(lds + QA_X + 4096);  // merged heads [G][128]
@@ -726,7 +703,7 @@ int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t 
                  const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
                  uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
-                 const uint8_t *wo, float *x_acc) {
+                 const uint8_t *wo, float *x_acc, const float *xb, float *x_out, float *zero) {
     QaP P = {};
     AttnP &p = P.a;
     p.q = q; p.k_new = k; p.v_new = v; p.q_norm = qw; p.k_norm = kw; p.rope_cs = rope_cs;
@@ -734,8 +711,10 @@ int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t 
     p.scale = scale; p.eps = eps; p.part = partials; p.n_chunks = QA_PER; p.counters = nullptr;
     p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh; p.nd = QA_PER; p.no_wait = 0; p.ident = 1; p.ctl = c->err_dev;
     P.wq = wq; P.wk = wk; P.wv = wv; P.x = x; P.norm_w = norm_w; P.flags = flags;
-    P.wo = wo; P.x_acc = x_acc;
-    P.kv_defer = (uint32_t)zh_knob_int("ZH_QA_DEFER", 0);
+    P.wo = wo; P.x_acc = x_acc; P.xb = xb; P.x_out = x_out; P.zero = zero;
+    P.kv_defer = xb ? 0u : (uint32_t)zh_knob_int("ZH_QA_DEFER", 0);
+    if (xb && (!wo || !x_out || !zero || ((uintptr_t)xb & 15) || ((uintptr_t)x_out & 15)))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: split residual needs the O phase and aligned rows");
     const uint32_t G = nh / QA_NXCD;
     if ((wo && (!x_acc || ((uintptr_t)wo & 15))) || !pos.dev || ((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wq & 15) || ((uintptr_t)wk & 15) ||
         ((uintptr_t)wv & 15))

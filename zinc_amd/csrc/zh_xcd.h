@@ -1,0 +1,63 @@
+// zh_xcd.h — helpers for launches whose workgroups exchange data inside one
+// XCD (zh_qkv_attn.hip, zh_ffn_xcd.hip): the workgroup's XCD, device-scope
+// DMA, and the bounded wait for an XCD's flag words.
+//
+// Every launch of these kernels has 256 workgroups, one per CU of an MI355X
+// (8 XCDs x 32 CUs). The dispatcher deals a launch's workgroups round robin
+// over the XCDs, starting where the previous launch stopped (measured:
+// workgroup w lands on XCD (w + s) % 8 for a launch-dependent s; the engine
+// checks this once per context with zhk_xcd_round_robin). A workgroup reads
+// its XCD from the XCC_ID register and takes slot j = w / 8 of it: every run
+// of 8 consecutive workgroups covers the 8 XCDs once, so the (XCD, j) pairs
+// are all distinct.
+//
+// Exchange protocol inside an XCD: plain stores (they land in the XCD's L2),
+// s_waitcnt vmcnt(0) for their acknowledgement, then a plain store of the
+// flag word carrying the launch's epoch; consumers poll the flags with
+// device-scope loads and read the data with device-scope loads or DMA, or
+// with plain loads of lines they have not read before in the launch.
+#pragma once
+#include "zh_device.h"
+#include "zh_internal.h"
+
+constexpr uint32_t XCD_N = 8, XCD_PER = 32;  // XCDs, workgroups per XCD
+
+ZH_DEV uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xFu;
+}
+
+// 16 B per lane into LDS at device scope: data another workgroup of this XCD
+// stored in the shared L2
+ZH_DEV void dma16_dev(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+
+// Waits (bounded by ctl[1] ticks) until flag words f[0 .. n) reach epoch E;
+// wave `pw` polls, one word per lane (its outstanding vector-memory
+// operations drain on the first poll). Returns false after giving up (and
+// sets ZH_DEVERR_ATTN_WAIT). Every thread of the workgroup calls it; DMA copies the
+// other waves issued before it stay in flight.
+ZH_DEV bool xcd_wait(const uint32_t *f, uint32_t n, uint32_t E, uint32_t *ctl, uint32_t tid, uint32_t pw = 0) {
+    __shared__ uint32_t s_ok;
+    if (tid / 64 == pw) {
+        const uint32_t lane = tid & 63;
+        bool ok = true;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        const uint64_t limit = __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        while (true) {
+            const uint32_t v = lane < n ? __hip_atomic_load(f + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : E;
+            if (__builtin_amdgcn_ballot_w64((int32_t)(v - E) < 0) == 0 && limit != 0) break;
+            if (__builtin_amdgcn_s_memrealtime() - t0 >= limit) {
+                ok = false;
+                if (lane == 0) __hip_atomic_fetch_or(ctl, ZH_DEVERR_ATTN_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+        if (lane == 0) s_ok = ok ? 1u : 0u;
+    }
+    lds_bar();  // (not __syncthreads: its fence may wait for the callers' copies in flight)
+    return s_ok != 0;
+}

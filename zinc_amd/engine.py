@@ -182,11 +182,16 @@ class InferenceEngine:
         """Q/K/V projection and attention in one launch where the model takes it (default on)."""
         self.ctx.check(lib().zh_engine_set_fused_attn(self.h, int(bool(on))))
 
+    def set_fused_ffn(self, on=True):
+        """The dense FFN as one per-XCD launch where the model takes it (default on)."""
+        self.ctx.check(lib().zh_engine_set_fused_ffn(self.h, int(bool(on))))
+
     def bytes_per_token(self, L):
         return lib().zh_engine_bytes_per_token(self.h, L)
 
     # per-layer launch groups of the decode step (zinc_hip.h ZH_GROUP_*)
-    GROUPS = {"qkv": 1, "attn": 2, "qkv_attn": 3, "qkv_attn_o": 7, "o": 4, "ffn_in": 8, "ffn_out": 16, "head": 32}
+    GROUPS = {"qkv": 1, "attn": 2, "qkv_attn": 3, "qkv_attn_o": 7, "o": 4, "ffn_in": 8, "ffn_out": 16, "ffn": 24,
+              "head": 32}
 
     def time_kernel(self, group, iters=200):
         """Average us per launch of one launch group, replayed with the

@@ -127,6 +127,7 @@ SIGNATURES = {
     "zh_engine_set_pages": (_i32, [_P, _P, _u32]),
     "zh_engine_set_persistent": (_i32, [_P, _i32]),
     "zh_engine_set_fused_attn": (_i32, [_P, _i32]),
+    "zh_engine_set_fused_ffn": (_i32, [_P, _i32]),
     "zh_dmmv_supported": (_i32, [_u32, _u32]),
     "zh_engine_group_kernels": (_i32, [_P, _u32, C.c_char_p, C.c_size_t]),
     "zh_kv_pool_create": (_i32, [_u32, _u32, C.POINTER(_P)]),
