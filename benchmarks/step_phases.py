@@ -117,9 +117,8 @@ def qkv_attn():
 RING_POINTS = ["start", "activation landed", "XQ limbs in registers", "ring done", "outputs stored"]
 
 
-FFN_POINTS = ["start", "activation landed", "XQ limbs in registers", "gate/up done", "slices ready",
-              "slice XQ in registers", "end", "down tile 0", "down tile 1", "down tile 2", "down tile 3",
-              "gate/up tile 0 in LDS", "slice in LDS", "slice XQ built"]
+FFN_POINTS = ["start", "activation landed", "XQ limbs in registers", "gate/up done", "down activation ready",
+              "down done", "partials seen", "end", "", "", "", "gate/up tile 0 in LDS"]
 
 
 TILE_POINTS = ["start", "activation staged", "batch 0 in LDS", "batch 1", "batch 2", "batch 3", "batch 4+", "end"]

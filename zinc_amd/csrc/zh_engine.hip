@@ -80,6 +80,12 @@ struct zh_engine {
     // rres[r] + dres[d] (plain rows + atomic sums), alternating per launch
     float *rres = nullptr;         // [2][H]
     float *dres = nullptr;         // [3][H]
+    // the per-XCD FFN's copy of every layer's ffn_down (zhk_ffn_pack_down),
+    // made before a step runs when the arena may have changed since, and its
+    // partial sums
+    uint8_t *down_pk = nullptr;
+    bool pk_stale = true;
+    float *ffn_part = nullptr;
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
@@ -342,6 +348,7 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->qa_flags, 4ull * zhk_qkv_attn_flag_words()}, {(void **)&e->xin, 4ull * H},
         {(void **)&e->ffn_flags, 4ull * zhk_ffn_xcd_flag_words()}, {(void **)&e->rres, 8ull * H},
         {(void **)&e->dres, 12ull * H},
+        {(void **)&e->ffn_part, c.ffn == 12288 && H == 4096 ? zhk_ffn_part_bytes() : 0ull},
     };
     uint64_t aoff = 0;
     for (auto &a : acts) aoff = align256(aoff + a.bytes);
@@ -526,6 +533,7 @@ extern "C" void zh_engine_destroy(zh_engine *e) {
     if (e->kv) hipFree(e->kv);
     if (e->act_arena) hipFree(e->act_arena);
     if (e->pf.arena) hipFree(e->pf.arena);
+    if (e->down_pk) hipFree(e->down_pk);
     delete e;
 }
 
@@ -747,6 +755,24 @@ static bool step_xcd(zh_engine *e) {
            step_qa_o(e);
 }
 
+// The per-XCD FFN's packed ffn_down of every layer: allocated on first use,
+// rewritten from the arena when it may have changed (outside any capture).
+static int ensure_packed(zh_engine *e) {
+    if (!step_xcd(e)) return ZH_OK;
+    const uint64_t per = zhk_ffn_pack_bytes();
+    if (!e->down_pk && hipMalloc((void **)&e->down_pk, per * e->c.n_layers) != hipSuccess) {
+        e->down_pk = nullptr;
+        return zh_set_err(e->ctx, ZH_ERR_OUT_OF_MEMORY, "packed ffn_down (%llu B)",
+                          (unsigned long long)(per * e->c.n_layers));
+    }
+    if (e->pk_stale) {
+        for (uint32_t l = 0; l < e->c.n_layers; l++)
+            ERC(zhk_ffn_pack_down(e->ctx, e->arena + e->L[l].down.off, e->down_pk + per * l));
+        e->pk_stale = false;
+    }
+    return ZH_OK;
+}
+
 __global__ void k_fold_residual(float *hidden, const float *r, float *d, uint32_t kd, uint32_t n) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -865,8 +891,9 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         }
         if (lpb_ffn && xl && (mask & SK_FFN_IN) && (mask & SK_FFN_OUT)) {
             // ffn_norm, gate/up + SwiGLU and down in one launch, split by XCD
-            ERC(zhk_ffn_xcd(c, e->rres + H, dr(ka + 1), Wf(y.ffn_norm), m.eps, W(y.gate), W(y.up), W(y.down), e->s,
-                            e->rres, dr(ka + 2), dr(ka + 3), e->ffn_flags));
+            ERC(zhk_ffn_xcd(c, e->rres + H, dr(ka + 1), Wf(y.ffn_norm), m.eps, W(y.gate), W(y.up),
+                            e->down_pk + zhk_ffn_pack_bytes() * l, e->ffn_part, e->rres, dr(ka + 2), dr(ka + 3),
+                            e->ffn_flags));
             continue;
         }
         if (lpb_ffn) {
@@ -964,6 +991,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
 extern "C" int zh_engine_group_kernels(zh_engine *e, uint32_t group, char *names, size_t len) {
     if (!e || !names || len == 0 || group == 0 || (group & ~(uint32_t)SK_ALL)) return ZH_ERR_INVALID_ARGUMENT;
     zh_ctx *c = e->ctx;
+    ERC(ensure_packed(e));
     hipGraph_t g = nullptr;
     EHIP(e, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
     int rc = record_step(e, false, 0, 1, group);
@@ -1008,6 +1036,7 @@ extern "C" int zh_engine_time_kernel(zh_engine *e, uint32_t group, uint32_t iter
     zh_ctx *c = e->ctx;
     const uint32_t L = e->c.n_layers;
     auto launch = [&](uint32_t i) { return head ? record_collect(e) : record_step(e, false, i % L, i % L + 1, group); };
+    ERC(ensure_packed(e));
     for (uint32_t l = 0; l < (head ? 1u : L); l++) ERC(launch(l));
     hipEvent_t ev[2];
     EHIP(e, hipEventCreate(&ev[0]));
@@ -1062,6 +1091,7 @@ static int set_state(zh_engine *e, uint32_t n_prompt, uint32_t pos, uint32_t fir
 }
 
 static int run_step(zh_engine *e, bool collect) {
+    ERC(ensure_packed(e));
     if (zh_knob("ZH_NO_GRAPH")) return record_step(e, collect);
     ERC(ensure_graphs(e));
     EHIP(e, hipGraphLaunch(collect ? e->g_out : e->g_noout, e->ctx->stream));
@@ -1416,6 +1446,7 @@ extern "C" int zh_engine_tensor(zh_engine *e, uint64_t stream, zh_buf **buf, uin
     if (!e || !buf || !offset || !bytes) return ZH_ERR_INVALID_ARGUMENT;
     auto it = e->tensors.find(stream);
     if (it == e->tensors.end()) return zh_set_err(e->ctx, ZH_ERR_TENSOR_NOT_FOUND, "stream %llu", (unsigned long long)stream);
+    e->pk_stale = true;  // the caller may write the weights through the view
     static thread_local zh_buf view;
     view.ptr = e->arena;
     view.size = e->arena_bytes;

@@ -1,76 +1,85 @@
 // zh_ffn_xcd.hip — the dense FFN of one decode layer (ffn_norm, gate/up +
-// SwiGLU, down + residual) in one launch, split by XCD (8B shape: hidden
-// 4096, FFN 12288, Q4_K gate/up, Q6_K down).
+// SwiGLU, down + residual) in one launch (8B shape: hidden 4096, FFN 12288,
+// Q4_K gate/up, Q6_K down).
 //
 // Replaces three dispatches of the reference's decode step: ffn_norm, the
 // fused gate/up/SwiGLU DMMV and the down DMMV with its residual add
 // (forward.zig:8237-8290; dmmv_q4k.comp, dmmv_q6k.comp).
 //
-// XCD h owns FFN rows [1536 h, 1536 h + 1536): its 32 workgroups compute those
-// gate/up rows and their SwiGLU outputs (48 rows each, the Q4_K ring's
-// arithmetic, zh_ring_q4k.h), publish them in the XCD's L2 and meet at an
-// XCD-local flag barrier (zh_xcd.h); then every workgroup multiplies the
-// 1536 outputs by the down matrix's columns [1536 h, 1536 h + 1536) for its
-// 128 rows (six Q6_K super-blocks of each row, 1260 bytes) and adds the 128
-// partial sums into the residual with device-scope float atomics (one per
-// XCD and row). The down projection thus needs no launch, no global
-// exchange of the SwiGLU vector and no staging of the whole 12288-element
-// activation: each XCD only ever sees its own slice of it.
+// Workgroup w (= 32 XCD + slot, zh_xcd.h) owns FFN rows [48 w, 48 w + 48):
+//   1. gate/up: its 48 gate and 48 up rows against ffn_norm(x) as XQ limbs
+//      (the Q4_K ring's arithmetic, zh_ring_q4k.h), SwiGLU of the 48 pairs;
+//   2. down: the down matrix's columns [48 w, 48 w + 48) for all 4096 rows,
+//      i.e. this workgroup's share of every row's dot product, from the
+//      SwiGLU values it just computed (no exchange), into 4096 partial sums;
+//   3. the 32 workgroups of an XCD publish their partial vectors in the XCD's
+//      L2, meet at an XCD-local flag barrier, and workgroup j adds rows
+//      [128 j, 128 j + 128) of the XCD's 32 partials into the residual with
+//      device atomics (one per XCD and row).
+// Steps 1 and 2 are one stream: the 6 gate/up tiles (36 KB) and then the 8
+// down tiles (22 KB) flow through one three-slot LDS ring of asynchronous
+// global_load_lds copies, so HBM does not wait for the SwiGLU step.
 //
-// The residual is kept as A + D1 + D2 (zh_engine.hip): this launch reads
-// x = A + D1 (A: the layer input, D1: the attention's O projection added by
-// atomics), adds the down projection into D2 (zeroed by the attention launch
-// of this layer) and zeroes D1 of the other parity (its last reader was this
-// layer's attention launch; the next layer's attention adds into it).
+// The down columns come from a copy of ffn_down that the engine repacks
+// (k_ffn_pack_down): for each workgroup's 48 columns, 4096 records of 44
+// bytes, one per row, contiguous — the 48 6-bit codes (three 16-element
+// groups: low nibbles in two dwords, high bit pairs in a third), the three
+// groups' int8 scales and the f16 super-block scales of groups 0 and 2
+// (group 1 shares one of them). 44-byte records make the lanes' LDS reads
+// conflict-free (11 dwords apart). The values are Q6_K's, unchanged: d *
+// scale * (code - 32).
 //
-// LDS: phase 1 is the Q4_K ring's layout (three 36 KB slots, XQ image, f32 x
-// and norm weight; D1 is staged in the third slot, which the ring fills only
-// after the activation work); phase 2 reuses it as three 40 KB slots of 32
-// down rows (1280 bytes each: the 1260-byte column segment from its 16-byte
-// aligned start), the SwiGLU slice and its XQ image.
+// The residual is kept as A + D (zh_engine.hip): this launch reads x = xa +
+// xb, stores its 16 rows of x into xout, adds the down projection into acc
+// (zeroed by the previous launch) and zeroes its 16 rows of `zero`.
 #include "zh_ring_q4k.h"
 #include "zh_xcd.h"
 
 namespace {
 constexpr uint32_t FX_H = 4096, FX_F = 12288;
 constexpr uint32_t FX_RA = FX_F / (XCD_N * XCD_PER);   // gate/up rows per workgroup (48)
-constexpr uint32_t FX_FS = FX_F / XCD_N;                // SwiGLU outputs per XCD (1536)
-constexpr uint32_t FX_NSB = FX_FS / 256;                // down super-blocks per row and XCD (6)
-constexpr uint32_t FX_HB = 2 * FX_NSB;                  // half super-blocks (12): lanes per down row
-constexpr uint32_t FX_RB = FX_H / XCD_PER;  // down rows per workgroup (128)
-constexpr uint32_t FX_DROWB = FX_F / 256 * 210;         // a down row (10080 B)
-constexpr uint32_t FX_SEGB = FX_NSB * 210;              // its XCD column segment (1260 B)
-constexpr uint32_t FX_SEGP = (FX_SEGB + 15 + 15) / 16;  // 16-byte pieces per row copy (80)
-constexpr uint32_t FX_RS = FX_SEGP * 16;                // LDS bytes per down row (1280)
-constexpr uint32_t FX_TR = 32;                          // down rows per tile (one pass: 32 teams of 16 lanes)
-constexpr uint32_t FX_NT = FX_RB / FX_TR;               // tiles (4)
-constexpr uint32_t FX_SLOT = FX_TR * FX_RS;             // 40 KB
-constexpr uint32_t FX_TCH = FX_SLOT / 1024;             // 1 KB copies per tile (40: 10 per copying wave)
-constexpr uint32_t FX_XQ2 = 3 * FX_SLOT;                // phase 2: XQ image of the slice
-constexpr uint32_t FX_SRAW = FX_XQ2 + 8192;             // phase 2: the slice as f32 (6 KB)
-static_assert(FX_SRAW + FX_FS * 4 <= RG_LDS, "phase 2 fits phase 1's LDS");
-static_assert(FX_TCH % 4 == 0 && FX_HB <= 16, "tile copies over 4 waves; a row's lanes in a 16-lane team");
+constexpr uint32_t FX_REC = 44;                         // packed down record per row and workgroup
+constexpr uint32_t FX_SLICE = FX_H * FX_REC;            // a workgroup's packed columns (176 KB)
+constexpr uint32_t FX_DR = 512;                         // down rows per tile (one per thread)
+constexpr uint32_t FX_DT = FX_H / FX_DR;                // down tiles (8)
+constexpr uint32_t FX_DTB = FX_DR * FX_REC;             // down tile bytes (22 KB)
+constexpr uint32_t FX_DCH = FX_DTB / 1024;              // its 1 KB copies (22)
+constexpr uint32_t FX_GT = 6;                           // gate/up tiles (48 rows / 8 per pass)
+constexpr uint32_t FX_NU = FX_GT + FX_DT;               // ring units
+constexpr uint32_t FX_RROWS = FX_H / XCD_PER;           // residual rows each workgroup reduces (128)
+// LDS beyond the ring (the layout of zh_ring_q4k.h): the XQ image's region
+// takes the 4096 partial sums, the f32 staging region the SwiGLU values'
+// limbs
+constexpr uint32_t FX_PART = RG_D * RG_TILE;
+constexpr uint32_t FX_ACT = RG_D * RG_TILE + RG_XQ_BYTES;
+static_assert(FX_DTB % 1024 == 0 && FX_DTB <= RG_TILE && FX_H * 4 <= RG_XQ_BYTES, "down tiles fit the ring");
+static_assert(FX_GT * 8 == FX_RA, "gate/up: 8 rows per pass (16 super-blocks, 32 lanes per row)");
 }  // namespace
 
-// Flag words (zero when the engine is created): [0, 256) SwiGLU slices
-// published (XCD h at h * 32), [256, 264) epochs.
+// Flag words (zero when the engine is created): [0, 256) partials published
+// (XCD h at h * 32), [256, 264) epochs.
 constexpr uint32_t FX_FLAG_WORDS = XCD_N * XCD_PER + XCD_N;
 
 struct FfnP {
-    const float *xa, *xb;        // x = xa + xb (A + D1 of the residual)
+    const float *xa, *xb;        // x = xa + xb
     const float *norm_w;         // ffn_norm weight
     float eps;
     const uint8_t *wg, *wu;      // Q4_K gate, up [12288][4096]
-    const uint8_t *wd;           // Q6_K down [4096][12288]
-    float *s;                    // SwiGLU outputs [12288] (exchanged inside each XCD)
+    const uint8_t *pk;           // packed down columns [256][4096][44 B]
+    float *part;                 // partial sums [256][4096] (exchanged inside each XCD)
     float *xout;                 // xa + xb (16 rows per workgroup)
-    float *acc;                  // D2: += the down projection (atomics)
-    float *zero;                 // D1 of the other parity: zeroed (16 rows per workgroup)
+    float *acc;                  // += the down projection (atomics)
+    float *zero;                 // zeroed (16 rows per workgroup)
     uint32_t *flags;             // FX_FLAG_WORDS
     uint32_t *ctl;               // device control words: [0] error word, [1] wait limit
-    uint32_t plain;
-    uint32_t pre, late;          // down tiles copied before the slices' wait (1..3); the rest after it (late 0) or after the slice landed (1)
 };
+
+ZH_DEV int row16_sum_i(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+    return v + __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+}
 
 __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -79,40 +88,58 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
     constexpr int TL = TT::TL, RPP = TT::RPP;
     constexpr uint32_t NBLK = NB * 8;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
-    const uint32_t h = min(xcc_id(), XCD_N - 1), j = blockIdx.x / XCD_N;
+    const uint32_t h = min(xcc_id(), XCD_N - 1), j = blockIdx.x / XCD_N, w = h * XCD_PER + j;
     uint32_t *fl = P.flags + h * XCD_PER, *ep = P.flags + XCD_N * XCD_PER + h;
     const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
     ZH_TRACE_POINT(0);
 
-    // ---- phase 1: gate/up rows [1536 h + 48 j, + 48) (the ring's workgroup
-    // h * 32 + j of 48 rows), ffn_norm(xa + xb) as XQ
     RingP p = {};
     p.norm_w = P.norm_w; p.eps = P.eps; p.M = FX_F; p.K = FX_H; p.nseg = 1; p.rpw = FX_RA;
     p.segW[0] = P.wg; p.segW[1] = P.wg; p.segW[2] = P.wg; p.W2 = P.wu;
     p.seg_end[0] = FX_F; p.seg_end[1] = FX_F; p.seg_end[2] = FX_F;
-    const TT tiles(p, h * XCD_PER + j, tid, lds);
-    const uint32_t wave = tiles.wave, r0 = tiles.r0, nt = tiles.nt, lds0 = tiles.lds0, tcw = tiles.tcw;
-    uint8_t *ring = lds, *xqa = lds + RG_D * RG_TILE, *raw = lds + RG_D * RG_TILE + RG_XQ_BYTES;
+    const TT tiles(p, w, tid, lds);
+    const uint32_t wave = tiles.wave, lds0 = tiles.lds0, tcw = tiles.tcw;
+    // a wave's 1 KB copies per down tile (chunk c = wave + 8 i < 22)
+    const uint32_t dcw = wave < FX_DCH % 8 ? FX_DCH / 8 + 1 : FX_DCH / 8;
+    const uint8_t *pk = P.pk + (size_t)w * FX_SLICE;
+    // unit u of the stream into ring slot s: gate/up tile u, then down tile u - 6
+    auto issue = [&](uint32_t u, uint32_t s) __attribute__((always_inline)) {
+        if (u < FX_GT) {
+            tiles.issue(u, s);
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < (FX_DCH + 7) / 8; i++) {
+                const uint32_t c = wave + 8 * i;
+                if (c < FX_DCH)  // uniform per wave
+                    dma16(pk + (u - FX_GT) * FX_DTB + c * 1024 + lane * 16, lds0 + s * RG_TILE + c * 1024);
+            }
+        }
+    };
+    // a wave's copies of unit u (the ring waits count them)
+    auto cnt = [&](uint32_t u) { return u < FX_GT ? tcw : dcw; };
+    uint8_t *ring = lds, *xqa = lds + RG_D * RG_TILE, *raw = lds + FX_ACT;
     float *yl = (float *)(lds + RG_D * RG_TILE + RG_XQ_BYTES + RG_RAW_BYTES), *red = yl + 2 * RG_MAXROWS;
-    // the activation: xa and the norm weight into the raw region, xb into
-    // the third ring slot (2 + 1 KB copies per wave per vector)
+
+    // ---- the activation: xa and the norm weight into the staging region,
+    // xb into the third ring slot (first filled by unit 2, issued after the
+    // XQ image is built); 2 + 1 KB copies per wave and vector
 #pragma unroll
     for (int i = 0; i < NB / 8; i++) {
         const uint32_t c = wave + 8 * i;
-        dma16((const uint8_t *)P.xa + c * 1024 + lane * 16, lds0 + RG_D * RG_TILE + RG_XQ_BYTES + c * 1024);
-        dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + RG_D * RG_TILE + RG_XQ_BYTES + NB * 1024 + c * 1024);
+        dma16((const uint8_t *)P.xa + c * 1024 + lane * 16, lds0 + FX_ACT + c * 1024);
+        dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + FX_ACT + NB * 1024 + c * 1024);
         dma16((const uint8_t *)P.xb + c * 1024 + lane * 16, lds0 + (RG_D - 1) * RG_TILE + c * 1024);
     }
-    const uint32_t npro = tiles.prologue();
-    for (uint32_t t = 0; t < npro; t++) tiles.issue(t, t);
-    wait_vm_dyn(npro * tcw);
+    issue(0, 0);
+    issue(1, 1);
+    wait_vm_dyn(2 * tcw);
     lds_bar();
     ZH_TRACE_POINT(1);
     float *ixs = (float *)(xqa + NB * 2 * RG_SEG), *ixz = ixs + NBLK;
     {
         const float *xr = (const float *)raw, *wr = (const float *)(raw + NB * 1024);
         const float *xr2 = (const float *)(ring + (RG_D - 1) * RG_TILE);
-        f32x4 v[NB / 8], w[NB / 8];
+        f32x4 v[NB / 8], wn[NB / 8];
         float sq = 0.f;
 #pragma unroll
         for (int it = 0; it < NB / 8; it++) {
@@ -120,10 +147,11 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
             const f32x4 a = *(const f32x4 *)(xr + e0), b = *(const f32x4 *)(xr2 + e0);
             v[it] = f32x4{a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
             if ((it * RG_T + tid) / 4 == blockIdx.x) *(f32x4 *)(P.xout + e0) = v[it];  // this workgroup's 16 rows
-            w[it] = *(const f32x4 *)(wr + e0);
+            wn[it] = *(const f32x4 *)(wr + e0);
             sq = fmaf(v[it].x, v[it].x, sq); sq = fmaf(v[it].y, v[it].y, sq);
             sq = fmaf(v[it].z, v[it].z, sq); sq = fmaf(v[it].w, v[it].w, sq);
         }
+        if (tid < 16) P.zero[blockIdx.x * 16 + tid] = 0.f;
         sq = wave_sum(sq);
         if (lane == 0) red[wave] = sq;
         lds_bar();
@@ -135,8 +163,8 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
         for (int it = 0; it < NB / 8; it++) {
             const uint32_t e0 = (it * RG_T + tid) * 4;
             f32x4 u = v[it];
-            u.x = w[it].x * (u.x * rms_inv); u.y = w[it].y * (u.y * rms_inv);
-            u.z = w[it].z * (u.z * rms_inv); u.w = w[it].w * (u.w * rms_inv);
+            u.x = wn[it].x * (u.x * rms_inv); u.y = wn[it].y * (u.y * rms_inv);
+            u.z = wn[it].z * (u.z * rms_inv); u.w = wn[it].w * (u.w * rms_inv);
             const float a = row8_max(fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
             float inv, sc;
             xq_scales(a, inv, sc);
@@ -158,6 +186,8 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
         }
         lds_bar();
     }
+    // ---- gate/up (units 0..5): this lane's half super-block of x (limbs,
+    // block scales, sums) in registers
     {
         const uint32_t team = tid / TL, tl = tid % TL, b = tl >> 1, hh = tl & 1;
         uint32_t L[4][24];
@@ -171,20 +201,20 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
         }
         ZH_TRACE_POINT(2);
         const uint32_t mrow = team / RPP, trow = team % RPP;
-        for (uint32_t t = 0; t < nt; t++) {
-            wait_vm_dyn(min(nt - 1 - t, (uint32_t)RG_D - 2) * tcw);
-            lds_bar();  // (t = 0: also every wave done with xb in the third slot)
-        if (t == 0) ZH_TRACE_POINT(11);
-            if (t + RG_D - 1 < nt) tiles.issue(t + RG_D - 1, (t + RG_D - 1) % RG_D);
-            const uint8_t *blk = ring + (t % RG_D) * RG_TILE + team * TT::ROWB + b * 144;
+        for (uint32_t u = 0; u < FX_GT; u++) {
+            wait_vm_dyn(cnt(u + 1));
+            lds_bar();  // (u = 0: also every wave done with xb in the third slot)
+            issue(u + 2, (u + 2) % RG_D);
+            if (u == 0) ZH_TRACE_POINT(11);
+            const uint8_t *blk = ring + (u % RG_D) * RG_TILE + team * TT::ROWB + b * 144;
             uint32_t hd[4], qs[16];
             {
-                const u32x4 v = *(const u32x4 *)blk;
-                hd[0] = v.x; hd[1] = v.y; hd[2] = v.z; hd[3] = v.w;
+                const u32x4 vv = *(const u32x4 *)blk;
+                hd[0] = vv.x; hd[1] = vv.y; hd[2] = vv.z; hd[3] = vv.w;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const u32x4 w = *(const u32x4 *)(blk + 16 + 64 * hh + 16 * i);
-                    qs[4 * i] = w.x; qs[4 * i + 1] = w.y; qs[4 * i + 2] = w.z; qs[4 * i + 3] = w.w;
+                    const u32x4 q4 = *(const u32x4 *)(blk + 16 + 64 * hh + 16 * i);
+                    qs[4 * i] = q4.x; qs[4 * i + 1] = q4.y; qs[4 * i + 2] = q4.z; qs[4 * i + 3] = q4.w;
                 }
             }
             const LpbQ4K::Hdr hdr = LpbQ4K::header(hd);
@@ -195,8 +225,8 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
                 int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    const uint32_t w = qs[8 * pl + i];
-                    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+                    const uint32_t q = qs[8 * pl + i];
+                    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
                     for (int k = 0; k < 3; k++) {
                         D[0][k] = sdot4(lo, L[2 * pl][k * 8 + i], D[0][k]);
@@ -214,177 +244,185 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
             }
             float res = fmaf(hdr.d, accd, -hdr.dmin * accm);
             res = team_sum_dpp<TL>(res);
-            const uint32_t i = t * RPP + trow;
-            if (tl == 0 && i < RG_MAXROWS) yl[mrow * RG_MAXROWS + i] = res;
+            if (tl == 0) yl[mrow * RG_MAXROWS + u * RPP + trow] = res;
         }
     }
     lds_bar();
     ZH_TRACE_POINT(3);
-    // ---- publish the 48 SwiGLU outputs in the XCD's L2 (wave 0), then the flag
+    // ---- SwiGLU of the 48 rows as XQ limbs in blocks of 16 (the Q6_K scale
+    // groups), by wave 0 (lanes 48..63 form an unused fourth group), then
+    // into every lane's registers. act: limbs [3 groups][3 limbs][16 B], xs
+    // [3], z [3] = -32 (sum of the group's X) xs.
+    uint8_t *act = lds + FX_ACT;
     if (wave == 0) {
-        if (lane < FX_RA) P.s[r0 + lane] = silu_mul(yl[lane], yl[RG_MAXROWS + lane]);
-        wait_vm<0>();
-        if (lane == 0) *(volatile uint32_t *)(fl + j) = E;
-    }
-    __syncthreads();  // phase 1's LDS is free
-
-    // ---- phase 2: down rows [128 j, 128 j + 128) x columns [1536 h, + 1536).
-    // Waves 0-3 copy the tiles (row segments from their 16-byte aligned
-    // start, oh bytes before the segment); waves 4-7 wait for the XCD's
-    // SwiGLU slices and copy the slice.
-    const uint32_t oh = (h * FX_SEGB) & 15u;
-    const uint8_t *dseg = P.wd + (size_t)(j * FX_RB) * FX_DROWB + h * FX_SEGB - oh;
-    // the last piece inside the row (XCD 7's segment ends at the row's end)
-    const uint32_t klast = (FX_DROWB - (h * FX_SEGB - oh)) / 16 - 1;
-    const bool wa = wave < 4;
-    const uint32_t wl4 = wave & 3;
-    auto issue_d = [&](uint32_t t, uint32_t s) __attribute__((always_inline)) {
-#pragma unroll
-        for (uint32_t i = 0; i < FX_TCH / 4; i++) {
-            const uint32_t c = wl4 + 4 * i, pc = c * 64 + lane;  // 16-byte piece of the tile
-            const uint32_t row = pc / FX_SEGP, k = min(pc - row * FX_SEGP, klast);
-            dma16(dseg + (size_t)(t * FX_TR + row) * FX_DROWB + k * 16, lds0 + s * FX_SLOT + c * 1024);
-        }
-    };
-    const uint32_t pre = P.pre;
-    if (wa)  // the first tiles (up to three; the fourth follows into slot 0)
-        for (uint32_t t = 0; t < pre; t++) issue_d(t, t);
-    if (tid < 16) P.zero[blockIdx.x * 16 + tid] = 0.f;  // D1 of the other parity
-    const bool ok = xcd_wait(fl, XCD_PER, E, P.ctl, tid, 4);
-    ZH_TRACE_POINT(4);
-    if (j == 0 && tid == 256) *(volatile uint32_t *)ep = E;  // every workgroup of the XCD has read the epoch (wave 4: no copies in flight)
-    if (wa && !P.late)
-        for (uint32_t t = pre; t < 3; t++) issue_d(t, t);
-    if (!wa) {  // the slice (6 KB): waves 4-7, 1 KB copies
-        for (uint32_t c = wl4; c < FX_FS * 4 / 1024; c += 4) {
-            const uint8_t *src = (const uint8_t *)(P.s + h * FX_FS) + c * 1024 + lane * 16;
-            if (P.plain) dma16(src, lds0 + FX_SRAW + c * 1024);
-            else dma16_dev(src, lds0 + FX_SRAW + c * 1024);
-        }
-        wait_vm<0>();
-    }
-    lds_bar();
-    ZH_TRACE_POINT(12);
-    if (wa && P.late)
-        for (uint32_t t = pre; t < 3; t++) issue_d(t, t);
-    // the slice as XQ (48 blocks of 32): threads 0..383, 4 elements each
-    const XQView xv = xq_view(lds + FX_XQ2, FX_FS / 32);
-    if (tid < FX_FS / 4) {
-        const uint32_t e0 = tid * 4;
-        const f32x4 u = *(const f32x4 *)((const float *)(lds + FX_SRAW) + e0);
-        const float a = row8_max(fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+        const float v = lane < FX_RA ? silu_mul(yl[lane], yl[RG_MAXROWS + lane]) : 0.f;
+        const float a = row16_max(fabsf(v));
         float inv, sc;
         xq_scales(a, inv, sc);
-        int X[4] = {xq_quant(u.x, inv), xq_quant(u.y, inv), xq_quant(u.z, inv), xq_quant(u.w, inv)};
-        int l0[4], l1[4], l2[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) xq_limbs(X[q], l0[q], l1[q], l2[q]);
-        const uint32_t blk = e0 / 32, lo = e0 % 32;
-        uint8_t *dst = (uint8_t *)xv.limb + blk * 96 + lo;
-        *(uint32_t *)(dst) = pack4(l0[0], l0[1], l0[2], l0[3]);
-        *(uint32_t *)(dst + 32) = pack4(l1[0], l1[1], l1[2], l1[3]);
-        *(uint32_t *)(dst + 64) = pack4(l2[0], l2[1], l2[2], l2[3]);
-        int sm = X[0] + X[1] + X[2] + X[3];
-        sm += __builtin_amdgcn_update_dpp(0, sm, 0xB1, 0xF, 0xF, false);
-        sm += __builtin_amdgcn_update_dpp(0, sm, 0x4E, 0xF, 0xF, false);
-        const uint32_t sub = tid & 7;
-        if (sub == 0) xv.xs[blk] = sc;
-        if ((sub & 3) == 0) xv.xsum[blk * 2 + (sub >> 2)] = (float)sm * sc;
+        const int X = xq_quant(v, inv);
+        int l0, l1, l2;
+        xq_limbs(X, l0, l1, l2);
+        const int sx = row16_sum_i(X);
+        if (lane < FX_RA) {
+            const uint32_t g = lane / 16, e = lane % 16;
+            act[(g * 3 + 0) * 16 + e] = (uint8_t)l0;
+            act[(g * 3 + 1) * 16 + e] = (uint8_t)l1;
+            act[(g * 3 + 2) * 16 + e] = (uint8_t)l2;
+            if (e == 0) {
+                ((float *)(act + 144))[g] = sc;
+                ((float *)(act + 156))[g] = -32.f * ((float)sx * sc);
+            }
+        }
     }
     lds_bar();
-    ZH_TRACE_POINT(13);
-    // lane: row (team) tid / 16 of a tile, half super-block tl = tid % 16
-    // (< 12) of the segment: super-block tl / 2, half tl % 2
-    const uint32_t team = tid / 16, tl = tid % 16;
-    const bool act = tl < FX_HB;
-    const uint32_t q = act ? tl : 0u, b = q >> 1, hh = q & 1, j0 = 4 * q;
-    uint32_t L[4][24];
-    float xs[4], z0[4], z1[4];
+    uint32_t A[3][3][4];
+    float axs[3], az[3];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        lds_load_limbs(L[k], (const uint8_t *)xv.limb + (j0 + k) * 96);
-        xs[k] = xv.xs[j0 + k];
-        z0[k] = -32.f * xv.xsum[2 * (j0 + k)];
-        z1[k] = -32.f * xv.xsum[2 * (j0 + k) + 1];
+    for (int g = 0; g < 3; g++) {
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const u32x4 q4 = *(const u32x4 *)(act + (g * 3 + k) * 16);
+            A[g][k][0] = q4.x; A[g][k][1] = q4.y; A[g][k][2] = q4.z; A[g][k][3] = q4.w;
+        }
+        axs[g] = ((const float *)(act + 144))[g];
+        az[g] = ((const float *)(act + 156))[g];
     }
-    ZH_TRACE_POINT(5);
-    for (uint32_t t = 0; t < FX_NT; t++) {
-        // copies after tile t's: tiles 1, 2 (t = 0); 2 (t = 1); 3 (t = 2)
-        static_assert(FX_NT == 4, "the ring schedule below");
-        if (wa) wait_vm_dyn((t == 0 ? 2u : t < 3 ? 1u : 0u) * (FX_TCH / 4));
+    ZH_TRACE_POINT(4);
+    // ---- down (units 6..13): thread tid takes row 512 (u - 6) + tid, its
+    // 44-byte record
+    float *part = (float *)(lds + FX_PART);
+    const bool g1b = (3 * w + 1) % 16 == 0;  // group 1 opens the second super-block
+    for (uint32_t u = FX_GT; u < FX_NU; u++) {
+        wait_vm_dyn(u + 1 < FX_NU ? cnt(u + 1) : 0u);
         lds_bar();
-        if (wa && t == 1) issue_d(3, 0);
-        ZH_TRACE_POINT(7 + t);
-        const uint8_t *slot = lds + (t % 3) * FX_SLOT;
-        const uint32_t boff = team * FX_RS + oh + b * 210;  // 2-byte aligned block start
-        const uint32_t sh = boff & 3;
-        uint32_t rq[17], rh[9], rs[3];
-        {
-            const uint32_t *a = (const uint32_t *)(slot + ((boff + 64 * hh) & ~3u));
+        if (u + 2 < FX_NU) issue(u + 2, (u + 2) % RG_D);
+        const uint32_t *rp = (const uint32_t *)(ring + (u % RG_D) * RG_TILE + tid * FX_REC);
+        uint32_t rc[11];
 #pragma unroll
-            for (int i = 0; i < 17; i++) rq[i] = a[i];
-            const uint32_t *c = (const uint32_t *)(slot + ((boff + 128 + 32 * hh) & ~3u));
+        for (int i = 0; i < 11; i++) rc[i] = rp[i];
+        float r3[3];
 #pragma unroll
-            for (int i = 0; i < 9; i++) rh[i] = c[i];
-            const uint32_t *sp = (const uint32_t *)(slot + ((boff + 192 + 8 * hh) & ~3u));
+        for (int g = 0; g < 3; g++) {
+            const uint32_t q0 = rc[3 * g], q1 = rc[3 * g + 1], qh = rc[3 * g + 2];
+            const uint32_t c[4] = {(q0 & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u),
+                                   ((q0 >> 4) & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u),
+                                   (q1 & 0x0F0F0F0Fu) | (qh & 0x30303030u),
+                                   ((q1 >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u)};
+            int D[3] = {0, 0, 0};
 #pragma unroll
-            for (int i = 0; i < 3; i++) rs[i] = sp[i];
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int k = 0; k < 3; k++) D[k] = sdot4(c[i], A[g][k][i], D[k]);
+            const float sc = (float)(int)(int8_t)((rc[9] >> (8 * g)) & 0xFF);
+            r3[g] = sc * fmaf(axs[g], comb_f(D[0], D[1], D[2]), az[g]);  // codes - 32 through az
         }
-        const uint32_t scw0 = __builtin_amdgcn_alignbyte(rs[1], rs[0], sh), scw1 = __builtin_amdgcn_alignbyte(rs[2], rs[1], sh);
-        const uint32_t dw = *(const uint16_t *)(slot + boff + 208);  // d (2-byte aligned)
-        float acc = 0.f;
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int qi = (g & 1) * 8 + i;
-                const uint32_t av = __builtin_amdgcn_alignbyte(rq[qi + 1], rq[qi], sh);
-                const uint32_t cv = __builtin_amdgcn_alignbyte(rh[i + 1], rh[i], sh);
-                const uint32_t lo4 = (g >> 1) ? ((av >> 4) & 0x0F0F0F0Fu) : (av & 0x0F0F0F0Fu);
-                const uint32_t hi2 = ((cv >> (2 * g)) << 4) & 0x30303030u;
-                const uint32_t qv = lo4 | hi2;  // unsigned code; the -32 offset enters through z0 / z1
-                const int grp = i >> 2;
-#pragma unroll
-                for (int k = 0; k < 3; k++) D[grp][k] = sdot4(qv, L[g][k * 8 + i], D[grp][k]);
-            }
-            const uint32_t sw = g >> 1 ? scw1 : scw0;
-            const int sc0 = (int)(int8_t)((sw >> (16 * (g & 1))) & 0xFF);  // scales[8 hh + 2 g]
-            const int sc1 = (int)(int8_t)((sw >> (16 * (g & 1) + 8)) & 0xFF);
-            const float S0 = comb_f(D[0][0], D[0][1], D[0][2]);
-            const float S1 = comb_f(D[1][0], D[1][1], D[1][2]);
-            acc = fmaf((float)sc0, fmaf(xs[g], S0, z0[g]), acc);
-            acc = fmaf((float)sc1, fmaf(xs[g], S1, z1[g]), acc);
-        }
-        float res = act ? h2f(dw) * acc : 0.f;
-        res = team_sum_dpp<16>(res);
-        if (!ok) res = __builtin_nanf("");  // the slices' wait gave up
-        if (tl == 0)
-            __hip_atomic_fetch_add(P.acc + j * FX_RB + t * FX_TR + team, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float da = h2f(rc[10]), db = h2f(rc[10] >> 16);
+        part[(u - FX_GT) * FX_DR + tid] = fmaf(da, r3[0], fmaf(g1b ? db : da, r3[1], db * r3[2]));
     }
+    lds_bar();
+    ZH_TRACE_POINT(5);
+    // ---- publish the 4096 partials in the XCD's L2, then the flag
+    {
+        float *dst = P.part + (size_t)w * FX_H;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t e0 = (i * RG_T + tid) * 4;
+            *(f32x4 *)(dst + e0) = *(const f32x4 *)(part + e0);
+        }
+    }
+    wait_vm<0>();
+    __syncthreads();
+    if (tid == 0) *(volatile uint32_t *)(fl + j) = E;
+    const bool ok = xcd_wait(fl, XCD_PER, E, P.ctl, tid);
     ZH_TRACE_POINT(6);
+    if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the XCD has read the epoch
+    // ---- rows [128 j, +128) of the XCD's 32 partials (16 KB) into ring
+    // slot 0: copy c holds partials 2c and 2c + 1
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t c = wave + 8 * i, pi = 2 * c + lane / 32;
+        dma16_dev(P.part + (size_t)(h * XCD_PER + pi) * FX_H + j * FX_RROWS + (lane % 32) * 4, lds0 + c * 1024);
+    }
+    wait_vm<0>();
+    lds_bar();
+    {
+        const float *rs = (const float *)lds;  // [32 partials][128 rows]
+        const uint32_t r = tid / 4, q = tid % 4;
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) s += rs[(q * 8 + k) * FX_RROWS + r];
+        s = team_sum_dpp<4>(s);
+        if (!ok) s = __builtin_nanf("");  // the partials' wait gave up
+        if (q == 0) __hip_atomic_fetch_add(P.acc + j * FX_RROWS + r, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ZH_TRACE_POINT(7);
 }
 
 ZH_TRACE_DUMP_FN(zh_debug_trace_ffn)
 
+// Packs ffn_down (Q6_K [4096][12288]) into the per-workgroup column records
+// k_ffn_xcd reads: one thread per (workgroup w, row r).
+__global__ void k_ffn_pack_down(const uint8_t *q6, uint8_t *pk) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= XCD_N * XCD_PER * FX_H) return;
+    const uint32_t w = gid / FX_H, r = gid % FX_H;
+    const uint8_t *row = q6 + (size_t)r * (FX_F / 256) * 210;
+    uint32_t rec[11] = {};
+    for (uint32_t g = 0; g < 3; g++) {
+        const uint32_t G = 3 * w + g, sb = G / 16, e0 = (G % 16) * 16;  // 16 elements of super-block sb
+        const uint8_t *blk = row + sb * 210;
+        uint32_t q0 = 0, q1 = 0, qh = 0;
+        for (uint32_t e = 0; e < 16; e++) {
+            // Q6_K element x of a super-block: half n = x / 128, sub-block
+            // s = (x % 128) / 32, i = x % 32: low 4 bits from
+            // ql[64 n + 32 (s & 1) + i] (nibble s >> 1), high 2 bits from
+            // qh[32 n + i] >> 2 s
+            const uint32_t x = e0 + e, n = x / 128, s = (x % 128) / 32, i = x % 32;
+            const uint32_t lo = (blk[64 * n + 32 * (s & 1) + i] >> (4 * (s >> 1))) & 0xF;
+            const uint32_t hi = (blk[128 + 32 * n + i] >> (2 * s)) & 3;
+            // record: elements 0-3 in the low nibbles of q0's bytes, 4-7 in
+            // the high nibbles; 8-15 likewise in q1; high pairs in byte e % 4
+            // of qh, bits 2 (e / 4)
+            if (e < 8) q0 |= lo << (8 * (e % 4) + 4 * (e / 4));
+            else q1 |= lo << (8 * (e % 4) + 4 * ((e - 8) / 4));
+            qh |= hi << (8 * (e % 4) + 2 * (e / 4));
+        }
+        rec[3 * g] = q0;
+        rec[3 * g + 1] = q1;
+        rec[3 * g + 2] = qh;
+        rec[9] |= (uint32_t)blk[192 + G % 16] << (8 * g);  // int8 scale of the 16 elements
+    }
+    const uint8_t *ba = row + ((3 * w) / 16) * 210, *bb = row + ((3 * w + 2) / 16) * 210;
+    rec[10] = (uint32_t)ba[208] | ((uint32_t)ba[209] << 8) | ((uint32_t)bb[208] << 16) | ((uint32_t)bb[209] << 24);
+    uint32_t *dst = (uint32_t *)(pk + (size_t)w * FX_SLICE + (size_t)r * FX_REC);
+    for (int i = 0; i < 11; i++) dst[i] = rec[i];
+}
+
 uint32_t zhk_ffn_xcd_flag_words() { return FX_FLAG_WORDS; }
+uint64_t zhk_ffn_pack_bytes() { return (uint64_t)XCD_N * XCD_PER * FX_SLICE; }
+uint64_t zhk_ffn_part_bytes() { return (uint64_t)XCD_N * XCD_PER * FX_H * 4; }
 
 bool zhk_ffn_xcd_supported(zh_ctx *c, uint32_t hidden, uint32_t ffn) {
     return hidden == FX_H && ffn == FX_F && !c->concurrent && zhk_xcd_round_robin(c);
 }
 
+int zhk_ffn_pack_down(zh_ctx *c, const uint8_t *q6, uint8_t *pk) {
+    const uint32_t n = XCD_N * XCD_PER * FX_H;
+    hipLaunchKernelGGL(k_ffn_pack_down, dim3((n + 255) / 256), dim3(256), 0, c->stream, q6, pk);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
 int zhk_ffn_xcd(zh_ctx *c, const float *xa, const float *xb, const float *norm_w, float eps, const uint8_t *wg,
-                const uint8_t *wu, const uint8_t *wd, float *s, float *xout, float *acc, float *zero,
+                const uint8_t *wu, const uint8_t *pk, float *part, float *xout, float *acc, float *zero,
                 uint32_t *flags) {
     if (((uintptr_t)xa & 15) || ((uintptr_t)xb & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wg & 15) ||
-        ((uintptr_t)wu & 15) || ((uintptr_t)wd & 15) || ((uintptr_t)s & 15) || ((uintptr_t)xout & 15) || !acc || !zero)
+        ((uintptr_t)wu & 15) || ((uintptr_t)pk & 15) || ((uintptr_t)part & 15) || ((uintptr_t)xout & 15) || !acc ||
+        !zero)
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "ffn_xcd: 16-byte aligned operands");
     FfnP P = {};
-    P.xa = xa; P.xb = xb; P.norm_w = norm_w; P.eps = eps; P.wg = wg; P.wu = wu; P.wd = wd;
-    P.pre = (uint32_t)min(max(zh_knob_int("ZH_FFN_PRE", 3), 1), 3);
-    P.late = (uint32_t)zh_knob_int("ZH_FFN_LATE", 0);
-    P.plain = (uint32_t)zh_knob_int("ZH_FFN_PLAIN", 0);
-    P.s = s; P.xout = xout; P.acc = acc; P.zero = zero; P.flags = flags; P.ctl = c->err_dev;
+    P.xa = xa; P.xb = xb; P.norm_w = norm_w; P.eps = eps; P.wg = wg; P.wu = wu; P.pk = pk;
+    P.part = part; P.xout = xout; P.acc = acc; P.zero = zero; P.flags = flags; P.ctl = c->err_dev;
     static bool attr = false;
     if (!attr) {
         ZH_HIP(c, hipFuncSetAttribute((const void *)k_ffn_xcd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)RG_LDS));

@@ -241,11 +241,16 @@ int zhk_qkv_attn(zh_ctx *ctx, const uint8_t *wq, const uint8_t *wk, const uint8_
 // per workgroup); x_acc starts at zero (it is not x's copy), `zero` (H
 // floats) is cleared. Per-XCD FFN (zh_ffn_xcd.hip) with the same split
 // residual: xa + xb in, xout = xa + xb, the down projection added into acc,
-// `zero` cleared; hidden 4096, FFN 12288, Q4_K gate/up, Q6_K down.
+// `zero` cleared; hidden 4096, FFN 12288, Q4_K gate/up, Q6_K down (read from
+// the copy zhk_ffn_pack_down makes, zhk_ffn_pack_bytes per layer); `part`:
+// zhk_ffn_part_bytes of scratch.
 bool zhk_ffn_xcd_supported(zh_ctx *ctx, uint32_t hidden, uint32_t ffn);
 uint32_t zhk_ffn_xcd_flag_words();
+uint64_t zhk_ffn_pack_bytes();
+uint64_t zhk_ffn_part_bytes();
+int zhk_ffn_pack_down(zh_ctx *ctx, const uint8_t *q6k_down, uint8_t *packed);
 int zhk_ffn_xcd(zh_ctx *ctx, const float *xa, const float *xb, const float *norm_w, float eps, const uint8_t *wg,
-                const uint8_t *wu, const uint8_t *wd, float *s, float *xout, float *acc, float *zero,
+                const uint8_t *wu, const uint8_t *packed, float *part, float *xout, float *acc, float *zero,
                 uint32_t *flags);
 // wo != nullptr (4 q heads per kv head): also the O projection, added into
 // x_acc with device atomics; x must then be a copy of x_acc (x_acc changes
