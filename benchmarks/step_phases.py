@@ -19,6 +19,11 @@ step, replayed by zh_engine_time_kernel.
 
 --ffn: the per-XCD FFN launch (k_ffn_xcd).
 
+--moe: the per-XCD MoE FFN launch of config 4's model (k_moe_xcd).
+
+--moe-attn: the attention launch of config 4's model (4 kv heads, 8 q heads
+each, identity pages, KV context 8192).
+
 --standalone: the same attention body as its own kernel (the per-phase
 step with a shuffled page table, i.e. k_attn_ring), its launches replayed by
 zh_engine_time_kernel; points relative to each workgroup's start.
@@ -32,7 +37,7 @@ import sys
 import numpy as np
 
 from zinc_amd import hip
-from zinc_amd.engine import DENSE_8B, InferenceEngine
+from zinc_amd.engine import DENSE_8B, MOE_48L, InferenceEngine
 
 ATTN_POINTS = {1: "small copies landed", 9: "q fragments", 10: "new K/V row ready", 5: "ring step 0 start",
                6: "ring step 0 end", 7: "ring step 1 start", 8: "ring step 1 end", 2: "after the ring",
@@ -51,16 +56,18 @@ def print_attn(ta):
         print(f"  {ATTN_POINTS[s]:22s}: n={m.sum():3d}  min {r.min():6.2f}  p50 {np.median(r):6.2f}  max {r.max():6.2f}")
 
 
-def standalone():
+def standalone(moe=False):
     L = hip.lib()
     L.zh_debug_trace_ops.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
     ctx = hip.Context(0)
-    cfg = dict(DENSE_8B)
-    cfg["max_ctx"] = 4096 + 64
+    cfg = dict(MOE_48L if moe else DENSE_8B)
+    ctxlen = 8192 if moe else 4096
+    cfg["max_ctx"] = ctxlen + 64
     eng = InferenceEngine(ctx, cfg)
-    eng.set_pages(np.random.default_rng(17).permutation(cfg["max_ctx"] // 16).astype(np.uint32))
-    eng.prefill_kv_random(4096, 7)
-    eng.generate([17, 18], 2, start_pos=4096)
+    if not moe:
+        eng.set_pages(np.random.default_rng(17).permutation(cfg["max_ctx"] // 16).astype(np.uint32))
+    eng.prefill_kv_random(ctxlen, 7)
+    eng.generate([17, 18], 2, start_pos=ctxlen)
     ctx.sync()
     n = 8192 * 16
     a = np.zeros(n, np.uint64)
@@ -121,21 +128,26 @@ FFN_POINTS = ["start", "activation landed", "XQ limbs in registers", "gate/up do
               "down done", "partials seen", "end", "", "", "", "gate/up tile 0 in LDS"]
 
 
+MOE_POINTS = ["start", "x, norm, router rows landed", "router logits of the XCD seen", "top-8 selected",
+              "gate/up done", "down done", "partials seen", "end"]
+
+
 TILE_POINTS = ["start", "activation staged", "batch 0 in LDS", "batch 1", "batch 2", "batch 3", "batch 4+", "end"]
 
 
-def ring(group, dump="zh_debug_trace_ring", points=None):
+def ring(group, dump="zh_debug_trace_ring", points=None, moe=False):
     """Per-workgroup timeline of a ring DMMV launch group (zh_ring_q4k.h) or,
     with dump="zh_debug_trace_lpb", of a tile kernel (zh_dmmv_lpb.hip)."""
     points = points or RING_POINTS
     L = hip.lib()
     getattr(L, dump).argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
     ctx = hip.Context(0)
-    cfg = dict(DENSE_8B)
-    cfg["max_ctx"] = 4096 + 64
+    cfg = dict(MOE_48L if moe else DENSE_8B)
+    ctxlen = 8192 if moe else 4096
+    cfg["max_ctx"] = ctxlen + 64
     eng = InferenceEngine(ctx, cfg)
-    eng.prefill_kv_random(4096, 7)
-    eng.generate([17, 18], 2, start_pos=4096)
+    eng.prefill_kv_random(ctxlen, 7)
+    eng.generate([17, 18], 2, start_pos=ctxlen)
     ctx.sync()
     n = 8192 * 16
     a = np.zeros(n, np.uint64)
@@ -163,10 +175,14 @@ def main():
         sys.exit("set ZH_LIB_PATH to the debug build's libzinc_hip.so")
     if "--standalone" in sys.argv[1:]:
         return standalone()
+    if "--moe-attn" in sys.argv[1:]:
+        return standalone(moe=True)
     if "--qkv-attn" in sys.argv[1:]:
         return qkv_attn()
     if "--ring" in sys.argv[1:]:
         return ring(sys.argv[sys.argv.index("--ring") + 1])
+    if "--moe" in sys.argv[1:]:
+        return ring("ffn", "zh_debug_trace_moe", MOE_POINTS, moe=True)
     if "--ffn" in sys.argv[1:]:
         return ring("ffn", "zh_debug_trace_ffn", FFN_POINTS)
     if "--tile" in sys.argv[1:]:

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libzinc_hip.so")
-SOURCES = ["zh_runtime.hip", "zh_dmmv.hip", "zh_dmmv_lpb.hip", "zh_dmmv_ring.hip", "zh_dmmv_batched.hip", "zh_ops.hip", "zh_engine.hip", "zh_step.hip", "zh_qkv_attn.hip", "zh_ffn_xcd.hip", "zh_prefill.hip",
+SOURCES = ["zh_runtime.hip", "zh_dmmv.hip", "zh_dmmv_lpb.hip", "zh_dmmv_ring.hip", "zh_dmmv_batched.hip", "zh_ops.hip", "zh_engine.hip", "zh_step.hip", "zh_qkv_attn.hip", "zh_ffn_xcd.hip", "zh_moe_xcd.hip", "zh_prefill.hip",
            "zh_gguf.cpp", "zh_sample.hip"]
 ARCH = os.environ.get("ZH_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -424,6 +424,7 @@ struct DmmvP {
     const uint8_t *segW[3];
     float *segY[3];
     uint32_t seg_end[3];
+    float *ycopy;  // plain mode, one matrix: the outputs also stored here
 };
 
 enum { MODE_PLAIN = 0, MODE_GATE_UP = 1 };
@@ -562,6 +563,7 @@ __global__ __launch_bounds__(NW == 1 ? 256 : NW * 64) void k_dmmv(DmmvP p) {
                 float out = res;
                 if (p.acc) out += yb[rr0 + idx];
                 yb[rr0 + idx] = out;
+                if (p.ycopy) p.ycopy[rr0 + idx] = out;
             }
         }
     }
@@ -646,7 +648,14 @@ static int try_ftile(zh_ctx *c, uint32_t qtype, const uint8_t *W, const void *xq
                      uint32_t M, uint32_t K, uint32_t acc);
 
 int zhk_dmmv(zh_ctx *c, uint32_t qtype, const uint8_t *W, const void *xq, float *y, uint32_t M,
-             uint32_t K, uint32_t acc) {
+             uint32_t K, uint32_t acc, float *ycopy) {
+    if (ycopy) {  // the team kernel writes the copy
+        DmmvP p = {};
+        p.W = W; p.W2 = W; p.xq = (const uint8_t *)xq; p.y = y; p.M = M; p.K = K;
+        p.row_bytes = zh_tensor_bytes(qtype, 1, K); p.acc = acc; p.ycopy = ycopy;
+        p.nseg = 1; p.segW[0] = W; p.segY[0] = y; p.seg_end[0] = M;
+        return launch_dmmv<MODE_PLAIN, false>(c, qtype, p, 1);
+    }
     if (qtype == ZH_MXFP4) {  // (Q8_0 on an XQ activation: the team kernel measured faster, 7.0 vs 8.5 us at 4096^2)
         const int rc = zhk_dmmv_fring(c, qtype, 1, &W, &y, &M, nullptr, nullptr, 0.f, xq, K, acc);
         if (rc >= 0) return rc;

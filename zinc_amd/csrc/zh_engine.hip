@@ -86,6 +86,11 @@ struct zh_engine {
     uint8_t *down_pk = nullptr;
     bool pk_stale = true;
     float *ffn_part = nullptr;
+    // the per-XCD MoE FFN (k_moe_xcd): flags, scratch (partials, logits) and
+    // its packed copy of every layer's expert down matrices
+    uint32_t *moe_flags = nullptr;
+    float *moe_scratch = nullptr;
+    uint8_t *moe_pk = nullptr;
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
@@ -349,6 +354,8 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->ffn_flags, 4ull * zhk_ffn_xcd_flag_words()}, {(void **)&e->rres, 8ull * H},
         {(void **)&e->dres, 12ull * H},
         {(void **)&e->ffn_part, c.ffn == 12288 && H == 4096 ? zhk_ffn_part_bytes() : 0ull},
+        {(void **)&e->moe_flags, 4ull * zhk_moe_xcd_flag_words()},
+        {(void **)&e->moe_scratch, c.n_experts ? zhk_moe_part_bytes() : 0ull},
     };
     uint64_t aoff = 0;
     for (auto &a : acts) aoff = align256(aoff + a.bytes);
@@ -534,6 +541,7 @@ extern "C" void zh_engine_destroy(zh_engine *e) {
     if (e->act_arena) hipFree(e->act_arena);
     if (e->pf.arena) hipFree(e->pf.arena);
     if (e->down_pk) hipFree(e->down_pk);
+    if (e->moe_pk) hipFree(e->moe_pk);
     delete e;
 }
 
@@ -755,9 +763,41 @@ static bool step_xcd(zh_engine *e) {
            step_qa_o(e);
 }
 
-// The per-XCD FFN's packed ffn_down of every layer: allocated on first use,
-// rewritten from the arena when it may have changed (outside any capture).
+// Whether every layer's MoE FFN runs as one per-XCD launch (k_moe_xcd): the
+// O projection then also writes the residual into e->xin, which the launch
+// reads while it adds into e->hidden.
+static bool step_moe(zh_engine *e) {
+    const zh_model_config &m = e->c;
+    if (!e->fused_ffn || zh_knob("ZH_NO_MOE_XCD") || zh_knob("ZH_NO_LDS_DMMV") || m.n_experts == 0 ||
+        !zhk_moe_xcd_supported(e->ctx, m.hidden, m.n_experts, m.n_experts_used, m.expert_ffn))
+        return false;
+    const uint32_t qd = m.n_heads * m.head_dim;
+    for (const Layer &y : e->L)
+        if (y.router.type != ZH_Q8_0 || y.egate.type != ZH_Q4_K || y.eup.type != ZH_Q4_K || y.edown.type != ZH_Q4_K ||
+            y.ffn_norm.off % 16 || y.router.off % 16 || y.egate.off % 16 || y.eup.off % 16 ||
+            (!zh_knob("ZH_NO_LPB") && zhk_lpb_supported(y.wo.type, qd)))
+            return false;
+    return true;
+}
+
+// The per-XCD launches' packed copies (ffn_down; the experts' down
+// matrices) of every layer: allocated on first use, rewritten from the arena
+// when it may have changed (outside any capture).
 static int ensure_packed(zh_engine *e) {
+    if (step_moe(e)) {
+        const uint64_t per = zhk_moe_pack_bytes();
+        if (!e->moe_pk && hipMalloc((void **)&e->moe_pk, per * e->c.n_layers) != hipSuccess) {
+            e->moe_pk = nullptr;
+            return zh_set_err(e->ctx, ZH_ERR_OUT_OF_MEMORY, "packed expert down (%llu B)",
+                              (unsigned long long)(per * e->c.n_layers));
+        }
+        if (e->pk_stale) {
+            for (uint32_t l = 0; l < e->c.n_layers; l++)
+                ERC(zhk_moe_pack_down(e->ctx, e->arena + e->L[l].edown.off, e->moe_pk + per * l));
+            e->pk_stale = false;
+        }
+        return ZH_OK;
+    }
     if (!step_xcd(e)) return ZH_OK;
     const uint64_t per = zhk_ffn_pack_bytes();
     if (!e->down_pk && hipMalloc((void **)&e->down_pk, per * e->c.n_layers) != hipSuccess) {
@@ -803,6 +843,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     const bool persistent = whole && step_args(e, sa);
     const bool qa_o = !persistent && step_qa_o(e);
     const bool xl = qa_o && step_xcd(e);
+    const bool moe_x = !persistent && step_moe(e);
     float *const D = e->dres;
     auto dr = [&](uint32_t k) { return D + (size_t)(k % 3) * H; };
     // embedToken (forward.zig:4255-4290), on the device.
@@ -887,7 +928,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             ERC(zhk_dmmv_lpb(c, y.wo.type, 0, 1, &wo, nullptr, &yo, &mo, nullptr, nullptr, 0.f, nullptr, qd, 1,
                              e->xq_q));
         } else {
-            ERC(zhk_dmmv(c, y.wo.type, W(y.wo), e->xq_q, e->hidden, H, qd, 1));
+            ERC(zhk_dmmv(c, y.wo.type, W(y.wo), e->xq_q, e->hidden, H, qd, 1, moe_x ? e->xin : nullptr));
         }
         if (lpb_ffn && xl && (mask & SK_FFN_IN) && (mask & SK_FFN_OUT)) {
             // ffn_norm, gate/up + SwiGLU and down in one launch, split by XCD
@@ -915,6 +956,14 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
                 ERC(zhk_dmmv_lpb(c, y.down.type, 0, 1, &wd, nullptr, &yd, &mh, swiglu_xq ? nullptr : e->s,
                                  nullptr, 0.f, nullptr, m.ffn, 1, swiglu_xq ? e->xq_f : nullptr, nullptr, nullptr,
                                  qa_o ? e->xin : nullptr));
+            continue;
+        }
+        if (moe_x && (mask & SK_FFN_IN) && (mask & SK_FFN_OUT)) {
+            // ffn_norm, router, top-k, the selected experts and the weighted
+            // sum in one launch, one expert per XCD
+            ERC(zhk_moe_xcd(c, e->xin, Wf(y.ffn_norm), m.eps, W(y.router), W(y.egate), W(y.eup),
+                            e->moe_pk + zhk_moe_pack_bytes() * l, e->hidden, e->moe_scratch, e->routing,
+                            e->moe_flags));
             continue;
         }
         if (lds_moe) {
@@ -1510,7 +1559,11 @@ extern "C" uint64_t zh_engine_group_bytes(zh_engine *e, uint32_t group, uint32_t
     case SK_ATTN:
         return 2 * kvd * 2 * Lctx + (qd + 2 * kvd) * 4 + 2 * hd * 4 + hd * 4 + 2 * kvd * 2 + qd * 4 + xqb(qd);
     case SK_O: return y.wo.bytes + xqb(qd) + 2 * H * 4;
-    case SK_FFN_IN | SK_FFN_OUT:  // one launch (k_ffn_xcd): x = two vectors in, one out, the sums added into a third
+    case SK_FFN_IN | SK_FFN_OUT:
+        // MoE (k_moe_xcd): the router, the selected experts, x and norm in, the sums added into y
+        if (c.n_experts)
+            return y.router.bytes + k * 3 * zh_tensor_bytes(y.egate.type, (uint32_t)F, (uint32_t)H) + 4 * H * 4;
+        // dense (k_ffn_xcd): x = two vectors in, one out, the sums added into a third
         return y.gate.bytes + y.up.bytes + y.down.bytes + 5 * H * 4;
     case SK_FFN_IN:
         if (c.n_experts == 0) return y.gate.bytes + y.up.bytes + 2 * H * 4 + F * 4 + xqb(F);

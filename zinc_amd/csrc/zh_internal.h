@@ -92,7 +92,7 @@ static inline uint64_t zh_xq_bytes_int(uint32_t K) { return (uint64_t)(K / 32) *
 int zhk_quantize_xq(zh_ctx *ctx, const float *x, void *xq, uint32_t K, uint32_t n_vec,
                     uint32_t x_stride);
 int zhk_dmmv(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, const void *xq, float *y, uint32_t M,
-             uint32_t K, uint32_t acc);
+             uint32_t K, uint32_t acc, float *ycopy = nullptr);  // ycopy: the outputs also stored there
 // Up to three stacked matrices sharing K and x (e.g. Q, K, V) in one launch.
 int zhk_dmmv_multi(zh_ctx *ctx, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, float *const *y,
                    const uint32_t *M, const void *xq, uint32_t K);
@@ -249,6 +249,17 @@ uint32_t zhk_ffn_xcd_flag_words();
 uint64_t zhk_ffn_pack_bytes();
 uint64_t zhk_ffn_part_bytes();
 int zhk_ffn_pack_down(zh_ctx *ctx, const uint8_t *q6k_down, uint8_t *packed);
+// Per-XCD MoE FFN (zh_moe_xcd.hip): hidden 2048, 128 experts top-8, expert FFN
+// 768, Q8_0 router, Q4_K experts (the down matrices from zhk_moe_pack_down's
+// copy); x is a copy of y taken before the launch; scratch: zhk_moe_part_bytes.
+bool zhk_moe_xcd_supported(zh_ctx *ctx, uint32_t hidden, uint32_t n_experts, uint32_t n_used, uint32_t expert_ffn);
+uint32_t zhk_moe_xcd_flag_words();
+uint64_t zhk_moe_pack_bytes();
+uint64_t zhk_moe_part_bytes();
+int zhk_moe_pack_down(zh_ctx *ctx, const uint8_t *q4k_edown, uint8_t *packed);
+int zhk_moe_xcd(zh_ctx *ctx, const float *x, const float *norm_w, float eps, const uint8_t *router,
+                const uint8_t *egate, const uint8_t *eup, const uint8_t *packed, float *y, float *scratch,
+                uint32_t *routing, uint32_t *flags);
 int zhk_ffn_xcd(zh_ctx *ctx, const float *xa, const float *xb, const float *norm_w, float eps, const uint8_t *wg,
                 const uint8_t *wu, const uint8_t *packed, float *part, float *xout, float *acc, float *zero,
                 uint32_t *flags);

@@ -1,0 +1,465 @@
+// zh_moe_xcd.hip — the sparse-MoE FFN of one decode layer (ffn_norm, router
+// + top-k, the selected experts' gate/up + SwiGLU and down, the weighted sum
+// added to the residual) in one launch, one selected expert per XCD (hidden
+// 2048, 128 experts, top-8, expert FFN 768; Q8_0 router, Q4_K experts).
+//
+// Replaces five dispatches of the reference's MoE decode step: ffn_norm, the
+// router DMMV, softmax_topk, the experts' gate/up/SwiGLU and down DMMVs and
+// the weighted accumulation (forward.zig:5958-6500; softmax_topk_v2.comp,
+// dmmv_q4k.comp, moe_weighted_acc.comp).
+//
+// The 32 workgroups of XCD h (zh_xcd.h; slot j):
+//   1. stage ffn_norm(x) as XQ limbs and compute router rows [4 j, 4 j + 4)
+//      (every XCD computes all 128 logits, bit-identically, from the same
+//      bytes), publish them in the XCD's L2 and meet at an XCD-local flag
+//      barrier;
+//   2. every workgroup selects the top 8 of the 128 logits itself (the
+//      lowest index wins ties; weights: softmax over the selected logits) —
+//      XCD h takes the h-th selected expert e and its weight;
+//   3. workgroup j: gate and up rows [24 j, 24 j + 24) of expert e and their
+//      SwiGLU, then expert e's down columns [24 j, 24 j + 24) for all 2048
+//      rows (a repacked copy of the down matrices, 24-byte row records) into
+//      2048 partial sums — gate/up and down tiles stream through one
+//      three-slot LDS ring of asynchronous copies;
+//   4. the XCD's 32 partial vectors meet in the L2 (second flag barrier) and
+//      workgroup j adds rows [64 j, 64 j + 64) of their sum, times the
+//      expert's weight, into the residual with device atomics.
+// Every exchange stays inside an XCD; the only device-wide traffic is the
+// final atomics (8 per row, one per expert).
+//
+// x is a copy of the residual taken before the launch (the O projection
+// writes both): y changes during the launch.
+#include "zh_ring_q4k.h"
+#include "zh_xcd.h"
+
+namespace {
+constexpr uint32_t MX_H = 2048, MX_E = 128, MX_K = 8, MX_F = 768;
+constexpr uint32_t MX_NB = MX_H / 256;                 // Q4_K super-blocks per gate/up row (8)
+constexpr uint32_t MX_RROW = MX_H / 32 * 34;           // router row bytes (Q8_0, 2176)
+constexpr uint32_t MX_RPW = MX_E / XCD_PER;            // router rows per workgroup (4)
+constexpr uint32_t MX_FR = MX_F / XCD_PER;             // FFN rows per workgroup (24)
+constexpr uint32_t MX_REC = 24;                        // packed down record per row and workgroup
+constexpr uint32_t MX_SLICE = MX_H * MX_REC;           // one workgroup's down columns of one expert (48 KB)
+constexpr uint32_t MX_DR = 512;                        // down rows per tile (one per thread)
+constexpr uint32_t MX_DT = MX_H / MX_DR;               // down tiles (4)
+constexpr uint32_t MX_DTB = MX_DR * MX_REC;            // 12 KB
+constexpr uint32_t MX_DCH = MX_DTB / 1024;             // its 1 KB copies (12)
+constexpr uint32_t MX_GT = 2;                          // gate/up tiles (24 rows, 16 per pass)
+constexpr uint32_t MX_NU = MX_GT + MX_DT;
+constexpr uint32_t MX_RR = MX_H / XCD_PER;             // residual rows each workgroup reduces (64)
+constexpr uint32_t MX_RT = (RG_D - 1) * RG_TILE;       // router rows staged in the third ring slot
+constexpr uint32_t MX_ACT = RG_D * RG_TILE + 8192;     // SwiGLU limbs (beyond the 7.2 KB XQ image)
+constexpr uint32_t MX_RAW = RG_D * RG_TILE + RG_XQ_BYTES;  // x | norm staging, then the partials
+static_assert(MX_RPW * MX_RROW <= 9 * 1024 && MX_DTB % 1024 == 0, "router rows in 9 copies; whole down copies");
+static_assert(MX_NB * 2 * RG_SEG + MX_NB * 8 * 12 <= 8192, "XQ image below the SwiGLU limbs");
+}  // namespace
+
+// Flag words (zero when the engine is created): [0, 256) router rows
+// published, [256, 512) partials published (XCD h at h * 32), [512, 520)
+// epochs.
+constexpr uint32_t MX_FLAG_WORDS = 2 * XCD_N * XCD_PER + XCD_N;
+
+struct MoeP {
+    const float *x;               // residual copy
+    const float *norm_w;          // ffn_norm weight
+    float eps;
+    const uint8_t *router;        // Q8_0 [128][2048]
+    const uint8_t *egate, *eup;   // Q4_K [128][768][2048]
+    const uint8_t *pk;            // packed down [128][32][2048][24 B]
+    float *y;                     // residual: += sum_k w_k down_k
+    float *logits;                // [8 XCDs][128] router logits (exchanged inside each XCD)
+    float *part;                  // [256][2048] partial sums (exchanged inside each XCD)
+    uint32_t *routing;            // [ids x 8][weights x 8], written by workgroup 0 (for inspection)
+    uint32_t *flags;              // MX_FLAG_WORDS
+    uint32_t *ctl;                // [0] error word, [1] wait limit
+};
+
+ZH_DEV int row8_sum_i(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    return v + __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+}
+
+__global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ uint32_t s_route[2 * MX_K];
+    constexpr int NB = MX_NB, MODE = LPB_GATE_UP;
+    using TT = Q4Tiles<NB, MODE>;
+    constexpr int TL = TT::TL, RPP = TT::RPP;
+    constexpr uint32_t NBLK = NB * 8;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t h = min(xcc_id(), XCD_N - 1), j = blockIdx.x / XCD_N, w = h * XCD_PER + j;
+    uint32_t *fl_r = P.flags + h * XCD_PER, *fl_p = P.flags + XCD_N * XCD_PER + h * XCD_PER;
+    uint32_t *ep = P.flags + 2 * XCD_N * XCD_PER + h;
+    const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
+    const uint32_t lds0 = lds_addr(lds);
+    uint8_t *ring = lds, *xqa = lds + RG_D * RG_TILE, *raw = lds + MX_RAW;
+    float *yl = (float *)(lds + RG_D * RG_TILE + RG_XQ_BYTES + RG_RAW_BYTES), *red = yl + 2 * RG_MAXROWS;
+    ZH_TRACE_POINT(0);
+
+    // ---- x, the norm weight (8 KB each: one copy per wave) and this
+    // workgroup's router rows (8.5 KB: 9 copies, the last clamped)
+    dma16((const uint8_t *)P.x + wave * 1024 + lane * 16, lds0 + MX_RAW + wave * 1024);
+    dma16((const uint8_t *)P.norm_w + wave * 1024 + lane * 16, lds0 + MX_RAW + NB * 1024 + wave * 1024);
+    {
+        const uint8_t *rr = P.router + (size_t)j * MX_RPW * MX_RROW;
+        for (uint32_t c = wave; c < 9; c += 8)
+            dma16(rr + min(c * 1024 + lane * 16, MX_RPW * MX_RROW - 16), lds0 + MX_RT + c * 1024);
+    }
+    wait_vm<0>();
+    lds_bar();
+    ZH_TRACE_POINT(1);
+    // ---- ffn_norm(x) as the XQ image (4 elements per thread)
+    float *ixs = (float *)(xqa + NB * 2 * RG_SEG), *ixz = ixs + NBLK;
+    {
+        const float *xr = (const float *)raw, *wr = xr + MX_H;
+        const uint32_t e0 = tid * 4;
+        f32x4 v = *(const f32x4 *)(xr + e0);
+        const f32x4 wn = *(const f32x4 *)(wr + e0);
+        float sq = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w)));
+        sq = wave_sum(sq);
+        if (lane == 0) red[wave] = sq;
+        lds_bar();
+        float tot = 0.f;
+#pragma unroll
+        for (int w8 = 0; w8 < 8; w8++) tot += red[w8];
+        const float rms_inv = 1.0f / sqrtf(tot / (float)MX_H + P.eps);
+        v.x = wn.x * (v.x * rms_inv); v.y = wn.y * (v.y * rms_inv);
+        v.z = wn.z * (v.z * rms_inv); v.w = wn.w * (v.w * rms_inv);
+        const float a = row8_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        float inv, sc;
+        xq_scales(a, inv, sc);
+        int X[4] = {xq_quant(v.x, inv), xq_quant(v.y, inv), xq_quant(v.z, inv), xq_quant(v.w, inv)};
+        int l0[4], l1[4], l2[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) xq_limbs(X[q], l0[q], l1[q], l2[q]);
+        const uint32_t blk = e0 / 32, lo = e0 % 32;
+        uint8_t *dst = xqa + (blk / 4) * RG_SEG + (blk % 4) * 96 + lo;
+        *(uint32_t *)(dst) = pack4(l0[0], l0[1], l0[2], l0[3]);
+        *(uint32_t *)(dst + 32) = pack4(l1[0], l1[1], l1[2], l1[3]);
+        *(uint32_t *)(dst + 64) = pack4(l2[0], l2[1], l2[2], l2[3]);
+        int sm = X[0] + X[1] + X[2] + X[3];
+        sm += __builtin_amdgcn_update_dpp(0, sm, 0xB1, 0xF, 0xF, false);
+        sm += __builtin_amdgcn_update_dpp(0, sm, 0x4E, 0xF, 0xF, false);
+        const uint32_t sub = tid & 7;
+        if (sub == 0) ixs[blk] = sc;
+        if ((sub & 3) == 0) ixz[blk * 2 + (sub >> 2)] = (float)sm * sc;
+        lds_bar();
+    }
+    // ---- router rows [4 j, 4 j + 4): wave r < 4 takes row r, lane = its
+    // 32-element block (Q8_0: f16 d, 32 int8; blocks 34 bytes apart)
+    if (wave < MX_RPW) {
+        const uint32_t off = MX_RT + wave * MX_RROW + lane * 34, sh = off & 3;
+        const uint32_t *wp = (const uint32_t *)(lds + (off & ~3u));
+        uint32_t wd[10];
+#pragma unroll
+        for (int i = 0; i < 10; i++) wd[i] = wp[i];
+        const uint32_t dw = __builtin_amdgcn_alignbyte(wd[1], wd[0], sh);
+        const uint8_t *lb = xqa + (lane / 4) * RG_SEG + (lane % 4) * 96;
+        int D[3] = {0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            // int8 quants i*4 .. i*4+3 at byte off + 2 + 4 i
+            const uint32_t q = sh ? wd[i + 1] : __builtin_amdgcn_alignbyte(wd[i + 1], wd[i], 2);
+#pragma unroll
+            for (int k = 0; k < 3; k++) D[k] = sdot4(q, ((const uint32_t *)(lb + 32 * k))[i], D[k]);
+        }
+        float v = h2f(dw) * (ixs[lane] * comb_f(D[0], D[1], D[2]));
+        v = wave_sum(v);
+        if (lane == 0) P.logits[h * MX_E + j * MX_RPW + wave] = v;
+        wait_vm<0>();
+    }
+    // ---- gate/up lanes: their half super-block of x in registers (before
+    // the SwiGLU limbs overwrite anything near the image)
+    const uint32_t team = tid / TL, tl = tid % TL, b = tl >> 1, hh = tl & 1;
+    uint32_t L[4][24];
+    float xs[4], xz[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t jb = b * 8 + 4 * hh + q;
+        lds_load_limbs(L[q], xqa + tl * RG_SEG + q * 96);
+        xs[q] = ixs[jb];
+        xz[q] = ixz[2 * jb] + ixz[2 * jb + 1];
+    }
+    __syncthreads();
+    if (tid == 0) *(volatile uint32_t *)(fl_r + j) = E;
+    const bool ok_r = xcd_wait(fl_r, XCD_PER, E, P.ctl, tid);
+    ZH_TRACE_POINT(2);
+    // ---- top 8 of the XCD's 128 logits (wave 0), this XCD's expert
+    if (wave == 0) {
+        const float v4[4] = {ld_dev(P.logits + h * MX_E + lane), ld_dev(P.logits + h * MX_E + 64 + lane), 0.f, 0.f};
+        topk_softmax_wave(v4, MX_E, MX_K, s_route);
+        if (blockIdx.x == 0 && lane < 2 * MX_K) P.routing[lane] = s_route[lane];
+    }
+    lds_bar();
+    uint32_t e = s_route[h];
+    if (e >= MX_E) {  // a NaN router: clamp, as the per-group kernels do
+        if (tid == 0) __hip_atomic_fetch_or(P.ctl, ZH_DEVERR_EXPERT_ID, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        e = MX_E - 1;
+    }
+    e = __builtin_amdgcn_readfirstlane(e);
+    const float wexp = __builtin_bit_cast(float, s_route[MX_K + h]);
+    ZH_TRACE_POINT(3);
+
+    // ---- the stream: gate/up tiles 0, 1 of expert e, then its 4 down tiles
+    RingP p = {};
+    p.M = MX_F; p.K = MX_H; p.nseg = 1; p.rpw = MX_FR;
+    const size_t gstride = (size_t)MX_F * NB * 144;
+    p.segW[0] = P.egate + e * gstride; p.segW[1] = p.segW[0]; p.segW[2] = p.segW[0];
+    p.W2 = P.eup + e * gstride;
+    p.seg_end[0] = MX_F; p.seg_end[1] = MX_F; p.seg_end[2] = MX_F;
+    const TT tiles(p, j, tid, lds);
+    const uint32_t tcw = tiles.tcw;
+    const uint32_t dcw = wave < MX_DCH % 8 ? MX_DCH / 8 + 1 : MX_DCH / 8;
+    const uint8_t *pk = P.pk + ((size_t)e * XCD_PER + j) * MX_SLICE;
+    auto issue = [&](uint32_t u, uint32_t s) __attribute__((always_inline)) {
+        if (u < MX_GT) {
+            tiles.issue(u, s);
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < (MX_DCH + 7) / 8; i++) {
+                const uint32_t c = wave + 8 * i;
+                if (c < MX_DCH)
+                    dma16(pk + (u - MX_GT) * MX_DTB + c * 1024 + lane * 16, lds0 + s * RG_TILE + c * 1024);
+            }
+        }
+    };
+    auto cnt = [&](uint32_t u) { return u < MX_GT ? tcw : dcw; };
+    issue(0, 0);
+    issue(1, 1);
+    {
+        const uint32_t mrow = team / RPP, trow = team % RPP;
+        for (uint32_t u = 0; u < MX_GT; u++) {
+            wait_vm_dyn(cnt(u + 1));
+            lds_bar();  // (u = 0: every wave done with the router rows in the third slot)
+            issue(u + 2, (u + 2) % RG_D);
+            const uint8_t *blk = ring + (u % RG_D) * RG_TILE + team * TT::ROWB + b * 144;
+            uint32_t hd[4], qs[16];
+            {
+                const u32x4 vv = *(const u32x4 *)blk;
+                hd[0] = vv.x; hd[1] = vv.y; hd[2] = vv.z; hd[3] = vv.w;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const u32x4 q4 = *(const u32x4 *)(blk + 16 + 64 * hh + 16 * i);
+                    qs[4 * i] = q4.x; qs[4 * i + 1] = q4.y; qs[4 * i + 2] = q4.z; qs[4 * i + 3] = q4.w;
+                }
+            }
+            const LpbQ4K::Hdr hdr = LpbQ4K::header(hd);
+            const uint32_t scw = hh ? hdr.scB : hdr.scA, mw = hh ? hdr.mB : hdr.mA;
+            float accd = 0.f, accm = 0.f;
+#pragma unroll
+            for (int pl = 0; pl < 2; pl++) {
+                int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t q = qs[8 * pl + i];
+                    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                    for (int k = 0; k < 3; k++) {
+                        D[0][k] = sdot4(lo, L[2 * pl][k * 8 + i], D[0][k]);
+                        D[1][k] = sdot4(hi, L[2 * pl + 1][k * 8 + i], D[1][k]);
+                    }
+                }
+                const float sc0 = ubyte_f(scw, 2 * pl), sc1 = ubyte_f(scw, 2 * pl + 1);
+                const float m0 = ubyte_f(mw, 2 * pl), m1 = ubyte_f(mw, 2 * pl + 1);
+                const float S0 = (float)comb_i(D[0][0], D[0][1], D[0][2]);
+                const float S1 = (float)comb_i(D[1][0], D[1][1], D[1][2]);
+                accd = fmaf(sc0 * xs[2 * pl], S0, accd);
+                accd = fmaf(sc1 * xs[2 * pl + 1], S1, accd);
+                accm = fmaf(m0, xz[2 * pl], accm);
+                accm = fmaf(m1, xz[2 * pl + 1], accm);
+            }
+            float res = fmaf(hdr.d, accd, -hdr.dmin * accm);
+            res = team_sum_dpp<TL>(res);
+            if (tl == 0) yl[mrow * RG_MAXROWS + u * RPP + trow] = res;
+        }
+    }
+    lds_bar();
+    ZH_TRACE_POINT(4);
+    // ---- SwiGLU of the 24 rows as XQ limbs in blocks of 8 (wave 0; lanes
+    // 24..63 form unused blocks). act: limbs [3 blocks][3 limbs][8 B], xs
+    // [3], xsum [3]
+    uint8_t *act = lds + MX_ACT;
+    if (wave == 0) {
+        const float v = lane < MX_FR ? silu_mul(yl[lane], yl[RG_MAXROWS + lane]) : 0.f;
+        const float a = row8_max(fabsf(v));
+        float inv, sc;
+        xq_scales(a, inv, sc);
+        const int X = xq_quant(v, inv);
+        int l0, l1, l2;
+        xq_limbs(X, l0, l1, l2);
+        const int sx = row8_sum_i(X);
+        if (lane < MX_FR) {
+            const uint32_t g = lane / 8, el = lane % 8;
+            act[(g * 3 + 0) * 8 + el] = (uint8_t)l0;
+            act[(g * 3 + 1) * 8 + el] = (uint8_t)l1;
+            act[(g * 3 + 2) * 8 + el] = (uint8_t)l2;
+            if (el == 0) {
+                ((float *)(act + 72))[g] = sc;
+                ((float *)(act + 84))[g] = (float)sx * sc;
+            }
+        }
+    }
+    lds_bar();
+    uint32_t A[3][3][2];
+    float axs[3], azs[3];
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            A[g][k][0] = ((const uint32_t *)(act + (g * 3 + k) * 8))[0];
+            A[g][k][1] = ((const uint32_t *)(act + (g * 3 + k) * 8))[1];
+        }
+        axs[g] = ((const float *)(act + 72))[g];
+        azs[g] = ((const float *)(act + 84))[g];
+    }
+    // the 24 columns [24 j, 24 j + 24) are three 8-column groups inside one
+    // or two 32-column Q4_K sub-blocks; group g uses the second one when it
+    // starts at or after column `split` of the slice
+    const uint32_t split = (24 * j) % 32 + 24 > 32 ? 32 - (24 * j) % 32 : 24u;
+    float *part = (float *)(lds + MX_RAW);
+    for (uint32_t u = MX_GT; u < MX_NU; u++) {
+        wait_vm_dyn(u + 1 < MX_NU ? cnt(u + 1) : 0u);
+        lds_bar();
+        if (u + 2 < MX_NU) issue(u + 2, (u + 2) % RG_D);
+        const uint32_t *rp = (const uint32_t *)(ring + (u % RG_D) * RG_TILE + tid * MX_REC);
+        uint32_t rc[6];
+#pragma unroll
+        for (int i = 0; i < 6; i++) rc[i] = rp[i];
+        // rc[3] = scale A, min A, scale B, min B (6-bit values in bytes);
+        // rc[4] = d A | dmin A (f16), rc[5] = d B | dmin B
+        const float dA = h2f(rc[4]), mnA = h2f(rc[4] >> 16), dB = h2f(rc[5]), mnB = h2f(rc[5] >> 16);
+        const float scA = dA * (float)(rc[3] & 0xFF), mA = mnA * (float)((rc[3] >> 8) & 0xFF);
+        const float scB = dB * (float)((rc[3] >> 16) & 0xFF), mB = mnB * (float)(rc[3] >> 24);
+        float acc = 0.f;
+#pragma unroll
+        for (int g = 0; g < 3; g++) {
+            const uint32_t c = rc[g], lo = c & 0x0F0F0F0Fu, hi = (c >> 4) & 0x0F0F0F0Fu;
+            int D[3];
+#pragma unroll
+            for (int k = 0; k < 3; k++) D[k] = sdot4(hi, A[g][k][1], sdot4(lo, A[g][k][0], 0));
+            const bool sb = 8u * g >= split;
+            const float s = sb ? scB : scA, m = sb ? mB : mA;
+            acc = fmaf(s * axs[g], comb_f(D[0], D[1], D[2]), fmaf(-m, azs[g], acc));
+        }
+        part[(u - MX_GT) * MX_DR + tid] = acc;
+    }
+    lds_bar();
+    ZH_TRACE_POINT(5);
+    // ---- publish the 2048 partials in the XCD's L2, then the flag
+    *(f32x4 *)(P.part + (size_t)w * MX_H + tid * 4) = *(const f32x4 *)(part + tid * 4);
+    wait_vm<0>();
+    __syncthreads();
+    if (tid == 0) *(volatile uint32_t *)(fl_p + j) = E;
+    const bool ok_p = xcd_wait(fl_p, XCD_PER, E, P.ctl, tid);
+    ZH_TRACE_POINT(6);
+    if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the XCD has read the epoch
+    // ---- rows [64 j, +64) of the XCD's 32 partials (8 KB) into ring slot 0:
+    // copy c (wave c) holds partials 4c .. 4c + 3
+    {
+        const uint32_t pi = 4 * wave + lane / 16;
+        dma16_dev(P.part + (size_t)(h * XCD_PER + pi) * MX_H + j * MX_RR + (lane % 16) * 4, lds0 + wave * 1024);
+    }
+    wait_vm<0>();
+    lds_bar();
+    if (tid < 4 * MX_RR) {
+        const float *rs = (const float *)lds;  // [32 partials][64 rows]
+        const uint32_t r = tid / 4, q = tid % 4;
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) s += rs[(q * 8 + k) * MX_RR + r];
+        s = team_sum_dpp<4>(s) * wexp;
+        if (!(ok_r && ok_p)) s = __builtin_nanf("");  // a wait gave up
+        if (q == 0) __hip_atomic_fetch_add(P.y + j * MX_RR + r, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ZH_TRACE_POINT(7);
+}
+
+ZH_TRACE_DUMP_FN(zh_debug_trace_moe)
+
+// Packs the experts' down matrices (Q4_K [128][2048][768]) into the records
+// k_moe_xcd reads: one thread per (expert, slice j, row r). Record: the 24
+// 4-bit codes of columns [24 j, 24 j + 24) (three dwords of 8 codes: low
+// nibbles columns 8g .. 8g + 3, high nibbles 8g + 4 .. 8g + 7), the 6-bit
+// scale and min of the first and second sub-block the slice touches, and the
+// f16 d / dmin of their super-blocks.
+__global__ void k_moe_pack_down(const uint8_t *q4, uint8_t *pk) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= MX_E * XCD_PER * MX_H) return;
+    const uint32_t r = gid % MX_H, j = (gid / MX_H) % XCD_PER, e = gid / (MX_H * XCD_PER);
+    const uint8_t *row = q4 + ((size_t)e * MX_H + r) * (MX_F / 256) * 144;
+    uint32_t rec[6] = {};
+    auto code = [&](uint32_t col) {  // Q4_K element col of the row: chunk of 64, low / high nibble
+        const uint8_t *blk = row + (col / 256) * 144;
+        const uint32_t x = col % 256;
+        return (uint32_t)(blk[16 + 32 * (x / 64) + x % 32] >> (4 * ((x / 32) & 1))) & 0xF;
+    };
+    auto scmin = [&](uint32_t col, uint32_t &sc, uint32_t &mn) {  // 6-bit scale / min of col's sub-block
+        const uint8_t *s = row + (col / 256) * 144 + 4;
+        const uint32_t sb = (col % 256) / 32;
+        if (sb < 4) {
+            sc = s[sb] & 63;
+            mn = s[sb + 4] & 63;
+        } else {
+            sc = (s[sb + 4] & 0xF) | ((s[sb - 4] >> 6) << 4);
+            mn = (s[sb + 4] >> 4) | ((s[sb] >> 6) << 4);
+        }
+    };
+    const uint32_t c0 = 24 * j;
+    for (uint32_t g = 0; g < 3; g++) {
+        uint32_t v = 0;
+        for (uint32_t i = 0; i < 4; i++) {
+            v |= code(c0 + 8 * g + i) << (8 * i);
+            v |= code(c0 + 8 * g + 4 + i) << (8 * i + 4);
+        }
+        rec[g] = v;
+    }
+    const uint32_t split = c0 % 32 + 24 > 32 ? 32 - c0 % 32 : 24u;
+    const uint32_t cA = c0, cB = split < 24 ? c0 + split : c0;
+    uint32_t sA, mA, sB, mB;
+    scmin(cA, sA, mA);
+    scmin(cB, sB, mB);
+    rec[3] = sA | (mA << 8) | (sB << 16) | (mB << 24);
+    const uint8_t *ba = row + (cA / 256) * 144, *bb = row + (cB / 256) * 144;
+    rec[4] = (uint32_t)ba[0] | ((uint32_t)ba[1] << 8) | ((uint32_t)ba[2] << 16) | ((uint32_t)ba[3] << 24);
+    rec[5] = (uint32_t)bb[0] | ((uint32_t)bb[1] << 8) | ((uint32_t)bb[2] << 16) | ((uint32_t)bb[3] << 24);
+    uint32_t *dst = (uint32_t *)(pk + ((size_t)e * XCD_PER + j) * MX_SLICE + (size_t)r * MX_REC);
+    for (int i = 0; i < 6; i++) dst[i] = rec[i];
+}
+
+uint32_t zhk_moe_xcd_flag_words() { return MX_FLAG_WORDS; }
+uint64_t zhk_moe_pack_bytes() { return (uint64_t)MX_E * XCD_PER * MX_SLICE; }
+uint64_t zhk_moe_part_bytes() { return (uint64_t)XCD_N * XCD_PER * MX_H * 4 + XCD_N * MX_E * 4; }
+
+bool zhk_moe_xcd_supported(zh_ctx *c, uint32_t hidden, uint32_t n_experts, uint32_t n_used, uint32_t expert_ffn) {
+    return hidden == MX_H && n_experts == MX_E && n_used == MX_K && expert_ffn == MX_F && !c->concurrent &&
+           zhk_xcd_round_robin(c);
+}
+
+int zhk_moe_pack_down(zh_ctx *c, const uint8_t *q4, uint8_t *pk) {
+    const uint32_t n = MX_E * XCD_PER * MX_H;
+    hipLaunchKernelGGL(k_moe_pack_down, dim3((n + 255) / 256), dim3(256), 0, c->stream, q4, pk);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
+
+int zhk_moe_xcd(zh_ctx *c, const float *x, const float *norm_w, float eps, const uint8_t *router,
+                const uint8_t *egate, const uint8_t *eup, const uint8_t *pk, float *y, float *scratch,
+                uint32_t *routing, uint32_t *flags) {
+    if (((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)router & 15) || ((uintptr_t)egate & 15) ||
+        ((uintptr_t)eup & 15) || ((uintptr_t)pk & 15) || ((uintptr_t)scratch & 15) || !y || !routing)
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "moe_xcd: 16-byte aligned operands");
+    MoeP P = {};
+    P.x = x; P.norm_w = norm_w; P.eps = eps; P.router = router; P.egate = egate; P.eup = eup; P.pk = pk; P.y = y;
+    P.part = scratch; P.logits = scratch + (size_t)XCD_N * XCD_PER * MX_H;
+    P.routing = routing; P.flags = flags; P.ctl = c->err_dev;
+    static bool attr = false;
+    if (!attr) {
+        ZH_HIP(c, hipFuncSetAttribute((const void *)k_moe_xcd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)RG_LDS));
+        attr = true;
+    }
+    hipLaunchKernelGGL(k_moe_xcd, dim3(XCD_N * XCD_PER), dim3(RG_T), RG_LDS, c->stream, P);
+    ZH_LAUNCH_CHECK(c);
+    return ZH_OK;
+}
