@@ -731,10 +731,15 @@ static bool step_args(zh_engine *e, zh_step_args &a) {
 static bool layer_qa(zh_engine *e, const Layer &y) {
     const zh_model_config &m = e->c;
     const uint32_t H = m.hidden, qd = m.n_heads * m.head_dim;
-    return e->fused_qa && e->pages_ident && !zh_knob("ZH_NO_LPB") && y.wq.type == ZH_Q4_K && y.wk.type == ZH_Q4_K &&
-           y.wv.type == ZH_Q4_K && zhk_lpb_supported(y.wo.type, qd) &&
+    // hidden 4096: Q4_K Q/K/V (and an O projection the tile kernels take);
+    // hidden 2048: Q8_0 Q/K/V
+    const uint32_t qt = H == 2048 ? ZH_Q8_0 : ZH_Q4_K;
+    return e->fused_qa && e->pages_ident && !zh_knob("ZH_NO_LPB") && y.wq.type == qt && y.wk.type == qt &&
+           y.wv.type == qt && (H == 2048 || zhk_lpb_supported(y.wo.type, qd)) &&
            zhk_qkv_attn_supported(e->ctx, H, m.n_heads, m.n_kv_heads, m.head_dim, m.max_ctx);
 }
+
+static bool step_moe(zh_engine *e);
 
 // Whether every layer's O projection also runs in that launch: then the
 // residual stream is kept twice at layer entry (the embedding and every down
@@ -742,7 +747,13 @@ static bool layer_qa(zh_engine *e, const Layer &y) {
 // e->xin and adds the O projection into e->hidden with device atomics.
 static bool step_qa_o(zh_engine *e) {
     const zh_model_config &m = e->c;
-    if (m.n_experts || m.n_heads != 4 * m.n_kv_heads) return false;
+    if (m.n_experts) {  // hidden 2048, Q8_0 O: only with the MoE FFN launch (the split residual)
+        if (!step_moe(e)) return false;
+        for (const Layer &y : e->L)
+            if (!layer_qa(e, y) || y.wo.type != ZH_Q8_0 || y.wo.off % 16) return false;
+        return true;
+    }
+    if (m.n_heads != 4 * m.n_kv_heads) return false;
     for (const Layer &y : e->L)
         if (!layer_qa(e, y) || y.wo.type != ZH_Q4_K || y.gate.type != ZH_Q4_K || y.up.type != ZH_Q4_K ||
             y.down.type != ZH_Q6_K || !zhk_lpb_supported(ZH_Q6_K, m.ffn))
@@ -842,7 +853,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     zh_step_args sa;
     const bool persistent = whole && step_args(e, sa);
     const bool qa_o = !persistent && step_qa_o(e);
-    const bool xl = qa_o && step_xcd(e);
+    const bool xl = qa_o && (m.n_experts ? true : step_xcd(e));  // qa_o with MoE implies its FFN launch
     const bool moe_x = !persistent && step_moe(e);
     float *const D = e->dres;
     auto dr = [&](uint32_t k) { return D + (size_t)(k % 3) * H; };
@@ -872,19 +883,19 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         const uint32_t qkv_m[3] = {qd, kvd, kvd};
         // Q/K/V and attention in one launch: 8 kv heads, one per XCD
         // (and the O projection, qa_o, when the launch group includes it)
-        const bool qa = (mask & SK_QKV) && (mask & SK_ATTN) && lpb_attn && layer_qa(e, y);
+        const bool qa = (mask & SK_QKV) && (mask & SK_ATTN) && layer_qa(e, y);
         const bool with_o = qa && qa_o && (mask & SK_O);
         const uint32_t ka = 2 * l;  // the split residual's launch index (xl)
         if (qa && with_o && xl) {
             ERC(zhk_qkv_attn(c, W(y.wq), W(y.wk), W(y.wv), e->rres, Wf(y.attn_norm), e->q, e->k, e->v,
                              Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc, m.max_ctx, e->attn, e->xq_q,
                              m.n_heads, pos, scale, m.eps, e->fd_part, e->qa_flags, W(y.wo), dr(ka + 1), dr(ka),
-                             e->rres + H, dr(ka + 2)));
+                             e->rres + H, dr(ka + 2), H));
         } else if (qa) {
             ERC(zhk_qkv_attn(c, W(y.wq), W(y.wk), W(y.wv), qa_o ? e->xin : e->hidden, Wf(y.attn_norm), e->q, e->k,
                              e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc, m.max_ctx, e->attn, e->xq_q,
                              m.n_heads, pos, scale, m.eps, e->fd_part, e->qa_flags, with_o ? W(y.wo) : nullptr,
-                             with_o ? e->hidden : nullptr));
+                             with_o ? e->hidden : nullptr, nullptr, nullptr, nullptr, H));
         } else if (!(mask & SK_QKV)) {
         } else if (lpb_attn) {
             // attn_norm fused into the Q/K/V mat-vec (every workgroup normalises x)
@@ -961,9 +972,15 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
         if (moe_x && (mask & SK_FFN_IN) && (mask & SK_FFN_OUT)) {
             // ffn_norm, router, top-k, the selected experts and the weighted
             // sum in one launch, one expert per XCD
-            ERC(zhk_moe_xcd(c, e->xin, Wf(y.ffn_norm), m.eps, W(y.router), W(y.egate), W(y.eup),
-                            e->moe_pk + zhk_moe_pack_bytes() * l, e->hidden, e->moe_scratch, e->routing,
-                            e->moe_flags));
+            // (split residual when the attention launch takes the O projection)
+            if (xl)
+                ERC(zhk_moe_xcd(c, e->rres + H, Wf(y.ffn_norm), m.eps, W(y.router), W(y.egate), W(y.eup),
+                                e->moe_pk + zhk_moe_pack_bytes() * l, dr(ka + 2), e->moe_scratch, e->routing,
+                                e->moe_flags, dr(ka + 1), e->rres, dr(ka + 3)));
+            else
+                ERC(zhk_moe_xcd(c, e->xin, Wf(y.ffn_norm), m.eps, W(y.router), W(y.egate), W(y.eup),
+                                e->moe_pk + zhk_moe_pack_bytes() * l, e->hidden, e->moe_scratch, e->routing,
+                                e->moe_flags));
             continue;
         }
         if (lds_moe) {

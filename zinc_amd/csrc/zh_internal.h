@@ -225,9 +225,11 @@ struct zh_step_args {
     uint32_t *ctl;                    // zh_step_ctl_bytes() zeroed bytes (barriers, merge counters)
 };
 uint64_t zh_step_ctl_bytes();
-// Q/K/V projection + decode attention in one launch (zh_qkv_attn.hip): 8 kv
-// heads, one per XCD of a 256-CU device, Q4_K Q/K/V with K = 4096, identity
-// page table, contexts up to 6144 tokens, the device to itself.
+// Q/K/V projection + decode attention in one launch (zh_qkv_attn.hip) on a
+// 256-CU device of 8 XCDs, identity page table, the device to itself: 8 kv
+// heads (one per XCD), Q4_K Q/K/V with K = 4096, contexts up to 6144; or 4
+// kv heads of 8 q heads (two XCDs each), Q8_0 Q/K/V with K = 2048, contexts
+// up to 10240 (hidden selects the shape).
 bool zhk_xcd_round_robin(zh_ctx *ctx);
 bool zhk_qkv_attn_supported(zh_ctx *ctx, uint32_t hidden, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx);
 uint32_t zhk_qkv_attn_flag_words();  // zeroed u32 words the caller keeps per engine
@@ -236,7 +238,7 @@ int zhk_qkv_attn(zh_ctx *ctx, const uint8_t *wq, const uint8_t *wk, const uint8_
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
                  uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
                  const uint8_t *wo = nullptr, float *x_acc = nullptr, const float *xb = nullptr,
-                 float *x_out = nullptr, float *zero = nullptr);
+                 float *x_out = nullptr, float *zero = nullptr, uint32_t hidden = 4096);
 // xb != nullptr (with wo): the input is x + xb, stored into x_out (16 rows
 // per workgroup); x_acc starts at zero (it is not x's copy), `zero` (H
 // floats) is cleared. Per-XCD FFN (zh_ffn_xcd.hip) with the same split
@@ -259,7 +261,8 @@ uint64_t zhk_moe_part_bytes();
 int zhk_moe_pack_down(zh_ctx *ctx, const uint8_t *q4k_edown, uint8_t *packed);
 int zhk_moe_xcd(zh_ctx *ctx, const float *x, const float *norm_w, float eps, const uint8_t *router,
                 const uint8_t *egate, const uint8_t *eup, const uint8_t *packed, float *y, float *scratch,
-                uint32_t *routing, uint32_t *flags);
+                uint32_t *routing, uint32_t *flags, const float *xb = nullptr, float *xout = nullptr,
+                float *zero = nullptr);  // xb: the split residual (x = x + xb, stored into xout; zero cleared)
 int zhk_ffn_xcd(zh_ctx *ctx, const float *xa, const float *xb, const float *norm_w, float eps, const uint8_t *wg,
                 const uint8_t *wu, const uint8_t *packed, float *part, float *xout, float *acc, float *zero,
                 uint32_t *flags);

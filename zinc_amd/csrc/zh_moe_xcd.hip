@@ -27,8 +27,10 @@
 // Every exchange stays inside an XCD; the only device-wide traffic is the
 // final atomics (8 per row, one per expert).
 //
-// x is a copy of the residual taken before the launch (the O projection
-// writes both): y changes during the launch.
+// x is not y, which changes during the launch: either a copy of the
+// residual taken before it (the O projection writes both), or the split
+// residual of the fused attention launch (zh_engine.hip): x = xa + xb, this
+// workgroup's 8 rows of x stored into xout, 8 rows of `zero` cleared.
 #include "zh_ring_q4k.h"
 #include "zh_xcd.h"
 
@@ -60,7 +62,9 @@ static_assert(MX_NB * 2 * RG_SEG + MX_NB * 8 * 12 <= 8192, "XQ image below the S
 constexpr uint32_t MX_FLAG_WORDS = 2 * XCD_N * XCD_PER + XCD_N;
 
 struct MoeP {
-    const float *x;               // residual copy
+    const float *x;               // residual copy (or its plain part, xa)
+    const float *xb;              // split residual: its atomic part (else nullptr)
+    float *xout, *zero;           // split residual: x = xa + xb stored / the vector to clear
     const float *norm_w;          // ffn_norm weight
     float eps;
     const uint8_t *router;        // Q8_0 [128][2048]
@@ -102,6 +106,7 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
     // workgroup's router rows (8.5 KB: 9 copies, the last clamped)
     dma16((const uint8_t *)P.x + wave * 1024 + lane * 16, lds0 + MX_RAW + wave * 1024);
     dma16((const uint8_t *)P.norm_w + wave * 1024 + lane * 16, lds0 + MX_RAW + NB * 1024 + wave * 1024);
+    if (P.xb) dma16((const uint8_t *)P.xb + wave * 1024 + lane * 16, lds0 + MX_RAW + 2 * NB * 1024 + wave * 1024);
     {
         const uint8_t *rr = P.router + (size_t)j * MX_RPW * MX_RROW;
         for (uint32_t c = wave; c < 9; c += 8)
@@ -116,6 +121,12 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
         const float *xr = (const float *)raw, *wr = xr + MX_H;
         const uint32_t e0 = tid * 4;
         f32x4 v = *(const f32x4 *)(xr + e0);
+        if (P.xb) {
+            const f32x4 d = *(const f32x4 *)(wr + MX_H + e0);
+            v.x += d.x; v.y += d.y; v.z += d.z; v.w += d.w;
+            if (e0 / (MX_H / 256) == blockIdx.x) *(f32x4 *)(P.xout + e0) = v;  // this workgroup's 8 rows
+            if (tid < MX_H / 256) P.zero[blockIdx.x * (MX_H / 256) + tid] = 0.f;
+        }
         const f32x4 wn = *(const f32x4 *)(wr + e0);
         float sq = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w)));
         sq = wave_sum(sq);
@@ -446,12 +457,13 @@ int zhk_moe_pack_down(zh_ctx *c, const uint8_t *q4, uint8_t *pk) {
 
 int zhk_moe_xcd(zh_ctx *c, const float *x, const float *norm_w, float eps, const uint8_t *router,
                 const uint8_t *egate, const uint8_t *eup, const uint8_t *pk, float *y, float *scratch,
-                uint32_t *routing, uint32_t *flags) {
+                uint32_t *routing, uint32_t *flags, const float *xb, float *xout, float *zero) {
     if (((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)router & 15) || ((uintptr_t)egate & 15) ||
-        ((uintptr_t)eup & 15) || ((uintptr_t)pk & 15) || ((uintptr_t)scratch & 15) || !y || !routing)
+        ((uintptr_t)eup & 15) || ((uintptr_t)pk & 15) || ((uintptr_t)scratch & 15) || !y || !routing ||
+        (xb && (((uintptr_t)xb & 15) || ((uintptr_t)xout & 15) || !zero)))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "moe_xcd: 16-byte aligned operands");
     MoeP P = {};
-    P.x = x; P.norm_w = norm_w; P.eps = eps; P.router = router; P.egate = egate; P.eup = eup; P.pk = pk; P.y = y;
+    P.x = x; P.xb = xb; P.xout = xout; P.zero = zero; P.norm_w = norm_w; P.eps = eps; P.router = router; P.egate = egate; P.eup = eup; P.pk = pk; P.y = y;
     P.part = scratch; P.logits = scratch + (size_t)XCD_N * XCD_PER * MX_H;
     P.routing = routing; P.flags = flags; P.ctl = c->err_dev;
     static bool attr = false;

@@ -54,18 +54,41 @@ namespace {
 constexpr int QA_T = 512;                       // 8 waves, two per SIMD
 constexpr uint32_t RG_SEG = 400;                // XQ image: bytes per 128-element half super-block (padded)
 constexpr int QA_AW = 8, QA_KVW = 32 / QA_AW;   // K/V copies per wave and sub-chunk
-constexpr uint32_t QA_NB = 16;                  // super-blocks per row (K = 4096)
-constexpr uint32_t QA_ROWB = QA_NB * 144;       // 2304 bytes per Q4_K row
-constexpr uint32_t QA_MAXR = 24;                // rows per workgroup (G = 4)
+constexpr uint32_t QA_MAXR = 24;                // rows per workgroup (4 q heads + k + v: 768 rows / 32)
 constexpr uint32_t QA_W = 2 * AR_SLOT;          // weight rows
-constexpr uint32_t QA_X = QA_W + QA_MAXR * QA_ROWB;  // x | norm weight, XQ image, K/V sub-chunk 2
-constexpr uint32_t QA_NRM = QA_X + AR_SLOT;     // q_norm | k_norm (1 KB)
-constexpr uint32_t QA_ROPE = QA_NRM + 1024;     // the position's (cos, sin) row (1 KB copy)
-constexpr uint32_t QA_YL = QA_ROPE + 1024;      // row results [32], RMS partials [8]
-constexpr uint32_t QA_LDS = QA_YL + 256;
-constexpr uint32_t QA_MAXSUB = 3;               // K/V sub-chunks per chunk
 constexpr uint32_t QA_NXCD = 8, QA_PER = 32;    // XCDs, workgroups per XCD
-static_assert(QA_NB * 2 * RG_SEG + QA_NB * 8 * 12 <= AR_SLOT, "XQ image fits the x region");
+
+// The two model shapes the kernel is built for:
+//   SH 3 (config 3): hidden 4096, 8 kv heads = one per XCD, Q4_K Q/K/V/O,
+//        contexts up to 32 x 3 sub-chunks of 64 tokens;
+//   SH 4 (config 4): hidden 2048, 4 kv heads of 8 q heads: kv head h / 2 on
+//        XCD h, which takes its q heads 4 (h % 2) .. + 3 (both XCDs of a
+//        pair compute the kv head's k and v rows, identically); Q8_0
+//        Q/K/V/O; contexts up to 32 x 5 sub-chunks.
+// Either way an XCD owns 4 q heads, 24 projection rows per workgroup and the
+// O projection's columns of its 4 heads.
+template <int SH>
+struct QaS {
+    static constexpr uint32_t H = SH == 3 ? 4096 : 2048;
+    static constexpr bool Q8 = SH == 4;                     // Q8_0 rows, else Q4_K
+    static constexpr uint32_t KVX = SH == 3 ? 1 : 2;        // XCDs per kv head
+    static constexpr uint32_t MAXSUB = SH == 3 ? 3 : 5;     // K/V sub-chunks per chunk
+    static constexpr uint32_t NB = H / 256;                 // 256-element super-blocks of x
+    static constexpr uint32_t ROWB = Q8 ? H / 32 * 34 : NB * 144;
+    static constexpr uint32_t X = QA_W + QA_MAXR * ROWB;    // x | norm weight, XQ image, K/V sub-chunk 2
+    static constexpr uint32_t NRM = X + AR_SLOT;            // q_norm | k_norm (1 KB)
+    static constexpr uint32_t ROPE = NRM + 1024;            // the position's (cos, sin) row (1 KB copy)
+    static constexpr uint32_t YL = ROPE + 1024;             // row results [32], RMS partials [8]
+    static constexpr uint32_t LDS = YL + 256;
+    static constexpr uint32_t OROWS = H / QA_PER;           // O-projection rows per workgroup
+    static constexpr uint32_t OROWB = Q8 ? 16 * 34 : 2 * 144;  // a row's columns of the XCD's 4 heads
+    static constexpr uint32_t OW = QA_W + 16384;            // the O rows' LDS copy
+    static constexpr uint32_t SUB3 = QA_W + 16384;          // K/V sub-chunk 3 (SH 4; the weight region, after the rows)
+    static constexpr uint32_t RROWS = H / (QA_NXCD * QA_PER);  // residual rows each workgroup stores / zeroes
+    static_assert(NB * 2 * RG_SEG + NB * 8 * 12 <= AR_SLOT && 2 * H * 4 <= AR_SLOT, "x | norm and the XQ image fit the x region");
+    static_assert(OW + OROWS * OROWB <= X && (MAXSUB <= 4 || SUB3 + AR_SLOT <= X), "O rows / sub-chunk 3 fit");
+    static_assert(QA_MAXR * ROWB % 1024 == 0, "whole 1 KB copies of the rows");
+};
 
 }  // namespace
 
@@ -73,10 +96,6 @@ static_assert(QA_NB * 2 * RG_SEG + QA_NB * 8 * 12 <= AR_SLOT, "XQ image fits the
 // published, [256, 512) partials published (head h at h * 32: one 128-byte
 // line per XCD), [512, 520) epochs.
 constexpr uint32_t QA_FLAG_WORDS = 2 * QA_NXCD * QA_PER + QA_NXCD;
-constexpr uint32_t QA_OROWS = 4096 / QA_PER;  // O-projection rows per workgroup (hidden 4096)
-constexpr uint32_t QA_OROWB = 2 * 144;        // a row's two super-blocks of the XCD's 512 columns
-constexpr uint32_t QA_OW = QA_W + 16384;      // their LDS copy (the attention uses the region's first 12.3 KB)
-static_assert(QA_OW + QA_OROWS * QA_OROWB <= QA_X, "O rows fit the weight region");
 
 struct QaP {
     AttnP a;                      // q / k_new / v_new: the projection outputs (written here)
@@ -98,11 +117,18 @@ struct QaP {
     float *x_out, *zero;
 };
 
-// LDS offset of K/V sub-chunk s
-ZH_DEV uint32_t qa_slot(uint32_t s) { return s == 0 ? 0u : s == 1 ? AR_SLOT : QA_X; }
+// LDS offset of K/V sub-chunk s (sub-chunk 4 reuses 0's slot)
+template <int SH>
+ZH_DEV uint32_t qa_slot(uint32_t s) {
+    return s == 0 || s == 4 ? 0u : s == 1 ? AR_SLOT : s == 2 ? QaS<SH>::X : QaS<SH>::SUB3;
+}
 
-template <int G, bool WITH_O>
+template <int G, bool WITH_O, int SH>
 __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
+    using S = QaS<SH>;
+    constexpr uint32_t QA_X = S::X, QA_NRM = S::NRM, QA_ROPE = S::ROPE, QA_YL = S::YL, QA_OW = S::OW;
+    constexpr uint32_t QA_OROWS = S::OROWS, QA_OROWB = S::OROWB, QA_NB = S::NB, QA_ROWB = S::ROWB;
+    constexpr uint32_t QA_MAXSUB = S::MAXSUB, H = S::H;
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t R = 4 * (G + 2);          // weight rows per workgroup
     constexpr uint32_t NCH = R * QA_ROWB / 1024;  // their 1 KB copies
@@ -116,7 +142,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // kv head = this workgroup's XCD; slice j = blockIdx / 8 (each run of 8
     // consecutive workgroups covers the 8 XCDs once)
-    const uint32_t h = min(xcc_id(), QA_NXCD - 1), j = blockIdx.x / QA_NXCD;
+    const uint32_t h = min(xcc_id(), QA_NXCD - 1), j = blockIdx.x / QA_NXCD, kvh = h / S::KVX;
     const uint32_t lds0 = lds_addr(lds);
     uint32_t *fl_q = P.flags + h * QA_PER, *fl_p = P.flags + QA_NXCD * QA_PER + h * QA_PER;
     uint32_t *ep = P.flags + 2 * QA_NXCD * QA_PER + h;
@@ -135,11 +161,11 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     const uint32_t nw = wl4 < NCH % 4 ? NCH / 4 + 1 : NCH / 4;  // weight copies of an A wave
     if (wa) {
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
+        for (uint32_t i = 0; i < H / 1024; i++) {  // H / 256 copies of 1 KB per vector over 4 waves
             const uint32_t c = wl4 + 4 * i;
             dma16((const uint8_t *)P.x + c * 1024 + lane * 16, lds0 + QA_X + c * 1024);
-            dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + QA_X + 16384 + c * 1024);
-            if (P.xb) dma16((const uint8_t *)P.xb + c * 1024 + lane * 16, lds0 + qa_slot(0) + c * 1024);
+            dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + QA_X + H * 4 + c * 1024);
+            if (P.xb) dma16((const uint8_t *)P.xb + c * 1024 + lane * 16, lds0 + qa_slot<SH>(0) + c * 1024);
         }
 #pragma unroll
         for (uint32_t i = 0; i < (NCH + 3) / 4; i++) {
@@ -148,8 +174,8 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
                 const uint32_t o = c * 1024 + lane * 16, r = o / QA_ROWB, within = o - r * QA_ROWB;
                 const uint32_t rr = j * R + r;  // row of the kv head's q | k | v rows
                 const uint8_t *src = rr < QR ? P.wq + (size_t)(h * QR + rr) * QA_ROWB
-                                   : rr < QR + FD_HD ? P.wk + (size_t)(h * FD_HD + rr - QR) * QA_ROWB
-                                                     : P.wv + (size_t)(h * FD_HD + rr - QR - FD_HD) * QA_ROWB;
+                                   : rr < QR + FD_HD ? P.wk + (size_t)(kvh * FD_HD + rr - QR) * QA_ROWB
+                                                     : P.wv + (size_t)(kvh * FD_HD + rr - QR - FD_HD) * QA_ROWB;
                 dma16(src + within, lds0 + QA_W + c * 1024);
             }
         }
@@ -167,8 +193,8 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         if (tid == 0) __hip_atomic_fetch_or(p.ctl, ZH_DEVERR_ATTN_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         nsub = QA_MAXSUB;
     }
-    const uint16_t *kbase = p.kc + (size_t)h * p.cache_tokens * FD_HD;
-    const uint16_t *vbase = p.vc + (size_t)h * p.cache_tokens * FD_HD;
+    const uint16_t *kbase = p.kc + (size_t)kvh * p.cache_tokens * FD_HD;
+    const uint16_t *vbase = p.vc + (size_t)kvh * p.cache_tokens * FD_HD;
     // sub-chunk s (B waves): 32 copies of 1 KB (4 token rows of K, then of
     // V); rows past the chunk re-read its last row (masked). 16-byte piece q
     // of LDS row rr holds the row's piece q ^ (rr % 16).
@@ -179,7 +205,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
             const uint32_t rr = 4 * (jj & 15) + (lane >> 4);
             const uint32_t t = min(t0 + s * AR_TS + rr, t1 - 1);
             const uint16_t *row = (kv ? vbase : kbase) + (size_t)t * FD_HD;
-            dma16(row + ((lane & 15) ^ (rr & 15)) * 8, lds0 + qa_slot(s) + jj * 1024);
+            dma16(row + ((lane & 15) ^ (rr & 15)) * 8, lds0 + qa_slot<SH>(s) + jj * 1024);
         }
     };
     const uint32_t n01 = min(nsub, 2u);
@@ -201,16 +227,18 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     float xs[4], xz[4];
     const uint32_t team = tid / 32, tl = tid % 32, b = tl >> 1, hh = tl & 1;
     {
-        const float *xr = (const float *)(lds + QA_X), *wr = xr + 4096;
-        f32x4 v[2], w[2];
+        constexpr int NIT = H / (4 * QA_T);  // 4 elements per thread and pass
+        const float *xr = (const float *)(lds + QA_X), *wr = xr + H;
+        f32x4 v[NIT], w[NIT];
         float sq = 0.f;
 #pragma unroll
-        for (int it = 0; it < 2; it++) {
+        for (int it = 0; it < NIT; it++) {
             v[it] = *(const f32x4 *)(xr + (it * QA_T + tid) * 4);
             if (P.xb) {
-                const f32x4 d = *(const f32x4 *)((const float *)(lds + qa_slot(0)) + (it * QA_T + tid) * 4);
+                const f32x4 d = *(const f32x4 *)((const float *)(lds + qa_slot<SH>(0)) + (it * QA_T + tid) * 4);
                 v[it].x += d.x; v[it].y += d.y; v[it].z += d.z; v[it].w += d.w;
-                if ((it * QA_T + tid) / 4 == blockIdx.x) *(f32x4 *)(P.x_out + (it * QA_T + tid) * 4) = v[it];
+                if ((it * QA_T + tid) * 4 / S::RROWS == blockIdx.x)  // this workgroup's rows
+                    *(f32x4 *)(P.x_out + (it * QA_T + tid) * 4) = v[it];
             }
             w[it] = *(const f32x4 *)(wr + (it * QA_T + tid) * 4);
             sq = fmaf(v[it].x, v[it].x, sq); sq = fmaf(v[it].y, v[it].y, sq);
@@ -220,15 +248,15 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         if (lane == 0) red[wave] = sq;
         lds_bar();  // (also: every x / weight value is in registers before the image overwrites them)
         if (!wa && P.xb && P.kv_defer == 0 && n01 > 0) issue_kv(0);  // xb is read: sub-chunk 0's slot is free
-        if (P.zero && tid < 16) P.zero[blockIdx.x * 16 + tid] = 0.f;
+        if (P.zero && tid < S::RROWS) P.zero[blockIdx.x * S::RROWS + tid] = 0.f;
         float tot = 0.f;
 #pragma unroll
         for (int w8 = 0; w8 < 8; w8++) tot += red[w8];
-        const float rms_inv = 1.0f / sqrtf(tot / 4096.f + p.eps);
+        const float rms_inv = 1.0f / sqrtf(tot / (float)H + p.eps);
         uint8_t *xqa = lds + QA_X;
         float *ixs = (float *)(xqa + QA_NB * 2 * RG_SEG), *ixz = ixs + QA_NB * 8;
 #pragma unroll
-        for (int it = 0; it < 2; it++) {
+        for (int it = 0; it < NIT; it++) {
             const uint32_t e0 = (it * QA_T + tid) * 4;
             f32x4 u = v[it];
             u.x = w[it].x * (u.x * rms_inv); u.y = w[it].y * (u.y * rms_inv);
@@ -253,13 +281,22 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
             if ((sub & 3) == 0) ixz[blk * 2 + (sub >> 2)] = (float)sm * sc;
         }
         lds_bar();
-        // this lane's half super-block: limbs, block scales and sums
+        if (!S::Q8) {
+            // this lane's half super-block: limbs, block scales and sums
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint32_t jb = b * 8 + 4 * hh + q;
-            lds_load_limbs(L[q], xqa + tl * RG_SEG + q * 96);
-            xs[q] = ixs[jb];
-            xz[q] = ixz[2 * jb] + ixz[2 * jb + 1];
+            for (int q = 0; q < 4; q++) {
+                const uint32_t jb = b * 8 + 4 * hh + q;
+                lds_load_limbs(L[q], xqa + tl * RG_SEG + q * 96);
+                xs[q] = ixs[jb];
+                xz[q] = ixz[2 * jb] + ixz[2 * jb + 1];
+            }
+        } else {
+            // Q8_0 (K = 2048): this lane's blocks 2 tl and 2 tl + 1
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                lds_load_limbs(L[q], xqa + (tl / 2) * RG_SEG + (tl % 2) * 192 + q * 96);
+                xs[q] = ixs[2 * tl + q];
+            }
         }
         lds_bar();  // the image is read: the region takes K/V sub-chunk 2
     }
@@ -276,56 +313,79 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     for (uint32_t ps = 0; ps < NP; ps++) {
         const uint32_t r = ps * 16 + team;
         if (r < R) {  // uniform per wave (R % 4 == 0)
-            const uint8_t *blk = lds + QA_W + r * QA_ROWB + b * 144;
-            uint32_t hd[4], qs[16];
-            {
-                const u32x4 v = *(const u32x4 *)blk;
-                hd[0] = v.x; hd[1] = v.y; hd[2] = v.z; hd[3] = v.w;
+            float res;
+            if constexpr (S::Q8) {
+                // Q8_0 blocks 2 tl and 2 tl + 1 of the row: 68 bytes from a
+                // 4-byte aligned start (f16 d, 32 int8; f16 d, 32 int8)
+                const uint32_t *wp = (const uint32_t *)(lds + QA_W + r * QA_ROWB + tl * 68);
+                uint32_t wd[17];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const u32x4 w = *(const u32x4 *)(blk + 16 + 64 * hh + 16 * i);
-                    qs[4 * i] = w.x; qs[4 * i + 1] = w.y; qs[4 * i + 2] = w.z; qs[4 * i + 3] = w.w;
-                }
-            }
-            const LpbQ4K::Hdr hdr = LpbQ4K::header(hd);
-            const uint32_t scw = hh ? hdr.scB : hdr.scA, mw = hh ? hdr.mB : hdr.mA;
-            float accd = 0.f, accm = 0.f;
-#pragma unroll
-            for (int pl = 0; pl < 2; pl++) {
-                int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+                for (int i = 0; i < 17; i++) wd[i] = wp[i];
+                int D0[3] = {0, 0, 0}, D1[3] = {0, 0, 0};
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    const uint32_t w = qs[8 * pl + i];
-                    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+                    const uint32_t q0 = __builtin_amdgcn_alignbyte(wd[i + 1], wd[i], 2), q1 = wd[9 + i];
 #pragma unroll
                     for (int k = 0; k < 3; k++) {
-                        D[0][k] = sdot4(lo, L[2 * pl][k * 8 + i], D[0][k]);
-                        D[1][k] = sdot4(hi, L[2 * pl + 1][k * 8 + i], D[1][k]);
+                        D0[k] = sdot4(q0, L[0][k * 8 + i], D0[k]);
+                        D1[k] = sdot4(q1, L[1][k * 8 + i], D1[k]);
                     }
                 }
-                const float sc0 = ubyte_f(scw, 2 * pl), sc1 = ubyte_f(scw, 2 * pl + 1);
-                const float m0 = ubyte_f(mw, 2 * pl), m1 = ubyte_f(mw, 2 * pl + 1);
-                const float S0 = (float)comb_i(D[0][0], D[0][1], D[0][2]);
-                const float S1 = (float)comb_i(D[1][0], D[1][1], D[1][2]);
-                accd = fmaf(sc0 * xs[2 * pl], S0, accd);
-                accd = fmaf(sc1 * xs[2 * pl + 1], S1, accd);
-                accm = fmaf(m0, xz[2 * pl], accm);
-                accm = fmaf(m1, xz[2 * pl + 1], accm);
+                res = fmaf(h2f(wd[0]) * xs[0], comb_f(D0[0], D0[1], D0[2]),
+                           h2f(wd[8] >> 16) * xs[1] * comb_f(D1[0], D1[1], D1[2]));
+            } else {
+                const uint8_t *blk = lds + QA_W + r * QA_ROWB + b * 144;
+                uint32_t hd[4], qs[16];
+                {
+                    const u32x4 v = *(const u32x4 *)blk;
+                    hd[0] = v.x; hd[1] = v.y; hd[2] = v.z; hd[3] = v.w;
+    #pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const u32x4 w = *(const u32x4 *)(blk + 16 + 64 * hh + 16 * i);
+                        qs[4 * i] = w.x; qs[4 * i + 1] = w.y; qs[4 * i + 2] = w.z; qs[4 * i + 3] = w.w;
+                    }
+                }
+                const LpbQ4K::Hdr hdr = LpbQ4K::header(hd);
+                const uint32_t scw = hh ? hdr.scB : hdr.scA, mw = hh ? hdr.mB : hdr.mA;
+                float accd = 0.f, accm = 0.f;
+    #pragma unroll
+                for (int pl = 0; pl < 2; pl++) {
+                    int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+    #pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const uint32_t w = qs[8 * pl + i];
+                        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    #pragma unroll
+                        for (int k = 0; k < 3; k++) {
+                            D[0][k] = sdot4(lo, L[2 * pl][k * 8 + i], D[0][k]);
+                            D[1][k] = sdot4(hi, L[2 * pl + 1][k * 8 + i], D[1][k]);
+                        }
+                    }
+                    const float sc0 = ubyte_f(scw, 2 * pl), sc1 = ubyte_f(scw, 2 * pl + 1);
+                    const float m0 = ubyte_f(mw, 2 * pl), m1 = ubyte_f(mw, 2 * pl + 1);
+                    const float S0 = (float)comb_i(D[0][0], D[0][1], D[0][2]);
+                    const float S1 = (float)comb_i(D[1][0], D[1][1], D[1][2]);
+                    accd = fmaf(sc0 * xs[2 * pl], S0, accd);
+                    accd = fmaf(sc1 * xs[2 * pl + 1], S1, accd);
+                    accm = fmaf(m0, xz[2 * pl], accm);
+                    accm = fmaf(m1, xz[2 * pl + 1], accm);
+                }
+                res = fmaf(hdr.d, accd, -hdr.dmin * accm);
             }
-            float res = fmaf(hdr.d, accd, -hdr.dmin * accm);
             res = team_sum_dpp<32>(res);
             if (tl == 0) yl[r] = res;
         }
     }
     lds_bar();
     ZH_TRACE_POINT(4);
+    if (QA_MAXSUB > 3 && !wa && nsub > 3) issue_kv(3);  // the weight rows are read: their region takes sub-chunk 3
     // ---- publish the rows (wave 0), then wait for the kv head's other slices
     if (wave == 0) {
         if (lane < R) {
             const uint32_t rr = j * R + lane;
             float *dst = rr < QR ? (float *)p.q + h * QR + rr
-                       : rr < QR + FD_HD ? (float *)p.k_new + h * FD_HD + rr - QR
-                                         : (float *)p.v_new + h * FD_HD + rr - QR - FD_HD;
+                       : rr < QR + FD_HD ? (float *)p.k_new + kvh * FD_HD + rr - QR
+                                         : (float *)p.v_new + kvh * FD_HD + rr - QR - FD_HD;
             *dst = yl[lane];
         }
         wait_vm<0>();  // the rows are in the L2 before the flag
@@ -339,8 +399,8 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     uint8_t *sm = lds + QA_W;  // q [G][128] f32 (QC KB), k_new | v_new (1 KB), new K / V rows f16, q fragments
     for (uint32_t k = wave; k <= QC; k += QA_AW) {  // uniform per wave
         const uint8_t *src = k < QC ? (const uint8_t *)(p.q + (size_t)h * QR) + min(k * 1024 + lane * 16, QR * 4 - 16)
-                           : lane < 32 ? (const uint8_t *)(p.k_new + (size_t)h * FD_HD) + lane * 16
-                                       : (const uint8_t *)(p.v_new + (size_t)h * FD_HD) + (lane - 32) * 16;
+                           : lane < 32 ? (const uint8_t *)(p.k_new + (size_t)kvh * FD_HD) + lane * 16
+                                       : (const uint8_t *)(p.v_new + (size_t)kvh * FD_HD) + (lane - 32) * 16;
         dma16_dev(src, lds0 + QA_W + k * 1024);
     }
     wait_vm<0>();  // ... and every K/V sub-chunk
@@ -349,13 +409,17 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     // ---- WITH_O: this workgroup's O rows (128 rows x the XCD's two
     // super-blocks, 36 KB) into the weight region's free part, by waves 4-7
     // while the attention runs (HBM is idle from here on)
-    if (WITH_O && !wa) {
+    // (SH 4: after the attention, its sub-chunk 3 occupies the region)
+    auto issue_o = [&]() __attribute__((always_inline)) {
+        constexpr uint32_t WO_ROWB = S::Q8 ? 4 * QA_NXCD * FD_HD / 32 * 34 : 16 * 144;  // a W_o row (4096 columns)
+        constexpr uint32_t PCS = QA_OROWB / 16;  // 16-byte pieces of a row's columns of the XCD
+        static_assert(QA_OROWS * QA_OROWB % 1024 == 0 && QA_OROWB % 16 == 0, "whole copies");
         for (uint32_t c = wl4; c < QA_OROWS * QA_OROWB / 1024; c += 4) {
-            const uint32_t pc = c * 64 + lane, row = pc / 18, within = pc - row * 18;  // 16-byte piece
-            dma16(P.wo + (size_t)(j * QA_OROWS + row) * (16 * 144) + 2 * h * 144 + within * 16,
-                  lds0 + QA_OW + c * 1024);
+            const uint32_t pc = c * 64 + lane, row = pc / PCS, within = pc - row * PCS;
+            dma16(P.wo + (size_t)(j * QA_OROWS + row) * WO_ROWB + h * QA_OROWB + within * 16, lds0 + QA_OW + c * 1024);
         }
-    }
+    };
+    if (WITH_O && !S::Q8 && !wa) issue_o();
     // ---- q as MFMA fragments (RMSNorm, RoPE, f16 hi + lo), shared through LDS
     const uint32_t sub = lane & 7, fg = lane & 15, fq = lane >> 4;
     const uint32_t gq = wave / 4, w4 = wave % 4;
@@ -435,23 +499,38 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     }
     const uint32_t s_own = owner ? (posv - t0) / AR_TS : ~0u, r_own = owner ? (posv - t0) % AR_TS : 0u;
     lds_bar();
-    if (owner && s_own < nsub) {  // substitute the new row for the copy (which predates it)
-        uint8_t *Ks = lds + qa_slot(s_own);
+    // substitute the new row for the copy (which predates it); sub-chunk 4
+    // is copied later, into sub-chunk 0's slot
+    auto substitute = [&]() __attribute__((always_inline)) {
+        uint8_t *Ks = lds + qa_slot<SH>(s_own);
         const uint32_t pc = ((tid & 15) ^ (r_own & 15)) * 16;
         if (tid < 16) *(u32x4 *)(Ks + r_own * 256 + pc) = *(const u32x4 *)((const uint8_t *)knew16 + tid * 16);
         else if (tid < 32)
             *(u32x4 *)(Ks + AR_SLOT / 2 + r_own * 256 + pc) = *(const u32x4 *)((const uint8_t *)vnew16 + (tid - 16) * 16);
-    }
+    };
+    if (owner && s_own < nsub && s_own != 4) substitute();
     lds_bar();
 
     // ---- scores and P V over the landed sub-chunks: group gq (4 waves) takes
-    // sub-chunks gq, gq + 2; wave w4 of a group tokens 16 w4 .. 16 w4 + 15
+    // sub-chunks gq, gq + 2 (, 4); wave w4 of a group tokens 16 w4 .. 16 w4 + 15
     float m_run = -INFINITY, l_run = 0.f;
     floatx4 acc[8];
 #pragma unroll
     for (int n = 0; n < 8; n++) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t s = gq; s < nsub; s += 2) {  // uniform per wave
-        const uint8_t *Ks = lds + qa_slot(s), *Vs = Ks + AR_SLOT / 2;
+    for (uint32_t it = 0; 2 * it < nsub; it++) {  // uniform: group gq takes sub-chunk 2 it + gq
+        if (QA_MAXSUB > 4 && it == 1 && nsub > 4) {
+            lds_bar();  // sub-chunk 0 is read: its slot takes sub-chunk 4
+            if (!wa) issue_kv(4);
+        }
+        if (QA_MAXSUB > 4 && it == 2) {
+            if (!wa) wait_vm<0>();
+            lds_bar();
+            if (owner && s_own == 4) substitute();
+            lds_bar();
+        }
+        const uint32_t s = 2 * it + gq;
+        if (s >= nsub) continue;  // uniform per wave
+        const uint8_t *Ks = lds + qa_slot<SH>(s), *Vs = Ks + AR_SLOT / 2;
         const uint32_t ts = t0 + s * AR_TS, tb = w4 * 16;
         half4 kf[8], vf[8];
         {
@@ -516,7 +595,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     ZH_TRACE_POINT(9);
     // ---- the new row to the cache
     if (owner && tid < 32) {
-        uint16_t *dst = (tid < 16 ? p.kc : p.vc) + ((size_t)h * p.cache_tokens + posv) * FD_HD + (tid & 15) * 8;
+        uint16_t *dst = (tid < 16 ? p.kc : p.vc) + ((size_t)kvh * p.cache_tokens + posv) * FD_HD + (tid & 15) * 8;
         *(u32x4 *)dst = *(const u32x4 *)((const uint8_t *)(tid < 16 ? knew16 : vnew16) + (tid & 15) * 16);
     }
     // ---- combine the waves (in sub-chunk 0's slot), publish the partials
@@ -570,6 +649,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         ZH_TRACE_POINT(12);
         return;
     }
+    if (S::Q8 && !wa) issue_o();
     // ---- WITH_O: every workgroup of the XCD merges the XCD's G heads itself
     // (their partials are in this XCD's L2) into LDS, as the XQ image of
     // the O projection's 4 G blocks of 32 (no second publication round)
@@ -594,7 +674,33 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     }
     const uint8_t *xlimb = lds + QA_X;
     const float *oxs = (const float *)(lds + QA_X + 4 * G * 96), *oxz = oxs + 4 * G;
-    {
+    if constexpr (S::Q8) {
+        // lane: row r = tid / 8 of the 64, blocks 2 q8 and 2 q8 + 1 of the
+        // XCD's 16 (Q8_0: 68 bytes from a 4-byte aligned start)
+        const uint32_t q8 = tid & 7, r = tid >> 3;
+        uint32_t Lo[2][24];
+#pragma unroll
+        for (int k = 0; k < 2; k++) lds_load_limbs(Lo[k], xlimb + (2 * q8 + k) * 96);
+        const uint32_t *wp = (const uint32_t *)(lds + QA_OW + r * QA_OROWB + q8 * 68);
+        uint32_t wd[17];
+#pragma unroll
+        for (int i = 0; i < 17; i++) wd[i] = wp[i];
+        int D0[3] = {0, 0, 0}, D1[3] = {0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t q0 = __builtin_amdgcn_alignbyte(wd[i + 1], wd[i], 2), q1 = wd[9 + i];
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                D0[k] = sdot4(q0, Lo[0][k * 8 + i], D0[k]);
+                D1[k] = sdot4(q1, Lo[1][k * 8 + i], D1[k]);
+            }
+        }
+        float res = fmaf(h2f(wd[0]) * oxs[2 * q8], comb_f(D0[0], D0[1], D0[2]),
+                         h2f(wd[8] >> 16) * oxs[2 * q8 + 1] * comb_f(D1[0], D1[1], D1[2]));
+        res = team_sum_dpp<8>(res);
+        if (!(ok && ok_rows)) res = __builtin_nanf("");  // a wait gave up: the rows' sums are poisoned
+        if (q8 == 0) __hip_atomic_fetch_add(P.x_acc + j * QA_OROWS + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
         // lane: row r = tid / 4 of the 128, half super-block q = tid % 4 of the
         // XCD's 4 G half-blocks (G = 4; fewer heads leave lanes idle)
         const uint32_t q = tid & 3, r = tid >> 2;
@@ -695,15 +801,18 @@ uint32_t zhk_qkv_attn_flag_words() { return QA_FLAG_WORDS; }
 // Whether k_qkv_attn takes a model of this shape on this context.
 bool zhk_qkv_attn_supported(zh_ctx *c, uint32_t hidden, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx) {
     const uint32_t G = nkv ? nh / nkv : 0;
-    return hidden == 4096 && nkv == QA_NXCD && hd == FD_HD && nh == G * nkv && (G == 1 || G == 2 || G == 4) &&
-           max_ctx <= QA_PER * QA_MAXSUB * AR_TS && !c->concurrent && zhk_xcd_round_robin(c);
+    const bool s3 = hidden == QaS<3>::H && nkv == QA_NXCD && nh == G * nkv && (G == 1 || G == 2 || G == 4) &&
+                    max_ctx <= QA_PER * QaS<3>::MAXSUB * AR_TS;
+    const bool s4 = hidden == QaS<4>::H && nkv == QA_NXCD / QaS<4>::KVX && nh == 4 * QA_NXCD &&
+                    max_ctx <= QA_PER * QaS<4>::MAXSUB * AR_TS;
+    return (s3 || s4) && hd == FD_HD && !c->concurrent && zhk_xcd_round_robin(c);
 }
 
 int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x,
                  const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
                  uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
-                 const uint8_t *wo, float *x_acc, const float *xb, float *x_out, float *zero) {
+                 const uint8_t *wo, float *x_acc, const float *xb, float *x_out, float *zero, uint32_t hidden) {
     QaP P = {};
     AttnP &p = P.a;
     p.q = q; p.k_new = k; p.v_new = v; p.q_norm = qw; p.k_norm = kw; p.rope_cs = rope_cs;
@@ -712,30 +821,35 @@ int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t 
     p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh; p.nd = QA_PER; p.no_wait = 0; p.ident = 1; p.ctl = c->err_dev;
     P.wq = wq; P.wk = wk; P.wv = wv; P.x = x; P.norm_w = norm_w; P.flags = flags;
     P.wo = wo; P.x_acc = x_acc; P.xb = xb; P.x_out = x_out; P.zero = zero;
-    P.kv_defer = xb ? 0u : (uint32_t)zh_knob_int("ZH_QA_DEFER", 0);
+    P.kv_defer = xb || hidden != QaS<3>::H ? 0u : (uint32_t)zh_knob_int("ZH_QA_DEFER", 0);
     if (xb && (!wo || !x_out || !zero || ((uintptr_t)xb & 15) || ((uintptr_t)x_out & 15)))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: split residual needs the O phase and aligned rows");
     const uint32_t G = nh / QA_NXCD;
     if ((wo && (!x_acc || ((uintptr_t)wo & 15))) || !pos.dev || ((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wq & 15) || ((uintptr_t)wk & 15) ||
         ((uintptr_t)wv & 15))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: device position and 16-byte aligned operands");
-#define QA_L(GG, WO)                                                                                             \
+#define QA_L(GG, WO, SS)                                                                                         \
     {                                                                                                            \
         static bool attr = false;                                                                                \
         if (!attr) {                                                                                             \
-            ZH_HIP(c, hipFuncSetAttribute((const void *)k_qkv_attn<GG, WO>,                                      \
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)QA_LDS));             \
+            ZH_HIP(c, hipFuncSetAttribute((const void *)k_qkv_attn<GG, WO, SS>,                                  \
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)QaS<SS>::LDS));       \
             attr = true;                                                                                         \
         }                                                                                                        \
-        hipLaunchKernelGGL((k_qkv_attn<GG, WO>), dim3(QA_NXCD * QA_PER), dim3(QA_T), QA_LDS, c->stream, P);      \
+        hipLaunchKernelGGL((k_qkv_attn<GG, WO, SS>), dim3(QA_NXCD * QA_PER), dim3(QA_T), QaS<SS>::LDS, c->stream, \
+                           P);                                                                                   \
         break;                                                                                                   \
     }
     if (wo && G != 4) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: O phase needs 4 q heads per kv head");
-    switch (G + (wo ? 100 : 0)) {
-    case 1: QA_L(1, false)
-    case 2: QA_L(2, false)
-    case 4: QA_L(4, false)
-    case 104: QA_L(4, true)
+    if (hidden != QaS<3>::H && (hidden != QaS<4>::H || G != 4))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: hidden %u with %u q heads", hidden, nh);
+    switch (G + (wo ? 100 : 0) + (hidden == QaS<4>::H ? 1000 : 0)) {
+    case 1: QA_L(1, false, 3)
+    case 2: QA_L(2, false, 3)
+    case 4: QA_L(4, false, 3)
+    case 104: QA_L(4, true, 3)
+    case 1004: QA_L(4, false, 4)
+    case 1104: QA_L(4, true, 4)
     default: return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: GQA group %u", G);
     }
 #undef QA_L
