@@ -256,6 +256,20 @@ ZH_DEV void xq_store_block32_dev(float xi, int l, XQView v, uint32_t blk) {
     if ((l & 15) == 0) st_dev(v.xsum + blk * 2 + (l >> 4), (float)s * sc);
 }
 
+// Argmax: first (lowest-index) maximum; NaN never compares greater, as the
+// reference's strict `>` scan (forward.zig:10348-10356).
+ZH_DEV void am_better(float &bv, uint32_t &bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+ZH_DEV void am_wave(float &bv, uint32_t &bi) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(bv, o, 64);
+        uint32_t oi = (uint32_t)__shfl_xor((int)bi, o, 64);
+        am_better(bv, bi, ov, oi);
+    }
+}
+
 // Router top-k with softmax over the selected logits (softmax_topk_v2.comp,
 // topKSoftmax forward.zig:496-537), in one wave: lane l holds logits l,
 // l+64, l+128, l+192 (n <= 256). Exact f32 comparisons, the lowest index wins

@@ -65,7 +65,8 @@ struct zh_engine {
     uint8_t *xq_h = nullptr, *xq_q = nullptr, *xq_f = nullptr;
     uint32_t *routing = nullptr, *am_part = nullptr, *st = nullptr, *prompt = nullptr, *ring = nullptr;
     uint32_t *grp_cnt = nullptr;  // SwiGLU-output XQ: one counter per 32-row group (kept zero between launches)
-    uint32_t *router_cnt = nullptr;  // router top-k: workgroups finished (kept zero between launches)
+    uint32_t *router_cnt = nullptr;
+    uint32_t *am_cnt = nullptr;      // k_argmax_advance: workgroups finished (kept zero between launches)  // router top-k: workgroups finished (kept zero between launches)
     // persistent decode-layers kernel: barrier / merge words (zero between
     // launches) and the device table of layer pointers
     uint32_t *step_ctl = nullptr;
@@ -126,6 +127,60 @@ __global__ void k_advance(uint32_t *st, const uint32_t *prompt) {
     st[ST_STEP] = s;
     st[ST_POS] += 1;
     st[ST_TOKEN_IN] = (s < np) ? prompt[s] : st[ST_TOKEN_OUT];
+}
+
+// The step's greedy token and the step advance in one launch: every
+// workgroup reduces a strided share of the logits (first maximum wins) and
+// publishes it with device-scope stores; the last workgroup to count itself
+// in (a relaxed device-scope counter after s_waitcnt 0, the engine's
+// publication pattern) reduces the shares, records the token
+// (argmaxGreedy, forward.zig:10348-10356) and advances the state as
+// k_advance. The counter is left zero for the next launch.
+constexpr uint32_t TAIL_WGS = 128;
+__global__ __launch_bounds__(256) void k_argmax_advance(const float *__restrict__ x, uint32_t n, uint32_t *partials,
+                                                        uint32_t *cnt, uint32_t *ring, uint32_t *st,
+                                                        const uint32_t *prompt) {
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) am_better(bv, bi, x[i], i);
+    am_wave(bv, bi);
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    __shared__ uint32_t s_last;
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) am_better(bv, bi, sv[w], si[w]);
+        __hip_atomic_store(partials + 2 * blockIdx.x, __float_as_uint(bv), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(partials + 2 * blockIdx.x + 1, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        s_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    bv = -INFINITY;
+    bi = 0xFFFFFFFFu;
+    for (uint32_t i = threadIdx.x; i < gridDim.x; i += 256)
+        am_better(bv, bi, __uint_as_float(__hip_atomic_load(partials + 2 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)),
+                  __hip_atomic_load(partials + 2 * i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    am_wave(bv, bi);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) am_better(bv, bi, sv[w], si[w]);
+        if (bi == 0xFFFFFFFFu) bi = 0;  // all NaN: the scan keeps index 0
+        st[ST_TOKEN_OUT] = bi;
+        ring[st[ST_GEN]] = bi;
+        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // k_advance
+        uint32_t s = st[ST_STEP], np = st[ST_NPROMPT];
+        if (s + 1 >= np) st[ST_GEN] += 1;
+        s += 1;
+        st[ST_STEP] = s;
+        st[ST_POS] += 1;
+        st[ST_TOKEN_IN] = (s < np) ? prompt[s] : bi;
+    }
 }
 
 // Seeded N(0,1) fp16 values for logical tokens [0, n) of one layer, written
@@ -348,7 +403,7 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->routing, 8ull * 16}, {(void **)&e->am_part, 8ull * 256}, {(void **)&e->st, 4ull * ST_WORDS},
         {(void **)&e->prompt, 4ull * MAX_PROMPT}, {(void **)&e->ring, 4ull * MAX_GEN}, {(void **)&e->pages, 4ull * e->n_pages},
         {(void **)&e->inv_freq, 4ull * hd / 2}, {(void **)&e->rope_cs, 8ull * c.max_ctx * (hd / 2)},
-        {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)}, {(void **)&e->router_cnt, 4},
+        {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)}, {(void **)&e->router_cnt, 4}, {(void **)&e->am_cnt, 4},
         {(void **)&e->step_ctl, zh_step_ctl_bytes()}, {(void **)&e->step_layers, sizeof(zh_step_layer) * c.n_layers},
         {(void **)&e->qa_flags, 4ull * zhk_qkv_attn_flag_words()}, {(void **)&e->xin, 4ull * H},
         {(void **)&e->ffn_flags, 4ull * zhk_ffn_xcd_flag_words()}, {(void **)&e->rres, 8ull * H},
@@ -679,7 +734,9 @@ extern "C" uint32_t zh_kv_pool_max_context(const zh_kv_pool *p, uint32_t page_co
 // ---------------------------------------------------------------------------
 // output_norm -> LM head -> greedy argmax on e->hidden (forward.zig:7757-7772,
 // sampleGreedy :10338-10357); the token goes to ST_TOKEN_OUT and the ring.
-static int record_collect(zh_engine *e) {
+// advance: the whole step's tail (the argmax and the step advance in one
+// launch, k_argmax_advance); else the argmax alone.
+static int record_collect(zh_engine *e, bool advance = false) {
     zh_ctx *c = e->ctx;
     const zh_model_config &m = e->c;
     const uint32_t H = m.hidden;
@@ -693,6 +750,12 @@ static int record_collect(zh_engine *e) {
     } else {
         ERC(zhk_rms_norm(c, e->hidden, (const float *)(A + e->out_norm.off), H, e->norm, e->xq_h, H, 1, m.eps));
         ERC(zhk_dmmv(c, e->lm.type, A + e->lm.off, e->xq_h, e->logits, m.vocab, H, 0));
+    }
+    if (advance) {
+        hipLaunchKernelGGL(k_argmax_advance, dim3(TAIL_WGS), dim3(256), 0, c->stream, e->logits, m.vocab, e->am_part,
+                           e->am_cnt, e->ring, e->st, (const uint32_t *)e->prompt);
+        ZH_LAUNCH_CHECK(c);
+        return ZH_OK;
     }
     return zhk_argmax(c, e->logits, m.vocab, e->st + ST_TOKEN_OUT, e->am_part, e->ring, e->st + ST_GEN);
 }
@@ -1044,7 +1107,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
                            e->dres, (2 * m.n_layers) % 3, H);
         ZH_LAUNCH_CHECK(c);
     }
-    if (collect) ERC(record_collect(e));
+    if (collect) return record_collect(e, true);  // (with the step advance)
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, c->stream, e->st, (const uint32_t *)e->prompt);
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;

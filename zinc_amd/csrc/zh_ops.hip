@@ -561,17 +561,6 @@ extern "C" int zh_moe_weighted_acc(zh_ctx *c, zh_buf *a, const zh_buf *b, const 
 // reference's strict `>` scan (forward.zig:10348-10356).
 // ---------------------------------------------------------------------------
 constexpr int AM_WGS = 256;
-ZH_DEV void am_better(float &bv, uint32_t &bi, float v, uint32_t i) {
-    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-}
-ZH_DEV void am_wave(float &bv, uint32_t &bi) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float ov = __shfl_xor(bv, o, 64);
-        uint32_t oi = (uint32_t)__shfl_xor((int)bi, o, 64);
-        am_better(bv, bi, ov, oi);
-    }
-}
 __global__ __launch_bounds__(256) void k_argmax0(const float *__restrict__ x, uint32_t n, uint32_t *partials) {
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
