@@ -80,6 +80,34 @@ def test_fused_step_matches_oracle(ctx, orc, prefill):
     om.close()
 
 
+# longer contexts stream their sub-chunks through the four-slot ring: 8300
+# (five per chunk: one slot reused), 11900 (the new token in sub-chunk 5 of its
+# chunk, written into its slot after the copy), 12000 (six per chunk)
+FUSED_LONG = dict(FUSED, max_ctx=12288)
+
+
+@pytest.mark.parametrize("prefill", [8300, 11900, 12000])
+def test_fused_long_context_matches_oracle(ctx, orc, prefill):
+    import zinc_amd
+    eng = _engine(ctx, FUSED_LONG)
+    assert "k_qkv_attn" in eng.group_kernels("qkv_attn")
+    om = orc.Model(FUSED_LONG)
+    eng.prefill_kv_random(prefill, 3)
+    om.prefill_kv_random(prefill, 3)
+    st = zinc_amd.DecodeState()
+    for step in range(2):
+        st.position = prefill + step
+        eng.decode_step(st, 31 + step, True)
+        g_log = eng.logits()
+        o_tok, o_log = om.decode_step(31 + step, prefill + step, want_logits=True)
+        scale = np.abs(o_log).max()
+        assert np.abs(g_log - o_log).max() <= 1e-4 + 1e-3 * scale, (step, np.abs(g_log - o_log).max(), scale)
+        assert eng.sample_greedy() == o_tok
+    ctx.sync()
+    eng.deinit()
+    om.close()
+
+
 def test_fused_equals_two_launch_path(ctx):
     """Same engine state through either path: the projection's rows are the
     same arithmetic (bit-identical); the attention differs only in summation

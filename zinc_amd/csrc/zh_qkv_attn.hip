@@ -42,8 +42,10 @@
 // (then its XQ image, then K/V sub-chunk 2), norm weights and the RoPE row.
 // The weight rows, x, the norm weights and (after the position) the K/V
 // sub-chunks are all requested at the start, so the K/V stream overlaps the
-// projection and the barrier. Contexts up to 32 x 192 tokens (three 64-token
-// sub-chunks per chunk); the engine uses the two-kernel path beyond.
+// projection and the barrier. Longer chunks stream their 64-token sub-chunks
+// through a ring of four slots (the x region and the weight region join it
+// once the projection is done), two sub-chunks ahead of the wave groups:
+// contexts up to 32 x 2048 tokens.
 #define TRACE_OPS(slot) ZH_TRACE_POINT((slot) == 11 ? 14 : (slot) == 13 ? 15 : 99)  // merge start, merge stats done
 #include "zh_attn_common.h"
 #include "zh_lpb_common.h"
@@ -60,11 +62,11 @@ constexpr uint32_t QA_NXCD = 8, QA_PER = 32;    // XCDs, workgroups per XCD
 
 // The two model shapes the kernel is built for:
 //   SH 3 (config 3): hidden 4096, 8 kv heads = one per XCD, Q4_K Q/K/V/O,
-//        contexts up to 32 x 3 sub-chunks of 64 tokens;
+//        contexts up to 65536;
 //   SH 4 (config 4): hidden 2048, 4 kv heads of 8 q heads: kv head h / 2 on
 //        XCD h, which takes its q heads 4 (h % 2) .. + 3 (both XCDs of a
 //        pair compute the kv head's k and v rows, identically); Q8_0
-//        Q/K/V/O; contexts up to 32 x 5 sub-chunks.
+//        Q/K/V/O; contexts up to 65536.
 // Either way an XCD owns 4 q heads, 24 projection rows per workgroup and the
 // O projection's columns of its 4 heads.
 template <int SH>
@@ -72,7 +74,7 @@ struct QaS {
     static constexpr uint32_t H = SH == 3 ? 4096 : 2048;
     static constexpr bool Q8 = SH == 4;                     // Q8_0 rows, else Q4_K
     static constexpr uint32_t KVX = SH == 3 ? 1 : 2;        // XCDs per kv head
-    static constexpr uint32_t MAXSUB = SH == 3 ? 3 : 5;     // K/V sub-chunks per chunk
+    static constexpr uint32_t MAXSUB = 32;                  // K/V sub-chunks per chunk (contexts up to 65536)
     static constexpr uint32_t NB = H / 256;                 // 256-element super-blocks of x
     static constexpr uint32_t ROWB = Q8 ? H / 32 * 34 : NB * 144;
     static constexpr uint32_t X = QA_W + QA_MAXR * ROWB;    // x | norm weight, XQ image, K/V sub-chunk 2
@@ -86,7 +88,7 @@ struct QaS {
     static constexpr uint32_t SUB3 = QA_W + 16384;          // K/V sub-chunk 3 (SH 4; the weight region, after the rows)
     static constexpr uint32_t RROWS = H / (QA_NXCD * QA_PER);  // residual rows each workgroup stores / zeroes
     static_assert(NB * 2 * RG_SEG + NB * 8 * 12 <= AR_SLOT && 2 * H * 4 <= AR_SLOT, "x | norm and the XQ image fit the x region");
-    static_assert(OW + OROWS * OROWB <= X && (MAXSUB <= 4 || SUB3 + AR_SLOT <= X), "O rows / sub-chunk 3 fit");
+    static_assert(OW + OROWS * OROWB <= X && SUB3 + AR_SLOT <= X, "O rows / sub-chunk slot 3 fit");
     static_assert(QA_MAXR * ROWB % 1024 == 0, "whole 1 KB copies of the rows");
 };
 
@@ -117,10 +119,13 @@ struct QaP {
     float *x_out, *zero;
 };
 
-// LDS offset of K/V sub-chunk s (sub-chunk 4 reuses 0's slot)
+// LDS offset of K/V sub-chunk s: a ring of four slots (the third is the x
+// region, free once the XQ image is in registers; the fourth the weight
+// region, free once the rows are computed)
 template <int SH>
 ZH_DEV uint32_t qa_slot(uint32_t s) {
-    return s == 0 || s == 4 ? 0u : s == 1 ? AR_SLOT : s == 2 ? QaS<SH>::X : QaS<SH>::SUB3;
+    const uint32_t r = s & 3;
+    return r == 0 ? 0u : r == 1 ? AR_SLOT : r == 2 ? QaS<SH>::X : QaS<SH>::SUB3;
 }
 
 template <int G, bool WITH_O, int SH>
@@ -189,7 +194,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     const uint32_t nv = (seq + CT - 1) / CT;  // chunks holding tokens
     const uint32_t t0 = j * CT, t1 = min(seq, t0 + CT);
     uint32_t nsub = j < nv ? (t1 - t0 + AR_TS - 1) / AR_TS : 0u;
-    if (nsub > QA_MAXSUB) {  // (the engine keeps the context within 32 x 192 tokens)
+    if (nsub > QA_MAXSUB) {  // (the engine keeps the context within 32 x 2048 tokens)
         if (tid == 0) __hip_atomic_fetch_or(p.ctl, ZH_DEVERR_ATTN_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         nsub = QA_MAXSUB;
     }
@@ -378,7 +383,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     }
     lds_bar();
     ZH_TRACE_POINT(4);
-    if (QA_MAXSUB > 3 && !wa && nsub > 3) issue_kv(3);  // the weight rows are read: their region takes sub-chunk 3
+    if (!wa && nsub > 3) issue_kv(3);  // the weight rows are read: their region takes sub-chunk 3
     // ---- publish the rows (wave 0), then wait for the kv head's other slices
     if (wave == 0) {
         if (lane < R) {
@@ -419,7 +424,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
             dma16(P.wo + (size_t)(j * QA_OROWS + row) * WO_ROWB + h * QA_OROWB + within * 16, lds0 + QA_OW + c * 1024);
         }
     };
-    if (WITH_O && !S::Q8 && !wa) issue_o();
+    if (WITH_O && nsub <= 3 && !wa) issue_o();  // (more sub-chunks: after the attention, see below)
     // ---- q as MFMA fragments (RMSNorm, RoPE, f16 hi + lo), shared through LDS
     const uint32_t sub = lane & 7, fg = lane & 15, fq = lane >> 4;
     const uint32_t gq = wave / 4, w4 = wave % 4;
@@ -508,7 +513,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         else if (tid < 32)
             *(u32x4 *)(Ks + AR_SLOT / 2 + r_own * 256 + pc) = *(const u32x4 *)((const uint8_t *)vnew16 + (tid - 16) * 16);
     };
-    if (owner && s_own < nsub && s_own != 4) substitute();
+    if (owner && s_own < nsub && s_own < 4) substitute();  // (later sub-chunks: once copied)
     lds_bar();
 
     // ---- scores and P V over the landed sub-chunks: group gq (4 waves) takes
@@ -518,15 +523,22 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
 #pragma unroll
     for (int n = 0; n < 8; n++) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (uint32_t it = 0; 2 * it < nsub; it++) {  // uniform: group gq takes sub-chunk 2 it + gq
-        if (QA_MAXSUB > 4 && it == 1 && nsub > 4) {
-            lds_bar();  // sub-chunk 0 is read: its slot takes sub-chunk 4
-            if (!wa) issue_kv(4);
-        }
-        if (QA_MAXSUB > 4 && it == 2) {
-            if (!wa) wait_vm<0>();
+        if (nsub > 4 && it >= 1) {  // (at most four sub-chunks: all copied before the loop)
+            // sub-chunks 2 it - 2 and 2 it - 1 are read: their slots take 2 it
+            // + 2 and 2 it + 3; then wait for this step's 2 it and 2 it + 1
+            // (copied one step earlier)
             lds_bar();
-            if (owner && s_own == 4) substitute();
+            uint32_t nnew = 0;
+            if (!wa) {
+                for (uint32_t s2 = 2 * it + 2; s2 < min(2 * it + 4, nsub); s2++) issue_kv(s2);
+                nnew = nsub > 2 * it + 2 ? min(nsub - (2 * it + 2), 2u) : 0u;
+                wait_vm_dyn(nnew * 8);
+            }
             lds_bar();
+            if (owner && s_own >= 4 && s_own / 2 == it) {
+                substitute();
+                lds_bar();
+            }
         }
         const uint32_t s = 2 * it + gq;
         if (s >= nsub) continue;  // uniform per wave
@@ -649,7 +661,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         ZH_TRACE_POINT(12);
         return;
     }
-    if (S::Q8 && !wa) issue_o();
+    if (nsub > 3 && !wa) issue_o();  // (the O rows' region held sub-chunk slot 3)
     // ---- WITH_O: every workgroup of the XCD merges the XCD's G heads itself
     // (their partials are in this XCD's L2) into LDS, as the XQ image of
     // the O projection's 4 G blocks of 32 (no second publication round)
@@ -802,7 +814,7 @@ uint32_t zhk_qkv_attn_flag_words() { return QA_FLAG_WORDS; }
 bool zhk_qkv_attn_supported(zh_ctx *c, uint32_t hidden, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx) {
     const uint32_t G = nkv ? nh / nkv : 0;
     const bool s3 = hidden == QaS<3>::H && nkv == QA_NXCD && nh == G * nkv && (G == 1 || G == 2 || G == 4) &&
-                    max_ctx <= QA_PER * QaS<3>::MAXSUB * AR_TS;
+                    max_ctx <= QA_PER * QaS<3>::MAXSUB * AR_TS;  // (the merge's 32 chunks of up to 2048 tokens)
     const bool s4 = hidden == QaS<4>::H && nkv == QA_NXCD / QaS<4>::KVX && nh == 4 * QA_NXCD &&
                     max_ctx <= QA_PER * QaS<4>::MAXSUB * AR_TS;
     return (s3 || s4) && hd == FD_HD && !c->concurrent && zhk_xcd_round_robin(c);
