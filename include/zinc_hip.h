@@ -314,11 +314,12 @@ int zh_engine_set_pages(zh_engine *eng, const uint32_t *pages, uint32_t n);
  * operation (decodeStep, forward.zig:4299). Default off. */
 int zh_engine_set_persistent(zh_engine *eng, int on);
 /* Run attn_norm + Q/K/V projections and the decode attention of each layer as
- * one launch (on != 0, the default) where it applies: 8 kv heads of 128 dims
- * on a device of 8 XCDs x 32 CUs (one kv head per XCD, so the projection's
- * outputs, the split-K partials and their flags are exchanged through that
- * XCD's L2), Q4_K Q/K/V over hidden 4096, identity page table, max_ctx <=
- * 6144, no engine sharing the device; elsewhere the two launches of
+ * one launch (on != 0, the default) where it applies, on a device of 8 XCDs x
+ * 32 CUs where each XCD owns 4 q heads (so the projection's outputs, the
+ * split-K partials and their flags are exchanged through that XCD's L2): 8
+ * kv heads of 128 dims with Q4_K Q/K/V over hidden 4096, or 4 kv heads of 8
+ * q heads with Q8_0 Q/K/V over hidden 2048; identity page table, max_ctx <=
+ * 65536, no engine sharing the device; elsewhere the two launches of
  * ZH_GROUP_QKV and ZH_GROUP_ATTN run. Replaces the reference's Q/K/V DMMV
  * dispatches plus its fused norm/RoPE/KV-write and flash-decode dispatches
  * (forward.zig:4776-4800, attention.zig:199-316). */

@@ -227,9 +227,9 @@ struct zh_step_args {
 uint64_t zh_step_ctl_bytes();
 // Q/K/V projection + decode attention in one launch (zh_qkv_attn.hip) on a
 // 256-CU device of 8 XCDs, identity page table, the device to itself: 8 kv
-// heads (one per XCD), Q4_K Q/K/V with K = 4096, contexts up to 6144; or 4
-// kv heads of 8 q heads (two XCDs each), Q8_0 Q/K/V with K = 2048, contexts
-// up to 10240 (hidden selects the shape).
+// heads (one per XCD), Q4_K Q/K/V with K = 4096; or 4 kv heads of 8 q heads
+// (two XCDs each), Q8_0 Q/K/V with K = 2048 (hidden selects the shape);
+// contexts up to 65536.
 bool zhk_xcd_round_robin(zh_ctx *ctx);
 bool zhk_qkv_attn_supported(zh_ctx *ctx, uint32_t hidden, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx);
 uint32_t zhk_qkv_attn_flag_words();  // zeroed u32 words the caller keeps per engine
