@@ -11,8 +11,8 @@
 // The 32 workgroups of XCD h (zh_xcd.h; slot j):
 //   1. stage ffn_norm(x) as XQ limbs and compute router rows [4 j, 4 j + 4)
 //      (every XCD computes all 128 logits, bit-identically, from the same
-//      bytes), publish them in the XCD's L2 and meet at an XCD-local flag
-//      barrier;
+//      bytes) and publish them in the XCD's L2 as epoch-tagged 64-bit words
+//      (zh_xcd.h tag_store), which every workgroup polls;
 //   2. every workgroup selects the top 8 of the 128 logits itself (the
 //      lowest index wins ties; weights: softmax over the selected logits) —
 //      XCD h takes the h-th selected expert e and its weight;
@@ -56,9 +56,9 @@ static_assert(MX_RPW * MX_RROW <= 9 * 1024 && MX_DTB % 1024 == 0, "router rows i
 static_assert(MX_NB * 2 * RG_SEG + MX_NB * 8 * 12 <= 8192, "XQ image below the SwiGLU limbs");
 }  // namespace
 
-// Flag words (zero when the engine is created): [0, 256) router rows
-// published, [256, 512) partials published (XCD h at h * 32), [512, 520)
-// epochs.
+// Flag words (zero when the engine is created): [0, 256) unused (the router
+// logits carry their own epoch tags), [256, 512) partials published (XCD h
+// at h * 32), [512, 520) epochs.
 constexpr uint32_t MX_FLAG_WORDS = 2 * XCD_N * XCD_PER + XCD_N;
 
 struct MoeP {
@@ -71,7 +71,7 @@ struct MoeP {
     const uint8_t *egate, *eup;   // Q4_K [128][768][2048]
     const uint8_t *pk;            // packed down [128][32][2048][24 B]
     float *y;                     // residual: += sum_k w_k down_k
-    float *logits;                // [8 XCDs][128] router logits (exchanged inside each XCD)
+    uint64_t *logits;             // [8 XCDs][128] tagged router logits (exchanged inside each XCD)
     float *part;                  // [256][2048] partial sums (exchanged inside each XCD)
     uint32_t *routing;            // [ids x 8][weights x 8], written by workgroup 0 (for inspection)
     uint32_t *flags;              // MX_FLAG_WORDS
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t h = min(xcc_id(), XCD_N - 1), j = blockIdx.x / XCD_N, w = h * XCD_PER + j;
-    uint32_t *fl_r = P.flags + h * XCD_PER, *fl_p = P.flags + XCD_N * XCD_PER + h * XCD_PER;
+    uint32_t *fl_p = P.flags + XCD_N * XCD_PER + h * XCD_PER;
     uint32_t *ep = P.flags + 2 * XCD_N * XCD_PER + h;
     const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
     const uint32_t lds0 = lds_addr(lds);
@@ -178,8 +178,7 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
         }
         float v = h2f(dw) * (ixs[lane] * comb_f(D[0], D[1], D[2]));
         v = wave_sum(v);
-        if (lane == 0) P.logits[h * MX_E + j * MX_RPW + wave] = v;
-        wait_vm<0>();
+        if (lane == 0) tag_store(P.logits + h * MX_E + j * MX_RPW + wave, v, E);
     }
     // ---- gate/up lanes: their half super-block of x in registers (before
     // the SwiGLU limbs overwrite anything near the image)
@@ -193,17 +192,20 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
         xs[q] = ixs[jb];
         xz[q] = ixz[2 * jb] + ixz[2 * jb + 1];
     }
-    __syncthreads();
-    if (tid == 0) *(volatile uint32_t *)(fl_r + j) = E;
-    const bool ok_r = xcd_wait(fl_r, XCD_PER, E, P.ctl, tid);
-    ZH_TRACE_POINT(2);
-    // ---- top 8 of the XCD's 128 logits (wave 0), this XCD's expert
+    // ---- top 8 of the XCD's 128 logits (wave 0, as they arrive), this
+    // XCD's expert
+    __shared__ uint32_t s_okr;
     if (wave == 0) {
-        const float v4[4] = {ld_dev(P.logits + h * MX_E + lane), ld_dev(P.logits + h * MX_E + 64 + lane), 0.f, 0.f};
+        float lv[2];
+        const bool okr = tag_wait<2>(P.logits + h * MX_E, E, P.ctl, lv);
+        ZH_TRACE_POINT(2);
+        const float v4[4] = {lv[0], lv[1], 0.f, 0.f};
         topk_softmax_wave(v4, MX_E, MX_K, s_route);
         if (blockIdx.x == 0 && lane < 2 * MX_K) P.routing[lane] = s_route[lane];
+        if (lane == 0) s_okr = okr ? 1u : 0u;
     }
     lds_bar();
+    const bool ok_r = s_okr != 0;
     uint32_t e = s_route[h];
     if (e >= MX_E) {  // a NaN router: clamp, as the per-group kernels do
         if (tid == 0) __hip_atomic_fetch_or(P.ctl, ZH_DEVERR_EXPERT_ID, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -441,7 +443,7 @@ __global__ void k_moe_pack_down(const uint8_t *q4, uint8_t *pk) {
 
 uint32_t zhk_moe_xcd_flag_words() { return MX_FLAG_WORDS; }
 uint64_t zhk_moe_pack_bytes() { return (uint64_t)MX_E * XCD_PER * MX_SLICE; }
-uint64_t zhk_moe_part_bytes() { return (uint64_t)XCD_N * XCD_PER * MX_H * 4 + XCD_N * MX_E * 4; }
+uint64_t zhk_moe_part_bytes() { return (uint64_t)XCD_N * XCD_PER * MX_H * 4 + XCD_N * MX_E * 8; }
 
 bool zhk_moe_xcd_supported(zh_ctx *c, uint32_t hidden, uint32_t n_experts, uint32_t n_used, uint32_t expert_ffn) {
     return hidden == MX_H && n_experts == MX_E && n_used == MX_K && expert_ffn == MX_F && !c->concurrent &&
@@ -464,7 +466,7 @@ int zhk_moe_xcd(zh_ctx *c, const float *x, const float *norm_w, float eps, const
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "moe_xcd: 16-byte aligned operands");
     MoeP P = {};
     P.x = x; P.xb = xb; P.xout = xout; P.zero = zero; P.norm_w = norm_w; P.eps = eps; P.router = router; P.egate = egate; P.eup = eup; P.pk = pk; P.y = y;
-    P.part = scratch; P.logits = scratch + (size_t)XCD_N * XCD_PER * MX_H;
+    P.part = scratch; P.logits = (uint64_t *)(scratch + (size_t)XCD_N * XCD_PER * MX_H);
     P.routing = routing; P.flags = flags; P.ctl = c->err_dev;
     static bool attr = false;
     if (!attr) {

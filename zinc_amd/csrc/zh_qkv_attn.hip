@@ -525,19 +525,21 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     for (uint32_t it = 0; 2 * it < nsub; it++) {  // uniform: group gq takes sub-chunk 2 it + gq
         if (nsub > 4 && it >= 1) {  // (at most four sub-chunks: all copied before the loop)
             // sub-chunks 2 it - 2 and 2 it - 1 are read: their slots take 2 it
-            // + 2 and 2 it + 3; then wait for this step's 2 it and 2 it + 1
-            // (copied one step earlier)
-            lds_bar();
-            uint32_t nnew = 0;
-            if (!wa) {
-                for (uint32_t s2 = 2 * it + 2; s2 < min(2 * it + 4, nsub); s2++) issue_kv(s2);
-                nnew = nsub > 2 * it + 2 ? min(nsub - (2 * it + 2), 2u) : 0u;
-                wait_vm_dyn(nnew * 8);
-            }
-            lds_bar();
-            if (owner && s_own >= 4 && s_own / 2 == it) {
-                substitute();
+            // + 2 and 2 it + 3; from step 2 on, wait for this step's 2 it and
+            // 2 it + 1 (copied one step earlier)
+            const uint32_t nnew = nsub > 2 * it + 2 ? min(nsub - (2 * it + 2), 2u) : 0u;
+            if (nnew) {
                 lds_bar();
+                if (!wa)
+                    for (uint32_t s2 = 2 * it + 2; s2 < 2 * it + 2 + nnew; s2++) issue_kv(s2);
+            }
+            if (it >= 2) {
+                if (!wa) wait_vm_dyn(nnew * 8);
+                lds_bar();
+                if (owner && s_own >= 4 && s_own / 2 == it) {
+                    substitute();
+                    lds_bar();
+                }
             }
         }
         const uint32_t s = 2 * it + gq;

@@ -61,3 +61,42 @@ ZH_DEV bool xcd_wait(const uint32_t *f, uint32_t n, uint32_t E, uint32_t *ctl, u
     lds_bar();  // (not __syncthreads: its fence may wait for the callers' copies in flight)
     return s_ok != 0;
 }
+
+// Tagged exchange: a value published as one 64-bit atomic word, the epoch in
+// the high half, so a reader polls the words themselves — no store
+// acknowledgement before a flag, no flag, no second read. (64-bit atomic
+// loads and stores are single-copy atomic.)
+ZH_DEV void tag_store(uint64_t *p, float v, uint32_t E) {
+    __hip_atomic_store(p, ((uint64_t)E << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// One wave: lane l reads words p[l + 64 i] (i < N) until all carry epoch E,
+// bounded by ctl[1] ticks as xcd_wait (a zero limit gives up at once). On
+// giving up the missing values are NaN, ZH_DEVERR_ATTN_WAIT is set and the
+// result is false (wave-uniform).
+template <int N>
+ZH_DEV bool tag_wait(const uint64_t *p, uint32_t E, uint32_t *ctl, float (&v)[N]) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    const uint64_t limit = __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t got = 0;
+    while (true) {
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            if (!((got >> i) & 1u)) {
+                const uint64_t w = __hip_atomic_load(p + lane + 64 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((uint32_t)(w >> 32) == E) {
+                    v[i] = __uint_as_float((uint32_t)w);
+                    got |= 1u << i;
+                }
+            }
+        }
+        if (__builtin_amdgcn_ballot_w64(got != (1u << N) - 1u) == 0 && limit != 0) return true;
+        if (__builtin_amdgcn_s_memrealtime() - t0 >= limit) {
+#pragma unroll
+            for (int i = 0; i < N; i++)
+                if (!((got >> i) & 1u)) v[i] = __builtin_nanf("");
+            if (lane == 0) __hip_atomic_fetch_or(ctl, ZH_DEVERR_ATTN_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+    }
+}
