@@ -74,6 +74,7 @@ struct zh_engine {
     bool persistent = false;  // zh_engine_set_persistent
     bool fused_qa = true;     // zh_engine_set_fused_attn: Q/K/V + attention in one launch where it applies
     uint32_t *qa_flags = nullptr;  // its XCD-local flag and epoch words (zero at creation)
+    uint64_t *qa_xrows = nullptr;  // its epoch-tagged Q/K/V rows (zero at creation)
     float *xin = nullptr;          // with the O projection in that launch: copy of the residual stream at layer entry
     bool fused_ffn = true;         // zh_engine_set_fused_ffn: the dense FFN as one per-XCD launch where it applies
     uint32_t *ffn_flags = nullptr; // its XCD-local flag and epoch words (zero at creation)
@@ -406,7 +407,7 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)}, {(void **)&e->router_cnt, 4}, {(void **)&e->am_cnt, 4},
         {(void **)&e->step_ctl, zh_step_ctl_bytes()}, {(void **)&e->step_layers, sizeof(zh_step_layer) * c.n_layers},
         {(void **)&e->qa_flags, 4ull * zhk_qkv_attn_flag_words()}, {(void **)&e->xin, 4ull * H},
-        {(void **)&e->ffn_flags, 4ull * zhk_ffn_xcd_flag_words()}, {(void **)&e->rres, 8ull * H},
+        {(void **)&e->ffn_flags, 4ull * zhk_ffn_xcd_flag_words()}, {(void **)&e->qa_xrows, zhk_qkv_attn_xrows_bytes()}, {(void **)&e->rres, 8ull * H},
         {(void **)&e->dres, 12ull * H},
         {(void **)&e->ffn_part, c.ffn == 12288 && H == 4096 ? zhk_ffn_part_bytes() : 0ull},
         {(void **)&e->moe_flags, 4ull * zhk_moe_xcd_flag_words()},
@@ -953,12 +954,12 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             ERC(zhk_qkv_attn(c, W(y.wq), W(y.wk), W(y.wv), e->rres, Wf(y.attn_norm), e->q, e->k, e->v,
                              Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc, m.max_ctx, e->attn, e->xq_q,
                              m.n_heads, pos, scale, m.eps, e->fd_part, e->qa_flags, W(y.wo), dr(ka + 1), dr(ka),
-                             e->rres + H, dr(ka + 2), H));
+                             e->rres + H, dr(ka + 2), H, e->qa_xrows));
         } else if (qa) {
             ERC(zhk_qkv_attn(c, W(y.wq), W(y.wk), W(y.wv), qa_o ? e->xin : e->hidden, Wf(y.attn_norm), e->q, e->k,
                              e->v, Wf(y.q_norm), Wf(y.k_norm), e->rope_cs, y.kc, y.vc, m.max_ctx, e->attn, e->xq_q,
                              m.n_heads, pos, scale, m.eps, e->fd_part, e->qa_flags, with_o ? W(y.wo) : nullptr,
-                             with_o ? e->hidden : nullptr, nullptr, nullptr, nullptr, H));
+                             with_o ? e->hidden : nullptr, nullptr, nullptr, nullptr, H, e->qa_xrows));
         } else if (!(mask & SK_QKV)) {
         } else if (lpb_attn) {
             // attn_norm fused into the Q/K/V mat-vec (every workgroup normalises x)

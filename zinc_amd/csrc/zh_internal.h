@@ -238,7 +238,8 @@ int zhk_qkv_attn(zh_ctx *ctx, const uint8_t *wq, const uint8_t *wk, const uint8_
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
                  uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
                  const uint8_t *wo = nullptr, float *x_acc = nullptr, const float *xb = nullptr,
-                 float *x_out = nullptr, float *zero = nullptr, uint32_t hidden = 4096);
+                 float *x_out = nullptr, float *zero = nullptr, uint32_t hidden = 4096, uint64_t *xrows = nullptr);
+uint64_t zhk_qkv_attn_xrows_bytes();  // zeroed bytes the caller keeps per engine (xrows: the rows' exchange)
 // xb != nullptr (with wo): the input is x + xb, stored into x_out (16 rows
 // per workgroup); x_acc starts at zero (it is not x's copy), `zero` (H
 // floats) is cleared. Per-XCD FFN (zh_ffn_xcd.hip) with the same split

@@ -94,10 +94,11 @@ struct QaS {
 
 }  // namespace
 
-// Flag words (zero when the engine is created): [0, 256) Q/K/V rows
-// published, [256, 512) partials published (head h at h * 32: one 128-byte
-// line per XCD), [512, 520) epochs.
+// Flag words (zero when the engine is created): [0, 256) unused (the Q/K/V
+// rows carry epoch tags), [256, 512) partials published (head h at h * 32:
+// one 128-byte line per XCD), [512, 520) epochs.
 constexpr uint32_t QA_FLAG_WORDS = 2 * QA_NXCD * QA_PER + QA_NXCD;
+constexpr uint32_t QA_XROWS = 4 * FD_HD + 2 * FD_HD;  // an XCD's q | k | v rows (at most 4 q heads)
 
 struct QaP {
     AttnP a;                      // q / k_new / v_new: the projection outputs (written here)
@@ -111,6 +112,7 @@ struct QaP {
     // the launch (a copy of it taken before, or the split residual below).
     const uint8_t *wo;
     float *x_acc;
+    uint64_t *xrows;              // [8][QA_XROWS] epoch-tagged Q/K/V rows (exchanged inside each XCD)
     // Split residual (with the O phase): the layer input is x + xb (xb: the
     // previous launch's atomic sums, staged in K/V sub-chunk 0's slot, whose
     // copy then waits until x is in registers); every workgroup stores its
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     // consecutive workgroups covers the 8 XCDs once)
     const uint32_t h = min(xcc_id(), QA_NXCD - 1), j = blockIdx.x / QA_NXCD, kvh = h / S::KVX;
     const uint32_t lds0 = lds_addr(lds);
-    uint32_t *fl_q = P.flags + h * QA_PER, *fl_p = P.flags + QA_NXCD * QA_PER + h * QA_PER;
+    uint32_t *fl_p = P.flags + QA_NXCD * QA_PER + h * QA_PER;
     uint32_t *ep = P.flags + 2 * QA_NXCD * QA_PER + h;
     // position and epoch through the scalar cache (no vector-memory count)
     const uint32_t posv = *(const __attribute__((address_space(4))) uint32_t *)p.pos.dev + p.pos.value;
@@ -384,32 +386,32 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     lds_bar();
     ZH_TRACE_POINT(4);
     if (!wa && nsub > 3) issue_kv(3);  // the weight rows are read: their region takes sub-chunk 3
-    // ---- publish the rows (wave 0), then wait for the kv head's other slices
-    if (wave == 0) {
-        if (lane < R) {
-            const uint32_t rr = j * R + lane;
-            float *dst = rr < QR ? (float *)p.q + h * QR + rr
-                       : rr < QR + FD_HD ? (float *)p.k_new + kvh * FD_HD + rr - QR
-                                         : (float *)p.v_new + kvh * FD_HD + rr - QR - FD_HD;
-            *dst = yl[lane];
-        }
-        wait_vm<0>();  // the rows are in the L2 before the flag
-        if (lane == 0) *(volatile uint32_t *)(fl_q + j) = E;
-    }
+    // ---- publish the rows as epoch-tagged words (wave 0): word rr of XCD h
+    // is row rr of its q | k | v rows (zh_xcd.h tag_store)
+    uint64_t *xr = P.xrows + (size_t)h * QA_XROWS;
+    if (wave == 0 && lane < R) tag_store(xr + j * R + lane, yl[lane], E);
     ZH_TRACE_POINT(5);
-    const bool ok_rows = xcd_wait(fl_q, QA_PER, E, p.ctl, tid);
-    ZH_TRACE_POINT(6);
-
-    // ---- the attention's inputs from the L2: the group's q, the new k | v
+    // ---- the attention's inputs: the XCD's q, the new k | v, polled from
+    // the L2 as they arrive (waves 0 .. NXW - 1, 128 words each) into LDS
     uint8_t *sm = lds + QA_W;  // q [G][128] f32 (QC KB), k_new | v_new (1 KB), new K / V rows f16, q fragments
-    for (uint32_t k = wave; k <= QC; k += QA_AW) {  // uniform per wave
-        const uint8_t *src = k < QC ? (const uint8_t *)(p.q + (size_t)h * QR) + min(k * 1024 + lane * 16, QR * 4 - 16)
-                           : lane < 32 ? (const uint8_t *)(p.k_new + (size_t)kvh * FD_HD) + lane * 16
-                                       : (const uint8_t *)(p.v_new + (size_t)kvh * FD_HD) + (lane - 32) * 16;
-        dma16_dev(src, lds0 + QA_W + k * 1024);
+    constexpr uint32_t NXW = (QR + 2 * FD_HD) / 128;
+    __shared__ uint32_t s_okw[QA_AW];
+    if (wave < NXW) {
+        float v2[2];
+        const bool okw = tag_wait<2>(xr + wave * 128, E, p.ctl, v2);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t rr = wave * 128 + 64 * i + lane;
+            ((float *)sm)[rr < QR ? rr : QC * 256 + rr - QR] = v2[i];
+        }
+        if (lane == 0) s_okw[wave] = okw ? 1u : 0u;
     }
-    wait_vm<0>();  // ... and every K/V sub-chunk
+    ZH_TRACE_POINT(6);
+    wait_vm<0>();  // every K/V sub-chunk
     lds_bar();
+    bool ok_rows = true;
+#pragma unroll
+    for (uint32_t w = 0; w < NXW; w++) ok_rows = ok_rows && s_okw[w] != 0;
     ZH_TRACE_POINT(7);
     // ---- WITH_O: this workgroup's O rows (128 rows x the XCD's two
     // super-blocks, 36 KB) into the weight region's free part, by waves 4-7
@@ -811,6 +813,7 @@ bool zhk_xcd_round_robin(zh_ctx *c) {
 }
 
 uint32_t zhk_qkv_attn_flag_words() { return QA_FLAG_WORDS; }
+uint64_t zhk_qkv_attn_xrows_bytes() { return 8ull * QA_NXCD * QA_XROWS; }
 
 // Whether k_qkv_attn takes a model of this shape on this context.
 bool zhk_qkv_attn_supported(zh_ctx *c, uint32_t hidden, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx) {
@@ -826,7 +829,8 @@ int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t 
                  const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
                  uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
-                 const uint8_t *wo, float *x_acc, const float *xb, float *x_out, float *zero, uint32_t hidden) {
+                 const uint8_t *wo, float *x_acc, const float *xb, float *x_out, float *zero, uint32_t hidden,
+                 uint64_t *xrows) {
     QaP P = {};
     AttnP &p = P.a;
     p.q = q; p.k_new = k; p.v_new = v; p.q_norm = qw; p.k_norm = kw; p.rope_cs = rope_cs;
@@ -834,12 +838,12 @@ int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t 
     p.scale = scale; p.eps = eps; p.part = partials; p.n_chunks = QA_PER; p.counters = nullptr;
     p.out = out; p.xq = (uint8_t *)xq_out; p.nq = nh; p.nd = QA_PER; p.no_wait = 0; p.ident = 1; p.ctl = c->err_dev;
     P.wq = wq; P.wk = wk; P.wv = wv; P.x = x; P.norm_w = norm_w; P.flags = flags;
-    P.wo = wo; P.x_acc = x_acc; P.xb = xb; P.x_out = x_out; P.zero = zero;
+    P.wo = wo; P.x_acc = x_acc; P.xb = xb; P.x_out = x_out; P.zero = zero; P.xrows = xrows;
     P.kv_defer = xb || hidden != QaS<3>::H ? 0u : (uint32_t)zh_knob_int("ZH_QA_DEFER", 0);
     if (xb && (!wo || !x_out || !zero || ((uintptr_t)xb & 15) || ((uintptr_t)x_out & 15)))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: split residual needs the O phase and aligned rows");
     const uint32_t G = nh / QA_NXCD;
-    if ((wo && (!x_acc || ((uintptr_t)wo & 15))) || !pos.dev || ((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wq & 15) || ((uintptr_t)wk & 15) ||
+    if (!xrows || (wo && (!x_acc || ((uintptr_t)wo & 15))) || !pos.dev || ((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wq & 15) || ((uintptr_t)wk & 15) ||
         ((uintptr_t)wv & 15))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "qkv_attn: device position and 16-byte aligned operands");
 #define QA_L(GG, WO, SS)                                                                                         \
