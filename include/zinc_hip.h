@@ -449,12 +449,13 @@ int zh_engine_tensor_type(zh_engine *eng, uint64_t stream, uint32_t *type);
 #define ZH_GROUP_FFN_OUT 16u /* down projection + residual (MoE: + weighted expert sum) */
 /* ZH_GROUP_FFN_IN | ZH_GROUP_FFN_OUT: both as the step runs them (one launch
  * when zh_engine_set_fused_ffn applies) */
+#define ZH_GROUP_HEAD 32u    /* output_norm + LM head + argmax (not per layer) */
 /* Average duration of one launch of `group`, replayed with the engine's own
  * arguments and state over `iters` launches rotating through the layers, by
  * HIP events on the engine's stream. Leaves the activations changed. */
 int zh_engine_time_kernel(zh_engine *eng, uint32_t group, uint32_t iters, float *us_per_launch);
 /* The kernels one launch group of layer 0 launches (mangled names, read
- * from the graph its launches capture into), joined with "; " into names. */
+ * from the graph its launches capture into; ZH_GROUP_HEAD: the output head), joined with "; " into names. */
 int zh_engine_group_kernels(zh_engine *eng, uint32_t group, char *names, size_t len);
 /* Algorithmic bytes of one launch of `group` at context length L. */
 uint64_t zh_engine_group_bytes(zh_engine *eng, uint32_t group, uint32_t L);

@@ -742,7 +742,7 @@ static int record_collect(zh_engine *e, bool advance = false) {
     const zh_model_config &m = e->c;
     const uint32_t H = m.hidden;
     const uint8_t *A = e->arena;
-    if (!zh_knob("ZH_NO_LPB")&& zhk_lpb_supported(e->lm.type, H) && m.vocab % 2 == 0) {
+    if (!zh_knob("ZH_NO_LPB") && zhk_lpb_supported(e->lm.type, H) && m.vocab % 2 == 0) {
         const uint8_t *wl = A + e->lm.off;
         float *yl = e->logits;
         const uint32_t mv = m.vocab;
@@ -1119,12 +1119,13 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
 // capture into (each kernel node's function, named by the runtime), joined
 // with "; " into names (at most len bytes, NUL-terminated).
 extern "C" int zh_engine_group_kernels(zh_engine *e, uint32_t group, char *names, size_t len) {
-    if (!e || !names || len == 0 || group == 0 || (group & ~(uint32_t)SK_ALL)) return ZH_ERR_INVALID_ARGUMENT;
+    if (!e || !names || len == 0 || group == 0 || (group != SK_HEAD && (group & ~(uint32_t)SK_ALL)))
+        return ZH_ERR_INVALID_ARGUMENT;
     zh_ctx *c = e->ctx;
     ERC(ensure_packed(e));
     hipGraph_t g = nullptr;
     EHIP(e, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    int rc = record_step(e, false, 0, 1, group);
+    int rc = group == SK_HEAD ? record_collect(e) : record_step(e, false, 0, 1, group);
     const hipError_t ce = hipStreamEndCapture(c->stream, &g);
     if (rc) return rc;
     if (ce != hipSuccess) return zh_set_err(c, ZH_ERR_HIP, "capture: %s", hipGetErrorString(ce));
