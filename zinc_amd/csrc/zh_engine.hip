@@ -66,7 +66,7 @@ struct zh_engine {
     uint32_t *routing = nullptr, *am_part = nullptr, *st = nullptr, *prompt = nullptr, *ring = nullptr;
     uint32_t *grp_cnt = nullptr;  // SwiGLU-output XQ: one counter per 32-row group (kept zero between launches)
     uint32_t *router_cnt = nullptr;
-    uint32_t *am_cnt = nullptr;      // k_argmax_advance: workgroups finished (kept zero between launches)  // router top-k: workgroups finished (kept zero between launches)
+    uint32_t *am_cnt = nullptr;      // k_argmax_advance: workgroups finished (kept zero between launches)
     // persistent decode-layers kernel: barrier / merge words (zero between
     // launches) and the device table of layer pointers
     uint32_t *step_ctl = nullptr;
@@ -137,13 +137,22 @@ __global__ void k_advance(uint32_t *st, const uint32_t *prompt) {
 // publication pattern) reduces the shares, records the token
 // (argmaxGreedy, forward.zig:10348-10356) and advances the state as
 // k_advance. The counter is left zero for the next launch.
-constexpr uint32_t TAIL_WGS = 128;
+constexpr uint32_t TAIL_WGS = 256;  // (am_part holds 256 (value, index) pairs)
 __global__ __launch_bounds__(256) void k_argmax_advance(const float *__restrict__ x, uint32_t n, uint32_t *partials,
                                                         uint32_t *cnt, uint32_t *ring, uint32_t *st,
                                                         const uint32_t *prompt) {
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
-    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) am_better(bv, bi, x[i], i);
+    // 4 logits per load (x is 16-byte aligned); workgroup 0 also takes the n % 4 last ones
+    const uint32_t n4 = n / 4;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += gridDim.x * 256) {
+        const float4 v = ((const float4 *)x)[i];
+        am_better(bv, bi, v.x, 4 * i);
+        am_better(bv, bi, v.y, 4 * i + 1);
+        am_better(bv, bi, v.z, 4 * i + 2);
+        am_better(bv, bi, v.w, 4 * i + 3);
+    }
+    if (blockIdx.x == 0 && 4 * n4 + threadIdx.x < n) am_better(bv, bi, x[4 * n4 + threadIdx.x], 4 * n4 + threadIdx.x);
     am_wave(bv, bi);
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
