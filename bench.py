@@ -10,7 +10,9 @@ import argparse
 import json
 import os
 import re
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -63,6 +65,15 @@ def cpu_baseline(cfg, n_tokens=16):
     """The CPU oracle (C restatement of the reference's dequantRow + serial f32
     dot path, threaded over rows as forward_metal.zig:3932-3933) decoding
     `n_tokens` tokens of the same model at position PREFILL."""
+    # the baseline runs a build for this host's own CPU (BASELINE's -march=native),
+    # made here from the committed source; the shipped x86-64-v3 copy if that fails
+    native = os.path.join(tempfile.gettempdir(), f"zo_native_{os.getpid()}", "libzinc_oracle.so")
+    os.makedirs(os.path.dirname(native), exist_ok=True)
+    mk = subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "MARCH=native", f"OUT={native}"],
+                        capture_output=True, text=True)
+    march = "native" if mk.returncode == 0 and os.path.exists(native) else "x86-64-v3"
+    if march == "native":
+        os.environ["ZO_LIB_PATH"] = native
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     nproc = os.cpu_count() or 1
@@ -80,7 +91,7 @@ def cpu_baseline(cfg, n_tokens=16):
     return {"value": round(n_tokens / dt, 4), "unit": "tok/s", "cores": threads, "threads": threads,
             "nproc": nproc, "kind": "port",
             "sample": f"{n_tokens} greedy decode steps of the same 8B-shaped model at context {PREFILL} "
-                      f"(oracle build {build_s:.0f}s untimed)"}
+                      f"(oracle built with -march={march}; model build {build_s:.0f}s untimed)"}
 
 
 def main():

@@ -10,9 +10,9 @@ build's s_memrealtime trace points (100 MHz clock):
 
 Build the debug library first (it also compiles the points in):
 
-    python -m zinc_amd.build --debug _work/dbg
-    ZH_LIB_PATH=_work/dbg/libzinc_hip.so python -m benchmarks.step_phases
-    ZH_LIB_PATH=_work/dbg/libzinc_hip.so python -m benchmarks.step_phases --standalone
+    python -m zinc_amd.build --debug build/debug
+    ZH_LIB_PATH=build/debug/libzinc_hip.so python -m benchmarks.step_phases
+    ZH_LIB_PATH=build/debug/libzinc_hip.so python -m benchmarks.step_phases --standalone
 
 --qkv-attn: the Q/K/V + attention launch (k_qkv_attn) of the per-phase
 step, replayed by zh_engine_time_kernel.
@@ -124,8 +124,8 @@ def qkv_attn():
 RING_POINTS = ["start", "activation landed", "XQ limbs in registers", "ring done", "outputs stored"]
 
 
-FFN_POINTS = ["start", "activation landed", "XQ limbs in registers", "gate/up done", "down activation ready",
-              "down done", "partials seen", "end", "", "", "", "gate/up tile 0 in LDS"]
+FFN_POINTS = ["start", "activation landed", "XQ limbs in registers", "gate/up done", "down activation in registers",
+              "down done", "SwiGLU blocks of the XCD seen", "end", "", "", "", "gate/up tile 0 in LDS"]
 
 
 MOE_POINTS = ["start", "x, norm, router rows landed", "router logits of the XCD seen", "top-8 selected",

@@ -295,6 +295,18 @@ int zh_engine_generate_batch(zh_engine *const *engines, uint32_t n_seq, const ui
 int zh_engine_logits(zh_engine *eng, float *dst);
 /* Copy the hidden state (hidden f32) after the last step to host. */
 int zh_engine_hidden(zh_engine *eng, float *dst);
+/* No counterpart in the reference (inspection, for parity tests): the
+ * n_experts_used expert ids and routing weights the last decode step's router
+ * top-k selected in `layer` (MoE models; ZH_ERR_INVALID_ARGUMENT otherwise). */
+int zh_engine_routing(zh_engine *eng, uint32_t layer, uint32_t *ids, float *weights);
+/* No counterpart in the reference (test hook): make the per-XCD MoE launch run
+ * the given experts (ids [n_layers][n_experts_used], n = their count) instead
+ * of its own selection, weighted by the softmax over their router logits; the
+ * selection it computed is still what zh_engine_routing returns. ids = NULL
+ * switches it off. ZH_ERR_INVALID_ARGUMENT for models that do not take that
+ * launch. For parity tests that follow another implementation's routing
+ * through near ties. */
+int zh_engine_force_routing(zh_engine *eng, const uint32_t *ids, uint32_t n);
 /* Weight tensor by oracle stream id ((layer+1)<<8 | kind, or 1/2/3 globals). */
 int zh_engine_tensor(zh_engine *eng, uint64_t stream, zh_buf **buf, uint64_t *offset, uint64_t *bytes);
 /* Gather n logical tokens of layer `layer` K (which=0) or V (1) as fp16,

@@ -38,9 +38,10 @@ _lib = None
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
+        path = os.environ.get("ZO_LIB_PATH") or LIB_PATH  # (bench.py: a -march=native build of the same source)
+        if path == LIB_PATH and not os.path.exists(LIB_PATH):
             build()
-        L = C.CDLL(LIB_PATH)
+        L = C.CDLL(path)
         u8p, f32p, f64p, u16p, u32p = (C.POINTER(C.c_uint8), C.POINTER(C.c_float),
                                        C.POINTER(C.c_double), C.POINTER(C.c_uint16),
                                        C.POINTER(C.c_uint32))
@@ -86,6 +87,7 @@ def lib():
             "zo_more_bits_layer": (C.c_int, [C.c_uint32, C.c_uint32]),
             "zo_model_hidden": (C.c_void_p, [C.c_void_p]),
             "zo_model_route_gap": (C.c_float, [C.c_void_p]),
+            "zo_model_routing": (C.c_int, [C.c_void_p, C.c_uint32, u32p, f32p, C.POINTER(C.c_float)]),
             "zo_model_kv": (C.c_void_p, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32]),
         }
         for name, (res, args) in sig.items():
@@ -343,6 +345,20 @@ class Model:
         last decode step over its MoE layers, relative to max |router logit|
         (inf for a dense model)."""
         return float(lib().zo_model_route_gap(self.h))
+
+    def routing(self, layer):
+        """(selected expert ids, their weights, router gap) of `layer` in the
+        last decode step: ids and weights in topKSoftmax's order, the gap as
+        route_gap's for that layer alone (inf: no near tie)."""
+        k = self.cfg["n_experts_used"]
+        ids = np.zeros(16, dtype=np.uint32)
+        w = np.zeros(16, dtype=np.float32)
+        gap = C.c_float()
+        rc = lib().zo_model_routing(self.h, layer, ids.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                    w.ctypes.data_as(C.POINTER(C.c_float)), C.byref(gap))
+        if rc != 0:
+            raise ValueError("routing: dense model or layer out of range")
+        return ids[:k].copy(), w[:k].copy(), float(gap.value)
 
     def hidden(self):
         p = lib().zo_model_hidden(self.h)

@@ -533,10 +533,20 @@ float zo_normal(uint64_t r) {
 }
 static inline uint16_t scale_f16(uint64_t r) { return zo_f32_to_f16(fabsf(zo_normal(r)) * 0.02f); }
 
+/* the router weights' scale shift: 2^-e with 2^e nearest to 1.466 sqrt(K), 1.466 being the standard
+ * deviation of the synthetic Q8_0 weights d * q (d = |N(0, .02)|, q uniform -127..127) */
+uint32_t zo_router_shift(uint64_t K) {
+    long e = lround(log2(1.466 * sqrt((double)K)));
+    return e < 0 ? 0u : e > 15 ? 15u : (uint32_t)e;
+}
+
 int zo_synth_tensor(uint8_t *dst, uint32_t type_flags, uint64_t rows, uint64_t cols,
                     uint64_t seed, uint64_t stream) {
     /* type | 0x100: model-init variant of Q4_K / Q5_K with dmin = f16(7.5 * d) / f16(15.5 * d) (zero-mean
      * sub-blocks); the synthetic models use it for every Q4_K tensor. */
+    /* type | 0x200 | e << 12: a router (Q8_0): d = f16(d * 2^-e), e = zo_router_shift(cols), so that the
+     * router logits of an RMS-normed input are about N(0,1), not the O(sqrt(cols))
+     * of the other projections, whose outputs the next RMSNorm rescales. */
     uint32_t type = type_flags & 0xFF;
     int centered = (type_flags & 0x100) != 0;
     uint64_t bs = zo_block_size(type), bpb = zo_bytes_per_block(type);
@@ -582,6 +592,8 @@ int zo_synth_tensor(uint8_t *dst, uint32_t type_flags, uint64_t rows, uint64_t c
         }
         case ZO_Q8_0: { /* f16 scale |N(0,.02)|; int8 uniform -127..127 */
             uint16_t d = scale_f16(zo_rand(seed, stream, b * 16 + 0));
+            if (type_flags & 0x200) /* router: d * 2^-e (e in bits 12..15) */
+                d = zo_f32_to_f16(ldexpf(zo_f16_to_f32(d), -(int)((type_flags >> 12) & 15)));
             o[0] = d & 0xFF; o[1] = d >> 8;
             for (int i = 0; i < 32; i++) {
                 uint64_t r = zo_rand(seed, stream, b * 16 + 1 + i / 4);
@@ -663,6 +675,11 @@ struct zo_model {
      * can flip); layers whose selection includes a zero-probability expert
      * have no such tie */
     float route_gap;
+    /* test diagnostic: per MoE layer of the last decode step, the selected
+     * expert ids (n_experts_used each) and that layer's gap as above
+     * (INFINITY when it has none) */
+    uint32_t *sel_ids;
+    float *sel_w, *sel_gap;
 };
 
 static uint8_t *alloc_tensor(uint32_t type, uint64_t rows, uint64_t cols, uint64_t seed, uint64_t stream) {
@@ -706,7 +723,9 @@ static void build_layer(zo_model *m, uint32_t l) {
         y->up = alloc_tensor(y->t[ZK_UP], c->ffn, H, s, ZS_LAYER(l, ZK_UP));
         y->down = alloc_tensor(y->t[ZK_DOWN], H, c->ffn, s, ZS_LAYER(l, ZK_DOWN));
     } else {
-        y->router = alloc_tensor(y->t[ZK_ROUTER], c->n_experts, H, s, ZS_LAYER(l, ZK_ROUTER));
+        y->router = (uint8_t *)malloc(zo_tensor_bytes(y->t[ZK_ROUTER], c->n_experts, H));
+        zo_synth_tensor(y->router, y->t[ZK_ROUTER] | 0x100 | 0x200 | (zo_router_shift(H) << 12), c->n_experts, H, s,
+                        ZS_LAYER(l, ZK_ROUTER));
         y->egate = alloc_tensor(y->t[ZK_EXP_GATE], (uint64_t)c->n_experts * c->expert_ffn, H, s, ZS_LAYER(l, ZK_EXP_GATE));
         y->eup = alloc_tensor(y->t[ZK_EXP_UP], (uint64_t)c->n_experts * c->expert_ffn, H, s, ZS_LAYER(l, ZK_EXP_UP));
         y->edown = alloc_tensor(y->t[ZK_EXP_DOWN], (uint64_t)c->n_experts * H, c->expert_ffn, s, ZS_LAYER(l, ZK_EXP_DOWN));
@@ -757,6 +776,9 @@ zo_model *zo_model_create(const zo_model_config *cfg, int nthreads) {
     m->logits = (float *)calloc(c->vocab, 4);
     m->rl = (float *)calloc(c->n_experts ? c->n_experts : 1, 4);
     m->eacc = (float *)calloc(H, 4);
+    m->sel_ids = (uint32_t *)calloc((size_t)c->n_layers * 16 + 1, 4);
+    m->sel_gap = (float *)calloc((size_t)c->n_layers + 1, 4);
+    m->sel_w = (float *)calloc((size_t)c->n_layers * 16 + 1, 4);
     return m;
 }
 
@@ -771,7 +793,7 @@ void zo_model_destroy(zo_model *m) {
     }
     free(m->L); free(m->embd); free(m->lm); free(m->out_norm); free(m->inv_freq);
     free(m->hidden); free(m->norm); free(m->q); free(m->k); free(m->v); free(m->attn);
-    free(m->g); free(m->u); free(m->s); free(m->logits); free(m->rl); free(m->eacc);
+    free(m->g); free(m->u); free(m->s); free(m->logits); free(m->rl); free(m->eacc); free(m->sel_ids); free(m->sel_w); free(m->sel_gap);
     free(m);
 }
 
@@ -856,6 +878,15 @@ int zo_model_set_tensor(zo_model *m, uint64_t stream, uint32_t type, const void 
 }
 const float *zo_model_hidden(zo_model *m) { return m->hidden; }
 float zo_model_route_gap(const zo_model *m) { return m->route_gap; }
+int zo_model_routing(const zo_model *m, uint32_t layer, uint32_t *ids, float *weights, float *gap) {
+    if (!m->c.n_experts || layer >= m->c.n_layers) return -1;
+    for (uint32_t j = 0; j < m->c.n_experts_used && j < 16; j++) {
+        ids[j] = m->sel_ids[(size_t)layer * 16 + j];
+        weights[j] = m->sel_w[(size_t)layer * 16 + j];
+    }
+    *gap = m->sel_gap[layer];
+    return 0;
+}
 const uint16_t *zo_model_kv(zo_model *m, uint32_t layer, uint32_t which, uint32_t token) {
     if (layer >= m->c.n_layers || which > 1 || token >= m->c.max_ctx) return NULL;
     const zo_layer *y = &m->L[layer];
@@ -962,7 +993,13 @@ uint32_t zo_model_decode_step(zo_model *m, uint32_t token, uint32_t pos, float *
                     if (!sel) rest = fmaxf(rest, m->rl[i]);
                     amax = fmaxf(amax, fabsf(m->rl[i]));
                 }
-                if (amax > 0.f && !zero) m->route_gap = fminf(m->route_gap, (kth - rest) / amax);
+                const float lg = amax > 0.f && !zero ? (kth - rest) / amax : INFINITY;
+                m->route_gap = fminf(m->route_gap, lg);
+                m->sel_gap[l] = lg;
+                for (uint32_t j = 0; j < c->n_experts_used && j < 16; j++) {
+                    m->sel_ids[(size_t)l * 16 + j] = ids[j];
+                    m->sel_w[(size_t)l * 16 + j] = w[j];
+                }
             }
             uint64_t gstride = zo_tensor_bytes(y->t[ZK_EXP_GATE], F, H), ustride = zo_tensor_bytes(y->t[ZK_EXP_UP], F, H);
             uint64_t dstride = zo_tensor_bytes(y->t[ZK_EXP_DOWN], H, F);

@@ -99,9 +99,13 @@ uint32_t zo_kv_page_count(uint32_t context_tokens);
 uint64_t zo_rand(uint64_t seed, uint64_t stream, uint64_t ctr);
 float    zo_normal(uint64_t r);
 /* Fill a rows x cols tensor of `type` with BASELINE-distributed random blocks.
- * type | 0x100 (Q4_K / Q5_K): model-init variant, dmin = f16(7.5*d) / f16(15.5*d). */
+ * type | 0x100 (Q4_K / Q5_K): model-init variant, dmin = f16(7.5*d) / f16(15.5*d).
+ * type | 0x200 | e << 12 (Q8_0): a router, d = f16(d * 2^-e). */
 int  zo_synth_tensor(uint8_t *dst, uint32_t type, uint64_t rows, uint64_t cols,
                      uint64_t seed, uint64_t stream);
+/* e of the router flag for a router with K columns: router logits of an
+ * RMS-normed input about N(0,1) */
+uint32_t zo_router_shift(uint64_t K);
 void zo_synth_normal_f32(float *dst, uint64_t n, float scale, uint64_t seed, uint64_t stream);
 void zo_synth_normal_f16(uint16_t *dst, uint64_t n, uint64_t seed, uint64_t stream);
 void zo_synth_norm_weight(float *dst, uint64_t n, uint64_t seed, uint64_t stream);
@@ -142,6 +146,11 @@ int       zo_model_set_tensor(zo_model *m, uint64_t stream, uint32_t type, const
 const float   *zo_model_hidden(zo_model *m);
 /* test diagnostic: smallest relative router top-k gap of the last step */
 float          zo_model_route_gap(const zo_model *m);
+/* test diagnostic: the experts the last decode step selected in `layer`
+ * (n_experts_used ids and weights, in topKSoftmax's order) and that layer's
+ * router gap as zo_model_route_gap's (INFINITY: no tie, e.g. a selection
+ * holding zero-probability experts); -1 for a dense model */
+int            zo_model_routing(const zo_model *m, uint32_t layer, uint32_t *ids, float *weights, float *gap);
 /* fp16 K (which 0) or V (1) cache row of `token` in `layer`: n_kv_heads*head_dim values. */
 const uint16_t *zo_model_kv(zo_model *m, uint32_t layer, uint32_t which, uint32_t token);
 

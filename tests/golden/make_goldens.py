@@ -6,7 +6,8 @@ dequantRow + serial f32 dot decode path, forward.zig / forward_metal.zig):
                experts top-8, expert FFN 768; experts Q4_K, router and
                attention Q8_0, LM head Q6_K over vocab 151936), KV prefilled to
                8192 positions, a 16-token prompt, then 256 greedy tokens
-               -> moe48_greedy256.json
+               -> moe48_greedy256.json, and every decode step's per-layer
+               expert selection and router gap -> moe48_routing.npz
   dense8b_32k  config 5 decode: the 8B-shaped dense model (config 3's),
                KV prefilled to 32768 positions, a 16-token prompt, then 128
                greedy tokens -> dense8b_32k_greedy128.json
@@ -43,9 +44,19 @@ def greedy_fixture(cfg, prefill, n_gen, out_name):
     om.prefill_kv_random(prefill, KV_SEED)
     print(f"{out_name}: model built in {time.time() - t0:.0f}s", flush=True)
     prompt = [int(t) for t in np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], N_PROMPT)]
+    routed = cfg.get("n_experts", 0) > 0
+    r_ids, r_gaps = [], []
+
+    def record_routing():
+        if routed:
+            sel = [om.routing(layer) for layer in range(cfg["n_layers"])]
+            r_ids.append([s[0].tolist() for s in sel])
+            r_gaps.append([s[2] for s in sel])
+
     pos = prefill
     for t in prompt[:-1]:
         om.decode_step(t, pos)
+        record_routing()
         pos += 1
     tok, toks, margins, gaps = prompt[-1], [], [], []
     for i in range(n_gen):
@@ -53,6 +64,7 @@ def greedy_fixture(cfg, prefill, n_gen, out_name):
         s = np.sort(lg)
         margins.append(float(s[-1] - s[-2]) / float(np.abs(lg).max()))
         gaps.append(min(om.route_gap(), 1.0))
+        record_routing()
         toks.append(int(tok))
         pos += 1
         if i % 16 == 0:
@@ -63,6 +75,12 @@ def greedy_fixture(cfg, prefill, n_gen, out_name):
            "rel_margins": margins, "route_gaps": gaps, "generator": "oracle/zinc_oracle.c zo_model_decode_step"}
     with open(os.path.join(HERE, out_name), "w") as f:
         json.dump(out, f)
+    if routed:
+        # decode step s (the prompt's first N_PROMPT - 1 tokens, then the
+        # generated steps), layer l: the oracle's selected experts and that
+        # layer's router gap (zo_model_routing)
+        np.savez_compressed(os.path.join(HERE, out_name.split("_")[0] + "_routing.npz"),
+                            ids=np.array(r_ids, dtype=np.uint8), gaps=np.array(r_gaps, dtype=np.float32))
     print(f"{out_name}: min relative margin {min(margins):.3g}, {time.time() - t0:.0f}s", flush=True)
 
 

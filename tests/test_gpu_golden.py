@@ -36,26 +36,26 @@ def test_dense8b_greedy_256_token_exact(persistent):
 
 # A greedy step whose top-2 logits the oracle separates by less than this
 # fraction of max |logit| is a near tie: a sum in another order may pick the
-# other token (the decode tolerance is 1e-3 of the scale). A mismatch is
-# accepted only at a near-tie step, and the run then continues from the
-# oracle's token (the prompt re-decoded with the oracle's tokens appended).
+# other token (the decode tolerance is 1e-3 of the scale). A mismatch there is
+# accepted, and the run then continues from the oracle's token (the prompt
+# re-decoded with the oracle's tokens appended).
 NEAR_TIE = 1e-3
-# A routed model adds a second, discrete source of divergence: in a layer
-# whose k-th selected router logit beats the best unselected one by a small
-# gap, the GPU's hidden state (~1e-5 of its scale from sums in another order)
-# can select the other expert, which moves that step's logits by up to tenths
-# of their scale and, through the K/V rows written at that step, every later
-# step a little. With config 4's 48 layers of near-uniform routing over 128
-# experts, 85% of the fixture's steps have a layer whose gap is below 1e-3 of
-# the layer's max |router logit|. Measured on MI355X: 57 of the 256 steps
-# mismatch, more of them late in the run (the cache rows of earlier swapped
-# steps add up), every one at a router gap of at most 1.5e-3 (most below
-# 3e-4, the first at 5e-6; later ones, after the cache has taken the rows of
-# swapped steps, up to 3e-3). So for a routed model the first mismatch must
-# sit at a step whose oracle margin is below NEAR_TIE or whose router gap is
-# below ROUTE_TIE (it comes from summation order alone), and at most
-# MAX_ROUTED_MISMATCH of the steps may mismatch.
-ROUTE_TIE, MAX_ROUTED_MISMATCH = 2e-3, 0.3
+# A routed model adds a second, discrete source of divergence. In a layer
+# whose k-th selected router logit beats the best unselected one by a gap
+# (relative to the layer's max |router logit|) of the order of the GPU's
+# hidden-state drift from the oracle (~1e-5 of its scale: the same sums in
+# another order), the GPU may select the other expert; that moves the step's
+# logits by tenths of their scale and, through the K/V rows it writes, every
+# later step. The fixture records each step's smallest gap over its layers.
+# In this free-running check (the engine's own generate, device-side token
+# feedback), before the first step whose gap is below ROUTE_FLIP the GPU's
+# cache rows are the oracle's to the drift, so a mismatch there needs an
+# oracle margin below NEAR_TIE or a gap below ROUTE_FLIP. From that step on
+# the cache holds rows of steps that may have run another expert, and
+# mismatches are only counted (at most MAX_ROUTED_MISMATCH): the strict
+# config-4 check is test_moe48_routing_followed_256, which runs the oracle's
+# selection so that no such rows arise.
+ROUTE_FLIP, MAX_ROUTED_MISMATCH = 1e-4, 64
 
 
 def _greedy_fixture(name):
@@ -65,7 +65,9 @@ def _greedy_fixture(name):
     ref, margins = g["tokens"], g["rel_margins"]
     routed = "route_gaps" in g
     gaps = g.get("route_gaps", [1.0] * len(ref))
-    print(f"{name}: {cfg['n_layers']} layers, KV prefill {g['prefill']}, {len(ref)} tokens", flush=True)
+    first_flip = next((i for i in range(len(ref)) if gaps[i] < ROUTE_FLIP), len(ref)) if routed else len(ref)
+    print(f"{name}: {cfg['n_layers']} layers, KV prefill {g['prefill']}, {len(ref)} tokens"
+          + (f", first step with a router gap below {ROUTE_FLIP:g}: {first_flip}" if routed else ""), flush=True)
     ctx = zinc_amd.Context(0)
     ties = []
     try:
@@ -78,16 +80,17 @@ def _greedy_fixture(name):
             if not bad:
                 break
             i = done + bad[0]
-            tie = margins[i] < NEAR_TIE or (routed and (ties or gaps[i] < ROUTE_TIE))
-            assert tie, (f"mismatch at step {i} (oracle margin there {margins[i]:.2e} of max |logit|, "
-                         f"router gap {gaps[i]:.2e})")
+            print(f"  mismatch at step {i}: oracle margin {margins[i]:.2e}, router gap {gaps[i]:.2e}", flush=True)
+            ok = margins[i] < NEAR_TIE or (routed and (gaps[i] < ROUTE_FLIP or i >= first_flip))
+            assert ok, (f"mismatch at step {i} (oracle margin there {margins[i]:.2e} of max |logit|, "
+                        f"router gap {gaps[i]:.2e}, first possible flip at step {first_flip})")
             ties.append(i)
             done = i + 1
         eng.deinit()
     finally:
         ctx.close()
     print(f"{name}: token-exact except at near ties {ties}", flush=True)
-    assert len(ties) <= (MAX_ROUTED_MISMATCH * len(ref) if routed else len(ref)), ties
+    assert len(ties) <= (MAX_ROUTED_MISMATCH if routed else len(ref)), ties
     return g
 
 
@@ -101,6 +104,68 @@ def test_moe48_greedy_256_token_exact():
     c = g["config"]
     assert c["n_layers"] == 48 and c["n_experts"] == 128 and c["n_experts_used"] == 8 and c["vocab"] == 151936
     assert g["prefill"] == 8192
+
+
+# above this router gap the GPU's own selection must be the oracle's (its
+# hidden state follows the oracle's to ~1e-5 of the scale when it runs the
+# oracle's experts)
+ROUTE_EXACT = 1e-4
+
+
+def test_moe48_routing_followed_256():
+    """Config 4 at full size, in lockstep with the oracle: every decode step
+    (the 15 prompt tokens before the last, then the 256 generated ones) runs
+    the oracle's experts in every layer (zh_engine_force_routing) and is fed
+    the oracle's token, so no step inherits another expert's K/V rows. Per
+    step: the GPU's own selection (what its router top-k computed, recorded
+    beside the forced ids) equals the oracle's in every layer whose router gap
+    exceeds ROUTE_EXACT (as a set: the order inside the selection is not
+    output-relevant), and the greedy token equals the oracle's except at a
+    logit near tie (fixtures: moe48_greedy256.json and moe48_routing.npz from
+    tests/golden/make_goldens.py moe48)."""
+    import numpy as np
+    import zinc_amd
+    here = os.path.join(os.path.dirname(__file__), "golden")
+    g = json.load(open(os.path.join(here, "moe48_greedy256.json")))
+    r = np.load(os.path.join(here, "moe48_routing.npz"))
+    cfg = dict(g["config"])
+    ref, margins = g["tokens"], g["rel_margins"]
+    seq = g["prompt"] + ref
+    n_pre = len(g["prompt"]) - 1
+    assert r["ids"].shape == (n_pre + len(ref), cfg["n_layers"], cfg["n_experts_used"])
+    ctx = zinc_amd.Context(0)
+    bad_sel, bad_tok, checked = [], [], 0
+    try:
+        eng = zinc_amd.InferenceEngine(ctx, cfg)
+        assert "k_moe_xcd" in eng.group_kernels("ffn")
+        eng.prefill_kv_random(g["prefill"], g["kv_seed"])
+        st = zinc_amd.DecodeState()
+        for s in range(n_pre + len(ref)):
+            eng.force_routing(r["ids"][s])
+            st.position = g["prefill"] + s
+            eng.decode_step(st, seq[s], True)
+            for layer in range(cfg["n_layers"]):
+                gap = float(r["gaps"][s, layer])
+                if gap > ROUTE_EXACT and np.isfinite(gap):
+                    checked += 1
+                    g_ids, _ = eng.routing(layer)
+                    if sorted(g_ids.tolist()) != sorted(r["ids"][s, layer].tolist()):
+                        bad_sel.append((s, layer, gap))
+            if s >= n_pre:
+                i = s - n_pre
+                tok = eng.sample_greedy()
+                if tok != ref[i]:
+                    print(f"  step {i}: token {tok} vs oracle {ref[i]} (oracle margin {margins[i]:.2e})", flush=True)
+                    bad_tok.append((i, margins[i]))
+        ctx.sync()
+        eng.force_routing(None)
+        eng.deinit()
+    finally:
+        ctx.close()
+    print(f"moe48 lockstep: {checked} layer selections compared, {len(bad_sel)} differ {bad_sel[:8]}; "
+          f"{len(bad_tok)} token mismatches {bad_tok}", flush=True)
+    assert not bad_sel, bad_sel[:8]
+    assert all(m < NEAR_TIE for _, m in bad_tok), bad_tok
 
 
 def test_dense8b_32k_greedy_128_token_exact():

@@ -4,7 +4,9 @@ Usage: python -m zinc_amd.build   (or zinc_amd.build.build())
 
 A debug build (ablation switches read from the environment, per-workgroup
 trace points) goes elsewhere and is loaded through ZH_LIB_PATH:
-    python -m zinc_amd.build --debug OUT_DIR
+    python -m zinc_amd.build --debug build/debug
+and so does a product build with extra defines (A/B of a compile-time variant):
+    python -m zinc_amd.build --out build/var/NAME -DNAME=1
 """
 import concurrent.futures as cf
 import os
@@ -40,10 +42,13 @@ def _compile(src, obj_dir=OBJ, defines=()):
     return out
 
 
-def build(verbose=True, debug_dir=None):
-    obj_dir = os.path.join(debug_dir, "_build") if debug_dir else OBJ
-    lib_path = os.path.join(debug_dir, "libzinc_hip.so") if debug_dir else LIB
-    defines = DEBUG_DEFINES if debug_dir else []
+def build(verbose=True, debug_dir=None, out_dir=None, defines=None):
+    """debug_dir: the debug build there; out_dir: a product build with extra
+    -D defines there (A/B builds of compile-time variants)."""
+    alt = debug_dir or out_dir
+    obj_dir = os.path.join(alt, "_build") if alt else OBJ
+    lib_path = os.path.join(alt, "libzinc_hip.so") if alt else LIB
+    defines = DEBUG_DEFINES if debug_dir else list(defines or [])
     os.makedirs(obj_dir, exist_ok=True)
     srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
     with cf.ThreadPoolExecutor(max_workers=min(len(srcs), 6)) as ex:
@@ -62,5 +67,7 @@ def build(verbose=True, debug_dir=None):
 if __name__ == "__main__":
     if len(sys.argv) == 3 and sys.argv[1] == "--debug":
         build(debug_dir=os.path.abspath(sys.argv[2]))
+    elif len(sys.argv) >= 3 and sys.argv[1] == "--out":
+        build(out_dir=os.path.abspath(sys.argv[2]), defines=sys.argv[3:])
     else:
         build()

@@ -30,6 +30,8 @@ static inline uint64_t S_KV(uint32_t l, uint32_t which) { return 0x100000ull + 2
 
 // Device state words.
 enum { ST_STEP = 0, ST_NPROMPT = 2, ST_TOKEN_OUT = 3, ST_POS = 5, ST_TOKEN_IN = 6, ST_GEN = 7, ST_WORDS = 16 };
+// words per layer of the routing buffer: [ids u32 x n_experts_used][weights f32 x n_experts_used]
+constexpr uint32_t ZH_ROUTE_WORDS = 32;
 constexpr uint32_t MAX_PROMPT = 8192;
 constexpr uint32_t MAX_GEN = 65536;
 
@@ -63,6 +65,7 @@ struct zh_engine {
     float *s = nullptr, *logits = nullptr, *rl = nullptr, *edown_out = nullptr, *fd_part = nullptr;
     float *u = nullptr;  // up projection when gate and up differ in format (dense)
     uint8_t *xq_h = nullptr, *xq_q = nullptr, *xq_f = nullptr;
+    uint32_t *force_ids = nullptr;  // zh_engine_force_routing: [n_layers][n_experts_used] (nullptr: off)
     uint32_t *routing = nullptr, *am_part = nullptr, *st = nullptr, *prompt = nullptr, *ring = nullptr;
     uint32_t *grp_cnt = nullptr;  // SwiGLU-output XQ: one counter per 32-row group (kept zero between launches)
     uint32_t *router_cnt = nullptr;
@@ -385,8 +388,10 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         bool is_norm = kv.first == S_OUTPUT_NORM || (kv.first > 0xFF && (kind == K_ATTN_NORM || kind == K_Q_NORM ||
                                                                          kind == K_K_NORM || kind == K_FFN_NORM));
         if (is_norm) rc = zhk_synth_vector(ctx, e->arena + t.off, 2, t.rows * t.cols, 1.f, c.seed, kv.first);
-        else rc = zhk_synth_tensor(ctx, e->arena + t.off, t.type | 0x100u /* centered model init */, t.rows, t.cols,
-                                   c.seed, kv.first);
+        else rc = zhk_synth_tensor(ctx, e->arena + t.off,
+                                   t.type | 0x100u /* centered model init */ |
+                                       (kv.first > 0xFF && kind == K_ROUTER ? 0x200u | zh_router_shift(t.cols) << 12 : 0u),
+                                   t.rows, t.cols, c.seed, kv.first);
         if (rc) { zh_engine_destroy(e); return rc; }
     }
     // --- KV cache [layer][K|V][nkv][max_ctx][hd] fp16 and identity page table
@@ -410,7 +415,7 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->fd_part, zhk_flash_decode_partials_bytes(c.n_heads, c.n_kv_heads, hd, c.max_ctx)},
         {(void **)&e->xq_h, zh_xq_bytes_int(H)}, {(void **)&e->xq_q, zh_xq_bytes_int(qd)},
         {(void **)&e->xq_f, zh_xq_bytes_int(c.n_experts ? c.expert_ffn : c.ffn) * (c.n_experts_used ? c.n_experts_used : 1)},
-        {(void **)&e->routing, 8ull * 16}, {(void **)&e->am_part, 8ull * 256}, {(void **)&e->st, 4ull * ST_WORDS},
+        {(void **)&e->routing, 4ull * ZH_ROUTE_WORDS * (c.n_layers ? c.n_layers : 1)}, {(void **)&e->am_part, 8ull * 256}, {(void **)&e->st, 4ull * ST_WORDS},
         {(void **)&e->prompt, 4ull * MAX_PROMPT}, {(void **)&e->ring, 4ull * MAX_GEN}, {(void **)&e->pages, 4ull * e->n_pages},
         {(void **)&e->inv_freq, 4ull * hd / 2}, {(void **)&e->rope_cs, 8ull * c.max_ctx * (hd / 2)},
         {(void **)&e->grp_cnt, 4ull * (F / 32 + 1)}, {(void **)&e->router_cnt, 4}, {(void **)&e->am_cnt, 4},
@@ -431,6 +436,13 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         *a.p = (char *)e->act_arena + aoff;
         aoff = align256(aoff + a.bytes);
     }
+    // the exchange words zh_sync resets after a wait gave up
+    ctx->xwords.push_back({e, e->qa_flags, 4ull * zhk_qkv_attn_flag_words()});
+    ctx->xwords.push_back({e, e->qa_xrows, zhk_qkv_attn_xrows_bytes()});
+    ctx->xwords.push_back({e, e->ffn_flags, 4ull * zhk_ffn_xcd_flag_words()});
+    if (c.ffn == 12288 && H == 4096) ctx->xwords.push_back({e, e->ffn_part, zhk_ffn_part_bytes()});
+    ctx->xwords.push_back({e, e->moe_flags, 4ull * zhk_moe_xcd_flag_words()});
+    if (c.n_experts) ctx->xwords.push_back({e, e->moe_scratch, zhk_moe_part_bytes()});
     hipError_t me = hipMemsetAsync(e->act_arena, 0, aoff, ctx->stream);
     if (me != hipSuccess) { zh_engine_destroy(e); return ZH_ERR_HIP; }
     me = hipMemsetAsync(e->kv, 0, per * 4 * c.n_layers, ctx->stream);
@@ -599,6 +611,9 @@ extern "C" int zh_engine_tensor_type(zh_engine *e, uint64_t stream, uint32_t *ty
 extern "C" void zh_engine_destroy(zh_engine *e) {
     if (!e) return;
     hipStreamSynchronize(e->ctx->stream);
+    auto &xw = e->ctx->xwords;
+    for (size_t i = xw.size(); i-- > 0;)
+        if (xw[i].owner == e) xw.erase(xw.begin() + i);
     if (e->g_out) hipGraphExecDestroy(e->g_out);
     if (e->g_noout) hipGraphExecDestroy(e->g_noout);
     if (e->arena && e->owns_arena) hipFree(e->arena);
@@ -607,6 +622,7 @@ extern "C" void zh_engine_destroy(zh_engine *e) {
     if (e->pf.arena) hipFree(e->pf.arena);
     if (e->down_pk) hipFree(e->down_pk);
     if (e->moe_pk) hipFree(e->moe_pk);
+    if (e->force_ids) hipFree(e->force_ids);
     delete e;
 }
 
@@ -678,6 +694,42 @@ extern "C" int zh_engine_set_fused_ffn(zh_engine *e, int on) {
         drop_graphs(e);
         e->fused_ffn = on != 0;
     }
+    return ZH_OK;
+}
+
+static bool step_moe(zh_engine *e);
+
+// Test hook (no counterpart in the reference): the per-XCD MoE launch runs
+// the given experts of each layer (ids [n_layers][n_experts_used], weighted
+// by the softmax over their router logits) instead of its own selection,
+// which it still records (zh_engine_routing); ids == nullptr switches it off.
+// Lets a parity test follow another implementation's routing through near
+// ties without the selections drifting apart.
+extern "C" int zh_engine_force_routing(zh_engine *e, const uint32_t *ids, uint32_t n) {
+    if (!e) return ZH_ERR_INVALID_ARGUMENT;
+    const zh_model_config &m = e->c;
+    ZH_HIP(e->ctx, hipStreamSynchronize(e->ctx->stream));
+    if (!ids) {
+        if (e->force_ids) {
+            drop_graphs(e);
+            hipFree(e->force_ids);
+            e->force_ids = nullptr;
+        }
+        return ZH_OK;
+    }
+    if (!step_moe(e) || m.n_experts_used != 8 || n != m.n_layers * m.n_experts_used)
+        return zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "forced routing: the per-XCD MoE launch, %u ids",
+                          m.n_layers * m.n_experts_used);
+    for (uint32_t i = 0; i < n; i++)
+        if (ids[i] >= m.n_experts) return zh_set_err(e->ctx, ZH_ERR_INVALID_ARGUMENT, "expert id %u", ids[i]);
+    if (!e->force_ids) {
+        if (hipMalloc((void **)&e->force_ids, 4ull * n) != hipSuccess) {
+            e->force_ids = nullptr;
+            return zh_set_err(e->ctx, ZH_ERR_OUT_OF_MEMORY, "forced routing ids");
+        }
+        drop_graphs(e);
+    }
+    ZH_HIP(e->ctx, hipMemcpy(e->force_ids, ids, 4ull * n, hipMemcpyHostToDevice));
     return ZH_OK;
 }
 
@@ -940,6 +992,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     if (persistent) ERC(zhk_step_layers(c, sa));
     for (uint32_t l = persistent ? m.n_layers : l0; l < m.n_layers && l < l1; l++) {
         const Layer &y = e->L[l];
+        uint32_t *const rt = e->routing + (size_t)ZH_ROUTE_WORDS * l;  // this layer's selection
         // kernel choice per layer, from the layer's own tensor types (a GGUF
         // Q4_K_M file mixes Q4_K and Q6_K attn_v / ffn_down across layers)
         const bool lpb_attn = lpb && zhk_lpb_supported(y.wq.type, H) && zhk_lpb_supported(y.wk.type, H) &&
@@ -1048,12 +1101,14 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             // (split residual when the attention launch takes the O projection)
             if (xl)
                 ERC(zhk_moe_xcd(c, e->rres + H, Wf(y.ffn_norm), m.eps, W(y.router), W(y.egate), W(y.eup),
-                                e->moe_pk + zhk_moe_pack_bytes() * l, dr(ka + 2), e->moe_scratch, e->routing,
-                                e->moe_flags, dr(ka + 1), e->rres, dr(ka + 3)));
+                                e->moe_pk + zhk_moe_pack_bytes() * l, dr(ka + 2), e->moe_scratch, rt,
+                                e->moe_flags, dr(ka + 1), e->rres, dr(ka + 3),
+                                e->force_ids ? e->force_ids + (size_t)m.n_experts_used * l : nullptr));
             else
                 ERC(zhk_moe_xcd(c, e->xin, Wf(y.ffn_norm), m.eps, W(y.router), W(y.egate), W(y.eup),
-                                e->moe_pk + zhk_moe_pack_bytes() * l, e->hidden, e->moe_scratch, e->routing,
-                                e->moe_flags));
+                                e->moe_pk + zhk_moe_pack_bytes() * l, e->hidden, e->moe_scratch, rt,
+                                e->moe_flags, nullptr, nullptr, nullptr,
+                                e->force_ids ? e->force_ids + (size_t)m.n_experts_used * l : nullptr));
             continue;
         }
         if (lds_moe) {
@@ -1070,18 +1125,18 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
                     // for the experts), the f32 mat-vec, then top-k
                     ERC(zhk_rms_norm(c, e->hidden, Wf(y.ffn_norm), H, e->norm, e->xq_h, H, 1, m.eps));
                     ERC(zhk_matvec_f32(c, Wf(y.router), e->norm, e->rl, E, H));
-                    ERC(zhk_softmax_topk(c, e->rl, E, k, e->routing));
+                    ERC(zhk_softmax_topk(c, e->rl, E, k, rt));
                 } else {
                     ERC(zhk_dmmv_lds_plain(c, y.router.type, 1, &wr, &rl, &E, e->hidden, Wf(y.ffn_norm), m.eps, H, 0,
-                                           e->xq_h, k, e->routing, e->router_cnt));
+                                           e->xq_h, k, rt, e->router_cnt));
                 }
                 ERC(zhk_dmmv_moe(c, y.egate.type, W(y.egate), zh_tensor_bytes(y.egate.type, F, H),
-                                 e->routing, e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
+                                 rt, e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
             }
             if (mask & SK_FFN_OUT) {
                 ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
                 ERC(zhk_dmmv_lds_down_acc(c, y.edown.type, W(y.edown), zh_tensor_bytes(y.edown.type, H, F),
-                                          e->routing, k, m.n_experts, e->xq_f, e->hidden, H, F));
+                                          rt, k, m.n_experts, e->xq_f, e->hidden, H, F));
             }
             continue;
         }
@@ -1102,13 +1157,13 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             const uint32_t F = m.expert_ffn, k = m.n_experts_used;
             if (y.router.type == ZH_F32) ERC(zhk_matvec_f32(c, Wf(y.router), e->norm, e->rl, m.n_experts, H));
             else ERC(zhk_dmmv(c, y.router.type, W(y.router), e->xq_h, e->rl, m.n_experts, H, 0));
-            ERC(zhk_softmax_topk(c, e->rl, m.n_experts, k, e->routing));
-            ERC(zhk_dmmv_moe(c, y.egate.type, W(y.egate), zh_tensor_bytes(y.egate.type, F, H), e->routing,
+            ERC(zhk_softmax_topk(c, e->rl, m.n_experts, k, rt));
+            ERC(zhk_dmmv_moe(c, y.egate.type, W(y.egate), zh_tensor_bytes(y.egate.type, F, H), rt,
                              e->xq_h, 0, e->s, F, H, k, 1, W(y.eup), m.n_experts));
             ERC(zhk_quantize_xq(c, e->s, e->xq_f, F, k, F));
-            ERC(zhk_dmmv_moe(c, y.edown.type, W(y.edown), zh_tensor_bytes(y.edown.type, H, F), e->routing,
+            ERC(zhk_dmmv_moe(c, y.edown.type, W(y.edown), zh_tensor_bytes(y.edown.type, H, F), rt,
                              e->xq_f, zh_xq_bytes_int(F), e->edown_out, H, F, k, 0, nullptr, m.n_experts));
-            ERC(zhk_moe_weighted_acc(c, e->hidden, e->edown_out, e->routing, H, k, H));
+            ERC(zhk_moe_weighted_acc(c, e->hidden, e->edown_out, rt, H, k, H));
         }
     }
     if (!whole) return ZH_OK;
@@ -1579,6 +1634,23 @@ extern "C" int zh_engine_hidden(zh_engine *e, float *dst) {
     if (!e || !dst) return ZH_ERR_INVALID_ARGUMENT;
     EHIP(e, hipMemcpyAsync(dst, e->hidden, 4ull * e->c.hidden, hipMemcpyDeviceToHost, e->ctx->stream));
     EHIP(e, hipStreamSynchronize(e->ctx->stream));
+    return ZH_OK;
+}
+
+// Inspection entry (no counterpart in the reference): the experts the last
+// decode step selected in `layer` and their routing weights (n_experts_used
+// of each), as the step's router top-k left them on the device.
+extern "C" int zh_engine_routing(zh_engine *e, uint32_t layer, uint32_t *ids, float *weights) {
+    if (!e || !ids || !weights || e->c.n_experts == 0 || layer >= e->c.n_layers) return ZH_ERR_INVALID_ARGUMENT;
+    const uint32_t k = e->c.n_experts_used;
+    uint32_t w[ZH_ROUTE_WORDS];
+    EHIP(e, hipMemcpyAsync(w, e->routing + (size_t)ZH_ROUTE_WORDS * layer, 8ull * k, hipMemcpyDeviceToHost,
+                           e->ctx->stream));
+    EHIP(e, hipStreamSynchronize(e->ctx->stream));
+    for (uint32_t i = 0; i < k; i++) {
+        ids[i] = w[i];
+        memcpy(&weights[i], &w[k + i], 4);
+    }
     return ZH_OK;
 }
 

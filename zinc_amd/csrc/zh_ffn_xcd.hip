@@ -6,28 +6,28 @@
 // fused gate/up/SwiGLU DMMV and the down DMMV with its residual add
 // (forward.zig:8237-8290; dmmv_q4k.comp, dmmv_q6k.comp).
 //
-// Workgroup w (= 32 XCD + slot, zh_xcd.h) owns FFN rows [48 w, 48 w + 48):
+// Workgroup w = 32 h + j (XCD h, slot j: zh_xcd.h) owns FFN rows
+// [48 w, 48 w + 48), so XCD h owns FFN rows [1536 h, 1536 h + 1536):
 //   1. gate/up: its 48 gate and 48 up rows against ffn_norm(x) as XQ limbs
 //      (the Q4_K ring's arithmetic, zh_ring_q4k.h), SwiGLU of the 48 pairs;
-//   2. down: the down matrix's columns [48 w, 48 w + 48) for all 4096 rows,
-//      i.e. this workgroup's share of every row's dot product, from the
-//      SwiGLU values it just computed (no exchange), into 4096 partial sums;
-//   3. the 32 workgroups of an XCD publish their partial vectors in the XCD's
-//      L2, meet at an XCD-local flag barrier, and workgroup j adds rows
-//      [128 j, 128 j + 128) of the XCD's 32 partials into the residual with
-//      device atomics (one per XCD and row).
-// Steps 1 and 2 are one stream: the 6 gate/up tiles (36 KB) and then the 8
+//   2. the SwiGLU values (as XQ limbs) go to the XCD's other 31 workgroups
+//      through its L2 (epoch-tagged words, zh_xcd.h);
+//   3. down: rows [128 j, 128 j + 128) of ffn_down over the XCD's 1536
+//      columns, i.e. the XCD's share of those rows' dot products, added into
+//      the residual with one device atomic per XCD and row.
+// Steps 1 and 3 are one stream: the 6 gate/up tiles (36 KB) and then the 8
 // down tiles (22 KB) flow through one three-slot LDS ring of asynchronous
-// global_load_lds copies, so HBM does not wait for the SwiGLU step.
+// global_load_lds copies; three down tiles are in flight while the exchange
+// of step 2 completes, so HBM does not wait for it.
 //
-// The down columns come from a copy of ffn_down that the engine repacks
-// (k_ffn_pack_down): for each workgroup's 48 columns, 4096 records of 44
-// bytes, one per row, contiguous — the 48 6-bit codes (three 16-element
-// groups: low nibbles in two dwords, high bit pairs in a third), the three
-// groups' int8 scales and the f16 super-block scales of groups 0 and 2
-// (group 1 shares one of them). 44-byte records make the lanes' LDS reads
-// conflict-free (11 dwords apart). The values are Q6_K's, unchanged: d *
-// scale * (code - 32).
+// The down matrix comes from a copy of ffn_down that the engine repacks
+// (k_ffn_pack_down): per workgroup, its 128 rows x the XCD's 32 column groups
+// of 48 as records of 44 bytes, [row][group], contiguous — the 48 6-bit
+// codes (three 16-element groups: low nibbles in two dwords, high bit pairs
+// in a third), the three groups' int8 scales and the f16 super-block scales
+// of groups 0 and 2 (group 1 shares one of them). 44-byte records make the
+// lanes' LDS reads conflict-free (11 dwords apart). The values are Q6_K's,
+// unchanged: d * scale * (code - 32).
 //
 // The residual is kept as A + D (zh_engine.hip): this launch reads x = xa +
 // xb, stores its 16 rows of x into xout, adds the down projection into acc
@@ -46,18 +46,33 @@ constexpr uint32_t FX_DTB = FX_DR * FX_REC;             // down tile bytes (22 K
 constexpr uint32_t FX_DCH = FX_DTB / 1024;              // its 1 KB copies (22)
 constexpr uint32_t FX_GT = 6;                           // gate/up tiles (48 rows / 8 per pass)
 constexpr uint32_t FX_NU = FX_GT + FX_DT;               // ring units
-constexpr uint32_t FX_RROWS = FX_H / XCD_PER;           // residual rows each workgroup reduces (128)
+constexpr uint32_t FX_RROWS = FX_H / XCD_PER;           // down rows of each workgroup (128)
+constexpr uint32_t FX_DWV = 6;                          // waves that copy the down tiles
+#ifndef ZH_FFN_DS
+#define ZH_FFN_DS 4
+#endif
+#ifndef ZH_FFN_EARLY
+#define ZH_FFN_EARLY 1
+#endif
+constexpr uint32_t FX_DS = ZH_FFN_DS;                   // down tile slots (22 KB apart)
+constexpr uint32_t FX_XW = 48;                          // tagged words of a workgroup's SwiGLU block (42 used)
+constexpr uint32_t FX_XPW = XCD_PER / 2 * FX_XW / 64;   // words per lane of each of the two polling waves (12)
+constexpr uint32_t FX_XBLK = XCD_PER * FX_XW * 4;       // LDS: the XCD's blocks, then this workgroup's own
 // LDS beyond the ring (the layout of zh_ring_q4k.h): the XQ image's region
 // takes the 4096 partial sums, the f32 staging region the SwiGLU values'
 // limbs
-constexpr uint32_t FX_PART = RG_D * RG_TILE;
 constexpr uint32_t FX_ACT = RG_D * RG_TILE + RG_XQ_BYTES;
-static_assert(FX_DTB % 1024 == 0 && FX_DTB <= RG_TILE && FX_H * 4 <= RG_XQ_BYTES, "down tiles fit the ring");
+static_assert(FX_DTB % 1024 == 0 && FX_DS * FX_DTB <= RG_D * RG_TILE + RG_XQ_BYTES, "down slots over the ring and the XQ image");
+// the down slots the gate/up loop fills lie in ring slots it no longer reads:
+// tile 0 (issued with unit 4) in unit 3's slot, tiles 1 and 2 (with unit 5)
+// in units 3 and 4's
+static_assert(FX_DTB <= RG_TILE && 3 * FX_DTB <= 2 * RG_TILE, "down slots 0-2 below unit 5's ring slot");
+static_assert(FX_XBLK + 256 + FX_RROWS * 4 <= RG_RAW_BYTES && XCD_PER / 2 * FX_XW % 64 == 0, "exchange in the staging region");
 static_assert(FX_GT * 8 == FX_RA, "gate/up: 8 rows per pass (16 super-blocks, 32 lanes per row)");
 }  // namespace
 
-// Flag words (zero when the engine is created): [0, 256) partials published
-// (XCD h at h * 32), [256, 264) epochs.
+// Flag words (zero when the engine is created): [0, 256) unused (the SwiGLU
+// blocks carry epoch tags), [256, 264) epochs.
 constexpr uint32_t FX_FLAG_WORDS = XCD_N * XCD_PER + XCD_N;
 
 struct FfnP {
@@ -66,7 +81,7 @@ struct FfnP {
     float eps;
     const uint8_t *wg, *wu;      // Q4_K gate, up [12288][4096]
     const uint8_t *pk;           // packed down columns [256][4096][44 B]
-    float *part;                 // partial sums [256][4096] (exchanged inside each XCD)
+    uint64_t *xact;              // [256][FX_XW] epoch-tagged SwiGLU blocks (exchanged inside each XCD)
     float *xout;                 // xa + xb (16 rows per workgroup)
     float *acc;                  // += the down projection (atomics)
     float *zero;                 // zeroed (16 rows per workgroup)
@@ -89,7 +104,7 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
     constexpr uint32_t NBLK = NB * 8;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t h = min(xcc_id(), XCD_N - 1), j = blockIdx.x / XCD_N, w = h * XCD_PER + j;
-    uint32_t *fl = P.flags + h * XCD_PER, *ep = P.flags + XCD_N * XCD_PER + h;
+    uint32_t *ep = P.flags + XCD_N * XCD_PER + h;
     const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
     ZH_TRACE_POINT(0);
 
@@ -99,19 +114,23 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
     p.seg_end[0] = FX_F; p.seg_end[1] = FX_F; p.seg_end[2] = FX_F;
     const TT tiles(p, w, tid, lds);
     const uint32_t wave = tiles.wave, lds0 = tiles.lds0, tcw = tiles.tcw;
-    // a wave's 1 KB copies per down tile (chunk c = wave + 8 i < 22)
-    const uint32_t dcw = wave < FX_DCH % 8 ? FX_DCH / 8 + 1 : FX_DCH / 8;
+    // a wave's 1 KB copies per down tile (chunk c = wave + 6 i < 22: waves
+    // 0-5; waves 6 and 7 poll the SwiGLU exchange)
+    const uint32_t dcw = wave >= FX_DWV ? 0u : wave < FX_DCH % FX_DWV ? FX_DCH / FX_DWV + 1 : FX_DCH / FX_DWV;
     const uint8_t *pk = P.pk + (size_t)w * FX_SLICE;
-    // unit u of the stream into ring slot s: gate/up tile u, then down tile u - 6
-    auto issue = [&](uint32_t u, uint32_t s) __attribute__((always_inline)) {
+    // unit u of the stream: gate/up tile u into ring slot u % 3, then down
+    // tile u - 6 into down slot (u - 6) % 5 (22 KB apart, over the ring and
+    // the XQ image's region: FX_DS)
+    auto issue = [&](uint32_t u) __attribute__((always_inline)) {
         if (u < FX_GT) {
-            tiles.issue(u, s);
+            tiles.issue(u, u % RG_D);
         } else {
+            const uint32_t s = (u - FX_GT) % FX_DS;
 #pragma unroll
-            for (uint32_t i = 0; i < (FX_DCH + 7) / 8; i++) {
-                const uint32_t c = wave + 8 * i;
-                if (c < FX_DCH)  // uniform per wave
-                    dma16(pk + (u - FX_GT) * FX_DTB + c * 1024 + lane * 16, lds0 + s * RG_TILE + c * 1024);
+            for (uint32_t i = 0; i < (FX_DCH + FX_DWV - 1) / FX_DWV; i++) {
+                const uint32_t c = wave + FX_DWV * i;
+                if (wave < FX_DWV && c < FX_DCH)  // uniform per wave
+                    dma16(pk + (u - FX_GT) * FX_DTB + c * 1024 + lane * 16, lds0 + s * FX_DTB + c * 1024);
             }
         }
     };
@@ -130,8 +149,8 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
         dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + FX_ACT + NB * 1024 + c * 1024);
         dma16((const uint8_t *)P.xb + c * 1024 + lane * 16, lds0 + (RG_D - 1) * RG_TILE + c * 1024);
     }
-    issue(0, 0);
-    issue(1, 1);
+    issue(0);
+    issue(1);
     wait_vm_dyn(2 * tcw);
     lds_bar();
     ZH_TRACE_POINT(1);
@@ -204,7 +223,9 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
         for (uint32_t u = 0; u < FX_GT; u++) {
             wait_vm_dyn(cnt(u + 1));
             lds_bar();  // (u = 0: also every wave done with xb in the third slot)
-            issue(u + 2, (u + 2) % RG_D);
+            issue(u + 2);
+            // (u = 5: down tile 2 too, into what was unit 4's slot)
+            if (ZH_FFN_EARLY && u == FX_GT - 1) issue(u + 3);
             if (u == 0) ZH_TRACE_POINT(11);
             const uint8_t *blk = ring + (u % RG_D) * RG_TILE + team * TT::ROWB + b * 144;
             uint32_t hd[4], qs[16];
@@ -250,10 +271,10 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
     lds_bar();
     ZH_TRACE_POINT(3);
     // ---- SwiGLU of the 48 rows as XQ limbs in blocks of 16 (the Q6_K scale
-    // groups), by wave 0 (lanes 48..63 form an unused fourth group), then
-    // into every lane's registers. act: limbs [3 groups][3 limbs][16 B], xs
-    // [3], z [3] = -32 (sum of the group's X) xs.
-    uint8_t *act = lds + FX_ACT;
+    // groups), by wave 0 (lanes 48..63 form an unused fourth group), published
+    // to the XCD as one block of FX_XW epoch-tagged words: limbs [3 groups][3
+    // limbs][16 B] as 36 dwords, xs [3], z [3] = -32 (sum of the group's X) xs.
+    uint8_t *act = lds + FX_ACT + FX_XBLK;
     if (wave == 0) {
         const float v = lane < FX_RA ? silu_mul(yl[lane], yl[RG_MAXROWS + lane]) : 0.f;
         const float a = row16_max(fabsf(v));
@@ -273,30 +294,62 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
                 ((float *)(act + 156))[g] = -32.f * ((float)sx * sc);
             }
         }
+        __builtin_amdgcn_wave_barrier();  // (one wave: its LDS accesses complete in order)
+        const uint32_t word = lane < 42 ? ((const uint32_t *)act)[lane] : 0u;
+        if (lane < FX_XW) tag_store(P.xact + (size_t)w * FX_XW + lane, __uint_as_float(word), E);
+    }
+    // ---- the XCD's 32 blocks (waves 6 and 7 poll 16 each; they issue no
+    // down-tile copies, so their polls drain nothing of the ring) into LDS
+    uint32_t *xact = (uint32_t *)(lds + FX_ACT);  // [32 blocks][FX_XW]
+    __shared__ uint32_t s_okx[2];
+    if (wave >= 6) {
+        float v[FX_XPW];
+        const uint32_t b0 = (wave - 6) * (XCD_PER / 2) * FX_XW;
+        const bool okw = tag_wait<FX_XPW>(P.xact + (size_t)h * XCD_PER * FX_XW + b0, E, P.ctl, v);
+#pragma unroll
+        for (int i = 0; i < FX_XPW; i++) xact[b0 + lane + 64 * i] = __float_as_uint(v[i]);
+        if (lane == 0) s_okx[wave - 6] = okw ? 1u : 0u;
     }
     lds_bar();
+    // unit 5's slot and the XQ image are free: down tiles 3 and 4 go there.
+    // (Issued only now: a CU returns vector-memory data in request order, so
+    // a poll issued behind them would wait for their bytes.)
+    for (uint32_t u = FX_GT + (ZH_FFN_EARLY ? 3 : 2); u < FX_GT + FX_DS; u++) issue(u);
+    const bool ok = s_okx[0] != 0 && s_okx[1] != 0;
+    ZH_TRACE_POINT(6);
+    // every workgroup of the XCD published, so every one has read the epoch
+    if (j == 0 && tid == 0 && ok) *(volatile uint32_t *)ep = E;
+    // ---- down (units 6..13): thread (rr, cg) = (tid / 32, tid % 32) takes
+    // the record of row 16 (u - 6) + rr of this workgroup's 128 and column
+    // group cg (the SwiGLU rows of the XCD's workgroup cg); a team of 32
+    // lanes sums a row
+    const uint32_t rr = tid / 32, cg = tid % 32;
     uint32_t A[3][3][4];
     float axs[3], az[3];
+    {
+        const uint32_t *blk = xact + cg * FX_XW;
 #pragma unroll
-    for (int g = 0; g < 3; g++) {
+        for (int g = 0; g < 3; g++) {
 #pragma unroll
-        for (int k = 0; k < 3; k++) {
-            const u32x4 q4 = *(const u32x4 *)(act + (g * 3 + k) * 16);
-            A[g][k][0] = q4.x; A[g][k][1] = q4.y; A[g][k][2] = q4.z; A[g][k][3] = q4.w;
+            for (int k = 0; k < 3; k++) {
+                const u32x4 q4 = *(const u32x4 *)(blk + (g * 3 + k) * 4);
+                A[g][k][0] = q4.x; A[g][k][1] = q4.y; A[g][k][2] = q4.z; A[g][k][3] = q4.w;
+            }
+            axs[g] = __uint_as_float(blk[36 + g]);
+            az[g] = __uint_as_float(blk[39 + g]);
         }
-        axs[g] = ((const float *)(act + 144))[g];
-        az[g] = ((const float *)(act + 156))[g];
     }
     ZH_TRACE_POINT(4);
-    // ---- down (units 6..13): thread tid takes row 512 (u - 6) + tid, its
-    // 44-byte record
-    float *part = (float *)(lds + FX_PART);
-    const bool g1b = (3 * w + 1) % 16 == 0;  // group 1 opens the second super-block
+    float *rsum = (float *)(lds + FX_ACT + FX_XBLK + 256);  // [128] the rows' sums
+    const uint32_t wc = 32 * h + cg;                         // the column group's workgroup
+    const bool g1b = (3 * wc + 1) % 16 == 0;                 // its group 1 opens the second super-block
     for (uint32_t u = FX_GT; u < FX_NU; u++) {
-        wait_vm_dyn(u + 1 < FX_NU ? cnt(u + 1) : 0u);
+        // copies still allowed in flight after unit u: u + 1 .. u + 4 (u = 6),
+        // else u + 1 .. u + 3 (those issued)
+        wait_vm_dyn(dcw * (u == FX_GT ? FX_DS - 1 : min(FX_DS - 2, FX_NU - 1 - u)));
         lds_bar();
-        if (u + 2 < FX_NU) issue(u + 2, (u + 2) % RG_D);
-        const uint32_t *rp = (const uint32_t *)(ring + (u % RG_D) * RG_TILE + tid * FX_REC);
+        if (u > FX_GT && u + FX_DS - 1 < FX_NU) issue(u + FX_DS - 1);  // into unit u - 1's slot
+        const uint32_t *rp = (const uint32_t *)(ring + ((u - FX_GT) % FX_DS) * FX_DTB + tid * FX_REC);
         uint32_t rc[11];
 #pragma unroll
         for (int i = 0; i < 11; i++) rc[i] = rp[i];
@@ -317,43 +370,18 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
             r3[g] = sc * fmaf(axs[g], comb_f(D[0], D[1], D[2]), az[g]);  // codes - 32 through az
         }
         const float da = h2f(rc[10]), db = h2f(rc[10] >> 16);
-        part[(u - FX_GT) * FX_DR + tid] = fmaf(da, r3[0], fmaf(g1b ? db : da, r3[1], db * r3[2]));
+        float r = fmaf(da, r3[0], fmaf(g1b ? db : da, r3[1], db * r3[2]));
+        r = team_sum_dpp<32>(r);
+        if (cg == 0) rsum[(u - FX_GT) * 16 + rr] = r;
     }
     lds_bar();
     ZH_TRACE_POINT(5);
-    // ---- publish the 4096 partials in the XCD's L2, then the flag
-    {
-        float *dst = P.part + (size_t)w * FX_H;
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint32_t e0 = (i * RG_T + tid) * 4;
-            *(f32x4 *)(dst + e0) = *(const f32x4 *)(part + e0);
-        }
-    }
-    wait_vm<0>();
-    __syncthreads();
-    if (tid == 0) *(volatile uint32_t *)(fl + j) = E;
-    const bool ok = xcd_wait(fl, XCD_PER, E, P.ctl, tid);
-    ZH_TRACE_POINT(6);
-    if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the XCD has read the epoch
-    // ---- rows [128 j, +128) of the XCD's 32 partials (16 KB) into ring
-    // slot 0: copy c holds partials 2c and 2c + 1
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const uint32_t c = wave + 8 * i, pi = 2 * c + lane / 32;
-        dma16_dev(P.part + (size_t)(h * XCD_PER + pi) * FX_H + j * FX_RROWS + (lane % 32) * 4, lds0 + c * 1024);
-    }
-    wait_vm<0>();
-    lds_bar();
-    {
-        const float *rs = (const float *)lds;  // [32 partials][128 rows]
-        const uint32_t r = tid / 4, q = tid % 4;
-        float s = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; k++) s += rs[(q * 8 + k) * FX_RROWS + r];
-        s = team_sum_dpp<4>(s);
-        if (!ok) s = __builtin_nanf("");  // the partials' wait gave up
-        if (q == 0) __hip_atomic_fetch_add(P.acc + j * FX_RROWS + r, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // ---- the XCD's share of rows [128 j, +128) into the residual (one
+    // device atomic per XCD and row)
+    if (tid < FX_RROWS) {
+        float s = rsum[tid];
+        if (!ok) s = __builtin_nanf("");  // the exchange's wait gave up
+        __hip_atomic_fetch_add(P.acc + j * FX_RROWS + tid, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     ZH_TRACE_POINT(7);
 }
@@ -365,6 +393,8 @@ ZH_TRACE_DUMP_FN(zh_debug_trace_ffn)
 __global__ void k_ffn_pack_down(const uint8_t *q6, uint8_t *pk) {
     const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= XCD_N * XCD_PER * FX_H) return;
+    // record of row r and column group w (columns [48 w, 48 w + 48)); stored
+    // for workgroup (XCD w / 32, slot r / 128) at [row r % 128][group w % 32]
     const uint32_t w = gid / FX_H, r = gid % FX_H;
     const uint8_t *row = q6 + (size_t)r * (FX_F / 256) * 210;
     uint32_t rec[11] = {};
@@ -394,13 +424,14 @@ __global__ void k_ffn_pack_down(const uint8_t *q6, uint8_t *pk) {
     }
     const uint8_t *ba = row + ((3 * w) / 16) * 210, *bb = row + ((3 * w + 2) / 16) * 210;
     rec[10] = (uint32_t)ba[208] | ((uint32_t)ba[209] << 8) | ((uint32_t)bb[208] << 16) | ((uint32_t)bb[209] << 24);
-    uint32_t *dst = (uint32_t *)(pk + (size_t)w * FX_SLICE + (size_t)r * FX_REC);
+    const uint32_t owner = (w / XCD_PER) * XCD_PER + r / FX_RROWS;
+    uint32_t *dst = (uint32_t *)(pk + (size_t)owner * FX_SLICE + ((size_t)(r % FX_RROWS) * XCD_PER + w % XCD_PER) * FX_REC);
     for (int i = 0; i < 11; i++) dst[i] = rec[i];
 }
 
 uint32_t zhk_ffn_xcd_flag_words() { return FX_FLAG_WORDS; }
 uint64_t zhk_ffn_pack_bytes() { return (uint64_t)XCD_N * XCD_PER * FX_SLICE; }
-uint64_t zhk_ffn_part_bytes() { return (uint64_t)XCD_N * XCD_PER * FX_H * 4; }
+uint64_t zhk_ffn_part_bytes() { return (uint64_t)XCD_N * XCD_PER * FX_XW * 8; }
 
 bool zhk_ffn_xcd_supported(zh_ctx *c, uint32_t hidden, uint32_t ffn) {
     return hidden == FX_H && ffn == FX_F && !c->concurrent && zhk_xcd_round_robin(c);
@@ -422,7 +453,7 @@ int zhk_ffn_xcd(zh_ctx *c, const float *xa, const float *xb, const float *norm_w
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "ffn_xcd: 16-byte aligned operands");
     FfnP P = {};
     P.xa = xa; P.xb = xb; P.norm_w = norm_w; P.eps = eps; P.wg = wg; P.wu = wu; P.pk = pk;
-    P.part = part; P.xout = xout; P.acc = acc; P.zero = zero; P.flags = flags; P.ctl = c->err_dev;
+    P.xact = (uint64_t *)part; P.xout = xout; P.acc = acc; P.zero = zero; P.flags = flags; P.ctl = c->err_dev;
     static bool attr = false;
     if (!attr) {
         ZH_HIP(c, hipFuncSetAttribute((const void *)k_ffn_xcd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)RG_LDS));

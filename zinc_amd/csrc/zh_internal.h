@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string>
+#include <vector>
 
 // Ablation switches for measuring one kernel path against another. Only a
 // debug build (-DZH_DEBUG_KNOBS) reads them from the environment; the product
@@ -47,6 +48,13 @@ struct zh_ctx {
     // 100 MHz s_memrealtime clock, read by the kernels at run time so that a
     // captured graph follows zh_set_attn_wait_limit.
     uint32_t *err_dev = nullptr;
+    // Device words of the cross-workgroup exchanges (flag and epoch words,
+    // epoch-tagged values) of the engines on this context. A bounded wait
+    // that gave up leaves them inconsistent (a late workgroup may publish
+    // after its launch's epoch was abandoned), so zh_sync zeroes them all
+    // when it reports ZH_ERR_WAIT_TIMEOUT: the next launch starts at epoch 1.
+    struct XWords { const void *owner; void *p; uint64_t bytes; };
+    std::vector<XWords> xwords;
 };
 enum : uint32_t { ZH_DEVERR_EXPERT_ID = 1u, ZH_DEVERR_ATTN_WAIT = 2u, ZH_DEVERR_STEP_BARRIER = 4u };
 // default merge wait: 50 ms
@@ -116,6 +124,7 @@ int zhk_dmmv_moe(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint64_t expert_
                  uint32_t *err = nullptr);
 int zhk_dequant_rows(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, uint32_t row0, uint32_t n_rows,
                      uint32_t K, float *out, const uint32_t *row_from_dev, uint32_t clamp_rows, uint32_t gather = 0);
+uint32_t zh_router_shift(uint64_t K);  // the router flag's shift of zhk_synth_tensor (zh_runtime.hip)
 int zhk_synth_tensor(zh_ctx *ctx, uint8_t *dst, uint32_t qtype, uint64_t rows, uint64_t cols,
                      uint64_t seed, uint64_t stream);
 int zhk_synth_vector(zh_ctx *ctx, void *dst, uint32_t kind, uint64_t n, float scale, uint64_t seed,
@@ -263,7 +272,8 @@ int zhk_moe_pack_down(zh_ctx *ctx, const uint8_t *q4k_edown, uint8_t *packed);
 int zhk_moe_xcd(zh_ctx *ctx, const float *x, const float *norm_w, float eps, const uint8_t *router,
                 const uint8_t *egate, const uint8_t *eup, const uint8_t *packed, float *y, float *scratch,
                 uint32_t *routing, uint32_t *flags, const float *xb = nullptr, float *xout = nullptr,
-                float *zero = nullptr);  // xb: the split residual (x = x + xb, stored into xout; zero cleared)
+                float *zero = nullptr,  // xb: the split residual (x = x + xb, stored into xout; zero cleared)
+                const uint32_t *force = nullptr);  // test hook: run these 8 expert ids instead of the selection
 int zhk_ffn_xcd(zh_ctx *ctx, const float *xa, const float *xb, const float *norm_w, float eps, const uint8_t *wg,
                 const uint8_t *wu, const uint8_t *packed, float *part, float *xout, float *acc, float *zero,
                 uint32_t *flags);

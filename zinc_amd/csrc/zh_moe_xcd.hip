@@ -73,7 +73,8 @@ struct MoeP {
     float *y;                     // residual: += sum_k w_k down_k
     uint64_t *logits;             // [8 XCDs][128] tagged router logits (exchanged inside each XCD)
     float *part;                  // [256][2048] partial sums (exchanged inside each XCD)
-    uint32_t *routing;            // [ids x 8][weights x 8], written by workgroup 0 (for inspection)
+    uint32_t *routing;            // [ids x 8][weights x 8] of the selection, written by workgroup 0 (for inspection)
+    const uint32_t *force;        // test hook: 8 expert ids to run instead of the selection (else nullptr)
     uint32_t *flags;              // MX_FLAG_WORDS
     uint32_t *ctl;                // [0] error word, [1] wait limit
 };
@@ -202,6 +203,23 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
         const float v4[4] = {lv[0], lv[1], 0.f, 0.f};
         topk_softmax_wave(v4, MX_E, MX_K, s_route);
         if (blockIdx.x == 0 && lane < 2 * MX_K) P.routing[lane] = s_route[lane];
+        if (P.force) {
+            // run the given experts, weighted by the softmax over their own
+            // logits (the selection above stays the recorded one)
+            __shared__ float s_lg[MX_E];
+            s_lg[lane] = lv[0];
+            s_lg[lane + 64] = lv[1];
+            __builtin_amdgcn_wave_barrier();  // (one wave: its LDS accesses complete in order)
+            const uint32_t fe = lane < MX_K ? min(P.force[lane], MX_E - 1) : 0u;
+            const float fl = lane < MX_K ? s_lg[fe] : -INFINITY;
+            const float fm = wave_max(fl);
+            const float fx = lane < MX_K ? expf(fl - fm) : 0.f;
+            const float fs = wave_sum(fx);
+            if (lane < MX_K) {
+                s_route[lane] = fe;
+                ((float *)s_route)[MX_K + lane] = fx / fs;
+            }
+        }
         if (lane == 0) s_okr = okr ? 1u : 0u;
     }
     lds_bar();
@@ -367,7 +385,7 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
     if (tid == 0) *(volatile uint32_t *)(fl_p + j) = E;
     const bool ok_p = xcd_wait(fl_p, XCD_PER, E, P.ctl, tid);
     ZH_TRACE_POINT(6);
-    if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the XCD has read the epoch
+    if (j == 0 && tid == 0 && ok_r && ok_p) *(volatile uint32_t *)ep = E;  // every workgroup of the XCD has read the epoch
     // ---- rows [64 j, +64) of the XCD's 32 partials (8 KB) into ring slot 0:
     // copy c (wave c) holds partials 4c .. 4c + 3
     {
@@ -459,7 +477,8 @@ int zhk_moe_pack_down(zh_ctx *c, const uint8_t *q4, uint8_t *pk) {
 
 int zhk_moe_xcd(zh_ctx *c, const float *x, const float *norm_w, float eps, const uint8_t *router,
                 const uint8_t *egate, const uint8_t *eup, const uint8_t *pk, float *y, float *scratch,
-                uint32_t *routing, uint32_t *flags, const float *xb, float *xout, float *zero) {
+                uint32_t *routing, uint32_t *flags, const float *xb, float *xout, float *zero,
+                const uint32_t *force) {
     if (((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)router & 15) || ((uintptr_t)egate & 15) ||
         ((uintptr_t)eup & 15) || ((uintptr_t)pk & 15) || ((uintptr_t)scratch & 15) || !y || !routing ||
         (xb && (((uintptr_t)xb & 15) || ((uintptr_t)xout & 15) || !zero)))
@@ -467,7 +486,7 @@ int zhk_moe_xcd(zh_ctx *c, const float *x, const float *norm_w, float eps, const
     MoeP P = {};
     P.x = x; P.xb = xb; P.xout = xout; P.zero = zero; P.norm_w = norm_w; P.eps = eps; P.router = router; P.egate = egate; P.eup = eup; P.pk = pk; P.y = y;
     P.part = scratch; P.logits = (uint64_t *)(scratch + (size_t)XCD_N * XCD_PER * MX_H);
-    P.routing = routing; P.flags = flags; P.ctl = c->err_dev;
+    P.routing = routing; P.force = force; P.flags = flags; P.ctl = c->err_dev;
     static bool attr = false;
     if (!attr) {
         ZH_HIP(c, hipFuncSetAttribute((const void *)k_moe_xcd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)RG_LDS));

@@ -433,9 +433,14 @@ static int noalloc_scratch(zh_ctx *c, void **out) {
     if (c->device < 0 || c->device >= 64) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "device %d", c->device);
     std::lock_guard<std::mutex> lock(mu);
     if (!ptr[c->device]) {
+        // (the caller's current device is restored afterwards)
+        int prev = 0;
+        ZH_HIP(c, hipGetDevice(&prev));
         ZH_HIP(c, hipSetDevice(c->device));
         void *p = nullptr;
-        ZH_HIP(c, hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        const hipError_t ge = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        ZH_HIP(c, hipSetDevice(prev));
+        ZH_HIP(c, ge);
         if (!p) return zh_set_err(c, ZH_ERR_HIP, "no device address for the no-alloc scratch");
         ptr[c->device] = p;
     }

@@ -660,7 +660,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         // ---- merger j: q head h G + j, once every chunk of the kv head published
         const bool ok = xcd_wait(fl_p, nv, E, p.ctl, tid);
         ZH_TRACE_POINT(11);
-        if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
+        if (j == 0 && tid == 0 && ok && ok_rows) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch (a wait that gave up leaves the words to zh_sync's reset)
         attn_merge<1, 32, false, true>(p, h * G + j, nv, !(ok && ok_rows));
         ZH_TRACE_POINT(12);
         return;
@@ -671,7 +671,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     // the O projection's 4 G blocks of 32 (no second publication round)
     const bool ok = xcd_wait(fl_p, nv, E, p.ctl, tid);
     ZH_TRACE_POINT(11);
-    if (j == 0 && tid == 0) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch
+    if (j == 0 && tid == 0 && ok && ok_rows) *(volatile uint32_t *)ep = E;  // every workgroup of the head has read the epoch (a wait that gave up leaves the words to zh_sync's reset)
     float *mo = (float *)(lds + QA_X + 4096);  // merged heads [G][128]
     {
         AttnP pm = p;

@@ -97,6 +97,10 @@ extern "C" int zh_sync(zh_ctx *c) {
     ZH_HIP(c, hipMemcpy(&e, c->err_dev, 4, hipMemcpyDeviceToHost));
     if (e) {
         ZH_HIP(c, hipMemset(c->err_dev, 0, 4));
+        if (e & (ZH_DEVERR_ATTN_WAIT | ZH_DEVERR_STEP_BARRIER)) {
+            for (const auto &w : c->xwords) ZH_HIP(c, hipMemset(w.p, 0, w.bytes));
+            ZH_HIP(c, hipDeviceSynchronize());
+        }
         if (e & ZH_DEVERR_STEP_BARRIER)
             return zh_set_err(c, ZH_ERR_WAIT_TIMEOUT, "a grid barrier of the decode-layers kernel gave up waiting "
                                                       "(its workgroups were not all resident); the step's output "
@@ -219,6 +223,10 @@ ZH_DEV uint16_t synth_scale_f16(uint64_t r) { return f2h_rn(__fmul_rn(fabsf(synt
 // every sub-block's expected weight zero-mean over random (sc, m), so mat-vec
 // outputs carry no common mode.
 #define ZH_SYNTH_CENTERED 0x100u
+// qtype | ZH_SYNTH_ROUTER | e << 12 (Q8_0): a router, d = f16(d * 2^-e), e from
+// zh_router_shift(K): the router logits of an RMS-normed input are then about
+// N(0,1), not O(sqrt(K)) as the other projections'.
+#define ZH_SYNTH_ROUTER 0x200u
 __global__ void k_synth_tensor(uint8_t *dst, uint32_t qtype_flags, uint64_t b0, uint64_t b1, uint64_t key) {
     uint64_t b = b0 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= b1) return;
@@ -265,6 +273,7 @@ __global__ void k_synth_tensor(uint8_t *dst, uint32_t qtype_flags, uint64_t b0, 
     case ZH_Q8_0: {
         uint8_t *o = dst + b * 34;
         uint16_t d = synth_scale_f16(synth_rand(key, b * 16 + 0));
+        if (qtype_flags & ZH_SYNTH_ROUTER) d = f2h_rn(ldexpf(h2f(d), -(int)((qtype_flags >> 12) & 15u)));
         o[0] = d & 0xFF; o[1] = d >> 8;
         for (int i = 0; i < 32; i++) {
             uint64_t r = synth_rand(key, b * 16 + 1 + i / 4);
@@ -317,6 +326,13 @@ static uint64_t host_synth_key(uint64_t seed, uint64_t stream) {
     return z ^ (z >> 31);
 }
 
+uint32_t zh_router_shift(uint64_t K) {
+    // 2^e nearest to 1.466 sqrt(K), 1.466 the standard deviation of the
+    // synthetic Q8_0 weights d * q (d = |N(0, .02)|, q uniform -127..127)
+    const long e = lround(log2(1.466 * sqrt((double)K)));
+    return e < 0 ? 0u : e > 15 ? 15u : (uint32_t)e;
+}
+
 int zhk_synth_tensor(zh_ctx *c, uint8_t *dst, uint32_t qtype_flags, uint64_t rows, uint64_t cols,
                      uint64_t seed, uint64_t stream) {
     const uint32_t qtype = qtype_flags & 0xFFu;
@@ -349,7 +365,8 @@ extern "C" int zh_synth_tensor(zh_ctx *c, zh_buf *buf, uint64_t off, uint32_t qt
                                uint64_t cols, uint64_t seed, uint64_t stream) {
     if (!c || !buf) return ZH_ERR_INVALID_ARGUMENT;
     const uint32_t qtype = qtype_flags & 0xFFu;
-    if (qtype_flags & ~(0xFFu | ZH_SYNTH_CENTERED)) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "synth flags");
+    if (qtype_flags & ~(0xFFu | ZH_SYNTH_CENTERED | ZH_SYNTH_ROUTER | 0xF000u))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "synth flags");
     uint32_t bs = zh_block_size(qtype), bpb = zh_bytes_per_block(qtype);
     if (bpb == 0) return zh_set_err(c, ZH_ERR_UNSUPPORTED_QUANT_TYPE, "qtype %u", qtype);
     if (cols % bs) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "cols %% block size");

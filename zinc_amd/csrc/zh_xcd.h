@@ -80,14 +80,17 @@ ZH_DEV bool tag_wait(const uint64_t *p, uint32_t E, uint32_t *ctl, float (&v)[N]
     const uint64_t limit = __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t got = 0;
     while (true) {
+        // every word is re-read each round, so the N loads are issued
+        // together and meet at one wait (a load per not-yet-seen word would
+        // put a branch, and so a wait, between them: N round trips a round)
+        uint64_t w[N];
+#pragma unroll
+        for (int i = 0; i < N; i++) w[i] = __hip_atomic_load(p + lane + 64 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
         for (int i = 0; i < N; i++) {
-            if (!((got >> i) & 1u)) {
-                const uint64_t w = __hip_atomic_load(p + lane + 64 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if ((uint32_t)(w >> 32) == E) {
-                    v[i] = __uint_as_float((uint32_t)w);
-                    got |= 1u << i;
-                }
+            if (!((got >> i) & 1u) && (uint32_t)(w[i] >> 32) == E) {
+                v[i] = __uint_as_float((uint32_t)w[i]);
+                got |= 1u << i;
             }
         }
         if (__builtin_amdgcn_ballot_w64(got != (1u << N) - 1u) == 0 && limit != 0) return true;

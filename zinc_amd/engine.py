@@ -151,6 +151,22 @@ class InferenceEngine:
         self.ctx.check(lib().zh_engine_hidden(self.h, C.c_void_p(out.ctypes.data)))
         return out
 
+    def routing(self, layer):
+        """(expert ids, routing weights) the last step selected in `layer`."""
+        k = self.config["n_experts_used"]
+        ids, w = np.empty(k, dtype=np.uint32), np.empty(k, dtype=np.float32)
+        self.ctx.check(lib().zh_engine_routing(self.h, layer, C.c_void_p(ids.ctypes.data), C.c_void_p(w.ctypes.data)))
+        return ids, w
+
+    def force_routing(self, ids):
+        """Run the given experts ([n_layers][n_experts_used]) instead of the
+        MoE launch's own selection (None: off); test hook."""
+        if ids is None:
+            self.ctx.check(lib().zh_engine_force_routing(self.h, None, 0))
+            return
+        a = np.ascontiguousarray(ids, dtype=np.uint32)
+        self.ctx.check(lib().zh_engine_force_routing(self.h, C.c_void_p(a.ctypes.data), a.size))
+
     def tensor_bytes(self, stream):
         b, off, n = C.c_void_p(), C.c_uint64(), C.c_uint64()
         self.ctx.check(lib().zh_engine_tensor(self.h, stream, C.byref(b), C.byref(off), C.byref(n)))

@@ -122,6 +122,8 @@ SIGNATURES = {
     "zh_engine_generate_batch": (_i32, [_P, _u32, _P, _u32, _u32, _u32, _P]),
     "zh_engine_logits": (_i32, [_P, _P]),
     "zh_engine_hidden": (_i32, [_P, _P]),
+    "zh_engine_routing": (_i32, [_P, _u32, _P, _P]),
+    "zh_engine_force_routing": (_i32, [_P, _P, _u32]),
     "zh_engine_tensor": (_i32, [_P, _u64, C.POINTER(_P), C.POINTER(_u64), C.POINTER(_u64)]),
     "zh_engine_read_kv": (_i32, [_P, _u32, _u32, _u32, _u32, _P]),
     "zh_engine_set_pages": (_i32, [_P, _P, _u32]),
