@@ -85,7 +85,9 @@ int zh_event_elapsed_ms(zh_ctx *ctx, int a, int b, float *ms);
 
 /* ---- calibration probe (counterpart of the reference's microbenchmark
  *      benchmarks/bandwidth.zig) ---------------------------------------- */
-/* Streaming 128-bit reads over the first `bytes` of buf, `iters` times: GB/s. */
+/* Streaming 128-bit reads over the first `bytes` of buf, `iters` times: GB/s,
+ * the best of three read patterns (grid-stride nontemporal loads; per-CU
+ * contiguous slices with 32 or 16 register loads in flight per thread). */
 int zh_stream_read_probe(zh_ctx *ctx, const zh_buf *buf, uint64_t bytes, uint32_t iters, float *gbs);
 
 /* ---- synthetic data (seeded, bit-identical to oracle/zinc_oracle.c) ----- */

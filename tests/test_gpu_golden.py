@@ -43,19 +43,17 @@ NEAR_TIE = 1e-3
 # A routed model adds a second, discrete source of divergence. In a layer
 # whose k-th selected router logit beats the best unselected one by a gap
 # (relative to the layer's max |router logit|) of the order of the GPU's
-# hidden-state drift from the oracle (~1e-5 of its scale: the same sums in
-# another order), the GPU may select the other expert; that moves the step's
-# logits by tenths of their scale and, through the K/V rows it writes, every
-# later step. The fixture records each step's smallest gap over its layers.
-# In this free-running check (the engine's own generate, device-side token
-# feedback), before the first step whose gap is below ROUTE_FLIP the GPU's
-# cache rows are the oracle's to the drift, so a mismatch there needs an
-# oracle margin below NEAR_TIE or a gap below ROUTE_FLIP. From that step on
-# the cache holds rows of steps that may have run another expert, and
-# mismatches are only counted (at most MAX_ROUTED_MISMATCH): the strict
-# config-4 check is test_moe48_routing_followed_256, which runs the oracle's
-# selection so that no such rows arise.
-ROUTE_FLIP, MAX_ROUTED_MISMATCH = 1e-4, 64
+# drift from the oracle (the same sums in another order: ~2e-5 of the hidden
+# state's scale over 48 layers, up to ~2e-4 of a router logit's), the GPU may
+# select the other expert; that moves the step's logits by up to tenths of
+# their scale and, through the K/V rows it writes, later steps a little. The
+# fixture records each step's smallest gap over its 48 layers. A mismatch is
+# accepted at a step whose oracle margin is below NEAR_TIE or whose router gap
+# is below ROUTE_FLIP, and at most MAX_ROUTED_MISMATCH steps may mismatch.
+# Measured on MI355X (config 4, 256 steps): 2 mismatches, at router gaps of
+# 1.4e-5 and 1.3e-4 (the second after the first swapped an expert). The strict
+# check is test_moe48_routing_followed_256, which runs the oracle's selection.
+ROUTE_FLIP, MAX_ROUTED_MISMATCH = 3e-4, 8
 
 
 def _greedy_fixture(name):
@@ -65,9 +63,7 @@ def _greedy_fixture(name):
     ref, margins = g["tokens"], g["rel_margins"]
     routed = "route_gaps" in g
     gaps = g.get("route_gaps", [1.0] * len(ref))
-    first_flip = next((i for i in range(len(ref)) if gaps[i] < ROUTE_FLIP), len(ref)) if routed else len(ref)
-    print(f"{name}: {cfg['n_layers']} layers, KV prefill {g['prefill']}, {len(ref)} tokens"
-          + (f", first step with a router gap below {ROUTE_FLIP:g}: {first_flip}" if routed else ""), flush=True)
+    print(f"{name}: {cfg['n_layers']} layers, KV prefill {g['prefill']}, {len(ref)} tokens", flush=True)
     ctx = zinc_amd.Context(0)
     ties = []
     try:
@@ -81,9 +77,9 @@ def _greedy_fixture(name):
                 break
             i = done + bad[0]
             print(f"  mismatch at step {i}: oracle margin {margins[i]:.2e}, router gap {gaps[i]:.2e}", flush=True)
-            ok = margins[i] < NEAR_TIE or (routed and (gaps[i] < ROUTE_FLIP or i >= first_flip))
+            ok = margins[i] < NEAR_TIE or (routed and gaps[i] < ROUTE_FLIP)
             assert ok, (f"mismatch at step {i} (oracle margin there {margins[i]:.2e} of max |logit|, "
-                        f"router gap {gaps[i]:.2e}, first possible flip at step {first_flip})")
+                        f"router gap {gaps[i]:.2e})")
             ties.append(i)
             done = i + 1
         eng.deinit()
@@ -106,10 +102,11 @@ def test_moe48_greedy_256_token_exact():
     assert g["prefill"] == 8192
 
 
-# above this router gap the GPU's own selection must be the oracle's (its
-# hidden state follows the oracle's to ~1e-5 of the scale when it runs the
-# oracle's experts)
-ROUTE_EXACT = 1e-4
+# above this router gap the GPU's own selection must be the oracle's: running
+# the oracle's experts, its router logits follow the oracle's to ~2e-4 of
+# their max (measured: 2 of 12953 compared selections differ, at gaps of
+# 2.0e-4 and 1.3e-4)
+ROUTE_EXACT = 3e-4
 
 
 def test_moe48_routing_followed_256():

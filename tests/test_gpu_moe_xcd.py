@@ -75,16 +75,23 @@ def test_moe_equals_per_group_launches(ctx):
 
 
 def test_moe_repeatable_after_replays(ctx):
-    """A second generation from the same state repeats the first, with group
-    replays (which leave sums in the residual) and a weight re-pack between."""
+    """A second generation from the same state repeats the first (to the
+    decode tolerance), with group replays (which leave sums in the residual)
+    and a weight re-pack between."""
     eng = _engine(ctx, MOE_C4)
     prefill = 150
     eng.prefill_kv_random(prefill, 6)
     prompt = [int(t) for t in np.random.default_rng(2).integers(0, MOE_C4["vocab"], 4)]
     got = eng.generate(prompt, 12, start_pos=prefill)
+    lg = eng.logits()
     eng.time_kernel("ffn", 4)
     eng.tensor_bytes(2)  # (output_norm) hands out the arena: the packed copy is rebuilt before the next step
     again = eng.generate(prompt, 12, start_pos=prefill)
+    # the 8 XCDs' device atomics into the residual add in a run-dependent
+    # order, so the second run's sums may differ in the last bits: logits
+    # within the decode tolerance, tokens equal (no near tie on this run)
+    scale = np.abs(lg).max()
+    assert np.abs(eng.logits() - lg).max() <= 1e-4 + 1e-3 * scale
     assert again == got
     ctx.sync()
     eng.deinit()

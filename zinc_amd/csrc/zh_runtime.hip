@@ -404,24 +404,72 @@ __global__ __launch_bounds__(256) void k_stream_read(const u32x4 *__restrict__ p
     if (acc == 0x9E3779B9u) out[0] = acc;  // keeps the loads live; practically never taken
 }
 
+// Register-load streaming over per-workgroup contiguous slices: workgroup b
+// reads 16-byte words [b per, (b + 1) per) of the buffer, U loads in flight
+// per thread (U x 16 B x the workgroup's threads per CU), plain loads.
+template <int U>
+__global__ __launch_bounds__(256) void k_stream_slice(const u32x4 *__restrict__ p, uint64_t n16, uint64_t per,
+                                                       uint32_t *out) {
+    const uint64_t b0 = (uint64_t)blockIdx.x * per, b1 = b0 + per < n16 ? b0 + per : n16;
+    const uint32_t nt = blockDim.x;
+    uint32_t acc = 0;
+    uint64_t i = b0 + threadIdx.x;
+    for (; i + (U - 1) * (uint64_t)nt < b1; i += (uint64_t)U * nt) {
+        u32x4 v[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) v[k] = p[i + (uint64_t)k * nt];
+#pragma unroll
+        for (int k = 0; k < U; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    for (; i < b1; i += nt) {
+        const u32x4 a = p[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    if (acc == 0x9E3779B9u) out[0] = acc;  // keeps the loads live; practically never taken
+}
+
+// The streaming-read ceiling: the best of three read patterns over the same
+// bytes, each timed over `iters` launches (HIP events):
+//   0 grid-stride nontemporal 16-byte loads, 8 workgroups of 256 per CU, 4 in flight per thread;
+//   1 per-workgroup contiguous slices, 4 workgroups of 256 per CU, 32 loads in flight per thread;
+//   2 per-workgroup contiguous slices, 8 workgroups of 256 per CU, 16 loads in flight per thread.
+// (Measured on MI355X: 5.8-6.3 TB/s for all of them over 1-4 GB; up to
+// 7.3 TB/s over 256 MB, which the 256 MB MALL partly serves.)
 extern "C" int zh_stream_read_probe(zh_ctx *c, const zh_buf *buf, uint64_t bytes, uint32_t iters, float *gbs) {
     if (!c || !buf || !gbs || bytes > buf->size || bytes < 16 || iters == 0) return ZH_ERR_INVALID_ARGUMENT;
     void *o;
     int rc = zh_scratch(c, 256, &o);
     if (rc) return rc;
-    uint32_t wgs = (uint32_t)c->cu_count * 8;
-    hipLaunchKernelGGL(k_stream_read, dim3(wgs), dim3(256), 0, c->stream, (const u32x4 *)buf->ptr, bytes / 16,
-                       (uint32_t *)o);
-    ZH_HIP(c, hipEventRecord(c->ev[62], c->stream));
-    for (uint32_t k = 0; k < iters; k++)
-        hipLaunchKernelGGL(k_stream_read, dim3(wgs), dim3(256), 0, c->stream, (const u32x4 *)buf->ptr, bytes / 16,
-                           (uint32_t *)o);
-    ZH_LAUNCH_CHECK(c);
-    ZH_HIP(c, hipEventRecord(c->ev[63], c->stream));
-    ZH_HIP(c, hipEventSynchronize(c->ev[63]));
-    float ms = 0.f;
-    ZH_HIP(c, hipEventElapsedTime(&ms, c->ev[62], c->ev[63]));
-    *gbs = (float)((double)(bytes / 16 * 16) * iters / (ms * 1e-3) / 1e9);
+    const u32x4 *src = (const u32x4 *)buf->ptr;
+    const uint64_t n16 = bytes / 16;
+    const uint32_t cu = (uint32_t)c->cu_count;
+    float best = 0.f;
+    for (int v = 0; v < 3; v++) {
+        auto launch = [&]() {
+            if (v == 0) {
+                hipLaunchKernelGGL(k_stream_read, dim3(cu * 8), dim3(256), 0, c->stream, src, n16, (uint32_t *)o);
+            } else {
+                const uint32_t wgs = v == 1 ? 4 * cu : 8 * cu;
+                const uint64_t per = (n16 + wgs - 1) / wgs;
+                if (v == 1)
+                    hipLaunchKernelGGL(k_stream_slice<32>, dim3(wgs), dim3(256), 0, c->stream, src, n16, per, (uint32_t *)o);
+                else
+                    hipLaunchKernelGGL(k_stream_slice<16>, dim3(wgs), dim3(256), 0, c->stream, src, n16, per, (uint32_t *)o);
+            }
+        };
+        launch();
+        ZH_HIP(c, hipEventRecord(c->ev[62], c->stream));
+        for (uint32_t k = 0; k < iters; k++) launch();
+        ZH_LAUNCH_CHECK(c);
+        ZH_HIP(c, hipEventRecord(c->ev[63], c->stream));
+        ZH_HIP(c, hipEventSynchronize(c->ev[63]));
+        float ms = 0.f;
+        ZH_HIP(c, hipEventElapsedTime(&ms, c->ev[62], c->ev[63]));
+        const float r = (float)((double)(n16 * 16) * iters / (ms * 1e-3) / 1e9);
+        if (r > best) best = r;
+    }
+
+    *gbs = best;
     return ZH_OK;
 }
 
