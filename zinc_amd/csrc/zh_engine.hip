@@ -95,7 +95,6 @@ struct zh_engine {
     // its packed copy of every layer's expert down matrices
     uint32_t *moe_flags = nullptr;
     float *moe_scratch = nullptr;
-    uint8_t *moe_pk = nullptr;
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
     bool have_logits = false;
@@ -621,7 +620,6 @@ extern "C" void zh_engine_destroy(zh_engine *e) {
     if (e->act_arena) hipFree(e->act_arena);
     if (e->pf.arena) hipFree(e->pf.arena);
     if (e->down_pk) hipFree(e->down_pk);
-    if (e->moe_pk) hipFree(e->moe_pk);
     if (e->force_ids) hipFree(e->force_ids);
     delete e;
 }
@@ -916,24 +914,10 @@ static bool step_moe(zh_engine *e) {
     return true;
 }
 
-// The per-XCD launches' packed copies (ffn_down; the experts' down
-// matrices) of every layer: allocated on first use, rewritten from the arena
-// when it may have changed (outside any capture).
+// The per-XCD FFN launch's packed copy of every layer's ffn_down: allocated
+// on first use, rewritten from the arena when it may have changed (outside
+// any capture).
 static int ensure_packed(zh_engine *e) {
-    if (step_moe(e)) {
-        const uint64_t per = zhk_moe_pack_bytes();
-        if (!e->moe_pk && hipMalloc((void **)&e->moe_pk, per * e->c.n_layers) != hipSuccess) {
-            e->moe_pk = nullptr;
-            return zh_set_err(e->ctx, ZH_ERR_OUT_OF_MEMORY, "packed expert down (%llu B)",
-                              (unsigned long long)(per * e->c.n_layers));
-        }
-        if (e->pk_stale) {
-            for (uint32_t l = 0; l < e->c.n_layers; l++)
-                ERC(zhk_moe_pack_down(e->ctx, e->arena + e->L[l].edown.off, e->moe_pk + per * l));
-            e->pk_stale = false;
-        }
-        return ZH_OK;
-    }
     if (!step_xcd(e)) return ZH_OK;
     const uint64_t per = zhk_ffn_pack_bytes();
     if (!e->down_pk && hipMalloc((void **)&e->down_pk, per * e->c.n_layers) != hipSuccess) {
@@ -1101,12 +1085,12 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
             // (split residual when the attention launch takes the O projection)
             if (xl)
                 ERC(zhk_moe_xcd(c, e->rres + H, Wf(y.ffn_norm), m.eps, W(y.router), W(y.egate), W(y.eup),
-                                e->moe_pk + zhk_moe_pack_bytes() * l, dr(ka + 2), e->moe_scratch, rt,
+                                W(y.edown), dr(ka + 2), e->moe_scratch, rt,
                                 e->moe_flags, dr(ka + 1), e->rres, dr(ka + 3),
                                 e->force_ids ? e->force_ids + (size_t)m.n_experts_used * l : nullptr));
             else
                 ERC(zhk_moe_xcd(c, e->xin, Wf(y.ffn_norm), m.eps, W(y.router), W(y.egate), W(y.eup),
-                                e->moe_pk + zhk_moe_pack_bytes() * l, e->hidden, e->moe_scratch, rt,
+                                W(y.edown), e->hidden, e->moe_scratch, rt,
                                 e->moe_flags, nullptr, nullptr, nullptr,
                                 e->force_ids ? e->force_ids + (size_t)m.n_experts_used * l : nullptr));
             continue;

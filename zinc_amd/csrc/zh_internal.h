@@ -262,15 +262,13 @@ uint64_t zhk_ffn_pack_bytes();
 uint64_t zhk_ffn_part_bytes();
 int zhk_ffn_pack_down(zh_ctx *ctx, const uint8_t *q6k_down, uint8_t *packed);
 // Per-XCD MoE FFN (zh_moe_xcd.hip): hidden 2048, 128 experts top-8, expert FFN
-// 768, Q8_0 router, Q4_K experts (the down matrices from zhk_moe_pack_down's
-// copy); x is a copy of y taken before the launch; scratch: zhk_moe_part_bytes.
+// 768, Q8_0 router, Q4_K experts (unmodified); x is a copy of y taken before
+// the launch; scratch: zhk_moe_part_bytes (epoch-tagged exchange words).
 bool zhk_moe_xcd_supported(zh_ctx *ctx, uint32_t hidden, uint32_t n_experts, uint32_t n_used, uint32_t expert_ffn);
 uint32_t zhk_moe_xcd_flag_words();
-uint64_t zhk_moe_pack_bytes();
 uint64_t zhk_moe_part_bytes();
-int zhk_moe_pack_down(zh_ctx *ctx, const uint8_t *q4k_edown, uint8_t *packed);
 int zhk_moe_xcd(zh_ctx *ctx, const float *x, const float *norm_w, float eps, const uint8_t *router,
-                const uint8_t *egate, const uint8_t *eup, const uint8_t *packed, float *y, float *scratch,
+                const uint8_t *egate, const uint8_t *eup, const uint8_t *edown, float *y, void *scratch,
                 uint32_t *routing, uint32_t *flags, const float *xb = nullptr, float *xout = nullptr,
                 float *zero = nullptr,  // xb: the split residual (x = x + xb, stored into xout; zero cleared)
                 const uint32_t *force = nullptr);  // test hook: run these 8 expert ids instead of the selection

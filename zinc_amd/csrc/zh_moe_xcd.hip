@@ -13,17 +13,17 @@
 //      (every XCD computes all 128 logits, bit-identically, from the same
 //      bytes) and publish them in the XCD's L2 as epoch-tagged 64-bit words
 //      (zh_xcd.h tag_store), which every workgroup polls;
-//   2. every workgroup selects the top 8 of the 128 logits itself (the
-//      lowest index wins ties; weights: softmax over the selected logits) —
-//      XCD h takes the h-th selected expert e and its weight;
+//   2. every workgroup ranks the 128 logits itself (512 threads, a quarter
+//      of the comparisons each; the lowest index wins ties) and takes the top
+//      8 (weights: softmax over the selected logits) — XCD h takes the h-th
+//      selected expert e and its weight;
 //   3. workgroup j: gate and up rows [24 j, 24 j + 24) of expert e and their
-//      SwiGLU, then expert e's down columns [24 j, 24 j + 24) for all 2048
-//      rows (a repacked copy of the down matrices, 24-byte row records) into
-//      2048 partial sums — gate/up and down tiles stream through one
-//      three-slot LDS ring of asynchronous copies;
-//   4. the XCD's 32 partial vectors meet in the L2 (second flag barrier) and
-//      workgroup j adds rows [64 j, 64 j + 64) of their sum, times the
-//      expert's weight, into the residual with device atomics.
+//      SwiGLU, published to the XCD (tagged words), while expert e's down rows
+//      [64 j, 64 j + 64) (the unmodified Q4_K bytes) stream in behind the
+//      gate/up tiles;
+//   4. every workgroup reads the XCD's 768 SwiGLU values, quantises them as
+//      XQ limbs and adds its 64 down rows, times the expert's weight, into the
+//      residual with device atomics.
 // Every exchange stays inside an XCD; the only device-wide traffic is the
 // final atomics (8 per row, one per expert).
 //
@@ -40,25 +40,20 @@ constexpr uint32_t MX_NB = MX_H / 256;                 // Q4_K super-blocks per 
 constexpr uint32_t MX_RROW = MX_H / 32 * 34;           // router row bytes (Q8_0, 2176)
 constexpr uint32_t MX_RPW = MX_E / XCD_PER;            // router rows per workgroup (4)
 constexpr uint32_t MX_FR = MX_F / XCD_PER;             // FFN rows per workgroup (24)
-constexpr uint32_t MX_REC = 24;                        // packed down record per row and workgroup
-constexpr uint32_t MX_SLICE = MX_H * MX_REC;           // one workgroup's down columns of one expert (48 KB)
-constexpr uint32_t MX_DR = 512;                        // down rows per tile (one per thread)
-constexpr uint32_t MX_DT = MX_H / MX_DR;               // down tiles (4)
-constexpr uint32_t MX_DTB = MX_DR * MX_REC;            // 12 KB
-constexpr uint32_t MX_DCH = MX_DTB / 1024;             // its 1 KB copies (12)
+constexpr uint32_t MX_DR = MX_H / XCD_PER;             // down rows of each workgroup (64)
+constexpr uint32_t MX_DNB = MX_F / 256;                // Q4_K super-blocks per down row (3)
+constexpr uint32_t MX_DROWB = MX_DNB * 144;            // a down row (432 B)
+constexpr uint32_t MX_DCH = MX_DR * MX_DROWB / 1024;   // the workgroup's down rows as 1 KB copies (27)
 constexpr uint32_t MX_GT = 2;                          // gate/up tiles (24 rows, 16 per pass)
-constexpr uint32_t MX_NU = MX_GT + MX_DT;
-constexpr uint32_t MX_RR = MX_H / XCD_PER;             // residual rows each workgroup reduces (64)
 constexpr uint32_t MX_RT = (RG_D - 1) * RG_TILE;       // router rows staged in the third ring slot
-constexpr uint32_t MX_ACT = RG_D * RG_TILE + 8192;     // SwiGLU limbs (beyond the 7.2 KB XQ image)
-constexpr uint32_t MX_RAW = RG_D * RG_TILE + RG_XQ_BYTES;  // x | norm staging, then the partials
-static_assert(MX_RPW * MX_RROW <= 9 * 1024 && MX_DTB % 1024 == 0, "router rows in 9 copies; whole down copies");
-static_assert(MX_NB * 2 * RG_SEG + MX_NB * 8 * 12 <= 8192, "XQ image below the SwiGLU limbs");
+constexpr uint32_t MX_RAW = RG_D * RG_TILE + RG_XQ_BYTES;  // x | norm staging, then the SwiGLU values
+static_assert(MX_RPW * MX_RROW <= 9 * 1024 && MX_DR * MX_DROWB % 1024 == 0 && MX_DCH * 1024 <= RG_TILE,
+              "router rows in 9 copies; the down rows in whole copies in one ring slot");
+static_assert(MX_DR * 8 == RG_T && MX_F % 64 == 0 && MX_F * 4 <= RG_RAW_BYTES, "down: 8 lanes per row");
 }  // namespace
 
-// Flag words (zero when the engine is created): [0, 256) unused (the router
-// logits carry their own epoch tags), [256, 512) partials published (XCD h
-// at h * 32), [512, 520) epochs.
+// Flag words (zero when the engine is created): [0, 512) unused (the
+// exchanged values carry epoch tags), [512, 520) epochs.
 constexpr uint32_t MX_FLAG_WORDS = 2 * XCD_N * XCD_PER + XCD_N;
 
 struct MoeP {
@@ -69,21 +64,15 @@ struct MoeP {
     float eps;
     const uint8_t *router;        // Q8_0 [128][2048]
     const uint8_t *egate, *eup;   // Q4_K [128][768][2048]
-    const uint8_t *pk;            // packed down [128][32][2048][24 B]
+    const uint8_t *edown;         // Q4_K [128][2048][768]
     float *y;                     // residual: += sum_k w_k down_k
     uint64_t *logits;             // [8 XCDs][128] tagged router logits (exchanged inside each XCD)
-    float *part;                  // [256][2048] partial sums (exchanged inside each XCD)
+    uint64_t *xsw;                // [8 XCDs][768] tagged SwiGLU values (exchanged inside each XCD)
     uint32_t *routing;            // [ids x 8][weights x 8] of the selection, written by workgroup 0 (for inspection)
     const uint32_t *force;        // test hook: 8 expert ids to run instead of the selection (else nullptr)
     uint32_t *flags;              // MX_FLAG_WORDS
     uint32_t *ctl;                // [0] error word, [1] wait limit
 };
-
-ZH_DEV int row8_sum_i(int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
-    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
-    return v + __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
-}
 
 __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -193,34 +182,60 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
         xs[q] = ixs[jb];
         xz[q] = ixz[2 * jb] + ixz[2 * jb + 1];
     }
-    // ---- top 8 of the XCD's 128 logits (wave 0, as they arrive), this
-    // XCD's expert
+    // ---- the XCD's 128 logits (wave 0, as they arrive) into LDS; the top 8
+    // by rank: thread t counts, for logit t / 4, the logits in its quarter
+    // [32 (t % 4), +32) that precede it (a larger value, or an equal value
+    // at a lower index); rank < 8 places it (the order of
+    // topk_softmax_wave: value descending, lowest index first)
+    __shared__ float s_lg[MX_E];
     __shared__ uint32_t s_okr;
     if (wave == 0) {
         float lv[2];
         const bool okr = tag_wait<2>(P.logits + h * MX_E, E, P.ctl, lv);
-        ZH_TRACE_POINT(2);
-        const float v4[4] = {lv[0], lv[1], 0.f, 0.f};
-        topk_softmax_wave(v4, MX_E, MX_K, s_route);
+        s_lg[lane] = lv[0];
+        s_lg[lane + 64] = lv[1];
+        if (lane < MX_K) s_route[lane] = 0xFFFFFFFFu;  // (a NaN logit ranks nowhere: clamped below)
+        if (lane == 0) s_okr = okr ? 1u : 0u;
+    }
+    lds_bar();
+    ZH_TRACE_POINT(2);
+    {
+        const uint32_t i = tid >> 2, q = tid & 3;
+        const float li = s_lg[i];
+        uint32_t r = 0;
+#pragma unroll 8
+        for (uint32_t k = 32 * q; k < 32 * q + 32; k++) {
+            const float lk = s_lg[k];
+            r += (lk > li || (lk == li && k < i)) ? 1u : 0u;
+        }
+        r += __shfl_xor(r, 1, 64);
+        r += __shfl_xor(r, 2, 64);
+        if (q == 0 && r < MX_K) s_route[r] = i;
+    }
+    lds_bar();
+    if (wave == 0) {
+        // weights: softmax over the selected logits (rank 0 holds the max)
+        const uint32_t id = lane < MX_K ? s_route[lane] : 0u;
+        const float l0 = s_lg[min(s_route[0], MX_E - 1)];
+        const float ex = lane < MX_K && id < MX_E ? expf(s_lg[id] - l0) : 0.f;
+        const float sm = wave_sum(ex);
+        if (lane < MX_K) ((float *)s_route)[MX_K + lane] = ex / sm;
+        __builtin_amdgcn_wave_barrier();  // (one wave: its LDS accesses complete in order)
         if (blockIdx.x == 0 && lane < 2 * MX_K) P.routing[lane] = s_route[lane];
         if (P.force) {
             // run the given experts, weighted by the softmax over their own
             // logits (the selection above stays the recorded one)
-            __shared__ float s_lg[MX_E];
-            s_lg[lane] = lv[0];
-            s_lg[lane + 64] = lv[1];
-            __builtin_amdgcn_wave_barrier();  // (one wave: its LDS accesses complete in order)
             const uint32_t fe = lane < MX_K ? min(P.force[lane], MX_E - 1) : 0u;
             const float fl = lane < MX_K ? s_lg[fe] : -INFINITY;
             const float fm = wave_max(fl);
             const float fx = lane < MX_K ? expf(fl - fm) : 0.f;
             const float fs = wave_sum(fx);
+            __builtin_amdgcn_wave_barrier();
             if (lane < MX_K) {
                 s_route[lane] = fe;
                 ((float *)s_route)[MX_K + lane] = fx / fs;
             }
         }
-        if (lane == 0) s_okr = okr ? 1u : 0u;
     }
     lds_bar();
     const bool ok_r = s_okr != 0;
@@ -233,7 +248,8 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
     const float wexp = __builtin_bit_cast(float, s_route[MX_K + h]);
     ZH_TRACE_POINT(3);
 
-    // ---- the stream: gate/up tiles 0, 1 of expert e, then its 4 down tiles
+    // ---- the stream: gate/up tiles 0, 1 of expert e, then its down rows
+    // [64 j, +64) (unmodified Q4_K, 27 KB) into the third slot
     RingP p = {};
     p.M = MX_F; p.K = MX_H; p.nseg = 1; p.rpw = MX_FR;
     const size_t gstride = (size_t)MX_F * NB * 144;
@@ -242,29 +258,23 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
     p.seg_end[0] = MX_F; p.seg_end[1] = MX_F; p.seg_end[2] = MX_F;
     const TT tiles(p, j, tid, lds);
     const uint32_t tcw = tiles.tcw;
+    tiles.issue(0, 0);
+    tiles.issue(1, 1);
     const uint32_t dcw = wave < MX_DCH % 8 ? MX_DCH / 8 + 1 : MX_DCH / 8;
-    const uint8_t *pk = P.pk + ((size_t)e * XCD_PER + j) * MX_SLICE;
-    auto issue = [&](uint32_t u, uint32_t s) __attribute__((always_inline)) {
-        if (u < MX_GT) {
-            tiles.issue(u, s);
-        } else {
+    {
+        const uint8_t *dr = P.edown + ((size_t)e * MX_H + (size_t)j * MX_DR) * MX_DROWB;
 #pragma unroll
-            for (uint32_t i = 0; i < (MX_DCH + 7) / 8; i++) {
-                const uint32_t c = wave + 8 * i;
-                if (c < MX_DCH)
-                    dma16(pk + (u - MX_GT) * MX_DTB + c * 1024 + lane * 16, lds0 + s * RG_TILE + c * 1024);
-            }
+        for (uint32_t i = 0; i < (MX_DCH + 7) / 8; i++) {
+            const uint32_t c = wave + 8 * i;
+            if (c < MX_DCH) dma16(dr + c * 1024 + lane * 16, lds0 + 2 * RG_TILE + c * 1024);
         }
-    };
-    auto cnt = [&](uint32_t u) { return u < MX_GT ? tcw : dcw; };
-    issue(0, 0);
-    issue(1, 1);
+    }
     {
         const uint32_t mrow = team / RPP, trow = team % RPP;
         for (uint32_t u = 0; u < MX_GT; u++) {
-            wait_vm_dyn(cnt(u + 1));
-            lds_bar();  // (u = 0: every wave done with the router rows in the third slot)
-            issue(u + 2, (u + 2) % RG_D);
+            // copies still allowed in flight: tile 1 (u = 0) and the down rows
+            wait_vm_dyn(dcw + (u == 0 ? tcw : 0u));
+            lds_bar();
             const uint8_t *blk = ring + (u % RG_D) * RG_TILE + team * TT::ROWB + b * 144;
             uint32_t hd[4], qs[16];
             {
@@ -308,184 +318,132 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
     }
     lds_bar();
     ZH_TRACE_POINT(4);
-    // ---- SwiGLU of the 24 rows as XQ limbs in blocks of 8 (wave 0; lanes
-    // 24..63 form unused blocks). act: limbs [3 blocks][3 limbs][8 B], xs
-    // [3], xsum [3]
-    uint8_t *act = lds + MX_ACT;
+    // ---- SwiGLU of the 24 rows, published to the XCD as epoch-tagged words
+    // [XCD][768]; wave 0 then reads the XCD's 768 values into LDS
+    float *swv = (float *)(lds + MX_RAW);  // [768]
+    __shared__ uint32_t s_oks;
     if (wave == 0) {
-        const float v = lane < MX_FR ? silu_mul(yl[lane], yl[RG_MAXROWS + lane]) : 0.f;
-        const float a = row8_max(fabsf(v));
-        float inv, sc;
-        xq_scales(a, inv, sc);
-        const int X = xq_quant(v, inv);
-        int l0, l1, l2;
-        xq_limbs(X, l0, l1, l2);
-        const int sx = row8_sum_i(X);
-        if (lane < MX_FR) {
-            const uint32_t g = lane / 8, el = lane % 8;
-            act[(g * 3 + 0) * 8 + el] = (uint8_t)l0;
-            act[(g * 3 + 1) * 8 + el] = (uint8_t)l1;
-            act[(g * 3 + 2) * 8 + el] = (uint8_t)l2;
-            if (el == 0) {
-                ((float *)(act + 72))[g] = sc;
-                ((float *)(act + 84))[g] = (float)sx * sc;
-            }
-        }
+        if (lane < MX_FR)
+            tag_store(P.xsw + (size_t)h * MX_F + j * MX_FR + lane, silu_mul(yl[lane], yl[RG_MAXROWS + lane]), E);
+        float v[MX_F / 64];
+        const bool oks = tag_wait<MX_F / 64>(P.xsw + (size_t)h * MX_F, E, P.ctl, v);
+#pragma unroll
+        for (int i = 0; i < (int)(MX_F / 64); i++) swv[lane + 64 * i] = v[i];
+        if (lane == 0) s_oks = oks ? 1u : 0u;
     }
     lds_bar();
-    uint32_t A[3][3][2];
-    float axs[3], azs[3];
-#pragma unroll
-    for (int g = 0; g < 3; g++) {
-#pragma unroll
-        for (int k = 0; k < 3; k++) {
-            A[g][k][0] = ((const uint32_t *)(act + (g * 3 + k) * 8))[0];
-            A[g][k][1] = ((const uint32_t *)(act + (g * 3 + k) * 8))[1];
-        }
-        axs[g] = ((const float *)(act + 72))[g];
-        azs[g] = ((const float *)(act + 84))[g];
-    }
-    // the 24 columns [24 j, 24 j + 24) are three 8-column groups inside one
-    // or two 32-column Q4_K sub-blocks; group g uses the second one when it
-    // starts at or after column `split` of the slice
-    const uint32_t split = (24 * j) % 32 + 24 > 32 ? 32 - (24 * j) % 32 : 24u;
-    float *part = (float *)(lds + MX_RAW);
-    for (uint32_t u = MX_GT; u < MX_NU; u++) {
-        wait_vm_dyn(u + 1 < MX_NU ? cnt(u + 1) : 0u);
-        lds_bar();
-        if (u + 2 < MX_NU) issue(u + 2, (u + 2) % RG_D);
-        const uint32_t *rp = (const uint32_t *)(ring + (u % RG_D) * RG_TILE + tid * MX_REC);
-        uint32_t rc[6];
-#pragma unroll
-        for (int i = 0; i < 6; i++) rc[i] = rp[i];
-        // rc[3] = scale A, min A, scale B, min B (6-bit values in bytes);
-        // rc[4] = d A | dmin A (f16), rc[5] = d B | dmin B
-        const float dA = h2f(rc[4]), mnA = h2f(rc[4] >> 16), dB = h2f(rc[5]), mnB = h2f(rc[5] >> 16);
-        const float scA = dA * (float)(rc[3] & 0xFF), mA = mnA * (float)((rc[3] >> 8) & 0xFF);
-        const float scB = dB * (float)((rc[3] >> 16) & 0xFF), mB = mnB * (float)(rc[3] >> 24);
-        float acc = 0.f;
-#pragma unroll
-        for (int g = 0; g < 3; g++) {
-            const uint32_t c = rc[g], lo = c & 0x0F0F0F0Fu, hi = (c >> 4) & 0x0F0F0F0Fu;
-            int D[3];
-#pragma unroll
-            for (int k = 0; k < 3; k++) D[k] = sdot4(hi, A[g][k][1], sdot4(lo, A[g][k][0], 0));
-            const bool sb = 8u * g >= split;
-            const float s = sb ? scB : scA, m = sb ? mB : mA;
-            acc = fmaf(s * axs[g], comb_f(D[0], D[1], D[2]), fmaf(-m, azs[g], acc));
-        }
-        part[(u - MX_GT) * MX_DR + tid] = acc;
-    }
-    lds_bar();
+    const bool ok_s = s_oks != 0;
+    // every workgroup of the XCD published, so every one has read the epoch
+    // (a wait that gave up leaves the words to zh_sync's reset)
+    if (j == 0 && tid == 0 && ok_r && ok_s) *(volatile uint32_t *)ep = E;
     ZH_TRACE_POINT(5);
-    // ---- publish the 2048 partials in the XCD's L2, then the flag
-    *(f32x4 *)(P.part + (size_t)w * MX_H + tid * 4) = *(const f32x4 *)(part + tid * 4);
-    wait_vm<0>();
-    __syncthreads();
-    if (tid == 0) *(volatile uint32_t *)(fl_p + j) = E;
-    const bool ok_p = xcd_wait(fl_p, XCD_PER, E, P.ctl, tid);
-    ZH_TRACE_POINT(6);
-    if (j == 0 && tid == 0 && ok_r && ok_p) *(volatile uint32_t *)ep = E;  // every workgroup of the XCD has read the epoch
-    // ---- rows [64 j, +64) of the XCD's 32 partials (8 KB) into ring slot 0:
-    // copy c (wave c) holds partials 4c .. 4c + 3
+    // ---- the 768 values as the XQ image (waves 0-2, 4 elements per thread)
     {
-        const uint32_t pi = 4 * wave + lane / 16;
-        dma16_dev(P.part + (size_t)(h * XCD_PER + pi) * MX_H + j * MX_RR + (lane % 16) * 4, lds0 + wave * 1024);
-    }
-    wait_vm<0>();
-    lds_bar();
-    if (tid < 4 * MX_RR) {
-        const float *rs = (const float *)lds;  // [32 partials][64 rows]
-        const uint32_t r = tid / 4, q = tid % 4;
-        float s = 0.f;
+        float *ixs2 = (float *)(xqa + MX_DNB * 2 * RG_SEG), *ixz2 = ixs2 + MX_DNB * 8;
+        if (tid < MX_F / 4) {
+            const uint32_t e0 = tid * 4;
+            const f32x4 u = *(const f32x4 *)(swv + e0);
+            const float a = row8_max(fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+            float inv, sc;
+            xq_scales(a, inv, sc);
+            int X[4] = {xq_quant(u.x, inv), xq_quant(u.y, inv), xq_quant(u.z, inv), xq_quant(u.w, inv)};
+            int l0[4], l1[4], l2[4];
 #pragma unroll
-        for (int k = 0; k < 8; k++) s += rs[(q * 8 + k) * MX_RR + r];
-        s = team_sum_dpp<4>(s) * wexp;
-        if (!(ok_r && ok_p)) s = __builtin_nanf("");  // a wait gave up
-        if (q == 0) __hip_atomic_fetch_add(P.y + j * MX_RR + r, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int q = 0; q < 4; q++) xq_limbs(X[q], l0[q], l1[q], l2[q]);
+            const uint32_t blk = e0 / 32, lo = e0 % 32;
+            uint8_t *dst = xqa + (blk / 4) * RG_SEG + (blk % 4) * 96 + lo;
+            *(uint32_t *)(dst) = pack4(l0[0], l0[1], l0[2], l0[3]);
+            *(uint32_t *)(dst + 32) = pack4(l1[0], l1[1], l1[2], l1[3]);
+            *(uint32_t *)(dst + 64) = pack4(l2[0], l2[1], l2[2], l2[3]);
+            int sm = X[0] + X[1] + X[2] + X[3];
+            sm += __builtin_amdgcn_update_dpp(0, sm, 0xB1, 0xF, 0xF, false);
+            sm += __builtin_amdgcn_update_dpp(0, sm, 0x4E, 0xF, 0xF, false);
+            const uint32_t sub = tid & 7;
+            if (sub == 0) ixs2[blk] = sc;
+            if ((sub & 3) == 0) ixz2[blk * 2 + (sub >> 2)] = (float)sm * sc;
+        }
+        wait_vm<0>();  // the down rows
+        lds_bar();
+        // ---- down: lane (row r = tid / 8, half super-block hb = tid % 8 < 6)
+        const uint32_t r = tid >> 3, hb = tid & 7;
+        float res = 0.f;
+        if (hb < 2 * MX_DNB) {
+            const uint32_t bb = hb >> 1, h2 = hb & 1;
+            uint32_t Ld[4][24];
+            float dxs[4], dxz[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t jb = bb * 8 + 4 * h2 + q;
+                lds_load_limbs(Ld[q], xqa + hb * RG_SEG + q * 96);
+                dxs[q] = ixs2[jb];
+                dxz[q] = ixz2[2 * jb] + ixz2[2 * jb + 1];
+            }
+            const uint8_t *blk = lds + 2 * RG_TILE + r * MX_DROWB + bb * 144;
+            uint32_t hd[4], qs[16];
+            {
+                const u32x4 vv = *(const u32x4 *)blk;
+                hd[0] = vv.x; hd[1] = vv.y; hd[2] = vv.z; hd[3] = vv.w;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const u32x4 q4 = *(const u32x4 *)(blk + 16 + 64 * h2 + 16 * i);
+                    qs[4 * i] = q4.x; qs[4 * i + 1] = q4.y; qs[4 * i + 2] = q4.z; qs[4 * i + 3] = q4.w;
+                }
+            }
+            const LpbQ4K::Hdr hdr = LpbQ4K::header(hd);
+            const uint32_t scw = h2 ? hdr.scB : hdr.scA, mw = h2 ? hdr.mB : hdr.mA;
+            float accd = 0.f, accm = 0.f;
+#pragma unroll
+            for (int pl = 0; pl < 2; pl++) {
+                int D[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t q = qs[8 * pl + i];
+                    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                    for (int k = 0; k < 3; k++) {
+                        D[0][k] = sdot4(lo, Ld[2 * pl][k * 8 + i], D[0][k]);
+                        D[1][k] = sdot4(hi, Ld[2 * pl + 1][k * 8 + i], D[1][k]);
+                    }
+                }
+                const float sc0 = ubyte_f(scw, 2 * pl), sc1 = ubyte_f(scw, 2 * pl + 1);
+                const float m0 = ubyte_f(mw, 2 * pl), m1 = ubyte_f(mw, 2 * pl + 1);
+                const float S0 = (float)comb_i(D[0][0], D[0][1], D[0][2]);
+                const float S1 = (float)comb_i(D[1][0], D[1][1], D[1][2]);
+                accd = fmaf(sc0 * dxs[2 * pl], S0, accd);
+                accd = fmaf(sc1 * dxs[2 * pl + 1], S1, accd);
+                accm = fmaf(m0, dxz[2 * pl], accm);
+                accm = fmaf(m1, dxz[2 * pl + 1], accm);
+            }
+            res = fmaf(hdr.d, accd, -hdr.dmin * accm);
+        }
+        res = team_sum_dpp<8>(res) * wexp;
+        if (!(ok_r && ok_s)) res = __builtin_nanf("");  // a wait gave up
+        if (hb == 0) __hip_atomic_fetch_add(P.y + j * MX_DR + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     ZH_TRACE_POINT(7);
 }
 
 ZH_TRACE_DUMP_FN(zh_debug_trace_moe)
 
-// Packs the experts' down matrices (Q4_K [128][2048][768]) into the records
-// k_moe_xcd reads: one thread per (expert, slice j, row r). Record: the 24
-// 4-bit codes of columns [24 j, 24 j + 24) (three dwords of 8 codes: low
-// nibbles columns 8g .. 8g + 3, high nibbles 8g + 4 .. 8g + 7), the 6-bit
-// scale and min of the first and second sub-block the slice touches, and the
-// f16 d / dmin of their super-blocks.
-__global__ void k_moe_pack_down(const uint8_t *q4, uint8_t *pk) {
-    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= MX_E * XCD_PER * MX_H) return;
-    const uint32_t r = gid % MX_H, j = (gid / MX_H) % XCD_PER, e = gid / (MX_H * XCD_PER);
-    const uint8_t *row = q4 + ((size_t)e * MX_H + r) * (MX_F / 256) * 144;
-    uint32_t rec[6] = {};
-    auto code = [&](uint32_t col) {  // Q4_K element col of the row: chunk of 64, low / high nibble
-        const uint8_t *blk = row + (col / 256) * 144;
-        const uint32_t x = col % 256;
-        return (uint32_t)(blk[16 + 32 * (x / 64) + x % 32] >> (4 * ((x / 32) & 1))) & 0xF;
-    };
-    auto scmin = [&](uint32_t col, uint32_t &sc, uint32_t &mn) {  // 6-bit scale / min of col's sub-block
-        const uint8_t *s = row + (col / 256) * 144 + 4;
-        const uint32_t sb = (col % 256) / 32;
-        if (sb < 4) {
-            sc = s[sb] & 63;
-            mn = s[sb + 4] & 63;
-        } else {
-            sc = (s[sb + 4] & 0xF) | ((s[sb - 4] >> 6) << 4);
-            mn = (s[sb + 4] >> 4) | ((s[sb] >> 6) << 4);
-        }
-    };
-    const uint32_t c0 = 24 * j;
-    for (uint32_t g = 0; g < 3; g++) {
-        uint32_t v = 0;
-        for (uint32_t i = 0; i < 4; i++) {
-            v |= code(c0 + 8 * g + i) << (8 * i);
-            v |= code(c0 + 8 * g + 4 + i) << (8 * i + 4);
-        }
-        rec[g] = v;
-    }
-    const uint32_t split = c0 % 32 + 24 > 32 ? 32 - c0 % 32 : 24u;
-    const uint32_t cA = c0, cB = split < 24 ? c0 + split : c0;
-    uint32_t sA, mA, sB, mB;
-    scmin(cA, sA, mA);
-    scmin(cB, sB, mB);
-    rec[3] = sA | (mA << 8) | (sB << 16) | (mB << 24);
-    const uint8_t *ba = row + (cA / 256) * 144, *bb = row + (cB / 256) * 144;
-    rec[4] = (uint32_t)ba[0] | ((uint32_t)ba[1] << 8) | ((uint32_t)ba[2] << 16) | ((uint32_t)ba[3] << 24);
-    rec[5] = (uint32_t)bb[0] | ((uint32_t)bb[1] << 8) | ((uint32_t)bb[2] << 16) | ((uint32_t)bb[3] << 24);
-    uint32_t *dst = (uint32_t *)(pk + ((size_t)e * XCD_PER + j) * MX_SLICE + (size_t)r * MX_REC);
-    for (int i = 0; i < 6; i++) dst[i] = rec[i];
-}
-
 uint32_t zhk_moe_xcd_flag_words() { return MX_FLAG_WORDS; }
-uint64_t zhk_moe_pack_bytes() { return (uint64_t)MX_E * XCD_PER * MX_SLICE; }
-uint64_t zhk_moe_part_bytes() { return (uint64_t)XCD_N * XCD_PER * MX_H * 4 + XCD_N * MX_E * 8; }
+uint64_t zhk_moe_part_bytes() { return (uint64_t)XCD_N * (MX_E + MX_F) * 8; }
 
 bool zhk_moe_xcd_supported(zh_ctx *c, uint32_t hidden, uint32_t n_experts, uint32_t n_used, uint32_t expert_ffn) {
     return hidden == MX_H && n_experts == MX_E && n_used == MX_K && expert_ffn == MX_F && !c->concurrent &&
            zhk_xcd_round_robin(c);
 }
 
-int zhk_moe_pack_down(zh_ctx *c, const uint8_t *q4, uint8_t *pk) {
-    const uint32_t n = MX_E * XCD_PER * MX_H;
-    hipLaunchKernelGGL(k_moe_pack_down, dim3((n + 255) / 256), dim3(256), 0, c->stream, q4, pk);
-    ZH_LAUNCH_CHECK(c);
-    return ZH_OK;
-}
-
 int zhk_moe_xcd(zh_ctx *c, const float *x, const float *norm_w, float eps, const uint8_t *router,
-                const uint8_t *egate, const uint8_t *eup, const uint8_t *pk, float *y, float *scratch,
+                const uint8_t *egate, const uint8_t *eup, const uint8_t *edown, float *y, void *scratch,
                 uint32_t *routing, uint32_t *flags, const float *xb, float *xout, float *zero,
                 const uint32_t *force) {
     if (((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)router & 15) || ((uintptr_t)egate & 15) ||
-        ((uintptr_t)eup & 15) || ((uintptr_t)pk & 15) || ((uintptr_t)scratch & 15) || !y || !routing ||
+        ((uintptr_t)eup & 15) || ((uintptr_t)edown & 15) || ((uintptr_t)scratch & 15) || !y || !routing ||
         (xb && (((uintptr_t)xb & 15) || ((uintptr_t)xout & 15) || !zero)))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "moe_xcd: 16-byte aligned operands");
     MoeP P = {};
-    P.x = x; P.xb = xb; P.xout = xout; P.zero = zero; P.norm_w = norm_w; P.eps = eps; P.router = router; P.egate = egate; P.eup = eup; P.pk = pk; P.y = y;
-    P.part = scratch; P.logits = (uint64_t *)(scratch + (size_t)XCD_N * XCD_PER * MX_H);
+    P.x = x; P.xb = xb; P.xout = xout; P.zero = zero; P.norm_w = norm_w; P.eps = eps; P.router = router; P.egate = egate; P.eup = eup; P.edown = edown; P.y = y;
+    P.logits = (uint64_t *)scratch; P.xsw = P.logits + XCD_N * MX_E;
     P.routing = routing; P.force = force; P.flags = flags; P.ctl = c->err_dev;
     static bool attr = false;
     if (!attr) {
