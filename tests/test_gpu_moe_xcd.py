@@ -9,6 +9,9 @@ import pytest
 from test_gpu_engine import MOE_C4
 
 pytestmark = pytest.mark.gpu
+# below this router gap (k-th selected minus best unselected logit, over max
+# |logit|) the GPU's selection may differ from the oracle's
+ROUTE_EXACT = 1e-4
 
 
 @pytest.fixture(scope="module")
@@ -100,11 +103,15 @@ def test_moe_repeatable_after_replays(ctx):
 def test_moe_wait_give_up_reports_and_recovers(orc):
     """With the wait limit at 0 every bounded wait gives up at once (every
     workgroup still finishes): the output is NaN, zh_sync reports
-    WaitTimeout; the next steps with the default limit match the oracle."""
+    WaitTimeout; the next steps with the default limit equal those of an
+    engine that never gave up, and match the oracle (logits within the decode
+    tolerance wherever every layer's router gap exceeds ROUTE_EXACT: below it
+    the hidden state's ~1e-5 difference from the oracle may flip an expert)."""
     import zinc_amd
     c = zinc_amd.Context(0)
     try:
         eng = _engine(c, MOE_C4)
+        clean = _engine(c, MOE_C4)
         assert "k_moe_xcd" in eng.group_kernels("ffn")
         om = orc.Model(MOE_C4)
         st = zinc_amd.DecodeState()
@@ -117,18 +124,35 @@ def test_moe_wait_give_up_reports_and_recovers(orc):
         assert e.value.name == "WaitTimeout"
         c.sync()
         c.set_attn_wait_limit(50000)
-        om.decode_step(5, 0)
+        # the failed position again: until this step writes them, its cache
+        # rows hold what the failed step wrote (NaN where a wait gave up),
+        # which the attention's masked tail rows copy
+        _, o_log = om.decode_step(5, 0, want_logits=True)
         st.position = 0
-        eng.decode_step(st, 5, False)  # rewrite the cache rows of position 0
+        eng.decode_step(st, 5, True)
+        scale = np.abs(o_log).max()
+        assert np.abs(eng.logits() - o_log).max() <= 1e-4 + 1e-3 * scale
+        st.position = 0
+        clean.decode_step(st, 5, False)
         for step in range(1, 3):
             st.position = step
             eng.decode_step(st, 9 + step, True)
             g_log = eng.logits()
+            st.position = step  # (decode_step advanced it)
+            clean.decode_step(st, 9 + step, True)
+            c_log = clean.logits()
             o_tok, o_log = om.decode_step(9 + step, step, want_logits=True)
             scale = np.abs(o_log).max()
-            assert np.abs(g_log - o_log).max() <= 1e-4 + 1e-3 * scale, step
+            gaps = [om.routing(layer)[2] for layer in range(MOE_C4["n_layers"])]
+            print(f"step {step}: |recovered - clean| {np.abs(g_log - c_log).max() / scale:.2e}, "
+                  f"|recovered - oracle| {np.abs(g_log - o_log).max() / scale:.2e} of scale, "
+                  f"router gaps {gaps}", flush=True)
+            assert np.abs(g_log - c_log).max() <= 1e-4 * scale, step
+            if min(gaps) > ROUTE_EXACT:
+                assert np.abs(g_log - o_log).max() <= 1e-4 + 1e-3 * scale, step
         c.sync()
         eng.deinit()
+        clean.deinit()
         om.close()
     finally:
         c.close()

@@ -177,11 +177,14 @@ def test_fused_wait_give_up_reports_and_recovers(orc):
         assert e.value.name == "WaitTimeout"
         c.sync()
         c.set_attn_wait_limit(50000)
-        om.decode_step(7, prefill)
-        # the cache row of position `prefill` is rewritten by the next steps'
-        # prompt: re-decode it with the default limit first
+        # the failed position again: until this step writes them, its cache
+        # rows hold what the failed step wrote (NaN where a wait gave up),
+        # which the attention's masked tail rows copy
+        _, o_log = om.decode_step(7, prefill, want_logits=True)
         st.position = prefill
-        eng.decode_step(st, 7, False)
+        eng.decode_step(st, 7, True)
+        scale = np.abs(o_log).max()
+        assert np.abs(eng.logits() - o_log).max() <= 1e-4 + 1e-3 * scale
         for step in range(1, 3):
             st.position = prefill + step
             eng.decode_step(st, 9 + step, True)

@@ -555,13 +555,19 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
             for (int s8 = 0; s8 < 8; s8++)
                 kf[s8] = *(const half4 *)(Ks + t * 256 + (((2 * s8 + (fq >> 1)) ^ (t & 15)) * 16) + 8 * (fq & 1));
             const uint32_t tv = tb + 4 * fq, off = 2 * (fg & 7);
+            // V rows past the chunk are zeroed, not only weighted 0: they copy
+            // the cache's row of the new token, which this launch has not
+            // written yet and may hold anything (NaN after a step whose waits
+            // gave up), and 0 x NaN is NaN
+            const uint32_t tvalid = t1 - ts;  // tokens of the sub-chunk in the chunk
 #pragma unroll
             for (int n = 0; n < 8; n++) {
                 const uint32_t pc = 2 * n + (fg >> 3);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const uint32_t t2 = tv + r;
-                    vf[n][r] = *(const _Float16 *)(Vs + t2 * 256 + (pc ^ (t2 & 15)) * 16 + off);
+                    const _Float16 vv = *(const _Float16 *)(Vs + t2 * 256 + (pc ^ (t2 & 15)) * 16 + off);
+                    vf[n][r] = t2 < tvalid ? vv : (_Float16)0.f;
                 }
             }
         }
