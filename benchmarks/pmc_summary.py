@@ -3,7 +3,7 @@
 every launch group of the decode step, calibrated against kernels of known
 size in the same run:
 
-    FETCH factor = bytes read by k_stream_read / its FETCH_SIZE (KiB)
+    FETCH factor = bytes read by each k_stream_* launch / its FETCH_SIZE (KiB)
     WRITE factor = bytes written by the k_synth_vector calibration write
                    (its dispatches right after the reads) / their WRITE_SIZE (KiB)
     traffic      = FETCH_SIZE(kernel) * FETCH factor + WRITE_SIZE(kernel) * WRITE factor
@@ -35,8 +35,11 @@ def _rows(d):
 
 def _split(rows, groups, per_group):
     """Calibration dispatches and the per-group blocks after them."""
-    last_read = max(i for i, r in enumerate(rows) if r["Kernel_Name"].startswith("k_stream_read"))
-    cal_r = [float(r["Counter_Value"]) for r in rows if r["Kernel_Name"].startswith("k_stream_read")]
+    # (the probe's three read patterns, each reading the calibration bytes)
+    def is_read(r):
+        return r["Kernel_Name"].removeprefix("void ").startswith("k_stream_")
+    last_read = max(i for i, r in enumerate(rows) if is_read(r))
+    cal_r = [float(r["Counter_Value"]) for r in rows if is_read(r)]
     after = rows[last_read + 1:]
     nw = 0  # the calibration write: the k_synth_vector dispatches right after the reads
     while nw < len(after) and after[nw]["Kernel_Name"].startswith("k_synth_vector"):
@@ -76,22 +79,27 @@ def main():
         return 2
     probe = json.loads(open(sys.argv[3]).read().strip().splitlines()[-1])
     s = summarize(sys.argv[1], sys.argv[2], probe)
-    cmd = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && timeout -s KILL 120 rocprofv3 --pmc {c} "
-           "-d gpurun_out/pmc_{d} -o run --output-format csv -- python3 -m benchmarks.roofline_probe --pmc "
-           "> gpurun_out/pmc_{d}.json")
+    cfg = probe.get("config", 3)
+    sfx = "" if cfg == 3 else f" --config {cfg}"
+    tag = "" if cfg == 3 else f"_c{cfg}"
+    cmd = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && timeout -s KILL 180 rocprofv3 --pmc {c} "
+           "-d gpurun_out/pmc_{d} -o run --output-format csv -- python3 -m benchmarks.roofline_probe --pmc" + sfx +
+           " > gpurun_out/pmc_{d}.json")
+    title = ("the 8B decode step's kernels (config 3)" if cfg == 3 else
+             "the 48-layer MoE decode step's kernels (config 4)")
     with open(sys.argv[4], "w") as f:
-        f.write("# HBM traffic per launch of the 8B decode step's kernels (config 3)\n\n")
+        f.write(f"# HBM traffic per launch of {title}\n\n")
         f.write("Commands (one counter per run, from the repository root):\n\n")
-        f.write("    " + cmd.format(c="FETCH_SIZE", d="fetch") + "\n")
-        f.write("    " + cmd.format(c="WRITE_SIZE", d="write") + "\n")
-        f.write("    python -m benchmarks.pmc_summary gpurun_out/pmc_fetch gpurun_out/pmc_write "
-                "gpurun_out/pmc_fetch.json <this file>\n\n")
+        f.write("    " + cmd.format(c="FETCH_SIZE", d="fetch" + tag) + "\n")
+        f.write("    " + cmd.format(c="WRITE_SIZE", d="write" + tag) + "\n")
+        f.write(f"    python -m benchmarks.pmc_summary gpurun_out/pmc_fetch{tag} gpurun_out/pmc_write{tag} "
+                f"gpurun_out/pmc_fetch{tag}.json <this file>\n\n")
         f.write("Calibration (kernels of known size in the same run):\n\n")
-        f.write(f"- k_stream_read of {probe['cal_bytes']} B: FETCH_SIZE factor {s['fetch_factor']:.4f} "
+        f.write(f"- k_stream_read / k_stream_slice of {probe['cal_bytes']} B: FETCH_SIZE factor {s['fetch_factor']:.4f} "
                 "(bytes = counter KiB x 1024 x factor)\n")
         f.write(f"- k_synth_vector write of {probe['cal_bytes']} B: WRITE_SIZE factor {s['write_factor']:.4f}\n\n")
         f.write(f"Per launch (mean over {probe['layers'] + probe['iters']} launches per group, rotating through "
-                f"the {probe['layers']} layers; KV context 4098):\n\n")
+                f"the {probe['layers']} layers; KV context {probe.get('context', 4098)}):\n\n")
         f.write("| group | kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic B | algorithmic B | traffic / alg |\n")
         f.write("|---|---|---|---|---|---|---|\n")
         for g, r in s["groups"].items():
