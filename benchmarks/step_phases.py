@@ -107,7 +107,7 @@ def qkv_attn():
     ctx.sync()
     L.zh_debug_trace_qa(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
     t = a.reshape(8192, 16)[:256].astype(np.int64)
-    base = t[:, 0].min()
+    base = t[t[:, 0] > 0, 0].min()  # (rows of workgroups that ran)
     print(f"{grp} ({eng.group_kernels(grp)}): {us:.2f} us per launch (events, debug build); "
           "points of the last launch, us from the first workgroup's start / from each workgroup's start:")
     for s, nm in enumerate(QA_POINTS):
@@ -156,7 +156,7 @@ def ring(group, dump="zh_debug_trace_ring", points=None, moe=False):
     ctx.sync()
     getattr(L, dump)(a.ctypes.data_as(C.POINTER(C.c_uint64)), n)
     t = a.reshape(8192, 16)[:512].astype(np.int64)
-    base = t[:, 0].min()
+    base = t[t[:, 0] > 0, 0].min()  # (rows of workgroups that ran)
     print(f"{group} ({eng.group_kernels(group)}): {us:.2f} us per launch (events, debug build); "
           "points of the last launch, us from the first workgroup's start / from each workgroup's start:")
     for s, nm in enumerate(points):
@@ -200,7 +200,7 @@ def main():
     a = np.zeros(1024 * 32, np.uint64)
     L.zh_debug_trace_step(a.ctypes.data_as(C.POINTER(C.c_uint64)), 1024 * 32)
     t = a.reshape(1024, 32)[:ctx.info()[1]].astype(np.int64)
-    base = t[:, 0].min()
+    base = t[t[:, 0] > 0, 0].min()  # (rows of workgroups that ran)
     names = ["Q/K/V", "attention", "O", "gate/up", "down"]
     print("persistent kernel, layer 10 (us from the first workgroup's start):")
     for s in list(range(10)) + [10]:
