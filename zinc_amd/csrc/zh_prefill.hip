@@ -148,7 +148,8 @@ ZH_DEV void deq_q6k_unit(const RawQ6K &r, uint32_t g, _Float16 *dst) {
 // Waves 2 x 2: wave (wi, wj) owns tokens 64 wi .. +63 and rows TJ/2 wj ..
 // +TJ/2 (4 x TJ/32 MFMA tiles). Each step the threads dequantise the tile's
 // TJ x 4 units of 32 elements (UPT per thread) into LDS while the X chunks
-// and raw weight bytes of the next step are in flight in registers. 70 KB of
+// of the next step and the raw weight bytes of the next two steps are in
+// flight in registers. 70 KB of
 // LDS (TJ = 128): two workgroups per CU, so one's dequantisation overlaps
 // the other's MFMAs.
 template <int QT, int TJ>
@@ -179,14 +180,20 @@ __global__ __launch_bounds__(GT, 2) void k_gemm(GemmP p) {
     constexpr int UPT = TJ * 4 / GT;      // units (row, 32-element group u4) per thread per step
     half8 xr[XC];
     typedef typename std::conditional<QT == ZH_Q4_K, RawQ4K, RawQ6K>::type Raw;
-    Raw wr[UPT];
-    auto load_step = [&](uint32_t st) {
+    // the raw weight bytes (HBM) are requested two K-steps ahead, in two
+    // register sets with fixed roles (steps alternate between them, so no
+    // register copy waits for bytes still in flight); X (L2-resident) one
+    // step ahead
+    Raw wa[UPT], wb[UPT];
+    auto load_x = [&](uint32_t st) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < XC; c++) {
             const uint32_t idx = c * GT + tid, t = idx / (KS / 8), ch = idx % (KS / 8);
             const uint32_t tok = min(n0 + t, p.N - 1);
             xr[c] = *(const half8 *)(p.X + (size_t)tok * p.ldx + (size_t)st * KS + ch * 8);
         }
+    };
+    auto load_w = [&](uint32_t st, Raw (&wr)[UPT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < UPT; k++) {
             const uint32_t u = k * GT + tid, r = u >> 2, u4 = u & 3;
@@ -196,8 +203,9 @@ __global__ __launch_bounds__(GT, 2) void k_gemm(GemmP p) {
             else load_q6k_unit(blk, st & 1, u4, wr[k]);
         }
     };
-    load_step(st_begin);
-    for (uint32_t st = st_begin; st < nst; st++) {
+    // one K-step: X and the dequantised weights into LDS, the next loads,
+    // the MFMAs
+    auto step = [&](uint32_t st, Raw (&wr)[UPT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < XC; c++) {
             const uint32_t idx = c * GT + tid, t = idx / (KS / 8), ch = idx % (KS / 8);
@@ -211,7 +219,10 @@ __global__ __launch_bounds__(GT, 2) void k_gemm(GemmP p) {
             else deq_q6k_unit(wr[k], u4, ws + r * LDR + 32 * u4);
         }
         __syncthreads();
-        if (st + 1 < nst) load_step(st + 1);
+        // X first: a wave's loads complete in order, so waiting for this X
+        // next step does not wait for the weight bytes requested after it
+        if (st + 1 < nst) load_x(st + 1);
+        if (st + 2 < nst) load_w(st + 2, wr);
 #pragma unroll
         for (int kk = 0; kk < KS / 32; kk++) {
             const uint32_t ko = kk * 32 + 8 * (lane / 16);
@@ -226,6 +237,13 @@ __global__ __launch_bounds__(GT, 2) void k_gemm(GemmP p) {
             }
         }
         __syncthreads();
+    };
+    load_w(st_begin, wa);
+    if (st_begin + 1 < nst) load_w(st_begin + 1, wb);
+    load_x(st_begin);
+    for (uint32_t st = st_begin; st < nst; st += 2) {
+        step(st, wa);
+        if (st + 1 < nst) step(st + 1, wb);
     }
 #pragma unroll
     for (int i = 0; i < NI; i++)
