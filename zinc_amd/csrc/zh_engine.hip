@@ -20,6 +20,7 @@
 
 #include "zh_device.h"
 #include "zh_internal.h"
+#include "zh_xcd.h"
 
 // Tensor stream ids (shared with oracle/zinc_oracle.c).
 enum : uint64_t { S_TOKEN_EMBD = 1, S_OUTPUT_NORM = 2, S_OUTPUT = 3 };
@@ -84,7 +85,7 @@ struct zh_engine {
     // split residual of the per-XCD launches: the residual stream is
     // rres[r] + dres[d] (plain rows + atomic sums), alternating per launch
     float *rres = nullptr;         // [2][H]
-    float *dres = nullptr;         // [3][H]
+    zh_fix *dres = nullptr;        // [3][H] (64-bit fixed point: zh_xcd.h)
     // the per-XCD FFN's copy of every layer's ffn_down (zhk_ffn_pack_down),
     // made before a step runs when the arena may have changed since, and its
     // partial sums
@@ -421,7 +422,7 @@ static int engine_build(zh_ctx *ctx, const zh_model_config *cfg, const BuildOpts
         {(void **)&e->step_ctl, zh_step_ctl_bytes()}, {(void **)&e->step_layers, sizeof(zh_step_layer) * c.n_layers},
         {(void **)&e->qa_flags, 4ull * zhk_qkv_attn_flag_words()}, {(void **)&e->xin, 4ull * H},
         {(void **)&e->ffn_flags, 4ull * zhk_ffn_xcd_flag_words()}, {(void **)&e->qa_xrows, zhk_qkv_attn_xrows_bytes()}, {(void **)&e->rres, 8ull * H},
-        {(void **)&e->dres, 12ull * H},
+        {(void **)&e->dres, 24ull * H},
         {(void **)&e->ffn_part, c.ffn == 12288 && H == 4096 ? zhk_ffn_part_bytes() : 0ull},
         {(void **)&e->moe_flags, 4ull * zhk_moe_xcd_flag_words()},
         {(void **)&e->moe_scratch, c.n_experts ? zhk_moe_part_bytes() : 0ull},
@@ -891,7 +892,8 @@ static bool step_qa_o(zh_engine *e) {
 // device atomics and zeroes dres[(k + 2) % 3] (last read by launch k - 1,
 // next added into by launch k + 1). The step starts from the embedding in
 // rres[0] and dres all zero; k_fold_residual leaves the sum in e->hidden and
-// dres zero again.
+// dres zero again. dres is 64-bit fixed point (zh_xcd.h fix_add): its sums do
+// not depend on the order of the atomics, so the step is deterministic.
 static bool step_xcd(zh_engine *e) {
     return e->fused_ffn && !zh_knob("ZH_NO_FFN_XCD") && zhk_ffn_xcd_supported(e->ctx, e->c.hidden, e->c.ffn) &&
            step_qa_o(e);
@@ -933,13 +935,13 @@ static int ensure_packed(zh_engine *e) {
     return ZH_OK;
 }
 
-__global__ void k_fold_residual(float *hidden, const float *r, float *d, uint32_t kd, uint32_t n) {
+__global__ void k_fold_residual(float *hidden, const float *r, zh_fix *d, uint32_t kd, uint32_t n) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    hidden[i] = r[i] + d[kd * n + i];
-    d[i] = 0.f;
-    d[n + i] = 0.f;
-    d[2 * n + i] = 0.f;
+    hidden[i] = r[i] + fix_to_f(d[kd * n + i]);
+    d[i] = 0;
+    d[n + i] = 0;
+    d[2 * n + i] = 0;
 }
 
 // Records the decode step: embedding, layers [l0, l1) (only the launch
@@ -964,7 +966,7 @@ static int record_step(zh_engine *e, bool collect, uint32_t l0 = 0, uint32_t l1 
     const bool qa_o = !persistent && step_qa_o(e);
     const bool xl = qa_o && (m.n_experts ? true : step_xcd(e));  // qa_o with MoE implies its FFN launch
     const bool moe_x = !persistent && step_moe(e);
-    float *const D = e->dres;
+    zh_fix *const D = e->dres;
     auto dr = [&](uint32_t k) { return D + (size_t)(k % 3) * H; };
     // embedToken (forward.zig:4255-4290), on the device.
     if (whole) {
@@ -1234,7 +1236,7 @@ extern "C" int zh_engine_time_kernel(zh_engine *e, uint32_t group, uint32_t iter
     if (rc == ZH_OK) *us_per_launch = ms * 1e3f / (float)iters;
     // the replays leave atomic sums in the split residual's dres, which a
     // decode step expects zero
-    if (rc == ZH_OK && hipMemsetAsync(e->dres, 0, 12ull * e->c.hidden, c->stream) != hipSuccess)
+    if (rc == ZH_OK && hipMemsetAsync(e->dres, 0, 24ull * e->c.hidden, c->stream) != hipSuccess)
         rc = zh_set_err(c, ZH_ERR_HIP, "time_kernel reset");
     return rc;
 }

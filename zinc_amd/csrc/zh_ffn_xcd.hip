@@ -76,15 +76,16 @@ static_assert(FX_GT * 8 == FX_RA, "gate/up: 8 rows per pass (16 super-blocks, 32
 constexpr uint32_t FX_FLAG_WORDS = XCD_N * XCD_PER + XCD_N;
 
 struct FfnP {
-    const float *xa, *xb;        // x = xa + xb
+    const float *xa;             // x = xa + xb
+    const zh_fix *xb;            //   (xb: fixed point, zh_xcd.h)
     const float *norm_w;         // ffn_norm weight
     float eps;
     const uint8_t *wg, *wu;      // Q4_K gate, up [12288][4096]
     const uint8_t *pk;           // packed down columns [256][4096][44 B]
     uint64_t *xact;              // [256][FX_XW] epoch-tagged SwiGLU blocks (exchanged inside each XCD)
     float *xout;                 // xa + xb (16 rows per workgroup)
-    float *acc;                  // += the down projection (atomics)
-    float *zero;                 // zeroed (16 rows per workgroup)
+    zh_fix *acc;                 // += the down projection (fixed-point atomics)
+    zh_fix *zero;                // zeroed (16 rows per workgroup)
     uint32_t *flags;             // FX_FLAG_WORDS
     uint32_t *ctl;               // device control words: [0] error word, [1] wait limit
 };
@@ -141,12 +142,16 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
 
     // ---- the activation: xa and the norm weight into the staging region,
     // xb into the third ring slot (first filled by unit 2, issued after the
-    // XQ image is built); 2 + 1 KB copies per wave and vector
+    // XQ image is built); 2 + 2 + 4 copies of 1 KB per wave
 #pragma unroll
     for (int i = 0; i < NB / 8; i++) {
         const uint32_t c = wave + 8 * i;
         dma16((const uint8_t *)P.xa + c * 1024 + lane * 16, lds0 + FX_ACT + c * 1024);
         dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + FX_ACT + NB * 1024 + c * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < NB / 4; i++) {  // xb: 8 bytes per element
+        const uint32_t c = wave + 8 * i;
         dma16((const uint8_t *)P.xb + c * 1024 + lane * 16, lds0 + (RG_D - 1) * RG_TILE + c * 1024);
     }
     issue(0);
@@ -157,20 +162,21 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
     float *ixs = (float *)(xqa + NB * 2 * RG_SEG), *ixz = ixs + NBLK;
     {
         const float *xr = (const float *)raw, *wr = (const float *)(raw + NB * 1024);
-        const float *xr2 = (const float *)(ring + (RG_D - 1) * RG_TILE);
+        const zh_fix *xr2 = (const zh_fix *)(ring + (RG_D - 1) * RG_TILE);
         f32x4 v[NB / 8], wn[NB / 8];
         float sq = 0.f;
 #pragma unroll
         for (int it = 0; it < NB / 8; it++) {
             const uint32_t e0 = (it * RG_T + tid) * 4;
-            const f32x4 a = *(const f32x4 *)(xr + e0), b = *(const f32x4 *)(xr2 + e0);
-            v[it] = f32x4{a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
+            const f32x4 a = *(const f32x4 *)(xr + e0);
+            v[it] = f32x4{a.x + fix_to_f(xr2[e0]), a.y + fix_to_f(xr2[e0 + 1]), a.z + fix_to_f(xr2[e0 + 2]),
+                          a.w + fix_to_f(xr2[e0 + 3])};
             if ((it * RG_T + tid) / 4 == blockIdx.x) *(f32x4 *)(P.xout + e0) = v[it];  // this workgroup's 16 rows
             wn[it] = *(const f32x4 *)(wr + e0);
             sq = fmaf(v[it].x, v[it].x, sq); sq = fmaf(v[it].y, v[it].y, sq);
             sq = fmaf(v[it].z, v[it].z, sq); sq = fmaf(v[it].w, v[it].w, sq);
         }
-        if (tid < 16) P.zero[blockIdx.x * 16 + tid] = 0.f;
+        if (tid < 16) P.zero[blockIdx.x * 16 + tid] = 0;
         sq = wave_sum(sq);
         if (lane == 0) red[wave] = sq;
         lds_bar();
@@ -381,7 +387,17 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
     if (tid < FX_RROWS) {
         float s = rsum[tid];
         if (!ok) s = __builtin_nanf("");  // the exchange's wait gave up
-        __hip_atomic_fetch_add(P.acc + j * FX_RROWS + tid, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        fix_add(P.acc + j * FX_RROWS + tid, s);
+    }
+    // the wait gave up: the fixed-point sums cannot carry a NaN, so the
+    // workgroup's rows of the plain part become NaN instead (written by the
+    // threads that stored them, so in program order after them)
+    if (!ok) {
+#pragma unroll
+        for (int it = 0; it < NB / 8; it++)
+            if ((it * RG_T + tid) / 4 == blockIdx.x)
+                *(f32x4 *)(P.xout + (it * RG_T + tid) * 4) = f32x4{__builtin_nanf(""), __builtin_nanf(""),
+                                                                   __builtin_nanf(""), __builtin_nanf("")};
     }
     ZH_TRACE_POINT(7);
 }
@@ -444,8 +460,8 @@ int zhk_ffn_pack_down(zh_ctx *c, const uint8_t *q6, uint8_t *pk) {
     return ZH_OK;
 }
 
-int zhk_ffn_xcd(zh_ctx *c, const float *xa, const float *xb, const float *norm_w, float eps, const uint8_t *wg,
-                const uint8_t *wu, const uint8_t *pk, float *part, float *xout, float *acc, float *zero,
+int zhk_ffn_xcd(zh_ctx *c, const float *xa, const zh_fix *xb, const float *norm_w, float eps, const uint8_t *wg,
+                const uint8_t *wu, const uint8_t *pk, float *part, float *xout, zh_fix *acc, zh_fix *zero,
                 uint32_t *flags) {
     if (((uintptr_t)xa & 15) || ((uintptr_t)xb & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)wg & 15) ||
         ((uintptr_t)wu & 15) || ((uintptr_t)pk & 15) || ((uintptr_t)part & 15) || ((uintptr_t)xout & 15) || !acc ||

@@ -242,12 +242,16 @@ uint64_t zh_step_ctl_bytes();
 bool zhk_xcd_round_robin(zh_ctx *ctx);
 bool zhk_qkv_attn_supported(zh_ctx *ctx, uint32_t hidden, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx);
 uint32_t zhk_qkv_attn_flag_words();  // zeroed u32 words the caller keeps per engine
+// The split residual's atomic part: 64-bit fixed point in units of 2^-32
+// (zh_xcd.h fix_add / fix_to_f), so that its sums do not depend on the order
+// of the atomics.
+typedef long long zh_fix;
 int zhk_qkv_attn(zh_ctx *ctx, const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x,
                  const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
                  uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
-                 const uint8_t *wo = nullptr, float *x_acc = nullptr, const float *xb = nullptr,
-                 float *x_out = nullptr, float *zero = nullptr, uint32_t hidden = 4096, uint64_t *xrows = nullptr);
+                 const uint8_t *wo = nullptr, void *x_acc = nullptr, const zh_fix *xb = nullptr,
+                 float *x_out = nullptr, zh_fix *zero = nullptr, uint32_t hidden = 4096, uint64_t *xrows = nullptr);
 uint64_t zhk_qkv_attn_xrows_bytes();  // zeroed bytes the caller keeps per engine (xrows: the rows' exchange)
 // xb != nullptr (with wo): the input is x + xb, stored into x_out (16 rows
 // per workgroup); x_acc starts at zero (it is not x's copy), `zero` (H
@@ -268,12 +272,13 @@ bool zhk_moe_xcd_supported(zh_ctx *ctx, uint32_t hidden, uint32_t n_experts, uin
 uint32_t zhk_moe_xcd_flag_words();
 uint64_t zhk_moe_part_bytes();
 int zhk_moe_xcd(zh_ctx *ctx, const float *x, const float *norm_w, float eps, const uint8_t *router,
-                const uint8_t *egate, const uint8_t *eup, const uint8_t *edown, float *y, void *scratch,
-                uint32_t *routing, uint32_t *flags, const float *xb = nullptr, float *xout = nullptr,
-                float *zero = nullptr,  // xb: the split residual (x = x + xb, stored into xout; zero cleared)
+                const uint8_t *egate, const uint8_t *eup, const uint8_t *edown, void *y, void *scratch,
+                uint32_t *routing, uint32_t *flags, const zh_fix *xb = nullptr, float *xout = nullptr,
+                zh_fix *zero = nullptr,  // xb: the split residual (x = x + xb, stored into xout; zero cleared;
+                                         // y then zh_fix, else f32)
                 const uint32_t *force = nullptr);  // test hook: run these 8 expert ids instead of the selection
-int zhk_ffn_xcd(zh_ctx *ctx, const float *xa, const float *xb, const float *norm_w, float eps, const uint8_t *wg,
-                const uint8_t *wu, const uint8_t *packed, float *part, float *xout, float *acc, float *zero,
+int zhk_ffn_xcd(zh_ctx *ctx, const float *xa, const zh_fix *xb, const float *norm_w, float eps, const uint8_t *wg,
+                const uint8_t *wu, const uint8_t *packed, float *part, float *xout, zh_fix *acc, zh_fix *zero,
                 uint32_t *flags);
 // wo != nullptr (4 q heads per kv head): also the O projection, added into
 // x_acc with device atomics; x must then be a copy of x_acc (x_acc changes

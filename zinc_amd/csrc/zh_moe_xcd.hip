@@ -58,14 +58,15 @@ constexpr uint32_t MX_FLAG_WORDS = 2 * XCD_N * XCD_PER + XCD_N;
 
 struct MoeP {
     const float *x;               // residual copy (or its plain part, xa)
-    const float *xb;              // split residual: its atomic part (else nullptr)
-    float *xout, *zero;           // split residual: x = xa + xb stored / the vector to clear
+    const zh_fix *xb;             // split residual: its atomic part, fixed point (else nullptr)
+    float *xout;                  // split residual: x = xa + xb stored
+    zh_fix *zero;                 // split residual: the vector to clear
     const float *norm_w;          // ffn_norm weight
     float eps;
     const uint8_t *router;        // Q8_0 [128][2048]
     const uint8_t *egate, *eup;   // Q4_K [128][768][2048]
     const uint8_t *edown;         // Q4_K [128][2048][768]
-    float *y;                     // residual: += sum_k w_k down_k
+    void *y;                      // residual: += sum_k w_k down_k (zh_fix with the split residual, else f32)
     uint64_t *logits;             // [8 XCDs][128] tagged router logits (exchanged inside each XCD)
     uint64_t *xsw;                // [8 XCDs][768] tagged SwiGLU values (exchanged inside each XCD)
     uint32_t *routing;            // [ids x 8][weights x 8] of the selection, written by workgroup 0 (for inspection)
@@ -96,7 +97,10 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
     // workgroup's router rows (8.5 KB: 9 copies, the last clamped)
     dma16((const uint8_t *)P.x + wave * 1024 + lane * 16, lds0 + MX_RAW + wave * 1024);
     dma16((const uint8_t *)P.norm_w + wave * 1024 + lane * 16, lds0 + MX_RAW + NB * 1024 + wave * 1024);
-    if (P.xb) dma16((const uint8_t *)P.xb + wave * 1024 + lane * 16, lds0 + MX_RAW + 2 * NB * 1024 + wave * 1024);
+    if (P.xb)  // (8 bytes per element: 2 copies per wave)
+        for (uint32_t i = 0; i < 2; i++)
+            dma16((const uint8_t *)P.xb + (wave + 8 * i) * 1024 + lane * 16,
+                  lds0 + MX_RAW + 2 * NB * 1024 + (wave + 8 * i) * 1024);
     {
         const uint8_t *rr = P.router + (size_t)j * MX_RPW * MX_RROW;
         for (uint32_t c = wave; c < 9; c += 8)
@@ -112,10 +116,10 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
         const uint32_t e0 = tid * 4;
         f32x4 v = *(const f32x4 *)(xr + e0);
         if (P.xb) {
-            const f32x4 d = *(const f32x4 *)(wr + MX_H + e0);
-            v.x += d.x; v.y += d.y; v.z += d.z; v.w += d.w;
+            const zh_fix *dq = (const zh_fix *)(wr + MX_H) + e0;
+            v.x += fix_to_f(dq[0]); v.y += fix_to_f(dq[1]); v.z += fix_to_f(dq[2]); v.w += fix_to_f(dq[3]);
             if (e0 / (MX_H / 256) == blockIdx.x) *(f32x4 *)(P.xout + e0) = v;  // this workgroup's 8 rows
-            if (tid < MX_H / 256) P.zero[blockIdx.x * (MX_H / 256) + tid] = 0.f;
+            if (tid < MX_H / 256) P.zero[blockIdx.x * (MX_H / 256) + tid] = 0;
         }
         const f32x4 wn = *(const f32x4 *)(wr + e0);
         float sq = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w)));
@@ -418,8 +422,17 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
         }
         res = team_sum_dpp<8>(res) * wexp;
         if (!(ok_r && ok_s)) res = __builtin_nanf("");  // a wait gave up
-        if (hb == 0) __hip_atomic_fetch_add(P.y + j * MX_DR + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (hb == 0) {
+            if (P.xb) fix_add((zh_fix *)P.y + j * MX_DR + r, res);
+            else __hip_atomic_fetch_add((float *)P.y + j * MX_DR + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
+    // a wait gave up: the fixed-point sums cannot carry a NaN, so the
+    // workgroup's rows of the plain part become NaN instead (written by the
+    // threads that stored them, so in program order after them)
+    if (P.xb && !(ok_r && ok_s) && (tid * 4) / (MX_H / 256) == blockIdx.x)
+        *(f32x4 *)(P.xout + tid * 4) = f32x4{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
+                                             __builtin_nanf("")};
     ZH_TRACE_POINT(7);
 }
 
@@ -434,8 +447,8 @@ bool zhk_moe_xcd_supported(zh_ctx *c, uint32_t hidden, uint32_t n_experts, uint3
 }
 
 int zhk_moe_xcd(zh_ctx *c, const float *x, const float *norm_w, float eps, const uint8_t *router,
-                const uint8_t *egate, const uint8_t *eup, const uint8_t *edown, float *y, void *scratch,
-                uint32_t *routing, uint32_t *flags, const float *xb, float *xout, float *zero,
+                const uint8_t *egate, const uint8_t *eup, const uint8_t *edown, void *y, void *scratch,
+                uint32_t *routing, uint32_t *flags, const zh_fix *xb, float *xout, zh_fix *zero,
                 const uint32_t *force) {
     if (((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)router & 15) || ((uintptr_t)egate & 15) ||
         ((uintptr_t)eup & 15) || ((uintptr_t)edown & 15) || ((uintptr_t)scratch & 15) || !y || !routing ||

@@ -111,14 +111,16 @@ struct QaP {
     // atomics; x (the Q/K/V input) is then not x_acc, which changes during
     // the launch (a copy of it taken before, or the split residual below).
     const uint8_t *wo;
-    float *x_acc;
+    void *x_acc;                  // f32 (no split residual) or zh_fix (split residual: zh_xcd.h fix_add)
     uint64_t *xrows;              // [8][QA_XROWS] epoch-tagged Q/K/V rows (exchanged inside each XCD)
     // Split residual (with the O phase): the layer input is x + xb (xb: the
-    // previous launch's atomic sums, staged in K/V sub-chunk 0's slot, whose
-    // copy then waits until x is in registers); every workgroup stores its
-    // 16 rows of x + xb into x_out and zeroes its 16 rows of `zero`.
-    const float *xb;
-    float *x_out, *zero;
+    // previous launch's atomic sums in fixed point, staged in K/V sub-chunk
+    // 0's slot, whose copy then waits until x is in registers); every
+    // workgroup stores its 16 rows of x + xb into x_out and zeroes its 16
+    // rows of `zero`.
+    const zh_fix *xb;
+    float *x_out;
+    zh_fix *zero;
 };
 
 // LDS offset of K/V sub-chunk s: a ring of four slots (the third is the x
@@ -172,8 +174,13 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
             const uint32_t c = wl4 + 4 * i;
             dma16((const uint8_t *)P.x + c * 1024 + lane * 16, lds0 + QA_X + c * 1024);
             dma16((const uint8_t *)P.norm_w + c * 1024 + lane * 16, lds0 + QA_X + H * 4 + c * 1024);
-            if (P.xb) dma16((const uint8_t *)P.xb + c * 1024 + lane * 16, lds0 + qa_slot<SH>(0) + c * 1024);
         }
+        if (P.xb)  // (8 bytes per element: H / 128 copies of 1 KB)
+#pragma unroll
+            for (uint32_t i = 0; i < H / 512; i++) {
+                const uint32_t c = wl4 + 4 * i;
+                dma16((const uint8_t *)P.xb + c * 1024 + lane * 16, lds0 + qa_slot<SH>(0) + c * 1024);
+            }
 #pragma unroll
         for (uint32_t i = 0; i < (NCH + 3) / 4; i++) {
             const uint32_t c = wl4 + 4 * i;
@@ -242,8 +249,9 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         for (int it = 0; it < NIT; it++) {
             v[it] = *(const f32x4 *)(xr + (it * QA_T + tid) * 4);
             if (P.xb) {
-                const f32x4 d = *(const f32x4 *)((const float *)(lds + qa_slot<SH>(0)) + (it * QA_T + tid) * 4);
-                v[it].x += d.x; v[it].y += d.y; v[it].z += d.z; v[it].w += d.w;
+                const zh_fix *dq = (const zh_fix *)(lds + qa_slot<SH>(0)) + (it * QA_T + tid) * 4;
+                v[it].x += fix_to_f(dq[0]); v[it].y += fix_to_f(dq[1]);
+                v[it].z += fix_to_f(dq[2]); v[it].w += fix_to_f(dq[3]);
                 if ((it * QA_T + tid) * 4 / S::RROWS == blockIdx.x)  // this workgroup's rows
                     *(f32x4 *)(P.x_out + (it * QA_T + tid) * 4) = v[it];
             }
@@ -255,7 +263,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         if (lane == 0) red[wave] = sq;
         lds_bar();  // (also: every x / weight value is in registers before the image overwrites them)
         if (!wa && P.xb && P.kv_defer == 0 && n01 > 0) issue_kv(0);  // xb is read: sub-chunk 0's slot is free
-        if (P.zero && tid < S::RROWS) P.zero[blockIdx.x * S::RROWS + tid] = 0.f;
+        if (P.zero && tid < S::RROWS) P.zero[blockIdx.x * S::RROWS + tid] = 0;
         float tot = 0.f;
 #pragma unroll
         for (int w8 = 0; w8 < 8; w8++) tot += red[w8];
@@ -721,7 +729,10 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
                          h2f(wd[8] >> 16) * oxs[2 * q8 + 1] * comb_f(D1[0], D1[1], D1[2]));
         res = team_sum_dpp<8>(res);
         if (!(ok && ok_rows)) res = __builtin_nanf("");  // a wait gave up: the rows' sums are poisoned
-        if (q8 == 0) __hip_atomic_fetch_add(P.x_acc + j * QA_OROWS + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (q8 == 0) {
+            if (P.xb) fix_add((zh_fix *)P.x_acc + j * QA_OROWS + r, res);
+            else __hip_atomic_fetch_add((float *)P.x_acc + j * QA_OROWS + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     } else {
         // lane: row r = tid / 4 of the 128, half super-block q = tid % 4 of the
         // XCD's 4 G half-blocks (G = 4; fewer heads leave lanes idle)
@@ -777,7 +788,20 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         float res = act ? fmaf(hdr.d, accd, -hdr.dmin * accm) : 0.f;
         res = team_sum_dpp<4>(res);
         if (!(ok && ok_rows)) res = __builtin_nanf("");  // a wait gave up: the rows' sums are poisoned
-        if (q == 0) __hip_atomic_fetch_add(P.x_acc + j * QA_OROWS + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (q == 0) {
+            if (P.xb) fix_add((zh_fix *)P.x_acc + j * QA_OROWS + r, res);
+            else __hip_atomic_fetch_add((float *)P.x_acc + j * QA_OROWS + r, res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    // a wait gave up: the fixed-point sums cannot carry a NaN, so the
+    // workgroup's rows of the plain part become NaN instead (written by the
+    // threads that stored them above, so in program order after them)
+    if (P.x_out && !(ok && ok_rows)) {
+#pragma unroll
+        for (int it = 0; it < (int)(H / (4 * QA_T)); it++)
+            if ((it * QA_T + tid) * 4 / S::RROWS == blockIdx.x)
+                *(f32x4 *)(P.x_out + (it * QA_T + tid) * 4) = f32x4{__builtin_nanf(""), __builtin_nanf(""),
+                                                                     __builtin_nanf(""), __builtin_nanf("")};
     }
     ZH_TRACE_POINT(13);
 }
@@ -835,7 +859,7 @@ int zhk_qkv_attn(zh_ctx *c, const uint8_t *wq, const uint8_t *wk, const uint8_t 
                  const float *norm_w, float *q, float *k, float *v, const float *qw, const float *kw,
                  const float *rope_cs, uint16_t *kc, uint16_t *vc, uint32_t cache_tokens, float *out, void *xq_out,
                  uint32_t nh, zh_pos_src pos, float scale, float eps, float *partials, uint32_t *flags,
-                 const uint8_t *wo, float *x_acc, const float *xb, float *x_out, float *zero, uint32_t hidden,
+                 const uint8_t *wo, void *x_acc, const zh_fix *xb, float *x_out, zh_fix *zero, uint32_t hidden,
                  uint64_t *xrows) {
     QaP P = {};
     AttnP &p = P.a;
