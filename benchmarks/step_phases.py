@@ -117,8 +117,17 @@ def qkv_attn():
         g, r = (t[m, s] - base) * 0.01, (t[m, s] - t[m, 0]) * 0.01
         print(f"  {nm:24s}: n={m.sum():3d}  abs p50 {np.median(g):6.2f} max {g.max():6.2f}   "
               f"rel min {r.min():6.2f} p50 {np.median(r):6.2f} max {r.max():6.2f}")
+        _by_xcd(t, m, g, s)
     eng.deinit()
     ctx.close()
+
+
+def _by_xcd(t, m, g, s):
+    """The per-XCD launches record their XCD (+ 1) in slot 15: abs p50 / max per XCD."""
+    xcd = t[:, 15]
+    if s > 0 and ((xcd[m] >= 1) & (xcd[m] <= 8)).all():
+        per = [(np.median(g[xcd[m] == h + 1]), g[xcd[m] == h + 1].max()) for h in range(8) if (xcd[m] == h + 1).any()]
+        print("      by XCD (abs p50/max): " + "  ".join(f"{a:5.2f}/{b:5.2f}" for a, b in per))
 
 
 RING_POINTS = ["start", "activation landed", "XQ limbs in registers", "ring done", "outputs stored"]
@@ -166,6 +175,7 @@ def ring(group, dump="zh_debug_trace_ring", points=None, moe=False):
         g, r = (t[m, s] - base) * 0.01, (t[m, s] - t[m, 0]) * 0.01
         print(f"  {nm:24s}: n={m.sum():3d}  abs p50 {np.median(g):6.2f} max {g.max():6.2f}   "
               f"rel min {r.min():6.2f} p50 {np.median(r):6.2f} max {r.max():6.2f}")
+        _by_xcd(t, m, g, s)
     eng.deinit()
     ctx.close()
 

@@ -31,6 +31,12 @@ static __device__ uint64_t g_zh_trace[8192 * 16];
         const uint32_t bl_ = blockIdx.x + blockIdx.y * gridDim.x;                                     \
         if (threadIdx.x == 0 && bl_ < 8192 && (slot) < 16) g_zh_trace[bl_ * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
+// a value instead of a time stamp (e.g. the workgroup's XCD), in slot 15
+#define ZH_TRACE_VALUE(v)                                                                             \
+    do {                                                                                              \
+        const uint32_t bl_ = blockIdx.x + blockIdx.y * gridDim.x;                                     \
+        if (threadIdx.x == 0 && bl_ < 8192) g_zh_trace[bl_ * 16 + 15] = (uint64_t)(v);                \
+    } while (0)
 #define ZH_TRACE_DUMP_FN(name)                                                                        \
     extern "C" int name(uint64_t *host, uint32_t n) {                                                 \
         static uint64_t zeros[8192 * 16];                                                             \
@@ -39,6 +45,7 @@ static __device__ uint64_t g_zh_trace[8192 * 16];
     }
 #else
 #define ZH_TRACE_POINT(slot) do { } while (0)
+#define ZH_TRACE_VALUE(v) do { } while (0)
 #define ZH_TRACE_DUMP_FN(name)
 #endif
 

@@ -108,6 +108,7 @@ __global__ __launch_bounds__(RG_T, 1) void k_ffn_xcd(FfnP P) {
     uint32_t *ep = P.flags + XCD_N * XCD_PER + h;
     const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
     ZH_TRACE_POINT(0);
+    ZH_TRACE_VALUE(h + 1);  // (the XCD, + 1: a slot of 0 reads as unset)
 
     RingP p = {};
     p.norm_w = P.norm_w; p.eps = P.eps; p.M = FX_F; p.K = FX_H; p.nseg = 1; p.rpw = FX_RA;

@@ -92,6 +92,7 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
     uint8_t *ring = lds, *xqa = lds + RG_D * RG_TILE, *raw = lds + MX_RAW;
     float *yl = (float *)(lds + RG_D * RG_TILE + RG_XQ_BYTES + RG_RAW_BYTES), *red = yl + 2 * RG_MAXROWS;
     ZH_TRACE_POINT(0);
+    ZH_TRACE_VALUE(h + 1);  // (the XCD, + 1: a slot of 0 reads as unset)
 
     // ---- x, the norm weight (8 KB each: one copy per wave) and this
     // workgroup's router rows (8.5 KB: 9 copies, the last clamped)

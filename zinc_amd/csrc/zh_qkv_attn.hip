@@ -159,6 +159,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
     const uint32_t posv = *(const __attribute__((address_space(4))) uint32_t *)p.pos.dev + p.pos.value;
     const uint32_t E = *(const __attribute__((address_space(4))) uint32_t *)ep + 1u;
     ZH_TRACE_POINT(0);
+    ZH_TRACE_VALUE(h + 1);  // (the XCD, + 1: a slot of 0 reads as unset)
 
     // ---- copies. Waves 0-3 copy what the projection needs (x | attn_norm
     // weight, then the slice's weight rows); waves 4-7 the attention's (K/V
