@@ -176,6 +176,9 @@ def test_fused_wait_give_up_reports_and_recovers(orc):
             c.sync()
         assert e.value.name == "WaitTimeout"
         c.sync()
+        # zh_sync checked the workgroup placement again (it holds: the fused
+        # launch stays) and the engine re-records its step
+        assert "k_qkv_attn" in eng.group_kernels("qkv_attn")
         c.set_attn_wait_limit(50000)
         # the failed position again: until this step writes them, its cache
         # rows hold what the failed step wrote (NaN where a wait gave up),

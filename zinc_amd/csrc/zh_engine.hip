@@ -98,6 +98,7 @@ struct zh_engine {
     float *moe_scratch = nullptr;
     void *act_arena = nullptr;
     hipGraphExec_t g_out = nullptr, g_noout = nullptr;
+    uint32_t place_gen = 0;  // the context's place_gen the graphs were recorded under
     bool have_logits = false;
     // batched prefill activations (allocated on first use, PF_CHUNK tokens)
     struct {
@@ -1272,6 +1273,15 @@ static int set_state(zh_engine *e, uint32_t n_prompt, uint32_t pos, uint32_t fir
 }
 
 static int run_step(zh_engine *e, bool collect) {
+    if (e->place_gen != e->ctx->place_gen) {
+        // a bounded wait gave up since the graphs were recorded and zh_sync
+        // checked the placement again: record the step anew (with the
+        // per-group launches if the check failed)
+        if (e->g_out) hipGraphExecDestroy(e->g_out);
+        if (e->g_noout) hipGraphExecDestroy(e->g_noout);
+        e->g_out = e->g_noout = nullptr;
+        e->place_gen = e->ctx->place_gen;
+    }
     ERC(ensure_packed(e));
     if (zh_knob("ZH_NO_GRAPH")) return record_step(e, collect);
     ERC(ensure_graphs(e));

@@ -31,6 +31,11 @@ struct zh_ctx {
     int device = 0;
     int cu_count = 0;
     int xcd_rr = -1;  // zhk_xcd_round_robin: -1 unknown, 0 no, 1 yes
+    // Bumped by zh_sync when a bounded wait gave up, after it probed the
+    // workgroup placement again (xcd_rr): every engine re-records its step
+    // graph before its next step, which takes the per-group launches if the
+    // placement the per-XCD launches rely on no longer holds.
+    uint32_t place_gen = 0;
     hipStream_t stream = nullptr;
     hipEvent_t ev[64] = {};
     std::string err;

@@ -100,6 +100,11 @@ extern "C" int zh_sync(zh_ctx *c) {
         if (e & (ZH_DEVERR_ATTN_WAIT | ZH_DEVERR_STEP_BARRIER)) {
             for (const auto &w : c->xwords) ZH_HIP(c, hipMemset(w.p, 0, w.bytes));
             ZH_HIP(c, hipDeviceSynchronize());
+            // check the workgroup placement again (here, outside any graph
+            // capture: the probe synchronises); engines re-record their step
+            c->xcd_rr = -1;
+            zhk_xcd_round_robin(c);
+            c->place_gen++;
         }
         if (e & ZH_DEVERR_STEP_BARRIER)
             return zh_set_err(c, ZH_ERR_WAIT_TIMEOUT, "a grid barrier of the decode-layers kernel gave up waiting "
