@@ -13,10 +13,10 @@
 //      (every XCD computes all 128 logits, bit-identically, from the same
 //      bytes) and publish them in the XCD's L2 as epoch-tagged 64-bit words
 //      (zh_xcd.h tag_store), which every workgroup polls;
-//   2. every workgroup ranks the 128 logits itself (512 threads, a quarter
-//      of the comparisons each; the lowest index wins ties) and takes the top
-//      8 (weights: softmax over the selected logits) — XCD h takes the h-th
-//      selected expert e and its weight;
+//   2. every workgroup's polling wave takes the top 8 of the 128 logits
+//      itself (eight rounds of a wave maximum; the lowest index wins ties)
+//      and their weights (softmax over the selected logits) — XCD h takes
+//      the h-th selected expert e and its weight;
 //   3. workgroup j: gate and up rows [24 j, 24 j + 24) of expert e and their
 //      SwiGLU, published to the XCD (tagged words), while expert e's down rows
 //      [64 j, 64 j + 64) (the unmodified Q4_K bytes) stream in behind the
@@ -187,11 +187,11 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
         xs[q] = ixs[jb];
         xz[q] = ixz[2 * jb] + ixz[2 * jb + 1];
     }
-    // ---- the XCD's 128 logits (wave 0, as they arrive) into LDS; the top 8
-    // by rank: thread t counts, for logit t / 4, the logits in its quarter
-    // [32 (t % 4), +32) that precede it (a larger value, or an equal value
-    // at a lower index); rank < 8 places it (the order of
-    // topk_softmax_wave: value descending, lowest index first)
+    // ---- the XCD's 128 logits (wave 0, as they arrive); the top 8 in the
+    // same wave: eight rounds of a wave maximum over the logits not yet
+    // taken, the lowest index among equal values first (the order of
+    // topk_softmax_wave: value descending, lowest index first); a NaN logit
+    // is never taken (a NaN router leaves ids past the experts: clamped below)
     __shared__ float s_lg[MX_E];
     __shared__ uint32_t s_okr;
     if (wave == 0) {
@@ -199,32 +199,30 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
         const bool okr = tag_wait<2>(P.logits + h * MX_E, E, P.ctl, lv);
         s_lg[lane] = lv[0];
         s_lg[lane + 64] = lv[1];
-        if (lane < MX_K) s_route[lane] = 0xFFFFFFFFu;  // (a NaN logit ranks nowhere: clamped below)
         if (lane == 0) s_okr = okr ? 1u : 0u;
-    }
-    lds_bar();
-    ZH_TRACE_POINT(2);
-    {
-        const uint32_t i = tid >> 2, q = tid & 3;
-        const float li = s_lg[i];
-        uint32_t r = 0;
-#pragma unroll 8
-        for (uint32_t k = 32 * q; k < 32 * q + 32; k++) {
-            const float lk = s_lg[k];
-            r += (lk > li || (lk == li && k < i)) ? 1u : 0u;
+        ZH_TRACE_POINT(2);
+        bool t0 = false, t1 = false;  // taken
+        uint32_t id = 0xFFFFFFFFu;    // lane k < 8: the k-th selected expert
+        float lsel = -INFINITY;       //   and its logit
+#pragma unroll
+        for (int k = 0; k < (int)MX_K; k++) {
+            const float a0 = t0 ? -INFINITY : lv[0], a1 = t1 ? -INFINITY : lv[1];
+            const float m = wave_max(fmaxf(a0, a1));
+            const uint64_t b0 = __builtin_amdgcn_ballot_w64(!t0 && lv[0] == m);
+            const uint64_t b1 = __builtin_amdgcn_ballot_w64(!t1 && lv[1] == m);
+            const uint32_t i = b0 ? (uint32_t)__builtin_ctzll(b0) : b1 ? 64u + (uint32_t)__builtin_ctzll(b1) : 0xFFFFFFFFu;
+            if (lane == (uint32_t)k) { id = i; lsel = m; }
+            t0 = t0 || lane == i;
+            t1 = t1 || lane + 64 == i;
         }
-        r += __shfl_xor(r, 1, 64);
-        r += __shfl_xor(r, 2, 64);
-        if (q == 0 && r < MX_K) s_route[r] = i;
-    }
-    lds_bar();
-    if (wave == 0) {
         // weights: softmax over the selected logits (rank 0 holds the max)
-        const uint32_t id = lane < MX_K ? s_route[lane] : 0u;
-        const float l0 = s_lg[min(s_route[0], MX_E - 1)];
-        const float ex = lane < MX_K && id < MX_E ? expf(s_lg[id] - l0) : 0.f;
+        const float l0 = lane_f(lsel, 0);
+        const float ex = lane < MX_K && id < MX_E ? expf(lsel - l0) : 0.f;
         const float sm = wave_sum(ex);
-        if (lane < MX_K) ((float *)s_route)[MX_K + lane] = ex / sm;
+        if (lane < MX_K) {
+            s_route[lane] = id;
+            ((float *)s_route)[MX_K + lane] = ex / sm;
+        }
         __builtin_amdgcn_wave_barrier();  // (one wave: its LDS accesses complete in order)
         if (blockIdx.x == 0 && lane < 2 * MX_K) P.routing[lane] = s_route[lane];
         if (P.force) {
