@@ -138,7 +138,7 @@ FFN_POINTS = ["start", "activation landed", "XQ limbs in registers", "gate/up do
 
 
 MOE_POINTS = ["start", "x, norm, router rows landed", "router logits of the XCD seen", "top-8 selected",
-              "gate/up done", "SwiGLU values of the XCD seen", "", "end"]
+              "gate/up done", "SwiGLU values of the XCD seen", "top-8 ids (polling wave)", "end"]
 
 
 TILE_POINTS = ["start", "activation staged", "batch 0 in LDS", "batch 1", "batch 2", "batch 3", "batch 4+", "end"]

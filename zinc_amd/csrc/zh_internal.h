@@ -247,7 +247,7 @@ uint64_t zh_step_ctl_bytes();
 bool zhk_xcd_round_robin(zh_ctx *ctx);
 bool zhk_qkv_attn_supported(zh_ctx *ctx, uint32_t hidden, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx);
 uint32_t zhk_qkv_attn_flag_words();  // zeroed u32 words the caller keeps per engine
-// The split residual's atomic part: 64-bit fixed point in units of 2^-32
+// The split residual's atomic part: 64-bit fixed point in units of 2^-24
 // (zh_xcd.h fix_add / fix_to_f), so that its sums do not depend on the order
 // of the atomics.
 typedef long long zh_fix;

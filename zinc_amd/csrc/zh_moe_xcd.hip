@@ -215,6 +215,7 @@ __global__ __launch_bounds__(RG_T, 1) void k_moe_xcd(MoeP P) {
             t0 = t0 || lane == i;
             t1 = t1 || lane + 64 == i;
         }
+        ZH_TRACE_POINT(6);
         // weights: softmax over the selected logits (rank 0 holds the max)
         const float l0 = lane_f(lsel, 0);
         const float ex = lane < MX_K && id < MX_E ? expf(lsel - l0) : 0.f;

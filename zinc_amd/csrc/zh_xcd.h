@@ -105,21 +105,25 @@ ZH_DEV bool tag_wait(const uint64_t *p, uint32_t E, uint32_t *ctl, float (&v)[N]
 }
 
 // The split residual's atomic part (zh_engine.hip step_xcd): 64-bit fixed
-// point in units of 2^-32. Integer adds commute, so the sum of a row's
+// point in units of 2^-24. Integer adds commute, so the sum of a row's
 // contributions (one per XCD or expert) does not depend on the order the
 // atomics land in, and the decode step is deterministic; each contribution
-// is rounded once, to 2^-32 absolute. Values must stay below 2^30 in
-// magnitude: a NaN or out-of-range contribution adds a poison value that
-// reads back as NaN. (zh_fix: zh_internal.h)
+// is rounded once, to 2^-24 absolute (finer than f32 above magnitude 1).
+// Sums must stay below 2^37 in magnitude (the synthetic 8B-shape model's
+// residual reaches ~2^31): a NaN or out-of-range contribution adds a poison
+// value (-2^38 in value) that reads back as NaN while at most three of them
+// meet in one element. (The launches also write NaN into the plain part of
+// the residual when a wait gives up, which carries it whatever the
+// accumulator holds.) (zh_fix: zh_internal.h)
 ZH_DEV void fix_add(zh_fix *p, float v) {
-    const double s = (double)v * 4294967296.0;
+    const double s = (double)v * 16777216.0;
     const long long q = fabs(s) < 0x1p61 ? (long long)__builtin_rint(s) : (long long)(-0x1p62);
     __hip_atomic_fetch_add(p, q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 ZH_DEV float fix_to_f(zh_fix q) {
-    const int hi = (int)(q >> 32);
+    const int hi = (int)(q >> 32);  // units of 2^8
     const uint32_t lo = (uint32_t)q;
-    if ((uint32_t)(hi + (1 << 30)) >= (1u << 31)) return __builtin_nanf("");
-    return fmaf((float)lo, 0x1p-32f, (float)hi);
+    if ((uint32_t)hi + (1u << 29) >= (1u << 30)) return __builtin_nanf("");  // |value| >= 2^37
+    return fmaf((float)lo, 0x1p-24f, (float)hi * 256.f);
 }
 
