@@ -14,6 +14,15 @@ A streaming read of 1 GiB gives the measured ceiling beside it.
 
     python -m benchmarks.dmmv_sweep --batched [--md OUT.md]
 
+Under rocprofv3 --kernel-trace, each timed block of launches is bracketed by
+two four-element k_swiglu launches (separators), so
+
+    python -m benchmarks.dmmv_sweep --from-trace RUN_kernel_trace.csv SWEEP.json [--md OUT.md]
+
+recovers every (shape, activation) entry's kernel time per call from the
+trace: per kernel of the call, the mean of the middle 80% of its dispatch
+durations, summed over the kernels the call launches.
+
 instead times the batched DMMV (zh_dmmv_batched / the gate/up form, the
 skinny GEMM of recordBatchDispatchPush, dmmv.zig:880-925) on the config-3
 decode shapes at 1, 2, 4 and 8 activation vectors: microseconds per launch
@@ -22,6 +31,7 @@ times the speed-up over one launch per vector).
 """
 import argparse
 import json
+import statistics
 import sys
 
 from zinc_amd import hip
@@ -53,6 +63,7 @@ def measure(ctx, name, qt, M, K, iters):
     xq = ctx.alloc(ctx.xq_bytes(K))
     ctx.quantize_activation(x, 0, K, xq)
     y = ctx.alloc(M * 4)
+    sep = ctx.alloc(256)
     alg = wb + 4 * K + 4 * M
     res = {"shape": name, "qtype": qt, "M": M, "K": K, "weight_bytes": wb, "alg_bytes": alg, "copies": ncp}
     for label, fn in (("f32_x", lambda c: ctx.dmmv(qt, W, c * wb, x, 0, y, 0, M, K, 0)),
@@ -65,17 +76,64 @@ def measure(ctx, name, qt, M, K, iters):
         for i in range(2 * ncp):
             fn(i % ncp)
         ctx.sync()
+        ctx.swiglu(sep, sep, sep, 4)  # separator (kernel trace: the sweep launches no other k_swiglu)
         ctx.record(0)
         for i in range(iters):
             fn(i % ncp)
         ctx.record(1)
+        ctx.swiglu(sep, sep, sep, 4)
         ctx.sync()
         us = ctx.elapsed_ms(0, 1) * 1e3 / iters
         gbs = alg / (us * 1e-6) / 1e9
         res[label] = {"us": round(us, 3), "GBs": round(gbs, 1), "frac": round(gbs / PEAK, 4)}
-    for b in (W, x, xq, y):
+    for b in (W, x, xq, y, sep):
         ctx.free(b)
     return res
+
+
+def from_trace(csv_path, sweep_json):
+    """Per (shape, activation) entry: the kernels between each pair of
+    separators and their time per call (middle-80% mean per kernel, summed).
+    Given a counter-collection CSV (rocprofv3 --pmc FETCH_SIZE) instead: the
+    fetched bytes per call, calibrated against the sweep's 1 GiB stream
+    probe (k_stream_read / k_stream_slice) in the same run."""
+    import csv
+    rows = list(csv.DictReader(open(csv_path)))
+    pmc = "Counter_Value" in rows[0]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"] if pmc else r["Start_Timestamp"]))
+    factor = 1.0
+    if pmc:
+        cal = [float(r["Counter_Value"]) for r in rows if r["Kernel_Name"].removeprefix("void ").startswith("k_stream_")]
+        factor = (1 << 30) / (statistics.mean(cal) * 1024.0)
+    sweep = json.loads(open(sweep_json).read().strip().splitlines()[-1])
+    entries = [(r["shape"], lab) for r in sweep["shapes"] for lab in ("f32_x", "xq_x") if "us" in r[lab]]
+    seps = [i for i, r in enumerate(rows) if "k_swiglu" in r["Kernel_Name"]]
+    if len(seps) != 2 * len(entries):
+        raise SystemExit(f"expected {2 * len(entries)} separators, found {len(seps)}")
+    out = []
+    for k, (shape, lab) in enumerate(entries):
+        block = rows[seps[2 * k] + 1:seps[2 * k + 1]]
+        by = {}
+        for r in block:
+            v = (float(r["Counter_Value"]) * 1024.0 * factor if pmc
+                 else (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            by.setdefault(r["Kernel_Name"], []).append(v)
+        calls = max(len(v) for v in by.values())
+        us, names = 0.0, []
+        for name, d in by.items():
+            d = sorted(d)
+            cut = len(d) // 10
+            mid = d[cut:len(d) - cut] or d
+            us += sum(mid) / len(mid) * len(d) / calls
+            names.append(name.split("(")[0])
+        alg = next(r["alg_bytes"] for r in sweep["shapes"] if r["shape"] == shape)
+        if pmc:  # (us holds bytes here)
+            out.append({"shape": shape, "entry": lab, "kernels": names, "fetch_bytes": round(us),
+                        "alg_bytes": alg, "fetch_over_alg": round(us / alg, 4)})
+        else:
+            out.append({"shape": shape, "entry": lab, "kernels": names, "us": round(us, 3),
+                        "frac": round(alg / (us * 1e-6) / 1e9 / PEAK, 4), "alg_bytes": alg})
+    return out
 
 
 BATCH_SHAPES = [
@@ -108,10 +166,12 @@ def measure_batched(ctx, name, qt, M, K, gate_up, ncols=(1, 2, 4, 8), iters=40):
         for i in range(2 * ncp):
             fn(i % ncp)
         ctx.sync()
+        ctx.swiglu(sep, sep, sep, 4)  # separator (kernel trace: the sweep launches no other k_swiglu)
         ctx.record(0)
         for i in range(iters):
             fn(i % ncp)
         ctx.record(1)
+        ctx.swiglu(sep, sep, sep, 4)
         ctx.sync()
         us = ctx.elapsed_ms(0, 1) * 1e3 / iters
         res["cols"][n] = {"us": round(us, 2), "us_per_col": round(us / n, 2)}
@@ -125,7 +185,27 @@ def main():
     ap.add_argument("--batched", action="store_true", help="time the batched DMMV at 1, 2, 4, 8 vectors")
     ap.add_argument("--iters", type=int, default=60)
     ap.add_argument("--md", default=None, help="also write a markdown table here")
+    ap.add_argument("--from-trace", nargs=2, metavar=("TRACE_CSV", "SWEEP_JSON"),
+                    help="kernel times per entry from a kernel trace of a sweep run")
     a = ap.parse_args()
+    if a.from_trace:
+        rows = from_trace(*a.from_trace)
+        print(json.dumps(rows))
+        if a.md:
+            with open(a.md, "w") as f:
+                if "us" in rows[0]:
+                    f.write("| shape | activation | kernels | alg bytes | us per call | of 8 TB/s |\n"
+                            "|---|---|---|---|---|---|\n")
+                    for r in rows:
+                        f.write(f"| {r['shape']} | {r['entry']} | `{' + '.join(r['kernels'])}` | {r['alg_bytes']:,} | "
+                                f"{r['us']} | {r['frac']:.1%} |\n")
+                else:
+                    f.write("| shape | activation | kernels | alg bytes | FETCH bytes per call | fetch / alg |\n"
+                            "|---|---|---|---|---|---|\n")
+                    for r in rows:
+                        f.write(f"| {r['shape']} | {r['entry']} | `{' + '.join(r['kernels'])}` | {r['alg_bytes']:,} | "
+                                f"{r['fetch_bytes']:,} | {r['fetch_over_alg']:.3f} |\n")
+        return 0
     ctx = hip.Context(0)
     if a.batched:
         rows = [measure_batched(ctx, *s) for s in BATCH_SHAPES]
