@@ -26,7 +26,10 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 constexpr int GT = 256;         // threads (4 waves)
 constexpr int TI = 128;         // tokens per tile
 constexpr int KS = 128;         // k per step: half a super-block
-constexpr int LDR = KS + 8;     // halfs per LDS row (272 B: 16-byte reads of 8 rows hit distinct banks)
+// halfs per LDS row: 288 B (measured on the 512-token prefill: 15.45 ms
+// against 15.88 for 272 B rows, 24.6 for unpadded 256 B rows; strides that
+// are not a multiple of 16 B split the 16-byte reads)
+constexpr int LDR = KS + 16;
 
 struct GemmP {
     // up to three stacked weight matrices sharing X (Q/K/V, gate/up): rows
@@ -149,7 +152,7 @@ ZH_DEV void deq_q6k_unit(const RawQ6K &r, uint32_t g, _Float16 *dst) {
 // +TJ/2 (4 x TJ/32 MFMA tiles). Each step the threads dequantise the tile's
 // TJ x 4 units of 32 elements (UPT per thread) into LDS while the X chunks
 // of the next step and the raw weight bytes of the next two steps are in
-// flight in registers. 70 KB of
+// flight in registers. 74 KB of
 // LDS (TJ = 128): two workgroups per CU, so one's dequantisation overlaps
 // the other's MFMAs.
 template <int QT, int TJ>
