@@ -28,7 +28,8 @@ constexpr int TI = 128;         // tokens per tile
 constexpr int KS = 128;         // k per step: half a super-block
 // halfs per LDS row: 288 B (measured on the 512-token prefill: 15.45 ms
 // against 15.88 for 272 B rows, 24.6 for unpadded 256 B rows; strides that
-// are not a multiple of 16 B split the 16-byte reads)
+// are not a multiple of 16 B split the 16-byte reads; unpadded rows with the
+// 16-byte chunks XOR-swizzled by the row: 15.97)
 constexpr int LDR = KS + 16;
 
 struct GemmP {
