@@ -184,7 +184,8 @@ def main():
                    "token_roofline_frac": round(bytes_tok * tok_s / 1e9 / PEAK_HBM_GBS, 4),
                    "token_frac_of_stream_ceiling": round(bytes_tok * tok_s / 1e9 / ceiling, 4),
                    "gpu_ms_per_step": round(gpu_ms / args.steps, 4),
-                   "kv_pages": args.pages, "persistent_layers": bool(args.persistent)},
+                   "kv_pages": args.pages, "persistent_layers": bool(args.persistent),
+                   "residual_sums": "64-bit fixed point (bit-reproducible decode)"},
         "roofline": roof,
         "per_kernel": per_kernel,
         "step_consistency": per_kernel_graph,
