@@ -132,18 +132,19 @@ ZH_DEV const uint16_t *kv_row(const uint16_t *h, size_t pa, size_t pb, size_t pc
 // LOCAL: every partial was written by a workgroup on this XCD (plain stores,
 // held in the XCD's L2) and this workgroup has not read them before in this
 // launch (its L1 holds no copy): plain loads, which hit the L2.
-template <int GM, int NBAT, bool COH = false, bool LOCAL = false>
+template <int GM, int NBAT, bool COH = false, bool LOCAL = false, int NT = AD_T>
 ZH_DEV void attn_merge(const AttnP &p, uint32_t h0, uint32_t nv, bool poison, float *lds_out = nullptr) {
     auto ld1 = [](const float *q) { return LOCAL ? *q : ld_dev(q); };
     auto ld2 = [](const float *q) { return LOCAL ? *(const uint64_t *)q : ld_dev64(q); };
-    // any workgroup size of at least AD_T threads (every thread calls it)
+    // any workgroup size of at least NT threads (every thread calls it)
     const uint32_t tid = COH ? phase_tid() : threadIdx.x, wave = tid >> 6, lane = tid & 63, nthr = blockDim.x;
     TRACE_OPS(11);
     // Chunk merge. The first batch of each thread's O dims (NBAT chunks) is
     // requested before the chunk statistics, so both arrive in about one
     // round trip; the statistics pass leaves m_c in LDS for the weights.
-    // dims per thread: power of two with G*128/OPT <= AD_T
-    constexpr int OPT = GM * FD_HD <= AD_T ? 1 : GM * FD_HD <= 2 * AD_T ? 2 : GM * FD_HD <= 4 * AD_T ? 4 : 8;
+    // dims per thread: the smallest power of two with G*128/OPT <= NT (more
+    // threads means more partial loads in flight; the merge waits on them)
+    constexpr int OPT = GM * FD_HD <= NT ? 1 : GM * FD_HD <= 2 * NT ? 2 : GM * FD_HD <= 4 * NT ? 4 : 8;
     constexpr int NTH = GM * FD_HD / OPT;
     constexpr int MB = 256;                 // chunk statistics kept in LDS
     __shared__ __align__(16) float sm[GM][MB];
@@ -697,7 +698,7 @@ ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *ld
         if (s_prev != nv - 1) return;
         TRACE_OPS(4);
         if (tid == 0) __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        attn_merge<G, G <= 4 ? 40 : 12, COH>(p, kvh * G, nv, false);
+        attn_merge<G, G <= 4 ? 40 : 12, COH, false, AT>(p, kvh * G, nv, false);
         return;
     }
     // Every workgroup resident (the persistent kernel, or a launch with the
@@ -732,7 +733,7 @@ ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *ld
         }
     }
     __syncthreads();
-    if (nm == 1) attn_merge<G, G <= 4 ? 40 : 12, COH>(p, kvh * G, nv, !s_ok);
+    if (nm == 1) attn_merge<G, G <= 4 ? 40 : 12, COH, false, AT>(p, kvh * G, nv, !s_ok);
     else attn_merge<1, 32, COH>(p, kvh * G + slot, nv, !s_ok);
 }
 

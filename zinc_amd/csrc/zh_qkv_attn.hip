@@ -692,7 +692,7 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
         AttnP pm = p;
         pm.out = nullptr;
         pm.xq = nullptr;
-        attn_merge<G, 32, false, true>(pm, h * G, nv, false, mo);
+        attn_merge<G, 32, false, true, QA_T>(pm, h * G, nv, false, mo);
     }
     ZH_TRACE_POINT(12);
     __syncthreads();
