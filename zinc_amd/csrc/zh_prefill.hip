@@ -104,9 +104,13 @@ ZH_DEV void deq_q4k_unit(const RawQ4K &r, uint32_t p, uint32_t nib, _Float16 *ds
         half8 o[2];
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            const uint32_t n4 = (qw[w] >> (4 * nib)) & 0x0F0F0F0Fu;
+            uint32_t n4 = (qw[w] >> (4 * nib)) & 0x0F0F0F0Fu;
+            // (kept as one word: each element is then a byte conversion,
+            // v_cvt_f32_ubyteN, instead of a bit-field extract and a
+            // conversion)
+            asm volatile("" : "+v"(n4));
 #pragma unroll
-            for (int b = 0; b < 4; b++) {  // byte-to-float conversions (v_cvt_f32_ubyteN)
+            for (int b = 0; b < 4; b++) {
                 const int e = 4 * w + b;
                 o[e >> 3][e & 7] = to_h(__fsub_rn(__fmul_rn(dj, (float)((n4 >> (8 * b)) & 0xFF)), mj));
             }
