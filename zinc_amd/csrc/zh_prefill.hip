@@ -85,8 +85,10 @@ ZH_DEV void load_q6k_unit(const uint8_t *blk, uint32_t h, uint32_t g, RawQ6K &r)
 
 // Q4_K sub-block j = 2p + nib (32 elements: nibble nib of qs[32p .. 32p+31])
 // into LDS. dequantRow Q4_K (forward.zig:370-409): dj = d*sc[j],
-// mj = dmin*m[j], out = dj*q - mj; the f32 operations rounded one by one (no
-// contraction), then to fp16 (nearest even).
+// mj = dmin*m[j], out = dj*q - mj in f32, then to fp16 (nearest even). dj
+// and mj (an 11-bit f16 times a 6-bit integer) and dj*q (times a 4-bit q)
+// are exact in f32, so the fused multiply-add the compiler forms rounds
+// once, exactly where dequantRow's subtraction does.
 ZH_DEV void deq_q4k_unit(const RawQ4K &r, uint32_t p, uint32_t nib, _Float16 *dst) {
     const uint32_t w0 = r.hdr.x, w1 = r.hdr.y, w2 = r.hdr.z, w3 = r.hdr.w;
     const float d = h2f(w0), dmin = h2f(w0 >> 16);
