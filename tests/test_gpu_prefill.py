@@ -38,6 +38,28 @@ def test_gemm_one_hot_gives_the_fp16_weights_exactly(ctx, orc, qtype):
         ctx.free(b)
 
 
+def test_gemm_rounds_the_f32_dequant_value_to_fp16(ctx):
+    """The weight operand is dequantRow's f32 value rounded to fp16, not the
+    exact value rounded once: on the block of test_oracle.py's
+    test_dequant_q4k_f32_tie_block (f32 value 2051/2048, an fp16 tie) every
+    weight is 1 + 2^-9; a conversion fused into the multiply-add gives
+    1 + 2^-10."""
+    M, K = 128, 256
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([293 / 2048], np.float16).view(np.uint8)
+    blk[2:4] = np.array([1], np.uint16).view(np.uint8)  # dmin = 2^-24
+    blk[4:16] = [1] * 8 + [0x11] * 4                     # every sc and m = 1
+    blk[16:] = 0x77                                      # every q = 7
+    W = ctx.upload(np.tile(blk, M))
+    X = ctx.upload(np.eye(K, dtype=np.float16))
+    Y = ctx.alloc(4 * M * K)
+    ctx.gemm_xw(12, W, 0, X, 0, Y, 0, M, K, K)
+    y = Y.download(np.float32, (K, M))
+    assert np.all(y == np.float32(1 + 2 ** -9)), np.unique(y)
+    for b in (W, X, Y):
+        ctx.free(b)
+
+
 @pytest.mark.parametrize("qtype,M,K,N", [
     (12, 256, 512, 37), (12, 1024, 4096, 512), (12, 4096, 4096, 128), (12, 6144, 4096, 300),
     (14, 256, 512, 64), (14, 4096, 12288, 130), (14, 384, 1024, 1),

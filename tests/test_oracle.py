@@ -628,3 +628,21 @@ def test_sampling_ties_nonfinite_and_penalty(orc):
                                   repetition_penalty=2.0) == 0
     # a single finite candidate is returned whatever u is
     assert orc.sample_from_logits(np.array([np.nan, 7.0, np.nan], np.float32), temperature=0.9, u=0.99) == 1
+
+
+def test_dequant_q4k_f32_tie_block(orc):
+    """d = 293/2048, dmin = 2^-24 (the smallest fp16 subnormal), every sc and
+    m = 1, every q = 7: dj*q - mj = 2051/2048 - 2^-24 lies halfway between two
+    f32 values and rounds to the even one, 2051/2048 -- itself halfway between
+    fp16 1 + 2^-10 and 1 + 2^-9, which rounds to 1 + 2^-9. (The GPU prefill
+    GEMM's fp16 operand test uses this block: rounding the exact value to
+    fp16 once would give 1 + 2^-10.)"""
+    blk = np.zeros(144, np.uint8)
+    put16(blk, 0, np.float16(293 / 2048))
+    blk[2:4] = np.array([1], np.uint16).view(np.uint8)
+    blk[4:16] = pack_scale_min_k4([1] * 8, [1] * 8)
+    assert list(blk[4:16]) == [1] * 8 + [0x11] * 4
+    blk[16:] = 0x77
+    out = orc.dequant_row(blk, 0, 256, orc.Q4_K)
+    assert np.all(out == np.float32(2051 / 2048))
+    assert np.all(out.astype(np.float16) == np.float16(1 + 2 ** -9))

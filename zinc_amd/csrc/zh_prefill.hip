@@ -51,7 +51,14 @@ struct GemmP {
     float *part;
 };
 
-ZH_DEV _Float16 to_h(float v) { return (_Float16)v; }  // round to nearest even
+// f32 -> fp16, round to nearest even, from the f32 value: the empty asm
+// keeps the compiler from fusing the conversion into the producing
+// multiply-add (v_fma_mix rounds the exact result to fp16 once, which
+// differs from rounding the f32 value when that lands on an fp16 tie)
+ZH_DEV _Float16 to_h(float v) {
+    asm("" : "+v"(v));
+    return (_Float16)v;
+}
 
 // Raw bytes of one dequantisation unit -- 32 elements of one weight row --
 // loaded a K-step ahead.
@@ -87,8 +94,9 @@ ZH_DEV void load_q6k_unit(const uint8_t *blk, uint32_t h, uint32_t g, RawQ6K &r)
 // into LDS. dequantRow Q4_K (forward.zig:370-409): dj = d*sc[j],
 // mj = dmin*m[j], out = dj*q - mj in f32, then to fp16 (nearest even). dj
 // and mj (an 11-bit f16 times a 6-bit integer) and dj*q (times a 4-bit q)
-// are exact in f32, so the fused multiply-add the compiler forms rounds
-// once, exactly where dequantRow's subtraction does.
+// are exact in f32, so the f32 multiply-add the compiler forms rounds once,
+// exactly where dequantRow's subtraction does; to_h then rounds that f32
+// value.
 ZH_DEV void deq_q4k_unit(const RawQ4K &r, uint32_t p, uint32_t nib, _Float16 *dst) {
     const uint32_t w0 = r.hdr.x, w1 = r.hdr.y, w2 = r.hdr.z, w3 = r.hdr.w;
     const float d = h2f(w0), dmin = h2f(w0 >> 16);
