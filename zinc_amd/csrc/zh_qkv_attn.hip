@@ -563,20 +563,27 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
 #pragma unroll
             for (int s8 = 0; s8 < 8; s8++)
                 kf[s8] = *(const half4 *)(Ks + t * 256 + (((2 * s8 + (fq >> 1)) ^ (t & 15)) * 16) + 8 * (fq & 1));
-            const uint32_t tv = tb + 4 * fq, off = 2 * (fg & 7);
-            // V rows past the chunk are zeroed, not only weighted 0: they copy
-            // the cache's row of the new token, which this launch has not
-            // written yet and may hold anything (NaN after a step whose waits
-            // gave up), and 0 x NaN is NaN
+            // P V's column j of MFMA tile n is dim 8 j + n, so a lane's
+            // operands are dims 8 fg .. 8 fg + 7 of its 4 tokens: one 16-byte
+            // piece of each token's row. V rows past the chunk are zeroed,
+            // not only weighted 0: they copy the cache's row of the new token,
+            // which this launch has not written yet and may hold anything
+            // (NaN after a step whose waits gave up), and 0 x NaN is NaN
+            const uint32_t tv = tb + 4 * fq;
             const uint32_t tvalid = t1 - ts;  // tokens of the sub-chunk in the chunk
+            u32x4 pv[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t t2 = tv + r;
+                const u32x4 w = *(const u32x4 *)(Vs + t2 * 256 + (fg ^ (t2 & 15)) * 16);
+                pv[r] = t2 < tvalid ? w : u32x4{0u, 0u, 0u, 0u};
+            }
 #pragma unroll
             for (int n = 0; n < 8; n++) {
-                const uint32_t pc = 2 * n + (fg >> 3);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const uint32_t t2 = tv + r;
-                    const _Float16 vv = *(const _Float16 *)(Vs + t2 * 256 + (pc ^ (t2 & 15)) * 16 + off);
-                    vf[n][r] = t2 < tvalid ? vv : (_Float16)0.f;
+                    const uint32_t d = pv[r][n >> 1];
+                    vf[n][r] = __builtin_bit_cast(_Float16, (uint16_t)((n & 1) ? d >> 16 : d));
                 }
             }
         }
@@ -635,9 +642,11 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const uint32_t g = 4 * fq + r;
-        if (g < (uint32_t)G)
-#pragma unroll
-            for (int n = 0; n < 8; n++) wo[(wave * G + g) * FD_HD + 16 * n + fg] = acc[n][r];
+        if (g < (uint32_t)G) {  // dims 8 fg .. 8 fg + 7 of head g: two 16-byte stores
+            f32x4 *o = (f32x4 *)(wo + (wave * G + g) * FD_HD + 8 * fg);
+            o[0] = f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+            o[1] = f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+        }
     }
     if (fq == 0 && fg < (uint32_t)G) {
         wm[wave * G + fg] = m_run;
