@@ -574,20 +574,28 @@ ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *ld
 #pragma unroll
                 for (int s8 = 0; s8 < 8; s8++)
                     kf[s8] = *(const half4 *)(Ks + t * 256 + (((2 * s8 + (fq >> 1)) ^ (t & 15)) * 16) + 8 * (fq & 1));
-                const uint32_t tv = tb + 4 * fq, off = 2 * (fg & 7);
-                // V rows past the chunk are zeroed, not only weighted 0: they copy
-                // the cache's row of the new token, which this launch has not
-                // written yet and may hold anything (NaN after a step whose waits
-                // gave up), and 0 x NaN is NaN
+                // P V's column j of MFMA tile n is dim 8 j + n, so a lane's
+                // operands are dims 8 fg .. 8 fg + 7 of its 4 tokens: one
+                // 16-byte piece of each token's row. V rows past the chunk are
+                // zeroed, not only weighted 0: they copy the cache's row of the
+                // new token, which this launch has not written yet and may hold
+                // anything (NaN after a step whose waits gave up), and 0 x NaN
+                // is NaN
+                const uint32_t tv = tb + 4 * fq;
                 const uint32_t tvalid = t1 - ts;  // tokens of the sub-chunk in the chunk
+                u32x4 pv[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t t2 = tv + r;
+                    const u32x4 w = *(const u32x4 *)(Vs + t2 * 256 + (fg ^ (t2 & 15)) * 16);
+                    pv[r] = t2 < tvalid ? w : u32x4{0u, 0u, 0u, 0u};
+                }
 #pragma unroll
                 for (int n = 0; n < 8; n++) {
-                    const uint32_t pc = 2 * n + (fg >> 3);
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        const uint32_t t2 = tv + r;
-                        const _Float16 vv = *(const _Float16 *)(Vs + t2 * 256 + (pc ^ (t2 & 15)) * 16 + off);
-                        vf[n][r] = t2 < tvalid ? vv : (_Float16)0.f;
+                        const uint32_t d = pv[r][n >> 1];
+                        vf[n][r] = __builtin_bit_cast(_Float16, (uint16_t)((n & 1) ? d >> 16 : d));
                     }
                 }
             }
@@ -650,14 +658,16 @@ ZH_DEV void attn_ring_body(const AttnP &p, uint32_t kvh, uint32_t c, uint8_t *ld
     // a wave, then waves
     float *wm = (float *)lds, *wl = wm + AW * G, *wo = wl + AW * G;  // [AW][G], [AW][G], [AW][G][128]
     lds_bar();  // every wave is done with the ring
-    // lane l: heads 4 fq + r, dim 16 n + fg; the running statistics of head
-    // fg are in the lanes with fq = 0
+    // lane l: heads 4 fq + r, dims 8 fg + n (two 16-byte stores per head);
+    // the running statistics of head fg are in the lanes with fq = 0
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const uint32_t g = 4 * fq + r;
-        if (g < (uint32_t)G)
-#pragma unroll
-            for (int n = 0; n < 8; n++) wo[(wave * G + g) * FD_HD + 16 * n + fg] = acc[n][r];
+        if (g < (uint32_t)G) {
+            f32x4 *o = (f32x4 *)(wo + (wave * G + g) * FD_HD + 8 * fg);
+            o[0] = f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+            o[1] = f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+        }
     }
     if (fq == 0 && fg < (uint32_t)G) {
         wm[wave * G + fg] = m_run;
