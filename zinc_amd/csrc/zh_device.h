@@ -121,6 +121,26 @@ ZH_DEV float team_sum(float v) {
     for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+// Butterfly exchanges across rows, lane l with lane l ^ 16 / l ^ 32, as
+// VALU permlane swaps (no LDS round trip): swapping v with itself leaves the
+// lower lane's value in r[0] and the upper lane's in r[1] in both lanes of a
+// pair, so both compute op(lower, upper) -- the same bits in both lanes.
+ZH_DEV float xor16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+ZH_DEV float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+ZH_DEV float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+ZH_DEV float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 // DPP lane exchanges inside a 16-lane row and readlane across rows: a few
 // cycles each instead of an LDS-crossbar round trip. All 64 lanes of the
 // wave must be active. Controls: quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] =
@@ -156,7 +176,7 @@ ZH_DEV float team_sum_dpp(float v) {
     }
     if (TL == 8) return row8_sum(v);
     v = row16_sum(v);
-    if (TL == 32) return v + __shfl_xor(v, 16, 64);
+    if (TL == 32) return xor16_sum(v);
     if (TL >= 64) return rows_sum(v);
     return v;
 }

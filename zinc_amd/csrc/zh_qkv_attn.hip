@@ -597,8 +597,8 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
 #pragma unroll
         for (int r = 0; r < 4; r++) sc[r] = ts + tb + 4 * fq + r < t1 ? d1[r] * p.scale : -INFINITY;
         float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        m = fmaxf(m, __shfl_xor(m, 16, 64));
-        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        m = xor16_max(m);
+        m = xor32_max(m);
         const float mn = fmaxf(m_run, m);
         const float ms = mn == -INFINITY ? 0.f : mn;
         const float f = m_run == -INFINITY ? 0.f : expf(m_run - ms);
@@ -608,8 +608,8 @@ __global__ __launch_bounds__(QA_T, 1) void k_qkv_attn(QaP P) {
             pr[r] = fg < (uint32_t)G ? expf(sc[r] - ms) : 0.f;
             lsum += pr[r];
         }
-        lsum += __shfl_xor(lsum, 16, 64);
-        lsum += __shfl_xor(lsum, 32, 64);
+        lsum = xor16_sum(lsum);
+        lsum = xor32_sum(lsum);
         l_run = fmaf(l_run, f, lsum);
         m_run = mn;
         half4 ph, pl;
