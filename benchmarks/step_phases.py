@@ -14,8 +14,9 @@ Build the debug library first (it also compiles the points in):
     ZH_LIB_PATH=build/debug/libzinc_hip.so python -m benchmarks.step_phases
     ZH_LIB_PATH=build/debug/libzinc_hip.so python -m benchmarks.step_phases --standalone
 
---qkv-attn: the Q/K/V + attention launch (k_qkv_attn) of the per-phase
-step, replayed by zh_engine_time_kernel.
+--qkv-attn [--ctx N]: the Q/K/V + attention launch (k_qkv_attn) of the
+per-phase step, replayed by zh_engine_time_kernel (KV context N, default
+4096).
 
 --ffn: the per-XCD FFN launch (k_ffn_xcd).
 
@@ -88,16 +89,17 @@ QA_POINTS = ["start", "x landed", "XQ limbs in registers", "weight rows landed",
              "merge: start", "merge: statistics done"]
 
 
-def qkv_attn():
-    """Per-workgroup timeline of k_qkv_attn (Q/K/V + attention in one launch)."""
+def qkv_attn(ctxlen=4096):
+    """Per-workgroup timeline of k_qkv_attn (Q/K/V + attention in one launch)
+    at a KV context of ctxlen (+ 2 decoded tokens)."""
     L = hip.lib()
     L.zh_debug_trace_qa.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
     ctx = hip.Context(0)
     cfg = dict(DENSE_8B)
-    cfg["max_ctx"] = 4096 + 64
+    cfg["max_ctx"] = ctxlen + 64
     eng = InferenceEngine(ctx, cfg)
-    eng.prefill_kv_random(4096, 7)
-    eng.generate([17, 18], 2, start_pos=4096)
+    eng.prefill_kv_random(ctxlen, 7)
+    eng.generate([17, 18], 2, start_pos=ctxlen)
     ctx.sync()
     n = 8192 * 16
     a = np.zeros(n, np.uint64)
@@ -188,7 +190,7 @@ def main():
     if "--moe-attn" in sys.argv[1:]:
         return standalone(moe=True)
     if "--qkv-attn" in sys.argv[1:]:
-        return qkv_attn()
+        return qkv_attn(int(sys.argv[sys.argv.index("--ctx") + 1]) if "--ctx" in sys.argv[1:] else 4096)
     if "--ring" in sys.argv[1:]:
         return ring(sys.argv[sys.argv.index("--ring") + 1])
     if "--moe" in sys.argv[1:]:
