@@ -1576,7 +1576,8 @@ extern "C" int zh_engine_prefill(zh_engine *e, const uint32_t *tokens, uint32_t 
         ERC(zhk_dequant_rows(c, e->embd.type, W(e->embd), 0, nt, H, e->pf.hid, e->pf.ids + off, m.vocab, 1));
         for (uint32_t l = 0; l < m.n_layers; l++) {
             const Layer &y = e->L[l];
-            ERC(zhk_rms_norm_rows_f16(c, e->pf.hid, Wf(y.attn_norm), e->pf.xh, H, nt, m.eps));
+            // attn_norm: layer 0 here, later layers in the previous layer's down projection
+            if (l == 0) ERC(zhk_rms_norm_rows_f16(c, e->pf.hid, Wf(y.attn_norm), e->pf.xh, H, nt, m.eps));
             {  // Q, K and V: one launch per run of equal types (one when all agree)
                 const Tensor *ts[3] = {&y.wq, &y.wk, &y.wv};
                 float *ys[3] = {e->pf.q, e->pf.k, e->pf.v};
@@ -1595,8 +1596,9 @@ extern "C" int zh_engine_prefill(zh_engine *e, const uint32_t *tokens, uint32_t 
                                     zh_pos_src{pos0, nullptr}, m.eps, nt));
             ERC(zhk_attn_prefill(c, e->pf.q, y.kc, y.vc, e->pages, e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd,
                                  pos0, nt, scale, e->pf.att));
-            ERC(zhk_gemm(c, y.wo.type, W(y.wo), e->pf.att, qd, e->pf.hid, H, H, qd, nt, 1));
-            ERC(zhk_rms_norm_rows_f16(c, e->pf.hid, Wf(y.ffn_norm), e->pf.xh, H, nt, m.eps));
+            // O added into the residual, then ffn_norm (one pass with the split-K sums)
+            ERC(zhk_gemm_norm(c, y.wo.type, W(y.wo), e->pf.att, qd, e->pf.hid, H, qd, nt, 1, nullptr,
+                              Wf(y.ffn_norm), e->pf.xh, m.eps));
             if (y.gate.type == y.up.type) {  // gate and up in one launch
                 const uint8_t *ws[2] = {W(y.gate), W(y.up)};
                 float *ys[2] = {e->pf.g, e->pf.u};
@@ -1607,7 +1609,11 @@ extern "C" int zh_engine_prefill(zh_engine *e, const uint32_t *tokens, uint32_t 
                 ERC(zhk_gemm(c, y.up.type, W(y.up), e->pf.xh, H, e->pf.u, F, F, H, nt, 0));
             }
             ERC(zhk_swiglu_rows_f16(c, e->pf.g, e->pf.u, e->pf.s, e->pf.s_unscale, F, nt));
-            ERC(zhk_gemm(c, y.down.type, W(y.down), e->pf.s, F, e->pf.hid, H, H, F, nt, 1, e->pf.s_unscale));
+            if (l + 1 < m.n_layers)  // down added into the residual, then the next layer's attn_norm
+                ERC(zhk_gemm_norm(c, y.down.type, W(y.down), e->pf.s, F, e->pf.hid, H, F, nt, 1, e->pf.s_unscale,
+                                  Wf(e->L[l + 1].attn_norm), e->pf.xh, m.eps));
+            else
+                ERC(zhk_gemm(c, y.down.type, W(y.down), e->pf.s, F, e->pf.hid, H, H, F, nt, 1, e->pf.s_unscale));
         }
     }
     EHIP(e, hipMemcpyAsync(e->hidden, e->pf.hid + (size_t)(last - 1) * H, 4ull * H, hipMemcpyDeviceToDevice,

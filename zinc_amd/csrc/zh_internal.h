@@ -175,7 +175,14 @@ int zhk_gemm(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, const _Float16 *X, u
 // Up to three stacked matrices sharing X (segment rows multiples of 64).
 int zhk_gemm_multi(zh_ctx *ctx, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, const _Float16 *X,
                    uint32_t ldx, float *const *Y, const uint32_t *ldy, const uint32_t *M, uint32_t K, uint32_t N,
-                   uint32_t acc, const float *x_unscale = nullptr);
+                   uint32_t acc, const float *x_unscale = nullptr, const float *norm_w = nullptr,
+                   _Float16 *norm_out = nullptr, float eps = 0.f);
+// Y (+)= X W^T (one matrix, Y rows M apart), then norm_out = fp16 RMSNorm of
+// Y's rows times norm_w (the next GEMM's input; fused into the split-K
+// epilogue when K is split).
+int zhk_gemm_norm(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, const _Float16 *X, uint32_t ldx, float *Y,
+                  uint32_t M, uint32_t K, uint32_t N, uint32_t acc, const float *x_unscale, const float *norm_w,
+                  _Float16 *norm_out, float eps);
 int zhk_rms_norm_rows_f16(zh_ctx *ctx, const float *x, const float *w, _Float16 *out, uint32_t n, uint32_t rows,
                           float eps);
 int zhk_swiglu_rows_f16(zh_ctx *ctx, const float *g, const float *u, _Float16 *out, float *unscale, uint32_t n,

@@ -297,14 +297,75 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
     *yp = acc ? *yp + v : v;
 }
 
+// The same split-K epilogue fused with the RMSNorm the next GEMM takes as
+// its input, one workgroup per token row (M <= 16384, M % 4 == 0, Y rows M
+// apart): row n of Y (+)= (sum over z of part[z][n], in split order) *
+// unscale[n], exactly as k_gemm_reduce, then out[n] = fp16(w * (y * rms_inv))
+// with the sums of squares in k_rms_norm_rows_f16's order (cpuRmsNormMul,
+// forward.zig:618-626).
+constexpr int RN_RV = 16;
+__global__ __launch_bounds__(256) void k_reduce_rms_rows_f16(const float *__restrict__ part, uint32_t ksplit,
+                                                             uint32_t N, uint32_t M, float *__restrict__ Y,
+                                                             uint32_t acc, const float *__restrict__ x_unscale,
+                                                             const float *__restrict__ w, _Float16 *__restrict__ out,
+                                                             float eps) {
+    const uint32_t r = blockIdx.x, t = threadIdx.x;
+    __shared__ float red[4];
+    f32x4 v[RN_RV];
+    float sq = 0.f;
+    const float us = x_unscale ? x_unscale[r] : 1.0f;
+#pragma unroll
+    for (int j = 0; j < RN_RV; j++) {
+        const uint32_t i = 4 * (t + 256 * j);
+        if (i < M) {
+            const size_t o = (size_t)r * M + i;
+            f32x4 s = *(const f32x4 *)(part + o);
+            for (uint32_t z = 1; z < ksplit; z++) {
+                const f32x4 pz = *(const f32x4 *)(part + (size_t)z * N * M + o);
+                s.x += pz.x; s.y += pz.y; s.z += pz.z; s.w += pz.w;
+            }
+            if (x_unscale) {  // exact: a power of two
+                s.x *= us; s.y *= us; s.z *= us; s.w *= us;
+            }
+            f32x4 y = s;
+            if (acc) {
+                const f32x4 yo = *(const f32x4 *)(Y + o);
+                y = f32x4{yo.x + s.x, yo.y + s.y, yo.z + s.z, yo.w + s.w};
+            }
+            *(f32x4 *)(Y + o) = y;
+            v[j] = y;
+        } else {
+            v[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        sq = fmaf(v[j].x, v[j].x, fmaf(v[j].y, v[j].y, fmaf(v[j].z, v[j].z, fmaf(v[j].w, v[j].w, sq))));
+    }
+    sq = wave_sum(sq);
+    if ((t & 63) == 0) red[t >> 6] = sq;
+    __syncthreads();
+    const float rms_inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)M + eps);
+#pragma unroll
+    for (int j = 0; j < RN_RV; j++) {
+        const uint32_t i = 4 * (t + 256 * j);
+        if (i < M) {
+            const f32x4 wv = *(const f32x4 *)(w + i);
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            *(h4 *)(out + (size_t)r * M + i) =
+                h4{(_Float16)(wv.x * (v[j].x * rms_inv)), (_Float16)(wv.y * (v[j].y * rms_inv)),
+                   (_Float16)(wv.z * (v[j].z * rms_inv)), (_Float16)(wv.w * (v[j].w * rms_inv))};
+        }
+    }
+}
+
 }  // namespace
 
 int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, const _Float16 *X, uint32_t ldx,
                    float *const *Y, const uint32_t *ldy, const uint32_t *M, uint32_t K, uint32_t N, uint32_t acc,
-                   const float *x_unscale) {
+                   const float *x_unscale, const float *norm_w, _Float16 *norm_out, float eps) {
     if ((qtype != ZH_Q4_K && qtype != ZH_Q6_K) || K % 256 || N == 0 || nseg < 1 || nseg > 3)
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: qtype %u K %u N %u nseg %u", qtype, K, N, nseg);
     GemmP p = {};
+    if (norm_out && (nseg != 1 || !norm_w || ldy[0] != M[0] || M[0] % 4 || M[0] > 4u * 256u * RN_RV))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: fused norm needs one matrix of rows %u apart", M[0]);
     p.nseg = nseg; p.row_bytes = zh_tensor_bytes(qtype, 1, K); p.X = X; p.x_unscale = x_unscale;
     p.K = K; p.N = N; p.ldx = ldx; p.acc = acc;
     uint32_t end = 0;
@@ -349,10 +410,16 @@ int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *cons
     if (qtype == ZH_Q4_K) { if (small) GL(ZH_Q4_K, 64); else GL(ZH_Q4_K, 128); }
     else { if (small) GL(ZH_Q6_K, 64); else GL(ZH_Q6_K, 128); }
 #undef GL
-    if (p.ksplit > 1) {
+    if (p.ksplit > 1 && norm_out) {
+        hipLaunchKernelGGL(k_reduce_rms_rows_f16, dim3(N), dim3(256), 0, c->stream, p.part, p.ksplit, N, end, Y[0],
+                           acc, x_unscale, norm_w, norm_out, eps);
+    } else if (p.ksplit > 1) {
         const uint64_t n = (uint64_t)N * end;
         hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c->stream, p.part, p.ksplit,
                            N, end, Y[0], ldy[0], acc, x_unscale);
+    } else if (norm_out) {
+        ZH_LAUNCH_CHECK(c);
+        return zhk_rms_norm_rows_f16(c, Y[0], norm_w, norm_out, end, N, eps);
     }
     ZH_LAUNCH_CHECK(c);
     return ZH_OK;
@@ -361,6 +428,12 @@ int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *cons
 int zhk_gemm(zh_ctx *c, uint32_t qtype, const uint8_t *W, const _Float16 *X, uint32_t ldx, float *Y, uint32_t ldy,
              uint32_t M, uint32_t K, uint32_t N, uint32_t acc, const float *x_unscale) {
     return zhk_gemm_multi(c, qtype, 1, &W, X, ldx, &Y, &ldy, &M, K, N, acc, x_unscale);
+}
+
+int zhk_gemm_norm(zh_ctx *c, uint32_t qtype, const uint8_t *W, const _Float16 *X, uint32_t ldx, float *Y, uint32_t M,
+                  uint32_t K, uint32_t N, uint32_t acc, const float *x_unscale, const float *norm_w,
+                  _Float16 *norm_out, float eps) {
+    return zhk_gemm_multi(c, qtype, 1, &W, X, ldx, &Y, &M, &M, K, N, acc, x_unscale, norm_w, norm_out, eps);
 }
 
 // Y[n][m] (+)= X[n][:] . W[m][:], X fp16 token-major, Y f32 token-major
