@@ -551,7 +551,12 @@ __global__ __launch_bounds__(256) void k_swiglu_rows_f16(const float *__restrict
 // blocks).
 constexpr int AQ = 64, AK = 64;
 constexpr int AKLD = 128 + 8;  // halfs per K row (272 B)
-constexpr int AVLD = AK + 8;   // halfs per transposed V row and per P row (144 B)
+constexpr int AVLD = AK + 8;   // halfs per P row (144 B)
+// V transposed, [d][key] with 64 keys per row (128 B, no padding): the 16-byte
+// chunk of keys 8c .. 8c + 7 of row d sits at chunk c ^ ((d / 8) % 8), so the
+// 16 lanes that store one key's 16 chunks of dims (2-byte stores) spread over
+// 8 bank groups instead of one, and a B fragment is still one 16-byte read
+ZH_DEV uint32_t vt_at(uint32_t d, uint32_t key) { return d * AK + ((((key >> 3) ^ (d >> 3)) & 7) << 3) + (key & 7); }
 __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float *__restrict__ q, const uint16_t *__restrict__ kc,
                                                            const uint16_t *__restrict__ vc,
                                                            const uint32_t *__restrict__ pages, uint32_t n_pages,
@@ -560,7 +565,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float *__restri
                                                            _Float16 *__restrict__ out) {
     constexpr int HD = 128;
     __shared__ __align__(16) _Float16 ks[AK * AKLD];
-    __shared__ __align__(16) uint16_t vt[HD * AVLD];
+    __shared__ __align__(16) uint16_t vt[HD * AK];
     __shared__ __align__(16) _Float16 pl[4][16 * AVLD];
     const uint32_t h = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t i0 = (gridDim.y - 1 - blockIdx.y) * AQ;  // longest tiles first
@@ -587,21 +592,33 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float *__restri
     const uint32_t kmax = pos0 + min(i0 + AQ, N) - 1;  // last key any query of the workgroup sees
     const uint32_t qpos = pos0 + i0 + 16 * wave + 4 * lg;  // position of this lane's row r = 0
     _Float16 *pw = pl[wave];
-    for (uint32_t kb = 0; kb * AK <= kmax; kb++) {
-        // stage the key block: K rows as they are, V transposed (rows past
-        // kmax are loaded clamped and masked below)
-        for (uint32_t c = tid; c < AK * 16; c += 256) {
-            const uint32_t key = c / 16, ch = c % 16, t = min(kb * AK + key, kmax);
+    // the key block's K and V chunks (16 B of one key each: 4 per thread)
+    // wait in registers, requested while the previous block computes; rows
+    // past kmax are loaded clamped and masked below
+    u32x4 pk[4], pv[4];
+    auto load_kv = [&](uint32_t kb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const uint32_t c = tid + 256 * it, key = c / 16, ch = c % 16, t = min(kb * AK + key, kmax);
             uint32_t ph = pages[min(t / 16, n_pages - 1)] * 16 + t % 16;
             ph = ph < cache_tokens ? ph : 0u;
-            const u32x4 kv = *(const u32x4 *)(kh + (size_t)ph * HD + ch * 8);
-            const u32x4 vv = *(const u32x4 *)(vh + (size_t)ph * HD + ch * 8);
-            *(u32x4 *)(ks + key * AKLD + ch * 8) = kv;
-            const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+            pk[it] = *(const u32x4 *)(kh + (size_t)ph * HD + ch * 8);
+            pv[it] = *(const u32x4 *)(vh + (size_t)ph * HD + ch * 8);
+        }
+    };
+    load_kv(0);
+    for (uint32_t kb = 0; kb * AK <= kmax; kb++) {
+        // stage the key block: K rows as they are, V transposed
 #pragma unroll
-            for (int e = 0; e < 8; e++) vt[(ch * 8 + e) * AVLD + key] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        for (int it = 0; it < 4; it++) {
+            const uint32_t c = tid + 256 * it, key = c / 16, ch = c % 16;
+            *(u32x4 *)(ks + key * AKLD + ch * 8) = pk[it];
+            const uint32_t w[4] = {pv[it].x, pv[it].y, pv[it].z, pv[it].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) vt[vt_at(ch * 8 + e, key)] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
         }
         __syncthreads();
+        if ((kb + 1) * AK <= kmax) load_kv(kb + 1);
         f32x4v sc[4];
 #pragma unroll
         for (int jb = 0; jb < 4; jb++) {
@@ -650,7 +667,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float *__restri
             const half8 a = *(const half8 *)(pw + li * AVLD + 32 * k2 + 8 * lg);
 #pragma unroll
             for (int db = 0; db < 8; db++) {
-                const half8 b = *(const half8 *)(vt + (16 * db + li) * AVLD + 32 * k2 + 8 * lg);
+                const half8 b = *(const half8 *)(vt + vt_at(16 * db + li, 32 * k2 + 8 * lg));
                 o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, o[db], 0, 0, 0);
             }
         }
