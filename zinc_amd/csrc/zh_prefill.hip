@@ -272,7 +272,7 @@ __global__ __launch_bounds__(GT, 2) void k_gemm(GemmP p) {
             for (int r = 0; r < 4; r++) {
                 const uint32_t tok = n0 + wi * 64 + i * 16 + 4 * (lane / 16) + r;
                 if (p.ksplit > 1) {
-                    if (tok < p.N && row < Ms) p.part[((size_t)z * p.N + tok) * p.M + row] = acc[i][j][r];
+                    if (tok < p.N && row < Ms) p.part[((size_t)z * p.N + tok) * p.M + seg_start + row] = acc[i][j][r];
                 } else if (tok < p.N && row < Ms) {
                     float *yp = p.segY[sg] + (size_t)tok * p.segLdy[sg] + row;
                     const float v = p.x_unscale ? acc[i][j][r] * p.x_unscale[tok] : acc[i][j][r];  // exact
@@ -295,6 +295,20 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
     if (x_unscale) v *= x_unscale[n];  // exact: a power of two
     float *yp = Y + (size_t)n * ldy + m;
     *yp = acc ? *yp + v : v;
+}
+
+// The same over stacked segments: column m of part goes to the segment
+// holding row m.
+__global__ __launch_bounds__(256) void k_gemm_reduce_seg(GemmP p) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint64_t)p.N * p.M) return;
+    const uint32_t n = (uint32_t)(i / p.M), m = (uint32_t)(i % p.M);
+    float v = p.part[i];
+    for (uint32_t z = 1; z < p.ksplit; z++) v += p.part[(size_t)z * p.N * p.M + i];
+    if (p.x_unscale) v *= p.x_unscale[n];  // exact: a power of two
+    const uint32_t sg = (m >= p.seg_end[0] ? 1u : 0u) + (p.nseg > 2 && m >= p.seg_end[1] ? 1u : 0u);
+    float *yp = p.segY[sg] + (size_t)n * p.segLdy[sg] + (m - (sg ? p.seg_end[sg - 1] : 0u));
+    *yp = p.acc ? *yp + v : v;
 }
 
 // The same split-K epilogue fused with the RMSNorm the next GEMM takes as
@@ -378,24 +392,25 @@ int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *cons
     for (uint32_t s = nseg; s < 3; s++) p.seg_end[s] = end;
     p.M = end;
     const uint32_t ni = (N + TI - 1) / TI;
-    // Stacked matrices: 64-row tiles when 128-row tiles would leave CUs idle;
-    // every segment but the last must then be a whole number of tiles. A
-    // single matrix keeps 128-row tiles and splits K instead (below).
-    bool small = (uint64_t)((end + 127) / 128) * ni < (uint64_t)c->cu_count &&
-                 (nseg > 1 || zh_knob("ZH_GEMM_TJ64"));
+    // 128-row tiles, K split when there are fewer tiles than two per CU
+    // (below); 64-row tiles only where a segment boundary needs them (every
+    // segment but the last is a whole number of tiles)
+    bool small = zh_knob("ZH_GEMM_TJ64");
     for (uint32_t s = 0; s + 1 < nseg; s++)
         if (M[s] % 128) small = true;
     for (uint32_t s = 0; s + 1 < nseg; s++)
         if (M[s] % 64) return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: segment rows %u not a multiple of 64", M[s]);
     const uint32_t TJv = small ? 64 : 128;
     const uint32_t lds = (TI + TJv) * LDR * 2;
-    // A single matrix with fewer tiles than two per CU (O, down) splits K so
+    // Fewer tiles than two per CU (O, down, the stacked Q/K/V): split K so
     // two workgroups share each CU (one's dequantisation overlapping the
-    // other's MFMAs); at least 8 K-steps per split.
+    // other's MFMAs), within one round of resident workgroups (rounding the
+    // split up measured slower for Q/K/V: 576 workgroups for 512 slots); at
+    // least 8 K-steps per split.
     const uint64_t tiles = (uint64_t)((end + TJv - 1) / TJv) * ni, slots = 2ull * (uint64_t)c->cu_count;
     p.ksplit = 1;
-    if (nseg == 1 && tiles < slots && !zh_knob("ZH_NO_SPLITK")) {
-        uint32_t sk = (uint32_t)((slots + tiles - 1) / tiles);
+    if (tiles < slots && !zh_knob("ZH_NO_SPLITK")) {
+        uint32_t sk = (uint32_t)(slots / tiles);
         while (sk > 1 && K / KS < 8 * sk) sk--;
         p.ksplit = sk;
     }
@@ -413,6 +428,9 @@ int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *cons
     if (p.ksplit > 1 && norm_out) {
         hipLaunchKernelGGL(k_reduce_rms_rows_f16, dim3(N), dim3(256), 0, c->stream, p.part, p.ksplit, N, end, Y[0],
                            acc, x_unscale, norm_w, norm_out, eps);
+    } else if (p.ksplit > 1 && nseg > 1) {
+        const uint64_t n = (uint64_t)N * end;
+        hipLaunchKernelGGL(k_gemm_reduce_seg, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c->stream, p);
     } else if (p.ksplit > 1) {
         const uint64_t n = (uint64_t)N * end;
         hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c->stream, p.part, p.ksplit,
