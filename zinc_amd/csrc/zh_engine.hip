@@ -1582,18 +1582,25 @@ extern "C" int zh_engine_prefill(zh_engine *e, const uint32_t *tokens, uint32_t 
                 const Tensor *ts[3] = {&y.wq, &y.wk, &y.wv};
                 float *ys[3] = {e->pf.q, e->pf.k, e->pf.v};
                 const uint32_t ld[3] = {qd, kvd, kvd}, ms[3] = {qd, kvd, kvd};
+                // one launch for all three (head_dim 128): q/k norm, RoPE and the
+                // KV-cache write in its epilogue
+                const zh_gemm_rope rope = {Wf(y.q_norm), Wf(y.k_norm), e->inv_freq, y.kc, y.vc, e->pages,
+                                           e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, pos0, m.eps};
+                const bool fused = hd == 128 && ts[0]->type == ts[1]->type && ts[1]->type == ts[2]->type;
                 for (uint32_t i0 = 0; i0 < 3;) {
                     uint32_t i1 = i0 + 1;
                     while (i1 < 3 && ts[i1]->type == ts[i0]->type) i1++;
                     const uint8_t *ws[3];
                     for (uint32_t i = i0; i < i1; i++) ws[i - i0] = W(*ts[i]);
-                    ERC(zhk_gemm_multi(c, ts[i0]->type, i1 - i0, ws, e->pf.xh, H, ys + i0, ld + i0, ms + i0, H, nt, 0));
+                    ERC(zhk_gemm_multi(c, ts[i0]->type, i1 - i0, ws, e->pf.xh, H, ys + i0, ld + i0, ms + i0, H, nt, 0,
+                                       nullptr, nullptr, nullptr, 0.f, fused ? &rope : nullptr));
                     i0 = i1;
                 }
+                if (!fused)
+                    ERC(zhk_qk_norm_rope_kv(c, e->pf.q, Wf(y.q_norm), e->pf.k, Wf(y.k_norm), e->pf.v, e->inv_freq, y.kc,
+                                            y.vc, e->pages, e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd,
+                                            zh_pos_src{pos0, nullptr}, m.eps, nt));
             }
-            ERC(zhk_qk_norm_rope_kv(c, e->pf.q, Wf(y.q_norm), e->pf.k, Wf(y.k_norm), e->pf.v, e->inv_freq, y.kc, y.vc,
-                                    e->pages, e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd,
-                                    zh_pos_src{pos0, nullptr}, m.eps, nt));
             ERC(zhk_attn_prefill(c, e->pf.q, y.kc, y.vc, e->pages, e->n_pages, m.max_ctx, m.n_heads, m.n_kv_heads, hd,
                                  pos0, nt, scale, e->pf.att));
             // O added into the residual, then ffn_norm (one pass with the split-K sums)

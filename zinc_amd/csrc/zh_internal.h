@@ -172,11 +172,21 @@ int zhk_attn_decode_fused_z(zh_ctx *ctx, uint32_t n, const float *const *q, cons
 // Prefill (zh_prefill.hip)
 int zhk_gemm(zh_ctx *ctx, uint32_t qtype, const uint8_t *W, const _Float16 *X, uint32_t ldx, float *Y, uint32_t ldy,
              uint32_t M, uint32_t K, uint32_t N, uint32_t acc, const float *x_unscale = nullptr);
+// Epilogue of the stacked q | k | v projection (head_dim 128): q/k RMSNorm +
+// RoPE, q written back in place, k and v into the KV cache (the work of
+// zhk_qk_norm_rope_kv, fused into the split-K sums when K is split).
+struct zh_gemm_rope {
+    const float *q_norm, *k_norm, *inv_freq;
+    uint16_t *kc, *vc;
+    const uint32_t *pages;
+    uint32_t n_pages, cache_tokens, nq, nkv, pos0;
+    float eps;
+};
 // Up to three stacked matrices sharing X (segment rows multiples of 64).
 int zhk_gemm_multi(zh_ctx *ctx, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, const _Float16 *X,
                    uint32_t ldx, float *const *Y, const uint32_t *ldy, const uint32_t *M, uint32_t K, uint32_t N,
                    uint32_t acc, const float *x_unscale = nullptr, const float *norm_w = nullptr,
-                   _Float16 *norm_out = nullptr, float eps = 0.f);
+                   _Float16 *norm_out = nullptr, float eps = 0.f, const zh_gemm_rope *rope = nullptr);
 // Y (+)= X W^T (one matrix, Y rows M apart), then norm_out = fp16 RMSNorm of
 // Y's rows times norm_w (the next GEMM's input; fused into the split-K
 // epilogue when K is split).

@@ -311,6 +311,63 @@ __global__ __launch_bounds__(256) void k_gemm_reduce_seg(GemmP p) {
     *yp = p.acc ? *yp + v : v;
 }
 
+// The split-K epilogue of the stacked q | k | v projection (acc 0, no
+// unscale) fused with the q/k RMSNorm, RoPE and the KV-cache write of
+// k_qk_norm_rope_kv (zh_ops.hip; cpuRmsNormMul + applyRope, the same f32
+// operations in the same order), one workgroup per token: wave w takes
+// heads w, w + 4, ... of the 40 (q, then k, then v), lane dims lane and
+// lane + 64 (a RoPE pair).
+__global__ __launch_bounds__(256) void k_reduce_qkv_rope(GemmP p, zh_gemm_rope r) {
+    constexpr uint32_t HD = 128;
+    const uint32_t n = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t pos = r.pos0 + n;
+    const uint32_t slot = pos / 16;
+    bool ok = slot < r.n_pages;
+    const uint32_t phys = ok ? r.pages[slot] * 16 + pos % 16 : 0;
+    ok = ok && phys < r.cache_tokens;
+    const float *pn = p.part + (size_t)n * p.M;
+    const size_t zs = (size_t)p.N * p.M;
+    for (uint32_t hh = wave; hh < r.nq + 2 * r.nkv; hh += 4) {  // uniform per wave
+        const uint32_t c0 = hh * HD;
+        float a = pn[c0 + lane], b = pn[c0 + lane + 64];
+        for (uint32_t z = 1; z < p.ksplit; z++) {
+            a += pn[z * zs + c0 + lane];
+            b += pn[z * zs + c0 + lane + 64];
+        }
+        if (hh < r.nq + r.nkv) {
+            const bool is_q = hh < r.nq;
+            const uint32_t head = is_q ? hh : hh - r.nq;
+            float sq = 0.f;
+            sq = fmaf(a, a, sq);
+            sq = fmaf(b, b, sq);
+            sq = wave_sum(sq);
+            const float rms_inv = 1.0f / sqrtf(sq / (float)HD + r.eps);
+            const float *wt = is_q ? r.q_norm : r.k_norm;
+            const uint32_t i = lane;
+            const float lo = wt[i] * (a * rms_inv);
+            const float hi = wt[i + 64] * (b * rms_inv);
+            const float th = (float)pos * r.inv_freq[i];
+            float sn, co;
+            sincosf(th, &sn, &co);
+            const float rlo = lo * co - hi * sn;
+            const float rhi = lo * sn + hi * co;
+            if (is_q) {
+                float *qo = p.segY[0] + (size_t)n * p.segLdy[0] + (size_t)head * HD;
+                qo[i] = rlo;
+                qo[i + 64] = rhi;
+            } else if (ok) {
+                uint16_t *kdst = r.kc + ((size_t)head * r.cache_tokens + phys) * HD;
+                kdst[i] = f2h_rn(rlo);
+                kdst[i + 64] = f2h_rn(rhi);
+            }
+        } else if (ok) {
+            uint16_t *vdst = r.vc + ((size_t)(hh - r.nq - r.nkv) * r.cache_tokens + phys) * HD;
+            vdst[lane] = f2h_rn(a);
+            vdst[lane + 64] = f2h_rn(b);
+        }
+    }
+}
+
 // The same split-K epilogue fused with the RMSNorm the next GEMM takes as
 // its input, one workgroup per token row (M <= 16384, M % 4 == 0, Y rows M
 // apart): row n of Y (+)= (sum over z of part[z][n], in split order) *
@@ -374,12 +431,16 @@ __global__ __launch_bounds__(256) void k_reduce_rms_rows_f16(const float *__rest
 
 int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *const *W, const _Float16 *X, uint32_t ldx,
                    float *const *Y, const uint32_t *ldy, const uint32_t *M, uint32_t K, uint32_t N, uint32_t acc,
-                   const float *x_unscale, const float *norm_w, _Float16 *norm_out, float eps) {
+                   const float *x_unscale, const float *norm_w, _Float16 *norm_out, float eps,
+                   const zh_gemm_rope *rope) {
     if ((qtype != ZH_Q4_K && qtype != ZH_Q6_K) || K % 256 || N == 0 || nseg < 1 || nseg > 3)
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: qtype %u K %u N %u nseg %u", qtype, K, N, nseg);
     GemmP p = {};
     if (norm_out && (nseg != 1 || !norm_w || ldy[0] != M[0] || M[0] % 4 || M[0] > 4u * 256u * RN_RV))
         return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: fused norm needs one matrix of rows %u apart", M[0]);
+    if (rope && (nseg != 3 || acc || x_unscale || M[0] != rope->nq * 128u || M[1] != rope->nkv * 128u ||
+                 M[2] != rope->nkv * 128u || ldy[0] != M[0] || ldy[1] != M[1] || ldy[2] != M[2]))
+        return zh_set_err(c, ZH_ERR_INVALID_ARGUMENT, "gemm: the q | k | v epilogue needs head_dim 128 rows");
     p.nseg = nseg; p.row_bytes = zh_tensor_bytes(qtype, 1, K); p.X = X; p.x_unscale = x_unscale;
     p.K = K; p.N = N; p.ldx = ldx; p.acc = acc;
     uint32_t end = 0;
@@ -425,6 +486,17 @@ int zhk_gemm_multi(zh_ctx *c, uint32_t qtype, uint32_t nseg, const uint8_t *cons
     if (qtype == ZH_Q4_K) { if (small) GL(ZH_Q4_K, 64); else GL(ZH_Q4_K, 128); }
     else { if (small) GL(ZH_Q6_K, 64); else GL(ZH_Q6_K, 128); }
 #undef GL
+    if (rope && p.ksplit > 1) {
+        hipLaunchKernelGGL(k_reduce_qkv_rope, dim3(N), dim3(256), 0, c->stream, p, *rope);
+        ZH_LAUNCH_CHECK(c);
+        return ZH_OK;
+    }
+    if (rope) {  // (K not split: the sums are in Y already)
+        ZH_LAUNCH_CHECK(c);
+        return zhk_qk_norm_rope_kv(c, Y[0], rope->q_norm, Y[1], rope->k_norm, Y[2], rope->inv_freq, rope->kc, rope->vc,
+                                   rope->pages, rope->n_pages, rope->cache_tokens, rope->nq, rope->nkv, 128,
+                                   zh_pos_src{rope->pos0, nullptr}, rope->eps, N);
+    }
     if (p.ksplit > 1 && norm_out) {
         hipLaunchKernelGGL(k_reduce_rms_rows_f16, dim3(N), dim3(256), 0, c->stream, p.part, p.ksplit, N, end, Y[0],
                            acc, x_unscale, norm_w, norm_out, eps);
