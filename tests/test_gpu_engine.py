@@ -189,7 +189,7 @@ def test_engine_long_context_subchunks(ctx, orc, prefill):
     om.close()
 
 
-# Paged KV cache (SURVEY a13): the engine's page table comes from a page pool
+# Paged KV cache: the engine's page table comes from a page pool
 # (KvPagePool, kv_cache.zig:43-125: a fresh pool hands out pages in
 # descending order) or is an arbitrary permutation; the decode kernel then
 # looks every 16-token page up (logicalTokenToPhysicalToken,
